@@ -1,0 +1,81 @@
+// Shared host/device helpers for libhbt.so (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "hbt.h"
+
+namespace hbt {
+
+// ---- error reporting -------------------------------------------------------------
+// One message per host thread; set by a failing entry point, read by hbt_last_error().
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+void clear_error();
+
+// Returns HBT_ERR_HIP (with a message naming `what`) if a HIP call or the last
+// launch failed, else HBT_OK.
+int32_t check_hip(hipError_t status, const char* what);
+int32_t check_launch(const char* what);
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Number of compute units of the current device (cached per device id).
+int device_cu_count();
+
+// ---- dtype helpers -------------------------------------------------------------------
+inline int dtype_size(int32_t dtype) {
+    switch (dtype) {
+        case HBT_DTYPE_F32: return 4;
+        case HBT_DTYPE_BF16: return 2;
+        case HBT_DTYPE_F16: return 2;
+        case HBT_DTYPE_F64: return 8;
+        default: return 0;
+    }
+}
+
+// bf16 <-> fp32.  Widening is exact (the bf16 bits are the high half of the fp32).
+// Narrowing rounds to nearest, ties to even; any NaN becomes the quiet NaN 0x7FC0.
+__device__ __forceinline__ float bf16_to_f32(uint32_t bits16) {
+    return __uint_as_float(bits16 << 16);
+}
+
+__device__ __forceinline__ uint32_t f32_to_bf16(float x) {
+    uint32_t u = __float_as_uint(x);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0u;
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+
+// ---- fixed-order reductions ----------------------------------------------------------
+// Butterfly over the 64 lanes of a wavefront; every lane ends with the same total and
+// the pairing order is fixed, so the result is reproducible bit for bit.
+__device__ __forceinline__ double wave_sum(double x) {
+#pragma unroll
+    for (int offset = 32; offset >= 1; offset >>= 1) x += __shfl_xor(x, offset, 64);
+    return x;
+}
+
+// Sum over a block of BLOCK threads (BLOCK a multiple of 64, at most 1024).  Wave
+// totals are combined by wave 0 in wave order.  Result valid in thread 0.
+template <int BLOCK>
+__device__ __forceinline__ double block_sum(double x) {
+    constexpr int kWaves = BLOCK / 64;
+    __shared__ double wave_totals[kWaves];
+    x = wave_sum(x);
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    if (lane == 0) wave_totals[wave] = x;
+    __syncthreads();
+    double total = 0.0;
+    if (threadIdx.x == 0) {
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) total += wave_totals[w];
+    }
+    return total;
+}
+
+}  // namespace hbt

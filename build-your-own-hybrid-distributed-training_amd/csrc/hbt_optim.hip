@@ -1,0 +1,467 @@
+// Fused clip + AdamW step and the deterministic fp64 gradient norm (gfx950).
+//
+// Both kernels stream their operands exactly once from HBM with 16-byte loads and
+// stores.  Work is split into fixed-size tiles; a launch covers a table of up to
+// HBT_MAX_TENSORS_PER_LAUNCH tensors, so a list of flat shards (or of DDP-style
+// per-parameter tensors) costs one launch per 16 tensors.
+#include <cmath>
+
+#include "hbt_common.hpp"
+
+namespace hbt {
+namespace {
+
+constexpr int kMaxT = HBT_MAX_TENSORS_PER_LAUNCH;
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+#ifndef HBT_ADAMW_UNROLL
+#define HBT_ADAMW_UNROLL 2
+#endif
+#ifndef HBT_ADAMW_BLOCK
+#define HBT_ADAMW_BLOCK 256
+#endif
+#ifndef HBT_ADAMW_NONTEMPORAL
+#define HBT_ADAMW_NONTEMPORAL 0
+#endif
+#ifndef HBT_NORM_UNROLL
+#define HBT_NORM_UNROLL 4
+#endif
+#ifndef HBT_NORM_BLOCKS
+#define HBT_NORM_BLOCKS 2048
+#endif
+
+constexpr int kAdamBlock = HBT_ADAMW_BLOCK;
+constexpr int kAdamUnroll = HBT_ADAMW_UNROLL;
+constexpr int64_t kAdamTile = int64_t(kAdamBlock) * 4 * kAdamUnroll;
+
+constexpr int kNormBlock = 256;
+constexpr int kNormUnroll = HBT_NORM_UNROLL;
+constexpr int kNormBlocks = HBT_NORM_BLOCKS;
+constexpr int64_t kNormTile = int64_t(kNormBlock) * 4 * kNormUnroll;
+
+// ---- 16-byte memory helpers ------------------------------------------------------
+template <bool NT>
+__device__ __forceinline__ f32x4 ld4(const float* p) {
+    if constexpr (NT) return __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+    return *reinterpret_cast<const f32x4*>(p);
+}
+template <bool NT>
+__device__ __forceinline__ void st4(float* p, f32x4 x) {
+    if constexpr (NT) {
+        __builtin_nontemporal_store(x, reinterpret_cast<f32x4*>(p));
+    } else {
+        *reinterpret_cast<f32x4*>(p) = x;
+    }
+}
+// Four gradient values widened to fp32.
+template <typename GradT, bool NT>
+__device__ __forceinline__ f32x4 ld_grad4(const GradT* p);
+template <>
+__device__ __forceinline__ f32x4 ld_grad4<float, false>(const float* p) { return ld4<false>(p); }
+template <>
+[[maybe_unused]] __device__ __forceinline__ f32x4 ld_grad4<float, true>(const float* p) { return ld4<true>(p); }
+template <>
+__device__ __forceinline__ f32x4 ld_grad4<uint16_t, false>(const uint16_t* p) {
+    const u32x2 w = *reinterpret_cast<const u32x2*>(p);
+    return f32x4{bf16_to_f32(w.x & 0xFFFFu), bf16_to_f32(w.x >> 16), bf16_to_f32(w.y & 0xFFFFu),
+                 bf16_to_f32(w.y >> 16)};
+}
+template <>
+[[maybe_unused]] __device__ __forceinline__ f32x4 ld_grad4<uint16_t, true>(const uint16_t* p) {
+    const u32x2 w = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
+    return f32x4{bf16_to_f32(w.x & 0xFFFFu), bf16_to_f32(w.x >> 16), bf16_to_f32(w.y & 0xFFFFu),
+                 bf16_to_f32(w.y >> 16)};
+}
+__device__ __forceinline__ float ld_grad1(const float* p) { return *p; }
+__device__ __forceinline__ float ld_grad1(const uint16_t* p) { return bf16_to_f32(*p); }
+
+// ---- AdamW -----------------------------------------------------------------------
+struct AdamTable {
+    float* p[kMaxT];
+    const void* g[kMaxT];
+    float* m[kMaxT];
+    float* v[kMaxT];
+    int64_t n[kMaxT];
+    int64_t first_block[kMaxT + 1];
+    int32_t vec_ok[kMaxT];
+    int32_t count;
+};
+
+struct AdamScalars {
+    float unscale;
+    float decay;
+    float lerp_w;
+    float lerp_w_minus_1;
+    float beta2;
+    float one_minus_beta2;
+    float bc2_sqrt;
+    float eps;
+    float neg_step;
+    int32_t lerp_small;
+};
+
+// One element of torch's single-tensor AdamW, preceded by the unscale and clip
+// multiplies.  Compiled with -ffp-contract=off: only the two explicit fmaf calls fuse.
+__device__ __forceinline__ void adamw_update(float& p, float g, float& m, float& v, float gmul,
+                                             const AdamScalars& s) {
+    g = g * s.unscale;
+    g = g * gmul;
+    p = p * s.decay;
+    const float diff = g - m;
+    m = s.lerp_small ? __builtin_fmaf(s.lerp_w, diff, m) : __builtin_fmaf(s.lerp_w_minus_1, diff, g);
+    v = v * s.beta2;
+    v = __builtin_fmaf(s.one_minus_beta2 * g, g, v);
+    const float denom = __builtin_sqrtf(v) / s.bc2_sqrt + s.eps;
+    p = p + (s.neg_step * m) / denom;
+}
+
+template <typename GradT, bool NT>
+__global__ __launch_bounds__(kAdamBlock) void adamw_kernel(AdamTable tab, AdamScalars s,
+                                                           const float* __restrict__ grad_mul) {
+    const int64_t block = blockIdx.x;
+    int t = 0;
+    while (t + 1 < tab.count && block >= tab.first_block[t + 1]) ++t;
+    const int64_t base = (block - tab.first_block[t]) * kAdamTile;
+    const int64_t n = tab.n[t];
+    const float gmul = grad_mul != nullptr ? *grad_mul : 1.0f;
+    float* __restrict__ P = tab.p[t];
+    const GradT* __restrict__ G = static_cast<const GradT*>(tab.g[t]);
+    float* __restrict__ M = tab.m[t];
+    float* __restrict__ V = tab.v[t];
+
+    if (tab.vec_ok[t] && base + kAdamTile <= n) {
+        f32x4 pv[kAdamUnroll], gv[kAdamUnroll], mv[kAdamUnroll], vv[kAdamUnroll];
+#pragma unroll
+        for (int u = 0; u < kAdamUnroll; ++u) {
+            const int64_t e = base + (int64_t(u) * kAdamBlock + threadIdx.x) * 4;
+            gv[u] = ld_grad4<GradT, NT>(G + e);
+            mv[u] = ld4<NT>(M + e);
+            vv[u] = ld4<NT>(V + e);
+            pv[u] = ld4<NT>(P + e);
+        }
+#pragma unroll
+        for (int u = 0; u < kAdamUnroll; ++u) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                float p = pv[u][c], m = mv[u][c], v = vv[u][c];
+                adamw_update(p, gv[u][c], m, v, gmul, s);
+                pv[u][c] = p;
+                mv[u][c] = m;
+                vv[u][c] = v;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kAdamUnroll; ++u) {
+            const int64_t e = base + (int64_t(u) * kAdamBlock + threadIdx.x) * 4;
+            st4<NT>(M + e, mv[u]);
+            st4<NT>(V + e, vv[u]);
+            st4<NT>(P + e, pv[u]);
+        }
+    } else {
+        const int64_t end = base + kAdamTile < n ? base + kAdamTile : n;
+        for (int64_t e = base + threadIdx.x; e < end; e += kAdamBlock) {
+            float p = P[e], m = M[e], v = V[e];
+            adamw_update(p, ld_grad1(G + e), m, v, gmul, s);
+            P[e] = p;
+            M[e] = m;
+            V[e] = v;
+        }
+    }
+}
+
+// ---- squared norm ------------------------------------------------------------------
+struct NormTable {
+    const void* g[kMaxT];
+    int64_t n[kMaxT];
+    double w[kMaxT];
+    int64_t first_tile[kMaxT + 1];
+    int32_t vec_ok[kMaxT];
+    int32_t count;
+};
+
+__device__ __forceinline__ double sq(float x) {
+    const double d = static_cast<double>(x);
+    return d * d;
+}
+
+// Block b sums tiles b, b + gridDim.x, ... of the concatenated tensors.  Inside a
+// thread the tile sums are added in tile order; threads and waves are combined by
+// the fixed trees of block_sum.  The tile -> block map depends only on the numels.
+template <typename GradT>
+__global__ __launch_bounds__(kNormBlock) void sqnorm_kernel(NormTable tab, float unscale,
+                                                            double* __restrict__ partials) {
+    const int64_t total = tab.first_tile[tab.count];
+    double acc = 0.0;
+    int t = 0;
+    for (int64_t k = blockIdx.x; k < total; k += gridDim.x) {
+        while (k >= tab.first_tile[t + 1]) ++t;
+        const int64_t base = (k - tab.first_tile[t]) * kNormTile;
+        const int64_t n = tab.n[t];
+        const GradT* __restrict__ G = static_cast<const GradT*>(tab.g[t]);
+        double tile_acc = 0.0;
+        if (tab.vec_ok[t] && base + kNormTile <= n) {
+            f32x4 gv[kNormUnroll];
+#pragma unroll
+            for (int u = 0; u < kNormUnroll; ++u) {
+                gv[u] = ld_grad4<GradT, false>(G + base + (int64_t(u) * kNormBlock + threadIdx.x) * 4);
+            }
+#pragma unroll
+            for (int u = 0; u < kNormUnroll; ++u) {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) tile_acc += sq(gv[u][c] * unscale);
+            }
+        } else {
+            const int64_t end = base + kNormTile < n ? base + kNormTile : n;
+            for (int64_t e = base + threadIdx.x; e < end; e += kNormBlock) {
+                tile_acc += sq(ld_grad1(G + e) * unscale);
+            }
+        }
+        acc += tile_acc * tab.w[t];
+    }
+    const double block_total = block_sum<kNormBlock>(acc);
+    if (threadIdx.x == 0) partials[blockIdx.x] = block_total;
+}
+
+constexpr int kFinalBlock = 256;
+
+__global__ __launch_bounds__(kFinalBlock) void norm_finalize_kernel(
+    const double* __restrict__ partials, int64_t count, double max_norm, double* __restrict__ sum_out,
+    double* __restrict__ norm_out, float* __restrict__ grad_mul_out, int32_t* __restrict__ nonfinite_out) {
+    double acc = 0.0;
+    for (int64_t i = threadIdx.x; i < count; i += kFinalBlock) acc += partials[i];
+    const double total = block_sum<kFinalBlock>(acc);
+    if (threadIdx.x != 0) return;
+    // clamp_min(0) keeps NaN; sqrt of fp64 is correctly rounded.
+    const double clamped = total < 0.0 ? 0.0 : total;
+    const double norm = sqrt(clamped);
+    if (sum_out != nullptr) sum_out[0] = total;
+    if (norm_out != nullptr) norm_out[0] = norm;
+    if (grad_mul_out != nullptr) {
+        float mul = 1.0f;
+        if (max_norm > 0.0) {
+            const double coef = max_norm / (norm + 1e-6);
+            if (coef < 1.0) mul = static_cast<float>(coef);
+        }
+        grad_mul_out[0] = mul;
+    }
+    if (nonfinite_out != nullptr) nonfinite_out[0] = isfinite(total) ? 0 : 1;
+}
+
+// ---- in-place scaling ---------------------------------------------------------------
+struct ScaleTable {
+    void* x[kMaxT];
+    int64_t n[kMaxT];
+    int32_t count;
+};
+
+template <typename T>
+__device__ __forceinline__ float to_f32(T x);
+template <>
+__device__ __forceinline__ float to_f32<float>(float x) { return x; }
+template <>
+__device__ __forceinline__ float to_f32<uint16_t>(uint16_t x) { return bf16_to_f32(x); }
+template <typename T>
+__device__ __forceinline__ T from_f32(float x);
+template <>
+__device__ __forceinline__ float from_f32<float>(float x) { return x; }
+template <>
+__device__ __forceinline__ uint16_t from_f32<uint16_t>(float x) {
+    return static_cast<uint16_t>(f32_to_bf16(x));
+}
+
+// Two separate multiplies, each rounded to T, as two in-place mul_ calls would do.
+template <typename T>
+__global__ __launch_bounds__(256) void scale_kernel(ScaleTable tab, float unscale,
+                                                    const float* __restrict__ grad_mul) {
+    const float mul = grad_mul != nullptr ? *grad_mul : 1.0f;
+    for (int t = 0; t < tab.count; ++t) {
+        T* __restrict__ x = static_cast<T*>(tab.x[t]);
+        const int64_t n = tab.n[t];
+        for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += int64_t(gridDim.x) * 256) {
+            T y = from_f32<T>(to_f32<T>(x[i]) * unscale);
+            x[i] = from_f32<T>(to_f32<T>(y) * mul);
+        }
+    }
+}
+
+inline bool aligned(const void* ptr, uintptr_t bytes) {
+    return (reinterpret_cast<uintptr_t>(ptr) % bytes) == 0;
+}
+
+}  // namespace
+}  // namespace hbt
+
+using namespace hbt;
+
+extern "C" {
+
+int32_t hbt_adamw_step(float* const* params, const void* const* grads, float* const* exp_avgs,
+                       float* const* exp_avg_sqs, const int64_t* numels, int32_t count,
+                       int32_t grad_dtype, float unscale, const float* grad_mul, float decay,
+                       float lerp_weight, float beta2, float one_minus_beta2,
+                       float bias_correction2_sqrt, float eps, float neg_step_size, void* stream) {
+    clear_error();
+    if (count < 0 || count > kMaxT) {
+        set_error("hbt_adamw_step: count must lie in [0, %d], got %d", kMaxT, count);
+        return HBT_ERR_INVALID_ARGUMENT;
+    }
+    if (grad_dtype != HBT_DTYPE_F32 && grad_dtype != HBT_DTYPE_BF16) {
+        set_error("hbt_adamw_step: gradient dtype %d is not F32 or BF16", grad_dtype);
+        return HBT_ERR_INVALID_ARGUMENT;
+    }
+    if (count > 0 && (params == nullptr || grads == nullptr || exp_avgs == nullptr ||
+                      exp_avg_sqs == nullptr || numels == nullptr)) {
+        set_error("hbt_adamw_step: null table pointer");
+        return HBT_ERR_INVALID_ARGUMENT;
+    }
+    AdamTable tab{};
+    tab.count = count;
+    const uintptr_t grad_align = grad_dtype == HBT_DTYPE_F32 ? 16 : 8;
+    int64_t blocks = 0;
+    for (int i = 0; i < count; ++i) {
+        if (numels[i] < 0) {
+            set_error("hbt_adamw_step: tensor %d has negative numel %lld", i,
+                      static_cast<long long>(numels[i]));
+            return HBT_ERR_INVALID_ARGUMENT;
+        }
+        if (numels[i] > 0 && (params[i] == nullptr || grads[i] == nullptr || exp_avgs[i] == nullptr ||
+                              exp_avg_sqs[i] == nullptr)) {
+            set_error("hbt_adamw_step: tensor %d has a null data pointer", i);
+            return HBT_ERR_INVALID_ARGUMENT;
+        }
+        tab.p[i] = params[i];
+        tab.g[i] = grads[i];
+        tab.m[i] = exp_avgs[i];
+        tab.v[i] = exp_avg_sqs[i];
+        tab.n[i] = numels[i];
+        tab.vec_ok[i] = aligned(params[i], 16) && aligned(grads[i], grad_align) &&
+                        aligned(exp_avgs[i], 16) && aligned(exp_avg_sqs[i], 16);
+        tab.first_block[i] = blocks;
+        blocks += (numels[i] + kAdamTile - 1) / kAdamTile;
+    }
+    tab.first_block[count] = blocks;
+    for (int i = count + 1; i <= kMaxT; ++i) tab.first_block[i] = blocks;
+    if (blocks == 0) return HBT_OK;
+    if (blocks > 0x7FFFFFFFLL) {
+        set_error("hbt_adamw_step: %lld tiles exceed the grid limit", static_cast<long long>(blocks));
+        return HBT_ERR_UNSUPPORTED;
+    }
+    AdamScalars s{};
+    s.unscale = unscale;
+    s.decay = decay;
+    s.lerp_w = lerp_weight;
+    s.lerp_w_minus_1 = lerp_weight - 1.0f;
+    s.beta2 = beta2;
+    s.one_minus_beta2 = one_minus_beta2;
+    s.bc2_sqrt = bias_correction2_sqrt;
+    s.eps = eps;
+    s.neg_step = neg_step_size;
+    s.lerp_small = std::fabs(lerp_weight) < 0.5f ? 1 : 0;
+    const dim3 grid(static_cast<unsigned>(blocks));
+    constexpr bool kNT = HBT_ADAMW_NONTEMPORAL != 0;
+    if (grad_dtype == HBT_DTYPE_F32) {
+        adamw_kernel<float, kNT><<<grid, kAdamBlock, 0, as_stream(stream)>>>(tab, s, grad_mul);
+    } else {
+        adamw_kernel<uint16_t, kNT><<<grid, kAdamBlock, 0, as_stream(stream)>>>(tab, s, grad_mul);
+    }
+    return check_launch("hbt_adamw_step");
+}
+
+int32_t hbt_norm_partials_per_launch(void) { return kNormBlocks; }
+
+int32_t hbt_grad_sqnorm_partials(const void* const* grads, const int64_t* numels,
+                                 const double* weights, int32_t count, int32_t grad_dtype,
+                                 float unscale, double* partials, void* stream) {
+    clear_error();
+    if (count < 0 || count > kMaxT) {
+        set_error("hbt_grad_sqnorm_partials: count must lie in [0, %d], got %d", kMaxT, count);
+        return HBT_ERR_INVALID_ARGUMENT;
+    }
+    if (grad_dtype != HBT_DTYPE_F32 && grad_dtype != HBT_DTYPE_BF16) {
+        set_error("hbt_grad_sqnorm_partials: gradient dtype %d is not F32 or BF16", grad_dtype);
+        return HBT_ERR_INVALID_ARGUMENT;
+    }
+    if (partials == nullptr || (count > 0 && (grads == nullptr || numels == nullptr || weights == nullptr))) {
+        set_error("hbt_grad_sqnorm_partials: null pointer argument");
+        return HBT_ERR_INVALID_ARGUMENT;
+    }
+    NormTable tab{};
+    tab.count = count;
+    const uintptr_t grad_align = grad_dtype == HBT_DTYPE_F32 ? 16 : 8;
+    int64_t tiles = 0;
+    for (int i = 0; i < count; ++i) {
+        if (numels[i] < 0 || (numels[i] > 0 && grads[i] == nullptr)) {
+            set_error("hbt_grad_sqnorm_partials: tensor %d has a bad pointer or numel", i);
+            return HBT_ERR_INVALID_ARGUMENT;
+        }
+        tab.g[i] = grads[i];
+        tab.n[i] = numels[i];
+        tab.w[i] = weights[i];
+        tab.vec_ok[i] = aligned(grads[i], grad_align);
+        tab.first_tile[i] = tiles;
+        tiles += (numels[i] + kNormTile - 1) / kNormTile;
+    }
+    tab.first_tile[count] = tiles;
+    for (int i = count + 1; i <= kMaxT; ++i) tab.first_tile[i] = tiles;
+    if (grad_dtype == HBT_DTYPE_F32) {
+        sqnorm_kernel<float><<<kNormBlocks, kNormBlock, 0, as_stream(stream)>>>(tab, unscale, partials);
+    } else {
+        sqnorm_kernel<uint16_t><<<kNormBlocks, kNormBlock, 0, as_stream(stream)>>>(tab, unscale, partials);
+    }
+    return check_launch("hbt_grad_sqnorm_partials");
+}
+
+int32_t hbt_grad_norm_finalize(const double* partials, int64_t count, double max_norm,
+                               double* sum_out, double* norm_out, float* grad_mul_out,
+                               int32_t* nonfinite_out, void* stream) {
+    clear_error();
+    if (count < 0 || (count > 0 && partials == nullptr)) {
+        set_error("hbt_grad_norm_finalize: bad partials/count");
+        return HBT_ERR_INVALID_ARGUMENT;
+    }
+    norm_finalize_kernel<<<1, kFinalBlock, 0, as_stream(stream)>>>(partials, count, max_norm, sum_out,
+                                                                   norm_out, grad_mul_out, nonfinite_out);
+    return check_launch("hbt_grad_norm_finalize");
+}
+
+int32_t hbt_scale_inplace(void* const* tensors, const int64_t* numels, int32_t count,
+                          int32_t dtype, float unscale, const float* grad_mul, void* stream) {
+    clear_error();
+    if (count < 0 || count > kMaxT || (count > 0 && (tensors == nullptr || numels == nullptr))) {
+        set_error("hbt_scale_inplace: bad table (count=%d)", count);
+        return HBT_ERR_INVALID_ARGUMENT;
+    }
+    if (dtype != HBT_DTYPE_F32 && dtype != HBT_DTYPE_BF16) {
+        set_error("hbt_scale_inplace: dtype %d is not F32 or BF16", dtype);
+        return HBT_ERR_INVALID_ARGUMENT;
+    }
+    ScaleTable tab{};
+    tab.count = count;
+    int64_t largest = 0;
+    for (int i = 0; i < count; ++i) {
+        if (numels[i] < 0 || (numels[i] > 0 && tensors[i] == nullptr)) {
+            set_error("hbt_scale_inplace: tensor %d has a bad pointer or numel", i);
+            return HBT_ERR_INVALID_ARGUMENT;
+        }
+        tab.x[i] = tensors[i];
+        tab.n[i] = numels[i];
+        if (numels[i] > largest) largest = numels[i];
+    }
+    if (largest == 0) return HBT_OK;
+    int64_t blocks = (largest + 255) / 256;
+    const int64_t cap = int64_t(device_cu_count()) * 16;
+    if (blocks > cap) blocks = cap;
+    if (dtype == HBT_DTYPE_F32) {
+        scale_kernel<float><<<dim3(static_cast<unsigned>(blocks)), 256, 0, as_stream(stream)>>>(
+            tab, unscale, grad_mul);
+    } else {
+        scale_kernel<uint16_t><<<dim3(static_cast<unsigned>(blocks)), 256, 0, as_stream(stream)>>>(
+            tab, unscale, grad_mul);
+    }
+    return check_launch("hbt_scale_inplace");
+}
+
+}  // extern "C"
+

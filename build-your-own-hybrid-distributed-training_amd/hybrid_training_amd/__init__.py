@@ -1,0 +1,51 @@
+"""MI355X-native data-parallel hot path of hybrid distributed training.
+
+Drop-in replacements for the reference's flat-parameter, gradient-bucket,
+sharded-optimizer, loss-scaler and checkpoint-interval objects, whose tensor work
+runs in hand-written gfx950 HIP kernels reached through ``libhbt.so``'s C ABI
+(``include/hbt.h``).  Importing the package does not load the library; the first
+call that moves data does, and raises if it is missing.
+"""
+
+from __future__ import annotations
+
+from .config import (
+    DDPConfig,
+    FSDPConfig,
+    GradScalerConfig,
+    MixedPrecisionConfig,
+    OptimizerConfig,
+    resolve_dtype,
+)
+from .errors import (
+    CheckpointCorruptionError,
+    CheckpointError,
+    HybridTrainingError,
+    IncompleteCheckpointError,
+    NativeKernelError,
+    ShardingError,
+    UnsupportedFeatureError,
+    format_error,
+)
+from .groups import GroupHandle
+from .optim import (
+    NormContribution,
+    ShardedOptimizer,
+    build_gradient_norm_contributions,
+    build_inner_optimizer,
+    distributed_gradient_norm,
+)
+from .tensors import (
+    FlatEntry,
+    ShardRange,
+    build_flat_layout,
+    concat_shard_sizes,
+    even_shard_ranges,
+    flatten_dense_tensors,
+    intersect_ranges,
+    pad_flat_tensor,
+    shard_range_for,
+    unflatten_to_views,
+)
+
+__version__ = "0.1.0"

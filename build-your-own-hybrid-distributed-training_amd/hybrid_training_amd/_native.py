@@ -1,0 +1,340 @@
+"""ctypes binding of ``libhbt.so`` and the host-side plumbing around it.
+
+This is the only module that touches the C ABI declared in ``include/hbt.h``.  It
+loads the library that sits next to this file, checks its ABI version, declares
+every entry point's signature, turns non-zero status codes into
+:class:`~hybrid_training_amd.errors.NativeKernelError`, and builds the interval
+tables the gather-copy kernel consumes.
+
+There is no fallback: when the library is missing, or a tensor is not on a HIP
+device, the call raises.  Pointers come from ``Tensor.data_ptr()`` and the stream
+from torch's current stream on the tensor's device, so every kernel is ordered
+with the caller's other work on that stream.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from collections.abc import Sequence
+
+import torch
+
+from .errors import NativeKernelError, UnsupportedFeatureError, format_error
+
+__all__ = [
+    "ABI_VERSION",
+    "COPY_OP_COPY",
+    "COPY_OP_DIVIDE",
+    "CopyPlan",
+    "DTYPE_BF16",
+    "DTYPE_F16",
+    "DTYPE_F32",
+    "DTYPE_F64",
+    "EXPORTED_SYMBOLS",
+    "MAX_LOCAL_RANKS",
+    "MAX_TENSORS_PER_LAUNCH",
+    "check",
+    "contiguous_source",
+    "dtype_code",
+    "library",
+    "library_path",
+    "require_device_tensor",
+    "stream_of",
+]
+
+ABI_VERSION = 1
+MAX_TENSORS_PER_LAUNCH = 16
+MAX_LOCAL_RANKS = 64
+
+DTYPE_F32 = 0
+DTYPE_BF16 = 1
+DTYPE_F16 = 2
+DTYPE_F64 = 3
+
+COPY_OP_COPY = 0
+COPY_OP_DIVIDE = 1
+
+_c_void_p = ctypes.c_void_p
+_c_i32 = ctypes.c_int32
+_c_i64 = ctypes.c_int64
+_c_f32 = ctypes.c_float
+_c_f64 = ctypes.c_double
+_ptr_array = ctypes.POINTER(ctypes.c_void_p)
+_i64_array = ctypes.POINTER(ctypes.c_int64)
+_f64_array = ctypes.POINTER(ctypes.c_double)
+
+#: Every entry point of include/hbt.h with its (restype, argtypes).
+EXPORTED_SYMBOLS: dict[str, tuple[object, tuple[object, ...]]] = {
+    "hbt_last_error": (ctypes.c_char_p, ()),
+    "hbt_abi_version": (_c_i32, ()),
+    "hbt_symbol_count": (_c_i32, ()),
+    "hbt_adamw_step": (
+        _c_i32,
+        (
+            _ptr_array, _ptr_array, _ptr_array, _ptr_array, _i64_array, _c_i32, _c_i32,
+            _c_f32, _c_void_p, _c_f32, _c_f32, _c_f32, _c_f32, _c_f32, _c_f32, _c_f32,
+            _c_void_p,
+        ),
+    ),
+    "hbt_norm_partials_per_launch": (_c_i32, ()),
+    "hbt_grad_sqnorm_partials": (
+        _c_i32,
+        (_ptr_array, _i64_array, _f64_array, _c_i32, _c_i32, _c_f32, _c_void_p, _c_void_p),
+    ),
+    "hbt_grad_norm_finalize": (
+        _c_i32,
+        (_c_void_p, _c_i64, _c_f64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p),
+    ),
+    "hbt_copy_chunk_elems": (_c_i64, ()),
+    "hbt_copy_intervals": (
+        _c_i32,
+        (_c_void_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_f32, _c_void_p),
+    ),
+    "hbt_grad_local_share": (
+        _c_i32,
+        (_ptr_array, _c_i32, _c_i32, _c_i64, _c_i64, _c_i32, _c_f32, _c_void_p, _c_void_p),
+    ),
+    "hbt_scale_inplace": (
+        _c_i32,
+        (_ptr_array, _i64_array, _c_i32, _c_i32, _c_f32, _c_void_p, _c_void_p),
+    ),
+}
+
+_LOCK = threading.Lock()
+_LIB: ctypes.CDLL | None = None
+
+
+def library_path() -> str:
+    """Absolute path of ``libhbt.so`` inside this package."""
+    return os.path.join(os.path.dirname(os.path.abspath(__file__)), "libhbt.so")
+
+
+def library() -> ctypes.CDLL:
+    """Load (once) and return ``libhbt.so`` with every signature declared.
+
+    Raises:
+        NativeKernelError: if the file is absent, fails to load, exports the wrong
+            symbol set, or reports a different ABI version.
+    """
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    with _LOCK:
+        if _LIB is not None:
+            return _LIB
+        path = library_path()
+        if not os.path.exists(path):
+            raise NativeKernelError(
+                format_error(
+                    "native.library",
+                    "libhbt.so has not been built; there is no non-native fallback",
+                    expected=path,
+                    observed="missing",
+                    resolution="run __graft_entry__.build() or `make -C <package>/csrc`",
+                )
+            )
+        try:
+            lib = ctypes.CDLL(path)
+        except OSError as exc:
+            raise NativeKernelError(
+                format_error("native.library", f"cannot load libhbt.so: {exc}", observed=path)
+            ) from exc
+        for name, (restype, argtypes) in EXPORTED_SYMBOLS.items():
+            try:
+                fn = getattr(lib, name)
+            except AttributeError as exc:
+                raise NativeKernelError(
+                    format_error("native.library", "missing entry point", expected=name, observed=path)
+                ) from exc
+            fn.restype = restype
+            fn.argtypes = list(argtypes)
+        version = lib.hbt_abi_version()
+        if version != ABI_VERSION:
+            raise NativeKernelError(
+                format_error(
+                    "native.library",
+                    "libhbt.so was built from a different ABI",
+                    expected=ABI_VERSION,
+                    observed=version,
+                    resolution="rebuild the library",
+                )
+            )
+        if lib.hbt_symbol_count() != len(EXPORTED_SYMBOLS):
+            raise NativeKernelError(
+                format_error(
+                    "native.library",
+                    "the library and the binding disagree on the entry-point count",
+                    expected=len(EXPORTED_SYMBOLS),
+                    observed=lib.hbt_symbol_count(),
+                    resolution="rebuild the library",
+                )
+            )
+        _LIB = lib
+        return lib
+
+
+def check(status: int, operation: str) -> None:
+    """Raise :class:`NativeKernelError` for a non-zero status from ``libhbt.so``."""
+    if status != 0:
+        message = library().hbt_last_error() or b""
+        raise NativeKernelError(
+            format_error(operation, message.decode(errors="replace") or "native call failed",
+                         observed=f"status {status}")
+        )
+
+
+_DTYPE_CODES = {
+    torch.float32: DTYPE_F32,
+    torch.bfloat16: DTYPE_BF16,
+    torch.float16: DTYPE_F16,
+    torch.float64: DTYPE_F64,
+}
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    """ABI code of a floating dtype."""
+    try:
+        return _DTYPE_CODES[dtype]
+    except KeyError as exc:
+        raise UnsupportedFeatureError(
+            format_error(
+                "native.dtype_code",
+                "dtype not handled by the HIP kernels",
+                expected=sorted(str(d) for d in _DTYPE_CODES),
+                observed=str(dtype),
+            )
+        ) from exc
+
+
+def require_device_tensor(tensor: torch.Tensor, operation: str) -> None:
+    """Refuse host tensors: every data path here runs on the HIP device."""
+    if tensor.device.type != "cuda":
+        raise UnsupportedFeatureError(
+            format_error(
+                operation,
+                "this build runs the hot path only as HIP kernels, so tensors must live "
+                "on a HIP device",
+                expected="device type 'cuda' (HIP)",
+                observed=str(tensor.device),
+                resolution="move the tensors to the GPU first",
+            )
+        )
+
+
+def stream_of(device: torch.device) -> int:
+    """Raw ``hipStream_t`` of torch's current stream on ``device``."""
+    return int(torch.cuda.current_stream(device).cuda_stream)
+
+
+def contiguous_source(tensor: torch.Tensor) -> torch.Tensor:
+    """``tensor`` when it is dense, else a dense copy (the reference's ``reshape(-1)``)."""
+    return tensor if tensor.is_contiguous() else tensor.contiguous()
+
+
+def pointer_array(values: Sequence[int]) -> ctypes.Array:
+    """ctypes ``void*[]`` holding device addresses."""
+    return (ctypes.c_void_p * max(1, len(values)))(*values)
+
+
+def int64_array(values: Sequence[int]) -> ctypes.Array:
+    """ctypes ``int64_t[]``."""
+    return (ctypes.c_int64 * max(1, len(values)))(*values)
+
+
+def double_array(values: Sequence[float]) -> ctypes.Array:
+    """ctypes ``double[]``."""
+    return (ctypes.c_double * max(1, len(values)))(*values)
+
+
+class CopyPlan:
+    """Interval table for one ``hbt_copy_intervals`` launch.
+
+    Each :meth:`add` appends ``n`` elements from ``src[src_offset:]`` to
+    ``dst[dst_offset:]`` (offsets in elements of each tensor's own dtype, counted
+    from the tensor's first element); :meth:`add_zero` appends a zero fill.  All
+    records of one plan share a source dtype, a destination dtype and an op.  Ranges
+    must not overlap between records.
+    """
+
+    def __init__(self, device: torch.device) -> None:
+        self.device = torch.device(device)
+        self._rows: list[tuple[int, int, int]] = []
+
+    def __len__(self) -> int:
+        return len(self._rows)
+
+    def add(self, src: torch.Tensor, src_offset: int, dst: torch.Tensor, dst_offset: int, n: int) -> None:
+        """Queue ``dst[dst_offset : dst_offset + n] = src[src_offset : src_offset + n]``."""
+        require_device_tensor(src, "native.CopyPlan")
+        require_device_tensor(dst, "native.CopyPlan")
+        if n < 0 or src_offset < 0 or dst_offset < 0:
+            raise ValueError("negative copy extent")
+        if src_offset + n > src.numel() or dst_offset + n > dst.numel():
+            raise ValueError(
+                f"copy of {n} elements runs past a tensor end "
+                f"(src {src_offset}+{n}>{src.numel()} or dst {dst_offset}+{n}>{dst.numel()})"
+            )
+        if not (src.is_contiguous() and dst.is_contiguous()):
+            raise ValueError("copy plans address dense tensors only")
+        if n == 0:
+            return
+        self._rows.append(
+            (
+                src.data_ptr() + src_offset * src.element_size(),
+                dst.data_ptr() + dst_offset * dst.element_size(),
+                n,
+            )
+        )
+
+    def add_zero(self, dst: torch.Tensor, dst_offset: int, n: int) -> None:
+        """Queue ``dst[dst_offset : dst_offset + n] = 0``."""
+        require_device_tensor(dst, "native.CopyPlan")
+        if n < 0 or dst_offset < 0 or dst_offset + n > dst.numel():
+            raise ValueError("zero fill runs past the tensor end")
+        if not dst.is_contiguous():
+            raise ValueError("copy plans address dense tensors only")
+        if n == 0:
+            return
+        self._rows.append((0, dst.data_ptr() + dst_offset * dst.element_size(), n))
+
+    def run(
+        self,
+        *,
+        src_dtype: torch.dtype,
+        dst_dtype: torch.dtype,
+        op: int = COPY_OP_COPY,
+        divisor: float = 1.0,
+    ) -> None:
+        """Launch the copy on the current stream of the plan's device."""
+        if not self._rows:
+            return
+        src_code = dtype_code(src_dtype)
+        dst_code = dtype_code(dst_dtype)
+        scale = 1
+        if src_dtype == dst_dtype and op == COPY_OP_COPY and src_code == DTYPE_F64:
+            # An 8-byte element moves as two dwords.
+            src_code = dst_code = DTYPE_F32
+            scale = 2
+        lib = library()
+        chunk = int(lib.hbt_copy_chunk_elems())
+        flat: list[int] = []
+        first = 0
+        for src_addr, dst_addr, n in self._rows:
+            n_units = n * scale
+            flat.extend((src_addr, dst_addr, n_units, first))
+            first += -(-n_units // chunk)
+        table = torch.tensor(flat, dtype=torch.int64).to(self.device)
+        with torch.cuda.device(self.device):
+            status = lib.hbt_copy_intervals(
+                table.data_ptr(),
+                len(self._rows),
+                first,
+                src_code,
+                dst_code,
+                op,
+                float(divisor),
+                stream_of(self.device),
+            )
+        check(status, "native.hbt_copy_intervals")

@@ -1,0 +1,693 @@
+"""Sharded AdamW step and the deterministic global gradient-norm clip on HIP.
+
+Drop-in for ``optim/sharded_optimizer.py`` of the reference.  The public names,
+constructor arguments, return types, error classes and the state-dict format are
+the reference's; what changes is where the arithmetic runs:
+
+* the weighted fp64 squared norm is one pass of ``hbt_grad_sqnorm_partials``
+  (fixed tile-to-block map, fixed reduction trees, so it is bitwise reproducible)
+  followed by ``hbt_grad_norm_finalize``, which also derives the clip multiplier
+  on the device, so no host round trip sits between the norm and the update;
+* the update is ``hbt_adamw_step``, one pass that reads ``p, g, m, v`` once and
+  writes ``p, m, v`` once, with torch's per-element arithmetic
+  (``torch/optim/adam.py:396-547``) reproduced exactly (see ``include/hbt.h``).
+
+The inner ``torch.optim.AdamW`` object is still built (``build_inner_optimizer``)
+and owns ``param_groups`` and ``state``, so ``state_dict``/``load_state_dict``,
+``inner`` and learning-rate changes behave as in the reference; only its
+``step`` is never called.
+
+Clip placement.  ``clip_grad_norm`` scales the gradients in place, exactly as the
+reference does, at the cost of one extra read and write of every gradient.  With
+``defer_clip=True`` the multiplier stays on the device and ``step()`` applies it
+inside the fused update instead; ``clip_and_step`` does the same in one call.
+The result is bitwise the same as clip-then-step, but ``.grad`` holds the
+unclipped values until ``step()`` runs.
+"""
+
+from __future__ import annotations
+
+from collections.abc import Iterable, Sequence
+from dataclasses import dataclass, field
+from typing import Any
+
+import torch
+import torch.nn as nn
+from torch.autograd.graph import increment_version
+
+from . import _native
+from .config import OptimizerConfig
+from .errors import ShardingError, UnsupportedFeatureError, format_error
+from .groups import GroupHandle
+
+__all__ = [
+    "NormContribution",
+    "ShardedOptimizer",
+    "build_gradient_norm_contributions",
+    "build_inner_optimizer",
+    "distributed_gradient_norm",
+    "gradient_norm_pass",
+]
+
+#: Attribute a deferred loss-scale factor travels under on a gradient tensor.
+PENDING_UNSCALE_ATTR = "_hbt_pending_unscale"
+
+
+def build_inner_optimizer(
+    parameters: Iterable[nn.Parameter], config: OptimizerConfig
+) -> torch.optim.Optimizer:
+    """The torch optimizer object holding param groups and state (``sharded_optimizer.py:84-126``)."""
+    params = [p for p in parameters if p.requires_grad]
+    if not params:
+        raise ShardingError(
+            format_error(
+                "optim.build_inner_optimizer",
+                "no trainable parameters were supplied",
+                expected=">= 1 parameter with requires_grad=True",
+                observed=0,
+                resolution="check that the model was wrapped before the optimizer was built",
+            )
+        )
+    if config.name == "adamw":
+        return torch.optim.AdamW(
+            params,
+            lr=config.learning_rate,
+            betas=(float(config.betas[0]), float(config.betas[1])),
+            eps=config.eps,
+            weight_decay=config.weight_decay,
+        )
+    return torch.optim.SGD(
+        params, lr=config.learning_rate, momentum=config.momentum, weight_decay=config.weight_decay
+    )
+
+
+# ---------------------------------------------------------------------------------------
+# gradient norm
+# ---------------------------------------------------------------------------------------
+def _weight_runs(scale: torch.Tensor) -> list[tuple[int, int, float]]:
+    """Run-length form ``(offset, length, weight)`` of a per-element fp64 weight vector."""
+    weights = scale.detach().to(device="cpu", dtype=torch.float64).reshape(-1)
+    n = int(weights.numel())
+    if n == 0:
+        return []
+    change = torch.nonzero(weights[1:] != weights[:-1]).reshape(-1).tolist()
+    starts = [0] + [c + 1 for c in change]
+    ends = starts[1:] + [n]
+    values = weights[starts].tolist()
+    return [(s, e - s, float(w)) for s, e, w in zip(starts, ends, values)]
+
+
+@dataclass
+class NormContribution:
+    """One parameter's share of the global squared gradient norm.
+
+    ``scale`` is a scalar weight or a per-element weight vector
+    (``sharded_optimizer.py:129-158``).  A vector is piecewise constant over the
+    flat layout, so it is kept as runs and each run becomes one weighted segment
+    of the device reduction.
+    """
+
+    parameter: nn.Parameter
+    scale: float | torch.Tensor
+    label: str
+    runs: list[tuple[int, int, float]] = field(default_factory=list, repr=False)
+
+    def __post_init__(self) -> None:
+        if isinstance(self.scale, torch.Tensor) and not self.runs:
+            self.runs = _weight_runs(self.scale)
+
+    def segments(self) -> list[tuple[torch.Tensor, int, int, float]]:
+        """``(grad, offset, length, weight)`` pieces of this contribution, or ``[]``."""
+        grad = self.parameter.grad
+        if grad is None:
+            return []
+        if isinstance(self.scale, torch.Tensor):
+            if sum(length for _, length, _ in self.runs) != grad.numel():
+                raise ShardingError(
+                    format_error(
+                        "optim.NormContribution",
+                        "the per-element norm weights do not match the gradient length",
+                        expected=grad.numel(),
+                        observed=sum(length for _, length, _ in self.runs),
+                        resolution="rebuild the contributions after re-sharding",
+                    )
+                )
+            return [(grad, offset, length, weight) for offset, length, weight in self.runs]
+        return [(grad, 0, int(grad.numel()), float(self.scale))]
+
+    def squared_norm(self) -> torch.Tensor:
+        """This contribution's weighted squared norm as a 0-dim fp64 device tensor."""
+        grad = self.parameter.grad
+        if grad is None:
+            return torch.zeros((), dtype=torch.float64, device=self.parameter.device)
+        result = gradient_norm_pass(self.segments(), grad.device, max_norm=0.0)
+        return result.sum
+
+
+def build_gradient_norm_contributions(
+    parameters: Sequence[nn.Parameter], *, world_size: int
+) -> list[NormContribution]:
+    """Per-parameter norm weights (``sharded_optimizer.py:161-212``).
+
+    A parameter carrying ``gradient_norm_scale_vector`` (an FSDP flat shard) gets
+    that vector, in fp64, divided by ``world_size``; any other parameter gets
+    ``partitioned / world_size`` with ``partitioned`` its tensor-parallel width when
+    it is not replicated, else 1.
+    """
+    if world_size < 1:
+        raise ShardingError(
+            format_error(
+                "optim.build_gradient_norm_contributions",
+                "world_size must be positive",
+                expected=">= 1",
+                observed=world_size,
+                resolution="pass the size of the reduction group",
+            )
+        )
+    contributions: list[NormContribution] = []
+    for index, param in enumerate(parameters):
+        vector = getattr(param, "gradient_norm_scale_vector", None)
+        if vector is not None:
+            contributions.append(
+                NormContribution(
+                    parameter=param,
+                    scale=vector.to(torch.float64) / world_size,
+                    label=getattr(param, "gradient_norm_label", f"flat_param#{index}"),
+                )
+            )
+            continue
+        partitioned = 1
+        if not getattr(param, "is_tensor_parallel_replicated", True):
+            partitioned = int(getattr(param, "tensor_parallel_group_size", 1))
+        contributions.append(
+            NormContribution(parameter=param, scale=partitioned / world_size, label=f"param#{index}")
+        )
+    return contributions
+
+
+@dataclass
+class NormResult:
+    """Device outputs of one norm pass (all 0-dim or 1-element device tensors)."""
+
+    sum: torch.Tensor
+    norm: torch.Tensor
+    grad_mul: torch.Tensor
+    nonfinite: torch.Tensor
+
+
+def _pending_unscale(grad: torch.Tensor) -> float:
+    return float(getattr(grad, PENDING_UNSCALE_ATTR, 1.0))
+
+
+def gradient_norm_pass(
+    segments: Sequence[tuple[torch.Tensor, int, int, float]],
+    device: torch.device,
+    *,
+    max_norm: float,
+) -> NormResult:
+    """Weighted fp64 squared norm of gradient segments, plus the clip multiplier.
+
+    ``segments`` are ``(grad, offset, length, weight)``; a grad tagged with a
+    pending loss-scale factor is read through that factor.  Segments are batched
+    by (dtype, factor) into launches of at most 16; every launch writes its own
+    block of partials and one finalize launch sums all of them in a fixed order.
+    """
+    lib = _native.library()
+    per_launch = int(lib.hbt_norm_partials_per_launch())
+    batches: dict[tuple[torch.dtype, float], list[tuple[torch.Tensor, int, int, float]]] = {}
+    for grad, offset, length, weight in segments:
+        _native.require_device_tensor(grad, "optim.gradient_norm")
+        if grad.dtype not in (torch.float32, torch.bfloat16):
+            raise UnsupportedFeatureError(
+                format_error(
+                    "optim.gradient_norm",
+                    "gradients must be float32 or bfloat16",
+                    observed=str(grad.dtype),
+                )
+            )
+        if not grad.is_contiguous():
+            raise ShardingError(
+                format_error("optim.gradient_norm", "gradients must be dense", observed=tuple(grad.stride()))
+            )
+        if length > 0:
+            batches.setdefault((grad.dtype, _pending_unscale(grad)), []).append(
+                (grad, offset, length, weight)
+            )
+    launches: list[tuple[torch.dtype, float, list[tuple[torch.Tensor, int, int, float]]]] = []
+    for (dtype, unscale), items in batches.items():
+        for start in range(0, len(items), _native.MAX_TENSORS_PER_LAUNCH):
+            launches.append((dtype, unscale, items[start : start + _native.MAX_TENSORS_PER_LAUNCH]))
+    partials = torch.empty(max(1, len(launches)) * per_launch, dtype=torch.float64, device=device)
+    outputs = torch.empty(2, dtype=torch.float64, device=device)
+    grad_mul = torch.empty(1, dtype=torch.float32, device=device)
+    nonfinite = torch.empty(1, dtype=torch.int32, device=device)
+    stream = _native.stream_of(device)
+    with torch.cuda.device(device):
+        for index, (dtype, unscale, items) in enumerate(launches):
+            ptrs = [g.data_ptr() + off * g.element_size() for g, off, _, _ in items]
+            status = lib.hbt_grad_sqnorm_partials(
+                _native.pointer_array(ptrs),
+                _native.int64_array([n for _, _, n, _ in items]),
+                _native.double_array([w for _, _, _, w in items]),
+                len(items),
+                _native.dtype_code(dtype),
+                unscale,
+                partials.data_ptr() + index * per_launch * 8,
+                stream,
+            )
+            _native.check(status, "optim.hbt_grad_sqnorm_partials")
+        count = len(launches) * per_launch
+        status = lib.hbt_grad_norm_finalize(
+            partials.data_ptr(),
+            count,
+            float(max_norm),
+            outputs.data_ptr(),
+            outputs.data_ptr() + 8,
+            grad_mul.data_ptr(),
+            nonfinite.data_ptr(),
+            stream,
+        )
+        _native.check(status, "optim.hbt_grad_norm_finalize")
+    return NormResult(sum=outputs[0], norm=outputs[1], grad_mul=grad_mul, nonfinite=nonfinite)
+
+
+def _check_group(group: GroupHandle, operation: str) -> None:
+    if group.size > 1 and group.process_group is not None:
+        raise UnsupportedFeatureError(
+            format_error(
+                operation,
+                "this build computes one rank's share on one device and issues no collectives",
+                expected="a trivial group or GroupHandle.local_view(...)",
+                observed=repr(group),
+                resolution="reduce the fp64 partial sum across ranks outside this library",
+            )
+        )
+
+
+def distributed_gradient_norm(
+    contributions: Sequence[NormContribution],
+    group: GroupHandle,
+    *,
+    device: torch.device,
+    recorder: Any = None,
+) -> torch.Tensor:
+    """Global L2 norm as a 0-dim fp64 device tensor (``sharded_optimizer.py:215-241``).
+
+    Over a trivial group this is the whole norm.  Over a
+    :meth:`GroupHandle.local_view` group it is this rank's share before the
+    one-scalar fp64 SUM all-reduce, which this build does not issue.
+    """
+    _check_group(group, "optim.distributed_gradient_norm")
+    segments = [s for c in contributions for s in c.segments()]
+    return gradient_norm_pass(segments, torch.device(device), max_norm=0.0).norm
+
+
+# ---------------------------------------------------------------------------------------
+# optimizer
+# ---------------------------------------------------------------------------------------
+def _grad_signature(params: Sequence[nn.Parameter]) -> tuple[tuple[int, int, int], ...]:
+    """Identity, address and version of every gradient: detects any change to them."""
+    sig = []
+    for p in params:
+        g = p.grad
+        sig.append((0, 0, 0) if g is None else (id(g), g.data_ptr(), g._version))
+    return tuple(sig)
+
+
+class ShardedOptimizer:
+    """AdamW over this rank's shards with a global-norm clip, on HIP kernels.
+
+    Same constructor, methods and properties as ``sharded_optimizer.py:244-499``.
+    ``defer_clip`` is the one addition (see the module docstring).  The CPU-offload
+    branch and the SGD inner optimizer are not implemented and raise
+    :class:`UnsupportedFeatureError` rather than falling back to torch.
+    """
+
+    def __init__(
+        self,
+        parameters: Iterable[nn.Parameter],
+        config: OptimizerConfig,
+        *,
+        norm_group: GroupHandle,
+        device: torch.device,
+        recorder: Any = None,
+        defer_clip: bool = False,
+    ) -> None:
+        self._parameters = [p for p in parameters if p.requires_grad]
+        self._config = config
+        self._norm_group = norm_group
+        self._device = torch.device(device)
+        self._recorder = recorder
+        self._defer_clip = defer_clip
+        if config.cpu_offload_state:
+            raise UnsupportedFeatureError(
+                format_error(
+                    "optim.ShardedOptimizer",
+                    "optimizer-state CPU offload is not part of this build",
+                    expected="cpu_offload_state=False",
+                    observed=True,
+                    resolution="keep the optimizer state in HBM (288 GB per device)",
+                )
+            )
+        if config.name != "adamw":
+            raise UnsupportedFeatureError(
+                format_error(
+                    "optim.ShardedOptimizer",
+                    "only the AdamW inner optimizer has a HIP kernel in this build",
+                    expected="adamw",
+                    observed=config.name,
+                )
+            )
+        _check_group(norm_group, "optim.ShardedOptimizer")
+        self._optimizer = build_inner_optimizer(self._parameters, config)
+        for param in self._parameters:
+            _native.require_device_tensor(param, "optim.ShardedOptimizer")
+            if param.dtype != torch.float32:
+                raise UnsupportedFeatureError(
+                    format_error(
+                        "optim.ShardedOptimizer",
+                        "master parameters must be float32",
+                        observed=str(param.dtype),
+                    )
+                )
+        self._contributions = build_gradient_norm_contributions(
+            self._parameters, world_size=norm_group.size
+        )
+        self._offload = False
+        self._pending_mul: torch.Tensor | None = None
+        self._pending_signature: tuple[tuple[int, int, int], ...] | None = None
+        self._last_check: tuple[tuple[tuple[int, int, int], ...], torch.Tensor] | None = None
+
+    # -- norm and clip ---------------------------------------------------------------
+    def _norm(self, max_norm: float) -> NormResult:
+        segments = [s for c in self._contributions for s in c.segments()]
+        result = gradient_norm_pass(segments, self._device, max_norm=max_norm)
+        self._last_check = (_grad_signature(self._parameters), result.nonfinite)
+        return result
+
+    def _scale_grads(self, grad_mul: torch.Tensor | None, unscale_attr: bool) -> None:
+        """Apply pending multipliers to the gradients in place (materialisation)."""
+        lib = _native.library()
+        groups: dict[tuple[torch.dtype, float], list[torch.Tensor]] = {}
+        for p in self._parameters:
+            g = p.grad
+            if g is None:
+                continue
+            unscale = _pending_unscale(g) if unscale_attr else 1.0
+            groups.setdefault((g.dtype, unscale), []).append(g)
+        with torch.cuda.device(self._device):
+            for (dtype, unscale), grads in groups.items():
+                for start in range(0, len(grads), _native.MAX_TENSORS_PER_LAUNCH):
+                    chunk = grads[start : start + _native.MAX_TENSORS_PER_LAUNCH]
+                    status = lib.hbt_scale_inplace(
+                        _native.pointer_array([g.data_ptr() for g in chunk]),
+                        _native.int64_array([g.numel() for g in chunk]),
+                        len(chunk),
+                        _native.dtype_code(dtype),
+                        unscale,
+                        None if grad_mul is None else grad_mul.data_ptr(),
+                        _native.stream_of(self._device),
+                    )
+                    _native.check(status, "optim.hbt_scale_inplace")
+                    increment_version(chunk)
+        if unscale_attr:
+            for p in self._parameters:
+                if p.grad is not None and hasattr(p.grad, PENDING_UNSCALE_ATTR):
+                    delattr(p.grad, PENDING_UNSCALE_ATTR)
+
+    def materialize_pending(self) -> None:
+        """Apply any deferred loss-scale and clip factors to ``.grad`` in place."""
+        has_unscale = any(
+            p.grad is not None and hasattr(p.grad, PENDING_UNSCALE_ATTR) for p in self._parameters
+        )
+        mul = self._pending_mul if self._pending_valid() else None
+        if has_unscale or mul is not None:
+            self._scale_grads(mul, unscale_attr=has_unscale)
+        self._pending_mul = None
+        self._pending_signature = None
+
+    def _pending_valid(self) -> bool:
+        if self._pending_mul is None:
+            return False
+        if self._pending_signature != _grad_signature(self._parameters):
+            raise ShardingError(
+                format_error(
+                    "optim.ShardedOptimizer",
+                    "gradients changed between a deferred clip and the step, so the clip "
+                    "can no longer be applied where the reference would have applied it",
+                    resolution="construct the optimizer with defer_clip=False when gradients "
+                    "are modified after clip_grad_norm()",
+                )
+            )
+        return True
+
+    def clip_grad_norm(self, max_norm: float) -> torch.Tensor:
+        """Clip to a global L2 norm; return the pre-clip norm (0-dim fp64 device tensor).
+
+        ``max_norm <= 0`` only computes the norm (``sharded_optimizer.py:310-338``).
+        """
+        if self._pending_mul is not None:
+            self.materialize_pending()
+        result = self._norm(max_norm)
+        if max_norm <= 0:
+            return result.norm
+        if self._defer_clip:
+            self._pending_mul = result.grad_mul
+            self._pending_signature = _grad_signature(self._parameters)
+        else:
+            self._scale_grads(result.grad_mul, unscale_attr=True)
+            self._last_check = (_grad_signature(self._parameters), result.nonfinite)
+        return result.norm
+
+    def clip_and_step(self, max_norm: float) -> torch.Tensor:
+        """Norm pass, then one fused clip + AdamW pass; returns the pre-clip norm.
+
+        Bitwise equal to ``clip_grad_norm(max_norm); step()``; ``.grad`` is left
+        unclipped.  Two kernels read the gradients: the norm (4 B/element) and the
+        update (28 B/element of p, g, m, v traffic).
+        """
+        if self._pending_mul is not None:
+            self.materialize_pending()
+        result = self._norm(max_norm)
+        self._run_step(result.grad_mul if max_norm > 0 else None)
+        return result.norm
+
+    def last_nonfinite_flag(self) -> torch.Tensor | None:
+        """Device flag from the latest norm pass, if the gradients have not changed since."""
+        if self._last_check is None:
+            return None
+        signature, flag = self._last_check
+        return flag if signature == _grad_signature(self._parameters) else None
+
+    # -- update ----------------------------------------------------------------------
+    def step(self) -> None:
+        """One AdamW step over this rank's shards (``sharded_optimizer.py:340-355``)."""
+        mul = self._pending_mul if self._pending_valid() else None
+        self._run_step(mul)
+
+    def _run_step(self, grad_mul: torch.Tensor | None) -> None:
+        lib = _native.library()
+        batches: dict[tuple, list[nn.Parameter]] = {}
+        for group in self._optimizer.param_groups:
+            if group.get("amsgrad") or group.get("maximize"):
+                raise UnsupportedFeatureError(
+                    format_error(
+                        "optim.ShardedOptimizer.step",
+                        "amsgrad and maximize have no HIP kernel in this build",
+                        observed={"amsgrad": group.get("amsgrad"), "maximize": group.get("maximize")},
+                    )
+                )
+            lr = float(group["lr"])
+            beta1, beta2 = (float(b) for b in group["betas"])
+            eps = float(group["eps"])
+            weight_decay = float(group["weight_decay"])
+            for p in group["params"]:
+                grad = p.grad
+                if grad is None:
+                    continue
+                _native.require_device_tensor(grad, "optim.ShardedOptimizer.step")
+                if grad.shape != p.shape or not grad.is_contiguous() or not p.is_contiguous():
+                    raise ShardingError(
+                        format_error(
+                            "optim.ShardedOptimizer.step",
+                            "gradient and parameter must be dense and of equal shape",
+                            expected=tuple(p.shape),
+                            observed=tuple(grad.shape),
+                        )
+                    )
+                if grad.dtype not in (torch.float32, torch.bfloat16):
+                    raise UnsupportedFeatureError(
+                        format_error("optim.ShardedOptimizer.step",
+                                     "gradients must be float32 or bfloat16", observed=str(grad.dtype))
+                    )
+                state = self._optimizer.state[p]
+                if len(state) == 0:
+                    # Same initial state as torch.optim.Adam._init_group.
+                    state["step"] = torch.tensor(0.0, dtype=torch.float32)
+                    state["exp_avg"] = torch.zeros_like(p, memory_format=torch.preserve_format)
+                    state["exp_avg_sq"] = torch.zeros_like(p, memory_format=torch.preserve_format)
+                step_t = state["step"]
+                step_t += 1
+                step = float(step_t.item())
+                # Host scalars exactly as torch/optim/adam.py:416-547 forms them (double).
+                bias_correction1 = 1 - beta1**step
+                bias_correction2 = 1 - beta2**step
+                step_size = lr / bias_correction1
+                bias_correction2_sqrt = bias_correction2**0.5
+                decay = 1 - lr * weight_decay if weight_decay != 0 else 1.0
+                scalars = (
+                    decay,
+                    1 - beta1,
+                    beta2,
+                    1 - beta2,
+                    bias_correction2_sqrt,
+                    eps,
+                    -step_size,
+                )
+                key = (scalars, grad.dtype, _pending_unscale(grad))
+                batches.setdefault(key, []).append(p)
+        stream = _native.stream_of(self._device)
+        with torch.cuda.device(self._device):
+            for (scalars, gdtype, unscale), params in batches.items():
+                for start in range(0, len(params), _native.MAX_TENSORS_PER_LAUNCH):
+                    chunk = params[start : start + _native.MAX_TENSORS_PER_LAUNCH]
+                    states = [self._optimizer.state[p] for p in chunk]
+                    status = lib.hbt_adamw_step(
+                        _native.pointer_array([p.data_ptr() for p in chunk]),
+                        _native.pointer_array([p.grad.data_ptr() for p in chunk]),
+                        _native.pointer_array([s["exp_avg"].data_ptr() for s in states]),
+                        _native.pointer_array([s["exp_avg_sq"].data_ptr() for s in states]),
+                        _native.int64_array([p.numel() for p in chunk]),
+                        len(chunk),
+                        _native.dtype_code(gdtype),
+                        unscale,
+                        None if grad_mul is None else grad_mul.data_ptr(),
+                        *scalars,
+                        stream,
+                    )
+                    _native.check(status, "optim.hbt_adamw_step")
+                    increment_version(chunk)
+                    increment_version([s["exp_avg"] for s in states])
+                    increment_version([s["exp_avg_sq"] for s in states])
+        self._pending_mul = None
+        self._pending_signature = None
+
+    def zero_grad(self, *, set_to_none: bool = True) -> None:
+        """Release or zero the gradients (``sharded_optimizer.py:357-372``)."""
+        self._pending_mul = None
+        self._pending_signature = None
+        self._last_check = None
+        for param in self._parameters:
+            if set_to_none:
+                param.grad = None
+            elif param.grad is not None:
+                if hasattr(param.grad, PENDING_UNSCALE_ATTR):
+                    delattr(param.grad, PENDING_UNSCALE_ATTR)
+                param.grad.detach().zero_()
+
+    # -- introspection -------------------------------------------------------------------
+    @property
+    def parameters(self) -> tuple[nn.Parameter, ...]:
+        """The parameters this optimizer updates."""
+        return tuple(self._parameters)
+
+    @property
+    def inner(self) -> torch.optim.Optimizer:
+        """The torch optimizer object that owns param groups and state."""
+        return self._optimizer
+
+    @property
+    def norm_group(self) -> GroupHandle:
+        """The group the gradient norm is reduced over."""
+        return self._norm_group
+
+    @property
+    def contributions(self) -> tuple[NormContribution, ...]:
+        """Per-parameter norm weights."""
+        return tuple(self._contributions)
+
+    @property
+    def learning_rate(self) -> float:
+        """Learning rate of the first parameter group."""
+        return float(self._optimizer.param_groups[0]["lr"])
+
+    def set_learning_rate(self, value: float) -> None:
+        """Set the learning rate of every parameter group."""
+        for group in self._optimizer.param_groups:
+            group["lr"] = value
+
+    def state_bytes(self) -> int:
+        """Bytes of optimizer state held by this rank."""
+        total = 0
+        for state in self._optimizer.state.values():
+            for value in state.values():
+                if torch.is_tensor(value):
+                    total += value.numel() * value.element_size()
+        return total
+
+    # -- serialisation -------------------------------------------------------------------
+    def state_dict(self) -> dict[str, Any]:
+        """Optimizer state keyed by parameter index (``sharded_optimizer.py:420-443``)."""
+        inner = self._optimizer.state_dict()
+        state: dict[int, dict[str, Any]] = {}
+        for index, entry in inner["state"].items():
+            state[int(index)] = {
+                key: (value.detach().cpu().clone() if torch.is_tensor(value) else value)
+                for key, value in entry.items()
+            }
+        return {
+            "param_groups": [
+                {k: v for k, v in group.items() if k != "params"} for group in inner["param_groups"]
+            ],
+            "state": state,
+            "num_parameters": len(self._parameters),
+        }
+
+    def load_state_dict(self, payload: dict[str, Any]) -> None:
+        """Restore :meth:`state_dict` output (``sharded_optimizer.py:445-493``)."""
+        expected = len(self._parameters)
+        observed = int(payload.get("num_parameters", -1))
+        if observed != expected:
+            raise ShardingError(
+                format_error(
+                    "optim.load_state_dict",
+                    "the checkpoint holds optimizer state for a different number of "
+                    "parameters, so the state cannot be matched to the current model",
+                    rank=self._norm_group.global_rank,
+                    expected=expected,
+                    observed=observed,
+                    resolution=(
+                        "resume with the same model definition and the same wrapping "
+                        "granularity that produced the checkpoint"
+                    ),
+                )
+            )
+        inner_groups = self._optimizer.state_dict()["param_groups"]
+        groups: list[dict[str, Any]] = []
+        for saved, existing in zip(payload["param_groups"], inner_groups):
+            merged = dict(existing)
+            merged.update(saved)
+            merged["params"] = existing["params"]
+            groups.append(merged)
+        state: dict[int, dict[str, Any]] = {}
+        for index, entry in payload["state"].items():
+            target = self._parameters[int(index)]
+            state[int(index)] = {
+                key: (
+                    value.to(device=target.device, dtype=target.dtype)
+                    if torch.is_tensor(value) and value.dtype.is_floating_point
+                    and value.dim() > 0
+                    else value
+                )
+                for key, value in entry.items()
+            }
+        self._optimizer.load_state_dict({"state": state, "param_groups": groups})
+        self._pending_mul = None
+        self._pending_signature = None
+
+    def __repr__(self) -> str:
+        return (
+            f"ShardedOptimizer({self._config.name}, params={len(self._parameters)}, "
+            f"norm_group={self._norm_group.name!r}, offload={self._offload})"
+        )
+

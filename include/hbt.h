@@ -1,0 +1,190 @@
+/*
+ * hbt.h - C ABI of the MI355X (gfx950) data-parallel hot-path library, libhbt.so.
+ *
+ * Every entry point takes plain device pointers, element counts, host scalars and a
+ * hipStream_t passed as void*.  No torch types cross this boundary.  All work is
+ * stream-ordered and asynchronous: an entry point returns once its kernels are
+ * enqueued.  The return value is HBT_OK (0) or a negative status; hbt_last_error()
+ * then holds a message for the calling thread.
+ *
+ * The reference (sdivyanshu90/build-your-own-hybrid-distributed-training, pure
+ * Python) has no FFI of its own.  Each entry point below names the reference
+ * function(s) whose torch op sequence it replaces, by file:line relative to the
+ * reference's src/hybrid_training/ directory, or relative to the installed torch
+ * package for the AdamW arithmetic the reference delegates to.
+ */
+#ifndef HBT_H
+#define HBT_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ---------------------------------------------------------- */
+#define HBT_OK 0
+#define HBT_ERR_INVALID_ARGUMENT (-1) /* null pointer, negative size, bad dtype/op  */
+#define HBT_ERR_UNSUPPORTED (-2)      /* legal request this build does not handle   */
+#define HBT_ERR_HIP (-3)              /* a HIP runtime call or kernel launch failed */
+
+/* ---- element types ----------------------------------------------------------- */
+#define HBT_DTYPE_F32 0
+#define HBT_DTYPE_BF16 1
+#define HBT_DTYPE_F16 2 /* byte copies only */
+#define HBT_DTYPE_F64 3 /* byte copies only */
+
+/* ---- per-call limits ---------------------------------------------------------- */
+#define HBT_MAX_TENSORS_PER_LAUNCH 16 /* AdamW / norm tables; the host splits larger lists */
+
+/* Message describing the last failed call on this thread ("" if none). */
+const char* hbt_last_error(void);
+
+/* ABI version of the loaded library; the Python loader refuses a mismatch. */
+int32_t hbt_abi_version(void);
+
+/* Number of HBT_* entry points exported (used by the loader's symbol check). */
+int32_t hbt_symbol_count(void);
+
+/* ------------------------------------------------------------------------------
+ * Fused gradient-clip + AdamW step over up to HBT_MAX_TENSORS_PER_LAUNCH tensors.
+ *
+ * Replaces: ShardedOptimizer.step (optim/sharded_optimizer.py:340-355) ->
+ *   torch.optim.AdamW built at optim/sharded_optimizer.py:111-120 ->
+ *   torch/optim/adam.py:396-547 (_single_tensor_adam, decoupled weight decay),
+ *   preceded by the clip multiply of ShardedOptimizer.clip_grad_norm
+ *   (optim/sharded_optimizer.py:333-337) and, for loss-scaled gradients, the
+ *   unscale multiply of GradScaler.unscale_ (optim/grad_scaler.py:181-186).
+ *
+ * Per element, in this order and in fp32 (each step rounded once):
+ *   g  = g_in * unscale            (skipped when unscale == 1)
+ *   g  = g * (*grad_mul)           (grad_mul: device fp32 written by
+ *                                   hbt_grad_norm_finalize, or NULL for 1)
+ *   p  = p * decay                 (decay = fp32(1 - lr*weight_decay))
+ *   m  = fma(w, g - m, m)          if |w| < 0.5, else fma(w - 1, g - m, g)
+ *                                  (w = fp32(1 - beta1); lerp in its fused form)
+ *   v  = v * beta2
+ *   v  = fma(one_minus_beta2 * g, g, v)
+ *   p  = p + (neg_step_size * m) / (sqrt(v) / bias_correction2_sqrt + eps)
+ * sqrt and both divisions are correctly rounded.  The host computes the scalars in
+ * double exactly as torch does and rounds them to fp32.
+ *
+ * grad_dtype is HBT_DTYPE_F32 or HBT_DTYPE_BF16 (bf16 gradients are widened
+ * exactly to fp32 before the unscale multiply).  params/exp_avgs/exp_avg_sqs are
+ * fp32.  Each tensor i has numels[i] elements; numels[i] may be 0.
+ * ---------------------------------------------------------------------------- */
+int32_t hbt_adamw_step(float* const* params, const void* const* grads, float* const* exp_avgs,
+                       float* const* exp_avg_sqs, const int64_t* numels, int32_t count,
+                       int32_t grad_dtype, float unscale, const float* grad_mul, float decay,
+                       float lerp_weight, float beta2, float one_minus_beta2,
+                       float bias_correction2_sqrt, float eps, float neg_step_size, void* stream);
+
+/* ------------------------------------------------------------------------------
+ * Deterministic squared L2 norm, stage 1: per-block fp64 partial sums.
+ *
+ * Replaces: NormContribution.squared_norm (optim/sharded_optimizer.py:145-158)
+ *   summed by distributed_gradient_norm (optim/sharded_optimizer.py:236-238).
+ * Computes sum_i weights[i] * sum_j (double)(g_ij * unscale)^2 over up to
+ * HBT_MAX_TENSORS_PER_LAUNCH gradient tensors (grad_dtype F32 or BF16), writing
+ * exactly hbt_norm_partials_per_launch() doubles to partials.  The block-to-element
+ * assignment depends only on the numels, so the result is bitwise reproducible.
+ * A non-finite element makes the sum non-finite, which is the overflow signal of
+ * GradScaler._detect_non_finite (optim/grad_scaler.py:189-200).
+ * ---------------------------------------------------------------------------- */
+int32_t hbt_norm_partials_per_launch(void);
+int32_t hbt_grad_sqnorm_partials(const void* const* grads, const int64_t* numels,
+                                 const double* weights, int32_t count, int32_t grad_dtype,
+                                 float unscale, double* partials, void* stream);
+
+/* ------------------------------------------------------------------------------
+ * Stage 2: fixed-order sum of `count` partials, sqrt, clip coefficient.
+ *
+ * Replaces: distributed_gradient_norm's clamp_min(0).sqrt()
+ *   (optim/sharded_optimizer.py:241) and the clip-coefficient arithmetic of
+ *   ShardedOptimizer.clip_grad_norm (optim/sharded_optimizer.py:331-337).
+ * Writes sum_out[0] = the fp64 sum (if sum_out is non-NULL) and norm_out[0] =
+ * sqrt(max(sum, 0)) (if norm_out is non-NULL).  If grad_mul_out is non-NULL it writes
+ * fp32(max_norm / (norm + 1e-6)) when max_norm > 0 and that quotient is < 1, else
+ * 1.0f.  If nonfinite_out is non-NULL it writes 1 when the sum is not finite, else 0.
+ * In a multi-rank job the stage-1 sum is what an fp64 all-reduce would combine
+ * between the two stages.
+ * ---------------------------------------------------------------------------- */
+int32_t hbt_grad_norm_finalize(const double* partials, int64_t count, double max_norm,
+                               double* sum_out, double* norm_out, float* grad_mul_out,
+                               int32_t* nonfinite_out, void* stream);
+
+/* ------------------------------------------------------------------------------
+ * Interval gather-copy: the one data-movement kernel behind flat-parameter
+ * pack/pad/shard, unpack, DDP bucket pack with the AVG pre-divide, and
+ * checkpoint interval resharding.
+ *
+ * Replaces:
+ *   FlatParamHandle._build_shard     (parallel/fsdp.py:434-454)     pack + zero pad
+ *   flatten_dense_tensors            (utils/tensors.py:199-260)     pack
+ *   FlatParamHandle.full_tensors     (parallel/fsdp.py:912-925)     unpack copy
+ *   FlatParamHandle.load_local_pieces(parallel/fsdp.py:862-910)     full -> shard slice
+ *   _on_grad_ready pack + all_reduce AVG pre-divide
+ *                                    (parallel/ddp.py:513, distributed/collectives.py:366-367)
+ *   read_tensor_range                (checkpoint/reshard.py:200-305) interval copy
+ *   FSDP destination fill            (checkpoint/reader.py:328-351, :423-443)
+ *
+ * `table` is a DEVICE array of `count` records of 4 int64 each:
+ *   { src_address (0 => write zeros), dst_address, numel, first_chunk }
+ * where first_chunk is the exclusive prefix sum over records of
+ * ceil(numel / HBT_COPY_CHUNK) (hbt_copy_chunk_elems()), and total_chunks is the
+ * sum.  All records share src_dtype/dst_dtype and op:
+ *   HBT_COPY_OP_COPY    dst = src               (same dtype: byte copy; F32->BF16
+ *                                                rounds to nearest even, NaN -> 0x7FC0;
+ *                                                BF16->F32 widens exactly)
+ *   HBT_COPY_OP_DIVIDE  dst = src / divisor     (true fp32 division, in fp32 for F32 and
+ *                                                BF16 data, result rounded to dst_dtype)
+ * Source and destination ranges of one call must not overlap.  Addresses need no
+ * particular alignment.
+ * ---------------------------------------------------------------------------- */
+#define HBT_COPY_OP_COPY 0
+#define HBT_COPY_OP_DIVIDE 1
+int64_t hbt_copy_chunk_elems(void);
+int32_t hbt_copy_intervals(const int64_t* table, int64_t count, int64_t total_chunks,
+                           int32_t src_dtype, int32_t dst_dtype, int32_t op, float divisor,
+                           void* stream);
+
+/* ------------------------------------------------------------------------------
+ * FSDP gradient local share on one device.
+ *
+ * Replaces: FlatParamHandle.reduce_scatter_gradient (parallel/fsdp.py:704-769) with
+ *   reduce_scatter_tensor AVG (distributed/collectives.py:588-595) and
+ *   _zero_padding_region (parallel/fsdp.py:771-781).
+ * `rank_grads` is a HOST array of `group_size` (at most HBT_MAX_LOCAL_RANKS) device
+ * addresses, each the padded full gradient (group_size * shard_numel elements,
+ * in_dtype F32 or BF16) of one rank, all resident on this device.  Writes the fp32
+ * shard of `rank`:
+ *   out[i] = sum over q = 0..group_size-1, in that order, of
+ *            fp32(rank_grads[q][rank*shard_numel + i]) / divisor
+ * (divisor = G for AVG, 1 for SUM), then +0.0 for i >= valid_numel (the padding tail).
+ * With group_size == 1 this is the whole local share of one rank: cast to the fp32
+ * reduce dtype, AVG pre-divide, cast to the fp32 master dtype, zero padding.
+ * ---------------------------------------------------------------------------- */
+#define HBT_MAX_LOCAL_RANKS 64
+int32_t hbt_grad_local_share(const void* const* rank_grads, int32_t group_size, int32_t rank,
+                             int64_t shard_numel, int64_t valid_numel, int32_t in_dtype,
+                             float divisor, float* out, void* stream);
+
+/* ------------------------------------------------------------------------------
+ * In-place gradient scaling: x = (x * unscale) * (*grad_mul), each product rounded to
+ * the tensor's dtype (F32 or BF16), over up to HBT_MAX_TENSORS_PER_LAUNCH tensors.
+ *
+ * Replaces: the grad.mul_(inverse) loop of GradScaler.unscale_
+ *   (optim/grad_scaler.py:181-186) and the grad.mul_(clip_coefficient) loop of
+ *   ShardedOptimizer.clip_grad_norm (optim/sharded_optimizer.py:333-337).  The fused
+ *   optimizer path folds both multiplies into hbt_adamw_step instead; this entry
+ *   point materialises them when a caller needs the scaled gradients themselves.
+ * grad_mul may be NULL (treated as 1).
+ * ---------------------------------------------------------------------------- */
+int32_t hbt_scale_inplace(void* const* tensors, const int64_t* numels, int32_t count,
+                          int32_t dtype, float unscale, const float* grad_mul, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HBT_H */
