@@ -1,0 +1,639 @@
+"""FSDP flat parameter on one device: layout, pack/pad/shard, unpack, gradient share.
+
+Drop-in for the data path of ``FlatParamHandle`` (``parallel/fsdp.py:300-958``) and
+the piece helpers around it (``:150-200``, ``:1670-1730``).  Construction, the
+properties, the piece layout and the error behaviour are the reference's.  The
+tensor work is the interval gather-copy kernel and the local-share kernel of
+``libhbt.so``:
+
+* ``_build_shard`` writes this rank's ``S`` elements straight from the parameters
+  into the shard, casting to the master dtype and zero-filling padding, in one
+  launch; the reference materialises the whole padded buffer first and slices it.
+* ``reduce_scatter_gradient`` is the rank's local share of the AVG reduce-scatter:
+  cast to fp32, divide by ``G``, sum over the ranks' buffers in rank order, zero
+  the padding tail (one launch).  There are no collectives: a group of size 1 is
+  the whole job; a :meth:`GroupHandle.local_view` group needs the other ranks'
+  buffers resident on this device (``peer_grads``), as the stand-in for the
+  reduce-scatter.
+* ``full_tensors``/``load_local_pieces``/``local_pieces`` are copy plans over the
+  same intervals the reference slices with ``intersect_ranges``.
+
+The storage-resize lifecycle (``reshard``/``refill``) and autograd plumbing of the
+reference are outside this path.
+"""
+
+from __future__ import annotations
+
+from collections.abc import Sequence
+from dataclasses import dataclass
+from typing import Any
+
+import torch
+import torch.nn as nn
+
+from . import _native
+from .config import FSDPConfig, MixedPrecisionConfig, resolve_dtype
+from .errors import ShardingError, UnsupportedFeatureError, format_error
+from .groups import GroupHandle
+from .tensors import FlatEntry, ShardRange, build_flat_layout, intersect_ranges
+
+__all__ = [
+    "FlatParamHandle",
+    "PieceLayout",
+    "ShardedTensorPiece",
+    "reshard_state_dict_pieces",
+]
+
+
+@dataclass(frozen=True)
+class ShardedTensorPiece:
+    """This rank's slice of one parameter in global coordinates (``fsdp.py:150-178``)."""
+
+    name: str
+    global_shape: tuple[int, ...]
+    offset: int
+    data: torch.Tensor
+
+    @property
+    def length(self) -> int:
+        """Number of owned elements."""
+        return int(self.data.numel())
+
+    @property
+    def range(self) -> ShardRange:
+        """The owned interval of the parameter's row-major flattening."""
+        return ShardRange(start=self.offset, length=self.length)
+
+
+@dataclass(frozen=True)
+class PieceLayout:
+    """Where a parameter's owned elements sit in this rank's shard (``fsdp.py:181-200``)."""
+
+    name: str
+    global_shape: tuple[int, ...]
+    parameter_offset: int
+    length: int
+    local_offset: int
+
+
+def _check_cast(src: torch.dtype, dst: torch.dtype, operation: str) -> None:
+    supported = {torch.float32, torch.bfloat16}
+    if src != dst and not (src in supported and dst in supported):
+        raise UnsupportedFeatureError(
+            format_error(
+                operation,
+                "the copy kernel converts only between float32 and bfloat16",
+                observed=f"{src} -> {dst}",
+            )
+        )
+
+
+class FlatParamHandle:
+    """One FSDP unit's flat parameter, sharded over ``shard_group``.
+
+    Args mirror ``parallel/fsdp.py:325-431``.  ``locations`` may be ``None`` when no
+    module attributes are to be rebound.  ``keep_originals=True`` leaves the
+    original parameters' storage alone (the reference always frees it).
+    """
+
+    def __init__(
+        self,
+        named_parameters: Sequence[tuple[str, nn.Parameter]],
+        locations: dict[int, list[tuple[nn.Module, str]]] | None,
+        shard_group: GroupHandle,
+        config: FSDPConfig,
+        mixed_precision: MixedPrecisionConfig,
+        device: torch.device,
+        *,
+        replica_group: GroupHandle | None = None,
+        recorder: Any = None,
+        keep_originals: bool = False,
+    ) -> None:
+        if not named_parameters:
+            raise ShardingError(
+                format_error(
+                    "fsdp.FlatParamHandle",
+                    "an FSDP unit needs at least one parameter",
+                    rank=shard_group.global_rank,
+                    expected=">= 1",
+                    observed=0,
+                    resolution="do not create a unit for a parameter-free module",
+                )
+            )
+        flags = {bool(p.requires_grad) for _, p in named_parameters}
+        if len(flags) > 1:
+            frozen = [n for n, p in named_parameters if not p.requires_grad]
+            raise UnsupportedFeatureError(
+                format_error(
+                    "fsdp.FlatParamHandle",
+                    "an FSDP unit flattens its parameters into a single tensor, so all of "
+                    "them must share one requires_grad flag; a unit cannot freeze part of "
+                    "its flat parameter",
+                    rank=shard_group.global_rank,
+                    expected="a uniform requires_grad within the unit",
+                    observed=f"frozen parameters present: {frozen[:8]}",
+                    resolution=(
+                        "wrap the frozen submodule as its own FSDP unit (auto-wrapping "
+                        "does this at module boundaries), or unfreeze it"
+                    ),
+                )
+            )
+        if replica_group is not None and replica_group.size > 1:
+            raise UnsupportedFeatureError(
+                format_error(
+                    "fsdp.FlatParamHandle",
+                    "hybrid sharding needs a replica all-reduce, and this build issues no "
+                    "collectives",
+                    observed=repr(replica_group),
+                )
+            )
+        self._shard_group = shard_group
+        self._replica_group = replica_group
+        self._config = config
+        self._mixed_precision = mixed_precision
+        self._device = torch.device(device)
+        self._recorder = recorder
+        self._requires_grad = next(iter(flags))
+        self._names = tuple(name for name, _ in named_parameters)
+        self._params = tuple(param for _, param in named_parameters)
+        self._locations = (
+            {id(p): list(locations.get(id(p), [])) for p in self._params} if locations else {}
+        )
+        first = self._params[0].dtype
+        enabled = mixed_precision.enabled
+        self._master_dtype = resolve_dtype(mixed_precision.master_dtype) if enabled else first
+        self._compute_dtype = resolve_dtype(mixed_precision.param_dtype) if enabled else first
+        self._reduce_dtype = resolve_dtype(mixed_precision.reduce_dtype) if enabled else first
+
+        self._entries, self._total_numel = build_flat_layout(list(named_parameters))
+        group = shard_group.size
+        self._shard_numel = -(-self._total_numel // group)
+        self._padded_numel = self._shard_numel * group
+        self._padding = self._padded_numel - self._total_numel
+
+        if config.limit_all_gather_bytes:
+            gathered = self._padded_numel * torch.empty(0, dtype=self._compute_dtype).element_size()
+            if gathered > config.limit_all_gather_bytes:
+                raise ShardingError(
+                    format_error(
+                        "fsdp.FlatParamHandle",
+                        "this unit's all-gather would exceed limit_all_gather_bytes; a unit "
+                        "that large defeats the purpose of sharding because its transient "
+                        "full copy dominates the memory saved",
+                        rank=shard_group.global_rank,
+                        expected=f"<= {config.limit_all_gather_bytes} bytes",
+                        observed=gathered,
+                        resolution=(
+                            "lower FSDPConfig.auto_wrap_min_num_params so the model is split "
+                            "into more units, or raise limit_all_gather_bytes"
+                        ),
+                    )
+                )
+        if config.cpu_offload_params:
+            raise UnsupportedFeatureError(
+                format_error("fsdp.FlatParamHandle", "parameter CPU offload is not part of this build",
+                             expected=False, observed=True)
+            )
+        self.flat_param = self._build_shard()
+        self._attach_gradient_norm_scale()
+        self._reduction_count = 0
+        if not keep_originals:
+            self._detach_original_parameters()
+
+    # -- construction -----------------------------------------------------------------
+    def _build_shard(self) -> nn.Parameter:
+        """This rank's shard, packed directly from the parameters (``fsdp.py:434-454``)."""
+        shard = torch.empty(self._shard_numel, dtype=self._master_dtype, device=self._device)
+        local = self.local_shard_range()
+        plans: dict[torch.dtype, _native.CopyPlan] = {}
+        for entry, param in zip(self._entries, self._params):
+            overlap = intersect_ranges(local, ShardRange(entry.offset, entry.numel))
+            if overlap is None:
+                continue
+            _check_cast(param.dtype, self._master_dtype, "fsdp._build_shard")
+            source = _native.contiguous_source(param.detach().to(self._device))
+            plan = plans.setdefault(param.dtype, _native.CopyPlan(self._device))
+            plan.add(source, overlap.start - entry.offset, shard, overlap.start - local.start,
+                     overlap.length)
+        padding = intersect_ranges(local, ShardRange(self._total_numel, self._padding))
+        zero_plan = plans.setdefault(self._master_dtype, _native.CopyPlan(self._device))
+        if padding is not None:
+            zero_plan.add_zero(shard, padding.start - local.start, padding.length)
+        for dtype, plan in plans.items():
+            plan.run(src_dtype=dtype, dst_dtype=self._master_dtype)
+        return nn.Parameter(shard, requires_grad=self._requires_grad)
+
+    def _attach_gradient_norm_scale(self) -> None:
+        """Per-element norm weights: partitioned width on real elements, 0 on padding.
+
+        Same vector as ``fsdp.py:456-483`` (kept on the host, as there), plus its
+        run-length form ``gradient_norm_scale_runs`` that the norm kernel consumes.
+        """
+        local = self.local_shard_range()
+        runs: list[tuple[int, int, float]] = []
+        for entry, param in zip(self._entries, self._params):
+            partitioned = self._shard_group.size
+            if not getattr(param, "is_tensor_parallel_replicated", True):
+                partitioned *= int(getattr(param, "tensor_parallel_group_size", 1))
+            overlap = intersect_ranges(local, ShardRange(entry.offset, entry.numel))
+            if overlap is not None:
+                runs.append((overlap.start - local.start, overlap.length, float(partitioned)))
+        padding = intersect_ranges(local, ShardRange(self._total_numel, self._padding))
+        if padding is not None:
+            runs.append((padding.start - local.start, padding.length, 0.0))
+        vector = torch.zeros(self._shard_numel, dtype=torch.float32)
+        for offset, length, value in runs:
+            vector[offset : offset + length] = value
+        self.flat_param.gradient_norm_scale_vector = vector  # type: ignore[attr-defined]
+        self.flat_param.gradient_norm_scale_runs = runs  # type: ignore[attr-defined]
+        self.flat_param.gradient_norm_label = (  # type: ignore[attr-defined]
+            f"flat_param[{self._names[0]} .. {self._names[-1]}]"
+        )
+
+    def _detach_original_parameters(self) -> None:
+        """Deregister and free the originals (``fsdp.py:485-504``)."""
+        placeholder = torch.empty(0, dtype=self._compute_dtype, device=self._device)
+        for param in self._params:
+            for module, attribute in self._locations.get(id(param), []):
+                if attribute in module._parameters:
+                    del module._parameters[attribute]
+                setattr(module, attribute, placeholder)
+            param.data = torch.empty(0, dtype=param.dtype, device=param.device)
+
+    # -- properties -------------------------------------------------------------------
+    @property
+    def entries(self) -> tuple[FlatEntry, ...]:
+        """Layout of the parameters inside the flat buffer."""
+        return self._entries
+
+    @property
+    def managed_parameters(self) -> tuple[nn.Parameter, ...]:
+        """The original parameter objects this unit flattened."""
+        return self._params
+
+    @property
+    def names(self) -> tuple[str, ...]:
+        """Managed parameter names in flat order."""
+        return self._names
+
+    @property
+    def total_numel(self) -> int:
+        """Logical element count, excluding padding."""
+        return self._total_numel
+
+    @property
+    def padded_numel(self) -> int:
+        """Element count including padding."""
+        return self._padded_numel
+
+    @property
+    def shard_numel(self) -> int:
+        """Elements stored per rank."""
+        return self._shard_numel
+
+    @property
+    def padding(self) -> int:
+        """Padding elements at the end of the flat buffer."""
+        return self._padding
+
+    @property
+    def shard_group(self) -> GroupHandle:
+        """The group the flat parameter is split across."""
+        return self._shard_group
+
+    @property
+    def replica_group(self) -> GroupHandle | None:
+        """The outer replication group (always trivial or ``None`` here)."""
+        return self._replica_group
+
+    @property
+    def reduction_count(self) -> int:
+        """Gradient reductions performed so far."""
+        return self._reduction_count
+
+    @property
+    def is_sharded(self) -> bool:
+        """Only the shard is resident between uses."""
+        return True
+
+    def local_shard_range(self) -> ShardRange:
+        """This rank's interval of the padded flat buffer."""
+        return ShardRange(start=self._shard_group.local_rank * self._shard_numel, length=self._shard_numel)
+
+    # -- gather / unpack -------------------------------------------------------------
+    def _all_shards(self, peer_shards: Sequence[torch.Tensor] | None, operation: str) -> list[torch.Tensor]:
+        if peer_shards is None:
+            if self._shard_group.size != 1:
+                raise UnsupportedFeatureError(
+                    format_error(
+                        operation,
+                        "materialising the full flat parameter needs every rank's shard; "
+                        "this build issues no all-gather",
+                        expected="peer_shards holding all group members' shards",
+                        observed=None,
+                        resolution="pass peer_shards=[shard_0, ..., shard_G-1] resident on this device",
+                    )
+                )
+            return [self.flat_param.detach()]
+        if len(peer_shards) != self._shard_group.size or any(
+            s.numel() != self._shard_numel for s in peer_shards
+        ):
+            raise ShardingError(
+                format_error(
+                    operation,
+                    "peer shards must be one equal-sized shard per group member",
+                    expected=f"{self._shard_group.size} x {self._shard_numel}",
+                    observed=[int(s.numel()) for s in peer_shards],
+                )
+            )
+        return list(peer_shards)
+
+    def gather_full(self, peer_shards: Sequence[torch.Tensor] | None = None) -> torch.Tensor:
+        """The padded full buffer in compute dtype (``fsdp.py:564-591``), built on this device
+        from every rank's shard (the all-gather's output)."""
+        shards = self._all_shards(peer_shards, "fsdp.gather_full")
+        full = torch.empty(self._padded_numel, dtype=self._compute_dtype, device=self._device)
+        src_dtype = shards[0].dtype
+        _check_cast(src_dtype, self._compute_dtype, "fsdp.gather_full")
+        plan = _native.CopyPlan(self._device)
+        for rank, shard in enumerate(shards):
+            plan.add(_native.contiguous_source(shard.detach()), 0, full, rank * self._shard_numel,
+                     self._shard_numel)
+        plan.run(src_dtype=src_dtype, dst_dtype=self._compute_dtype)
+        return full
+
+    def bind_views(self, full: torch.Tensor) -> None:
+        """Point every managed module attribute at its slice of ``full`` (zero copy)."""
+        sizes = [entry.numel for entry in self._entries]
+        if self._padding:
+            sizes.append(self._padding)
+        pieces = torch.split(full, sizes)
+        for index, entry in enumerate(self._entries):
+            view = pieces[index].view(entry.shape)
+            for module, attribute in self._locations.get(id(self._params[index]), []):
+                setattr(module, attribute, view)
+
+    def full_tensors(self, peer_shards: Sequence[torch.Tensor] | None = None) -> dict[str, torch.Tensor]:
+        """Every managed parameter, reconstructed by copy (``fsdp.py:912-925``)."""
+        shards = self._all_shards(peer_shards, "fsdp.full_tensors")
+        dtype = shards[0].dtype
+        out = {e.name: torch.empty(e.shape, dtype=dtype, device=self._device) for e in self._entries}
+        plan = _native.CopyPlan(self._device)
+        for entry in self._entries:
+            dest = out[entry.name].view(-1)
+            for rank, shard in enumerate(shards):
+                piece = intersect_ranges(
+                    ShardRange(rank * self._shard_numel, self._shard_numel),
+                    ShardRange(entry.offset, entry.numel),
+                )
+                if piece is not None:
+                    plan.add(_native.contiguous_source(shard.detach()), piece.start - rank * self._shard_numel,
+                             dest, piece.start - entry.offset, piece.length)
+        plan.run(src_dtype=dtype, dst_dtype=dtype)
+        return out
+
+    # -- gradient ---------------------------------------------------------------------
+    def reduce_scatter_gradient(
+        self, grad_full: torch.Tensor, *, peer_grads: Sequence[torch.Tensor] | None = None
+    ) -> torch.Tensor:
+        """This rank's fp32 gradient shard (``fsdp.py:704-769``), padding forced to 0.0.
+
+        ``grad_full`` is this rank's padded full gradient.  With a group of size 1
+        that is all there is; otherwise ``peer_grads`` must hold every rank's padded
+        gradient (``grad_full`` among them, in rank order), summed in rank order.
+        """
+        if self._reduce_dtype != torch.float32 or self._master_dtype != torch.float32:
+            raise UnsupportedFeatureError(
+                format_error(
+                    "fsdp.reduce_scatter_gradient",
+                    "the local-share kernel reduces in float32 into a float32 master shard",
+                    observed=f"reduce {self._reduce_dtype}, master {self._master_dtype}",
+                )
+            )
+        grads = [grad_full] if peer_grads is None else list(peer_grads)
+        group = self._shard_group.size
+        if len(grads) != group:
+            raise UnsupportedFeatureError(
+                format_error(
+                    "fsdp.reduce_scatter_gradient",
+                    "the reduce-scatter needs every rank's gradient; this build issues no "
+                    "collectives",
+                    expected=f"{group} gradients (peer_grads)",
+                    observed=len(grads),
+                )
+            )
+        for g in grads:
+            _native.require_device_tensor(g, "fsdp.reduce_scatter_gradient")
+            if g.numel() != self._padded_numel or g.dtype not in (torch.float32, torch.bfloat16) \
+                    or g.dtype != grads[0].dtype or not g.is_contiguous():
+                raise ShardingError(
+                    format_error(
+                        "fsdp.reduce_scatter_gradient",
+                        "each gradient must be a dense padded full buffer of one float dtype",
+                        expected=f"{self._padded_numel} float32/bfloat16 elements",
+                        observed=f"{g.numel()} {g.dtype}",
+                    )
+                )
+        local = self.local_shard_range()
+        valid = max(0, min(self._shard_numel, self._total_numel - local.start))
+        divisor = float(group) if (self._config.average_gradients and group > 1) else 1.0
+        out = torch.empty(self._shard_numel, dtype=torch.float32, device=self._device)
+        lib = _native.library()
+        with torch.cuda.device(self._device):
+            status = lib.hbt_grad_local_share(
+                _native.pointer_array([g.data_ptr() for g in grads]),
+                group,
+                self._shard_group.local_rank,
+                self._shard_numel,
+                valid,
+                _native.dtype_code(grads[0].dtype),
+                divisor,
+                out.data_ptr(),
+                _native.stream_of(self._device),
+            )
+        _native.check(status, "fsdp.hbt_grad_local_share")
+        self._reduction_count += 1
+        return out
+
+    def zero_padding_region(self, shard_grad: torch.Tensor) -> None:
+        """Zero the padding part of a gradient shard (``fsdp.py:771-781``)."""
+        padding = intersect_ranges(self.local_shard_range(), ShardRange(self._total_numel, self._padding))
+        if padding is None or padding.length == 0:
+            return
+        plan = _native.CopyPlan(self._device)
+        plan.add_zero(shard_grad, padding.start - self.local_shard_range().start, padding.length)
+        plan.run(src_dtype=shard_grad.dtype, dst_dtype=shard_grad.dtype)
+
+    # -- state dict -------------------------------------------------------------------
+    def local_piece_layout(self) -> list[PieceLayout]:
+        """Which elements of which parameters this rank owns (``fsdp.py:810-843``)."""
+        local = self.local_shard_range()
+        layout: list[PieceLayout] = []
+        for entry in self._entries:
+            overlap = intersect_ranges(local, ShardRange(entry.offset, entry.numel))
+            if overlap is None:
+                continue
+            layout.append(
+                PieceLayout(
+                    name=entry.name,
+                    global_shape=entry.shape,
+                    parameter_offset=overlap.start - entry.offset,
+                    length=overlap.length,
+                    local_offset=overlap.start - local.start,
+                )
+            )
+        return layout
+
+    def local_pieces(self) -> list[ShardedTensorPiece]:
+        """This rank's slice of each owned parameter, copied out (``fsdp.py:845-860``)."""
+        shard = self.flat_param.detach()
+        layout = self.local_piece_layout()
+        datas = [torch.empty(item.length, dtype=shard.dtype, device=shard.device) for item in layout]
+        plan = _native.CopyPlan(shard.device)
+        for item, data in zip(layout, datas):
+            plan.add(shard, item.local_offset, data, 0, item.length)
+        plan.run(src_dtype=shard.dtype, dst_dtype=shard.dtype)
+        return [
+            ShardedTensorPiece(name=item.name, global_shape=item.global_shape,
+                               offset=item.parameter_offset, data=data)
+            for item, data in zip(layout, datas)
+        ]
+
+    def load_local_pieces(self, pieces: dict[str, torch.Tensor]) -> None:
+        """Write whole parameter tensors' owned parts into the shard (``fsdp.py:862-910``)."""
+        local = self.local_shard_range()
+        shard = self.flat_param.data
+        plans: dict[torch.dtype, _native.CopyPlan] = {}
+        for entry in self._entries:
+            tensor = pieces.get(entry.name)
+            if tensor is None:
+                raise ShardingError(
+                    format_error(
+                        "fsdp.load_local_pieces",
+                        "missing parameter in the state dict",
+                        rank=self._shard_group.global_rank,
+                        expected=entry.name,
+                        observed=sorted(pieces)[:8],
+                        resolution="load a state dict produced by the same model definition",
+                    )
+                )
+            if tuple(tensor.shape) != entry.shape:
+                raise ShardingError(
+                    format_error(
+                        "fsdp.load_local_pieces",
+                        f"shape mismatch for {entry.name!r}",
+                        rank=self._shard_group.global_rank,
+                        expected=entry.shape,
+                        observed=tuple(tensor.shape),
+                        resolution="the checkpoint was written by a differently shaped model",
+                    )
+                )
+            overlap = intersect_ranges(local, ShardRange(entry.offset, entry.numel))
+            if overlap is None:
+                continue
+            _check_cast(tensor.dtype, shard.dtype, "fsdp.load_local_pieces")
+            source = _native.contiguous_source(tensor.detach().to(self._device))
+            plans.setdefault(tensor.dtype, _native.CopyPlan(self._device)).add(
+                source, overlap.start - entry.offset, shard, overlap.start - local.start, overlap.length
+            )
+        for dtype, plan in plans.items():
+            plan.run(src_dtype=dtype, dst_dtype=shard.dtype)
+
+    def memory_summary(self) -> dict[str, int]:
+        """Per-rank byte counts of this unit (``fsdp.py:927-942``)."""
+        element = self.flat_param.element_size()
+        grad = self.flat_param.grad
+        return {
+            "shard_bytes": self._shard_numel * element,
+            "full_bytes": 0,
+            "grad_shard_bytes": 0 if grad is None else grad.numel() * grad.element_size(),
+            "padding_bytes": self._padding * element,
+        }
+
+    def metadata(self) -> dict[str, Any]:
+        """Deterministic layout description (``fsdp.py:944-952``)."""
+        return {
+            "names": list(self._names),
+            "entries": [entry.as_dict() for entry in self._entries],
+            "total_numel": self._total_numel,
+            "padded_numel": self._padded_numel,
+            "shard_numel": self._shard_numel,
+        }
+
+    def __repr__(self) -> str:
+        return (
+            f"FlatParamHandle(params={len(self._params)}, total_numel={self._total_numel}, "
+            f"shard_numel={self._shard_numel}, padding={self._padding}, sharded=True)"
+        )
+
+
+def reshard_state_dict_pieces(
+    pieces: Sequence[ShardedTensorPiece], global_shape: tuple[int, ...]
+) -> torch.Tensor:
+    """Reassemble a parameter from covering pieces placed by offset (``fsdp.py:1670-1730``)."""
+    total = 1
+    for dim in global_shape:
+        total *= dim
+    if not pieces:
+        raise ShardingError(
+            format_error(
+                "fsdp.reshard_state_dict_pieces",
+                "no pieces supplied",
+                expected=">= 1 piece",
+                observed=0,
+                resolution="check that the manifest lists shards for this tensor",
+            )
+        )
+    dtype = pieces[0].data.dtype
+    device = pieces[0].data.device
+    intervals: list[tuple[int, int]] = []
+    for piece in pieces:
+        end = piece.offset + piece.length
+        if end > total:
+            raise ShardingError(
+                format_error(
+                    "fsdp.reshard_state_dict_pieces",
+                    f"piece for {piece.name!r} runs past the end of the tensor",
+                    expected=f"offset + length <= {total}",
+                    observed=end,
+                    resolution="the manifest disagrees with the model definition",
+                )
+            )
+        intervals.append((piece.offset, end))
+    covered, cursor = 0, 0
+    for start, end in sorted(intervals):
+        if end > cursor:
+            covered += end - max(start, cursor)
+            cursor = end
+    if covered != total:
+        missing = total - covered
+        raise ShardingError(
+            format_error(
+                "fsdp.reshard_state_dict_pieces",
+                f"the supplied pieces leave {missing} element(s) of {pieces[0].name!r} uncovered",
+                expected=f"{total} covered elements",
+                observed=covered,
+                resolution="a shard file is missing from the checkpoint",
+            )
+        )
+    flat = torch.empty(total, dtype=dtype, device=device)
+    # Later pieces overwrite earlier ones where they overlap, as sequential slice
+    # assignment does; keep only the last writer of every element.
+    plan = _native.CopyPlan(device)
+    claimed: list[tuple[int, int]] = []
+    for piece in reversed(list(pieces)):
+        start, end = piece.offset, piece.offset + piece.length
+        cursor = start
+        for c_start, c_end in sorted(claimed):
+            if c_end <= cursor or c_start >= end:
+                continue
+            if c_start > cursor:
+                plan.add(_native.contiguous_source(piece.data.reshape(-1)), cursor - start, flat, cursor,
+                         c_start - cursor)
+            cursor = max(cursor, c_end)
+        if cursor < end:
+            plan.add(_native.contiguous_source(piece.data.reshape(-1)), cursor - start, flat, cursor,
+                     end - cursor)
+        claimed.append((start, end))
+    plan.run(src_dtype=dtype, dst_dtype=dtype)
+    return flat.view(global_shape)
