@@ -56,7 +56,33 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--cpu-numel", type=int, default=1 << 26, help="CPU-baseline sample size")
     ap.add_argument("--cpu-steps", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument(
+        "--calibrate-copy",
+        action="store_true",
+        help="instead of the benchmark, run the library's interval-copy kernel over a 1 GiB fp32 "
+        "buffer (known traffic: 1 GiB read + 1 GiB written per launch) to scale HBM counters",
+    )
     return ap.parse_args()
+
+
+def calibrate_copy() -> int:
+    """Three launches of hbt_copy_intervals moving one 1 GiB fp32 buffer into another."""
+    import torch
+
+    from hybrid_training_amd import _native
+
+    device = torch.device("cuda", 0)
+    n = 1 << 28
+    src = torch.ones(n, dtype=torch.float32, device=device)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        plan = _native.CopyPlan(device)
+        plan.add(src, 0, dst, 0, n)
+        plan.run(src_dtype=torch.float32, dst_dtype=torch.float32)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration": "hbt_copy_intervals", "bytes_read": 4 * n, "bytes_written": 4 * n,
+                      "launches": 3, "ok": bool(torch.equal(src, dst))}), flush=True)
+    return 0
 
 
 def cpu_baseline(numel: int, steps: int) -> dict:
@@ -101,6 +127,8 @@ def read_traffic() -> float | None:
 
 def main() -> int:
     args = parse_args()
+    if args.calibrate_copy:
+        return calibrate_copy()
     if args.gpus != 1:
         print(
             "bench.py measures one GPU: this build runs one rank's share of the work on one "

@@ -44,7 +44,7 @@ __all__ = [
     "stream_of",
 ]
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 MAX_TENSORS_PER_LAUNCH = 16
 MAX_LOCAL_RANKS = 64
 
@@ -78,7 +78,7 @@ EXPORTED_SYMBOLS: dict[str, tuple[object, tuple[object, ...]]] = {
             _c_void_p,
         ),
     ),
-    "hbt_norm_partials_per_launch": (_c_i32, ()),
+    "hbt_norm_partials_count": (_c_i64, (_i64_array, _c_i32)),
     "hbt_grad_sqnorm_partials": (
         _c_i32,
         (_ptr_array, _i64_array, _f64_array, _c_i32, _c_i32, _c_f32, _c_void_p, _c_void_p),

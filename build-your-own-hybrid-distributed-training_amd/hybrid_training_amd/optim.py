@@ -210,10 +210,10 @@ def gradient_norm_pass(
     ``segments`` are ``(grad, offset, length, weight)``; a grad tagged with a
     pending loss-scale factor is read through that factor.  Segments are batched
     by (dtype, factor) into launches of at most 16; every launch writes its own
-    block of partials and one finalize launch sums all of them in a fixed order.
+    run of per-chunk partials and one finalize launch sums all of them in a fixed
+    order.
     """
     lib = _native.library()
-    per_launch = int(lib.hbt_norm_partials_per_launch())
     batches: dict[tuple[torch.dtype, float], list[tuple[torch.Tensor, int, int, float]]] = {}
     for grad, offset, length, weight in segments:
         _native.require_device_tensor(grad, "optim.gradient_norm")
@@ -233,17 +233,22 @@ def gradient_norm_pass(
             batches.setdefault((grad.dtype, _pending_unscale(grad)), []).append(
                 (grad, offset, length, weight)
             )
-    launches: list[tuple[torch.dtype, float, list[tuple[torch.Tensor, int, int, float]]]] = []
+    launches: list[tuple[torch.dtype, float, list[tuple[torch.Tensor, int, int, float]], int]] = []
+    total_partials = 0
     for (dtype, unscale), items in batches.items():
         for start in range(0, len(items), _native.MAX_TENSORS_PER_LAUNCH):
-            launches.append((dtype, unscale, items[start : start + _native.MAX_TENSORS_PER_LAUNCH]))
-    partials = torch.empty(max(1, len(launches)) * per_launch, dtype=torch.float64, device=device)
+            chunk = items[start : start + _native.MAX_TENSORS_PER_LAUNCH]
+            count = int(lib.hbt_norm_partials_count(_native.int64_array([n for _, _, n, _ in chunk]),
+                                                    len(chunk)))
+            launches.append((dtype, unscale, chunk, total_partials))
+            total_partials += count
+    partials = torch.empty(max(1, total_partials), dtype=torch.float64, device=device)
     outputs = torch.empty(2, dtype=torch.float64, device=device)
     grad_mul = torch.empty(1, dtype=torch.float32, device=device)
     nonfinite = torch.empty(1, dtype=torch.int32, device=device)
     stream = _native.stream_of(device)
     with torch.cuda.device(device):
-        for index, (dtype, unscale, items) in enumerate(launches):
+        for dtype, unscale, items, first in launches:
             ptrs = [g.data_ptr() + off * g.element_size() for g, off, _, _ in items]
             status = lib.hbt_grad_sqnorm_partials(
                 _native.pointer_array(ptrs),
@@ -252,14 +257,13 @@ def gradient_norm_pass(
                 len(items),
                 _native.dtype_code(dtype),
                 unscale,
-                partials.data_ptr() + index * per_launch * 8,
+                partials.data_ptr() + first * 8,
                 stream,
             )
             _native.check(status, "optim.hbt_grad_sqnorm_partials")
-        count = len(launches) * per_launch
         status = lib.hbt_grad_norm_finalize(
             partials.data_ptr(),
-            count,
+            total_partials,
             float(max_norm),
             outputs.data_ptr(),
             outputs.data_ptr() + 8,
