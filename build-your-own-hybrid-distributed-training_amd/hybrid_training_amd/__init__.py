@@ -27,7 +27,11 @@ from .errors import (
     UnsupportedFeatureError,
     format_error,
 )
+from .buckets import BucketedGradients, BucketLayout, GradientBucket, build_buckets
+from .flat_param import FlatParamHandle, PieceLayout, ShardedTensorPiece, reshard_state_dict_pieces
+from .grad_scaler import GradScaler, GradScalerState
 from .groups import GroupHandle
+from .manifest import ShardRecord, TensorRecord, shard_filename, validate_shard_filename
 from .optim import (
     NormContribution,
     ShardedOptimizer,
@@ -35,6 +39,7 @@ from .optim import (
     build_inner_optimizer,
     distributed_gradient_norm,
 )
+from .reshard import DeviceShardCache, load_flat_shard, read_tensor_range
 from .tensors import (
     FlatEntry,
     ShardRange,

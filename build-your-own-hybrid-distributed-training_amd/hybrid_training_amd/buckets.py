@@ -1,0 +1,310 @@
+"""DDP gradient buckets on one device: layout, pack with the AVG pre-divide, unpack.
+
+Drop-in for the data path of ``parallel/ddp.py``: ``BucketLayout`` and
+``GradientBucket`` keep the reference's fields and methods (``ddp.py:111-230``), and
+:func:`build_buckets` applies the reference's grouping rule (``ddp.py:397-463``):
+walk the parameters in reverse registration order and close a bucket when the next
+parameter would push it past ``int(bucket_cap_mb * 2**20)`` bytes, or when dtype or
+device changes.
+
+Where the reference copies each gradient into its bucket from a Python hook and
+later divides the whole bucket by the group size (``ddp.py:513``,
+``distributed/collectives.py:366-367``), :meth:`BucketedGradients.pack` moves every
+gradient of every bucket into place and divides it in one launch of the interval
+copy kernel: ``bucket[offset + i] = grad[i] / W`` in fp32 true division, which is
+bitwise the copy-then-``div_`` of the reference.  :meth:`bind_gradients` then points
+each ``param.grad`` at its slice of the bucket (``ddp.py:635-640``), with no copy.
+The cross-rank SUM all-reduce of each bucket is not issued: over a trivial group it
+is the identity, and over a :meth:`GroupHandle.local_view` group the bucket holds
+this rank's pre-divided contribution, ready for it.
+"""
+
+from __future__ import annotations
+
+from collections.abc import Sequence
+from dataclasses import dataclass, field
+from typing import Any
+
+import torch
+import torch.nn as nn
+
+from . import _native
+from .config import DDPConfig
+from .errors import ShardingError, UnsupportedFeatureError, format_error
+from .groups import GroupHandle
+
+__all__ = ["BucketLayout", "BucketedGradients", "DDPStatistics", "GradientBucket", "build_buckets"]
+
+_BYTES_PER_MIB = 1024 * 1024
+
+
+@dataclass(frozen=True)
+class BucketLayout:
+    """Static description of one bucket (``ddp.py:111-143``)."""
+
+    index: int
+    parameter_names: tuple[str, ...]
+    offsets: tuple[int, ...]
+    numels: tuple[int, ...]
+    total_numel: int
+    dtype_str: str
+    device_str: str
+
+    def as_dict(self) -> dict[str, Any]:
+        """JSON form used by cross-rank layout checks."""
+        return {
+            "index": self.index,
+            "parameter_names": list(self.parameter_names),
+            "offsets": list(self.offsets),
+            "numels": list(self.numels),
+            "total_numel": self.total_numel,
+            "dtype": self.dtype_str,
+        }
+
+
+class GradientBucket:
+    """A flat buffer holding several parameters' gradients (``ddp.py:146-230``)."""
+
+    __slots__ = ("_buffer", "_device", "_dtype", "launched", "layout", "parameters", "pending", "ready", "work")
+
+    def __init__(
+        self,
+        layout: BucketLayout,
+        parameters: Sequence[nn.Parameter],
+        dtype: torch.dtype,
+        device: torch.device,
+    ) -> None:
+        self.layout = layout
+        self.parameters = tuple(parameters)
+        self._dtype = dtype
+        self._device = torch.device(device)
+        self._buffer: torch.Tensor | None = None
+        self.pending: int = len(parameters)
+        self.ready: bool = False
+        self.launched: bool = False
+        self.work: Any = None
+
+    @property
+    def buffer(self) -> torch.Tensor:
+        """The flat gradient buffer, allocated and zero-filled on first access."""
+        if self._buffer is None:
+            buffer = torch.empty(self.layout.total_numel, dtype=self._dtype, device=self._device)
+            plan = _native.CopyPlan(self._device)
+            plan.add_zero(buffer, 0, self.layout.total_numel)
+            plan.run(src_dtype=self._dtype, dst_dtype=self._dtype)
+            self._buffer = buffer
+        return self._buffer
+
+    @property
+    def is_allocated(self) -> bool:
+        """Whether the flat buffer exists yet."""
+        return self._buffer is not None
+
+    def view_for(self, position: int) -> torch.Tensor:
+        """The bucket slice of the ``position``-th parameter, shaped like it."""
+        offset = self.layout.offsets[position]
+        numel = self.layout.numels[position]
+        return self.buffer[offset : offset + numel].view(self.parameters[position].shape)
+
+    def reset(self) -> None:
+        """Prepare for another backward pass."""
+        self.pending = len(self.parameters)
+        self.ready = False
+        self.launched = False
+        self.work = None
+
+    def num_bytes(self) -> int:
+        """Size of the flat buffer in bytes."""
+        return self.layout.total_numel * torch.empty(0, dtype=self._dtype).element_size()
+
+    def __repr__(self) -> str:
+        return (
+            f"GradientBucket(index={self.layout.index}, params={len(self.parameters)}, "
+            f"numel={self.layout.total_numel}, pending={self.pending})"
+        )
+
+
+def build_buckets(
+    named_parameters: Sequence[tuple[str, nn.Parameter]], bucket_cap_mb: float
+) -> list[GradientBucket]:
+    """Reverse-order greedy buckets under a byte cap (``ddp.py:397-463``)."""
+    cap_bytes = int(bucket_cap_mb * _BYTES_PER_MIB)
+    buckets: list[GradientBucket] = []
+    current: list[tuple[str, nn.Parameter]] = []
+    current_bytes = 0
+    current_key: tuple[torch.dtype, torch.device] | None = None
+
+    def close() -> None:
+        nonlocal current, current_bytes, current_key
+        if not current:
+            return
+        offsets, numels, cursor = [], [], 0
+        for _, param in current:
+            offsets.append(cursor)
+            numels.append(int(param.numel()))
+            cursor += int(param.numel())
+        first = current[0][1]
+        layout = BucketLayout(
+            index=len(buckets),
+            parameter_names=tuple(name for name, _ in current),
+            offsets=tuple(offsets),
+            numels=tuple(numels),
+            total_numel=cursor,
+            dtype_str=str(first.dtype),
+            device_str=str(first.device),
+        )
+        buckets.append(GradientBucket(layout, [p for _, p in current], first.dtype, first.device))
+        current, current_bytes, current_key = [], 0, None
+
+    for name, param in reversed(list(named_parameters)):
+        key = (param.dtype, param.device)
+        nbytes = int(param.numel()) * param.element_size()
+        if current_key is not None and (key != current_key or current_bytes + nbytes > cap_bytes):
+            close()
+        current_key = key
+        current.append((name, param))
+        current_bytes += nbytes
+    close()
+    return buckets
+
+
+@dataclass
+class DDPStatistics:
+    """Counters of the bucketing path (``ddp.py:233-263``)."""
+
+    steps: int = 0
+    buckets_reduced: int = 0
+    bytes_reduced: int = 0
+    unused_parameters: tuple[str, ...] = field(default_factory=tuple)
+
+    def as_dict(self) -> dict[str, Any]:
+        """JSON form."""
+        return {
+            "steps": self.steps,
+            "buckets_reduced": self.buckets_reduced,
+            "bytes_reduced": self.bytes_reduced,
+            "unused_parameters": list(self.unused_parameters),
+        }
+
+
+class BucketedGradients:
+    """One replica's gradient buckets: pack + AVG pre-divide in one launch, view unpack."""
+
+    def __init__(
+        self,
+        named_parameters: Sequence[tuple[str, nn.Parameter]],
+        group: GroupHandle,
+        config: DDPConfig | None = None,
+    ) -> None:
+        self._config = config or DDPConfig()
+        self._group = group
+        self._named = [(n, p) for n, p in named_parameters if p.requires_grad]
+        if not self._named:
+            raise ShardingError(
+                format_error(
+                    "ddp.DistributedDataParallel",
+                    "the wrapped module has no trainable parameters",
+                    rank=group.global_rank,
+                    expected=">= 1 parameter with requires_grad=True",
+                    observed=0,
+                    resolution="check that the module was built before wrapping",
+                )
+            )
+        if group.size > 1 and group.process_group is not None:
+            raise UnsupportedFeatureError(
+                format_error(
+                    "ddp.BucketedGradients",
+                    "this build packs one replica's buckets on one device and issues no all-reduce",
+                    observed=repr(group),
+                )
+            )
+        for _, p in self._named:
+            _native.require_device_tensor(p, "ddp.BucketedGradients")
+        self._buckets = build_buckets(self._named, self._config.bucket_cap_mb)
+        self._name_of = {id(p): n for n, p in self._named}
+        self.statistics = DDPStatistics()
+
+    @property
+    def buckets(self) -> tuple[GradientBucket, ...]:
+        """The buckets in launch order."""
+        return tuple(self._buckets)
+
+    def bucket_layouts(self) -> list[BucketLayout]:
+        """Static layouts in launch order."""
+        return [b.layout for b in self._buckets]
+
+    def _divisor(self) -> float:
+        # AVG over a trivial group returns before dividing (collectives.py:361-363).
+        if self._config.average_gradients and self._group.size > 1:
+            return float(self._group.size)
+        return 1.0
+
+    def pack(self) -> None:
+        """Copy every gradient into its bucket slice, divided by the group size for AVG.
+
+        A parameter without a gradient contributes zeros when
+        ``find_unused_parameters`` is set and raises otherwise (``ddp.py:579-615``).
+        """
+        missing: list[str] = []
+        divisor = self._divisor()
+        plans: dict[tuple[torch.dtype, torch.dtype], _native.CopyPlan] = {}
+        for bucket in self._buckets:
+            buffer = bucket.buffer
+            for position, param in enumerate(bucket.parameters):
+                offset = bucket.layout.offsets[position]
+                numel = bucket.layout.numels[position]
+                grad = param.grad
+                if grad is None:
+                    missing.append(self._name_of.get(id(param), f"<param#{position}>"))
+                    plans.setdefault((buffer.dtype, buffer.dtype), _native.CopyPlan(buffer.device)).add_zero(
+                        buffer, offset, numel
+                    )
+                    continue
+                source = _native.contiguous_source(grad.detach())
+                if source.numel() != numel:
+                    raise ShardingError(
+                        format_error("ddp.pack", "gradient size differs from its parameter",
+                                     expected=numel, observed=source.numel())
+                    )
+                same = source.data_ptr() == buffer.data_ptr() + offset * buffer.element_size()
+                if same and divisor == 1.0 and source.dtype == buffer.dtype:
+                    continue  # the gradient already is this bucket slice
+                plans.setdefault((source.dtype, buffer.dtype), _native.CopyPlan(buffer.device)).add(
+                    source, 0, buffer, offset, numel
+                )
+        if missing and not self._config.find_unused_parameters:
+            raise ShardingError(
+                format_error(
+                    "ddp.finish_gradient_synchronization",
+                    "some parameters received no gradient, so their buckets can never "
+                    "become ready and the all-reduce would never be issued (every other "
+                    "rank would block waiting for it)",
+                    rank=self._group.global_rank,
+                    world_size=self._group.size,
+                    expected="every trainable parameter to receive a gradient",
+                    observed=f"{len(missing)} without gradients: {missing[:8]}",
+                    resolution=(
+                        "set DDPConfig(find_unused_parameters=True), or stop marking "
+                        "unused parameters as requires_grad=True"
+                    ),
+                )
+            )
+        for (src_dtype, dst_dtype), plan in plans.items():
+            op = _native.COPY_OP_DIVIDE if divisor != 1.0 else _native.COPY_OP_COPY
+            plan.run(src_dtype=src_dtype, dst_dtype=dst_dtype, op=op, divisor=divisor)
+        self.statistics.unused_parameters = tuple(missing)
+        self.statistics.buckets_reduced += len(self._buckets)
+        self.statistics.bytes_reduced += sum(b.num_bytes() for b in self._buckets)
+
+    def bind_gradients(self) -> None:
+        """Point every ``param.grad`` at its bucket slice (gradient-as-bucket-view)."""
+        for bucket in self._buckets:
+            for position, param in enumerate(bucket.parameters):
+                param.grad = bucket.view_for(position)
+            bucket.reset()
+
+    def synchronize(self) -> None:
+        """Pack (with the AVG pre-divide), then rebind gradients to the buckets."""
+        self.pack()
+        self.bind_gradients()
+        self.statistics.steps += 1

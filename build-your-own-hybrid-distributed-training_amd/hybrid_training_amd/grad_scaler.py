@@ -1,0 +1,242 @@
+"""Dynamic loss scaler whose gradient passes run on HIP kernels.
+
+Drop-in for ``optim/grad_scaler.py`` of the reference: the state machine
+(``unscale_`` / ``step`` / ``update``, growth and backoff, skip on overflow) and the
+serialised state are the reference's (``grad_scaler.py:52-298``).  The gradient work
+is native:
+
+* ``unscale_`` multiplies each gradient by ``fp32(1/scale)`` in its own dtype
+  (``hbt_scale_inplace``, as ``grad.mul_(inverse)`` does) and checks finiteness with
+  one fp64 norm pass: the sum of squares is non-finite exactly when some element is.
+* With ``defer_unscale=True`` the multiply is not applied to ``.grad``; the factor
+  travels with each gradient tensor and the optimizer's norm pass and fused AdamW
+  pass apply it while they read the gradient, so a clipped, loss-scaled step costs
+  one norm pass and one update pass.  ``unscale_`` then returns a lazily evaluated
+  flag, and ``step`` takes the overflow decision from the optimizer's norm pass when
+  it covered the same gradients.
+
+The overflow decision is taken over this device's gradients only; the one-element
+MAX all-reduce that agrees on it across ranks (``grad_scaler.py:191-199``) is not
+issued.
+"""
+
+from __future__ import annotations
+
+from collections.abc import Iterable, Sequence
+from dataclasses import dataclass
+from typing import Any
+
+import torch
+import torch.nn as nn
+
+from . import _native
+from .config import GradScalerConfig
+from .groups import GroupHandle
+from .optim import PENDING_UNSCALE_ATTR, gradient_norm_pass
+
+__all__ = ["GradScaler", "GradScalerState"]
+
+
+@dataclass
+class GradScalerState:
+    """Serialisable scaler state (``grad_scaler.py:52-92``)."""
+
+    scale: float
+    growth_tracker: int = 0
+    total_steps: int = 0
+    skipped_steps: int = 0
+
+    def as_dict(self) -> dict[str, float]:
+        """JSON form."""
+        return {
+            "scale": float(self.scale),
+            "growth_tracker": int(self.growth_tracker),
+            "total_steps": int(self.total_steps),
+            "skipped_steps": int(self.skipped_steps),
+        }
+
+    @classmethod
+    def from_dict(cls, payload: dict[str, Any]) -> GradScalerState:
+        """Rebuild from :meth:`as_dict` output."""
+        return cls(
+            scale=float(payload["scale"]),
+            growth_tracker=int(payload.get("growth_tracker", 0)),
+            total_steps=int(payload.get("total_steps", 0)),
+            skipped_steps=int(payload.get("skipped_steps", 0)),
+        )
+
+
+class _DeviceFlag:
+    """Truth value of a device-side non-finite flag, read (one sync) on first use."""
+
+    def __init__(self, compute) -> None:
+        self._compute = compute
+        self._value: bool | None = None
+
+    def __bool__(self) -> bool:
+        if self._value is None:
+            self._value = bool(self._compute())
+        return self._value
+
+    def __repr__(self) -> str:
+        return f"_DeviceFlag({'unevaluated' if self._value is None else self._value})"
+
+
+def _nonfinite_flag(params: Sequence[nn.Parameter]) -> torch.Tensor | None:
+    grads = [p.grad for p in params if p.grad is not None]
+    if not grads:
+        return None
+    segments = [(g, 0, int(g.numel()), 1.0) for g in grads]
+    return gradient_norm_pass(segments, grads[0].device, max_norm=0.0).nonfinite
+
+
+class GradScaler:
+    """Loss scaler with a native unscale and overflow check (``grad_scaler.py:95-298``)."""
+
+    def __init__(
+        self,
+        config: GradScalerConfig,
+        group: GroupHandle,
+        device: torch.device,
+        *,
+        recorder: Any = None,
+        defer_unscale: bool = False,
+    ) -> None:
+        self._config = config
+        self._group = group
+        self._device = torch.device(device)
+        self._recorder = recorder
+        self._defer = defer_unscale
+        self._state = GradScalerState(scale=config.init_scale if config.enabled else 1.0)
+        self._unscaled = False
+        self._skipped_on_last_step = False
+
+    @property
+    def enabled(self) -> bool:
+        """Whether scaling is active."""
+        return self._config.enabled
+
+    @property
+    def scale_value(self) -> float:
+        """Current loss scale (1.0 when disabled)."""
+        return self._state.scale if self._config.enabled else 1.0
+
+    @property
+    def state(self) -> GradScalerState:
+        """Current scaler state."""
+        return self._state
+
+    def scale(self, loss: torch.Tensor) -> torch.Tensor:
+        """Multiply the loss by the current scale (unchanged when disabled)."""
+        if not self._config.enabled:
+            return loss
+        self._unscaled = False
+        return loss * self._state.scale
+
+    def unscale_(self, parameters: Iterable[nn.Parameter]) -> bool:
+        """Divide gradients by the scale and report whether any is non-finite."""
+        params = [p for p in parameters if p.grad is not None]
+        if not self._config.enabled:
+            return self._detect_non_finite(params)
+        inverse = 1.0 / self._state.scale
+        if self._defer:
+            for p in params:
+                setattr(p.grad, PENDING_UNSCALE_ATTR, inverse)
+            self._unscaled = True
+            return _DeviceFlag(lambda: self._detect_non_finite(params))  # type: ignore[return-value]
+        lib = _native.library()
+        groups: dict[tuple[torch.device, torch.dtype], list[torch.Tensor]] = {}
+        for p in params:
+            _native.require_device_tensor(p.grad, "grad_scaler.unscale_")
+            groups.setdefault((p.grad.device, p.grad.dtype), []).append(p.grad)
+        for (device, dtype), grads in groups.items():
+            with torch.cuda.device(device):
+                for start in range(0, len(grads), _native.MAX_TENSORS_PER_LAUNCH):
+                    chunk = grads[start : start + _native.MAX_TENSORS_PER_LAUNCH]
+                    status = lib.hbt_scale_inplace(
+                        _native.pointer_array([g.data_ptr() for g in chunk]),
+                        _native.int64_array([g.numel() for g in chunk]),
+                        len(chunk),
+                        _native.dtype_code(dtype),
+                        inverse,
+                        None,
+                        _native.stream_of(device),
+                    )
+                    _native.check(status, "grad_scaler.hbt_scale_inplace")
+                    torch.autograd.graph.increment_version(chunk)
+        self._unscaled = True
+        return self._detect_non_finite(params)
+
+    def _detect_non_finite(
+        self, parameters: Sequence[nn.Parameter], optimizer: Any = None
+    ) -> bool:
+        """Whether any gradient element is inf or NaN (one device flag, one sync)."""
+        flag = None
+        if optimizer is not None and hasattr(optimizer, "last_nonfinite_flag"):
+            covered = {id(p) for p in getattr(optimizer, "parameters", ()) if p.grad is not None}
+            if covered == {id(p) for p in parameters}:
+                flag = optimizer.last_nonfinite_flag()
+        if flag is None:
+            flag = _nonfinite_flag(parameters)
+        if flag is None:
+            return False
+        return bool(int(flag.item()) != 0)
+
+    def step(
+        self,
+        optimizer: Any,
+        parameters: Iterable[nn.Parameter],
+        *,
+        already_unscaled: bool = False,
+    ) -> bool:
+        """Step the optimizer unless a gradient is non-finite (``grad_scaler.py:202-241``)."""
+        params = list(parameters)
+        if already_unscaled or self._unscaled:
+            found = self._detect_non_finite([p for p in params if p.grad is not None], optimizer)
+        else:
+            found = bool(self.unscale_(params))
+        self._state.total_steps += 1
+        self._skipped_on_last_step = found
+        if found:
+            self._state.skipped_steps += 1
+            return False
+        optimizer.step()
+        return True
+
+    def update(self, *, found_non_finite: bool | None = None) -> float:
+        """Grow or back off the scale (``grad_scaler.py:243-269``)."""
+        if not self._config.enabled:
+            return 1.0
+        overflowed = found_non_finite if found_non_finite is not None else self._skipped_on_last_step
+        if overflowed:
+            self._state.scale = max(self._state.scale * self._config.backoff_factor, 1.0)
+            self._state.growth_tracker = 0
+        else:
+            self._state.growth_tracker += 1
+            if self._state.growth_tracker >= self._config.growth_interval:
+                self._state.scale = min(
+                    self._state.scale * self._config.growth_factor, self._config.max_scale
+                )
+                self._state.growth_tracker = 0
+        self._unscaled = False
+        return self._state.scale
+
+    @property
+    def last_step_skipped(self) -> bool:
+        """Whether the most recent :meth:`step` was skipped."""
+        return self._skipped_on_last_step
+
+    def state_dict(self) -> dict[str, float]:
+        """Scaler state for checkpointing."""
+        return self._state.as_dict()
+
+    def load_state_dict(self, payload: dict[str, Any]) -> None:
+        """Restore :meth:`state_dict` output."""
+        self._state = GradScalerState.from_dict(payload)
+        self._unscaled = False
+
+    def __repr__(self) -> str:
+        return (
+            f"GradScaler(enabled={self._config.enabled}, scale={self.scale_value}, "
+            f"skipped={self._state.skipped_steps}/{self._state.total_steps})"
+        )

@@ -168,11 +168,15 @@ def build_gradient_norm_contributions(
     for index, param in enumerate(parameters):
         vector = getattr(param, "gradient_norm_scale_vector", None)
         if vector is not None:
+            # A flat shard built here also carries the vector's run-length form, so a
+            # billion-element shard is never scanned on the host.
+            runs = getattr(param, "gradient_norm_scale_runs", None)
             contributions.append(
                 NormContribution(
                     parameter=param,
                     scale=vector.to(torch.float64) / world_size,
                     label=getattr(param, "gradient_norm_label", f"flat_param#{index}"),
+                    runs=[] if runs is None else [(o, n, float(w) / world_size) for o, n, w in runs],
                 )
             )
             continue

@@ -1,0 +1,271 @@
+"""Checkpoint resharding as device interval copies.
+
+A checkpoint stores every tensor as shards: intervals of its row-major flattening.
+A loading rank wants intervals of its own; the bytes to move are the
+intersections, whatever the saving and loading widths were.  This module keeps the
+reference's reader interface (``read_tensor_range``, ``checkpoint/reshard.py:200-305``)
+and error behaviour, and adds :func:`load_flat_shard`, the FSDP destination fill of
+``checkpoint/reader.py:328-351`` (and the optimizer-state fill of ``:423-443``) done
+as ONE launch of the interval copy kernel straight from the stored shards into the
+destination shard.  The reference copies twice per piece (into a temporary, then
+into the destination) and runs a Python loop per piece.
+
+Payloads are expected to be resident on the device already
+(:class:`DeviceShardCache`); reading ``.pt`` files and verifying their digests is
+host I/O outside this path.
+"""
+
+from __future__ import annotations
+
+from collections.abc import Callable, Mapping, Sequence
+
+import torch
+
+from . import _native
+from .errors import CheckpointCorruptionError, CheckpointError, IncompleteCheckpointError, format_error
+from .flat_param import PieceLayout
+from .manifest import TensorRecord, validate_shard_filename
+from .tensors import ShardRange
+
+__all__ = ["DeviceShardCache", "load_flat_shard", "read_tensor_range"]
+
+
+class DeviceShardCache:
+    """Shard payloads already on the device, keyed like ``ShardFileCache`` (``reshard.py:54-197``).
+
+    ``payloads`` maps a shard file name (``rank-NNNNN.pt``) to ``{storage_key: tensor}``.
+    """
+
+    def __init__(self, payloads: Mapping[str, Mapping[str, torch.Tensor]] | None = None) -> None:
+        self._payloads: dict[str, dict[str, torch.Tensor]] = {}
+        self._loaded: set[str] = set()
+        for name, payload in (payloads or {}).items():
+            for key, tensor in payload.items():
+                self.add(name, key, tensor)
+
+    def add(self, filename: str, key: str, tensor: torch.Tensor) -> None:
+        """Register one stored shard tensor."""
+        validate_shard_filename(filename)
+        _native.require_device_tensor(tensor, "reshard.DeviceShardCache")
+        self._payloads.setdefault(filename, {})[key] = tensor
+
+    def get(self, filename: str) -> Mapping[str, torch.Tensor]:
+        """The tensors stored under ``filename``."""
+        payload = self._payloads.get(validate_shard_filename(filename))
+        if payload is None:
+            raise IncompleteCheckpointError(
+                format_error(
+                    "reshard.ShardFileCache.get",
+                    "a shard file listed in the manifest is missing",
+                    expected=filename,
+                    observed="not present in the checkpoint directory",
+                    resolution=(
+                        "the checkpoint is incomplete; restore the missing file or "
+                        "resume from an earlier checkpoint"
+                    ),
+                )
+            )
+        self._loaded.add(filename)
+        return payload
+
+    def loaded_files(self) -> tuple[str, ...]:
+        """Files read so far."""
+        return tuple(sorted(self._loaded))
+
+
+def _queue_range(
+    record: TensorRecord,
+    wanted: ShardRange,
+    cache: DeviceShardCache,
+    dest: torch.Tensor | None,
+    dest_offset: int,
+    add: Callable[[torch.Tensor, int, int, int], None],
+) -> torch.dtype:
+    """Queue the copies that fill ``wanted`` of ``record``; returns the first shard's dtype.
+
+    ``add(source_flat, source_offset, dest_offset, length)`` receives one interval per
+    intersecting shard, in offset order.  The checks and messages are those of
+    ``reshard.py:224-302``.
+    """
+    if wanted.end > record.numel:
+        raise CheckpointError(
+            format_error(
+                "reshard.read_tensor_range",
+                f"the requested range of {record.key!r} runs past the end of the tensor; "
+                "the current model is larger than the one that was saved",
+                expected=f"end <= {record.numel}",
+                observed=wanted.end,
+                resolution="resume with the model definition that produced the checkpoint",
+            )
+        )
+    overlaps = record.shards_overlapping(wanted)
+    if not overlaps:
+        raise IncompleteCheckpointError(
+            format_error(
+                "reshard.read_tensor_range",
+                f"no shard of {record.key!r} covers the requested range",
+                expected=f"a shard intersecting [{wanted.start}, {wanted.end})",
+                observed=[(s.offset, s.length) for s in record.shards],
+                resolution="the checkpoint is incomplete",
+            )
+        )
+    first_dtype: torch.dtype | None = None
+    filled = 0
+    cursor = wanted.start
+    for shard, overlap in overlaps:
+        if overlap.start != cursor:
+            raise IncompleteCheckpointError(
+                format_error(
+                    "reshard.read_tensor_range",
+                    f"a gap exists in the shards of {record.key!r}",
+                    expected=f"a shard starting at element {cursor}",
+                    observed=f"next shard starts at {overlap.start}",
+                    resolution="a shard file is missing from the checkpoint",
+                )
+            )
+        payload = cache.get(shard.file)
+        stored = payload.get(shard.key)
+        if stored is None:
+            raise CheckpointCorruptionError(
+                format_error(
+                    "reshard.read_tensor_range",
+                    f"shard file {shard.file!r} does not contain key {shard.key!r}",
+                    expected=shard.key,
+                    observed=sorted(payload)[:8],
+                    resolution="the manifest and the payload disagree; the checkpoint is corrupt",
+                )
+            )
+        flat = _native.contiguous_source(stored.reshape(-1))
+        if flat.numel() != shard.length:
+            raise CheckpointCorruptionError(
+                format_error(
+                    "reshard.read_tensor_range",
+                    f"shard {shard.key!r} has a different length from its manifest record",
+                    expected=shard.length,
+                    observed=flat.numel(),
+                    resolution="the manifest and the payload disagree; the checkpoint is corrupt",
+                )
+            )
+        if first_dtype is None:
+            first_dtype = flat.dtype
+        add(flat, overlap.start - shard.offset, dest_offset + filled, overlap.length)
+        filled += overlap.length
+        cursor = overlap.end
+    if filled != wanted.length:
+        raise IncompleteCheckpointError(
+            format_error(
+                "reshard.read_tensor_range",
+                f"the shards of {record.key!r} cover only part of the requested range",
+                expected=wanted.length,
+                observed=filled,
+                resolution="a shard file is missing from the checkpoint",
+            )
+        )
+    assert first_dtype is not None
+    return first_dtype
+
+
+class _PlanSet:
+    """Copy plans keyed by source dtype, all writing one destination dtype."""
+
+    def __init__(self, device: torch.device, dst_dtype: torch.dtype) -> None:
+        self.device = device
+        self.dst_dtype = dst_dtype
+        self.plans: dict[torch.dtype, _native.CopyPlan] = {}
+
+    def add(self, src: torch.Tensor, src_offset: int, dst: torch.Tensor, dst_offset: int, n: int) -> None:
+        if src.dtype != dst.dtype and {src.dtype, dst.dtype} - {torch.float32, torch.bfloat16}:
+            raise CheckpointError(
+                format_error("reshard.read_tensor_range", "unsupported dtype conversion",
+                             observed=f"{src.dtype} -> {dst.dtype}")
+            )
+        self.plans.setdefault(src.dtype, _native.CopyPlan(self.device)).add(src, src_offset, dst, dst_offset, n)
+
+    def run(self) -> None:
+        for src_dtype, plan in self.plans.items():
+            plan.run(src_dtype=src_dtype, dst_dtype=self.dst_dtype)
+
+
+def read_tensor_range(
+    record: TensorRecord,
+    wanted: ShardRange,
+    cache: DeviceShardCache,
+    *,
+    dtype: torch.dtype | None = None,
+) -> torch.Tensor:
+    """Elements ``wanted`` of a stored tensor as a new 1-D device tensor (one launch).
+
+    ``dtype`` casts the result (float32 <-> bfloat16); by default the result has the
+    first intersecting shard's dtype.
+    """
+    if wanted.length == 0:
+        device = next(
+            (t.device for name in (s.file for s in record.shards) for t in cache.get(name).values()),
+            None,
+        )
+        return torch.empty(0, dtype=dtype or torch.float32, device=device)
+    pending: list[tuple[torch.Tensor, int, int, int]] = []
+    first = _queue_range(record, wanted, cache, None, 0,
+                         lambda src, so, do, n: pending.append((src, so, do, n)))
+    out_dtype = dtype or first
+    out = torch.empty(wanted.length, dtype=out_dtype, device=pending[0][0].device)
+    plans = _PlanSet(out.device, out_dtype)
+    for src, so, do, n in pending:
+        plans.add(src, so, out, do, n)
+    plans.run()
+    return out
+
+
+def load_flat_shard(
+    destination: torch.Tensor,
+    layout: Sequence[PieceLayout],
+    records: Mapping[str, TensorRecord],
+    cache: DeviceShardCache,
+    *,
+    key_of: Callable[[PieceLayout], str] | None = None,
+    strict: bool = True,
+) -> int:
+    """Fill a flat shard's pieces from the checkpoint in one launch; returns pieces loaded.
+
+    ``layout`` is the destination's ``local_piece_layout()`` (``fsdp.py:810-843``);
+    each piece ``(name, parameter_offset, length, local_offset)`` receives elements
+    ``[parameter_offset, parameter_offset + length)`` of the stored tensor at
+    ``destination[local_offset:]``, cast to the destination dtype.  ``key_of`` maps
+    a piece to its record key (default: the piece name; optimizer state uses
+    ``f"{name}::{state}"``).  A missing record raises ``IncompleteCheckpointError``
+    when ``strict``, else the piece is left unchanged (``reader.py:328-351``).
+    """
+    _native.require_device_tensor(destination, "reshard.load_flat_shard")
+    dest = destination.detach().view(-1)
+    if not dest.is_contiguous():
+        raise CheckpointError(format_error("reshard.load_flat_shard", "the destination must be dense"))
+    plans = _PlanSet(dest.device, dest.dtype)
+    loaded = 0
+    for item in layout:
+        key = key_of(item) if key_of is not None else item.name
+        record = records.get(key)
+        if record is None:
+            if strict:
+                raise IncompleteCheckpointError(
+                    format_error(
+                        "checkpoint.load",
+                        f"the checkpoint has no tensor {key!r}",
+                        expected=key,
+                        observed=sorted(records)[:8],
+                        resolution="load a checkpoint produced by the same model definition",
+                    )
+                )
+            continue
+        if item.local_offset + item.length > dest.numel():
+            raise CheckpointError(
+                format_error("reshard.load_flat_shard", "a piece runs past the destination shard",
+                             expected=f"<= {dest.numel()}", observed=item.local_offset + item.length)
+            )
+        if item.length == 0:
+            continue
+        _queue_range(record, ShardRange(item.parameter_offset, item.length), cache, dest,
+                     item.local_offset,
+                     lambda src, so, do, n: plans.add(src, so, dest, do, n))
+        loaded += 1
+    plans.run()
+    return loaded

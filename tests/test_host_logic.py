@@ -1,0 +1,121 @@
+"""Host-only behaviour: error messages, configuration validation, the scaler state
+machine and the oracle's local-share restatement (no GPU)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from hybrid_training_amd import (
+    DDPConfig,
+    FSDPConfig,
+    GradScalerConfig,
+    GroupHandle,
+    MixedPrecisionConfig,
+    OptimizerConfig,
+    format_error,
+)
+from hybrid_training_amd.errors import ConfigurationError, UnsupportedFeatureError
+from hybrid_training_amd.grad_scaler import GradScaler, GradScalerState
+
+
+def test_format_error_matches_the_reference_example():
+    msg = format_error(
+        "topology.validate",
+        "parallel sizes do not factor the world size",
+        rank=3, world_size=8, expected=8, observed=6,
+        resolution="set dp*shard*seq*tensor == world_size",
+    )
+    assert msg == (
+        "[rank 3/8] topology.validate: parallel sizes do not factor the world size; "
+        "expected 8, observed 6. Fix: set dp*shard*seq*tensor == world_size"
+    )
+    assert format_error("a.b", "bad") == "a.b: bad"
+    assert format_error("a.b", "bad", rank=1) == "[rank 1] a.b: bad"
+
+
+def test_config_validation():
+    with pytest.raises(ConfigurationError, match="bucket_cap_mb must be positive"):
+        DDPConfig(bucket_cap_mb=0)
+    with pytest.raises(ConfigurationError, match="use_padding=False is not supported"):
+        FSDPConfig(use_padding=False)
+    with pytest.raises(ConfigurationError, match="betas must be two values"):
+        OptimizerConfig(betas=(0.9, 1.0))
+    with pytest.raises(ConfigurationError, match="unknown optimizer"):
+        OptimizerConfig(name="lamb")
+    with pytest.raises(ConfigurationError, match="backoff_factor"):
+        GradScalerConfig(backoff_factor=1.5)
+    with pytest.raises(ConfigurationError, match="only meaningful for float16"):
+        MixedPrecisionConfig(enabled=True, param_dtype="bfloat16", scaler=GradScalerConfig(enabled=True))
+    assert OptimizerConfig().weight_decay == 0.0 and OptimizerConfig().eps == 1e-8
+
+
+def test_scaler_state_machine():
+    cfg = GradScalerConfig(enabled=True, init_scale=65536.0, growth_interval=3, max_scale=2.0**17)
+    scaler = GradScaler(cfg, GroupHandle.trivial(), device="cpu")
+    assert scaler.scale_value == 65536.0
+    assert scaler.update(found_non_finite=True) == 32768.0
+    assert scaler.state.growth_tracker == 0
+    for _ in range(2):
+        assert scaler.update(found_non_finite=False) == 32768.0
+    assert scaler.update(found_non_finite=False) == 65536.0
+    for _ in range(6):
+        scaler.update(found_non_finite=False)
+    assert scaler.scale_value == 2.0**17  # capped at max_scale
+    low = GradScaler(GradScalerConfig(enabled=True, init_scale=1.0), GroupHandle.trivial(), device="cpu")
+    assert low.update(found_non_finite=True) == 1.0  # floor at 1
+    state = scaler.state_dict()
+    again = GradScaler(cfg, GroupHandle.trivial(), device="cpu")
+    again.load_state_dict(state)
+    assert again.state == GradScalerState.from_dict(state)
+    disabled = GradScaler(GradScalerConfig(), GroupHandle.trivial(), device="cpu")
+    assert disabled.scale_value == 1.0 and disabled.update() == 1.0
+
+
+def test_group_handles():
+    g = GroupHandle.trivial()
+    assert g.size == 1 and g.is_trivial and g.process_group is None
+    v = GroupHandle.local_view("shard", 4, 2)
+    assert v.size == 4 and v.local_rank == 2 and not v.is_trivial
+
+
+def test_real_process_groups_are_refused():
+    import torch
+
+    from hybrid_training_amd import ShardedOptimizer
+
+    group = GroupHandle(name="world", ranks=(0, 1), local_rank=0, global_rank=0, process_group=object())
+    with pytest.raises(UnsupportedFeatureError, match="no collectives"):
+        ShardedOptimizer([torch.nn.Parameter(torch.zeros(2))], OptimizerConfig(), norm_group=group,
+                         device=torch.device("cpu"))
+
+
+def test_oracle_local_share_closed_form():
+    rng = np.random.default_rng(0)
+    group, shard, total = 3, 5, 13
+    grads = [rng.standard_normal(group * shard).astype(np.float32) for _ in range(group)]
+    for rank in range(group):
+        valid = max(0, min(shard, total - rank * shard))
+        got = oracle.local_share(grads, rank, shard, valid, float(group))
+        want = np.zeros(shard, np.float32)
+        for i in range(valid):
+            acc = np.float32(grads[0][rank * shard + i] / np.float32(group))
+            for q in range(1, group):
+                acc = np.float32(acc + np.float32(grads[q][rank * shard + i] / np.float32(group)))
+            want[i] = acc
+        assert np.array_equal(got, want)
+        assert np.all(got[valid:] == 0.0)
+
+
+def test_oracle_pack_matches_concatenation():
+    rng = np.random.default_rng(1)
+    tensors = [rng.standard_normal(s).astype(np.float32) for s in ((25, 14), (25,), (7, 25), (7,))]
+    flat = np.concatenate([t.reshape(-1) for t in tensors])
+    for group in (1, 2, 3, 4, 7):
+        shard, padded, pad = oracle.even_shards(flat.size, group)
+        pieces = [oracle.pack_shard(tensors, group, r) for r in range(group)]
+        joined = np.concatenate(pieces)
+        assert np.array_equal(joined[: flat.size], flat) and np.all(joined[flat.size :] == 0)
+        back = oracle.unpack_full(joined, [t.shape for t in tensors])
+        assert all(np.array_equal(a, b) for a, b in zip(back, tensors))
