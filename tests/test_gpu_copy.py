@@ -1,0 +1,158 @@
+"""GPU parity of the interval gather-copy kernel (``hbt_copy_intervals``).
+
+Every case builds the expected destination on the CPU with numpy slicing (and the
+oracle's bf16 rounding) and requires bitwise equality: copies are byte work.
+Intervals start at arbitrary element offsets on both sides, so the aligned, the
+byte-shifted and the head/tail paths all run.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from hybrid_training_amd import _native
+
+pytestmark = pytest.mark.gpu
+
+
+def _bits(t: torch.Tensor) -> np.ndarray:
+    t = t.detach().cpu().contiguous()
+    return {1: t.view(torch.uint8), 2: t.view(torch.int16), 4: t.view(torch.int32), 8: t.view(torch.int64)}[
+        t.element_size()
+    ].numpy().copy()
+
+
+def _as_f32(bits16: np.ndarray) -> np.ndarray:
+    return (bits16.astype(np.uint32) << 16).view(np.float32)
+
+
+def _random_intervals(rng, n_src, n_dst, count, max_len):
+    """Non-overlapping destination intervals (random order), random source offsets."""
+    cuts = np.sort(rng.choice(np.arange(1, n_dst), size=2 * count, replace=False))
+    rows = []
+    for k in range(count):
+        d0, d1 = int(cuts[2 * k]), int(cuts[2 * k + 1])
+        n = min(d1 - d0, max_len)
+        s0 = int(rng.integers(0, n_src - n))
+        rows.append((s0, d0, n))
+    rng.shuffle(rows)
+    return rows
+
+
+def _expected(src_vals, dst_init, rows, convert):
+    out = dst_init.copy()
+    for s0, d0, n in rows:
+        out[d0 : d0 + n] = convert(src_vals[s0 : s0 + n])
+    return out
+
+
+CASES = [
+    # (src dtype, dst dtype, op)
+    (torch.float32, torch.float32, _native.COPY_OP_COPY),
+    (torch.bfloat16, torch.bfloat16, _native.COPY_OP_COPY),
+    (torch.float16, torch.float16, _native.COPY_OP_COPY),
+    (torch.float64, torch.float64, _native.COPY_OP_COPY),
+    (torch.float32, torch.bfloat16, _native.COPY_OP_COPY),
+    (torch.bfloat16, torch.float32, _native.COPY_OP_COPY),
+    (torch.float32, torch.float32, _native.COPY_OP_DIVIDE),
+    (torch.bfloat16, torch.bfloat16, _native.COPY_OP_DIVIDE),
+    (torch.bfloat16, torch.float32, _native.COPY_OP_DIVIDE),
+    (torch.float32, torch.bfloat16, _native.COPY_OP_DIVIDE),
+]
+
+
+@pytest.mark.parametrize(("sdt", "ddt", "op"), CASES)
+@pytest.mark.parametrize("count,max_len", [(7, 100_000), (300, 3_000), (2000, 40)])
+def test_random_interval_plans(device, sdt, ddt, op, count, max_len):
+    rng = np.random.default_rng(count * 7 + int(op) + 31 * CASES.index((sdt, ddt, op)))
+    n_src, n_dst = 400_003, 500_009
+    src = (torch.randn(n_src, dtype=torch.float32, device=device) * 3).to(sdt)
+    dst = (torch.randn(n_dst, dtype=torch.float32, device=device)).to(ddt)
+    dst_init = _bits(dst)
+    rows = _random_intervals(rng, n_src, n_dst, count, max_len)
+    divisor = 3.0 if op == _native.COPY_OP_DIVIDE else 1.0
+    plan = _native.CopyPlan(device)
+    for s0, d0, n in rows:
+        plan.add(src, s0, dst, d0, n)
+    plan.run(src_dtype=sdt, dst_dtype=ddt, op=op, divisor=divisor)
+    sbits = _bits(src)
+    if sdt == ddt and op == _native.COPY_OP_COPY:
+        convert = lambda x: x  # noqa: E731
+    else:
+        def convert(x):
+            vals = x.view(np.float32) if sdt == torch.float32 else _as_f32(x)
+            if op == _native.COPY_OP_DIVIDE:
+                vals = (vals / np.float32(divisor)).astype(np.float32)
+            return vals.view(np.int32) if ddt == torch.float32 else oracle.f32_to_bf16(vals).view(np.int16)
+    expect = _expected(sbits, dst_init, rows, convert)
+    assert np.array_equal(_bits(dst), expect)
+
+
+def test_zero_fill_mixed_with_copies(device):
+    src = torch.randn(10_000, device=device)
+    dst = torch.full((20_000,), 7.0, device=device)
+    plan = _native.CopyPlan(device)
+    plan.add(src, 1, dst, 3, 5000)
+    plan.add_zero(dst, 5003, 1234)
+    plan.add_zero(dst, 19_999, 1)
+    plan.add(src, 5000, dst, 7001, 4999)
+    plan.run(src_dtype=torch.float32, dst_dtype=torch.float32)
+    expect = np.full(20_000, 7.0, np.float32)
+    s = src.cpu().numpy()
+    expect[3:5003] = s[1:5001]
+    expect[5003:6237] = 0.0
+    expect[19_999] = 0.0
+    expect[7001:12_000] = s[5000:9999]
+    assert np.array_equal(dst.cpu().numpy().view(np.int32), expect.view(np.int32))
+
+
+@pytest.mark.parametrize("src_off,dst_off", [(0, 0), (3, 0), (0, 5), (7, 1), (1, 6)])
+def test_large_interval_every_alignment(device, src_off, dst_off):
+    n = 50_000_000 + 13
+    src = torch.randint(-(2**15), 2**15 - 1, (n + 8,), dtype=torch.int16, device=device).view(torch.bfloat16)
+    dst = torch.zeros(n + 8, dtype=torch.bfloat16, device=device)
+    plan = _native.CopyPlan(device)
+    plan.add(src, src_off, dst, dst_off, n)
+    plan.run(src_dtype=torch.bfloat16, dst_dtype=torch.bfloat16)
+    assert torch.equal(dst[dst_off : dst_off + n].view(torch.int16), src[src_off : src_off + n].view(torch.int16))
+    assert int(dst[:dst_off].view(torch.int16).abs().sum()) == 0
+    assert int(dst[dst_off + n :].view(torch.int16).abs().sum()) == 0
+
+
+def test_in_place_divide(device):
+    x = torch.randn(1_000_003, device=device)
+    expect = (x.cpu().numpy() / np.float32(8.0)).astype(np.float32)
+    plan = _native.CopyPlan(device)
+    plan.add(x, 0, x, 0, x.numel())
+    plan.run(src_dtype=torch.float32, dst_dtype=torch.float32, op=_native.COPY_OP_DIVIDE, divisor=8.0)
+    assert np.array_equal(x.cpu().numpy().view(np.int32), expect.view(np.int32))
+
+
+def test_specials_round_trip_and_divide(device):
+    vals = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 1e-40, -1e-40, 3.4e38, 1.0, 1.00390625], np.float32)
+    src = torch.from_numpy(vals).to(device)
+    out16 = torch.empty(vals.size, dtype=torch.bfloat16, device=device)
+    plan = _native.CopyPlan(device)
+    plan.add(src, 0, out16, 0, vals.size)
+    plan.run(src_dtype=torch.float32, dst_dtype=torch.bfloat16)
+    assert np.array_equal(_bits(out16).view(np.uint16), oracle.f32_to_bf16(vals))
+    div = torch.empty_like(src)
+    plan = _native.CopyPlan(device)
+    plan.add(src, 0, div, 0, vals.size)
+    plan.run(src_dtype=torch.float32, dst_dtype=torch.float32, op=_native.COPY_OP_DIVIDE, divisor=3.0)
+    expect = (vals / np.float32(3.0)).astype(np.float32)
+    got = div.cpu().numpy()
+    assert np.array_equal(np.isnan(got), np.isnan(expect))
+    assert np.array_equal(got[~np.isnan(got)].view(np.int32), expect[~np.isnan(expect)].view(np.int32))
+
+
+def test_plan_bounds_are_checked_on_the_host(device):
+    a = torch.zeros(10, device=device)
+    plan = _native.CopyPlan(device)
+    with pytest.raises(ValueError, match="runs past"):
+        plan.add(a, 5, a, 0, 6)
+    with pytest.raises(ValueError, match="runs past"):
+        plan.add_zero(a, 8, 3)

@@ -1,0 +1,151 @@
+"""GPU parity of the FSDP flat parameter: pack/pad/shard, unpack, pieces, gradient share.
+
+The 1857-parameter MLPs of the reference tests (``test_fsdp.py:42-46``) at group sizes
+1, 2, 3 and 4 cover padding of 0, 1, 2 and 3 elements; every rank's shard, piece set
+and gradient share is checked bitwise against the oracle's restatement
+(``oracle.pack_shard``, ``oracle.local_share``) and against the reference's
+invariants: padding is exactly 0.0 in parameters and gradients, pieces cover every
+parameter once, and ``full_tensors`` reproduces the originals bitwise.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from hybrid_training_amd import (
+    FlatParamHandle,
+    FSDPConfig,
+    GroupHandle,
+    MixedPrecisionConfig,
+    ShardingError,
+    reshard_state_dict_pieces,
+)
+from hybrid_training_amd.errors import UnsupportedFeatureError
+
+from .model_shapes import MLP_1857_BASELINE, MLP_1857_REFERENCE
+
+pytestmark = pytest.mark.gpu
+
+
+def _params(shapes, device, seed=3, dtype=torch.float32):
+    gen = torch.Generator().manual_seed(seed)
+    return [(f"p{i}", torch.nn.Parameter((torch.randn(s, generator=gen) * 0.1).to(dtype).to(device)))
+            for i, s in enumerate(shapes)]
+
+
+def _handles(shapes, group, device, **kw):
+    named = _params(shapes, device)
+    originals = [p.detach().clone() for _, p in named]
+    handles = [
+        FlatParamHandle(named, None, GroupHandle.local_view("shard", group, r), FSDPConfig(),
+                        MixedPrecisionConfig(), device, keep_originals=True, **kw)
+        for r in range(group)
+    ]
+    return named, originals, handles
+
+
+@pytest.mark.parametrize("shapes", [MLP_1857_REFERENCE, MLP_1857_BASELINE])
+@pytest.mark.parametrize("group", [1, 2, 3, 4])
+def test_pack_pad_shard_matches_oracle(device, shapes, group):
+    named, originals, handles = _handles(shapes, group, device)
+    host = [o.cpu().numpy() for o in originals]
+    shard, padded, pad = oracle.even_shards(1857, group)
+    for rank, h in enumerate(handles):
+        assert (h.total_numel, h.shard_numel, h.padded_numel, h.padding) == (1857, shard, padded, pad)
+        assert h.local_shard_range().as_tuple() == (rank * shard, shard)
+        expect = oracle.pack_shard(host, group, rank)
+        assert np.array_equal(h.flat_param.detach().cpu().numpy().view(np.int32), expect.view(np.int32))
+        assert h.memory_summary()["padding_bytes"] == pad * 4
+    # pieces cover every parameter exactly once across the group
+    owned = sum(item.length for h in handles for item in h.local_piece_layout())
+    assert owned == 1857
+    full = handles[0].full_tensors(peer_shards=[h.flat_param for h in handles])
+    for (name, _), orig in zip(named, originals):
+        assert torch.equal(full[name], orig)
+    pieces = [p for h in handles for p in h.local_pieces()]
+    for (name, _), orig in zip(named, originals):
+        mine = [p for p in pieces if p.name == name]
+        assert torch.equal(reshard_state_dict_pieces(mine, tuple(orig.shape)), orig)
+
+
+def test_norm_weights_and_padding_runs(device):
+    _, _, handles = _handles(MLP_1857_REFERENCE, 4, device)
+    last = handles[-1]
+    runs = last.flat_param.gradient_norm_scale_runs
+    assert runs[-1] == (465 - 3, 3, 0.0)
+    vector = last.flat_param.gradient_norm_scale_vector
+    assert vector.shape == (465,) and float(vector[-3:].abs().sum()) == 0.0 and float(vector[0]) == 4.0
+
+
+@pytest.mark.parametrize("group", [1, 2, 3, 4])
+@pytest.mark.parametrize("in_dtype", [torch.float32, torch.bfloat16])
+def test_gradient_local_share_matches_oracle(device, group, in_dtype):
+    _, _, handles = _handles(MLP_1857_REFERENCE, group, device)
+    padded = handles[0].padded_numel
+    gen = torch.Generator(device=device).manual_seed(group)
+    grads = [(torch.randn(padded, device=device, generator=gen) * 1e-2).to(in_dtype) for _ in range(group)]
+    host = [g.float().cpu().numpy() for g in grads]
+    for rank, h in enumerate(handles):
+        out = h.reduce_scatter_gradient(grads[rank], peer_grads=grads if group > 1 else None)
+        valid = max(0, min(h.shard_numel, 1857 - rank * h.shard_numel))
+        expect = oracle.local_share(host, rank, h.shard_numel, valid, float(group) if group > 1 else 1.0)
+        assert np.array_equal(out.cpu().numpy().view(np.int32), expect.view(np.int32))
+        assert float(out[valid:].abs().sum()) == 0.0 if valid < h.shard_numel else True
+        assert h.reduction_count == 1
+
+
+def test_local_share_needs_every_rank(device):
+    _, _, handles = _handles(MLP_1857_REFERENCE, 2, device)
+    with pytest.raises(UnsupportedFeatureError, match="reduce-scatter needs every rank"):
+        handles[0].reduce_scatter_gradient(torch.zeros(handles[0].padded_numel, device=device))
+    with pytest.raises(UnsupportedFeatureError, match="needs every rank's shard"):
+        handles[0].full_tensors()
+
+
+def test_load_local_pieces_round_trip(device):
+    named, originals, handles = _handles(MLP_1857_BASELINE, 4, device)
+    state = {name: torch.randn_like(orig) for (name, _), orig in zip(named, originals)}
+    host = [state[name].cpu().numpy() for name, _ in named]
+    for rank, h in enumerate(handles):
+        h.load_local_pieces(state)
+        assert np.array_equal(h.flat_param.detach().cpu().numpy(), oracle.pack_shard(host, 4, rank))
+    full = handles[0].full_tensors(peer_shards=[h.flat_param for h in handles])
+    assert all(torch.equal(full[n], state[n]) for n in state)
+    with pytest.raises(ShardingError, match="missing parameter"):
+        handles[0].load_local_pieces({})
+    bad = dict(state)
+    bad["p0"] = torch.zeros(3, device=device)
+    with pytest.raises(ShardingError, match="shape mismatch"):
+        handles[0].load_local_pieces(bad)
+
+
+def test_mixed_precision_master_cast_and_gather(device):
+    named = _params(MLP_1857_REFERENCE, device, dtype=torch.bfloat16)
+    mp = MixedPrecisionConfig(enabled=True, param_dtype="bfloat16", reduce_dtype="float32", master_dtype="float32")
+    handles = [FlatParamHandle(named, None, GroupHandle.local_view("shard", 2, r), FSDPConfig(), mp, device,
+                               keep_originals=True) for r in range(2)]
+    host = [p.detach().float().cpu().numpy() for _, p in named]
+    for rank, h in enumerate(handles):
+        assert h.flat_param.dtype == torch.float32
+        assert np.array_equal(h.flat_param.detach().cpu().numpy(), oracle.pack_shard(host, 2, rank))
+    full = handles[0].gather_full([h.flat_param for h in handles])
+    assert full.dtype == torch.bfloat16 and full.numel() == 1858
+    expect = oracle.f32_to_bf16(np.concatenate([oracle.pack_shard(host, 2, r) for r in range(2)]))
+    assert np.array_equal(full.view(torch.int16).cpu().numpy().view(np.uint16), expect)
+
+
+def test_detaching_frees_originals_and_binds_views(device):
+    module = torch.nn.Linear(4, 3).to(device)
+    named = list(module.named_parameters())
+    locations = {id(p): [(module, n)] for n, p in named}
+    w = module.weight.detach().clone()
+    h = FlatParamHandle(named, locations, GroupHandle.trivial(), FSDPConfig(), MixedPrecisionConfig(), device)
+    assert "weight" not in module._parameters and module.weight.numel() == 0
+    full = h.gather_full()
+    h.bind_views(full)
+    assert torch.equal(module.weight, w)
+    with pytest.raises(ShardingError, match="at least one parameter"):
+        FlatParamHandle([], None, GroupHandle.trivial(), FSDPConfig(), MixedPrecisionConfig(), device)
