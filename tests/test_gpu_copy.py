@@ -20,9 +20,8 @@ pytestmark = pytest.mark.gpu
 
 def _bits(t: torch.Tensor) -> np.ndarray:
     t = t.detach().cpu().contiguous()
-    return {1: t.view(torch.uint8), 2: t.view(torch.int16), 4: t.view(torch.int32), 8: t.view(torch.int64)}[
-        t.element_size()
-    ].numpy().copy()
+    as_int = {1: torch.uint8, 2: torch.int16, 4: torch.int32, 8: torch.int64}[t.element_size()]
+    return t.view(as_int).numpy().copy()
 
 
 def _as_f32(bits16: np.ndarray) -> np.ndarray:

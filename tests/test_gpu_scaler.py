@@ -23,6 +23,8 @@ SCALE = 65536.0
 
 
 def _setup(param, defer=True):
+    # bf16 gradients on fp32 master parameters: torch requires the grad dtype to be declared.
+    param.grad_dtype = None
     opt = ShardedOptimizer([param], OptimizerConfig(learning_rate=3e-4, betas=(0.9, 0.95), weight_decay=0.1),
                            norm_group=GroupHandle.trivial(), device=param.device, defer_clip=defer)
     scaler = GradScaler(GradScalerConfig(enabled=True, init_scale=SCALE), GroupHandle.trivial(), param.device,
