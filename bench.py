@@ -57,6 +57,14 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--cpu-steps", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument(
+        "--workload",
+        choices=["adamw", "buckets", "reshard", "scaler"],
+        default="adamw",
+        help="adamw (default): the Llama-3-8B W=8 shard step above; buckets: GPT-2-small DDP bucket "
+        "pack + AVG divide at W=8; reshard: Llama-3-8B bf16 flat shards W=4 -> W=8 and W=2; scaler: "
+        "one Llama-3-70B W=8 rank shard with bf16 gradients, loss scale 2^16, clip and AdamW",
+    )
+    ap.add_argument(
         "--calibrate-copy",
         action="store_true",
         help="instead of the benchmark, run the library's interval-copy kernel over a 1 GiB fp32 "
@@ -129,6 +137,8 @@ def main() -> int:
     args = parse_args()
     if args.calibrate_copy:
         return calibrate_copy()
+    if args.workload != "adamw":
+        return SECONDARY[args.workload](args.steps, args.warmup)
     if args.gpus != 1:
         print(
             "bench.py measures one GPU: this build runs one rank's share of the work on one "
@@ -238,6 +248,194 @@ def main() -> int:
         result["cpu_baseline"] = cpu_baseline(args.cpu_numel, args.cpu_steps)
     print(json.dumps(result), flush=True)
     return 0
+
+
+# ---------------------------------------------------------------------------------------
+# Secondary workloads (one JSON line each; the default run is the AdamW shard step).
+# ---------------------------------------------------------------------------------------
+def _time_events(fn, steps: int, warmup: int) -> float:
+    """Mean milliseconds of fn() over `steps` runs, HIP events on the current stream."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / steps
+
+
+def _gpt2_small_shapes():
+    d, vocab, ctx = 768, 50257, 1024
+    named = [("wte.weight", (vocab, d)), ("wpe.weight", (ctx, d))]
+    for i in range(12):
+        p = f"h.{i}."
+        named += [(p + "ln_1.weight", (d,)), (p + "ln_1.bias", (d,)),
+                  (p + "attn.c_attn.weight", (d, 3 * d)), (p + "attn.c_attn.bias", (3 * d,)),
+                  (p + "attn.c_proj.weight", (d, d)), (p + "attn.c_proj.bias", (d,)),
+                  (p + "ln_2.weight", (d,)), (p + "ln_2.bias", (d,)),
+                  (p + "mlp.c_fc.weight", (d, 4 * d)), (p + "mlp.c_fc.bias", (4 * d,)),
+                  (p + "mlp.c_proj.weight", (4 * d, d)), (p + "mlp.c_proj.bias", (d,))]
+    return named + [("ln_f.weight", (d,)), ("ln_f.bias", (d,))]
+
+
+def _llama3_shapes(layers, d, ffn, kv_dim, vocab):
+    named = [("model.embed_tokens.weight", (vocab, d))]
+    for i in range(layers):
+        p = f"model.layers.{i}."
+        named += [(p + "self_attn.q_proj.weight", (d, d)), (p + "self_attn.k_proj.weight", (kv_dim, d)),
+                  (p + "self_attn.v_proj.weight", (kv_dim, d)), (p + "self_attn.o_proj.weight", (d, d)),
+                  (p + "mlp.gate_proj.weight", (ffn, d)), (p + "mlp.up_proj.weight", (ffn, d)),
+                  (p + "mlp.down_proj.weight", (d, ffn)), (p + "input_layernorm.weight", (d,)),
+                  (p + "post_attention_layernorm.weight", (d,))]
+    return named + [("model.norm.weight", (d,)), ("lm_head.weight", (vocab, d))]
+
+
+def _emit(metric, unit, value, ms, steps, warmup, dtype, workload, bytes_per_run, extra=None):
+    gbps = bytes_per_run / (ms * 1e-3) / 1e9
+    line = {
+        "metric": metric, "value": value, "unit": unit, "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": dtype,
+        "data": "synthetic (device-generated)", "config": {"workload": workload},
+        "roofline": {"bound": "hbm", "achieved": gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": gbps / HBM_PEAK_GBPS, "traffic": None},
+    }
+    if extra:
+        line["config"].update(extra)
+    print(json.dumps(line), flush=True)
+
+
+def bench_buckets(steps: int, warmup: int) -> int:
+    """GPT-2 small (124,439,808 fp32), 25 MiB buckets, pack + AVG divide at W=8: 8 B/param."""
+    import torch
+
+    from hybrid_training_amd import BucketedGradients, DDPConfig, GroupHandle
+
+    device = torch.device("cuda", 0)
+    named = [(n, torch.nn.Parameter(torch.empty(s, device=device))) for n, s in _gpt2_small_shapes()]
+    gen = torch.Generator(device=device).manual_seed(2)
+    grads = [torch.randn(p.shape, device=device, generator=gen).mul_(1e-3) for _, p in named]
+    ddp = BucketedGradients(named, GroupHandle.local_view("data_parallel", 8, 0), DDPConfig(bucket_cap_mb=25.0))
+    n = sum(p.numel() for _, p in named)
+
+    def run():
+        for (_, p), g in zip(named, grads):
+            p.grad = g
+        ddp.pack()
+
+    ms = _time_events(run, max(steps, 20), max(warmup, 3))
+    _emit("DDP bucket pack + AVG divide: params/s", "params/s", n / (ms * 1e-3), ms, max(steps, 20),
+          max(warmup, 3), "f32", "GPT-2 small gradients, 17 buckets of <= 25 MiB, W=8", 8 * n,
+          {"params": n, "buckets": len(ddp.buckets), "bytes_per_param": 8})
+    return 0
+
+
+def bench_reshard(steps: int, warmup: int) -> int:
+    """Llama-3-8B bf16 (8,030,261,248) saved by 4 ranks, loaded by 8 and by 2: 4 B/elem per re-slice."""
+    import torch
+
+    from hybrid_training_amd import (DeviceShardCache, PieceLayout, ShardRange, ShardRecord, TensorRecord,
+                                     intersect_ranges, load_flat_shard, shard_filename)
+
+    device = torch.device("cuda", 0)
+    shapes = _llama3_shapes(32, 4096, 14336, 1024, 128256)
+    numels = [int(torch.Size(s).numel()) for _, s in shapes]
+    total = sum(numels)
+    s_src = total // 4
+    gen = torch.Generator(device=device).manual_seed(4)
+    shards = [torch.randint(-(2**15), 2**15, (s_src,), dtype=torch.int16, device=device, generator=gen)
+              .view(torch.bfloat16) for _ in range(4)]
+    records, cache, cursor = {}, DeviceShardCache(), 0
+    for (name, shape), numel in zip(shapes, numels):
+        rec = TensorRecord(key=name, name=name, global_shape=tuple(shape), dtype="torch.bfloat16")
+        for rank in range(4):
+            ov = intersect_ranges(ShardRange(rank * s_src, s_src), ShardRange(cursor, numel))
+            if ov is None:
+                continue
+            key = f"model::{name}@{ov.start - cursor}"
+            rec.shards.append(ShardRecord(rank=rank, file=shard_filename(rank), offset=ov.start - cursor,
+                                          length=ov.length, key=key))
+            cache.add(shard_filename(rank), key, shards[rank][ov.start - rank * s_src : ov.end - rank * s_src])
+        records[name] = rec
+        cursor += numel
+    for w_dst in (8, 2):
+        s_dst = -(-total // w_dst)
+        dests = [torch.empty(s_dst, dtype=torch.bfloat16, device=device) for _ in range(w_dst)]
+        layouts = []
+        for rank in range(w_dst):
+            local, items, cur = ShardRange(rank * s_dst, s_dst), [], 0
+            for (name, shape), numel in zip(shapes, numels):
+                ov = intersect_ranges(local, ShardRange(cur, numel))
+                if ov is not None:
+                    items.append(PieceLayout(name, tuple(shape), ov.start - cur, ov.length, ov.start - local.start))
+                cur += numel
+            layouts.append(items)
+
+        def run():
+            for dest, items in zip(dests, layouts):
+                load_flat_shard(dest, items, records, cache)
+
+        ms = _time_events(run, max(steps, 5), max(warmup, 2))
+        _emit("flat-interval reshard: elements/s", "elements/s", total / (ms * 1e-3), ms, max(steps, 5),
+              max(warmup, 2), "bf16", f"Llama-3-8B bf16 flat shards, W=4 -> W={w_dst}", 4 * total,
+              {"elements": total, "bytes_per_element": 4})
+        del dests
+        torch.cuda.empty_cache()
+    return 0
+
+
+def bench_scaler(steps: int, warmup: int) -> int:
+    """One Llama-3-70B FSDP rank at W=8: 8,819,213,312 fp32 master params, bf16 grads at scale 2^16.
+
+    Clean step: fused unscale + inf check + norm (2 B/param) and unscale + clip + AdamW
+    (26 B/param) = 28 B/param.  Overflowing step: the check pass only (2 B/param), then skip.
+    """
+    import torch
+
+    from hybrid_training_amd import GradScaler, GradScalerConfig, GroupHandle, OptimizerConfig, ShardedOptimizer
+
+    device = torch.device("cuda", 0)
+    n = 8_819_213_312
+    gen = torch.Generator(device=device).manual_seed(70)
+    param = torch.nn.Parameter(torch.empty(n, device=device))
+    param.grad_dtype = None
+    grad = torch.empty(n, dtype=torch.bfloat16, device=device)
+    for start in range(0, n, 1 << 30):
+        stop = min(n, start + (1 << 30))
+        param.data[start:stop].normal_(0.0, 0.02, generator=gen)
+        grad[start:stop] = torch.randn(stop - start, device=device, generator=gen).mul_(1e-4 * 65536).to(torch.bfloat16)
+    opt = ShardedOptimizer([param], OptimizerConfig(learning_rate=3e-4, betas=(0.9, 0.95), weight_decay=0.1),
+                           norm_group=GroupHandle.trivial("world"), device=device, defer_clip=True)
+    scaler = GradScaler(GradScalerConfig(enabled=True, init_scale=65536.0, growth_interval=10**9),
+                        GroupHandle.trivial("world"), device, defer_unscale=True)
+
+    def engine_step():
+        param.grad = grad
+        scaler.unscale_([param])
+        opt.clip_grad_norm(1.0)
+        stepped = scaler.step(opt, [param], already_unscaled=True)
+        scaler.update(found_non_finite=False)  # keep the scale fixed across timed steps
+        opt.zero_grad(set_to_none=True)
+        return stepped
+
+    ms = _time_events(engine_step, max(steps, 5), max(warmup, 2))
+    _emit("loss-scaled clipped AdamW step (bf16 grads): params/s", "params/s", n / (ms * 1e-3), ms,
+          max(steps, 5), max(warmup, 2), "f32", "Llama-3-70B FSDP rank shard at W=8, bf16 grads, scale 2^16",
+          28 * n, {"params": n, "bytes_per_param": 28, "skipped": False})
+    bad = torch.randint(0, n, (n // 1000,), device=device, generator=gen)
+    grad[bad] = float("inf")
+    ms = _time_events(engine_step, max(steps, 5), max(warmup, 2))
+    _emit("loss-scaled step with 0.1% inf gradients (skipped): params/s", "params/s", n / (ms * 1e-3), ms,
+          max(steps, 5), max(warmup, 2), "bf16", "Llama-3-70B FSDP rank shard at W=8, bf16 grads, 0.1% inf",
+          2 * n, {"params": n, "bytes_per_param": 2, "skipped": True})
+    return 0
+
+
+SECONDARY = {"buckets": bench_buckets, "reshard": bench_reshard, "scaler": bench_scaler}
 
 
 if __name__ == "__main__":

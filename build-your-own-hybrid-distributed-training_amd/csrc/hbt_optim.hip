@@ -24,11 +24,14 @@ constexpr int kAdamBlock = 64;
 constexpr int kAdamUnroll = 2;
 constexpr int64_t kAdamTile = int64_t(kAdamBlock) * 4 * kAdamUnroll;
 
-// Norm: 1024-thread workgroups, each summing one contiguous chunk of 8 tiles.
+// Norm: 1024-thread workgroups, each summing one contiguous chunk of 8 tiles; a tile
+// is one 16-byte load per lane (4 fp32 or 8 bf16 gradients).
 constexpr int kNormBlock = 1024;
-constexpr int64_t kNormTile = int64_t(kNormBlock) * 4;
 constexpr int kNormTilesPerChunk = 8;
-constexpr int64_t kNormChunk = kNormTile * kNormTilesPerChunk;
+template <typename GradT>
+constexpr int64_t norm_tile() { return int64_t(kNormBlock) * (16 / sizeof(GradT)); }
+template <typename GradT>
+constexpr int64_t norm_chunk() { return norm_tile<GradT>() * kNormTilesPerChunk; }
 
 // ---- 16-byte memory helpers ------------------------------------------------------
 // Every operand is touched exactly once per step, so loads and stores are marked
@@ -45,6 +48,15 @@ __device__ __forceinline__ f32x4 ld_grad4_nt(const uint16_t* p) {
     const u32x2 w = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
     return f32x4{bf16_to_f32(w.x & 0xFFFFu), bf16_to_f32(w.x >> 16), bf16_to_f32(w.y & 0xFFFFu),
                  bf16_to_f32(w.y >> 16)};
+}
+// Eight bf16 gradients (one 16-byte load) widened to fp32, as two 4-vectors.
+__device__ __forceinline__ void ld_bf16x8_nt(const uint16_t* p, f32x4& lo, f32x4& hi) {
+    typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+    const u32x4v w = __builtin_nontemporal_load(reinterpret_cast<const u32x4v*>(p));
+    lo = f32x4{bf16_to_f32(w.x & 0xFFFFu), bf16_to_f32(w.x >> 16), bf16_to_f32(w.y & 0xFFFFu),
+               bf16_to_f32(w.y >> 16)};
+    hi = f32x4{bf16_to_f32(w.z & 0xFFFFu), bf16_to_f32(w.z >> 16), bf16_to_f32(w.w & 0xFFFFu),
+               bf16_to_f32(w.w >> 16)};
 }
 __device__ __forceinline__ float ld_grad1(const float* p) { return *p; }
 __device__ __forceinline__ float ld_grad1(const uint16_t* p) { return bf16_to_f32(*p); }
@@ -170,32 +182,46 @@ __device__ __forceinline__ double sq(float x) {
     return d * d;
 }
 
-// Workgroup c sums chunk c of the concatenated tensors (kNormChunk elements of one
-// tensor) into partials[c].  Inside a thread the squares are added in element order;
+// Workgroup c sums chunk c of the concatenated tensors (8 tiles of one tensor: 32768
+// fp32 or 65536 bf16 elements) into partials[c].  Inside a thread the squares are added in element order;
 // threads and waves are combined by the fixed trees of block_sum, so the partials,
 // and the sum of them, depend only on the data and the numels.
 template <typename GradT, bool kUnscale>
 __global__ __launch_bounds__(kNormBlock) void sqnorm_kernel(NormTable tab, float unscale,
                                                             double* __restrict__ partials) {
+    constexpr int64_t kTile = norm_tile<GradT>();
+    constexpr int64_t kChunk = norm_chunk<GradT>();
     const int64_t chunk = blockIdx.x;
     int t = 0;
     while (t + 1 < tab.count && chunk >= tab.first_chunk[t + 1]) ++t;
-    const int64_t start = (chunk - tab.first_chunk[t]) * kNormChunk;
+    const int64_t start = (chunk - tab.first_chunk[t]) * kChunk;
     const int64_t n = tab.n[t];
     const GradT* __restrict__ G = static_cast<const GradT*>(tab.g[t]);
     double acc = 0.0;
     for (int k = 0; k < kNormTilesPerChunk; ++k) {
-        const int64_t base = start + int64_t(k) * kNormTile;
+        const int64_t base = start + int64_t(k) * kTile;
         if (base >= n) break;
-        if (tab.vec_ok[t] && base + kNormTile <= n) {
-            f32x4 x = ld_grad4_nt(G + base + int64_t(threadIdx.x) * 4);
+        if (tab.vec_ok[t] && base + kTile <= n) {
+            f32x4 x, y;
+            if constexpr (sizeof(GradT) == 4) {
+                x = ld_grad4_nt(G + base + int64_t(threadIdx.x) * 4);
+            } else {
+                ld_bf16x8_nt(G + base + int64_t(threadIdx.x) * 8, x, y);
+            }
             if constexpr (kUnscale) x = x * unscale;
             acc += sq(x.x);
             acc += sq(x.y);
             acc += sq(x.z);
             acc += sq(x.w);
+            if constexpr (sizeof(GradT) == 2) {
+                if constexpr (kUnscale) y = y * unscale;
+                acc += sq(y.x);
+                acc += sq(y.y);
+                acc += sq(y.z);
+                acc += sq(y.w);
+            }
         } else {
-            const int64_t end = base + kNormTile < n ? base + kNormTile : n;
+            const int64_t end = base + kTile < n ? base + kTile : n;
             for (int64_t e = base + threadIdx.x; e < end; e += kNormBlock) {
                 float x = ld_grad1(G + e);
                 if constexpr (kUnscale) x = x * unscale;
@@ -212,9 +238,18 @@ constexpr int kFinalBlock = 1024;
 __global__ __launch_bounds__(kFinalBlock) void norm_finalize_kernel(
     const double* __restrict__ partials, int64_t count, double max_norm, double* __restrict__ sum_out,
     double* __restrict__ norm_out, float* __restrict__ grad_mul_out, int32_t* __restrict__ nonfinite_out) {
-    double acc = 0.0;
-    for (int64_t i = threadIdx.x; i < count; i += kFinalBlock) acc += partials[i];
-    const double total = block_sum<kFinalBlock>(acc);
+    // Four independent accumulators per thread keep four loads in flight; they are
+    // combined in a fixed order, so the sum stays reproducible.
+    double a0 = 0.0, a1 = 0.0, a2 = 0.0, a3 = 0.0;
+    int64_t i = threadIdx.x;
+    for (; i + 3 * kFinalBlock < count; i += 4 * kFinalBlock) {
+        a0 += partials[i];
+        a1 += partials[i + kFinalBlock];
+        a2 += partials[i + 2 * kFinalBlock];
+        a3 += partials[i + 3 * kFinalBlock];
+    }
+    for (; i < count; i += kFinalBlock) a0 += partials[i];
+    const double total = block_sum<kFinalBlock>((a0 + a1) + (a2 + a3));
     if (threadIdx.x != 0) return;
     // clamp_min(0) keeps NaN; sqrt of fp64 is correctly rounded.
     const double clamped = total < 0.0 ? 0.0 : total;
@@ -364,12 +399,14 @@ int32_t hbt_adamw_step(float* const* params, const void* const* grads, float* co
     return check_launch("hbt_adamw_step");
 }
 
-int64_t hbt_norm_partials_count(const int64_t* numels, int32_t count) {
+int64_t hbt_norm_partials_count(const int64_t* numels, int32_t count, int32_t grad_dtype) {
     if (count < 0 || count > kMaxT || (count > 0 && numels == nullptr)) return -1;
+    if (grad_dtype != HBT_DTYPE_F32 && grad_dtype != HBT_DTYPE_BF16) return -1;
+    const int64_t chunk = grad_dtype == HBT_DTYPE_F32 ? norm_chunk<float>() : norm_chunk<uint16_t>();
     int64_t chunks = 0;
     for (int i = 0; i < count; ++i) {
         if (numels[i] < 0) return -1;
-        chunks += (numels[i] + kNormChunk - 1) / kNormChunk;
+        chunks += (numels[i] + chunk - 1) / chunk;
     }
     return chunks;
 }
@@ -392,7 +429,8 @@ int32_t hbt_grad_sqnorm_partials(const void* const* grads, const int64_t* numels
     }
     NormTable tab{};
     tab.count = count;
-    const uintptr_t grad_align = grad_dtype == HBT_DTYPE_F32 ? 16 : 8;
+    const uintptr_t grad_align = 16;
+    const int64_t kChunk = grad_dtype == HBT_DTYPE_F32 ? norm_chunk<float>() : norm_chunk<uint16_t>();
     int64_t chunks = 0;
     for (int i = 0; i < count; ++i) {
         if (numels[i] < 0 || (numels[i] > 0 && grads[i] == nullptr)) {
@@ -404,7 +442,7 @@ int32_t hbt_grad_sqnorm_partials(const void* const* grads, const int64_t* numels
         tab.w[i] = weights[i];
         tab.vec_ok[i] = aligned(grads[i], grad_align);
         tab.first_chunk[i] = chunks;
-        chunks += (numels[i] + kNormChunk - 1) / kNormChunk;
+        chunks += (numels[i] + kChunk - 1) / kChunk;
     }
     tab.first_chunk[count] = chunks;
     for (int i = count + 1; i <= kMaxT; ++i) tab.first_chunk[i] = chunks;

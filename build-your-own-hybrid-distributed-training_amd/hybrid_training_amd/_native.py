@@ -17,6 +17,7 @@ from __future__ import annotations
 import ctypes
 import os
 import threading
+from collections import OrderedDict
 from collections.abc import Sequence
 
 import torch
@@ -44,7 +45,7 @@ __all__ = [
     "stream_of",
 ]
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 MAX_TENSORS_PER_LAUNCH = 16
 MAX_LOCAL_RANKS = 64
 
@@ -78,7 +79,7 @@ EXPORTED_SYMBOLS: dict[str, tuple[object, tuple[object, ...]]] = {
             _c_void_p,
         ),
     ),
-    "hbt_norm_partials_count": (_c_i64, (_i64_array, _c_i32)),
+    "hbt_norm_partials_count": (_c_i64, (_i64_array, _c_i32, _c_i32)),
     "hbt_grad_sqnorm_partials": (
         _c_i32,
         (_ptr_array, _i64_array, _f64_array, _c_i32, _c_i32, _c_f32, _c_void_p, _c_void_p),
@@ -104,6 +105,13 @@ EXPORTED_SYMBOLS: dict[str, tuple[object, tuple[object, ...]]] = {
 
 _LOCK = threading.Lock()
 _LIB: ctypes.CDLL | None = None
+
+# Device copies of interval tables, keyed by their exact content.  A table is a pure
+# function of its rows (addresses, lengths, chunk prefix), so an entry stays valid
+# even after the tensors it was built for are freed; reuse skips the host-to-device
+# upload, which for a few hundred rows costs more than moving a GB on the device.
+_TABLE_CACHE: "OrderedDict[tuple, torch.Tensor]" = OrderedDict()
+_TABLE_CACHE_SIZE = 256
 
 
 def library_path() -> str:
@@ -248,6 +256,32 @@ def double_array(values: Sequence[float]) -> ctypes.Array:
     return (ctypes.c_double * max(1, len(values)))(*values)
 
 
+_CHUNK: int | None = None
+
+
+def _copy_chunk(lib: ctypes.CDLL) -> int:
+    global _CHUNK
+    if _CHUNK is None:
+        _CHUNK = int(lib.hbt_copy_chunk_elems())
+    return _CHUNK
+
+
+def _device_table(flat: tuple[int, ...], device: torch.device) -> torch.Tensor:
+    """The int64 table on ``device``, uploaded once per distinct content and stream."""
+    key = (device, stream_of(device), flat)
+    table = _TABLE_CACHE.get(key)
+    if table is not None:
+        _TABLE_CACHE.move_to_end(key)
+        return table
+    host = torch.tensor(flat, dtype=torch.int64).pin_memory()
+    with torch.cuda.device(device):
+        table = host.to(device, non_blocking=True)
+    _TABLE_CACHE[key] = table
+    if len(_TABLE_CACHE) > _TABLE_CACHE_SIZE:
+        _TABLE_CACHE.popitem(last=False)
+    return table
+
+
 class CopyPlan:
     """Interval table for one ``hbt_copy_intervals`` launch.
 
@@ -318,14 +352,14 @@ class CopyPlan:
             src_code = dst_code = DTYPE_F32
             scale = 2
         lib = library()
-        chunk = int(lib.hbt_copy_chunk_elems())
+        chunk = _copy_chunk(lib)
         flat: list[int] = []
         first = 0
         for src_addr, dst_addr, n in self._rows:
             n_units = n * scale
             flat.extend((src_addr, dst_addr, n_units, first))
             first += -(-n_units // chunk)
-        table = torch.tensor(flat, dtype=torch.int64).to(self.device)
+        table = _device_table(tuple(flat), self.device)
         with torch.cuda.device(self.device):
             status = lib.hbt_copy_intervals(
                 table.data_ptr(),

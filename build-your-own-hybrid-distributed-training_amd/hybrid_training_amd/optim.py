@@ -243,7 +243,7 @@ def gradient_norm_pass(
         for start in range(0, len(items), _native.MAX_TENSORS_PER_LAUNCH):
             chunk = items[start : start + _native.MAX_TENSORS_PER_LAUNCH]
             count = int(lib.hbt_norm_partials_count(_native.int64_array([n for _, _, n, _ in chunk]),
-                                                    len(chunk)))
+                                                    len(chunk), _native.dtype_code(dtype)))
             launches.append((dtype, unscale, chunk, total_partials))
             total_partials += count
     partials = torch.empty(max(1, total_partials), dtype=torch.float64, device=device)

@@ -86,14 +86,14 @@ int32_t hbt_adamw_step(float* const* params, const void* const* grads, float* co
  *   summed by distributed_gradient_norm (optim/sharded_optimizer.py:236-238).
  * Computes sum_i weights[i] * sum_j (double)(g_ij * unscale)^2 over up to
  * HBT_MAX_TENSORS_PER_LAUNCH gradient tensors (grad_dtype F32 or BF16), writing
- * hbt_norm_partials_count(numels, count) doubles to partials: one per chunk of
- * 32768 consecutive elements of one tensor, already multiplied by that tensor's
- * weight.  The chunk -> partial map and every summation order depend only on the
+ * hbt_norm_partials_count(numels, count, grad_dtype) doubles to partials: one per
+ * chunk of consecutive elements of one tensor (32768 fp32 or 65536 bf16), already
+ * multiplied by that tensor's weight.  The chunk -> partial map and every summation order depend only on the
  * numels, so the result is bitwise reproducible.  A non-finite element makes the
  * sum non-finite, which is the overflow signal of GradScaler._detect_non_finite
  * (optim/grad_scaler.py:189-200).
  * ---------------------------------------------------------------------------- */
-int64_t hbt_norm_partials_count(const int64_t* numels, int32_t count);
+int64_t hbt_norm_partials_count(const int64_t* numels, int32_t count, int32_t grad_dtype);
 int32_t hbt_grad_sqnorm_partials(const void* const* grads, const int64_t* numels,
                                  const double* weights, int32_t count, int32_t grad_dtype,
                                  float unscale, double* partials, void* stream);

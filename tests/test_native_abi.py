@@ -34,8 +34,10 @@ def test_library_loads_and_exports_every_declared_symbol():
         assert hasattr(lib, name), name
     assert lib.hbt_abi_version() == _native.ABI_VERSION
     assert lib.hbt_symbol_count() == len(_declared_functions())
-    assert lib.hbt_norm_partials_count(_native.int64_array([1, 32768, 32769]), 3) == 1 + 1 + 2
-    assert lib.hbt_norm_partials_count(None, 99) == -1
+    assert lib.hbt_norm_partials_count(_native.int64_array([1, 32768, 32769]), 3, 0) == 1 + 1 + 2
+    assert lib.hbt_norm_partials_count(_native.int64_array([1, 65536, 65537]), 3, 1) == 1 + 1 + 2
+    assert lib.hbt_norm_partials_count(None, 99, 0) == -1
+    assert lib.hbt_norm_partials_count(_native.int64_array([1]), 1, 7) == -1
     assert lib.hbt_copy_chunk_elems() > 0
     assert lib.hbt_last_error() == b""
 
