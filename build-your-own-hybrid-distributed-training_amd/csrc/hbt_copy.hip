@@ -3,98 +3,91 @@
 // One launch moves any number of [src, src + n) -> [dst, dst + n) intervals.  Each
 // interval is cut into chunks of kCopyChunk elements; one workgroup owns one chunk
 // and finds its interval by binary search over the records' first_chunk column.  Inside
-// a chunk the destination is written with aligned 16-byte stores; the source is read
-// with aligned 16-byte loads and shifted into place with v_alignbyte, so intervals at
-// any element offset stream at full width.  A load never touches a 16-byte block that
-// holds no byte of the source interval.
+// a chunk each lane moves units of 16 / max(source, destination element bytes)
+// elements, consecutive lanes taking consecutive units, so every load and store
+// instruction of a wave covers one contiguous span.  The destination is written with
+// aligned stores; the source is read with aligned loads of the unit's width and
+// shifted into place with v_alignbyte, so intervals at any element offset stream at
+// full width.  A load never touches an aligned block that holds no byte of the source
+// interval.
 #include "hbt_common.hpp"
 
 namespace hbt {
 namespace {
 
-// One wavefront per workgroup and one 8-element unit per lane: a workgroup moves a
-// 512-element chunk and retires.  Measured on MI355X (Llama-3-8B bf16 reshard, 32 GB
-// moved), this shape sustains 6.3 TB/s against 5.0 TB/s for 256-thread workgroups
-// walking 64K-element chunks.
+// One wavefront per workgroup: a workgroup moves a 512-element chunk and retires.
+// Measured on MI355X (Llama-3-8B bf16 reshard, 32 GB moved), this shape sustains
+// 6.3 TB/s against 5.0 TB/s for 256-thread workgroups walking 64K-element chunks.
 #ifndef HBT_COPY_BLOCK
 #define HBT_COPY_BLOCK 64
 #endif
 #ifndef HBT_COPY_CHUNK
 #define HBT_COPY_CHUNK 512
 #endif
-#ifndef HBT_COPY_UNROLL
-#define HBT_COPY_UNROLL 1
-#endif
 #ifndef HBT_COPY_NT
 #define HBT_COPY_NT 1
 #endif
 constexpr int kCopyBlock = HBT_COPY_BLOCK;
 constexpr int64_t kCopyChunk = HBT_COPY_CHUNK;  // elements per block
-constexpr int kCopyUnroll = HBT_COPY_UNROLL;    // 8-element units per thread per iteration
 constexpr bool kCopyNT = HBT_COPY_NT != 0;
 
-typedef uint32_t u32x4_nt __attribute__((ext_vector_type(4)));
-// 16-byte load/store, non-temporal when kCopyNT: every byte is moved exactly once.
-__device__ __forceinline__ u32x4_nt ld16(const void* p) {
-    if constexpr (kCopyNT) return __builtin_nontemporal_load(reinterpret_cast<const u32x4_nt*>(p));
-    return *reinterpret_cast<const u32x4_nt*>(p);
+// Aligned vector load/store of NW dwords (NW = 2 or 4), non-temporal when kCopyNT:
+// every byte is moved exactly once.
+template <int NW>
+struct Vec {
+    typedef uint32_t type __attribute__((ext_vector_type(NW)));
+};
+template <int NW>
+__device__ __forceinline__ typename Vec<NW>::type ldv(const void* p) {
+    typedef typename Vec<NW>::type V;
+    if constexpr (kCopyNT) return __builtin_nontemporal_load(reinterpret_cast<const V*>(p));
+    return *reinterpret_cast<const V*>(p);
 }
-__device__ __forceinline__ void st16(void* p, u32x4_nt x) {
+template <int NW>
+__device__ __forceinline__ void stv(void* p, typename Vec<NW>::type x) {
+    typedef typename Vec<NW>::type V;
     if constexpr (kCopyNT) {
-        __builtin_nontemporal_store(x, reinterpret_cast<u32x4_nt*>(p));
+        __builtin_nontemporal_store(x, reinterpret_cast<V*>(p));
     } else {
-        *reinterpret_cast<u32x4_nt*>(p) = x;
+        *reinterpret_cast<V*>(p) = x;
     }
 }
 
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-// Loads NW dwords starting at byte address `s`, where `k` = s & 15 (uniform across the
-// wave).  For k != 0 one extra aligned block is read; it holds source bytes s+NW*4-1
-// and earlier ones only up to the block boundary, so it lies inside the source's page.
+// Loads NW dwords (NW = 2 or 4: one 8- or 16-byte block) starting at byte address
+// `s`, where `k` = s mod 4*NW (uniform across the wave).  For k != 0 one extra aligned
+// block is read; it holds source bytes s + 4*NW - 1 and earlier ones only up to the
+// block boundary, so it lies inside the source's page.
 template <int NW>
 __device__ __forceinline__ void load_shifted(const uint8_t* s, uint32_t k, uint32_t (&out)[NW]) {
-    static_assert(NW == 4 || NW == 8, "units are 16 or 32 bytes");
-    constexpr int kBlocks = NW / 4;
+    static_assert(NW == 2 || NW == 4, "units are 8 or 16 bytes");
     const uint8_t* a = s - k;
+    const typename Vec<NW>::type x = ldv<NW>(a);
     if (k == 0) {
 #pragma unroll
-        for (int b = 0; b < kBlocks; ++b) {
-            const u32x4 x = ld16(a + 16 * b);
-            out[4 * b + 0] = x.x;
-            out[4 * b + 1] = x.y;
-            out[4 * b + 2] = x.z;
-            out[4 * b + 3] = x.w;
-        }
+        for (int i = 0; i < NW; ++i) out[i] = x[i];
         return;
     }
-    uint32_t w[NW + 4];
+    const typename Vec<NW>::type y = ldv<NW>(a + 4 * NW);
+    uint32_t w[2 * NW];
 #pragma unroll
-    for (int b = 0; b <= kBlocks; ++b) {
-        const u32x4 x = ld16(a + 16 * b);
-        w[4 * b + 0] = x.x;
-        w[4 * b + 1] = x.y;
-        w[4 * b + 2] = x.z;
-        w[4 * b + 3] = x.w;
+    for (int i = 0; i < NW; ++i) {
+        w[i] = x[i];
+        w[NW + i] = y[i];
     }
     const uint32_t r = k & 3u;
-    switch (k >> 2) {
-        case 0:
+    const uint32_t q = k >> 2;  // whole dwords to skip, < NW
 #pragma unroll
-            for (int i = 0; i < NW; ++i) out[i] = __builtin_amdgcn_alignbyte(w[i + 1], w[i], r);
-            break;
-        case 1:
+    for (int i = 0; i < NW; ++i) {
+        // Select w[i + q] and w[i + q + 1] with q uniform; unrolled over q's range.
+        uint32_t lo = w[i], hi = w[i + 1];
 #pragma unroll
-            for (int i = 0; i < NW; ++i) out[i] = __builtin_amdgcn_alignbyte(w[i + 2], w[i + 1], r);
-            break;
-        case 2:
-#pragma unroll
-            for (int i = 0; i < NW; ++i) out[i] = __builtin_amdgcn_alignbyte(w[i + 3], w[i + 2], r);
-            break;
-        default:
-#pragma unroll
-            for (int i = 0; i < NW; ++i) out[i] = __builtin_amdgcn_alignbyte(w[i + 4], w[i + 3], r);
-            break;
+        for (int j = 1; j < NW; ++j) {
+            if (q == static_cast<uint32_t>(j)) {
+                lo = w[i + j];
+                hi = w[i + j + 1];
+            }
+        }
+        out[i] = __builtin_amdgcn_alignbyte(hi, lo, r);
     }
 }
 
@@ -133,28 +126,36 @@ __device__ __forceinline__ void store_elem(uint8_t* p, uint32_t bits) {
     }
 }
 
-// Unpack the 8 elements held in `words` (SB bytes each) into element bit patterns.
-template <int SB>
-__device__ __forceinline__ void unpack8(const uint32_t (&words)[2 * SB], uint32_t (&e)[8]) {
+// Elements per lane unit: one 16-byte access on the wider side of the copy.
+template <int SB, int DB>
+constexpr int unit_elems() { return 16 / (SB > DB ? SB : DB); }
+
+// Unpack the U elements held in `words` (SB bytes each) into element bit patterns.
+template <int SB, int U>
+__device__ __forceinline__ void unpack_unit(const uint32_t (&words)[U * SB / 4], uint32_t (&e)[U]) {
     if constexpr (SB == 4) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) e[i] = words[i];
+        for (int i = 0; i < U; ++i) e[i] = words[i];
     } else {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < U / 2; ++i) {
             e[2 * i] = words[i] & 0xFFFFu;
             e[2 * i + 1] = words[i] >> 16;
         }
     }
 }
-template <int DB>
-__device__ __forceinline__ void pack8_store(uint8_t* d, const uint32_t (&e)[8]) {
+template <int DB, int U>
+__device__ __forceinline__ void pack_unit_store(uint8_t* d, const uint32_t (&e)[U]) {
+    constexpr int NW = U * DB / 4;
+    typename Vec<NW>::type x;
     if constexpr (DB == 4) {
-        st16(d, u32x4{e[0], e[1], e[2], e[3]});
-        st16(d + 16, u32x4{e[4], e[5], e[6], e[7]});
+#pragma unroll
+        for (int i = 0; i < U; ++i) x[i] = e[i];
     } else {
-        st16(d, u32x4{e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16), e[6] | (e[7] << 16)});
+#pragma unroll
+        for (int i = 0; i < U / 2; ++i) x[i] = e[2 * i] | (e[2 * i + 1] << 16);
     }
+    stv<NW>(d, x);
 }
 
 template <int SB, int DB, int OP>
@@ -185,8 +186,9 @@ __global__ __launch_bounds__(kCopyBlock) void copy_kernel(const int64_t* __restr
     // Head: elements until the destination is 16-byte aligned.
     int64_t head = static_cast<int64_t>(((16u - (reinterpret_cast<uintptr_t>(d) & 15u)) & 15u) / DB);
     if (head > len) head = len;
-    const int64_t units = (len - head) / 8;
-    const int64_t tail_begin = head + units * 8;
+    constexpr int U = unit_elems<SB, DB>();
+    const int64_t units = (len - head) / U;
+    const int64_t tail_begin = head + units * U;
 
     if (threadIdx.x < head) {
         const int64_t e = threadIdx.x;
@@ -202,37 +204,24 @@ __global__ __launch_bounds__(kCopyBlock) void copy_kernel(const int64_t* __restr
     uint8_t* dbody = d + head * DB;
     if (s == nullptr) {
         for (int64_t u = threadIdx.x; u < units; u += kCopyBlock) {
-            const uint32_t zero[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-            pack8_store<DB>(dbody + u * 8 * DB, zero);
+            uint32_t zero[U];
+#pragma unroll
+            for (int i = 0; i < U; ++i) zero[i] = 0u;
+            pack_unit_store<DB, U>(dbody + u * U * DB, zero);
         }
         return;
     }
     const uint8_t* sbody = s + head * SB;
-    const uint32_t k = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(sbody) & 15u);
-    int64_t u = threadIdx.x;
-    for (; u + int64_t(kCopyUnroll - 1) * kCopyBlock < units; u += int64_t(kCopyUnroll) * kCopyBlock) {
-        uint32_t words[kCopyUnroll][2 * SB];
+    constexpr int kSrcWords = U * SB / 4;
+    const uint32_t k = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(sbody) & (4u * kSrcWords - 1u));
+    for (int64_t u = threadIdx.x; u < units; u += kCopyBlock) {
+        uint32_t words[kSrcWords];
+        load_shifted<kSrcWords>(sbody + u * U * SB, k, words);
+        uint32_t e[U];
+        unpack_unit<SB, U>(words, e);
 #pragma unroll
-        for (int j = 0; j < kCopyUnroll; ++j) {
-            load_shifted<2 * SB>(sbody + (u + int64_t(j) * kCopyBlock) * 8 * SB, k, words[j]);
-        }
-#pragma unroll
-        for (int j = 0; j < kCopyUnroll; ++j) {
-            uint32_t e[8];
-            unpack8<SB>(words[j], e);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) e[i] = convert<SB, DB, OP>(e[i], divisor);
-            pack8_store<DB>(dbody + (u + int64_t(j) * kCopyBlock) * 8 * DB, e);
-        }
-    }
-    for (; u < units; u += kCopyBlock) {
-        uint32_t words[2 * SB];
-        load_shifted<2 * SB>(sbody + u * 8 * SB, k, words);
-        uint32_t e[8];
-        unpack8<SB>(words, e);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) e[i] = convert<SB, DB, OP>(e[i], divisor);
-        pack8_store<DB>(dbody + u * 8 * DB, e);
+        for (int i = 0; i < U; ++i) e[i] = convert<SB, DB, OP>(e[i], divisor);
+        pack_unit_store<DB, U>(dbody + u * U * DB, e);
     }
 }
 

@@ -299,6 +299,17 @@ class CopyPlan:
     def __len__(self) -> int:
         return len(self._rows)
 
+    @classmethod
+    def from_rows(cls, device: torch.device, rows: list[tuple[int, int, int]]) -> "CopyPlan":
+        """A plan over rows ``(source address or 0 for a zero fill, destination address, n)``.
+
+        For callers that have already checked every address against a dense device
+        tensor of the plan's dtypes and every extent against that tensor's end.
+        """
+        plan = cls(device)
+        plan._rows = [row for row in rows if row[2] > 0]
+        return plan
+
     def add(self, src: torch.Tensor, src_offset: int, dst: torch.Tensor, dst_offset: int, n: int) -> None:
         """Queue ``dst[dst_offset : dst_offset + n] = src[src_offset : src_offset + n]``."""
         require_device_tensor(src, "native.CopyPlan")

@@ -115,7 +115,7 @@ class GradientBucket:
 
     def num_bytes(self) -> int:
         """Size of the flat buffer in bytes."""
-        return self.layout.total_numel * torch.empty(0, dtype=self._dtype).element_size()
+        return self.layout.total_numel * self._dtype.itemsize
 
     def __repr__(self) -> str:
         return (
@@ -247,31 +247,43 @@ class BucketedGradients:
         """
         missing: list[str] = []
         divisor = self._divisor()
-        plans: dict[tuple[torch.dtype, torch.dtype], _native.CopyPlan] = {}
+        # Rows per (device, source dtype, bucket dtype): (source address, destination
+        # address, n), source address 0 meaning a zero fill.  Built with plain attribute
+        # reads: this loop runs once per step over every parameter.
+        rows: dict[tuple[int, torch.dtype, torch.dtype], list[tuple[int, int, int]]] = {}
         for bucket in self._buckets:
             buffer = bucket.buffer
+            base = buffer.data_ptr()
+            item = buffer.element_size()
+            bucket_dtype = buffer.dtype
+            device_index = buffer.get_device()
+            layout = bucket.layout
             for position, param in enumerate(bucket.parameters):
-                offset = bucket.layout.offsets[position]
-                numel = bucket.layout.numels[position]
+                offset = layout.offsets[position]
+                numel = layout.numels[position]
+                destination = base + offset * item
                 grad = param.grad
                 if grad is None:
                     missing.append(self._name_of.get(id(param), f"<param#{position}>"))
-                    plans.setdefault((buffer.dtype, buffer.dtype), _native.CopyPlan(buffer.device)).add_zero(
-                        buffer, offset, numel
-                    )
+                    rows.setdefault((device_index, bucket_dtype, bucket_dtype), []).append((0, destination, numel))
                     continue
-                source = _native.contiguous_source(grad.detach())
-                if source.numel() != numel:
+                if grad.get_device() != device_index:
+                    _native.require_device_tensor(grad, "ddp.pack")
+                    raise ShardingError(
+                        format_error("ddp.pack", "gradient lives on another device than its bucket",
+                                     expected=str(buffer.device), observed=str(grad.device))
+                    )
+                if not grad.is_contiguous():
+                    grad = grad.contiguous()
+                if grad.numel() != numel:
                     raise ShardingError(
                         format_error("ddp.pack", "gradient size differs from its parameter",
-                                     expected=numel, observed=source.numel())
+                                     expected=numel, observed=grad.numel())
                     )
-                same = source.data_ptr() == buffer.data_ptr() + offset * buffer.element_size()
-                if same and divisor == 1.0 and source.dtype == buffer.dtype:
+                source = grad.data_ptr()
+                if source == destination and divisor == 1.0 and grad.dtype == bucket_dtype:
                     continue  # the gradient already is this bucket slice
-                plans.setdefault((source.dtype, buffer.dtype), _native.CopyPlan(buffer.device)).add(
-                    source, 0, buffer, offset, numel
-                )
+                rows.setdefault((device_index, grad.dtype, bucket_dtype), []).append((source, destination, numel))
         if missing and not self._config.find_unused_parameters:
             raise ShardingError(
                 format_error(
@@ -289,8 +301,9 @@ class BucketedGradients:
                     ),
                 )
             )
-        for (src_dtype, dst_dtype), plan in plans.items():
-            op = _native.COPY_OP_DIVIDE if divisor != 1.0 else _native.COPY_OP_COPY
+        op = _native.COPY_OP_DIVIDE if divisor != 1.0 else _native.COPY_OP_COPY
+        for (device_index, src_dtype, dst_dtype), table in rows.items():
+            plan = _native.CopyPlan.from_rows(torch.device("cuda", device_index), table)
             plan.run(src_dtype=src_dtype, dst_dtype=dst_dtype, op=op, divisor=divisor)
         self.statistics.unused_parameters = tuple(missing)
         self.statistics.buckets_reduced += len(self._buckets)
