@@ -41,6 +41,7 @@ HBM_PEAK_GBPS = 8000.0
 BYTES_NORM = 4  # read g
 BYTES_ADAMW = 28  # read p, g, m, v; write p, m, v
 TRAFFIC_SUMMARY = os.path.join(HERE, "profiles", "adamw_llama3_8b_w8_shard_traffic.json")
+SECONDARY_TRAFFIC = os.path.join(HERE, "profiles", "secondary_workloads_traffic.json")
 
 
 def log(msg: str) -> None:
@@ -315,14 +316,26 @@ def _llama3_shapes(layers, d, ffn, kv_dim, vocab):
     return named + [("model.norm.weight", (d,)), ("lm_head.weight", (vocab, d))]
 
 
-def _emit(metric, unit, value, ms, steps, warmup, dtype, workload, bytes_per_run, extra=None):
+def _secondary_traffic(workload: str, labels: list[str], launches: list[int]) -> float | None:
+    """HBM bytes per step from the committed counter summary: sum of launches x bytes per launch."""
+    try:
+        with open(SECONDARY_TRAFFIC, encoding="utf-8") as f:
+            data = json.load(f)[workload]
+        return sum(k * float(data[label]["hbm_bytes_per_launch"]) for label, k in zip(labels, launches))
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def _emit(metric, unit, value, ms, steps, warmup, dtype, workload, bytes_per_run, extra=None, traffic=None):
+    """One JSON line for a secondary workload.  Its roofline is per step: algorithmic bytes
+    of the step over the step time, and HBM traffic per step (``traffic_per`` says so)."""
     gbps = bytes_per_run / (ms * 1e-3) / 1e9
     line = {
         "metric": metric, "value": value, "unit": unit, "n_gpus": 1, "steps": steps, "warmup": warmup,
         "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": dtype,
         "data": "synthetic (device-generated)", "config": {"workload": workload},
         "roofline": {"bound": "hbm", "achieved": gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": gbps / HBM_PEAK_GBPS, "traffic": None},
+                     "frac": gbps / HBM_PEAK_GBPS, "traffic": traffic, "traffic_per": "step"},
     }
     if extra:
         line["config"].update(extra)
@@ -350,7 +363,8 @@ def bench_buckets(steps: int, warmup: int) -> int:
     ms = _time_events(run, max(steps, 20), max(warmup, 3))
     _emit("DDP bucket pack + AVG divide: params/s", "params/s", n / (ms * 1e-3), ms, max(steps, 20),
           max(warmup, 3), "f32", "GPT-2 small gradients, 17 buckets of <= 25 MiB, W=8", 8 * n,
-          {"params": n, "buckets": len(ddp.buckets), "bytes_per_param": 8})
+          {"params": n, "buckets": len(ddp.buckets), "bytes_per_param": 8},
+          _secondary_traffic("buckets", ["pack + AVG divide (one launch)"], [1]))
     return 0
 
 
@@ -402,7 +416,8 @@ def bench_reshard(steps: int, warmup: int) -> int:
         ms = _time_events(run, max(steps, 5), max(warmup, 2))
         _emit("flat-interval reshard: elements/s", "elements/s", total / (ms * 1e-3), ms, max(steps, 5),
               max(warmup, 2), "bf16", f"Llama-3-8B bf16 flat shards, W=4 -> W={w_dst}", 4 * total,
-              {"elements": total, "bytes_per_element": 4})
+              {"elements": total, "bytes_per_element": 4},
+              _secondary_traffic("reshard", [f"one destination shard of {s_dst:,} elements (W={w_dst})"], [w_dst]))
         del dests
         torch.cuda.empty_cache()
     return 0
@@ -445,13 +460,15 @@ def bench_scaler(steps: int, warmup: int) -> int:
     ms = _time_events(engine_step, max(steps, 5), max(warmup, 2))
     _emit("loss-scaled clipped AdamW step (bf16 grads): params/s", "params/s", n / (ms * 1e-3), ms,
           max(steps, 5), max(warmup, 2), "f32", "Llama-3-70B FSDP rank shard at W=8, bf16 grads, scale 2^16",
-          28 * n, {"params": n, "bytes_per_param": 28, "skipped": False})
+          28 * n, {"params": n, "bytes_per_param": 28, "skipped": False},
+          _secondary_traffic("scaler", ["fused unscale + clip + AdamW", "unscale + check + norm"], [1, 1]))
     bad = torch.randint(0, n, (n // 1000,), device=device, generator=gen)
     grad[bad] = float("inf")
     ms = _time_events(engine_step, max(steps, 5), max(warmup, 2))
     _emit("loss-scaled step with 0.1% inf gradients (skipped): params/s", "params/s", n / (ms * 1e-3), ms,
           max(steps, 5), max(warmup, 2), "bf16", "Llama-3-70B FSDP rank shard at W=8, bf16 grads, 0.1% inf",
-          2 * n, {"params": n, "bytes_per_param": 2, "skipped": True})
+          2 * n, {"params": n, "bytes_per_param": 2, "skipped": True},
+          _secondary_traffic("scaler", ["unscale + check + norm"], [1]))
     return 0
 
 
