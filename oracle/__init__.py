@@ -59,8 +59,8 @@ PINNED_BY = {
     "f32_to_bf16": "torch Tensor.to(torch.bfloat16) bitwise on specials and random values",
     "read_range": "reference known answers: shards_overlapping [(0,(0,3)),(1,(3,1))] "
     "(test_checkpoint_format.py:242-247); bitwise re-slicing of the global flat vector",
-    "local_share": "closed form: fixed-order sum of x_q / G (collectives.py:593-594), "
-    "padding tail exactly 0.0 (test_fsdp.py:477-481)",
+    "local_share": "torch Tensor.div + add + padding zero, bitwise (order-free for G <= 2; "
+    "collectives.py:593-594); padding tail exactly 0.0 (test_fsdp.py:477-481)",
 }
 
 

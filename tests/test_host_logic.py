@@ -91,21 +91,36 @@ def test_real_process_groups_are_refused():
                          device=torch.device("cpu"))
 
 
-def test_oracle_local_share_closed_form():
-    rng = np.random.default_rng(0)
-    group, shard, total = 3, 5, 13
-    grads = [rng.standard_normal(group * shard).astype(np.float32) for _ in range(group)]
-    for rank in range(group):
-        valid = max(0, min(shard, total - rank * shard))
-        got = oracle.local_share(grads, rank, shard, valid, float(group))
-        want = np.zeros(shard, np.float32)
-        for i in range(valid):
-            acc = np.float32(grads[0][rank * shard + i] / np.float32(group))
-            for q in range(1, group):
-                acc = np.float32(acc + np.float32(grads[q][rank * shard + i] / np.float32(group)))
-            want[i] = acc
-        assert np.array_equal(got, want)
-        assert np.all(got[valid:] == 0.0)
+def test_oracle_local_share_against_torch_avg():
+    """The reference's AVG local share with torch's own ops.
+
+    Each rank's padded gradient is divided by G with ``Tensor.div`` (IEEE division,
+    ``distributed/collectives.py:593-594``), the reduce-scatter sums the divided
+    buffers, and the padding tail is zeroed (``parallel/fsdp.py:771-781``).  For G <= 2
+    the sum does not depend on its order (IEEE addition commutes), so torch pins the
+    result bitwise; it is formed here in reverse rank order to show that.  For G > 2
+    the rank order is the fixed order the oracle and the kernel share.
+    """
+    import functools
+
+    import torch
+
+    gen = torch.Generator().manual_seed(0)
+    for group, shard, pad in ((1, 7, 2), (2, 5, 1), (3, 5, 2), (4, 6, 3)):
+        total = group * shard - pad
+        grads = [torch.randn(group * shard, generator=gen) for _ in range(group)]
+        divided = [g.div(group) for g in grads]
+        if group <= 2:
+            summed = functools.reduce(torch.add, reversed(divided))
+        else:
+            summed = functools.reduce(torch.add, divided)
+        summed[total:] = 0.0
+        host = [g.numpy() for g in grads]
+        for rank in range(group):
+            valid = max(0, min(shard, total - rank * shard))
+            got = oracle.local_share(host, rank, shard, valid, float(group))
+            assert np.array_equal(got, summed[rank * shard : (rank + 1) * shard].numpy()), (group, rank)
+            assert np.all(got[valid:] == 0.0)
 
 
 def test_oracle_pack_matches_concatenation():
