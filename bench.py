@@ -59,11 +59,13 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument(
         "--workload",
-        choices=["adamw", "buckets", "reshard", "scaler"],
+        choices=["adamw", "buckets", "reshard", "scaler", "fsdp", "inplace_clip", "torch_adamw"],
         default="adamw",
         help="adamw (default): the Llama-3-8B W=8 shard step above; buckets: GPT-2-small DDP bucket "
         "pack + AVG divide at W=8; reshard: Llama-3-8B bf16 flat shards W=4 -> W=8 and W=2; scaler: "
-        "one Llama-3-70B W=8 rank shard with bf16 gradients, loss scale 2^16, clip and AdamW",
+        "one Llama-3-70B W=8 rank shard with bf16 gradients, loss scale 2^16, clip and AdamW; fsdp: "
+        "Llama-3-8B FSDP pack, unpack and gradient local share at W=8; inplace_clip: the headline step with "
+        "the reference's in-place clip; torch_adamw: the headline step with stock torch GPU kernels",
     )
     ap.add_argument(
         "--calibrate-copy",
@@ -472,7 +474,140 @@ def bench_scaler(steps: int, warmup: int) -> int:
     return 0
 
 
-SECONDARY = {"buckets": bench_buckets, "reshard": bench_reshard, "scaler": bench_scaler}
+def bench_fsdp(steps: int, warmup: int) -> int:
+    """Llama-3-8B (291 bf16 tensors, 8,030,261,248 params), FSDP at W=8 with fp32 master shards.
+
+    Pack: the 8 ranks' ``FlatParamHandle`` construction (read bf16 2 B + write fp32
+    4 B per param).  Unpack: ``full_tensors`` from the 8 shards (read 4 B + write 4 B).
+    Local share: rank 0's ``reduce_scatter_gradient`` over the 8 ranks' padded bf16
+    gradients resident on the device (read 8 x 2 B + write 4 B per shard element).
+    """
+    import torch
+
+    from hybrid_training_amd import FlatParamHandle, FSDPConfig, GroupHandle, MixedPrecisionConfig
+
+    device = torch.device("cuda", 0)
+    world = 8
+    shapes = _llama3_shapes(32, 4096, 14336, 1024, 128256)
+    gen = torch.Generator(device=device).manual_seed(5)
+    # Finite bf16 bit patterns of magnitude < 2 (exponent field below 0x80).
+    named = [(name, torch.nn.Parameter(torch.randint(-16000, 16000, shape, dtype=torch.int16, device=device,
+                                                      generator=gen).view(torch.bfloat16)))
+             for name, shape in shapes]
+    total = sum(p.numel() for _, p in named)
+    mp = MixedPrecisionConfig(enabled=True, param_dtype="bfloat16", reduce_dtype="float32", master_dtype="float32")
+
+    def build():
+        return [FlatParamHandle(named, None, GroupHandle.local_view("shard", world, r), FSDPConfig(), mp, device,
+                                keep_originals=True) for r in range(world)]
+
+    handles = []
+
+    def pack():
+        handles.clear()
+        handles.extend(build())
+
+    ms = _time_events(pack, max(steps, 3), max(warmup, 1))
+    shard = handles[0].shard_numel
+    _emit("FSDP pack/pad/shard (FlatParamHandle build): params/s", "params/s", total / (ms * 1e-3), ms,
+          max(steps, 3), max(warmup, 1), "bf16->f32", f"Llama-3-8B bf16 params -> {world} fp32 master shards",
+          6 * total, {"params": total, "world": world, "shard_numel": shard, "bytes_per_param": 6})
+    shards = [h.flat_param for h in handles]
+    outputs = {}
+
+    def unpack():
+        outputs.clear()
+        outputs.update(handles[0].full_tensors(peer_shards=shards))
+
+    ms = _time_events(unpack, max(steps, 3), max(warmup, 1))
+    _emit("FSDP unpack (full_tensors from all shards): params/s", "params/s", total / (ms * 1e-3), ms,
+          max(steps, 3), max(warmup, 1), "f32", f"Llama-3-8B, {world} fp32 shards -> 291 fp32 tensors",
+          8 * total, {"params": total, "world": world, "bytes_per_param": 8})
+    outputs.clear()
+    del shards
+    owner = handles[0]
+    handles.clear()
+    torch.cuda.empty_cache()
+    padded = owner.padded_numel
+    grads = [torch.randint(-16000, 16000, (padded,), dtype=torch.int16, device=device, generator=gen)
+             .view(torch.bfloat16) for _ in range(world)]
+
+    def share():
+        return owner.reduce_scatter_gradient(grads[0], peer_grads=grads)
+
+    ms = _time_events(share, max(steps, 5), max(warmup, 2))
+    _emit("FSDP gradient local share (AVG reduce-scatter stand-in): shard elements/s", "elements/s",
+          shard / (ms * 1e-3), ms, max(steps, 5), max(warmup, 2), "bf16->f32",
+          f"Llama-3-8B rank 0 of W={world}: {world} padded bf16 gradients -> fp32 shard", (2 * world + 4) * shard,
+          {"shard_numel": shard, "world": world, "bytes_per_element": 2 * world + 4})
+    del grads, owner, named
+    torch.cuda.empty_cache()
+    return 0
+
+
+def _headline_inputs(device, n):
+    import torch
+
+    gen = torch.Generator(device=device).manual_seed(0)
+    param = torch.nn.Parameter(torch.randn(n, device=device, generator=gen).mul_(0.02))
+    grad = torch.randn(n, device=device, generator=torch.Generator(device=device).manual_seed(1)).mul_(1e-4)
+    return param, grad
+
+
+def bench_inplace_clip(steps: int, warmup: int) -> int:
+    """The headline shard with the reference's in-place clip (``defer_clip=False``).
+
+    clip_grad_norm: norm pass (4 B) + ``grad.mul_`` (8 B); step: fused AdamW (28 B).
+    """
+    import torch
+
+    from hybrid_training_amd import GroupHandle, OptimizerConfig, ShardedOptimizer
+
+    device = torch.device("cuda", 0)
+    n = SHARD_NUMEL
+    param, grad = _headline_inputs(device, n)
+    opt = ShardedOptimizer([param], OptimizerConfig(learning_rate=LR, betas=BETAS, eps=EPS, weight_decay=WD),
+                           norm_group=GroupHandle.trivial("world"), device=device, defer_clip=False)
+    param.grad = grad
+
+    def step():
+        opt.clip_grad_norm(MAX_NORM)
+        opt.step()
+
+    ms = _time_events(step, steps, warmup)
+    _emit("sharded AdamW + in-place clip step: params/s", "params/s", n / (ms * 1e-3), ms, steps, warmup, "f32",
+          "Llama-3-8B FSDP rank shard at W=8: norm, in-place clip, AdamW (reference semantics)", 40 * n,
+          {"shard_numel": n, "bytes_per_param": 40})
+    return 0
+
+
+def bench_torch_adamw(steps: int, warmup: int) -> int:
+    """Stock PyTorch on the same GPU and shard: clip_grad_norm_ (foreach) + AdamW(fused=True).
+
+    A comparison point, not this library: the same step written with torch's own GPU
+    kernels.  Algorithmic bytes as for the fused path with an in-place clip (40 B/param).
+    """
+    import torch
+
+    device = torch.device("cuda", 0)
+    n = SHARD_NUMEL
+    param, grad = _headline_inputs(device, n)
+    opt = torch.optim.AdamW([param], lr=LR, betas=BETAS, eps=EPS, weight_decay=WD, fused=True)
+    param.grad = grad
+
+    def step():
+        torch.nn.utils.clip_grad_norm_([param], MAX_NORM, foreach=True)
+        opt.step()
+
+    ms = _time_events(step, steps, warmup)
+    _emit("torch clip_grad_norm_ + AdamW(fused=True) step: params/s", "params/s", n / (ms * 1e-3), ms, steps,
+          warmup, "f32", "Llama-3-8B FSDP rank shard at W=8, stock PyTorch-ROCm kernels (comparison)", 40 * n,
+          {"shard_numel": n, "bytes_per_param": 40, "torch": torch.__version__})
+    return 0
+
+
+SECONDARY = {"buckets": bench_buckets, "reshard": bench_reshard, "scaler": bench_scaler, "fsdp": bench_fsdp,
+             "inplace_clip": bench_inplace_clip, "torch_adamw": bench_torch_adamw}
 
 
 if __name__ == "__main__":

@@ -37,6 +37,9 @@ template <int NW>
 struct Vec {
     typedef uint32_t type __attribute__((ext_vector_type(NW)));
 };
+typedef Vec<4>::type u32x4v;
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
 template <int NW>
 __device__ __forceinline__ typename Vec<NW>::type ldv(const void* p) {
     typedef typename Vec<NW>::type V;
@@ -230,13 +233,54 @@ struct RankTable {
     const uint8_t* g[HBT_MAX_LOCAL_RANKS];
 };
 
+// One wavefront per workgroup and 512 shard elements per workgroup: each lane owns
+// two 4-element groups (fp32 input: one 16-byte load per rank and group; bf16 input:
+// one 8-byte load), adds the G ranks' quotients in rank order and stores 16 bytes.
+constexpr int kShareBlock = 64;
+constexpr int64_t kShareTile = int64_t(kShareBlock) * 4 * 2;
+
 template <int SB>
-__global__ __launch_bounds__(256) void local_share_kernel(RankTable ranks, int32_t group_size,
-                                                          int64_t offset, int64_t shard_numel,
-                                                          int64_t valid_numel, float divisor,
-                                                          float* __restrict__ out) {
-    const int64_t stride = int64_t(gridDim.x) * 256;
-    for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < shard_numel; i += stride) {
+__device__ __forceinline__ f32x4 load_quad(const uint8_t* p) {
+    if constexpr (SB == 4) {
+        const u32x4v w = ldv<4>(p);
+        return f32x4{__uint_as_float(w.x), __uint_as_float(w.y), __uint_as_float(w.z), __uint_as_float(w.w)};
+    } else {
+        const typename Vec<2>::type w = ldv<2>(p);
+        return f32x4{bf16_to_f32(w.x & 0xFFFFu), bf16_to_f32(w.x >> 16), bf16_to_f32(w.y & 0xFFFFu),
+                     bf16_to_f32(w.y >> 16)};
+    }
+}
+
+template <int SB>
+__global__ __launch_bounds__(kShareBlock) void local_share_kernel(RankTable ranks, int32_t group_size,
+                                                                  int64_t offset, int64_t shard_numel,
+                                                                  int64_t valid_numel, float divisor,
+                                                                  int32_t vec_ok,
+                                                                  float* __restrict__ out) {
+    const int64_t base = int64_t(blockIdx.x) * kShareTile;
+    if (vec_ok && base + kShareTile <= valid_numel) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int64_t e = base + (int64_t(u) * kShareBlock + threadIdx.x) * 4;
+            f32x4 acc = load_quad<SB>(ranks.g[0] + (offset + e) * SB) / divisor;
+            for (int32_t q = 1; q < group_size; ++q) {
+                acc = acc + load_quad<SB>(ranks.g[q] + (offset + e) * SB) / divisor;
+            }
+            stv<4>(out + e, u32x4v{__float_as_uint(acc.x), __float_as_uint(acc.y),
+                                     __float_as_uint(acc.z), __float_as_uint(acc.w)});
+        }
+        return;
+    }
+    if (vec_ok && base >= valid_numel && base + kShareTile <= shard_numel) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int64_t e = base + (int64_t(u) * kShareBlock + threadIdx.x) * 4;
+            stv<4>(out + e, u32x4v{0u, 0u, 0u, 0u});
+        }
+        return;
+    }
+    const int64_t end = base + kShareTile < shard_numel ? base + kShareTile : shard_numel;
+    for (int64_t i = base + threadIdx.x; i < end; i += kShareBlock) {
         float acc = 0.0f;
         if (i < valid_numel) {
             acc = elem_to_f32<SB>(load_elem<SB>(ranks.g[0] + (offset + i) * SB)) / divisor;
@@ -347,17 +391,27 @@ int32_t hbt_grad_local_share(const void* const* rank_grads, int32_t group_size, 
         ranks.g[q] = static_cast<const uint8_t*>(rank_grads[q]);
     }
     if (shard_numel == 0) return HBT_OK;
-    int64_t blocks = (shard_numel + 255) / 256;
-    const int64_t cap = int64_t(device_cu_count()) * 16;
-    if (blocks > cap) blocks = cap;
     const int64_t offset = int64_t(rank) * shard_numel;
+    const int64_t tiles = (shard_numel + kShareTile - 1) / kShareTile;
+    if (tiles > 0x7FFFFFFFLL) {
+        set_error("hbt_grad_local_share: %lld tiles exceed the grid limit", static_cast<long long>(tiles));
+        return HBT_ERR_UNSUPPORTED;
+    }
+    // Vector path: every rank's slice and the output start on a 16-byte (fp32 input) or
+    // 8-byte (bf16 input) boundary.
+    const int elem = in_dtype == HBT_DTYPE_F32 ? 4 : 2;
+    int32_t vec_ok = (reinterpret_cast<uintptr_t>(out) & 15u) == 0;
+    for (int q = 0; q < group_size && vec_ok; ++q) {
+        const uintptr_t a = reinterpret_cast<uintptr_t>(ranks.g[q]) + static_cast<uintptr_t>(offset * elem);
+        vec_ok = (a & static_cast<uintptr_t>(4 * elem - 1)) == 0;
+    }
     hipStream_t s = as_stream(stream);
     if (in_dtype == HBT_DTYPE_F32) {
-        local_share_kernel<4><<<dim3(static_cast<unsigned>(blocks)), 256, 0, s>>>(
-            ranks, group_size, offset, shard_numel, valid_numel, divisor, out);
+        local_share_kernel<4><<<dim3(static_cast<unsigned>(tiles)), kShareBlock, 0, s>>>(
+            ranks, group_size, offset, shard_numel, valid_numel, divisor, vec_ok, out);
     } else {
-        local_share_kernel<2><<<dim3(static_cast<unsigned>(blocks)), 256, 0, s>>>(
-            ranks, group_size, offset, shard_numel, valid_numel, divisor, out);
+        local_share_kernel<2><<<dim3(static_cast<unsigned>(tiles)), kShareBlock, 0, s>>>(
+            ranks, group_size, offset, shard_numel, valid_numel, divisor, vec_ok, out);
     }
     return check_launch("hbt_grad_local_share");
 }

@@ -268,9 +268,16 @@ __global__ __launch_bounds__(kFinalBlock) void norm_finalize_kernel(
 }
 
 // ---- in-place scaling ---------------------------------------------------------------
+// Same tiling as the AdamW kernel: one wave per workgroup, 512 elements per workgroup,
+// each lane two 4-element groups (fp32) or one 8-element group (bf16, 16 bytes).
+constexpr int kScaleBlock = 64;
+constexpr int64_t kScaleTile = int64_t(kScaleBlock) * 8;
+
 struct ScaleTable {
     void* x[kMaxT];
     int64_t n[kMaxT];
+    int64_t first_block[kMaxT + 1];
+    int32_t vec_ok[kMaxT];
     int32_t count;
 };
 
@@ -291,17 +298,47 @@ __device__ __forceinline__ uint16_t from_f32<uint16_t>(float x) {
 
 // Two separate multiplies, each rounded to T, as two in-place mul_ calls would do.
 template <typename T>
-__global__ __launch_bounds__(256) void scale_kernel(ScaleTable tab, float unscale,
-                                                    const float* __restrict__ grad_mul) {
+__device__ __forceinline__ T scale_one(T x, float unscale, float mul) {
+    const T y = from_f32<T>(to_f32<T>(x) * unscale);
+    return from_f32<T>(to_f32<T>(y) * mul);
+}
+
+template <typename T>
+__global__ __launch_bounds__(kScaleBlock) void scale_kernel(ScaleTable tab, float unscale,
+                                                            const float* __restrict__ grad_mul) {
+    const int64_t block = blockIdx.x;
+    int t = 0;
+    while (t + 1 < tab.count && block >= tab.first_block[t + 1]) ++t;
+    const int64_t base = (block - tab.first_block[t]) * kScaleTile;
+    const int64_t n = tab.n[t];
     const float mul = grad_mul != nullptr ? *grad_mul : 1.0f;
-    for (int t = 0; t < tab.count; ++t) {
-        T* __restrict__ x = static_cast<T*>(tab.x[t]);
-        const int64_t n = tab.n[t];
-        for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += int64_t(gridDim.x) * 256) {
-            T y = from_f32<T>(to_f32<T>(x[i]) * unscale);
-            x[i] = from_f32<T>(to_f32<T>(y) * mul);
+    T* __restrict__ x = static_cast<T*>(tab.x[t]);
+    typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+    if (tab.vec_ok[t] && base + kScaleTile <= n) {
+        if constexpr (sizeof(T) == 4) {
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                float* p = reinterpret_cast<float*>(x) + base + (int64_t(u) * kScaleBlock + threadIdx.x) * 4;
+                f32x4 v = ld4_nt(p);
+#pragma unroll
+                for (int c = 0; c < 4; ++c) v[c] = scale_one<float>(v[c], unscale, mul);
+                st4_nt(p, v);
+            }
+        } else {
+            uint16_t* p = reinterpret_cast<uint16_t*>(x) + base + int64_t(threadIdx.x) * 8;
+            u32x4v w = __builtin_nontemporal_load(reinterpret_cast<const u32x4v*>(p));
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const uint32_t lo = scale_one<uint16_t>(static_cast<uint16_t>(w[c] & 0xFFFFu), unscale, mul);
+                const uint32_t hi = scale_one<uint16_t>(static_cast<uint16_t>(w[c] >> 16), unscale, mul);
+                w[c] = lo | (hi << 16);
+            }
+            __builtin_nontemporal_store(w, reinterpret_cast<u32x4v*>(p));
         }
+        return;
     }
+    const int64_t end = base + kScaleTile < n ? base + kScaleTile : n;
+    for (int64_t i = base + threadIdx.x; i < end; i += kScaleBlock) x[i] = scale_one<T>(x[i], unscale, mul);
 }
 
 inline bool aligned(const void* ptr, uintptr_t bytes) {
@@ -497,7 +534,7 @@ int32_t hbt_scale_inplace(void* const* tensors, const int64_t* numels, int32_t c
     }
     ScaleTable tab{};
     tab.count = count;
-    int64_t largest = 0;
+    int64_t blocks = 0;
     for (int i = 0; i < count; ++i) {
         if (numels[i] < 0 || (numels[i] > 0 && tensors[i] == nullptr)) {
             set_error("hbt_scale_inplace: tensor %d has a bad pointer or numel", i);
@@ -505,17 +542,22 @@ int32_t hbt_scale_inplace(void* const* tensors, const int64_t* numels, int32_t c
         }
         tab.x[i] = tensors[i];
         tab.n[i] = numels[i];
-        if (numels[i] > largest) largest = numels[i];
+        tab.vec_ok[i] = aligned(tensors[i], 16);
+        tab.first_block[i] = blocks;
+        blocks += (numels[i] + kScaleTile - 1) / kScaleTile;
     }
-    if (largest == 0) return HBT_OK;
-    int64_t blocks = (largest + 255) / 256;
-    const int64_t cap = int64_t(device_cu_count()) * 16;
-    if (blocks > cap) blocks = cap;
+    tab.first_block[count] = blocks;
+    for (int i = count + 1; i <= kMaxT; ++i) tab.first_block[i] = blocks;
+    if (blocks == 0) return HBT_OK;
+    if (blocks > 0x7FFFFFFFLL) {
+        set_error("hbt_scale_inplace: %lld tiles exceed the grid limit", static_cast<long long>(blocks));
+        return HBT_ERR_UNSUPPORTED;
+    }
     if (dtype == HBT_DTYPE_F32) {
-        scale_kernel<float><<<dim3(static_cast<unsigned>(blocks)), 256, 0, as_stream(stream)>>>(
+        scale_kernel<float><<<dim3(static_cast<unsigned>(blocks)), kScaleBlock, 0, as_stream(stream)>>>(
             tab, unscale, grad_mul);
     } else {
-        scale_kernel<uint16_t><<<dim3(static_cast<unsigned>(blocks)), 256, 0, as_stream(stream)>>>(
+        scale_kernel<uint16_t><<<dim3(static_cast<unsigned>(blocks)), kScaleBlock, 0, as_stream(stream)>>>(
             tab, unscale, grad_mul);
     }
     return check_launch("hbt_scale_inplace");

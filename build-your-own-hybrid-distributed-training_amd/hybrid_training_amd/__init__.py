@@ -28,7 +28,7 @@ from .errors import (
     format_error,
 )
 from .buckets import BucketedGradients, BucketLayout, GradientBucket, build_buckets
-from .flat_param import FlatParamHandle, PieceLayout, ShardedTensorPiece, reshard_state_dict_pieces
+from .flat_param import FlatParameter, FlatParamHandle, PieceLayout, ShardedTensorPiece, reshard_state_dict_pieces
 from .grad_scaler import GradScaler, GradScalerState
 from .groups import GroupHandle
 from .manifest import ShardRecord, TensorRecord, shard_filename, validate_shard_filename

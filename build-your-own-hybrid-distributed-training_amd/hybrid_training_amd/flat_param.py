@@ -39,6 +39,7 @@ from .tensors import FlatEntry, ShardRange, build_flat_layout, intersect_ranges
 
 __all__ = [
     "FlatParamHandle",
+    "FlatParameter",
     "PieceLayout",
     "ShardedTensorPiece",
     "reshard_state_dict_pieces",
@@ -74,6 +75,26 @@ class PieceLayout:
     parameter_offset: int
     length: int
     local_offset: int
+
+
+class FlatParameter(nn.Parameter):
+    """A rank's flat shard.
+
+    ``gradient_norm_scale_runs`` holds the per-element norm weights as runs
+    ``(offset, length, weight)``: the partitioned width over real elements, 0 over
+    padding.  ``gradient_norm_scale_vector``, the same weights as one host vector
+    (``fsdp.py:456-483``), is built from the runs on first access only.
+    """
+
+    @property
+    def gradient_norm_scale_vector(self) -> torch.Tensor:
+        cached = self.__dict__.get("_norm_scale_vector")
+        if cached is None:
+            cached = torch.zeros(self.numel(), dtype=torch.float32)
+            for offset, length, value in self.__dict__.get("gradient_norm_scale_runs", []):
+                cached[offset : offset + length] = value
+            self.__dict__["_norm_scale_vector"] = cached
+        return cached
 
 
 def _check_cast(src: torch.dtype, dst: torch.dtype, operation: str) -> None:
@@ -221,13 +242,14 @@ class FlatParamHandle:
             zero_plan.add_zero(shard, padding.start - local.start, padding.length)
         for dtype, plan in plans.items():
             plan.run(src_dtype=dtype, dst_dtype=self._master_dtype)
-        return nn.Parameter(shard, requires_grad=self._requires_grad)
+        return FlatParameter(shard, requires_grad=self._requires_grad)
 
     def _attach_gradient_norm_scale(self) -> None:
         """Per-element norm weights: partitioned width on real elements, 0 on padding.
 
-        Same vector as ``fsdp.py:456-483`` (kept on the host, as there), plus its
-        run-length form ``gradient_norm_scale_runs`` that the norm kernel consumes.
+        Stored as runs (``gradient_norm_scale_runs``), which the norm kernel consumes;
+        the reference's host vector (``fsdp.py:456-483``) is built from them only if
+        read (:class:`FlatParameter`).
         """
         local = self.local_shard_range()
         runs: list[tuple[int, int, float]] = []
@@ -241,10 +263,6 @@ class FlatParamHandle:
         padding = intersect_ranges(local, ShardRange(self._total_numel, self._padding))
         if padding is not None:
             runs.append((padding.start - local.start, padding.length, 0.0))
-        vector = torch.zeros(self._shard_numel, dtype=torch.float32)
-        for offset, length, value in runs:
-            vector[offset : offset + length] = value
-        self.flat_param.gradient_norm_scale_vector = vector  # type: ignore[attr-defined]
         self.flat_param.gradient_norm_scale_runs = runs  # type: ignore[attr-defined]
         self.flat_param.gradient_norm_label = (  # type: ignore[attr-defined]
             f"flat_param[{self._names[0]} .. {self._names[-1]}]"

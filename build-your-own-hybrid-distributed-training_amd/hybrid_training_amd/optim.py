@@ -103,25 +103,50 @@ class NormContribution:
 
     ``scale`` is a scalar weight or a per-element weight vector
     (``sharded_optimizer.py:129-158``).  A vector is piecewise constant over the
-    flat layout, so it is kept as runs and each run becomes one weighted segment
-    of the device reduction.
+    flat layout, so it is kept as runs ``(offset, length, weight)`` and each run
+    becomes one weighted segment of the device reduction.  A contribution may be
+    built from the runs alone (``scale=None``): an FSDP flat shard is, so a
+    billion-element weight vector is never materialised; :meth:`scale_vector`
+    builds it on demand.
     """
 
     parameter: nn.Parameter
-    scale: float | torch.Tensor
+    scale: float | torch.Tensor | None
     label: str
     runs: list[tuple[int, int, float]] = field(default_factory=list, repr=False)
 
     def __post_init__(self) -> None:
         if isinstance(self.scale, torch.Tensor) and not self.runs:
             self.runs = _weight_runs(self.scale)
+        if self.scale is None and not self.runs and self.parameter.numel() > 0:
+            raise ShardingError(
+                format_error(
+                    "optim.NormContribution",
+                    "a contribution needs a scalar weight, a weight vector or weight runs",
+                    observed=self.label,
+                )
+            )
+
+    @property
+    def per_element(self) -> bool:
+        """Whether the weights vary per element (a vector or runs)."""
+        return not isinstance(self.scale, (int, float))
+
+    def scale_vector(self) -> torch.Tensor:
+        """The per-element fp64 weights on the host (built from the runs when needed)."""
+        if isinstance(self.scale, torch.Tensor):
+            return self.scale
+        vector = torch.zeros(self.parameter.numel(), dtype=torch.float64)
+        for offset, length, weight in self.runs:
+            vector[offset : offset + length] = weight
+        return vector
 
     def segments(self) -> list[tuple[torch.Tensor, int, int, float]]:
         """``(grad, offset, length, weight)`` pieces of this contribution, or ``[]``."""
         grad = self.parameter.grad
         if grad is None:
             return []
-        if isinstance(self.scale, torch.Tensor):
+        if self.per_element:
             if sum(length for _, length, _ in self.runs) != grad.numel():
                 raise ShardingError(
                     format_error(
@@ -150,7 +175,8 @@ def build_gradient_norm_contributions(
     """Per-parameter norm weights (``sharded_optimizer.py:161-212``).
 
     A parameter carrying ``gradient_norm_scale_vector`` (an FSDP flat shard) gets
-    that vector, in fp64, divided by ``world_size``; any other parameter gets
+    that vector, in fp64, divided by ``world_size`` (from its run-length form
+    ``gradient_norm_scale_runs`` when present); any other parameter gets
     ``partitioned / world_size`` with ``partitioned`` its tensor-parallel width when
     it is not replicated, else 1.
     """
@@ -166,18 +192,20 @@ def build_gradient_norm_contributions(
         )
     contributions: list[NormContribution] = []
     for index, param in enumerate(parameters):
+        label = getattr(param, "gradient_norm_label", f"flat_param#{index}")
+        # A flat shard built here carries its weights in run-length form, so a
+        # billion-element shard's weight vector is neither built nor scanned.
+        runs = getattr(param, "gradient_norm_scale_runs", None)
+        if runs is not None:
+            contributions.append(
+                NormContribution(parameter=param, scale=None, label=label,
+                                 runs=[(o, n, float(w) / world_size) for o, n, w in runs])
+            )
+            continue
         vector = getattr(param, "gradient_norm_scale_vector", None)
         if vector is not None:
-            # A flat shard built here also carries the vector's run-length form, so a
-            # billion-element shard is never scanned on the host.
-            runs = getattr(param, "gradient_norm_scale_runs", None)
             contributions.append(
-                NormContribution(
-                    parameter=param,
-                    scale=vector.to(torch.float64) / world_size,
-                    label=getattr(param, "gradient_norm_label", f"flat_param#{index}"),
-                    runs=[] if runs is None else [(o, n, float(w) / world_size) for o, n, w in runs],
-                )
+                NormContribution(parameter=param, scale=vector.to(torch.float64) / world_size, label=label)
             )
             continue
         partitioned = 1

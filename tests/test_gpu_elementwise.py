@@ -1,0 +1,99 @@
+"""GPU parity of the two element-wise entry points at sizes that exercise every tile path.
+
+* ``hbt_grad_local_share`` (the FSDP gradient local share, ``parallel/fsdp.py:704-781``):
+  bitwise against the oracle for G in {1, 3, 8}, fp32 and bf16 inputs, shards with
+  full vector tiles, a partial tile at the valid/padding boundary, whole tiles of
+  padding, and misaligned input and output addresses (scalar path).
+* ``hbt_scale_inplace`` (the ``grad.mul_`` loops of ``optim/grad_scaler.py:181-186``
+  and ``optim/sharded_optimizer.py:333-337``): bitwise against torch's own CPU
+  ``mul_`` by a Python float, twice, in the tensor's dtype, over several tensors per
+  launch, tails of every length and a misaligned view.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from hybrid_training_amd import _native
+
+pytestmark = pytest.mark.gpu
+
+
+def _bits(t: torch.Tensor) -> np.ndarray:
+    t = t.detach().cpu().contiguous()
+    return t.view({2: torch.int16, 4: torch.int32}[t.element_size()]).numpy().copy()
+
+
+@pytest.mark.parametrize("in_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("group", [1, 3, 8])
+@pytest.mark.parametrize("misaligned", [False, True])
+def test_local_share_tiles(device, in_dtype, group, misaligned):
+    lib = _native.library()
+    shard = 20_000
+    gen = torch.Generator(device=device).manual_seed(group)
+    lead = 1 if misaligned else 0
+    # Each rank's padded full gradient (group * shard elements), optionally one element
+    # into its allocation so the vector path is not taken.
+    storage = [(torch.randn(group * shard + lead, device=device, generator=gen) * 1e-2).to(in_dtype)
+               for _ in range(group)]
+    grads = [s[lead:] for s in storage]
+    host = [g.float().cpu().numpy() for g in grads]
+    out_storage = torch.full((shard + lead,), 7.0, device=device)
+    out = out_storage[lead:]
+    divisor = float(group) if group > 1 else 1.0
+    for rank in sorted({0, group - 1}):
+        for valid in (shard, shard - 1537, 700, 0):
+            status = lib.hbt_grad_local_share(
+                _native.pointer_array([g.data_ptr() for g in grads]), group, rank, shard, valid,
+                _native.dtype_code(in_dtype), divisor, ctypes.c_void_p(out.data_ptr()),
+                ctypes.c_void_p(_native.stream_of(device)),
+            )
+            _native.check(status, "test.local_share")
+            expect = oracle.local_share(host, rank, shard, valid, divisor)
+            assert np.array_equal(_bits(out), expect.view(np.int32)), (rank, valid)
+    assert float(out_storage[:lead].sum()) == 7.0 * lead  # nothing written before the output
+
+
+def _scale_reference(t: torch.Tensor, unscale: float, mul: float) -> torch.Tensor:
+    """The reference's two in-place multiplies by Python floats, on the CPU in t's dtype."""
+    return t.detach().cpu().clone().mul_(unscale).mul_(mul)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_scale_inplace_tiles(device, dtype):
+    lib = _native.library()
+    gen = torch.Generator(device=device).manual_seed(3)
+    sizes = [1, 7, 511, 512, 513, 4097, 100_003]
+    base = torch.randn(sum(sizes) + 1, device=device, generator=gen).mul_(65536.0 * 1e-3).to(dtype)
+    base[5] = float("inf")
+    base[600] = float("nan")
+    base[700] = 1e-41  # fp32 denormal / bf16 underflow after scaling
+    tensors, cursor = [], 1  # the first tensor starts one element in: misaligned
+    for n in sizes:
+        tensors.append(base[cursor : cursor + n])
+        cursor += n
+    before = [t.detach().cpu().clone() for t in tensors]
+    lead = _bits(base[:1])
+    unscale = 1.0 / 65536.0
+    mul = 0.31622776601683794
+    grad_mul = torch.tensor([mul], dtype=torch.float32, device=device)
+    status = lib.hbt_scale_inplace(
+        _native.pointer_array([t.data_ptr() for t in tensors]), _native.int64_array(sizes), len(sizes),
+        _native.dtype_code(dtype), unscale, ctypes.c_void_p(grad_mul.data_ptr()),
+        ctypes.c_void_p(_native.stream_of(device)),
+    )
+    _native.check(status, "test.scale_inplace")
+    # torch multiplies by the fp32 rounding of the Python float in fp32 arithmetic
+    mul32 = float(np.float32(mul))
+    for t, b in zip(tensors, before):
+        expect = _scale_reference(b, unscale, mul32)
+        got = t.detach().cpu()
+        nan = torch.isnan(expect)
+        assert torch.equal(torch.isnan(got), nan)
+        assert np.array_equal(_bits(got)[~nan.numpy()], _bits(expect)[~nan.numpy()])
+    assert np.array_equal(_bits(base[:1]), lead)  # the element before the first tensor is untouched

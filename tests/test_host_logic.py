@@ -5,6 +5,7 @@ from __future__ import annotations
 
 import numpy as np
 import pytest
+import torch
 
 import oracle
 from hybrid_training_amd import (
@@ -134,3 +135,20 @@ def test_oracle_pack_matches_concatenation():
         assert np.array_equal(joined[: flat.size], flat) and np.all(joined[flat.size :] == 0)
         back = oracle.unpack_full(joined, [t.shape for t in tensors])
         assert all(np.array_equal(a, b) for a, b in zip(back, tensors))
+
+
+def test_norm_contribution_from_runs_matches_the_vector_form():
+    from hybrid_training_amd import build_gradient_norm_contributions
+    from hybrid_training_amd.flat_param import FlatParameter
+
+    p = FlatParameter(torch.zeros(10), requires_grad=True)
+    p.gradient_norm_scale_runs = [(0, 7, 2.0), (7, 3, 0.0)]
+    (c,) = build_gradient_norm_contributions([p], world_size=4)
+    assert c.scale is None and c.per_element and c.runs == [(0, 7, 0.5), (7, 3, 0.0)]
+    assert torch.equal(c.scale_vector(), torch.tensor([0.5] * 7 + [0.0] * 3, dtype=torch.float64))
+    # the reference's host vector, built lazily from the runs, gives the same runs
+    assert torch.equal(p.gradient_norm_scale_vector, torch.tensor([2.0] * 7 + [0.0] * 3))
+    q = torch.nn.Parameter(torch.zeros(10))
+    q.gradient_norm_scale_vector = torch.tensor([2.0] * 7 + [0.0] * 3)
+    (d,) = build_gradient_norm_contributions([q], world_size=4)
+    assert d.runs == c.runs and torch.equal(d.scale_vector(), c.scale_vector())
