@@ -538,9 +538,25 @@ def bench_fsdp(steps: int, warmup: int) -> int:
     ms = _time_events(share, max(steps, 5), max(warmup, 2))
     _emit("FSDP gradient local share (AVG reduce-scatter stand-in): shard elements/s", "elements/s",
           shard / (ms * 1e-3), ms, max(steps, 5), max(warmup, 2), "bf16->f32",
-          f"Llama-3-8B rank 0 of W={world}: {world} padded bf16 gradients -> fp32 shard", (2 * world + 4) * shard,
-          {"shard_numel": shard, "world": world, "bytes_per_element": 2 * world + 4})
-    del grads, owner, named
+          f"Llama-3-8B rank 0 of W={world}: {world} padded bf16 gradients -> fp32 shard, with norm partials",
+          (2 * world + 4) * shard, {"shard_numel": shard, "world": world, "bytes_per_element": 2 * world + 4})
+
+    from hybrid_training_amd import OptimizerConfig, ShardedOptimizer
+
+    opt = ShardedOptimizer([owner.flat_param], OptimizerConfig(learning_rate=LR, betas=BETAS, eps=EPS, weight_decay=WD),
+                           norm_group=GroupHandle.local_view("world", world, 0), device=device, defer_clip=True)
+
+    def tail():
+        owner.flat_param.grad = owner.reduce_scatter_gradient(grads[0], peer_grads=grads)
+        opt.clip_grad_norm(MAX_NORM)
+        opt.step()
+
+    ms = _time_events(tail, max(steps, 5), max(warmup, 2))
+    _emit("FSDP optimizer tail (local share + clip + AdamW): shard elements/s", "elements/s", shard / (ms * 1e-3),
+          ms, max(steps, 5), max(warmup, 2), "bf16->f32",
+          f"Llama-3-8B rank 0 of W={world}: local share with norm partials, clip from them, fused AdamW",
+          (2 * world + 4 + 28) * shard, {"shard_numel": shard, "world": world, "bytes_per_element": 2 * world + 32})
+    del opt, grads, owner, named
     torch.cuda.empty_cache()
     return 0
 

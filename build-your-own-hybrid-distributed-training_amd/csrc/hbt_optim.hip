@@ -233,6 +233,82 @@ __global__ __launch_bounds__(kNormBlock) void sqnorm_kernel(NormTable tab, float
     if (threadIdx.x == 0) partials[chunk] = block_total * tab.w[t];
 }
 
+// ---- FSDP gradient local share fused with the norm partials -----------------------
+// Writes the rank's fp32 gradient shard exactly as the local-share kernel does (sum
+// over ranks, in rank order, of fp32(x_q) / divisor; +0.0 over the padding tail) and,
+// in the same pass, the unweighted squared-norm partials of the shard's two segments
+// [0, valid) and [valid, shard): one per chunk of 32768 elements from each segment's
+// start.  Element-to-thread assignment, accumulation order and reduction tree are
+// those of sqnorm_kernel<float> over the output, so the partials are bitwise the
+// ones a separate norm pass would write with weight 1.
+struct ShareRanks {
+    const uint8_t* g[HBT_MAX_LOCAL_RANKS];
+};
+
+template <int SB>
+__device__ __forceinline__ float share_load1(const uint8_t* p) {
+    if constexpr (SB == 4) return *reinterpret_cast<const float*>(p);
+    return bf16_to_f32(*reinterpret_cast<const uint16_t*>(p));
+}
+template <int SB>
+__device__ __forceinline__ f32x4 share_load4(const uint8_t* p, bool vec) {
+    if (vec) {
+        if constexpr (SB == 4) return ld4_nt(reinterpret_cast<const float*>(p));
+        return ld_grad4_nt(reinterpret_cast<const uint16_t*>(p));
+    }
+    return f32x4{share_load1<SB>(p), share_load1<SB>(p + SB), share_load1<SB>(p + 2 * SB),
+                 share_load1<SB>(p + 3 * SB)};
+}
+
+template <int SB>
+__global__ __launch_bounds__(kNormBlock) void local_share_sqnorm_kernel(
+    ShareRanks ranks, int32_t group_size, int64_t offset, int64_t shard_numel, int64_t valid_numel,
+    float divisor, int32_t in_vec, int32_t out_vec, int64_t valid_chunks, float* __restrict__ out,
+    double* __restrict__ partials) {
+    constexpr int64_t kTile = norm_tile<float>();
+    constexpr int64_t kChunk = norm_chunk<float>();
+    const int64_t chunk = blockIdx.x;
+    if (chunk >= valid_chunks) {
+        // Padding segment: zeros, and a zero partial (the square sum of zeros).
+        const int64_t start = valid_numel + (chunk - valid_chunks) * kChunk;
+        const int64_t end = start + kChunk < shard_numel ? start + kChunk : shard_numel;
+        for (int64_t e = start + threadIdx.x; e < end; e += kNormBlock) out[e] = 0.0f;
+        if (threadIdx.x == 0) partials[chunk] = 0.0;
+        return;
+    }
+    const int64_t start = chunk * kChunk;
+    const int64_t n = valid_numel;
+    double acc = 0.0;
+    for (int k = 0; k < kNormTilesPerChunk; ++k) {
+        const int64_t base = start + int64_t(k) * kTile;
+        if (base >= n) break;
+        if (out_vec && base + kTile <= n) {
+            const int64_t e = base + int64_t(threadIdx.x) * 4;
+            f32x4 sum = share_load4<SB>(ranks.g[0] + (offset + e) * SB, in_vec) / divisor;
+            for (int32_t q = 1; q < group_size; ++q) {
+                sum = sum + share_load4<SB>(ranks.g[q] + (offset + e) * SB, in_vec) / divisor;
+            }
+            st4_nt(out + e, sum);
+            acc += sq(sum.x);
+            acc += sq(sum.y);
+            acc += sq(sum.z);
+            acc += sq(sum.w);
+        } else {
+            const int64_t end = base + kTile < n ? base + kTile : n;
+            for (int64_t e = base + threadIdx.x; e < end; e += kNormBlock) {
+                float v = share_load1<SB>(ranks.g[0] + (offset + e) * SB) / divisor;
+                for (int32_t q = 1; q < group_size; ++q) {
+                    v = v + share_load1<SB>(ranks.g[q] + (offset + e) * SB) / divisor;
+                }
+                out[e] = v;
+                acc += sq(v);
+            }
+        }
+    }
+    const double block_total = block_sum<kNormBlock>(acc);
+    if (threadIdx.x == 0) partials[chunk] = block_total;
+}
+
 constexpr int kFinalBlock = 1024;
 
 __global__ __launch_bounds__(kFinalBlock) void norm_finalize_kernel(
@@ -561,6 +637,58 @@ int32_t hbt_scale_inplace(void* const* tensors, const int64_t* numels, int32_t c
             tab, unscale, grad_mul);
     }
     return check_launch("hbt_scale_inplace");
+}
+
+
+int32_t hbt_grad_local_share_sqnorm(const void* const* rank_grads, int32_t group_size, int32_t rank,
+                                    int64_t shard_numel, int64_t valid_numel, int32_t in_dtype,
+                                    float divisor, float* out, double* partials, void* stream) {
+    clear_error();
+    if (rank_grads == nullptr || out == nullptr || partials == nullptr || group_size < 1 ||
+        group_size > HBT_MAX_LOCAL_RANKS || rank < 0 || rank >= group_size || shard_numel < 0 ||
+        valid_numel < 0 || valid_numel > shard_numel) {
+        set_error("hbt_grad_local_share_sqnorm: bad arguments (group_size=%d rank=%d shard=%lld valid=%lld)",
+                  group_size, rank, static_cast<long long>(shard_numel), static_cast<long long>(valid_numel));
+        return HBT_ERR_INVALID_ARGUMENT;
+    }
+    if (in_dtype != HBT_DTYPE_F32 && in_dtype != HBT_DTYPE_BF16) {
+        set_error("hbt_grad_local_share_sqnorm: input dtype %d is not F32 or BF16", in_dtype);
+        return HBT_ERR_INVALID_ARGUMENT;
+    }
+    ShareRanks ranks{};
+    const int elem = in_dtype == HBT_DTYPE_F32 ? 4 : 2;
+    const int64_t offset = int64_t(rank) * shard_numel;
+    int32_t in_vec = 1;
+    for (int q = 0; q < group_size; ++q) {
+        if (rank_grads[q] == nullptr && valid_numel > 0) {
+            set_error("hbt_grad_local_share_sqnorm: rank %d gradient pointer is null", q);
+            return HBT_ERR_INVALID_ARGUMENT;
+        }
+        ranks.g[q] = static_cast<const uint8_t*>(rank_grads[q]);
+        const uintptr_t a = reinterpret_cast<uintptr_t>(ranks.g[q]) + static_cast<uintptr_t>(offset * elem);
+        if ((a & static_cast<uintptr_t>(4 * elem - 1)) != 0) in_vec = 0;
+    }
+    const int64_t chunk = norm_chunk<float>();
+    const int64_t valid_chunks = (valid_numel + chunk - 1) / chunk;
+    const int64_t pad_chunks = (shard_numel - valid_numel + chunk - 1) / chunk;
+    const int64_t blocks = valid_chunks + pad_chunks;
+    if (blocks == 0) return HBT_OK;
+    if (blocks > 0x7FFFFFFFLL) {
+        set_error("hbt_grad_local_share_sqnorm: %lld chunks exceed the grid limit", static_cast<long long>(blocks));
+        return HBT_ERR_UNSUPPORTED;
+    }
+    const int32_t out_vec = aligned(out, 16);
+    hipStream_t st = as_stream(stream);
+    if (in_dtype == HBT_DTYPE_F32) {
+        local_share_sqnorm_kernel<4><<<dim3(static_cast<unsigned>(blocks)), kNormBlock, 0, st>>>(
+            ranks, group_size, offset, shard_numel, valid_numel, divisor, in_vec, out_vec, valid_chunks, out,
+            partials);
+    } else {
+        local_share_sqnorm_kernel<2><<<dim3(static_cast<unsigned>(blocks)), kNormBlock, 0, st>>>(
+            ranks, group_size, offset, shard_numel, valid_numel, divisor, in_vec, out_vec, valid_chunks, out,
+            partials);
+    }
+    return check_launch("hbt_grad_local_share_sqnorm");
 }
 
 }  // extern "C"

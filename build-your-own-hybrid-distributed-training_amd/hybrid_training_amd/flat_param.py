@@ -11,7 +11,9 @@ tensor work is the interval gather-copy kernel and the local-share kernel of
   launch; the reference materialises the whole padded buffer first and slices it.
 * ``reduce_scatter_gradient`` is the rank's local share of the AVG reduce-scatter:
   cast to fp32, divide by ``G``, sum over the ranks' buffers in rank order, zero
-  the padding tail (one launch).  There are no collectives: a group of size 1 is
+  the padding tail, and in the same pass the squared-norm partials of the result,
+  which the next ``clip_grad_norm`` picks up instead of reading the shard again
+  (one launch).  There are no collectives: a group of size 1 is
   the whole job; a :meth:`GroupHandle.local_view` group needs the other ranks'
   buffers resident on this device (``peer_grads``), as the stand-in for the
   reduce-scatter.
@@ -35,6 +37,7 @@ from . import _native
 from .config import FSDPConfig, MixedPrecisionConfig, resolve_dtype
 from .errors import ShardingError, UnsupportedFeatureError, format_error
 from .groups import GroupHandle
+from .optim import NORM_PARTIALS_ATTR, NormPartials
 from .tensors import FlatEntry, ShardRange, build_flat_layout, intersect_ranges
 
 __all__ = [
@@ -253,16 +256,25 @@ class FlatParamHandle:
         """
         local = self.local_shard_range()
         runs: list[tuple[int, int, float]] = []
+
+        def append(offset: int, length: int, value: float) -> None:
+            # Adjacent elements of equal weight form one run: a pure FSDP shard is one
+            # run of real elements and at most one run of padding.
+            if runs and runs[-1][2] == value and runs[-1][0] + runs[-1][1] == offset:
+                runs[-1] = (runs[-1][0], runs[-1][1] + length, value)
+            else:
+                runs.append((offset, length, value))
+
         for entry, param in zip(self._entries, self._params):
             partitioned = self._shard_group.size
             if not getattr(param, "is_tensor_parallel_replicated", True):
                 partitioned *= int(getattr(param, "tensor_parallel_group_size", 1))
             overlap = intersect_ranges(local, ShardRange(entry.offset, entry.numel))
             if overlap is not None:
-                runs.append((overlap.start - local.start, overlap.length, float(partitioned)))
+                append(overlap.start - local.start, overlap.length, float(partitioned))
         padding = intersect_ranges(local, ShardRange(self._total_numel, self._padding))
         if padding is not None:
-            runs.append((padding.start - local.start, padding.length, 0.0))
+            append(padding.start - local.start, padding.length, 0.0)
         self.flat_param.gradient_norm_scale_runs = runs  # type: ignore[attr-defined]
         self.flat_param.gradient_norm_label = (  # type: ignore[attr-defined]
             f"flat_param[{self._names[0]} .. {self._names[-1]}]"
@@ -456,9 +468,13 @@ class FlatParamHandle:
         valid = max(0, min(self._shard_numel, self._total_numel - local.start))
         divisor = float(group) if (self._config.average_gradients and group > 1) else 1.0
         out = torch.empty(self._shard_numel, dtype=torch.float32, device=self._device)
+        chunk = 32768  # elements per norm partial (hbt_grad_local_share_sqnorm)
+        valid_chunks = -(-valid // chunk)
+        pad = self._shard_numel - valid
+        partials = torch.empty(max(1, valid_chunks + -(-pad // chunk)), dtype=torch.float64, device=self._device)
         lib = _native.library()
         with torch.cuda.device(self._device):
-            status = lib.hbt_grad_local_share(
+            status = lib.hbt_grad_local_share_sqnorm(
                 _native.pointer_array([g.data_ptr() for g in grads]),
                 group,
                 self._shard_group.local_rank,
@@ -467,9 +483,18 @@ class FlatParamHandle:
                 _native.dtype_code(grads[0].dtype),
                 divisor,
                 out.data_ptr(),
+                partials.data_ptr(),
                 _native.stream_of(self._device),
             )
-        _native.check(status, "fsdp.hbt_grad_local_share")
+        _native.check(status, "fsdp.hbt_grad_local_share_sqnorm")
+        # The squared-norm partials of the shard's real and padding segments ride on
+        # the gradient, so the next clip_grad_norm does not read it again.
+        segments = {}
+        if valid:
+            segments[(0, valid)] = partials[:valid_chunks]
+        if pad:
+            segments[(valid, pad)] = partials[valid_chunks:]
+        setattr(out, NORM_PARTIALS_ATTR, NormPartials(out.data_ptr(), out._version, segments))
         self._reduction_count += 1
         return out
 

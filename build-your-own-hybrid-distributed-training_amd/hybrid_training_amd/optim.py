@@ -52,6 +52,39 @@ __all__ = [
 #: Attribute a deferred loss-scale factor travels under on a gradient tensor.
 PENDING_UNSCALE_ATTR = "_hbt_pending_unscale"
 
+#: Attribute under which a kernel that produced a gradient leaves its squared-norm
+#: partials (see :class:`NormPartials`).
+NORM_PARTIALS_ATTR = "_hbt_norm_partials"
+
+
+@dataclass
+class NormPartials:
+    """Unweighted fp32-gradient norm partials a producing kernel wrote for its output.
+
+    ``segments`` maps ``(offset, length)`` of the gradient to the partials of that
+    segment: one fp64 per 32768-element chunk from the segment's start, bitwise what
+    ``hbt_grad_sqnorm_partials`` writes for it with weight 1.  The record is valid
+    while the gradient keeps the storage address and version counter it had when
+    the partials were written; any in-place change invalidates it.
+    """
+
+    data_ptr: int
+    version: int
+    segments: dict[tuple[int, int], torch.Tensor]
+
+    def lookup(self, grad: torch.Tensor, offset: int, length: int) -> torch.Tensor | None:
+        """The segment's partials if the record still describes ``grad``."""
+        if grad.data_ptr() != self.data_ptr or grad._version != self.version or grad.dtype != torch.float32:
+            return None
+        return self.segments.get((offset, length))
+
+
+def _cached_partials(grad: torch.Tensor, offset: int, length: int, unscale: float) -> torch.Tensor | None:
+    record = getattr(grad, NORM_PARTIALS_ATTR, None)
+    if record is None or unscale != 1.0:
+        return None
+    return record.lookup(grad, offset, length)
+
 
 def build_inner_optimizer(
     parameters: Iterable[nn.Parameter], config: OptimizerConfig
@@ -281,18 +314,31 @@ def gradient_norm_pass(
     stream = _native.stream_of(device)
     with torch.cuda.device(device):
         for dtype, unscale, items, first in launches:
-            ptrs = [g.data_ptr() + off * g.element_size() for g, off, _, _ in items]
-            status = lib.hbt_grad_sqnorm_partials(
-                _native.pointer_array(ptrs),
-                _native.int64_array([n for _, _, n, _ in items]),
-                _native.double_array([w for _, _, _, w in items]),
-                len(items),
-                _native.dtype_code(dtype),
-                unscale,
-                partials.data_ptr() + first * 8,
-                stream,
-            )
-            _native.check(status, "optim.hbt_grad_sqnorm_partials")
+            # Items whose producer already wrote their partials take them from there
+            # (times the weight, as the kernel would multiply); the others are summed
+            # here, each run of consecutive uncached items in one launch.  Every item
+            # keeps its slot, so the partials, and the norm, are the same either way.
+            slot = first
+            pending: list[tuple[torch.Tensor, int, int, float]] = []
+            pending_first = slot
+            for grad, offset, length, weight in items:
+                count = int(lib.hbt_norm_partials_count(_native.int64_array([length]), 1, _native.dtype_code(dtype)))
+                cached = _cached_partials(grad, offset, length, unscale)
+                if cached is not None and cached.numel() == count:
+                    _launch_sqnorm(lib, pending, dtype, unscale, partials, pending_first, stream)
+                    pending = []
+                    target = partials[slot : slot + count]
+                    if weight == 1.0:
+                        plan = _native.CopyPlan(device)
+                        plan.add(cached, 0, target, 0, count)
+                        plan.run(src_dtype=torch.float64, dst_dtype=torch.float64)
+                    else:
+                        torch.mul(cached, weight, out=target)
+                    pending_first = slot + count
+                else:
+                    pending.append((grad, offset, length, weight))
+                slot += count
+            _launch_sqnorm(lib, pending, dtype, unscale, partials, pending_first, stream)
         status = lib.hbt_grad_norm_finalize(
             partials.data_ptr(),
             total_partials,
@@ -305,6 +351,24 @@ def gradient_norm_pass(
         )
         _native.check(status, "optim.hbt_grad_norm_finalize")
     return NormResult(sum=outputs[0], norm=outputs[1], grad_mul=grad_mul, nonfinite=nonfinite)
+
+
+def _launch_sqnorm(lib, items, dtype, unscale, partials, first, stream) -> None:
+    """One ``hbt_grad_sqnorm_partials`` launch writing ``items``' partials from slot ``first``."""
+    if not items:
+        return
+    ptrs = [g.data_ptr() + off * g.element_size() for g, off, _, _ in items]
+    status = lib.hbt_grad_sqnorm_partials(
+        _native.pointer_array(ptrs),
+        _native.int64_array([n for _, _, n, _ in items]),
+        _native.double_array([w for _, _, _, w in items]),
+        len(items),
+        _native.dtype_code(dtype),
+        unscale,
+        partials.data_ptr() + first * 8,
+        stream,
+    )
+    _native.check(status, "optim.hbt_grad_sqnorm_partials")
 
 
 def _check_group(group: GroupHandle, operation: str) -> None:

@@ -149,3 +149,51 @@ def test_detaching_frees_originals_and_binds_views(device):
     assert torch.equal(module.weight, w)
     with pytest.raises(ShardingError, match="at least one parameter"):
         FlatParamHandle([], None, GroupHandle.trivial(), FSDPConfig(), MixedPrecisionConfig(), device)
+
+
+def _wide_model(device):
+    """Enough elements for several 32768-element norm chunks per shard, odd total."""
+    shapes = [("a", (700, 300)), ("b", (301,)), ("c", (200, 300)), ("d", (9,))]  # 270,310 elements
+    gen = torch.Generator(device=device).manual_seed(9)
+    return [(n, torch.nn.Parameter(torch.randn(s, device=device, generator=gen))) for n, s in shapes]
+
+
+@pytest.mark.parametrize("in_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("norm_world", [4, 8])
+def test_local_share_norm_partials_are_the_norm_pass(device, in_dtype, norm_world):
+    """The fused local share leaves partials that make clip_grad_norm bitwise equal to
+    a separate norm pass over the same shard, for weight 1 (norm group = shard group)
+    and weight 1/2 (norm group twice as wide); an in-place change invalidates them."""
+    from hybrid_training_amd import GroupHandle, OptimizerConfig, ShardedOptimizer
+    from hybrid_training_amd.optim import NORM_PARTIALS_ATTR
+
+    named = _wide_model(device)
+    group = 4
+    handles = [FlatParamHandle(named, None, GroupHandle.local_view("shard", group, r), FSDPConfig(),
+                               MixedPrecisionConfig(), device, keep_originals=True) for r in range(group)]
+    total = sum(p.numel() for _, p in named)
+    assert handles[-1].padding > 0 and handles[0].shard_numel > 2 * 32768
+    gen = torch.Generator(device=device).manual_seed(4)
+    grads = [(torch.randn(handles[0].padded_numel, device=device, generator=gen) * 1e-2).to(in_dtype)
+             for _ in range(group)]
+    host = [g.float().cpu().numpy() for g in grads]
+    for rank, h in enumerate(handles):
+        assert len(h.flat_param.gradient_norm_scale_runs) <= 2  # merged equal-weight runs
+        opt = ShardedOptimizer([h.flat_param], OptimizerConfig(), norm_group=GroupHandle.local_view("world", norm_world, rank),
+                               device=device)
+        fused = h.reduce_scatter_gradient(grads[rank], peer_grads=grads)
+        valid = max(0, min(h.shard_numel, total - rank * h.shard_numel))
+        assert getattr(fused, NORM_PARTIALS_ATTR).lookup(fused, 0, valid) is not None
+        expect = oracle.local_share(host, rank, h.shard_numel, valid, float(group))
+        assert np.array_equal(fused.cpu().numpy().view(np.int32), expect.view(np.int32))
+        plain = fused.clone()  # same values, no partials attached
+        h.flat_param.grad = plain
+        n_plain = opt.clip_grad_norm(0.0)
+        h.flat_param.grad = fused
+        n_fused = opt.clip_grad_norm(0.0)
+        assert float(n_fused) == float(n_plain), (rank, float(n_fused), float(n_plain))
+        ref = float((torch.from_numpy(expect).double() ** 2).sum()) * group / norm_world
+        assert abs(float(n_fused) ** 2 - ref) <= 1e-12 * ref
+        # an in-place change bumps the version counter: the partials are not reused
+        fused.mul_(2.0)
+        assert float(opt.clip_grad_norm(0.0)) == 2.0 * float(n_plain)
