@@ -59,13 +59,14 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument(
         "--workload",
-        choices=["adamw", "buckets", "reshard", "scaler", "fsdp", "inplace_clip", "torch_adamw"],
+        choices=["adamw", "buckets", "reshard", "scaler", "fsdp", "inplace_clip", "torch_adamw", "sgd"],
         default="adamw",
         help="adamw (default): the Llama-3-8B W=8 shard step above; buckets: GPT-2-small DDP bucket "
         "pack + AVG divide at W=8; reshard: Llama-3-8B bf16 flat shards W=4 -> W=8 and W=2; scaler: "
         "one Llama-3-70B W=8 rank shard with bf16 gradients, loss scale 2^16, clip and AdamW; fsdp: "
         "Llama-3-8B FSDP pack, unpack and gradient local share at W=8; inplace_clip: the headline step with "
-        "the reference's in-place clip; torch_adamw: the headline step with stock torch GPU kernels",
+        "the reference's in-place clip; torch_adamw: the headline step with stock torch GPU kernels; sgd: "
+        "the headline shard with SGD (momentum 0.9)",
     )
     ap.add_argument(
         "--calibrate-copy",
@@ -597,6 +598,35 @@ def bench_inplace_clip(steps: int, warmup: int) -> int:
     return 0
 
 
+def bench_sgd(steps: int, warmup: int) -> int:
+    """The headline shard with the reference's other inner optimizer: SGD, momentum 0.9.
+
+    Norm pass (4 B) + fused clip + SGD with a momentum buffer (read p, g, buf; write
+    p, buf: 20 B) = 24 B/param.
+    """
+    import torch
+
+    from hybrid_training_amd import GroupHandle, OptimizerConfig, ShardedOptimizer
+
+    device = torch.device("cuda", 0)
+    n = SHARD_NUMEL
+    param, grad = _headline_inputs(device, n)
+    opt = ShardedOptimizer([param], OptimizerConfig(name="sgd", learning_rate=LR, momentum=0.9, weight_decay=WD),
+                           norm_group=GroupHandle.trivial("world"), device=device, defer_clip=True)
+    param.grad = grad
+
+    def step():
+        opt.clip_grad_norm(MAX_NORM)
+        opt.step()
+        param.grad = grad
+
+    ms = _time_events(step, steps, warmup)
+    _emit("sharded SGD(momentum 0.9)+clip step: params/s", "params/s", n / (ms * 1e-3), ms, steps, warmup, "f32",
+          "Llama-3-8B FSDP rank shard at W=8: global-norm clip + SGD with momentum", 24 * n,
+          {"shard_numel": n, "bytes_per_param": 24})
+    return 0
+
+
 def bench_torch_adamw(steps: int, warmup: int) -> int:
     """Stock PyTorch on the same GPU and shard: clip_grad_norm_ (foreach) + AdamW(fused=True).
 
@@ -623,7 +653,7 @@ def bench_torch_adamw(steps: int, warmup: int) -> int:
 
 
 SECONDARY = {"buckets": bench_buckets, "reshard": bench_reshard, "scaler": bench_scaler, "fsdp": bench_fsdp,
-             "inplace_clip": bench_inplace_clip, "torch_adamw": bench_torch_adamw}
+             "inplace_clip": bench_inplace_clip, "torch_adamw": bench_torch_adamw, "sgd": bench_sgd}
 
 
 if __name__ == "__main__":

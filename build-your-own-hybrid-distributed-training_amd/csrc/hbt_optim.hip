@@ -167,6 +167,99 @@ __global__ __launch_bounds__(kAdamBlock) void adamw_kernel(AdamTable tab, AdamSc
     }
 }
 
+// ---- SGD -------------------------------------------------------------------------
+// torch's single-tensor SGD (torch/optim/sgd.py, _single_tensor_sgd) per element, with
+// the unscale and clip multiplies in front.  Every `x.add(y, alpha=a)` of torch's CPU
+// path is one fused multiply-add, fma(y, a, x); mul_ is one rounded multiply.
+enum SgdMode { kSgdPlain = 0, kSgdFirst = 1, kSgdMomentum = 2 };
+
+struct SgdTable {
+    float* p[kMaxT];
+    const void* g[kMaxT];
+    float* buf[kMaxT];
+    int64_t n[kMaxT];
+    int64_t first_block[kMaxT + 1];
+    int32_t vec_ok[kMaxT];
+    int32_t count;
+};
+
+struct SgdScalars {
+    float unscale;
+    float weight_decay;
+    float momentum;
+    float one_minus_dampening;
+    float neg_lr;
+    int32_t apply_weight_decay;
+    int32_t nesterov;
+};
+
+template <bool kUnscale, int kMode>
+__device__ __forceinline__ void sgd_update(float& p, float g, float& buf, float gmul, const SgdScalars& s) {
+    if constexpr (kUnscale) g = g * s.unscale;
+    g = g * gmul;
+    if (s.apply_weight_decay) g = __builtin_fmaf(p, s.weight_decay, g);  // grad.add(param, alpha=wd)
+    if constexpr (kMode == kSgdFirst) {
+        buf = g;  // the buffer starts as a clone of the gradient
+    } else if constexpr (kMode == kSgdMomentum) {
+        buf = buf * s.momentum;
+        buf = __builtin_fmaf(g, s.one_minus_dampening, buf);  // buf.mul_(m).add_(grad, alpha=1-d)
+    }
+    if constexpr (kMode != kSgdPlain) g = s.nesterov ? __builtin_fmaf(buf, s.momentum, g) : buf;
+    p = __builtin_fmaf(g, s.neg_lr, p);  // param.add_(grad, alpha=-lr)
+}
+
+template <typename GradT, bool kUnscale, int kMode>
+__global__ __launch_bounds__(kAdamBlock) void sgd_kernel(SgdTable tab, SgdScalars s,
+                                                         const float* __restrict__ grad_mul) {
+    const int64_t block = blockIdx.x;
+    int t = 0;
+    while (t + 1 < tab.count && block >= tab.first_block[t + 1]) ++t;
+    const int64_t base = (block - tab.first_block[t]) * kAdamTile;
+    const int64_t n = tab.n[t];
+    const float gmul = grad_mul != nullptr ? *grad_mul : 1.0f;
+    float* __restrict__ P = tab.p[t];
+    const GradT* __restrict__ G = static_cast<const GradT*>(tab.g[t]);
+    float* __restrict__ B = tab.buf[t];
+    if (tab.vec_ok[t] && base + kAdamTile <= n) {
+        f32x4 pv[kAdamUnroll], gv[kAdamUnroll], bv[kAdamUnroll];
+#pragma unroll
+        for (int u = 0; u < kAdamUnroll; ++u) {
+            const int64_t e = base + (int64_t(u) * kAdamBlock + threadIdx.x) * 4;
+            gv[u] = ld_grad4_nt(G + e);
+            if constexpr (kMode == kSgdMomentum) {
+                wait_vmem();
+                bv[u] = ld4_nt(B + e);
+            }
+            wait_vmem();
+            pv[u] = ld4_nt(P + e);
+        }
+#pragma unroll
+        for (int u = 0; u < kAdamUnroll; ++u) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                float p = pv[u][c], b = kMode == kSgdMomentum ? bv[u][c] : 0.0f;
+                sgd_update<kUnscale, kMode>(p, gv[u][c], b, gmul, s);
+                pv[u][c] = p;
+                bv[u][c] = b;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kAdamUnroll; ++u) {
+            const int64_t e = base + (int64_t(u) * kAdamBlock + threadIdx.x) * 4;
+            if constexpr (kMode != kSgdPlain) st4_nt(B + e, bv[u]);
+            st4_nt(P + e, pv[u]);
+        }
+    } else {
+        const int64_t end = base + kAdamTile < n ? base + kAdamTile : n;
+        for (int64_t e = base + threadIdx.x; e < end; e += kAdamBlock) {
+            float p = P[e], b = kMode == kSgdMomentum ? B[e] : 0.0f;
+            sgd_update<kUnscale, kMode>(p, ld_grad1(G + e), b, gmul, s);
+            P[e] = p;
+            if constexpr (kMode != kSgdPlain) B[e] = b;
+        }
+    }
+}
+
 // ---- squared norm ------------------------------------------------------------------
 struct NormTable {
     const void* g[kMaxT];
@@ -689,6 +782,81 @@ int32_t hbt_grad_local_share_sqnorm(const void* const* rank_grads, int32_t group
             partials);
     }
     return check_launch("hbt_grad_local_share_sqnorm");
+}
+
+
+int32_t hbt_sgd_step(float* const* params, const void* const* grads, float* const* momentum_buffers,
+                     const int64_t* numels, int32_t count, int32_t grad_dtype, float unscale,
+                     const float* grad_mul, float weight_decay, float momentum, float one_minus_dampening,
+                     float neg_lr, int32_t flags, void* stream) {
+    clear_error();
+    if (count < 0 || count > kMaxT) {
+        set_error("hbt_sgd_step: count must lie in [0, %d], got %d", kMaxT, count);
+        return HBT_ERR_INVALID_ARGUMENT;
+    }
+    if (grad_dtype != HBT_DTYPE_F32 && grad_dtype != HBT_DTYPE_BF16) {
+        set_error("hbt_sgd_step: gradient dtype %d is not F32 or BF16", grad_dtype);
+        return HBT_ERR_INVALID_ARGUMENT;
+    }
+    if ((flags & ~(HBT_SGD_MOMENTUM | HBT_SGD_FIRST_STEP | HBT_SGD_NESTEROV | HBT_SGD_WEIGHT_DECAY)) != 0 ||
+        ((flags & (HBT_SGD_FIRST_STEP | HBT_SGD_NESTEROV)) != 0 && (flags & HBT_SGD_MOMENTUM) == 0)) {
+        set_error("hbt_sgd_step: bad flags 0x%x", flags);
+        return HBT_ERR_INVALID_ARGUMENT;
+    }
+    const bool with_momentum = (flags & HBT_SGD_MOMENTUM) != 0;
+    if (count > 0 && (params == nullptr || grads == nullptr || numels == nullptr ||
+                      (with_momentum && momentum_buffers == nullptr))) {
+        set_error("hbt_sgd_step: null pointer argument");
+        return HBT_ERR_INVALID_ARGUMENT;
+    }
+    SgdTable tab{};
+    tab.count = count;
+    const uintptr_t grad_align = grad_dtype == HBT_DTYPE_F32 ? 16 : 8;
+    int64_t blocks = 0;
+    for (int i = 0; i < count; ++i) {
+        if (numels[i] < 0 || (numels[i] > 0 && (params[i] == nullptr || grads[i] == nullptr ||
+                                                (with_momentum && momentum_buffers[i] == nullptr)))) {
+            set_error("hbt_sgd_step: tensor %d has a bad pointer or numel", i);
+            return HBT_ERR_INVALID_ARGUMENT;
+        }
+        tab.p[i] = params[i];
+        tab.g[i] = grads[i];
+        tab.buf[i] = with_momentum ? momentum_buffers[i] : nullptr;
+        tab.n[i] = numels[i];
+        tab.vec_ok[i] = aligned(params[i], 16) && aligned(grads[i], grad_align) &&
+                        (!with_momentum || aligned(momentum_buffers[i], 16));
+        tab.first_block[i] = blocks;
+        blocks += (numels[i] + kAdamTile - 1) / kAdamTile;
+    }
+    tab.first_block[count] = blocks;
+    for (int i = count + 1; i <= kMaxT; ++i) tab.first_block[i] = blocks;
+    if (blocks == 0) return HBT_OK;
+    if (blocks > 0x7FFFFFFFLL) {
+        set_error("hbt_sgd_step: %lld tiles exceed the grid limit", static_cast<long long>(blocks));
+        return HBT_ERR_UNSUPPORTED;
+    }
+    SgdScalars sc{unscale, weight_decay, momentum, one_minus_dampening, neg_lr,
+                  (flags & HBT_SGD_WEIGHT_DECAY) != 0, (flags & HBT_SGD_NESTEROV) != 0};
+    const int mode = !with_momentum ? kSgdPlain : ((flags & HBT_SGD_FIRST_STEP) ? kSgdFirst : kSgdMomentum);
+    const bool scaled = unscale != 1.0f;
+    const dim3 grid(static_cast<unsigned>(blocks));
+    hipStream_t st = as_stream(stream);
+#define HBT_SGD_LAUNCH(GT, SCALED, MODE) \
+    sgd_kernel<GT, SCALED, MODE><<<grid, kAdamBlock, 0, st>>>(tab, sc, grad_mul)
+#define HBT_SGD_MODES(GT, SCALED)                                          \
+    do {                                                                   \
+        if (mode == kSgdPlain) HBT_SGD_LAUNCH(GT, SCALED, kSgdPlain);      \
+        else if (mode == kSgdFirst) HBT_SGD_LAUNCH(GT, SCALED, kSgdFirst); \
+        else HBT_SGD_LAUNCH(GT, SCALED, kSgdMomentum);                     \
+    } while (0)
+    if (grad_dtype == HBT_DTYPE_F32) {
+        if (scaled) HBT_SGD_MODES(float, true); else HBT_SGD_MODES(float, false);
+    } else {
+        if (scaled) HBT_SGD_MODES(uint16_t, true); else HBT_SGD_MODES(uint16_t, false);
+    }
+#undef HBT_SGD_MODES
+#undef HBT_SGD_LAUNCH
+    return check_launch("hbt_sgd_step");
 }
 
 }  // extern "C"

@@ -28,6 +28,10 @@ __all__ = [
     "ABI_VERSION",
     "COPY_OP_COPY",
     "COPY_OP_DIVIDE",
+    "SGD_FIRST_STEP",
+    "SGD_MOMENTUM",
+    "SGD_NESTEROV",
+    "SGD_WEIGHT_DECAY",
     "CopyPlan",
     "DTYPE_BF16",
     "DTYPE_F16",
@@ -45,7 +49,7 @@ __all__ = [
     "stream_of",
 ]
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 MAX_TENSORS_PER_LAUNCH = 16
 MAX_LOCAL_RANKS = 64
 
@@ -56,6 +60,10 @@ DTYPE_F64 = 3
 
 COPY_OP_COPY = 0
 COPY_OP_DIVIDE = 1
+SGD_MOMENTUM = 1
+SGD_FIRST_STEP = 2
+SGD_NESTEROV = 4
+SGD_WEIGHT_DECAY = 8
 
 _c_void_p = ctypes.c_void_p
 _c_i32 = ctypes.c_int32
@@ -77,6 +85,13 @@ EXPORTED_SYMBOLS: dict[str, tuple[object, tuple[object, ...]]] = {
             _ptr_array, _ptr_array, _ptr_array, _ptr_array, _i64_array, _c_i32, _c_i32,
             _c_f32, _c_void_p, _c_f32, _c_f32, _c_f32, _c_f32, _c_f32, _c_f32, _c_f32,
             _c_void_p,
+        ),
+    ),
+    "hbt_sgd_step": (
+        _c_i32,
+        (
+            _ptr_array, _ptr_array, _ptr_array, _i64_array, _c_i32, _c_i32, _c_f32, _c_void_p,
+            _c_f32, _c_f32, _c_f32, _c_f32, _c_i32, _c_void_p,
         ),
     ),
     "hbt_norm_partials_count": (_c_i64, (_i64_array, _c_i32, _c_i32)),

@@ -449,15 +449,6 @@ class ShardedOptimizer:
                     resolution="keep the optimizer state in HBM (288 GB per device)",
                 )
             )
-        if config.name != "adamw":
-            raise UnsupportedFeatureError(
-                format_error(
-                    "optim.ShardedOptimizer",
-                    "only the AdamW inner optimizer has a HIP kernel in this build",
-                    expected="adamw",
-                    observed=config.name,
-                )
-            )
         _check_group(norm_group, "optim.ShardedOptimizer")
         self._optimizer = build_inner_optimizer(self._parameters, config)
         for param in self._parameters:
@@ -581,45 +572,59 @@ class ShardedOptimizer:
 
     # -- update ----------------------------------------------------------------------
     def step(self) -> None:
-        """One AdamW step over this rank's shards (``sharded_optimizer.py:340-355``)."""
+        """One AdamW or SGD step over this rank's shards (``sharded_optimizer.py:340-355``)."""
         mul = self._pending_mul if self._pending_valid() else None
         self._run_step(mul)
 
     def _run_step(self, grad_mul: torch.Tensor | None) -> None:
+        if isinstance(self._optimizer, torch.optim.SGD):
+            self._run_sgd_step(grad_mul)
+        else:
+            self._run_adamw_step(grad_mul)
+        self._pending_mul = None
+        self._pending_signature = None
+
+    def _checked_grad(self, p: nn.Parameter, group: dict) -> torch.Tensor | None:
+        if group.get("amsgrad") or group.get("maximize"):
+            raise UnsupportedFeatureError(
+                format_error(
+                    "optim.ShardedOptimizer.step",
+                    "amsgrad and maximize have no HIP kernel in this build",
+                    observed={"amsgrad": group.get("amsgrad"), "maximize": group.get("maximize")},
+                )
+            )
+        grad = p.grad
+        if grad is None:
+            return None
+        _native.require_device_tensor(grad, "optim.ShardedOptimizer.step")
+        if grad.shape != p.shape or not grad.is_contiguous() or not p.is_contiguous():
+            raise ShardingError(
+                format_error(
+                    "optim.ShardedOptimizer.step",
+                    "gradient and parameter must be dense and of equal shape",
+                    expected=tuple(p.shape),
+                    observed=tuple(grad.shape),
+                )
+            )
+        if grad.dtype not in (torch.float32, torch.bfloat16):
+            raise UnsupportedFeatureError(
+                format_error("optim.ShardedOptimizer.step",
+                             "gradients must be float32 or bfloat16", observed=str(grad.dtype))
+            )
+        return grad
+
+    def _run_adamw_step(self, grad_mul: torch.Tensor | None) -> None:
         lib = _native.library()
         batches: dict[tuple, list[nn.Parameter]] = {}
         for group in self._optimizer.param_groups:
-            if group.get("amsgrad") or group.get("maximize"):
-                raise UnsupportedFeatureError(
-                    format_error(
-                        "optim.ShardedOptimizer.step",
-                        "amsgrad and maximize have no HIP kernel in this build",
-                        observed={"amsgrad": group.get("amsgrad"), "maximize": group.get("maximize")},
-                    )
-                )
             lr = float(group["lr"])
             beta1, beta2 = (float(b) for b in group["betas"])
             eps = float(group["eps"])
             weight_decay = float(group["weight_decay"])
             for p in group["params"]:
-                grad = p.grad
+                grad = self._checked_grad(p, group)
                 if grad is None:
                     continue
-                _native.require_device_tensor(grad, "optim.ShardedOptimizer.step")
-                if grad.shape != p.shape or not grad.is_contiguous() or not p.is_contiguous():
-                    raise ShardingError(
-                        format_error(
-                            "optim.ShardedOptimizer.step",
-                            "gradient and parameter must be dense and of equal shape",
-                            expected=tuple(p.shape),
-                            observed=tuple(grad.shape),
-                        )
-                    )
-                if grad.dtype not in (torch.float32, torch.bfloat16):
-                    raise UnsupportedFeatureError(
-                        format_error("optim.ShardedOptimizer.step",
-                                     "gradients must be float32 or bfloat16", observed=str(grad.dtype))
-                    )
                 state = self._optimizer.state[p]
                 if len(state) == 0:
                     # Same initial state as torch.optim.Adam._init_group.
@@ -669,8 +674,61 @@ class ShardedOptimizer:
                     increment_version(chunk)
                     increment_version([s["exp_avg"] for s in states])
                     increment_version([s["exp_avg_sq"] for s in states])
-        self._pending_mul = None
-        self._pending_signature = None
+
+    def _run_sgd_step(self, grad_mul: torch.Tensor | None) -> None:
+        """torch.optim.SGD's step (``torch/optim/sgd.py``) as one fused kernel per batch."""
+        lib = _native.library()
+        batches: dict[tuple, list[nn.Parameter]] = {}
+        for group in self._optimizer.param_groups:
+            lr = float(group["lr"])
+            momentum = float(group["momentum"])
+            dampening = float(group["dampening"])
+            weight_decay = float(group["weight_decay"])
+            nesterov = bool(group["nesterov"])
+            for p in group["params"]:
+                grad = self._checked_grad(p, group)
+                if grad is None:
+                    continue
+                flags = 0
+                if weight_decay != 0:
+                    flags |= _native.SGD_WEIGHT_DECAY
+                if momentum != 0:
+                    flags |= _native.SGD_MOMENTUM
+                    if nesterov:
+                        flags |= _native.SGD_NESTEROV
+                    state = self._optimizer.state[p]
+                    if state.get("momentum_buffer") is None:
+                        # torch starts the buffer as a clone of the first gradient.
+                        state["momentum_buffer"] = torch.empty_like(p, memory_format=torch.preserve_format)
+                        flags |= _native.SGD_FIRST_STEP
+                # Scalars exactly as torch forms them: Python doubles, rounded to fp32.
+                scalars = (weight_decay, momentum, 1 - dampening, -lr)
+                key = (scalars, flags, grad.dtype, _pending_unscale(grad))
+                batches.setdefault(key, []).append(p)
+        stream = _native.stream_of(self._device)
+        with torch.cuda.device(self._device):
+            for (scalars, flags, gdtype, unscale), params in batches.items():
+                for start in range(0, len(params), _native.MAX_TENSORS_PER_LAUNCH):
+                    chunk = params[start : start + _native.MAX_TENSORS_PER_LAUNCH]
+                    buffers = ([self._optimizer.state[p]["momentum_buffer"] for p in chunk]
+                               if flags & _native.SGD_MOMENTUM else [])
+                    status = lib.hbt_sgd_step(
+                        _native.pointer_array([p.data_ptr() for p in chunk]),
+                        _native.pointer_array([p.grad.data_ptr() for p in chunk]),
+                        _native.pointer_array([b.data_ptr() for b in buffers]) if buffers else None,
+                        _native.int64_array([p.numel() for p in chunk]),
+                        len(chunk),
+                        _native.dtype_code(gdtype),
+                        unscale,
+                        None if grad_mul is None else grad_mul.data_ptr(),
+                        *scalars,
+                        flags,
+                        stream,
+                    )
+                    _native.check(status, "optim.hbt_sgd_step")
+                    increment_version(chunk)
+                    if buffers:
+                        increment_version(buffers)
 
     def zero_grad(self, *, set_to_none: bool = True) -> None:
         """Release or zero the gradients (``sharded_optimizer.py:357-372``)."""

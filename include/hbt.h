@@ -80,6 +80,33 @@ int32_t hbt_adamw_step(float* const* params, const void* const* grads, float* co
                        float bias_correction2_sqrt, float eps, float neg_step_size, void* stream);
 
 /* ------------------------------------------------------------------------------
+ * Fused gradient-clip + SGD step over up to HBT_MAX_TENSORS_PER_LAUNCH tensors.
+ *
+ * Replaces: ShardedOptimizer.step (optim/sharded_optimizer.py:340-355) ->
+ *   torch.optim.SGD built at optim/sharded_optimizer.py:121-126 ->
+ *   torch/optim/sgd.py (_single_tensor_sgd), preceded by the clip and unscale
+ *   multiplies as in hbt_adamw_step.
+ * Per element, in fp32, with fma() a single rounding as torch's CPU `add(.., alpha=)`:
+ *   g = (g_in * unscale) * (*grad_mul)          (unscale skipped when 1; grad_mul NULL = 1)
+ *   if HBT_SGD_WEIGHT_DECAY:  g = fma(p, weight_decay, g)
+ *   if HBT_SGD_MOMENTUM:
+ *       if HBT_SGD_FIRST_STEP: buf = g
+ *       else:                  buf = fma(g, one_minus_dampening, buf * momentum)
+ *       g = HBT_SGD_NESTEROV ? fma(buf, momentum, g) : buf
+ *   p = fma(g, neg_lr, p)
+ * momentum_buffers may be NULL without HBT_SGD_MOMENTUM.  Flags other than the four
+ * below, or FIRST_STEP / NESTEROV without MOMENTUM, are rejected.
+ * ---------------------------------------------------------------------------- */
+#define HBT_SGD_MOMENTUM 1
+#define HBT_SGD_FIRST_STEP 2
+#define HBT_SGD_NESTEROV 4
+#define HBT_SGD_WEIGHT_DECAY 8
+int32_t hbt_sgd_step(float* const* params, const void* const* grads, float* const* momentum_buffers,
+                     const int64_t* numels, int32_t count, int32_t grad_dtype, float unscale,
+                     const float* grad_mul, float weight_decay, float momentum, float one_minus_dampening,
+                     float neg_lr, int32_t flags, void* stream);
+
+/* ------------------------------------------------------------------------------
  * Deterministic squared L2 norm, stage 1: per-block fp64 partial sums.
  *
  * Replaces: NormContribution.squared_norm (optim/sharded_optimizer.py:145-158)

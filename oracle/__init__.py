@@ -33,6 +33,7 @@ __all__ = [
     "local_share",
     "pack_shard",
     "read_range",
+    "sgd_step",
     "sqnorm",
     "unpack_full",
 ]
@@ -57,6 +58,8 @@ PINNED_BY = {
     "adamw_step": "torch.optim.AdamW on CPU: bitwise with torch's own sqrt injected, within "
     "1e-6 relative otherwise; closed form of step 1",
     "f32_to_bf16": "torch Tensor.to(torch.bfloat16) bitwise on specials and random values",
+    "sgd_step": "torch.optim.SGD(foreach=False) on CPU, bitwise, with and without momentum, "
+    "weight decay, dampening and Nesterov; closed form of a plain step",
     "read_range": "reference known answers: shards_overlapping [(0,(0,3)),(1,(3,1))] "
     "(test_checkpoint_format.py:242-247); bitwise re-slicing of the global flat vector",
     "local_share": "torch Tensor.div + add + padding zero, bitwise (order-free for G <= 2; "
@@ -81,6 +84,10 @@ def library() -> ctypes.CDLL:
         lib.oracle_adamw_bf16grad.argtypes = [f32p, u16p, f32p, f32p, ctypes.c_int64] + [
             ctypes.c_float
         ] * 9
+        lib.oracle_sgd.restype = None
+        lib.oracle_sgd.argtypes = [f32p, f32p, f32p, ctypes.c_int64, ctypes.c_float, ctypes.c_float,
+                                   ctypes.c_int, ctypes.c_float, ctypes.c_int, ctypes.c_float,
+                                   ctypes.c_float, ctypes.c_int, ctypes.c_float]
         lib.oracle_sqnorm_f32.restype = ctypes.c_double
         lib.oracle_sqnorm_f32.argtypes = [f32p, ctypes.c_int64, ctypes.c_float]
         lib.oracle_sqnorm_bf16.restype = ctypes.c_double
@@ -141,6 +148,31 @@ def adamw_step(
     override = None if sqrt_override is None else _f32(np.ascontiguousarray(sqrt_override, np.float32))
     lib.oracle_adamw_f32(_f32(p), _f32(np.ascontiguousarray(g)), _f32(m), _f32(v), n, unscale, grad_mul,
                          *scalars, override)
+
+
+def sgd_step(
+    p: np.ndarray,
+    g: np.ndarray,
+    buf: np.ndarray | None,
+    *,
+    lr: float,
+    momentum: float = 0.0,
+    dampening: float = 0.0,
+    weight_decay: float = 0.0,
+    nesterov: bool = False,
+    first: bool = False,
+    unscale: float = 1.0,
+    grad_mul: float = 1.0,
+) -> None:
+    """One SGD step in place on fp32 ``p`` (and ``buf``), torch's scalars rounded to fp32."""
+    assert p.dtype == np.float32 and p.flags.c_contiguous and g.dtype == np.float32
+    mode = 0 if momentum == 0 else (1 if first else 2)
+    if mode:
+        assert buf is not None and buf.dtype == np.float32 and buf.flags.c_contiguous
+    b = _f32(buf) if buf is not None else None
+    library().oracle_sgd(_f32(p), _f32(np.ascontiguousarray(g)), b, p.size, unscale, grad_mul,
+                         int(weight_decay != 0), weight_decay, mode, momentum, 1 - dampening,
+                         int(nesterov), -lr)
 
 
 # ---------------------------------------------------------------------------------------

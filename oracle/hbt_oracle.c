@@ -26,6 +26,16 @@
  *       sqrt is correctly rounded (sqrtf) unless `sqrt_override` supplies the square
  *       roots to use; the tests pass torch's own exp_avg_sq.sqrt() there, which pins
  *       every other operation of the restatement bitwise against torch.
+ *   oracle_sgd - torch.optim.SGD's single-tensor path on CPU tensors,
+ *       torch/optim/sgd.py (_single_tensor_sgd, torch 2.10.0), which the reference
+ *       builds at optim/sharded_optimizer.py:121-126.  torch's CPU `add(.., alpha=a)`
+ *       is one fused multiply-add (pinned by the tests), `mul_` one rounded multiply:
+ *         grad = grad.add(param, alpha=wd)            fma(p, wd, g)      (wd != 0)
+ *         buf = grad.clone()                           first step
+ *         buf.mul_(m).add_(grad, alpha=1-dampening)    fma(g, 1-d, buf*m) later steps
+ *         grad = grad.add(buf, alpha=m) | buf          nesterov | plain
+ *         param.add_(grad, alpha=-lr)                  fma(g, -lr, p)
+ *       preceded by the unscale and clip multiplies, as for AdamW.
  *   oracle_sqnorm_* - sum of (double)(g * unscale)^2 with Neumaier compensation, the
  *       quantity NormContribution.squared_norm computes in fp64
  *       (optim/sharded_optimizer.py:145-158).
@@ -94,6 +104,26 @@ static void neumaier_add(double* sum, double* comp, double x) {
         *comp += (x - t) + *sum;
     }
     *sum = t;
+}
+
+/* mode: 0 no momentum, 1 momentum first step (buf := g), 2 momentum. */
+void oracle_sgd(float* p, const float* g, float* buf, int64_t n, float unscale, float grad_mul,
+                int apply_wd, float wd, int mode, float momentum, float one_minus_dampening,
+                int nesterov, float neg_lr) {
+    for (int64_t i = 0; i < n; ++i) {
+        float x = g[i];
+        if (unscale != 1.0f) x = x * unscale;
+        x = x * grad_mul;
+        if (apply_wd) x = fmaf(p[i], wd, x);
+        if (mode == 1) {
+            buf[i] = x;
+        } else if (mode == 2) {
+            const float b = buf[i] * momentum;
+            buf[i] = fmaf(x, one_minus_dampening, b);
+        }
+        if (mode != 0) x = nesterov ? fmaf(buf[i], momentum, x) : buf[i];
+        p[i] = fmaf(x, neg_lr, p[i]);
+    }
 }
 
 double oracle_sqnorm_f32(const float* g, int64_t n, float unscale) {
