@@ -414,6 +414,86 @@ def _grad_signature(params: Sequence[nn.Parameter]) -> tuple[tuple[int, int, int
     return tuple(sig)
 
 
+def _pinned_like(p: torch.Tensor) -> torch.Tensor:
+    """An uninitialised host tensor shaped like ``p``, in pinned (page-locked) memory."""
+    return torch.empty(p.shape, dtype=p.dtype, device="cpu", pin_memory=True)
+
+
+class _HostStatePipeline:
+    """Streams host-resident optimizer state through device staging buffers.
+
+    The reference's offload path (``sharded_optimizer.py:284-296``, ``:342-353``) keeps
+    master parameters and state on the host, copies gradients down, steps on the CPU
+    and copies parameters back up, all synchronously.  Here the step runs on the
+    device parameter itself, and the state travels in chunks: while chunk ``c`` is
+    updated on the compute stream, chunk ``c + 1``'s state is uploaded on one copy
+    stream and chunk ``c - 1``'s updated state and master parameter are written back
+    on another.  Two staging slots per state tensor bound the device memory used.
+    """
+
+    #: Elements per chunk (128 MB of fp32 per state tensor and slot).
+    chunk_elems = 1 << 25
+    slots = 2
+
+    def __init__(self, device: torch.device) -> None:
+        self.device = device
+        self.upload = torch.cuda.Stream(device)
+        self.download = torch.cuda.Stream(device)
+        self._staging: dict[tuple[int, int], torch.Tensor] = {}
+        self.done: torch.cuda.Event | None = None
+
+    def _stage(self, slot: int, k: int, n: int) -> torch.Tensor:
+        buf = self._staging.get((slot, k))
+        if buf is None or buf.numel() < n:
+            buf = torch.empty(n, dtype=torch.float32, device=self.device)
+            self._staging[(slot, k)] = buf
+        return buf[:n]
+
+    def run(self, device_param: torch.Tensor, host_param: torch.Tensor, host_states: list[torch.Tensor],
+            load_states: bool, launch) -> None:
+        """Update ``device_param`` chunk by chunk; ``launch(start, n, staged)`` runs the kernel."""
+        compute = torch.cuda.current_stream(self.device)
+        flat_dev = device_param.detach().view(-1)
+        flat_host = host_param.detach().view(-1)
+        flat_states = [s.view(-1) for s in host_states]
+        total = flat_dev.numel()
+        free: list[torch.cuda.Event | None] = [None] * self.slots
+        self.upload.wait_stream(compute)  # the previous step's copies and kernels are done
+        for index, start in enumerate(range(0, total, self.chunk_elems)):
+            n = min(self.chunk_elems, total - start)
+            slot = index % self.slots
+            staged = [self._stage(slot, k, n) for k in range(len(flat_states))]
+            loaded = torch.cuda.Event()
+            with torch.cuda.stream(self.upload):
+                if free[slot] is not None:
+                    self.upload.wait_event(free[slot])
+                if load_states:
+                    for d, h in zip(staged, flat_states):
+                        d.copy_(h[start : start + n], non_blocking=True)
+                loaded.record(self.upload)
+            compute.wait_event(loaded)
+            launch(start, n, staged)
+            computed = torch.cuda.Event()
+            computed.record(compute)
+            released = torch.cuda.Event()
+            with torch.cuda.stream(self.download):
+                self.download.wait_event(computed)
+                for d, h in zip(staged, flat_states):
+                    h[start : start + n].copy_(d, non_blocking=True)
+                flat_host[start : start + n].copy_(flat_dev[start : start + n], non_blocking=True)
+                released.record(self.download)
+            free[slot] = released
+        end = torch.cuda.Event()
+        end.record(self.download)
+        compute.wait_event(end)  # later device work sees the finished copies
+        self.done = end
+
+    def synchronize(self) -> None:
+        """Block the host until the last step's write-back has landed."""
+        if self.done is not None:
+            self.done.synchronize()
+
+
 class ShardedOptimizer:
     """AdamW over this rank's shards with a global-norm clip, on HIP kernels.
 
@@ -439,18 +519,7 @@ class ShardedOptimizer:
         self._device = torch.device(device)
         self._recorder = recorder
         self._defer_clip = defer_clip
-        if config.cpu_offload_state:
-            raise UnsupportedFeatureError(
-                format_error(
-                    "optim.ShardedOptimizer",
-                    "optimizer-state CPU offload is not part of this build",
-                    expected="cpu_offload_state=False",
-                    observed=True,
-                    resolution="keep the optimizer state in HBM (288 GB per device)",
-                )
-            )
         _check_group(norm_group, "optim.ShardedOptimizer")
-        self._optimizer = build_inner_optimizer(self._parameters, config)
         for param in self._parameters:
             _native.require_device_tensor(param, "optim.ShardedOptimizer")
             if param.dtype != torch.float32:
@@ -461,10 +530,24 @@ class ShardedOptimizer:
                         observed=str(param.dtype),
                     )
                 )
+        self._offload = bool(config.cpu_offload_state) and self._device.type != "cpu"
+        if self._offload:
+            # As in the reference, master copies live on the host and the inner
+            # optimizer's state is keyed by them; here they and the state sit in
+            # pinned memory and stream through the device every step.
+            self._cpu_parameters = [
+                nn.Parameter(_pinned_like(p).copy_(p.detach()), requires_grad=True) for p in self._parameters
+            ]
+            self._optimizer = build_inner_optimizer(self._cpu_parameters, config)
+            self._pipeline: _HostStatePipeline | None = _HostStatePipeline(self._device)
+        else:
+            self._cpu_parameters = []
+            self._optimizer = build_inner_optimizer(self._parameters, config)
+            self._pipeline = None
+        self._device_param = {id(h): d for h, d in zip(self._cpu_parameters, self._parameters)}
         self._contributions = build_gradient_norm_contributions(
             self._parameters, world_size=norm_group.size
         )
-        self._offload = False
         self._pending_mul: torch.Tensor | None = None
         self._pending_signature: tuple[tuple[int, int, int], ...] | None = None
         self._last_check: tuple[tuple[tuple[int, int, int], ...], torch.Tensor] | None = None
@@ -622,15 +705,15 @@ class ShardedOptimizer:
             eps = float(group["eps"])
             weight_decay = float(group["weight_decay"])
             for p in group["params"]:
-                grad = self._checked_grad(p, group)
+                grad = self._checked_grad(self._device_param.get(id(p), p), group)
                 if grad is None:
                     continue
                 state = self._optimizer.state[p]
                 if len(state) == 0:
                     # Same initial state as torch.optim.Adam._init_group.
                     state["step"] = torch.tensor(0.0, dtype=torch.float32)
-                    state["exp_avg"] = torch.zeros_like(p, memory_format=torch.preserve_format)
-                    state["exp_avg_sq"] = torch.zeros_like(p, memory_format=torch.preserve_format)
+                    state["exp_avg"] = self._zero_state(p)
+                    state["exp_avg_sq"] = self._zero_state(p)
                 step_t = state["step"]
                 step_t += 1
                 step = float(step_t.item())
@@ -652,8 +735,13 @@ class ShardedOptimizer:
                 key = (scalars, grad.dtype, _pending_unscale(grad))
                 batches.setdefault(key, []).append(p)
         stream = _native.stream_of(self._device)
+        mul_ptr = None if grad_mul is None else grad_mul.data_ptr()
         with torch.cuda.device(self._device):
             for (scalars, gdtype, unscale), params in batches.items():
+                if self._pipeline is not None:
+                    for p in params:
+                        self._offloaded_adamw(lib, p, scalars, gdtype, unscale, mul_ptr)
+                    continue
                 for start in range(0, len(params), _native.MAX_TENSORS_PER_LAUNCH):
                     chunk = params[start : start + _native.MAX_TENSORS_PER_LAUNCH]
                     states = [self._optimizer.state[p] for p in chunk]
@@ -666,7 +754,7 @@ class ShardedOptimizer:
                         len(chunk),
                         _native.dtype_code(gdtype),
                         unscale,
-                        None if grad_mul is None else grad_mul.data_ptr(),
+                        mul_ptr,
                         *scalars,
                         stream,
                     )
@@ -674,6 +762,45 @@ class ShardedOptimizer:
                     increment_version(chunk)
                     increment_version([s["exp_avg"] for s in states])
                     increment_version([s["exp_avg_sq"] for s in states])
+
+    def _place_state(self, value: torch.Tensor, reference: torch.Tensor) -> torch.Tensor:
+        """A loaded state tensor on the reference parameter's device and dtype (pinned if host)."""
+        if self._pipeline is not None:
+            return _pinned_like(reference).copy_(value.detach().reshape(reference.shape))
+        return value.to(device=reference.device, dtype=reference.dtype)
+
+    def _zero_state(self, p: torch.Tensor) -> torch.Tensor:
+        """A zero state tensor beside ``p``: in HBM, or pinned host memory when offloaded."""
+        if self._pipeline is not None:
+            return _pinned_like(p).zero_()
+        return torch.zeros_like(p, memory_format=torch.preserve_format)
+
+    def _offloaded_adamw(self, lib, host_p, scalars, gdtype, unscale, mul_ptr) -> None:
+        """AdamW on the device parameter with its host-resident state streamed through."""
+        dev = self._device_param[id(host_p)]
+        grad = dev.grad
+        state = self._optimizer.state[host_p]
+        stream = _native.stream_of(self._device)
+        gsize = grad.element_size()
+
+        def launch(start: int, n: int, staged: list[torch.Tensor]) -> None:
+            status = lib.hbt_adamw_step(
+                _native.pointer_array([dev.data_ptr() + 4 * start]),
+                _native.pointer_array([grad.data_ptr() + gsize * start]),
+                _native.pointer_array([staged[0].data_ptr()]),
+                _native.pointer_array([staged[1].data_ptr()]),
+                _native.int64_array([n]),
+                1,
+                _native.dtype_code(gdtype),
+                unscale,
+                mul_ptr,
+                *scalars,
+                stream,
+            )
+            _native.check(status, "optim.hbt_adamw_step")
+
+        self._pipeline.run(dev, host_p, [state["exp_avg"], state["exp_avg_sq"]], True, launch)
+        increment_version([dev, host_p, state["exp_avg"], state["exp_avg_sq"]])
 
     def _run_sgd_step(self, grad_mul: torch.Tensor | None) -> None:
         """torch.optim.SGD's step (``torch/optim/sgd.py``) as one fused kernel per batch."""
@@ -686,7 +813,7 @@ class ShardedOptimizer:
             weight_decay = float(group["weight_decay"])
             nesterov = bool(group["nesterov"])
             for p in group["params"]:
-                grad = self._checked_grad(p, group)
+                grad = self._checked_grad(self._device_param.get(id(p), p), group)
                 if grad is None:
                     continue
                 flags = 0
@@ -699,15 +826,21 @@ class ShardedOptimizer:
                     state = self._optimizer.state[p]
                     if state.get("momentum_buffer") is None:
                         # torch starts the buffer as a clone of the first gradient.
-                        state["momentum_buffer"] = torch.empty_like(p, memory_format=torch.preserve_format)
+                        state["momentum_buffer"] = (_pinned_like(p) if self._pipeline is not None
+                                                    else torch.empty_like(p, memory_format=torch.preserve_format))
                         flags |= _native.SGD_FIRST_STEP
                 # Scalars exactly as torch forms them: Python doubles, rounded to fp32.
                 scalars = (weight_decay, momentum, 1 - dampening, -lr)
                 key = (scalars, flags, grad.dtype, _pending_unscale(grad))
                 batches.setdefault(key, []).append(p)
         stream = _native.stream_of(self._device)
+        mul_ptr = None if grad_mul is None else grad_mul.data_ptr()
         with torch.cuda.device(self._device):
             for (scalars, flags, gdtype, unscale), params in batches.items():
+                if self._pipeline is not None:
+                    for p in params:
+                        self._offloaded_sgd(lib, p, scalars, flags, gdtype, unscale, mul_ptr)
+                    continue
                 for start in range(0, len(params), _native.MAX_TENSORS_PER_LAUNCH):
                     chunk = params[start : start + _native.MAX_TENSORS_PER_LAUNCH]
                     buffers = ([self._optimizer.state[p]["momentum_buffer"] for p in chunk]
@@ -720,7 +853,7 @@ class ShardedOptimizer:
                         len(chunk),
                         _native.dtype_code(gdtype),
                         unscale,
-                        None if grad_mul is None else grad_mul.data_ptr(),
+                        mul_ptr,
                         *scalars,
                         flags,
                         stream,
@@ -730,8 +863,41 @@ class ShardedOptimizer:
                     if buffers:
                         increment_version(buffers)
 
+    def _offloaded_sgd(self, lib, host_p, scalars, flags, gdtype, unscale, mul_ptr) -> None:
+        """SGD on the device parameter with its host-resident momentum buffer streamed through."""
+        dev = self._device_param[id(host_p)]
+        grad = dev.grad
+        stream = _native.stream_of(self._device)
+        gsize = grad.element_size()
+        momentum = bool(flags & _native.SGD_MOMENTUM)
+        host_states = [self._optimizer.state[host_p]["momentum_buffer"]] if momentum else []
+
+        def launch(start: int, n: int, staged: list[torch.Tensor]) -> None:
+            status = lib.hbt_sgd_step(
+                _native.pointer_array([dev.data_ptr() + 4 * start]),
+                _native.pointer_array([grad.data_ptr() + gsize * start]),
+                _native.pointer_array([staged[0].data_ptr()]) if staged else None,
+                _native.int64_array([n]),
+                1,
+                _native.dtype_code(gdtype),
+                unscale,
+                mul_ptr,
+                *scalars,
+                flags,
+                stream,
+            )
+            _native.check(status, "optim.hbt_sgd_step")
+
+        # A first step writes the buffer without reading it: nothing to upload.
+        self._pipeline.run(dev, host_p, host_states, not (flags & _native.SGD_FIRST_STEP), launch)
+        increment_version([dev, host_p, *host_states])
+
     def zero_grad(self, *, set_to_none: bool = True) -> None:
-        """Release or zero the gradients (``sharded_optimizer.py:357-372``)."""
+        """Release or zero the gradients (``sharded_optimizer.py:357-372``).
+
+        With offloaded state the host master copies never hold gradients (the step
+        reads the device gradients), so there is nothing to clear on the host.
+        """
         self._pending_mul = None
         self._pending_signature = None
         self._last_check = None
@@ -786,6 +952,8 @@ class ShardedOptimizer:
     # -- serialisation -------------------------------------------------------------------
     def state_dict(self) -> dict[str, Any]:
         """Optimizer state keyed by parameter index (``sharded_optimizer.py:420-443``)."""
+        if self._pipeline is not None:
+            self._pipeline.synchronize()
         inner = self._optimizer.state_dict()
         state: dict[int, dict[str, Any]] = {}
         for index, entry in inner["state"].items():
@@ -827,12 +995,13 @@ class ShardedOptimizer:
             merged.update(saved)
             merged["params"] = existing["params"]
             groups.append(merged)
+        target = self._cpu_parameters if self._pipeline is not None else self._parameters
         state: dict[int, dict[str, Any]] = {}
         for index, entry in payload["state"].items():
-            target = self._parameters[int(index)]
+            reference = target[int(index)]
             state[int(index)] = {
                 key: (
-                    value.to(device=target.device, dtype=target.dtype)
+                    self._place_state(value, reference)
                     if torch.is_tensor(value) and value.dtype.is_floating_point
                     and value.dim() > 0
                     else value
