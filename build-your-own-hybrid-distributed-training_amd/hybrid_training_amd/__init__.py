@@ -20,6 +20,7 @@ from .config import (
 from .errors import (
     CheckpointCorruptionError,
     CheckpointError,
+    CheckpointVersionError,
     HybridTrainingError,
     IncompleteCheckpointError,
     NativeKernelError,
@@ -31,7 +32,15 @@ from .buckets import BucketedGradients, BucketLayout, GradientBucket, build_buck
 from .flat_param import FlatParameter, FlatParamHandle, PieceLayout, ShardedTensorPiece, reshard_state_dict_pieces
 from .grad_scaler import GradScaler, GradScalerState
 from .groups import GroupHandle
-from .manifest import ShardRecord, TensorRecord, shard_filename, validate_shard_filename
+from .manifest import (
+    CheckpointManifest,
+    FileRecord,
+    ShardRecord,
+    TensorRecord,
+    checkpoint_directory_name,
+    shard_filename,
+    validate_shard_filename,
+)
 from .optim import (
     NormContribution,
     ShardedOptimizer,
@@ -40,6 +49,7 @@ from .optim import (
     distributed_gradient_norm,
 )
 from .reshard import DeviceShardCache, load_flat_shard, read_tensor_range
+from .checkpoint import ShardFileCache, collect_flat_shard_payload, load_flat_shard_checkpoint, write_checkpoint
 from .tensors import (
     FlatEntry,
     ShardRange,

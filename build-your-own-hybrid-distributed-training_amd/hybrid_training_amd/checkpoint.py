@@ -1,0 +1,424 @@
+"""Checkpoints on disk around the device interval copy: save pieces, load shards.
+
+The reference writes one ``rank-NNNNN.pt`` payload per rank (storage key ->
+1-D tensor), a ``manifest.json`` of global intervals with SHA-256 integrity
+records, and ``metadata.json``, into a staging directory that is renamed into
+place last (``checkpoint/writer.py:147-567``, ``checkpoint/format.py``).  It reads
+them back through ``ShardFileCache`` and ``read_tensor_range``
+(``checkpoint/reshard.py:54-305``, ``checkpoint/reader.py:314-470``), copying each
+piece twice on the CPU.
+
+This module keeps that format, its checks and its errors, and moves the tensor
+work to the device:
+
+* saving a flat shard copies the shard (and each optimizer-state tensor) to pinned
+  host memory in one transfer; the payload pieces are views into it, so no piece is
+  copied again (the reference moves and clones every piece separately);
+* :class:`ShardFileCache` verifies a file (name rule, containment, size, SHA-256),
+  loads it with ``weights_only=True`` and uploads its storage to the device once;
+* :func:`load_flat_shard_checkpoint` fills a rank's flat shard and its optimizer
+  state from any saved layout with one interval-copy launch per destination.
+"""
+
+from __future__ import annotations
+
+import json
+import uuid
+from collections.abc import Mapping, Sequence
+from pathlib import Path
+from typing import Any
+
+import torch
+from torch.autograd.graph import increment_version
+
+from .errors import CheckpointCorruptionError, CheckpointError, IncompleteCheckpointError, format_error
+from .manifest import (
+    CURRENT_FORMAT_VERSION,
+    MANIFEST_FILENAME,
+    METADATA_FILENAME,
+    CheckpointManifest,
+    FileRecord,
+    ShardRecord,
+    TensorRecord,
+    checkpoint_directory_name,
+    file_digest,
+    resolve_inside,
+    shard_filename,
+    staging_directory_name,
+    validate_shard_filename,
+)
+from .reshard import load_flat_shard
+
+__all__ = [
+    "ShardFileCache",
+    "collect_flat_shard_payload",
+    "load_flat_shard_checkpoint",
+    "write_checkpoint",
+]
+
+
+class ShardFileCache:
+    """Shard payload files, each verified, loaded and uploaded to the device at most once.
+
+    Same checks, errors and interface as ``ShardFileCache`` (``reshard.py:54-197``);
+    :meth:`get` returns device tensors, ready for the interval copy.
+    """
+
+    def __init__(
+        self,
+        directory: Path,
+        manifest: CheckpointManifest,
+        *,
+        verify_checksums: bool = True,
+        device: torch.device | None = None,
+    ) -> None:
+        self._directory = Path(directory)
+        self._manifest = manifest
+        self._verify = verify_checksums
+        self._device = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+        self._loaded: dict[str, dict[str, torch.Tensor]] = {}
+
+    def get(self, filename: str) -> Mapping[str, torch.Tensor]:
+        """The tensors stored in ``filename``, on the device."""
+        cached = self._loaded.get(filename)
+        if cached is not None:
+            return cached
+        validate_shard_filename(filename)
+        path = resolve_inside(self._directory, filename)
+        if not path.is_file():
+            raise IncompleteCheckpointError(
+                format_error(
+                    "reshard.ShardFileCache.get",
+                    "a shard file listed in the manifest is missing",
+                    expected=filename,
+                    observed="not present in the checkpoint directory",
+                    resolution=(
+                        "the checkpoint is incomplete; restore the missing file or "
+                        "resume from an earlier checkpoint"
+                    ),
+                )
+            )
+        record = self._manifest.files.get(filename)
+        if record is None:
+            raise CheckpointCorruptionError(
+                format_error(
+                    "reshard.ShardFileCache.get",
+                    "the file has no integrity record in the manifest",
+                    expected="an entry under manifest['files']",
+                    observed=filename,
+                    resolution="the manifest is truncated or hand-edited",
+                )
+            )
+        actual_size = path.stat().st_size
+        if actual_size != record.bytes:
+            raise CheckpointCorruptionError(
+                format_error(
+                    "reshard.ShardFileCache.get",
+                    f"shard file {filename!r} has the wrong size, so it was truncated "
+                    "or overwritten after the checkpoint was published",
+                    expected=f"{record.bytes} bytes",
+                    observed=f"{actual_size} bytes",
+                    resolution="restore the file from a backup or discard the checkpoint",
+                )
+            )
+        if self._verify:
+            digest = file_digest(path)
+            if digest != record.sha256:
+                raise CheckpointCorruptionError(
+                    format_error(
+                        "reshard.ShardFileCache.get",
+                        f"shard file {filename!r} failed checksum verification; its "
+                        "contents differ from what the writer recorded",
+                        expected=record.sha256,
+                        observed=digest,
+                        resolution=(
+                            "the file is corrupt; restore it from a backup or discard "
+                            "the checkpoint. Pass verify_checksums=False only when you "
+                            "have another reason to trust the bytes."
+                        ),
+                    )
+                )
+        try:
+            # weights_only=True admits tensors and primitives only: a hostile payload
+            # cannot execute code.
+            payload = torch.load(path, map_location="cpu", weights_only=True, mmap=True)
+        except Exception as exc:
+            raise CheckpointCorruptionError(
+                format_error(
+                    "reshard.ShardFileCache.get",
+                    f"shard file {filename!r} could not be deserialised",
+                    expected="a tensor mapping saved with torch.save",
+                    observed=repr(exc),
+                    resolution=(
+                        "the file is corrupt, or was written by a different tool; note "
+                        "that this reader deliberately refuses pickled objects other "
+                        "than tensors"
+                    ),
+                )
+            ) from exc
+        if not isinstance(payload, dict):
+            raise CheckpointCorruptionError(
+                format_error(
+                    "reshard.ShardFileCache.get",
+                    f"shard file {filename!r} does not contain a mapping",
+                    expected="dict[str, Tensor]",
+                    observed=type(payload).__name__,
+                    resolution="the file was not written by this package",
+                )
+            )
+        uploaded = _upload(payload, self._device)
+        self._loaded[filename] = uploaded
+        return uploaded
+
+    def clear(self) -> None:
+        """Drop every cached payload."""
+        self._loaded.clear()
+
+    @property
+    def loaded_files(self) -> tuple[str, ...]:
+        """Names of the files loaded so far."""
+        return tuple(sorted(self._loaded))
+
+
+def _upload(payload: Mapping[str, Any], device: torch.device) -> dict[str, torch.Tensor]:
+    """Every tensor of a payload on ``device``; tensors sharing a storage share one upload."""
+    storages: dict[int, torch.Tensor] = {}
+    out: dict[str, torch.Tensor] = {}
+    for key, value in payload.items():
+        if not torch.is_tensor(value):
+            continue
+        if not value.is_contiguous():
+            out[key] = value.contiguous().to(device)
+            continue
+        storage = value.untyped_storage()
+        base = storages.get(storage.data_ptr())
+        if base is None:
+            host_bytes = torch.empty(0, dtype=torch.uint8).set_(storage)
+            base = host_bytes.to(device)
+            storages[storage.data_ptr()] = base
+        size = value.element_size()
+        begin = value.storage_offset() * size
+        out[key] = base[begin : begin + value.numel() * size].view(value.dtype).view(value.shape)
+    return out
+
+
+def _pinned_copy(tensor: torch.Tensor) -> torch.Tensor:
+    """A 1-D pinned host copy of a device tensor (one transfer, on the current stream)."""
+    host = torch.empty(tensor.numel(), dtype=tensor.dtype, device="cpu", pin_memory=True)
+    host.copy_(tensor.detach().reshape(-1), non_blocking=True)
+    return host
+
+
+def collect_flat_shard_payload(
+    handle: Any,
+    *,
+    rank: int,
+    optimizer: Any = None,
+) -> tuple[dict[str, torch.Tensor], list[dict[str, Any]], dict[str, Any]]:
+    """One rank's payload, manifest records and optimizer scalars for a flat shard.
+
+    Mirrors ``_collect_payload`` (``checkpoint/writer.py:433-567``) for an FSDP flat
+    parameter: each piece of the shard is stored under ``model::{name}@{offset}``
+    and each piece of each optimizer-state tensor under
+    ``optimizer::{name}::{state}@{offset}``, in the parameter's own coordinates, so
+    any later layout can read them back.  Non-tensor state (AdamW's step) goes to
+    the scalars, which must agree across parameters.
+    """
+    filename = shard_filename(rank)
+    layout = handle.local_piece_layout()
+    payload: dict[str, torch.Tensor] = {}
+    records: list[dict[str, Any]] = []
+    scalars: dict[str, Any] = {}
+
+    def add(flat: torch.Tensor, *, key: str, category: str, state_name: str = "") -> None:
+        for item in layout:
+            storage_key = f"{category}::{key.format(name=item.name)}@{item.parameter_offset}"
+            payload[storage_key] = flat[item.local_offset : item.local_offset + item.length]
+            records.append({
+                "key": key.format(name=item.name),
+                "name": item.name,
+                "global_shape": list(item.global_shape),
+                "dtype": str(flat.dtype),
+                "category": category,
+                "partition_dim": None,
+                "tensor_parallel_size": 1,
+                "tensor_parallel_rank": 0,
+                "state_name": state_name,
+                "rank": rank,
+                "file": filename,
+                "offset": item.parameter_offset,
+                "length": item.length,
+                "storage_key": storage_key,
+            })
+
+    hosts = [_pinned_copy(handle.flat_param)]
+    add(hosts[0], key="{name}", category="model")
+    if optimizer is not None:
+        state = optimizer.inner.state.get(_state_key(optimizer, handle.flat_param), {})
+        for state_name, value in state.items():
+            if not torch.is_tensor(value) or value.dim() == 0 or value.numel() != handle.flat_param.numel():
+                scalar = value.item() if torch.is_tensor(value) else value
+                previous = scalars.get(state_name)
+                if previous is not None and previous != scalar:
+                    raise CheckpointError(
+                        format_error("checkpoint.save", f"optimizer state {state_name!r} differs between parameters",
+                                     rank=rank, expected=previous, observed=scalar)
+                    )
+                scalars[state_name] = scalar
+                continue
+            if value.device.type == "cpu":  # offloaded state already lives on the host
+                host = value.detach().reshape(-1)
+            else:
+                host = _pinned_copy(value)
+            hosts.append(host)
+            add(host, key="{name}::" + state_name, category="optimizer", state_name=state_name)
+    torch.cuda.current_stream(handle.flat_param.device).synchronize()
+    return payload, records, scalars
+
+
+def _state_key(optimizer: Any, param: torch.Tensor) -> torch.Tensor:
+    """The tensor the inner optimizer keys ``param``'s state by (its host master when offloaded)."""
+    hosts = getattr(optimizer, "_cpu_parameters", [])
+    for host, dev in zip(hosts, optimizer.parameters):
+        if dev is param:
+            return host
+    return param
+
+
+def write_checkpoint(
+    directory: Path,
+    step: int,
+    shards: Sequence[tuple[int, Mapping[str, torch.Tensor], Sequence[dict[str, Any]], Mapping[str, Any]]],
+    *,
+    topology: dict[str, Any] | None = None,
+    extra_metadata: dict[str, Any] | None = None,
+) -> Path:
+    """Write ``checkpoint-step-NNNNNN`` atomically from every rank's payload.
+
+    ``shards`` holds ``(rank, payload, records, scalars)`` per writer, as
+    :func:`collect_flat_shard_payload` returns them.  Files go to a staging
+    directory; the manifest is validated, written last, and the directory renamed
+    into place (``checkpoint/writer.py:147-430``).
+    """
+    root = Path(directory)
+    root.mkdir(parents=True, exist_ok=True)
+    final = root / checkpoint_directory_name(step)
+    if final.exists():
+        raise CheckpointError(
+            format_error("checkpoint.save", "a checkpoint for this step already exists", expected="a new step",
+                         observed=str(final), resolution="remove it or save under another step")
+        )
+    staging = root / staging_directory_name(final.name, uuid.uuid4().hex[:12])
+    staging.mkdir()
+    created_by = f"hybrid_training_amd {_version()}"
+    manifest = CheckpointManifest(writer_world_size=len(shards), topology=dict(topology or {}), step=step,
+                                  created_by=created_by)
+    optimizer_scalars: dict[str, Any] = {}
+    for rank, payload, records, scalars in shards:
+        name = shard_filename(rank)
+        path = staging / name
+        torch.save(dict(payload), path)
+        manifest.files[name] = FileRecord(name=name, sha256=file_digest(path), bytes=path.stat().st_size)
+        for item in records:
+            manifest.add_shard(
+                TensorRecord(key=item["key"], name=item["name"], global_shape=tuple(item["global_shape"]),
+                             dtype=item["dtype"], category=item["category"], partition_dim=item["partition_dim"],
+                             tensor_parallel_size=item["tensor_parallel_size"],
+                             tensor_parallel_rank=item["tensor_parallel_rank"], state_name=item["state_name"]),
+                ShardRecord(rank=item["rank"], file=item["file"], offset=item["offset"], length=item["length"],
+                            key=item["storage_key"], padding=item.get("padding", 0)),
+            )
+        for key, value in scalars.items():
+            if key in optimizer_scalars and optimizer_scalars[key] != value:
+                raise CheckpointError(
+                    format_error("checkpoint.save", f"optimizer state {key!r} differs between ranks",
+                                 rank=rank, expected=optimizer_scalars[key], observed=value)
+                )
+            optimizer_scalars[key] = value
+    manifest.complete = True
+    manifest.validate()
+    metadata = {
+        "format_version": CURRENT_FORMAT_VERSION,
+        "created_by": created_by,
+        "training_state": {"step": step},
+        "scheduler": {},
+        "scaler": {},
+        "config": None,
+        "topology": dict(topology or {}),
+        "world_size": len(shards),
+        "rng": {"saved": False, "ranks": [], "meta": {}},
+        "optimizer_scalars": optimizer_scalars,
+        "extra": extra_metadata or {},
+    }
+    (staging / METADATA_FILENAME).write_text(json.dumps(metadata, indent=2, sort_keys=True), encoding="utf-8")
+    manifest.write(staging / MANIFEST_FILENAME)
+    staging.replace(final)
+    return final
+
+
+def _version() -> str:
+    from . import __version__
+
+    return __version__
+
+
+def load_flat_shard_checkpoint(
+    directory: Path,
+    handle: Any,
+    *,
+    optimizer: Any = None,
+    verify_checksums: bool = True,
+    strict: bool = True,
+) -> int:
+    """Fill ``handle.flat_param`` (and ``optimizer``'s state for it) from a checkpoint.
+
+    The saved layout may be any width: every piece of this rank's shard is read from
+    the intervals that intersect it (``checkpoint/reader.py:314-470``), one
+    interval-copy launch per destination tensor.  Returns the number of model
+    pieces loaded.
+    """
+    directory = Path(directory)
+    manifest = CheckpointManifest.read(directory / MANIFEST_FILENAME)
+    manifest.validate()
+    metadata_path = directory / METADATA_FILENAME
+    metadata = json.loads(metadata_path.read_text(encoding="utf-8")) if metadata_path.is_file() else {}
+    flat = handle.flat_param
+    cache = ShardFileCache(directory, manifest, verify_checksums=verify_checksums, device=flat.device)
+    layout = handle.local_piece_layout()
+    loaded = load_flat_shard(flat.data, layout, manifest.tensors_by_category("model"), cache, strict=strict)
+    increment_version(flat)
+    if optimizer is None:
+        return loaded
+    records = manifest.tensors_by_category("optimizer")
+    state_names = sorted({r.state_name for r in records.values()} - {""})
+    scalars = dict(metadata.get("optimizer_scalars", {}))
+    if not state_names and not scalars:
+        return loaded
+    index = next(i for i, p in enumerate(optimizer.parameters) if p is flat)
+    entry: dict[str, Any] = {}
+    for state_name in state_names:
+        buffer = torch.zeros(flat.numel(), dtype=flat.dtype, device=flat.device)
+        found = load_flat_shard(buffer, layout, records, cache,
+                                key_of=lambda item, s=state_name: f"{item.name}::{s}", strict=False)
+        if found:
+            entry[state_name] = buffer.view(flat.shape)
+        elif strict:
+            raise IncompleteCheckpointError(
+                format_error(
+                    "checkpoint.load_optimizer",
+                    f"optimizer state {state_name!r} is missing for parameter {index}",
+                    expected=f"state entries for parameter {index}",
+                    observed="none",
+                    resolution="the checkpoint was written with save_optimizer=False",
+                )
+            )
+    for name, value in scalars.items():
+        entry[name] = torch.tensor(value) if isinstance(value, (int, float)) else value
+    state = {} if not entry else {index: entry}
+    inner_groups = optimizer.inner.state_dict()["param_groups"]
+    optimizer.load_state_dict({
+        "param_groups": [{k: v for k, v in g.items() if k != "params"} for g in inner_groups],
+        "state": state,
+        "num_parameters": len(optimizer.parameters),
+    })
+    return loaded

@@ -15,6 +15,7 @@ __all__ = [
     "CheckpointCorruptionError",
     "CheckpointError",
     "CheckpointTopologyError",
+    "CheckpointVersionError",
     "CollectiveError",
     "ConfigurationError",
     "HybridTrainingError",
@@ -88,6 +89,10 @@ class IncompleteCheckpointError(CheckpointError):
 
 class CheckpointCorruptionError(CheckpointError):
     """Stored data disagrees with its manifest record."""
+
+
+class CheckpointVersionError(CheckpointError):
+    """The checkpoint format version is not readable by this build."""
 
 
 class CheckpointTopologyError(CheckpointError):

@@ -1,24 +1,122 @@
-"""Checkpoint shard records: which file holds which interval of which tensor.
+"""The checkpoint format: manifest, shard records, file integrity, naming rules.
 
-``ShardRecord`` and ``TensorRecord`` keep the fields, validation and JSON form of
-``checkpoint/manifest.py:63-281`` of the reference, and ``validate_shard_filename``
-enforces the same ``rank-NNNNN.pt`` naming rule (``checkpoint/format.py:80``,
-``:176-205``), so records written by the reference load here.  The manifest file
-itself (JSON I/O, file integrity records) is not part of this path.
+``ShardRecord``, ``TensorRecord``, ``FileRecord`` and ``CheckpointManifest`` keep the
+fields, validation, errors and JSON form of ``checkpoint/manifest.py`` of the
+reference, and the naming and path rules are those of ``checkpoint/format.py``
+(``rank-NNNNN.pt`` payloads, ``manifest.json`` written last, staging directories,
+format version "1.0"), so a checkpoint written by either side reads on the other.
 """
 
 from __future__ import annotations
 
+import hashlib
+import json
 import re
 from dataclasses import dataclass, field
+from pathlib import Path
 from typing import Any
 
-from .errors import CheckpointCorruptionError, CheckpointError, IncompleteCheckpointError, format_error
+from .errors import (
+    CheckpointCorruptionError,
+    CheckpointError,
+    CheckpointVersionError,
+    IncompleteCheckpointError,
+    format_error,
+)
 from .tensors import ShardRange, intersect_ranges
 
-__all__ = ["ShardRecord", "TensorRecord", "shard_filename", "validate_shard_filename"]
+__all__ = [
+    "CURRENT_FORMAT_VERSION",
+    "CheckpointManifest",
+    "FileRecord",
+    "MANIFEST_FILENAME",
+    "METADATA_FILENAME",
+    "ShardRecord",
+    "TensorRecord",
+    "checkpoint_directory_name",
+    "file_digest",
+    "resolve_inside",
+    "shard_filename",
+    "staging_directory_name",
+    "step_from_directory_name",
+    "validate_format_version",
+    "validate_shard_filename",
+]
 
 _SHARD_FILENAME = re.compile(r"^rank-(\d{5,})\.pt$")
+CHECKPOINT_DIRECTORY_PATTERN = re.compile(r"^checkpoint-step-(\d{6,})$")
+CURRENT_FORMAT_VERSION = "1.0"
+SUPPORTED_FORMAT_VERSIONS = frozenset({"1.0"})
+MANIFEST_FILENAME = "manifest.json"
+METADATA_FILENAME = "metadata.json"
+_STAGING_PREFIX = ".staging-"
+
+
+def checkpoint_directory_name(step: int) -> str:
+    """``checkpoint-step-NNNNNN`` (``checkpoint/format.py:85-108``)."""
+    if step < 0:
+        raise CheckpointError(
+            format_error("checkpoint.directory_name", "step must be non-negative", expected=">= 0",
+                         observed=step, resolution="pass the current optimizer step")
+        )
+    return f"checkpoint-step-{step:06d}"
+
+
+def step_from_directory_name(name: str) -> int | None:
+    """The step of a checkpoint directory name, or ``None``."""
+    match = CHECKPOINT_DIRECTORY_PATTERN.match(name)
+    return int(match.group(1)) if match else None
+
+
+def staging_directory_name(final_name: str, token: str) -> str:
+    """The hidden directory a checkpoint is written into before its atomic rename."""
+    return f"{_STAGING_PREFIX}{final_name}-{token}"
+
+
+def validate_format_version(version: str) -> str:
+    """Refuse a format version this build cannot read."""
+    if version not in SUPPORTED_FORMAT_VERSIONS:
+        raise CheckpointVersionError(
+            format_error(
+                "checkpoint.validate_format_version",
+                "the checkpoint was written in a format version this build cannot read",
+                expected=sorted(SUPPORTED_FORMAT_VERSIONS),
+                observed=version,
+                resolution="read it with the version of the package that wrote it",
+            )
+        )
+    return version
+
+
+def resolve_inside(root: Path, name: str) -> Path:
+    """``root / name``, proven to stay inside ``root`` after resolving symlinks."""
+    root_resolved = Path(root).resolve()
+    candidate = (root_resolved / name).resolve()
+    try:
+        candidate.relative_to(root_resolved)
+    except ValueError as exc:
+        raise CheckpointError(
+            format_error(
+                "checkpoint.resolve_inside",
+                "the resolved path escapes the checkpoint directory",
+                expected=f"a path under {root_resolved}",
+                observed=str(candidate),
+                resolution="remove the symlink or path component that redirects outside",
+            )
+        ) from exc
+    return candidate
+
+
+def file_digest(path: Path, *, chunk_size: int = 1 << 22) -> str:
+    """SHA-256 hex digest of a file, streamed in chunks."""
+    digest = hashlib.sha256()
+    with open(path, "rb") as handle:
+        while True:
+            block = handle.read(chunk_size)
+            if not block:
+                break
+            digest.update(block)
+    return digest.hexdigest()
 
 
 def shard_filename(rank: int) -> str:
@@ -205,3 +303,177 @@ class TensorRecord:
             state_name=str(payload.get("state_name", "")),
             shards=[ShardRecord.from_dict(s) for s in payload.get("shards", [])],
         )
+
+
+@dataclass(frozen=True)
+class FileRecord:
+    """Integrity metadata of one payload file (``checkpoint/manifest.py:286-311``)."""
+
+    name: str
+    sha256: str
+    bytes: int
+
+    def as_dict(self) -> dict[str, Any]:
+        """JSON form."""
+        return {"name": self.name, "sha256": self.sha256, "bytes": self.bytes}
+
+    @classmethod
+    def from_dict(cls, payload: dict[str, Any]) -> FileRecord:
+        """Rebuild from :meth:`as_dict` output."""
+        return cls(name=validate_shard_filename(str(payload["name"])), sha256=str(payload["sha256"]),
+                   bytes=int(payload["bytes"]))
+
+
+@dataclass
+class CheckpointManifest:
+    """The rank-independent description of a checkpoint (``checkpoint/manifest.py:314-561``)."""
+
+    format_version: str = CURRENT_FORMAT_VERSION
+    writer_world_size: int = 1
+    topology: dict[str, Any] = field(default_factory=dict)
+    step: int = 0
+    tensors: dict[str, TensorRecord] = field(default_factory=dict)
+    files: dict[str, FileRecord] = field(default_factory=dict)
+    complete: bool = False
+    created_by: str = ""
+
+    def add_shard(self, record: TensorRecord, shard: ShardRecord) -> None:
+        """Register one shard, creating or extending the tensor's record."""
+        existing = self.tensors.get(record.key)
+        if existing is None:
+            self.tensors[record.key] = TensorRecord(
+                key=record.key, name=record.name, global_shape=record.global_shape, dtype=record.dtype,
+                category=record.category, partition_dim=record.partition_dim,
+                tensor_parallel_size=record.tensor_parallel_size,
+                tensor_parallel_rank=record.tensor_parallel_rank, state_name=record.state_name,
+                shards=[shard],
+            )
+            return
+        if existing.global_shape != record.global_shape or existing.dtype != record.dtype:
+            raise CheckpointCorruptionError(
+                format_error(
+                    "manifest.add_shard",
+                    f"two ranks describe tensor {record.key!r} differently, so the "
+                    "manifest cannot describe a single global tensor",
+                    expected=f"shape={existing.global_shape}, dtype={existing.dtype}",
+                    observed=f"shape={record.global_shape}, dtype={record.dtype}",
+                    resolution=(
+                        "the ranks are running different model definitions; check that "
+                        "every rank built the model from the same configuration"
+                    ),
+                )
+            )
+        existing.shards.append(shard)
+
+    def validate(self) -> None:
+        """Complete, version-readable, every tensor tiled, every file recorded."""
+        validate_format_version(self.format_version)
+        if not self.complete:
+            raise IncompleteCheckpointError(
+                format_error(
+                    "manifest.validate",
+                    "the manifest is not marked complete, which means the writer did not "
+                    "finish; a checkpoint is only published after every shard validates",
+                    expected=True,
+                    observed=self.complete,
+                    resolution="discard this checkpoint and resume from an earlier one",
+                )
+            )
+        for record in self.tensors.values():
+            record.validate()
+            for shard in record.shards:
+                if shard.file not in self.files:
+                    raise IncompleteCheckpointError(
+                        format_error(
+                            "manifest.validate",
+                            f"tensor {record.key!r} references file {shard.file!r}, which "
+                            "has no integrity record",
+                            expected=sorted(self.files),
+                            observed=shard.file,
+                            resolution="the manifest is truncated or hand-edited",
+                        )
+                    )
+
+    def referenced_files(self) -> set[str]:
+        """File names any tensor depends on."""
+        return {shard.file for record in self.tensors.values() for shard in record.shards}
+
+    def tensors_by_category(self, category: str) -> dict[str, TensorRecord]:
+        """The records of one category (``"model"``, ``"optimizer"``, ``"buffer"``)."""
+        return {k: v for k, v in self.tensors.items() if v.category == category}
+
+    def as_dict(self) -> dict[str, Any]:
+        """JSON form with a deterministic key order."""
+        return {
+            "format_version": self.format_version,
+            "created_by": self.created_by,
+            "writer_world_size": self.writer_world_size,
+            "topology": self.topology,
+            "step": self.step,
+            "complete": self.complete,
+            "tensors": {k: self.tensors[k].as_dict() for k in sorted(self.tensors)},
+            "files": {k: self.files[k].as_dict() for k in sorted(self.files)},
+        }
+
+    def to_json(self, *, indent: int | None = 2) -> str:
+        """The manifest as JSON text."""
+        return json.dumps(self.as_dict(), indent=indent, sort_keys=True)
+
+    def write(self, path: Path) -> Path:
+        """Write the manifest to ``path``."""
+        Path(path).write_text(self.to_json(), encoding="utf-8")
+        return Path(path)
+
+    @classmethod
+    def from_dict(cls, payload: dict[str, Any]) -> CheckpointManifest:
+        """Rebuild from :meth:`as_dict` output; a malformed payload raises ``CheckpointError``."""
+        try:
+            return cls(
+                format_version=str(payload["format_version"]),
+                created_by=str(payload.get("created_by", "")),
+                writer_world_size=int(payload.get("writer_world_size", 1)),
+                topology=dict(payload.get("topology", {})),
+                step=int(payload.get("step", 0)),
+                complete=bool(payload.get("complete", False)),
+                tensors={k: TensorRecord.from_dict(v) for k, v in payload.get("tensors", {}).items()},
+                files={k: FileRecord.from_dict(v) for k, v in payload.get("files", {}).items()},
+            )
+        except (KeyError, TypeError, ValueError) as exc:
+            raise CheckpointError(
+                format_error(
+                    "manifest.from_dict",
+                    "the manifest is malformed",
+                    expected="a manifest written by this package",
+                    observed=repr(exc),
+                    resolution="the file is not a valid checkpoint manifest",
+                )
+            ) from exc
+
+    @classmethod
+    def read(cls, path: Path) -> CheckpointManifest:
+        """Load (not yet validate) a manifest; a missing file means an unfinished write."""
+        path = Path(path)
+        if not path.is_file():
+            raise IncompleteCheckpointError(
+                format_error(
+                    "manifest.read",
+                    "no manifest found; the manifest is written last, so its absence "
+                    "means the checkpoint was never completed",
+                    expected=str(path),
+                    observed="missing",
+                    resolution="resume from an earlier checkpoint",
+                )
+            )
+        try:
+            payload = json.loads(path.read_text(encoding="utf-8"))
+        except json.JSONDecodeError as exc:
+            raise CheckpointError(
+                format_error("manifest.read", "the manifest is not valid JSON", expected="a JSON object",
+                             observed=str(exc), resolution="the file is corrupt")
+            ) from exc
+        if not isinstance(payload, dict):
+            raise CheckpointError(
+                format_error("manifest.read", "the manifest is not a JSON object", expected="object",
+                             observed=type(payload).__name__, resolution="the file is corrupt")
+            )
+        return cls.from_dict(payload)

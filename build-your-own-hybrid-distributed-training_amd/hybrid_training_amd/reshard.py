@@ -10,9 +10,9 @@ as ONE launch of the interval copy kernel straight from the stored shards into t
 destination shard.  The reference copies twice per piece (into a temporary, then
 into the destination) and runs a Python loop per piece.
 
-Payloads are expected to be resident on the device already
-(:class:`DeviceShardCache`); reading ``.pt`` files and verifying their digests is
-host I/O outside this path.
+Payloads are resident on the device: :class:`DeviceShardCache` holds tensors
+already there, and ``checkpoint.ShardFileCache`` verifies, loads and uploads
+``.pt`` files.
 """
 
 from __future__ import annotations
