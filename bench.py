@@ -513,7 +513,8 @@ def bench_fsdp(steps: int, warmup: int) -> int:
     shard = handles[0].shard_numel
     _emit("FSDP pack/pad/shard (FlatParamHandle build): params/s", "params/s", total / (ms * 1e-3), ms,
           max(steps, 3), max(warmup, 1), "bf16->f32", f"Llama-3-8B bf16 params -> {world} fp32 master shards",
-          6 * total, {"params": total, "world": world, "shard_numel": shard, "bytes_per_param": 6})
+          6 * total, {"params": total, "world": world, "shard_numel": shard, "bytes_per_param": 6},
+          _secondary_traffic("fsdp", ["pack: one rank's fp32 master shard"], [world]))
     shards = [h.flat_param for h in handles]
     outputs = {}
 
@@ -524,7 +525,8 @@ def bench_fsdp(steps: int, warmup: int) -> int:
     ms = _time_events(unpack, max(steps, 3), max(warmup, 1))
     _emit("FSDP unpack (full_tensors from all shards): params/s", "params/s", total / (ms * 1e-3), ms,
           max(steps, 3), max(warmup, 1), "f32", f"Llama-3-8B, {world} fp32 shards -> 291 fp32 tensors",
-          8 * total, {"params": total, "world": world, "bytes_per_param": 8})
+          8 * total, {"params": total, "world": world, "bytes_per_param": 8},
+          _secondary_traffic("fsdp", ["unpack: all 291 tensors from 8 shards"], [1]))
     outputs.clear()
     del shards
     owner = handles[0]
@@ -541,7 +543,8 @@ def bench_fsdp(steps: int, warmup: int) -> int:
     _emit("FSDP gradient local share (AVG reduce-scatter stand-in): shard elements/s", "elements/s",
           shard / (ms * 1e-3), ms, max(steps, 5), max(warmup, 2), "bf16->f32",
           f"Llama-3-8B rank 0 of W={world}: {world} padded bf16 gradients -> fp32 shard, with norm partials",
-          (2 * world + 4) * shard, {"shard_numel": shard, "world": world, "bytes_per_element": 2 * world + 4})
+          (2 * world + 4) * shard, {"shard_numel": shard, "world": world, "bytes_per_element": 2 * world + 4},
+          _secondary_traffic("fsdp", ["gradient local share with norm partials"], [1]))
 
     from hybrid_training_amd import OptimizerConfig, ShardedOptimizer
 
@@ -557,7 +560,9 @@ def bench_fsdp(steps: int, warmup: int) -> int:
     _emit("FSDP optimizer tail (local share + clip + AdamW): shard elements/s", "elements/s", shard / (ms * 1e-3),
           ms, max(steps, 5), max(warmup, 2), "bf16->f32",
           f"Llama-3-8B rank 0 of W={world}: local share with norm partials, clip from them, fused AdamW",
-          (2 * world + 4 + 28) * shard, {"shard_numel": shard, "world": world, "bytes_per_element": 2 * world + 32})
+          (2 * world + 4 + 28) * shard, {"shard_numel": shard, "world": world, "bytes_per_element": 2 * world + 32},
+          _secondary_traffic("fsdp", ["gradient local share with norm partials", "fused clip + AdamW in the tail"],
+                             [1, 1]))
     del opt, grads, owner, named
     torch.cuda.empty_cache()
     return 0
@@ -666,7 +671,8 @@ def bench_sgd(steps: int, warmup: int) -> int:
     ms = _time_events(step, steps, warmup)
     _emit("sharded SGD(momentum 0.9)+clip step: params/s", "params/s", n / (ms * 1e-3), ms, steps, warmup, "f32",
           "Llama-3-8B FSDP rank shard at W=8: global-norm clip + SGD with momentum", 24 * n,
-          {"shard_numel": n, "bytes_per_param": 24})
+          {"shard_numel": n, "bytes_per_param": 24},
+          _secondary_traffic("sgd", ["SGD with momentum (20 B/param)", "norm pass"], [1, 1]))
     return 0
 
 
