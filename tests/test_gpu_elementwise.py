@@ -1,9 +1,11 @@
-"""GPU parity of the two element-wise entry points at sizes that exercise every tile path.
+"""GPU parity of the element-wise entry points at sizes that exercise every tile path.
 
-* ``hbt_grad_local_share`` (the FSDP gradient local share, ``parallel/fsdp.py:704-781``):
-  bitwise against the oracle for G in {1, 3, 8}, fp32 and bf16 inputs, shards with
-  full vector tiles, a partial tile at the valid/padding boundary, whole tiles of
-  padding, and misaligned input and output addresses (scalar path).
+* ``hbt_grad_local_share`` and ``hbt_grad_local_share_sqnorm`` (the FSDP gradient
+  local share, ``parallel/fsdp.py:704-781``, the latter with the norm partials of its
+  output): bitwise against the oracle for G in {1, 3, 8}, fp32 and bf16 inputs,
+  shards with full vector tiles, a partial tile at the valid/padding boundary, whole
+  tiles of padding, and misaligned input and output addresses (scalar path); the
+  partials sum to the oracle's squared norm within 1e-12.
 * ``hbt_scale_inplace`` (the ``grad.mul_`` loops of ``optim/grad_scaler.py:181-186``
   and ``optim/sharded_optimizer.py:333-337``): bitwise against torch's own CPU
   ``mul_`` by a Python float, twice, in the tensor's dtype, over several tensors per
@@ -56,6 +58,21 @@ def test_local_share_tiles(device, in_dtype, group, misaligned):
             _native.check(status, "test.local_share")
             expect = oracle.local_share(host, rank, shard, valid, divisor)
             assert np.array_equal(_bits(out), expect.view(np.int32)), (rank, valid)
+            # the fused entry point: the same shard, plus its squared-norm partials
+            chunk = 32768
+            partials = torch.full((-(-valid // chunk) + -(-(shard - valid) // chunk) or 1,), 7.0,
+                                  dtype=torch.float64, device=device)
+            out.fill_(7.0)
+            status = lib.hbt_grad_local_share_sqnorm(
+                _native.pointer_array([g.data_ptr() for g in grads]), group, rank, shard, valid,
+                _native.dtype_code(in_dtype), divisor, ctypes.c_void_p(out.data_ptr()),
+                ctypes.c_void_p(partials.data_ptr()), ctypes.c_void_p(_native.stream_of(device)),
+            )
+            _native.check(status, "test.local_share_sqnorm")
+            assert np.array_equal(_bits(out), expect.view(np.int32)), (rank, valid)
+            ref = oracle.sqnorm(expect)
+            got = float(partials.sum())
+            assert abs(got - ref) <= 1e-12 * max(ref, 1e-300), (rank, valid, got, ref)
     assert float(out_storage[:lead].sum()) == 7.0 * lead  # nothing written before the output
 
 
