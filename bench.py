@@ -59,7 +59,8 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument(
         "--workload",
-        choices=["adamw", "buckets", "reshard", "scaler", "fsdp", "inplace_clip", "torch_adamw", "sgd", "offload"],
+        choices=["adamw", "buckets", "reshard", "scaler", "fsdp", "inplace_clip", "torch_adamw", "sgd", "offload",
+                 "checkpoint"],
         default="adamw",
         help="adamw (default): the Llama-3-8B W=8 shard step above; buckets: GPT-2-small DDP bucket "
         "pack + AVG divide at W=8; reshard: Llama-3-8B bf16 flat shards W=4 -> W=8 and W=2; scaler: "
@@ -67,7 +68,7 @@ def parse_args() -> argparse.Namespace:
         "Llama-3-8B FSDP pack, unpack and gradient local share at W=8; inplace_clip: the headline step with "
         "the reference's in-place clip; torch_adamw: the headline step with stock torch GPU kernels; sgd: "
         "the headline shard with SGD (momentum 0.9); offload: the headline step with AdamW state in pinned "
-        "host memory",
+        "host memory; checkpoint: Llama-3-8B bf16 saved by 4 FSDP ranks and loaded back at W=8",
     )
     ap.add_argument(
         "--calibrate-copy",
@@ -604,6 +605,103 @@ def bench_inplace_clip(steps: int, warmup: int) -> int:
     return 0
 
 
+def bench_checkpoint(steps: int, warmup: int) -> int:
+    """Llama-3-8B bf16 saved by 4 FSDP ranks to a RAM-backed directory, loaded back at W=8.
+
+    Save: each rank's shard to pinned host memory in one transfer, ``torch.save`` of
+    its pieces, SHA-256, manifest, atomic rename.  Load: manifest validation, SHA-256
+    verification, ``torch.load(weights_only=True)``, upload, and the device reshard
+    into 8 destination shards.  Reported per phase; the device reshard is the part
+    this library's kernels do, the rest is host I/O.
+    """
+    import shutil
+    import tempfile
+
+    import torch
+
+    from hybrid_training_amd import (FlatParamHandle, FSDPConfig, GroupHandle, MixedPrecisionConfig,
+                                     collect_flat_shard_payload, load_flat_shard_checkpoint, write_checkpoint)
+
+    device = torch.device("cuda", 0)
+    shapes = _llama3_shapes(32, 4096, 14336, 1024, 128256)
+    gen = torch.Generator(device=device).manual_seed(6)
+    named = [(name, torch.nn.Parameter(torch.randint(-16000, 16000, shape, dtype=torch.int16, device=device,
+                                                      generator=gen).view(torch.bfloat16)))
+             for name, shape in shapes]
+    total = sum(p.numel() for _, p in named)
+    writers = [FlatParamHandle(named, None, GroupHandle.local_view("shard", 4, r), FSDPConfig(), MixedPrecisionConfig(),
+                               device, keep_originals=True) for r in range(4)]
+    readers = [FlatParamHandle(named, None, GroupHandle.local_view("shard", 8, r), FSDPConfig(), MixedPrecisionConfig(),
+                               device, keep_originals=True) for r in range(8)]
+    need = 2 * 2 * total  # the files, with room to spare
+    root = None
+    if os.path.isdir("/dev/shm") and shutil.disk_usage("/dev/shm").free > need:
+        root = "/dev/shm"
+    workdir = tempfile.mkdtemp(prefix="hbt-ckpt-", dir=root)
+    try:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        shards = [(r, *collect_flat_shard_payload(h, rank=r)) for r, h in enumerate(writers)]
+        t1 = time.perf_counter()
+        path = write_checkpoint(workdir, 1, shards)
+        t2 = time.perf_counter()
+        del shards
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t3 = time.perf_counter()
+        # One cache for the 8 simulated readers: each file is verified and opened once,
+        # as each rank of a real job would open only its own.
+        from hybrid_training_amd import CheckpointManifest, ShardFileCache
+        from hybrid_training_amd.manifest import MANIFEST_FILENAME
+
+        saved = CheckpointManifest.read(path / MANIFEST_FILENAME)
+        shared = ShardFileCache(path, saved, device=device)
+        shared.prefetch(sorted(saved.files))  # the ranks of a real job verify their files concurrently
+        t_verified = time.perf_counter()
+        for r, h in enumerate(readers):
+            if r == 0:
+                start.record()
+            load_flat_shard_checkpoint(path, h, cache=shared)
+        stop.record()
+        torch.cuda.synchronize()
+        t4 = time.perf_counter()
+        # the device part of the load on its own: the interval copies from payloads already uploaded
+        from hybrid_training_amd import load_flat_shard
+
+        manifest = CheckpointManifest.read(path / MANIFEST_FILENAME)
+        cache = ShardFileCache(path, manifest, verify_checksums=False, device=device)
+        for f in sorted(manifest.files):
+            cache.get(f)
+        records = manifest.tensors_by_category("model")
+        layouts = [h.local_piece_layout() for h in readers]
+
+        def reshard():
+            for h, layout in zip(readers, layouts):
+                load_flat_shard(h.flat_param.data, layout, records, cache)
+
+        ms = _time_events(reshard, max(steps, 3), max(warmup, 1))
+        size = sum((path / f).stat().st_size for f in manifest.files)
+    finally:
+        shutil.rmtree(workdir, ignore_errors=True)
+    line = {
+        "metric": "checkpoint save (W=4) + load with reshard (W=8): seconds", "value": (t2 - t0) + (t4 - t3),
+        "unit": "s", "n_gpus": 1, "steps": 1, "warmup": 0, "ms_per_step": ((t2 - t0) + (t4 - t3)) * 1e3,
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (device-generated)",
+        "config": {"workload": "Llama-3-8B bf16 FSDP checkpoint, W=4 writers -> W=8 readers",
+                   "directory": "RAM-backed (/dev/shm)" if root else "the default temporary directory",
+                   "elements": total, "file_bytes": size,
+                   "phases_s": {"collect_to_pinned_host": t1 - t0, "torch_save_digest_manifest": t2 - t1,
+                                "load_verify_upload_reshard": t4 - t3,
+                                "of_which_verify_and_open": t_verified - t3},
+                   "device_reshard_ms": ms},
+        "roofline": {"bound": "hbm", "achieved": 4 * total / (ms * 1e-3) / 1e9, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": 4 * total / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, "traffic": None,
+                     "traffic_per": "device reshard of all 8 destination shards"},
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def bench_offload(steps: int, warmup: int) -> int:
     """The headline shard with optimizer state offloaded to pinned host memory.
 
@@ -703,7 +801,7 @@ def bench_torch_adamw(steps: int, warmup: int) -> int:
 
 SECONDARY = {"buckets": bench_buckets, "reshard": bench_reshard, "scaler": bench_scaler, "fsdp": bench_fsdp,
              "inplace_clip": bench_inplace_clip, "torch_adamw": bench_torch_adamw, "sgd": bench_sgd,
-             "offload": bench_offload}
+             "offload": bench_offload, "checkpoint": bench_checkpoint}
 
 
 if __name__ == "__main__":

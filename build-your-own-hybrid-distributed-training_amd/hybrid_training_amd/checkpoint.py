@@ -22,9 +22,11 @@ work to the device:
 
 from __future__ import annotations
 
+import hashlib
 import json
 import uuid
 from collections.abc import Mapping, Sequence
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 from typing import Any
 
@@ -48,6 +50,7 @@ from .manifest import (
     validate_shard_filename,
 )
 from .reshard import load_flat_shard
+from .tensors import ShardRange
 
 __all__ = [
     "ShardFileCache",
@@ -79,10 +82,26 @@ class ShardFileCache:
         self._loaded: dict[str, dict[str, torch.Tensor]] = {}
 
     def get(self, filename: str) -> Mapping[str, torch.Tensor]:
-        """The tensors stored in ``filename``, on the device."""
+        """The tensors stored in ``filename``; each moves to the device on first access."""
         cached = self._loaded.get(filename)
         if cached is not None:
             return cached
+        payload = self._verified_payload(filename, verify=self._verify)
+        lazy = _DevicePayload(payload, self._device)
+        self._loaded[filename] = lazy
+        return lazy
+
+    def prefetch(self, filenames: Sequence[str], *, max_workers: int = 8) -> None:
+        """Verify and open several files in parallel (hashing releases the GIL)."""
+        todo = [f for f in dict.fromkeys(filenames) if f not in self._loaded]
+        if not todo:
+            return
+        with ThreadPoolExecutor(max_workers=max(1, min(max_workers, len(todo)))) as pool:
+            payloads = list(pool.map(lambda f: self._verified_payload(f, verify=self._verify), todo))
+        for name, payload in zip(todo, payloads):
+            self._loaded[name] = _DevicePayload(payload, self._device)
+
+    def _verified_payload(self, filename: str, *, verify: bool) -> dict[str, Any]:
         validate_shard_filename(filename)
         path = resolve_inside(self._directory, filename)
         if not path.is_file():
@@ -121,7 +140,7 @@ class ShardFileCache:
                     resolution="restore the file from a backup or discard the checkpoint",
                 )
             )
-        if self._verify:
+        if verify:
             digest = file_digest(path)
             if digest != record.sha256:
                 raise CheckpointCorruptionError(
@@ -140,7 +159,8 @@ class ShardFileCache:
                 )
         try:
             # weights_only=True admits tensors and primitives only: a hostile payload
-            # cannot execute code.
+            # cannot execute code.  mmap leaves the bytes in the page cache until a
+            # piece is needed.
             payload = torch.load(path, map_location="cpu", weights_only=True, mmap=True)
         except Exception as exc:
             raise CheckpointCorruptionError(
@@ -166,9 +186,7 @@ class ShardFileCache:
                     resolution="the file was not written by this package",
                 )
             )
-        uploaded = _upload(payload, self._device)
-        self._loaded[filename] = uploaded
-        return uploaded
+        return payload
 
     def clear(self) -> None:
         """Drop every cached payload."""
@@ -180,26 +198,30 @@ class ShardFileCache:
         return tuple(sorted(self._loaded))
 
 
-def _upload(payload: Mapping[str, Any], device: torch.device) -> dict[str, torch.Tensor]:
-    """Every tensor of a payload on ``device``; tensors sharing a storage share one upload."""
-    storages: dict[int, torch.Tensor] = {}
-    out: dict[str, torch.Tensor] = {}
-    for key, value in payload.items():
-        if not torch.is_tensor(value):
-            continue
-        if not value.is_contiguous():
-            out[key] = value.contiguous().to(device)
-            continue
-        storage = value.untyped_storage()
-        base = storages.get(storage.data_ptr())
-        if base is None:
-            host_bytes = torch.empty(0, dtype=torch.uint8).set_(storage)
-            base = host_bytes.to(device)
-            storages[storage.data_ptr()] = base
-        size = value.element_size()
-        begin = value.storage_offset() * size
-        out[key] = base[begin : begin + value.numel() * size].view(value.dtype).view(value.shape)
-    return out
+class _DevicePayload(Mapping[str, torch.Tensor]):
+    """A loaded payload whose tensors are uploaded to the device when first read.
+
+    A reader touches only the pieces that intersect its own shard, so only those
+    cross the host link.
+    """
+
+    def __init__(self, payload: Mapping[str, Any], device: torch.device) -> None:
+        self._host = {k: v for k, v in payload.items() if torch.is_tensor(v)}
+        self._device = device
+        self._uploaded: dict[str, torch.Tensor] = {}
+
+    def __getitem__(self, key: str) -> torch.Tensor:
+        tensor = self._uploaded.get(key)
+        if tensor is None:
+            tensor = self._host[key].to(self._device)
+            self._uploaded[key] = tensor
+        return tensor
+
+    def __iter__(self):
+        return iter(self._host)
+
+    def __len__(self) -> int:
+        return len(self._host)
 
 
 def _pinned_copy(tensor: torch.Tensor) -> torch.Tensor:
@@ -285,6 +307,37 @@ def _state_key(optimizer: Any, param: torch.Tensor) -> torch.Tensor:
     return param
 
 
+class _HashingWriter:
+    """A binary file that hashes what is written to it, so saving needs no re-read."""
+
+    def __init__(self, path: Path) -> None:
+        self._file = open(path, "wb")
+        self._digest = hashlib.sha256()
+        self.bytes = 0
+
+    def write(self, data) -> int:
+        view = memoryview(data)
+        self._digest.update(view)
+        self.bytes += view.nbytes
+        return self._file.write(view)
+
+    def flush(self) -> None:
+        self._file.flush()
+
+    def close(self) -> str:
+        self._file.close()
+        return self._digest.hexdigest()
+
+
+def _save_payload(path: Path, payload: Mapping[str, torch.Tensor]) -> FileRecord:
+    writer = _HashingWriter(path)
+    try:
+        torch.save(dict(payload), writer)
+    finally:
+        digest = writer.close()
+    return FileRecord(name=path.name, sha256=digest, bytes=path.stat().st_size)
+
+
 def write_checkpoint(
     directory: Path,
     step: int,
@@ -314,11 +367,11 @@ def write_checkpoint(
     manifest = CheckpointManifest(writer_world_size=len(shards), topology=dict(topology or {}), step=step,
                                   created_by=created_by)
     optimizer_scalars: dict[str, Any] = {}
-    for rank, payload, records, scalars in shards:
-        name = shard_filename(rank)
-        path = staging / name
-        torch.save(dict(payload), path)
-        manifest.files[name] = FileRecord(name=name, sha256=file_digest(path), bytes=path.stat().st_size)
+    # One writer per rank, as in a multi-rank job; hashing and file writes release the GIL.
+    with ThreadPoolExecutor(max_workers=max(1, min(8, len(shards)))) as pool:
+        files = list(pool.map(lambda shard: _save_payload(staging / shard_filename(shard[0]), shard[1]), shards))
+    for (rank, payload, records, scalars), record in zip(shards, files):
+        manifest.files[record.name] = record
         for item in records:
             manifest.add_shard(
                 TensorRecord(key=item["key"], name=item["name"], global_shape=tuple(item["global_shape"]),
@@ -369,12 +422,15 @@ def load_flat_shard_checkpoint(
     optimizer: Any = None,
     verify_checksums: bool = True,
     strict: bool = True,
+    cache: ShardFileCache | None = None,
 ) -> int:
     """Fill ``handle.flat_param`` (and ``optimizer``'s state for it) from a checkpoint.
 
     The saved layout may be any width: every piece of this rank's shard is read from
     the intervals that intersect it (``checkpoint/reader.py:314-470``), one
-    interval-copy launch per destination tensor.  Returns the number of model
+    interval-copy launch per destination tensor.  The files this shard intersects
+    are verified in parallel first; only the pieces it needs are uploaded.  Pass one
+    ``cache`` to several calls to open each file once.  Returns the number of model
     pieces loaded.
     """
     directory = Path(directory)
@@ -383,8 +439,19 @@ def load_flat_shard_checkpoint(
     metadata_path = directory / METADATA_FILENAME
     metadata = json.loads(metadata_path.read_text(encoding="utf-8")) if metadata_path.is_file() else {}
     flat = handle.flat_param
-    cache = ShardFileCache(directory, manifest, verify_checksums=verify_checksums, device=flat.device)
+    if cache is None:
+        cache = ShardFileCache(directory, manifest, verify_checksums=verify_checksums, device=flat.device)
     layout = handle.local_piece_layout()
+    keys = [[item.name] for item in layout]
+    if optimizer is not None:
+        states = sorted({r.state_name for r in manifest.tensors_by_category("optimizer").values()} - {""})
+        for names, item in zip(keys, layout):
+            names.extend(f"{item.name}::{state}" for state in states)
+    needed = [shard.file
+              for item, names in zip(layout, keys)
+              for record in (manifest.tensors.get(name) for name in names) if record is not None
+              for shard, _ in record.shards_overlapping(ShardRange(item.parameter_offset, item.length))]
+    cache.prefetch(needed)
     loaded = load_flat_shard(flat.data, layout, manifest.tensors_by_category("model"), cache, strict=strict)
     increment_version(flat)
     if optimizer is None:
