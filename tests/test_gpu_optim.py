@@ -317,3 +317,38 @@ def test_full_size_llama_shard(device):
         opt.zero_grad()
     del opt, param
     torch.cuda.empty_cache()
+
+
+def test_learning_rate_schedule_without_weight_decay(device):
+    """``set_learning_rate`` between steps (a scheduler) with weight decay 0 (the
+    reference's ``OptimizerConfig`` default): bitwise the oracle, and torch's CPU
+    AdamW for m and v (p within the square-root tolerance)."""
+    n = 50_001
+    gen = torch.Generator(device=device).manual_seed(31)
+    param = torch.nn.Parameter(torch.randn(n, device=device, generator=gen))
+    opt = ShardedOptimizer([param], OptimizerConfig(learning_rate=1e-3, weight_decay=0.0),
+                           norm_group=GroupHandle.trivial(), device=device)
+    ref = torch.nn.Parameter(param.detach().cpu().clone())
+    ref_opt = torch.optim.AdamW([ref], lr=1e-3, weight_decay=0.0, foreach=False)
+    host_p = param.detach().cpu().numpy().copy()
+    host_m = np.zeros(n, np.float32)
+    host_v = np.zeros(n, np.float32)
+    for step, lr in enumerate((1e-3, 7.5e-4, 5e-4, 2.5e-4), start=1):
+        opt.set_learning_rate(lr)
+        for group in ref_opt.param_groups:
+            group["lr"] = lr
+        g = torch.randn(n, device=device, generator=gen) * 1e-2
+        param.grad = g
+        ref.grad = g.cpu()
+        opt.step()
+        ref_opt.step()
+        sc = oracle.adamw_scalars(lr=lr, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.0, step=float(step))
+        oracle.adamw_step(host_p, g.cpu().numpy(), host_m, host_v, sc)
+        got = param.detach().cpu().numpy()
+        assert np.array_equal(got.view(np.int32), host_p.view(np.int32)), step
+        state = opt.inner.state[param]
+        assert torch.equal(state["exp_avg"].cpu(), ref_opt.state[ref]["exp_avg"])
+        assert torch.equal(state["exp_avg_sq"].cpu(), ref_opt.state[ref]["exp_avg_sq"])
+        rel = np.abs(got - ref.detach().numpy()) / np.maximum(np.abs(ref.detach().numpy()), lr)
+        assert float(rel.max()) <= 1e-6
+    assert opt.learning_rate == 2.5e-4
