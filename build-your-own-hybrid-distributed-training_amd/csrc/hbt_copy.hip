@@ -1,7 +1,7 @@
 // Interval gather-copy and the FSDP gradient local share (gfx950).
 //
 // One launch moves any number of [src, src + n) -> [dst, dst + n) intervals.  Each
-// interval is cut into chunks of kCopyChunk elements; one workgroup owns one chunk
+// interval is cut into chunks of 512 elements; one workgroup owns one chunk
 // and finds its interval by binary search over the records' first_chunk column.  Inside
 // a chunk each lane moves units of 16 / max(source, destination element bytes)
 // elements, consecutive lanes taking consecutive units, so every load and store
@@ -18,17 +18,16 @@ namespace {
 // One wavefront per workgroup: a workgroup moves a 512-element chunk and retires.
 // Measured on MI355X (Llama-3-8B bf16 reshard, 32 GB moved), this shape sustains
 // 6.3 TB/s against 5.0 TB/s for 256-thread workgroups walking 64K-element chunks.
+// Halving the chunk of 4-byte data (one unit per lane) measured slower in the
+// product (6.6 -> 5.2 TB/s for bf16 -> fp32 packs): each workgroup's interval
+// search is then paid twice per byte.
 #ifndef HBT_COPY_BLOCK
 #define HBT_COPY_BLOCK 64
-#endif
-#ifndef HBT_COPY_CHUNK
-#define HBT_COPY_CHUNK 512
 #endif
 #ifndef HBT_COPY_NT
 #define HBT_COPY_NT 1
 #endif
 constexpr int kCopyBlock = HBT_COPY_BLOCK;
-constexpr int64_t kCopyChunk = HBT_COPY_CHUNK;  // elements per block
 constexpr bool kCopyNT = HBT_COPY_NT != 0;
 
 // Aligned vector load/store of NW dwords (NW = 2 or 4), non-temporal when kCopyNT:
@@ -132,6 +131,9 @@ __device__ __forceinline__ void store_elem(uint8_t* p, uint32_t bits) {
 // Elements per lane unit: one 16-byte access on the wider side of the copy.
 template <int SB, int DB>
 constexpr int unit_elems() { return 16 / (SB > DB ? SB : DB); }
+// Elements per chunk (per workgroup), the same for every dtype pair.
+template <int SB, int DB>
+constexpr int64_t chunk_elems() { return 512; }
 
 // Unpack the U elements held in `words` (SB bytes each) into element bit patterns.
 template <int SB, int U>
@@ -180,8 +182,9 @@ __global__ __launch_bounds__(kCopyBlock) void copy_kernel(const int64_t* __restr
     const uint8_t* src = reinterpret_cast<const uint8_t*>(rec[0]);
     uint8_t* dst = reinterpret_cast<uint8_t*>(rec[1]);
     const int64_t n = rec[2];
-    const int64_t e0 = (chunk - rec[3]) * kCopyChunk;
-    const int64_t len = (n - e0) < kCopyChunk ? (n - e0) : kCopyChunk;
+    constexpr int64_t kChunk = chunk_elems<SB, DB>();
+    const int64_t e0 = (chunk - rec[3]) * kChunk;
+    const int64_t len = (n - e0) < kChunk ? (n - e0) : kChunk;
 
     uint8_t* d = dst + e0 * DB;
     const uint8_t* s = src != nullptr ? src + e0 * SB : nullptr;
@@ -233,11 +236,13 @@ struct RankTable {
     const uint8_t* g[HBT_MAX_LOCAL_RANKS];
 };
 
-// One wavefront per workgroup and 512 shard elements per workgroup: each lane owns
-// two 4-element groups (fp32 input: one 16-byte load per rank and group; bf16 input:
-// one 8-byte load), adds the G ranks' quotients in rank order and stores 16 bytes.
+// One wavefront per workgroup and 256 shard elements per workgroup: each lane owns one
+// 4-element group (fp32 input: one 16-byte load per rank; bf16 input: one 8-byte
+// load), adds the G ranks' quotients in rank order and stores 16 bytes.  Measured on
+// MI355X (8 bf16 ranks -> fp32): 6.0 TB/s, against 5.7 TB/s with two groups per lane.
 constexpr int kShareBlock = 64;
-constexpr int64_t kShareTile = int64_t(kShareBlock) * 4 * 2;
+constexpr int kShareGroups = 1;
+constexpr int64_t kShareTile = int64_t(kShareBlock) * 4 * kShareGroups;
 
 template <int SB>
 __device__ __forceinline__ f32x4 load_quad(const uint8_t* p) {
@@ -260,7 +265,7 @@ __global__ __launch_bounds__(kShareBlock) void local_share_kernel(RankTable rank
     const int64_t base = int64_t(blockIdx.x) * kShareTile;
     if (vec_ok && base + kShareTile <= valid_numel) {
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
+        for (int u = 0; u < kShareGroups; ++u) {
             const int64_t e = base + (int64_t(u) * kShareBlock + threadIdx.x) * 4;
             f32x4 acc = load_quad<SB>(ranks.g[0] + (offset + e) * SB) / divisor;
             for (int32_t q = 1; q < group_size; ++q) {
@@ -273,7 +278,7 @@ __global__ __launch_bounds__(kShareBlock) void local_share_kernel(RankTable rank
     }
     if (vec_ok && base >= valid_numel && base + kShareTile <= shard_numel) {
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
+        for (int u = 0; u < kShareGroups; ++u) {
             const int64_t e = base + (int64_t(u) * kShareBlock + threadIdx.x) * 4;
             stv<4>(out + e, u32x4v{0u, 0u, 0u, 0u});
         }
@@ -304,7 +309,15 @@ using namespace hbt;
 
 extern "C" {
 
-int64_t hbt_copy_chunk_elems(void) { return kCopyChunk; }
+int64_t hbt_copy_chunk_elems(int32_t src_dtype, int32_t dst_dtype) {
+    const int ssz = dtype_size(src_dtype);
+    const int dsz = dtype_size(dst_dtype);
+    if (ssz == 4 && dsz == 4) return chunk_elems<4, 4>();
+    if (ssz == 2 && dsz == 2) return chunk_elems<2, 2>();
+    if (ssz == 4 && dsz == 2) return chunk_elems<4, 2>();
+    if (ssz == 2 && dsz == 4) return chunk_elems<2, 4>();
+    return -1;  // 8-byte elements travel as F32 dword pairs
+}
 
 int32_t hbt_copy_intervals(const int64_t* table, int64_t count, int64_t total_chunks,
                            int32_t src_dtype, int32_t dst_dtype, int32_t op, float divisor,

@@ -49,7 +49,7 @@ __all__ = [
     "stream_of",
 ]
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 MAX_TENSORS_PER_LAUNCH = 16
 MAX_LOCAL_RANKS = 64
 
@@ -103,7 +103,7 @@ EXPORTED_SYMBOLS: dict[str, tuple[object, tuple[object, ...]]] = {
         _c_i32,
         (_c_void_p, _c_i64, _c_f64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p),
     ),
-    "hbt_copy_chunk_elems": (_c_i64, ()),
+    "hbt_copy_chunk_elems": (_c_i64, (_c_i32, _c_i32)),
     "hbt_copy_intervals": (
         _c_i32,
         (_c_void_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_f32, _c_void_p),
@@ -275,14 +275,22 @@ def double_array(values: Sequence[float]) -> ctypes.Array:
     return (ctypes.c_double * max(1, len(values)))(*values)
 
 
-_CHUNK: int | None = None
+_CHUNKS: dict[tuple[int, int], int] = {}
 
 
-def _copy_chunk(lib: ctypes.CDLL) -> int:
-    global _CHUNK
-    if _CHUNK is None:
-        _CHUNK = int(lib.hbt_copy_chunk_elems())
-    return _CHUNK
+def _copy_chunk(lib: ctypes.CDLL, src_code: int, dst_code: int) -> int:
+    """Elements per copy-kernel chunk for a dtype pair."""
+    key = (src_code, dst_code)
+    chunk = _CHUNKS.get(key)
+    if chunk is None:
+        chunk = int(lib.hbt_copy_chunk_elems(src_code, dst_code))
+        if chunk <= 0:
+            raise UnsupportedFeatureError(
+                format_error("native.CopyPlan", "the copy kernel does not move this dtype pair",
+                             observed=key)
+            )
+        _CHUNKS[key] = chunk
+    return chunk
 
 
 def _device_table(flat: tuple[int, ...], device: torch.device) -> torch.Tensor:
@@ -382,7 +390,7 @@ class CopyPlan:
             src_code = dst_code = DTYPE_F32
             scale = 2
         lib = library()
-        chunk = _copy_chunk(lib)
+        chunk = _copy_chunk(lib, src_code, dst_code)
         flat: list[int] = []
         first = 0
         for src_addr, dst_addr, n in self._rows:

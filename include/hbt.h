@@ -160,8 +160,9 @@ int32_t hbt_grad_norm_finalize(const double* partials, int64_t count, double max
  * `table` is a DEVICE array of `count` records of 4 int64 each:
  *   { src_address (0 => write zeros), dst_address, numel, first_chunk }
  * where first_chunk is the exclusive prefix sum over records of
- * ceil(numel / HBT_COPY_CHUNK) (hbt_copy_chunk_elems()), and total_chunks is the
- * sum.  All records share src_dtype/dst_dtype and op:
+ * ceil(numel / hbt_copy_chunk_elems(src_dtype, dst_dtype)), and total_chunks is the
+ * sum.  A chunk is 512 elements for every pair the kernel moves; the function
+ * returns -1 for a pair it does not move (8-byte data travels as F32 pairs).  All records share src_dtype/dst_dtype and op:
  *   HBT_COPY_OP_COPY    dst = src               (same dtype: byte copy; F32->BF16
  *                                                rounds to nearest even, NaN -> 0x7FC0;
  *                                                BF16->F32 widens exactly)
@@ -172,7 +173,7 @@ int32_t hbt_grad_norm_finalize(const double* partials, int64_t count, double max
  * ---------------------------------------------------------------------------- */
 #define HBT_COPY_OP_COPY 0
 #define HBT_COPY_OP_DIVIDE 1
-int64_t hbt_copy_chunk_elems(void);
+int64_t hbt_copy_chunk_elems(int32_t src_dtype, int32_t dst_dtype);
 int32_t hbt_copy_intervals(const int64_t* table, int64_t count, int64_t total_chunks,
                            int32_t src_dtype, int32_t dst_dtype, int32_t op, float divisor,
                            void* stream);

@@ -38,7 +38,9 @@ def test_library_loads_and_exports_every_declared_symbol():
     assert lib.hbt_norm_partials_count(_native.int64_array([1, 65536, 65537]), 3, 1) == 1 + 1 + 2
     assert lib.hbt_norm_partials_count(None, 99, 0) == -1
     assert lib.hbt_norm_partials_count(_native.int64_array([1]), 1, 7) == -1
-    assert lib.hbt_copy_chunk_elems() > 0
+    assert lib.hbt_copy_chunk_elems(0, 0) == 512 and lib.hbt_copy_chunk_elems(1, 1) == 512
+    assert lib.hbt_copy_chunk_elems(0, 1) == 512 and lib.hbt_copy_chunk_elems(1, 0) == 512
+    assert lib.hbt_copy_chunk_elems(3, 3) == -1
     assert lib.hbt_last_error() == b""
 
 
