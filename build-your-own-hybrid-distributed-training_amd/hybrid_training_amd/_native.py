@@ -49,7 +49,7 @@ __all__ = [
     "stream_of",
 ]
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 MAX_TENSORS_PER_LAUNCH = 16
 MAX_LOCAL_RANKS = 64
 
@@ -114,7 +114,8 @@ EXPORTED_SYMBOLS: dict[str, tuple[object, tuple[object, ...]]] = {
     ),
     "hbt_grad_local_share_sqnorm": (
         _c_i32,
-        (_ptr_array, _c_i32, _c_i32, _c_i64, _c_i64, _c_i32, _c_f32, _c_void_p, _c_void_p, _c_void_p),
+        (_ptr_array, _c_i32, _c_i32, _c_i64, _c_i64, _c_i32, _c_f32, _c_void_p, _c_void_p, _c_void_p,
+         _c_void_p),
     ),
     "hbt_scale_inplace": (
         _c_i32,

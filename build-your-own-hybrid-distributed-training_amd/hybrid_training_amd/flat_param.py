@@ -472,6 +472,7 @@ class FlatParamHandle:
         valid_chunks = -(-valid // chunk)
         pad = self._shard_numel - valid
         partials = torch.empty(max(1, valid_chunks + -(-pad // chunk)), dtype=torch.float64, device=self._device)
+        tile_sums = torch.empty(max(1, -(-self._shard_numel // 256)), dtype=torch.float64, device=self._device)
         lib = _native.library()
         with torch.cuda.device(self._device):
             status = lib.hbt_grad_local_share_sqnorm(
@@ -484,6 +485,7 @@ class FlatParamHandle:
                 divisor,
                 out.data_ptr(),
                 partials.data_ptr(),
+                tile_sums.data_ptr(),
                 _native.stream_of(self._device),
             )
         _native.check(status, "fsdp.hbt_grad_local_share_sqnorm")

@@ -62,10 +62,11 @@ class NormPartials:
     """Unweighted fp32-gradient norm partials a producing kernel wrote for its output.
 
     ``segments`` maps ``(offset, length)`` of the gradient to the partials of that
-    segment: one fp64 per 32768-element chunk from the segment's start, bitwise what
-    ``hbt_grad_sqnorm_partials`` writes for it with weight 1.  The record is valid
-    while the gradient keeps the storage address and version counter it had when
-    the partials were written; any in-place change invalidates it.
+    segment: one fp64 per 32768-element chunk from the segment's start, the layout of
+    ``hbt_grad_sqnorm_partials`` with weight 1, each summed in the producer's own
+    fixed order.  The record is valid while the gradient keeps the storage address
+    and version counter it had when the partials were written; any in-place change
+    invalidates it.
     """
 
     data_ptr: int
@@ -317,7 +318,7 @@ def gradient_norm_pass(
             # Items whose producer already wrote their partials take them from there
             # (times the weight, as the kernel would multiply); the others are summed
             # here, each run of consecutive uncached items in one launch.  Every item
-            # keeps its slot, so the partials, and the norm, are the same either way.
+            # keeps its slot, and the finalize sums the slots in a fixed order.
             slot = first
             pending: list[tuple[torch.Tensor, int, int, float]] = []
             pending_first = slot

@@ -206,16 +206,19 @@ int32_t hbt_grad_local_share(const void* const* rank_grads, int32_t group_size, 
  *   NormContribution.squared_norm pass over the produced shard
  *   (optim/sharded_optimizer.py:145-158) that the next clip_grad_norm runs.
  * Writes `out` exactly as hbt_grad_local_share does, and to `partials` the unweighted
- * squared-norm partials of out's two segments, [0, valid_numel) then
- * [valid_numel, shard_numel): ceil(valid_numel / 32768) + ceil((shard_numel -
+ * squared norms of out's two segments, [0, valid_numel) then [valid_numel,
+ * shard_numel), chunk by chunk: ceil(valid_numel / 32768) + ceil((shard_numel -
  * valid_numel) / 32768) doubles, one per 32768-element chunk from each segment's
- * start.  They are bitwise the partials hbt_grad_sqnorm_partials would write for
- * those two segments (F32, weight 1, unscale 1), so a caller can skip that pass and
- * multiply by the segment weights itself.
+ * start, in the layout hbt_grad_sqnorm_partials uses for those segments (F32, weight
+ * 1, unscale 1), so a caller can stand them in for that pass.  Each is summed in a
+ * fixed order (per 256-element tile, then per chunk), so it is reproducible, though
+ * not bitwise the norm pass's own tree.  `tile_scratch` is caller-provided device
+ * memory for ceil(shard_numel / 256) doubles.
  * ---------------------------------------------------------------------------- */
 int32_t hbt_grad_local_share_sqnorm(const void* const* rank_grads, int32_t group_size, int32_t rank,
                                     int64_t shard_numel, int64_t valid_numel, int32_t in_dtype,
-                                    float divisor, float* out, double* partials, void* stream);
+                                    float divisor, float* out, double* partials, double* tile_scratch,
+                                    void* stream);
 
 /* ------------------------------------------------------------------------------
  * In-place gradient scaling: x = (x * unscale) * (*grad_mul), each product rounded to

@@ -62,11 +62,13 @@ def test_local_share_tiles(device, in_dtype, group, misaligned):
             chunk = 32768
             partials = torch.full((-(-valid // chunk) + -(-(shard - valid) // chunk) or 1,), 7.0,
                                   dtype=torch.float64, device=device)
+            tile_sums = torch.empty(-(-shard // 256), dtype=torch.float64, device=device)
             out.fill_(7.0)
             status = lib.hbt_grad_local_share_sqnorm(
                 _native.pointer_array([g.data_ptr() for g in grads]), group, rank, shard, valid,
                 _native.dtype_code(in_dtype), divisor, ctypes.c_void_p(out.data_ptr()),
-                ctypes.c_void_p(partials.data_ptr()), ctypes.c_void_p(_native.stream_of(device)),
+                ctypes.c_void_p(partials.data_ptr()), ctypes.c_void_p(tile_sums.data_ptr()),
+                ctypes.c_void_p(_native.stream_of(device)),
             )
             _native.check(status, "test.local_share_sqnorm")
             assert np.array_equal(_bits(out), expect.view(np.int32)), (rank, valid)
