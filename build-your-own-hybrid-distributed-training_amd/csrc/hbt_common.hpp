@@ -3,6 +3,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <cstdint>
 #include <cstdio>
 #include <string>
@@ -25,6 +26,16 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 
 // Number of compute units of the current device (cached per device id).
 int device_cu_count();
+
+// 1 / divisor when divisor is a power of two whose reciprocal is a normal float, else 0.
+// For such a divisor x * (1 / divisor) and x / divisor are the same correctly rounded
+// value (both round the same real number), so a division becomes a multiply.
+inline float exact_reciprocal(float divisor) {
+    int exponent = 0;
+    const float mantissa = std::frexp(divisor, &exponent);
+    const bool exact = divisor > 0.0f && mantissa == 0.5f && exponent > -125 && exponent < 126;
+    return exact ? std::ldexp(1.0f, 1 - exponent) : 0.0f;
+}
 
 // ---- dtype helpers -------------------------------------------------------------------
 inline int dtype_size(int32_t dtype) {

@@ -1,26 +1,31 @@
 // Interval gather-copy and the FSDP gradient local share (gfx950).
 //
 // One launch moves any number of [src, src + n) -> [dst, dst + n) intervals.  Each
-// interval is cut into chunks of 512 elements; one workgroup owns one chunk
-// and finds its interval by binary search over the records' first_chunk column.  Inside
-// a chunk each lane moves units of 16 / max(source, destination element bytes)
-// elements, consecutive lanes taking consecutive units, so every load and store
-// instruction of a wave covers one contiguous span.  The destination is written with
-// aligned stores; the source is read with aligned loads of the unit's width and
-// shifted into place with v_alignbyte, so intervals at any element offset stream at
-// full width.  A load never touches an aligned block that holds no byte of the source
-// interval.
+// interval is cut into chunks of 64 x 16 bytes of source (256 elements of a 4-byte
+// source, 512 of a 2-byte one); one workgroup owns one chunk and finds its interval by
+// a binary search over the records' first_chunk column.  Inside a chunk each lane moves
+// units of 16 / max(source, destination element bytes) elements, consecutive lanes
+// taking consecutive units, so every load and store instruction of a wave covers one
+// contiguous span.
+//
+// Two kernels share that layout.  copy_aligned_kernel serves plans whose records all
+// start on aligned addresses (the host certifies this): one aligned load and one aligned
+// store per unit.  copy_kernel serves any plan: the destination is written with aligned
+// stores after an element-wise head, and the source is read with aligned loads of the
+// unit's width and shifted into place with v_alignbyte, so intervals at any element
+// offset stream at full width.  A load never touches an aligned block that holds no byte
+// of the source interval.
 #include "hbt_common.hpp"
 
 namespace hbt {
 namespace {
 
-// One wavefront per workgroup: a workgroup moves a 512-element chunk and retires.
-// Measured on MI355X (Llama-3-8B bf16 reshard, 32 GB moved), this shape sustains
-// 6.3 TB/s against 5.0 TB/s for 256-thread workgroups walking 64K-element chunks.
-// Halving the chunk of 4-byte data (one unit per lane) measured slower in the
-// product (6.6 -> 5.2 TB/s for bf16 -> fp32 packs): each workgroup's interval
-// search is then paid twice per byte.
+// One wavefront per workgroup reading 16 bytes of source per lane: a workgroup reads
+// 1 KB and retires.  Measured on MI355X with the aligned kernel:
+//   * fp32 -> fp32, Llama-3-8B unpack (298 records, 64 GB moved): 6.6 TB/s, against
+//     6.0 TB/s reading 2 KB per workgroup;
+//   * bf16 -> fp32 pack of the same model: 6.5 TB/s, against 5.0 TB/s reading 512 B.
+// 256-thread workgroups walking 64K-element chunks ran at 5.0 TB/s.
 #ifndef HBT_COPY_BLOCK
 #define HBT_COPY_BLOCK 64
 #endif
@@ -55,26 +60,58 @@ __device__ __forceinline__ void stv(void* p, typename Vec<NW>::type x) {
     }
 }
 
-// Loads NW dwords (NW = 2 or 4: one 8- or 16-byte block) starting at byte address
-// `s`, where `k` = s mod 4*NW (uniform across the wave).  For k != 0 one extra aligned
-// block is read; it holds source bytes s + 4*NW - 1 and earlier ones only up to the
-// block boundary, so it lies inside the source's page.
+// The copy kernel reads its addresses from a table in device memory, so the compiler
+// cannot tell which address space they point into and would issue flat loads and
+// stores.  These views name global memory (address space 1): global_load/global_store
+// instructions, which wait on the vector counter alone.
+typedef __attribute__((address_space(1))) uint8_t gbyte;
+
 template <int NW>
-__device__ __forceinline__ void load_shifted(const uint8_t* s, uint32_t k, uint32_t (&out)[NW]) {
+__device__ __forceinline__ typename Vec<NW>::type ldg(const gbyte* p) {
+    typedef typename Vec<NW>::type V;
+    typedef __attribute__((address_space(1))) const V GV;
+    if constexpr (kCopyNT) return __builtin_nontemporal_load(reinterpret_cast<GV*>(p));
+    return *reinterpret_cast<GV*>(p);
+}
+template <int NW>
+__device__ __forceinline__ void stg(gbyte* p, typename Vec<NW>::type x) {
+    typedef typename Vec<NW>::type V;
+    typedef __attribute__((address_space(1))) V GV;
+    if constexpr (kCopyNT) {
+        __builtin_nontemporal_store(x, reinterpret_cast<GV*>(p));
+    } else {
+        *reinterpret_cast<GV*>(p) = x;
+    }
+}
+
+// A unit's source bytes as loaded: one aligned block, plus the next one when the
+// source is misaligned by k = s mod 4*NW bytes (k is uniform across the wave).  The
+// second block holds source bytes s + 4*NW - 1 and earlier ones only up to the block
+// boundary, so it lies inside the source's page.
+template <int NW>
+struct Raw {
+    typename Vec<NW>::type x, y;
+};
+template <int NW>
+__device__ __forceinline__ void load_raw(const gbyte* s, uint32_t k, Raw<NW>& r) {
     static_assert(NW == 2 || NW == 4, "units are 8 or 16 bytes");
-    const uint8_t* a = s - k;
-    const typename Vec<NW>::type x = ldv<NW>(a);
+    const gbyte* a = s - k;
+    r.x = ldg<NW>(a);
+    if (k != 0) r.y = ldg<NW>(a + 4 * NW);
+}
+// Shifts a loaded unit into place with v_alignbyte.
+template <int NW>
+__device__ __forceinline__ void align_raw(const Raw<NW>& raw, uint32_t k, uint32_t (&out)[NW]) {
     if (k == 0) {
 #pragma unroll
-        for (int i = 0; i < NW; ++i) out[i] = x[i];
+        for (int i = 0; i < NW; ++i) out[i] = raw.x[i];
         return;
     }
-    const typename Vec<NW>::type y = ldv<NW>(a + 4 * NW);
     uint32_t w[2 * NW];
 #pragma unroll
     for (int i = 0; i < NW; ++i) {
-        w[i] = x[i];
-        w[NW + i] = y[i];
+        w[i] = raw.x[i];
+        w[NW + i] = raw.y[i];
     }
     const uint32_t r = k & 3u;
     const uint32_t q = k >> 2;  // whole dwords to skip, < NW
@@ -106,34 +143,47 @@ __device__ __forceinline__ uint32_t f32_to_elem(float x) {
     if constexpr (DB == 4) return __float_as_uint(x);
     return f32_to_bf16(x);
 }
+// kOpScale: HBT_COPY_OP_DIVIDE by a power of two, run as a multiply by its exact
+// reciprocal (passed in place of the divisor); the bits are those of the division.
+constexpr int kOpScale = 2;
 template <int SB, int DB, int OP>
 __device__ __forceinline__ uint32_t convert(uint32_t bits, float divisor) {
     if constexpr (SB == DB && OP == HBT_COPY_OP_COPY) return bits;
     float x = elem_to_f32<SB>(bits);
     if constexpr (OP == HBT_COPY_OP_DIVIDE) x = x / divisor;
+    if constexpr (OP == kOpScale) x = x * divisor;
     return f32_to_elem<DB>(x);
 }
 
-template <int EB>
-__device__ __forceinline__ uint32_t load_elem(const uint8_t* p) {
+template <int EB, typename B>
+__device__ __forceinline__ uint32_t load_elem(const B* p) {
     if constexpr (EB == 4) return *reinterpret_cast<const uint32_t*>(p);
     return *reinterpret_cast<const uint16_t*>(p);
 }
 template <int EB>
-__device__ __forceinline__ void store_elem(uint8_t* p, uint32_t bits) {
+__device__ __forceinline__ uint32_t load_elem(const gbyte* p) {
+    typedef __attribute__((address_space(1))) const uint32_t G32;
+    typedef __attribute__((address_space(1))) const uint16_t G16;
+    if constexpr (EB == 4) return *reinterpret_cast<G32*>(p);
+    return *reinterpret_cast<G16*>(p);
+}
+template <int EB>
+__device__ __forceinline__ void store_elem(gbyte* p, uint32_t bits) {
+    typedef __attribute__((address_space(1))) uint32_t G32;
+    typedef __attribute__((address_space(1))) uint16_t G16;
     if constexpr (EB == 4) {
-        *reinterpret_cast<uint32_t*>(p) = bits;
+        *reinterpret_cast<G32*>(p) = bits;
     } else {
-        *reinterpret_cast<uint16_t*>(p) = static_cast<uint16_t>(bits);
+        *reinterpret_cast<G16*>(p) = static_cast<uint16_t>(bits);
     }
 }
 
 // Elements per lane unit: one 16-byte access on the wider side of the copy.
 template <int SB, int DB>
 constexpr int unit_elems() { return 16 / (SB > DB ? SB : DB); }
-// Elements per chunk (per workgroup), the same for every dtype pair.
+// Elements per chunk (per workgroup): 16 bytes of source per lane.
 template <int SB, int DB>
-constexpr int64_t chunk_elems() { return 512; }
+constexpr int64_t chunk_elems() { return int64_t(kCopyBlock) * 16 / SB; }
 
 // Unpack the U elements held in `words` (SB bytes each) into element bit patterns.
 template <int SB, int U>
@@ -150,7 +200,7 @@ __device__ __forceinline__ void unpack_unit(const uint32_t (&words)[U * SB / 4],
     }
 }
 template <int DB, int U>
-__device__ __forceinline__ void pack_unit_store(uint8_t* d, const uint32_t (&e)[U]) {
+__device__ __forceinline__ void pack_unit_store(gbyte* d, const uint32_t (&e)[U]) {
     constexpr int NW = U * DB / 4;
     typename Vec<NW>::type x;
     if constexpr (DB == 4) {
@@ -160,15 +210,16 @@ __device__ __forceinline__ void pack_unit_store(uint8_t* d, const uint32_t (&e)[
 #pragma unroll
         for (int i = 0; i < U / 2; ++i) x[i] = e[2 * i] | (e[2 * i + 1] << 16);
     }
-    stv<NW>(d, x);
+    stg<NW>(d, x);
 }
 
-template <int SB, int DB, int OP>
-__global__ __launch_bounds__(kCopyBlock) void copy_kernel(const int64_t* __restrict__ table,
-                                                          int64_t count, float divisor) {
-    const int64_t chunk = static_cast<int64_t>(blockIdx.x);
-    // Last record whose first_chunk <= chunk (records with no chunks are skipped by
-    // the host, so this is the owning record).
+// Index of the record that owns `chunk`: the last record whose first_chunk <= chunk
+// (the host drops records with no chunks, so first_chunk strictly increases).  The
+// search runs on the scalar unit: its loads hit the scalar cache and do not queue behind
+// the vector traffic of the waves in flight.  (A 64-way search with one ballot over
+// vector loads measured slower: 5.8 against 6.5 TB/s on a 40-record reshard.)
+__device__ __forceinline__ int64_t owning_record(const int64_t* __restrict__ table, int64_t count,
+                                                 int64_t chunk) {
     int64_t lo = 0, hi = count - 1;
     while (lo < hi) {
         const int64_t mid = (lo + hi + 1) >> 1;
@@ -178,21 +229,32 @@ __global__ __launch_bounds__(kCopyBlock) void copy_kernel(const int64_t* __restr
             hi = mid - 1;
         }
     }
-    const int64_t* rec = table + 4 * lo;
-    const uint8_t* src = reinterpret_cast<const uint8_t*>(rec[0]);
-    uint8_t* dst = reinterpret_cast<uint8_t*>(rec[1]);
+    return lo;
+}
+
+template <int SB, int DB, int OP>
+__global__ __launch_bounds__(kCopyBlock) void copy_kernel(const int64_t* __restrict__ table,
+                                                          int64_t count, float divisor) {
+    static_assert(kCopyBlock == 64, "the record search uses one 64-lane ballot");
+    const int64_t chunk = static_cast<int64_t>(blockIdx.x);
+    const int64_t* rec = table + 4 * owning_record(table, count, chunk);
+    const gbyte* src = reinterpret_cast<const gbyte*>(static_cast<uintptr_t>(rec[0]));
+    gbyte* dst = reinterpret_cast<gbyte*>(static_cast<uintptr_t>(rec[1]));
     const int64_t n = rec[2];
     constexpr int64_t kChunk = chunk_elems<SB, DB>();
     const int64_t e0 = (chunk - rec[3]) * kChunk;
     const int64_t len = (n - e0) < kChunk ? (n - e0) : kChunk;
 
-    uint8_t* d = dst + e0 * DB;
-    const uint8_t* s = src != nullptr ? src + e0 * SB : nullptr;
+    gbyte* d = dst + e0 * DB;
+    const gbyte* s = src != nullptr ? src + e0 * SB : nullptr;
+    constexpr int U = unit_elems<SB, DB>();
+    constexpr int kSrcWords = U * SB / 4;
+    constexpr int kPerLane = static_cast<int>(kChunk / U / kCopyBlock);
+    static_assert(kChunk == int64_t(kPerLane) * kCopyBlock * U, "a chunk is whole units on every lane");
 
     // Head: elements until the destination is 16-byte aligned.
-    int64_t head = static_cast<int64_t>(((16u - (reinterpret_cast<uintptr_t>(d) & 15u)) & 15u) / DB);
+    int64_t head = static_cast<int64_t>(((16u - (static_cast<uint32_t>(reinterpret_cast<uintptr_t>(d)) & 15u)) & 15u) / DB);
     if (head > len) head = len;
-    constexpr int U = unit_elems<SB, DB>();
     const int64_t units = (len - head) / U;
     const int64_t tail_begin = head + units * U;
 
@@ -207,27 +269,100 @@ __global__ __launch_bounds__(kCopyBlock) void copy_kernel(const int64_t* __restr
         store_elem<DB>(d + e * DB, bits);
     }
 
-    uint8_t* dbody = d + head * DB;
+    // Units per lane: kPerLane (2 for bf16 -> fp32, else 1).  Every unit's loads are
+    // issued before the first store, so a workgroup pays one memory round trip.
+    gbyte* dbody = d + head * DB;
     if (s == nullptr) {
-        for (int64_t u = threadIdx.x; u < units; u += kCopyBlock) {
-            uint32_t zero[U];
+        uint32_t zero[U];
 #pragma unroll
-            for (int i = 0; i < U; ++i) zero[i] = 0u;
-            pack_unit_store<DB, U>(dbody + u * U * DB, zero);
+        for (int i = 0; i < U; ++i) zero[i] = 0u;
+#pragma unroll
+        for (int j = 0; j < kPerLane; ++j) {
+            const int64_t u = threadIdx.x + j * kCopyBlock;
+            if (u < units) pack_unit_store<DB, U>(dbody + u * U * DB, zero);
         }
         return;
     }
-    const uint8_t* sbody = s + head * SB;
-    constexpr int kSrcWords = U * SB / 4;
-    const uint32_t k = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(sbody) & (4u * kSrcWords - 1u));
-    for (int64_t u = threadIdx.x; u < units; u += kCopyBlock) {
-        uint32_t words[kSrcWords];
-        load_shifted<kSrcWords>(sbody + u * U * SB, k, words);
-        uint32_t e[U];
-        unpack_unit<SB, U>(words, e);
+    const gbyte* sbody = s + head * SB;
+    const uint32_t k = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(sbody)) & (4u * kSrcWords - 1u);
+    Raw<kSrcWords> raw[kPerLane];
 #pragma unroll
-        for (int i = 0; i < U; ++i) e[i] = convert<SB, DB, OP>(e[i], divisor);
-        pack_unit_store<DB, U>(dbody + u * U * DB, e);
+    for (int j = 0; j < kPerLane; ++j) {
+        const int64_t u = threadIdx.x + j * kCopyBlock;
+        if (u < units) load_raw<kSrcWords>(sbody + u * U * SB, k, raw[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < kPerLane; ++j) {
+        const int64_t u = threadIdx.x + j * kCopyBlock;
+        if (u < units) {
+            uint32_t words[kSrcWords];
+            align_raw<kSrcWords>(raw[j], k, words);
+            uint32_t e[U];
+            unpack_unit<SB, U>(words, e);
+#pragma unroll
+            for (int i = 0; i < U; ++i) e[i] = convert<SB, DB, OP>(e[i], divisor);
+            pack_unit_store<DB, U>(dbody + u * U * DB, e);
+        }
+    }
+}
+
+// Aligned-record copy: every record's destination is 16-byte aligned and its source is
+// aligned to the unit's source width (the host certifies this for the whole plan), so a
+// lane moves its unit with one aligned load and one aligned store.  A chunk's units past
+// the record's end are masked off; a record whose length is not a whole number of units
+// finishes with an element loop in its last chunk.
+template <int SB, int DB, int OP>
+__global__ __launch_bounds__(kCopyBlock) void copy_aligned_kernel(const int64_t* __restrict__ table,
+                                                                  int64_t count, float divisor) {
+    constexpr int U = unit_elems<SB, DB>();
+    constexpr int kSrcWords = U * SB / 4;
+    constexpr int64_t kChunk = chunk_elems<SB, DB>();
+    constexpr int kPerLane = static_cast<int>(kChunk / U / kCopyBlock);
+    static_assert(kChunk == int64_t(kPerLane) * kCopyBlock * U, "a chunk is whole units on every lane");
+    const int64_t chunk = static_cast<int64_t>(blockIdx.x);
+    const int64_t* rec = table + 4 * owning_record(table, count, chunk);
+    const int64_t e0 = (chunk - rec[3]) * kChunk;
+    const int64_t n = rec[2];
+    const int64_t len = (n - e0) < kChunk ? (n - e0) : kChunk;
+    const int64_t units = len / U;
+    const gbyte* s = reinterpret_cast<const gbyte*>(static_cast<uintptr_t>(rec[0]));
+    gbyte* d = reinterpret_cast<gbyte*>(static_cast<uintptr_t>(rec[1])) + e0 * DB;
+    if (s == nullptr) {
+        uint32_t zero[U];
+#pragma unroll
+        for (int i = 0; i < U; ++i) zero[i] = 0u;
+#pragma unroll
+        for (int j = 0; j < kPerLane; ++j) {
+            const int64_t u = threadIdx.x + j * kCopyBlock;
+            if (u < units) pack_unit_store<DB, U>(d + u * U * DB, zero);
+        }
+        if (threadIdx.x < len - units * U) store_elem<DB>(d + (units * U + threadIdx.x) * DB, 0u);
+        return;
+    }
+    s += e0 * SB;
+    typename Vec<kSrcWords>::type x[kPerLane];
+#pragma unroll
+    for (int j = 0; j < kPerLane; ++j) {
+        const int64_t u = threadIdx.x + j * kCopyBlock;
+        if (u < units) x[j] = ldg<kSrcWords>(s + u * U * SB);
+    }
+#pragma unroll
+    for (int j = 0; j < kPerLane; ++j) {
+        const int64_t u = threadIdx.x + j * kCopyBlock;
+        if (u < units) {
+            uint32_t words[kSrcWords];
+#pragma unroll
+            for (int i = 0; i < kSrcWords; ++i) words[i] = x[j][i];
+            uint32_t e[U];
+            unpack_unit<SB, U>(words, e);
+#pragma unroll
+            for (int i = 0; i < U; ++i) e[i] = convert<SB, DB, OP>(e[i], divisor);
+            pack_unit_store<DB, U>(d + u * U * DB, e);
+        }
+    }
+    if (threadIdx.x < len - units * U) {
+        const int64_t e = units * U + threadIdx.x;
+        store_elem<DB>(d + e * DB, convert<SB, DB, OP>(load_elem<SB>(s + e * SB), divisor));
     }
 }
 
@@ -298,8 +433,14 @@ __global__ __launch_bounds__(kShareBlock) void local_share_kernel(RankTable rank
 }
 
 template <int SB, int DB, int OP>
-void launch_copy(const int64_t* table, int64_t count, int64_t chunks, float divisor, hipStream_t s) {
-    copy_kernel<SB, DB, OP><<<dim3(static_cast<unsigned>(chunks)), kCopyBlock, 0, s>>>(table, count, divisor);
+void launch_copy(const int64_t* table, int64_t count, int64_t chunks, float divisor, bool aligned,
+                 hipStream_t s) {
+    if (aligned) {
+        copy_aligned_kernel<SB, DB, OP>
+            <<<dim3(static_cast<unsigned>(chunks)), kCopyBlock, 0, s>>>(table, count, divisor);
+    } else {
+        copy_kernel<SB, DB, OP><<<dim3(static_cast<unsigned>(chunks)), kCopyBlock, 0, s>>>(table, count, divisor);
+    }
 }
 
 }  // namespace
@@ -321,12 +462,17 @@ int64_t hbt_copy_chunk_elems(int32_t src_dtype, int32_t dst_dtype) {
 
 int32_t hbt_copy_intervals(const int64_t* table, int64_t count, int64_t total_chunks,
                            int32_t src_dtype, int32_t dst_dtype, int32_t op, float divisor,
-                           void* stream) {
+                           int32_t flags, void* stream) {
     clear_error();
     if (count < 0 || total_chunks < 0 || (count > 0 && table == nullptr)) {
         set_error("hbt_copy_intervals: bad table/count/total_chunks");
         return HBT_ERR_INVALID_ARGUMENT;
     }
+    if ((flags & ~HBT_COPY_ALIGNED) != 0) {
+        set_error("hbt_copy_intervals: unknown flags 0x%x", static_cast<unsigned>(flags));
+        return HBT_ERR_INVALID_ARGUMENT;
+    }
+    const bool aligned = (flags & HBT_COPY_ALIGNED) != 0;
     if (count == 0 || total_chunks == 0) return HBT_OK;
     if (total_chunks > 0x7FFFFFFFLL) {
         set_error("hbt_copy_intervals: %lld chunks exceed the grid limit",
@@ -345,9 +491,9 @@ int32_t hbt_copy_intervals(const int64_t* table, int64_t count, int64_t total_ch
     if (op == HBT_COPY_OP_COPY && src_dtype == dst_dtype) {
         // Bit copy; fp64 moves as pairs of dwords (the host doubles its numels).
         if (ssz == 2) {
-            launch_copy<2, 2, HBT_COPY_OP_COPY>(table, count, total_chunks, divisor, s);
+            launch_copy<2, 2, HBT_COPY_OP_COPY>(table, count, total_chunks, divisor, aligned, s);
         } else if (ssz == 4) {
-            launch_copy<4, 4, HBT_COPY_OP_COPY>(table, count, total_chunks, divisor, s);
+            launch_copy<4, 4, HBT_COPY_OP_COPY>(table, count, total_chunks, divisor, aligned, s);
         } else {
             set_error("hbt_copy_intervals: 8-byte elements must be passed as dword pairs (F32)");
             return HBT_ERR_UNSUPPORTED;
@@ -358,22 +504,37 @@ int32_t hbt_copy_intervals(const int64_t* table, int64_t count, int64_t total_ch
         set_error("hbt_copy_intervals: conversions and division support F32 and BF16 only");
         return HBT_ERR_UNSUPPORTED;
     }
+    // Division by a power of two (the AVG pre-divide at a power-of-two world size) runs
+    // as a multiply by the exact reciprocal: the same bits, without the division sequence.
+    const float recip = op == HBT_COPY_OP_DIVIDE ? exact_reciprocal(divisor) : 0.0f;
+    if (op == HBT_COPY_OP_DIVIDE && recip != 0.0f) {
+        if (ssz == 4 && dsz == 4) {
+            launch_copy<4, 4, kOpScale>(table, count, total_chunks, recip, aligned, s);
+        } else if (ssz == 2 && dsz == 2) {
+            launch_copy<2, 2, kOpScale>(table, count, total_chunks, recip, aligned, s);
+        } else if (ssz == 4 && dsz == 2) {
+            launch_copy<4, 2, kOpScale>(table, count, total_chunks, recip, aligned, s);
+        } else {
+            launch_copy<2, 4, kOpScale>(table, count, total_chunks, recip, aligned, s);
+        }
+        return check_launch("hbt_copy_intervals");
+    }
     const bool div = op == HBT_COPY_OP_DIVIDE;
     if (ssz == 4 && dsz == 4) {
-        launch_copy<4, 4, HBT_COPY_OP_DIVIDE>(table, count, total_chunks, divisor, s);
+        launch_copy<4, 4, HBT_COPY_OP_DIVIDE>(table, count, total_chunks, divisor, aligned, s);
     } else if (ssz == 2 && dsz == 2) {
-        launch_copy<2, 2, HBT_COPY_OP_DIVIDE>(table, count, total_chunks, divisor, s);
+        launch_copy<2, 2, HBT_COPY_OP_DIVIDE>(table, count, total_chunks, divisor, aligned, s);
     } else if (ssz == 4 && dsz == 2) {
         if (div) {
-            launch_copy<4, 2, HBT_COPY_OP_DIVIDE>(table, count, total_chunks, divisor, s);
+            launch_copy<4, 2, HBT_COPY_OP_DIVIDE>(table, count, total_chunks, divisor, aligned, s);
         } else {
-            launch_copy<4, 2, HBT_COPY_OP_COPY>(table, count, total_chunks, divisor, s);
+            launch_copy<4, 2, HBT_COPY_OP_COPY>(table, count, total_chunks, divisor, aligned, s);
         }
     } else {
         if (div) {
-            launch_copy<2, 4, HBT_COPY_OP_DIVIDE>(table, count, total_chunks, divisor, s);
+            launch_copy<2, 4, HBT_COPY_OP_DIVIDE>(table, count, total_chunks, divisor, aligned, s);
         } else {
-            launch_copy<2, 4, HBT_COPY_OP_COPY>(table, count, total_chunks, divisor, s);
+            launch_copy<2, 4, HBT_COPY_OP_COPY>(table, count, total_chunks, divisor, aligned, s);
         }
     }
     return check_launch("hbt_copy_intervals");

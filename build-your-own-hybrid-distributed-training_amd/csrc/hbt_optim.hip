@@ -829,10 +829,8 @@ int32_t hbt_grad_local_share_sqnorm(const void* const* rank_grads, int32_t group
     }
     hipStream_t st = as_stream(stream);
     // An exact power of two (or 1) divides as a multiply by its exact reciprocal.
-    int exponent = 0;
-    const float mantissa = std::frexp(divisor, &exponent);
-    const bool recip_exact = divisor > 0.0f && mantissa == 0.5f && exponent > -125 && exponent < 126;
-    const float recip = recip_exact ? std::ldexp(1.0f, 1 - exponent) : 0.0f;
+    const float recip = exact_reciprocal(divisor);
+    const bool recip_exact = recip != 0.0f;
     const dim3 grid(static_cast<unsigned>(tiles));
 #define HBT_TILES(SBYTES, G, R)                                                                 \
     local_share_tiles_kernel<SBYTES, G, R><<<grid, kShareBlock, 0, st>>>(                         \

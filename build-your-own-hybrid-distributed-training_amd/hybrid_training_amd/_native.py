@@ -26,6 +26,7 @@ from .errors import NativeKernelError, UnsupportedFeatureError, format_error
 
 __all__ = [
     "ABI_VERSION",
+    "COPY_ALIGNED",
     "COPY_OP_COPY",
     "COPY_OP_DIVIDE",
     "SGD_FIRST_STEP",
@@ -49,7 +50,7 @@ __all__ = [
     "stream_of",
 ]
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 MAX_TENSORS_PER_LAUNCH = 16
 MAX_LOCAL_RANKS = 64
 
@@ -60,6 +61,8 @@ DTYPE_F64 = 3
 
 COPY_OP_COPY = 0
 COPY_OP_DIVIDE = 1
+COPY_ALIGNED = 1
+_CODE_BYTES = {DTYPE_F32: 4, DTYPE_BF16: 2, DTYPE_F16: 2, DTYPE_F64: 8}
 SGD_MOMENTUM = 1
 SGD_FIRST_STEP = 2
 SGD_NESTEROV = 4
@@ -106,7 +109,7 @@ EXPORTED_SYMBOLS: dict[str, tuple[object, tuple[object, ...]]] = {
     "hbt_copy_chunk_elems": (_c_i64, (_c_i32, _c_i32)),
     "hbt_copy_intervals": (
         _c_i32,
-        (_c_void_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_f32, _c_void_p),
+        (_c_void_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_f32, _c_i32, _c_void_p),
     ),
     "hbt_grad_local_share": (
         _c_i32,
@@ -130,7 +133,7 @@ _LIB: ctypes.CDLL | None = None
 # function of its rows (addresses, lengths, chunk prefix), so an entry stays valid
 # even after the tensors it was built for are freed; reuse skips the host-to-device
 # upload, which for a few hundred rows costs more than moving a GB on the device.
-_TABLE_CACHE: "OrderedDict[tuple, torch.Tensor]" = OrderedDict()
+_TABLE_CACHE: "OrderedDict[tuple, tuple[torch.Tensor, int, bool]]" = OrderedDict()
 _TABLE_CACHE_SIZE = 256
 
 
@@ -294,20 +297,39 @@ def _copy_chunk(lib: ctypes.CDLL, src_code: int, dst_code: int) -> int:
     return chunk
 
 
-def _device_table(flat: tuple[int, ...], device: torch.device) -> torch.Tensor:
-    """The int64 table on ``device``, uploaded once per distinct content and stream."""
-    key = (device, stream_of(device), flat)
-    table = _TABLE_CACHE.get(key)
-    if table is not None:
+def _prepared_plan(
+    device: torch.device, rows: tuple[tuple[int, int, int], ...], src_code: int, dst_code: int, scale: int
+) -> tuple[torch.Tensor, int, bool]:
+    """(device table, total chunks, aligned) for a plan, built once per distinct plan and
+    stream.  The table is uploaded on that stream, so later launches on it see it."""
+    stream = stream_of(device)
+    key = (device, stream, src_code, dst_code, scale, rows)
+    entry = _TABLE_CACHE.get(key)
+    if entry is not None:
         _TABLE_CACHE.move_to_end(key)
-        return table
+        return entry
+    chunk = _copy_chunk(library(), src_code, dst_code)
+    # The aligned kernel needs every destination on a 16-byte boundary and every source
+    # on the source width of one 16-byte unit.
+    src_bytes, dst_bytes = _CODE_BYTES[src_code], _CODE_BYTES[dst_code]
+    src_align = 16 * src_bytes // max(src_bytes, dst_bytes)
+    aligned = True
+    flat: list[int] = []
+    first = 0
+    for src_addr, dst_addr, n in rows:
+        n_units = n * scale
+        flat.extend((src_addr, dst_addr, n_units, first))
+        first += -(-n_units // chunk)
+        if dst_addr % 16 or src_addr % src_align:
+            aligned = False
     host = torch.tensor(flat, dtype=torch.int64).pin_memory()
     with torch.cuda.device(device):
         table = host.to(device, non_blocking=True)
-    _TABLE_CACHE[key] = table
+    entry = (table, first, aligned)
+    _TABLE_CACHE[key] = entry
     if len(_TABLE_CACHE) > _TABLE_CACHE_SIZE:
         _TABLE_CACHE.popitem(last=False)
-    return table
+    return entry
 
 
 class CopyPlan:
@@ -391,14 +413,7 @@ class CopyPlan:
             src_code = dst_code = DTYPE_F32
             scale = 2
         lib = library()
-        chunk = _copy_chunk(lib, src_code, dst_code)
-        flat: list[int] = []
-        first = 0
-        for src_addr, dst_addr, n in self._rows:
-            n_units = n * scale
-            flat.extend((src_addr, dst_addr, n_units, first))
-            first += -(-n_units // chunk)
-        table = _device_table(tuple(flat), self.device)
+        table, first, aligned = _prepared_plan(self.device, tuple(self._rows), src_code, dst_code, scale)
         with torch.cuda.device(self.device):
             status = lib.hbt_copy_intervals(
                 table.data_ptr(),
@@ -408,6 +423,7 @@ class CopyPlan:
                 dst_code,
                 op,
                 float(divisor),
+                COPY_ALIGNED if aligned else 0,
                 stream_of(self.device),
             )
         check(status, "native.hbt_copy_intervals")

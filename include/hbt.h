@@ -161,8 +161,9 @@ int32_t hbt_grad_norm_finalize(const double* partials, int64_t count, double max
  *   { src_address (0 => write zeros), dst_address, numel, first_chunk }
  * where first_chunk is the exclusive prefix sum over records of
  * ceil(numel / hbt_copy_chunk_elems(src_dtype, dst_dtype)), and total_chunks is the
- * sum.  A chunk is 512 elements for every pair the kernel moves; the function
- * returns -1 for a pair it does not move (8-byte data travels as F32 pairs).  All records share src_dtype/dst_dtype and op:
+ * sum.  A chunk is 1 KB of source: 256 elements of a 4-byte source, 512 of a 2-byte
+ * one; hbt_copy_chunk_elems returns -1 for a pair the kernel does not move (8-byte data
+ * travels as F32 pairs).  All records share src_dtype/dst_dtype and op:
  *   HBT_COPY_OP_COPY    dst = src               (same dtype: byte copy; F32->BF16
  *                                                rounds to nearest even, NaN -> 0x7FC0;
  *                                                BF16->F32 widens exactly)
@@ -170,13 +171,22 @@ int32_t hbt_grad_norm_finalize(const double* partials, int64_t count, double max
  *                                                BF16 data, result rounded to dst_dtype)
  * Source and destination ranges of one call must not overlap.  Addresses need no
  * particular alignment.
+ *
+ * flags: 0, or HBT_COPY_ALIGNED when the caller certifies that every record's
+ * dst_address is a multiple of 16 and every nonzero src_address a multiple of the
+ * source width of one 16-byte destination-or-source unit, 16 * S / max(S, D) bytes for
+ * S- and D-byte elements (16 for F32 -> F32, 8 for BF16 -> F32, 16 for the others).
+ * Aligned plans run a kernel without the head and shifted-load paths (measured 6.6
+ * against 5.7 TB/s on a 298-record fp32 unpack).  The results are the same bits
+ * either way.
  * ---------------------------------------------------------------------------- */
 #define HBT_COPY_OP_COPY 0
 #define HBT_COPY_OP_DIVIDE 1
+#define HBT_COPY_ALIGNED 1
 int64_t hbt_copy_chunk_elems(int32_t src_dtype, int32_t dst_dtype);
 int32_t hbt_copy_intervals(const int64_t* table, int64_t count, int64_t total_chunks,
                            int32_t src_dtype, int32_t dst_dtype, int32_t op, float divisor,
-                           void* stream);
+                           int32_t flags, void* stream);
 
 /* ------------------------------------------------------------------------------
  * FSDP gradient local share on one device.

@@ -130,8 +130,13 @@ def test_in_place_divide(device):
     assert np.array_equal(x.cpu().numpy().view(np.int32), expect.view(np.int32))
 
 
-def test_specials_round_trip_and_divide(device):
-    vals = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 1e-40, -1e-40, 3.4e38, 1.0, 1.00390625], np.float32)
+@pytest.mark.parametrize("divisor", [3.0, 8.0, 0.5, 2.0**-120])
+def test_specials_round_trip_and_divide(device, divisor):
+    """Specials through the bf16 narrowing and the divide.  Power-of-two divisors take the
+    exact-reciprocal multiply and must give the bits of numpy's division, subnormal
+    results and overflow to inf included."""
+    vals = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 1e-40, -1e-40, 3.4e38, 1.0, 1.00390625,
+                     1.1754944e-38, 3e-45, 1.5e-38, -2.3e-38, 7.0, 1e30], np.float32)
     src = torch.from_numpy(vals).to(device)
     out16 = torch.empty(vals.size, dtype=torch.bfloat16, device=device)
     plan = _native.CopyPlan(device)
@@ -141,8 +146,9 @@ def test_specials_round_trip_and_divide(device):
     div = torch.empty_like(src)
     plan = _native.CopyPlan(device)
     plan.add(src, 0, div, 0, vals.size)
-    plan.run(src_dtype=torch.float32, dst_dtype=torch.float32, op=_native.COPY_OP_DIVIDE, divisor=3.0)
-    expect = (vals / np.float32(3.0)).astype(np.float32)
+    plan.run(src_dtype=torch.float32, dst_dtype=torch.float32, op=_native.COPY_OP_DIVIDE, divisor=divisor)
+    with np.errstate(over="ignore", under="ignore"):
+        expect = (vals / np.float32(divisor)).astype(np.float32)
     got = div.cpu().numpy()
     assert np.array_equal(np.isnan(got), np.isnan(expect))
     assert np.array_equal(got[~np.isnan(got)].view(np.int32), expect[~np.isnan(expect)].view(np.int32))
@@ -155,3 +161,66 @@ def test_plan_bounds_are_checked_on_the_host(device):
         plan.add(a, 5, a, 0, 6)
     with pytest.raises(ValueError, match="runs past"):
         plan.add_zero(a, 8, 3)
+
+
+def _element_size(dtype):
+    return torch.empty(0, dtype=dtype).element_size()
+
+
+@pytest.mark.parametrize("divisor", [3.0, 8.0])
+@pytest.mark.parametrize(("sdt", "ddt", "op"), [c for c in CASES if c[0] != torch.float64])
+def test_aligned_kernel_matches_general_kernel(device, sdt, ddt, op, divisor):
+    """Plans whose records all start aligned run through both kernels of
+    ``hbt_copy_intervals`` (flags = HBT_COPY_ALIGNED and flags = 0) and must give the
+    same bits as numpy: lengths below one unit, around one chunk, with unit tails, and
+    zero-fill records.  Divisor 8 takes the exact-reciprocal multiply, 3 the division."""
+    if op != _native.COPY_OP_DIVIDE and divisor != 3.0:
+        pytest.skip("the divisor only matters for DIVIDE")
+    lib = _native.library()
+    rng = np.random.default_rng(11 + CASES.index((sdt, ddt, op)))
+    ssz, dsz = _element_size(sdt), _element_size(ddt)
+    s_code, d_code = _native.dtype_code(sdt), _native.dtype_code(ddt)
+    chunk = lib.hbt_copy_chunk_elems(s_code, d_code)
+    s_quant = (16 * ssz // max(ssz, dsz)) // ssz  # source elements per aligned step
+    d_quant = 16 // dsz
+    lengths = [1, 3, 7, 8, 9, chunk - 1, chunk, chunk + 1, 2 * chunk + 5, 100_003, 250_000]
+    n_src = 2_000_000
+    src = (torch.randn(n_src, dtype=torch.float32, device=device) * 3).to(sdt)
+    sbits = _bits(src)
+    rows, d_cursor = [], 0
+    for k, n in enumerate(lengths * 2):
+        d0 = d_cursor + int(rng.integers(0, 4)) * d_quant
+        s0 = -1 if k % 5 == 4 else int(rng.integers(0, (n_src - n) // s_quant)) * s_quant
+        rows.append((s0, d0, n))
+        d_cursor = d0 + n + (-(d0 + n)) % d_quant
+    n_dst = d_cursor + 64
+    if op != _native.COPY_OP_DIVIDE:
+        divisor = 1.0
+    outs = []
+    for flags in (_native.COPY_ALIGNED, 0):
+        dst = torch.full((n_dst,), 5.0, dtype=torch.float32, device=device).to(ddt)
+        assert src.data_ptr() % 16 == 0 and dst.data_ptr() % 16 == 0
+        flat, first = [], 0
+        for s0, d0, n in rows:
+            assert d0 + n <= n_dst and s0 + n <= n_src
+            s_addr = 0 if s0 < 0 else src.data_ptr() + s0 * ssz
+            flat += [s_addr, dst.data_ptr() + d0 * dsz, n, first]
+            first += -(-n // chunk)
+        table = torch.tensor(flat, dtype=torch.int64).to(device)
+        status = lib.hbt_copy_intervals(table.data_ptr(), len(rows), first, s_code, d_code, op, divisor, flags,
+                                        _native.stream_of(device))
+        _native.check(status, "test.copy_intervals")
+        outs.append(_bits(dst))
+    if sdt == ddt and op == _native.COPY_OP_COPY:
+        convert = lambda x: x  # noqa: E731
+    else:
+        def convert(x):
+            vals = x.view(np.float32) if sdt == torch.float32 else _as_f32(x)
+            if op == _native.COPY_OP_DIVIDE:
+                vals = (vals / np.float32(divisor)).astype(np.float32)
+            return vals.view(np.int32) if ddt == torch.float32 else oracle.f32_to_bf16(vals).view(np.int16)
+    expect = _bits(torch.full((n_dst,), 5.0, dtype=torch.float32).to(ddt))
+    for s0, d0, n in rows:
+        expect[d0 : d0 + n] = 0 if s0 < 0 else convert(sbits[s0 : s0 + n])
+    assert np.array_equal(outs[0], expect)
+    assert np.array_equal(outs[1], expect)

@@ -38,8 +38,9 @@ def test_library_loads_and_exports_every_declared_symbol():
     assert lib.hbt_norm_partials_count(_native.int64_array([1, 65536, 65537]), 3, 1) == 1 + 1 + 2
     assert lib.hbt_norm_partials_count(None, 99, 0) == -1
     assert lib.hbt_norm_partials_count(_native.int64_array([1]), 1, 7) == -1
-    assert lib.hbt_copy_chunk_elems(0, 0) == 512 and lib.hbt_copy_chunk_elems(1, 1) == 512
-    assert lib.hbt_copy_chunk_elems(0, 1) == 512 and lib.hbt_copy_chunk_elems(1, 0) == 512
+    # 1 KB of source per chunk
+    assert lib.hbt_copy_chunk_elems(0, 0) == 256 and lib.hbt_copy_chunk_elems(1, 1) == 512
+    assert lib.hbt_copy_chunk_elems(0, 1) == 256 and lib.hbt_copy_chunk_elems(1, 0) == 512
     assert lib.hbt_copy_chunk_elems(3, 3) == -1
     assert lib.hbt_last_error() == b""
 
@@ -53,8 +54,9 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     assert b"count" in lib.hbt_last_error()
     with pytest.raises(NativeKernelError, match="count"):
         _native.check(status, "test")
-    assert lib.hbt_copy_intervals(None, 1, 1, 0, 0, 0, 1.0, None) == -1
-    assert lib.hbt_copy_intervals(None, 0, 0, 0, 0, 0, 1.0, None) == 0
+    assert lib.hbt_copy_intervals(None, 1, 1, 0, 0, 0, 1.0, 0, None) == -1
+    assert lib.hbt_copy_intervals(None, 0, 0, 0, 0, 0, 1.0, 0, None) == 0
+    assert lib.hbt_copy_intervals(None, 0, 0, 0, 0, 0, 1.0, 2, None) == -1  # unknown flag
     assert lib.hbt_grad_local_share(None, 0, 0, 1, 1, 0, 1.0, None, None) == -1
     assert lib.hbt_grad_local_share_sqnorm(None, 1, 0, 1, 1, 0, 1.0, None, None, None, None) == -1
     assert b"hbt_grad_local_share_sqnorm" in lib.hbt_last_error()
