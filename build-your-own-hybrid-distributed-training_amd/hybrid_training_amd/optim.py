@@ -496,12 +496,14 @@ class _HostStatePipeline:
 
 
 class ShardedOptimizer:
-    """AdamW over this rank's shards with a global-norm clip, on HIP kernels.
+    """AdamW or SGD over this rank's shards with a global-norm clip, on HIP kernels.
 
     Same constructor, methods and properties as ``sharded_optimizer.py:244-499``.
-    ``defer_clip`` is the one addition (see the module docstring).  The CPU-offload
-    branch and the SGD inner optimizer are not implemented and raise
-    :class:`UnsupportedFeatureError` rather than falling back to torch.
+    ``defer_clip`` is the one addition (see the module docstring).  With
+    ``config.cpu_offload_state`` the master copies and the optimizer state live in
+    pinned host memory, as in the reference, and stream through the device each step
+    (:class:`_HostStatePipeline`).  ``amsgrad`` and ``maximize`` have no kernel and
+    raise :class:`UnsupportedFeatureError` rather than falling back to torch.
     """
 
     def __init__(
