@@ -55,7 +55,8 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--numel", type=int, default=SHARD_NUMEL, help="shard size (default: Llama-3-8B / 8)")
     ap.add_argument("--cpu-numel", type=int, default=1 << 28, help="CPU-baseline sample size")
-    ap.add_argument("--cpu-steps", type=int, default=6)
+    ap.add_argument("--cpu-steps", type=int, default=20,
+                    help="timed CPU-baseline steps (about 11 s of CPU work at the default size)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument(
         "--workload",
