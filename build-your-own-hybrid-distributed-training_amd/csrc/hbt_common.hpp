@@ -61,6 +61,34 @@ __device__ __forceinline__ uint32_t f32_to_bf16(float x) {
     return u >> 16;
 }
 
+// IEEE fp16 <-> fp32.  Widening is exact (subnormals included) and keeps a NaN's sign
+// and payload bits, as torch's CPU conversion does.  Narrowing rounds to nearest, ties
+// to even, overflows to +-inf and keeps fp16 subnormals; any NaN becomes sign | 0x7E00.
+__device__ __forceinline__ float f16_to_f32(uint32_t bits16) {
+    if ((bits16 & 0x7C00u) == 0x7C00u && (bits16 & 0x03FFu) != 0u) {
+        return __uint_as_float(((bits16 & 0x8000u) << 16) | 0x7F800000u | ((bits16 & 0x03FFu) << 13));
+    }
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits16)));
+}
+
+__device__ __forceinline__ uint32_t f32_to_f16(float x) {
+    const uint32_t u = __float_as_uint(x);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return ((u >> 16) & 0x8000u) | 0x7E00u;
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
+}
+
+// A 2-byte element's fp32 value and back: IEEE fp16 when kHalf, else bf16.
+template <bool kHalf>
+__device__ __forceinline__ float b16_to_f32(uint32_t bits16) {
+    if constexpr (kHalf) return f16_to_f32(bits16);
+    return bf16_to_f32(bits16);
+}
+template <bool kHalf>
+__device__ __forceinline__ uint32_t f32_to_b16(float x) {
+    if constexpr (kHalf) return f32_to_f16(x);
+    return f32_to_bf16(x);
+}
+
 // ---- fixed-order reductions ----------------------------------------------------------
 // Butterfly over the 64 lanes of a wavefront; every lane ends with the same total and
 // the pairing order is fixed, so the result is reproducible bit for bit.

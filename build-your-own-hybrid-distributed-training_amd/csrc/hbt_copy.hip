@@ -130,29 +130,30 @@ __device__ __forceinline__ void align_raw(const Raw<NW>& raw, uint32_t k, uint32
     }
 }
 
-// Element semantics.  SB/DB are source/destination element bytes.  Same-size COPY is
-// a bit copy; 4->2 narrows fp32 to bf16, 2->4 widens bf16 to fp32; DIVIDE goes through
-// fp32 (true division) and rounds to the destination type.
-template <int SB>
+// Element semantics.  SB/DB are source/destination element bytes; a 2-byte element is
+// bf16, or IEEE fp16 when H is set (a conversion never mixes the two).  Same-size COPY
+// is a bit copy; 4->2 narrows fp32 (round to nearest even), 2->4 widens exactly; DIVIDE
+// goes through fp32 (true division) and rounds to the destination type.
+template <int SB, bool H>
 __device__ __forceinline__ float elem_to_f32(uint32_t bits) {
     if constexpr (SB == 4) return __uint_as_float(bits);
-    return bf16_to_f32(bits);
+    return b16_to_f32<H>(bits);
 }
-template <int DB>
+template <int DB, bool H>
 __device__ __forceinline__ uint32_t f32_to_elem(float x) {
     if constexpr (DB == 4) return __float_as_uint(x);
-    return f32_to_bf16(x);
+    return f32_to_b16<H>(x);
 }
 // kOpScale: HBT_COPY_OP_DIVIDE by a power of two, run as a multiply by its exact
 // reciprocal (passed in place of the divisor); the bits are those of the division.
 constexpr int kOpScale = 2;
-template <int SB, int DB, int OP>
+template <int SB, int DB, int OP, bool H>
 __device__ __forceinline__ uint32_t convert(uint32_t bits, float divisor) {
     if constexpr (SB == DB && OP == HBT_COPY_OP_COPY) return bits;
-    float x = elem_to_f32<SB>(bits);
+    float x = elem_to_f32<SB, H>(bits);
     if constexpr (OP == HBT_COPY_OP_DIVIDE) x = x / divisor;
     if constexpr (OP == kOpScale) x = x * divisor;
-    return f32_to_elem<DB>(x);
+    return f32_to_elem<DB, H>(x);
 }
 
 template <int EB, typename B>
@@ -232,7 +233,7 @@ __device__ __forceinline__ int64_t owning_record(const int64_t* __restrict__ tab
     return lo;
 }
 
-template <int SB, int DB, int OP>
+template <int SB, int DB, int OP, bool H>
 __global__ __launch_bounds__(kCopyBlock) void copy_kernel(const int64_t* __restrict__ table,
                                                           int64_t count, float divisor) {
     static_assert(kCopyBlock == 64, "the record search uses one 64-lane ballot");
@@ -260,12 +261,12 @@ __global__ __launch_bounds__(kCopyBlock) void copy_kernel(const int64_t* __restr
 
     if (threadIdx.x < head) {
         const int64_t e = threadIdx.x;
-        const uint32_t bits = s != nullptr ? convert<SB, DB, OP>(load_elem<SB>(s + e * SB), divisor) : 0u;
+        const uint32_t bits = s != nullptr ? convert<SB, DB, OP, H>(load_elem<SB>(s + e * SB), divisor) : 0u;
         store_elem<DB>(d + e * DB, bits);
     }
     if (threadIdx.x < len - tail_begin) {
         const int64_t e = tail_begin + threadIdx.x;
-        const uint32_t bits = s != nullptr ? convert<SB, DB, OP>(load_elem<SB>(s + e * SB), divisor) : 0u;
+        const uint32_t bits = s != nullptr ? convert<SB, DB, OP, H>(load_elem<SB>(s + e * SB), divisor) : 0u;
         store_elem<DB>(d + e * DB, bits);
     }
 
@@ -300,7 +301,7 @@ __global__ __launch_bounds__(kCopyBlock) void copy_kernel(const int64_t* __restr
             uint32_t e[U];
             unpack_unit<SB, U>(words, e);
 #pragma unroll
-            for (int i = 0; i < U; ++i) e[i] = convert<SB, DB, OP>(e[i], divisor);
+            for (int i = 0; i < U; ++i) e[i] = convert<SB, DB, OP, H>(e[i], divisor);
             pack_unit_store<DB, U>(dbody + u * U * DB, e);
         }
     }
@@ -311,7 +312,7 @@ __global__ __launch_bounds__(kCopyBlock) void copy_kernel(const int64_t* __restr
 // lane moves its unit with one aligned load and one aligned store.  A chunk's units past
 // the record's end are masked off; a record whose length is not a whole number of units
 // finishes with an element loop in its last chunk.
-template <int SB, int DB, int OP>
+template <int SB, int DB, int OP, bool H>
 __global__ __launch_bounds__(kCopyBlock) void copy_aligned_kernel(const int64_t* __restrict__ table,
                                                                   int64_t count, float divisor) {
     constexpr int U = unit_elems<SB, DB>();
@@ -356,13 +357,13 @@ __global__ __launch_bounds__(kCopyBlock) void copy_aligned_kernel(const int64_t*
             uint32_t e[U];
             unpack_unit<SB, U>(words, e);
 #pragma unroll
-            for (int i = 0; i < U; ++i) e[i] = convert<SB, DB, OP>(e[i], divisor);
+            for (int i = 0; i < U; ++i) e[i] = convert<SB, DB, OP, H>(e[i], divisor);
             pack_unit_store<DB, U>(d + u * U * DB, e);
         }
     }
     if (threadIdx.x < len - units * U) {
         const int64_t e = units * U + threadIdx.x;
-        store_elem<DB>(d + e * DB, convert<SB, DB, OP>(load_elem<SB>(s + e * SB), divisor));
+        store_elem<DB>(d + e * DB, convert<SB, DB, OP, H>(load_elem<SB>(s + e * SB), divisor));
     }
 }
 
@@ -379,19 +380,19 @@ constexpr int kShareBlock = 64;
 constexpr int kShareGroups = 1;
 constexpr int64_t kShareTile = int64_t(kShareBlock) * 4 * kShareGroups;
 
-template <int SB>
+template <int SB, bool H>
 __device__ __forceinline__ f32x4 load_quad(const uint8_t* p) {
     if constexpr (SB == 4) {
         const u32x4v w = ldv<4>(p);
         return f32x4{__uint_as_float(w.x), __uint_as_float(w.y), __uint_as_float(w.z), __uint_as_float(w.w)};
     } else {
         const typename Vec<2>::type w = ldv<2>(p);
-        return f32x4{bf16_to_f32(w.x & 0xFFFFu), bf16_to_f32(w.x >> 16), bf16_to_f32(w.y & 0xFFFFu),
-                     bf16_to_f32(w.y >> 16)};
+        return f32x4{b16_to_f32<H>(w.x & 0xFFFFu), b16_to_f32<H>(w.x >> 16), b16_to_f32<H>(w.y & 0xFFFFu),
+                     b16_to_f32<H>(w.y >> 16)};
     }
 }
 
-template <int SB>
+template <int SB, bool H>
 __global__ __launch_bounds__(kShareBlock) void local_share_kernel(RankTable ranks, int32_t group_size,
                                                                   int64_t offset, int64_t shard_numel,
                                                                   int64_t valid_numel, float divisor,
@@ -402,9 +403,9 @@ __global__ __launch_bounds__(kShareBlock) void local_share_kernel(RankTable rank
 #pragma unroll
         for (int u = 0; u < kShareGroups; ++u) {
             const int64_t e = base + (int64_t(u) * kShareBlock + threadIdx.x) * 4;
-            f32x4 acc = load_quad<SB>(ranks.g[0] + (offset + e) * SB) / divisor;
+            f32x4 acc = load_quad<SB, H>(ranks.g[0] + (offset + e) * SB) / divisor;
             for (int32_t q = 1; q < group_size; ++q) {
-                acc = acc + load_quad<SB>(ranks.g[q] + (offset + e) * SB) / divisor;
+                acc = acc + load_quad<SB, H>(ranks.g[q] + (offset + e) * SB) / divisor;
             }
             stv<4>(out + e, u32x4v{__float_as_uint(acc.x), __float_as_uint(acc.y),
                                      __float_as_uint(acc.z), __float_as_uint(acc.w)});
@@ -423,23 +424,57 @@ __global__ __launch_bounds__(kShareBlock) void local_share_kernel(RankTable rank
     for (int64_t i = base + threadIdx.x; i < end; i += kShareBlock) {
         float acc = 0.0f;
         if (i < valid_numel) {
-            acc = elem_to_f32<SB>(load_elem<SB>(ranks.g[0] + (offset + i) * SB)) / divisor;
+            acc = elem_to_f32<SB, H>(load_elem<SB>(ranks.g[0] + (offset + i) * SB)) / divisor;
             for (int32_t q = 1; q < group_size; ++q) {
-                acc = acc + elem_to_f32<SB>(load_elem<SB>(ranks.g[q] + (offset + i) * SB)) / divisor;
+                acc = acc + elem_to_f32<SB, H>(load_elem<SB>(ranks.g[q] + (offset + i) * SB)) / divisor;
             }
         }
         out[i] = acc;
     }
 }
 
-template <int SB, int DB, int OP>
+template <int SB, int DB, int OP, bool H = false>
 void launch_copy(const int64_t* table, int64_t count, int64_t chunks, float divisor, bool aligned,
                  hipStream_t s) {
     if (aligned) {
-        copy_aligned_kernel<SB, DB, OP>
+        copy_aligned_kernel<SB, DB, OP, H>
             <<<dim3(static_cast<unsigned>(chunks)), kCopyBlock, 0, s>>>(table, count, divisor);
     } else {
-        copy_kernel<SB, DB, OP><<<dim3(static_cast<unsigned>(chunks)), kCopyBlock, 0, s>>>(table, count, divisor);
+        copy_kernel<SB, DB, OP, H><<<dim3(static_cast<unsigned>(chunks)), kCopyBlock, 0, s>>>(table, count, divisor);
+    }
+}
+
+// Conversions and division for 4- and 2-byte elements; H: the 2-byte side is fp16.
+// Division by a power of two (the AVG pre-divide at a power-of-two world size) runs as a
+// multiply by the exact reciprocal: the same bits, without the division sequence.
+template <bool H>
+void launch_arith(int ssz, int dsz, int32_t op, float divisor, const int64_t* table, int64_t count,
+                  int64_t chunks, bool aligned, hipStream_t s) {
+    const float recip = op == HBT_COPY_OP_DIVIDE ? exact_reciprocal(divisor) : 0.0f;
+    if (op == HBT_COPY_OP_DIVIDE && recip != 0.0f) {
+        if (ssz == 4 && dsz == 4) {
+            launch_copy<4, 4, kOpScale>(table, count, chunks, recip, aligned, s);
+        } else if (ssz == 2 && dsz == 2) {
+            launch_copy<2, 2, kOpScale, H>(table, count, chunks, recip, aligned, s);
+        } else if (ssz == 4) {
+            launch_copy<4, 2, kOpScale, H>(table, count, chunks, recip, aligned, s);
+        } else {
+            launch_copy<2, 4, kOpScale, H>(table, count, chunks, recip, aligned, s);
+        }
+    } else if (op == HBT_COPY_OP_DIVIDE) {
+        if (ssz == 4 && dsz == 4) {
+            launch_copy<4, 4, HBT_COPY_OP_DIVIDE>(table, count, chunks, divisor, aligned, s);
+        } else if (ssz == 2 && dsz == 2) {
+            launch_copy<2, 2, HBT_COPY_OP_DIVIDE, H>(table, count, chunks, divisor, aligned, s);
+        } else if (ssz == 4) {
+            launch_copy<4, 2, HBT_COPY_OP_DIVIDE, H>(table, count, chunks, divisor, aligned, s);
+        } else {
+            launch_copy<2, 4, HBT_COPY_OP_DIVIDE, H>(table, count, chunks, divisor, aligned, s);
+        }
+    } else if (ssz == 4) {  // conversions (same-dtype copies are bit copies)
+        launch_copy<4, 2, HBT_COPY_OP_COPY, H>(table, count, chunks, divisor, aligned, s);
+    } else {
+        launch_copy<2, 4, HBT_COPY_OP_COPY, H>(table, count, chunks, divisor, aligned, s);
     }
 }
 
@@ -485,8 +520,6 @@ int32_t hbt_copy_intervals(const int64_t* table, int64_t count, int64_t total_ch
         set_error("hbt_copy_intervals: bad dtype pair (%d, %d) or op %d", src_dtype, dst_dtype, op);
         return HBT_ERR_INVALID_ARGUMENT;
     }
-    const bool arithmetic = src_dtype == HBT_DTYPE_F32 || src_dtype == HBT_DTYPE_BF16;
-    const bool arithmetic_dst = dst_dtype == HBT_DTYPE_F32 || dst_dtype == HBT_DTYPE_BF16;
     hipStream_t s = as_stream(stream);
     if (op == HBT_COPY_OP_COPY && src_dtype == dst_dtype) {
         // Bit copy; fp64 moves as pairs of dwords (the host doubles its numels).
@@ -500,42 +533,19 @@ int32_t hbt_copy_intervals(const int64_t* table, int64_t count, int64_t total_ch
         }
         return check_launch("hbt_copy_intervals");
     }
-    if (!arithmetic || !arithmetic_dst) {
-        set_error("hbt_copy_intervals: conversions and division support F32 and BF16 only");
+    const bool arithmetic = src_dtype == HBT_DTYPE_F32 || src_dtype == HBT_DTYPE_BF16 || src_dtype == HBT_DTYPE_F16;
+    const bool arithmetic_dst = dst_dtype == HBT_DTYPE_F32 || dst_dtype == HBT_DTYPE_BF16 || dst_dtype == HBT_DTYPE_F16;
+    const bool mixed_16 = (src_dtype == HBT_DTYPE_BF16 && dst_dtype == HBT_DTYPE_F16) ||
+                          (src_dtype == HBT_DTYPE_F16 && dst_dtype == HBT_DTYPE_BF16);
+    if (!arithmetic || !arithmetic_dst || mixed_16) {
+        set_error("hbt_copy_intervals: conversions and division move F32, BF16 and F16 data, and "
+                  "convert F32 <-> BF16 and F32 <-> F16 only (got %d -> %d)", src_dtype, dst_dtype);
         return HBT_ERR_UNSUPPORTED;
     }
-    // Division by a power of two (the AVG pre-divide at a power-of-two world size) runs
-    // as a multiply by the exact reciprocal: the same bits, without the division sequence.
-    const float recip = op == HBT_COPY_OP_DIVIDE ? exact_reciprocal(divisor) : 0.0f;
-    if (op == HBT_COPY_OP_DIVIDE && recip != 0.0f) {
-        if (ssz == 4 && dsz == 4) {
-            launch_copy<4, 4, kOpScale>(table, count, total_chunks, recip, aligned, s);
-        } else if (ssz == 2 && dsz == 2) {
-            launch_copy<2, 2, kOpScale>(table, count, total_chunks, recip, aligned, s);
-        } else if (ssz == 4 && dsz == 2) {
-            launch_copy<4, 2, kOpScale>(table, count, total_chunks, recip, aligned, s);
-        } else {
-            launch_copy<2, 4, kOpScale>(table, count, total_chunks, recip, aligned, s);
-        }
-        return check_launch("hbt_copy_intervals");
-    }
-    const bool div = op == HBT_COPY_OP_DIVIDE;
-    if (ssz == 4 && dsz == 4) {
-        launch_copy<4, 4, HBT_COPY_OP_DIVIDE>(table, count, total_chunks, divisor, aligned, s);
-    } else if (ssz == 2 && dsz == 2) {
-        launch_copy<2, 2, HBT_COPY_OP_DIVIDE>(table, count, total_chunks, divisor, aligned, s);
-    } else if (ssz == 4 && dsz == 2) {
-        if (div) {
-            launch_copy<4, 2, HBT_COPY_OP_DIVIDE>(table, count, total_chunks, divisor, aligned, s);
-        } else {
-            launch_copy<4, 2, HBT_COPY_OP_COPY>(table, count, total_chunks, divisor, aligned, s);
-        }
+    if (src_dtype == HBT_DTYPE_F16 || dst_dtype == HBT_DTYPE_F16) {
+        launch_arith<true>(ssz, dsz, op, divisor, table, count, total_chunks, aligned, s);
     } else {
-        if (div) {
-            launch_copy<2, 4, HBT_COPY_OP_DIVIDE>(table, count, total_chunks, divisor, aligned, s);
-        } else {
-            launch_copy<2, 4, HBT_COPY_OP_COPY>(table, count, total_chunks, divisor, aligned, s);
-        }
+        launch_arith<false>(ssz, dsz, op, divisor, table, count, total_chunks, aligned, s);
     }
     return check_launch("hbt_copy_intervals");
 }
@@ -552,8 +562,8 @@ int32_t hbt_grad_local_share(const void* const* rank_grads, int32_t group_size, 
                   static_cast<long long>(valid_numel));
         return HBT_ERR_INVALID_ARGUMENT;
     }
-    if (in_dtype != HBT_DTYPE_F32 && in_dtype != HBT_DTYPE_BF16) {
-        set_error("hbt_grad_local_share: input dtype %d is not F32 or BF16", in_dtype);
+    if (in_dtype != HBT_DTYPE_F32 && in_dtype != HBT_DTYPE_BF16 && in_dtype != HBT_DTYPE_F16) {
+        set_error("hbt_grad_local_share: input dtype %d is not F32, BF16 or F16", in_dtype);
         return HBT_ERR_INVALID_ARGUMENT;
     }
     RankTable ranks{};
@@ -572,7 +582,7 @@ int32_t hbt_grad_local_share(const void* const* rank_grads, int32_t group_size, 
         return HBT_ERR_UNSUPPORTED;
     }
     // Vector path: every rank's slice and the output start on a 16-byte (fp32 input) or
-    // 8-byte (bf16 input) boundary.
+    // 8-byte (bf16 or fp16 input) boundary.
     const int elem = in_dtype == HBT_DTYPE_F32 ? 4 : 2;
     int32_t vec_ok = (reinterpret_cast<uintptr_t>(out) & 15u) == 0;
     for (int q = 0; q < group_size && vec_ok; ++q) {
@@ -580,12 +590,16 @@ int32_t hbt_grad_local_share(const void* const* rank_grads, int32_t group_size, 
         vec_ok = (a & static_cast<uintptr_t>(4 * elem - 1)) == 0;
     }
     hipStream_t s = as_stream(stream);
+    const dim3 grid(static_cast<unsigned>(tiles));
     if (in_dtype == HBT_DTYPE_F32) {
-        local_share_kernel<4><<<dim3(static_cast<unsigned>(tiles)), kShareBlock, 0, s>>>(
-            ranks, group_size, offset, shard_numel, valid_numel, divisor, vec_ok, out);
+        local_share_kernel<4, false><<<grid, kShareBlock, 0, s>>>(ranks, group_size, offset, shard_numel,
+                                                                   valid_numel, divisor, vec_ok, out);
+    } else if (in_dtype == HBT_DTYPE_BF16) {
+        local_share_kernel<2, false><<<grid, kShareBlock, 0, s>>>(ranks, group_size, offset, shard_numel,
+                                                                   valid_numel, divisor, vec_ok, out);
     } else {
-        local_share_kernel<2><<<dim3(static_cast<unsigned>(tiles)), kShareBlock, 0, s>>>(
-            ranks, group_size, offset, shard_numel, valid_numel, divisor, vec_ok, out);
+        local_share_kernel<2, true><<<grid, kShareBlock, 0, s>>>(ranks, group_size, offset, shard_numel,
+                                                                  valid_numel, divisor, vec_ok, out);
     }
     return check_launch("hbt_grad_local_share");
 }

@@ -347,10 +347,12 @@ constexpr int kShareBlock = 64;
 constexpr int64_t kShareTile = int64_t(kShareBlock) * 4;  // 256 elements, one wave
 constexpr int64_t kTilesPerNormChunk = norm_chunk<float>() / kShareTile;  // 128
 
-template <int SB>
+// Loads of one rank's gradient widened to fp32: SB-byte elements, a 2-byte element
+// being bf16, or IEEE fp16 when H is set.
+template <int SB, bool H>
 __device__ __forceinline__ float share_load1(const uint8_t* p) {
     if constexpr (SB == 4) return *reinterpret_cast<const float*>(p);
-    return bf16_to_f32(*reinterpret_cast<const uint16_t*>(p));
+    return b16_to_f32<H>(*reinterpret_cast<const uint16_t*>(p));
 }
 
 // Division by a power of two is exact scaling, so x / d == x * (1 / d) bitwise for
@@ -365,17 +367,24 @@ __device__ __forceinline__ float share_div1(float x, float divisor, float recip)
     if constexpr (kRecip) return x * recip;
     return x / divisor;
 }
-template <int SB>
+template <int SB, bool H>
 __device__ __forceinline__ f32x4 share_load4(const uint8_t* p) {
-    if constexpr (SB == 4) return ld4_nt(reinterpret_cast<const float*>(p));
-    return ld_grad4_nt(reinterpret_cast<const uint16_t*>(p));
+    if constexpr (SB == 4) {
+        return ld4_nt(reinterpret_cast<const float*>(p));
+    } else if constexpr (H) {
+        const u32x2 w = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
+        return f32x4{f16_to_f32(w.x & 0xFFFFu), f16_to_f32(w.x >> 16), f16_to_f32(w.y & 0xFFFFu),
+                     f16_to_f32(w.y >> 16)};
+    } else {
+        return ld_grad4_nt(reinterpret_cast<const uint16_t*>(p));
+    }
 }
 
 // One wave per 256-element tile: measured on MI355X (8 bf16 ranks -> fp32) this
 // short-lived shape streams at 6.4 TB/s, against 5.6 TB/s for the norm kernel's
 // 1024-thread, 8-tile workgroups.  kG > 0 fixes the group size so that every rank's
 // load is issued before the first is used; kG == 0 reads group_size at run time.
-template <int SB, int kG, bool kRecip>
+template <int SB, int kG, bool kRecip, bool H>
 __global__ __launch_bounds__(kShareBlock) void local_share_tiles_kernel(
     ShareRanks ranks, int32_t group_size, int64_t offset, int64_t shard_numel, int64_t valid_numel,
     float divisor, float recip, int32_t vec_ok, float* __restrict__ out, double* __restrict__ tile_sums) {
@@ -387,14 +396,14 @@ __global__ __launch_bounds__(kShareBlock) void local_share_tiles_kernel(
         if constexpr (kG > 0) {
             f32x4 x[kG];
 #pragma unroll
-            for (int q = 0; q < kG; ++q) x[q] = share_load4<SB>(ranks.g[q] + (offset + e) * SB);
+            for (int q = 0; q < kG; ++q) x[q] = share_load4<SB, H>(ranks.g[q] + (offset + e) * SB);
             sum = share_div<kRecip>(x[0], divisor, recip);
 #pragma unroll
             for (int q = 1; q < kG; ++q) sum = sum + share_div<kRecip>(x[q], divisor, recip);
         } else {
-            sum = share_div<kRecip>(share_load4<SB>(ranks.g[0] + (offset + e) * SB), divisor, recip);
+            sum = share_div<kRecip>(share_load4<SB, H>(ranks.g[0] + (offset + e) * SB), divisor, recip);
             for (int32_t q = 1; q < group_size; ++q) {
-                sum = sum + share_div<kRecip>(share_load4<SB>(ranks.g[q] + (offset + e) * SB), divisor, recip);
+                sum = sum + share_div<kRecip>(share_load4<SB, H>(ranks.g[q] + (offset + e) * SB), divisor, recip);
             }
         }
         st4_nt(out + e, sum);
@@ -409,9 +418,9 @@ __global__ __launch_bounds__(kShareBlock) void local_share_tiles_kernel(
         for (int64_t e = base + threadIdx.x; e < end; e += kShareBlock) {
             float v = 0.0f;
             if (e < valid_numel) {
-                v = share_div1<kRecip>(share_load1<SB>(ranks.g[0] + (offset + e) * SB), divisor, recip);
+                v = share_div1<kRecip>(share_load1<SB, H>(ranks.g[0] + (offset + e) * SB), divisor, recip);
                 for (int32_t q = 1; q < group_size; ++q) {
-                    v = v + share_div1<kRecip>(share_load1<SB>(ranks.g[q] + (offset + e) * SB), divisor, recip);
+                    v = v + share_div1<kRecip>(share_load1<SB, H>(ranks.g[q] + (offset + e) * SB), divisor, recip);
                 }
             }
             out[e] = v;
@@ -800,8 +809,8 @@ int32_t hbt_grad_local_share_sqnorm(const void* const* rank_grads, int32_t group
                   group_size, rank, static_cast<long long>(shard_numel), static_cast<long long>(valid_numel));
         return HBT_ERR_INVALID_ARGUMENT;
     }
-    if (in_dtype != HBT_DTYPE_F32 && in_dtype != HBT_DTYPE_BF16) {
-        set_error("hbt_grad_local_share_sqnorm: input dtype %d is not F32 or BF16", in_dtype);
+    if (in_dtype != HBT_DTYPE_F32 && in_dtype != HBT_DTYPE_BF16 && in_dtype != HBT_DTYPE_F16) {
+        set_error("hbt_grad_local_share_sqnorm: input dtype %d is not F32, BF16 or F16", in_dtype);
         return HBT_ERR_INVALID_ARGUMENT;
     }
     ShareRanks ranks{};
@@ -832,23 +841,25 @@ int32_t hbt_grad_local_share_sqnorm(const void* const* rank_grads, int32_t group
     const float recip = exact_reciprocal(divisor);
     const bool recip_exact = recip != 0.0f;
     const dim3 grid(static_cast<unsigned>(tiles));
-#define HBT_TILES(SBYTES, G, R)                                                                 \
-    local_share_tiles_kernel<SBYTES, G, R><<<grid, kShareBlock, 0, st>>>(                         \
+#define HBT_TILES(SBYTES, G, R, H)                                                              \
+    local_share_tiles_kernel<SBYTES, G, R, H><<<grid, kShareBlock, 0, st>>>(                      \
         ranks, group_size, offset, shard_numel, valid_numel, divisor, recip, vec_ok, out, tile_scratch)
-#define HBT_TILES_G(SBYTES, R)                            \
-    do {                                                  \
-        switch (group_size) {                             \
-            case 1: HBT_TILES(SBYTES, 1, R); break;       \
-            case 2: HBT_TILES(SBYTES, 2, R); break;       \
-            case 4: HBT_TILES(SBYTES, 4, R); break;       \
-            case 8: HBT_TILES(SBYTES, 8, R); break;       \
-            default: HBT_TILES(SBYTES, 0, R); break;      \
-        }                                                 \
+#define HBT_TILES_G(SBYTES, R, H)                            \
+    do {                                                     \
+        switch (group_size) {                                \
+            case 1: HBT_TILES(SBYTES, 1, R, H); break;       \
+            case 2: HBT_TILES(SBYTES, 2, R, H); break;       \
+            case 4: HBT_TILES(SBYTES, 4, R, H); break;       \
+            case 8: HBT_TILES(SBYTES, 8, R, H); break;       \
+            default: HBT_TILES(SBYTES, 0, R, H); break;      \
+        }                                                    \
     } while (0)
     if (in_dtype == HBT_DTYPE_F32) {
-        if (recip_exact) HBT_TILES_G(4, true); else HBT_TILES_G(4, false);
+        if (recip_exact) HBT_TILES_G(4, true, false); else HBT_TILES_G(4, false, false);
+    } else if (in_dtype == HBT_DTYPE_BF16) {
+        if (recip_exact) HBT_TILES_G(2, true, false); else HBT_TILES_G(2, false, false);
     } else {
-        if (recip_exact) HBT_TILES_G(2, true); else HBT_TILES_G(2, false);
+        if (recip_exact) HBT_TILES_G(2, true, true); else HBT_TILES_G(2, false, true);
     }
 #undef HBT_TILES_G
 #undef HBT_TILES

@@ -27,6 +27,7 @@ from .errors import NativeKernelError, UnsupportedFeatureError, format_error
 __all__ = [
     "ABI_VERSION",
     "COPY_ALIGNED",
+    "COPY_CONVERSIONS",
     "COPY_OP_COPY",
     "COPY_OP_DIVIDE",
     "SGD_FIRST_STEP",
@@ -63,6 +64,12 @@ COPY_OP_COPY = 0
 COPY_OP_DIVIDE = 1
 COPY_ALIGNED = 1
 _CODE_BYTES = {DTYPE_F32: 4, DTYPE_BF16: 2, DTYPE_F16: 2, DTYPE_F64: 8}
+
+#: Dtype pairs ``hbt_copy_intervals`` converts between (same-dtype copies are bit copies).
+COPY_CONVERSIONS = frozenset({
+    (torch.float32, torch.bfloat16), (torch.bfloat16, torch.float32),
+    (torch.float32, torch.float16), (torch.float16, torch.float32),
+})
 SGD_MOMENTUM = 1
 SGD_FIRST_STEP = 2
 SGD_NESTEROV = 4

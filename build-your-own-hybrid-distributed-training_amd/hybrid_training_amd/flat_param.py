@@ -101,12 +101,11 @@ class FlatParameter(nn.Parameter):
 
 
 def _check_cast(src: torch.dtype, dst: torch.dtype, operation: str) -> None:
-    supported = {torch.float32, torch.bfloat16}
-    if src != dst and not (src in supported and dst in supported):
+    if src != dst and (src, dst) not in _native.COPY_CONVERSIONS:
         raise UnsupportedFeatureError(
             format_error(
                 operation,
-                "the copy kernel converts only between float32 and bfloat16",
+                "the copy kernel converts only between float32 and bfloat16 or float16",
                 observed=f"{src} -> {dst}",
             )
         )
@@ -454,13 +453,14 @@ class FlatParamHandle:
             )
         for g in grads:
             _native.require_device_tensor(g, "fsdp.reduce_scatter_gradient")
-            if g.numel() != self._padded_numel or g.dtype not in (torch.float32, torch.bfloat16) \
+            if g.numel() != self._padded_numel \
+                    or g.dtype not in (torch.float32, torch.bfloat16, torch.float16) \
                     or g.dtype != grads[0].dtype or not g.is_contiguous():
                 raise ShardingError(
                     format_error(
                         "fsdp.reduce_scatter_gradient",
                         "each gradient must be a dense padded full buffer of one float dtype",
-                        expected=f"{self._padded_numel} float32/bfloat16 elements",
+                        expected=f"{self._padded_numel} float32/bfloat16/float16 elements",
                         observed=f"{g.numel()} {g.dtype}",
                     )
                 )

@@ -174,7 +174,7 @@ class _PlanSet:
         self.plans: dict[torch.dtype, _native.CopyPlan] = {}
 
     def add(self, src: torch.Tensor, src_offset: int, dst: torch.Tensor, dst_offset: int, n: int) -> None:
-        if src.dtype != dst.dtype and {src.dtype, dst.dtype} - {torch.float32, torch.bfloat16}:
+        if src.dtype != dst.dtype and (src.dtype, dst.dtype) not in _native.COPY_CONVERSIONS:
             raise CheckpointError(
                 format_error("reshard.read_tensor_range", "unsupported dtype conversion",
                              observed=f"{src.dtype} -> {dst.dtype}")
@@ -195,7 +195,7 @@ def read_tensor_range(
 ) -> torch.Tensor:
     """Elements ``wanted`` of a stored tensor as a new 1-D device tensor (one launch).
 
-    ``dtype`` casts the result (float32 <-> bfloat16); by default the result has the
+    ``dtype`` casts the result (float32 <-> bfloat16 or float16); by default the result has the
     first intersecting shard's dtype.
     """
     if wanted.length == 0:

@@ -31,7 +31,7 @@ extern "C" {
 /* ---- element types ----------------------------------------------------------- */
 #define HBT_DTYPE_F32 0
 #define HBT_DTYPE_BF16 1
-#define HBT_DTYPE_F16 2 /* byte copies only */
+#define HBT_DTYPE_F16 2 /* copies, F32 <-> F16 casts and division; local-share input */
 #define HBT_DTYPE_F64 3 /* byte copies only */
 
 /* ---- per-call limits ---------------------------------------------------------- */
@@ -166,16 +166,19 @@ int32_t hbt_grad_norm_finalize(const double* partials, int64_t count, double max
  * travels as F32 pairs).  All records share src_dtype/dst_dtype and op:
  *   HBT_COPY_OP_COPY    dst = src               (same dtype: byte copy; F32->BF16
  *                                                rounds to nearest even, NaN -> 0x7FC0;
- *                                                BF16->F32 widens exactly)
- *   HBT_COPY_OP_DIVIDE  dst = src / divisor     (true fp32 division, in fp32 for F32 and
- *                                                BF16 data, result rounded to dst_dtype)
+ *                                                F32->F16 rounds to nearest even, overflows
+ *                                                to inf, keeps subnormals, NaN -> sign|0x7E00;
+ *                                                BF16->F32 and F16->F32 widen exactly)
+ *   HBT_COPY_OP_DIVIDE  dst = src / divisor     (true fp32 division, in fp32 for F32, BF16
+ *                                                and F16 data, result rounded to dst_dtype)
+ * BF16 <-> F16 is not converted.
  * Source and destination ranges of one call must not overlap.  Addresses need no
  * particular alignment.
  *
  * flags: 0, or HBT_COPY_ALIGNED when the caller certifies that every record's
  * dst_address is a multiple of 16 and every nonzero src_address a multiple of the
  * source width of one 16-byte destination-or-source unit, 16 * S / max(S, D) bytes for
- * S- and D-byte elements (16 for F32 -> F32, 8 for BF16 -> F32, 16 for the others).
+ * S- and D-byte elements (16 for F32 -> F32, 8 for BF16 or F16 -> F32, 16 for the others).
  * Aligned plans run a kernel without the head and shifted-load paths (measured 6.6
  * against 5.7 TB/s on a 298-record fp32 unpack).  The results are the same bits
  * either way.
@@ -196,7 +199,7 @@ int32_t hbt_copy_intervals(const int64_t* table, int64_t count, int64_t total_ch
  *   _zero_padding_region (parallel/fsdp.py:771-781).
  * `rank_grads` is a HOST array of `group_size` (at most HBT_MAX_LOCAL_RANKS) device
  * addresses, each the padded full gradient (group_size * shard_numel elements,
- * in_dtype F32 or BF16) of one rank, all resident on this device.  Writes the fp32
+ * in_dtype F32, BF16 or F16) of one rank, all resident on this device.  Writes the fp32
  * shard of `rank`:
  *   out[i] = sum over q = 0..group_size-1, in that order, of
  *            fp32(rank_grads[q][rank*shard_numel + i]) / divisor

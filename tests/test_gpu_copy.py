@@ -28,6 +28,39 @@ def _as_f32(bits16: np.ndarray) -> np.ndarray:
     return (bits16.astype(np.uint32) << 16).view(np.float32)
 
 
+def _to_f32(bits: np.ndarray, dtype: torch.dtype) -> np.ndarray:
+    """fp32 values of element bit patterns (widening is exact for every dtype here)."""
+    if dtype == torch.float32:
+        return bits.view(np.float32)
+    if dtype == torch.float16:
+        return bits.view(np.float16).astype(np.float32)
+    return _as_f32(bits)
+
+
+def _from_f32(vals: np.ndarray, dtype: torch.dtype) -> np.ndarray:
+    """Bit patterns of fp32 values rounded to ``dtype`` (round to nearest even)."""
+    if dtype == torch.float32:
+        return vals.view(np.int32)
+    if dtype == torch.float16:
+        with np.errstate(over="ignore"):
+            return vals.astype(np.float16).view(np.int16)
+    return oracle.f32_to_bf16(vals).view(np.int16)
+
+
+def _converter(sdt, ddt, op, divisor):
+    """The expected element map of one plan, on bit patterns."""
+    if sdt == ddt and op == _native.COPY_OP_COPY:
+        return lambda x: x
+
+    def convert(x):
+        vals = _to_f32(x, sdt)
+        if op == _native.COPY_OP_DIVIDE:
+            vals = (vals / np.float32(divisor)).astype(np.float32)
+        return _from_f32(vals, ddt)
+
+    return convert
+
+
 def _random_intervals(rng, n_src, n_dst, count, max_len):
     """Non-overlapping destination intervals (random order), random source offsets."""
     cuts = np.sort(rng.choice(np.arange(1, n_dst), size=2 * count, replace=False))
@@ -60,6 +93,11 @@ CASES = [
     (torch.bfloat16, torch.bfloat16, _native.COPY_OP_DIVIDE),
     (torch.bfloat16, torch.float32, _native.COPY_OP_DIVIDE),
     (torch.float32, torch.bfloat16, _native.COPY_OP_DIVIDE),
+    (torch.float32, torch.float16, _native.COPY_OP_COPY),
+    (torch.float16, torch.float32, _native.COPY_OP_COPY),
+    (torch.float16, torch.float16, _native.COPY_OP_DIVIDE),
+    (torch.float32, torch.float16, _native.COPY_OP_DIVIDE),
+    (torch.float16, torch.float32, _native.COPY_OP_DIVIDE),
 ]
 
 
@@ -78,15 +116,7 @@ def test_random_interval_plans(device, sdt, ddt, op, count, max_len):
         plan.add(src, s0, dst, d0, n)
     plan.run(src_dtype=sdt, dst_dtype=ddt, op=op, divisor=divisor)
     sbits = _bits(src)
-    if sdt == ddt and op == _native.COPY_OP_COPY:
-        convert = lambda x: x  # noqa: E731
-    else:
-        def convert(x):
-            vals = x.view(np.float32) if sdt == torch.float32 else _as_f32(x)
-            if op == _native.COPY_OP_DIVIDE:
-                vals = (vals / np.float32(divisor)).astype(np.float32)
-            return vals.view(np.int32) if ddt == torch.float32 else oracle.f32_to_bf16(vals).view(np.int16)
-    expect = _expected(sbits, dst_init, rows, convert)
+    expect = _expected(sbits, dst_init, rows, _converter(sdt, ddt, op, divisor))
     assert np.array_equal(_bits(dst), expect)
 
 
@@ -211,16 +241,45 @@ def test_aligned_kernel_matches_general_kernel(device, sdt, ddt, op, divisor):
                                         _native.stream_of(device))
         _native.check(status, "test.copy_intervals")
         outs.append(_bits(dst))
-    if sdt == ddt and op == _native.COPY_OP_COPY:
-        convert = lambda x: x  # noqa: E731
-    else:
-        def convert(x):
-            vals = x.view(np.float32) if sdt == torch.float32 else _as_f32(x)
-            if op == _native.COPY_OP_DIVIDE:
-                vals = (vals / np.float32(divisor)).astype(np.float32)
-            return vals.view(np.int32) if ddt == torch.float32 else oracle.f32_to_bf16(vals).view(np.int16)
+    convert = _converter(sdt, ddt, op, divisor)
     expect = _bits(torch.full((n_dst,), 5.0, dtype=torch.float32).to(ddt))
     for s0, d0, n in rows:
         expect[d0 : d0 + n] = 0 if s0 < 0 else convert(sbits[s0 : s0 + n])
     assert np.array_equal(outs[0], expect)
     assert np.array_equal(outs[1], expect)
+
+
+def test_float16_specials_match_torch(device):
+    """fp32 -> fp16 narrowing and fp16 -> fp32 widening against torch's CPU ``.to``:
+    ties to even, the overflow threshold (65520 rounds to inf, 65519 to 65504),
+    subnormal results down to 2^-24 and below, and NaN staying NaN."""
+    vals = np.array([0.0, -0.0, 1.0, 65504.0, 65519.0, 65520.0, -70000.0, 3.4e38, np.inf, -np.inf, np.nan,
+                     2.0**-14, 2.0**-24, 2.0**-25, 1.5 * 2.0**-25, 2.0**-26, -3e-8, 1e-40,
+                     1.0 + 2.0**-11, 1.0 + 3 * 2.0**-11, 2049.0, 2051.0, 0.1, -1e-5], np.float32)
+    src = torch.from_numpy(vals).to(device)
+    out = torch.empty(vals.size, dtype=torch.float16, device=device)
+    plan = _native.CopyPlan(device)
+    plan.add(src, 0, out, 0, vals.size)
+    plan.run(src_dtype=torch.float32, dst_dtype=torch.float16)
+    expect = torch.from_numpy(vals).to(torch.float16)
+    got = out.cpu()
+    nan = torch.isnan(expect)
+    assert torch.equal(torch.isnan(got), nan)
+    assert torch.equal(got[~nan].view(torch.int16), expect[~nan].view(torch.int16))
+    # every finite fp16 bit pattern widens exactly
+    every = torch.arange(-(2**15), 2**15, dtype=torch.int32).to(torch.int16).view(torch.float16)
+    finite = every[torch.isfinite(every)].to(device)
+    wide = torch.empty(finite.numel(), dtype=torch.float32, device=device)
+    plan = _native.CopyPlan(device)
+    plan.add(finite, 0, wide, 0, finite.numel())
+    plan.run(src_dtype=torch.float16, dst_dtype=torch.float32)
+    assert torch.equal(wide.cpu().view(torch.int32), finite.cpu().to(torch.float32).view(torch.int32))
+
+
+def test_bf16_float16_conversion_is_refused(device):
+    a = torch.zeros(8, dtype=torch.bfloat16, device=device)
+    b = torch.zeros(8, dtype=torch.float16, device=device)
+    plan = _native.CopyPlan(device)
+    plan.add(a, 0, b, 0, 8)
+    with pytest.raises(Exception, match="convert"):
+        plan.run(src_dtype=torch.bfloat16, dst_dtype=torch.float16)

@@ -2,7 +2,7 @@
 
 * ``hbt_grad_local_share`` and ``hbt_grad_local_share_sqnorm`` (the FSDP gradient
   local share, ``parallel/fsdp.py:704-781``, the latter with the norm partials of its
-  output): bitwise against the oracle for G in {1, 3, 8}, fp32 and bf16 inputs,
+  output): bitwise against the oracle for G in {1, 3, 8}, fp32, bf16 and fp16 inputs,
   shards with full vector tiles, a partial tile at the valid/padding boundary, whole
   tiles of padding, and misaligned input and output addresses (scalar path); the
   partials sum to the oracle's squared norm within 1e-12.
@@ -31,7 +31,7 @@ def _bits(t: torch.Tensor) -> np.ndarray:
     return t.view({2: torch.int16, 4: torch.int32}[t.element_size()]).numpy().copy()
 
 
-@pytest.mark.parametrize("in_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("in_dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("group", [1, 3, 8])
 @pytest.mark.parametrize("misaligned", [False, True])
 def test_local_share_tiles(device, in_dtype, group, misaligned):

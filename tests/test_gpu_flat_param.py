@@ -81,7 +81,7 @@ def test_norm_weights_and_padding_runs(device):
 
 
 @pytest.mark.parametrize("group", [1, 2, 3, 4])
-@pytest.mark.parametrize("in_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("in_dtype", [torch.float32, torch.bfloat16, torch.float16])
 def test_gradient_local_share_matches_oracle(device, group, in_dtype):
     _, _, handles = _handles(MLP_1857_REFERENCE, group, device)
     padded = handles[0].padded_numel
@@ -135,6 +135,36 @@ def test_mixed_precision_master_cast_and_gather(device):
     assert full.dtype == torch.bfloat16 and full.numel() == 1858
     expect = oracle.f32_to_bf16(np.concatenate([oracle.pack_shard(host, 2, r) for r in range(2)]))
     assert np.array_equal(full.view(torch.int16).cpu().numpy().view(np.uint16), expect)
+
+
+def test_float16_compute_master_cast_gather_and_local_share(device):
+    """fp16 compute (the only precision the reference pairs with loss scaling): fp16
+    parameters widen exactly into the fp32 master shards, ``gather_full`` narrows the
+    masters to fp16 as torch's ``.to(torch.float16)`` does (``fsdp.py:578-579``), and the
+    fp16 full gradients widen exactly before the AVG divide (``fsdp.py:734-735``)."""
+    named = _params(MLP_1857_REFERENCE, device, dtype=torch.float16)
+    mp = MixedPrecisionConfig(enabled=True, param_dtype="float16", reduce_dtype="float32", master_dtype="float32")
+    handles = [FlatParamHandle(named, None, GroupHandle.local_view("shard", 2, r), FSDPConfig(), mp, device,
+                               keep_originals=True) for r in range(2)]
+    host = [p.detach().float().cpu().numpy() for _, p in named]
+    for rank, h in enumerate(handles):
+        assert h.flat_param.dtype == torch.float32
+        assert np.array_equal(h.flat_param.detach().cpu().numpy(), oracle.pack_shard(host, 2, rank))
+    # masters that need rounding: scale them off the fp16 grid
+    for h in handles:
+        h.flat_param.data.mul_(1.0 + 2.0**-13).add_(3e-6)
+    full = handles[0].gather_full([h.flat_param for h in handles])
+    assert full.dtype == torch.float16 and full.numel() == 1858
+    expect = torch.cat([h.flat_param.detach().cpu() for h in handles]).to(torch.float16)
+    assert torch.equal(full.cpu().view(torch.int16), expect.view(torch.int16))
+    gen = torch.Generator(device=device).manual_seed(16)
+    grads = [(torch.randn(1858, device=device, generator=gen) * 1e-2).to(torch.float16) for _ in range(2)]
+    host_g = [g.float().cpu().numpy() for g in grads]
+    for rank, h in enumerate(handles):
+        out = h.reduce_scatter_gradient(grads[rank], peer_grads=grads)
+        valid = max(0, min(h.shard_numel, 1857 - rank * h.shard_numel))
+        expect_g = oracle.local_share(host_g, rank, h.shard_numel, valid, 2.0)
+        assert np.array_equal(out.cpu().numpy().view(np.int32), expect_g.view(np.int32))
 
 
 def test_detaching_frees_originals_and_binds_views(device):
