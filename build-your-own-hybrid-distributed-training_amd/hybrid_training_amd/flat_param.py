@@ -500,6 +500,26 @@ class FlatParamHandle:
         self._reduction_count += 1
         return out
 
+    def set_accumulate_without_reduction(self, value: bool) -> None:
+        """``no_sync`` accumulation of unsharded gradients (``fsdp.py:791-797``).
+
+        Not built: the accumulate-then-reduce path has no kernel here, so enabling it
+        raises rather than silently reducing every micro-batch.
+        """
+        if value:
+            raise UnsupportedFeatureError(
+                format_error(
+                    "fsdp.set_accumulate_without_reduction",
+                    "no_sync gradient accumulation is not part of this build",
+                    resolution="reduce every micro-batch's gradient (no no_sync block)",
+                )
+            )
+
+    @property
+    def has_pending_accumulation(self) -> bool:
+        """Whether unreduced gradients are held from a ``no_sync`` block (never here)."""
+        return False
+
     def zero_padding_region(self, shard_grad: torch.Tensor) -> None:
         """Zero the padding part of a gradient shard (``fsdp.py:771-781``)."""
         padding = intersect_ranges(self.local_shard_range(), ShardRange(self._total_numel, self._padding))

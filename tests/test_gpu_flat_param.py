@@ -103,6 +103,11 @@ def test_local_share_needs_every_rank(device):
         handles[0].reduce_scatter_gradient(torch.zeros(handles[0].padded_numel, device=device))
     with pytest.raises(UnsupportedFeatureError, match="needs every rank's shard"):
         handles[0].full_tensors()
+    # no_sync accumulation is refused up front; turning it off is a no-op
+    handles[0].set_accumulate_without_reduction(False)
+    assert handles[0].has_pending_accumulation is False
+    with pytest.raises(UnsupportedFeatureError, match="no_sync"):
+        handles[0].set_accumulate_without_reduction(True)
 
 
 def test_load_local_pieces_round_trip(device):
