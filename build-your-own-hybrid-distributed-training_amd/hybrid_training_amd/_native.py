@@ -304,6 +304,29 @@ def _copy_chunk(lib: ctypes.CDLL, src_code: int, dst_code: int) -> int:
     return chunk
 
 
+def plan_table(rows: Sequence[tuple[int, int, int]], chunk: int, scale: int = 1) -> tuple[list[int], int]:
+    """The flat ``{src, dst, numel, first_chunk}`` records of a plan and its chunk count.
+
+    ``scale`` multiplies every numel (2 when 8-byte elements travel as dword pairs).
+    """
+    flat: list[int] = []
+    first = 0
+    for src_addr, dst_addr, n in rows:
+        n_units = n * scale
+        flat.extend((src_addr, dst_addr, n_units, first))
+        first += -(-n_units // chunk)
+    return flat, first
+
+
+def plan_is_aligned(rows: Sequence[tuple[int, int, int]], src_code: int, dst_code: int) -> bool:
+    """Whether a plan qualifies for ``HBT_COPY_ALIGNED``: every destination on a 16-byte
+    boundary and every source (0 for a zero fill) on the source width of one 16-byte
+    unit, ``16 * S / max(S, D)`` bytes for S- and D-byte elements."""
+    src_bytes, dst_bytes = _CODE_BYTES[src_code], _CODE_BYTES[dst_code]
+    src_align = 16 * src_bytes // max(src_bytes, dst_bytes)
+    return all(dst_addr % 16 == 0 and src_addr % src_align == 0 for src_addr, dst_addr, _ in rows)
+
+
 def _prepared_plan(
     device: torch.device, rows: tuple[tuple[int, int, int], ...], src_code: int, dst_code: int, scale: int
 ) -> tuple[torch.Tensor, int, bool]:
@@ -316,19 +339,8 @@ def _prepared_plan(
         _TABLE_CACHE.move_to_end(key)
         return entry
     chunk = _copy_chunk(library(), src_code, dst_code)
-    # The aligned kernel needs every destination on a 16-byte boundary and every source
-    # on the source width of one 16-byte unit.
-    src_bytes, dst_bytes = _CODE_BYTES[src_code], _CODE_BYTES[dst_code]
-    src_align = 16 * src_bytes // max(src_bytes, dst_bytes)
-    aligned = True
-    flat: list[int] = []
-    first = 0
-    for src_addr, dst_addr, n in rows:
-        n_units = n * scale
-        flat.extend((src_addr, dst_addr, n_units, first))
-        first += -(-n_units // chunk)
-        if dst_addr % 16 or src_addr % src_align:
-            aligned = False
+    flat, first = plan_table(rows, chunk, scale)
+    aligned = plan_is_aligned(rows, src_code, dst_code)
     host = torch.tensor(flat, dtype=torch.int64).pin_memory()
     with torch.cuda.device(device):
         table = host.to(device, non_blocking=True)

@@ -152,3 +152,24 @@ def test_norm_contribution_from_runs_matches_the_vector_form():
     q.gradient_norm_scale_vector = torch.tensor([2.0] * 7 + [0.0] * 3)
     (d,) = build_gradient_norm_contributions([q], world_size=4)
     assert d.runs == c.runs and torch.equal(d.scale_vector(), c.scale_vector())
+
+
+def test_copy_plan_table_and_alignment_class():
+    """The copy plan's records, chunk prefix sums and the aligned-kernel test (host only)."""
+    from hybrid_training_amd import _native
+
+    rows = [(4096, 8192, 600), (0, 65536, 256), (12288, 99328, 1)]
+    flat, total = _native.plan_table(rows, 256)
+    assert flat == [4096, 8192, 600, 0, 0, 65536, 256, 3, 12288, 99328, 1, 4]
+    assert total == 5
+    flat2, total2 = _native.plan_table(rows[:1], 256, scale=2)  # fp64 as dword pairs
+    assert flat2 == [4096, 8192, 1200, 0] and total2 == 5
+    f32, bf16, f16 = _native.DTYPE_F32, _native.DTYPE_BF16, _native.DTYPE_F16
+    assert _native.plan_is_aligned(rows, f32, f32)
+    assert not _native.plan_is_aligned([(4100, 8192, 4)], f32, f32)   # source off 16 B
+    assert not _native.plan_is_aligned([(4096, 8200, 4)], f32, f32)   # destination off 16 B
+    assert _native.plan_is_aligned([(4104, 8192, 4)], bf16, f32)      # 8-byte source units
+    assert _native.plan_is_aligned([(4104, 8192, 4)], f16, f32)
+    assert not _native.plan_is_aligned([(4100, 8192, 4)], bf16, f32)
+    assert not _native.plan_is_aligned([(4104, 8192, 4)], f32, bf16)  # 16-byte source units
+    assert _native.plan_is_aligned([(0, 8192, 4)], bf16, bf16)         # zero fill
