@@ -61,7 +61,7 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument(
         "--workload",
         choices=["adamw", "buckets", "reshard", "scaler", "fsdp", "inplace_clip", "torch_adamw", "sgd", "offload",
-                 "checkpoint"],
+                 "checkpoint", "copy_ceiling"],
         default="adamw",
         help="adamw (default): the Llama-3-8B W=8 shard step above; buckets: GPT-2-small DDP bucket "
         "pack + AVG divide at W=8; reshard: Llama-3-8B bf16 flat shards W=4 -> W=8 and W=2; scaler: "
@@ -69,7 +69,8 @@ def parse_args() -> argparse.Namespace:
         "Llama-3-8B FSDP pack, unpack and gradient local share at W=8; inplace_clip: the headline step with "
         "the reference's in-place clip; torch_adamw: the headline step with stock torch GPU kernels; sgd: "
         "the headline shard with SGD (momentum 0.9); offload: the headline step with AdamW state in pinned "
-        "host memory; checkpoint: Llama-3-8B bf16 saved by 4 FSDP ranks and loaded back at W=8",
+        "host memory; checkpoint: Llama-3-8B bf16 saved by 4 FSDP ranks and loaded back at W=8; "
+        "copy_ceiling: torch's device-to-device copy against the interval copy on 1 and 16 GiB",
     )
     ap.add_argument(
         "--calibrate-copy",
@@ -800,9 +801,31 @@ def bench_torch_adamw(steps: int, warmup: int) -> int:
     return 0
 
 
+def bench_copy_ceiling(steps: int, warmup: int) -> int:
+    """The copy ceilings: torch's device-to-device ``copy_`` (a hipMemcpy blit) against the
+    library's interval copy, one fp32 record of 1 GiB and of 16 GiB (8 B per element moved)."""
+    import torch
+
+    from hybrid_training_amd import _native
+
+    device = torch.device("cuda", 0)
+    big = 1 << 32
+    src = torch.ones(big, dtype=torch.float32, device=device)
+    dst = torch.empty_like(src)
+    for n in (1 << 28, big):
+        plan = _native.CopyPlan(device)
+        plan.add(src, 0, dst, 0, n)
+        ms_lib = _time_events(lambda: plan.run(src_dtype=torch.float32, dst_dtype=torch.float32), steps, warmup)
+        ms_torch = _time_events(lambda: dst[:n].copy_(src[:n]), steps, warmup)
+        for name, ms in (("hbt_copy_intervals (aligned kernel)", ms_lib), ("torch copy_ (hipMemcpy D2D)", ms_torch)):
+            _emit(f"fp32 copy ceiling, {name}: GB/s", "GB/s", 8 * n / (ms * 1e-3) / 1e9, ms, steps, warmup, "f32",
+                  f"one {4 * n / 2**30:.0f} GiB fp32 buffer copied to another", 8 * n, {"elements": n})
+    return 0
+
+
 SECONDARY = {"buckets": bench_buckets, "reshard": bench_reshard, "scaler": bench_scaler, "fsdp": bench_fsdp,
              "inplace_clip": bench_inplace_clip, "torch_adamw": bench_torch_adamw, "sgd": bench_sgd,
-             "offload": bench_offload, "checkpoint": bench_checkpoint}
+             "offload": bench_offload, "checkpoint": bench_checkpoint, "copy_ceiling": bench_copy_ceiling}
 
 
 if __name__ == "__main__":
