@@ -134,6 +134,8 @@ EXPORTED_SYMBOLS: dict[str, tuple[object, tuple[object, ...]]] = {
 }
 
 _LOCK = threading.Lock()
+# Guards the copy-table cache for callers that run copy plans from several host threads.
+_TABLE_LOCK = threading.Lock()
 _LIB: ctypes.CDLL | None = None
 
 # Device copies of interval tables, keyed by their exact content.  A table is a pure
@@ -334,10 +336,11 @@ def _prepared_plan(
     stream.  The table is uploaded on that stream, so later launches on it see it."""
     stream = stream_of(device)
     key = (device, stream, src_code, dst_code, scale, rows)
-    entry = _TABLE_CACHE.get(key)
-    if entry is not None:
-        _TABLE_CACHE.move_to_end(key)
-        return entry
+    with _TABLE_LOCK:
+        entry = _TABLE_CACHE.get(key)
+        if entry is not None:
+            _TABLE_CACHE.move_to_end(key)
+            return entry
     chunk = _copy_chunk(library(), src_code, dst_code)
     flat, first = plan_table(rows, chunk, scale)
     aligned = plan_is_aligned(rows, src_code, dst_code)
@@ -345,9 +348,10 @@ def _prepared_plan(
     with torch.cuda.device(device):
         table = host.to(device, non_blocking=True)
     entry = (table, first, aligned)
-    _TABLE_CACHE[key] = entry
-    if len(_TABLE_CACHE) > _TABLE_CACHE_SIZE:
-        _TABLE_CACHE.popitem(last=False)
+    with _TABLE_LOCK:
+        _TABLE_CACHE[key] = entry
+        if len(_TABLE_CACHE) > _TABLE_CACHE_SIZE:
+            _TABLE_CACHE.popitem(last=False)
     return entry
 
 
