@@ -22,6 +22,7 @@ issued.
 
 from __future__ import annotations
 
+import logging
 from collections.abc import Iterable, Sequence
 from dataclasses import dataclass
 from typing import Any
@@ -35,6 +36,8 @@ from .groups import GroupHandle
 from .optim import PENDING_UNSCALE_ATTR, gradient_norm_pass
 
 __all__ = ["GradScaler", "GradScalerState"]
+
+_LOGGER = logging.getLogger(__name__)
 
 
 @dataclass
@@ -199,6 +202,12 @@ class GradScaler:
         self._skipped_on_last_step = found
         if found:
             self._state.skipped_steps += 1
+            # The reference logs every skipped step (grad_scaler.py:229-236).
+            _LOGGER.warning(
+                "non-finite gradient detected; skipping optimizer step %d and reducing the loss scale from %.1f",
+                self._state.total_steps,
+                self._state.scale,
+            )
             return False
         optimizer.step()
         return True

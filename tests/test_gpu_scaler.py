@@ -46,7 +46,7 @@ def _bf16_bits(t):
     return t.detach().cpu().view(torch.int16).numpy().view(np.uint16)
 
 
-def test_overflow_skip_then_clean_step(device):
+def test_overflow_skip_then_clean_step(device, caplog):
     n = 1 << 22
     gen = torch.Generator(device=device).manual_seed(5)
     param = torch.nn.Parameter(torch.randn(n, device=device, generator=gen) * 0.02)
@@ -57,8 +57,10 @@ def test_overflow_skip_then_clean_step(device):
     g[bad[: bad.numel() // 2]] = float("inf")
     g[bad[bad.numel() // 2 :]] = float("nan")
     param.grad = g
-    norm, stepped = _engine_step(opt, scaler, param)
+    with caplog.at_level("WARNING"):
+        norm, stepped = _engine_step(opt, scaler, param)
     assert not stepped and not torch.isfinite(norm)
+    assert "skipping optimizer step 1" in caplog.text  # logged as the reference does
     assert torch.equal(param.detach(), p0)
     assert scaler.scale_value == SCALE / 2 and scaler.state.skipped_steps == 1
     assert opt.inner.state[param] == {} or float(opt.inner.state[param]["step"]) == 0.0
