@@ -116,3 +116,43 @@ def test_scale_inplace_tiles(device, dtype):
         assert torch.equal(torch.isnan(got), nan)
         assert np.array_equal(_bits(got)[~nan.numpy()], _bits(expect)[~nan.numpy()])
     assert np.array_equal(_bits(base[:1]), lead)  # the element before the first tensor is untouched
+
+
+def test_local_share_full_size_rank7_of_llama3_8b_w8(device):
+    """Rank 7 of Llama-3-8B at W=8 through ``hbt_grad_local_share_sqnorm``: its slice starts
+    7,026,478,592 elements into each rank's padded bf16 gradient, far past 2^31, so every
+    offset must be 64-bit.  2^20 sampled outputs and both ends of the shard are checked
+    bitwise against numpy on the same eight bf16 values in rank order; the partials'
+    sum against torch's fp64 sum of squares of the whole output."""
+    lib = _native.library()
+    group, shard = 8, 1_003_782_656
+    rank = group - 1
+    offset = rank * shard
+    gen = torch.Generator(device=device).manual_seed(77)
+    grads = []
+    for _ in range(group):
+        g = torch.empty(group * shard, dtype=torch.bfloat16, device=device)  # only rank 7's slice is read
+        g[offset:].copy_(torch.randn(shard, device=device, generator=gen).mul_(1e-2))
+        grads.append(g)
+    out = torch.empty(shard, dtype=torch.float32, device=device)
+    chunk = 32768
+    partials = torch.empty(-(-shard // chunk), dtype=torch.float64, device=device)
+    tile_sums = torch.empty(-(-shard // 256), dtype=torch.float64, device=device)
+    status = lib.hbt_grad_local_share_sqnorm(
+        _native.pointer_array([g.data_ptr() for g in grads]), group, rank, shard, shard,
+        _native.dtype_code(torch.bfloat16), float(group), ctypes.c_void_p(out.data_ptr()),
+        ctypes.c_void_p(partials.data_ptr()), ctypes.c_void_p(tile_sums.data_ptr()),
+        ctypes.c_void_p(_native.stream_of(device)),
+    )
+    _native.check(status, "test.local_share_full")
+    idx = torch.randint(0, shard, (1 << 20,), device=device, generator=gen)
+    idx = torch.cat([idx, torch.arange(0, 4096, device=device), torch.arange(shard - 4096, shard, device=device)])
+    vals = np.stack([g[offset:][idx].float().cpu().numpy() for g in grads])  # exact widening
+    expect = vals[0] / np.float32(group)
+    for q in range(1, group):
+        expect = (expect + vals[q] / np.float32(group)).astype(np.float32)
+    assert np.array_equal(out[idx].cpu().numpy().view(np.int32), expect.view(np.int32))
+    ref = float(out.double().pow(2).sum())
+    assert abs(float(partials.sum()) - ref) <= 1e-10 * ref
+    del grads
+    torch.cuda.empty_cache()
