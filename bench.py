@@ -51,8 +51,8 @@ def log(msg: str) -> None:
 def parse_args() -> argparse.Namespace:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--numel", type=int, default=SHARD_NUMEL, help="shard size (default: Llama-3-8B / 8)")
     ap.add_argument("--cpu-numel", type=int, default=1 << 28, help="CPU-baseline sample size")
     ap.add_argument("--cpu-steps", type=int, default=20,
