@@ -11,7 +11,7 @@
 from __future__ import annotations
 
 MLP_1857_REFERENCE = [(25, 14), (25,), (25, 25), (25,), (25, 25), (25,), (7, 25), (7,)]
-MLP_1857_BASELINE = [(32, 23), (32,), (32, 32), (32,), (1, 32), (1,)]
+MLP_23_32_32_1 = [(32, 23), (32,), (32, 32), (32,), (1, 32), (1,)]
 
 
 def gpt2_small() -> list[tuple[str, tuple[int, ...]]]:

@@ -25,7 +25,7 @@ from hybrid_training_amd import (
 )
 from hybrid_training_amd.errors import UnsupportedFeatureError
 
-from .model_shapes import MLP_1857_BASELINE, MLP_1857_REFERENCE
+from .model_shapes import MLP_23_32_32_1, MLP_1857_REFERENCE
 
 pytestmark = pytest.mark.gpu
 
@@ -47,7 +47,7 @@ def _handles(shapes, group, device, **kw):
     return named, originals, handles
 
 
-@pytest.mark.parametrize("shapes", [MLP_1857_REFERENCE, MLP_1857_BASELINE])
+@pytest.mark.parametrize("shapes", [MLP_1857_REFERENCE, MLP_23_32_32_1])
 @pytest.mark.parametrize("group", [1, 2, 3, 4])
 def test_pack_pad_shard_matches_oracle(device, shapes, group):
     named, originals, handles = _handles(shapes, group, device)
@@ -111,7 +111,7 @@ def test_local_share_needs_every_rank(device):
 
 
 def test_load_local_pieces_round_trip(device):
-    named, originals, handles = _handles(MLP_1857_BASELINE, 4, device)
+    named, originals, handles = _handles(MLP_23_32_32_1, 4, device)
     state = {name: torch.randn_like(orig) for (name, _), orig in zip(named, originals)}
     host = [state[name].cpu().numpy() for name, _ in named]
     for rank, h in enumerate(handles):

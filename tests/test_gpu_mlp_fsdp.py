@@ -1,7 +1,7 @@
 """The 1857-parameter MLP trained FSDP-style at W=2 and W=4 on one device.
 
 Mirrors the reference's FSDP equivalence test (``tests/distributed/test_fsdp.py:86-151``,
-``:425-455``) with the BASELINE MLP ``Linear(23,32)-ReLU-Linear(32,32)-ReLU-Linear(32,1)``,
+``:425-455``) with the MLP ``Linear(23,32)-ReLU-Linear(32,32)-ReLU-Linear(32,1)``,
 micro-batches of 16 rows per rank, MSE against N(0,1) targets, AdamW lr 1e-3,
 weight decay 0.01, 5 steps.  Every rank's work runs through the product: shard
 packing (``FlatParamHandle``), the gradient local share over all ranks' gradients

@@ -26,7 +26,7 @@ from hybrid_training_amd import (
 )
 from hybrid_training_amd.tensors import bytes_of, numel_of
 
-from .model_shapes import LLAMA3_8B, LLAMA3_70B_TOTAL, MLP_1857_BASELINE, MLP_1857_REFERENCE
+from .model_shapes import LLAMA3_8B, LLAMA3_70B_TOTAL, MLP_23_32_32_1, MLP_1857_REFERENCE
 
 
 def test_documented_layout_example():
@@ -101,7 +101,7 @@ def test_reshard_scenario_from_the_reference():
     assert table == [[(0, 3), (3, 1)], [(4, 2), (6, 2)], [(8, 1), (9, 3)]]
 
 
-@pytest.mark.parametrize("shapes", [MLP_1857_REFERENCE, MLP_1857_BASELINE])
+@pytest.mark.parametrize("shapes", [MLP_1857_REFERENCE, MLP_23_32_32_1])
 def test_1857_parameter_mlp_shards(shapes):
     numels = [int(torch.Size(s).numel()) for s in shapes]
     _, total = oracle.flat_layout(numels)
