@@ -1,7 +1,8 @@
 """CPU oracle for the data-parallel hot path.
 
 TEST INFRASTRUCTURE ONLY.  Only ``tests/``, ``__graft_entry__.smoke()`` and the
-CPU-baseline leg of ``bench.py`` import this package, and only to check results.
+CPU-baseline leg of ``bench.py`` import this package: to check results, or to time
+the reference's CPU arithmetic.
 The product (``libhbt.so`` and ``hybrid_training_amd``) never imports it.
 
 Each function restates the reference's algorithm for one piece of the path with

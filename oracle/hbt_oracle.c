@@ -1,9 +1,10 @@
 /*
  * hbt_oracle.c - CPU restatement of the hot path's floating-point arithmetic.
  *
- * TEST INFRASTRUCTURE ONLY.  Only tests/, the smoke()
- * entry point and bench.py's CPU-baseline leg load this oracle, to check results.  The product (libhbt.so and
- * the hybrid_training_amd package) never links or calls it.
+ * TEST INFRASTRUCTURE ONLY.  Only tests/, the smoke() entry point and bench.py's
+ * CPU-baseline leg load this oracle: to check results, or to time the reference's CPU
+ * arithmetic.  The product (libhbt.so and the hybrid_training_amd package) never links
+ * or calls it.
  *
  * Compiled with -ffp-contract=off so that only the fmaf() calls below fuse.
  *
