@@ -21,7 +21,7 @@ this rank's pre-divided contribution, ready for it.
 
 from __future__ import annotations
 
-from collections.abc import Sequence
+from collections.abc import Iterable, Sequence
 from dataclasses import dataclass, field
 from typing import Any
 
@@ -239,19 +239,33 @@ class BucketedGradients:
             return float(self._group.size)
         return 1.0
 
-    def pack(self) -> None:
-        """Copy every gradient into its bucket slice, divided by the group size for AVG.
+    def pack(self, buckets: Iterable[int] | None = None) -> None:
+        """Copy gradients into their bucket slices, divided by the group size for AVG.
 
+        By default every bucket is packed in one launch.  ``buckets`` selects bucket
+        indices instead, so a caller driven by gradient-ready hooks can pack each
+        bucket as soon as its last gradient arrives, as the reference copies them
+        (``ddp.py:479-523``), and start that bucket's all-reduce while backward runs.
         A parameter without a gradient contributes zeros when
         ``find_unused_parameters`` is set and raises otherwise (``ddp.py:579-615``).
         """
+        if buckets is None:
+            selected = self._buckets
+        else:
+            indices = list(buckets)
+            if any(not 0 <= i < len(self._buckets) for i in indices) or len(set(indices)) != len(indices):
+                raise ShardingError(
+                    format_error("ddp.pack", "bucket indices must be distinct and in range",
+                                 expected=f"distinct values in [0, {len(self._buckets)})", observed=indices)
+                )
+            selected = [self._buckets[i] for i in indices]
         missing: list[str] = []
         divisor = self._divisor()
         # Rows per (device, source dtype, bucket dtype): (source address, destination
         # address, n), source address 0 meaning a zero fill.  Built with plain attribute
         # reads: this loop runs once per step over every parameter.
         rows: dict[tuple[int, torch.dtype, torch.dtype], list[tuple[int, int, int]]] = {}
-        for bucket in self._buckets:
+        for bucket in selected:
             buffer = bucket.buffer
             base = buffer.data_ptr()
             item = buffer.element_size()
@@ -306,8 +320,8 @@ class BucketedGradients:
             plan = _native.CopyPlan.from_rows(torch.device("cuda", device_index), table)
             plan.run(src_dtype=src_dtype, dst_dtype=dst_dtype, op=op, divisor=divisor)
         self.statistics.unused_parameters = tuple(missing)
-        self.statistics.buckets_reduced += len(self._buckets)
-        self.statistics.bytes_reduced += sum(b.num_bytes() for b in self._buckets)
+        self.statistics.buckets_reduced += len(selected)
+        self.statistics.bytes_reduced += sum(b.num_bytes() for b in selected)
 
     def bind_gradients(self) -> None:
         """Point every ``param.grad`` at its bucket slice (gradient-as-bucket-view)."""

@@ -73,3 +73,30 @@ def test_unused_parameters(device):
 def test_parameterless_module_rejected(device):
     with pytest.raises(ShardingError, match="no trainable parameters"):
         BucketedGradients([], GroupHandle.trivial(), DDPConfig())
+
+
+def test_bucket_by_bucket_pack_matches_one_launch(device):
+    """Packing the buckets one at a time, in the order a backward pass completes them
+    (reverse registration order, bucket 0 first), gives the same bits as one launch."""
+    named = _gpt2_params(device)
+    gen = torch.Generator(device=device).manual_seed(11)
+    grads = [torch.randn(p.shape, device=device, generator=gen) * 1e-3 for _, p in named]
+    group = GroupHandle.local_view("data_parallel", 8, 0)
+    results = []
+    for per_bucket in (False, True):
+        for (_, p), g in zip(named, grads):
+            p.grad = g.clone()
+        ddp = BucketedGradients(named, group, DDPConfig(bucket_cap_mb=25.0))
+        if per_bucket:
+            for index in range(len(ddp.buckets)):
+                ddp.pack([index])
+        else:
+            ddp.pack()
+        results.append([b.buffer.detach().cpu().clone() for b in ddp.buckets])
+        assert ddp.statistics.buckets_reduced == 17
+    for a, b in zip(*results):
+        assert torch.equal(a.view(torch.int32), b.view(torch.int32))
+    with pytest.raises(ShardingError, match="distinct and in range"):
+        ddp.pack([17])
+    with pytest.raises(ShardingError, match="distinct and in range"):
+        ddp.pack([3, 3])
