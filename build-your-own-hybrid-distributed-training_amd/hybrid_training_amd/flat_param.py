@@ -20,8 +20,11 @@ tensor work is the interval gather-copy kernel and the local-share kernel of
 * ``full_tensors``/``load_local_pieces``/``local_pieces`` are copy plans over the
   same intervals the reference slices with ``intersect_ranges``.
 
-The storage-resize lifecycle (``reshard``/``refill``) and autograd plumbing of the
-reference are outside this path.
+* ``unshard``/``reshard``/``refill``/``free_full`` manage the gathered buffer's storage
+  as the reference does (release the bytes, keep the tensor object and its views,
+  refill the same bytes with the version counter kept).  The reference's autograd
+  function, whose backward reduce-scatters, is outside this path: the caller hands
+  the full gradient to ``reduce_scatter_gradient``.
 """
 
 from __future__ import annotations
@@ -220,6 +223,8 @@ class FlatParamHandle:
         self.flat_param = self._build_shard()
         self._attach_gradient_norm_scale()
         self._reduction_count = 0
+        self._full: torch.Tensor | None = None
+        self._is_sharded = True
         if not keep_originals:
             self._detach_original_parameters()
 
@@ -342,8 +347,8 @@ class FlatParamHandle:
 
     @property
     def is_sharded(self) -> bool:
-        """Only the shard is resident between uses."""
-        return True
+        """Whether only the shard is resident (no gathered full buffer holds storage)."""
+        return self._is_sharded
 
     def local_shard_range(self) -> ShardRange:
         """This rank's interval of the padded flat buffer."""
@@ -382,14 +387,72 @@ class FlatParamHandle:
         from every rank's shard (the all-gather's output)."""
         shards = self._all_shards(peer_shards, "fsdp.gather_full")
         full = torch.empty(self._padded_numel, dtype=self._compute_dtype, device=self._device)
+        self._gather_into(full, shards, "fsdp.gather_full")
+        self._full = full
+        self._is_sharded = False
+        return full
+
+    def _gather_into(self, full: torch.Tensor, shards: Sequence[torch.Tensor], operation: str) -> None:
         src_dtype = shards[0].dtype
-        _check_cast(src_dtype, self._compute_dtype, "fsdp.gather_full")
+        _check_cast(src_dtype, self._compute_dtype, operation)
         plan = _native.CopyPlan(self._device)
         for rank, shard in enumerate(shards):
             plan.add(_native.contiguous_source(shard.detach()), 0, full, rank * self._shard_numel,
                      self._shard_numel)
         plan.run(src_dtype=src_dtype, dst_dtype=self._compute_dtype)
+
+    def unshard(self, peer_shards: Sequence[torch.Tensor] | None = None) -> torch.Tensor:
+        """Gather the full parameters and bind them to the modules (``fsdp.py:624-634``).
+
+        The reference gathers through an autograd function whose backward
+        reduce-scatters the gradient; here the buffer is a plain tensor, and the caller
+        passes its gradient to :meth:`reduce_scatter_gradient`.
+        """
+        full = self.gather_full(peer_shards)
+        self.bind_views(full)
         return full
+
+    def reshard(self) -> None:
+        """Release the gathered buffer's storage, keeping the tensor object (``fsdp.py:636-658``).
+
+        Views of it stay valid objects over zero bytes until :meth:`refill`.
+        """
+        if self._full is None or self._is_sharded:
+            return
+        self._full.untyped_storage().resize_(0)
+        self._is_sharded = True
+
+    def refill(self, full: torch.Tensor, peer_shards: Sequence[torch.Tensor] | None = None) -> None:
+        """Restore the bytes of a buffer freed by :meth:`reshard` (``fsdp.py:660-701``).
+
+        The bytes written are the ones the gather produced, so the tensor's autograd
+        version counter is kept, as the reference keeps it.  A buffer that still holds
+        its storage is left alone.
+        """
+        required = self._padded_numel * full.element_size()
+        if full.untyped_storage().nbytes() == required:
+            return
+        shards = self._all_shards(peer_shards, "fsdp.refill")
+        with torch.no_grad(), torch.autograd._unsafe_preserve_version_counter(full):
+            full.untyped_storage().resize_(required)
+            self._gather_into(full.detach(), shards, "fsdp.refill")
+        if full is self._full:
+            self._is_sharded = False
+
+    def free_full(self) -> None:
+        """Drop the gathered buffer and unbind the views (``fsdp.py:783-789``)."""
+        if self._full is not None:
+            self._full.untyped_storage().resize_(0)
+        self._full = None
+        self._is_sharded = True
+        self.unbind_views()
+
+    def unbind_views(self) -> None:
+        """Point the module attributes at empty placeholders (``fsdp.py:613-622``)."""
+        placeholder = torch.empty(0, dtype=self._compute_dtype, device=self._device)
+        for param in self._params:
+            for module, attribute in self._locations.get(id(param), []):
+                setattr(module, attribute, placeholder)
 
     def bind_views(self, full: torch.Tensor) -> None:
         """Point every managed module attribute at its slice of ``full`` (zero copy)."""

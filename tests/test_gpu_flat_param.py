@@ -238,3 +238,31 @@ def test_local_share_norm_partials_are_the_norm_pass(device, in_dtype, norm_worl
         # an in-place change bumps the version counter: the partials are not reused
         fused.mul_(2.0)
         assert float(opt.clip_grad_norm(0.0)) == 2.0 * float(n_plain)
+
+
+def test_unshard_reshard_refill_free_full_lifecycle(device):
+    """The gathered buffer's lifecycle (``fsdp.py:613-701``, ``:783-789``) on a real module:
+    unshard binds views, reshard releases the bytes but keeps the tensor and its views,
+    refill restores the same bits with the autograd version unchanged, free_full unbinds."""
+    module = torch.nn.Linear(25, 14).to(device)
+    named = list(module.named_parameters())
+    locations = {id(p): [(module, name)] for name, p in named}
+    originals = {name: p.detach().clone() for name, p in named}
+    mp = MixedPrecisionConfig(enabled=True, param_dtype="bfloat16", reduce_dtype="float32", master_dtype="float32")
+    h = FlatParamHandle(named, locations, GroupHandle.trivial("shard"), FSDPConfig(), mp, device)
+    assert h.is_sharded
+    full = h.unshard()
+    assert not h.is_sharded and full.dtype == torch.bfloat16
+    assert torch.equal(module.weight, originals["weight"].to(torch.bfloat16))
+    assert module.weight.untyped_storage().data_ptr() == full.untyped_storage().data_ptr()
+    bits = full.detach().clone()
+    version = full._version
+    h.reshard()
+    assert h.is_sharded and full.untyped_storage().nbytes() == 0
+    h.refill(full)
+    assert not h.is_sharded and full._version == version
+    assert torch.equal(full.view(torch.int16), bits.view(torch.int16))
+    assert torch.equal(module.bias, originals["bias"].to(torch.bfloat16))  # the views see the refilled bytes
+    h.refill(full)  # a buffer that holds its storage is left alone
+    h.free_full()
+    assert h.is_sharded and module.weight.numel() == 0
