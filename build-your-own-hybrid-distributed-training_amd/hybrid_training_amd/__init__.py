@@ -48,8 +48,14 @@ from .optim import (
     build_inner_optimizer,
     distributed_gradient_norm,
 )
-from .reshard import DeviceShardCache, load_flat_shard, read_tensor_range
-from .checkpoint import ShardFileCache, collect_flat_shard_payload, load_flat_shard_checkpoint, write_checkpoint
+from .reshard import DeviceShardCache, describe_reshard, load_flat_shard, read_tensor_range
+from .checkpoint import (
+    ShardFileCache,
+    collect_flat_shard_payload,
+    load_flat_shard_checkpoint,
+    verify_files,
+    write_checkpoint,
+)
 from .tensors import (
     FlatEntry,
     ShardRange,

@@ -56,6 +56,7 @@ __all__ = [
     "ShardFileCache",
     "collect_flat_shard_payload",
     "load_flat_shard_checkpoint",
+    "verify_files",
     "write_checkpoint",
 ]
 
@@ -102,61 +103,8 @@ class ShardFileCache:
             self._loaded[name] = _DevicePayload(payload, self._device)
 
     def _verified_payload(self, filename: str, *, verify: bool) -> dict[str, Any]:
-        validate_shard_filename(filename)
-        path = resolve_inside(self._directory, filename)
-        if not path.is_file():
-            raise IncompleteCheckpointError(
-                format_error(
-                    "reshard.ShardFileCache.get",
-                    "a shard file listed in the manifest is missing",
-                    expected=filename,
-                    observed="not present in the checkpoint directory",
-                    resolution=(
-                        "the checkpoint is incomplete; restore the missing file or "
-                        "resume from an earlier checkpoint"
-                    ),
-                )
-            )
-        record = self._manifest.files.get(filename)
-        if record is None:
-            raise CheckpointCorruptionError(
-                format_error(
-                    "reshard.ShardFileCache.get",
-                    "the file has no integrity record in the manifest",
-                    expected="an entry under manifest['files']",
-                    observed=filename,
-                    resolution="the manifest is truncated or hand-edited",
-                )
-            )
-        actual_size = path.stat().st_size
-        if actual_size != record.bytes:
-            raise CheckpointCorruptionError(
-                format_error(
-                    "reshard.ShardFileCache.get",
-                    f"shard file {filename!r} has the wrong size, so it was truncated "
-                    "or overwritten after the checkpoint was published",
-                    expected=f"{record.bytes} bytes",
-                    observed=f"{actual_size} bytes",
-                    resolution="restore the file from a backup or discard the checkpoint",
-                )
-            )
-        if verify:
-            digest = file_digest(path)
-            if digest != record.sha256:
-                raise CheckpointCorruptionError(
-                    format_error(
-                        "reshard.ShardFileCache.get",
-                        f"shard file {filename!r} failed checksum verification; its "
-                        "contents differ from what the writer recorded",
-                        expected=record.sha256,
-                        observed=digest,
-                        resolution=(
-                            "the file is corrupt; restore it from a backup or discard "
-                            "the checkpoint. Pass verify_checksums=False only when you "
-                            "have another reason to trust the bytes."
-                        ),
-                    )
-                )
+        path = _check_file(self._directory, self._manifest, filename, verify=verify,
+                           operation="reshard.ShardFileCache.get")
         try:
             # weights_only=True admits tensors and primitives only: a hostile payload
             # cannot execute code.  mmap leaves the bytes in the page cache until a
@@ -196,6 +144,101 @@ class ShardFileCache:
     def loaded_files(self) -> tuple[str, ...]:
         """Names of the files loaded so far."""
         return tuple(sorted(self._loaded))
+
+
+def _check_file(directory: Path, manifest: CheckpointManifest, filename: str, *, verify: bool,
+                operation: str) -> Path:
+    """The path of one listed shard file after the reference's checks (name rule,
+    containment, presence, integrity record, size, and SHA-256 when ``verify``)."""
+    validate_shard_filename(filename)
+    path = resolve_inside(directory, filename)
+    if not path.is_file():
+        raise IncompleteCheckpointError(
+            format_error(
+                operation,
+                "a shard file listed in the manifest is missing",
+                expected=filename,
+                observed="not present in the checkpoint directory",
+                resolution=(
+                    "the checkpoint is incomplete; restore the missing file or "
+                    "resume from an earlier checkpoint"
+                ),
+            )
+        )
+    record = manifest.files.get(filename)
+    if record is None:
+        raise CheckpointCorruptionError(
+            format_error(
+                operation,
+                "the file has no integrity record in the manifest",
+                expected="an entry under manifest['files']",
+                observed=filename,
+                resolution="the manifest is truncated or hand-edited",
+            )
+        )
+    actual_size = path.stat().st_size
+    if actual_size != record.bytes:
+        raise CheckpointCorruptionError(
+            format_error(
+                operation,
+                f"shard file {filename!r} has the wrong size, so it was truncated "
+                "or overwritten after the checkpoint was published",
+                expected=f"{record.bytes} bytes",
+                observed=f"{actual_size} bytes",
+                resolution="restore the file from a backup or discard the checkpoint",
+            )
+        )
+    if verify:
+        digest = file_digest(path)
+        if digest != record.sha256:
+            raise CheckpointCorruptionError(
+                format_error(
+                    operation,
+                    f"shard file {filename!r} failed checksum verification; its "
+                    "contents differ from what the writer recorded",
+                    expected=record.sha256,
+                    observed=digest,
+                    resolution=(
+                        "the file is corrupt; restore it from a backup or discard "
+                        "the checkpoint. Pass verify_checksums=False only when you "
+                        "have another reason to trust the bytes."
+                    ),
+                )
+            )
+    return path
+
+
+def verify_files(
+    directory: Path, manifest: CheckpointManifest, *, filenames: set[str] | None = None, max_workers: int = 8
+) -> dict[str, str]:
+    """Check shard files against the manifest (``reshard.py:308-374``): presence, size and
+    SHA-256, every file in parallel (hashing releases the GIL).  Returns each file's
+    digest; raises the reference's error for the first bad file in name order."""
+    directory = Path(directory)
+    targets = sorted(filenames if filenames is not None else manifest.referenced_files())
+
+    def one(name: str) -> str:
+        _check_file(directory, manifest, name, verify=False, operation="reshard.verify_files")
+        return name
+
+    for name in targets:  # the cheap checks first, in order
+        one(name)
+    with ThreadPoolExecutor(max_workers=max(1, min(max_workers, len(targets) or 1))) as pool:
+        digests = list(pool.map(lambda n: file_digest(resolve_inside(directory, n)), targets))
+    for name, digest in zip(targets, digests):
+        expected = manifest.files[name].sha256
+        if digest != expected:
+            raise CheckpointCorruptionError(
+                format_error(
+                    "reshard.verify_files",
+                    f"shard file {name!r} failed checksum verification; its contents differ "
+                    "from what the writer recorded",
+                    expected=expected,
+                    observed=digest,
+                    resolution="the file is corrupt; restore it from a backup or discard the checkpoint",
+                )
+            )
+    return dict(zip(targets, digests))
 
 
 class _DevicePayload(Mapping[str, torch.Tensor]):

@@ -18,16 +18,17 @@ already there, and ``checkpoint.ShardFileCache`` verifies, loads and uploads
 from __future__ import annotations
 
 from collections.abc import Callable, Mapping, Sequence
+from typing import Any
 
 import torch
 
 from . import _native
 from .errors import CheckpointCorruptionError, CheckpointError, IncompleteCheckpointError, format_error
 from .flat_param import PieceLayout
-from .manifest import TensorRecord, validate_shard_filename
+from .manifest import CheckpointManifest, TensorRecord, validate_shard_filename
 from .tensors import ShardRange
 
-__all__ = ["DeviceShardCache", "load_flat_shard", "read_tensor_range"]
+__all__ = ["DeviceShardCache", "describe_reshard", "load_flat_shard", "read_tensor_range"]
 
 
 class DeviceShardCache:
@@ -269,3 +270,29 @@ def load_flat_shard(
         loaded += 1
     plans.run()
     return loaded
+
+
+def describe_reshard(manifest: CheckpointManifest, key: str, wanted: ShardRange) -> dict[str, Any]:
+    """The plan of a read, without reading (``reshard.py:377-421``): which saved shards
+    the interval ``wanted`` of tensor ``key`` touches, and where."""
+    record = manifest.tensors.get(key)
+    if record is None:
+        raise CheckpointError(
+            format_error(
+                "reshard.describe_reshard",
+                "unknown tensor key",
+                expected=sorted(manifest.tensors)[:8],
+                observed=key,
+                resolution="check the key against the manifest",
+            )
+        )
+    return {
+        "key": key,
+        "global_shape": list(record.global_shape),
+        "wanted": [wanted.start, wanted.length],
+        "sources": [
+            {"file": shard.file, "saved_rank": shard.rank, "shard_range": [shard.offset, shard.length],
+             "overlap": [overlap.start, overlap.length]}
+            for shard, overlap in record.shards_overlapping(wanted)
+        ],
+    }

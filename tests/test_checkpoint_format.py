@@ -24,8 +24,11 @@ from hybrid_training_amd import (
     IncompleteCheckpointError,
     ShardFileCache,
     ShardRecord,
+    ShardRange,
     TensorRecord,
     checkpoint_directory_name,
+    describe_reshard,
+    verify_files,
     write_checkpoint,
 )
 from hybrid_training_amd.errors import CheckpointCorruptionError
@@ -134,3 +137,28 @@ def test_corruption_is_detected(tmp_path):
         ShardFileCache(path, manifest, device="cpu").get("rank-00000.pt")
     with pytest.raises(CheckpointError, match="naming rule"):
         ShardFileCache(path, manifest, device="cpu").get("../rank-00000.pt")
+
+
+def test_verify_files_and_describe_reshard(tmp_path):
+    """``verify_files`` digests every referenced file and refuses a corrupt or missing one;
+    ``describe_reshard`` lists the saved shards a read touches (``reshard.py:308-421``)."""
+    path, _ = _cpu_checkpoint(tmp_path)
+    manifest = CheckpointManifest.read(path / MANIFEST_FILENAME)
+    digests = verify_files(path, manifest)
+    assert set(digests) == {"rank-00000.pt", "rank-00001.pt"}
+    assert all(d == file_digest(path / f) for f, d in digests.items())
+    assert set(verify_files(path, manifest, filenames={"rank-00001.pt"})) == {"rank-00001.pt"}
+    plan = describe_reshard(manifest, "w", ShardRange(4, 4))
+    assert plan["global_shape"] == [3, 4] and plan["wanted"] == [4, 4]
+    assert [(s["saved_rank"], s["overlap"]) for s in plan["sources"]] == [(0, [4, 2]), (1, [6, 2])]
+    with pytest.raises(CheckpointError, match="unknown tensor key"):
+        describe_reshard(manifest, "nope", ShardRange(0, 1))
+    target = path / "rank-00001.pt"
+    data = bytearray(target.read_bytes())
+    data[-1] ^= 0xFF
+    target.write_bytes(bytes(data))
+    with pytest.raises(CheckpointCorruptionError, match="checksum"):
+        verify_files(path, manifest)
+    target.unlink()
+    with pytest.raises(IncompleteCheckpointError, match="missing"):
+        verify_files(path, manifest)
