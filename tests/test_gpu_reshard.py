@@ -10,7 +10,6 @@ and the W=3 padding tail must stay untouched.
 
 from __future__ import annotations
 
-import numpy as np
 import pytest
 import torch
 
