@@ -68,3 +68,49 @@ def test_host_tensors_are_refused():
 
     with pytest.raises(UnsupportedFeatureError, match="HIP device"):
         _native.require_device_tensor(torch.zeros(3), "test")
+
+
+_C_HOST = r"""
+#include <stdio.h>
+#include <string.h>
+#include "hbt.h"
+
+int main(void) {
+    int failures = 0;
+    if (hbt_abi_version() != %(abi)d) { printf("abi %%d\n", hbt_abi_version()); failures++; }
+    if (hbt_symbol_count() != %(symbols)d) { printf("symbols %%d\n", hbt_symbol_count()); failures++; }
+    if (hbt_copy_chunk_elems(HBT_DTYPE_F32, HBT_DTYPE_F32) != 256) failures++;
+    if (hbt_copy_chunk_elems(HBT_DTYPE_BF16, HBT_DTYPE_F32) != 512) failures++;
+    /* refused on the host before any device work: a null table with records */
+    if (hbt_copy_intervals(NULL, 1, 1, HBT_DTYPE_F32, HBT_DTYPE_F32, HBT_COPY_OP_COPY, 1.0f, 0, NULL)
+        != HBT_ERR_INVALID_ARGUMENT) failures++;
+    if (strstr(hbt_last_error(), "hbt_copy_intervals") == NULL) failures++;
+    if (hbt_adamw_step(NULL, NULL, NULL, NULL, NULL, HBT_MAX_TENSORS_PER_LAUNCH + 1, HBT_DTYPE_F32, 1.0f,
+                       NULL, 1.0f, 0.1f, 0.9f, 0.1f, 1.0f, 1e-8f, -1e-3f, NULL) != HBT_ERR_INVALID_ARGUMENT)
+        failures++;
+    printf("c host: %%d failures\n", failures);
+    return failures;
+}
+"""
+
+
+def test_c_host_compiles_against_the_header_and_links(tmp_path):
+    """A plain C host (gcc, no HIP headers) includes ``include/hbt.h``, links ``libhbt.so``
+    and makes the calls that need no device: the header is valid C and matches the
+    library's exports, argument order included."""
+    import shutil
+    import subprocess
+
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("no C compiler")
+    lib = _native.library()  # builds the checks above only against a present library
+    src = tmp_path / "host.c"
+    src.write_text(_C_HOST % {"abi": _native.ABI_VERSION, "symbols": len(_declared_functions())})
+    exe = tmp_path / "host"
+    libdir = os.path.dirname(_native.library_path())
+    subprocess.run([gcc, "-std=c11", "-Wall", "-Werror", "-I", os.path.dirname(HEADER), str(src),
+                    "-L", libdir, "-lhbt", f"-Wl,-rpath,{libdir}", "-o", str(exe)], check=True)
+    run = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
+    assert run.returncode == 0, run.stdout + run.stderr
+    assert lib.hbt_abi_version() == _native.ABI_VERSION
