@@ -15,17 +15,20 @@ import pytest
 import torch
 
 from hybrid_training_amd import (
+    CheckpointManifest,
     FlatParamHandle,
     FSDPConfig,
     GroupHandle,
     MixedPrecisionConfig,
     OptimizerConfig,
     ShardedOptimizer,
+    ShardFileCache,
     collect_flat_shard_payload,
     load_flat_shard_checkpoint,
     write_checkpoint,
 )
 from hybrid_training_amd.errors import CheckpointCorruptionError
+from hybrid_training_amd.manifest import MANIFEST_FILENAME
 
 pytestmark = pytest.mark.gpu
 
@@ -74,9 +77,16 @@ def test_load_at_any_width(device, saved, group):
     path, flat, m, v = saved
     named = _model(device, seed=123)  # different initial values: everything must come from disk
     handles, opts = _world(named, group, device)
+    writer_shard = -(-TOTAL // 4)
     for r, (h, opt) in enumerate(zip(handles, opts)):
-        loaded = load_flat_shard_checkpoint(path, h, optimizer=opt)
+        cache = ShardFileCache(path, CheckpointManifest.read(path / MANIFEST_FILENAME), device=device)
+        loaded = load_flat_shard_checkpoint(path, h, optimizer=opt, cache=cache)
         assert loaded == len(h.local_piece_layout())
+        # a reader opens exactly the writers' files its interval intersects (tests/integration/
+        # test_checkpoint.py:351-371; the reference's extra file holds RNG state, not on this path)
+        lo, hi = r * h.shard_numel, min(TOTAL, (r + 1) * h.shard_numel)
+        expect = {f"rank-{k:05d}.pt" for k in range(4) if k * writer_shard < hi and lo < (k + 1) * writer_shard}
+        assert set(cache.loaded_files) == expect, (r, cache.loaded_files)
         start = r * h.shard_numel
         valid = max(0, min(h.shard_numel, TOTAL - start))
         assert torch.equal(h.flat_param.detach()[:valid], flat[start : start + valid])
