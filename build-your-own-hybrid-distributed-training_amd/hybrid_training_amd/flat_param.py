@@ -671,9 +671,10 @@ class FlatParamHandle:
         """Per-rank byte counts of this unit (``fsdp.py:927-942``)."""
         element = self.flat_param.element_size()
         grad = self.flat_param.grad
+        full = self._full
         return {
             "shard_bytes": self._shard_numel * element,
-            "full_bytes": 0,
+            "full_bytes": 0 if self._is_sharded or full is None else full.numel() * full.element_size(),
             "grad_shard_bytes": 0 if grad is None else grad.numel() * grad.element_size(),
             "padding_bytes": self._padding * element,
         }

@@ -255,10 +255,12 @@ def test_unshard_reshard_refill_free_full_lifecycle(device):
     assert not h.is_sharded and full.dtype == torch.bfloat16
     assert torch.equal(module.weight, originals["weight"].to(torch.bfloat16))
     assert module.weight.untyped_storage().data_ptr() == full.untyped_storage().data_ptr()
+    assert h.memory_summary()["full_bytes"] == full.numel() * 2
     bits = full.detach().clone()
     version = full._version
     h.reshard()
     assert h.is_sharded and full.untyped_storage().nbytes() == 0
+    assert h.memory_summary()["full_bytes"] == 0
     h.refill(full)
     assert not h.is_sharded and full._version == version
     assert torch.equal(full.view(torch.int16), bits.view(torch.int16))
