@@ -169,7 +169,7 @@ def main() -> int:
         return SECONDARY[args.workload](args.steps, args.warmup)
     if args.gpus != 1:
         print(
-            "bench.py measures one GPU: this build runs one rank's share of the work on one "
+            "bench.py measures one GPU: the library runs one rank's share of the work on one "
             "device and issues no collectives; --gpus must be 1",
             file=sys.stderr,
         )

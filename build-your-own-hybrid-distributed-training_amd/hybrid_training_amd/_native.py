@@ -254,7 +254,7 @@ def require_device_tensor(tensor: torch.Tensor, operation: str) -> None:
         raise UnsupportedFeatureError(
             format_error(
                 operation,
-                "this build runs the hot path only as HIP kernels, so tensors must live "
+                "hybrid_training_amd runs the hot path only as HIP kernels, so tensors must live "
                 "on a HIP device",
                 expected="device type 'cuda' (HIP)",
                 observed=str(tensor.device),

@@ -214,7 +214,7 @@ class BucketedGradients:
             raise UnsupportedFeatureError(
                 format_error(
                     "ddp.BucketedGradients",
-                    "this build packs one replica's buckets on one device and issues no all-reduce",
+                    "hybrid_training_amd packs one replica's buckets on one device and issues no all-reduce",
                     observed=repr(group),
                 )
             )

@@ -76,7 +76,7 @@ class ShardingError(HybridTrainingError):
 
 
 class UnsupportedFeatureError(HybridTrainingError, NotImplementedError):
-    """A legal request this build deliberately does not implement."""
+    """A legal request this library deliberately does not implement."""
 
 
 class CheckpointError(HybridTrainingError):
@@ -92,7 +92,7 @@ class CheckpointCorruptionError(CheckpointError):
 
 
 class CheckpointVersionError(CheckpointError):
-    """The checkpoint format version is not readable by this build."""
+    """The checkpoint format version is not readable by this library."""
 
 
 class CheckpointTopologyError(CheckpointError):

@@ -168,7 +168,7 @@ class FlatParamHandle:
             raise UnsupportedFeatureError(
                 format_error(
                     "fsdp.FlatParamHandle",
-                    "hybrid sharding needs a replica all-reduce, and this build issues no "
+                    "hybrid sharding needs a replica all-reduce, and hybrid_training_amd issues no "
                     "collectives",
                     observed=repr(replica_group),
                 )
@@ -217,7 +217,7 @@ class FlatParamHandle:
                 )
         if config.cpu_offload_params:
             raise UnsupportedFeatureError(
-                format_error("fsdp.FlatParamHandle", "parameter CPU offload is not part of this build",
+                format_error("fsdp.FlatParamHandle", "parameter CPU offload is not implemented by hybrid_training_amd",
                              expected=False, observed=True)
             )
         self.flat_param = self._build_shard()
@@ -362,7 +362,7 @@ class FlatParamHandle:
                     format_error(
                         operation,
                         "materialising the full flat parameter needs every rank's shard; "
-                        "this build issues no all-gather",
+                        "hybrid_training_amd issues no all-gather",
                         expected="peer_shards holding all group members' shards",
                         observed=None,
                         resolution="pass peer_shards=[shard_0, ..., shard_G-1] resident on this device",
@@ -508,7 +508,7 @@ class FlatParamHandle:
             raise UnsupportedFeatureError(
                 format_error(
                     "fsdp.reduce_scatter_gradient",
-                    "the reduce-scatter needs every rank's gradient; this build issues no "
+                    "the reduce-scatter needs every rank's gradient; hybrid_training_amd issues no "
                     "collectives",
                     expected=f"{group} gradients (peer_grads)",
                     observed=len(grads),
@@ -573,7 +573,7 @@ class FlatParamHandle:
             raise UnsupportedFeatureError(
                 format_error(
                     "fsdp.set_accumulate_without_reduction",
-                    "no_sync gradient accumulation is not part of this build",
+                    "no_sync gradient accumulation is not implemented by hybrid_training_amd",
                     resolution="reduce every micro-batch's gradient (no no_sync block)",
                 )
             )

@@ -3,7 +3,7 @@
 The flat-parameter layout, the AVG pre-divide and the norm weighting depend only
 on a group's size and on the rank's index in it.  :class:`GroupHandle` keeps the
 fields of ``distributed/groups.py:78-144`` of the reference so objects built for
-it carry over; no process group is ever used, because this build issues no
+it carry over; no process group is ever used, because this library issues no
 collectives.  :meth:`GroupHandle.local_view` describes rank ``r`` of a ``G``-rank
 group for a single device that holds that rank's share of the work.
 """

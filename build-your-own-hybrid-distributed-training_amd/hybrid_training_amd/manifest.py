@@ -74,12 +74,12 @@ def staging_directory_name(final_name: str, token: str) -> str:
 
 
 def validate_format_version(version: str) -> str:
-    """Refuse a format version this build cannot read."""
+    """Refuse a format version this library cannot read."""
     if version not in SUPPORTED_FORMAT_VERSIONS:
         raise CheckpointVersionError(
             format_error(
                 "checkpoint.validate_format_version",
-                "the checkpoint was written in a format version this build cannot read",
+                "the checkpoint was written in a format version this library cannot read",
                 expected=sorted(SUPPORTED_FORMAT_VERSIONS),
                 observed=version,
                 resolution="read it with the version of the package that wrote it",

@@ -377,7 +377,7 @@ def _check_group(group: GroupHandle, operation: str) -> None:
         raise UnsupportedFeatureError(
             format_error(
                 operation,
-                "this build computes one rank's share on one device and issues no collectives",
+                "hybrid_training_amd computes one rank's share on one device and issues no collectives",
                 expected="a trivial group or GroupHandle.local_view(...)",
                 observed=repr(group),
                 resolution="reduce the fp64 partial sum across ranks outside this library",
@@ -396,7 +396,7 @@ def distributed_gradient_norm(
 
     Over a trivial group this is the whole norm.  Over a
     :meth:`GroupHandle.local_view` group it is this rank's share before the
-    one-scalar fp64 SUM all-reduce, which this build does not issue.
+    one-scalar fp64 SUM all-reduce, which this library does not issue.
     """
     _check_group(group, "optim.distributed_gradient_norm")
     segments = [s for c in contributions for s in c.segments()]
@@ -675,7 +675,7 @@ class ShardedOptimizer:
             raise UnsupportedFeatureError(
                 format_error(
                     "optim.ShardedOptimizer.step",
-                    "amsgrad and maximize have no HIP kernel in this build",
+                    "amsgrad and maximize have no HIP kernel in hybrid_training_amd",
                     observed={"amsgrad": group.get("amsgrad"), "maximize": group.get("maximize")},
                 )
             )

@@ -25,7 +25,7 @@ extern "C" {
 /* ---- status codes ---------------------------------------------------------- */
 #define HBT_OK 0
 #define HBT_ERR_INVALID_ARGUMENT (-1) /* null pointer, negative size, bad dtype/op  */
-#define HBT_ERR_UNSUPPORTED (-2)      /* legal request this build does not handle   */
+#define HBT_ERR_UNSUPPORTED (-2)      /* legal request libhbt does not handle       */
 #define HBT_ERR_HIP (-3)              /* a HIP runtime call or kernel launch failed */
 
 /* ---- element types ----------------------------------------------------------- */
