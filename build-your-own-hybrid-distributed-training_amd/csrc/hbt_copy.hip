@@ -236,7 +236,7 @@ __device__ __forceinline__ int64_t owning_record(const int64_t* __restrict__ tab
 template <int SB, int DB, int OP, bool H>
 __global__ __launch_bounds__(kCopyBlock) void copy_kernel(const int64_t* __restrict__ table,
                                                           int64_t count, float divisor) {
-    static_assert(kCopyBlock == 64, "the record search uses one 64-lane ballot");
+    static_assert(kCopyBlock == 64, "a workgroup is one wave; its chunk is one wave-wide span of 16-byte source loads");
     const int64_t chunk = static_cast<int64_t>(blockIdx.x);
     const int64_t* rec = table + 4 * owning_record(table, count, chunk);
     const gbyte* src = reinterpret_cast<const gbyte*>(static_cast<uintptr_t>(rec[0]));

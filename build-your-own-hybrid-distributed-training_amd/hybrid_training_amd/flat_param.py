@@ -746,23 +746,35 @@ def reshard_state_dict_pieces(
             )
         )
     flat = torch.empty(total, dtype=dtype, device=device)
-    # Later pieces overwrite earlier ones where they overlap, as sequential slice
-    # assignment does; keep only the last writer of every element.
     plan = _native.CopyPlan(device)
+    sources = [_native.contiguous_source(piece.data.reshape(-1)) for piece in pieces]
+    for index, start, end in _last_writer_segments(intervals):
+        plan.add(sources[index], start - pieces[index].offset, flat, start, end - start)
+    plan.run(src_dtype=dtype, dst_dtype=dtype)
+    return flat.view(global_shape)
+
+
+def _last_writer_segments(intervals: Sequence[tuple[int, int]]) -> list[tuple[int, int, int]]:
+    """``(index, start, end)`` segments giving every covered element to the last interval
+    that covers it.
+
+    Sequential slice assignment in list order lets later pieces overwrite earlier ones
+    where they overlap; copying each element once from its last writer gives the same
+    result in one launch.  The segments are disjoint and their union is the union of
+    the intervals.
+    """
+    segments: list[tuple[int, int, int]] = []
     claimed: list[tuple[int, int]] = []
-    for piece in reversed(list(pieces)):
-        start, end = piece.offset, piece.offset + piece.length
+    for index in range(len(intervals) - 1, -1, -1):
+        start, end = intervals[index]
         cursor = start
         for c_start, c_end in sorted(claimed):
             if c_end <= cursor or c_start >= end:
                 continue
             if c_start > cursor:
-                plan.add(_native.contiguous_source(piece.data.reshape(-1)), cursor - start, flat, cursor,
-                         c_start - cursor)
+                segments.append((index, cursor, c_start))
             cursor = max(cursor, c_end)
         if cursor < end:
-            plan.add(_native.contiguous_source(piece.data.reshape(-1)), cursor - start, flat, cursor,
-                     end - cursor)
+            segments.append((index, cursor, end))
         claimed.append((start, end))
-    plan.run(src_dtype=dtype, dst_dtype=dtype)
-    return flat.view(global_shape)
+    return segments

@@ -20,6 +20,7 @@ from hybrid_training_amd import (
     FSDPConfig,
     GroupHandle,
     MixedPrecisionConfig,
+    ShardedTensorPiece,
     ShardingError,
     reshard_state_dict_pieces,
 )
@@ -69,6 +70,44 @@ def test_pack_pad_shard_matches_oracle(device, shapes, group):
     for (name, _), orig in zip(named, originals):
         mine = [p for p in pieces if p.name == name]
         assert torch.equal(reshard_state_dict_pieces(mine, tuple(orig.shape)), orig)
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_reshard_state_dict_pieces_overlapping_pieces_last_writer_wins(device, seed):
+    """``parallel/fsdp.py:1670-1730`` assigns the pieces' slices in list order, so where
+    pieces overlap the later one's values stand.  The expected tensor is that sequential
+    assignment done on the CPU; pieces start at odd offsets (misaligned sources and
+    destinations) and one piece's data is a non-contiguous view."""
+    rng = np.random.default_rng(seed)
+    shape = (37, 29)
+    total = shape[0] * shape[1]
+    spans = [(0, total // 2 + 5), (total // 2 - 11, total - total // 2 + 11)]
+    for _ in range(5):
+        start = int(rng.integers(0, total - 1))
+        spans.append((start, int(rng.integers(1, total - start + 1))))
+    order = rng.permutation(len(spans))
+    spans = [spans[i] for i in order]
+    expected = torch.full((total,), float("nan"))
+    pieces = []
+    for k, (offset, length) in enumerate(spans):
+        values = torch.arange(length, dtype=torch.float32) + 1000.0 * (k + 1)
+        expected[offset:offset + length] = values
+        data = values.to(device)
+        if k == 1:
+            wide = torch.empty((length, 2), device=device)
+            wide[:, 0] = data
+            data = wide[:, 0]
+            assert not data.is_contiguous()
+        pieces.append(ShardedTensorPiece(name="w", global_shape=shape, offset=offset, data=data))
+    assert not torch.isnan(expected).any()
+    got = reshard_state_dict_pieces(pieces, shape)
+    assert got.shape == shape
+    assert torch.equal(got.reshape(-1).cpu().view(torch.int32), expected.view(torch.int32))
+    with pytest.raises(ShardingError, match="uncovered"):
+        reshard_state_dict_pieces([p for p in pieces if p.offset != 0], shape)
+    with pytest.raises(ShardingError, match="past the end"):
+        reshard_state_dict_pieces(pieces + [ShardedTensorPiece(name="w", global_shape=shape, offset=total - 2,
+                                                               data=torch.zeros(3, device=device))], shape)
 
 
 def test_norm_weights_and_padding_runs(device):
