@@ -66,7 +66,7 @@ def parse_args() -> argparse.Namespace:
         help="adamw (default): the Llama-3-8B W=8 shard step above; buckets: GPT-2-small DDP bucket "
         "pack + AVG divide at W=8; reshard: Llama-3-8B bf16 flat shards W=4 -> W=8 and W=2; scaler: "
         "one Llama-3-70B W=8 rank shard with bf16 gradients, loss scale 2^16, clip and AdamW; fsdp: "
-        "Llama-3-8B FSDP pack, unpack and gradient local share at W=8; inplace_clip: the headline step with "
+        "Llama-3-8B FSDP pack, unpack, gradient local share and no_sync accumulation at W=8; inplace_clip: the headline step with "
         "the reference's in-place clip; torch_adamw: the headline step with stock torch GPU kernels; sgd: "
         "the headline shard with SGD (momentum 0.9); offload: the headline step with AdamW state in pinned "
         "host memory; checkpoint: Llama-3-8B bf16 saved by 4 FSDP ranks and loaded back at W=8; "
@@ -165,8 +165,6 @@ def main() -> int:
     args = parse_args()
     if args.calibrate_copy:
         return calibrate_copy()
-    if args.workload != "adamw":
-        return SECONDARY[args.workload](args.steps, args.warmup)
     if args.gpus != 1:
         print(
             "bench.py measures one GPU: the library runs one rank's share of the work on one "
@@ -174,6 +172,8 @@ def main() -> int:
             file=sys.stderr,
         )
         return 2
+    if args.workload != "adamw":
+        return SECONDARY[args.workload](args.steps, args.warmup)
 
     import torch
 
@@ -486,6 +486,8 @@ def bench_fsdp(steps: int, warmup: int) -> int:
     4 B per param).  Unpack: ``full_tensors`` from the 8 shards (read 4 B + write 4 B).
     Local share: rank 0's ``reduce_scatter_gradient`` over the 8 ranks' padded bf16
     gradients resident on the device (read 8 x 2 B + write 4 B per shard element).
+    no_sync: one micro-batch's accumulation of rank 0's slices of the 8 bf16 gradients
+    into its fp32 accumulator (read 4 + 2 B, write 4 B per accumulated element).
     """
     import torch
 
@@ -566,6 +568,24 @@ def bench_fsdp(steps: int, warmup: int) -> int:
           (2 * world + 4 + 28) * shard, {"shard_numel": shard, "world": world, "bytes_per_element": 2 * world + 32},
           _secondary_traffic("fsdp", ["gradient local share with norm partials", "fused clip + AdamW in the tail"],
                              [1, 1]))
+
+    # no_sync: the first micro-batch copies rank 0's slice of each rank's gradient into
+    # the fp32 accumulator (untimed); each timed micro-batch adds the eight slices to it.
+    owner.set_accumulate_without_reduction(True)
+    owner.reduce_scatter_gradient(grads[0], peer_grads=grads)
+
+    def accumulate():
+        owner.reduce_scatter_gradient(grads[0], peer_grads=grads)
+
+    ms = _time_events(accumulate, max(steps, 5), max(warmup, 2))
+    _emit("FSDP no_sync gradient accumulation: accumulated elements/s", "elements/s", world * shard / (ms * 1e-3),
+          ms, max(steps, 5), max(warmup, 2), "bf16->f32",
+          f"Llama-3-8B rank 0 of W={world}: one micro-batch of {world} bf16 gradient slices added to the fp32 "
+          "accumulator", 10 * world * shard,
+          {"shard_numel": shard, "world": world, "bytes_per_element": 10},
+          _secondary_traffic("fsdp", ["no_sync accumulation"], [1]))
+    owner.set_accumulate_without_reduction(False)
+    owner.flat_param.grad = owner.reduce_scatter_gradient(grads[0], peer_grads=grads)
     del opt, grads, owner, named
     torch.cuda.empty_cache()
     return 0

@@ -573,6 +573,70 @@ __global__ __launch_bounds__(kScaleBlock) void scale_kernel(ScaleTable tab, floa
     for (int64_t i = base + threadIdx.x; i < end; i += kScaleBlock) x[i] = scale_one<T>(x[i], unscale, mul);
 }
 
+// ---- no_sync gradient accumulation ----------------------------------------------------
+// acc = acc + fp32(grad): one fp32 addition per element, the gradient widened exactly.
+// The scale kernel's shape: half-wave workgroups, two 4-element vectors of the
+// accumulator per lane, 256 accumulator elements per workgroup.
+constexpr int64_t kAccumTile = int64_t(kScaleBlock) * 2 * 4;
+
+struct AccumTable {
+    float* acc[kMaxT];
+    const void* grad[kMaxT];
+    int64_t n[kMaxT];
+    int64_t first_block[kMaxT + 1];
+    int32_t vec_ok[kMaxT];
+    int32_t count;
+};
+
+// Four gradient elements of SB bytes each (fp32, or bf16 / fp16 when H), widened.
+template <int SB, bool H>
+__device__ __forceinline__ f32x4 load_grad4(const unsigned char* p) {
+    if constexpr (SB == 4) {
+        return ld4_nt(reinterpret_cast<const float*>(p));
+    } else {
+        const u32x2 w = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
+        return f32x4{b16_to_f32<H>(w.x & 0xFFFFu), b16_to_f32<H>(w.x >> 16), b16_to_f32<H>(w.y & 0xFFFFu),
+                     b16_to_f32<H>(w.y >> 16)};
+    }
+}
+template <int SB, bool H>
+__device__ __forceinline__ float load_grad1(const unsigned char* p, int64_t i) {
+    if constexpr (SB == 4) return reinterpret_cast<const float*>(p)[i];
+    return b16_to_f32<H>(reinterpret_cast<const uint16_t*>(p)[i]);
+}
+
+template <int SB, bool H>
+__global__ __launch_bounds__(kScaleBlock) void accumulate_kernel(AccumTable tab) {
+    const int64_t block = blockIdx.x;
+    int t = 0;
+    while (t + 1 < tab.count && block >= tab.first_block[t + 1]) ++t;
+    const int64_t base = (block - tab.first_block[t]) * kAccumTile;
+    const int64_t n = tab.n[t];
+    float* __restrict__ acc = tab.acc[t];
+    const unsigned char* __restrict__ grad = static_cast<const unsigned char*>(tab.grad[t]);
+    if (tab.vec_ok[t] && base + kAccumTile <= n) {
+        f32x4 a[2], g[2];
+        float* p[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int64_t i = base + (int64_t(u) * kScaleBlock + threadIdx.x) * 4;
+            p[u] = acc + i;
+            g[u] = load_grad4<SB, H>(grad + i * SB);
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) a[u] = ld4_nt(p[u]);
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) a[u][c] = a[u][c] + g[u][c];
+            st4_nt(p[u], a[u]);
+        }
+        return;
+    }
+    const int64_t end = base + kAccumTile < n ? base + kAccumTile : n;
+    for (int64_t i = base + threadIdx.x; i < end; i += kScaleBlock) acc[i] = acc[i] + load_grad1<SB, H>(grad, i);
+}
+
 inline bool aligned(const void* ptr, uintptr_t bytes) {
     return (reinterpret_cast<uintptr_t>(ptr) % bytes) == 0;
 }
@@ -794,6 +858,52 @@ int32_t hbt_scale_inplace(void* const* tensors, const int64_t* numels, int32_t c
             tab, unscale, grad_mul);
     }
     return check_launch("hbt_scale_inplace");
+}
+
+int32_t hbt_grad_accumulate(float* const* accumulators, const void* const* grads, const int64_t* numels,
+                            int32_t count, int32_t grad_dtype, void* stream) {
+    clear_error();
+    if (count < 0 || count > kMaxT ||
+        (count > 0 && (accumulators == nullptr || grads == nullptr || numels == nullptr))) {
+        set_error("hbt_grad_accumulate: bad table (count=%d)", count);
+        return HBT_ERR_INVALID_ARGUMENT;
+    }
+    if (grad_dtype != HBT_DTYPE_F32 && grad_dtype != HBT_DTYPE_BF16 && grad_dtype != HBT_DTYPE_F16) {
+        set_error("hbt_grad_accumulate: gradient dtype %d is not F32, BF16 or F16", grad_dtype);
+        return HBT_ERR_INVALID_ARGUMENT;
+    }
+    const int grad_bytes = dtype_size(grad_dtype);
+    AccumTable tab{};
+    tab.count = count;
+    int64_t blocks = 0;
+    for (int i = 0; i < count; ++i) {
+        if (numels[i] < 0 || (numels[i] > 0 && (accumulators[i] == nullptr || grads[i] == nullptr))) {
+            set_error("hbt_grad_accumulate: pair %d has a bad pointer or numel", i);
+            return HBT_ERR_INVALID_ARGUMENT;
+        }
+        tab.acc[i] = accumulators[i];
+        tab.grad[i] = grads[i];
+        tab.n[i] = numels[i];
+        tab.vec_ok[i] = aligned(accumulators[i], 16) && aligned(grads[i], 4 * static_cast<uintptr_t>(grad_bytes));
+        tab.first_block[i] = blocks;
+        blocks += (numels[i] + kAccumTile - 1) / kAccumTile;
+    }
+    tab.first_block[count] = blocks;
+    for (int i = count + 1; i <= kMaxT; ++i) tab.first_block[i] = blocks;
+    if (blocks == 0) return HBT_OK;
+    if (blocks > 0x7FFFFFFFLL) {
+        set_error("hbt_grad_accumulate: %lld tiles exceed the grid limit", static_cast<long long>(blocks));
+        return HBT_ERR_UNSUPPORTED;
+    }
+    const dim3 grid(static_cast<unsigned>(blocks));
+    if (grad_dtype == HBT_DTYPE_F32) {
+        accumulate_kernel<4, false><<<grid, kScaleBlock, 0, as_stream(stream)>>>(tab);
+    } else if (grad_dtype == HBT_DTYPE_BF16) {
+        accumulate_kernel<2, false><<<grid, kScaleBlock, 0, as_stream(stream)>>>(tab);
+    } else {
+        accumulate_kernel<2, true><<<grid, kScaleBlock, 0, as_stream(stream)>>>(tab);
+    }
+    return check_launch("hbt_grad_accumulate");
 }
 
 

@@ -51,7 +51,7 @@ __all__ = [
     "stream_of",
 ]
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 MAX_TENSORS_PER_LAUNCH = 16
 MAX_LOCAL_RANKS = 64
 
@@ -131,6 +131,7 @@ EXPORTED_SYMBOLS: dict[str, tuple[object, tuple[object, ...]]] = {
         _c_i32,
         (_ptr_array, _i64_array, _c_i32, _c_i32, _c_f32, _c_void_p, _c_void_p),
     ),
+    "hbt_grad_accumulate": (_c_i32, (_ptr_array, _ptr_array, _i64_array, _c_i32, _c_i32, _c_void_p)),
 }
 
 _LOCK = threading.Lock()

@@ -223,6 +223,10 @@ class FlatParamHandle:
         self.flat_param = self._build_shard()
         self._attach_gradient_norm_scale()
         self._reduction_count = 0
+        self._accumulate_without_reduction = False
+        # no_sync accumulation: row q holds rank q's accumulated gradient restricted to
+        # this rank's slice, the only part of it this rank's reduce-scatter reads.
+        self._grad_accumulator: torch.Tensor | None = None
         self._full: torch.Tensor | None = None
         self._is_sharded = True
         if not keep_originals:
@@ -487,12 +491,18 @@ class FlatParamHandle:
     # -- gradient ---------------------------------------------------------------------
     def reduce_scatter_gradient(
         self, grad_full: torch.Tensor, *, peer_grads: Sequence[torch.Tensor] | None = None
-    ) -> torch.Tensor:
+    ) -> torch.Tensor | None:
         """This rank's fp32 gradient shard (``fsdp.py:704-769``), padding forced to 0.0.
 
         ``grad_full`` is this rank's padded full gradient.  With a group of size 1
         that is all there is; otherwise ``peer_grads`` must hold every rank's padded
         gradient (``grad_full`` among them, in rank order), summed in rank order.
+
+        Inside ``no_sync`` (:meth:`set_accumulate_without_reduction`) the gradients
+        are accumulated instead and ``None`` is returned (``fsdp.py:738-745``): the
+        first call keeps a copy of each, later calls add to it in fp32.  The next call
+        outside ``no_sync`` adds its gradients to the accumulated ones and reduces the
+        sums (``fsdp.py:747-749``).
         """
         if self._reduce_dtype != torch.float32 or self._master_dtype != torch.float32:
             raise UnsupportedFeatureError(
@@ -528,6 +538,17 @@ class FlatParamHandle:
                     )
                 )
         local = self.local_shard_range()
+        if self._accumulate_without_reduction or self._grad_accumulator is not None:
+            self._accumulate(grads, local.start)
+            if self._accumulate_without_reduction:
+                return None
+            # Reduce the accumulated sums: row q is rank q's total restricted to this
+            # rank's slice, so the local share reads it at rank offset 0.
+            accumulator, self._grad_accumulator = self._grad_accumulator, None
+            grads = list(accumulator.unbind(0))
+            source_rank = 0
+        else:
+            source_rank = self._shard_group.local_rank
         valid = max(0, min(self._shard_numel, self._total_numel - local.start))
         divisor = float(group) if (self._config.average_gradients and group > 1) else 1.0
         out = torch.empty(self._shard_numel, dtype=torch.float32, device=self._device)
@@ -541,7 +562,7 @@ class FlatParamHandle:
             status = lib.hbt_grad_local_share_sqnorm(
                 _native.pointer_array([g.data_ptr() for g in grads]),
                 group,
-                self._shard_group.local_rank,
+                source_rank,
                 self._shard_numel,
                 valid,
                 _native.dtype_code(grads[0].dtype),
@@ -563,25 +584,50 @@ class FlatParamHandle:
         self._reduction_count += 1
         return out
 
-    def set_accumulate_without_reduction(self, value: bool) -> None:
-        """``no_sync`` accumulation of unsharded gradients (``fsdp.py:791-797``).
-
-        Not built: the accumulate-then-reduce path has no kernel here, so enabling it
-        raises rather than silently reducing every micro-batch.
-        """
-        if value:
-            raise UnsupportedFeatureError(
-                format_error(
-                    "fsdp.set_accumulate_without_reduction",
-                    "no_sync gradient accumulation is not implemented by hybrid_training_amd",
-                    resolution="reduce every micro-batch's gradient (no no_sync block)",
+    def _accumulate(self, grads: Sequence[torch.Tensor], start: int) -> None:
+        """Add every rank's gradient, restricted to this rank's slice, into the
+        accumulator (``fsdp.py:738-749``): a copy on the first call (``clone``, which
+        keeps -0.0), then one fp32 addition per element (``add_``)."""
+        shard = self._shard_numel
+        if self._grad_accumulator is None:
+            # Rows start on 256-byte boundaries so both kernels take their vector paths.
+            stride = -(-shard // 64) * 64
+            accumulator = torch.empty((len(grads), stride), dtype=torch.float32, device=self._device)[:, :shard]
+            plan = _native.CopyPlan(self._device)
+            for q, g in enumerate(grads):
+                plan.add(g, start, accumulator[q], 0, shard)
+            plan.run(src_dtype=grads[0].dtype, dst_dtype=torch.float32)
+            self._grad_accumulator = accumulator
+            return
+        accumulator = self._grad_accumulator
+        lib = _native.library()
+        step = _native.MAX_TENSORS_PER_LAUNCH
+        offset_bytes = start * grads[0].element_size()
+        with torch.cuda.device(self._device):
+            for first in range(0, len(grads), step):
+                rows = range(first, min(first + step, len(grads)))
+                status = lib.hbt_grad_accumulate(
+                    _native.pointer_array([accumulator[q].data_ptr() for q in rows]),
+                    _native.pointer_array([grads[q].data_ptr() + offset_bytes for q in rows]),
+                    _native.int64_array([shard] * len(rows)),
+                    len(rows),
+                    _native.dtype_code(grads[0].dtype),
+                    _native.stream_of(self._device),
                 )
-            )
+                _native.check(status, "fsdp.hbt_grad_accumulate")
+
+    def set_accumulate_without_reduction(self, value: bool) -> None:
+        """Enable or disable ``no_sync`` accumulation for this unit (``fsdp.py:791-797``).
+
+        While enabled, :meth:`reduce_scatter_gradient` accumulates and returns ``None``;
+        the first call after disabling it reduces the accumulated gradients.
+        """
+        self._accumulate_without_reduction = bool(value)
 
     @property
     def has_pending_accumulation(self) -> bool:
-        """Whether unreduced gradients are held from a ``no_sync`` block (never here)."""
-        return False
+        """Whether unreduced gradients are held from a ``no_sync`` block (``fsdp.py:799-802``)."""
+        return self._grad_accumulator is not None
 
     def zero_padding_region(self, shard_grad: torch.Tensor) -> None:
         """Zero the padding part of a gradient shard (``fsdp.py:771-781``)."""

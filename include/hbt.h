@@ -31,7 +31,7 @@ extern "C" {
 /* ---- element types ----------------------------------------------------------- */
 #define HBT_DTYPE_F32 0
 #define HBT_DTYPE_BF16 1
-#define HBT_DTYPE_F16 2 /* copies, F32 <-> F16 casts and division; local-share input */
+#define HBT_DTYPE_F16 2 /* copies, F32 <-> F16 casts and division; local-share and accumulate input */
 #define HBT_DTYPE_F64 3 /* byte copies only */
 
 /* ---- per-call limits ---------------------------------------------------------- */
@@ -199,8 +199,10 @@ int32_t hbt_copy_intervals(const int64_t* table, int64_t count, int64_t total_ch
  *   _zero_padding_region (parallel/fsdp.py:771-781).
  * `rank_grads` is a HOST array of `group_size` (at most HBT_MAX_LOCAL_RANKS) device
  * addresses, each the padded full gradient (group_size * shard_numel elements,
- * in_dtype F32, BF16 or F16) of one rank, all resident on this device.  Writes the fp32
- * shard of `rank`:
+ * in_dtype F32, BF16 or F16) of one rank, all resident on this device.  Only elements
+ * [rank*shard_numel, (rank+1)*shard_numel) of each are read, so a caller holding just
+ * those slices (as the no_sync accumulator does) passes them with rank 0.  Writes the
+ * fp32 shard of `rank`:
  *   out[i] = sum over q = 0..group_size-1, in that order, of
  *            fp32(rank_grads[q][rank*shard_numel + i]) / divisor
  * (divisor = G for AVG, 1 for SUM), then +0.0 for i >= valid_numel (the padding tail).
@@ -232,6 +234,23 @@ int32_t hbt_grad_local_share_sqnorm(const void* const* rank_grads, int32_t group
                                     int64_t shard_numel, int64_t valid_numel, int32_t in_dtype,
                                     float divisor, float* out, double* partials, double* tile_scratch,
                                     void* stream);
+
+/* ------------------------------------------------------------------------------
+ * FSDP no_sync gradient accumulation: acc = acc + fp32(grad), element by element,
+ * over up to HBT_MAX_TENSORS_PER_LAUNCH (accumulator, gradient) pairs.
+ *
+ * Replaces: the accumulate branch of FlatParamHandle.reduce_scatter_gradient
+ *   (parallel/fsdp.py:733-749): grad.to(reduce_dtype) followed by
+ *   accumulator.add_(grad) inside no_sync(), and the synchronising call's
+ *   grad + accumulator before the reduce-scatter.
+ * `accumulators` and `grads` are HOST arrays of `count` device addresses.  Accumulator
+ * k holds numels[k] fp32 elements; gradient k holds as many elements of grad_dtype
+ * (F32, BF16 or F16).  The widening is exact and the sum is one fp32 addition rounded
+ * to nearest even, as torch's fp32 add_ gives.  A gradient must not overlap its
+ * accumulator.
+ * ---------------------------------------------------------------------------- */
+int32_t hbt_grad_accumulate(float* const* accumulators, const void* const* grads, const int64_t* numels,
+                            int32_t count, int32_t grad_dtype, void* stream);
 
 /* ------------------------------------------------------------------------------
  * In-place gradient scaling: x = (x * unscale) * (*grad_mul), each product rounded to

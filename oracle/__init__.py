@@ -32,6 +32,7 @@ __all__ = [
     "flat_layout",
     "library",
     "local_share",
+    "no_sync_accumulate",
     "pack_shard",
     "read_range",
     "sgd_step",
@@ -65,6 +66,8 @@ PINNED_BY = {
     "(test_checkpoint_format.py:242-247); bitwise re-slicing of the global flat vector",
     "local_share": "torch Tensor.div + add + padding zero, bitwise (order-free for G <= 2; "
     "collectives.py:593-594); padding tail exactly 0.0 (test_fsdp.py:477-481)",
+    "no_sync_accumulate": "torch's own CPU sequence of fsdp.py:733-749 (to(float32), clone, add_, "
+    "grad + accumulator), bitwise on signed zeros, subnormals, overflow and random values",
 }
 
 
@@ -273,6 +276,22 @@ def local_share(rank_grads: Sequence[np.ndarray], rank: int, shard: int, valid: 
     acc = acc.astype(np.float32)
     acc[valid:] = 0.0
     return acc
+
+
+def no_sync_accumulate(micro_grads: Sequence[np.ndarray]) -> np.ndarray:
+    """The fp32 gradient one rank reduces after ``no_sync`` accumulation
+    (parallel/fsdp.py:733-749).  ``micro_grads`` are the micro-batches' gradients in
+    order, already widened to fp32 (bf16 and fp16 widen exactly); all but the last ran
+    inside ``no_sync``.  The first is kept as a copy (``clone``), each later one inside
+    ``no_sync`` is added with one fp32 addition (``add_``), and the last, synchronising
+    one is added in front (``grad + accumulator``)."""
+    acc = np.array(micro_grads[0], dtype=np.float32, copy=True)
+    if len(micro_grads) == 1:
+        return acc
+    with np.errstate(over="ignore", invalid="ignore"):  # IEEE overflow to +-inf is the answer
+        for g in micro_grads[1:-1]:
+            acc = np.add(acc, np.asarray(g, dtype=np.float32), dtype=np.float32)
+        return np.add(np.asarray(micro_grads[-1], dtype=np.float32), acc, dtype=np.float32)
 
 
 def read_range(shards: Sequence[tuple[int, np.ndarray]], start: int, length: int) -> np.ndarray:

@@ -10,6 +10,9 @@
   and ``optim/sharded_optimizer.py:333-337``): bitwise against torch's own CPU
   ``mul_`` by a Python float, twice, in the tensor's dtype, over several tensors per
   launch, tails of every length and a misaligned view.
+* ``hbt_grad_accumulate`` (the ``no_sync`` accumulation of ``parallel/fsdp.py:738-749``):
+  bitwise against torch's CPU ``add_`` after ``to(float32)``, fp32, bf16 and fp16
+  gradients, tails of every length, a misaligned pair and IEEE specials.
 """
 
 from __future__ import annotations
@@ -156,3 +159,55 @@ def test_local_share_full_size_rank7_of_llama3_8b_w8(device):
     assert abs(float(partials.sum()) - ref) <= 1e-10 * ref
     del grads
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("grad_dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_grad_accumulate_tiles(device, grad_dtype):
+    """``hbt_grad_accumulate`` (the ``no_sync`` ``accumulator.add_(grad.to(float32))`` of
+    ``parallel/fsdp.py:738-749``) against torch's CPU ``add_``: bitwise except that NaN
+    results are compared as NaN.  Several pairs per launch, tails of every length, a
+    misaligned first accumulator and gradient (scalar path), signed zeros, infinities,
+    a NaN and subnormal sums."""
+    lib = _native.library()
+    gen = torch.Generator(device=device).manual_seed(11)
+    sizes = [1, 7, 255, 256, 257, 4097, 100_003]
+    acc_base = torch.randn(sum(sizes) + 1, device=device, generator=gen) * 1e-2
+    grad_base = (torch.randn(sum(sizes) + 1, device=device, generator=gen) * 1e-2).to(grad_dtype)
+    acc_base[1:5] = -0.0
+    grad_base[1:3] = -0.0     # -0 + -0 = -0
+    grad_base[3:5] = 0.0      # -0 + +0 = +0
+    acc_base[300] = float("inf")
+    grad_base[301] = -float("inf")
+    grad_base[302] = float("nan")
+    acc_base[303] = 1e-40     # fp32 subnormal plus a small gradient
+    grad_base[303] = torch.finfo(grad_dtype).tiny
+    accs, grads, cursor = [], [], 1  # the first pair starts one element in: misaligned
+    for n in sizes:
+        accs.append(acc_base[cursor:cursor + n])
+        grads.append(grad_base[cursor:cursor + n])
+        cursor += n
+    before = [a.detach().cpu().clone() for a in accs]
+    lead = _bits(acc_base[:1])
+    stream = ctypes.c_void_p(_native.stream_of(device))
+    status = lib.hbt_grad_accumulate(
+        _native.pointer_array([a.data_ptr() for a in accs]), _native.pointer_array([g.data_ptr() for g in grads]),
+        _native.int64_array(sizes), len(sizes), _native.dtype_code(grad_dtype), stream,
+    )
+    _native.check(status, "test.grad_accumulate")
+    for a, b, g in zip(accs, before, grads):
+        expect = b.add_(g.detach().cpu().to(torch.float32))
+        got = a.detach().cpu()
+        nan = torch.isnan(expect)
+        assert torch.equal(torch.isnan(got), nan)
+        assert np.array_equal(_bits(got)[~nan.numpy()], _bits(expect)[~nan.numpy()])
+    assert np.array_equal(_bits(acc_base[:1]), lead)  # the element before the first pair is untouched
+    assert bool(torch.signbit(accs[0][0])) and not bool(torch.signbit(accs[1][2]))
+    # host-side refusals: no launch
+    too_many = _native.MAX_TENSORS_PER_LAUNCH + 1
+    assert lib.hbt_grad_accumulate(_native.pointer_array([accs[0].data_ptr()] * too_many),
+                                   _native.pointer_array([grads[0].data_ptr()] * too_many),
+                                   _native.int64_array([1] * too_many), too_many,
+                                   _native.dtype_code(grad_dtype), stream) == -1
+    assert lib.hbt_grad_accumulate(_native.pointer_array([accs[0].data_ptr()]),
+                                   _native.pointer_array([grads[0].data_ptr()]), _native.int64_array([1]), 1,
+                                   3, stream) == -1  # fp64 gradients

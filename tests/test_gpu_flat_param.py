@@ -5,7 +5,9 @@ The 1857-parameter MLPs of the reference tests (``test_fsdp.py:42-46``) at group
 and gradient share is checked bitwise against the oracle's restatement
 (``oracle.pack_shard``, ``oracle.local_share``) and against the reference's
 invariants: padding is exactly 0.0 in parameters and gradients, pieces cover every
-parameter once, and ``full_tensors`` reproduces the originals bitwise.
+parameter once, and ``full_tensors`` reproduces the originals bitwise.  ``no_sync``
+accumulation is checked against the oracle's restatement of the reference's
+clone/add_/add sequence followed by its local share.
 """
 
 from __future__ import annotations
@@ -25,6 +27,7 @@ from hybrid_training_amd import (
     reshard_state_dict_pieces,
 )
 from hybrid_training_amd.errors import UnsupportedFeatureError
+from hybrid_training_amd.optim import NORM_PARTIALS_ATTR
 
 from .model_shapes import MLP_23_32_32_1, MLP_1857_REFERENCE
 
@@ -142,11 +145,59 @@ def test_local_share_needs_every_rank(device):
         handles[0].reduce_scatter_gradient(torch.zeros(handles[0].padded_numel, device=device))
     with pytest.raises(UnsupportedFeatureError, match="needs every rank's shard"):
         handles[0].full_tensors()
-    # no_sync accumulation is refused up front; turning it off is a no-op
-    handles[0].set_accumulate_without_reduction(False)
+    # ... inside no_sync too: accumulation also needs every rank's gradient
+    handles[0].set_accumulate_without_reduction(True)
+    with pytest.raises(UnsupportedFeatureError, match="reduce-scatter needs every rank"):
+        handles[0].reduce_scatter_gradient(torch.zeros(handles[0].padded_numel, device=device))
     assert handles[0].has_pending_accumulation is False
-    with pytest.raises(UnsupportedFeatureError, match="no_sync"):
-        handles[0].set_accumulate_without_reduction(True)
+
+
+@pytest.mark.parametrize("group", [1, 2, 3, 4])
+@pytest.mark.parametrize("in_dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("micro", [2, 4])
+def test_no_sync_accumulation_matches_oracle(device, group, in_dtype, micro):
+    """``no_sync`` (``parallel/fsdp.py:733-749``): the first ``micro - 1`` micro-batches
+    accumulate and return None; the last reduces the sums.  Bitwise against the
+    oracle's local share of the oracle's accumulated gradients, with -0.0 planted in
+    every rank's slice (a copy, not an add onto zeros, keeps its sign)."""
+    _, _, handles = _handles(MLP_1857_REFERENCE, group, device)
+    padded, shard = handles[0].padded_numel, handles[0].shard_numel
+    gen = torch.Generator(device=device).manual_seed(100 * group + micro)
+    grads = []
+    for _ in range(micro):
+        batch = []
+        for _ in range(group):
+            g = (torch.randn(padded, device=device, generator=gen) * 1e-2).to(in_dtype)
+            for r in range(group):
+                g[r * shard + 5] = -0.0
+            batch.append(g)
+        grads.append(batch)
+    divisor = float(group) if group > 1 else 1.0
+    for rank, h in enumerate(handles):
+        def reduce(m):
+            return h.reduce_scatter_gradient(grads[m][rank], peer_grads=grads[m] if group > 1 else None)
+
+        h.set_accumulate_without_reduction(True)
+        for m in range(micro - 1):
+            assert reduce(m) is None
+            assert h.has_pending_accumulation
+        assert h.reduction_count == 0
+        h.set_accumulate_without_reduction(False)
+        out = reduce(micro - 1)
+        assert not h.has_pending_accumulation and h.reduction_count == 1
+        totals = [oracle.no_sync_accumulate([grads[m][q].float().cpu().numpy() for m in range(micro)])
+                  for q in range(group)]
+        valid = max(0, min(shard, 1857 - rank * shard))
+        expect = oracle.local_share(totals, rank, shard, valid, divisor)
+        assert np.array_equal(out.cpu().numpy().view(np.int32), expect.view(np.int32)), rank
+        assert np.signbit(out[5].item())
+        assert getattr(out, NORM_PARTIALS_ATTR, None) is not None
+        # the accumulator is gone: the next call reduces its own gradients only
+        again = reduce(micro - 1)
+        plain = oracle.local_share([g.float().cpu().numpy() for g in grads[micro - 1]], rank, shard, valid,
+                                   divisor)
+        assert np.array_equal(again.cpu().numpy().view(np.int32), plain.view(np.int32)), rank
+        assert h.reduction_count == 2
 
 
 def test_load_local_pieces_round_trip(device):

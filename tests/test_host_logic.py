@@ -1,5 +1,5 @@
 """Host-only behaviour: error messages, configuration validation, the scaler state
-machine and the oracle's local-share restatement (no GPU)."""
+machine and the oracle's local-share and no_sync restatements (no GPU)."""
 
 from __future__ import annotations
 
@@ -122,6 +122,54 @@ def test_oracle_local_share_against_torch_avg():
             got = oracle.local_share(host, rank, shard, valid, float(group))
             assert np.array_equal(got, summed[rank * shard : (rank + 1) * shard].numpy()), (group, rank)
             assert np.all(got[valid:] == 0.0)
+
+
+def _torch_no_sync(micro):
+    """The reference's own op sequence on CPU (``parallel/fsdp.py:733-749``)."""
+    accumulator = None
+    for g in micro[:-1]:
+        grad = g.to(torch.float32).contiguous()
+        if accumulator is None:
+            accumulator = grad.clone()
+        else:
+            accumulator.add_(grad)
+    grad = micro[-1].to(torch.float32).contiguous()
+    return grad if accumulator is None else grad + accumulator
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("micro", [1, 2, 3, 5])
+def test_oracle_no_sync_accumulate_against_torch(dtype, micro):
+    """Bitwise against torch on CPU, with signed zeros (a copy keeps -0.0 where adding
+    to zeros would not), subnormal sums, overflow to infinity and random values."""
+    gen = torch.Generator().manual_seed(micro)
+    n = 4096
+    grads = []
+    for m in range(micro):
+        g = (torch.randn(n, generator=gen) * 1e-2).to(dtype)
+        g[:8] = -0.0                          # -0.0 in every micro-batch
+        g[8] = 0.0 if m else -0.0             # -0.0 then +0.0: the sum is +0.0
+        g[9] = torch.finfo(dtype).tiny / 4    # subnormal (fp32, fp16) or a tiny normal sum
+        g[10] = torch.finfo(dtype).max        # fp32/bf16: +inf once added twice; fp16: exact in fp32
+        g[11] = -torch.finfo(dtype).max
+        grads.append(g)
+    expect = _torch_no_sync(grads)
+    got = oracle.no_sync_accumulate([g.float().numpy() for g in grads])
+    assert got.dtype == np.float32
+    assert np.array_equal(got.view(np.uint32), expect.numpy().view(np.uint32))
+    if micro > 1:
+        assert np.all(np.signbit(got[:8])) and not np.signbit(got[8])
+        if dtype == torch.float16:
+            # The sum is formed in fp32, where micro * 65504 is exact; fp16 would overflow.
+            assert got[10] == 65504.0 * micro and got[11] == -65504.0 * micro
+        else:
+            assert np.isinf(got[10]) and got[10] > 0 and np.isinf(got[11]) and got[11] < 0
+        # Accumulating onto zeros instead of copying the first micro-batch loses the sign of -0.0.
+        from_zeros = np.zeros(n, dtype=np.float32)
+        with np.errstate(over="ignore"):
+            for g in grads:
+                from_zeros = np.add(from_zeros, g.float().numpy(), dtype=np.float32)
+        assert not np.array_equal(from_zeros.view(np.uint32), got.view(np.uint32))
 
 
 def test_oracle_pack_matches_concatenation():
