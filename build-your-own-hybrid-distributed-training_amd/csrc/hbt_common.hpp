@@ -89,6 +89,23 @@ __device__ __forceinline__ uint32_t f32_to_b16(float x) {
     return f32_to_bf16(x);
 }
 
+// x rounded to dtype RD and widened back to fp32, exactly: unchanged for HBT_DTYPE_F32;
+// round to nearest even for HBT_DTYPE_BF16 and HBT_DTYPE_F16, with the narrowing's
+// overflow and NaN rules above.  This is the value torch holds after an op whose result
+// dtype is RD (the op computed in fp32, then rounded once).
+template <int RD>
+__device__ __forceinline__ float round_to(float x) {
+    if constexpr (RD == HBT_DTYPE_BF16) return bf16_to_f32(f32_to_bf16(x));
+    else if constexpr (RD == HBT_DTYPE_F16) return f16_to_f32(f32_to_f16(x));
+    else return x;
+}
+
+// The dtype code of SB-byte elements (a 2-byte element being fp16 when H, else bf16).
+template <int SB, bool H>
+constexpr int dtype_of() {
+    return SB == 4 ? HBT_DTYPE_F32 : (H ? HBT_DTYPE_F16 : HBT_DTYPE_BF16);
+}
+
 // ---- fixed-order reductions ----------------------------------------------------------
 // Butterfly over the 64 lanes of a wavefront; every lane ends with the same total and
 // the pairing order is fixed, so the result is reproducible bit for bit.

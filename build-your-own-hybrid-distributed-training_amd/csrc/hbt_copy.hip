@@ -392,7 +392,28 @@ __device__ __forceinline__ f32x4 load_quad(const uint8_t* p) {
     }
 }
 
-template <int SB, bool H>
+// The reduce dtype's steps (RD: its dtype code): the gradient cast to RD unless it
+// already has that dtype, each quotient and each partial sum rounded to RD.  For RD = F32
+// every step is the identity.
+template <int RD>
+__device__ __forceinline__ f32x4 share_round4(f32x4 v) {
+    if constexpr (RD == HBT_DTYPE_F32) return v;
+    return f32x4{round_to<RD>(v.x), round_to<RD>(v.y), round_to<RD>(v.z), round_to<RD>(v.w)};
+}
+template <int SB, bool H, int RD>
+__device__ __forceinline__ f32x4 share_input4(const uint8_t* p) {
+    const f32x4 x = load_quad<SB, H>(p);
+    if constexpr (dtype_of<SB, H>() == RD) return x;
+    return share_round4<RD>(x);
+}
+template <int SB, bool H, int RD>
+__device__ __forceinline__ float share_input1(const uint8_t* p) {
+    const float x = elem_to_f32<SB, H>(load_elem<SB>(p));
+    if constexpr (dtype_of<SB, H>() == RD) return x;
+    return round_to<RD>(x);
+}
+
+template <int SB, bool H, int RD>
 __global__ __launch_bounds__(kShareBlock) void local_share_kernel(RankTable ranks, int32_t group_size,
                                                                   int64_t offset, int64_t shard_numel,
                                                                   int64_t valid_numel, float divisor,
@@ -403,9 +424,10 @@ __global__ __launch_bounds__(kShareBlock) void local_share_kernel(RankTable rank
 #pragma unroll
         for (int u = 0; u < kShareGroups; ++u) {
             const int64_t e = base + (int64_t(u) * kShareBlock + threadIdx.x) * 4;
-            f32x4 acc = load_quad<SB, H>(ranks.g[0] + (offset + e) * SB) / divisor;
+            f32x4 acc = share_round4<RD>(share_input4<SB, H, RD>(ranks.g[0] + (offset + e) * SB) / divisor);
             for (int32_t q = 1; q < group_size; ++q) {
-                acc = acc + load_quad<SB, H>(ranks.g[q] + (offset + e) * SB) / divisor;
+                const f32x4 x = share_input4<SB, H, RD>(ranks.g[q] + (offset + e) * SB);
+                acc = share_round4<RD>(acc + share_round4<RD>(x / divisor));
             }
             stv<4>(out + e, u32x4v{__float_as_uint(acc.x), __float_as_uint(acc.y),
                                      __float_as_uint(acc.z), __float_as_uint(acc.w)});
@@ -424,9 +446,9 @@ __global__ __launch_bounds__(kShareBlock) void local_share_kernel(RankTable rank
     for (int64_t i = base + threadIdx.x; i < end; i += kShareBlock) {
         float acc = 0.0f;
         if (i < valid_numel) {
-            acc = elem_to_f32<SB, H>(load_elem<SB>(ranks.g[0] + (offset + i) * SB)) / divisor;
+            acc = round_to<RD>(share_input1<SB, H, RD>(ranks.g[0] + (offset + i) * SB) / divisor);
             for (int32_t q = 1; q < group_size; ++q) {
-                acc = acc + elem_to_f32<SB, H>(load_elem<SB>(ranks.g[q] + (offset + i) * SB)) / divisor;
+                acc = round_to<RD>(acc + round_to<RD>(share_input1<SB, H, RD>(ranks.g[q] + (offset + i) * SB) / divisor));
             }
         }
         out[i] = acc;
@@ -552,7 +574,7 @@ int32_t hbt_copy_intervals(const int64_t* table, int64_t count, int64_t total_ch
 
 int32_t hbt_grad_local_share(const void* const* rank_grads, int32_t group_size, int32_t rank,
                              int64_t shard_numel, int64_t valid_numel, int32_t in_dtype,
-                             float divisor, float* out, void* stream) {
+                             int32_t reduce_dtype, float divisor, float* out, void* stream) {
     clear_error();
     if (rank_grads == nullptr || out == nullptr || group_size < 1 ||
         group_size > HBT_MAX_LOCAL_RANKS || rank < 0 || rank >= group_size || shard_numel < 0 ||
@@ -564,6 +586,10 @@ int32_t hbt_grad_local_share(const void* const* rank_grads, int32_t group_size, 
     }
     if (in_dtype != HBT_DTYPE_F32 && in_dtype != HBT_DTYPE_BF16 && in_dtype != HBT_DTYPE_F16) {
         set_error("hbt_grad_local_share: input dtype %d is not F32, BF16 or F16", in_dtype);
+        return HBT_ERR_INVALID_ARGUMENT;
+    }
+    if (reduce_dtype != HBT_DTYPE_F32 && reduce_dtype != HBT_DTYPE_BF16 && reduce_dtype != HBT_DTYPE_F16) {
+        set_error("hbt_grad_local_share: reduce dtype %d is not F32, BF16 or F16", reduce_dtype);
         return HBT_ERR_INVALID_ARGUMENT;
     }
     RankTable ranks{};
@@ -591,16 +617,24 @@ int32_t hbt_grad_local_share(const void* const* rank_grads, int32_t group_size, 
     }
     hipStream_t s = as_stream(stream);
     const dim3 grid(static_cast<unsigned>(tiles));
+#define HBT_SHARE(SB, H, RD)                                                                       \
+    local_share_kernel<SB, H, RD><<<grid, kShareBlock, 0, s>>>(ranks, group_size, offset, shard_numel,  \
+                                                               valid_numel, divisor, vec_ok, out)
+#define HBT_SHARE_RD(SB, H)                                                    \
+    do {                                                                       \
+        if (reduce_dtype == HBT_DTYPE_F32) HBT_SHARE(SB, H, HBT_DTYPE_F32);     \
+        else if (reduce_dtype == HBT_DTYPE_BF16) HBT_SHARE(SB, H, HBT_DTYPE_BF16); \
+        else HBT_SHARE(SB, H, HBT_DTYPE_F16);                                  \
+    } while (0)
     if (in_dtype == HBT_DTYPE_F32) {
-        local_share_kernel<4, false><<<grid, kShareBlock, 0, s>>>(ranks, group_size, offset, shard_numel,
-                                                                   valid_numel, divisor, vec_ok, out);
+        HBT_SHARE_RD(4, false);
     } else if (in_dtype == HBT_DTYPE_BF16) {
-        local_share_kernel<2, false><<<grid, kShareBlock, 0, s>>>(ranks, group_size, offset, shard_numel,
-                                                                   valid_numel, divisor, vec_ok, out);
+        HBT_SHARE_RD(2, false);
     } else {
-        local_share_kernel<2, true><<<grid, kShareBlock, 0, s>>>(ranks, group_size, offset, shard_numel,
-                                                                  valid_numel, divisor, vec_ok, out);
+        HBT_SHARE_RD(2, true);
     }
+#undef HBT_SHARE_RD
+#undef HBT_SHARE
     return check_launch("hbt_grad_local_share");
 }
 

@@ -380,11 +380,32 @@ __device__ __forceinline__ f32x4 share_load4(const uint8_t* p) {
     }
 }
 
+// The reduce dtype's steps of the reference's AVG reduce-scatter (RD: the dtype code).
+// The gradient is cast to RD unless it already has that dtype (Tensor.to), each
+// division and each addition is rounded to RD (torch computes them in fp32 and rounds
+// once), and the result widens exactly to the fp32 master.  For RD = F32 every step is
+// the identity, so the fp32 instantiations are the plain fp32 local share.
+template <int RD>
+__device__ __forceinline__ f32x4 round4(f32x4 v) {
+    if constexpr (RD == HBT_DTYPE_F32) return v;
+    return f32x4{round_to<RD>(v.x), round_to<RD>(v.y), round_to<RD>(v.z), round_to<RD>(v.w)};
+}
+template <int SB, bool H, int RD>
+__device__ __forceinline__ f32x4 share_cast4(f32x4 x) {
+    if constexpr (dtype_of<SB, H>() == RD) return x;
+    return round4<RD>(x);
+}
+template <int SB, bool H, int RD>
+__device__ __forceinline__ float share_cast1(float x) {
+    if constexpr (dtype_of<SB, H>() == RD) return x;
+    return round_to<RD>(x);
+}
+
 // One wave per 256-element tile: measured on MI355X (8 bf16 ranks -> fp32) this
 // short-lived shape streams at 6.4 TB/s, against 5.6 TB/s for the norm kernel's
 // 1024-thread, 8-tile workgroups.  kG > 0 fixes the group size so that every rank's
 // load is issued before the first is used; kG == 0 reads group_size at run time.
-template <int SB, int kG, bool kRecip, bool H>
+template <int SB, int kG, bool kRecip, bool H, int RD>
 __global__ __launch_bounds__(kShareBlock) void local_share_tiles_kernel(
     ShareRanks ranks, int32_t group_size, int64_t offset, int64_t shard_numel, int64_t valid_numel,
     float divisor, float recip, int32_t vec_ok, float* __restrict__ out, double* __restrict__ tile_sums) {
@@ -397,13 +418,17 @@ __global__ __launch_bounds__(kShareBlock) void local_share_tiles_kernel(
             f32x4 x[kG];
 #pragma unroll
             for (int q = 0; q < kG; ++q) x[q] = share_load4<SB, H>(ranks.g[q] + (offset + e) * SB);
-            sum = share_div<kRecip>(x[0], divisor, recip);
+            sum = round4<RD>(share_div<kRecip>(share_cast4<SB, H, RD>(x[0]), divisor, recip));
 #pragma unroll
-            for (int q = 1; q < kG; ++q) sum = sum + share_div<kRecip>(x[q], divisor, recip);
+            for (int q = 1; q < kG; ++q) {
+                sum = round4<RD>(sum + round4<RD>(share_div<kRecip>(share_cast4<SB, H, RD>(x[q]), divisor, recip)));
+            }
         } else {
-            sum = share_div<kRecip>(share_load4<SB, H>(ranks.g[0] + (offset + e) * SB), divisor, recip);
+            sum = round4<RD>(share_div<kRecip>(
+                share_cast4<SB, H, RD>(share_load4<SB, H>(ranks.g[0] + (offset + e) * SB)), divisor, recip));
             for (int32_t q = 1; q < group_size; ++q) {
-                sum = sum + share_div<kRecip>(share_load4<SB, H>(ranks.g[q] + (offset + e) * SB), divisor, recip);
+                const f32x4 x = share_cast4<SB, H, RD>(share_load4<SB, H>(ranks.g[q] + (offset + e) * SB));
+                sum = round4<RD>(sum + round4<RD>(share_div<kRecip>(x, divisor, recip)));
             }
         }
         st4_nt(out + e, sum);
@@ -418,9 +443,11 @@ __global__ __launch_bounds__(kShareBlock) void local_share_tiles_kernel(
         for (int64_t e = base + threadIdx.x; e < end; e += kShareBlock) {
             float v = 0.0f;
             if (e < valid_numel) {
-                v = share_div1<kRecip>(share_load1<SB, H>(ranks.g[0] + (offset + e) * SB), divisor, recip);
+                v = round_to<RD>(share_div1<kRecip>(
+                    share_cast1<SB, H, RD>(share_load1<SB, H>(ranks.g[0] + (offset + e) * SB)), divisor, recip));
                 for (int32_t q = 1; q < group_size; ++q) {
-                    v = v + share_div1<kRecip>(share_load1<SB, H>(ranks.g[q] + (offset + e) * SB), divisor, recip);
+                    const float x = share_cast1<SB, H, RD>(share_load1<SB, H>(ranks.g[q] + (offset + e) * SB));
+                    v = round_to<RD>(v + round_to<RD>(share_div1<kRecip>(x, divisor, recip)));
                 }
             }
             out[e] = v;
@@ -574,13 +601,15 @@ __global__ __launch_bounds__(kScaleBlock) void scale_kernel(ScaleTable tab, floa
 }
 
 // ---- no_sync gradient accumulation ----------------------------------------------------
-// acc = acc + fp32(grad): one fp32 addition per element, the gradient widened exactly.
-// The scale kernel's shape: half-wave workgroups, two 4-element vectors of the
-// accumulator per lane, 256 accumulator elements per workgroup.
+// acc = R(acc + R(grad)), R rounding to the accumulator's dtype (the reduce dtype): the
+// gradient's cast to that dtype (Tensor.to) and one addition computed in fp32 and
+// rounded once (add_).  kAssign writes R(grad) instead: the first micro-batch's clone.
+// The scale kernel's shape: half-wave workgroups, two 4-element vectors per lane,
+// 256 accumulator elements per workgroup.
 constexpr int64_t kAccumTile = int64_t(kScaleBlock) * 2 * 4;
 
 struct AccumTable {
-    float* acc[kMaxT];
+    void* acc[kMaxT];
     const void* grad[kMaxT];
     int64_t n[kMaxT];
     int64_t first_block[kMaxT + 1];
@@ -588,10 +617,10 @@ struct AccumTable {
     int32_t count;
 };
 
-// Four gradient elements of SB bytes each (fp32, or bf16 / fp16 when H), widened.
-template <int SB, bool H>
-__device__ __forceinline__ f32x4 load_grad4(const unsigned char* p) {
-    if constexpr (SB == 4) {
+// Four elements of B bytes each (fp32, or bf16 / fp16 when H), widened exactly.
+template <int B, bool H>
+__device__ __forceinline__ f32x4 load4_as_f32(const unsigned char* p) {
+    if constexpr (B == 4) {
         return ld4_nt(reinterpret_cast<const float*>(p));
     } else {
         const u32x2 w = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
@@ -599,42 +628,75 @@ __device__ __forceinline__ f32x4 load_grad4(const unsigned char* p) {
                      b16_to_f32<H>(w.y >> 16)};
     }
 }
-template <int SB, bool H>
-__device__ __forceinline__ float load_grad1(const unsigned char* p, int64_t i) {
-    if constexpr (SB == 4) return reinterpret_cast<const float*>(p)[i];
+// Four values already representable in the B-byte dtype, stored in it.
+template <int B, bool H>
+__device__ __forceinline__ void store4_from_f32(unsigned char* p, f32x4 v) {
+    if constexpr (B == 4) {
+        st4_nt(reinterpret_cast<float*>(p), v);
+    } else {
+        const u32x2 w{f32_to_b16<H>(v.x) | (f32_to_b16<H>(v.y) << 16), f32_to_b16<H>(v.z) | (f32_to_b16<H>(v.w) << 16)};
+        __builtin_nontemporal_store(w, reinterpret_cast<u32x2*>(p));
+    }
+}
+template <int B, bool H>
+__device__ __forceinline__ float load1_as_f32(const unsigned char* p, int64_t i) {
+    if constexpr (B == 4) return reinterpret_cast<const float*>(p)[i];
     return b16_to_f32<H>(reinterpret_cast<const uint16_t*>(p)[i]);
 }
+template <int B, bool H>
+__device__ __forceinline__ void store1_from_f32(unsigned char* p, int64_t i, float v) {
+    if constexpr (B == 4) {
+        reinterpret_cast<float*>(p)[i] = v;
+    } else {
+        reinterpret_cast<uint16_t*>(p)[i] = static_cast<uint16_t>(f32_to_b16<H>(v));
+    }
+}
 
-template <int SB, bool H>
+// SB/SH: the gradient's element size and fp16 flag; AB/AH: the accumulator's.
+template <int SB, bool SH, int AB, bool AH, bool kAssign>
 __global__ __launch_bounds__(kScaleBlock) void accumulate_kernel(AccumTable tab) {
+    constexpr int RD = dtype_of<AB, AH>();
     const int64_t block = blockIdx.x;
     int t = 0;
     while (t + 1 < tab.count && block >= tab.first_block[t + 1]) ++t;
     const int64_t base = (block - tab.first_block[t]) * kAccumTile;
     const int64_t n = tab.n[t];
-    float* __restrict__ acc = tab.acc[t];
+    unsigned char* __restrict__ acc = static_cast<unsigned char*>(tab.acc[t]);
     const unsigned char* __restrict__ grad = static_cast<const unsigned char*>(tab.grad[t]);
     if (tab.vec_ok[t] && base + kAccumTile <= n) {
         f32x4 a[2], g[2];
-        float* p[2];
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             const int64_t i = base + (int64_t(u) * kScaleBlock + threadIdx.x) * 4;
-            p[u] = acc + i;
-            g[u] = load_grad4<SB, H>(grad + i * SB);
+            g[u] = share_cast4<SB, SH, RD>(load4_as_f32<SB, SH>(grad + i * SB));
+        }
+        if constexpr (!kAssign) {
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int64_t i = base + (int64_t(u) * kScaleBlock + threadIdx.x) * 4;
+                a[u] = load4_as_f32<AB, AH>(acc + i * AB);
+            }
         }
 #pragma unroll
-        for (int u = 0; u < 2; ++u) a[u] = ld4_nt(p[u]);
-#pragma unroll
         for (int u = 0; u < 2; ++u) {
-#pragma unroll
-            for (int c = 0; c < 4; ++c) a[u][c] = a[u][c] + g[u][c];
-            st4_nt(p[u], a[u]);
+            const int64_t i = base + (int64_t(u) * kScaleBlock + threadIdx.x) * 4;
+            if constexpr (kAssign) {
+                store4_from_f32<AB, AH>(acc + i * AB, g[u]);
+            } else {
+                store4_from_f32<AB, AH>(acc + i * AB, round4<RD>(a[u] + g[u]));
+            }
         }
         return;
     }
     const int64_t end = base + kAccumTile < n ? base + kAccumTile : n;
-    for (int64_t i = base + threadIdx.x; i < end; i += kScaleBlock) acc[i] = acc[i] + load_grad1<SB, H>(grad, i);
+    for (int64_t i = base + threadIdx.x; i < end; i += kScaleBlock) {
+        const float g = share_cast1<SB, SH, RD>(load1_as_f32<SB, SH>(grad, i));
+        if constexpr (kAssign) {
+            store1_from_f32<AB, AH>(acc, i, g);
+        } else {
+            store1_from_f32<AB, AH>(acc, i, round_to<RD>(load1_as_f32<AB, AH>(acc, i) + g));
+        }
+    }
 }
 
 inline bool aligned(const void* ptr, uintptr_t bytes) {
@@ -860,19 +922,28 @@ int32_t hbt_scale_inplace(void* const* tensors, const int64_t* numels, int32_t c
     return check_launch("hbt_scale_inplace");
 }
 
-int32_t hbt_grad_accumulate(float* const* accumulators, const void* const* grads, const int64_t* numels,
-                            int32_t count, int32_t grad_dtype, void* stream) {
+int32_t hbt_grad_accumulate(void* const* accumulators, const void* const* grads, const int64_t* numels,
+                            int32_t count, int32_t acc_dtype, int32_t grad_dtype, int32_t flags, void* stream) {
     clear_error();
     if (count < 0 || count > kMaxT ||
         (count > 0 && (accumulators == nullptr || grads == nullptr || numels == nullptr))) {
         set_error("hbt_grad_accumulate: bad table (count=%d)", count);
         return HBT_ERR_INVALID_ARGUMENT;
     }
-    if (grad_dtype != HBT_DTYPE_F32 && grad_dtype != HBT_DTYPE_BF16 && grad_dtype != HBT_DTYPE_F16) {
-        set_error("hbt_grad_accumulate: gradient dtype %d is not F32, BF16 or F16", grad_dtype);
+    const auto float_code = [](int32_t d) {
+        return d == HBT_DTYPE_F32 || d == HBT_DTYPE_BF16 || d == HBT_DTYPE_F16;
+    };
+    if (!float_code(acc_dtype) || !float_code(grad_dtype)) {
+        set_error("hbt_grad_accumulate: dtypes (accumulator %d, gradient %d) must be F32, BF16 or F16",
+                  acc_dtype, grad_dtype);
         return HBT_ERR_INVALID_ARGUMENT;
     }
-    const int grad_bytes = dtype_size(grad_dtype);
+    if ((flags & ~HBT_ACCUMULATE_ASSIGN) != 0) {
+        set_error("hbt_grad_accumulate: unknown flags 0x%x", static_cast<unsigned>(flags));
+        return HBT_ERR_INVALID_ARGUMENT;
+    }
+    const uintptr_t acc_bytes = static_cast<uintptr_t>(dtype_size(acc_dtype));
+    const uintptr_t grad_bytes = static_cast<uintptr_t>(dtype_size(grad_dtype));
     AccumTable tab{};
     tab.count = count;
     int64_t blocks = 0;
@@ -884,7 +955,7 @@ int32_t hbt_grad_accumulate(float* const* accumulators, const void* const* grads
         tab.acc[i] = accumulators[i];
         tab.grad[i] = grads[i];
         tab.n[i] = numels[i];
-        tab.vec_ok[i] = aligned(accumulators[i], 16) && aligned(grads[i], 4 * static_cast<uintptr_t>(grad_bytes));
+        tab.vec_ok[i] = aligned(accumulators[i], 4 * acc_bytes) && aligned(grads[i], 4 * grad_bytes);
         tab.first_block[i] = blocks;
         blocks += (numels[i] + kAccumTile - 1) / kAccumTile;
     }
@@ -896,21 +967,36 @@ int32_t hbt_grad_accumulate(float* const* accumulators, const void* const* grads
         return HBT_ERR_UNSUPPORTED;
     }
     const dim3 grid(static_cast<unsigned>(blocks));
+    hipStream_t st = as_stream(stream);
+    const bool assign = (flags & HBT_ACCUMULATE_ASSIGN) != 0;
+#define HBT_ACC(SB, SH, AB, AH)                                                                    \
+    do {                                                                                           \
+        if (assign) accumulate_kernel<SB, SH, AB, AH, true><<<grid, kScaleBlock, 0, st>>>(tab);    \
+        else accumulate_kernel<SB, SH, AB, AH, false><<<grid, kScaleBlock, 0, st>>>(tab);          \
+    } while (0)
+#define HBT_ACC_A(SB, SH)                                                          \
+    do {                                                                           \
+        if (acc_dtype == HBT_DTYPE_F32) HBT_ACC(SB, SH, 4, false);                  \
+        else if (acc_dtype == HBT_DTYPE_BF16) HBT_ACC(SB, SH, 2, false);            \
+        else HBT_ACC(SB, SH, 2, true);                                             \
+    } while (0)
     if (grad_dtype == HBT_DTYPE_F32) {
-        accumulate_kernel<4, false><<<grid, kScaleBlock, 0, as_stream(stream)>>>(tab);
+        HBT_ACC_A(4, false);
     } else if (grad_dtype == HBT_DTYPE_BF16) {
-        accumulate_kernel<2, false><<<grid, kScaleBlock, 0, as_stream(stream)>>>(tab);
+        HBT_ACC_A(2, false);
     } else {
-        accumulate_kernel<2, true><<<grid, kScaleBlock, 0, as_stream(stream)>>>(tab);
+        HBT_ACC_A(2, true);
     }
+#undef HBT_ACC_A
+#undef HBT_ACC
     return check_launch("hbt_grad_accumulate");
 }
 
 
 int32_t hbt_grad_local_share_sqnorm(const void* const* rank_grads, int32_t group_size, int32_t rank,
                                     int64_t shard_numel, int64_t valid_numel, int32_t in_dtype,
-                                    float divisor, float* out, double* partials, double* tile_scratch,
-                                    void* stream) {
+                                    int32_t reduce_dtype, float divisor, float* out, double* partials,
+                                    double* tile_scratch, void* stream) {
     clear_error();
     if (rank_grads == nullptr || out == nullptr || partials == nullptr || tile_scratch == nullptr ||
         group_size < 1 || group_size > HBT_MAX_LOCAL_RANKS || rank < 0 || rank >= group_size ||
@@ -921,6 +1007,10 @@ int32_t hbt_grad_local_share_sqnorm(const void* const* rank_grads, int32_t group
     }
     if (in_dtype != HBT_DTYPE_F32 && in_dtype != HBT_DTYPE_BF16 && in_dtype != HBT_DTYPE_F16) {
         set_error("hbt_grad_local_share_sqnorm: input dtype %d is not F32, BF16 or F16", in_dtype);
+        return HBT_ERR_INVALID_ARGUMENT;
+    }
+    if (reduce_dtype != HBT_DTYPE_F32 && reduce_dtype != HBT_DTYPE_BF16 && reduce_dtype != HBT_DTYPE_F16) {
+        set_error("hbt_grad_local_share_sqnorm: reduce dtype %d is not F32, BF16 or F16", reduce_dtype);
         return HBT_ERR_INVALID_ARGUMENT;
     }
     ShareRanks ranks{};
@@ -951,26 +1041,39 @@ int32_t hbt_grad_local_share_sqnorm(const void* const* rank_grads, int32_t group
     const float recip = exact_reciprocal(divisor);
     const bool recip_exact = recip != 0.0f;
     const dim3 grid(static_cast<unsigned>(tiles));
-#define HBT_TILES(SBYTES, G, R, H)                                                              \
-    local_share_tiles_kernel<SBYTES, G, R, H><<<grid, kShareBlock, 0, st>>>(                      \
+#define HBT_TILES(SBYTES, G, R, H, RD)                                                          \
+    local_share_tiles_kernel<SBYTES, G, R, H, RD><<<grid, kShareBlock, 0, st>>>(                  \
         ranks, group_size, offset, shard_numel, valid_numel, divisor, recip, vec_ok, out, tile_scratch)
-#define HBT_TILES_G(SBYTES, R, H)                            \
-    do {                                                     \
-        switch (group_size) {                                \
-            case 1: HBT_TILES(SBYTES, 1, R, H); break;       \
-            case 2: HBT_TILES(SBYTES, 2, R, H); break;       \
-            case 4: HBT_TILES(SBYTES, 4, R, H); break;       \
-            case 8: HBT_TILES(SBYTES, 8, R, H); break;       \
-            default: HBT_TILES(SBYTES, 0, R, H); break;      \
-        }                                                    \
+#define HBT_TILES_G(SBYTES, R, H)                                          \
+    do {                                                                   \
+        switch (group_size) {                                              \
+            case 1: HBT_TILES(SBYTES, 1, R, H, HBT_DTYPE_F32); break;      \
+            case 2: HBT_TILES(SBYTES, 2, R, H, HBT_DTYPE_F32); break;      \
+            case 4: HBT_TILES(SBYTES, 4, R, H, HBT_DTYPE_F32); break;      \
+            case 8: HBT_TILES(SBYTES, 8, R, H, HBT_DTYPE_F32); break;      \
+            default: HBT_TILES(SBYTES, 0, R, H, HBT_DTYPE_F32); break;     \
+        }                                                                  \
+    } while (0)
+// A 2-byte reduce dtype runs the run-time group size kernel only: the fp32 reduction
+// is the configuration the group-size specialisations were tuned for.
+#define HBT_TILES_RD(SBYTES, R, H)                                                            \
+    do {                                                                                      \
+        if (reduce_dtype == HBT_DTYPE_F32) {                                                  \
+            HBT_TILES_G(SBYTES, R, H);                                                        \
+        } else if (reduce_dtype == HBT_DTYPE_BF16) {                                          \
+            HBT_TILES(SBYTES, 0, R, H, HBT_DTYPE_BF16);                                       \
+        } else {                                                                              \
+            HBT_TILES(SBYTES, 0, R, H, HBT_DTYPE_F16);                                        \
+        }                                                                                     \
     } while (0)
     if (in_dtype == HBT_DTYPE_F32) {
-        if (recip_exact) HBT_TILES_G(4, true, false); else HBT_TILES_G(4, false, false);
+        if (recip_exact) HBT_TILES_RD(4, true, false); else HBT_TILES_RD(4, false, false);
     } else if (in_dtype == HBT_DTYPE_BF16) {
-        if (recip_exact) HBT_TILES_G(2, true, false); else HBT_TILES_G(2, false, false);
+        if (recip_exact) HBT_TILES_RD(2, true, false); else HBT_TILES_RD(2, false, false);
     } else {
-        if (recip_exact) HBT_TILES_G(2, true, true); else HBT_TILES_G(2, false, true);
+        if (recip_exact) HBT_TILES_RD(2, true, true); else HBT_TILES_RD(2, false, true);
     }
+#undef HBT_TILES_RD
 #undef HBT_TILES_G
 #undef HBT_TILES
     const hipError_t launched = hipGetLastError();

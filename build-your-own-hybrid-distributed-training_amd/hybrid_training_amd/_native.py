@@ -26,6 +26,7 @@ from .errors import NativeKernelError, UnsupportedFeatureError, format_error
 
 __all__ = [
     "ABI_VERSION",
+    "ACCUMULATE_ASSIGN",
     "COPY_ALIGNED",
     "COPY_CONVERSIONS",
     "COPY_OP_COPY",
@@ -51,7 +52,7 @@ __all__ = [
     "stream_of",
 ]
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 MAX_TENSORS_PER_LAUNCH = 16
 MAX_LOCAL_RANKS = 64
 
@@ -63,6 +64,7 @@ DTYPE_F64 = 3
 COPY_OP_COPY = 0
 COPY_OP_DIVIDE = 1
 COPY_ALIGNED = 1
+ACCUMULATE_ASSIGN = 1
 _CODE_BYTES = {DTYPE_F32: 4, DTYPE_BF16: 2, DTYPE_F16: 2, DTYPE_F64: 8}
 
 #: Dtype pairs ``hbt_copy_intervals`` converts between (same-dtype copies are bit copies).
@@ -120,18 +122,21 @@ EXPORTED_SYMBOLS: dict[str, tuple[object, tuple[object, ...]]] = {
     ),
     "hbt_grad_local_share": (
         _c_i32,
-        (_ptr_array, _c_i32, _c_i32, _c_i64, _c_i64, _c_i32, _c_f32, _c_void_p, _c_void_p),
+        (_ptr_array, _c_i32, _c_i32, _c_i64, _c_i64, _c_i32, _c_i32, _c_f32, _c_void_p, _c_void_p),
     ),
     "hbt_grad_local_share_sqnorm": (
         _c_i32,
-        (_ptr_array, _c_i32, _c_i32, _c_i64, _c_i64, _c_i32, _c_f32, _c_void_p, _c_void_p, _c_void_p,
-         _c_void_p),
+        (_ptr_array, _c_i32, _c_i32, _c_i64, _c_i64, _c_i32, _c_i32, _c_f32, _c_void_p, _c_void_p,
+         _c_void_p, _c_void_p),
     ),
     "hbt_scale_inplace": (
         _c_i32,
         (_ptr_array, _i64_array, _c_i32, _c_i32, _c_f32, _c_void_p, _c_void_p),
     ),
-    "hbt_grad_accumulate": (_c_i32, (_ptr_array, _ptr_array, _i64_array, _c_i32, _c_i32, _c_void_p)),
+    "hbt_grad_accumulate": (
+        _c_i32,
+        (_ptr_array, _ptr_array, _i64_array, _c_i32, _c_i32, _c_i32, _c_i32, _c_void_p),
+    ),
 }
 
 _LOCK = threading.Lock()

@@ -10,10 +10,12 @@ tensor work is the interval gather-copy kernel and the local-share kernel of
   into the shard, casting to the master dtype and zero-filling padding, in one
   launch; the reference materialises the whole padded buffer first and slices it.
 * ``reduce_scatter_gradient`` is the rank's local share of the AVG reduce-scatter:
-  cast to fp32, divide by ``G``, sum over the ranks' buffers in rank order, zero
-  the padding tail, and in the same pass the squared-norm partials of the result,
-  which the next ``clip_grad_norm`` picks up instead of reading the shard again
-  (one launch).  There are no collectives: a group of size 1 is
+  cast to the reduce dtype (fp32, bf16 or fp16), divide by ``G`` and sum over the
+  ranks' buffers in rank order with every step rounded to that dtype, widen to the
+  fp32 master, zero the padding tail, and in the same pass the squared-norm partials
+  of the result, which the next ``clip_grad_norm`` picks up instead of reading the
+  shard again (one launch).  Inside ``no_sync`` it accumulates the gradients in the
+  reduce dtype instead.  There are no collectives: a group of size 1 is
   the whole job; a :meth:`GroupHandle.local_view` group needs the other ranks'
   buffers resident on this device (``peer_grads``), as the stand-in for the
   reduce-scatter.
@@ -497,18 +499,23 @@ class FlatParamHandle:
         ``grad_full`` is this rank's padded full gradient.  With a group of size 1
         that is all there is; otherwise ``peer_grads`` must hold every rank's padded
         gradient (``grad_full`` among them, in rank order), summed in rank order.
+        The gradients are cast to the reduce dtype (float32, bfloat16 or float16), and
+        the AVG divide and the sum are rounded to it, as the reference's ops in that
+        dtype are (``collectives.py:593-594``); the result widens to the fp32 master.
 
         Inside ``no_sync`` (:meth:`set_accumulate_without_reduction`) the gradients
-        are accumulated instead and ``None`` is returned (``fsdp.py:738-745``): the
-        first call keeps a copy of each, later calls add to it in fp32.  The next call
-        outside ``no_sync`` adds its gradients to the accumulated ones and reduces the
-        sums (``fsdp.py:747-749``).
+        are accumulated in the reduce dtype instead and ``None`` is returned
+        (``fsdp.py:738-745``): the first call keeps a copy of each, later calls add to
+        it.  The next call outside ``no_sync`` adds its gradients to the accumulated
+        ones and reduces the sums (``fsdp.py:747-749``).
         """
-        if self._reduce_dtype != torch.float32 or self._master_dtype != torch.float32:
+        if self._reduce_dtype not in (torch.float32, torch.bfloat16, torch.float16) \
+                or self._master_dtype != torch.float32:
             raise UnsupportedFeatureError(
                 format_error(
                     "fsdp.reduce_scatter_gradient",
-                    "the local-share kernel reduces in float32 into a float32 master shard",
+                    "the local-share kernel reduces in float32, bfloat16 or float16 into a float32 "
+                    "master shard",
                     observed=f"reduce {self._reduce_dtype}, master {self._master_dtype}",
                 )
             )
@@ -566,6 +573,7 @@ class FlatParamHandle:
                 self._shard_numel,
                 valid,
                 _native.dtype_code(grads[0].dtype),
+                _native.dtype_code(self._reduce_dtype),
                 divisor,
                 out.data_ptr(),
                 partials.data_ptr(),
@@ -586,19 +594,17 @@ class FlatParamHandle:
 
     def _accumulate(self, grads: Sequence[torch.Tensor], start: int) -> None:
         """Add every rank's gradient, restricted to this rank's slice, into the
-        accumulator (``fsdp.py:738-749``): a copy on the first call (``clone``, which
-        keeps -0.0), then one fp32 addition per element (``add_``)."""
+        accumulator in the reduce dtype (``fsdp.py:738-749``): the cast gradient itself
+        on the first call (``clone``, which keeps -0.0), then one addition per element
+        rounded to the reduce dtype (``add_``)."""
         shard = self._shard_numel
+        flags = 0
         if self._grad_accumulator is None:
-            # Rows start on 256-byte boundaries so both kernels take their vector paths.
+            # Rows start on 64-element boundaries so both kernels take their vector paths.
             stride = -(-shard // 64) * 64
-            accumulator = torch.empty((len(grads), stride), dtype=torch.float32, device=self._device)[:, :shard]
-            plan = _native.CopyPlan(self._device)
-            for q, g in enumerate(grads):
-                plan.add(g, start, accumulator[q], 0, shard)
-            plan.run(src_dtype=grads[0].dtype, dst_dtype=torch.float32)
-            self._grad_accumulator = accumulator
-            return
+            self._grad_accumulator = torch.empty((len(grads), stride), dtype=self._reduce_dtype,
+                                                 device=self._device)[:, :shard]
+            flags = _native.ACCUMULATE_ASSIGN
         accumulator = self._grad_accumulator
         lib = _native.library()
         step = _native.MAX_TENSORS_PER_LAUNCH
@@ -611,7 +617,9 @@ class FlatParamHandle:
                     _native.pointer_array([grads[q].data_ptr() + offset_bytes for q in rows]),
                     _native.int64_array([shard] * len(rows)),
                     len(rows),
+                    _native.dtype_code(self._reduce_dtype),
                     _native.dtype_code(grads[0].dtype),
+                    flags,
                     _native.stream_of(self._device),
                 )
                 _native.check(status, "fsdp.hbt_grad_accumulate")

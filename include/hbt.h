@@ -31,7 +31,7 @@ extern "C" {
 /* ---- element types ----------------------------------------------------------- */
 #define HBT_DTYPE_F32 0
 #define HBT_DTYPE_BF16 1
-#define HBT_DTYPE_F16 2 /* copies, F32 <-> F16 casts and division; local-share and accumulate input */
+#define HBT_DTYPE_F16 2 /* copies, F32 <-> F16 casts and division; local-share, reduce and accumulate dtype */
 #define HBT_DTYPE_F64 3 /* byte copies only */
 
 /* ---- per-call limits ---------------------------------------------------------- */
@@ -202,17 +202,21 @@ int32_t hbt_copy_intervals(const int64_t* table, int64_t count, int64_t total_ch
  * in_dtype F32, BF16 or F16) of one rank, all resident on this device.  Only elements
  * [rank*shard_numel, (rank+1)*shard_numel) of each are read, so a caller holding just
  * those slices (as the no_sync accumulator does) passes them with rank 0.  Writes the
- * fp32 shard of `rank`:
- *   out[i] = sum over q = 0..group_size-1, in that order, of
- *            fp32(rank_grads[q][rank*shard_numel + i]) / divisor
- * (divisor = G for AVG, 1 for SUM), then +0.0 for i >= valid_numel (the padding tail).
- * With group_size == 1 this is the whole local share of one rank: cast to the fp32
- * reduce dtype, AVG pre-divide, cast to the fp32 master dtype, zero padding.
+ * fp32 shard of `rank`, reducing in `reduce_dtype` (F32, BF16 or F16), with R rounding
+ * to it (round to nearest even; the identity for F32):
+ *   x_q    = R(rank_grads[q][rank*shard_numel + i])   (the cast; none if in_dtype ==
+ *                                                      reduce_dtype)
+ *   out[i] = R(...R(R(x_0 / divisor) + R(x_1 / divisor)) + ... + R(x_{G-1} / divisor))
+ * in rank order, each quotient and sum computed in fp32 and rounded once, as torch's
+ * ops in that dtype give (divisor = G for AVG, 1 for SUM); then the exact widening to
+ * the fp32 master, and +0.0 for i >= valid_numel (the padding tail).  With
+ * group_size == 1 this is the whole local share of one rank: cast to the reduce
+ * dtype, AVG pre-divide, cast to the fp32 master dtype, zero padding.
  * ---------------------------------------------------------------------------- */
 #define HBT_MAX_LOCAL_RANKS 64
 int32_t hbt_grad_local_share(const void* const* rank_grads, int32_t group_size, int32_t rank,
                              int64_t shard_numel, int64_t valid_numel, int32_t in_dtype,
-                             float divisor, float* out, void* stream);
+                             int32_t reduce_dtype, float divisor, float* out, void* stream);
 
 /* ------------------------------------------------------------------------------
  * FSDP gradient local share fused with the squared-norm partials of its output.
@@ -232,25 +236,30 @@ int32_t hbt_grad_local_share(const void* const* rank_grads, int32_t group_size, 
  * ---------------------------------------------------------------------------- */
 int32_t hbt_grad_local_share_sqnorm(const void* const* rank_grads, int32_t group_size, int32_t rank,
                                     int64_t shard_numel, int64_t valid_numel, int32_t in_dtype,
-                                    float divisor, float* out, double* partials, double* tile_scratch,
-                                    void* stream);
+                                    int32_t reduce_dtype, float divisor, float* out, double* partials,
+                                    double* tile_scratch, void* stream);
 
 /* ------------------------------------------------------------------------------
- * FSDP no_sync gradient accumulation: acc = acc + fp32(grad), element by element,
- * over up to HBT_MAX_TENSORS_PER_LAUNCH (accumulator, gradient) pairs.
+ * FSDP no_sync gradient accumulation over up to HBT_MAX_TENSORS_PER_LAUNCH
+ * (accumulator, gradient) pairs.
  *
  * Replaces: the accumulate branch of FlatParamHandle.reduce_scatter_gradient
- *   (parallel/fsdp.py:733-749): grad.to(reduce_dtype) followed by
- *   accumulator.add_(grad) inside no_sync(), and the synchronising call's
- *   grad + accumulator before the reduce-scatter.
+ *   (parallel/fsdp.py:733-749): grad.to(reduce_dtype), then accumulator =
+ *   grad.clone() on the first micro-batch inside no_sync() and accumulator.add_(grad)
+ *   on later ones, and the synchronising call's grad + accumulator before the
+ *   reduce-scatter.
  * `accumulators` and `grads` are HOST arrays of `count` device addresses.  Accumulator
- * k holds numels[k] fp32 elements; gradient k holds as many elements of grad_dtype
- * (F32, BF16 or F16).  The widening is exact and the sum is one fp32 addition rounded
- * to nearest even, as torch's fp32 add_ gives.  A gradient must not overlap its
- * accumulator.
+ * k holds numels[k] elements of acc_dtype (the reduce dtype); gradient k as many of
+ * grad_dtype (each F32, BF16 or F16).  With R rounding to acc_dtype (round to nearest
+ * even; the identity for F32), each element becomes
+ *   acc = R(grad)                    with HBT_ACCUMULATE_ASSIGN (the clone; no read of acc)
+ *   acc = R(acc + R(grad))           otherwise (the sum computed in fp32, rounded once)
+ * where R(grad) is the cast (none when the dtypes match).  A gradient must not overlap
+ * its accumulator.
  * ---------------------------------------------------------------------------- */
-int32_t hbt_grad_accumulate(float* const* accumulators, const void* const* grads, const int64_t* numels,
-                            int32_t count, int32_t grad_dtype, void* stream);
+#define HBT_ACCUMULATE_ASSIGN 1
+int32_t hbt_grad_accumulate(void* const* accumulators, const void* const* grads, const int64_t* numels,
+                            int32_t count, int32_t acc_dtype, int32_t grad_dtype, int32_t flags, void* stream);
 
 /* ------------------------------------------------------------------------------
  * In-place gradient scaling: x = (x * unscale) * (*grad_mul), each product rounded to

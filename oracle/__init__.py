@@ -35,6 +35,7 @@ __all__ = [
     "no_sync_accumulate",
     "pack_shard",
     "read_range",
+    "round_to",
     "sgd_step",
     "sqnorm",
     "unpack_full",
@@ -64,10 +65,13 @@ PINNED_BY = {
     "weight decay, dampening and Nesterov; closed form of a plain step",
     "read_range": "reference known answers: shards_overlapping [(0,(0,3)),(1,(3,1))] "
     "(test_checkpoint_format.py:242-247); bitwise re-slicing of the global flat vector",
-    "local_share": "torch Tensor.div + add + padding zero, bitwise (order-free for G <= 2; "
-    "collectives.py:593-594); padding tail exactly 0.0 (test_fsdp.py:477-481)",
-    "no_sync_accumulate": "torch's own CPU sequence of fsdp.py:733-749 (to(float32), clone, add_, "
-    "grad + accumulator), bitwise on signed zeros, subnormals, overflow and random values",
+    "local_share": "torch Tensor.to(reduce dtype) + div + add + padding zero in fp32, bf16 and fp16, "
+    "bitwise (order-free for G <= 2; collectives.py:593-594); padding tail exactly 0.0 "
+    "(test_fsdp.py:477-481)",
+    "no_sync_accumulate": "torch's own CPU sequence of fsdp.py:733-749 (to(reduce dtype), clone, add_, "
+    "grad + accumulator) in fp32, bf16 and fp16, bitwise on signed zeros, subnormals, overflow and "
+    "random values",
+    "round_to": "torch Tensor.to(bfloat16 / float16).to(float32) bitwise on specials and random values",
 }
 
 
@@ -265,33 +269,57 @@ def bucket_layout(
     return buckets
 
 
+def round_to(x: np.ndarray, reduce: str = "float32") -> np.ndarray:
+    """fp32 ``x`` rounded to the dtype ``reduce`` names (round to nearest even) and widened
+    back, exactly: the value a torch op whose result has that dtype holds."""
+    x = np.asarray(x, dtype=np.float32)
+    if reduce == "float32":
+        return x
+    if reduce == "bfloat16":
+        return (f32_to_bf16(x).astype(np.uint32) << 16).view(np.float32)
+    if reduce == "float16":
+        with np.errstate(over="ignore"):
+            return x.astype(np.float16).astype(np.float32)
+    raise ValueError(f"unknown reduce dtype {reduce!r}")
+
+
 def local_share(rank_grads: Sequence[np.ndarray], rank: int, shard: int, valid: int,
-                divisor: float) -> np.ndarray:
-    """fp32 shard ``rank`` of the AVG reduce-scatter, summed in rank order
-    (parallel/fsdp.py:704-781, distributed/collectives.py:593-594)."""
+                divisor: float, reduce: str = "float32") -> np.ndarray:
+    """fp32 shard ``rank`` of the AVG reduce-scatter in the reduce dtype, summed in rank
+    order (parallel/fsdp.py:733-769, distributed/collectives.py:593-594): each rank's
+    slice cast to ``reduce``, divided by ``divisor`` and added, every result rounded to
+    ``reduce``; then widened to fp32 with the padding tail zeroed.  ``rank_grads`` hold
+    each rank's padded full gradient widened to fp32 (bf16 and fp16 widen exactly)."""
     div = np.float32(divisor)
-    acc = rank_grads[0].astype(np.float32)[rank * shard : (rank + 1) * shard] / div
-    for g in rank_grads[1:]:
-        acc = (acc + g.astype(np.float32)[rank * shard : (rank + 1) * shard] / div).astype(np.float32)
-    acc = acc.astype(np.float32)
+
+    def term(g: np.ndarray) -> np.ndarray:
+        x = round_to(np.asarray(g, dtype=np.float32)[rank * shard : (rank + 1) * shard], reduce)
+        return round_to(x / div, reduce)
+
+    with np.errstate(over="ignore", invalid="ignore"):
+        acc = term(rank_grads[0])
+        for g in rank_grads[1:]:
+            acc = round_to(acc + term(g), reduce)
+    acc = np.array(acc, dtype=np.float32)
     acc[valid:] = 0.0
     return acc
 
 
-def no_sync_accumulate(micro_grads: Sequence[np.ndarray]) -> np.ndarray:
-    """The fp32 gradient one rank reduces after ``no_sync`` accumulation
-    (parallel/fsdp.py:733-749).  ``micro_grads`` are the micro-batches' gradients in
-    order, already widened to fp32 (bf16 and fp16 widen exactly); all but the last ran
-    inside ``no_sync``.  The first is kept as a copy (``clone``), each later one inside
-    ``no_sync`` is added with one fp32 addition (``add_``), and the last, synchronising
-    one is added in front (``grad + accumulator``)."""
-    acc = np.array(micro_grads[0], dtype=np.float32, copy=True)
+def no_sync_accumulate(micro_grads: Sequence[np.ndarray], reduce: str = "float32") -> np.ndarray:
+    """The gradient one rank reduces after ``no_sync`` accumulation in the reduce dtype
+    (parallel/fsdp.py:733-749), as fp32 values exactly representable in ``reduce``.
+    ``micro_grads`` are the micro-batches' gradients in order, widened to fp32 (bf16 and
+    fp16 widen exactly); all but the last ran inside ``no_sync``.  Each is cast to
+    ``reduce``; the first is kept as it is (``clone``), each later one inside ``no_sync``
+    is added to it (``add_``), and the last, synchronising one is added in front
+    (``grad + accumulator``), every sum rounded to ``reduce``."""
+    acc = np.array(round_to(micro_grads[0], reduce), dtype=np.float32, copy=True)
     if len(micro_grads) == 1:
         return acc
     with np.errstate(over="ignore", invalid="ignore"):  # IEEE overflow to +-inf is the answer
         for g in micro_grads[1:-1]:
-            acc = np.add(acc, np.asarray(g, dtype=np.float32), dtype=np.float32)
-        return np.add(np.asarray(micro_grads[-1], dtype=np.float32), acc, dtype=np.float32)
+            acc = round_to(np.add(acc, round_to(g, reduce), dtype=np.float32), reduce)
+        return round_to(np.add(round_to(micro_grads[-1], reduce), acc, dtype=np.float32), reduce)
 
 
 def read_range(shards: Sequence[tuple[int, np.ndarray]], start: int, length: int) -> np.ndarray:

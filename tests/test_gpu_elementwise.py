@@ -11,8 +11,10 @@
   ``mul_`` by a Python float, twice, in the tensor's dtype, over several tensors per
   launch, tails of every length and a misaligned view.
 * ``hbt_grad_accumulate`` (the ``no_sync`` accumulation of ``parallel/fsdp.py:738-749``):
-  bitwise against torch's CPU ``add_`` after ``to(float32)``, fp32, bf16 and fp16
-  gradients, tails of every length, a misaligned pair and IEEE specials.
+  bitwise against torch's CPU ``add_`` (or the cast alone, for the first micro-batch)
+  in an fp32, bf16 or fp16 accumulator, fp32, bf16 and fp16 gradients, tails of every
+  length, a misaligned pair and IEEE specials.
+The local share runs in each reduce dtype (fp32, bf16, fp16) against the oracle's.
 """
 
 from __future__ import annotations
@@ -34,10 +36,14 @@ def _bits(t: torch.Tensor) -> np.ndarray:
     return t.view({2: torch.int16, 4: torch.int32}[t.element_size()]).numpy().copy()
 
 
+_REDUCE = {torch.float32: "float32", torch.bfloat16: "bfloat16", torch.float16: "float16"}
+
+
 @pytest.mark.parametrize("in_dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("group", [1, 3, 8])
 @pytest.mark.parametrize("misaligned", [False, True])
-def test_local_share_tiles(device, in_dtype, group, misaligned):
+@pytest.mark.parametrize("reduce", [torch.float32, torch.bfloat16, torch.float16])
+def test_local_share_tiles(device, in_dtype, group, misaligned, reduce):
     lib = _native.library()
     shard = 20_000
     gen = torch.Generator(device=device).manual_seed(group)
@@ -55,11 +61,11 @@ def test_local_share_tiles(device, in_dtype, group, misaligned):
         for valid in (shard, shard - 1537, 700, 0):
             status = lib.hbt_grad_local_share(
                 _native.pointer_array([g.data_ptr() for g in grads]), group, rank, shard, valid,
-                _native.dtype_code(in_dtype), divisor, ctypes.c_void_p(out.data_ptr()),
-                ctypes.c_void_p(_native.stream_of(device)),
+                _native.dtype_code(in_dtype), _native.dtype_code(reduce), divisor,
+                ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(_native.stream_of(device)),
             )
             _native.check(status, "test.local_share")
-            expect = oracle.local_share(host, rank, shard, valid, divisor)
+            expect = oracle.local_share(host, rank, shard, valid, divisor, _REDUCE[reduce])
             assert np.array_equal(_bits(out), expect.view(np.int32)), (rank, valid)
             # the fused entry point: the same shard, plus its squared-norm partials
             chunk = 32768
@@ -69,9 +75,9 @@ def test_local_share_tiles(device, in_dtype, group, misaligned):
             out.fill_(7.0)
             status = lib.hbt_grad_local_share_sqnorm(
                 _native.pointer_array([g.data_ptr() for g in grads]), group, rank, shard, valid,
-                _native.dtype_code(in_dtype), divisor, ctypes.c_void_p(out.data_ptr()),
-                ctypes.c_void_p(partials.data_ptr()), ctypes.c_void_p(tile_sums.data_ptr()),
-                ctypes.c_void_p(_native.stream_of(device)),
+                _native.dtype_code(in_dtype), _native.dtype_code(reduce), divisor,
+                ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(partials.data_ptr()),
+                ctypes.c_void_p(tile_sums.data_ptr()), ctypes.c_void_p(_native.stream_of(device)),
             )
             _native.check(status, "test.local_share_sqnorm")
             assert np.array_equal(_bits(out), expect.view(np.int32)), (rank, valid)
@@ -143,7 +149,8 @@ def test_local_share_full_size_rank7_of_llama3_8b_w8(device):
     tile_sums = torch.empty(-(-shard // 256), dtype=torch.float64, device=device)
     status = lib.hbt_grad_local_share_sqnorm(
         _native.pointer_array([g.data_ptr() for g in grads]), group, rank, shard, shard,
-        _native.dtype_code(torch.bfloat16), float(group), ctypes.c_void_p(out.data_ptr()),
+        _native.dtype_code(torch.bfloat16), _native.dtype_code(torch.float32), float(group),
+        ctypes.c_void_p(out.data_ptr()),
         ctypes.c_void_p(partials.data_ptr()), ctypes.c_void_p(tile_sums.data_ptr()),
         ctypes.c_void_p(_native.stream_of(device)),
     )
@@ -161,17 +168,20 @@ def test_local_share_full_size_rank7_of_llama3_8b_w8(device):
     torch.cuda.empty_cache()
 
 
+@pytest.mark.parametrize("acc_dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("grad_dtype", [torch.float32, torch.bfloat16, torch.float16])
-def test_grad_accumulate_tiles(device, grad_dtype):
-    """``hbt_grad_accumulate`` (the ``no_sync`` ``accumulator.add_(grad.to(float32))`` of
-    ``parallel/fsdp.py:738-749``) against torch's CPU ``add_``: bitwise except that NaN
-    results are compared as NaN.  Several pairs per launch, tails of every length, a
-    misaligned first accumulator and gradient (scalar path), signed zeros, infinities,
-    a NaN and subnormal sums."""
+@pytest.mark.parametrize("assign", [False, True])
+def test_grad_accumulate_tiles(device, acc_dtype, grad_dtype, assign):
+    """``hbt_grad_accumulate`` (the ``no_sync`` accumulation of ``parallel/fsdp.py:738-749``)
+    against torch's CPU ops in the accumulator's dtype: ``acc.add_(grad.to(acc_dtype))``,
+    or ``grad.to(acc_dtype)`` itself with ``HBT_ACCUMULATE_ASSIGN`` (the first
+    micro-batch's clone).  Bitwise except that NaN results are compared as NaN.  Several
+    pairs per launch, tails of every length, a misaligned first pair (scalar path),
+    signed zeros, infinities, a NaN and subnormal sums."""
     lib = _native.library()
     gen = torch.Generator(device=device).manual_seed(11)
     sizes = [1, 7, 255, 256, 257, 4097, 100_003]
-    acc_base = torch.randn(sum(sizes) + 1, device=device, generator=gen) * 1e-2
+    acc_base = (torch.randn(sum(sizes) + 1, device=device, generator=gen) * 1e-2).to(acc_dtype)
     grad_base = (torch.randn(sum(sizes) + 1, device=device, generator=gen) * 1e-2).to(grad_dtype)
     acc_base[1:5] = -0.0
     grad_base[1:3] = -0.0     # -0 + -0 = -0
@@ -179,8 +189,9 @@ def test_grad_accumulate_tiles(device, grad_dtype):
     acc_base[300] = float("inf")
     grad_base[301] = -float("inf")
     grad_base[302] = float("nan")
-    acc_base[303] = 1e-40     # fp32 subnormal plus a small gradient
+    acc_base[303] = torch.finfo(acc_dtype).tiny / 8   # subnormal where the dtype has them
     grad_base[303] = torch.finfo(grad_dtype).tiny
+    grad_base[304] = torch.finfo(grad_dtype).max      # overflows a narrower accumulator dtype
     accs, grads, cursor = [], [], 1  # the first pair starts one element in: misaligned
     for n in sizes:
         accs.append(acc_base[cursor:cursor + n])
@@ -191,23 +202,26 @@ def test_grad_accumulate_tiles(device, grad_dtype):
     stream = ctypes.c_void_p(_native.stream_of(device))
     status = lib.hbt_grad_accumulate(
         _native.pointer_array([a.data_ptr() for a in accs]), _native.pointer_array([g.data_ptr() for g in grads]),
-        _native.int64_array(sizes), len(sizes), _native.dtype_code(grad_dtype), stream,
+        _native.int64_array(sizes), len(sizes), _native.dtype_code(acc_dtype), _native.dtype_code(grad_dtype),
+        _native.ACCUMULATE_ASSIGN if assign else 0, stream,
     )
     _native.check(status, "test.grad_accumulate")
     for a, b, g in zip(accs, before, grads):
-        expect = b.add_(g.detach().cpu().to(torch.float32))
+        cast = g.detach().cpu().to(acc_dtype)
+        expect = cast if assign else b.add_(cast)
         got = a.detach().cpu()
         nan = torch.isnan(expect)
         assert torch.equal(torch.isnan(got), nan)
         assert np.array_equal(_bits(got)[~nan.numpy()], _bits(expect)[~nan.numpy()])
     assert np.array_equal(_bits(acc_base[:1]), lead)  # the element before the first pair is untouched
-    assert bool(torch.signbit(accs[0][0])) and not bool(torch.signbit(accs[1][2]))
+    if not assign:
+        assert bool(torch.signbit(accs[0][0])) and not bool(torch.signbit(accs[1][2]))
     # host-side refusals: no launch
     too_many = _native.MAX_TENSORS_PER_LAUNCH + 1
     assert lib.hbt_grad_accumulate(_native.pointer_array([accs[0].data_ptr()] * too_many),
                                    _native.pointer_array([grads[0].data_ptr()] * too_many),
-                                   _native.int64_array([1] * too_many), too_many,
-                                   _native.dtype_code(grad_dtype), stream) == -1
+                                   _native.int64_array([1] * too_many), too_many, _native.dtype_code(acc_dtype),
+                                   _native.dtype_code(grad_dtype), 0, stream) == -1
     assert lib.hbt_grad_accumulate(_native.pointer_array([accs[0].data_ptr()]),
                                    _native.pointer_array([grads[0].data_ptr()]), _native.int64_array([1]), 1,
-                                   3, stream) == -1  # fp64 gradients
+                                   _native.dtype_code(acc_dtype), 3, 0, stream) == -1  # fp64 gradients

@@ -139,6 +139,45 @@ def test_gradient_local_share_matches_oracle(device, group, in_dtype):
         assert h.reduction_count == 1
 
 
+def _mp_handles(group, device, reduce):
+    named = _params(MLP_1857_REFERENCE, device)
+    mp = MixedPrecisionConfig(enabled=True, param_dtype="bfloat16", reduce_dtype=reduce, master_dtype="float32")
+    return [FlatParamHandle(named, None, GroupHandle.local_view("shard", group, r), FSDPConfig(), mp, device,
+                            keep_originals=True) for r in range(group)]
+
+
+@pytest.mark.parametrize("group", [1, 2, 3, 4])
+@pytest.mark.parametrize("in_dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("reduce", ["bfloat16", "float16"])
+def test_gradient_local_share_in_reduce_dtype_matches_oracle(device, group, in_dtype, reduce):
+    """``MixedPrecisionConfig(reduce_dtype=...)``: the cast, the AVG divide and the rank sum
+    rounded to bf16 or fp16 (``collectives.py:593-594`` in that dtype), widened to the
+    fp32 master; bitwise against the oracle."""
+    handles = _mp_handles(group, device, reduce)
+    padded = handles[0].padded_numel
+    gen = torch.Generator(device=device).manual_seed(group + 7)
+    grads = [(torch.randn(padded, device=device, generator=gen) * 3.0).to(in_dtype) for _ in range(group)]
+    host = [g.float().cpu().numpy() for g in grads]
+    divisor = float(group) if group > 1 else 1.0
+    for rank, h in enumerate(handles):
+        out = h.reduce_scatter_gradient(grads[rank], peer_grads=grads if group > 1 else None)
+        assert out.dtype == torch.float32
+        valid = max(0, min(h.shard_numel, 1857 - rank * h.shard_numel))
+        expect = oracle.local_share(host, rank, h.shard_numel, valid, divisor, reduce)
+        assert np.array_equal(out.cpu().numpy().view(np.int32), expect.view(np.int32)), rank
+        assert torch.equal(out.to(getattr(torch, reduce)).to(torch.float32), out)  # representable in it
+
+
+def test_reduce_and_master_dtype_limits(device):
+    """A float64 reduction and a non-fp32 master shard have no kernel: refused up front."""
+    named = _params(MLP_1857_REFERENCE, device)
+    for mp in (MixedPrecisionConfig(enabled=True, reduce_dtype="float64"),
+               MixedPrecisionConfig(enabled=True, master_dtype="bfloat16")):
+        h = FlatParamHandle(named, None, GroupHandle.trivial("shard"), FSDPConfig(), mp, device, keep_originals=True)
+        with pytest.raises(UnsupportedFeatureError, match="float32, bfloat16 or float16 into a float32 master"):
+            h.reduce_scatter_gradient(torch.zeros(h.padded_numel, device=device))
+
+
 def test_local_share_needs_every_rank(device):
     _, _, handles = _handles(MLP_1857_REFERENCE, 2, device)
     with pytest.raises(UnsupportedFeatureError, match="reduce-scatter needs every rank"):
@@ -155,12 +194,13 @@ def test_local_share_needs_every_rank(device):
 @pytest.mark.parametrize("group", [1, 2, 3, 4])
 @pytest.mark.parametrize("in_dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("micro", [2, 4])
-def test_no_sync_accumulation_matches_oracle(device, group, in_dtype, micro):
+@pytest.mark.parametrize("reduce", ["float32", "bfloat16", "float16"])
+def test_no_sync_accumulation_matches_oracle(device, group, in_dtype, micro, reduce):
     """``no_sync`` (``parallel/fsdp.py:733-749``): the first ``micro - 1`` micro-batches
-    accumulate and return None; the last reduces the sums.  Bitwise against the
-    oracle's local share of the oracle's accumulated gradients, with -0.0 planted in
-    every rank's slice (a copy, not an add onto zeros, keeps its sign)."""
-    _, _, handles = _handles(MLP_1857_REFERENCE, group, device)
+    accumulate in the reduce dtype and return None; the last reduces the sums.  Bitwise
+    against the oracle's local share of the oracle's accumulated gradients, with -0.0
+    planted in every rank's slice (a copy, not an add onto zeros, keeps its sign)."""
+    handles = _mp_handles(group, device, reduce)
     padded, shard = handles[0].padded_numel, handles[0].shard_numel
     gen = torch.Generator(device=device).manual_seed(100 * group + micro)
     grads = []
@@ -174,28 +214,28 @@ def test_no_sync_accumulation_matches_oracle(device, group, in_dtype, micro):
         grads.append(batch)
     divisor = float(group) if group > 1 else 1.0
     for rank, h in enumerate(handles):
-        def reduce(m):
+        def micro_batch(m):
             return h.reduce_scatter_gradient(grads[m][rank], peer_grads=grads[m] if group > 1 else None)
 
         h.set_accumulate_without_reduction(True)
         for m in range(micro - 1):
-            assert reduce(m) is None
+            assert micro_batch(m) is None
             assert h.has_pending_accumulation
         assert h.reduction_count == 0
         h.set_accumulate_without_reduction(False)
-        out = reduce(micro - 1)
+        out = micro_batch(micro - 1)
         assert not h.has_pending_accumulation and h.reduction_count == 1
-        totals = [oracle.no_sync_accumulate([grads[m][q].float().cpu().numpy() for m in range(micro)])
+        totals = [oracle.no_sync_accumulate([grads[m][q].float().cpu().numpy() for m in range(micro)], reduce)
                   for q in range(group)]
         valid = max(0, min(shard, 1857 - rank * shard))
-        expect = oracle.local_share(totals, rank, shard, valid, divisor)
+        expect = oracle.local_share(totals, rank, shard, valid, divisor, reduce)
         assert np.array_equal(out.cpu().numpy().view(np.int32), expect.view(np.int32)), rank
         assert np.signbit(out[5].item())
         assert getattr(out, NORM_PARTIALS_ATTR, None) is not None
         # the accumulator is gone: the next call reduces its own gradients only
-        again = reduce(micro - 1)
+        again = micro_batch(micro - 1)
         plain = oracle.local_share([g.float().cpu().numpy() for g in grads[micro - 1]], rank, shard, valid,
-                                   divisor)
+                                   divisor, reduce)
         assert np.array_equal(again.cpu().numpy().view(np.int32), plain.view(np.int32)), rank
         assert h.reduction_count == 2
 

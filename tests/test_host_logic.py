@@ -124,24 +124,28 @@ def test_oracle_local_share_against_torch_avg():
             assert np.all(got[valid:] == 0.0)
 
 
-def _torch_no_sync(micro):
+def _torch_no_sync(micro, reduce=torch.float32):
     """The reference's own op sequence on CPU (``parallel/fsdp.py:733-749``)."""
     accumulator = None
     for g in micro[:-1]:
-        grad = g.to(torch.float32).contiguous()
+        grad = g.to(reduce).contiguous()
         if accumulator is None:
             accumulator = grad.clone()
         else:
             accumulator.add_(grad)
-    grad = micro[-1].to(torch.float32).contiguous()
+    grad = micro[-1].to(reduce).contiguous()
     return grad if accumulator is None else grad + accumulator
 
 
+_REDUCE_NAMES = {torch.float32: "float32", torch.bfloat16: "bfloat16", torch.float16: "float16"}
+
+
+@pytest.mark.parametrize("reduce", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("micro", [1, 2, 3, 5])
-def test_oracle_no_sync_accumulate_against_torch(dtype, micro):
+def test_oracle_no_sync_accumulate_against_torch(reduce, dtype, micro):
     """Bitwise against torch on CPU, with signed zeros (a copy keeps -0.0 where adding
-    to zeros would not), subnormal sums, overflow to infinity and random values."""
+    to zeros would not), subnormal sums, overflow and random values."""
     gen = torch.Generator().manual_seed(micro)
     n = 4096
     grads = []
@@ -150,18 +154,20 @@ def test_oracle_no_sync_accumulate_against_torch(dtype, micro):
         g[:8] = -0.0                          # -0.0 in every micro-batch
         g[8] = 0.0 if m else -0.0             # -0.0 then +0.0: the sum is +0.0
         g[9] = torch.finfo(dtype).tiny / 4    # subnormal (fp32, fp16) or a tiny normal sum
-        g[10] = torch.finfo(dtype).max        # fp32/bf16: +inf once added twice; fp16: exact in fp32
+        g[10] = torch.finfo(dtype).max        # overflows in the sum or in the cast to a narrower dtype
         g[11] = -torch.finfo(dtype).max
         grads.append(g)
-    expect = _torch_no_sync(grads)
-    got = oracle.no_sync_accumulate([g.float().numpy() for g in grads])
+    expect = _torch_no_sync(grads, reduce).to(torch.float32)
+    got = oracle.no_sync_accumulate([g.float().numpy() for g in grads], _REDUCE_NAMES[reduce])
     assert got.dtype == np.float32
     assert np.array_equal(got.view(np.uint32), expect.numpy().view(np.uint32))
     if micro > 1:
         assert np.all(np.signbit(got[:8])) and not np.signbit(got[8])
-        if dtype == torch.float16:
+        if reduce is torch.float32 and dtype == torch.float16:
             # The sum is formed in fp32, where micro * 65504 is exact; fp16 would overflow.
             assert got[10] == 65504.0 * micro and got[11] == -65504.0 * micro
+        elif reduce is torch.bfloat16 and dtype == torch.float16:
+            assert np.isfinite(got[10]) and got[10] > 0 and np.isfinite(got[11]) and got[11] < 0
         else:
             assert np.isinf(got[10]) and got[10] > 0 and np.isinf(got[11]) and got[11] < 0
         # Accumulating onto zeros instead of copying the first micro-batch loses the sign of -0.0.
@@ -170,6 +176,48 @@ def test_oracle_no_sync_accumulate_against_torch(dtype, micro):
             for g in grads:
                 from_zeros = np.add(from_zeros, g.float().numpy(), dtype=np.float32)
         assert not np.array_equal(from_zeros.view(np.uint32), got.view(np.uint32))
+
+
+@pytest.mark.parametrize("reduce", [torch.bfloat16, torch.float16])
+def test_oracle_round_to_against_torch(reduce):
+    """``round_to`` is torch's cast to the reduce dtype and back, on specials (ties,
+    overflow, subnormals, signed zeros, infinities) and random values of every scale."""
+    gen = torch.Generator().manual_seed(7)
+    x = torch.randn(1 << 16, generator=gen) * torch.logspace(-45, 38, 1 << 16, base=2.0)
+    specials = torch.tensor([0.0, -0.0, float("inf"), -float("inf"), 65504.0, 65520.0, 65519.99,
+                             3.3895314e38, 3.4028235e38, 1e-8, 5.9604645e-8, 2.9802322e-8,
+                             1.0 + 2.0**-8, 1.0 + 3 * 2.0**-8, 1.0 + 2.0**-11, 1.0 + 3 * 2.0**-11])
+    x = torch.cat([specials, -specials, x])
+    expect = x.to(reduce).to(torch.float32).numpy()
+    got = oracle.round_to(x.numpy(), _REDUCE_NAMES[reduce])
+    assert np.array_equal(got.view(np.uint32), expect.view(np.uint32))
+
+
+@pytest.mark.parametrize("reduce", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_oracle_local_share_reduce_dtype_against_torch(reduce, dtype):
+    """The reference's AVG local share in a 2-byte reduce dtype, with torch's own ops:
+    ``Tensor.to(reduce)``, ``div(G)`` and the rank sum in that dtype, then the cast to
+    the fp32 master and the padding zero.  Order-free for G <= 2, as in fp32."""
+    import functools
+
+    gen = torch.Generator().manual_seed(1)
+    for group, shard, pad in ((1, 7, 2), (2, 64, 1), (3, 50, 2), (4, 66, 3)):
+        total = group * shard - pad
+        grads = [(torch.randn(group * shard, generator=gen) * 3.0).to(dtype) for _ in range(group)]
+        divided = [g.to(reduce).div(group) for g in grads]
+        summed = functools.reduce(torch.add, reversed(divided) if group <= 2 else divided).to(torch.float32)
+        summed[total:] = 0.0
+        host = [g.float().numpy() for g in grads]
+        for rank in range(group):
+            valid = max(0, min(shard, total - rank * shard))
+            got = oracle.local_share(host, rank, shard, valid, float(group), _REDUCE_NAMES[reduce])
+            expect = summed[rank * shard:(rank + 1) * shard].numpy()
+            assert np.array_equal(got.view(np.uint32), expect.view(np.uint32)), (group, rank)
+            if group > 1:
+                # Reducing in fp32 instead gives different bits on some element.
+                fp32 = oracle.local_share(host, rank, shard, valid, float(group))
+                assert not np.array_equal(fp32.view(np.uint32), got.view(np.uint32))
 
 
 def test_oracle_pack_matches_concatenation():

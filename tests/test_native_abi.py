@@ -57,9 +57,14 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     assert lib.hbt_copy_intervals(None, 1, 1, 0, 0, 0, 1.0, 0, None) == -1
     assert lib.hbt_copy_intervals(None, 0, 0, 0, 0, 0, 1.0, 0, None) == 0
     assert lib.hbt_copy_intervals(None, 0, 0, 0, 0, 0, 1.0, 2, None) == -1  # unknown flag
-    assert lib.hbt_grad_local_share(None, 0, 0, 1, 1, 0, 1.0, None, None) == -1
-    assert lib.hbt_grad_local_share_sqnorm(None, 1, 0, 1, 1, 0, 1.0, None, None, None, None) == -1
+    assert lib.hbt_grad_local_share(None, 0, 0, 1, 1, 0, 0, 1.0, None, None) == -1
+    assert lib.hbt_grad_local_share_sqnorm(None, 1, 0, 1, 1, 0, 0, 1.0, None, None, None, None) == -1
     assert b"hbt_grad_local_share_sqnorm" in lib.hbt_last_error()
+    assert lib.hbt_grad_accumulate(None, None, None, 0, 0, 0, 0, None) == 0  # empty table
+    assert lib.hbt_grad_accumulate(None, None, None, 0, 3, 0, 0, None) == -1  # fp64 accumulator
+    assert b"F32, BF16 or F16" in lib.hbt_last_error()
+    assert lib.hbt_grad_accumulate(None, None, None, 0, 0, 0, 2, None) == -1  # unknown flag
+    assert lib.hbt_grad_accumulate(None, None, None, 1, 0, 0, 0, None) == -1  # null table
     assert lib.hbt_grad_norm_finalize(None, 5, 1.0, None, None, None, None, None) == -1
 
 
