@@ -29,7 +29,8 @@ from .errors import (
     format_error,
 )
 from .buckets import BucketedGradients, BucketLayout, GradientBucket, build_buckets
-from .flat_param import FlatParameter, FlatParamHandle, PieceLayout, ShardedTensorPiece, reshard_state_dict_pieces
+from .flat_param import (FlatParameter, FlatParamHandle, PieceLayout, ShardedTensorPiece, optimizer_parameter_layout,
+                         reshard_state_dict_pieces)
 from .grad_scaler import GradScaler, GradScalerState
 from .groups import GroupHandle
 from .manifest import (

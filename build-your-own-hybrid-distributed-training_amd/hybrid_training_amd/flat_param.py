@@ -31,6 +31,7 @@ tensor work is the interval gather-copy kernel and the local-share kernel of
 
 from __future__ import annotations
 
+import dataclasses
 from collections.abc import Sequence
 from dataclasses import dataclass
 from typing import Any
@@ -50,6 +51,7 @@ __all__ = [
     "FlatParameter",
     "PieceLayout",
     "ShardedTensorPiece",
+    "optimizer_parameter_layout",
     "reshard_state_dict_pieces",
 ]
 
@@ -806,6 +808,24 @@ def reshard_state_dict_pieces(
         plan.add(sources[index], start - pieces[index].offset, flat, start, end - start)
     plan.run(src_dtype=dtype, dst_dtype=dtype)
     return flat.view(global_shape)
+
+
+def optimizer_parameter_layout(
+    units: Sequence[tuple[str, FlatParamHandle]],
+) -> list[tuple[nn.Parameter, list[PieceLayout]]]:
+    """Each unit's flat shard with the parameter pieces it holds, names carrying the
+    unit's prefix (``fsdp.py:1477-1510``).
+
+    Optimizer state has the flat shard's shape, so this layout checkpoints it in the
+    parameters' global coordinates and lets it reshard across group sizes.  The
+    reference's wrapper walks its module tree for the ``(prefix, handle)`` pairs; the
+    caller passes them here, in the order of the optimizer's parameters.
+    """
+    return [
+        (handle.flat_param,
+         [dataclasses.replace(item, name=prefix + item.name) for item in handle.local_piece_layout()])
+        for prefix, handle in units
+    ]
 
 
 def _last_writer_segments(intervals: Sequence[tuple[int, int]]) -> list[tuple[int, int, int]]:

@@ -24,6 +24,7 @@ from hybrid_training_amd import (
     MixedPrecisionConfig,
     ShardedTensorPiece,
     ShardingError,
+    optimizer_parameter_layout,
     reshard_state_dict_pieces,
 )
 from hybrid_training_amd.errors import UnsupportedFeatureError
@@ -111,6 +112,22 @@ def test_reshard_state_dict_pieces_overlapping_pieces_last_writer_wins(device, s
     with pytest.raises(ShardingError, match="past the end"):
         reshard_state_dict_pieces(pieces + [ShardedTensorPiece(name="w", global_shape=shape, offset=total - 2,
                                                                data=torch.zeros(3, device=device))], shape)
+
+
+def test_optimizer_parameter_layout_prefixes_each_units_pieces(device):
+    """``fsdp.py:1477-1510``: every unit's flat shard with its local pieces, the piece
+    names carrying the unit's prefix and everything else as ``local_piece_layout``."""
+    _, _, first = _handles(MLP_1857_REFERENCE, 2, device)
+    _, _, second = _handles(MLP_23_32_32_1, 3, device)
+    units = [("layers.0.", first[1]), ("layers.1.", second[2])]
+    layout = optimizer_parameter_layout(units)
+    assert len(layout) == 2 and all(p is h.flat_param for (p, _), (_, h) in zip(layout, units))
+    for (prefix, h), (_, pieces) in zip(units, layout):
+        plain = h.local_piece_layout()
+        assert [p.name for p in pieces] == [prefix + q.name for q in plain]
+        assert [(p.global_shape, p.parameter_offset, p.length, p.local_offset) for p in pieces] == \
+            [(q.global_shape, q.parameter_offset, q.length, q.local_offset) for q in plain]
+        assert sum(p.length for p in pieces) <= h.shard_numel
 
 
 def test_norm_weights_and_padding_runs(device):
