@@ -1,8 +1,9 @@
 """Property tests of the host-side interval arithmetic against brute force (no GPU).
 
 Every kernel launch on the path is driven by integer plans the host builds: flat
-offsets and shard ranges, DDP bucket boundaries, checkpoint shard intersections,
-the last-writer segments of a piece reassembly and the copy kernel's chunk table.
+offsets and shard ranges, DDP bucket boundaries, checkpoint shard intersections and
+manifests, the last-writer segments of a piece reassembly and the copy kernel's
+chunk table.
 Each property below answers the same question element by element on small inputs
 (which tensor owns position i, which shard covers it, which piece wrote it last)
 and compares.  A wrong offset, an off-by-one bound or a swapped operand fails on
@@ -13,6 +14,7 @@ every run.
 from __future__ import annotations
 
 import bisect
+import json
 
 import numpy as np
 import pytest
@@ -24,6 +26,8 @@ from hypothesis import strategies as st
 from hybrid_training_amd import (
     CheckpointCorruptionError,
     CheckpointError,
+    CheckpointManifest,
+    FileRecord,
     IncompleteCheckpointError,
     ShardRange,
     ShardRecord,
@@ -33,6 +37,7 @@ from hybrid_training_amd import (
     concat_shard_sizes,
     even_shard_ranges,
     intersect_ranges,
+    shard_filename,
     shard_range_for,
 )
 from hybrid_training_amd import reshard as reshard_module
@@ -280,3 +285,49 @@ def test_copy_table_assigns_every_chunk_to_the_row_that_holds_it(rows, chunk, sc
     for c, (index, k) in enumerate(owners):
         found = bisect.bisect_right(firsts, c) - 1
         assert (found, c - firsts[found]) == (index, k)
+
+
+@PROPERTY
+@given(numels=st.lists(st.integers(1, 40), min_size=1, max_size=6), writers=st.integers(1, 5), data=st.data())
+def test_flat_sharded_manifest_round_trips_and_validates(numels, writers, data):
+    """``checkpoint/manifest.py:63-561``: the manifest of a flat-sharded save, built
+    piece by piece as writers record them, covers every element of every tensor once,
+    survives its JSON form unchanged and validates.  Dropping a shard, a file's
+    integrity record or the completion mark is refused with the reference's classes."""
+    entries, total = build_flat_layout([(f"t{i}", torch.empty(n)) for i, n in enumerate(numels)])
+    manifest = CheckpointManifest(writer_world_size=writers, step=7, complete=True)
+    for rank, shard in enumerate(even_shard_ranges(total, writers)):
+        name = shard_filename(rank)
+        manifest.files[name] = FileRecord(name=name, sha256="0" * 64, bytes=1)
+        for entry in entries:
+            overlap = intersect_ranges(shard, ShardRange(entry.offset, entry.numel))
+            if overlap is None:
+                continue
+            manifest.add_shard(
+                TensorRecord(key=entry.name, name=entry.name, global_shape=entry.shape, dtype="torch.float32"),
+                ShardRecord(rank=rank, file=name, offset=overlap.start - entry.offset, length=overlap.length,
+                            key=entry.name),
+            )
+    for entry in entries:
+        count = np.zeros(entry.numel, dtype=np.int64)
+        for shard in manifest.tensors[entry.name].shards:
+            count[shard.offset:shard.offset + shard.length] += 1
+        assert (count == 1).all()
+    manifest.validate()
+    again = CheckpointManifest.from_dict(json.loads(manifest.to_json()))
+    assert again.as_dict() == manifest.as_dict()
+    again.validate()
+
+    key = data.draw(st.sampled_from(sorted(again.tensors)), label="tensor")
+    shards = again.tensors[key].shards
+    del shards[data.draw(st.integers(0, len(shards) - 1), label="dropped shard")]
+    with pytest.raises(IncompleteCheckpointError, match="do not cover"):
+        again.validate()
+    unrecorded = CheckpointManifest.from_dict(manifest.as_dict())
+    unrecorded.files.pop(shard_filename(0))  # writer 0 always holds the first element
+    with pytest.raises(IncompleteCheckpointError, match="integrity record"):
+        unrecorded.validate()
+    unfinished = CheckpointManifest.from_dict(manifest.as_dict())
+    unfinished.complete = False
+    with pytest.raises(IncompleteCheckpointError, match="not marked complete"):
+        unfinished.validate()
