@@ -374,6 +374,11 @@ class CopyPlan:
     def __init__(self, device: torch.device) -> None:
         self.device = torch.device(device)
         self._rows: list[tuple[int, int, int]] = []
+        # The tensors the rows address, held for the plan's lifetime.  A row records
+        # only addresses: a temporary the caller made for it (a dense or device copy)
+        # and dropped before run() would hand its memory to the next allocation on the
+        # stream, this plan's own table among them, before the kernel reads it.
+        self._keep: list[torch.Tensor] = []
 
     def __len__(self) -> int:
         return len(self._rows)
@@ -383,7 +388,8 @@ class CopyPlan:
         """A plan over rows ``(source address or 0 for a zero fill, destination address, n)``.
 
         For callers that have already checked every address against a dense device
-        tensor of the plan's dtypes and every extent against that tensor's end.
+        tensor of the plan's dtypes and every extent against that tensor's end, and
+        that keep those tensors alive until :meth:`run` has returned.
         """
         plan = cls(device)
         plan._rows = [row for row in rows if row[2] > 0]
@@ -404,6 +410,8 @@ class CopyPlan:
             raise ValueError("copy plans address dense tensors only")
         if n == 0:
             return
+        self._keep.append(src)
+        self._keep.append(dst)
         self._rows.append(
             (
                 src.data_ptr() + src_offset * src.element_size(),
@@ -421,6 +429,7 @@ class CopyPlan:
             raise ValueError("copy plans address dense tensors only")
         if n == 0:
             return
+        self._keep.append(dst)
         self._rows.append((0, dst.data_ptr() + dst_offset * dst.element_size(), n))
 
     def run(

@@ -265,6 +265,9 @@ class BucketedGradients:
         # address, n), source address 0 meaning a zero fill.  Built with plain attribute
         # reads: this loop runs once per step over every parameter.
         rows: dict[tuple[int, torch.dtype, torch.dtype], list[tuple[int, int, int]]] = {}
+        # Dense copies of non-contiguous gradients, alive until the plans have run: the
+        # rows hold their addresses only.
+        dense_copies: list[torch.Tensor] = []
         for bucket in selected:
             buffer = bucket.buffer
             base = buffer.data_ptr()
@@ -289,6 +292,7 @@ class BucketedGradients:
                     )
                 if not grad.is_contiguous():
                     grad = grad.contiguous()
+                    dense_copies.append(grad)
                 if grad.numel() != numel:
                     raise ShardingError(
                         format_error("ddp.pack", "gradient size differs from its parameter",

@@ -100,3 +100,50 @@ def test_bucket_by_bucket_pack_matches_one_launch(device):
         ddp.pack([17])
     with pytest.raises(ShardingError, match="distinct and in range"):
         ddp.pack([3, 3])
+
+
+def test_bucket_size_is_never_numerical(device):
+    """``tests/distributed/test_ddp.py:314-358``: the bucket cap moves bucket boundaries
+    only.  Caps that give one parameter per bucket, a few buckets or a single bucket
+    yield the same averaged gradients bitwise, and the statistics count every byte."""
+    named = [(f"p{i}", torch.nn.Parameter(torch.empty(n, device=device)))
+             for i, n in enumerate([5, 1031, 64, 7, 4096, 3, 65536, 300])]
+    gen = torch.Generator(device=device).manual_seed(9)
+    grads = [torch.randn(p.shape, device=device, generator=gen) for _, p in named]
+    group = GroupHandle.local_view("data_parallel", 3, 0)
+    results, counts = [], []
+    for cap_mb in (1e-6, 0.01, 25.0):
+        for (_, p), g in zip(named, grads):
+            p.grad = g.clone()
+        ddp = BucketedGradients(named, group, DDPConfig(bucket_cap_mb=cap_mb))
+        ddp.synchronize()
+        counts.append(len(ddp.buckets))
+        results.append([p.grad.detach().cpu().view(torch.int32).clone() for _, p in named])
+        assert ddp.statistics.bytes_reduced == 4 * sum(p.numel() for _, p in named)
+        assert ddp.statistics.buckets_reduced == len(ddp.buckets)
+    assert counts[0] == len(named) and counts[-1] == 1 and counts[0] > counts[1] > counts[2]
+    expect = [(g.detach().cpu().numpy() / np.float32(3)).astype(np.float32) for g in grads]
+    for packed in results:
+        for got, want in zip(packed, expect):
+            assert np.array_equal(got.numpy(), want.view(np.int32))
+
+
+def test_non_contiguous_gradients_are_packed(device):
+    """A non-contiguous gradient is packed from a dense copy that stays alive until the
+    pack has run; the averaged values are bitwise numpy's."""
+    shapes = [(33, 17), (5,), (8, 64), (129, 3), (7,)]
+    named = [(f"w{i}", torch.nn.Parameter(torch.empty(s, device=device))) for i, s in enumerate(shapes)]
+    gen = torch.Generator(device=device).manual_seed(13)
+    expect = {}
+    for name, p in named:
+        if p.dim() == 2:
+            p.grad = torch.randn(tuple(reversed(p.shape)), device=device, generator=gen).t()
+            assert not p.grad.is_contiguous()
+        else:
+            p.grad = torch.randn(p.shape, device=device, generator=gen)
+        expect[name] = (p.grad.detach().cpu().contiguous().numpy() / np.float32(2)).astype(np.float32)
+    ddp = BucketedGradients(named, GroupHandle.local_view("data_parallel", 2, 0), DDPConfig(bucket_cap_mb=25.0))
+    ddp.synchronize()
+    for name, p in named:
+        assert p.grad.is_contiguous()
+        assert np.array_equal(p.grad.detach().cpu().numpy().view(np.int32), expect[name].view(np.int32)), name

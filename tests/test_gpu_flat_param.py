@@ -130,6 +130,31 @@ def test_optimizer_parameter_layout_prefixes_each_units_pieces(device):
         assert sum(p.length for p in pieces) <= h.shard_numel
 
 
+def test_build_and_load_from_host_tensors(device):
+    """Parameters and state-dict tensors on the host are uploaded tensor by tensor, and
+    each upload (and each dense copy of a non-contiguous tensor) must stay alive until
+    the copy that reads it has run; a dropped one would hand its memory to the next
+    upload first.  Shards bitwise against the oracle."""
+    gen = torch.Generator().manual_seed(21)
+    named = [(f"p{i}", torch.nn.Parameter(torch.randn(s, generator=gen))) for i, s in enumerate(MLP_1857_REFERENCE)]
+    host = [p.detach().numpy().copy() for _, p in named]
+    for group in (1, 3):
+        for rank in range(group):
+            h = FlatParamHandle(named, None, GroupHandle.local_view("shard", group, rank), FSDPConfig(),
+                                MixedPrecisionConfig(), device, keep_originals=True)
+            expect = oracle.pack_shard(host, group, rank)
+            assert np.array_equal(h.flat_param.detach().cpu().numpy().view(np.int32), expect.view(np.int32))
+            state = {}
+            for name, p in named:
+                if p.dim() == 2:  # a transposed view: non-contiguous
+                    state[name] = torch.randn(tuple(reversed(p.shape)), generator=gen).t()
+                else:
+                    state[name] = torch.randn(p.shape, generator=gen)
+            h.load_local_pieces(state)
+            expect = oracle.pack_shard([state[name].contiguous().numpy() for name, _ in named], group, rank)
+            assert np.array_equal(h.flat_param.detach().cpu().numpy().view(np.int32), expect.view(np.int32))
+
+
 def test_norm_weights_and_padding_runs(device):
     _, _, handles = _handles(MLP_1857_REFERENCE, 4, device)
     last = handles[-1]
