@@ -22,7 +22,7 @@ from collections.abc import Sequence
 
 import torch
 
-from .errors import NativeKernelError, UnsupportedFeatureError, format_error
+from .errors import NativeKernelError, ShardingError, UnsupportedFeatureError, format_error
 
 __all__ = [
     "ABI_VERSION",
@@ -48,6 +48,7 @@ __all__ = [
     "dtype_code",
     "library",
     "library_path",
+    "require_dense",
     "require_device_tensor",
     "stream_of",
 ]
@@ -266,6 +267,17 @@ def require_device_tensor(tensor: torch.Tensor, operation: str) -> None:
                 observed=str(tensor.device),
                 resolution="move the tensors to the GPU first",
             )
+        )
+
+
+def require_dense(tensor: torch.Tensor, operation: str) -> None:
+    """Refuse a tensor whose elements are not the ``numel`` consecutive ones from its
+    address: the element-wise kernels address exactly that range."""
+    if not tensor.is_contiguous():
+        raise ShardingError(
+            format_error(operation, "gradients must be dense", expected="a contiguous tensor",
+                         observed=f"shape {tuple(tensor.shape)}, strides {tuple(tensor.stride())}",
+                         resolution="pass a contiguous gradient (for example grad.contiguous())")
         )
 
 

@@ -32,6 +32,7 @@ import torch.nn as nn
 
 from . import _native
 from .config import GradScalerConfig
+from .errors import UnsupportedFeatureError, format_error
 from .groups import GroupHandle
 from .optim import PENDING_UNSCALE_ATTR, gradient_norm_pass
 
@@ -151,6 +152,12 @@ class GradScaler:
         groups: dict[tuple[torch.device, torch.dtype], list[torch.Tensor]] = {}
         for p in params:
             _native.require_device_tensor(p.grad, "grad_scaler.unscale_")
+            _native.require_dense(p.grad, "grad_scaler.unscale_")
+            if p.grad.dtype not in (torch.float32, torch.bfloat16):
+                raise UnsupportedFeatureError(
+                    format_error("grad_scaler.unscale_", "gradients must be float32 or bfloat16",
+                                 observed=str(p.grad.dtype))
+                )
             groups.setdefault((p.grad.device, p.grad.dtype), []).append(p.grad)
         for (device, dtype), grads in groups.items():
             with torch.cuda.device(device):

@@ -570,6 +570,7 @@ class ShardedOptimizer:
             g = p.grad
             if g is None:
                 continue
+            _native.require_dense(g, "optim.scale_gradients")
             unscale = _pending_unscale(g) if unscale_attr else 1.0
             groups.setdefault((g.dtype, unscale), []).append(g)
         with torch.cuda.device(self._device):

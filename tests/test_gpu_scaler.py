@@ -16,6 +16,7 @@ import torch
 
 import oracle
 from hybrid_training_amd import GradScaler, GradScalerConfig, GroupHandle, OptimizerConfig, ShardedOptimizer
+from hybrid_training_amd.errors import ShardingError, UnsupportedFeatureError
 
 pytestmark = pytest.mark.gpu
 
@@ -105,6 +106,23 @@ def test_unscale_return_value_is_the_overflow_flag(device):
         param.grad = torch.ones(10, device=device)
         param.grad[3] = float("nan")
         assert bool(scaler.unscale_([param]))
+
+
+def test_unscale_refuses_gradients_the_kernel_cannot_address(device):
+    """The in-place scale reads ``numel`` consecutive elements from a gradient's address:
+    a strided gradient is refused (``ShardingError``) rather than scaled in the wrong
+    places, and an fp16 gradient, which the kernel does not take, is refused up front."""
+    scaler = GradScaler(GradScalerConfig(enabled=True, init_scale=1024.0), GroupHandle.trivial(), device)
+    p = torch.nn.Parameter(torch.zeros(10, device=device))
+    storage = torch.arange(20.0, device=device)
+    p.grad = storage[::2]
+    with pytest.raises(ShardingError, match="must be dense"):
+        scaler.unscale_([p])
+    assert torch.equal(storage, torch.arange(20.0, device=device))  # nothing was touched
+    q = torch.nn.Parameter(torch.zeros(10, device=device, dtype=torch.float16))
+    q.grad = torch.ones(10, device=device, dtype=torch.float16)
+    with pytest.raises(UnsupportedFeatureError, match="float32 or bfloat16"):
+        scaler.unscale_([q])
 
 
 def test_llama3_70b_rank_shard_full_size(device):
