@@ -718,6 +718,8 @@ class ShardedOptimizer:
                     state["step"] = torch.tensor(0.0, dtype=torch.float32)
                     state["exp_avg"] = self._zero_state(p)
                     state["exp_avg_sq"] = self._zero_state(p)
+                _native.require_dense(state["exp_avg"], "optim.ShardedOptimizer.step")
+                _native.require_dense(state["exp_avg_sq"], "optim.ShardedOptimizer.step")
                 step_t = state["step"]
                 step_t += 1
                 step = float(step_t.item())
@@ -771,7 +773,8 @@ class ShardedOptimizer:
         """A loaded state tensor on the reference parameter's device and dtype (pinned if host)."""
         if self._pipeline is not None:
             return _pinned_like(reference).copy_(value.detach().reshape(reference.shape))
-        return value.to(device=reference.device, dtype=reference.dtype)
+        # The update kernels address numel consecutive elements, so the state is dense.
+        return value.to(device=reference.device, dtype=reference.dtype).contiguous()
 
     def _zero_state(self, p: torch.Tensor) -> torch.Tensor:
         """A zero state tensor beside ``p``: in HBM, or pinned host memory when offloaded."""
@@ -833,6 +836,8 @@ class ShardedOptimizer:
                         state["momentum_buffer"] = (_pinned_like(p) if self._pipeline is not None
                                                     else torch.empty_like(p, memory_format=torch.preserve_format))
                         flags |= _native.SGD_FIRST_STEP
+                    else:
+                        _native.require_dense(state["momentum_buffer"], "optim.ShardedOptimizer.step")
                 # Scalars exactly as torch forms them: Python doubles, rounded to fp32.
                 scalars = (weight_decay, momentum, 1 - dampening, -lr)
                 key = (scalars, flags, grad.dtype, _pending_unscale(grad))

@@ -19,6 +19,7 @@ The HIP kernels are called through the C ABI (directly, and through
 
 from __future__ import annotations
 
+import copy
 import math
 
 import numpy as np
@@ -271,6 +272,40 @@ def test_many_parameters_and_state_dict_round_trip(device):
     fresh.load_state_dict(saved)
     assert float(fresh.inner.state[params[0]]["step"]) == 3.0
     assert fresh.state_bytes() == opt.state_bytes() == 2 * 4 * sum(p.numel() for p in params) + 4 * len(params)
+
+
+def test_loaded_non_contiguous_state_steps_like_dense_state(device):
+    """State tensors loaded with another layout (here transposed, non-contiguous) are
+    placed dense, so the next step is bitwise the step from the saved dense state."""
+    params = [torch.nn.Parameter(torch.randn(s, device=device) * 0.1) for s in [(33, 17), (17,), (8, 64)]]
+    opt = _make_optimizer(params, lr=1e-3, betas=(0.9, 0.999), wd=0.01)
+    for p in params:
+        p.grad = torch.randn_like(p) * 1e-2
+    opt.clip_grad_norm(1.0)
+    opt.step()
+    saved = opt.state_dict()
+    # Separate copies: torch's load_state_dict keeps the loaded "step" tensor itself.
+    strided = copy.deepcopy(saved)
+    for entry in strided["state"].values():
+        for k, v in entry.items():
+            if torch.is_tensor(v) and v.dim() == 2:
+                entry[k] = v.t().contiguous().t()
+    assert any(not v.is_contiguous() for e in strided["state"].values() for v in e.values() if torch.is_tensor(v))
+    copies = [torch.nn.Parameter(p.detach().clone()) for p in params]
+    dense = _make_optimizer([torch.nn.Parameter(p.detach().clone()) for p in params], lr=1e-3,
+                            betas=(0.9, 0.999), wd=0.01)
+    dense_params = dense.parameters
+    dense.load_state_dict(copy.deepcopy(saved))
+    other = _make_optimizer(copies, lr=1e-3, betas=(0.9, 0.999), wd=0.01)
+    other.load_state_dict(strided)
+    for a, b in zip(dense_params, copies):
+        a.grad = torch.ones_like(a) * 1e-3
+        b.grad = torch.ones_like(b) * 1e-3
+    for o in (dense, other):
+        o.clip_grad_norm(1.0)
+        o.step()
+    for a, b in zip(dense_params, copies):
+        assert torch.equal(a.detach().view(torch.int32), b.detach().view(torch.int32))
 
 
 def test_pending_unscale_is_read_through(device):
