@@ -21,7 +21,8 @@ this rank's pre-divided contribution, ready for it.
 
 from __future__ import annotations
 
-from collections.abc import Iterable, Sequence
+from collections.abc import Iterable, Iterator, Sequence
+from contextlib import contextmanager
 from dataclasses import dataclass, field
 from typing import Any
 
@@ -222,7 +223,23 @@ class BucketedGradients:
             _native.require_device_tensor(p, "ddp.BucketedGradients")
         self._buckets = build_buckets(self._named, self._config.bucket_cap_mb)
         self._name_of = {id(p): n for n, p in self._named}
+        self._require_backward_grad_sync = True
         self.statistics = DDPStatistics()
+
+    @contextmanager
+    def no_sync(self) -> Iterator[None]:
+        """Accumulate gradients without packing them (``ddp.py:702-733``).
+
+        Inside, :meth:`pack` and :meth:`synchronize` leave the buckets alone, so the
+        micro-batches' gradients keep accumulating in ``param.grad``; the first call
+        outside packs (and averages) the accumulated sums.
+        """
+        previous = self._require_backward_grad_sync
+        self._require_backward_grad_sync = False
+        try:
+            yield
+        finally:
+            self._require_backward_grad_sync = previous
 
     @property
     def buckets(self) -> tuple[GradientBucket, ...]:
@@ -248,7 +265,10 @@ class BucketedGradients:
         (``ddp.py:479-523``), and start that bucket's all-reduce while backward runs.
         A parameter without a gradient contributes zeros when
         ``find_unused_parameters`` is set and raises otherwise (``ddp.py:579-615``).
+        Inside :meth:`no_sync` it does nothing (``ddp.py:485-489``).
         """
+        if not self._require_backward_grad_sync:
+            return
         if buckets is None:
             selected = self._buckets
         else:
@@ -335,7 +355,10 @@ class BucketedGradients:
             bucket.reset()
 
     def synchronize(self) -> None:
-        """Pack (with the AVG pre-divide), then rebind gradients to the buckets."""
+        """Pack (with the AVG pre-divide), then rebind gradients to the buckets; inside
+        :meth:`no_sync`, nothing (``ddp.py:574-577``)."""
+        if not self._require_backward_grad_sync:
+            return
         self.pack()
         self.bind_gradients()
         self.statistics.steps += 1

@@ -147,3 +147,30 @@ def test_non_contiguous_gradients_are_packed(device):
     for name, p in named:
         assert p.grad.is_contiguous()
         assert np.array_equal(p.grad.detach().cpu().numpy().view(np.int32), expect[name].view(np.int32)), name
+
+
+def test_no_sync_accumulates_then_packs_the_sum(device):
+    """``ddp.py:702-733``: inside ``no_sync`` the buckets stay untouched while the
+    micro-batches' gradients accumulate in ``param.grad`` (as autograd adds them); the
+    first synchronisation outside packs the averaged sum, bitwise numpy's."""
+    named = [(f"w{i}", torch.nn.Parameter(torch.empty(n, device=device))) for i, n in enumerate([300, 7, 4096])]
+    gen = torch.Generator(device=device).manual_seed(17)
+    micro = [[torch.randn(p.shape, device=device, generator=gen) for _, p in named] for _ in range(3)]
+    ddp = BucketedGradients(named, GroupHandle.local_view("data_parallel", 4, 0), DDPConfig())
+    for (_, p), g in zip(named, micro[0]):
+        p.grad = g.clone()
+    with ddp.no_sync():
+        ddp.synchronize()
+        for (_, p), g in zip(named, micro[1]):
+            p.grad.add_(g)
+        ddp.pack()
+    assert ddp.statistics.steps == 0 and not any(b.is_allocated for b in ddp.buckets)
+    for (_, p), g in zip(named, micro[2]):
+        p.grad.add_(g)
+    ddp.synchronize()
+    assert ddp.statistics.steps == 1
+    for i, (name, p) in enumerate(named):
+        total = micro[0][i].cpu().numpy() + micro[1][i].cpu().numpy()
+        total = (total + micro[2][i].cpu().numpy()).astype(np.float32)
+        expect = (total / np.float32(4)).astype(np.float32)
+        assert np.array_equal(p.grad.detach().cpu().numpy().view(np.int32), expect.view(np.int32)), name
