@@ -155,6 +155,40 @@ def test_build_and_load_from_host_tensors(device):
             assert np.array_equal(h.flat_param.detach().cpu().numpy().view(np.int32), expect.view(np.int32))
 
 
+def test_padding_only_ranks_and_empty_parameters(device):
+    """Three one-element parameters and an empty one over 8 ranks: ranks 3-7 hold only
+    padding.  Every rank's shard, pieces, gathered tensors, local share and no_sync
+    result follow the reference's layout rules, bitwise against the oracle."""
+    values = [torch.tensor([1.5], device=device), torch.empty(0, device=device),
+              torch.tensor([-2.25], device=device), torch.tensor([0.75], device=device)]
+    named = [(f"t{i}", torch.nn.Parameter(v.clone())) for i, v in enumerate(values)]
+    group = 8
+    handles = [FlatParamHandle(named, None, GroupHandle.local_view("shard", group, r), FSDPConfig(),
+                               MixedPrecisionConfig(), device, keep_originals=True) for r in range(group)]
+    host = [v.cpu().numpy() for v in values]
+    assert (handles[0].total_numel, handles[0].shard_numel, handles[0].padding) == (3, 1, 5)
+    for rank, h in enumerate(handles):
+        expect = oracle.pack_shard(host, group, rank)
+        assert np.array_equal(h.flat_param.detach().cpu().numpy().view(np.int32), expect.view(np.int32))
+        assert [p.name for p in h.local_piece_layout()] == ([["t0"], ["t2"], ["t3"]][rank] if rank < 3 else [])
+    full = handles[0].full_tensors(peer_shards=[h.flat_param for h in handles])
+    for (name, _), v in zip(named, values):
+        assert torch.equal(full[name], v) and full[name].shape == v.shape
+    gen = torch.Generator(device=device).manual_seed(2)
+    micro = [[torch.randn(group, device=device, generator=gen) for _ in range(group)] for _ in range(2)]
+    for rank, h in enumerate(handles):
+        out = h.reduce_scatter_gradient(micro[0][rank], peer_grads=micro[0])
+        expect = oracle.local_share([g.cpu().numpy() for g in micro[0]], rank, 1, 1 if rank < 3 else 0, 8.0)
+        assert np.array_equal(out.cpu().numpy().view(np.int32), expect.view(np.int32))
+        h.set_accumulate_without_reduction(True)
+        assert h.reduce_scatter_gradient(micro[0][rank], peer_grads=micro[0]) is None
+        h.set_accumulate_without_reduction(False)
+        out = h.reduce_scatter_gradient(micro[1][rank], peer_grads=micro[1])
+        totals = [oracle.no_sync_accumulate([micro[m][q].cpu().numpy() for m in range(2)]) for q in range(group)]
+        expect = oracle.local_share(totals, rank, 1, 1 if rank < 3 else 0, 8.0)
+        assert np.array_equal(out.cpu().numpy().view(np.int32), expect.view(np.int32))
+
+
 def test_norm_weights_and_padding_runs(device):
     _, _, handles = _handles(MLP_1857_REFERENCE, 4, device)
     last = handles[-1]
