@@ -1,11 +1,12 @@
-"""Seeded random FSDP configurations through the whole flat-parameter path (GPU).
+"""Seeded random configurations through the flat-parameter, checkpoint and DDP paths (GPU).
 
 Each case draws a parameter list (odd sizes, empty tensors and multiples of 256 mixed,
 so plans take both the aligned and the general copy kernel), a group size, parameter
 and gradient dtypes and a reduce dtype, then checks every rank bitwise against the
 oracle: the packed shard (``parallel/fsdp.py:434-454``), the gathered tensors
 (``:912-925``), the gradient local share (``:704-781``) and a two-micro-batch
-``no_sync`` reduction (``:733-749``).
+``no_sync`` reduction (``:733-749``).  Random checkpoint reshards and DDP bucket packs
+follow, each against the global vector or torch's own CPU arithmetic.
 """
 
 from __future__ import annotations
@@ -84,3 +85,74 @@ def test_random_fsdp_configurations(device, case):
                   for q in range(group)]
         expect = oracle.local_share(totals, rank, shard, valid, divisor, _NAMES[reduce])
         assert np.array_equal(out.cpu().numpy().view(np.int32), expect.view(np.int32)), (context, rank)
+
+
+@pytest.mark.parametrize("case", range(60))
+def test_random_checkpoint_reshards(device, case):
+    """Random layouts saved by 1-5 writers as per-tensor shard records and loaded by 1-6
+    readers (``checkpoint/reshard.py:200-305``, ``checkpoint/reader.py:328-351``): every
+    reader's shard is the matching slice of the global flat vector, cast to the
+    destination dtype as torch casts it, and its padding tail is left untouched."""
+    from hybrid_training_amd import load_flat_shard
+
+    from .test_gpu_reshard import _layout, _save
+
+    rng = np.random.default_rng(5000 + case)
+    shapes = _shapes(rng)
+    named = [(f"p{i}", s) for i, s in enumerate(shapes)]
+    src_dtype = [torch.float32, torch.bfloat16][int(rng.integers(0, 2))]
+    dst_dtype = [torch.float32, torch.bfloat16][int(rng.integers(0, 2))]
+    writers, readers = int(rng.integers(1, 6)), int(rng.integers(1, 7))
+    total = sum(int(np.prod(s)) for s in shapes)
+    gen = torch.Generator(device=device).manual_seed(case)
+    flat = torch.randn(total, device=device, generator=gen).to(src_dtype)
+    s_src, padded_src, _ = oracle.even_shards(total, writers)
+    padded = torch.zeros(padded_src, dtype=src_dtype, device=device)
+    padded[:total] = flat
+    shards = [padded[r * s_src:(r + 1) * s_src].clone() for r in range(writers)]
+    records, cache = _save(named, shards, s_src, str(src_dtype))
+    expect_flat = flat.cpu().to(dst_dtype)
+    s_dst, _, _ = oracle.even_shards(total, readers)
+    context = f"case {case}: shapes {shapes}, {writers} -> {readers}, {src_dtype} -> {dst_dtype}"
+    for rank in range(readers):
+        dest = torch.full((s_dst,), 7.0, device=device).to(dst_dtype)
+        load_flat_shard(dest, _layout(named, rank, s_dst), records, cache)
+        valid = max(0, min(s_dst, total - rank * s_dst))
+        got = dest.cpu()
+        assert torch.equal(got[:valid], expect_flat[rank * s_dst:rank * s_dst + valid]), (context, rank)
+        assert bool((got[valid:] == 7.0).all()), (context, rank)
+
+
+@pytest.mark.parametrize("case", range(60))
+def test_random_ddp_bucket_packs(device, case):
+    """Random fp32/bf16 parameter lists, bucket caps and world sizes, with unused
+    parameters (``parallel/ddp.py:397-463``, ``:479-523``, ``:579-640``): every gradient
+    comes back as its bucket view holding ``grad / W`` rounded to its dtype, as torch's
+    CPU ``div`` gives, and an unused parameter's view holds zeros."""
+    from hybrid_training_amd import BucketedGradients, DDPConfig
+
+    rng = np.random.default_rng(9000 + case)
+    shapes = _shapes(rng)
+    world = int(rng.integers(1, 9))
+    cap_mb = float(rng.choice([1e-5, 1e-3, 0.01, 25.0]))
+    gen = torch.Generator(device=device).manual_seed(case)
+    named, expect = [], {}
+    for i, s in enumerate(shapes):
+        dtype = [torch.float32, torch.bfloat16][int(rng.integers(0, 2))]
+        p = torch.nn.Parameter(torch.empty(s, device=device, dtype=dtype))
+        if rng.random() < 0.15:
+            expect[f"p{i}"] = torch.zeros(s, dtype=dtype)
+        else:
+            p.grad = torch.randn(s, device=device, generator=gen).to(dtype)
+            g = p.grad.detach().cpu()
+            expect[f"p{i}"] = g.div(world) if world > 1 else g
+        named.append((f"p{i}", p))
+    group = GroupHandle.local_view("data_parallel", world, 0) if world > 1 else GroupHandle.trivial()
+    ddp = BucketedGradients(named, group, DDPConfig(bucket_cap_mb=cap_mb, find_unused_parameters=True))
+    ddp.synchronize()
+    context = f"case {case}: shapes {shapes}, W={world}, cap {cap_mb} MB"
+    for name, p in named:
+        got = p.grad.detach().cpu()
+        assert got.dtype == expect[name].dtype and got.shape == expect[name].shape, (context, name)
+        bits = torch.int16 if got.element_size() == 2 else torch.int32
+        assert torch.equal(got.contiguous().view(bits), expect[name].contiguous().view(bits)), (context, name)
