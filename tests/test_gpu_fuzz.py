@@ -6,7 +6,8 @@ and gradient dtypes and a reduce dtype, then checks every rank bitwise against t
 oracle: the packed shard (``parallel/fsdp.py:434-454``), the gathered tensors
 (``:912-925``), the gradient local share (``:704-781``) and a two-micro-batch
 ``no_sync`` reduction (``:733-749``).  Random checkpoint reshards and DDP bucket packs
-follow, each against the global vector or torch's own CPU arithmetic.
+follow, each against the global vector or torch's own CPU arithmetic, and random AdamW
+runs with the global-norm clip against the oracle.
 """
 
 from __future__ import annotations
@@ -156,3 +157,47 @@ def test_random_ddp_bucket_packs(device, case):
         assert got.dtype == expect[name].dtype and got.shape == expect[name].shape, (context, name)
         bits = torch.int16 if got.element_size() == 2 else torch.int32
         assert torch.equal(got.contiguous().view(bits), expect[name].contiguous().view(bits)), (context, name)
+
+
+@pytest.mark.parametrize("case", range(40))
+def test_random_adamw_clip_steps(device, case):
+    """Random parameter lists (up to 40 tensors, so launches split at 16, empty ones
+    included), hyperparameters (both branches of torch's lerp), clip thresholds and
+    deferred or in-place clipping, two steps of ``clip_grad_norm`` + ``step``
+    (``optim/sharded_optimizer.py:310-355``): parameters and state bitwise the oracle's
+    AdamW with the clip multiplier formed from the returned norm."""
+    from hybrid_training_amd import OptimizerConfig, ShardedOptimizer
+
+    rng = np.random.default_rng(7000 + case)
+    sizes = [int(rng.choice([0, 1, 7, 256, 1000, 4097])) if rng.random() < 0.3 else int(rng.integers(1, 20000))
+             for _ in range(int(rng.integers(1, 41)))]
+    lr = float(rng.choice([1e-4, 3e-4, 1e-3]))
+    betas = [(0.9, 0.95), (0.8, 0.999), (0.4, 0.9)][int(rng.integers(0, 3))]
+    wd = float(rng.choice([0.0, 0.01, 0.1]))
+    eps = float(rng.choice([1e-8, 1e-6]))
+    max_norm = float(rng.choice([1e-3, 0.05, 1.0, 100.0]))
+    defer = bool(rng.integers(0, 2))
+    gen = torch.Generator(device=device).manual_seed(case)
+    params = [torch.nn.Parameter(torch.randn(n, device=device, generator=gen) * 0.02) for n in sizes]
+    opt = ShardedOptimizer(params, OptimizerConfig(name="adamw", learning_rate=lr, betas=betas, weight_decay=wd,
+                                                   eps=eps), norm_group=GroupHandle.trivial(), device=device,
+                           defer_clip=defer)
+    P = [p.detach().cpu().numpy().copy() for p in params]
+    M = [np.zeros_like(a) for a in P]
+    V = [np.zeros_like(a) for a in P]
+    context = f"case {case}: {len(sizes)} tensors, lr {lr}, betas {betas}, wd {wd}, eps {eps}, clip {max_norm}, defer {defer}"
+    for step in (1, 2):
+        for p in params:
+            p.grad = torch.randn(p.shape, device=device, generator=gen) * 1e-3
+        G = [p.grad.detach().cpu().numpy().copy() for p in params]
+        norm = float(opt.clip_grad_norm(max_norm))
+        mul = oracle.clip_multiplier(norm, max_norm)
+        opt.step()
+        sc = oracle.adamw_scalars(lr=lr, beta1=betas[0], beta2=betas[1], eps=eps, weight_decay=wd, step=float(step))
+        for a, g, m, v in zip(P, G, M, V):
+            oracle.adamw_step(a, g, m, v, sc, grad_mul=mul)
+    for p, a, m, v in zip(params, P, M, V):
+        state = opt.inner.state[p]
+        assert np.array_equal(p.detach().cpu().numpy().view(np.int32), a.view(np.int32)), context
+        assert np.array_equal(state["exp_avg"].cpu().numpy().view(np.int32), m.view(np.int32)), context
+        assert np.array_equal(state["exp_avg_sq"].cpu().numpy().view(np.int32), v.view(np.int32)), context
