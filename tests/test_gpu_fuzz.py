@@ -7,7 +7,7 @@ oracle: the packed shard (``parallel/fsdp.py:434-454``), the gathered tensors
 (``:912-925``), the gradient local share (``:704-781``) and a two-micro-batch
 ``no_sync`` reduction (``:733-749``).  Random checkpoint reshards and DDP bucket packs
 follow, each against the global vector or torch's own CPU arithmetic, and random AdamW
-runs with the global-norm clip against the oracle.
+and SGD runs with the global-norm clip against the oracle.
 """
 
 from __future__ import annotations
@@ -201,3 +201,47 @@ def test_random_adamw_clip_steps(device, case):
         assert np.array_equal(p.detach().cpu().numpy().view(np.int32), a.view(np.int32)), context
         assert np.array_equal(state["exp_avg"].cpu().numpy().view(np.int32), m.view(np.int32)), context
         assert np.array_equal(state["exp_avg_sq"].cpu().numpy().view(np.int32), v.view(np.int32)), context
+
+
+@pytest.mark.parametrize("case", range(30))
+def test_random_sgd_clip_steps(device, case):
+    """Random SGD configurations (momentum, dampening, Nesterov, weight decay, learning
+    rate), parameter lists and clip thresholds, three steps of ``clip_grad_norm`` +
+    ``step`` (``optim/sharded_optimizer.py:121-126``, torch's ``_single_tensor_sgd``):
+    parameters and momentum buffers bitwise the oracle's."""
+    from hybrid_training_amd import OptimizerConfig, ShardedOptimizer
+
+    rng = np.random.default_rng(8000 + case)
+    sizes = [int(rng.integers(1, 30000)) for _ in range(int(rng.integers(1, 25)))]
+    lr = float(rng.choice([0.01, 0.05, 0.3]))
+    momentum = float(rng.choice([0.0, 0.5, 0.9]))
+    dampening = float(rng.choice([0.0, 0.25])) if momentum else 0.0
+    nesterov = bool(rng.integers(0, 2)) and momentum > 0 and dampening == 0.0
+    wd = float(rng.choice([0.0, 1e-4, 0.01]))
+    max_norm = float(rng.choice([0.01, 1.0, 1e3]))
+    defer = bool(rng.integers(0, 2))
+    gen = torch.Generator(device=device).manual_seed(case)
+    params = [torch.nn.Parameter(torch.randn(n, device=device, generator=gen)) for n in sizes]
+    opt = ShardedOptimizer(params, OptimizerConfig(name="sgd", learning_rate=lr, momentum=momentum, weight_decay=wd),
+                           norm_group=GroupHandle.trivial(), device=device, defer_clip=defer)
+    for group in opt.inner.param_groups:
+        group["dampening"] = dampening
+        group["nesterov"] = nesterov
+    P = [p.detach().cpu().numpy().copy() for p in params]
+    B = [np.zeros(n, np.float32) for n in sizes] if momentum else [None] * len(sizes)
+    context = (f"case {case}: {len(sizes)} tensors, lr {lr}, momentum {momentum}, dampening {dampening}, "
+               f"nesterov {nesterov}, wd {wd}, clip {max_norm}, defer {defer}")
+    for step in range(3):
+        for p in params:
+            p.grad = torch.randn(p.shape, device=device, generator=gen) * 0.1
+        G = [p.grad.detach().cpu().numpy().copy() for p in params]
+        mul = oracle.clip_multiplier(float(opt.clip_grad_norm(max_norm)), max_norm)
+        opt.step()
+        for a, g, b in zip(P, G, B):
+            oracle.sgd_step(a, g, b, lr=lr, momentum=momentum, dampening=dampening, weight_decay=wd,
+                            nesterov=nesterov, first=step == 0, grad_mul=mul)
+    for p, a, b in zip(params, P, B):
+        assert np.array_equal(p.detach().cpu().numpy().view(np.int32), a.view(np.int32)), context
+        if momentum:
+            buf = opt.inner.state[p]["momentum_buffer"].cpu().numpy()
+            assert np.array_equal(buf.view(np.int32), b.view(np.int32)), context
