@@ -7,7 +7,8 @@ oracle: the packed shard (``parallel/fsdp.py:434-454``), the gathered tensors
 (``:912-925``), the gradient local share (``:704-781``) and a two-micro-batch
 ``no_sync`` reduction (``:733-749``).  Random checkpoint reshards and DDP bucket packs
 follow, each against the global vector or torch's own CPU arithmetic, and random AdamW
-and SGD runs with the global-norm clip against the oracle.
+and SGD runs with the global-norm clip and loss-scaled runs with injected overflows
+against the oracle.
 """
 
 from __future__ import annotations
@@ -245,3 +246,69 @@ def test_random_sgd_clip_steps(device, case):
         if momentum:
             buf = opt.inner.state[p]["momentum_buffer"].cpu().numpy()
             assert np.array_equal(buf.view(np.int32), b.view(np.int32)), context
+
+
+@pytest.mark.parametrize("case", range(30))
+def test_random_loss_scaled_runs(device, case):
+    """Six engine steps (``training/engine.py:392-400``: ``unscale_``, ``clip_grad_norm``,
+    ``scaler.step``, ``update``) with random tensors, fp32 or bf16 gradients, deferred
+    or eager multipliers, growth intervals and inf/nan injected on random steps
+    (``optim/grad_scaler.py:164-269``).  A step is skipped exactly when some gradient is
+    non-finite, leaving parameters and state untouched and halving the scale; clean
+    steps are bitwise the oracle's AdamW with the unscale and the clip."""
+    from hybrid_training_amd import GradScaler, GradScalerConfig, OptimizerConfig, ShardedOptimizer
+
+    rng = np.random.default_rng(6000 + case)
+    sizes = [int(rng.integers(1, 50000)) for _ in range(int(rng.integers(1, 6)))]
+    bf16 = bool(rng.integers(0, 2))
+    defer = True if bf16 else bool(rng.integers(0, 2))
+    interval = int(rng.integers(1, 4))
+    max_norm = float(rng.choice([0.01, 1.0]))
+    gen = torch.Generator(device=device).manual_seed(case)
+    params = [torch.nn.Parameter(torch.randn(n, device=device, generator=gen) * 0.02) for n in sizes]
+    for p in params:
+        p.grad_dtype = None
+    opt = ShardedOptimizer(params, OptimizerConfig(learning_rate=3e-4, betas=(0.9, 0.95), weight_decay=0.1),
+                           norm_group=GroupHandle.trivial(), device=device, defer_clip=defer)
+    scaler = GradScaler(GradScalerConfig(enabled=True, init_scale=2.0**16, growth_interval=interval),
+                        GroupHandle.trivial(), device, defer_unscale=defer)
+    P = [p.detach().cpu().numpy().copy() for p in params]
+    M = [np.zeros(n, np.float32) for n in sizes]
+    V = [np.zeros(n, np.float32) for n in sizes]
+    taken, tracker = 0, 0
+    context = f"case {case}: sizes {sizes}, bf16 {bf16}, defer {defer}, interval {interval}, clip {max_norm}"
+    for step in range(6):
+        scale = scaler.scale_value
+        grads = [torch.randn(n, device=device, generator=gen) * 1e-4 * scale for n in sizes]
+        if bf16:
+            grads = [g.to(torch.bfloat16) for g in grads]
+        poison = rng.random() < 0.35
+        if poison:
+            victim = grads[int(rng.integers(0, len(grads)))]
+            victim[int(rng.integers(0, victim.numel()))] = float(rng.choice([np.inf, -np.inf, np.nan]))
+        for p, g in zip(params, grads):
+            p.grad = g
+        host = [(g.detach().cpu().view(torch.int16).numpy().view(np.uint16) if bf16 else g.detach().cpu().numpy())
+                for g in grads]
+        scaler.unscale_(params)
+        norm = float(opt.clip_grad_norm(max_norm))
+        stepped = scaler.step(opt, params, already_unscaled=True)
+        scaler.update()
+        opt.zero_grad(set_to_none=True)
+        nonfinite = any(not torch.isfinite(g.float()).all() for g in grads)
+        assert stepped == (not nonfinite), (context, step)
+        if nonfinite:
+            assert scaler.scale_value == max(scale / 2, 1.0) and scaler.state.growth_tracker == 0, (context, step)
+            tracker = 0
+        else:
+            taken += 1
+            sc = oracle.adamw_scalars(lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1, step=float(taken))
+            mul = oracle.clip_multiplier(norm, max_norm)
+            for a, g, m, v in zip(P, host, M, V):
+                oracle.adamw_step(a, g, m, v, sc, unscale=1.0 / scale, grad_mul=mul)
+            tracker += 1
+            grown = tracker == interval
+            tracker = 0 if grown else tracker
+            assert scaler.scale_value == (scale * 2 if grown else scale), (context, step)
+        for p, a in zip(params, P):
+            assert np.array_equal(p.detach().cpu().numpy().view(np.int32), a.view(np.int32)), (context, step)
