@@ -28,6 +28,28 @@ def test_header_and_binding_agree():
     assert declared == set(_native.EXPORTED_SYMBOLS), declared ^ set(_native.EXPORTED_SYMBOLS)
 
 
+# Entry points that compute on the path; the others are introspection helpers that
+# share the comment block of the entry point they serve.
+_HELPERS = {"hbt_last_error", "hbt_abi_version", "hbt_symbol_count", "hbt_copy_chunk_elems",
+            "hbt_norm_partials_count"}
+
+
+def test_every_entry_point_cites_the_reference_interface_it_replaces():
+    """Each compute entry point's comment block names the reference function it
+    replaces with a ``file.py:line`` citation."""
+    text = open(HEADER, encoding="utf-8").read()
+    blocks = re.split(r"/\* -{10,}", text)
+    cited = {}
+    for block in blocks:
+        comment, _, code = block.partition("*/")
+        code = re.sub(r"/\*.*?\*/", "", code, flags=re.S)
+        for name in re.findall(r"\b(hbt_[a-z0-9_]+)\s*\(", code):
+            cited[name] = "Replaces:" in comment and re.search(r"[a-z_/]+\.py:\d+", comment) is not None
+    compute = _declared_functions() - _HELPERS
+    assert compute <= set(cited), compute - set(cited)
+    assert all(cited[name] for name in compute), [name for name in compute if not cited[name]]
+
+
 def test_library_loads_and_exports_every_declared_symbol():
     lib = _native.library()
     for name in _declared_functions():
