@@ -91,8 +91,8 @@ def test_random_fsdp_configurations(device, case):
 
 @pytest.mark.parametrize("case", range(60))
 def test_random_checkpoint_reshards(device, case):
-    """Random layouts saved by 1-5 writers as per-tensor shard records and loaded by 1-6
-    readers (``checkpoint/reshard.py:200-305``, ``checkpoint/reader.py:328-351``): every
+    """Random layouts saved by 1-5 writers (fp32, bf16 or fp16) as per-tensor shard records
+    and loaded by 1-6 readers (``checkpoint/reshard.py:200-305``, ``checkpoint/reader.py:328-351``): every
     reader's shard is the matching slice of the global flat vector, cast to the
     destination dtype as torch casts it, and its padding tail is left untouched."""
     from hybrid_training_amd import load_flat_shard
@@ -102,8 +102,10 @@ def test_random_checkpoint_reshards(device, case):
     rng = np.random.default_rng(5000 + case)
     shapes = _shapes(rng)
     named = [(f"p{i}", s) for i, s in enumerate(shapes)]
-    src_dtype = [torch.float32, torch.bfloat16][int(rng.integers(0, 2))]
-    dst_dtype = [torch.float32, torch.bfloat16][int(rng.integers(0, 2))]
+    src_dtype = [torch.float32, torch.bfloat16, torch.float16][int(rng.integers(0, 3))]
+    # Same dtype, or a cast the copy kernel makes (fp32 <-> bf16 / fp16; not bf16 <-> fp16).
+    targets = [src_dtype] + ([torch.bfloat16, torch.float16] if src_dtype == torch.float32 else [torch.float32])
+    dst_dtype = targets[int(rng.integers(0, len(targets)))]
     writers, readers = int(rng.integers(1, 6)), int(rng.integers(1, 7))
     total = sum(int(np.prod(s)) for s in shapes)
     gen = torch.Generator(device=device).manual_seed(case)
