@@ -129,7 +129,7 @@ def test_random_checkpoint_reshards(device, case):
 
 @pytest.mark.parametrize("case", range(60))
 def test_random_ddp_bucket_packs(device, case):
-    """Random fp32/bf16 parameter lists, bucket caps and world sizes, with unused
+    """Random fp32/bf16/fp16 parameter lists, bucket caps and world sizes, with unused
     parameters (``parallel/ddp.py:397-463``, ``:479-523``, ``:579-640``): every gradient
     comes back as its bucket view holding ``grad / W`` rounded to its dtype, as torch's
     CPU ``div`` gives, and an unused parameter's view holds zeros."""
@@ -142,7 +142,7 @@ def test_random_ddp_bucket_packs(device, case):
     gen = torch.Generator(device=device).manual_seed(case)
     named, expect = [], {}
     for i, s in enumerate(shapes):
-        dtype = [torch.float32, torch.bfloat16][int(rng.integers(0, 2))]
+        dtype = [torch.float32, torch.bfloat16, torch.float16][int(rng.integers(0, 3))]
         p = torch.nn.Parameter(torch.empty(s, device=device, dtype=dtype))
         if rng.random() < 0.15:
             expect[f"p{i}"] = torch.zeros(s, dtype=dtype)
