@@ -8,7 +8,8 @@ oracle: the packed shard (``parallel/fsdp.py:434-454``), the gathered tensors
 ``no_sync`` reduction (``:733-749``).  Random checkpoint reshards and DDP bucket packs
 follow, each against the global vector or torch's own CPU arithmetic, and random AdamW
 and SGD runs with the global-norm clip and loss-scaled runs with injected overflows
-against the oracle; offloaded runs against the in-HBM path.
+against the oracle; offloaded runs against the in-HBM path; weighted norms against a
+brute-force fp64 sum.
 """
 
 from __future__ import annotations
@@ -357,3 +358,37 @@ def test_random_offloaded_runs(device, monkeypatch, case):
                 other = saved[1][index][key]
                 assert value.dtype == other.dtype == torch.float32, (context, index, key)
                 assert torch.equal(value.view(torch.int32), other.view(torch.int32)), (context, index, key)
+
+
+@pytest.mark.parametrize("case", range(30))
+def test_random_weighted_norms(device, case):
+    """The deterministic fp64 norm (``optim/sharded_optimizer.py:145-158``, ``:215-241``)
+    over random segments of random fp32/bf16 tensors with the weights the path uses
+    (the partitioned width, 0 over padding, 1/W for replicated parameters): the sum is
+    within 1e-12 of a brute-force ``math.fsum`` of w * g^2 in fp64, the clip multiplier
+    is the oracle's, and two runs agree bitwise."""
+    import math
+
+    from hybrid_training_amd.optim import gradient_norm_pass
+
+    rng = np.random.default_rng(3000 + case)
+    gen = torch.Generator(device=device).manual_seed(case)
+    segments, terms = [], []
+    for _ in range(int(rng.integers(1, 30))):
+        dtype = [torch.float32, torch.bfloat16][int(rng.integers(0, 2))]
+        n = int(rng.integers(1, 200_000))
+        g = (torch.randn(n, device=device, generator=gen) * 1e-3).to(dtype)
+        start = int(rng.integers(0, n))
+        length = int(rng.integers(0, n - start + 1))
+        weight = float(rng.choice([0.0, 0.125, 0.5, 1.0, 2.0, 8.0]))
+        segments.append((g, start, length, weight))
+        values = g[start:start + length].double().cpu().numpy()
+        terms.extend((weight * values * values).tolist())
+    max_norm = float(rng.choice([1e-3, 1.0, 1e6]))
+    first = gradient_norm_pass(segments, device, max_norm=max_norm)
+    second = gradient_norm_pass(segments, device, max_norm=max_norm)
+    expect = math.fsum(terms)
+    got = float(first.sum)
+    assert abs(got - expect) <= 1e-12 * max(expect, 1e-300), (case, got, expect)
+    assert float(first.sum) == float(second.sum) and float(first.norm) == float(second.norm)
+    assert float(first.grad_mul) == oracle.clip_multiplier(float(first.norm), max_norm)
