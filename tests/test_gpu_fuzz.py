@@ -9,7 +9,8 @@ oracle: the packed shard (``parallel/fsdp.py:434-454``), the gathered tensors
 follow, each against the global vector or torch's own CPU arithmetic, and random AdamW
 and SGD runs with the global-norm clip and loss-scaled runs with injected overflows
 against the oracle; offloaded runs against the in-HBM path; weighted norms against a
-brute-force fp64 sum.
+brute-force fp64 sum; checkpoints saved and reloaded at random widths through the format
+on disk.
 """
 
 from __future__ import annotations
@@ -392,3 +393,60 @@ def test_random_weighted_norms(device, case):
     assert abs(got - expect) <= 1e-12 * max(expect, 1e-300), (case, got, expect)
     assert float(first.sum) == float(second.sum) and float(first.norm) == float(second.norm)
     assert float(first.grad_mul) == oracle.clip_multiplier(float(first.norm), max_norm)
+
+
+@pytest.mark.parametrize("case", range(12))
+def test_random_checkpoint_save_and_load(device, tmp_path, case):
+    """Random models saved by 1-5 FSDP writers after AdamW steps, through the on-disk
+    format (``checkpoint/writer.py:433-567``, ``checkpoint/manifest.py:313-561``,
+    ``checkpoint/reader.py:314-470``), and loaded at a random width: every reader's
+    shard, ``exp_avg``, ``exp_avg_sq`` and ``step`` are the saved global values
+    bitwise, and its padding stays zero."""
+    from hybrid_training_amd import (OptimizerConfig, ShardedOptimizer, collect_flat_shard_payload,
+                                     load_flat_shard_checkpoint, write_checkpoint)
+
+    rng = np.random.default_rng(2000 + case)
+    shapes = _shapes(rng)
+    writers, readers = int(rng.integers(1, 6)), int(rng.integers(1, 7))
+    steps = int(rng.integers(1, 3))
+    total = sum(int(np.prod(s)) for s in shapes)
+    gen = torch.Generator(device=device).manual_seed(case)
+
+    def world(group, seed):
+        init = torch.Generator(device=device).manual_seed(seed)
+        named = [(f"p{i}", torch.nn.Parameter(torch.randn(s, device=device, generator=init)))
+                 for i, s in enumerate(shapes)]
+        handles = [FlatParamHandle(named, None, GroupHandle.local_view("shard", group, r), FSDPConfig(),
+                                   MixedPrecisionConfig(), device, keep_originals=True) for r in range(group)]
+        opts = [ShardedOptimizer([h.flat_param], OptimizerConfig(learning_rate=1e-3, weight_decay=0.01),
+                                 norm_group=GroupHandle.local_view("world", group, r), device=device)
+                for r, h in enumerate(handles)]
+        return handles, opts
+
+    handles, opts = world(writers, 1)
+    for _ in range(steps):
+        for h, opt in zip(handles, opts):
+            h.flat_param.grad = torch.randn(h.shard_numel, device=device, generator=gen) * 1e-2
+            opt.step()
+    payloads = [(r, *collect_flat_shard_payload(h, rank=r, optimizer=o)) for r, (h, o) in
+                enumerate(zip(handles, opts))]
+    path = write_checkpoint(tmp_path, steps, payloads, topology={"fsdp": writers})
+
+    def flat_of(tensors):
+        return torch.cat([t.detach().reshape(-1) for t in tensors])[:total]
+
+    flat = flat_of([h.flat_param for h in handles])
+    m = flat_of([o.inner.state[h.flat_param]["exp_avg"] for h, o in zip(handles, opts)])
+    v = flat_of([o.inner.state[h.flat_param]["exp_avg_sq"] for h, o in zip(handles, opts)])
+    new_handles, new_opts = world(readers, 99)   # different values: everything must come from disk
+    context = f"case {case}: shapes {shapes}, {writers} -> {readers} ranks, {steps} steps"
+    for r, (h, o) in enumerate(zip(new_handles, new_opts)):
+        load_flat_shard_checkpoint(path, h, optimizer=o)
+        start = r * h.shard_numel
+        valid = max(0, min(h.shard_numel, total - start))
+        state = o.inner.state[h.flat_param]
+        assert torch.equal(h.flat_param.detach()[:valid], flat[start:start + valid]), (context, r)
+        assert float(h.flat_param.detach()[valid:].abs().sum()) == 0.0, (context, r)
+        assert torch.equal(state["exp_avg"][:valid], m[start:start + valid]), (context, r)
+        assert torch.equal(state["exp_avg_sq"][:valid], v[start:start + valid]), (context, r)
+        assert float(state["step"]) == float(steps), (context, r)
