@@ -406,49 +406,63 @@ def write_checkpoint(
         )
     staging = root / staging_directory_name(final.name, uuid.uuid4().hex[:12])
     staging.mkdir()
-    created_by = f"hybrid_training_amd {_version()}"
-    manifest = CheckpointManifest(writer_world_size=len(shards), topology=dict(topology or {}), step=step,
-                                  created_by=created_by)
-    optimizer_scalars: dict[str, Any] = {}
-    # One writer per rank, as in a multi-rank job; hashing and file writes release the GIL.
-    with ThreadPoolExecutor(max_workers=max(1, min(8, len(shards)))) as pool:
-        files = list(pool.map(lambda shard: _save_payload(staging / shard_filename(shard[0]), shard[1]), shards))
-    for (rank, payload, records, scalars), record in zip(shards, files):
-        manifest.files[record.name] = record
-        for item in records:
-            manifest.add_shard(
-                TensorRecord(key=item["key"], name=item["name"], global_shape=tuple(item["global_shape"]),
-                             dtype=item["dtype"], category=item["category"], partition_dim=item["partition_dim"],
-                             tensor_parallel_size=item["tensor_parallel_size"],
-                             tensor_parallel_rank=item["tensor_parallel_rank"], state_name=item["state_name"]),
-                ShardRecord(rank=item["rank"], file=item["file"], offset=item["offset"], length=item["length"],
-                            key=item["storage_key"], padding=item.get("padding", 0)),
-            )
-        for key, value in scalars.items():
-            if key in optimizer_scalars and optimizer_scalars[key] != value:
-                raise CheckpointError(
-                    format_error("checkpoint.save", f"optimizer state {key!r} differs between ranks",
-                                 rank=rank, expected=optimizer_scalars[key], observed=value)
+    try:
+        created_by = f"hybrid_training_amd {_version()}"
+        manifest = CheckpointManifest(writer_world_size=len(shards), topology=dict(topology or {}), step=step,
+                                      created_by=created_by)
+        optimizer_scalars: dict[str, Any] = {}
+        # One writer per rank, as in a multi-rank job; hashing and file writes release the GIL.
+        with ThreadPoolExecutor(max_workers=max(1, min(8, len(shards)))) as pool:
+            files = list(pool.map(lambda shard: _save_payload(staging / shard_filename(shard[0]), shard[1]), shards))
+        for (rank, payload, records, scalars), record in zip(shards, files):
+            manifest.files[record.name] = record
+            for item in records:
+                manifest.add_shard(
+                    TensorRecord(key=item["key"], name=item["name"], global_shape=tuple(item["global_shape"]),
+                                 dtype=item["dtype"], category=item["category"], partition_dim=item["partition_dim"],
+                                 tensor_parallel_size=item["tensor_parallel_size"],
+                                 tensor_parallel_rank=item["tensor_parallel_rank"], state_name=item["state_name"]),
+                    ShardRecord(rank=item["rank"], file=item["file"], offset=item["offset"], length=item["length"],
+                                key=item["storage_key"], padding=item.get("padding", 0)),
                 )
-            optimizer_scalars[key] = value
-    manifest.complete = True
-    manifest.validate()
-    metadata = {
-        "format_version": CURRENT_FORMAT_VERSION,
-        "created_by": created_by,
-        "training_state": {"step": step},
-        "scheduler": {},
-        "scaler": {},
-        "config": None,
-        "topology": dict(topology or {}),
-        "world_size": len(shards),
-        "rng": {"saved": False, "ranks": [], "meta": {}},
-        "optimizer_scalars": optimizer_scalars,
-        "extra": extra_metadata or {},
-    }
-    (staging / METADATA_FILENAME).write_text(json.dumps(metadata, indent=2, sort_keys=True), encoding="utf-8")
-    manifest.write(staging / MANIFEST_FILENAME)
-    staging.replace(final)
+            for key, value in scalars.items():
+                if key in optimizer_scalars and optimizer_scalars[key] != value:
+                    raise CheckpointError(
+                        format_error("checkpoint.save", f"optimizer state {key!r} differs between ranks",
+                                     rank=rank, expected=optimizer_scalars[key], observed=value)
+                    )
+                optimizer_scalars[key] = value
+        manifest.complete = True
+        manifest.validate()
+        metadata = {
+            "format_version": CURRENT_FORMAT_VERSION,
+            "created_by": created_by,
+            "training_state": {"step": step},
+            "scheduler": {},
+            "scaler": {},
+            "config": None,
+            "topology": dict(topology or {}),
+            "world_size": len(shards),
+            "rng": {"saved": False, "ranks": [], "meta": {}},
+            "optimizer_scalars": optimizer_scalars,
+            "extra": extra_metadata or {},
+        }
+        (staging / METADATA_FILENAME).write_text(json.dumps(metadata, indent=2, sort_keys=True), encoding="utf-8")
+        manifest.write(staging / MANIFEST_FILENAME)
+        staging.replace(final)
+    except Exception as error:
+        # As the reference reports a failed publish (checkpoint/writer.py:290-307): nothing was
+        # renamed into place, and the staging directory stays for inspection.
+        raise CheckpointError(
+            format_error(
+                "checkpoint.save",
+                "the checkpoint could not be published; nothing was renamed into place, so the "
+                "checkpoint directory is unchanged",
+                expected="a validated manifest covering every tensor exactly once",
+                observed=f"{type(error).__name__}: {error}",
+                resolution=f"the staging directory {staging.name!r} is left behind for inspection",
+            )
+        ) from error
     return final
 
 

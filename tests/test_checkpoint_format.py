@@ -120,6 +120,26 @@ def test_written_checkpoint_is_complete_and_verified(tmp_path):
         _cpu_checkpoint(tmp_path)
 
 
+def test_failed_publish_renames_nothing_and_keeps_the_staging_directory(tmp_path):
+    """``checkpoint/writer.py:290-307``: when the manifest cannot be validated (here two
+    writers claim the same elements) nothing is renamed into place, the error is the
+    reference's, and the staging directory stays for inspection."""
+    data = torch.arange(12, dtype=torch.float32)
+    shards = []
+    for rank in (0, 1):
+        records = [{"key": "w", "name": "w", "global_shape": [3, 4], "dtype": "torch.float32",
+                    "category": "model", "partition_dim": None, "tensor_parallel_size": 1,
+                    "tensor_parallel_rank": 0, "state_name": "", "rank": rank, "file": f"rank-0000{rank}.pt",
+                    "offset": 0, "length": 12, "storage_key": "model::w@0"}]
+        shards.append((rank, {"model::w@0": data.clone()}, records, {"step": 1}))
+    with pytest.raises(CheckpointError, match="could not be published") as info:
+        write_checkpoint(tmp_path, 1, shards)
+    assert "overlap" in str(info.value)
+    assert not (tmp_path / "checkpoint-step-000001").exists()
+    staged = [p for p in tmp_path.iterdir() if p.name.startswith(".staging")]
+    assert len(staged) == 1 and staged[0].name in str(info.value)
+
+
 def test_corruption_is_detected(tmp_path):
     path, _ = _cpu_checkpoint(tmp_path)
     manifest = CheckpointManifest.read(path / MANIFEST_FILENAME)
