@@ -106,6 +106,15 @@ constexpr int dtype_of() {
     return SB == 4 ? HBT_DTYPE_F32 : (H ? HBT_DTYPE_F16 : HBT_DTYPE_BF16);
 }
 
+// Element i of an array of B-byte floats (float64, float32, or bf16 / fp16 when H)
+// widened exactly to double: Tensor.to(float64).
+template <int B, bool H>
+__device__ __forceinline__ double widen_f64(const unsigned char* p, int64_t i) {
+    if constexpr (B == 8) return reinterpret_cast<const double*>(p)[i];
+    else if constexpr (B == 4) return static_cast<double>(reinterpret_cast<const float*>(p)[i]);
+    else return static_cast<double>(b16_to_f32<H>(reinterpret_cast<const uint16_t*>(p)[i]));
+}
+
 // ---- fixed-order reductions ----------------------------------------------------------
 // Butterfly over the 64 lanes of a wavefront; every lane ends with the same total and
 // the pairing order is fixed, so the result is reproducible bit for bit.

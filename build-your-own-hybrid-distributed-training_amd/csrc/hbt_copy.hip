@@ -455,6 +455,26 @@ __global__ __launch_bounds__(kShareBlock) void local_share_kernel(RankTable rank
     }
 }
 
+// Reduce dtype float64: the rank-order sum of widen(x_q) / divisor in double, rounded
+// once to fp32 (the fused kernel's arithmetic, without the norm).
+template <int SB, bool H>
+__global__ __launch_bounds__(kShareBlock) void local_share_f64_kernel(RankTable ranks, int32_t group_size,
+                                                                      int64_t offset, int64_t shard_numel,
+                                                                      int64_t valid_numel, double divisor,
+                                                                      float* __restrict__ out) {
+    const int64_t base = int64_t(blockIdx.x) * kShareTile;
+    const int64_t end = base + kShareTile < shard_numel ? base + kShareTile : shard_numel;
+    for (int64_t i = base + threadIdx.x; i < end; i += kShareBlock) {
+        float v = 0.0f;
+        if (i < valid_numel) {
+            double s = widen_f64<SB, H>(ranks.g[0], offset + i) / divisor;
+            for (int32_t q = 1; q < group_size; ++q) s = s + widen_f64<SB, H>(ranks.g[q], offset + i) / divisor;
+            v = static_cast<float>(s);
+        }
+        out[i] = v;
+    }
+}
+
 template <int SB, int DB, int OP, bool H = false>
 void launch_copy(const int64_t* table, int64_t count, int64_t chunks, float divisor, bool aligned,
                  hipStream_t s) {
@@ -584,12 +604,15 @@ int32_t hbt_grad_local_share(const void* const* rank_grads, int32_t group_size, 
                   static_cast<long long>(valid_numel));
         return HBT_ERR_INVALID_ARGUMENT;
     }
-    if (in_dtype != HBT_DTYPE_F32 && in_dtype != HBT_DTYPE_BF16 && in_dtype != HBT_DTYPE_F16) {
-        set_error("hbt_grad_local_share: input dtype %d is not F32, BF16 or F16", in_dtype);
+    const bool f64 = reduce_dtype == HBT_DTYPE_F64;
+    if (in_dtype != HBT_DTYPE_F32 && in_dtype != HBT_DTYPE_BF16 && in_dtype != HBT_DTYPE_F16 &&
+        !(f64 && in_dtype == HBT_DTYPE_F64)) {
+        set_error("hbt_grad_local_share: input dtype %d is not F32, BF16 or F16 (or F64 with reduce dtype F64)",
+                  in_dtype);
         return HBT_ERR_INVALID_ARGUMENT;
     }
-    if (reduce_dtype != HBT_DTYPE_F32 && reduce_dtype != HBT_DTYPE_BF16 && reduce_dtype != HBT_DTYPE_F16) {
-        set_error("hbt_grad_local_share: reduce dtype %d is not F32, BF16 or F16", reduce_dtype);
+    if (reduce_dtype != HBT_DTYPE_F32 && reduce_dtype != HBT_DTYPE_BF16 && reduce_dtype != HBT_DTYPE_F16 && !f64) {
+        set_error("hbt_grad_local_share: reduce dtype %d is not F32, BF16, F16 or F64", reduce_dtype);
         return HBT_ERR_INVALID_ARGUMENT;
     }
     RankTable ranks{};
@@ -609,7 +632,7 @@ int32_t hbt_grad_local_share(const void* const* rank_grads, int32_t group_size, 
     }
     // Vector path: every rank's slice and the output start on a 16-byte (fp32 input) or
     // 8-byte (bf16 or fp16 input) boundary.
-    const int elem = in_dtype == HBT_DTYPE_F32 ? 4 : 2;
+    const int elem = dtype_size(in_dtype);
     int32_t vec_ok = (reinterpret_cast<uintptr_t>(out) & 15u) == 0;
     for (int q = 0; q < group_size && vec_ok; ++q) {
         const uintptr_t a = reinterpret_cast<uintptr_t>(ranks.g[q]) + static_cast<uintptr_t>(offset * elem);
@@ -626,7 +649,15 @@ int32_t hbt_grad_local_share(const void* const* rank_grads, int32_t group_size, 
         else if (reduce_dtype == HBT_DTYPE_BF16) HBT_SHARE(SB, H, HBT_DTYPE_BF16); \
         else HBT_SHARE(SB, H, HBT_DTYPE_F16);                                  \
     } while (0)
-    if (in_dtype == HBT_DTYPE_F32) {
+#define HBT_SHARE64(SB, H)                                                                        \
+    local_share_f64_kernel<SB, H><<<grid, kShareBlock, 0, s>>>(ranks, group_size, offset, shard_numel, \
+                                                               valid_numel, static_cast<double>(divisor), out)
+    if (f64) {
+        if (in_dtype == HBT_DTYPE_F64) HBT_SHARE64(8, false);
+        else if (in_dtype == HBT_DTYPE_F32) HBT_SHARE64(4, false);
+        else if (in_dtype == HBT_DTYPE_BF16) HBT_SHARE64(2, false);
+        else HBT_SHARE64(2, true);
+    } else if (in_dtype == HBT_DTYPE_F32) {
         HBT_SHARE_RD(4, false);
     } else if (in_dtype == HBT_DTYPE_BF16) {
         HBT_SHARE_RD(2, false);
@@ -634,6 +665,7 @@ int32_t hbt_grad_local_share(const void* const* rank_grads, int32_t group_size, 
         HBT_SHARE_RD(2, true);
     }
 #undef HBT_SHARE_RD
+#undef HBT_SHARE64
 #undef HBT_SHARE
     return check_launch("hbt_grad_local_share");
 }

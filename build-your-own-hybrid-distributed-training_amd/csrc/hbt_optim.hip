@@ -458,6 +458,33 @@ __global__ __launch_bounds__(kShareBlock) void local_share_tiles_kernel(
     if (threadIdx.x == 0) tile_sums[blockIdx.x] = acc;
 }
 
+// Reduce dtype float64: each rank's element widens exactly to double (SB = 8 reads a
+// float64 no_sync accumulator), the divide and the rank-order sum run in double, both
+// correctly rounded as torch's float64 div and add are, and the sum rounds once, to
+// nearest even, to the fp32 master (Tensor.to).  Lane l owns elements 4l .. 4l + 3 of
+// its tile, so the tile sums add the squares in the fp32 kernel's order.
+template <int SB, bool H>
+__global__ __launch_bounds__(kShareBlock) void local_share_f64_tiles_kernel(
+    ShareRanks ranks, int32_t group_size, int64_t offset, int64_t shard_numel, int64_t valid_numel,
+    double divisor, float* __restrict__ out, double* __restrict__ tile_sums) {
+    const int64_t first = int64_t(blockIdx.x) * kShareTile + int64_t(threadIdx.x) * 4;
+    double acc = 0.0;
+    for (int j = 0; j < 4; ++j) {
+        const int64_t e = first + j;
+        if (e >= shard_numel) break;
+        float v = 0.0f;
+        if (e < valid_numel) {
+            double s = widen_f64<SB, H>(ranks.g[0], offset + e) / divisor;
+            for (int32_t q = 1; q < group_size; ++q) s = s + widen_f64<SB, H>(ranks.g[q], offset + e) / divisor;
+            v = static_cast<float>(s);
+        }
+        out[e] = v;
+        acc += sq(v);
+    }
+    acc = wave_sum(acc);
+    if (threadIdx.x == 0) tile_sums[blockIdx.x] = acc;
+}
+
 // Chunk c < valid_chunks: the sum of tile sums 128c .. 128c + 127 (those below
 // valid_tiles); padding chunks: 0, the square sum of zeros.
 __global__ __launch_bounds__(kShareBlock) void tile_sums_to_partials_kernel(
@@ -708,6 +735,24 @@ inline bool aligned(const void* ptr, uintptr_t bytes) {
 
 using namespace hbt;
 
+// Accumulator float64: the gradient widens exactly (Tensor.to) and each add runs in
+// double, as add_ on float64 tensors does; kAssign writes the widened gradient.
+template <int SB, bool SH, bool kAssign>
+__global__ __launch_bounds__(kScaleBlock) void accumulate_f64_kernel(AccumTable tab) {
+    const int64_t block = blockIdx.x;
+    int t = 0;
+    while (t + 1 < tab.count && block >= tab.first_block[t + 1]) ++t;
+    const int64_t base = (block - tab.first_block[t]) * kAccumTile;
+    const int64_t n = tab.n[t];
+    double* __restrict__ acc = static_cast<double*>(tab.acc[t]);
+    const unsigned char* __restrict__ grad = static_cast<const unsigned char*>(tab.grad[t]);
+    const int64_t end = base + kAccumTile < n ? base + kAccumTile : n;
+    for (int64_t i = base + threadIdx.x; i < end; i += kScaleBlock) {
+        const double g = widen_f64<SB, SH>(grad, i);
+        acc[i] = kAssign ? g : acc[i] + g;
+    }
+}
+
 extern "C" {
 
 int32_t hbt_adamw_step(float* const* params, const void* const* grads, float* const* exp_avgs,
@@ -933,8 +978,10 @@ int32_t hbt_grad_accumulate(void* const* accumulators, const void* const* grads,
     const auto float_code = [](int32_t d) {
         return d == HBT_DTYPE_F32 || d == HBT_DTYPE_BF16 || d == HBT_DTYPE_F16;
     };
-    if (!float_code(acc_dtype) || !float_code(grad_dtype)) {
-        set_error("hbt_grad_accumulate: dtypes (accumulator %d, gradient %d) must be F32, BF16 or F16",
+    const bool f64 = acc_dtype == HBT_DTYPE_F64;
+    if (!(float_code(acc_dtype) || f64) || !(float_code(grad_dtype) || (f64 && grad_dtype == HBT_DTYPE_F64))) {
+        set_error("hbt_grad_accumulate: dtypes (accumulator %d, gradient %d) must be F32, BF16 or F16 "
+                  "(or an F64 accumulator, whose gradient may also be F64)",
                   acc_dtype, grad_dtype);
         return HBT_ERR_INVALID_ARGUMENT;
     }
@@ -980,7 +1027,17 @@ int32_t hbt_grad_accumulate(void* const* accumulators, const void* const* grads,
         else if (acc_dtype == HBT_DTYPE_BF16) HBT_ACC(SB, SH, 2, false);            \
         else HBT_ACC(SB, SH, 2, true);                                             \
     } while (0)
-    if (grad_dtype == HBT_DTYPE_F32) {
+#define HBT_ACC64(SB, SH)                                                                    \
+    do {                                                                                     \
+        if (assign) accumulate_f64_kernel<SB, SH, true><<<grid, kScaleBlock, 0, st>>>(tab);   \
+        else accumulate_f64_kernel<SB, SH, false><<<grid, kScaleBlock, 0, st>>>(tab);         \
+    } while (0)
+    if (f64) {
+        if (grad_dtype == HBT_DTYPE_F64) HBT_ACC64(8, false);
+        else if (grad_dtype == HBT_DTYPE_F32) HBT_ACC64(4, false);
+        else if (grad_dtype == HBT_DTYPE_BF16) HBT_ACC64(2, false);
+        else HBT_ACC64(2, true);
+    } else if (grad_dtype == HBT_DTYPE_F32) {
         HBT_ACC_A(4, false);
     } else if (grad_dtype == HBT_DTYPE_BF16) {
         HBT_ACC_A(2, false);
@@ -988,6 +1045,7 @@ int32_t hbt_grad_accumulate(void* const* accumulators, const void* const* grads,
         HBT_ACC_A(2, true);
     }
 #undef HBT_ACC_A
+#undef HBT_ACC64
 #undef HBT_ACC
     return check_launch("hbt_grad_accumulate");
 }
@@ -1005,16 +1063,19 @@ int32_t hbt_grad_local_share_sqnorm(const void* const* rank_grads, int32_t group
                   group_size, rank, static_cast<long long>(shard_numel), static_cast<long long>(valid_numel));
         return HBT_ERR_INVALID_ARGUMENT;
     }
-    if (in_dtype != HBT_DTYPE_F32 && in_dtype != HBT_DTYPE_BF16 && in_dtype != HBT_DTYPE_F16) {
-        set_error("hbt_grad_local_share_sqnorm: input dtype %d is not F32, BF16 or F16", in_dtype);
+    const bool f64 = reduce_dtype == HBT_DTYPE_F64;
+    if (in_dtype != HBT_DTYPE_F32 && in_dtype != HBT_DTYPE_BF16 && in_dtype != HBT_DTYPE_F16 &&
+        !(f64 && in_dtype == HBT_DTYPE_F64)) {
+        set_error("hbt_grad_local_share_sqnorm: input dtype %d is not F32, BF16 or F16 (or F64 with reduce dtype F64)",
+                  in_dtype);
         return HBT_ERR_INVALID_ARGUMENT;
     }
-    if (reduce_dtype != HBT_DTYPE_F32 && reduce_dtype != HBT_DTYPE_BF16 && reduce_dtype != HBT_DTYPE_F16) {
-        set_error("hbt_grad_local_share_sqnorm: reduce dtype %d is not F32, BF16 or F16", reduce_dtype);
+    if (reduce_dtype != HBT_DTYPE_F32 && reduce_dtype != HBT_DTYPE_BF16 && reduce_dtype != HBT_DTYPE_F16 && !f64) {
+        set_error("hbt_grad_local_share_sqnorm: reduce dtype %d is not F32, BF16, F16 or F64", reduce_dtype);
         return HBT_ERR_INVALID_ARGUMENT;
     }
     ShareRanks ranks{};
-    const int elem = in_dtype == HBT_DTYPE_F32 ? 4 : 2;
+    const int elem = dtype_size(in_dtype);
     const int64_t offset = int64_t(rank) * shard_numel;
     int32_t vec_ok = aligned(out, 16);
     for (int q = 0; q < group_size; ++q) {
@@ -1066,7 +1127,15 @@ int32_t hbt_grad_local_share_sqnorm(const void* const* rank_grads, int32_t group
             HBT_TILES(SBYTES, 0, R, H, HBT_DTYPE_F16);                                        \
         }                                                                                     \
     } while (0)
-    if (in_dtype == HBT_DTYPE_F32) {
+#define HBT_TILES64(SBYTES, H)                                                                    \
+    local_share_f64_tiles_kernel<SBYTES, H><<<grid, kShareBlock, 0, st>>>(                          \
+        ranks, group_size, offset, shard_numel, valid_numel, static_cast<double>(divisor), out, tile_scratch)
+    if (f64) {
+        if (in_dtype == HBT_DTYPE_F64) HBT_TILES64(8, false);
+        else if (in_dtype == HBT_DTYPE_F32) HBT_TILES64(4, false);
+        else if (in_dtype == HBT_DTYPE_BF16) HBT_TILES64(2, false);
+        else HBT_TILES64(2, true);
+    } else if (in_dtype == HBT_DTYPE_F32) {
         if (recip_exact) HBT_TILES_RD(4, true, false); else HBT_TILES_RD(4, false, false);
     } else if (in_dtype == HBT_DTYPE_BF16) {
         if (recip_exact) HBT_TILES_RD(2, true, false); else HBT_TILES_RD(2, false, false);
@@ -1074,6 +1143,7 @@ int32_t hbt_grad_local_share_sqnorm(const void* const* rank_grads, int32_t group
         if (recip_exact) HBT_TILES_RD(2, true, true); else HBT_TILES_RD(2, false, true);
     }
 #undef HBT_TILES_RD
+#undef HBT_TILES64
 #undef HBT_TILES_G
 #undef HBT_TILES
     const hipError_t launched = hipGetLastError();

@@ -10,7 +10,7 @@ tensor work is the interval gather-copy kernel and the local-share kernel of
   into the shard, casting to the master dtype and zero-filling padding, in one
   launch; the reference materialises the whole padded buffer first and slices it.
 * ``reduce_scatter_gradient`` is the rank's local share of the AVG reduce-scatter:
-  cast to the reduce dtype (fp32, bf16 or fp16), divide by ``G`` and sum over the
+  cast to the reduce dtype (fp32, bf16, fp16 or fp64), divide by ``G`` and sum over the
   ranks' buffers in rank order with every step rounded to that dtype, widen to the
   fp32 master, zero the padding tail, and in the same pass the squared-norm partials
   of the result, which the next ``clip_grad_norm`` picks up instead of reading the
@@ -501,9 +501,10 @@ class FlatParamHandle:
         ``grad_full`` is this rank's padded full gradient.  With a group of size 1
         that is all there is; otherwise ``peer_grads`` must hold every rank's padded
         gradient (``grad_full`` among them, in rank order), summed in rank order.
-        The gradients are cast to the reduce dtype (float32, bfloat16 or float16), and
-        the AVG divide and the sum are rounded to it, as the reference's ops in that
-        dtype are (``collectives.py:593-594``); the result widens to the fp32 master.
+        The gradients are cast to the reduce dtype (float32, bfloat16, float16 or
+        float64), and the AVG divide and the sum are rounded to it, as the reference's
+        ops in that dtype are (``collectives.py:593-594``); the result is cast to the
+        fp32 master (exactly, or for float64 rounded to nearest even).
 
         Inside ``no_sync`` (:meth:`set_accumulate_without_reduction`) the gradients
         are accumulated in the reduce dtype instead and ``None`` is returned
@@ -511,13 +512,13 @@ class FlatParamHandle:
         it.  The next call outside ``no_sync`` adds its gradients to the accumulated
         ones and reduces the sums (``fsdp.py:747-749``).
         """
-        if self._reduce_dtype not in (torch.float32, torch.bfloat16, torch.float16) \
+        if self._reduce_dtype not in (torch.float32, torch.bfloat16, torch.float16, torch.float64) \
                 or self._master_dtype != torch.float32:
             raise UnsupportedFeatureError(
                 format_error(
                     "fsdp.reduce_scatter_gradient",
-                    "the local-share kernel reduces in float32, bfloat16 or float16 into a float32 "
-                    "master shard",
+                    "the local-share kernel reduces in float32, bfloat16, float16 or float64 into a "
+                    "float32 master shard",
                     observed=f"reduce {self._reduce_dtype}, master {self._master_dtype}",
                 )
             )

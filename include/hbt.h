@@ -32,7 +32,7 @@ extern "C" {
 #define HBT_DTYPE_F32 0
 #define HBT_DTYPE_BF16 1
 #define HBT_DTYPE_F16 2 /* copies, F32 <-> F16 casts and division; local-share, reduce and accumulate dtype */
-#define HBT_DTYPE_F64 3 /* byte copies only */
+#define HBT_DTYPE_F64 3 /* byte copies; local-share reduce dtype and accumulate dtype */
 
 /* ---- per-call limits ---------------------------------------------------------- */
 #define HBT_MAX_TENSORS_PER_LAUNCH 16 /* AdamW / norm tables; the host splits larger lists */
@@ -212,6 +212,11 @@ int32_t hbt_copy_intervals(const int64_t* table, int64_t count, int64_t total_ch
  * the fp32 master, and +0.0 for i >= valid_numel (the padding tail).  With
  * group_size == 1 this is the whole local share of one rank: cast to the reduce
  * dtype, AVG pre-divide, cast to the fp32 master dtype, zero padding.
+ * reduce_dtype F64 (which also admits in_dtype F64, the float64 no_sync accumulator)
+ * computes in double instead: out[i] = fp32(((x_0 / divisor + x_1 / divisor) + ...)),
+ * each x_q widened exactly, each quotient and sum correctly rounded in double and the
+ * sum rounded once to fp32 (round to nearest even), as torch's float64 ops and
+ * Tensor.to give.
  * ---------------------------------------------------------------------------- */
 #define HBT_MAX_LOCAL_RANKS 64
 int32_t hbt_grad_local_share(const void* const* rank_grads, int32_t group_size, int32_t rank,
@@ -254,8 +259,9 @@ int32_t hbt_grad_local_share_sqnorm(const void* const* rank_grads, int32_t group
  * even; the identity for F32), each element becomes
  *   acc = R(grad)                    with HBT_ACCUMULATE_ASSIGN (the clone; no read of acc)
  *   acc = R(acc + R(grad))           otherwise (the sum computed in fp32, rounded once)
- * where R(grad) is the cast (none when the dtypes match).  A gradient must not overlap
- * its accumulator.
+ * where R(grad) is the cast (none when the dtypes match).  An F64 accumulator (reduce
+ * dtype float64) takes F64 gradients too and adds in double: acc = acc + double(grad).
+ * A gradient must not overlap its accumulator.
  * ---------------------------------------------------------------------------- */
 #define HBT_ACCUMULATE_ASSIGN 1
 int32_t hbt_grad_accumulate(void* const* accumulators, const void* const* grads, const int64_t* numels,

@@ -67,10 +67,11 @@ PINNED_BY = {
     "(test_checkpoint_format.py:242-247); bitwise re-slicing of the global flat vector",
     "local_share": "torch Tensor.to(reduce dtype) + div + add + padding zero in fp32, bf16 and fp16, "
     "bitwise (order-free for G <= 2; collectives.py:593-594); padding tail exactly 0.0 "
-    "(test_fsdp.py:477-481)",
+    "(test_fsdp.py:477-481); in float64 against torch's float64 ops bitwise and, for G a power of two, "
+    "the exact rational mean rounded once to fp32",
     "no_sync_accumulate": "torch's own CPU sequence of fsdp.py:733-749 (to(reduce dtype), clone, add_, "
     "grad + accumulator) in fp32, bf16 and fp16, bitwise on signed zeros, subnormals, overflow and "
-    "random values",
+    "random values; in float64 bitwise against torch and equal to the exact sum",
     "round_to": "torch Tensor.to(bfloat16 / float16).to(float32) bitwise on specials and random values",
 }
 
@@ -289,7 +290,20 @@ def local_share(rank_grads: Sequence[np.ndarray], rank: int, shard: int, valid: 
     order (parallel/fsdp.py:733-769, distributed/collectives.py:593-594): each rank's
     slice cast to ``reduce``, divided by ``divisor`` and added, every result rounded to
     ``reduce``; then widened to fp32 with the padding tail zeroed.  ``rank_grads`` hold
-    each rank's padded full gradient widened to fp32 (bf16 and fp16 widen exactly)."""
+    each rank's padded full gradient widened to fp32 (bf16 and fp16 widen exactly).
+
+    ``reduce="float64"`` widens each slice to float64 (the rank grads may then also be
+    float64 arrays, the no_sync accumulator's rows), divides and sums in float64 and
+    rounds the sum once to fp32 (``Tensor.to``, round to nearest even)."""
+    if reduce == "float64":
+        div64 = np.float64(divisor)
+        with np.errstate(over="ignore", invalid="ignore"):
+            acc64 = np.asarray(rank_grads[0], dtype=np.float64)[rank * shard : (rank + 1) * shard] / div64
+            for g in rank_grads[1:]:
+                acc64 = acc64 + np.asarray(g, dtype=np.float64)[rank * shard : (rank + 1) * shard] / div64
+            out = acc64.astype(np.float32)
+        out[valid:] = 0.0
+        return out
     div = np.float32(divisor)
 
     def term(g: np.ndarray) -> np.ndarray:
@@ -312,7 +326,16 @@ def no_sync_accumulate(micro_grads: Sequence[np.ndarray], reduce: str = "float32
     fp16 widen exactly); all but the last ran inside ``no_sync``.  Each is cast to
     ``reduce``; the first is kept as it is (``clone``), each later one inside ``no_sync``
     is added to it (``add_``), and the last, synchronising one is added in front
-    (``grad + accumulator``), every sum rounded to ``reduce``."""
+    (``grad + accumulator``), every sum rounded to ``reduce``.  For ``reduce="float64"``
+    the sums run in float64 and the float64 array is returned."""
+    if reduce == "float64":
+        acc64 = np.array(micro_grads[0], dtype=np.float64, copy=True)
+        with np.errstate(over="ignore", invalid="ignore"):
+            for g in micro_grads[1:-1]:
+                acc64 = acc64 + np.asarray(g, dtype=np.float64)
+            if len(micro_grads) > 1:
+                acc64 = np.asarray(micro_grads[-1], dtype=np.float64) + acc64
+        return acc64
     acc = np.array(round_to(micro_grads[0], reduce), dtype=np.float32, copy=True)
     if len(micro_grads) == 1:
         return acc

@@ -33,16 +33,17 @@ pytestmark = pytest.mark.gpu
 
 def _bits(t: torch.Tensor) -> np.ndarray:
     t = t.detach().cpu().contiguous()
-    return t.view({2: torch.int16, 4: torch.int32}[t.element_size()]).numpy().copy()
+    return t.view({2: torch.int16, 4: torch.int32, 8: torch.int64}[t.element_size()]).numpy().copy()
 
 
-_REDUCE = {torch.float32: "float32", torch.bfloat16: "bfloat16", torch.float16: "float16"}
+_REDUCE = {torch.float32: "float32", torch.bfloat16: "bfloat16", torch.float16: "float16",
+           torch.float64: "float64"}
 
 
 @pytest.mark.parametrize("in_dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("group", [1, 3, 8])
 @pytest.mark.parametrize("misaligned", [False, True])
-@pytest.mark.parametrize("reduce", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("reduce", [torch.float32, torch.bfloat16, torch.float16, torch.float64])
 def test_local_share_tiles(device, in_dtype, group, misaligned, reduce):
     lib = _native.library()
     shard = 20_000
@@ -168,7 +169,7 @@ def test_local_share_full_size_rank7_of_llama3_8b_w8(device):
     torch.cuda.empty_cache()
 
 
-@pytest.mark.parametrize("acc_dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("acc_dtype", [torch.float32, torch.bfloat16, torch.float16, torch.float64])
 @pytest.mark.parametrize("grad_dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("assign", [False, True])
 def test_grad_accumulate_tiles(device, acc_dtype, grad_dtype, assign):
@@ -224,4 +225,5 @@ def test_grad_accumulate_tiles(device, acc_dtype, grad_dtype, assign):
                                    _native.dtype_code(grad_dtype), 0, stream) == -1
     assert lib.hbt_grad_accumulate(_native.pointer_array([accs[0].data_ptr()]),
                                    _native.pointer_array([grads[0].data_ptr()]), _native.int64_array([1]), 1,
-                                   _native.dtype_code(acc_dtype), 3, 0, stream) == -1  # fp64 gradients
+                                   0 if acc_dtype == torch.float64 else _native.dtype_code(acc_dtype), 3, 0,
+                                   stream) == -1  # fp64 gradients need an fp64 accumulator

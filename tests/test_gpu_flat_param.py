@@ -224,7 +224,7 @@ def _mp_handles(group, device, reduce):
 
 @pytest.mark.parametrize("group", [1, 2, 3, 4])
 @pytest.mark.parametrize("in_dtype", [torch.float32, torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("reduce", ["bfloat16", "float16"])
+@pytest.mark.parametrize("reduce", ["bfloat16", "float16", "float64"])
 def test_gradient_local_share_in_reduce_dtype_matches_oracle(device, group, in_dtype, reduce):
     """``MixedPrecisionConfig(reduce_dtype=...)``: the cast, the AVG divide and the rank sum
     rounded to bf16 or fp16 (``collectives.py:593-594`` in that dtype), widened to the
@@ -245,13 +245,16 @@ def test_gradient_local_share_in_reduce_dtype_matches_oracle(device, group, in_d
 
 
 def test_reduce_and_master_dtype_limits(device):
-    """A float64 reduction and a non-fp32 master shard have no kernel: refused up front."""
+    """A non-fp32 master shard has no kernel: refused up front."""
     named = _params(MLP_1857_REFERENCE, device)
-    for mp in (MixedPrecisionConfig(enabled=True, reduce_dtype="float64"),
-               MixedPrecisionConfig(enabled=True, master_dtype="bfloat16")):
-        h = FlatParamHandle(named, None, GroupHandle.trivial("shard"), FSDPConfig(), mp, device, keep_originals=True)
-        with pytest.raises(UnsupportedFeatureError, match="float32, bfloat16 or float16 into a float32 master"):
-            h.reduce_scatter_gradient(torch.zeros(h.padded_numel, device=device))
+    mp = MixedPrecisionConfig(enabled=True, master_dtype="bfloat16")
+    h = FlatParamHandle(named, None, GroupHandle.trivial("shard"), FSDPConfig(), mp, device, keep_originals=True)
+    with pytest.raises(UnsupportedFeatureError, match="float16 or float64 into a float32 master"):
+        h.reduce_scatter_gradient(torch.zeros(h.padded_numel, device=device))
+    # A float64 master is refused earlier, when the fp32 parameters are packed into it.
+    mp = MixedPrecisionConfig(enabled=True, reduce_dtype="float64", master_dtype="float64")
+    with pytest.raises(UnsupportedFeatureError, match="converts only between float32 and bfloat16 or float16"):
+        FlatParamHandle(named, None, GroupHandle.trivial("shard"), FSDPConfig(), mp, device, keep_originals=True)
 
 
 def test_local_share_needs_every_rank(device):
@@ -270,7 +273,7 @@ def test_local_share_needs_every_rank(device):
 @pytest.mark.parametrize("group", [1, 2, 3, 4])
 @pytest.mark.parametrize("in_dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("micro", [2, 4])
-@pytest.mark.parametrize("reduce", ["float32", "bfloat16", "float16"])
+@pytest.mark.parametrize("reduce", ["float32", "bfloat16", "float16", "float64"])
 def test_no_sync_accumulation_matches_oracle(device, group, in_dtype, micro, reduce):
     """``no_sync`` (``parallel/fsdp.py:733-749``): the first ``micro - 1`` micro-batches
     accumulate in the reduce dtype and return None; the last reduces the sums.  Bitwise

@@ -178,6 +178,52 @@ def test_oracle_no_sync_accumulate_against_torch(reduce, dtype, micro):
         assert not np.array_equal(from_zeros.view(np.uint32), got.view(np.uint32))
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_oracle_float64_local_share_against_torch_and_exact_mean(dtype):
+    """``reduce_dtype="float64"``: torch's own ops (``Tensor.to(float64)``, ``div(G)``,
+    the rank sum, ``Tensor.to(float32)``) pin the oracle bitwise for every G; for G a
+    power of two the float64 sum of fp32-representable values of one scale is exact,
+    so the result is also the exact rational mean rounded once to fp32."""
+    import functools
+    from fractions import Fraction
+
+    gen = torch.Generator().manual_seed(3)
+    for group, shard, pad in ((1, 9, 2), (2, 7, 1), (3, 8, 3), (4, 6, 0), (8, 5, 4)):
+        total = group * shard - pad
+        grads = [(torch.randn(group * shard, generator=gen) * 3.0).to(dtype) for _ in range(group)]
+        summed = functools.reduce(torch.add, [g.to(torch.float64).div(group) for g in grads]).to(torch.float32)
+        summed[total:] = 0.0
+        host = [g.float().numpy() for g in grads]
+        for rank in range(group):
+            valid = max(0, min(shard, total - rank * shard))
+            got = oracle.local_share(host, rank, shard, valid, float(group), "float64")
+            assert got.dtype == np.float32
+            assert np.array_equal(got.view(np.uint32), summed[rank * shard:(rank + 1) * shard].numpy().view(np.uint32))
+            if group & (group - 1) == 0:
+                for i in range(valid):
+                    exact = sum(Fraction(float(h[rank * shard + i])) for h in host) / group
+                    assert Fraction(float(exact)) == exact  # representable in float64
+                    assert got[i] == np.float32(float(exact))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("micro", [1, 2, 5])
+def test_oracle_float64_no_sync_against_torch(dtype, micro):
+    """The float64 accumulator: torch's op sequence pins the oracle bitwise, and for
+    values of one scale the float64 sum is the exact sum."""
+    from fractions import Fraction
+
+    gen = torch.Generator().manual_seed(micro)
+    grads = [(torch.randn(512, generator=gen) * 1e-2).to(dtype) for _ in range(micro)]
+    grads[0][:4] = -0.0
+    expect = _torch_no_sync(grads, torch.float64).numpy()
+    got = oracle.no_sync_accumulate([g.float().numpy() for g in grads], "float64")
+    assert got.dtype == np.float64
+    assert np.array_equal(got.view(np.uint64), expect.view(np.uint64))
+    for i in range(4, 512, 37):
+        assert Fraction(float(got[i])) == sum(Fraction(float(g[i])) for g in grads)
+
+
 @pytest.mark.parametrize("reduce", [torch.bfloat16, torch.float16])
 def test_oracle_round_to_against_torch(reduce):
     """``round_to`` is torch's cast to the reduce dtype and back, on specials (ties,

@@ -6,6 +6,7 @@ issues no device call.
 
 from __future__ import annotations
 
+import ctypes
 import os
 import re
 
@@ -83,8 +84,14 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     assert lib.hbt_grad_local_share_sqnorm(None, 1, 0, 1, 1, 0, 0, 1.0, None, None, None, None) == -1
     assert b"hbt_grad_local_share_sqnorm" in lib.hbt_last_error()
     assert lib.hbt_grad_accumulate(None, None, None, 0, 0, 0, 0, None) == 0  # empty table
-    assert lib.hbt_grad_accumulate(None, None, None, 0, 3, 0, 0, None) == -1  # fp64 accumulator
+    assert lib.hbt_grad_accumulate(None, None, None, 0, 3, 0, 0, None) == 0  # fp64 accumulator, empty table
+    assert lib.hbt_grad_accumulate(None, None, None, 0, 0, 3, 0, None) == -1  # fp64 gradient, fp32 accumulator
     assert b"F32, BF16 or F16" in lib.hbt_last_error()
+    assert lib.hbt_grad_accumulate(None, None, None, 0, 5, 0, 0, None) == -1  # unknown accumulator dtype
+    # fp64 input with an fp32 reduce dtype: refused by the dtype check, before any pointer is read
+    fake = ctypes.c_void_p(4096)
+    assert lib.hbt_grad_local_share(_native.pointer_array([4096]), 1, 0, 1, 1, 3, 0, 1.0, fake, None) == -1
+    assert b"input dtype 3" in lib.hbt_last_error()
     assert lib.hbt_grad_accumulate(None, None, None, 0, 0, 0, 2, None) == -1  # unknown flag
     assert lib.hbt_grad_accumulate(None, None, None, 1, 0, 0, 0, None) == -1  # null table
     assert lib.hbt_grad_norm_finalize(None, 5, 1.0, None, None, None, None, None) == -1
