@@ -24,7 +24,8 @@ from hybrid_training_amd import FlatParamHandle, FSDPConfig, GroupHandle, MixedP
 
 pytestmark = pytest.mark.gpu
 
-_NAMES = {torch.float32: "float32", torch.bfloat16: "bfloat16", torch.float16: "float16"}
+_NAMES = {torch.float32: "float32", torch.bfloat16: "bfloat16", torch.float16: "float16",
+          torch.float64: "float64"}
 
 
 def _shapes(rng: np.random.Generator) -> list[tuple[int, ...]]:
@@ -51,7 +52,7 @@ def test_random_fsdp_configurations(device, case):
     group = int(rng.integers(1, 10))
     param_dtype = [torch.float32, torch.bfloat16][int(rng.integers(0, 2))]
     grad_dtype = [torch.float32, torch.bfloat16, torch.float16][int(rng.integers(0, 3))]
-    reduce = [torch.float32, torch.bfloat16, torch.float16][int(rng.integers(0, 3))]
+    reduce = [torch.float32, torch.bfloat16, torch.float16, torch.float64][int(rng.integers(0, 4))]
     gen = torch.Generator(device=device).manual_seed(case)
     named = [(f"p{i}", torch.nn.Parameter(torch.randn(s, device=device, generator=gen).to(param_dtype)))
              for i, s in enumerate(shapes)]
