@@ -5,8 +5,16 @@
 // covers a table of up to HBT_MAX_TENSORS_PER_LAUNCH tensors, so a list of flat
 // shards (or of DDP-style per-parameter tensors) costs one launch per 16 tensors.
 #include <cmath>
+#include <mutex>
 
 #include "hbt_common.hpp"
+
+// Static scratch of hbt_grad_norm_noalloc: its per-chunk norm partials live here rather
+// than in a caller or library allocation.  Every device holds its own copy (2 MiB) until
+// the process ends.  In host code `scratch` names a host-side stand-in, not device memory:
+// the device address is looked up once per device with hipGetSymbolAddress
+// (noalloc_scratch below) and only that address is passed to kernels.
+static __device__ __align__(256) double scratch[HBT_NOALLOC_MAX_PARTIALS];
 
 namespace hbt {
 namespace {
@@ -730,6 +738,103 @@ inline bool aligned(const void* ptr, uintptr_t bytes) {
     return (reinterpret_cast<uintptr_t>(ptr) % bytes) == 0;
 }
 
+
+// ---- norm launch helpers (shared by the workspace and the no-allocation entry points) --
+// Validates a gradient table and fills the norm kernel's table; `chunks` is the number
+// of partials the launch writes.
+int32_t build_norm_table(const char* who, const void* const* grads, const int64_t* numels,
+                         const double* weights, int32_t count, int32_t grad_dtype, NormTable& tab,
+                         int64_t& chunks) {
+    if (count < 0 || count > kMaxT) {
+        set_error("%s: count must lie in [0, %d], got %d", who, kMaxT, count);
+        return HBT_ERR_INVALID_ARGUMENT;
+    }
+    if (grad_dtype != HBT_DTYPE_F32 && grad_dtype != HBT_DTYPE_BF16) {
+        set_error("%s: gradient dtype %d is not F32 or BF16", who, grad_dtype);
+        return HBT_ERR_INVALID_ARGUMENT;
+    }
+    if (count > 0 && (grads == nullptr || numels == nullptr || weights == nullptr)) {
+        set_error("%s: null pointer argument", who);
+        return HBT_ERR_INVALID_ARGUMENT;
+    }
+    tab = NormTable{};
+    tab.count = count;
+    const int64_t kChunk = grad_dtype == HBT_DTYPE_F32 ? norm_chunk<float>() : norm_chunk<uint16_t>();
+    chunks = 0;
+    for (int i = 0; i < count; ++i) {
+        if (numels[i] < 0 || (numels[i] > 0 && grads[i] == nullptr)) {
+            set_error("%s: tensor %d has a bad pointer or numel", who, i);
+            return HBT_ERR_INVALID_ARGUMENT;
+        }
+        tab.g[i] = grads[i];
+        tab.n[i] = numels[i];
+        tab.w[i] = weights[i];
+        tab.vec_ok[i] = aligned(grads[i], 16);
+        tab.first_chunk[i] = chunks;
+        chunks += (numels[i] + kChunk - 1) / kChunk;
+    }
+    tab.first_chunk[count] = chunks;
+    for (int i = count + 1; i <= kMaxT; ++i) tab.first_chunk[i] = chunks;
+    return HBT_OK;
+}
+
+// One sqnorm_kernel launch writing partials[0, chunks).
+int32_t launch_sqnorm(const char* who, const NormTable& tab, int64_t chunks, int32_t grad_dtype, float unscale,
+                      double* partials, hipStream_t st) {
+    if (chunks == 0) return HBT_OK;
+    if (chunks > 0x7FFFFFFFLL) {
+        set_error("%s: %lld chunks exceed the grid limit", who, static_cast<long long>(chunks));
+        return HBT_ERR_UNSUPPORTED;
+    }
+    const dim3 grid(static_cast<unsigned>(chunks));
+    const bool scaled = unscale != 1.0f;
+    if (grad_dtype == HBT_DTYPE_F32) {
+        if (scaled) {
+            sqnorm_kernel<float, true><<<grid, kNormBlock, 0, st>>>(tab, unscale, partials);
+        } else {
+            sqnorm_kernel<float, false><<<grid, kNormBlock, 0, st>>>(tab, unscale, partials);
+        }
+    } else {
+        if (scaled) {
+            sqnorm_kernel<uint16_t, true><<<grid, kNormBlock, 0, st>>>(tab, unscale, partials);
+        } else {
+            sqnorm_kernel<uint16_t, false><<<grid, kNormBlock, 0, st>>>(tab, unscale, partials);
+        }
+    }
+    return check_launch(who);
+}
+
+// ---- device address of the no-allocation norm's static scratch ------------------------
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+double* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// The device address of this device's copy of `scratch` (looked up on the first call per
+// device, with that device current).
+int32_t noalloc_scratch(const char* who, double** out) {
+    int device = -1;
+    hipError_t e = hipGetDevice(&device);
+    if (e != hipSuccess) return check_hip(e, who);
+    if (device < 0 || device >= kMaxScratchDevices) {
+        set_error("%s: device %d is beyond the %d devices the scratch table covers", who, device,
+                  kMaxScratchDevices);
+        return HBT_ERR_UNSUPPORTED;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_ptr[device] == nullptr) {
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return check_hip(e, who);
+        if (ptr == nullptr) {
+            set_error("%s: hipGetSymbolAddress returned a null scratch address", who);
+            return HBT_ERR_HIP;
+        }
+        g_scratch_ptr[device] = static_cast<double*>(ptr);
+    }
+    *out = g_scratch_ptr[device];
+    return HBT_OK;
+}
+
 }  // namespace
 }  // namespace hbt
 
@@ -855,60 +960,17 @@ int32_t hbt_grad_sqnorm_partials(const void* const* grads, const int64_t* numels
                                  const double* weights, int32_t count, int32_t grad_dtype,
                                  float unscale, double* partials, void* stream) {
     clear_error();
-    if (count < 0 || count > kMaxT) {
-        set_error("hbt_grad_sqnorm_partials: count must lie in [0, %d], got %d", kMaxT, count);
-        return HBT_ERR_INVALID_ARGUMENT;
-    }
-    if (grad_dtype != HBT_DTYPE_F32 && grad_dtype != HBT_DTYPE_BF16) {
-        set_error("hbt_grad_sqnorm_partials: gradient dtype %d is not F32 or BF16", grad_dtype);
-        return HBT_ERR_INVALID_ARGUMENT;
-    }
-    if (count > 0 && (grads == nullptr || numels == nullptr || weights == nullptr || partials == nullptr)) {
-        set_error("hbt_grad_sqnorm_partials: null pointer argument");
+    if (count > 0 && partials == nullptr) {
+        set_error("hbt_grad_sqnorm_partials: null partials pointer");
         return HBT_ERR_INVALID_ARGUMENT;
     }
     NormTable tab{};
-    tab.count = count;
-    const uintptr_t grad_align = 16;
-    const int64_t kChunk = grad_dtype == HBT_DTYPE_F32 ? norm_chunk<float>() : norm_chunk<uint16_t>();
     int64_t chunks = 0;
-    for (int i = 0; i < count; ++i) {
-        if (numels[i] < 0 || (numels[i] > 0 && grads[i] == nullptr)) {
-            set_error("hbt_grad_sqnorm_partials: tensor %d has a bad pointer or numel", i);
-            return HBT_ERR_INVALID_ARGUMENT;
-        }
-        tab.g[i] = grads[i];
-        tab.n[i] = numels[i];
-        tab.w[i] = weights[i];
-        tab.vec_ok[i] = aligned(grads[i], grad_align);
-        tab.first_chunk[i] = chunks;
-        chunks += (numels[i] + kChunk - 1) / kChunk;
-    }
-    tab.first_chunk[count] = chunks;
-    for (int i = count + 1; i <= kMaxT; ++i) tab.first_chunk[i] = chunks;
-    if (chunks == 0) return HBT_OK;
-    if (chunks > 0x7FFFFFFFLL) {
-        set_error("hbt_grad_sqnorm_partials: %lld chunks exceed the grid limit",
-                  static_cast<long long>(chunks));
-        return HBT_ERR_UNSUPPORTED;
-    }
-    const dim3 grid(static_cast<unsigned>(chunks));
-    hipStream_t st = as_stream(stream);
-    const bool scaled = unscale != 1.0f;
-    if (grad_dtype == HBT_DTYPE_F32) {
-        if (scaled) {
-            sqnorm_kernel<float, true><<<grid, kNormBlock, 0, st>>>(tab, unscale, partials);
-        } else {
-            sqnorm_kernel<float, false><<<grid, kNormBlock, 0, st>>>(tab, unscale, partials);
-        }
-    } else {
-        if (scaled) {
-            sqnorm_kernel<uint16_t, true><<<grid, kNormBlock, 0, st>>>(tab, unscale, partials);
-        } else {
-            sqnorm_kernel<uint16_t, false><<<grid, kNormBlock, 0, st>>>(tab, unscale, partials);
-        }
-    }
-    return check_launch("hbt_grad_sqnorm_partials");
+    const int32_t status = build_norm_table("hbt_grad_sqnorm_partials", grads, numels, weights, count,
+                                            grad_dtype, tab, chunks);
+    if (status != HBT_OK) return status;
+    return launch_sqnorm("hbt_grad_sqnorm_partials", tab, chunks, grad_dtype, unscale, partials,
+                         as_stream(stream));
 }
 
 int32_t hbt_grad_norm_finalize(const double* partials, int64_t count, double max_norm,
@@ -922,6 +984,37 @@ int32_t hbt_grad_norm_finalize(const double* partials, int64_t count, double max
     norm_finalize_kernel<<<1, kFinalBlock, 0, as_stream(stream)>>>(partials, count, max_norm, sum_out,
                                                                    norm_out, grad_mul_out, nonfinite_out);
     return check_launch("hbt_grad_norm_finalize");
+}
+
+int32_t hbt_grad_norm_noalloc(const void* const* grads, const int64_t* numels, const double* weights,
+                              int32_t count, int32_t grad_dtype, float unscale, double max_norm,
+                              double* sum_out, double* norm_out, float* grad_mul_out,
+                              int32_t* nonfinite_out, void* stream) {
+    clear_error();
+    NormTable tab{};
+    int64_t chunks = 0;
+    int32_t status = build_norm_table("hbt_grad_norm_noalloc", grads, numels, weights, count, grad_dtype,
+                                      tab, chunks);
+    if (status != HBT_OK) return status;
+    if (chunks > HBT_NOALLOC_MAX_PARTIALS) {
+        set_error("hbt_grad_norm_noalloc: the gradients need %lld norm partials, more than the %d the "
+                  "static scratch holds (at most %lld fp32 or %lld bf16 elements per call)",
+                  static_cast<long long>(chunks), HBT_NOALLOC_MAX_PARTIALS,
+                  static_cast<long long>(HBT_NOALLOC_MAX_PARTIALS * norm_chunk<float>()),
+                  static_cast<long long>(HBT_NOALLOC_MAX_PARTIALS * norm_chunk<uint16_t>()));
+        return HBT_ERR_UNSUPPORTED;
+    }
+    double* partials = nullptr;
+    status = noalloc_scratch("hbt_grad_norm_noalloc", &partials);
+    if (status != HBT_OK) return status;
+    hipStream_t st = as_stream(stream);
+    // Every slot below `chunks` is written by the norm kernel before the finalize
+    // kernel reads it, so the array needs no clearing between calls.
+    status = launch_sqnorm("hbt_grad_norm_noalloc", tab, chunks, grad_dtype, unscale, partials, st);
+    if (status != HBT_OK) return status;
+    norm_finalize_kernel<<<1, kFinalBlock, 0, st>>>(partials, chunks, max_norm, sum_out, norm_out,
+                                                   grad_mul_out, nonfinite_out);
+    return check_launch("hbt_grad_norm_noalloc");
 }
 
 int32_t hbt_scale_inplace(void* const* tensors, const int64_t* numels, int32_t count,

@@ -56,9 +56,9 @@ extern "C" {
 const char* hbt_last_error(void) { return hbt::g_last_error.c_str(); }
 
 // Bumped whenever an exported signature or a table layout changes.
-int32_t hbt_abi_version(void) { return 10; }
+int32_t hbt_abi_version(void) { return 11; }
 
 // Entry points declared in include/hbt.h (hbt_last_error .. hbt_scale_inplace).
-int32_t hbt_symbol_count(void) { return 14; }
+int32_t hbt_symbol_count(void) { return 15; }
 
 }  // extern "C"

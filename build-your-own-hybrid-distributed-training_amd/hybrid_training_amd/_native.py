@@ -53,7 +53,7 @@ __all__ = [
     "stream_of",
 ]
 
-ABI_VERSION = 10
+ABI_VERSION = 11
 MAX_TENSORS_PER_LAUNCH = 16
 MAX_LOCAL_RANKS = 64
 
@@ -115,6 +115,11 @@ EXPORTED_SYMBOLS: dict[str, tuple[object, tuple[object, ...]]] = {
     "hbt_grad_norm_finalize": (
         _c_i32,
         (_c_void_p, _c_i64, _c_f64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p),
+    ),
+    "hbt_grad_norm_noalloc": (
+        _c_i32,
+        (_ptr_array, _i64_array, _f64_array, _c_i32, _c_i32, _c_f32, _c_f64, _c_void_p, _c_void_p,
+         _c_void_p, _c_void_p, _c_void_p),
     ),
     "hbt_copy_chunk_elems": (_c_i64, (_c_i32, _c_i32)),
     "hbt_copy_intervals": (

@@ -143,6 +143,30 @@ int32_t hbt_grad_norm_finalize(const double* partials, int64_t count, double max
                                int32_t* nonfinite_out, void* stream);
 
 /* ------------------------------------------------------------------------------
+ * Weighted squared norm and clip coefficient with no allocation and no workspace.
+ *
+ * This entry point has no counterpart in the reference.  It is for callers that
+ * cannot allocate device memory: code under HIP graph capture, serving loops, or
+ * harnesses that forbid hipMalloc.  It computes exactly what hbt_grad_sqnorm_partials
+ * followed by hbt_grad_norm_finalize computes (same kernels, same partials layout,
+ * same summation order, so the outputs are bitwise equal), but keeps the partials in
+ * a static device array of HBT_NOALLOC_MAX_PARTIALS doubles (2 MiB per device, held
+ * until the process ends) instead of a caller workspace.  It calls no hipMalloc,
+ * hipFree or other allocating routine.
+ * Limit: hbt_norm_partials_count(numels, count, grad_dtype) must not exceed
+ * HBT_NOALLOC_MAX_PARTIALS (8,589,934,592 fp32 or 17,179,869,184 bf16 elements per
+ * call); a larger request returns HBT_ERR_UNSUPPORTED before any launch.
+ * Every call on one device shares that device's array: calls that overlap in time on
+ * one device (on different streams, or from different host threads) race.  Calls
+ * ordered on one stream do not.  The outputs are as for hbt_grad_norm_finalize.
+ * ---------------------------------------------------------------------------- */
+#define HBT_NOALLOC_MAX_PARTIALS 262144
+int32_t hbt_grad_norm_noalloc(const void* const* grads, const int64_t* numels, const double* weights,
+                              int32_t count, int32_t grad_dtype, float unscale, double max_norm,
+                              double* sum_out, double* norm_out, float* grad_mul_out,
+                              int32_t* nonfinite_out, void* stream);
+
+/* ------------------------------------------------------------------------------
  * Interval gather-copy: the one data-movement kernel behind flat-parameter
  * pack/pad/shard, unpack, DDP bucket pack with the AVG pre-divide, and
  * checkpoint interval resharding.

@@ -33,6 +33,9 @@ def test_header_and_binding_agree():
 # share the comment block of the entry point they serve.
 _HELPERS = {"hbt_last_error", "hbt_abi_version", "hbt_symbol_count", "hbt_copy_chunk_elems",
             "hbt_norm_partials_count"}
+# Entry points with no counterpart in the reference: their comment says so and names
+# the callers they serve instead of citing a reference function.
+_NO_COUNTERPART = {"hbt_grad_norm_noalloc"}
 
 
 def test_every_entry_point_cites_the_reference_interface_it_replaces():
@@ -45,7 +48,10 @@ def test_every_entry_point_cites_the_reference_interface_it_replaces():
         comment, _, code = block.partition("*/")
         code = re.sub(r"/\*.*?\*/", "", code, flags=re.S)
         for name in re.findall(r"\b(hbt_[a-z0-9_]+)\s*\(", code):
-            cited[name] = "Replaces:" in comment and re.search(r"[a-z_/]+\.py:\d+", comment) is not None
+            if name in _NO_COUNTERPART:
+                cited[name] = "no counterpart in the reference" in comment and "cannot allocate" in comment
+            else:
+                cited[name] = "Replaces:" in comment and re.search(r"[a-z_/]+\.py:\d+", comment) is not None
     compute = _declared_functions() - _HELPERS
     assert compute <= set(cited), compute - set(cited)
     assert all(cited[name] for name in compute), [name for name in compute if not cited[name]]
@@ -95,6 +101,15 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     assert lib.hbt_grad_accumulate(None, None, None, 0, 0, 0, 2, None) == -1  # unknown flag
     assert lib.hbt_grad_accumulate(None, None, None, 1, 0, 0, 0, None) == -1  # null table
     assert lib.hbt_grad_norm_finalize(None, 5, 1.0, None, None, None, None, None) == -1
+    # no-allocation norm: bad table, then a request beyond the static scratch, both refused
+    # on the host before the scratch address is looked up or anything is launched
+    assert lib.hbt_grad_norm_noalloc(None, None, None, 99, 0, 1.0, 1.0, None, None, None, None, None) == -1
+    assert b"count" in lib.hbt_last_error()
+    too_many = 32768 * 262144 + 1
+    status = lib.hbt_grad_norm_noalloc(_native.pointer_array([4096]), _native.int64_array([too_many]),
+                                       _native.double_array([1.0]), 1, 0, 1.0, 1.0, None, None, None, None, None)
+    assert status == -2
+    assert b"static scratch" in lib.hbt_last_error()
 
 
 def test_host_tensors_are_refused():
