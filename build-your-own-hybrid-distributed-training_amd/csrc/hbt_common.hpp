@@ -37,6 +37,33 @@ inline float exact_reciprocal(float divisor) {
     return exact ? std::ldexp(1.0f, 1 - exponent) : 0.0f;
 }
 
+// ---- launch limits -------------------------------------------------------------------
+// A HIP grid dimension holds at most 2^32 - 1 work-items (workgroups x workgroup size),
+// so a launch of `threads`-lane workgroups takes at most grid_max_blocks(threads)
+// workgroups.  Larger launches are split into consecutive slices of workgroups; slice k
+// covers blocks [k * grid_max_blocks, min((k + 1) * grid_max_blocks, blocks)), and each
+// kernel adds its slice's first block to blockIdx.x.
+constexpr int64_t kGridMaxItems = 0xFFFFFFFFLL;
+inline int64_t grid_max_blocks(int threads) { return threads > 0 ? kGridMaxItems / threads : 0; }
+inline int64_t grid_slice_count(int64_t blocks, int threads) {
+    const int64_t per = grid_max_blocks(threads);
+    return (blocks <= 0 || per <= 0) ? 0 : (blocks + per - 1) / per;
+}
+
+// Runs launch(first_block, slice_blocks) for every slice of a `blocks`-workgroup grid of
+// `threads`-lane workgroups and checks each launch; `who` names the caller in errors.
+template <typename Launch>
+int32_t launch_sliced(const char* who, int64_t blocks, int threads, Launch&& launch) {
+    const int64_t per = grid_max_blocks(threads);
+    for (int64_t first = 0; first < blocks; first += per) {
+        const int64_t n = blocks - first < per ? blocks - first : per;
+        launch(first, dim3(static_cast<unsigned>(n)));
+        const int32_t status = check_launch(who);
+        if (status != HBT_OK) return status;
+    }
+    return HBT_OK;
+}
+
 // ---- dtype helpers -------------------------------------------------------------------
 inline int dtype_size(int32_t dtype) {
     switch (dtype) {
@@ -90,14 +117,30 @@ __device__ __forceinline__ uint32_t f32_to_b16(float x) {
 }
 
 // x rounded to dtype RD and widened back to fp32, exactly: unchanged for HBT_DTYPE_F32;
-// round to nearest even for HBT_DTYPE_BF16 and HBT_DTYPE_F16, with the narrowing's
-// overflow and NaN rules above.  This is the value torch holds after an op whose result
-// dtype is RD (the op computed in fp32, then rounded once).
+// round to nearest even for HBT_DTYPE_BF16 and HBT_DTYPE_F16 (fp16: overflow to +-inf,
+// subnormals kept).  This is the value torch holds after an op whose result dtype is RD
+// (the op computed in fp32, then rounded once).  It uses gfx950's conversion
+// instructions (v_cvt_pk_bf16_f32, v_cvt_f16_f32), which round to nearest even in the
+// IEEE mode these kernels are built for; a NaN stays a NaN (its payload is not
+// specified here: every store of a 2-byte value goes through f32_to_b16 above).  The
+// empty asm makes the fp32 value opaque to the compiler, so the rounding stays an
+// explicit step: otherwise it folds fp32 arithmetic on widened 2-byte operands followed
+// by a narrowing into native 2-byte arithmetic (v_add_f16, v_fma_mixlo_f16), whose
+// single rounding differs from torch's fp32 operation rounded afterwards.  It costs no
+// instruction.
+__device__ __forceinline__ float opaque(float x) {
+    asm("" : "+v"(x));
+    return x;
+}
 template <int RD>
 __device__ __forceinline__ float round_to(float x) {
-    if constexpr (RD == HBT_DTYPE_BF16) return bf16_to_f32(f32_to_bf16(x));
-    else if constexpr (RD == HBT_DTYPE_F16) return f16_to_f32(f32_to_f16(x));
-    else return x;
+    if constexpr (RD == HBT_DTYPE_BF16) {
+        return static_cast<float>(static_cast<__bf16>(opaque(x)));
+    } else if constexpr (RD == HBT_DTYPE_F16) {
+        return static_cast<float>(static_cast<_Float16>(opaque(x)));
+    } else {
+        return x;
+    }
 }
 
 // The dtype code of SB-byte elements (a 2-byte element being fp16 when H, else bf16).

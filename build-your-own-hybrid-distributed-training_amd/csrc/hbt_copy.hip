@@ -1,4 +1,4 @@
-// Interval gather-copy and the FSDP gradient local share (gfx950).
+// Interval gather-copy (gfx950).
 //
 // One launch moves any number of [src, src + n) -> [dst, dst + n) intervals.  Each
 // interval is cut into chunks of 64 x 16 bytes of source (256 elements of a 4-byte
@@ -235,9 +235,9 @@ __device__ __forceinline__ int64_t owning_record(const int64_t* __restrict__ tab
 
 template <int SB, int DB, int OP, bool H>
 __global__ __launch_bounds__(kCopyBlock) void copy_kernel(const int64_t* __restrict__ table,
-                                                          int64_t count, float divisor) {
+                                                          int64_t count, float divisor, int64_t chunk_base) {
     static_assert(kCopyBlock == 64, "a workgroup is one wave; its chunk is one wave-wide span of 16-byte source loads");
-    const int64_t chunk = static_cast<int64_t>(blockIdx.x);
+    const int64_t chunk = chunk_base + static_cast<int64_t>(blockIdx.x);
     const int64_t* rec = table + 4 * owning_record(table, count, chunk);
     const gbyte* src = reinterpret_cast<const gbyte*>(static_cast<uintptr_t>(rec[0]));
     gbyte* dst = reinterpret_cast<gbyte*>(static_cast<uintptr_t>(rec[1]));
@@ -314,13 +314,13 @@ __global__ __launch_bounds__(kCopyBlock) void copy_kernel(const int64_t* __restr
 // finishes with an element loop in its last chunk.
 template <int SB, int DB, int OP, bool H>
 __global__ __launch_bounds__(kCopyBlock) void copy_aligned_kernel(const int64_t* __restrict__ table,
-                                                                  int64_t count, float divisor) {
+                                                                  int64_t count, float divisor, int64_t chunk_base) {
     constexpr int U = unit_elems<SB, DB>();
     constexpr int kSrcWords = U * SB / 4;
     constexpr int64_t kChunk = chunk_elems<SB, DB>();
     constexpr int kPerLane = static_cast<int>(kChunk / U / kCopyBlock);
     static_assert(kChunk == int64_t(kPerLane) * kCopyBlock * U, "a chunk is whole units on every lane");
-    const int64_t chunk = static_cast<int64_t>(blockIdx.x);
+    const int64_t chunk = chunk_base + static_cast<int64_t>(blockIdx.x);
     const int64_t* rec = table + 4 * owning_record(table, count, chunk);
     const int64_t e0 = (chunk - rec[3]) * kChunk;
     const int64_t n = rec[2];
@@ -367,157 +367,108 @@ __global__ __launch_bounds__(kCopyBlock) void copy_aligned_kernel(const int64_t*
     }
 }
 
-// ---- FSDP gradient local share -------------------------------------------------------
-struct RankTable {
-    const uint8_t* g[HBT_MAX_LOCAL_RANKS];
-};
-
-// One wavefront per workgroup and 256 shard elements per workgroup: each lane owns one
-// 4-element group (fp32 input: one 16-byte load per rank; bf16 or fp16 input: one
-// 8-byte load), adds the G ranks' quotients in rank order and stores 16 bytes.  Measured on
-// MI355X (8 bf16 ranks -> fp32): 6.0 TB/s, against 5.7 TB/s with two groups per lane.
-constexpr int kShareBlock = 64;
-constexpr int kShareGroups = 1;
-constexpr int64_t kShareTile = int64_t(kShareBlock) * 4 * kShareGroups;
-
-template <int SB, bool H>
-__device__ __forceinline__ f32x4 load_quad(const uint8_t* p) {
-    if constexpr (SB == 4) {
-        const u32x4v w = ldv<4>(p);
-        return f32x4{__uint_as_float(w.x), __uint_as_float(w.y), __uint_as_float(w.z), __uint_as_float(w.w)};
+// ---- element-wise conversions ----------------------------------------------------------
+// The dtype pairs the vector kernels do not move: float64 to or from another dtype, and
+// bf16 <-> fp16.  Each value widens exactly to double and narrows as torch's Tensor.to
+// does: to fp32 with one rounding to nearest even, then, for a 2-byte destination, to that
+// dtype (double -> fp32 -> bf16/fp16, as c10's conversions go; bf16 <-> fp16 through the
+// exact fp32 value).  A chunk is 1 KB of source, as in the vector kernels; lane l moves
+// elements l, l + 64, ... of it, so every load and store instruction of the wave covers
+// one contiguous span.
+template <int D>
+__device__ __forceinline__ double widen_elem(const gbyte* p) {
+    typedef __attribute__((address_space(1))) const double G64;
+    if constexpr (D == HBT_DTYPE_F64) return *reinterpret_cast<G64*>(p);
+    else if constexpr (D == HBT_DTYPE_F32) return static_cast<double>(__uint_as_float(load_elem<4>(p)));
+    else return static_cast<double>(b16_to_f32<D == HBT_DTYPE_F16>(load_elem<2>(p)));
+}
+template <int D>
+__device__ __forceinline__ void narrow_store(gbyte* p, double x) {
+    typedef __attribute__((address_space(1))) double G64;
+    if constexpr (D == HBT_DTYPE_F64) {
+        *reinterpret_cast<G64*>(p) = x;
+    } else if constexpr (D == HBT_DTYPE_F32) {
+        store_elem<4>(p, __float_as_uint(static_cast<float>(x)));
     } else {
-        const typename Vec<2>::type w = ldv<2>(p);
-        return f32x4{b16_to_f32<H>(w.x & 0xFFFFu), b16_to_f32<H>(w.x >> 16), b16_to_f32<H>(w.y & 0xFFFFu),
-                     b16_to_f32<H>(w.y >> 16)};
+        store_elem<2>(p, f32_to_b16<D == HBT_DTYPE_F16>(static_cast<float>(x)));
+    }
+}
+template <int D>
+constexpr int64_t elem_bytes() { return D == HBT_DTYPE_F64 ? 8 : (D == HBT_DTYPE_F32 ? 4 : 2); }
+
+template <int SD, int DD>
+__global__ __launch_bounds__(kCopyBlock) void convert_kernel(const int64_t* __restrict__ table, int64_t count,
+                                                             int64_t chunk_base) {
+    constexpr int64_t SB = elem_bytes<SD>();
+    constexpr int64_t DB = elem_bytes<DD>();
+    constexpr int64_t kChunk = int64_t(kCopyBlock) * 16 / SB;
+    const int64_t chunk = chunk_base + static_cast<int64_t>(blockIdx.x);
+    const int64_t* rec = table + 4 * owning_record(table, count, chunk);
+    const int64_t e0 = (chunk - rec[3]) * kChunk;
+    const int64_t n = rec[2];
+    const int64_t len = (n - e0) < kChunk ? (n - e0) : kChunk;
+    const gbyte* s = reinterpret_cast<const gbyte*>(static_cast<uintptr_t>(rec[0]));
+    gbyte* d = reinterpret_cast<gbyte*>(static_cast<uintptr_t>(rec[1])) + e0 * DB;
+    if (s != nullptr) s += e0 * SB;
+    for (int64_t i = threadIdx.x; i < len; i += kCopyBlock) {
+        narrow_store<DD>(d + i * DB, s != nullptr ? widen_elem<SD>(s + i * SB) : 0.0);
     }
 }
 
-// The reduce dtype's steps (RD: its dtype code): the gradient cast to RD unless it
-// already has that dtype, each quotient and each partial sum rounded to RD.  For RD = F32
-// every step is the identity.
-template <int RD>
-__device__ __forceinline__ f32x4 share_round4(f32x4 v) {
-    if constexpr (RD == HBT_DTYPE_F32) return v;
-    return f32x4{round_to<RD>(v.x), round_to<RD>(v.y), round_to<RD>(v.z), round_to<RD>(v.w)};
-}
-template <int SB, bool H, int RD>
-__device__ __forceinline__ f32x4 share_input4(const uint8_t* p) {
-    const f32x4 x = load_quad<SB, H>(p);
-    if constexpr (dtype_of<SB, H>() == RD) return x;
-    return share_round4<RD>(x);
-}
-template <int SB, bool H, int RD>
-__device__ __forceinline__ float share_input1(const uint8_t* p) {
-    const float x = elem_to_f32<SB, H>(load_elem<SB>(p));
-    if constexpr (dtype_of<SB, H>() == RD) return x;
-    return round_to<RD>(x);
-}
-
-template <int SB, bool H, int RD>
-__global__ __launch_bounds__(kShareBlock) void local_share_kernel(RankTable ranks, int32_t group_size,
-                                                                  int64_t offset, int64_t shard_numel,
-                                                                  int64_t valid_numel, float divisor,
-                                                                  int32_t vec_ok,
-                                                                  float* __restrict__ out) {
-    const int64_t base = int64_t(blockIdx.x) * kShareTile;
-    if (vec_ok && base + kShareTile <= valid_numel) {
-#pragma unroll
-        for (int u = 0; u < kShareGroups; ++u) {
-            const int64_t e = base + (int64_t(u) * kShareBlock + threadIdx.x) * 4;
-            f32x4 acc = share_round4<RD>(share_input4<SB, H, RD>(ranks.g[0] + (offset + e) * SB) / divisor);
-            for (int32_t q = 1; q < group_size; ++q) {
-                const f32x4 x = share_input4<SB, H, RD>(ranks.g[q] + (offset + e) * SB);
-                acc = share_round4<RD>(acc + share_round4<RD>(x / divisor));
-            }
-            stv<4>(out + e, u32x4v{__float_as_uint(acc.x), __float_as_uint(acc.y),
-                                     __float_as_uint(acc.z), __float_as_uint(acc.w)});
-        }
-        return;
-    }
-    if (vec_ok && base >= valid_numel && base + kShareTile <= shard_numel) {
-#pragma unroll
-        for (int u = 0; u < kShareGroups; ++u) {
-            const int64_t e = base + (int64_t(u) * kShareBlock + threadIdx.x) * 4;
-            stv<4>(out + e, u32x4v{0u, 0u, 0u, 0u});
-        }
-        return;
-    }
-    const int64_t end = base + kShareTile < shard_numel ? base + kShareTile : shard_numel;
-    for (int64_t i = base + threadIdx.x; i < end; i += kShareBlock) {
-        float acc = 0.0f;
-        if (i < valid_numel) {
-            acc = round_to<RD>(share_input1<SB, H, RD>(ranks.g[0] + (offset + i) * SB) / divisor);
-            for (int32_t q = 1; q < group_size; ++q) {
-                acc = round_to<RD>(acc + round_to<RD>(share_input1<SB, H, RD>(ranks.g[q] + (offset + i) * SB) / divisor));
-            }
-        }
-        out[i] = acc;
-    }
-}
-
-// Reduce dtype float64: the rank-order sum of widen(x_q) / divisor in double, rounded
-// once to fp32 (the fused kernel's arithmetic, without the norm).
-template <int SB, bool H>
-__global__ __launch_bounds__(kShareBlock) void local_share_f64_kernel(RankTable ranks, int32_t group_size,
-                                                                      int64_t offset, int64_t shard_numel,
-                                                                      int64_t valid_numel, double divisor,
-                                                                      float* __restrict__ out) {
-    const int64_t base = int64_t(blockIdx.x) * kShareTile;
-    const int64_t end = base + kShareTile < shard_numel ? base + kShareTile : shard_numel;
-    for (int64_t i = base + threadIdx.x; i < end; i += kShareBlock) {
-        float v = 0.0f;
-        if (i < valid_numel) {
-            double s = widen_f64<SB, H>(ranks.g[0], offset + i) / divisor;
-            for (int32_t q = 1; q < group_size; ++q) s = s + widen_f64<SB, H>(ranks.g[q], offset + i) / divisor;
-            v = static_cast<float>(s);
-        }
-        out[i] = v;
-    }
+int32_t launch_convert(int32_t src_dtype, int32_t dst_dtype, const int64_t* table, int64_t count, int64_t chunks,
+                       hipStream_t st) {
+    return launch_sliced("hbt_copy_intervals", chunks, kCopyBlock, [&](int64_t first, dim3 grid) {
+#define HBT_CVT(SD, DD) convert_kernel<SD, DD><<<grid, kCopyBlock, 0, st>>>(table, count, first)
+#define HBT_CVT_TO(SD)                                                     \
+    do {                                                                   \
+        if (dst_dtype == HBT_DTYPE_F64) HBT_CVT(SD, HBT_DTYPE_F64);        \
+        else if (dst_dtype == HBT_DTYPE_F32) HBT_CVT(SD, HBT_DTYPE_F32);   \
+        else if (dst_dtype == HBT_DTYPE_BF16) HBT_CVT(SD, HBT_DTYPE_BF16); \
+        else HBT_CVT(SD, HBT_DTYPE_F16);                                   \
+    } while (0)
+        if (src_dtype == HBT_DTYPE_F64) HBT_CVT_TO(HBT_DTYPE_F64);
+        else if (src_dtype == HBT_DTYPE_F32) HBT_CVT_TO(HBT_DTYPE_F32);
+        else if (src_dtype == HBT_DTYPE_BF16) HBT_CVT_TO(HBT_DTYPE_BF16);
+        else HBT_CVT_TO(HBT_DTYPE_F16);
+#undef HBT_CVT_TO
+#undef HBT_CVT
+    });
 }
 
 template <int SB, int DB, int OP, bool H = false>
-void launch_copy(const int64_t* table, int64_t count, int64_t chunks, float divisor, bool aligned,
-                 hipStream_t s) {
-    if (aligned) {
-        copy_aligned_kernel<SB, DB, OP, H>
-            <<<dim3(static_cast<unsigned>(chunks)), kCopyBlock, 0, s>>>(table, count, divisor);
-    } else {
-        copy_kernel<SB, DB, OP, H><<<dim3(static_cast<unsigned>(chunks)), kCopyBlock, 0, s>>>(table, count, divisor);
-    }
+int32_t launch_copy(const int64_t* table, int64_t count, int64_t chunks, float divisor, bool aligned,
+                    hipStream_t s) {
+    return launch_sliced("hbt_copy_intervals", chunks, kCopyBlock, [&](int64_t first, dim3 grid) {
+        if (aligned) {
+            copy_aligned_kernel<SB, DB, OP, H><<<grid, kCopyBlock, 0, s>>>(table, count, divisor, first);
+        } else {
+            copy_kernel<SB, DB, OP, H><<<grid, kCopyBlock, 0, s>>>(table, count, divisor, first);
+        }
+    });
 }
 
 // Conversions and division for 4- and 2-byte elements; H: the 2-byte side is fp16.
 // Division by a power of two (the AVG pre-divide at a power-of-two world size) runs as a
 // multiply by the exact reciprocal: the same bits, without the division sequence.
 template <bool H>
-void launch_arith(int ssz, int dsz, int32_t op, float divisor, const int64_t* table, int64_t count,
-                  int64_t chunks, bool aligned, hipStream_t s) {
+int32_t launch_arith(int ssz, int dsz, int32_t op, float divisor, const int64_t* table, int64_t count,
+                     int64_t chunks, bool aligned, hipStream_t s) {
     const float recip = op == HBT_COPY_OP_DIVIDE ? exact_reciprocal(divisor) : 0.0f;
     if (op == HBT_COPY_OP_DIVIDE && recip != 0.0f) {
-        if (ssz == 4 && dsz == 4) {
-            launch_copy<4, 4, kOpScale>(table, count, chunks, recip, aligned, s);
-        } else if (ssz == 2 && dsz == 2) {
-            launch_copy<2, 2, kOpScale, H>(table, count, chunks, recip, aligned, s);
-        } else if (ssz == 4) {
-            launch_copy<4, 2, kOpScale, H>(table, count, chunks, recip, aligned, s);
-        } else {
-            launch_copy<2, 4, kOpScale, H>(table, count, chunks, recip, aligned, s);
-        }
-    } else if (op == HBT_COPY_OP_DIVIDE) {
-        if (ssz == 4 && dsz == 4) {
-            launch_copy<4, 4, HBT_COPY_OP_DIVIDE>(table, count, chunks, divisor, aligned, s);
-        } else if (ssz == 2 && dsz == 2) {
-            launch_copy<2, 2, HBT_COPY_OP_DIVIDE, H>(table, count, chunks, divisor, aligned, s);
-        } else if (ssz == 4) {
-            launch_copy<4, 2, HBT_COPY_OP_DIVIDE, H>(table, count, chunks, divisor, aligned, s);
-        } else {
-            launch_copy<2, 4, HBT_COPY_OP_DIVIDE, H>(table, count, chunks, divisor, aligned, s);
-        }
-    } else if (ssz == 4) {  // conversions (same-dtype copies are bit copies)
-        launch_copy<4, 2, HBT_COPY_OP_COPY, H>(table, count, chunks, divisor, aligned, s);
-    } else {
-        launch_copy<2, 4, HBT_COPY_OP_COPY, H>(table, count, chunks, divisor, aligned, s);
+        if (ssz == 4 && dsz == 4) return launch_copy<4, 4, kOpScale>(table, count, chunks, recip, aligned, s);
+        if (ssz == 2 && dsz == 2) return launch_copy<2, 2, kOpScale, H>(table, count, chunks, recip, aligned, s);
+        if (ssz == 4) return launch_copy<4, 2, kOpScale, H>(table, count, chunks, recip, aligned, s);
+        return launch_copy<2, 4, kOpScale, H>(table, count, chunks, recip, aligned, s);
     }
+    if (op == HBT_COPY_OP_DIVIDE) {
+        if (ssz == 4 && dsz == 4) return launch_copy<4, 4, HBT_COPY_OP_DIVIDE>(table, count, chunks, divisor, aligned, s);
+        if (ssz == 2 && dsz == 2) return launch_copy<2, 2, HBT_COPY_OP_DIVIDE, H>(table, count, chunks, divisor, aligned, s);
+        if (ssz == 4) return launch_copy<4, 2, HBT_COPY_OP_DIVIDE, H>(table, count, chunks, divisor, aligned, s);
+        return launch_copy<2, 4, HBT_COPY_OP_DIVIDE, H>(table, count, chunks, divisor, aligned, s);
+    }
+    // conversions (same-dtype copies are bit copies)
+    if (ssz == 4) return launch_copy<4, 2, HBT_COPY_OP_COPY, H>(table, count, chunks, divisor, aligned, s);
+    return launch_copy<2, 4, HBT_COPY_OP_COPY, H>(table, count, chunks, divisor, aligned, s);
 }
 
 }  // namespace
@@ -530,11 +481,9 @@ extern "C" {
 int64_t hbt_copy_chunk_elems(int32_t src_dtype, int32_t dst_dtype) {
     const int ssz = dtype_size(src_dtype);
     const int dsz = dtype_size(dst_dtype);
-    if (ssz == 4 && dsz == 4) return chunk_elems<4, 4>();
-    if (ssz == 2 && dsz == 2) return chunk_elems<2, 2>();
-    if (ssz == 4 && dsz == 2) return chunk_elems<4, 2>();
-    if (ssz == 2 && dsz == 4) return chunk_elems<2, 4>();
-    return -1;  // 8-byte elements travel as F32 dword pairs
+    if (ssz == 0 || dsz == 0) return -1;
+    if (ssz == 8 && dsz == 8) return -1;  // same-dtype 8-byte data travels as F32 dword pairs
+    return int64_t(kCopyBlock) * 16 / ssz;  // 1 KB of source
 }
 
 int32_t hbt_copy_intervals(const int64_t* table, int64_t count, int64_t total_chunks,
@@ -551,11 +500,6 @@ int32_t hbt_copy_intervals(const int64_t* table, int64_t count, int64_t total_ch
     }
     const bool aligned = (flags & HBT_COPY_ALIGNED) != 0;
     if (count == 0 || total_chunks == 0) return HBT_OK;
-    if (total_chunks > 0x7FFFFFFFLL) {
-        set_error("hbt_copy_intervals: %lld chunks exceed the grid limit",
-                  static_cast<long long>(total_chunks));
-        return HBT_ERR_UNSUPPORTED;
-    }
     const int ssz = dtype_size(src_dtype);
     const int dsz = dtype_size(dst_dtype);
     if (ssz == 0 || dsz == 0 || (op != HBT_COPY_OP_COPY && op != HBT_COPY_OP_DIVIDE)) {
@@ -565,109 +509,26 @@ int32_t hbt_copy_intervals(const int64_t* table, int64_t count, int64_t total_ch
     hipStream_t s = as_stream(stream);
     if (op == HBT_COPY_OP_COPY && src_dtype == dst_dtype) {
         // Bit copy; fp64 moves as pairs of dwords (the host doubles its numels).
-        if (ssz == 2) {
-            launch_copy<2, 2, HBT_COPY_OP_COPY>(table, count, total_chunks, divisor, aligned, s);
-        } else if (ssz == 4) {
-            launch_copy<4, 4, HBT_COPY_OP_COPY>(table, count, total_chunks, divisor, aligned, s);
-        } else {
-            set_error("hbt_copy_intervals: 8-byte elements must be passed as dword pairs (F32)");
-            return HBT_ERR_UNSUPPORTED;
-        }
-        return check_launch("hbt_copy_intervals");
+        if (ssz == 2) return launch_copy<2, 2, HBT_COPY_OP_COPY>(table, count, total_chunks, divisor, aligned, s);
+        if (ssz == 4) return launch_copy<4, 4, HBT_COPY_OP_COPY>(table, count, total_chunks, divisor, aligned, s);
+        set_error("hbt_copy_intervals: 8-byte elements must be passed as dword pairs (F32)");
+        return HBT_ERR_UNSUPPORTED;
     }
-    const bool arithmetic = src_dtype == HBT_DTYPE_F32 || src_dtype == HBT_DTYPE_BF16 || src_dtype == HBT_DTYPE_F16;
-    const bool arithmetic_dst = dst_dtype == HBT_DTYPE_F32 || dst_dtype == HBT_DTYPE_BF16 || dst_dtype == HBT_DTYPE_F16;
+    const bool wide = ssz == 8 || dsz == 8;
     const bool mixed_16 = (src_dtype == HBT_DTYPE_BF16 && dst_dtype == HBT_DTYPE_F16) ||
                           (src_dtype == HBT_DTYPE_F16 && dst_dtype == HBT_DTYPE_BF16);
-    if (!arithmetic || !arithmetic_dst || mixed_16) {
-        set_error("hbt_copy_intervals: conversions and division move F32, BF16 and F16 data, and "
-                  "convert F32 <-> BF16 and F32 <-> F16 only (got %d -> %d)", src_dtype, dst_dtype);
-        return HBT_ERR_UNSUPPORTED;
+    if (wide || mixed_16) {
+        if (op != HBT_COPY_OP_COPY) {
+            set_error("hbt_copy_intervals: division moves F32, BF16 and F16 data within one dtype or "
+                      "between F32 and a 2-byte dtype (got %d -> %d)", src_dtype, dst_dtype);
+            return HBT_ERR_UNSUPPORTED;
+        }
+        return launch_convert(src_dtype, dst_dtype, table, count, total_chunks, s);
     }
     if (src_dtype == HBT_DTYPE_F16 || dst_dtype == HBT_DTYPE_F16) {
-        launch_arith<true>(ssz, dsz, op, divisor, table, count, total_chunks, aligned, s);
-    } else {
-        launch_arith<false>(ssz, dsz, op, divisor, table, count, total_chunks, aligned, s);
+        return launch_arith<true>(ssz, dsz, op, divisor, table, count, total_chunks, aligned, s);
     }
-    return check_launch("hbt_copy_intervals");
-}
-
-int32_t hbt_grad_local_share(const void* const* rank_grads, int32_t group_size, int32_t rank,
-                             int64_t shard_numel, int64_t valid_numel, int32_t in_dtype,
-                             int32_t reduce_dtype, float divisor, float* out, void* stream) {
-    clear_error();
-    if (rank_grads == nullptr || out == nullptr || group_size < 1 ||
-        group_size > HBT_MAX_LOCAL_RANKS || rank < 0 || rank >= group_size || shard_numel < 0 ||
-        valid_numel < 0 || valid_numel > shard_numel) {
-        set_error("hbt_grad_local_share: bad arguments (group_size=%d rank=%d shard=%lld valid=%lld)",
-                  group_size, rank, static_cast<long long>(shard_numel),
-                  static_cast<long long>(valid_numel));
-        return HBT_ERR_INVALID_ARGUMENT;
-    }
-    const bool f64 = reduce_dtype == HBT_DTYPE_F64;
-    if (in_dtype != HBT_DTYPE_F32 && in_dtype != HBT_DTYPE_BF16 && in_dtype != HBT_DTYPE_F16 &&
-        !(f64 && in_dtype == HBT_DTYPE_F64)) {
-        set_error("hbt_grad_local_share: input dtype %d is not F32, BF16 or F16 (or F64 with reduce dtype F64)",
-                  in_dtype);
-        return HBT_ERR_INVALID_ARGUMENT;
-    }
-    if (reduce_dtype != HBT_DTYPE_F32 && reduce_dtype != HBT_DTYPE_BF16 && reduce_dtype != HBT_DTYPE_F16 && !f64) {
-        set_error("hbt_grad_local_share: reduce dtype %d is not F32, BF16, F16 or F64", reduce_dtype);
-        return HBT_ERR_INVALID_ARGUMENT;
-    }
-    RankTable ranks{};
-    for (int q = 0; q < group_size; ++q) {
-        if (rank_grads[q] == nullptr && valid_numel > 0) {
-            set_error("hbt_grad_local_share: rank %d gradient pointer is null", q);
-            return HBT_ERR_INVALID_ARGUMENT;
-        }
-        ranks.g[q] = static_cast<const uint8_t*>(rank_grads[q]);
-    }
-    if (shard_numel == 0) return HBT_OK;
-    const int64_t offset = int64_t(rank) * shard_numel;
-    const int64_t tiles = (shard_numel + kShareTile - 1) / kShareTile;
-    if (tiles > 0x7FFFFFFFLL) {
-        set_error("hbt_grad_local_share: %lld tiles exceed the grid limit", static_cast<long long>(tiles));
-        return HBT_ERR_UNSUPPORTED;
-    }
-    // Vector path: every rank's slice and the output start on a 16-byte (fp32 input) or
-    // 8-byte (bf16 or fp16 input) boundary.
-    const int elem = dtype_size(in_dtype);
-    int32_t vec_ok = (reinterpret_cast<uintptr_t>(out) & 15u) == 0;
-    for (int q = 0; q < group_size && vec_ok; ++q) {
-        const uintptr_t a = reinterpret_cast<uintptr_t>(ranks.g[q]) + static_cast<uintptr_t>(offset * elem);
-        vec_ok = (a & static_cast<uintptr_t>(4 * elem - 1)) == 0;
-    }
-    hipStream_t s = as_stream(stream);
-    const dim3 grid(static_cast<unsigned>(tiles));
-#define HBT_SHARE(SB, H, RD)                                                                       \
-    local_share_kernel<SB, H, RD><<<grid, kShareBlock, 0, s>>>(ranks, group_size, offset, shard_numel,  \
-                                                               valid_numel, divisor, vec_ok, out)
-#define HBT_SHARE_RD(SB, H)                                                    \
-    do {                                                                       \
-        if (reduce_dtype == HBT_DTYPE_F32) HBT_SHARE(SB, H, HBT_DTYPE_F32);     \
-        else if (reduce_dtype == HBT_DTYPE_BF16) HBT_SHARE(SB, H, HBT_DTYPE_BF16); \
-        else HBT_SHARE(SB, H, HBT_DTYPE_F16);                                  \
-    } while (0)
-#define HBT_SHARE64(SB, H)                                                                        \
-    local_share_f64_kernel<SB, H><<<grid, kShareBlock, 0, s>>>(ranks, group_size, offset, shard_numel, \
-                                                               valid_numel, static_cast<double>(divisor), out)
-    if (f64) {
-        if (in_dtype == HBT_DTYPE_F64) HBT_SHARE64(8, false);
-        else if (in_dtype == HBT_DTYPE_F32) HBT_SHARE64(4, false);
-        else if (in_dtype == HBT_DTYPE_BF16) HBT_SHARE64(2, false);
-        else HBT_SHARE64(2, true);
-    } else if (in_dtype == HBT_DTYPE_F32) {
-        HBT_SHARE_RD(4, false);
-    } else if (in_dtype == HBT_DTYPE_BF16) {
-        HBT_SHARE_RD(2, false);
-    } else {
-        HBT_SHARE_RD(2, true);
-    }
-#undef HBT_SHARE_RD
-#undef HBT_SHARE64
-#undef HBT_SHARE
-    return check_launch("hbt_grad_local_share");
+    return launch_arith<false>(ssz, dsz, op, divisor, table, count, total_chunks, aligned, s);
 }
 
 }  // extern "C"

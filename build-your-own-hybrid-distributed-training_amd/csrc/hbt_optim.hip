@@ -1,10 +1,17 @@
-// Fused clip + AdamW step and the deterministic fp64 gradient norm (gfx950).
+// Fused clip + AdamW / SGD steps, the deterministic fp64 gradient norm, the FSDP
+// gradient local share, in-place gradient scaling and no_sync accumulation (gfx950).
 //
-// Both kernels stream their operands exactly once from HBM with 16-byte
-// non-temporal loads and stores.  Work is split into fixed-size tiles; a launch
-// covers a table of up to HBT_MAX_TENSORS_PER_LAUNCH tensors, so a list of flat
-// shards (or of DDP-style per-parameter tensors) costs one launch per 16 tensors.
+// Every kernel streams its operands exactly once from HBM with 8- or 16-byte
+// non-temporal vector loads and stores.  Work is split into fixed-size tiles; a launch
+// covers a table of up to HBT_MAX_TENSORS_PER_LAUNCH tensors, so a list of flat shards
+// (or of DDP-style per-parameter tensors) costs one launch per 16 tensors.
+//
+// Dtypes are template parameters given as HBT_DTYPE_* codes.  Arithmetic runs in fp32
+// and, wherever a tensor of a 2-byte dtype holds an intermediate result, is rounded to
+// that dtype (round_to<D>), as torch's CPU ops on bf16 / fp16 tensors compute in fp32 and
+// round each result once.  For fp32 every rounding is the identity.
 #include <cmath>
+#include <cstring>
 #include <mutex>
 
 #include "hbt_common.hpp"
@@ -20,70 +27,126 @@ namespace hbt {
 namespace {
 
 constexpr int kMaxT = HBT_MAX_TENSORS_PER_LAUNCH;
+constexpr int F32 = HBT_DTYPE_F32;
+constexpr int BF16 = HBT_DTYPE_BF16;
+constexpr int F16 = HBT_DTYPE_F16;
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-// AdamW (and SGD): 32-thread workgroups, i.e. half a wavefront each, two 16-byte
-// vectors per lane and operand, 256 elements per workgroup.  Measured on MI355X on
-// this 4-read/3-write stream (1e9 elements): 6.38 TB/s, against 5.87 TB/s for
-// full-wave 64-thread workgroups, 5.4 TB/s for 128 threads and under 5 TB/s for
-// 16 threads or 256-thread workgroups; persistent grid-stride variants are slower.
+template <int D>
+constexpr int64_t bytes_of() { return D == F32 ? 4 : (D == HBT_DTYPE_F64 ? 8 : 2); }
+
+// ---- vector memory helpers ----------------------------------------------------------
+// Every operand is touched exactly once per step, so loads and stores are marked
+// non-temporal: the lines are not kept in L2/MALL for reuse that never comes.
+//
+// K consecutive elements of dtype D starting at element e of `base`, widened exactly to
+// fp32, with one vector load of K * bytes(D) bytes (16 for 4 fp32 or 8 bf16/fp16, 8 for
+// 4 bf16/fp16).
+template <int D, int K>
+__device__ __forceinline__ void load_vec(const void* base, int64_t e, float (&x)[K]) {
+    static_assert(D == F32 || D == BF16 || D == F16, "vector loads move fp32, bf16 and fp16");
+    if constexpr (D == F32) {
+        static_assert(K == 4, "fp32 vectors are four elements");
+        const f32x4 w = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(static_cast<const float*>(base) + e));
+        x[0] = w.x;
+        x[1] = w.y;
+        x[2] = w.z;
+        x[3] = w.w;
+    } else if constexpr (K == 4) {
+        const u32x2 w = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(static_cast<const uint16_t*>(base) + e));
+        x[0] = b16_to_f32<D == F16>(w.x & 0xFFFFu);
+        x[1] = b16_to_f32<D == F16>(w.x >> 16);
+        x[2] = b16_to_f32<D == F16>(w.y & 0xFFFFu);
+        x[3] = b16_to_f32<D == F16>(w.y >> 16);
+    } else {
+        static_assert(K == 8, "2-byte vectors are four or eight elements");
+        const u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(base) + e));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            x[2 * i] = b16_to_f32<D == F16>(w[i] & 0xFFFFu);
+            x[2 * i + 1] = b16_to_f32<D == F16>(w[i] >> 16);
+        }
+    }
+}
+// Stores K values, each already representable in D (so the narrowing is exact).
+template <int D, int K>
+__device__ __forceinline__ void store_vec(void* base, int64_t e, const float (&x)[K]) {
+    static_assert(D == F32 || D == BF16 || D == F16, "vector stores move fp32, bf16 and fp16");
+    if constexpr (D == F32) {
+        static_assert(K == 4, "fp32 vectors are four elements");
+        __builtin_nontemporal_store(f32x4{x[0], x[1], x[2], x[3]}, reinterpret_cast<f32x4*>(static_cast<float*>(base) + e));
+    } else if constexpr (K == 4) {
+        const u32x2 w{f32_to_b16<D == F16>(x[0]) | (f32_to_b16<D == F16>(x[1]) << 16),
+                      f32_to_b16<D == F16>(x[2]) | (f32_to_b16<D == F16>(x[3]) << 16)};
+        __builtin_nontemporal_store(w, reinterpret_cast<u32x2*>(static_cast<uint16_t*>(base) + e));
+    } else {
+        static_assert(K == 8, "2-byte vectors are four or eight elements");
+        u32x4 w;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w[i] = f32_to_b16<D == F16>(x[2 * i]) | (f32_to_b16<D == F16>(x[2 * i + 1]) << 16);
+        __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(static_cast<uint16_t*>(base) + e));
+    }
+}
+template <int D>
+__device__ __forceinline__ float load_one(const void* base, int64_t e) {
+    if constexpr (D == F32) return static_cast<const float*>(base)[e];
+    return b16_to_f32<D == F16>(static_cast<const uint16_t*>(base)[e]);
+}
+template <int D>
+__device__ __forceinline__ void store_one(void* base, int64_t e, float x) {
+    if constexpr (D == F32) {
+        static_cast<float*>(base)[e] = x;
+    } else {
+        static_cast<uint16_t*>(base)[e] = static_cast<uint16_t>(f32_to_b16<D == F16>(x));
+    }
+}
+
+// Wait for every outstanding vector-memory load of this wave (s_waitcnt vmcnt(0)).
+// Issuing a lane's operand streams one after the other, rather than all at once, keeps
+// the HBM request mix per wave simpler and measured ~2% faster.
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// The table entry owning workgroup `block`: the last t with first[t] <= block.
+__device__ __forceinline__ int owning_tensor(const int64_t* first, int32_t count, int64_t block) {
+    int t = 0;
+    while (t + 1 < count && block >= first[t + 1]) ++t;
+    return t;
+}
+
+// The gradient after the reference's in-place multiplies: the unscale (GradScaler.unscale_,
+// skipped when the factor is 1) and the clip, each computed in fp32 and rounded to the
+// gradient's dtype GD, as grad.mul_(python float) on a GD tensor does.
+template <int GD, bool kUnscale>
+__device__ __forceinline__ float scaled_grad(float g, float unscale, float gmul) {
+    if constexpr (kUnscale) g = round_to<GD>(g * unscale);
+    return round_to<GD>(g * gmul);
+}
+
+// ---- AdamW -----------------------------------------------------------------------
+// 32-thread workgroups, i.e. half a wavefront each, two 16-byte vectors per lane and
+// fp32 operand: 256 elements per workgroup (512 for 2-byte parameters, whose 16-byte
+// vectors hold eight).  Measured on MI355X on the fp32 4-read/3-write stream (1e9
+// elements): 6.38 TB/s, against 5.87 TB/s for full-wave 64-thread workgroups, 5.4 TB/s
+// for 128 threads and under 5 TB/s for 16 threads or 256-thread workgroups; persistent
+// grid-stride variants are slower.
 #ifndef HBT_ADAM_BLOCK
 #define HBT_ADAM_BLOCK 32
 #endif
 constexpr int kAdamBlock = HBT_ADAM_BLOCK;
 constexpr int kAdamUnroll = 2;
-constexpr int64_t kAdamTile = int64_t(kAdamBlock) * 4 * kAdamUnroll;
+template <int PD>
+constexpr int adam_vec() { return PD == F32 ? 4 : 8; }
+template <int PD>
+constexpr int64_t adam_tile() { return int64_t(kAdamBlock) * adam_vec<PD>() * kAdamUnroll; }
 
-// Norm: 1024-thread workgroups, each summing one contiguous chunk of 8 tiles; a tile
-// is one 16-byte load per lane (4 fp32 or 8 bf16 gradients).
-constexpr int kNormBlock = 1024;
-constexpr int kNormTilesPerChunk = 8;
-template <typename GradT>
-constexpr int64_t norm_tile() { return int64_t(kNormBlock) * (16 / sizeof(GradT)); }
-template <typename GradT>
-constexpr int64_t norm_chunk() { return norm_tile<GradT>() * kNormTilesPerChunk; }
-
-// ---- 16-byte memory helpers ------------------------------------------------------
-// Every operand is touched exactly once per step, so loads and stores are marked
-// non-temporal: the lines are not kept in L2/MALL for reuse that never comes.
-__device__ __forceinline__ f32x4 ld4_nt(const float* p) {
-    return __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
-}
-__device__ __forceinline__ void st4_nt(float* p, f32x4 x) {
-    __builtin_nontemporal_store(x, reinterpret_cast<f32x4*>(p));
-}
-// Four gradient values widened to fp32 (bf16 widening is exact).
-__device__ __forceinline__ f32x4 ld_grad4_nt(const float* p) { return ld4_nt(p); }
-__device__ __forceinline__ f32x4 ld_grad4_nt(const uint16_t* p) {
-    const u32x2 w = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
-    return f32x4{bf16_to_f32(w.x & 0xFFFFu), bf16_to_f32(w.x >> 16), bf16_to_f32(w.y & 0xFFFFu),
-                 bf16_to_f32(w.y >> 16)};
-}
-// Eight bf16 gradients (one 16-byte load) widened to fp32, as two 4-vectors.
-__device__ __forceinline__ void ld_bf16x8_nt(const uint16_t* p, f32x4& lo, f32x4& hi) {
-    typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
-    const u32x4v w = __builtin_nontemporal_load(reinterpret_cast<const u32x4v*>(p));
-    lo = f32x4{bf16_to_f32(w.x & 0xFFFFu), bf16_to_f32(w.x >> 16), bf16_to_f32(w.y & 0xFFFFu),
-               bf16_to_f32(w.y >> 16)};
-    hi = f32x4{bf16_to_f32(w.z & 0xFFFFu), bf16_to_f32(w.z >> 16), bf16_to_f32(w.w & 0xFFFFu),
-               bf16_to_f32(w.w >> 16)};
-}
-__device__ __forceinline__ float ld_grad1(const float* p) { return *p; }
-__device__ __forceinline__ float ld_grad1(const uint16_t* p) { return bf16_to_f32(*p); }
-
-// Wait for every outstanding vector-memory load of this wave (s_waitcnt vmcnt(0)).
-// Issuing a lane's four operand streams one after the other, rather than all at
-// once, keeps the HBM request mix per wave simpler and measured ~2% faster.
-__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
-
-// ---- AdamW -----------------------------------------------------------------------
 struct AdamTable {
-    float* p[kMaxT];
-    const void* g[kMaxT];
-    float* m[kMaxT];
-    float* v[kMaxT];
+    void* p[kMaxT];
+    void* g[kMaxT];
+    void* m[kMaxT];
+    void* v[kMaxT];
     int64_t n[kMaxT];
     int64_t first_block[kMaxT + 1];
     int32_t vec_ok[kMaxT];
@@ -98,83 +161,96 @@ struct AdamScalars {
     float beta2;
     float one_minus_beta2;
     float bc2_sqrt;
-    float eps;
+    float eps;  // rounded to the parameter dtype (torch's add_ of a Python scalar rounds it)
     float neg_step;
 };
 
-// One element of torch's single-tensor AdamW, preceded by the unscale and clip
-// multiplies.  Compiled with -ffp-contract=off: only the two explicit fmaf calls fuse.
-template <bool kLerpSmall, bool kUnscale>
-__device__ __forceinline__ void adamw_update(float& p, float g, float& m, float& v, float gmul,
-                                             const AdamScalars& s) {
-    if constexpr (kUnscale) g = g * s.unscale;
-    g = g * gmul;
-    p = p * s.decay;
+// One element of torch's single-tensor AdamW on tensors of dtype PD, given the already
+// scaled gradient g.  Compiled with -ffp-contract=off: only the two explicit fmaf calls
+// fuse.  For PD = fp32 this is exactly
+//   p *= decay; m = lerp(m, g, w); v = v * beta2 + (1 - beta2) g^2;
+//   p += (neg_step * m) / (sqrt(v) / bc2_sqrt + eps)
+// and for a 2-byte PD each op of that sequence that torch runs as its own tensor op
+// (mul_, lerp_, mul_, addcmul_, sqrt, div, add_, addcdiv_) rounds its result to PD.
+template <int PD, bool kLerpSmall>
+__device__ __forceinline__ void adamw_update(float& p, float g, float& m, float& v, const AdamScalars& s) {
+    p = round_to<PD>(p * s.decay);
     const float diff = g - m;
     if constexpr (kLerpSmall) {
-        m = __builtin_fmaf(s.lerp_w, diff, m);
+        m = round_to<PD>(__builtin_fmaf(s.lerp_w, diff, m));
     } else {
-        m = __builtin_fmaf(s.lerp_w_minus_1, diff, g);
+        m = round_to<PD>(__builtin_fmaf(s.lerp_w_minus_1, diff, g));
     }
-    v = v * s.beta2;
-    v = __builtin_fmaf(s.one_minus_beta2 * g, g, v);
-    const float denom = __builtin_sqrtf(v) / s.bc2_sqrt + s.eps;
-    p = p + (s.neg_step * m) / denom;
+    v = round_to<PD>(v * s.beta2);
+    v = round_to<PD>(__builtin_fmaf(s.one_minus_beta2 * g, g, v));
+    float denom;
+    if constexpr (PD == F32) {
+        denom = __builtin_sqrtf(v) / s.bc2_sqrt + s.eps;
+    } else {
+        denom = round_to<PD>(round_to<PD>(round_to<PD>(__builtin_sqrtf(v)) / s.bc2_sqrt) + s.eps);
+    }
+    p = round_to<PD>(p + (s.neg_step * m) / denom);
 }
 
-template <typename GradT, bool kLerpSmall, bool kUnscale>
+// PD: dtype of p, m, v; GD: dtype of g.  kWriteBack stores the scaled gradient back into
+// g whenever a multiply changed it: the clip multiplier differs from 1 (the reference
+// multiplies only when its coefficient is below 1) or an unscale factor is pending.
+template <int PD, int GD, bool kLerpSmall, bool kUnscale, bool kWriteBack>
 __global__ __launch_bounds__(kAdamBlock) void adamw_kernel(AdamTable tab, AdamScalars s,
-                                                           const float* __restrict__ grad_mul) {
-    const int64_t block = blockIdx.x;
-    int t = 0;
-    while (t + 1 < tab.count && block >= tab.first_block[t + 1]) ++t;
-    const int64_t base = (block - tab.first_block[t]) * kAdamTile;
+                                                           const float* __restrict__ grad_mul,
+                                                           int64_t block_base) {
+    constexpr int K = adam_vec<PD>();
+    constexpr int64_t kTile = adam_tile<PD>();
+    const int64_t block = block_base + blockIdx.x;
+    const int t = owning_tensor(tab.first_block, tab.count, block);
+    const int64_t base = (block - tab.first_block[t]) * kTile;
     const int64_t n = tab.n[t];
     const float gmul = grad_mul != nullptr ? *grad_mul : 1.0f;
-    float* __restrict__ P = tab.p[t];
-    const GradT* __restrict__ G = static_cast<const GradT*>(tab.g[t]);
-    float* __restrict__ M = tab.m[t];
-    float* __restrict__ V = tab.v[t];
+    const bool write_g = kWriteBack && (kUnscale || gmul != 1.0f);
+    void* P = tab.p[t];
+    void* G = tab.g[t];
+    void* M = tab.m[t];
+    void* V = tab.v[t];
 
-    if (tab.vec_ok[t] && base + kAdamTile <= n) {
-        f32x4 pv[kAdamUnroll], gv[kAdamUnroll], mv[kAdamUnroll], vv[kAdamUnroll];
+    if (tab.vec_ok[t] && base + kTile <= n) {
+        float pv[kAdamUnroll][K], gv[kAdamUnroll][K], mv[kAdamUnroll][K], vv[kAdamUnroll][K];
 #pragma unroll
         for (int u = 0; u < kAdamUnroll; ++u) {
-            const int64_t e = base + (int64_t(u) * kAdamBlock + threadIdx.x) * 4;
-            gv[u] = ld_grad4_nt(G + e);
+            const int64_t e = base + (int64_t(u) * kAdamBlock + threadIdx.x) * K;
+            load_vec<GD, K>(G, e, gv[u]);
             wait_vmem();
-            mv[u] = ld4_nt(M + e);
+            load_vec<PD, K>(M, e, mv[u]);
             wait_vmem();
-            vv[u] = ld4_nt(V + e);
+            load_vec<PD, K>(V, e, vv[u]);
             wait_vmem();
-            pv[u] = ld4_nt(P + e);
+            load_vec<PD, K>(P, e, pv[u]);
         }
 #pragma unroll
         for (int u = 0; u < kAdamUnroll; ++u) {
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                float p = pv[u][c], m = mv[u][c], v = vv[u][c];
-                adamw_update<kLerpSmall, kUnscale>(p, gv[u][c], m, v, gmul, s);
-                pv[u][c] = p;
-                mv[u][c] = m;
-                vv[u][c] = v;
+            for (int c = 0; c < K; ++c) {
+                gv[u][c] = scaled_grad<GD, kUnscale>(gv[u][c], s.unscale, gmul);
+                adamw_update<PD, kLerpSmall>(pv[u][c], gv[u][c], mv[u][c], vv[u][c], s);
             }
         }
 #pragma unroll
         for (int u = 0; u < kAdamUnroll; ++u) {
-            const int64_t e = base + (int64_t(u) * kAdamBlock + threadIdx.x) * 4;
-            st4_nt(M + e, mv[u]);
-            st4_nt(V + e, vv[u]);
-            st4_nt(P + e, pv[u]);
+            const int64_t e = base + (int64_t(u) * kAdamBlock + threadIdx.x) * K;
+            store_vec<PD, K>(M, e, mv[u]);
+            store_vec<PD, K>(V, e, vv[u]);
+            store_vec<PD, K>(P, e, pv[u]);
+            if (write_g) store_vec<GD, K>(G, e, gv[u]);
         }
     } else {
-        const int64_t end = base + kAdamTile < n ? base + kAdamTile : n;
+        const int64_t end = base + kTile < n ? base + kTile : n;
         for (int64_t e = base + threadIdx.x; e < end; e += kAdamBlock) {
-            float p = P[e], m = M[e], v = V[e];
-            adamw_update<kLerpSmall, kUnscale>(p, ld_grad1(G + e), m, v, gmul, s);
-            P[e] = p;
-            M[e] = m;
-            V[e] = v;
+            float p = load_one<PD>(P, e), m = load_one<PD>(M, e), v = load_one<PD>(V, e);
+            const float g = scaled_grad<GD, kUnscale>(load_one<GD>(G, e), s.unscale, gmul);
+            adamw_update<PD, kLerpSmall>(p, g, m, v, s);
+            store_one<PD>(P, e, p);
+            store_one<PD>(M, e, m);
+            store_one<PD>(V, e, v);
+            if (write_g) store_one<GD>(G, e, g);
         }
     }
 }
@@ -182,13 +258,15 @@ __global__ __launch_bounds__(kAdamBlock) void adamw_kernel(AdamTable tab, AdamSc
 // ---- SGD -------------------------------------------------------------------------
 // torch's single-tensor SGD (torch/optim/sgd.py, _single_tensor_sgd) per element, with
 // the unscale and clip multiplies in front.  Every `x.add(y, alpha=a)` of torch's CPU
-// path is one fused multiply-add, fma(y, a, x); mul_ is one rounded multiply.
+// path is one fused multiply-add, fma(y, a, x), whose alpha torch first rounds to the
+// tensor's dtype (the host passes the alphas so rounded); mul_ is one rounded multiply
+// by the unrounded fp32 scalar.  For a 2-byte PD each op's result is rounded to PD.
 enum SgdMode { kSgdPlain = 0, kSgdFirst = 1, kSgdMomentum = 2 };
 
 struct SgdTable {
-    float* p[kMaxT];
-    const void* g[kMaxT];
-    float* buf[kMaxT];
+    void* p[kMaxT];
+    void* g[kMaxT];
+    void* buf[kMaxT];
     int64_t n[kMaxT];
     int64_t first_block[kMaxT + 1];
     int32_t vec_ok[kMaxT];
@@ -197,82 +275,99 @@ struct SgdTable {
 
 struct SgdScalars {
     float unscale;
-    float weight_decay;
-    float momentum;
-    float one_minus_dampening;
-    float neg_lr;
+    float weight_decay;         // alpha of grad.add(param, alpha=wd)
+    float momentum;             // buf.mul_(momentum)
+    float momentum_alpha;       // alpha of grad.add(buf, alpha=momentum) (Nesterov)
+    float one_minus_dampening;  // alpha of buf.add_(grad, alpha=1 - dampening)
+    float neg_lr;               // alpha of param.add_(grad, alpha=-lr)
     int32_t apply_weight_decay;
     int32_t nesterov;
 };
 
-template <bool kUnscale, int kMode>
-__device__ __forceinline__ void sgd_update(float& p, float g, float& buf, float gmul, const SgdScalars& s) {
-    if constexpr (kUnscale) g = g * s.unscale;
-    g = g * gmul;
-    if (s.apply_weight_decay) g = __builtin_fmaf(p, s.weight_decay, g);  // grad.add(param, alpha=wd)
+template <int PD, int kMode>
+__device__ __forceinline__ void sgd_update(float& p, float g, float& buf, const SgdScalars& s) {
+    if (s.apply_weight_decay) g = round_to<PD>(__builtin_fmaf(p, s.weight_decay, g));  // grad.add(param, alpha=wd)
     if constexpr (kMode == kSgdFirst) {
         buf = g;  // the buffer starts as a clone of the gradient
     } else if constexpr (kMode == kSgdMomentum) {
-        buf = buf * s.momentum;
-        buf = __builtin_fmaf(g, s.one_minus_dampening, buf);  // buf.mul_(m).add_(grad, alpha=1-d)
+        buf = round_to<PD>(buf * s.momentum);
+        buf = round_to<PD>(__builtin_fmaf(g, s.one_minus_dampening, buf));  // buf.mul_(m).add_(grad, alpha=1-d)
     }
-    if constexpr (kMode != kSgdPlain) g = s.nesterov ? __builtin_fmaf(buf, s.momentum, g) : buf;
-    p = __builtin_fmaf(g, s.neg_lr, p);  // param.add_(grad, alpha=-lr)
+    if constexpr (kMode != kSgdPlain) g = s.nesterov ? round_to<PD>(__builtin_fmaf(buf, s.momentum_alpha, g)) : buf;
+    p = round_to<PD>(__builtin_fmaf(g, s.neg_lr, p));  // param.add_(grad, alpha=-lr)
 }
 
-template <typename GradT, bool kUnscale, int kMode>
+template <int PD, int GD, bool kUnscale, int kMode, bool kWriteBack>
 __global__ __launch_bounds__(kAdamBlock) void sgd_kernel(SgdTable tab, SgdScalars s,
-                                                         const float* __restrict__ grad_mul) {
-    const int64_t block = blockIdx.x;
-    int t = 0;
-    while (t + 1 < tab.count && block >= tab.first_block[t + 1]) ++t;
-    const int64_t base = (block - tab.first_block[t]) * kAdamTile;
+                                                         const float* __restrict__ grad_mul,
+                                                         int64_t block_base) {
+    constexpr int K = adam_vec<PD>();
+    constexpr int64_t kTile = adam_tile<PD>();
+    const int64_t block = block_base + blockIdx.x;
+    const int t = owning_tensor(tab.first_block, tab.count, block);
+    const int64_t base = (block - tab.first_block[t]) * kTile;
     const int64_t n = tab.n[t];
     const float gmul = grad_mul != nullptr ? *grad_mul : 1.0f;
-    float* __restrict__ P = tab.p[t];
-    const GradT* __restrict__ G = static_cast<const GradT*>(tab.g[t]);
-    float* __restrict__ B = tab.buf[t];
-    if (tab.vec_ok[t] && base + kAdamTile <= n) {
-        f32x4 pv[kAdamUnroll], gv[kAdamUnroll], bv[kAdamUnroll];
+    const bool write_g = kWriteBack && (kUnscale || gmul != 1.0f);
+    void* P = tab.p[t];
+    void* G = tab.g[t];
+    void* B = tab.buf[t];
+    if (tab.vec_ok[t] && base + kTile <= n) {
+        float pv[kAdamUnroll][K], gv[kAdamUnroll][K], bv[kAdamUnroll][K];
 #pragma unroll
         for (int u = 0; u < kAdamUnroll; ++u) {
-            const int64_t e = base + (int64_t(u) * kAdamBlock + threadIdx.x) * 4;
-            gv[u] = ld_grad4_nt(G + e);
+            const int64_t e = base + (int64_t(u) * kAdamBlock + threadIdx.x) * K;
+            load_vec<GD, K>(G, e, gv[u]);
             if constexpr (kMode == kSgdMomentum) {
                 wait_vmem();
-                bv[u] = ld4_nt(B + e);
+                load_vec<PD, K>(B, e, bv[u]);
             }
             wait_vmem();
-            pv[u] = ld4_nt(P + e);
+            load_vec<PD, K>(P, e, pv[u]);
         }
 #pragma unroll
         for (int u = 0; u < kAdamUnroll; ++u) {
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                float p = pv[u][c], b = kMode == kSgdMomentum ? bv[u][c] : 0.0f;
-                sgd_update<kUnscale, kMode>(p, gv[u][c], b, gmul, s);
-                pv[u][c] = p;
+            for (int c = 0; c < K; ++c) {
+                gv[u][c] = scaled_grad<GD, kUnscale>(gv[u][c], s.unscale, gmul);
+                float b = kMode == kSgdMomentum ? bv[u][c] : 0.0f;
+                sgd_update<PD, kMode>(pv[u][c], gv[u][c], b, s);
                 bv[u][c] = b;
             }
         }
 #pragma unroll
         for (int u = 0; u < kAdamUnroll; ++u) {
-            const int64_t e = base + (int64_t(u) * kAdamBlock + threadIdx.x) * 4;
-            if constexpr (kMode != kSgdPlain) st4_nt(B + e, bv[u]);
-            st4_nt(P + e, pv[u]);
+            const int64_t e = base + (int64_t(u) * kAdamBlock + threadIdx.x) * K;
+            if constexpr (kMode != kSgdPlain) store_vec<PD, K>(B, e, bv[u]);
+            store_vec<PD, K>(P, e, pv[u]);
+            if (write_g) store_vec<GD, K>(G, e, gv[u]);
         }
     } else {
-        const int64_t end = base + kAdamTile < n ? base + kAdamTile : n;
+        const int64_t end = base + kTile < n ? base + kTile : n;
         for (int64_t e = base + threadIdx.x; e < end; e += kAdamBlock) {
-            float p = P[e], b = kMode == kSgdMomentum ? B[e] : 0.0f;
-            sgd_update<kUnscale, kMode>(p, ld_grad1(G + e), b, gmul, s);
-            P[e] = p;
-            if constexpr (kMode != kSgdPlain) B[e] = b;
+            float p = load_one<PD>(P, e), b = kMode == kSgdMomentum ? load_one<PD>(B, e) : 0.0f;
+            const float g = scaled_grad<GD, kUnscale>(load_one<GD>(G, e), s.unscale, gmul);
+            sgd_update<PD, kMode>(p, g, b, s);
+            store_one<PD>(P, e, p);
+            if constexpr (kMode != kSgdPlain) store_one<PD>(B, e, b);
+            if (write_g) store_one<GD>(G, e, g);
         }
     }
 }
 
 // ---- squared norm ------------------------------------------------------------------
+// 1024-thread workgroups, each summing one contiguous chunk of 8 tiles; a tile is one
+// 16-byte load per lane (4 fp32 or 8 bf16/fp16 gradients).
+constexpr int kNormBlock = 1024;
+constexpr int kNormTilesPerChunk = 8;
+template <int GD>
+constexpr int norm_vec() { return GD == F32 ? 4 : 8; }
+template <int GD>
+constexpr int64_t norm_tile() { return int64_t(kNormBlock) * norm_vec<GD>(); }
+template <int GD>
+constexpr int64_t norm_chunk() { return norm_tile<GD>() * kNormTilesPerChunk; }
+inline int64_t norm_chunk_of(int32_t dtype) { return dtype == F32 ? norm_chunk<F32>() : norm_chunk<BF16>(); }
+
 struct NormTable {
     const void* g[kMaxT];
     int64_t n[kMaxT];
@@ -288,49 +383,40 @@ __device__ __forceinline__ double sq(float x) {
 }
 
 // Workgroup c sums chunk c of the concatenated tensors (8 tiles of one tensor: 32768
-// fp32 or 65536 bf16 elements) into partials[c].  Inside a thread the squares are added in element order;
-// threads and waves are combined by the fixed trees of block_sum, so the partials,
-// and the sum of them, depend only on the data and the numels.
-template <typename GradT, bool kUnscale>
+// fp32 or 65536 bf16/fp16 elements) into partials[c].  Inside a thread the squares are
+// added in element order; threads and waves are combined by the fixed trees of
+// block_sum, so the partials, and the sum of them, depend only on the data and the
+// numels.  A pending unscale is applied, rounded to the gradient's dtype, before squaring.
+template <int GD, bool kUnscale>
 __global__ __launch_bounds__(kNormBlock) void sqnorm_kernel(NormTable tab, float unscale,
-                                                            double* __restrict__ partials) {
-    constexpr int64_t kTile = norm_tile<GradT>();
-    constexpr int64_t kChunk = norm_chunk<GradT>();
-    const int64_t chunk = blockIdx.x;
-    int t = 0;
-    while (t + 1 < tab.count && chunk >= tab.first_chunk[t + 1]) ++t;
+                                                            double* __restrict__ partials, int64_t block_base) {
+    constexpr int K = norm_vec<GD>();
+    constexpr int64_t kTile = norm_tile<GD>();
+    constexpr int64_t kChunk = norm_chunk<GD>();
+    const int64_t chunk = block_base + blockIdx.x;
+    const int t = owning_tensor(tab.first_chunk, tab.count, chunk);
     const int64_t start = (chunk - tab.first_chunk[t]) * kChunk;
     const int64_t n = tab.n[t];
-    const GradT* __restrict__ G = static_cast<const GradT*>(tab.g[t]);
+    const void* G = tab.g[t];
     double acc = 0.0;
     for (int k = 0; k < kNormTilesPerChunk; ++k) {
         const int64_t base = start + int64_t(k) * kTile;
         if (base >= n) break;
         if (tab.vec_ok[t] && base + kTile <= n) {
-            f32x4 x, y;
-            if constexpr (sizeof(GradT) == 4) {
-                x = ld_grad4_nt(G + base + int64_t(threadIdx.x) * 4);
-            } else {
-                ld_bf16x8_nt(G + base + int64_t(threadIdx.x) * 8, x, y);
-            }
-            if constexpr (kUnscale) x = x * unscale;
-            acc += sq(x.x);
-            acc += sq(x.y);
-            acc += sq(x.z);
-            acc += sq(x.w);
-            if constexpr (sizeof(GradT) == 2) {
-                if constexpr (kUnscale) y = y * unscale;
-                acc += sq(y.x);
-                acc += sq(y.y);
-                acc += sq(y.z);
-                acc += sq(y.w);
+            float x[K];
+            load_vec<GD, K>(G, base + int64_t(threadIdx.x) * K, x);
+#pragma unroll
+            for (int c = 0; c < K; ++c) {
+                float y = x[c];
+                if constexpr (kUnscale) y = round_to<GD>(y * unscale);
+                acc += sq(y);
             }
         } else {
             const int64_t end = base + kTile < n ? base + kTile : n;
             for (int64_t e = base + threadIdx.x; e < end; e += kNormBlock) {
-                float x = ld_grad1(G + e);
-                if constexpr (kUnscale) x = x * unscale;
-                acc += sq(x);
+                float y = load_one<GD>(G, e);
+                if constexpr (kUnscale) y = round_to<GD>(y * unscale);
+                acc += sq(y);
             }
         }
     }
@@ -338,74 +424,38 @@ __global__ __launch_bounds__(kNormBlock) void sqnorm_kernel(NormTable tab, float
     if (threadIdx.x == 0) partials[chunk] = block_total * tab.w[t];
 }
 
-// ---- FSDP gradient local share fused with the norm partials -----------------------
-// Writes the rank's fp32 gradient shard exactly as the local-share kernel does (sum
-// over ranks, in rank order, of fp32(x_q) / divisor; +0.0 over the padding tail) and,
-// in the same pass, the squared norm of every 256-element tile of it.  A second,
-// small kernel adds each 128 consecutive tile sums into one partial per 32768-element
-// chunk of the segments [0, valid) and [valid, shard), the layout the norm pass uses,
-// so the optimizer can take them in its place.  Every sum has a fixed order: per lane
-// the 4 squares in element order, per tile a butterfly over the 64 lanes, per chunk
-// lane l's pair (tile l, tile l + 64) then a butterfly.
+// ---- FSDP gradient local share (optionally fused with the norm partials) ------------
+// Writes the rank's gradient shard (sum over ranks, in rank order, of cast(x_q) / divisor
+// in the reduce dtype; +0.0 over the padding tail), cast to the master dtype OD, and, in
+// the same pass, the squared norm of every 256-element tile of that output.  A second,
+// small kernel adds each chunk's tile sums into one partial per norm chunk (32768 fp32 or
+// 65536 2-byte elements) of the segments [0, valid) and [valid, shard), the layout the
+// norm pass uses, so the optimizer can take them in its place.  Every sum has a fixed
+// order: per lane the 4 squares in element order, per tile a butterfly over the 64 lanes,
+// per chunk lane l's tiles l, l + 64, ... in order, then a butterfly.
 struct ShareRanks {
     const uint8_t* g[HBT_MAX_LOCAL_RANKS];
 };
 
 constexpr int kShareBlock = 64;
 constexpr int64_t kShareTile = int64_t(kShareBlock) * 4;  // 256 elements, one wave
-constexpr int64_t kTilesPerNormChunk = norm_chunk<float>() / kShareTile;  // 128
-
-// Loads of one rank's gradient widened to fp32: SB-byte elements, a 2-byte element
-// being bf16, or IEEE fp16 when H is set.
-template <int SB, bool H>
-__device__ __forceinline__ float share_load1(const uint8_t* p) {
-    if constexpr (SB == 4) return *reinterpret_cast<const float*>(p);
-    return b16_to_f32<H>(*reinterpret_cast<const uint16_t*>(p));
-}
+template <int OD>
+constexpr int tiles_per_norm_chunk() { return static_cast<int>(norm_chunk<OD>() / kShareTile); }  // 128 or 256
 
 // Division by a power of two is exact scaling, so x / d == x * (1 / d) bitwise for
 // every x (both are the correctly rounded x * 2^-k); other divisors divide.
 template <bool kRecip>
-__device__ __forceinline__ f32x4 share_div(f32x4 x, float divisor, float recip) {
+__device__ __forceinline__ float share_div(float x, float divisor, float recip) {
     if constexpr (kRecip) return x * recip;
     return x / divisor;
-}
-template <bool kRecip>
-__device__ __forceinline__ float share_div1(float x, float divisor, float recip) {
-    if constexpr (kRecip) return x * recip;
-    return x / divisor;
-}
-template <int SB, bool H>
-__device__ __forceinline__ f32x4 share_load4(const uint8_t* p) {
-    if constexpr (SB == 4) {
-        return ld4_nt(reinterpret_cast<const float*>(p));
-    } else if constexpr (H) {
-        const u32x2 w = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
-        return f32x4{f16_to_f32(w.x & 0xFFFFu), f16_to_f32(w.x >> 16), f16_to_f32(w.y & 0xFFFFu),
-                     f16_to_f32(w.y >> 16)};
-    } else {
-        return ld_grad4_nt(reinterpret_cast<const uint16_t*>(p));
-    }
 }
 
-// The reduce dtype's steps of the reference's AVG reduce-scatter (RD: the dtype code).
-// The gradient is cast to RD unless it already has that dtype (Tensor.to), each
-// division and each addition is rounded to RD (torch computes them in fp32 and rounds
-// once), and the result widens exactly to the fp32 master.  For RD = F32 every step is
-// the identity, so the fp32 instantiations are the plain fp32 local share.
-template <int RD>
-__device__ __forceinline__ f32x4 round4(f32x4 v) {
-    if constexpr (RD == HBT_DTYPE_F32) return v;
-    return f32x4{round_to<RD>(v.x), round_to<RD>(v.y), round_to<RD>(v.z), round_to<RD>(v.w)};
-}
-template <int SB, bool H, int RD>
-__device__ __forceinline__ f32x4 share_cast4(f32x4 x) {
-    if constexpr (dtype_of<SB, H>() == RD) return x;
-    return round4<RD>(x);
-}
-template <int SB, bool H, int RD>
-__device__ __forceinline__ float share_cast1(float x) {
-    if constexpr (dtype_of<SB, H>() == RD) return x;
+// The reference's AVG reduce-scatter in reduce dtype RD over inputs of dtype ID: the
+// gradient is cast to RD unless it already has that dtype (Tensor.to), each division
+// and each addition is rounded to RD (torch computes them in fp32 and rounds once).
+template <int ID, int RD>
+__device__ __forceinline__ float share_cast(float x) {
+    if constexpr (ID == RD) return x;
     return round_to<RD>(x);
 }
 
@@ -413,99 +463,121 @@ __device__ __forceinline__ float share_cast1(float x) {
 // short-lived shape streams at 6.4 TB/s, against 5.6 TB/s for the norm kernel's
 // 1024-thread, 8-tile workgroups.  kG > 0 fixes the group size so that every rank's
 // load is issued before the first is used; kG == 0 reads group_size at run time.
-template <int SB, int kG, bool kRecip, bool H, int RD>
+// tile_sums may be null (the local share alone).
+template <int ID, int kG, bool kRecip, int RD, int OD>
 __global__ __launch_bounds__(kShareBlock) void local_share_tiles_kernel(
     ShareRanks ranks, int32_t group_size, int64_t offset, int64_t shard_numel, int64_t valid_numel,
-    float divisor, float recip, int32_t vec_ok, float* __restrict__ out, double* __restrict__ tile_sums) {
-    const int64_t base = int64_t(blockIdx.x) * kShareTile;
+    float divisor, float recip, int32_t vec_ok, void* __restrict__ out, double* __restrict__ tile_sums,
+    int64_t block_base) {
+    constexpr int64_t IB = bytes_of<ID>();
+    const int64_t tile = block_base + blockIdx.x;
+    const int64_t base = tile * kShareTile;
     double acc = 0.0;
     if (vec_ok && base + kShareTile <= valid_numel) {
         const int64_t e = base + int64_t(threadIdx.x) * 4;
-        f32x4 sum;
+        float sum[4];
         if constexpr (kG > 0) {
-            f32x4 x[kG];
+            float x[kG][4];
 #pragma unroll
-            for (int q = 0; q < kG; ++q) x[q] = share_load4<SB, H>(ranks.g[q] + (offset + e) * SB);
-            sum = round4<RD>(share_div<kRecip>(share_cast4<SB, H, RD>(x[0]), divisor, recip));
+            for (int q = 0; q < kG; ++q) load_vec<ID, 4>(ranks.g[q] + offset * IB, e, x[q]);
 #pragma unroll
-            for (int q = 1; q < kG; ++q) {
-                sum = round4<RD>(sum + round4<RD>(share_div<kRecip>(share_cast4<SB, H, RD>(x[q]), divisor, recip)));
+            for (int c = 0; c < 4; ++c) {
+                sum[c] = round_to<RD>(share_div<kRecip>(share_cast<ID, RD>(x[0][c]), divisor, recip));
+#pragma unroll
+                for (int q = 1; q < kG; ++q) {
+                    sum[c] = round_to<RD>(sum[c] + round_to<RD>(share_div<kRecip>(share_cast<ID, RD>(x[q][c]), divisor, recip)));
+                }
             }
         } else {
-            sum = round4<RD>(share_div<kRecip>(
-                share_cast4<SB, H, RD>(share_load4<SB, H>(ranks.g[0] + (offset + e) * SB)), divisor, recip));
+            float x[4];
+            load_vec<ID, 4>(ranks.g[0] + offset * IB, e, x);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) sum[c] = round_to<RD>(share_div<kRecip>(share_cast<ID, RD>(x[c]), divisor, recip));
             for (int32_t q = 1; q < group_size; ++q) {
-                const f32x4 x = share_cast4<SB, H, RD>(share_load4<SB, H>(ranks.g[q] + (offset + e) * SB));
-                sum = round4<RD>(sum + round4<RD>(share_div<kRecip>(x, divisor, recip)));
+                load_vec<ID, 4>(ranks.g[q] + offset * IB, e, x);
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    sum[c] = round_to<RD>(sum[c] + round_to<RD>(share_div<kRecip>(share_cast<ID, RD>(x[c]), divisor, recip)));
+                }
             }
         }
-        st4_nt(out + e, sum);
-        acc += sq(sum.x);
-        acc += sq(sum.y);
-        acc += sq(sum.z);
-        acc += sq(sum.w);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) sum[c] = round_to<OD>(sum[c]);
+        store_vec<OD, 4>(out, e, sum);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc += sq(sum[c]);
     } else if (vec_ok && base >= valid_numel && base + kShareTile <= shard_numel) {
-        st4_nt(out + base + int64_t(threadIdx.x) * 4, f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+        const float zero[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        store_vec<OD, 4>(out, base + int64_t(threadIdx.x) * 4, zero);
     } else {
         const int64_t end = base + kShareTile < shard_numel ? base + kShareTile : shard_numel;
         for (int64_t e = base + threadIdx.x; e < end; e += kShareBlock) {
             float v = 0.0f;
             if (e < valid_numel) {
-                v = round_to<RD>(share_div1<kRecip>(
-                    share_cast1<SB, H, RD>(share_load1<SB, H>(ranks.g[0] + (offset + e) * SB)), divisor, recip));
+                v = round_to<RD>(share_div<kRecip>(share_cast<ID, RD>(load_one<ID>(ranks.g[0], offset + e)), divisor, recip));
                 for (int32_t q = 1; q < group_size; ++q) {
-                    const float x = share_cast1<SB, H, RD>(share_load1<SB, H>(ranks.g[q] + (offset + e) * SB));
-                    v = round_to<RD>(v + round_to<RD>(share_div1<kRecip>(x, divisor, recip)));
+                    const float x = share_cast<ID, RD>(load_one<ID>(ranks.g[q], offset + e));
+                    v = round_to<RD>(v + round_to<RD>(share_div<kRecip>(x, divisor, recip)));
                 }
+                v = round_to<OD>(v);
             }
-            out[e] = v;
+            store_one<OD>(out, e, v);
             acc += sq(v);
         }
     }
+    if (tile_sums == nullptr) return;
     acc = wave_sum(acc);
-    if (threadIdx.x == 0) tile_sums[blockIdx.x] = acc;
+    if (threadIdx.x == 0) tile_sums[tile] = acc;
 }
 
-// Reduce dtype float64: each rank's element widens exactly to double (SB = 8 reads a
+// Reduce dtype float64: each rank's element widens exactly to double (IB = 8 reads a
 // float64 no_sync accumulator), the divide and the rank-order sum run in double, both
-// correctly rounded as torch's float64 div and add are, and the sum rounds once, to
-// nearest even, to the fp32 master (Tensor.to).  Lane l owns elements 4l .. 4l + 3 of
-// its tile, so the tile sums add the squares in the fp32 kernel's order.
-template <int SB, bool H>
+// correctly rounded as torch's float64 div and add are, and the sum narrows to the
+// master dtype OD as Tensor.to does (to fp32 rounding to nearest even, then, for a
+// 2-byte OD, to OD).  Lane l owns elements 4l .. 4l + 3 of its tile.  That is the fp32
+// kernel's order on full vector tiles; on a ragged tile the fp32 kernel walks elements
+// by lane stride instead, so tile sums there can round differently (the outputs are
+// the same).
+template <int IB, bool IH, int OD>
 __global__ __launch_bounds__(kShareBlock) void local_share_f64_tiles_kernel(
     ShareRanks ranks, int32_t group_size, int64_t offset, int64_t shard_numel, int64_t valid_numel,
-    double divisor, float* __restrict__ out, double* __restrict__ tile_sums) {
-    const int64_t first = int64_t(blockIdx.x) * kShareTile + int64_t(threadIdx.x) * 4;
+    double divisor, void* __restrict__ out, double* __restrict__ tile_sums, int64_t block_base) {
+    const int64_t tile = block_base + blockIdx.x;
+    const int64_t first = tile * kShareTile + int64_t(threadIdx.x) * 4;
     double acc = 0.0;
     for (int j = 0; j < 4; ++j) {
         const int64_t e = first + j;
         if (e >= shard_numel) break;
         float v = 0.0f;
         if (e < valid_numel) {
-            double s = widen_f64<SB, H>(ranks.g[0], offset + e) / divisor;
-            for (int32_t q = 1; q < group_size; ++q) s = s + widen_f64<SB, H>(ranks.g[q], offset + e) / divisor;
-            v = static_cast<float>(s);
+            double s = widen_f64<IB, IH>(ranks.g[0], offset + e) / divisor;
+            for (int32_t q = 1; q < group_size; ++q) s = s + widen_f64<IB, IH>(ranks.g[q], offset + e) / divisor;
+            v = round_to<OD>(static_cast<float>(s));
         }
-        out[e] = v;
+        store_one<OD>(out, e, v);
         acc += sq(v);
     }
+    if (tile_sums == nullptr) return;
     acc = wave_sum(acc);
-    if (threadIdx.x == 0) tile_sums[blockIdx.x] = acc;
+    if (threadIdx.x == 0) tile_sums[tile] = acc;
 }
 
-// Chunk c < valid_chunks: the sum of tile sums 128c .. 128c + 127 (those below
-// valid_tiles); padding chunks: 0, the square sum of zeros.
+// Chunk c < valid_chunks: the sum of its kTiles tile sums (those below valid_tiles), lane
+// l adding tiles l, l + 64, ... in order before the butterfly; padding chunks: 0, the
+// square sum of zeros.
+template <int kTiles>
 __global__ __launch_bounds__(kShareBlock) void tile_sums_to_partials_kernel(
     const double* __restrict__ tile_sums, int64_t valid_tiles, int64_t valid_chunks,
-    double* __restrict__ partials) {
-    const int64_t chunk = blockIdx.x;
+    double* __restrict__ partials, int64_t block_base) {
+    const int64_t chunk = block_base + blockIdx.x;
     double acc = 0.0;
     if (chunk < valid_chunks) {
-        const int64_t first = chunk * kTilesPerNormChunk;
-        const int64_t a = first + threadIdx.x;
-        const int64_t b = a + kShareBlock;
-        if (a < valid_tiles) acc = tile_sums[a];
-        if (b < valid_tiles) acc += tile_sums[b];
+        const int64_t first = chunk * kTiles + threadIdx.x;
+#pragma unroll
+        for (int k = 0; k < kTiles / kShareBlock; ++k) {
+            const int64_t a = first + int64_t(k) * kShareBlock;
+            if (a < valid_tiles) acc += tile_sums[a];
+        }
     }
     acc = wave_sum(acc);
     if (threadIdx.x == 0) partials[chunk] = acc;
@@ -546,12 +618,14 @@ __global__ __launch_bounds__(kFinalBlock) void norm_finalize_kernel(
 }
 
 // ---- in-place scaling ---------------------------------------------------------------
-// Half-wave (32-thread) workgroups, two 16-byte vectors per lane: 256 fp32 or 512 bf16
-// elements per workgroup.  Measured on MI355X (in-place, 1e9 fp32): 6.8 TB/s, against
-// 6.0 TB/s for 64 threads with one vector and 5.5 TB/s with two.
+// Half-wave (32-thread) workgroups, two 16-byte vectors per lane: 256 fp32 or 512
+// bf16/fp16 elements per workgroup.  Measured on MI355X (in-place, 1e9 fp32): 6.8 TB/s,
+// against 6.0 TB/s for 64 threads with one vector and 5.5 TB/s with two.
 constexpr int kScaleBlock = 32;
-template <typename T>
-constexpr int64_t scale_tile() { return int64_t(kScaleBlock) * 2 * (16 / sizeof(T)); }
+template <int D>
+constexpr int scale_vec() { return D == F32 ? 4 : 8; }
+template <int D>
+constexpr int64_t scale_tile() { return int64_t(kScaleBlock) * 2 * scale_vec<D>(); }
 
 struct ScaleTable {
     void* x[kMaxT];
@@ -561,78 +635,37 @@ struct ScaleTable {
     int32_t count;
 };
 
-template <typename T>
-__device__ __forceinline__ float to_f32(T x);
-template <>
-__device__ __forceinline__ float to_f32<float>(float x) { return x; }
-template <>
-__device__ __forceinline__ float to_f32<uint16_t>(uint16_t x) { return bf16_to_f32(x); }
-template <typename T>
-__device__ __forceinline__ T from_f32(float x);
-template <>
-__device__ __forceinline__ float from_f32<float>(float x) { return x; }
-template <>
-__device__ __forceinline__ uint16_t from_f32<uint16_t>(float x) {
-    return static_cast<uint16_t>(f32_to_bf16(x));
+// Two separate multiplies, each rounded to D, as two in-place mul_ calls would do.
+template <int D>
+__device__ __forceinline__ float scale_one(float x, float unscale, float mul) {
+    return round_to<D>(round_to<D>(x * unscale) * mul);
 }
 
-// Two separate multiplies, each rounded to T, as two in-place mul_ calls would do.
-template <typename T>
-__device__ __forceinline__ T scale_one(T x, float unscale, float mul) {
-    const T y = from_f32<T>(to_f32<T>(x) * unscale);
-    return from_f32<T>(to_f32<T>(y) * mul);
-}
-
-template <typename T>
+template <int D>
 __global__ __launch_bounds__(kScaleBlock) void scale_kernel(ScaleTable tab, float unscale,
-                                                            const float* __restrict__ grad_mul) {
-    const int64_t block = blockIdx.x;
-    int t = 0;
-    while (t + 1 < tab.count && block >= tab.first_block[t + 1]) ++t;
-    constexpr int64_t kTile = scale_tile<T>();
+                                                            const float* __restrict__ grad_mul, int64_t block_base) {
+    constexpr int K = scale_vec<D>();
+    constexpr int64_t kTile = scale_tile<D>();
+    const int64_t block = block_base + blockIdx.x;
+    const int t = owning_tensor(tab.first_block, tab.count, block);
     const int64_t base = (block - tab.first_block[t]) * kTile;
     const int64_t n = tab.n[t];
     const float mul = grad_mul != nullptr ? *grad_mul : 1.0f;
-    T* __restrict__ x = static_cast<T*>(tab.x[t]);
-    typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+    void* X = tab.x[t];
     if (tab.vec_ok[t] && base + kTile <= n) {
-        if constexpr (sizeof(T) == 4) {
-            f32x4 v[2];
-            float* p[2];
+        float v[2][K];
 #pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                p[u] = reinterpret_cast<float*>(x) + base + (int64_t(u) * kScaleBlock + threadIdx.x) * 4;
-                v[u] = ld4_nt(p[u]);
-            }
+        for (int u = 0; u < 2; ++u) load_vec<D, K>(X, base + (int64_t(u) * kScaleBlock + threadIdx.x) * K, v[u]);
 #pragma unroll
-            for (int u = 0; u < 2; ++u) {
+        for (int u = 0; u < 2; ++u) {
 #pragma unroll
-                for (int c = 0; c < 4; ++c) v[u][c] = scale_one<float>(v[u][c], unscale, mul);
-                st4_nt(p[u], v[u]);
-            }
-        } else {
-            u32x4v w[2];
-            uint16_t* p[2];
-#pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                p[u] = reinterpret_cast<uint16_t*>(x) + base + (int64_t(u) * kScaleBlock + threadIdx.x) * 8;
-                w[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4v*>(p[u]));
-            }
-#pragma unroll
-            for (int u = 0; u < 2; ++u) {
-#pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    const uint32_t lo = scale_one<uint16_t>(static_cast<uint16_t>(w[u][c] & 0xFFFFu), unscale, mul);
-                    const uint32_t hi = scale_one<uint16_t>(static_cast<uint16_t>(w[u][c] >> 16), unscale, mul);
-                    w[u][c] = lo | (hi << 16);
-                }
-                __builtin_nontemporal_store(w[u], reinterpret_cast<u32x4v*>(p[u]));
-            }
+            for (int c = 0; c < K; ++c) v[u][c] = scale_one<D>(v[u][c], unscale, mul);
+            store_vec<D, K>(X, base + (int64_t(u) * kScaleBlock + threadIdx.x) * K, v[u]);
         }
         return;
     }
     const int64_t end = base + kTile < n ? base + kTile : n;
-    for (int64_t i = base + threadIdx.x; i < end; i += kScaleBlock) x[i] = scale_one<T>(x[i], unscale, mul);
+    for (int64_t i = base + threadIdx.x; i < end; i += kScaleBlock) store_one<D>(X, i, scale_one<D>(load_one<D>(X, i), unscale, mul));
 }
 
 // ---- no_sync gradient accumulation ----------------------------------------------------
@@ -652,94 +685,89 @@ struct AccumTable {
     int32_t count;
 };
 
-// Four elements of B bytes each (fp32, or bf16 / fp16 when H), widened exactly.
-template <int B, bool H>
-__device__ __forceinline__ f32x4 load4_as_f32(const unsigned char* p) {
-    if constexpr (B == 4) {
-        return ld4_nt(reinterpret_cast<const float*>(p));
-    } else {
-        const u32x2 w = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
-        return f32x4{b16_to_f32<H>(w.x & 0xFFFFu), b16_to_f32<H>(w.x >> 16), b16_to_f32<H>(w.y & 0xFFFFu),
-                     b16_to_f32<H>(w.y >> 16)};
-    }
-}
-// Four values already representable in the B-byte dtype, stored in it.
-template <int B, bool H>
-__device__ __forceinline__ void store4_from_f32(unsigned char* p, f32x4 v) {
-    if constexpr (B == 4) {
-        st4_nt(reinterpret_cast<float*>(p), v);
-    } else {
-        const u32x2 w{f32_to_b16<H>(v.x) | (f32_to_b16<H>(v.y) << 16), f32_to_b16<H>(v.z) | (f32_to_b16<H>(v.w) << 16)};
-        __builtin_nontemporal_store(w, reinterpret_cast<u32x2*>(p));
-    }
-}
-template <int B, bool H>
-__device__ __forceinline__ float load1_as_f32(const unsigned char* p, int64_t i) {
-    if constexpr (B == 4) return reinterpret_cast<const float*>(p)[i];
-    return b16_to_f32<H>(reinterpret_cast<const uint16_t*>(p)[i]);
-}
-template <int B, bool H>
-__device__ __forceinline__ void store1_from_f32(unsigned char* p, int64_t i, float v) {
-    if constexpr (B == 4) {
-        reinterpret_cast<float*>(p)[i] = v;
-    } else {
-        reinterpret_cast<uint16_t*>(p)[i] = static_cast<uint16_t>(f32_to_b16<H>(v));
-    }
-}
-
-// SB/SH: the gradient's element size and fp16 flag; AB/AH: the accumulator's.
-template <int SB, bool SH, int AB, bool AH, bool kAssign>
-__global__ __launch_bounds__(kScaleBlock) void accumulate_kernel(AccumTable tab) {
-    constexpr int RD = dtype_of<AB, AH>();
-    const int64_t block = blockIdx.x;
-    int t = 0;
-    while (t + 1 < tab.count && block >= tab.first_block[t + 1]) ++t;
+// GD: the gradient's dtype; AD: the accumulator's.
+template <int GD, int AD, bool kAssign>
+__global__ __launch_bounds__(kScaleBlock) void accumulate_kernel(AccumTable tab, int64_t block_base) {
+    const int64_t block = block_base + blockIdx.x;
+    const int t = owning_tensor(tab.first_block, tab.count, block);
     const int64_t base = (block - tab.first_block[t]) * kAccumTile;
     const int64_t n = tab.n[t];
-    unsigned char* __restrict__ acc = static_cast<unsigned char*>(tab.acc[t]);
-    const unsigned char* __restrict__ grad = static_cast<const unsigned char*>(tab.grad[t]);
+    void* acc = tab.acc[t];
+    const void* grad = tab.grad[t];
     if (tab.vec_ok[t] && base + kAccumTile <= n) {
-        f32x4 a[2], g[2];
+        float a[2][4], g[2][4];
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-            const int64_t i = base + (int64_t(u) * kScaleBlock + threadIdx.x) * 4;
-            g[u] = share_cast4<SB, SH, RD>(load4_as_f32<SB, SH>(grad + i * SB));
+            load_vec<GD, 4>(grad, base + (int64_t(u) * kScaleBlock + threadIdx.x) * 4, g[u]);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) g[u][c] = share_cast<GD, AD>(g[u][c]);
         }
         if constexpr (!kAssign) {
 #pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                const int64_t i = base + (int64_t(u) * kScaleBlock + threadIdx.x) * 4;
-                a[u] = load4_as_f32<AB, AH>(acc + i * AB);
-            }
+            for (int u = 0; u < 2; ++u) load_vec<AD, 4>(acc, base + (int64_t(u) * kScaleBlock + threadIdx.x) * 4, a[u]);
         }
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-            const int64_t i = base + (int64_t(u) * kScaleBlock + threadIdx.x) * 4;
-            if constexpr (kAssign) {
-                store4_from_f32<AB, AH>(acc + i * AB, g[u]);
-            } else {
-                store4_from_f32<AB, AH>(acc + i * AB, round4<RD>(a[u] + g[u]));
+            if constexpr (!kAssign) {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) g[u][c] = round_to<AD>(a[u][c] + g[u][c]);
             }
+            store_vec<AD, 4>(acc, base + (int64_t(u) * kScaleBlock + threadIdx.x) * 4, g[u]);
         }
         return;
     }
     const int64_t end = base + kAccumTile < n ? base + kAccumTile : n;
     for (int64_t i = base + threadIdx.x; i < end; i += kScaleBlock) {
-        const float g = share_cast1<SB, SH, RD>(load1_as_f32<SB, SH>(grad, i));
-        if constexpr (kAssign) {
-            store1_from_f32<AB, AH>(acc, i, g);
-        } else {
-            store1_from_f32<AB, AH>(acc, i, round_to<RD>(load1_as_f32<AB, AH>(acc, i) + g));
-        }
+        const float g = share_cast<GD, AD>(load_one<GD>(grad, i));
+        store_one<AD>(acc, i, kAssign ? g : round_to<AD>(load_one<AD>(acc, i) + g));
     }
 }
 
+// Accumulator float64: the gradient widens exactly (Tensor.to) and each add runs in
+// double, as add_ on float64 tensors does; kAssign writes the widened gradient.
+template <int SB, bool SH, bool kAssign>
+__global__ __launch_bounds__(kScaleBlock) void accumulate_f64_kernel(AccumTable tab, int64_t block_base) {
+    const int64_t block = block_base + blockIdx.x;
+    const int t = owning_tensor(tab.first_block, tab.count, block);
+    const int64_t base = (block - tab.first_block[t]) * kAccumTile;
+    const int64_t n = tab.n[t];
+    double* __restrict__ acc = static_cast<double*>(tab.acc[t]);
+    const unsigned char* __restrict__ grad = static_cast<const unsigned char*>(tab.grad[t]);
+    const int64_t end = base + kAccumTile < n ? base + kAccumTile : n;
+    for (int64_t i = base + threadIdx.x; i < end; i += kScaleBlock) {
+        const double g = widen_f64<SB, SH>(grad, i);
+        acc[i] = kAssign ? g : acc[i] + g;
+    }
+}
+
+// ---- host helpers -----------------------------------------------------------------------
 inline bool aligned(const void* ptr, uintptr_t bytes) {
     return (reinterpret_cast<uintptr_t>(ptr) % bytes) == 0;
 }
 
+// x rounded to a 2-byte dtype and widened back (host side), as torch rounds a Python
+// scalar it adds or uses as an alpha on a tensor of that dtype; fp32 is unchanged.
+float host_round_to(float x, int32_t dtype) {
+    if (dtype == BF16) {
+        uint32_t u;
+        std::memcpy(&u, &x, sizeof u);
+        if ((u & 0x7FFFFFFFu) > 0x7F800000u) return x;
+        u += 0x7FFFu + ((u >> 16) & 1u);
+        u &= 0xFFFF0000u;
+        float y;
+        std::memcpy(&y, &u, sizeof y);
+        return y;
+    }
+    if (dtype == F16) return static_cast<float>(static_cast<_Float16>(x));
+    return x;
+}
 
-// ---- norm launch helpers (shared by the workspace and the no-allocation entry points) --
+// The optimizer dtype pairs (parameter, gradient) with a kernel.
+bool optimizer_dtypes_ok(int32_t param_dtype, int32_t grad_dtype) {
+    return (param_dtype == F32 && (grad_dtype == F32 || grad_dtype == BF16)) ||
+           (param_dtype == BF16 && grad_dtype == BF16) || (param_dtype == F16 && grad_dtype == F16);
+}
+
 // Validates a gradient table and fills the norm kernel's table; `chunks` is the number
 // of partials the launch writes.
 int32_t build_norm_table(const char* who, const void* const* grads, const int64_t* numels,
@@ -749,8 +777,8 @@ int32_t build_norm_table(const char* who, const void* const* grads, const int64_
         set_error("%s: count must lie in [0, %d], got %d", who, kMaxT, count);
         return HBT_ERR_INVALID_ARGUMENT;
     }
-    if (grad_dtype != HBT_DTYPE_F32 && grad_dtype != HBT_DTYPE_BF16) {
-        set_error("%s: gradient dtype %d is not F32 or BF16", who, grad_dtype);
+    if (grad_dtype != F32 && grad_dtype != BF16 && grad_dtype != F16) {
+        set_error("%s: gradient dtype %d is not F32, BF16 or F16", who, grad_dtype);
         return HBT_ERR_INVALID_ARGUMENT;
     }
     if (count > 0 && (grads == nullptr || numels == nullptr || weights == nullptr)) {
@@ -759,7 +787,7 @@ int32_t build_norm_table(const char* who, const void* const* grads, const int64_
     }
     tab = NormTable{};
     tab.count = count;
-    const int64_t kChunk = grad_dtype == HBT_DTYPE_F32 ? norm_chunk<float>() : norm_chunk<uint16_t>();
+    const int64_t kChunk = norm_chunk_of(grad_dtype);
     chunks = 0;
     for (int i = 0; i < count; ++i) {
         if (numels[i] < 0 || (numels[i] > 0 && grads[i] == nullptr)) {
@@ -778,30 +806,21 @@ int32_t build_norm_table(const char* who, const void* const* grads, const int64_
     return HBT_OK;
 }
 
-// One sqnorm_kernel launch writing partials[0, chunks).
+// sqnorm_kernel launches writing partials[0, chunks).
 int32_t launch_sqnorm(const char* who, const NormTable& tab, int64_t chunks, int32_t grad_dtype, float unscale,
                       double* partials, hipStream_t st) {
-    if (chunks == 0) return HBT_OK;
-    if (chunks > 0x7FFFFFFFLL) {
-        set_error("%s: %lld chunks exceed the grid limit", who, static_cast<long long>(chunks));
-        return HBT_ERR_UNSUPPORTED;
-    }
-    const dim3 grid(static_cast<unsigned>(chunks));
     const bool scaled = unscale != 1.0f;
-    if (grad_dtype == HBT_DTYPE_F32) {
-        if (scaled) {
-            sqnorm_kernel<float, true><<<grid, kNormBlock, 0, st>>>(tab, unscale, partials);
-        } else {
-            sqnorm_kernel<float, false><<<grid, kNormBlock, 0, st>>>(tab, unscale, partials);
-        }
-    } else {
-        if (scaled) {
-            sqnorm_kernel<uint16_t, true><<<grid, kNormBlock, 0, st>>>(tab, unscale, partials);
-        } else {
-            sqnorm_kernel<uint16_t, false><<<grid, kNormBlock, 0, st>>>(tab, unscale, partials);
-        }
-    }
-    return check_launch(who);
+    return launch_sliced(who, chunks, kNormBlock, [&](int64_t first, dim3 grid) {
+#define HBT_NORM(GD)                                                                                     \
+    do {                                                                                                 \
+        if (scaled) sqnorm_kernel<GD, true><<<grid, kNormBlock, 0, st>>>(tab, unscale, partials, first);  \
+        else sqnorm_kernel<GD, false><<<grid, kNormBlock, 0, st>>>(tab, unscale, partials, first);        \
+    } while (0)
+        if (grad_dtype == F32) HBT_NORM(F32);
+        else if (grad_dtype == BF16) HBT_NORM(BF16);
+        else HBT_NORM(F16);
+#undef HBT_NORM
+    });
 }
 
 // ---- device address of the no-allocation norm's static scratch ------------------------
@@ -835,43 +854,147 @@ int32_t noalloc_scratch(const char* who, double** out) {
     return HBT_OK;
 }
 
+// Shared by hbt_grad_local_share and hbt_grad_local_share_sqnorm (tile_scratch and
+// partials null for the former).
+int32_t local_share(const char* who, const void* const* rank_grads, int32_t group_size, int32_t rank,
+                    int64_t shard_numel, int64_t valid_numel, int32_t in_dtype, int32_t reduce_dtype,
+                    float divisor, int32_t out_dtype, void* out, double* partials, double* tile_scratch,
+                    hipStream_t st) {
+    if (rank_grads == nullptr || out == nullptr || group_size < 1 || group_size > HBT_MAX_LOCAL_RANKS ||
+        rank < 0 || rank >= group_size || shard_numel < 0 || valid_numel < 0 || valid_numel > shard_numel) {
+        set_error("%s: bad arguments (group_size=%d rank=%d shard=%lld valid=%lld)", who, group_size, rank,
+                  static_cast<long long>(shard_numel), static_cast<long long>(valid_numel));
+        return HBT_ERR_INVALID_ARGUMENT;
+    }
+    const bool f64 = reduce_dtype == HBT_DTYPE_F64;
+    if (in_dtype != F32 && in_dtype != BF16 && in_dtype != F16 && !(f64 && in_dtype == HBT_DTYPE_F64)) {
+        set_error("%s: input dtype %d is not F32, BF16 or F16 (or F64 with reduce dtype F64)", who, in_dtype);
+        return HBT_ERR_INVALID_ARGUMENT;
+    }
+    if (reduce_dtype != F32 && reduce_dtype != BF16 && reduce_dtype != F16 && !f64) {
+        set_error("%s: reduce dtype %d is not F32, BF16, F16 or F64", who, reduce_dtype);
+        return HBT_ERR_INVALID_ARGUMENT;
+    }
+    if (out_dtype != F32 && out_dtype != BF16 && out_dtype != F16) {
+        set_error("%s: output (master) dtype %d is not F32, BF16 or F16", who, out_dtype);
+        return HBT_ERR_INVALID_ARGUMENT;
+    }
+    ShareRanks ranks{};
+    const int elem = dtype_size(in_dtype);
+    const int64_t offset = int64_t(rank) * shard_numel;
+    int32_t vec_ok = aligned(out, 4 * static_cast<uintptr_t>(dtype_size(out_dtype)));
+    for (int q = 0; q < group_size; ++q) {
+        if (rank_grads[q] == nullptr && valid_numel > 0) {
+            set_error("%s: rank %d gradient pointer is null", who, q);
+            return HBT_ERR_INVALID_ARGUMENT;
+        }
+        ranks.g[q] = static_cast<const uint8_t*>(rank_grads[q]);
+        const uintptr_t a = reinterpret_cast<uintptr_t>(ranks.g[q]) + static_cast<uintptr_t>(offset * elem);
+        if ((a & static_cast<uintptr_t>(4 * elem - 1)) != 0) vec_ok = 0;
+    }
+    const int64_t tiles = (shard_numel + kShareTile - 1) / kShareTile;
+    if (tiles == 0) return HBT_OK;
+    // An exact power of two (or 1) divides as a multiply by its exact reciprocal.
+    const float recip = exact_reciprocal(divisor);
+    const bool recip_exact = recip != 0.0f;
+    int32_t status = launch_sliced(who, tiles, kShareBlock, [&](int64_t first, dim3 grid) {
+#define HBT_TILES(ID, G, R, RD, OD)                                                                         \
+    local_share_tiles_kernel<ID, G, R, RD, OD><<<grid, kShareBlock, 0, st>>>(                                 \
+        ranks, group_size, offset, shard_numel, valid_numel, divisor, recip, vec_ok, out, tile_scratch, first)
+// The fp32 reduction into an fp32 master has group-size specialisations (the measured
+// configuration); other reduce and master dtypes run the run-time group size kernel.
+#define HBT_TILES_G(ID, R)                                       \
+    do {                                                         \
+        switch (group_size) {                                    \
+            case 1: HBT_TILES(ID, 1, R, F32, F32); break;        \
+            case 2: HBT_TILES(ID, 2, R, F32, F32); break;        \
+            case 4: HBT_TILES(ID, 4, R, F32, F32); break;        \
+            case 8: HBT_TILES(ID, 8, R, F32, F32); break;        \
+            default: HBT_TILES(ID, 0, R, F32, F32); break;       \
+        }                                                        \
+    } while (0)
+#define HBT_TILES_OD(ID, R, RD)                                    \
+    do {                                                           \
+        if (out_dtype == F32) HBT_TILES(ID, 0, R, RD, F32);        \
+        else if (out_dtype == BF16) HBT_TILES(ID, 0, R, RD, BF16); \
+        else HBT_TILES(ID, 0, R, RD, F16);                         \
+    } while (0)
+#define HBT_TILES_RD(ID, R)                                              \
+    do {                                                                 \
+        if (reduce_dtype == F32 && out_dtype == F32) HBT_TILES_G(ID, R); \
+        else if (reduce_dtype == F32) HBT_TILES_OD(ID, R, F32);          \
+        else if (reduce_dtype == BF16) HBT_TILES_OD(ID, R, BF16);        \
+        else HBT_TILES_OD(ID, R, F16);                                   \
+    } while (0)
+#define HBT_TILES64(IB, IH, OD)                                                                          \
+    local_share_f64_tiles_kernel<IB, IH, OD><<<grid, kShareBlock, 0, st>>>(                                \
+        ranks, group_size, offset, shard_numel, valid_numel, static_cast<double>(divisor), out, tile_scratch, first)
+#define HBT_TILES64_OD(IB, IH)                                 \
+    do {                                                       \
+        if (out_dtype == F32) HBT_TILES64(IB, IH, F32);        \
+        else if (out_dtype == BF16) HBT_TILES64(IB, IH, BF16); \
+        else HBT_TILES64(IB, IH, F16);                         \
+    } while (0)
+        if (f64) {
+            if (in_dtype == HBT_DTYPE_F64) HBT_TILES64_OD(8, false);
+            else if (in_dtype == F32) HBT_TILES64_OD(4, false);
+            else if (in_dtype == BF16) HBT_TILES64_OD(2, false);
+            else HBT_TILES64_OD(2, true);
+        } else if (in_dtype == F32) {
+            if (recip_exact) HBT_TILES_RD(F32, true); else HBT_TILES_RD(F32, false);
+        } else if (in_dtype == BF16) {
+            if (recip_exact) HBT_TILES_RD(BF16, true); else HBT_TILES_RD(BF16, false);
+        } else {
+            if (recip_exact) HBT_TILES_RD(F16, true); else HBT_TILES_RD(F16, false);
+        }
+#undef HBT_TILES64_OD
+#undef HBT_TILES64
+#undef HBT_TILES_RD
+#undef HBT_TILES_OD
+#undef HBT_TILES_G
+#undef HBT_TILES
+    });
+    if (status != HBT_OK || partials == nullptr) return status;
+    const int64_t chunk = norm_chunk_of(out_dtype);
+    const int64_t valid_chunks = (valid_numel + chunk - 1) / chunk;
+    const int64_t pad_chunks = (shard_numel - valid_numel + chunk - 1) / chunk;
+    const int64_t valid_tiles = (valid_numel + kShareTile - 1) / kShareTile;
+    return launch_sliced(who, valid_chunks + pad_chunks, kShareBlock, [&](int64_t first, dim3 grid) {
+        if (out_dtype == F32) {
+            tile_sums_to_partials_kernel<tiles_per_norm_chunk<F32>()><<<grid, kShareBlock, 0, st>>>(
+                tile_scratch, valid_tiles, valid_chunks, partials, first);
+        } else {
+            tile_sums_to_partials_kernel<tiles_per_norm_chunk<BF16>()><<<grid, kShareBlock, 0, st>>>(
+                tile_scratch, valid_tiles, valid_chunks, partials, first);
+        }
+    });
+}
+
 }  // namespace
 }  // namespace hbt
 
 using namespace hbt;
 
-// Accumulator float64: the gradient widens exactly (Tensor.to) and each add runs in
-// double, as add_ on float64 tensors does; kAssign writes the widened gradient.
-template <int SB, bool SH, bool kAssign>
-__global__ __launch_bounds__(kScaleBlock) void accumulate_f64_kernel(AccumTable tab) {
-    const int64_t block = blockIdx.x;
-    int t = 0;
-    while (t + 1 < tab.count && block >= tab.first_block[t + 1]) ++t;
-    const int64_t base = (block - tab.first_block[t]) * kAccumTile;
-    const int64_t n = tab.n[t];
-    double* __restrict__ acc = static_cast<double*>(tab.acc[t]);
-    const unsigned char* __restrict__ grad = static_cast<const unsigned char*>(tab.grad[t]);
-    const int64_t end = base + kAccumTile < n ? base + kAccumTile : n;
-    for (int64_t i = base + threadIdx.x; i < end; i += kScaleBlock) {
-        const double g = widen_f64<SB, SH>(grad, i);
-        acc[i] = kAssign ? g : acc[i] + g;
-    }
-}
-
 extern "C" {
 
-int32_t hbt_adamw_step(float* const* params, const void* const* grads, float* const* exp_avgs,
-                       float* const* exp_avg_sqs, const int64_t* numels, int32_t count,
-                       int32_t grad_dtype, float unscale, const float* grad_mul, float decay,
-                       float lerp_weight, float beta2, float one_minus_beta2,
-                       float bias_correction2_sqrt, float eps, float neg_step_size, void* stream) {
+int32_t hbt_adamw_step(void* const* params, void* const* grads, void* const* exp_avgs,
+                       void* const* exp_avg_sqs, const int64_t* numels, int32_t count,
+                       int32_t param_dtype, int32_t grad_dtype, float unscale, const float* grad_mul,
+                       float decay, float lerp_weight, float beta2, float one_minus_beta2,
+                       float bias_correction2_sqrt, float eps, float neg_step_size, int32_t flags,
+                       void* stream) {
     clear_error();
     if (count < 0 || count > kMaxT) {
         set_error("hbt_adamw_step: count must lie in [0, %d], got %d", kMaxT, count);
         return HBT_ERR_INVALID_ARGUMENT;
     }
-    if (grad_dtype != HBT_DTYPE_F32 && grad_dtype != HBT_DTYPE_BF16) {
-        set_error("hbt_adamw_step: gradient dtype %d is not F32 or BF16", grad_dtype);
+    if (!optimizer_dtypes_ok(param_dtype, grad_dtype)) {
+        set_error("hbt_adamw_step: (parameter, gradient) dtypes (%d, %d) are not (F32, F32), (F32, BF16), "
+                  "(BF16, BF16) or (F16, F16)", param_dtype, grad_dtype);
+        return HBT_ERR_INVALID_ARGUMENT;
+    }
+    if ((flags & ~HBT_STEP_WRITE_GRAD) != 0) {
+        set_error("hbt_adamw_step: unknown flags 0x%x", static_cast<unsigned>(flags));
         return HBT_ERR_INVALID_ARGUMENT;
     }
     if (count > 0 && (params == nullptr || grads == nullptr || exp_avgs == nullptr ||
@@ -881,7 +1004,10 @@ int32_t hbt_adamw_step(float* const* params, const void* const* grads, float* co
     }
     AdamTable tab{};
     tab.count = count;
-    const uintptr_t grad_align = grad_dtype == HBT_DTYPE_F32 ? 16 : 8;
+    const int64_t tile = param_dtype == F32 ? adam_tile<F32>() : adam_tile<BF16>();
+    const int vec = param_dtype == F32 ? adam_vec<F32>() : adam_vec<BF16>();
+    const uintptr_t state_align = static_cast<uintptr_t>(vec * dtype_size(param_dtype));
+    const uintptr_t grad_align = static_cast<uintptr_t>(vec * dtype_size(grad_dtype));
     int64_t blocks = 0;
     for (int i = 0; i < count; ++i) {
         if (numels[i] < 0) {
@@ -899,18 +1025,13 @@ int32_t hbt_adamw_step(float* const* params, const void* const* grads, float* co
         tab.m[i] = exp_avgs[i];
         tab.v[i] = exp_avg_sqs[i];
         tab.n[i] = numels[i];
-        tab.vec_ok[i] = aligned(params[i], 16) && aligned(grads[i], grad_align) &&
-                        aligned(exp_avgs[i], 16) && aligned(exp_avg_sqs[i], 16);
+        tab.vec_ok[i] = aligned(params[i], state_align) && aligned(grads[i], grad_align) &&
+                        aligned(exp_avgs[i], state_align) && aligned(exp_avg_sqs[i], state_align);
         tab.first_block[i] = blocks;
-        blocks += (numels[i] + kAdamTile - 1) / kAdamTile;
+        blocks += (numels[i] + tile - 1) / tile;
     }
     tab.first_block[count] = blocks;
     for (int i = count + 1; i <= kMaxT; ++i) tab.first_block[i] = blocks;
-    if (blocks == 0) return HBT_OK;
-    if (blocks > 0x7FFFFFFFLL) {
-        set_error("hbt_adamw_step: %lld tiles exceed the grid limit", static_cast<long long>(blocks));
-        return HBT_ERR_UNSUPPORTED;
-    }
     AdamScalars s{};
     s.unscale = unscale;
     s.decay = decay;
@@ -919,35 +1040,45 @@ int32_t hbt_adamw_step(float* const* params, const void* const* grads, float* co
     s.beta2 = beta2;
     s.one_minus_beta2 = one_minus_beta2;
     s.bc2_sqrt = bias_correction2_sqrt;
-    s.eps = eps;
+    s.eps = host_round_to(eps, param_dtype);
     s.neg_step = neg_step_size;
     const bool lerp_small = std::fabs(lerp_weight) < 0.5f;
     const bool scaled = unscale != 1.0f;
-    const dim3 grid(static_cast<unsigned>(blocks));
+    const bool write_back = (flags & HBT_STEP_WRITE_GRAD) != 0;
     hipStream_t st = as_stream(stream);
-#define HBT_ADAMW_LAUNCH(GT, SMALL, SCALED) \
-    adamw_kernel<GT, SMALL, SCALED><<<grid, kAdamBlock, 0, st>>>(tab, s, grad_mul)
-    if (grad_dtype == HBT_DTYPE_F32) {
-        if (lerp_small) {
-            if (scaled) HBT_ADAMW_LAUNCH(float, true, true); else HBT_ADAMW_LAUNCH(float, true, false);
-        } else {
-            if (scaled) HBT_ADAMW_LAUNCH(float, false, true); else HBT_ADAMW_LAUNCH(float, false, false);
-        }
-    } else {
-        if (lerp_small) {
-            if (scaled) HBT_ADAMW_LAUNCH(uint16_t, true, true); else HBT_ADAMW_LAUNCH(uint16_t, true, false);
-        } else {
-            if (scaled) HBT_ADAMW_LAUNCH(uint16_t, false, true); else HBT_ADAMW_LAUNCH(uint16_t, false, false);
-        }
-    }
-#undef HBT_ADAMW_LAUNCH
-    return check_launch("hbt_adamw_step");
+    return launch_sliced("hbt_adamw_step", blocks, kAdamBlock, [&](int64_t first, dim3 grid) {
+#define HBT_ADAMW(PD, GD, SMALL, SCALED, WB) \
+    adamw_kernel<PD, GD, SMALL, SCALED, WB><<<grid, kAdamBlock, 0, st>>>(tab, s, grad_mul, first)
+#define HBT_ADAMW_WB(PD, GD, SMALL, SCALED)                     \
+    do {                                                        \
+        if (write_back) HBT_ADAMW(PD, GD, SMALL, SCALED, true); \
+        else HBT_ADAMW(PD, GD, SMALL, SCALED, false);           \
+    } while (0)
+#define HBT_ADAMW_SCALED(PD, GD, SMALL)                \
+    do {                                               \
+        if (scaled) HBT_ADAMW_WB(PD, GD, SMALL, true); \
+        else HBT_ADAMW_WB(PD, GD, SMALL, false);       \
+    } while (0)
+#define HBT_ADAMW_LERP(PD, GD)                          \
+    do {                                                \
+        if (lerp_small) HBT_ADAMW_SCALED(PD, GD, true); \
+        else HBT_ADAMW_SCALED(PD, GD, false);           \
+    } while (0)
+        if (param_dtype == F32 && grad_dtype == F32) HBT_ADAMW_LERP(F32, F32);
+        else if (param_dtype == F32) HBT_ADAMW_LERP(F32, BF16);
+        else if (param_dtype == BF16) HBT_ADAMW_LERP(BF16, BF16);
+        else HBT_ADAMW_LERP(F16, F16);
+#undef HBT_ADAMW_LERP
+#undef HBT_ADAMW_SCALED
+#undef HBT_ADAMW_WB
+#undef HBT_ADAMW
+    });
 }
 
 int64_t hbt_norm_partials_count(const int64_t* numels, int32_t count, int32_t grad_dtype) {
     if (count < 0 || count > kMaxT || (count > 0 && numels == nullptr)) return -1;
-    if (grad_dtype != HBT_DTYPE_F32 && grad_dtype != HBT_DTYPE_BF16) return -1;
-    const int64_t chunk = grad_dtype == HBT_DTYPE_F32 ? norm_chunk<float>() : norm_chunk<uint16_t>();
+    if (grad_dtype != F32 && grad_dtype != BF16 && grad_dtype != F16) return -1;
+    const int64_t chunk = norm_chunk_of(grad_dtype);
     int64_t chunks = 0;
     for (int i = 0; i < count; ++i) {
         if (numels[i] < 0) return -1;
@@ -998,10 +1129,10 @@ int32_t hbt_grad_norm_noalloc(const void* const* grads, const int64_t* numels, c
     if (status != HBT_OK) return status;
     if (chunks > HBT_NOALLOC_MAX_PARTIALS) {
         set_error("hbt_grad_norm_noalloc: the gradients need %lld norm partials, more than the %d the "
-                  "static scratch holds (at most %lld fp32 or %lld bf16 elements per call)",
+                  "static scratch holds (at most %lld fp32 or %lld bf16/fp16 elements per call)",
                   static_cast<long long>(chunks), HBT_NOALLOC_MAX_PARTIALS,
-                  static_cast<long long>(HBT_NOALLOC_MAX_PARTIALS * norm_chunk<float>()),
-                  static_cast<long long>(HBT_NOALLOC_MAX_PARTIALS * norm_chunk<uint16_t>()));
+                  static_cast<long long>(HBT_NOALLOC_MAX_PARTIALS * norm_chunk<F32>()),
+                  static_cast<long long>(HBT_NOALLOC_MAX_PARTIALS * norm_chunk<BF16>()));
         return HBT_ERR_UNSUPPORTED;
     }
     double* partials = nullptr;
@@ -1024,13 +1155,13 @@ int32_t hbt_scale_inplace(void* const* tensors, const int64_t* numels, int32_t c
         set_error("hbt_scale_inplace: bad table (count=%d)", count);
         return HBT_ERR_INVALID_ARGUMENT;
     }
-    if (dtype != HBT_DTYPE_F32 && dtype != HBT_DTYPE_BF16) {
-        set_error("hbt_scale_inplace: dtype %d is not F32 or BF16", dtype);
+    if (dtype != F32 && dtype != BF16 && dtype != F16) {
+        set_error("hbt_scale_inplace: dtype %d is not F32, BF16 or F16", dtype);
         return HBT_ERR_INVALID_ARGUMENT;
     }
     ScaleTable tab{};
     tab.count = count;
-    const int64_t tile = dtype == HBT_DTYPE_F32 ? scale_tile<float>() : scale_tile<uint16_t>();
+    const int64_t tile = dtype == F32 ? scale_tile<F32>() : scale_tile<BF16>();
     int64_t blocks = 0;
     for (int i = 0; i < count; ++i) {
         if (numels[i] < 0 || (numels[i] > 0 && tensors[i] == nullptr)) {
@@ -1045,19 +1176,12 @@ int32_t hbt_scale_inplace(void* const* tensors, const int64_t* numels, int32_t c
     }
     tab.first_block[count] = blocks;
     for (int i = count + 1; i <= kMaxT; ++i) tab.first_block[i] = blocks;
-    if (blocks == 0) return HBT_OK;
-    if (blocks > 0x7FFFFFFFLL) {
-        set_error("hbt_scale_inplace: %lld tiles exceed the grid limit", static_cast<long long>(blocks));
-        return HBT_ERR_UNSUPPORTED;
-    }
-    if (dtype == HBT_DTYPE_F32) {
-        scale_kernel<float><<<dim3(static_cast<unsigned>(blocks)), kScaleBlock, 0, as_stream(stream)>>>(
-            tab, unscale, grad_mul);
-    } else {
-        scale_kernel<uint16_t><<<dim3(static_cast<unsigned>(blocks)), kScaleBlock, 0, as_stream(stream)>>>(
-            tab, unscale, grad_mul);
-    }
-    return check_launch("hbt_scale_inplace");
+    hipStream_t st = as_stream(stream);
+    return launch_sliced("hbt_scale_inplace", blocks, kScaleBlock, [&](int64_t first, dim3 grid) {
+        if (dtype == F32) scale_kernel<F32><<<grid, kScaleBlock, 0, st>>>(tab, unscale, grad_mul, first);
+        else if (dtype == BF16) scale_kernel<BF16><<<grid, kScaleBlock, 0, st>>>(tab, unscale, grad_mul, first);
+        else scale_kernel<F16><<<grid, kScaleBlock, 0, st>>>(tab, unscale, grad_mul, first);
+    });
 }
 
 int32_t hbt_grad_accumulate(void* const* accumulators, const void* const* grads, const int64_t* numels,
@@ -1068,9 +1192,7 @@ int32_t hbt_grad_accumulate(void* const* accumulators, const void* const* grads,
         set_error("hbt_grad_accumulate: bad table (count=%d)", count);
         return HBT_ERR_INVALID_ARGUMENT;
     }
-    const auto float_code = [](int32_t d) {
-        return d == HBT_DTYPE_F32 || d == HBT_DTYPE_BF16 || d == HBT_DTYPE_F16;
-    };
+    const auto float_code = [](int32_t d) { return d == F32 || d == BF16 || d == F16; };
     const bool f64 = acc_dtype == HBT_DTYPE_F64;
     if (!(float_code(acc_dtype) || f64) || !(float_code(grad_dtype) || (f64 && grad_dtype == HBT_DTYPE_F64))) {
         set_error("hbt_grad_accumulate: dtypes (accumulator %d, gradient %d) must be F32, BF16 or F16 "
@@ -1101,158 +1223,66 @@ int32_t hbt_grad_accumulate(void* const* accumulators, const void* const* grads,
     }
     tab.first_block[count] = blocks;
     for (int i = count + 1; i <= kMaxT; ++i) tab.first_block[i] = blocks;
-    if (blocks == 0) return HBT_OK;
-    if (blocks > 0x7FFFFFFFLL) {
-        set_error("hbt_grad_accumulate: %lld tiles exceed the grid limit", static_cast<long long>(blocks));
-        return HBT_ERR_UNSUPPORTED;
-    }
-    const dim3 grid(static_cast<unsigned>(blocks));
     hipStream_t st = as_stream(stream);
     const bool assign = (flags & HBT_ACCUMULATE_ASSIGN) != 0;
-#define HBT_ACC(SB, SH, AB, AH)                                                                    \
+    return launch_sliced("hbt_grad_accumulate", blocks, kScaleBlock, [&](int64_t first, dim3 grid) {
+#define HBT_ACC(GD, AD)                                                                        \
+    do {                                                                                       \
+        if (assign) accumulate_kernel<GD, AD, true><<<grid, kScaleBlock, 0, st>>>(tab, first); \
+        else accumulate_kernel<GD, AD, false><<<grid, kScaleBlock, 0, st>>>(tab, first);       \
+    } while (0)
+#define HBT_ACC_A(GD)                                  \
+    do {                                               \
+        if (acc_dtype == F32) HBT_ACC(GD, F32);        \
+        else if (acc_dtype == BF16) HBT_ACC(GD, BF16); \
+        else HBT_ACC(GD, F16);                         \
+    } while (0)
+#define HBT_ACC64(SB, SH)                                                                          \
     do {                                                                                           \
-        if (assign) accumulate_kernel<SB, SH, AB, AH, true><<<grid, kScaleBlock, 0, st>>>(tab);    \
-        else accumulate_kernel<SB, SH, AB, AH, false><<<grid, kScaleBlock, 0, st>>>(tab);          \
+        if (assign) accumulate_f64_kernel<SB, SH, true><<<grid, kScaleBlock, 0, st>>>(tab, first); \
+        else accumulate_f64_kernel<SB, SH, false><<<grid, kScaleBlock, 0, st>>>(tab, first);       \
     } while (0)
-#define HBT_ACC_A(SB, SH)                                                          \
-    do {                                                                           \
-        if (acc_dtype == HBT_DTYPE_F32) HBT_ACC(SB, SH, 4, false);                  \
-        else if (acc_dtype == HBT_DTYPE_BF16) HBT_ACC(SB, SH, 2, false);            \
-        else HBT_ACC(SB, SH, 2, true);                                             \
-    } while (0)
-#define HBT_ACC64(SB, SH)                                                                    \
-    do {                                                                                     \
-        if (assign) accumulate_f64_kernel<SB, SH, true><<<grid, kScaleBlock, 0, st>>>(tab);   \
-        else accumulate_f64_kernel<SB, SH, false><<<grid, kScaleBlock, 0, st>>>(tab);         \
-    } while (0)
-    if (f64) {
-        if (grad_dtype == HBT_DTYPE_F64) HBT_ACC64(8, false);
-        else if (grad_dtype == HBT_DTYPE_F32) HBT_ACC64(4, false);
-        else if (grad_dtype == HBT_DTYPE_BF16) HBT_ACC64(2, false);
-        else HBT_ACC64(2, true);
-    } else if (grad_dtype == HBT_DTYPE_F32) {
-        HBT_ACC_A(4, false);
-    } else if (grad_dtype == HBT_DTYPE_BF16) {
-        HBT_ACC_A(2, false);
-    } else {
-        HBT_ACC_A(2, true);
-    }
+        if (f64) {
+            if (grad_dtype == HBT_DTYPE_F64) HBT_ACC64(8, false);
+            else if (grad_dtype == F32) HBT_ACC64(4, false);
+            else if (grad_dtype == BF16) HBT_ACC64(2, false);
+            else HBT_ACC64(2, true);
+        } else if (grad_dtype == F32) {
+            HBT_ACC_A(F32);
+        } else if (grad_dtype == BF16) {
+            HBT_ACC_A(BF16);
+        } else {
+            HBT_ACC_A(F16);
+        }
 #undef HBT_ACC_A
 #undef HBT_ACC64
 #undef HBT_ACC
-    return check_launch("hbt_grad_accumulate");
+    });
 }
 
+int32_t hbt_grad_local_share(const void* const* rank_grads, int32_t group_size, int32_t rank,
+                             int64_t shard_numel, int64_t valid_numel, int32_t in_dtype,
+                             int32_t reduce_dtype, float divisor, int32_t out_dtype, void* out, void* stream) {
+    clear_error();
+    return local_share("hbt_grad_local_share", rank_grads, group_size, rank, shard_numel, valid_numel, in_dtype,
+                       reduce_dtype, divisor, out_dtype, out, nullptr, nullptr, as_stream(stream));
+}
 
 int32_t hbt_grad_local_share_sqnorm(const void* const* rank_grads, int32_t group_size, int32_t rank,
                                     int64_t shard_numel, int64_t valid_numel, int32_t in_dtype,
-                                    int32_t reduce_dtype, float divisor, float* out, double* partials,
-                                    double* tile_scratch, void* stream) {
+                                    int32_t reduce_dtype, float divisor, int32_t out_dtype, void* out,
+                                    double* partials, double* tile_scratch, void* stream) {
     clear_error();
-    if (rank_grads == nullptr || out == nullptr || partials == nullptr || tile_scratch == nullptr ||
-        group_size < 1 || group_size > HBT_MAX_LOCAL_RANKS || rank < 0 || rank >= group_size ||
-        shard_numel < 0 || valid_numel < 0 || valid_numel > shard_numel) {
-        set_error("hbt_grad_local_share_sqnorm: bad arguments (group_size=%d rank=%d shard=%lld valid=%lld)",
-                  group_size, rank, static_cast<long long>(shard_numel), static_cast<long long>(valid_numel));
+    if (partials == nullptr || tile_scratch == nullptr) {
+        set_error("hbt_grad_local_share_sqnorm: null partials or tile scratch");
         return HBT_ERR_INVALID_ARGUMENT;
     }
-    const bool f64 = reduce_dtype == HBT_DTYPE_F64;
-    if (in_dtype != HBT_DTYPE_F32 && in_dtype != HBT_DTYPE_BF16 && in_dtype != HBT_DTYPE_F16 &&
-        !(f64 && in_dtype == HBT_DTYPE_F64)) {
-        set_error("hbt_grad_local_share_sqnorm: input dtype %d is not F32, BF16 or F16 (or F64 with reduce dtype F64)",
-                  in_dtype);
-        return HBT_ERR_INVALID_ARGUMENT;
-    }
-    if (reduce_dtype != HBT_DTYPE_F32 && reduce_dtype != HBT_DTYPE_BF16 && reduce_dtype != HBT_DTYPE_F16 && !f64) {
-        set_error("hbt_grad_local_share_sqnorm: reduce dtype %d is not F32, BF16, F16 or F64", reduce_dtype);
-        return HBT_ERR_INVALID_ARGUMENT;
-    }
-    ShareRanks ranks{};
-    const int elem = dtype_size(in_dtype);
-    const int64_t offset = int64_t(rank) * shard_numel;
-    int32_t vec_ok = aligned(out, 16);
-    for (int q = 0; q < group_size; ++q) {
-        if (rank_grads[q] == nullptr && valid_numel > 0) {
-            set_error("hbt_grad_local_share_sqnorm: rank %d gradient pointer is null", q);
-            return HBT_ERR_INVALID_ARGUMENT;
-        }
-        ranks.g[q] = static_cast<const uint8_t*>(rank_grads[q]);
-        const uintptr_t a = reinterpret_cast<uintptr_t>(ranks.g[q]) + static_cast<uintptr_t>(offset * elem);
-        if ((a & static_cast<uintptr_t>(4 * elem - 1)) != 0) vec_ok = 0;
-    }
-    const int64_t chunk = norm_chunk<float>();
-    const int64_t valid_chunks = (valid_numel + chunk - 1) / chunk;
-    const int64_t pad_chunks = (shard_numel - valid_numel + chunk - 1) / chunk;
-    const int64_t tiles = (shard_numel + kShareTile - 1) / kShareTile;
-    const int64_t valid_tiles = (valid_numel + kShareTile - 1) / kShareTile;
-    if (tiles == 0) return HBT_OK;
-    if (tiles > 0x7FFFFFFFLL) {
-        set_error("hbt_grad_local_share_sqnorm: %lld tiles exceed the grid limit", static_cast<long long>(tiles));
-        return HBT_ERR_UNSUPPORTED;
-    }
-    hipStream_t st = as_stream(stream);
-    // An exact power of two (or 1) divides as a multiply by its exact reciprocal.
-    const float recip = exact_reciprocal(divisor);
-    const bool recip_exact = recip != 0.0f;
-    const dim3 grid(static_cast<unsigned>(tiles));
-#define HBT_TILES(SBYTES, G, R, H, RD)                                                          \
-    local_share_tiles_kernel<SBYTES, G, R, H, RD><<<grid, kShareBlock, 0, st>>>(                  \
-        ranks, group_size, offset, shard_numel, valid_numel, divisor, recip, vec_ok, out, tile_scratch)
-#define HBT_TILES_G(SBYTES, R, H)                                          \
-    do {                                                                   \
-        switch (group_size) {                                              \
-            case 1: HBT_TILES(SBYTES, 1, R, H, HBT_DTYPE_F32); break;      \
-            case 2: HBT_TILES(SBYTES, 2, R, H, HBT_DTYPE_F32); break;      \
-            case 4: HBT_TILES(SBYTES, 4, R, H, HBT_DTYPE_F32); break;      \
-            case 8: HBT_TILES(SBYTES, 8, R, H, HBT_DTYPE_F32); break;      \
-            default: HBT_TILES(SBYTES, 0, R, H, HBT_DTYPE_F32); break;     \
-        }                                                                  \
-    } while (0)
-// A 2-byte reduce dtype runs the run-time group size kernel only: the fp32 reduction
-// is the configuration the group-size specialisations were tuned for.
-#define HBT_TILES_RD(SBYTES, R, H)                                                            \
-    do {                                                                                      \
-        if (reduce_dtype == HBT_DTYPE_F32) {                                                  \
-            HBT_TILES_G(SBYTES, R, H);                                                        \
-        } else if (reduce_dtype == HBT_DTYPE_BF16) {                                          \
-            HBT_TILES(SBYTES, 0, R, H, HBT_DTYPE_BF16);                                       \
-        } else {                                                                              \
-            HBT_TILES(SBYTES, 0, R, H, HBT_DTYPE_F16);                                        \
-        }                                                                                     \
-    } while (0)
-#define HBT_TILES64(SBYTES, H)                                                                    \
-    local_share_f64_tiles_kernel<SBYTES, H><<<grid, kShareBlock, 0, st>>>(                          \
-        ranks, group_size, offset, shard_numel, valid_numel, static_cast<double>(divisor), out, tile_scratch)
-    if (f64) {
-        if (in_dtype == HBT_DTYPE_F64) HBT_TILES64(8, false);
-        else if (in_dtype == HBT_DTYPE_F32) HBT_TILES64(4, false);
-        else if (in_dtype == HBT_DTYPE_BF16) HBT_TILES64(2, false);
-        else HBT_TILES64(2, true);
-    } else if (in_dtype == HBT_DTYPE_F32) {
-        if (recip_exact) HBT_TILES_RD(4, true, false); else HBT_TILES_RD(4, false, false);
-    } else if (in_dtype == HBT_DTYPE_BF16) {
-        if (recip_exact) HBT_TILES_RD(2, true, false); else HBT_TILES_RD(2, false, false);
-    } else {
-        if (recip_exact) HBT_TILES_RD(2, true, true); else HBT_TILES_RD(2, false, true);
-    }
-#undef HBT_TILES_RD
-#undef HBT_TILES64
-#undef HBT_TILES_G
-#undef HBT_TILES
-    const hipError_t launched = hipGetLastError();
-    if (launched != hipSuccess) {
-        set_error("hbt_grad_local_share_sqnorm: %s", hipGetErrorString(launched));
-        return HBT_ERR_HIP;
-    }
-    const int64_t chunks = valid_chunks + pad_chunks;
-    tile_sums_to_partials_kernel<<<dim3(static_cast<unsigned>(chunks)), kShareBlock, 0, st>>>(
-        tile_scratch, valid_tiles, valid_chunks, partials);
-    return check_launch("hbt_grad_local_share_sqnorm");
+    return local_share("hbt_grad_local_share_sqnorm", rank_grads, group_size, rank, shard_numel, valid_numel,
+                       in_dtype, reduce_dtype, divisor, out_dtype, out, partials, tile_scratch, as_stream(stream));
 }
 
-
-int32_t hbt_sgd_step(float* const* params, const void* const* grads, float* const* momentum_buffers,
-                     const int64_t* numels, int32_t count, int32_t grad_dtype, float unscale,
+int32_t hbt_sgd_step(void* const* params, void* const* grads, void* const* momentum_buffers,
+                     const int64_t* numels, int32_t count, int32_t param_dtype, int32_t grad_dtype, float unscale,
                      const float* grad_mul, float weight_decay, float momentum, float one_minus_dampening,
                      float neg_lr, int32_t flags, void* stream) {
     clear_error();
@@ -1260,11 +1290,14 @@ int32_t hbt_sgd_step(float* const* params, const void* const* grads, float* cons
         set_error("hbt_sgd_step: count must lie in [0, %d], got %d", kMaxT, count);
         return HBT_ERR_INVALID_ARGUMENT;
     }
-    if (grad_dtype != HBT_DTYPE_F32 && grad_dtype != HBT_DTYPE_BF16) {
-        set_error("hbt_sgd_step: gradient dtype %d is not F32 or BF16", grad_dtype);
+    if (!optimizer_dtypes_ok(param_dtype, grad_dtype)) {
+        set_error("hbt_sgd_step: (parameter, gradient) dtypes (%d, %d) are not (F32, F32), (F32, BF16), "
+                  "(BF16, BF16) or (F16, F16)", param_dtype, grad_dtype);
         return HBT_ERR_INVALID_ARGUMENT;
     }
-    if ((flags & ~(HBT_SGD_MOMENTUM | HBT_SGD_FIRST_STEP | HBT_SGD_NESTEROV | HBT_SGD_WEIGHT_DECAY)) != 0 ||
+    const int32_t known = HBT_SGD_MOMENTUM | HBT_SGD_FIRST_STEP | HBT_SGD_NESTEROV | HBT_SGD_WEIGHT_DECAY |
+                          HBT_STEP_WRITE_GRAD;
+    if ((flags & ~known) != 0 ||
         ((flags & (HBT_SGD_FIRST_STEP | HBT_SGD_NESTEROV)) != 0 && (flags & HBT_SGD_MOMENTUM) == 0)) {
         set_error("hbt_sgd_step: bad flags 0x%x", flags);
         return HBT_ERR_INVALID_ARGUMENT;
@@ -1277,7 +1310,10 @@ int32_t hbt_sgd_step(float* const* params, const void* const* grads, float* cons
     }
     SgdTable tab{};
     tab.count = count;
-    const uintptr_t grad_align = grad_dtype == HBT_DTYPE_F32 ? 16 : 8;
+    const int64_t tile = param_dtype == F32 ? adam_tile<F32>() : adam_tile<BF16>();
+    const int vec = param_dtype == F32 ? adam_vec<F32>() : adam_vec<BF16>();
+    const uintptr_t state_align = static_cast<uintptr_t>(vec * dtype_size(param_dtype));
+    const uintptr_t grad_align = static_cast<uintptr_t>(vec * dtype_size(grad_dtype));
     int64_t blocks = 0;
     for (int i = 0; i < count; ++i) {
         if (numels[i] < 0 || (numels[i] > 0 && (params[i] == nullptr || grads[i] == nullptr ||
@@ -1289,41 +1325,54 @@ int32_t hbt_sgd_step(float* const* params, const void* const* grads, float* cons
         tab.g[i] = grads[i];
         tab.buf[i] = with_momentum ? momentum_buffers[i] : nullptr;
         tab.n[i] = numels[i];
-        tab.vec_ok[i] = aligned(params[i], 16) && aligned(grads[i], grad_align) &&
-                        (!with_momentum || aligned(momentum_buffers[i], 16));
+        tab.vec_ok[i] = aligned(params[i], state_align) && aligned(grads[i], grad_align) &&
+                        (!with_momentum || aligned(momentum_buffers[i], state_align));
         tab.first_block[i] = blocks;
-        blocks += (numels[i] + kAdamTile - 1) / kAdamTile;
+        blocks += (numels[i] + tile - 1) / tile;
     }
     tab.first_block[count] = blocks;
     for (int i = count + 1; i <= kMaxT; ++i) tab.first_block[i] = blocks;
-    if (blocks == 0) return HBT_OK;
-    if (blocks > 0x7FFFFFFFLL) {
-        set_error("hbt_sgd_step: %lld tiles exceed the grid limit", static_cast<long long>(blocks));
-        return HBT_ERR_UNSUPPORTED;
-    }
-    SgdScalars sc{unscale, weight_decay, momentum, one_minus_dampening, neg_lr,
-                  (flags & HBT_SGD_WEIGHT_DECAY) != 0, (flags & HBT_SGD_NESTEROV) != 0};
+    // torch rounds each `alpha` (and nothing multiplied by mul_) to the parameter dtype.
+    const SgdScalars sc{unscale,
+                        host_round_to(weight_decay, param_dtype),
+                        momentum,
+                        host_round_to(momentum, param_dtype),
+                        host_round_to(one_minus_dampening, param_dtype),
+                        host_round_to(neg_lr, param_dtype),
+                        (flags & HBT_SGD_WEIGHT_DECAY) != 0,
+                        (flags & HBT_SGD_NESTEROV) != 0};
     const int mode = !with_momentum ? kSgdPlain : ((flags & HBT_SGD_FIRST_STEP) ? kSgdFirst : kSgdMomentum);
     const bool scaled = unscale != 1.0f;
-    const dim3 grid(static_cast<unsigned>(blocks));
+    const bool write_back = (flags & HBT_STEP_WRITE_GRAD) != 0;
     hipStream_t st = as_stream(stream);
-#define HBT_SGD_LAUNCH(GT, SCALED, MODE) \
-    sgd_kernel<GT, SCALED, MODE><<<grid, kAdamBlock, 0, st>>>(tab, sc, grad_mul)
-#define HBT_SGD_MODES(GT, SCALED)                                          \
-    do {                                                                   \
-        if (mode == kSgdPlain) HBT_SGD_LAUNCH(GT, SCALED, kSgdPlain);      \
-        else if (mode == kSgdFirst) HBT_SGD_LAUNCH(GT, SCALED, kSgdFirst); \
-        else HBT_SGD_LAUNCH(GT, SCALED, kSgdMomentum);                     \
+    return launch_sliced("hbt_sgd_step", blocks, kAdamBlock, [&](int64_t first, dim3 grid) {
+#define HBT_SGD(PD, GD, SCALED, MODE, WB) \
+    sgd_kernel<PD, GD, SCALED, MODE, WB><<<grid, kAdamBlock, 0, st>>>(tab, sc, grad_mul, first)
+#define HBT_SGD_WB(PD, GD, SCALED, MODE)                     \
+    do {                                                     \
+        if (write_back) HBT_SGD(PD, GD, SCALED, MODE, true); \
+        else HBT_SGD(PD, GD, SCALED, MODE, false);           \
     } while (0)
-    if (grad_dtype == HBT_DTYPE_F32) {
-        if (scaled) HBT_SGD_MODES(float, true); else HBT_SGD_MODES(float, false);
-    } else {
-        if (scaled) HBT_SGD_MODES(uint16_t, true); else HBT_SGD_MODES(uint16_t, false);
-    }
+#define HBT_SGD_MODES(PD, GD, SCALED)                                      \
+    do {                                                                   \
+        if (mode == kSgdPlain) HBT_SGD_WB(PD, GD, SCALED, kSgdPlain);      \
+        else if (mode == kSgdFirst) HBT_SGD_WB(PD, GD, SCALED, kSgdFirst); \
+        else HBT_SGD_WB(PD, GD, SCALED, kSgdMomentum);                     \
+    } while (0)
+#define HBT_SGD_SCALED(PD, GD)                   \
+    do {                                         \
+        if (scaled) HBT_SGD_MODES(PD, GD, true); \
+        else HBT_SGD_MODES(PD, GD, false);       \
+    } while (0)
+        if (param_dtype == F32 && grad_dtype == F32) HBT_SGD_SCALED(F32, F32);
+        else if (param_dtype == F32) HBT_SGD_SCALED(F32, BF16);
+        else if (param_dtype == BF16) HBT_SGD_SCALED(BF16, BF16);
+        else HBT_SGD_SCALED(F16, F16);
+#undef HBT_SGD_SCALED
 #undef HBT_SGD_MODES
-#undef HBT_SGD_LAUNCH
-    return check_launch("hbt_sgd_step");
+#undef HBT_SGD_WB
+#undef HBT_SGD
+    });
 }
 
 }  // extern "C"
-

@@ -56,9 +56,21 @@ extern "C" {
 const char* hbt_last_error(void) { return hbt::g_last_error.c_str(); }
 
 // Bumped whenever an exported signature or a table layout changes.
-int32_t hbt_abi_version(void) { return 11; }
+int32_t hbt_abi_version(void) { return 12; }
 
 // Entry points declared in include/hbt.h (hbt_last_error .. hbt_scale_inplace).
-int32_t hbt_symbol_count(void) { return 15; }
+int32_t hbt_symbol_count(void) { return 16; }
+
+int64_t hbt_grid_slices(int64_t blocks, int32_t threads, int64_t* first, int64_t* count, int64_t capacity) {
+    if (threads <= 0) return -1;
+    const int64_t slices = hbt::grid_slice_count(blocks, threads);
+    const int64_t per = hbt::grid_max_blocks(threads);
+    for (int64_t k = 0; k < slices && k < capacity; ++k) {
+        const int64_t start = k * per;
+        if (first != nullptr) first[k] = start;
+        if (count != nullptr) count[k] = blocks - start < per ? blocks - start : per;
+    }
+    return slices;
+}
 
 }  // extern "C"

@@ -29,6 +29,8 @@ __all__ = [
     "ACCUMULATE_ASSIGN",
     "COPY_ALIGNED",
     "COPY_CONVERSIONS",
+    "OPTIMIZER_DTYPES",
+    "STEP_WRITE_GRAD",
     "COPY_OP_COPY",
     "COPY_OP_DIVIDE",
     "SGD_FIRST_STEP",
@@ -53,7 +55,7 @@ __all__ = [
     "stream_of",
 ]
 
-ABI_VERSION = 11
+ABI_VERSION = 12
 MAX_TENSORS_PER_LAUNCH = 16
 MAX_LOCAL_RANKS = 64
 
@@ -68,15 +70,21 @@ COPY_ALIGNED = 1
 ACCUMULATE_ASSIGN = 1
 _CODE_BYTES = {DTYPE_F32: 4, DTYPE_BF16: 2, DTYPE_F16: 2, DTYPE_F64: 8}
 
-#: Dtype pairs ``hbt_copy_intervals`` converts between (same-dtype copies are bit copies).
-COPY_CONVERSIONS = frozenset({
-    (torch.float32, torch.bfloat16), (torch.bfloat16, torch.float32),
-    (torch.float32, torch.float16), (torch.float16, torch.float32),
-})
+_FLOATS = (torch.float64, torch.float32, torch.bfloat16, torch.float16)
+#: Dtype pairs ``hbt_copy_intervals`` converts between (same-dtype copies are bit copies):
+#: every ordered pair of float64, float32, bfloat16 and float16, as ``Tensor.to`` converts.
+COPY_CONVERSIONS = frozenset((a, b) for a in _FLOATS for b in _FLOATS if a != b)
 SGD_MOMENTUM = 1
 SGD_FIRST_STEP = 2
 SGD_NESTEROV = 4
 SGD_WEIGHT_DECAY = 8
+#: hbt_adamw_step / hbt_sgd_step flag: store the unscaled, clipped gradient back.
+STEP_WRITE_GRAD = 16
+#: (parameter, gradient) dtype pairs the optimizer kernels update.
+OPTIMIZER_DTYPES = frozenset({
+    (torch.float32, torch.float32), (torch.float32, torch.bfloat16),
+    (torch.bfloat16, torch.bfloat16), (torch.float16, torch.float16),
+})
 
 _c_void_p = ctypes.c_void_p
 _c_i32 = ctypes.c_int32
@@ -92,18 +100,19 @@ EXPORTED_SYMBOLS: dict[str, tuple[object, tuple[object, ...]]] = {
     "hbt_last_error": (ctypes.c_char_p, ()),
     "hbt_abi_version": (_c_i32, ()),
     "hbt_symbol_count": (_c_i32, ()),
+    "hbt_grid_slices": (_c_i64, (_c_i64, _c_i32, _i64_array, _i64_array, _c_i64)),
     "hbt_adamw_step": (
         _c_i32,
         (
-            _ptr_array, _ptr_array, _ptr_array, _ptr_array, _i64_array, _c_i32, _c_i32,
+            _ptr_array, _ptr_array, _ptr_array, _ptr_array, _i64_array, _c_i32, _c_i32, _c_i32,
             _c_f32, _c_void_p, _c_f32, _c_f32, _c_f32, _c_f32, _c_f32, _c_f32, _c_f32,
-            _c_void_p,
+            _c_i32, _c_void_p,
         ),
     ),
     "hbt_sgd_step": (
         _c_i32,
         (
-            _ptr_array, _ptr_array, _ptr_array, _i64_array, _c_i32, _c_i32, _c_f32, _c_void_p,
+            _ptr_array, _ptr_array, _ptr_array, _i64_array, _c_i32, _c_i32, _c_i32, _c_f32, _c_void_p,
             _c_f32, _c_f32, _c_f32, _c_f32, _c_i32, _c_void_p,
         ),
     ),
@@ -128,11 +137,11 @@ EXPORTED_SYMBOLS: dict[str, tuple[object, tuple[object, ...]]] = {
     ),
     "hbt_grad_local_share": (
         _c_i32,
-        (_ptr_array, _c_i32, _c_i32, _c_i64, _c_i64, _c_i32, _c_i32, _c_f32, _c_void_p, _c_void_p),
+        (_ptr_array, _c_i32, _c_i32, _c_i64, _c_i64, _c_i32, _c_i32, _c_f32, _c_i32, _c_void_p, _c_void_p),
     ),
     "hbt_grad_local_share_sqnorm": (
         _c_i32,
-        (_ptr_array, _c_i32, _c_i32, _c_i64, _c_i64, _c_i32, _c_i32, _c_f32, _c_void_p, _c_void_p,
+        (_ptr_array, _c_i32, _c_i32, _c_i64, _c_i64, _c_i32, _c_i32, _c_f32, _c_i32, _c_void_p, _c_void_p,
          _c_void_p, _c_void_p),
     ),
     "hbt_scale_inplace": (

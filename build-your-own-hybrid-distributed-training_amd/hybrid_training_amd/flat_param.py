@@ -112,7 +112,7 @@ def _check_cast(src: torch.dtype, dst: torch.dtype, operation: str) -> None:
         raise UnsupportedFeatureError(
             format_error(
                 operation,
-                "the copy kernel converts only between float32 and bfloat16 or float16",
+                "the copy kernel converts only between float64, float32, bfloat16 and float16",
                 observed=f"{src} -> {dst}",
             )
         )
@@ -496,7 +496,8 @@ class FlatParamHandle:
     def reduce_scatter_gradient(
         self, grad_full: torch.Tensor, *, peer_grads: Sequence[torch.Tensor] | None = None
     ) -> torch.Tensor | None:
-        """This rank's fp32 gradient shard (``fsdp.py:704-769``), padding forced to 0.0.
+        """This rank's gradient shard in the master dtype (``fsdp.py:704-769``), padding
+        forced to 0.0.
 
         ``grad_full`` is this rank's padded full gradient.  With a group of size 1
         that is all there is; otherwise ``peer_grads`` must hold every rank's padded
@@ -504,7 +505,8 @@ class FlatParamHandle:
         The gradients are cast to the reduce dtype (float32, bfloat16, float16 or
         float64), and the AVG divide and the sum are rounded to it, as the reference's
         ops in that dtype are (``collectives.py:593-594``); the result is cast to the
-        fp32 master (exactly, or for float64 rounded to nearest even).
+        master dtype (float32, bfloat16 or float16) as ``Tensor.to`` casts.  With mixed
+        precision off, all three dtypes are the parameters' own (``fsdp.py:379-392``).
 
         Inside ``no_sync`` (:meth:`set_accumulate_without_reduction`) the gradients
         are accumulated in the reduce dtype instead and ``None`` is returned
@@ -513,12 +515,12 @@ class FlatParamHandle:
         ones and reduces the sums (``fsdp.py:747-749``).
         """
         if self._reduce_dtype not in (torch.float32, torch.bfloat16, torch.float16, torch.float64) \
-                or self._master_dtype != torch.float32:
+                or self._master_dtype not in (torch.float32, torch.bfloat16, torch.float16):
             raise UnsupportedFeatureError(
                 format_error(
                     "fsdp.reduce_scatter_gradient",
                     "the local-share kernel reduces in float32, bfloat16, float16 or float64 into a "
-                    "float32 master shard",
+                    "float32, bfloat16 or float16 master shard",
                     observed=f"reduce {self._reduce_dtype}, master {self._master_dtype}",
                 )
             )
@@ -561,8 +563,9 @@ class FlatParamHandle:
             source_rank = self._shard_group.local_rank
         valid = max(0, min(self._shard_numel, self._total_numel - local.start))
         divisor = float(group) if (self._config.average_gradients and group > 1) else 1.0
-        out = torch.empty(self._shard_numel, dtype=torch.float32, device=self._device)
-        chunk = 32768  # elements per norm partial (hbt_grad_local_share_sqnorm)
+        out = torch.empty(self._shard_numel, dtype=self._master_dtype, device=self._device)
+        # elements per norm partial: the norm pass's chunk for the master dtype
+        chunk = 32768 if self._master_dtype == torch.float32 else 65536
         valid_chunks = -(-valid // chunk)
         pad = self._shard_numel - valid
         partials = torch.empty(max(1, valid_chunks + -(-pad // chunk)), dtype=torch.float64, device=self._device)
@@ -578,6 +581,7 @@ class FlatParamHandle:
                 _native.dtype_code(grads[0].dtype),
                 _native.dtype_code(self._reduce_dtype),
                 divisor,
+                _native.dtype_code(self._master_dtype),
                 out.data_ptr(),
                 partials.data_ptr(),
                 tile_sums.data_ptr(),
@@ -591,7 +595,7 @@ class FlatParamHandle:
             segments[(0, valid)] = partials[:valid_chunks]
         if pad:
             segments[(valid, pad)] = partials[valid_chunks:]
-        setattr(out, NORM_PARTIALS_ATTR, NormPartials(out.data_ptr(), out._version, segments))
+        setattr(out, NORM_PARTIALS_ATTR, NormPartials(out.data_ptr(), out._version, segments, out.dtype))
         self._reduction_count += 1
         return out
 

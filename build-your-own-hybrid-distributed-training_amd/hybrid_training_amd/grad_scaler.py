@@ -8,12 +8,16 @@ is native:
 * ``unscale_`` multiplies each gradient by ``fp32(1/scale)`` in its own dtype
   (``hbt_scale_inplace``, as ``grad.mul_(inverse)`` does) and checks finiteness with
   one fp64 norm pass: the sum of squares is non-finite exactly when some element is.
-* With ``defer_unscale=True`` the multiply is not applied to ``.grad``; the factor
-  travels with each gradient tensor and the optimizer's norm pass and fused AdamW
-  pass apply it while they read the gradient, so a clipped, loss-scaled step costs
-  one norm pass and one update pass.  ``unscale_`` then returns a lazily evaluated
-  flag, and ``step`` takes the overflow decision from the optimizer's norm pass when
-  it covered the same gradients.
+* With ``defer_unscale=True`` the multiply is not applied to ``.grad`` here; the
+  factor travels with each gradient tensor and the optimizer's norm pass and fused
+  update pass apply it while they read the gradient, rounding the product to the
+  gradient's dtype as the in-place multiply would, so the results are bitwise those
+  of the in-place sequence and a clipped, loss-scaled step costs one norm pass and one
+  update pass.  ``unscale_`` then returns a lazily evaluated flag, and ``step`` takes
+  the overflow decision from the optimizer's norm pass when it covered the same
+  gradients.  An optimizer with in-place semantics (``defer_clip=False``) writes the
+  unscaled, clipped gradients back during its step, or, when the step is skipped,
+  here.
 
 The overflow decision is taken over this device's gradients only; the one-element
 MAX all-reduce that agrees on it across ranks (``grad_scaler.py:191-199``) is not
@@ -153,9 +157,9 @@ class GradScaler:
         for p in params:
             _native.require_device_tensor(p.grad, "grad_scaler.unscale_")
             _native.require_dense(p.grad, "grad_scaler.unscale_")
-            if p.grad.dtype not in (torch.float32, torch.bfloat16):
+            if p.grad.dtype not in (torch.float32, torch.bfloat16, torch.float16):
                 raise UnsupportedFeatureError(
-                    format_error("grad_scaler.unscale_", "gradients must be float32 or bfloat16",
+                    format_error("grad_scaler.unscale_", "gradients must be float32, bfloat16 or float16",
                                  observed=str(p.grad.dtype))
                 )
             groups.setdefault((p.grad.device, p.grad.dtype), []).append(p.grad)
@@ -208,6 +212,11 @@ class GradScaler:
         self._state.total_steps += 1
         self._skipped_on_last_step = found
         if found:
+            # The reference has already unscaled and clipped .grad in place when it skips
+            # (grad_scaler.py:181-186, sharded_optimizer.py:333-337); an optimizer that
+            # keeps those semantics but defers the multiplies to its step applies them now.
+            if getattr(optimizer, "clips_in_place", False):
+                optimizer.materialize_pending()
             self._state.skipped_steps += 1
             # The reference logs every skipped step (grad_scaler.py:229-236).
             _LOGGER.warning(

@@ -10,19 +10,30 @@ the reference's; what changes is where the arithmetic runs:
   on the device, so no host round trip sits between the norm and the update;
 * the update is ``hbt_adamw_step``, one pass that reads ``p, g, m, v`` once and
   writes ``p, m, v`` once, with torch's per-element arithmetic
-  (``torch/optim/adam.py:396-547``) reproduced exactly (see ``include/hbt.h``).
+  (``torch/optim/adam.py:396-547``) reproduced exactly (see ``include/hbt.h``), on
+  fp32 masters or, as torch runs it on bf16 / fp16 tensors, on 2-byte masters.
 
 The inner ``torch.optim.AdamW`` object is still built (``build_inner_optimizer``)
 and owns ``param_groups`` and ``state``, so ``state_dict``/``load_state_dict``,
 ``inner`` and learning-rate changes behave as in the reference; only its
 ``step`` is never called.
 
-Clip placement.  ``clip_grad_norm`` scales the gradients in place, exactly as the
-reference does, at the cost of one extra read and write of every gradient.  With
-``defer_clip=True`` the multiplier stays on the device and ``step()`` applies it
-inside the fused update instead; ``clip_and_step`` does the same in one call.
-The result is bitwise the same as clip-then-step, but ``.grad`` holds the
-unclipped values until ``step()`` runs.
+Clip placement.  The clip multiplier never leaves the device: ``clip_grad_norm``
+computes the norm and the multiplier, and the fused update pass applies it.  Every
+multiply is rounded to the gradient's dtype exactly as the reference's in-place
+``grad.mul_`` calls round it, so the parameters and state come out bitwise the same
+either way.  What differs is ``.grad``:
+
+* default (``defer_clip=False``, the reference's semantics): the update pass also
+  writes the clipped (and, with a deferred loss scale, unscaled) gradient back into
+  ``.grad``, so after ``step()`` the gradients hold exactly what the reference's
+  in-place clip leaves there, for one extra 4 B/element write instead of a separate
+  read-and-write pass.  Between ``clip_grad_norm()`` and ``step()`` ``.grad`` still
+  holds the unclipped values; :meth:`ShardedOptimizer.materialize_pending` applies the
+  clip in place at once for a caller that reads them in that window, and a loss scaler
+  that skips the step does so itself;
+* ``defer_clip=True``: the gradients are never written; ``.grad`` keeps the unclipped
+  values.  This saves the write-back (32 instead of 36 B/element per clipped step).
 """
 
 from __future__ import annotations
@@ -59,23 +70,24 @@ NORM_PARTIALS_ATTR = "_hbt_norm_partials"
 
 @dataclass
 class NormPartials:
-    """Unweighted fp32-gradient norm partials a producing kernel wrote for its output.
+    """Unweighted gradient norm partials a producing kernel wrote for its output.
 
     ``segments`` maps ``(offset, length)`` of the gradient to the partials of that
-    segment: one fp64 per 32768-element chunk from the segment's start, the layout of
-    ``hbt_grad_sqnorm_partials`` with weight 1, each summed in the producer's own
-    fixed order.  The record is valid while the gradient keeps the storage address
-    and version counter it had when the partials were written; any in-place change
-    invalidates it.
+    segment: one fp64 per norm chunk from the segment's start (32768 elements of an
+    fp32 gradient, 65536 of a 2-byte one), the layout of ``hbt_grad_sqnorm_partials``
+    with weight 1, each summed in the producer's own fixed order.  The record is valid
+    while the gradient keeps the storage address, version counter and dtype it had when
+    the partials were written; any in-place change invalidates it.
     """
 
     data_ptr: int
     version: int
     segments: dict[tuple[int, int], torch.Tensor]
+    dtype: torch.dtype = torch.float32
 
     def lookup(self, grad: torch.Tensor, offset: int, length: int) -> torch.Tensor | None:
         """The segment's partials if the record still describes ``grad``."""
-        if grad.data_ptr() != self.data_ptr or grad._version != self.version or grad.dtype != torch.float32:
+        if grad.data_ptr() != self.data_ptr or grad._version != self.version or grad.dtype != self.dtype:
             return None
         return self.segments.get((offset, length))
 
@@ -283,11 +295,11 @@ def gradient_norm_pass(
     batches: dict[tuple[torch.dtype, float], list[tuple[torch.Tensor, int, int, float]]] = {}
     for grad, offset, length, weight in segments:
         _native.require_device_tensor(grad, "optim.gradient_norm")
-        if grad.dtype not in (torch.float32, torch.bfloat16):
+        if grad.dtype not in (torch.float32, torch.bfloat16, torch.float16):
             raise UnsupportedFeatureError(
                 format_error(
                     "optim.gradient_norm",
-                    "gradients must be float32 or bfloat16",
+                    "gradients must be float32, bfloat16 or float16",
                     observed=str(grad.dtype),
                 )
             )
@@ -443,11 +455,11 @@ class _HostStatePipeline:
         self._staging: dict[tuple[int, int], torch.Tensor] = {}
         self.done: torch.cuda.Event | None = None
 
-    def _stage(self, slot: int, k: int, n: int) -> torch.Tensor:
-        buf = self._staging.get((slot, k))
+    def _stage(self, slot: int, k: int, n: int, dtype: torch.dtype) -> torch.Tensor:
+        buf = self._staging.get((slot, k, dtype))
         if buf is None or buf.numel() < n:
-            buf = torch.empty(n, dtype=torch.float32, device=self.device)
-            self._staging[(slot, k)] = buf
+            buf = torch.empty(n, dtype=dtype, device=self.device)
+            self._staging[(slot, k, dtype)] = buf
         return buf[:n]
 
     def run(self, device_param: torch.Tensor, host_param: torch.Tensor, host_states: list[torch.Tensor],
@@ -463,7 +475,7 @@ class _HostStatePipeline:
         for index, start in enumerate(range(0, total, self.chunk_elems)):
             n = min(self.chunk_elems, total - start)
             slot = index % self.slots
-            staged = [self._stage(slot, k, n) for k in range(len(flat_states))]
+            staged = [self._stage(slot, k, n, h.dtype) for k, h in enumerate(flat_states)]
             loaded = torch.cuda.Event()
             with torch.cuda.stream(self.upload):
                 if free[slot] is not None:
@@ -499,8 +511,11 @@ class ShardedOptimizer:
     """AdamW or SGD over this rank's shards with a global-norm clip, on HIP kernels.
 
     Same constructor, methods and properties as ``sharded_optimizer.py:244-499``.
-    ``defer_clip`` is the one addition (see the module docstring).  With
-    ``config.cpu_offload_state`` the master copies and the optimizer state live in
+    ``defer_clip`` is the one addition (see the module docstring).  Master parameters
+    are float32, bfloat16 or float16, as the reference's flat shards are (the
+    parameters' own dtype when mixed precision is off, ``fsdp.py:379-384``); 2-byte
+    masters take gradients of their own dtype, fp32 masters fp32 or bf16 gradients.
+    With ``config.cpu_offload_state`` the master copies and the optimizer state live in
     pinned host memory, as in the reference, and stream through the device each step
     (:class:`_HostStatePipeline`).  ``amsgrad`` and ``maximize`` have no kernel and
     raise :class:`UnsupportedFeatureError` rather than falling back to torch.
@@ -525,11 +540,11 @@ class ShardedOptimizer:
         _check_group(norm_group, "optim.ShardedOptimizer")
         for param in self._parameters:
             _native.require_device_tensor(param, "optim.ShardedOptimizer")
-            if param.dtype != torch.float32:
+            if param.dtype not in (torch.float32, torch.bfloat16, torch.float16):
                 raise UnsupportedFeatureError(
                     format_error(
                         "optim.ShardedOptimizer",
-                        "master parameters must be float32",
+                        "master parameters must be float32, bfloat16 or float16",
                         observed=str(param.dtype),
                     )
                 )
@@ -600,7 +615,12 @@ class ShardedOptimizer:
         )
         mul = self._pending_mul if self._pending_valid() else None
         if has_unscale or mul is not None:
+            # Scaling keeps every element's finiteness (a finite norm gives a finite
+            # multiplier), so the last norm pass's non-finite flag stays valid.
+            flag = self.last_nonfinite_flag()
             self._scale_grads(mul, unscale_attr=has_unscale)
+            if flag is not None:
+                self._last_check = (_grad_signature(self._parameters), flag)
         self._pending_mul = None
         self._pending_signature = None
 
@@ -623,32 +643,35 @@ class ShardedOptimizer:
         """Clip to a global L2 norm; return the pre-clip norm (0-dim fp64 device tensor).
 
         ``max_norm <= 0`` only computes the norm (``sharded_optimizer.py:310-338``).
+        The multiplier is applied by the next :meth:`step` (and, by default, written
+        back into ``.grad`` there; see the module docstring).
         """
         if self._pending_mul is not None:
             self.materialize_pending()
         result = self._norm(max_norm)
         if max_norm <= 0:
             return result.norm
-        if self._defer_clip:
-            self._pending_mul = result.grad_mul
-            self._pending_signature = _grad_signature(self._parameters)
-        else:
-            self._scale_grads(result.grad_mul, unscale_attr=True)
-            self._last_check = (_grad_signature(self._parameters), result.nonfinite)
+        self._pending_mul = result.grad_mul
+        self._pending_signature = _grad_signature(self._parameters)
         return result.norm
 
     def clip_and_step(self, max_norm: float) -> torch.Tensor:
-        """Norm pass, then one fused clip + AdamW pass; returns the pre-clip norm.
+        """``clip_grad_norm(max_norm)`` then ``step()``; returns the pre-clip norm.
 
-        Bitwise equal to ``clip_grad_norm(max_norm); step()``; ``.grad`` is left
-        unclipped.  Two kernels read the gradients: the norm (4 B/element) and the
-        update (28 B/element of p, g, m, v traffic).
+        Two kernels read the gradients: the norm (4 B/element for fp32) and the fused
+        update (28 B/element of p, g, m, v traffic, plus the 4 B/element write-back
+        of the clipped gradient unless ``defer_clip`` is set).
         """
-        if self._pending_mul is not None:
-            self.materialize_pending()
-        result = self._norm(max_norm)
-        self._run_step(result.grad_mul if max_norm > 0 else None)
-        return result.norm
+        norm = self.clip_grad_norm(max_norm)
+        self.step()
+        return norm
+
+    @property
+    def clips_in_place(self) -> bool:
+        """Whether ``.grad`` ends up clipped (and unscaled) as the reference leaves it:
+        ``defer_clip=False``.  A loss scaler that skips the step materialises a pending
+        clip on such an optimizer (:meth:`materialize_pending`)."""
+        return not self._defer_clip
 
     def last_nonfinite_flag(self) -> torch.Tensor | None:
         """Device flag from the latest norm pass, if the gradients have not changed since."""
@@ -664,10 +687,21 @@ class ShardedOptimizer:
         self._run_step(mul)
 
     def _run_step(self, grad_mul: torch.Tensor | None) -> None:
+        # With in-place semantics the update pass writes the scaled gradient back: the
+        # clip, and a loss-scale factor deferred by the scaler, land in .grad as the
+        # reference's in-place multiplies would leave them.
+        write_back = not self._defer_clip
         if isinstance(self._optimizer, torch.optim.SGD):
-            self._run_sgd_step(grad_mul)
+            self._run_sgd_step(grad_mul, write_back)
         else:
-            self._run_adamw_step(grad_mul)
+            self._run_adamw_step(grad_mul, write_back)
+        if write_back:
+            written = [p.grad for p in self._parameters if p.grad is not None]
+            if written and (grad_mul is not None or any(_pending_unscale(g) != 1.0 for g in written)):
+                increment_version(written)
+            for g in written:
+                if hasattr(g, PENDING_UNSCALE_ATTR):
+                    delattr(g, PENDING_UNSCALE_ATTR)
         self._pending_mul = None
         self._pending_signature = None
 
@@ -693,15 +727,18 @@ class ShardedOptimizer:
                     observed=tuple(grad.shape),
                 )
             )
-        if grad.dtype not in (torch.float32, torch.bfloat16):
+        if (p.dtype, grad.dtype) not in _native.OPTIMIZER_DTYPES:
             raise UnsupportedFeatureError(
                 format_error("optim.ShardedOptimizer.step",
-                             "gradients must be float32 or bfloat16", observed=str(grad.dtype))
+                             "the update kernels take fp32 or bf16 gradients on fp32 masters, and "
+                             "gradients of the master's own dtype on bf16 / fp16 masters",
+                             observed=f"parameter {p.dtype}, gradient {grad.dtype}")
             )
         return grad
 
-    def _run_adamw_step(self, grad_mul: torch.Tensor | None) -> None:
+    def _run_adamw_step(self, grad_mul: torch.Tensor | None, write_back: bool) -> None:
         lib = _native.library()
+        flags = _native.STEP_WRITE_GRAD if write_back else 0
         batches: dict[tuple, list[nn.Parameter]] = {}
         for group in self._optimizer.param_groups:
             lr = float(group["lr"])
@@ -738,15 +775,15 @@ class ShardedOptimizer:
                     eps,
                     -step_size,
                 )
-                key = (scalars, grad.dtype, _pending_unscale(grad))
+                key = (scalars, p.dtype, grad.dtype, _pending_unscale(grad))
                 batches.setdefault(key, []).append(p)
         stream = _native.stream_of(self._device)
         mul_ptr = None if grad_mul is None else grad_mul.data_ptr()
         with torch.cuda.device(self._device):
-            for (scalars, gdtype, unscale), params in batches.items():
+            for (scalars, pdtype, gdtype, unscale), params in batches.items():
                 if self._pipeline is not None:
                     for p in params:
-                        self._offloaded_adamw(lib, p, scalars, gdtype, unscale, mul_ptr)
+                        self._offloaded_adamw(lib, p, scalars, pdtype, gdtype, unscale, mul_ptr, flags)
                     continue
                 for start in range(0, len(params), _native.MAX_TENSORS_PER_LAUNCH):
                     chunk = params[start : start + _native.MAX_TENSORS_PER_LAUNCH]
@@ -758,10 +795,12 @@ class ShardedOptimizer:
                         _native.pointer_array([s["exp_avg_sq"].data_ptr() for s in states]),
                         _native.int64_array([p.numel() for p in chunk]),
                         len(chunk),
+                        _native.dtype_code(pdtype),
                         _native.dtype_code(gdtype),
                         unscale,
                         mul_ptr,
                         *scalars,
+                        flags,
                         stream,
                     )
                     _native.check(status, "optim.hbt_adamw_step")
@@ -782,26 +821,29 @@ class ShardedOptimizer:
             return _pinned_like(p).zero_()
         return torch.zeros_like(p, memory_format=torch.preserve_format)
 
-    def _offloaded_adamw(self, lib, host_p, scalars, gdtype, unscale, mul_ptr) -> None:
+    def _offloaded_adamw(self, lib, host_p, scalars, pdtype, gdtype, unscale, mul_ptr, flags) -> None:
         """AdamW on the device parameter with its host-resident state streamed through."""
         dev = self._device_param[id(host_p)]
         grad = dev.grad
         state = self._optimizer.state[host_p]
         stream = _native.stream_of(self._device)
         gsize = grad.element_size()
+        psize = dev.element_size()
 
         def launch(start: int, n: int, staged: list[torch.Tensor]) -> None:
             status = lib.hbt_adamw_step(
-                _native.pointer_array([dev.data_ptr() + 4 * start]),
+                _native.pointer_array([dev.data_ptr() + psize * start]),
                 _native.pointer_array([grad.data_ptr() + gsize * start]),
                 _native.pointer_array([staged[0].data_ptr()]),
                 _native.pointer_array([staged[1].data_ptr()]),
                 _native.int64_array([n]),
                 1,
+                _native.dtype_code(pdtype),
                 _native.dtype_code(gdtype),
                 unscale,
                 mul_ptr,
                 *scalars,
+                flags,
                 stream,
             )
             _native.check(status, "optim.hbt_adamw_step")
@@ -809,9 +851,10 @@ class ShardedOptimizer:
         self._pipeline.run(dev, host_p, [state["exp_avg"], state["exp_avg_sq"]], True, launch)
         increment_version([dev, host_p, state["exp_avg"], state["exp_avg_sq"]])
 
-    def _run_sgd_step(self, grad_mul: torch.Tensor | None) -> None:
+    def _run_sgd_step(self, grad_mul: torch.Tensor | None, write_back: bool) -> None:
         """torch.optim.SGD's step (``torch/optim/sgd.py``) as one fused kernel per batch."""
         lib = _native.library()
+        write_flag = _native.STEP_WRITE_GRAD if write_back else 0
         batches: dict[tuple, list[nn.Parameter]] = {}
         for group in self._optimizer.param_groups:
             lr = float(group["lr"])
@@ -838,17 +881,18 @@ class ShardedOptimizer:
                         flags |= _native.SGD_FIRST_STEP
                     else:
                         _native.require_dense(state["momentum_buffer"], "optim.ShardedOptimizer.step")
-                # Scalars exactly as torch forms them: Python doubles, rounded to fp32.
+                # Scalars exactly as torch forms them: Python doubles, rounded to fp32 (and
+                # each alpha to a 2-byte parameter dtype inside the kernel's entry point).
                 scalars = (weight_decay, momentum, 1 - dampening, -lr)
-                key = (scalars, flags, grad.dtype, _pending_unscale(grad))
+                key = (scalars, flags | write_flag, p.dtype, grad.dtype, _pending_unscale(grad))
                 batches.setdefault(key, []).append(p)
         stream = _native.stream_of(self._device)
         mul_ptr = None if grad_mul is None else grad_mul.data_ptr()
         with torch.cuda.device(self._device):
-            for (scalars, flags, gdtype, unscale), params in batches.items():
+            for (scalars, flags, pdtype, gdtype, unscale), params in batches.items():
                 if self._pipeline is not None:
                     for p in params:
-                        self._offloaded_sgd(lib, p, scalars, flags, gdtype, unscale, mul_ptr)
+                        self._offloaded_sgd(lib, p, scalars, flags, pdtype, gdtype, unscale, mul_ptr)
                     continue
                 for start in range(0, len(params), _native.MAX_TENSORS_PER_LAUNCH):
                     chunk = params[start : start + _native.MAX_TENSORS_PER_LAUNCH]
@@ -860,6 +904,7 @@ class ShardedOptimizer:
                         _native.pointer_array([b.data_ptr() for b in buffers]) if buffers else None,
                         _native.int64_array([p.numel() for p in chunk]),
                         len(chunk),
+                        _native.dtype_code(pdtype),
                         _native.dtype_code(gdtype),
                         unscale,
                         mul_ptr,
@@ -872,22 +917,24 @@ class ShardedOptimizer:
                     if buffers:
                         increment_version(buffers)
 
-    def _offloaded_sgd(self, lib, host_p, scalars, flags, gdtype, unscale, mul_ptr) -> None:
+    def _offloaded_sgd(self, lib, host_p, scalars, flags, pdtype, gdtype, unscale, mul_ptr) -> None:
         """SGD on the device parameter with its host-resident momentum buffer streamed through."""
         dev = self._device_param[id(host_p)]
         grad = dev.grad
         stream = _native.stream_of(self._device)
         gsize = grad.element_size()
+        psize = dev.element_size()
         momentum = bool(flags & _native.SGD_MOMENTUM)
         host_states = [self._optimizer.state[host_p]["momentum_buffer"]] if momentum else []
 
         def launch(start: int, n: int, staged: list[torch.Tensor]) -> None:
             status = lib.hbt_sgd_step(
-                _native.pointer_array([dev.data_ptr() + 4 * start]),
+                _native.pointer_array([dev.data_ptr() + psize * start]),
                 _native.pointer_array([grad.data_ptr() + gsize * start]),
                 _native.pointer_array([staged[0].data_ptr()]) if staged else None,
                 _native.int64_array([n]),
                 1,
+                _native.dtype_code(pdtype),
                 _native.dtype_code(gdtype),
                 unscale,
                 mul_ptr,

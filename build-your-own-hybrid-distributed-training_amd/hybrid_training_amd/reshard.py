@@ -196,8 +196,9 @@ def read_tensor_range(
 ) -> torch.Tensor:
     """Elements ``wanted`` of a stored tensor as a new 1-D device tensor (one launch).
 
-    ``dtype`` casts the result (float32 <-> bfloat16 or float16); by default the result has the
-    first intersecting shard's dtype.
+    ``dtype`` casts the result as ``Tensor.to`` does (``checkpoint/reshard.py:290``), between any
+    of float64, float32, bfloat16 and float16; by default the result has the first
+    intersecting shard's dtype.
     """
     if wanted.length == 0:
         device = next(

@@ -31,8 +31,8 @@ extern "C" {
 /* ---- element types ----------------------------------------------------------- */
 #define HBT_DTYPE_F32 0
 #define HBT_DTYPE_BF16 1
-#define HBT_DTYPE_F16 2 /* copies, F32 <-> F16 casts and division; local-share, reduce and accumulate dtype */
-#define HBT_DTYPE_F64 3 /* byte copies; local-share reduce dtype and accumulate dtype */
+#define HBT_DTYPE_F16 2
+#define HBT_DTYPE_F64 3 /* copies and conversions; local-share reduce dtype and accumulate dtype */
 
 /* ---- per-call limits ---------------------------------------------------------- */
 #define HBT_MAX_TENSORS_PER_LAUNCH 16 /* AdamW / norm tables; the host splits larger lists */
@@ -46,6 +46,14 @@ int32_t hbt_abi_version(void);
 /* Number of HBT_* entry points exported (used by the loader's symbol check). */
 int32_t hbt_symbol_count(void);
 
+/* How the library splits a grid of `blocks` workgroups of `threads` lanes into launches:
+ * a HIP grid dimension holds at most 2^32 - 1 work-items, so each launch takes at most
+ * floor((2^32 - 1) / threads) workgroups.  Writes the first block and the block count of
+ * up to `capacity` slices to first[] / count[] (either may be NULL) and returns the number
+ * of slices (0 for blocks <= 0, -1 for threads <= 0).  Every kernel launch in the library
+ * goes through this split, so no request is refused for its size alone. */
+int64_t hbt_grid_slices(int64_t blocks, int32_t threads, int64_t* first, int64_t* count, int64_t capacity);
+
 /* ------------------------------------------------------------------------------
  * Fused gradient-clip + AdamW step over up to HBT_MAX_TENSORS_PER_LAUNCH tensors.
  *
@@ -56,28 +64,39 @@ int32_t hbt_symbol_count(void);
  *   (optim/sharded_optimizer.py:333-337) and, for loss-scaled gradients, the
  *   unscale multiply of GradScaler.unscale_ (optim/grad_scaler.py:181-186).
  *
- * Per element, in this order and in fp32 (each step rounded once):
- *   g  = g_in * unscale            (skipped when unscale == 1)
- *   g  = g * (*grad_mul)           (grad_mul: device fp32 written by
+ * Dtypes (param_dtype for params, exp_avgs and exp_avg_sqs; grad_dtype for grads):
+ * (F32, F32), (F32, BF16), (BF16, BF16) or (F16, F16).  Per element, in this order,
+ * every operation computed in fp32 and rounded once; R_G rounds to the gradient's
+ * dtype and R_P to the parameter's (both the identity for fp32):
+ *   g  = R_G(g_in * unscale)       (skipped when unscale == 1)
+ *   g  = R_G(g * (*grad_mul))      (grad_mul: device fp32 written by
  *                                   hbt_grad_norm_finalize, or NULL for 1)
- *   p  = p * decay                 (decay = fp32(1 - lr*weight_decay))
- *   m  = fma(w, g - m, m)          if |w| < 0.5, else fma(w - 1, g - m, g)
+ *   p  = R_P(p * decay)            (decay = fp32(1 - lr*weight_decay))
+ *   m  = R_P(fma(w, g - m, m))     if |w| < 0.5, else R_P(fma(w - 1, g - m, g))
  *                                  (w = fp32(1 - beta1); lerp in its fused form)
- *   v  = v * beta2
- *   v  = fma(one_minus_beta2 * g, g, v)
- *   p  = p + (neg_step_size * m) / (sqrt(v) / bias_correction2_sqrt + eps)
- * sqrt and both divisions are correctly rounded.  The host computes the scalars in
- * double exactly as torch does and rounds them to fp32.
+ *   v  = R_P(v * beta2)
+ *   v  = R_P(fma(one_minus_beta2 * g, g, v))
+ *   d  = sqrt(v) / bias_correction2_sqrt + eps                      (fp32 parameters)
+ *   d  = R_P(R_P(R_P(sqrt(v)) / bias_correction2_sqrt) + R_P(eps))  (2-byte parameters)
+ *   p  = R_P(p + (neg_step_size * m) / d)
+ * Each R_G is the gradient's in-place grad.mul_ of the reference, and each R_P one torch
+ * CPU op on a tensor of the parameter dtype (torch rounds the scalar of add_(eps) to
+ * that dtype).  sqrt and the divisions are correctly rounded.  The host computes the
+ * scalars in double exactly as torch does and rounds them to fp32.
  *
- * grad_dtype is HBT_DTYPE_F32 or HBT_DTYPE_BF16 (bf16 gradients are widened
- * exactly to fp32 before the unscale multiply).  params/exp_avgs/exp_avg_sqs are
- * fp32.  Each tensor i has numels[i] elements; numels[i] may be 0.
+ * flags: 0, or HBT_STEP_WRITE_GRAD to store the scaled gradient g back into grads[i]
+ * (in its own dtype) whenever a multiply changed it, i.e. when unscale != 1 or
+ * *grad_mul != 1.  That is the reference's in-place clip (and unscale) folded into the
+ * update pass: one read and one write of g instead of a separate scaling pass.
+ * Each tensor i has numels[i] elements; numels[i] may be 0.
  * ---------------------------------------------------------------------------- */
-int32_t hbt_adamw_step(float* const* params, const void* const* grads, float* const* exp_avgs,
-                       float* const* exp_avg_sqs, const int64_t* numels, int32_t count,
-                       int32_t grad_dtype, float unscale, const float* grad_mul, float decay,
-                       float lerp_weight, float beta2, float one_minus_beta2,
-                       float bias_correction2_sqrt, float eps, float neg_step_size, void* stream);
+#define HBT_STEP_WRITE_GRAD 16
+int32_t hbt_adamw_step(void* const* params, void* const* grads, void* const* exp_avgs,
+                       void* const* exp_avg_sqs, const int64_t* numels, int32_t count,
+                       int32_t param_dtype, int32_t grad_dtype, float unscale, const float* grad_mul,
+                       float decay, float lerp_weight, float beta2, float one_minus_beta2,
+                       float bias_correction2_sqrt, float eps, float neg_step_size, int32_t flags,
+                       void* stream);
 
 /* ------------------------------------------------------------------------------
  * Fused gradient-clip + SGD step over up to HBT_MAX_TENSORS_PER_LAUNCH tensors.
@@ -86,36 +105,40 @@ int32_t hbt_adamw_step(float* const* params, const void* const* grads, float* co
  *   torch.optim.SGD built at optim/sharded_optimizer.py:121-126 ->
  *   torch/optim/sgd.py (_single_tensor_sgd), preceded by the clip and unscale
  *   multiplies as in hbt_adamw_step.
- * Per element, in fp32, with fma() a single rounding as torch's CPU `add(.., alpha=)`:
- *   g = (g_in * unscale) * (*grad_mul)          (unscale skipped when 1; grad_mul NULL = 1)
- *   if HBT_SGD_WEIGHT_DECAY:  g = fma(p, weight_decay, g)
+ * Dtypes as for hbt_adamw_step (momentum_buffers in param_dtype).  Per element, with
+ * fma() a single rounding as torch's CPU `add(.., alpha=)`, R_G / R_P as above, and
+ * a(x) = R_P(x): torch rounds every alpha to the parameter dtype first:
+ *   g = R_G(R_G(g_in * unscale) * (*grad_mul))   (unscale skipped when 1; grad_mul NULL = 1)
+ *   if HBT_SGD_WEIGHT_DECAY:  g = R_P(fma(p, a(weight_decay), g))
  *   if HBT_SGD_MOMENTUM:
  *       if HBT_SGD_FIRST_STEP: buf = g
- *       else:                  buf = fma(g, one_minus_dampening, buf * momentum)
- *       g = HBT_SGD_NESTEROV ? fma(buf, momentum, g) : buf
- *   p = fma(g, neg_lr, p)
+ *       else:                  buf = R_P(fma(g, a(one_minus_dampening), R_P(buf * momentum)))
+ *       g = HBT_SGD_NESTEROV ? R_P(fma(buf, a(momentum), g)) : buf
+ *   p = R_P(fma(g, a(neg_lr), p))
  * momentum_buffers may be NULL without HBT_SGD_MOMENTUM.  Flags other than the four
- * below, or FIRST_STEP / NESTEROV without MOMENTUM, are rejected.
+ * below and HBT_STEP_WRITE_GRAD (as for hbt_adamw_step), or FIRST_STEP / NESTEROV
+ * without MOMENTUM, are rejected.
  * ---------------------------------------------------------------------------- */
 #define HBT_SGD_MOMENTUM 1
 #define HBT_SGD_FIRST_STEP 2
 #define HBT_SGD_NESTEROV 4
 #define HBT_SGD_WEIGHT_DECAY 8
-int32_t hbt_sgd_step(float* const* params, const void* const* grads, float* const* momentum_buffers,
-                     const int64_t* numels, int32_t count, int32_t grad_dtype, float unscale,
-                     const float* grad_mul, float weight_decay, float momentum, float one_minus_dampening,
-                     float neg_lr, int32_t flags, void* stream);
+int32_t hbt_sgd_step(void* const* params, void* const* grads, void* const* momentum_buffers,
+                     const int64_t* numels, int32_t count, int32_t param_dtype, int32_t grad_dtype,
+                     float unscale, const float* grad_mul, float weight_decay, float momentum,
+                     float one_minus_dampening, float neg_lr, int32_t flags, void* stream);
 
 /* ------------------------------------------------------------------------------
  * Deterministic squared L2 norm, stage 1: per-block fp64 partial sums.
  *
  * Replaces: NormContribution.squared_norm (optim/sharded_optimizer.py:145-158)
  *   summed by distributed_gradient_norm (optim/sharded_optimizer.py:236-238).
- * Computes sum_i weights[i] * sum_j (double)(g_ij * unscale)^2 over up to
- * HBT_MAX_TENSORS_PER_LAUNCH gradient tensors (grad_dtype F32 or BF16), writing
- * hbt_norm_partials_count(numels, count, grad_dtype) doubles to partials: one per
- * chunk of consecutive elements of one tensor (32768 fp32 or 65536 bf16), already
- * multiplied by that tensor's weight.  The chunk -> partial map and every summation order depend only on the
+ * Computes sum_i weights[i] * sum_j (double)(R_G(g_ij * unscale))^2 over up to
+ * HBT_MAX_TENSORS_PER_LAUNCH gradient tensors (grad_dtype F32, BF16 or F16; R_G rounds
+ * the unscaled value to that dtype, as the in-place unscale would have stored it),
+ * writing hbt_norm_partials_count(numels, count, grad_dtype) doubles to partials: one
+ * per chunk of consecutive elements of one tensor (32768 fp32 or 65536 bf16/fp16),
+ * already multiplied by that tensor's weight.  The chunk -> partial map and every summation order depend only on the
  * numels, so the result is bitwise reproducible.  A non-finite element makes the
  * sum non-finite, which is the overflow signal of GradScaler._detect_non_finite
  * (optim/grad_scaler.py:189-200).
@@ -185,17 +208,22 @@ int32_t hbt_grad_norm_noalloc(const void* const* grads, const int64_t* numels, c
  *   { src_address (0 => write zeros), dst_address, numel, first_chunk }
  * where first_chunk is the exclusive prefix sum over records of
  * ceil(numel / hbt_copy_chunk_elems(src_dtype, dst_dtype)), and total_chunks is the
- * sum.  A chunk is 1 KB of source: 256 elements of a 4-byte source, 512 of a 2-byte
- * one; hbt_copy_chunk_elems returns -1 for a pair the kernel does not move (8-byte data
- * travels as F32 pairs).  All records share src_dtype/dst_dtype and op:
+ * sum.  A chunk is 1 KB of source: 128 elements of an 8-byte source, 256 of a 4-byte
+ * one, 512 of a 2-byte one; hbt_copy_chunk_elems returns -1 for F64 -> F64 (a same-dtype
+ * 8-byte copy travels as F32 dword pairs) and for unknown dtypes.  All records share src_dtype/dst_dtype and op:
  *   HBT_COPY_OP_COPY    dst = src               (same dtype: byte copy; F32->BF16
  *                                                rounds to nearest even, NaN -> 0x7FC0;
  *                                                F32->F16 rounds to nearest even, overflows
  *                                                to inf, keeps subnormals, NaN -> sign|0x7E00;
  *                                                BF16->F32 and F16->F32 widen exactly)
+ *                                               F64 -> F32/BF16/F16 and BF16 <-> F16 convert
+ *                                                as torch's Tensor.to does: through the exact
+ *                                                or nearest-even fp32 value, then to nearest
+ *                                                even in the 2-byte dtype; F32/BF16/F16 -> F64
+ *                                                widen exactly)
  *   HBT_COPY_OP_DIVIDE  dst = src / divisor     (true fp32 division, in fp32 for F32, BF16
- *                                                and F16 data, result rounded to dst_dtype)
- * BF16 <-> F16 is not converted.
+ *                                                and F16 data, result rounded to dst_dtype;
+ *                                                not for F64 or BF16 <-> F16 pairs)
  * Source and destination ranges of one call must not overlap.  Addresses need no
  * particular alignment.
  *
@@ -226,26 +254,28 @@ int32_t hbt_copy_intervals(const int64_t* table, int64_t count, int64_t total_ch
  * in_dtype F32, BF16 or F16) of one rank, all resident on this device.  Only elements
  * [rank*shard_numel, (rank+1)*shard_numel) of each are read, so a caller holding just
  * those slices (as the no_sync accumulator does) passes them with rank 0.  Writes the
- * fp32 shard of `rank`, reducing in `reduce_dtype` (F32, BF16 or F16), with R rounding
- * to it (round to nearest even; the identity for F32):
+ * shard of `rank` in out_dtype (the master dtype: F32, BF16 or F16), reducing in
+ * `reduce_dtype` (F32, BF16 or F16), with R rounding to it (round to nearest even; the
+ * identity for F32):
  *   x_q    = R(rank_grads[q][rank*shard_numel + i])   (the cast; none if in_dtype ==
  *                                                      reduce_dtype)
- *   out[i] = R(...R(R(x_0 / divisor) + R(x_1 / divisor)) + ... + R(x_{G-1} / divisor))
+ *   s      = R(...R(R(x_0 / divisor) + R(x_1 / divisor)) + ... + R(x_{G-1} / divisor))
  * in rank order, each quotient and sum computed in fp32 and rounded once, as torch's
- * ops in that dtype give (divisor = G for AVG, 1 for SUM); then the exact widening to
- * the fp32 master, and +0.0 for i >= valid_numel (the padding tail).  With
- * group_size == 1 this is the whole local share of one rank: cast to the reduce
- * dtype, AVG pre-divide, cast to the fp32 master dtype, zero padding.
+ * ops in that dtype give (divisor = G for AVG, 1 for SUM); then out[i] = s cast to
+ * out_dtype (round to nearest even; exact when it is as wide), and +0.0 for
+ * i >= valid_numel (the padding tail).  With group_size == 1 this is the whole local
+ * share of one rank: cast to the reduce dtype, AVG pre-divide, cast to the master
+ * dtype, zero padding.
  * reduce_dtype F64 (which also admits in_dtype F64, the float64 no_sync accumulator)
- * computes in double instead: out[i] = fp32(((x_0 / divisor + x_1 / divisor) + ...)),
- * each x_q widened exactly, each quotient and sum correctly rounded in double and the
- * sum rounded once to fp32 (round to nearest even), as torch's float64 ops and
- * Tensor.to give.
+ * computes in double instead: s = ((x_0 / divisor + x_1 / divisor) + ...), each x_q
+ * widened exactly, each quotient and sum correctly rounded in double, and s narrows to
+ * out_dtype as Tensor.to does (to fp32 rounding to nearest even, then to a 2-byte
+ * out_dtype), as torch's float64 ops give.
  * ---------------------------------------------------------------------------- */
 #define HBT_MAX_LOCAL_RANKS 64
 int32_t hbt_grad_local_share(const void* const* rank_grads, int32_t group_size, int32_t rank,
                              int64_t shard_numel, int64_t valid_numel, int32_t in_dtype,
-                             int32_t reduce_dtype, float divisor, float* out, void* stream);
+                             int32_t reduce_dtype, float divisor, int32_t out_dtype, void* out, void* stream);
 
 /* ------------------------------------------------------------------------------
  * FSDP gradient local share fused with the squared-norm partials of its output.
@@ -255,18 +285,19 @@ int32_t hbt_grad_local_share(const void* const* rank_grads, int32_t group_size, 
  *   (optim/sharded_optimizer.py:145-158) that the next clip_grad_norm runs.
  * Writes `out` exactly as hbt_grad_local_share does, and to `partials` the unweighted
  * squared norms of out's two segments, [0, valid_numel) then [valid_numel,
- * shard_numel), chunk by chunk: ceil(valid_numel / 32768) + ceil((shard_numel -
- * valid_numel) / 32768) doubles, one per 32768-element chunk from each segment's
- * start, in the layout hbt_grad_sqnorm_partials uses for those segments (F32, weight
- * 1, unscale 1), so a caller can stand them in for that pass.  Each is summed in a
+ * shard_numel), chunk by chunk: ceil(valid_numel / C) + ceil((shard_numel -
+ * valid_numel) / C) doubles, one per C-element chunk from each segment's start (C =
+ * 32768 for an F32 out_dtype, 65536 for a 2-byte one), in the layout
+ * hbt_grad_sqnorm_partials uses for those segments (out_dtype, weight 1, unscale 1), so
+ * a caller can stand them in for that pass.  Each is summed in a
  * fixed order (per 256-element tile, then per chunk), so it is reproducible, though
  * not bitwise the norm pass's own tree.  `tile_scratch` is caller-provided device
  * memory for ceil(shard_numel / 256) doubles.
  * ---------------------------------------------------------------------------- */
 int32_t hbt_grad_local_share_sqnorm(const void* const* rank_grads, int32_t group_size, int32_t rank,
                                     int64_t shard_numel, int64_t valid_numel, int32_t in_dtype,
-                                    int32_t reduce_dtype, float divisor, float* out, double* partials,
-                                    double* tile_scratch, void* stream);
+                                    int32_t reduce_dtype, float divisor, int32_t out_dtype, void* out,
+                                    double* partials, double* tile_scratch, void* stream);
 
 /* ------------------------------------------------------------------------------
  * FSDP no_sync gradient accumulation over up to HBT_MAX_TENSORS_PER_LAUNCH

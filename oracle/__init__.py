@@ -22,6 +22,7 @@ from collections.abc import Sequence
 import numpy as np
 
 __all__ = [
+    "DTYPE_CODES",
     "PINNED_BY",
     "adamw_scalars",
     "adamw_step",
@@ -30,6 +31,7 @@ __all__ = [
     "even_shards",
     "f32_to_bf16",
     "flat_layout",
+    "from_bits",
     "library",
     "local_share",
     "no_sync_accumulate",
@@ -38,6 +40,7 @@ __all__ = [
     "round_to",
     "sgd_step",
     "sqnorm",
+    "to_bits",
     "unpack_full",
 ]
 
@@ -83,26 +86,20 @@ def library() -> ctypes.CDLL:
         if not os.path.exists(_LIB_PATH):
             subprocess.run(["make", "-C", _HERE], check=True, capture_output=True)
         lib = ctypes.CDLL(_LIB_PATH)
-        f32p = ctypes.POINTER(ctypes.c_float)
-        u16p = ctypes.POINTER(ctypes.c_uint16)
-        lib.oracle_adamw_f32.restype = None
-        lib.oracle_adamw_f32.argtypes = [f32p, f32p, f32p, f32p, ctypes.c_int64] + [
-            ctypes.c_float
-        ] * 9 + [f32p]
-        lib.oracle_adamw_bf16grad.restype = None
-        lib.oracle_adamw_bf16grad.argtypes = [f32p, u16p, f32p, f32p, ctypes.c_int64] + [
-            ctypes.c_float
-        ] * 9
+        vp, f32p, u16p = ctypes.c_void_p, ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_uint16)
+        i64, ci, cf = ctypes.c_int64, ctypes.c_int, ctypes.c_float
+        lib.oracle_adamw.restype = None
+        lib.oracle_adamw.argtypes = [vp, vp, vp, vp, i64, ci, ci] + [cf] * 9 + [f32p, vp]
         lib.oracle_sgd.restype = None
-        lib.oracle_sgd.argtypes = [f32p, f32p, f32p, ctypes.c_int64, ctypes.c_float, ctypes.c_float,
-                                   ctypes.c_int, ctypes.c_float, ctypes.c_int, ctypes.c_float,
-                                   ctypes.c_float, ctypes.c_int, ctypes.c_float]
-        lib.oracle_sqnorm_f32.restype = ctypes.c_double
-        lib.oracle_sqnorm_f32.argtypes = [f32p, ctypes.c_int64, ctypes.c_float]
-        lib.oracle_sqnorm_bf16.restype = ctypes.c_double
-        lib.oracle_sqnorm_bf16.argtypes = [u16p, ctypes.c_int64, ctypes.c_float]
+        lib.oracle_sgd.argtypes = [vp, vp, vp, i64, ci, ci, cf, cf, ci, cf, ci, cf, cf, ci, cf, vp, ci]
+        lib.oracle_sqnorm.restype = ctypes.c_double
+        lib.oracle_sqnorm.argtypes = [vp, i64, ci, cf]
+        lib.oracle_round.restype = None
+        lib.oracle_round.argtypes = [f32p, f32p, i64, ci]
         lib.oracle_f32_to_bf16.restype = None
-        lib.oracle_f32_to_bf16.argtypes = [f32p, u16p, ctypes.c_int64]
+        lib.oracle_f32_to_bf16.argtypes = [f32p, u16p, i64]
+        lib.oracle_f32_to_f16.restype = None
+        lib.oracle_f32_to_f16.argtypes = [f32p, u16p, i64]
         _LIB = lib
     return _LIB
 
@@ -113,6 +110,41 @@ def _f32(a: np.ndarray) -> ctypes.POINTER(ctypes.c_float):
 
 def _u16(a: np.ndarray) -> ctypes.POINTER(ctypes.c_uint16):
     return a.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16))
+
+
+def _vp(a: np.ndarray | None) -> ctypes.c_void_p | None:
+    return None if a is None else ctypes.c_void_p(a.ctypes.data)
+
+
+#: Dtype names and the codes the C restatement (and libhbt.so) use for them.
+DTYPE_CODES = {"float32": 0, "bfloat16": 1, "float16": 2}
+
+
+def _storage(a: np.ndarray, dtype: str) -> None:
+    """``a`` holds ``dtype`` values: float32 values, or 2-byte bit patterns as uint16."""
+    expected = np.float32 if dtype == "float32" else np.uint16
+    assert a.dtype == expected and a.flags.c_contiguous, (a.dtype, dtype)
+
+
+def to_bits(x: np.ndarray, dtype: str) -> np.ndarray:
+    """fp32 values rounded to ``dtype`` (nearest even), as that dtype's storage: float32
+    values for ``"float32"``, uint16 bit patterns for ``"bfloat16"`` / ``"float16"``."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    if dtype == "float32":
+        return x.copy()
+    out = np.empty(x.shape, dtype=np.uint16)
+    fn = library().oracle_f32_to_bf16 if dtype == "bfloat16" else library().oracle_f32_to_f16
+    fn(_f32(x), _u16(out), x.size)
+    return out
+
+
+def from_bits(a: np.ndarray, dtype: str) -> np.ndarray:
+    """The fp32 values of ``dtype`` storage (exact widening)."""
+    if dtype == "float32":
+        return np.asarray(a, dtype=np.float32)
+    if dtype == "bfloat16":
+        return (np.asarray(a, np.uint16).astype(np.uint32) << 16).view(np.float32)
+    return np.asarray(a, np.uint16).view(np.float16).astype(np.float32)
 
 
 # ---------------------------------------------------------------------------------------
@@ -133,6 +165,14 @@ def adamw_scalars(
     return (decay, 1 - beta1, beta2, 1 - beta2, bias_correction2**0.5, eps, -step_size)
 
 
+def _grad_dtype(g: np.ndarray, dtype: str, grad_dtype: str | None) -> str:
+    if grad_dtype is not None:
+        return grad_dtype
+    if g.dtype == np.float32:
+        return "float32"
+    return "bfloat16" if dtype == "float32" else dtype
+
+
 def adamw_step(
     p: np.ndarray,
     g: np.ndarray,
@@ -143,20 +183,25 @@ def adamw_step(
     unscale: float = 1.0,
     grad_mul: float = 1.0,
     sqrt_override: np.ndarray | None = None,
+    dtype: str = "float32",
+    grad_dtype: str | None = None,
+    grad_out: np.ndarray | None = None,
 ) -> None:
-    """One AdamW step in place on fp32 ``p, m, v`` (``g`` fp32, or bf16 bits as uint16)."""
+    """One AdamW step in place on ``p, m, v`` of ``dtype`` (float32 arrays, or uint16 bit
+    patterns of bfloat16 / float16).  ``g`` is float32, or uint16 bits of ``grad_dtype``
+    (bfloat16 by default for fp32 parameters, else the parameters' dtype).  The unscale
+    and clip multiplies are rounded to the gradient's dtype; ``grad_out`` (the gradient's
+    storage dtype) receives the scaled gradient."""
+    gdt = _grad_dtype(g, dtype, grad_dtype)
     for a in (p, m, v):
-        assert a.dtype == np.float32 and a.flags.c_contiguous
-    n = p.size
-    lib = library()
-    if g.dtype == np.uint16:
-        assert sqrt_override is None
-        lib.oracle_adamw_bf16grad(_f32(p), _u16(g), _f32(m), _f32(v), n, unscale, grad_mul, *scalars)
-        return
-    assert g.dtype == np.float32
+        _storage(a, dtype)
+    g = np.ascontiguousarray(g)
+    _storage(g, gdt)
+    if grad_out is not None:
+        _storage(grad_out, gdt)
     override = None if sqrt_override is None else _f32(np.ascontiguousarray(sqrt_override, np.float32))
-    lib.oracle_adamw_f32(_f32(p), _f32(np.ascontiguousarray(g)), _f32(m), _f32(v), n, unscale, grad_mul,
-                         *scalars, override)
+    library().oracle_adamw(_vp(p), _vp(g), _vp(m), _vp(v), p.size, DTYPE_CODES[dtype], DTYPE_CODES[gdt],
+                           unscale, grad_mul, *scalars, override, _vp(grad_out))
 
 
 def sgd_step(
@@ -172,28 +217,41 @@ def sgd_step(
     first: bool = False,
     unscale: float = 1.0,
     grad_mul: float = 1.0,
+    dtype: str = "float32",
+    grad_dtype: str | None = None,
+    grad_out: np.ndarray | None = None,
+    remainder: bool = False,
 ) -> None:
-    """One SGD step in place on fp32 ``p`` (and ``buf``), torch's scalars rounded to fp32."""
-    assert p.dtype == np.float32 and p.flags.c_contiguous and g.dtype == np.float32
+    """One SGD step in place on ``p`` (and ``buf``) of ``dtype``; torch's scalars rounded
+    to fp32, and each alpha to ``dtype``.  Storage as for :func:`adamw_step`.
+    ``remainder`` gives the arithmetic of torch's scalar remainder loop on 2-byte tensors
+    (each alpha product rounded to ``dtype`` before the add) instead of its vectorised
+    body's, which the kernels follow."""
+    gdt = _grad_dtype(g, dtype, grad_dtype)
+    _storage(p, dtype)
+    g = np.ascontiguousarray(g)
+    _storage(g, gdt)
     mode = 0 if momentum == 0 else (1 if first else 2)
     if mode:
-        assert buf is not None and buf.dtype == np.float32 and buf.flags.c_contiguous
-    b = _f32(buf) if buf is not None else None
-    library().oracle_sgd(_f32(p), _f32(np.ascontiguousarray(g)), b, p.size, unscale, grad_mul,
-                         int(weight_decay != 0), weight_decay, mode, momentum, 1 - dampening,
-                         int(nesterov), -lr)
+        assert buf is not None
+        _storage(buf, dtype)
+    if grad_out is not None:
+        _storage(grad_out, gdt)
+    library().oracle_sgd(_vp(p), _vp(g), _vp(buf) if mode else None, p.size, DTYPE_CODES[dtype], DTYPE_CODES[gdt],
+                         unscale, grad_mul, int(weight_decay != 0), weight_decay, mode, momentum, 1 - dampening,
+                         int(nesterov), -lr, _vp(grad_out), int(remainder))
 
 
 # ---------------------------------------------------------------------------------------
 # norm and clip
 # ---------------------------------------------------------------------------------------
-def sqnorm(g: np.ndarray, *, unscale: float = 1.0) -> float:
-    """Compensated fp64 sum of squares of ``g * unscale`` (fp32, or bf16 bits as uint16)."""
+def sqnorm(g: np.ndarray, *, unscale: float = 1.0, dtype: str | None = None) -> float:
+    """Compensated fp64 sum of squares of ``R(g * unscale)``: ``g`` float32, or uint16 bits
+    of ``dtype`` (bfloat16 by default), the product rounded to that dtype."""
     g = np.ascontiguousarray(g)
-    if g.dtype == np.uint16:
-        return float(library().oracle_sqnorm_bf16(_u16(g), g.size, unscale))
-    assert g.dtype == np.float32
-    return float(library().oracle_sqnorm_f32(_f32(g), g.size, unscale))
+    gdt = "float32" if g.dtype == np.float32 else (dtype or "bfloat16")
+    _storage(g, gdt)
+    return float(library().oracle_sqnorm(_vp(g), g.size, DTYPE_CODES[gdt], unscale))
 
 
 def clip_multiplier(norm: float, max_norm: float) -> float:
@@ -207,10 +265,7 @@ def clip_multiplier(norm: float, max_norm: float) -> float:
 
 def f32_to_bf16(x: np.ndarray) -> np.ndarray:
     """bf16 bit patterns (uint16) of ``x`` rounded to nearest even, NaN -> 0x7FC0."""
-    x = np.ascontiguousarray(x, dtype=np.float32)
-    out = np.empty(x.shape, dtype=np.uint16)
-    library().oracle_f32_to_bf16(_f32(x), _u16(out), x.size)
-    return out
+    return to_bits(x, "bfloat16")
 
 
 # ---------------------------------------------------------------------------------------
@@ -276,11 +331,11 @@ def round_to(x: np.ndarray, reduce: str = "float32") -> np.ndarray:
     x = np.asarray(x, dtype=np.float32)
     if reduce == "float32":
         return x
-    if reduce == "bfloat16":
-        return (f32_to_bf16(x).astype(np.uint32) << 16).view(np.float32)
-    if reduce == "float16":
-        with np.errstate(over="ignore"):
-            return x.astype(np.float16).astype(np.float32)
+    if reduce in ("bfloat16", "float16"):
+        flat = np.ascontiguousarray(x).reshape(-1)
+        out = np.empty_like(flat)
+        library().oracle_round(_f32(flat), _f32(out), flat.size, DTYPE_CODES[reduce])
+        return out.reshape(x.shape)
     raise ValueError(f"unknown reduce dtype {reduce!r}")
 
 

@@ -278,10 +278,21 @@ def test_float16_specials_match_torch(device):
     assert torch.equal(wide.cpu().view(torch.int32), finite.cpu().to(torch.float32).view(torch.int32))
 
 
-def test_bf16_float16_conversion_is_refused(device):
-    a = torch.zeros(8, dtype=torch.bfloat16, device=device)
-    b = torch.zeros(8, dtype=torch.float16, device=device)
-    plan = _native.CopyPlan(device)
-    plan.add(a, 0, b, 0, 8)
-    with pytest.raises(Exception, match="convert"):
-        plan.run(src_dtype=torch.bfloat16, dst_dtype=torch.float16)
+def test_bf16_float16_conversions_are_tensor_to(device):
+    """bf16 <-> fp16 convert through the exact fp32 value, as ``Tensor.to`` does: round to
+    nearest even, fp16 overflow to +-inf, subnormals kept, signed zeros kept."""
+    gen = torch.Generator().manual_seed(6)
+    exps = torch.rand(20_011, generator=gen) * 60 - 30
+    values = torch.randn(20_011, generator=gen) * torch.pow(2.0, exps)
+    values[:8] = torch.tensor([0.0, -0.0, float("inf"), -float("inf"), 65504.0, 65520.0, 1e-7, 3e-8])
+    for src, dst in ((torch.bfloat16, torch.float16), (torch.float16, torch.bfloat16)):
+        a = values.to(src)
+        b = torch.full((a.numel() + 3,), 7.0, dtype=dst, device=device)
+        plan = _native.CopyPlan(device)
+        plan.add(a.to(device), 1, b, 3, a.numel() - 1)  # odd offsets on both sides
+        plan.run(src_dtype=src, dst_dtype=dst)
+        expect = a[1:].to(dst)
+        got = b[3 : 3 + expect.numel()].cpu()
+        assert torch.equal(got.view(torch.int16), expect.view(torch.int16)), (src, dst)
+        untouched = torch.cat([b[:3], b[3 + expect.numel() :]]).cpu()
+        assert torch.equal(untouched, torch.full((4,), 7.0, dtype=dst))

@@ -40,11 +40,24 @@ _REDUCE = {torch.float32: "float32", torch.bfloat16: "bfloat16", torch.float16: 
            torch.float64: "float64"}
 
 
+def _master_bits(t: torch.Tensor) -> np.ndarray:
+    """Raw bits of a float32 (int32 view) or 2-byte (uint16 view) tensor."""
+    t = t.detach().cpu().contiguous()
+    if t.dtype == torch.float32:
+        return t.view(torch.int32).numpy()
+    return t.view(torch.int16).numpy().view(np.uint16)
+
+
 @pytest.mark.parametrize("in_dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("group", [1, 3, 8])
 @pytest.mark.parametrize("misaligned", [False, True])
 @pytest.mark.parametrize("reduce", [torch.float32, torch.bfloat16, torch.float16, torch.float64])
-def test_local_share_tiles(device, in_dtype, group, misaligned, reduce):
+@pytest.mark.parametrize("master", [torch.float32, torch.bfloat16, torch.float16])
+def test_local_share_tiles(device, in_dtype, group, misaligned, reduce, master):
+    """The shard in every (input, reduce, master) dtype combination: the oracle's
+    reduce-dtype sum, cast to the master dtype as Tensor.to casts (``fsdp.py:763-764``)."""
+    if master != torch.float32 and (group == 3 or reduce == torch.float16 and in_dtype == torch.bfloat16):
+        pytest.skip("2-byte masters: a representative subset of the combinations")
     lib = _native.library()
     shard = 20_000
     gen = torch.Generator(device=device).manual_seed(group)
@@ -55,37 +68,40 @@ def test_local_share_tiles(device, in_dtype, group, misaligned, reduce):
                for _ in range(group)]
     grads = [s[lead:] for s in storage]
     host = [g.float().cpu().numpy() for g in grads]
-    out_storage = torch.full((shard + lead,), 7.0, device=device)
+    out_storage = torch.full((shard + lead,), 7.0, device=device, dtype=master)
     out = out_storage[lead:]
     divisor = float(group) if group > 1 else 1.0
+    master_name = _REDUCE[master]
     for rank in sorted({0, group - 1}):
         for valid in (shard, shard - 1537, 700, 0):
             status = lib.hbt_grad_local_share(
                 _native.pointer_array([g.data_ptr() for g in grads]), group, rank, shard, valid,
-                _native.dtype_code(in_dtype), _native.dtype_code(reduce), divisor,
+                _native.dtype_code(in_dtype), _native.dtype_code(reduce), divisor, _native.dtype_code(master),
                 ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(_native.stream_of(device)),
             )
             _native.check(status, "test.local_share")
-            expect = oracle.local_share(host, rank, shard, valid, divisor, _REDUCE[reduce])
-            assert np.array_equal(_bits(out), expect.view(np.int32)), (rank, valid)
+            expect32 = oracle.local_share(host, rank, shard, valid, divisor, _REDUCE[reduce])
+            expect = oracle.to_bits(expect32, master_name)
+            expect = expect.view(np.int32) if master == torch.float32 else expect
+            assert np.array_equal(_master_bits(out), expect), (rank, valid)
             # the fused entry point: the same shard, plus its squared-norm partials
-            chunk = 32768
+            chunk = 32768 if master == torch.float32 else 65536
             partials = torch.full((-(-valid // chunk) + -(-(shard - valid) // chunk) or 1,), 7.0,
                                   dtype=torch.float64, device=device)
             tile_sums = torch.empty(-(-shard // 256), dtype=torch.float64, device=device)
             out.fill_(7.0)
             status = lib.hbt_grad_local_share_sqnorm(
                 _native.pointer_array([g.data_ptr() for g in grads]), group, rank, shard, valid,
-                _native.dtype_code(in_dtype), _native.dtype_code(reduce), divisor,
+                _native.dtype_code(in_dtype), _native.dtype_code(reduce), divisor, _native.dtype_code(master),
                 ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(partials.data_ptr()),
                 ctypes.c_void_p(tile_sums.data_ptr()), ctypes.c_void_p(_native.stream_of(device)),
             )
             _native.check(status, "test.local_share_sqnorm")
-            assert np.array_equal(_bits(out), expect.view(np.int32)), (rank, valid)
-            ref = oracle.sqnorm(expect)
+            assert np.array_equal(_master_bits(out), expect), (rank, valid)
+            ref = oracle.sqnorm(oracle.from_bits(oracle.to_bits(expect32, master_name), master_name))
             got = float(partials.sum())
             assert abs(got - ref) <= 1e-12 * max(ref, 1e-300), (rank, valid, got, ref)
-    assert float(out_storage[:lead].sum()) == 7.0 * lead  # nothing written before the output
+    assert float(out_storage[:lead].float().sum()) == 7.0 * lead  # nothing written before the output
 
 
 def _scale_reference(t: torch.Tensor, unscale: float, mul: float) -> torch.Tensor:
@@ -151,7 +167,7 @@ def test_local_share_full_size_rank7_of_llama3_8b_w8(device):
     status = lib.hbt_grad_local_share_sqnorm(
         _native.pointer_array([g.data_ptr() for g in grads]), group, rank, shard, shard,
         _native.dtype_code(torch.bfloat16), _native.dtype_code(torch.float32), float(group),
-        ctypes.c_void_p(out.data_ptr()),
+        _native.dtype_code(torch.float32), ctypes.c_void_p(out.data_ptr()),
         ctypes.c_void_p(partials.data_ptr()), ctypes.c_void_p(tile_sums.data_ptr()),
         ctypes.c_void_p(_native.stream_of(device)),
     )

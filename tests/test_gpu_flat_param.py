@@ -245,16 +245,23 @@ def test_gradient_local_share_in_reduce_dtype_matches_oracle(device, group, in_d
 
 
 def test_reduce_and_master_dtype_limits(device):
-    """A non-fp32 master shard has no kernel: refused up front."""
+    """A bf16 master shard (mixed precision with ``master_dtype="bfloat16"``) packs and
+    reduces into bf16; a float64 master packs (the copy kernel converts into float64) but
+    its gradient has no local-share kernel, so the reduction refuses it up front."""
     named = _params(MLP_1857_REFERENCE, device)
     mp = MixedPrecisionConfig(enabled=True, master_dtype="bfloat16")
     h = FlatParamHandle(named, None, GroupHandle.trivial("shard"), FSDPConfig(), mp, device, keep_originals=True)
-    with pytest.raises(UnsupportedFeatureError, match="float16 or float64 into a float32 master"):
-        h.reduce_scatter_gradient(torch.zeros(h.padded_numel, device=device))
-    # A float64 master is refused earlier, when the fp32 parameters are packed into it.
+    assert h.flat_param.dtype == torch.bfloat16
+    flat = torch.cat([p.detach().reshape(-1) for _, p in named])
+    assert torch.equal(h.flat_param.detach()[: flat.numel()], flat.to(torch.bfloat16))
+    grad = torch.randn(h.padded_numel, device=device)
+    out = h.reduce_scatter_gradient(grad)
+    assert out.dtype == torch.bfloat16 and torch.equal(out, grad.to(torch.bfloat16))
     mp = MixedPrecisionConfig(enabled=True, reduce_dtype="float64", master_dtype="float64")
-    with pytest.raises(UnsupportedFeatureError, match="converts only between float32 and bfloat16 or float16"):
-        FlatParamHandle(named, None, GroupHandle.trivial("shard"), FSDPConfig(), mp, device, keep_originals=True)
+    h = FlatParamHandle(named, None, GroupHandle.trivial("shard"), FSDPConfig(), mp, device, keep_originals=True)
+    assert torch.equal(h.flat_param.detach()[: flat.numel()], flat.to(torch.float64))
+    with pytest.raises(UnsupportedFeatureError, match="float32, bfloat16 or float16 master shard"):
+        h.reduce_scatter_gradient(torch.zeros(h.padded_numel, device=device))
 
 
 def test_local_share_needs_every_rank(device):

@@ -266,7 +266,7 @@ def test_random_loss_scaled_runs(device, case):
     rng = np.random.default_rng(6000 + case)
     sizes = [int(rng.integers(1, 50000)) for _ in range(int(rng.integers(1, 6)))]
     bf16 = bool(rng.integers(0, 2))
-    defer = True if bf16 else bool(rng.integers(0, 2))
+    defer = bool(rng.integers(0, 2))
     interval = int(rng.integers(1, 4))
     max_norm = float(rng.choice([0.01, 1.0]))
     gen = torch.Generator(device=device).manual_seed(case)
@@ -299,6 +299,23 @@ def test_random_loss_scaled_runs(device, case):
         norm = float(opt.clip_grad_norm(max_norm))
         stepped = scaler.step(opt, params, already_unscaled=True)
         scaler.update()
+        # .grad as the reference leaves it (unscaled and clipped in place, the step taken
+        # or skipped), or untouched with deferred multipliers
+        mul = oracle.clip_multiplier(norm, max_norm)
+        for p, g in zip(params, host):
+            got = p.grad.detach().cpu()
+            got = got.view(torch.int16).numpy().view(np.uint16) if bf16 else got.numpy()
+            if defer:
+                want = g
+            else:
+                want = np.empty_like(g)
+                oracle.adamw_step(np.zeros(g.size, np.float32), g, np.zeros(g.size, np.float32),
+                                  np.zeros(g.size, np.float32), (1.0,) * 7, unscale=1.0 / scale, grad_mul=mul,
+                                  grad_out=want)
+            dt = "bfloat16" if bf16 else "float32"
+            nan = np.isnan(oracle.from_bits(want, dt))
+            assert np.array_equal(np.isnan(oracle.from_bits(got, dt)), nan), (context, step)
+            assert np.array_equal(got[~nan], want[~nan]), (context, step)
         opt.zero_grad(set_to_none=True)
         nonfinite = any(not torch.isfinite(g.float()).all() for g in grads)
         assert stepped == (not nonfinite), (context, step)
@@ -308,7 +325,6 @@ def test_random_loss_scaled_runs(device, case):
         else:
             taken += 1
             sc = oracle.adamw_scalars(lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1, step=float(taken))
-            mul = oracle.clip_multiplier(norm, max_norm)
             for a, g, m, v in zip(P, host, M, V):
                 oracle.adamw_step(a, g, m, v, sc, unscale=1.0 / scale, grad_mul=mul)
             tracker += 1

@@ -11,7 +11,10 @@ forward.  Checked two ways:
 * bitwise against the oracle running the same pipeline (pack, rank-ordered AVG sum,
   AdamW restatement);
 * against single-process ``torch.optim.AdamW`` on the full batch: max abs weight
-  error < 1e-5, the reference's ``OPTIMIZER_STEP_TOLERANCE`` (``tests/conftest.py:78-80``).
+  error below 1e-7.  The reference's own test bound is 1e-5 (``OPTIMIZER_STEP_TOLERANCE``,
+  ``tests/conftest.py:78-80``); the errors it publishes for its 1857-parameter MLP are
+  3.0e-08 at W=2 and 4.5e-08 at W=4 (``README.md:106-107``), and this test holds the
+  same scale.  The measured error is printed (``pytest -s``).
 
 Per-rank gradients come from torch autograd on the CPU: the forward/backward pass
 is the caller of this path, not part of it.
@@ -37,6 +40,9 @@ from hybrid_training_amd import (
 pytestmark = pytest.mark.gpu
 
 OPTIMIZER_STEP_TOLERANCE = 1e-5
+#: The scale of the reference's published weight errors (3.0e-08 / 4.5e-08).
+PUBLISHED_SCALE_BOUND = 1e-7
+PUBLISHED = {2: 3.0e-08, 4: 4.5e-08}
 MICRO = 16
 STEPS = 5
 LR, WD = 1e-3, 0.01
@@ -112,7 +118,10 @@ def test_fsdp_mlp_matches_oracle_and_single_process(device, world):
 
     expected = dict(reference.named_parameters())
     error = max(float((p.detach() - expected[n].detach()).abs().max()) for n, p in named)
+    print(f"[fsdp mlp W={world}] max weight error vs single-process AdamW after {STEPS} steps: {error:.2e} "
+          f"(reference README: {PUBLISHED[world]:.1e})", flush=True)
     assert error < OPTIMIZER_STEP_TOLERANCE, error
+    assert error < PUBLISHED_SCALE_BOUND, error
     state_numel = sum(v.numel() for o in opts for s in o.inner.state.values() for v in s.values()
                       if torch.is_tensor(v) and v.numel() > 1)
     assert state_numel == 2 * shard * world  # optimizer state is sharded

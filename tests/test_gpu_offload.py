@@ -1,18 +1,28 @@
 """GPU parity of the optimizer-state offload path (``cpu_offload_state=True``).
 
 Reference semantics (``optim/sharded_optimizer.py:284-296``, ``:342-353``): master copies
-and optimizer state live on the host, and after every step the device parameters
-equal the host masters.  Here the state streams through the device in chunks, and
-the results must be bitwise those of the in-HBM path: parameters, host masters and
-state, over several steps, for AdamW (with the deferred clip) and for SGD with
-momentum, with a chunk size small enough that every tensor takes several chunks.
+and optimizer state live on the host, the gradients are copied down, torch's own
+optimizer steps the host masters on the CPU, and the device parameters are overwritten
+with them.  Here the state streams through the device in chunks instead, so the run is
+checked three ways, with a chunk size small enough that every tensor takes several
+chunks:
+
+* against that reference sequence itself, run beside it: ``torch.optim.AdamW`` /
+  ``torch.optim.SGD(foreach=False)`` stepping host masters after the reference's clip.
+  Momentum buffers, ``exp_avg`` and ``exp_avg_sq`` are bitwise equal; parameters are
+  bitwise equal for SGD and within ``1e-6 * max(|b|, lr)`` for AdamW, whose only
+  difference is torch's vectorised CPU square root (faithfully, not correctly, rounded);
+* against the oracle, bitwise, everything;
+* against the in-HBM path, bitwise: parameters, host masters and state.
 """
 
 from __future__ import annotations
 
+import numpy as np
 import pytest
 import torch
 
+import oracle
 from hybrid_training_amd import GroupHandle, OptimizerConfig, ShardedOptimizer
 from hybrid_training_amd import optim as optim_module
 
@@ -85,3 +95,78 @@ def test_offloaded_state_round_trip(device, small_chunks):
         params[0].grad = grad.clone()
         opt.step()
     assert torch.equal(hbm[0][0].detach(), off[0][0].detach())
+
+
+@pytest.mark.parametrize("name", ["adamw", "sgd"])
+@pytest.mark.parametrize("defer_clip", [False, True])
+def test_offload_matches_the_reference_cpu_offload_and_the_oracle(device, small_chunks, name, defer_clip):
+    sizes = [10_000, 4096, 1, 12_289]
+    lr = 3e-4 if name == "adamw" else 0.05
+    gen = torch.Generator().manual_seed(31)
+    init = [torch.randn(n, generator=gen) * 0.02 for n in sizes]
+    params = [torch.nn.Parameter(t.to(device)) for t in init]
+    if name == "adamw":
+        config = OptimizerConfig(learning_rate=lr, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, cpu_offload_state=True)
+    else:
+        config = OptimizerConfig(name="sgd", learning_rate=lr, momentum=0.9, weight_decay=0.01, cpu_offload_state=True)
+    opt = ShardedOptimizer(params, config, norm_group=GroupHandle.trivial(), device=device, defer_clip=defer_clip)
+    # The reference's offload: host masters stepped by torch's own optimizer on the CPU.
+    masters = [torch.nn.Parameter(t.clone()) for t in init]
+    if name == "adamw":
+        ref = torch.optim.AdamW(masters, lr=lr, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, foreach=False)
+    else:
+        ref = torch.optim.SGD(masters, lr=lr, momentum=0.9, weight_decay=0.01, foreach=False)
+    P = [t.numpy().copy() for t in init]
+    M = [np.zeros(n, np.float32) for n in sizes]
+    V = [np.zeros(n, np.float32) for n in sizes]
+    worst = 0.0
+    for step in range(1, 4):
+        grads = [torch.randn(n, generator=gen) * 0.1 for n in sizes]  # norm ~ 16: clipped
+        for p, g in zip(params, grads):
+            p.grad = g.to(device)
+        norm = float(opt.clip_grad_norm(1.0))
+        opt.step()
+        # the reference: fp64 norm, Python-double coefficient, in-place fp32 multiply
+        # (sharded_optimizer.py:310-338), then the host step (:342-353)
+        ref_grads = [g.clone() for g in grads]
+        ref_norm = float(sum(g.double().pow(2).sum() for g in ref_grads) ** 0.5)
+        coef = 1.0 / (ref_norm + 1e-6)
+        if coef < 1.0:
+            for g in ref_grads:
+                g.mul_(coef)
+        for m_, g in zip(masters, ref_grads):
+            m_.grad = g
+        ref.step()
+        assert abs(norm - ref_norm) <= 1e-12 * ref_norm
+        mul = oracle.clip_multiplier(norm, 1.0)
+        assert mul == oracle.clip_multiplier(ref_norm, 1.0) < 1.0
+        for k, g in enumerate(grads):
+            if name == "adamw":
+                sc = oracle.adamw_scalars(lr=lr, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1, step=float(step))
+                oracle.adamw_step(P[k], g.numpy(), M[k], V[k], sc, grad_mul=mul)
+            else:
+                oracle.sgd_step(P[k], g.numpy(), M[k], lr=lr, momentum=0.9, weight_decay=0.01, first=step == 1,
+                                grad_mul=mul)
+        saved = opt.state_dict()  # waits for the write-back of the streamed state
+        for k, (p, m_) in enumerate(zip(params, masters)):
+            got = p.detach().cpu()
+            context = (name, defer_clip, step, sizes[k])
+            assert np.array_equal(got.numpy().view(np.int32), P[k].view(np.int32)), context
+            state, ref_state = saved["state"][k], ref.state[m_]
+            first = "exp_avg" if name == "adamw" else "momentum_buffer"
+            assert np.array_equal(state[first].numpy().view(np.int32), M[k].view(np.int32)), context
+            assert torch.equal(state[first], ref_state[first]), context
+            if name == "adamw":
+                assert np.array_equal(state["exp_avg_sq"].numpy().view(np.int32), V[k].view(np.int32)), context
+                assert torch.equal(state["exp_avg_sq"], ref_state["exp_avg_sq"]), context
+                want = m_.detach()
+                worst = max(worst, float(((got - want).abs() / want.abs().clamp_min(lr)).max()))
+            else:
+                assert torch.equal(got, m_.detach()), context
+            # .grad: clipped in place as the reference leaves it, unless the clip is deferred
+            assert torch.equal(p.grad.cpu(), grads[k] if defer_clip else ref_grads[k]), context
+        opt.zero_grad()
+    assert worst <= 1e-6, worst
+    # the host masters are the device parameters
+    for dev, host in zip(params, opt.inner.param_groups[0]["params"]):
+        assert torch.equal(host, dev.detach().cpu())

@@ -45,10 +45,12 @@ def _adamw_launch(ps, gs, ms, vs, scalars, *, unscale=1.0, grad_mul=None):
         _native.pointer_array([t.data_ptr() for t in vs]),
         _native.int64_array([t.numel() for t in ps]),
         len(ps),
+        _native.dtype_code(ps[0].dtype),
         _native.dtype_code(gs[0].dtype),
         unscale,
         None if grad_mul is None else grad_mul.data_ptr(),
         *scalars,
+        0,
         _native.stream_of(ps[0].device),
     )
     _native.check(status, "test.hbt_adamw_step")
@@ -215,15 +217,32 @@ def test_sharded_optimizer_vs_torch_adamw(device):
 
 
 def test_clip_is_in_place_like_the_reference(device):
-    g = torch.full((4,), 3.0, device=device)
-    param = torch.nn.Parameter(torch.ones(4, device=device))
-    param.grad = g.clone()
-    opt = _make_optimizer([param])
-    norm = opt.clip_grad_norm(1.0)
-    assert float(norm) == 6.0
-    assert abs(float(param.grad.double().norm()) - 1.0) < 1e-5
+    """By default .grad ends up clipped as the reference's ``grad.mul_`` leaves it: written
+    back by the step's fused pass, or at once by ``materialize_pending``.  Both give the
+    same gradients and parameters; ``defer_clip=True`` leaves .grad unclipped."""
     expect = torch.full((4,), 3.0).mul_(1.0 / (6.0 + 1e-6))
-    assert torch.equal(param.grad.cpu(), expect)
+    results = {}
+    for mode in ("write_back", "materialize", "defer"):
+        param = torch.nn.Parameter(torch.ones(4, device=device))
+        param.grad = torch.full((4,), 3.0, device=device)
+        opt = _make_optimizer([param], defer=(mode == "defer"))
+        norm = opt.clip_grad_norm(1.0)
+        assert float(norm) == 6.0
+        if mode == "materialize":
+            opt.materialize_pending()
+            assert torch.equal(param.grad.cpu(), expect)
+        version = param.grad._version
+        opt.step()
+        if mode == "defer":
+            assert torch.equal(param.grad.cpu(), torch.full((4,), 3.0))
+        else:
+            assert torch.equal(param.grad.cpu(), expect)
+            assert abs(float(param.grad.double().norm()) - 1.0) < 1e-5
+            # the write-back is an in-place change: it bumps the version counter
+            assert (param.grad._version > version) == (mode == "write_back")
+        results[mode] = param.detach().cpu()
+    assert torch.equal(results["write_back"], results["materialize"])
+    assert torch.equal(results["write_back"], results["defer"])
 
 
 def test_deferred_and_fused_paths_are_bitwise_equal(device):
@@ -237,10 +256,13 @@ def test_deferred_and_fused_paths_are_bitwise_equal(device):
         for g in grads:
             param.grad = g.clone()
             if mode == "fused":
-                opt.clip_and_step(0.5)
+                norm = opt.clip_and_step(0.5)
             else:
-                opt.clip_grad_norm(0.5)
+                norm = opt.clip_grad_norm(0.5)
                 opt.step()
+            mul = oracle.clip_multiplier(float(norm), 0.5)
+            clipped = (g.cpu() * np.float32(mul)) if mode != "defer" else g.cpu()
+            assert torch.equal(param.grad.cpu(), clipped), mode
             opt.zero_grad()
         results.append(param.detach().clone())
     assert torch.equal(results[0], results[1]) and torch.equal(results[0], results[2])
@@ -322,6 +344,8 @@ def test_pending_unscale_is_read_through(device):
         opt.clip_grad_norm(0.1)
         opt.step()
     assert torch.equal(a.detach(), b.detach())
+    # in-place semantics: both gradients end unscaled and clipped, the factor consumed
+    assert torch.equal(a.grad, b.grad) and not hasattr(a.grad, PENDING_UNSCALE_ATTR)
 
 
 def test_full_size_llama_shard(device):

@@ -10,6 +10,8 @@ reduced size, and at the full size of one Llama-3-70B FSDP rank at W=8
 
 from __future__ import annotations
 
+import math
+
 import numpy as np
 import pytest
 import torch
@@ -111,7 +113,7 @@ def test_unscale_return_value_is_the_overflow_flag(device):
 def test_unscale_refuses_gradients_the_kernel_cannot_address(device):
     """The in-place scale reads ``numel`` consecutive elements from a gradient's address:
     a strided gradient is refused (``ShardingError``) rather than scaled in the wrong
-    places, and an fp16 gradient, which the kernel does not take, is refused up front."""
+    places, and a float64 gradient, which the kernel does not take, is refused up front."""
     scaler = GradScaler(GradScalerConfig(enabled=True, init_scale=1024.0), GroupHandle.trivial(), device)
     p = torch.nn.Parameter(torch.zeros(10, device=device))
     storage = torch.arange(20.0, device=device)
@@ -119,9 +121,9 @@ def test_unscale_refuses_gradients_the_kernel_cannot_address(device):
     with pytest.raises(ShardingError, match="must be dense"):
         scaler.unscale_([p])
     assert torch.equal(storage, torch.arange(20.0, device=device))  # nothing was touched
-    q = torch.nn.Parameter(torch.zeros(10, device=device, dtype=torch.float16))
-    q.grad = torch.ones(10, device=device, dtype=torch.float16)
-    with pytest.raises(UnsupportedFeatureError, match="float32 or bfloat16"):
+    q = torch.nn.Parameter(torch.zeros(10, device=device, dtype=torch.float64))
+    q.grad = torch.ones(10, device=device, dtype=torch.float64)
+    with pytest.raises(UnsupportedFeatureError, match="float32, bfloat16 or float16"):
         scaler.unscale_([q])
 
 
@@ -165,3 +167,63 @@ def test_llama3_70b_rank_shard_full_size(device):
     assert np.array_equal(state["exp_avg"][idx].cpu().numpy().view(np.int32), M.view(np.int32))
     del opt, param, grad, state
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("name", ["adamw", "sgd"])
+def test_bf16_engine_sequence_eager_and_deferred_match_the_oracle(device, name):
+    """The engine's tail (``unscale_``, ``clip_grad_norm``, ``scaler.step``, ``update``) on
+    bf16 gradients with a loss scale of 1000 (its inverse is not a power of two, so the
+    unscale rounds) and a clip coefficient near 0.3 (not a power of two either), run
+    three ways: everything in place (the defaults), everything deferred, and a deferred
+    unscale under an in-place clip.  Every way gives parameters and state bitwise equal to
+    the oracle, whose gradient is rounded to bf16 after each multiply as the reference's
+    ``grad.mul_`` calls round it (``optim/grad_scaler.py:181-186``,
+    ``optim/sharded_optimizer.py:333-337``), and the in-place ways leave exactly those
+    rounded gradients in ``.grad``."""
+    n = 300_001
+    scale = 1000.0
+    gen = torch.Generator(device=device).manual_seed(21)
+    p0 = torch.randn(n, device=device, generator=gen) * 0.02
+    grads = [(torch.randn(n, device=device, generator=gen) * 3e-3 * scale).to(torch.bfloat16) for _ in range(3)]
+    config = (OptimizerConfig(learning_rate=3e-4, betas=(0.9, 0.95), weight_decay=0.1) if name == "adamw"
+              else OptimizerConfig(name="sgd", learning_rate=0.05, momentum=0.9, weight_decay=0.01))
+    results = {}
+    for defer_unscale, defer_clip in ((False, False), (True, True), (True, False)):
+        param = torch.nn.Parameter(p0.clone())
+        param.grad_dtype = None
+        opt = ShardedOptimizer([param], config, norm_group=GroupHandle.trivial(), device=device, defer_clip=defer_clip)
+        scaler = GradScaler(GradScalerConfig(enabled=True, init_scale=scale, growth_interval=1000),
+                            GroupHandle.trivial(), device, defer_unscale=defer_unscale)
+        P = p0.cpu().numpy().copy()
+        M = np.zeros(n, np.float32)
+        V = np.zeros(n, np.float32)
+        for step, g in enumerate(grads, start=1):
+            G = _bf16_bits(g)
+            param.grad = g.clone()
+            scaler.unscale_([param])
+            norm = float(opt.clip_grad_norm(1.0))
+            assert scaler.step(opt, [param], already_unscaled=True)
+            scaler.update()
+            ref_sq = oracle.sqnorm(G, unscale=1.0 / scale)
+            assert abs(norm**2 - ref_sq) <= 1e-12 * ref_sq
+            mul = oracle.clip_multiplier(norm, 1.0)
+            assert mul < 1.0 and math.frexp(mul)[0] != 0.5  # clipping active, not a power of two
+            written = np.empty(n, np.uint16)
+            if name == "adamw":
+                sc = oracle.adamw_scalars(lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1, step=float(step))
+                oracle.adamw_step(P, G, M, V, sc, unscale=1.0 / scale, grad_mul=mul, grad_out=written)
+            else:
+                oracle.sgd_step(P, G, M, lr=0.05, momentum=0.9, weight_decay=0.01, first=step == 1,
+                                unscale=1.0 / scale, grad_mul=mul, grad_out=written)
+            assert np.array_equal(param.detach().cpu().numpy().view(np.int32), P.view(np.int32)), (step, defer_clip)
+            state = opt.inner.state[param]
+            first = state["exp_avg"] if name == "adamw" else state["momentum_buffer"]
+            assert np.array_equal(first.cpu().numpy().view(np.int32), M.view(np.int32)), (step, defer_clip)
+            if name == "adamw":
+                assert np.array_equal(state["exp_avg_sq"].cpu().numpy().view(np.int32), V.view(np.int32))
+            # .grad: the in-place sequence's rounded values, or untouched when both are deferred
+            assert np.array_equal(_bf16_bits(param.grad), G if defer_clip else written), (step, defer_clip)
+            opt.zero_grad(set_to_none=True)
+        results[(defer_unscale, defer_clip)] = param.detach().cpu()
+    first = results[(False, False)]
+    assert all(torch.equal(first, r) for r in results.values())

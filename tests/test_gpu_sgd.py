@@ -83,12 +83,13 @@ def test_sgd_with_deferred_clip_and_bf16_loss_scaled_grads(device):
         scaler.update()
         opt.zero_grad()
         bits = g.cpu().view(torch.int16).numpy().view(np.uint16)
-        g32 = (bits.astype(np.uint32) << 16).view(np.float32)
         ref = oracle.sqnorm(bits, unscale=1.0 / scale)
         assert abs(norm**2 - ref) <= 1e-12 * ref
         mul = oracle.clip_multiplier(norm, 1.0)
         assert mul < 1.0
-        oracle.sgd_step(hp, g32, hb, lr=lr, momentum=0.9, weight_decay=0.01, first=step == 0,
+        # the unscale and clip multiplies are each rounded to bf16, as the reference's
+        # in-place grad.mul_ calls on a bf16 gradient round them
+        oracle.sgd_step(hp, bits, hb, lr=lr, momentum=0.9, weight_decay=0.01, first=step == 0,
                         unscale=1.0 / scale, grad_mul=mul)
         assert np.array_equal(_i32(param.detach().cpu().numpy()), _i32(hp)), step
 

@@ -32,7 +32,7 @@ def test_header_and_binding_agree():
 # Entry points that compute on the path; the others are introspection helpers that
 # share the comment block of the entry point they serve.
 _HELPERS = {"hbt_last_error", "hbt_abi_version", "hbt_symbol_count", "hbt_copy_chunk_elems",
-            "hbt_norm_partials_count"}
+            "hbt_norm_partials_count", "hbt_grid_slices"}
 # Entry points with no counterpart in the reference: their comment says so and names
 # the callers they serve instead of citing a reference function.
 _NO_COUNTERPART = {"hbt_grad_norm_noalloc"}
@@ -77,8 +77,8 @@ def test_library_loads_and_exports_every_declared_symbol():
 def test_invalid_arguments_are_rejected_before_any_launch():
     lib = _native.library()
     # count out of range: refused on the host, no device touched.
-    status = lib.hbt_adamw_step(None, None, None, None, None, 99, 0, 1.0, None,
-                                1, 0.1, 0.9, 0.1, 1, 1e-8, -1e-3, None)
+    status = lib.hbt_adamw_step(None, None, None, None, None, 99, 0, 0, 1.0, None,
+                                1, 0.1, 0.9, 0.1, 1, 1e-8, -1e-3, 0, None)
     assert status == -1
     assert b"count" in lib.hbt_last_error()
     with pytest.raises(NativeKernelError, match="count"):
@@ -86,8 +86,8 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     assert lib.hbt_copy_intervals(None, 1, 1, 0, 0, 0, 1.0, 0, None) == -1
     assert lib.hbt_copy_intervals(None, 0, 0, 0, 0, 0, 1.0, 0, None) == 0
     assert lib.hbt_copy_intervals(None, 0, 0, 0, 0, 0, 1.0, 2, None) == -1  # unknown flag
-    assert lib.hbt_grad_local_share(None, 0, 0, 1, 1, 0, 0, 1.0, None, None) == -1
-    assert lib.hbt_grad_local_share_sqnorm(None, 1, 0, 1, 1, 0, 0, 1.0, None, None, None, None) == -1
+    assert lib.hbt_grad_local_share(None, 0, 0, 1, 1, 0, 0, 1.0, 0, None, None) == -1
+    assert lib.hbt_grad_local_share_sqnorm(None, 1, 0, 1, 1, 0, 0, 1.0, 0, None, None, None, None) == -1
     assert b"hbt_grad_local_share_sqnorm" in lib.hbt_last_error()
     assert lib.hbt_grad_accumulate(None, None, None, 0, 0, 0, 0, None) == 0  # empty table
     assert lib.hbt_grad_accumulate(None, None, None, 0, 3, 0, 0, None) == 0  # fp64 accumulator, empty table
@@ -96,8 +96,24 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     assert lib.hbt_grad_accumulate(None, None, None, 0, 5, 0, 0, None) == -1  # unknown accumulator dtype
     # fp64 input with an fp32 reduce dtype: refused by the dtype check, before any pointer is read
     fake = ctypes.c_void_p(4096)
-    assert lib.hbt_grad_local_share(_native.pointer_array([4096]), 1, 0, 1, 1, 3, 0, 1.0, fake, None) == -1
+    assert lib.hbt_grad_local_share(_native.pointer_array([4096]), 1, 0, 1, 1, 3, 0, 1.0, 0, fake, None) == -1
     assert b"input dtype 3" in lib.hbt_last_error()
+    # a master (output) dtype the kernels do not write
+    assert lib.hbt_grad_local_share(_native.pointer_array([4096]), 1, 0, 1, 1, 0, 0, 1.0, 3, fake, None) == -1
+    assert b"output (master) dtype 3" in lib.hbt_last_error()
+    # optimizer dtype pairs: fp32 parameters with fp16 gradients have no kernel; unknown flags
+    assert lib.hbt_adamw_step(None, None, None, None, None, 0, 0, 2, 1.0, None,
+                              1, 0.1, 0.9, 0.1, 1, 1e-8, -1e-3, 0, None) == -1
+    assert b"dtypes (0, 2)" in lib.hbt_last_error()
+    assert lib.hbt_adamw_step(None, None, None, None, None, 0, 1, 1, 1.0, None,
+                              1, 0.1, 0.9, 0.1, 1, 1e-8, -1e-3, 1, None) == -1
+    assert lib.hbt_sgd_step(None, None, None, None, 0, 2, 2, 1.0, None, 0.0, 0.0, 1.0, -0.1, 32, None) == -1
+    assert lib.hbt_sgd_step(None, None, None, None, 0, 2, 2, 1.0, None, 0.0, 0.0, 1.0, -0.1, 16, None) == 0
+    # conversions: division is refused for float64 and bf16 <-> fp16 pairs (before the table is read)
+    assert lib.hbt_copy_intervals(fake, 1, 1, 3, 0, 1, 2.0, 0, None) == -2
+    assert lib.hbt_copy_intervals(fake, 1, 1, 1, 2, 1, 2.0, 0, None) == -2
+    assert lib.hbt_copy_chunk_elems(3, 0) == 128 and lib.hbt_copy_chunk_elems(0, 3) == 256
+    assert lib.hbt_copy_chunk_elems(1, 2) == 512 and lib.hbt_copy_chunk_elems(3, 3) == -1
     assert lib.hbt_grad_accumulate(None, None, None, 0, 0, 0, 2, None) == -1  # unknown flag
     assert lib.hbt_grad_accumulate(None, None, None, 1, 0, 0, 0, None) == -1  # null table
     assert lib.hbt_grad_norm_finalize(None, 5, 1.0, None, None, None, None, None) == -1
@@ -134,9 +150,15 @@ int main(void) {
     if (hbt_copy_intervals(NULL, 1, 1, HBT_DTYPE_F32, HBT_DTYPE_F32, HBT_COPY_OP_COPY, 1.0f, 0, NULL)
         != HBT_ERR_INVALID_ARGUMENT) failures++;
     if (strstr(hbt_last_error(), "hbt_copy_intervals") == NULL) failures++;
-    if (hbt_adamw_step(NULL, NULL, NULL, NULL, NULL, HBT_MAX_TENSORS_PER_LAUNCH + 1, HBT_DTYPE_F32, 1.0f,
-                       NULL, 1.0f, 0.1f, 0.9f, 0.1f, 1.0f, 1e-8f, -1e-3f, NULL) != HBT_ERR_INVALID_ARGUMENT)
+    if (hbt_adamw_step(NULL, NULL, NULL, NULL, NULL, HBT_MAX_TENSORS_PER_LAUNCH + 1, HBT_DTYPE_F32, HBT_DTYPE_F32,
+                       1.0f, NULL, 1.0f, 0.1f, 0.9f, 0.1f, 1.0f, 1e-8f, -1e-3f, HBT_STEP_WRITE_GRAD, NULL)
+        != HBT_ERR_INVALID_ARGUMENT)
         failures++;
+    {
+        int64_t first[3], count[3];
+        if (hbt_grid_slices(70000000, 64, first, count, 3) != 2 || first[1] != 67108863 || count[0] != 67108863)
+            failures++;
+    }
     printf("c host: %%d failures\n", failures);
     return failures;
 }
