@@ -218,9 +218,19 @@ __device__ __forceinline__ void pack_unit_store(gbyte* d, const uint32_t (&e)[U]
 // (the host drops records with no chunks, so first_chunk strictly increases).  The
 // search runs on the scalar unit: its loads hit the scalar cache and do not queue behind
 // the vector traffic of the waves in flight.  (A 64-way search with one ballot over
-// vector loads measured slower: 5.8 against 6.5 TB/s on a 40-record reshard.)
+// vector loads measured slower: 5.8 against 6.5 TB/s on a 40-record reshard.)  With
+// hints (the table followed by hints[j] = the record owning chunk j * kHintStride) the
+// search starts at the hinted record and steps forward, at most as many records as
+// start inside one hint stride; without them it bisects the whole table, log2(count)
+// dependent loads before the workgroup's first data load.
+constexpr int kHintShift = 8;  // one hint per 256 chunks
 __device__ __forceinline__ int64_t owning_record(const int64_t* __restrict__ table, int64_t count,
-                                                 int64_t chunk) {
+                                                 int64_t chunk, const int64_t* __restrict__ hints) {
+    if (hints != nullptr) {
+        int64_t r = hints[chunk >> kHintShift];
+        while (r + 1 < count && table[4 * (r + 1) + 3] <= chunk) ++r;
+        return r;
+    }
     int64_t lo = 0, hi = count - 1;
     while (lo < hi) {
         const int64_t mid = (lo + hi + 1) >> 1;
@@ -235,10 +245,11 @@ __device__ __forceinline__ int64_t owning_record(const int64_t* __restrict__ tab
 
 template <int SB, int DB, int OP, bool H>
 __global__ __launch_bounds__(kCopyBlock) void copy_kernel(const int64_t* __restrict__ table,
-                                                          int64_t count, float divisor, int64_t chunk_base) {
+                                                          int64_t count, float divisor, int64_t chunk_base,
+                                                          const int64_t* __restrict__ hints) {
     static_assert(kCopyBlock == 64, "a workgroup is one wave; its chunk is one wave-wide span of 16-byte source loads");
     const int64_t chunk = chunk_base + static_cast<int64_t>(blockIdx.x);
-    const int64_t* rec = table + 4 * owning_record(table, count, chunk);
+    const int64_t* rec = table + 4 * owning_record(table, count, chunk, hints);
     const gbyte* src = reinterpret_cast<const gbyte*>(static_cast<uintptr_t>(rec[0]));
     gbyte* dst = reinterpret_cast<gbyte*>(static_cast<uintptr_t>(rec[1]));
     const int64_t n = rec[2];
@@ -314,14 +325,15 @@ __global__ __launch_bounds__(kCopyBlock) void copy_kernel(const int64_t* __restr
 // finishes with an element loop in its last chunk.
 template <int SB, int DB, int OP, bool H>
 __global__ __launch_bounds__(kCopyBlock) void copy_aligned_kernel(const int64_t* __restrict__ table,
-                                                                  int64_t count, float divisor, int64_t chunk_base) {
+                                                                  int64_t count, float divisor, int64_t chunk_base,
+                                                                  const int64_t* __restrict__ hints) {
     constexpr int U = unit_elems<SB, DB>();
     constexpr int kSrcWords = U * SB / 4;
     constexpr int64_t kChunk = chunk_elems<SB, DB>();
     constexpr int kPerLane = static_cast<int>(kChunk / U / kCopyBlock);
     static_assert(kChunk == int64_t(kPerLane) * kCopyBlock * U, "a chunk is whole units on every lane");
     const int64_t chunk = chunk_base + static_cast<int64_t>(blockIdx.x);
-    const int64_t* rec = table + 4 * owning_record(table, count, chunk);
+    const int64_t* rec = table + 4 * owning_record(table, count, chunk, hints);
     const int64_t e0 = (chunk - rec[3]) * kChunk;
     const int64_t n = rec[2];
     const int64_t len = (n - e0) < kChunk ? (n - e0) : kChunk;
@@ -398,12 +410,12 @@ constexpr int64_t elem_bytes() { return D == HBT_DTYPE_F64 ? 8 : (D == HBT_DTYPE
 
 template <int SD, int DD>
 __global__ __launch_bounds__(kCopyBlock) void convert_kernel(const int64_t* __restrict__ table, int64_t count,
-                                                             int64_t chunk_base) {
+                                                             int64_t chunk_base, const int64_t* __restrict__ hints) {
     constexpr int64_t SB = elem_bytes<SD>();
     constexpr int64_t DB = elem_bytes<DD>();
     constexpr int64_t kChunk = int64_t(kCopyBlock) * 16 / SB;
     const int64_t chunk = chunk_base + static_cast<int64_t>(blockIdx.x);
-    const int64_t* rec = table + 4 * owning_record(table, count, chunk);
+    const int64_t* rec = table + 4 * owning_record(table, count, chunk, hints);
     const int64_t e0 = (chunk - rec[3]) * kChunk;
     const int64_t n = rec[2];
     const int64_t len = (n - e0) < kChunk ? (n - e0) : kChunk;
@@ -416,9 +428,9 @@ __global__ __launch_bounds__(kCopyBlock) void convert_kernel(const int64_t* __re
 }
 
 int32_t launch_convert(int32_t src_dtype, int32_t dst_dtype, const int64_t* table, int64_t count, int64_t chunks,
-                       hipStream_t st) {
+                       const int64_t* hints, hipStream_t st) {
     return launch_sliced("hbt_copy_intervals", chunks, kCopyBlock, [&](int64_t first, dim3 grid) {
-#define HBT_CVT(SD, DD) convert_kernel<SD, DD><<<grid, kCopyBlock, 0, st>>>(table, count, first)
+#define HBT_CVT(SD, DD) convert_kernel<SD, DD><<<grid, kCopyBlock, 0, st>>>(table, count, first, hints)
 #define HBT_CVT_TO(SD)                                                     \
     do {                                                                   \
         if (dst_dtype == HBT_DTYPE_F64) HBT_CVT(SD, HBT_DTYPE_F64);        \
@@ -437,12 +449,12 @@ int32_t launch_convert(int32_t src_dtype, int32_t dst_dtype, const int64_t* tabl
 
 template <int SB, int DB, int OP, bool H = false>
 int32_t launch_copy(const int64_t* table, int64_t count, int64_t chunks, float divisor, bool aligned,
-                    hipStream_t s) {
+                    const int64_t* hints, hipStream_t s) {
     return launch_sliced("hbt_copy_intervals", chunks, kCopyBlock, [&](int64_t first, dim3 grid) {
         if (aligned) {
-            copy_aligned_kernel<SB, DB, OP, H><<<grid, kCopyBlock, 0, s>>>(table, count, divisor, first);
+            copy_aligned_kernel<SB, DB, OP, H><<<grid, kCopyBlock, 0, s>>>(table, count, divisor, first, hints);
         } else {
-            copy_kernel<SB, DB, OP, H><<<grid, kCopyBlock, 0, s>>>(table, count, divisor, first);
+            copy_kernel<SB, DB, OP, H><<<grid, kCopyBlock, 0, s>>>(table, count, divisor, first, hints);
         }
     });
 }
@@ -452,23 +464,23 @@ int32_t launch_copy(const int64_t* table, int64_t count, int64_t chunks, float d
 // multiply by the exact reciprocal: the same bits, without the division sequence.
 template <bool H>
 int32_t launch_arith(int ssz, int dsz, int32_t op, float divisor, const int64_t* table, int64_t count,
-                     int64_t chunks, bool aligned, hipStream_t s) {
+                     int64_t chunks, bool aligned, const int64_t* hints, hipStream_t s) {
     const float recip = op == HBT_COPY_OP_DIVIDE ? exact_reciprocal(divisor) : 0.0f;
     if (op == HBT_COPY_OP_DIVIDE && recip != 0.0f) {
-        if (ssz == 4 && dsz == 4) return launch_copy<4, 4, kOpScale>(table, count, chunks, recip, aligned, s);
-        if (ssz == 2 && dsz == 2) return launch_copy<2, 2, kOpScale, H>(table, count, chunks, recip, aligned, s);
-        if (ssz == 4) return launch_copy<4, 2, kOpScale, H>(table, count, chunks, recip, aligned, s);
-        return launch_copy<2, 4, kOpScale, H>(table, count, chunks, recip, aligned, s);
+        if (ssz == 4 && dsz == 4) return launch_copy<4, 4, kOpScale>(table, count, chunks, recip, aligned, hints, s);
+        if (ssz == 2 && dsz == 2) return launch_copy<2, 2, kOpScale, H>(table, count, chunks, recip, aligned, hints, s);
+        if (ssz == 4) return launch_copy<4, 2, kOpScale, H>(table, count, chunks, recip, aligned, hints, s);
+        return launch_copy<2, 4, kOpScale, H>(table, count, chunks, recip, aligned, hints, s);
     }
     if (op == HBT_COPY_OP_DIVIDE) {
-        if (ssz == 4 && dsz == 4) return launch_copy<4, 4, HBT_COPY_OP_DIVIDE>(table, count, chunks, divisor, aligned, s);
-        if (ssz == 2 && dsz == 2) return launch_copy<2, 2, HBT_COPY_OP_DIVIDE, H>(table, count, chunks, divisor, aligned, s);
-        if (ssz == 4) return launch_copy<4, 2, HBT_COPY_OP_DIVIDE, H>(table, count, chunks, divisor, aligned, s);
-        return launch_copy<2, 4, HBT_COPY_OP_DIVIDE, H>(table, count, chunks, divisor, aligned, s);
+        if (ssz == 4 && dsz == 4) return launch_copy<4, 4, HBT_COPY_OP_DIVIDE>(table, count, chunks, divisor, aligned, hints, s);
+        if (ssz == 2 && dsz == 2) return launch_copy<2, 2, HBT_COPY_OP_DIVIDE, H>(table, count, chunks, divisor, aligned, hints, s);
+        if (ssz == 4) return launch_copy<4, 2, HBT_COPY_OP_DIVIDE, H>(table, count, chunks, divisor, aligned, hints, s);
+        return launch_copy<2, 4, HBT_COPY_OP_DIVIDE, H>(table, count, chunks, divisor, aligned, hints, s);
     }
     // conversions (same-dtype copies are bit copies)
-    if (ssz == 4) return launch_copy<4, 2, HBT_COPY_OP_COPY, H>(table, count, chunks, divisor, aligned, s);
-    return launch_copy<2, 4, HBT_COPY_OP_COPY, H>(table, count, chunks, divisor, aligned, s);
+    if (ssz == 4) return launch_copy<4, 2, HBT_COPY_OP_COPY, H>(table, count, chunks, divisor, aligned, hints, s);
+    return launch_copy<2, 4, HBT_COPY_OP_COPY, H>(table, count, chunks, divisor, aligned, hints, s);
 }
 
 }  // namespace
@@ -494,12 +506,14 @@ int32_t hbt_copy_intervals(const int64_t* table, int64_t count, int64_t total_ch
         set_error("hbt_copy_intervals: bad table/count/total_chunks");
         return HBT_ERR_INVALID_ARGUMENT;
     }
-    if ((flags & ~HBT_COPY_ALIGNED) != 0) {
+    if ((flags & ~(HBT_COPY_ALIGNED | HBT_COPY_HINTS)) != 0) {
         set_error("hbt_copy_intervals: unknown flags 0x%x", static_cast<unsigned>(flags));
         return HBT_ERR_INVALID_ARGUMENT;
     }
     const bool aligned = (flags & HBT_COPY_ALIGNED) != 0;
     if (count == 0 || total_chunks == 0) return HBT_OK;
+    // The hints follow the count records of 4 int64 each.
+    const int64_t* hints = (flags & HBT_COPY_HINTS) != 0 ? table + 4 * count : nullptr;
     const int ssz = dtype_size(src_dtype);
     const int dsz = dtype_size(dst_dtype);
     if (ssz == 0 || dsz == 0 || (op != HBT_COPY_OP_COPY && op != HBT_COPY_OP_DIVIDE)) {
@@ -509,8 +523,8 @@ int32_t hbt_copy_intervals(const int64_t* table, int64_t count, int64_t total_ch
     hipStream_t s = as_stream(stream);
     if (op == HBT_COPY_OP_COPY && src_dtype == dst_dtype) {
         // Bit copy; fp64 moves as pairs of dwords (the host doubles its numels).
-        if (ssz == 2) return launch_copy<2, 2, HBT_COPY_OP_COPY>(table, count, total_chunks, divisor, aligned, s);
-        if (ssz == 4) return launch_copy<4, 4, HBT_COPY_OP_COPY>(table, count, total_chunks, divisor, aligned, s);
+        if (ssz == 2) return launch_copy<2, 2, HBT_COPY_OP_COPY>(table, count, total_chunks, divisor, aligned, hints, s);
+        if (ssz == 4) return launch_copy<4, 4, HBT_COPY_OP_COPY>(table, count, total_chunks, divisor, aligned, hints, s);
         set_error("hbt_copy_intervals: 8-byte elements must be passed as dword pairs (F32)");
         return HBT_ERR_UNSUPPORTED;
     }
@@ -523,12 +537,12 @@ int32_t hbt_copy_intervals(const int64_t* table, int64_t count, int64_t total_ch
                       "between F32 and a 2-byte dtype (got %d -> %d)", src_dtype, dst_dtype);
             return HBT_ERR_UNSUPPORTED;
         }
-        return launch_convert(src_dtype, dst_dtype, table, count, total_chunks, s);
+        return launch_convert(src_dtype, dst_dtype, table, count, total_chunks, hints, s);
     }
     if (src_dtype == HBT_DTYPE_F16 || dst_dtype == HBT_DTYPE_F16) {
-        return launch_arith<true>(ssz, dsz, op, divisor, table, count, total_chunks, aligned, s);
+        return launch_arith<true>(ssz, dsz, op, divisor, table, count, total_chunks, aligned, hints, s);
     }
-    return launch_arith<false>(ssz, dsz, op, divisor, table, count, total_chunks, aligned, s);
+    return launch_arith<false>(ssz, dsz, op, divisor, table, count, total_chunks, aligned, hints, s);
 }
 
 }  // extern "C"

@@ -462,8 +462,18 @@ __device__ __forceinline__ float share_cast(float x) {
 // One wave per 256-element tile: measured on MI355X (8 bf16 ranks -> fp32) this
 // short-lived shape streams at 6.4 TB/s, against 5.6 TB/s for the norm kernel's
 // 1024-thread, 8-tile workgroups.  kG > 0 fixes the group size so that every rank's
-// load is issued before the first is used; kG == 0 reads group_size at run time.
+// load is issued before the first is used; kG == 0 reads group_size at run time.  With
+// kG fixed the loads go out in pairs, each pair waited for before the next is issued:
+// 6.28 against 6.15 TB/s with all eight in flight at once (8 bf16 ranks in 16 GB
+// buffers; 6.63 against 6.38 TB/s when the rank slices are separate buffers).  Waiting
+// after every load, or after every four, measured no better than no wait.  The tile
+// sums cost nothing measurable (6.15 TB/s without them), and reducing them in LDS inside
+// 256- or 1024-thread workgroups measured slower (6.03 TB/s).
 // tile_sums may be null (the local share alone).
+#ifndef HBT_SHARE_ISSUE
+#define HBT_SHARE_ISSUE 2
+#endif
+constexpr int kShareIssue = HBT_SHARE_ISSUE;
 template <int ID, int kG, bool kRecip, int RD, int OD>
 __global__ __launch_bounds__(kShareBlock) void local_share_tiles_kernel(
     ShareRanks ranks, int32_t group_size, int64_t offset, int64_t shard_numel, int64_t valid_numel,
@@ -479,7 +489,10 @@ __global__ __launch_bounds__(kShareBlock) void local_share_tiles_kernel(
         if constexpr (kG > 0) {
             float x[kG][4];
 #pragma unroll
-            for (int q = 0; q < kG; ++q) load_vec<ID, 4>(ranks.g[q] + offset * IB, e, x[q]);
+            for (int q = 0; q < kG; ++q) {
+                load_vec<ID, 4>(ranks.g[q] + offset * IB, e, x[q]);
+                if ((q + 1) % kShareIssue == 0 && q + 1 < kG) wait_vmem();
+            }
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
                 sum[c] = round_to<RD>(share_div<kRecip>(share_cast<ID, RD>(x[0][c]), divisor, recip));

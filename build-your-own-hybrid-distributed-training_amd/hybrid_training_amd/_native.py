@@ -28,6 +28,7 @@ __all__ = [
     "ABI_VERSION",
     "ACCUMULATE_ASSIGN",
     "COPY_ALIGNED",
+    "COPY_HINTS",
     "COPY_CONVERSIONS",
     "OPTIMIZER_DTYPES",
     "STEP_WRITE_GRAD",
@@ -67,6 +68,9 @@ DTYPE_F64 = 3
 COPY_OP_COPY = 0
 COPY_OP_DIVIDE = 1
 COPY_ALIGNED = 1
+COPY_HINTS = 2
+#: Chunks per entry of a copy plan's hint table (HBT_COPY_HINTS).
+COPY_HINT_STRIDE = 256
 ACCUMULATE_ASSIGN = 1
 _CODE_BYTES = {DTYPE_F32: 4, DTYPE_BF16: 2, DTYPE_F16: 2, DTYPE_F64: 8}
 
@@ -163,7 +167,7 @@ _LIB: ctypes.CDLL | None = None
 # function of its rows (addresses, lengths, chunk prefix), so an entry stays valid
 # even after the tensors it was built for are freed; reuse skips the host-to-device
 # upload, which for a few hundred rows costs more than moving a GB on the device.
-_TABLE_CACHE: "OrderedDict[tuple, tuple[torch.Tensor, int, bool]]" = OrderedDict()
+_TABLE_CACHE: "OrderedDict[tuple, tuple[torch.Tensor, int, bool, bool]]" = OrderedDict()
 _TABLE_CACHE_SIZE = 256
 
 
@@ -352,6 +356,16 @@ def plan_table(rows: Sequence[tuple[int, int, int]], chunk: int, scale: int = 1)
     return flat, first
 
 
+def plan_hints(first_chunks: Sequence[int], total_chunks: int) -> list[int]:
+    """The ``HBT_COPY_HINTS`` table of a plan: for every ``COPY_HINT_STRIDE``-th chunk, the
+    index of the record that owns it (the last record starting at or before it)."""
+    import numpy as np
+
+    starts = np.asarray(first_chunks, dtype=np.int64)
+    probes = np.arange(0, total_chunks, COPY_HINT_STRIDE, dtype=np.int64)
+    return (np.searchsorted(starts, probes, side="right") - 1).tolist()
+
+
 def plan_is_aligned(rows: Sequence[tuple[int, int, int]], src_code: int, dst_code: int) -> bool:
     """Whether a plan qualifies for ``HBT_COPY_ALIGNED``: every destination on a 16-byte
     boundary and every source (0 for a zero fill) on the source width of one 16-byte
@@ -363,9 +377,9 @@ def plan_is_aligned(rows: Sequence[tuple[int, int, int]], src_code: int, dst_cod
 
 def _prepared_plan(
     device: torch.device, rows: tuple[tuple[int, int, int], ...], src_code: int, dst_code: int, scale: int
-) -> tuple[torch.Tensor, int, bool]:
-    """(device table, total chunks, aligned) for a plan, built once per distinct plan and
-    stream.  The table is uploaded on that stream, so later launches on it see it."""
+) -> tuple[torch.Tensor, int, bool, bool]:
+    """(device table, total chunks, aligned, hinted) for a plan, built once per distinct plan
+    and stream.  The table is uploaded on that stream, so later launches on it see it."""
     stream = stream_of(device)
     key = (device, stream, src_code, dst_code, scale, rows)
     with _TABLE_LOCK:
@@ -376,10 +390,14 @@ def _prepared_plan(
     chunk = _copy_chunk(library(), src_code, dst_code)
     flat, first = plan_table(rows, chunk, scale)
     aligned = plan_is_aligned(rows, src_code, dst_code)
+    # Plans of several records carry the hint table after their records.
+    hinted = len(rows) > 1
+    if hinted:
+        flat = flat + plan_hints(flat[3::4], first)
     host = torch.tensor(flat, dtype=torch.int64).pin_memory()
     with torch.cuda.device(device):
         table = host.to(device, non_blocking=True)
-    entry = (table, first, aligned)
+    entry = (table, first, aligned, hinted)
     with _TABLE_LOCK:
         _TABLE_CACHE[key] = entry
         if len(_TABLE_CACHE) > _TABLE_CACHE_SIZE:
@@ -477,7 +495,7 @@ class CopyPlan:
             src_code = dst_code = DTYPE_F32
             scale = 2
         lib = library()
-        table, first, aligned = _prepared_plan(self.device, tuple(self._rows), src_code, dst_code, scale)
+        table, first, aligned, hinted = _prepared_plan(self.device, tuple(self._rows), src_code, dst_code, scale)
         with torch.cuda.device(self.device):
             status = lib.hbt_copy_intervals(
                 table.data_ptr(),
@@ -487,7 +505,7 @@ class CopyPlan:
                 dst_code,
                 op,
                 float(divisor),
-                COPY_ALIGNED if aligned else 0,
+                (COPY_ALIGNED if aligned else 0) | (COPY_HINTS if hinted else 0),
                 stream_of(self.device),
             )
         check(status, "native.hbt_copy_intervals")

@@ -229,7 +229,8 @@ def test_aligned_kernel_matches_general_kernel(device, sdt, ddt, op, divisor):
     if op != _native.COPY_OP_DIVIDE:
         divisor = 1.0
     outs = []
-    for flags in (_native.COPY_ALIGNED, 0):
+    hints = _native.COPY_HINTS
+    for flags in (_native.COPY_ALIGNED, 0, _native.COPY_ALIGNED | hints, hints):
         dst = torch.full((n_dst,), 5.0, dtype=torch.float32, device=device).to(ddt)
         assert src.data_ptr() % 16 == 0 and dst.data_ptr() % 16 == 0
         flat, first = [], 0
@@ -238,6 +239,8 @@ def test_aligned_kernel_matches_general_kernel(device, sdt, ddt, op, divisor):
             s_addr = 0 if s0 < 0 else src.data_ptr() + s0 * ssz
             flat += [s_addr, dst.data_ptr() + d0 * dsz, n, first]
             first += -(-n // chunk)
+        if flags & hints:  # the record owning every 256th chunk, after the records
+            flat += _native.plan_hints(flat[3::4], first)
         table = torch.tensor(flat, dtype=torch.int64).to(device)
         status = lib.hbt_copy_intervals(table.data_ptr(), len(rows), first, s_code, d_code, op, divisor, flags,
                                         _native.stream_of(device))
@@ -247,8 +250,8 @@ def test_aligned_kernel_matches_general_kernel(device, sdt, ddt, op, divisor):
     expect = _bits(torch.full((n_dst,), 5.0, dtype=torch.float32).to(ddt))
     for s0, d0, n in rows:
         expect[d0 : d0 + n] = 0 if s0 < 0 else convert(sbits[s0 : s0 + n])
-    assert np.array_equal(outs[0], expect)
-    assert np.array_equal(outs[1], expect)
+    for out in outs:
+        assert np.array_equal(out, expect)
 
 
 def test_float16_specials_match_torch(device):

@@ -41,7 +41,7 @@ from hybrid_training_amd import (
     shard_range_for,
 )
 from hybrid_training_amd import reshard as reshard_module
-from hybrid_training_amd._native import plan_table
+from hybrid_training_amd._native import plan_hints, plan_table
 from hybrid_training_amd.flat_param import _last_writer_segments
 
 PROPERTY = settings(derandomize=True, max_examples=300, deadline=None,
@@ -285,6 +285,26 @@ def test_copy_table_assigns_every_chunk_to_the_row_that_holds_it(rows, chunk, sc
     for c, (index, k) in enumerate(owners):
         found = bisect.bisect_right(firsts, c) - 1
         assert (found, c - firsts[found]) == (index, k)
+
+
+@PROPERTY
+@given(sizes=st.lists(st.integers(0, 200_000), min_size=1, max_size=40), chunk=st.sampled_from([128, 256, 512]))
+def test_copy_hints_name_the_record_of_every_256th_chunk(sizes, chunk):
+    """``HBT_COPY_HINTS``: hint j is the owner of chunk 256 * j, found by brute force
+    over every row's chunks; stepping forward from a chunk's hint while the next record
+    starts at or before it lands on its owner (the kernel's search)."""
+    rows = [(4096, 8192, n) for n in sizes]
+    flat, total = plan_table(rows, chunk)
+    hints = plan_hints(flat[3::4], total)
+    owner = [i for i, (_, _, n) in enumerate(rows) for _ in range(-(-n // chunk))]
+    assert len(owner) == total and len(hints) == -(-total // 256)
+    assert hints == owner[::256]
+    firsts = flat[3::4]
+    for c in range(0, total, 97):
+        r = hints[c >> 8]
+        while r + 1 < len(rows) and firsts[r + 1] <= c:
+            r += 1
+        assert r == owner[c]
 
 
 @PROPERTY

@@ -85,7 +85,7 @@ def test_invalid_arguments_are_rejected_before_any_launch():
         _native.check(status, "test")
     assert lib.hbt_copy_intervals(None, 1, 1, 0, 0, 0, 1.0, 0, None) == -1
     assert lib.hbt_copy_intervals(None, 0, 0, 0, 0, 0, 1.0, 0, None) == 0
-    assert lib.hbt_copy_intervals(None, 0, 0, 0, 0, 0, 1.0, 2, None) == -1  # unknown flag
+    assert lib.hbt_copy_intervals(None, 0, 0, 0, 0, 0, 1.0, 4, None) == -1  # unknown flag
     assert lib.hbt_grad_local_share(None, 0, 0, 1, 1, 0, 0, 1.0, 0, None, None) == -1
     assert lib.hbt_grad_local_share_sqnorm(None, 1, 0, 1, 1, 0, 0, 1.0, 0, None, None, None, None) == -1
     assert b"hbt_grad_local_share_sqnorm" in lib.hbt_last_error()
