@@ -81,26 +81,25 @@ __device__ __forceinline__ float bf16_to_f32(uint32_t bits16) {
     return __uint_as_float(bits16 << 16);
 }
 
+// A select of a constant, not an early return: as a branch it compiles to a per-element
+// exec-mask jump, which made the 2-byte norm pass ALU-bound.
 __device__ __forceinline__ uint32_t f32_to_bf16(float x) {
-    uint32_t u = __float_as_uint(x);
-    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0u;
-    u += 0x7FFFu + ((u >> 16) & 1u);
-    return u >> 16;
+    const uint32_t u = __float_as_uint(x);
+    const uint32_t rounded = (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+    return (u & 0x7FFFFFFFu) > 0x7F800000u ? 0x7FC0u : rounded;
 }
 
-// IEEE fp16 <-> fp32.  Widening is exact (subnormals included) and keeps a NaN's sign
-// and payload bits, as torch's CPU conversion does.  Narrowing rounds to nearest, ties
-// to even, overflows to +-inf and keeps fp16 subnormals; any NaN becomes sign | 0x7E00.
+// IEEE fp16 <-> fp32 with gfx950's conversion instructions.  Widening (v_cvt_f32_f16) is
+// exact, subnormals included; narrowing (v_cvt_f16_f32) rounds to nearest, ties to even,
+// overflows to +-inf and keeps fp16 subnormals.  A NaN stays a NaN of the same sign with
+// the quiet bit set; its payload is kept (widening) or truncated (narrowing), the rule of
+// torch's vectorised CPU conversions (x86 F16C).  torch's scalar CPU loop writes other NaN
+// bits, so no NaN encoding is torch's in general.
 __device__ __forceinline__ float f16_to_f32(uint32_t bits16) {
-    if ((bits16 & 0x7C00u) == 0x7C00u && (bits16 & 0x03FFu) != 0u) {
-        return __uint_as_float(((bits16 & 0x8000u) << 16) | 0x7F800000u | ((bits16 & 0x03FFu) << 13));
-    }
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits16)));
 }
 
 __device__ __forceinline__ uint32_t f32_to_f16(float x) {
-    const uint32_t u = __float_as_uint(x);
-    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return ((u >> 16) & 0x8000u) | 0x7E00u;
     return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
 }
 

@@ -392,6 +392,18 @@ __global__ __launch_bounds__(kAdamBlock) void sgd_kernel(SgdTable tab, SgdScalar
 // 16-byte load per lane (4 fp32 or 8 bf16/fp16 gradients).
 constexpr int kNormBlock = 1024;
 constexpr int kNormTilesPerChunk = 8;
+// Tiles whose loads a thread issues together in a whole chunk (0: the tile loop, which
+// the compiler pipelines by itself for fp32 but not for 2-byte gradients).
+#ifndef HBT_NORM_BATCH_F32
+#define HBT_NORM_BATCH_F32 0
+#endif
+#ifndef HBT_NORM_BATCH_B16
+#define HBT_NORM_BATCH_B16 4
+#endif
+template <int GD>
+constexpr int norm_batch() { return GD == F32 ? HBT_NORM_BATCH_F32 : HBT_NORM_BATCH_B16; }
+static_assert(HBT_NORM_BATCH_F32 == 0 || kNormTilesPerChunk % HBT_NORM_BATCH_F32 == 0, "whole batches of tiles");
+static_assert(HBT_NORM_BATCH_B16 == 0 || kNormTilesPerChunk % HBT_NORM_BATCH_B16 == 0, "whole batches of tiles");
 template <int GD>
 constexpr int norm_vec() { return GD == F32 ? 4 : 8; }
 template <int GD>
@@ -431,6 +443,29 @@ __global__ __launch_bounds__(kNormBlock) void sqnorm_kernel(NormTable tab, float
     const int64_t n = tab.n[t];
     const void* G = tab.g[t];
     double acc = 0.0;
+    constexpr int kNormBatch = norm_batch<GD>() > 0 ? norm_batch<GD>() : 1;
+    if (norm_batch<GD>() > 0 && tab.vec_ok[t] && start + kChunk <= n) {
+        // a whole chunk: kNormBatch tiles' loads in flight before the first of them is summed
+#pragma unroll
+        for (int k0 = 0; k0 < kNormTilesPerChunk; k0 += kNormBatch) {
+            float x[kNormBatch][K];
+#pragma unroll
+            for (int k = 0; k < kNormBatch; ++k)
+                load_vec<GD, K>(G, start + int64_t(k0 + k) * kTile + int64_t(threadIdx.x) * K, x[k]);
+#pragma unroll
+            for (int k = 0; k < kNormBatch; ++k) {
+#pragma unroll
+                for (int c = 0; c < K; ++c) {
+                    float y = x[k][c];
+                    if constexpr (kUnscale) y = round_to<GD>(y * unscale);
+                    acc += sq(y);
+                }
+            }
+        }
+        const double block_total = block_sum<kNormBlock>(acc);
+        if (threadIdx.x == 0) partials[chunk] = block_total * tab.w[t];
+        return;
+    }
     for (int k = 0; k < kNormTilesPerChunk; ++k) {
         const int64_t base = start + int64_t(k) * kTile;
         if (base >= n) break;

@@ -214,8 +214,12 @@ int32_t hbt_grad_norm_noalloc(const void* const* grads, const int64_t* numels, c
  *   HBT_COPY_OP_COPY    dst = src               (same dtype: byte copy; F32->BF16
  *                                                rounds to nearest even, NaN -> 0x7FC0;
  *                                                F32->F16 rounds to nearest even, overflows
- *                                                to inf, keeps subnormals, NaN -> sign|0x7E00;
- *                                                BF16->F32 and F16->F32 widen exactly)
+ *                                                to inf, keeps subnormals; BF16->F32 and
+ *                                                F16->F32 widen exactly; an fp16 NaN keeps
+ *                                                its sign and gets the quiet bit, with the
+ *                                                payload kept (widening) or its top 10 bits
+ *                                                kept (narrowing), as x86 F16C and torch's
+ *                                                vectorised CPU conversions do)
  *                                               F64 -> F32/BF16/F16 and BF16 <-> F16 convert
  *                                                as torch's Tensor.to does: through the exact
  *                                                or nearest-even fp32 value, then to nearest

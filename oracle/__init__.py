@@ -29,6 +29,7 @@ __all__ = [
     "bucket_layout",
     "clip_multiplier",
     "even_shards",
+    "f16_nan_rules",
     "f32_to_bf16",
     "flat_layout",
     "from_bits",
@@ -76,6 +77,8 @@ PINNED_BY = {
     "grad + accumulator) in fp32, bf16 and fp16, bitwise on signed zeros, subnormals, overflow and "
     "random values; in float64 bitwise against torch and equal to the exact sum",
     "round_to": "torch Tensor.to(bfloat16 / float16).to(float32) bitwise on specials and random values",
+    "f16_nan_rules": "torch's vectorised CPU Tensor.to (x86 F16C) bitwise on all 65,536 fp16 bit patterns "
+    "(widening) and on NaN payloads of both signs, signalling and quiet (narrowing)",
 }
 
 
@@ -261,6 +264,36 @@ def clip_multiplier(norm: float, max_norm: float) -> float:
         return 1.0
     coef = float(max_norm) / (float(norm) + 1e-6)
     return float(np.float32(coef)) if coef < 1.0 else 1.0
+
+
+def f16_nan_rules():
+    """(widen, narrow): fp16 -> fp32 and fp32 -> fp16 on bit patterns, NaN bits included.
+
+    Non-NaN values convert as IEEE does (numpy's exact widening, round-to-nearest-even
+    narrowing with overflow to infinity).  A NaN keeps its sign and gets the quiet bit:
+    widening keeps the 10-bit payload as the top of the 23-bit one, narrowing keeps the
+    payload's top 10 bits.  These are the rules of x86 F16C, which torch's vectorised CPU
+    conversions use (the reference's fp16 casts, ``parallel/fsdp.py:578-579``, ``:734-735``).
+    """
+
+    def widen(bits16: np.ndarray) -> np.ndarray:
+        b = np.asarray(bits16, np.uint16)
+        with np.errstate(invalid="ignore"):
+            out = b.view(np.float16).astype(np.float32).view(np.uint32).copy()
+        b32 = b.astype(np.uint32)
+        nan = ((b32 & 0x7C00) == 0x7C00) & ((b32 & 0x03FF) != 0)
+        out[nan] = ((b32[nan] & 0x8000) << 16) | 0x7FC00000 | ((b32[nan] & 0x03FF) << 13)
+        return out
+
+    def narrow(bits32: np.ndarray) -> np.ndarray:
+        u = np.asarray(bits32, np.uint32)
+        with np.errstate(over="ignore", invalid="ignore"):
+            out = u.view(np.float32).astype(np.float16).view(np.uint16).copy()
+        nan = (u & 0x7FFFFFFF) > 0x7F800000
+        out[nan] = (((u[nan] >> 16) & 0x8000) | 0x7E00 | ((u[nan] >> 13) & 0x03FF)).astype(np.uint16)
+        return out
+
+    return widen, narrow
 
 
 def f32_to_bf16(x: np.ndarray) -> np.ndarray:

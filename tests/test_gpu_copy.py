@@ -281,6 +281,39 @@ def test_float16_specials_match_torch(device):
     assert torch.equal(wide.cpu().view(torch.int32), finite.cpu().to(torch.float32).view(torch.int32))
 
 
+def _f16_nan_rules():
+    """The NaN bits of x86 F16C conversions, which torch's vectorised CPU ``.to`` uses:
+    widening sets the quiet bit and keeps sign and payload; narrowing sets the quiet bit
+    and keeps the sign and the payload's top bits.  ``test_oracle_lowp.py`` pins torch's
+    vectorised conversions to these rules on the CPU."""
+    from oracle import f16_nan_rules
+
+    return f16_nan_rules()
+
+
+def test_float16_every_bit_pattern_widens_like_torch(device):
+    """All 65,536 fp16 bit patterns through fp16 -> fp32: bitwise torch's conversion for
+    every non-NaN, and the quiet-bit rule for all 2,046 NaNs (signalling ones included)."""
+    widen, narrow = _f16_nan_rules()
+    every = torch.arange(-(2**15), 2**15, dtype=torch.int32).to(torch.int16)
+    src = every.view(torch.float16).to(device)
+    out = torch.empty(every.numel(), dtype=torch.float32, device=device)
+    plan = _native.CopyPlan(device)
+    plan.add(src, 0, out, 0, every.numel())
+    plan.run(src_dtype=torch.float16, dst_dtype=torch.float32)
+    bits16 = every.numpy().astype(np.uint16)
+    assert np.array_equal(out.cpu().view(torch.int32).numpy().view(np.uint32), widen(bits16))
+    # narrowing NaNs of assorted payloads, signalling and quiet, both signs
+    payloads = np.array([0x7F800001, 0x7FC12345, 0xFFC00001, 0x7FBFFFFF, 0xFF812345, 0x7FFFFFFF, 0x7FC00000,
+                         0xFFFFE000, 0x7F802000], np.uint32)
+    nan32 = torch.from_numpy(payloads.view(np.float32)).to(device)
+    half = torch.empty(payloads.size, dtype=torch.float16, device=device)
+    plan = _native.CopyPlan(device)
+    plan.add(nan32, 0, half, 0, payloads.size)
+    plan.run(src_dtype=torch.float32, dst_dtype=torch.float16)
+    assert np.array_equal(half.cpu().view(torch.int16).numpy().view(np.uint16), narrow(payloads))
+
+
 def test_bf16_float16_conversions_are_tensor_to(device):
     """bf16 <-> fp16 convert through the exact fp32 value, as ``Tensor.to`` does: round to
     nearest even, fp16 overflow to +-inf, subnormals kept, signed zeros kept."""

@@ -195,3 +195,26 @@ def test_planted_mistakes_fail_the_pins():
     two = _bits(g.clone().mul_(1.0 / 1000.0).mul_(0.3167))
     once = oracle.to_bits(g.float().numpy() * np.float32(1.0 / 1000.0) * np.float32(0.3167), "bfloat16")
     assert not np.array_equal(two, once)
+
+
+def test_f16_nan_rules_are_torchs_vectorised_conversions():
+    """The fp16 NaN rules the device conversions are held to are torch's own vectorised
+    CPU conversions (whole tensors): every fp16 bit pattern widened, and fp32 NaNs of many
+    payloads narrowed, bitwise.  A rule that kept signalling NaNs unquieted, or that
+    narrowed every NaN to sign | 0x7E00, fails here."""
+    widen, narrow = oracle.f16_nan_rules()
+    every = torch.arange(-(2**15), 2**15, dtype=torch.int32).to(torch.int16)
+    bits16 = every.numpy().astype(np.uint16)
+    torch_wide = every.view(torch.float16).to(torch.float32).view(torch.int32).numpy().view(np.uint32)
+    assert np.array_equal(widen(bits16), torch_wide)
+    rng = np.random.default_rng(5)
+    payloads = rng.integers(1, 1 << 23, 4096).astype(np.uint32)
+    nans = (payloads | 0x7F800000) | (rng.integers(0, 2, 4096).astype(np.uint32) << 31)
+    torch_narrow = torch.from_numpy(nans.view(np.float32)).to(torch.float16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(narrow(nans), torch_narrow)
+    # planted: unquieted widening, and a canonical narrowed NaN
+    snan = (bits16.astype(np.uint32) & 0x7E00) == 0x7C00
+    snan &= (bits16.astype(np.uint32) & 0x01FF) != 0
+    assert snan.any() and not np.array_equal(widen(bits16) & ~(snan.astype(np.uint32) << 22), torch_wide)
+    canonical = ((nans >> 16) & 0x8000 | 0x7E00).astype(np.uint16)
+    assert not np.array_equal(canonical, torch_narrow)
