@@ -765,6 +765,41 @@ def bench_checkpoint(steps: int, warmup: int) -> int:
     return 0
 
 
+def _link_ceiling(device, nbytes: int = 1 << 30, reps: int = 3) -> dict:
+    """Host-link rates of plain pinned-memory copies (GB/s): each direction alone and
+    both at once on two streams (per direction), from 32-piece copies of ``nbytes``."""
+    import torch
+
+    n = nbytes // 4
+    host_down = torch.empty(n, dtype=torch.float32, pin_memory=True)
+    host_up = torch.ones(n, dtype=torch.float32, pin_memory=True)
+    dev_src = torch.ones(n, dtype=torch.float32, device=device)
+    dev_dst = torch.empty(n, dtype=torch.float32, device=device)
+    down, up = torch.cuda.Stream(device), torch.cuda.Stream(device)
+    pieces = 32
+
+    def copies(stream, dst, src):
+        with torch.cuda.stream(stream):
+            for a, b in zip(dst.chunk(pieces), src.chunk(pieces)):
+                a.copy_(b, non_blocking=True)
+
+    cases = {
+        "device_to_host": lambda: copies(down, host_down, dev_src),
+        "host_to_device": lambda: copies(up, dev_dst, host_up),
+        "duplex_per_direction": lambda: (copies(down, host_down, dev_src), copies(up, dev_dst, host_up)),
+    }
+    rates = {}
+    for name, fn in cases.items():
+        fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        torch.cuda.synchronize()
+        rates[name] = nbytes * reps / (time.perf_counter() - t0) / 1e9
+    return rates
+
+
 def bench_offload(steps: int, warmup: int) -> int:
     """The headline shard with optimizer state offloaded to pinned host memory.
 
@@ -772,12 +807,15 @@ def bench_offload(steps: int, warmup: int) -> int:
     (8 B) and writes back the master parameter, m and v (12 B) over the host link,
     overlapped with the update of neighbouring chunks.  The roofline is the link:
     PCIe 5.0 x16, 64 GB/s per direction, against the 12 B/param write-back direction.
+    The line also carries the link's measured rates (``_link_ceiling``, before the
+    timed steps): with both directions busy, as in the step, each gets less than alone.
     """
     import torch
 
     from hybrid_training_amd import GroupHandle, OptimizerConfig, ShardedOptimizer
 
     device = torch.device("cuda", 0)
+    link = _link_ceiling(device)
     n = SHARD_NUMEL
     param, grad = _headline_inputs(device, n)
     opt = ShardedOptimizer([param], OptimizerConfig(learning_rate=LR, betas=BETAS, eps=EPS, weight_decay=WD,
@@ -802,6 +840,8 @@ def bench_offload(steps: int, warmup: int) -> int:
                    "shard_numel": n, "link_bytes_per_param": {"host_to_device": 8, "device_to_host": 12}},
         "roofline": {"bound": "pcie", "achieved": link_gbps, "peak": 64.0, "unit": "GB/s",
                      "frac": link_gbps / 64.0, "traffic": None, "traffic_per": "step, device-to-host direction"},
+        "link_measured_gbps": link,
+        "frac_of_measured_duplex": link_gbps / link["duplex_per_direction"],
     }
     print(json.dumps(line), flush=True)
     return 0
