@@ -28,6 +28,15 @@ _NAMES = {torch.float32: "float32", torch.bfloat16: "bfloat16", torch.float16: "
           torch.float64: "float64"}
 
 
+def _host_bits(t: torch.Tensor) -> np.ndarray:
+    """A host copy in the oracle's storage: float32 values, or uint16 bit patterns of a
+    2-byte dtype (compared with np.array_equal, so bits, signed zeros included)."""
+    t = t.detach().cpu().contiguous()
+    if t.element_size() == 2:
+        return t.view(torch.int16).numpy().view(np.uint16).copy()
+    return t.numpy().copy()
+
+
 def _shapes(rng: np.random.Generator) -> list[tuple[int, ...]]:
     shapes = []
     for _ in range(int(rng.integers(1, 12))):
@@ -94,10 +103,11 @@ def test_random_fsdp_configurations(device, case):
 
 @pytest.mark.parametrize("case", range(60))
 def test_random_checkpoint_reshards(device, case):
-    """Random layouts saved by 1-5 writers (fp32, bf16 or fp16) as per-tensor shard records
-    and loaded by 1-6 readers (``checkpoint/reshard.py:200-305``, ``checkpoint/reader.py:328-351``): every
-    reader's shard is the matching slice of the global flat vector, cast to the
-    destination dtype as torch casts it, and its padding tail is left untouched."""
+    """Random layouts saved by 1-5 writers (fp64, fp32, bf16 or fp16) as per-tensor shard
+    records and loaded by 1-6 readers into any of those dtypes (``checkpoint/reshard.py:200-305``,
+    ``:290``; ``checkpoint/reader.py:328-351``): every reader's shard is the matching slice of the
+    global flat vector, cast to the destination dtype as torch's ``Tensor.to`` casts it, and
+    its padding tail is left untouched."""
     from hybrid_training_amd import load_flat_shard
 
     from .test_gpu_reshard import _layout, _save
@@ -105,10 +115,9 @@ def test_random_checkpoint_reshards(device, case):
     rng = np.random.default_rng(5000 + case)
     shapes = _shapes(rng)
     named = [(f"p{i}", s) for i, s in enumerate(shapes)]
-    src_dtype = [torch.float32, torch.bfloat16, torch.float16][int(rng.integers(0, 3))]
-    # Same dtype, or a cast the copy kernel makes (fp32 <-> bf16 / fp16; not bf16 <-> fp16).
-    targets = [src_dtype] + ([torch.bfloat16, torch.float16] if src_dtype == torch.float32 else [torch.float32])
-    dst_dtype = targets[int(rng.integers(0, len(targets)))]
+    dtypes = [torch.float64, torch.float32, torch.bfloat16, torch.float16]
+    src_dtype = dtypes[int(rng.integers(0, 4))]
+    dst_dtype = dtypes[int(rng.integers(0, 4))]
     writers, readers = int(rng.integers(1, 6)), int(rng.integers(1, 7))
     total = sum(int(np.prod(s)) for s in shapes)
     gen = torch.Generator(device=device).manual_seed(case)
@@ -168,10 +177,12 @@ def test_random_ddp_bucket_packs(device, case):
 @pytest.mark.parametrize("case", range(40))
 def test_random_adamw_clip_steps(device, case):
     """Random parameter lists (up to 40 tensors, so launches split at 16, empty ones
-    included), hyperparameters (both branches of torch's lerp), clip thresholds and
-    deferred or in-place clipping, two steps of ``clip_grad_norm`` + ``step``
-    (``optim/sharded_optimizer.py:310-355``): parameters and state bitwise the oracle's
-    AdamW with the clip multiplier formed from the returned norm."""
+    included), master dtypes (fp32, bf16, fp16), hyperparameters (both branches of torch's
+    lerp), clip thresholds and deferred or in-place clipping, two steps of
+    ``clip_grad_norm`` + ``step`` (``optim/sharded_optimizer.py:310-355``): parameters and
+    state bitwise the oracle's AdamW with the clip multiplier formed from the returned
+    norm, and ``.grad`` after the step the oracle's clipped gradient (in place) or the
+    untouched one (deferred)."""
     from hybrid_training_amd import OptimizerConfig, ShardedOptimizer
 
     rng = np.random.default_rng(7000 + case)
@@ -183,38 +194,47 @@ def test_random_adamw_clip_steps(device, case):
     eps = float(rng.choice([1e-8, 1e-6]))
     max_norm = float(rng.choice([1e-3, 0.05, 1.0, 100.0]))
     defer = bool(rng.integers(0, 2))
+    dtype = [torch.float32, torch.float32, torch.bfloat16, torch.float16][int(rng.integers(0, 4))]
+    dt = _NAMES[dtype]
+    g_scale = 0.05 if dtype == torch.float16 else 1e-3  # fp16: keep (1 - beta2) g^2 above its subnormals
+    if dtype == torch.float16:
+        eps = float(rng.choice([1e-4, 1e-3]))  # 1e-8 rounds to 0 in fp16
     gen = torch.Generator(device=device).manual_seed(case)
-    params = [torch.nn.Parameter(torch.randn(n, device=device, generator=gen) * 0.02) for n in sizes]
+    params = [torch.nn.Parameter((torch.randn(n, device=device, generator=gen) * 0.02).to(dtype)) for n in sizes]
     opt = ShardedOptimizer(params, OptimizerConfig(name="adamw", learning_rate=lr, betas=betas, weight_decay=wd,
                                                    eps=eps), norm_group=GroupHandle.trivial(), device=device,
                            defer_clip=defer)
-    P = [p.detach().cpu().numpy().copy() for p in params]
+    P = [_host_bits(p) for p in params]
     M = [np.zeros_like(a) for a in P]
     V = [np.zeros_like(a) for a in P]
-    context = f"case {case}: {len(sizes)} tensors, lr {lr}, betas {betas}, wd {wd}, eps {eps}, clip {max_norm}, defer {defer}"
+    context = (f"case {case}: {len(sizes)} tensors, {dt} masters, lr {lr}, betas {betas}, wd {wd}, eps {eps}, "
+               f"clip {max_norm}, defer {defer}")
     for step in (1, 2):
         for p in params:
-            p.grad = torch.randn(p.shape, device=device, generator=gen) * 1e-3
-        G = [p.grad.detach().cpu().numpy().copy() for p in params]
+            p.grad = (torch.randn(p.shape, device=device, generator=gen) * g_scale).to(dtype)
+        G = [_host_bits(p.grad) for p in params]
         norm = float(opt.clip_grad_norm(max_norm))
         mul = oracle.clip_multiplier(norm, max_norm)
         opt.step()
         sc = oracle.adamw_scalars(lr=lr, beta1=betas[0], beta2=betas[1], eps=eps, weight_decay=wd, step=float(step))
-        for a, g, m, v in zip(P, G, M, V):
-            oracle.adamw_step(a, g, m, v, sc, grad_mul=mul)
+        for p, a, g, m, v in zip(params, P, G, M, V):
+            clipped = np.empty_like(g)
+            oracle.adamw_step(a, g, m, v, sc, grad_mul=mul, dtype=dt, grad_out=clipped)
+            assert np.array_equal(_host_bits(p.grad), g if defer else clipped), (context, step)
     for p, a, m, v in zip(params, P, M, V):
         state = opt.inner.state[p]
-        assert np.array_equal(p.detach().cpu().numpy().view(np.int32), a.view(np.int32)), context
-        assert np.array_equal(state["exp_avg"].cpu().numpy().view(np.int32), m.view(np.int32)), context
-        assert np.array_equal(state["exp_avg_sq"].cpu().numpy().view(np.int32), v.view(np.int32)), context
+        assert np.array_equal(_host_bits(p), a), context
+        assert np.array_equal(_host_bits(state["exp_avg"]), m), context
+        assert np.array_equal(_host_bits(state["exp_avg_sq"]), v), context
 
 
 @pytest.mark.parametrize("case", range(30))
 def test_random_sgd_clip_steps(device, case):
     """Random SGD configurations (momentum, dampening, Nesterov, weight decay, learning
-    rate), parameter lists and clip thresholds, three steps of ``clip_grad_norm`` +
-    ``step`` (``optim/sharded_optimizer.py:121-126``, torch's ``_single_tensor_sgd``):
-    parameters and momentum buffers bitwise the oracle's."""
+    rate), master dtypes (fp32, bf16, fp16), parameter lists and clip thresholds, three
+    steps of ``clip_grad_norm`` + ``step`` (``optim/sharded_optimizer.py:121-126``, torch's
+    ``_single_tensor_sgd``): parameters and momentum buffers bitwise the oracle's, and
+    ``.grad`` the oracle's clipped gradient after an in-place clip."""
     from hybrid_training_amd import OptimizerConfig, ShardedOptimizer
 
     rng = np.random.default_rng(8000 + case)
@@ -226,31 +246,34 @@ def test_random_sgd_clip_steps(device, case):
     wd = float(rng.choice([0.0, 1e-4, 0.01]))
     max_norm = float(rng.choice([0.01, 1.0, 1e3]))
     defer = bool(rng.integers(0, 2))
+    dtype = [torch.float32, torch.float32, torch.bfloat16, torch.float16][int(rng.integers(0, 4))]
+    dt = _NAMES[dtype]
     gen = torch.Generator(device=device).manual_seed(case)
-    params = [torch.nn.Parameter(torch.randn(n, device=device, generator=gen)) for n in sizes]
+    params = [torch.nn.Parameter(torch.randn(n, device=device, generator=gen).to(dtype)) for n in sizes]
     opt = ShardedOptimizer(params, OptimizerConfig(name="sgd", learning_rate=lr, momentum=momentum, weight_decay=wd),
                            norm_group=GroupHandle.trivial(), device=device, defer_clip=defer)
     for group in opt.inner.param_groups:
         group["dampening"] = dampening
         group["nesterov"] = nesterov
-    P = [p.detach().cpu().numpy().copy() for p in params]
-    B = [np.zeros(n, np.float32) for n in sizes] if momentum else [None] * len(sizes)
-    context = (f"case {case}: {len(sizes)} tensors, lr {lr}, momentum {momentum}, dampening {dampening}, "
-               f"nesterov {nesterov}, wd {wd}, clip {max_norm}, defer {defer}")
+    P = [_host_bits(p) for p in params]
+    B = [np.zeros_like(a) for a in P] if momentum else [None] * len(sizes)
+    context = (f"case {case}: {len(sizes)} tensors, {dt} masters, lr {lr}, momentum {momentum}, "
+               f"dampening {dampening}, nesterov {nesterov}, wd {wd}, clip {max_norm}, defer {defer}")
     for step in range(3):
         for p in params:
-            p.grad = torch.randn(p.shape, device=device, generator=gen) * 0.1
-        G = [p.grad.detach().cpu().numpy().copy() for p in params]
+            p.grad = (torch.randn(p.shape, device=device, generator=gen) * 0.1).to(dtype)
+        G = [_host_bits(p.grad) for p in params]
         mul = oracle.clip_multiplier(float(opt.clip_grad_norm(max_norm)), max_norm)
         opt.step()
-        for a, g, b in zip(P, G, B):
+        for p, a, g, b in zip(params, P, G, B):
+            clipped = np.empty_like(g)
             oracle.sgd_step(a, g, b, lr=lr, momentum=momentum, dampening=dampening, weight_decay=wd,
-                            nesterov=nesterov, first=step == 0, grad_mul=mul)
+                            nesterov=nesterov, first=step == 0, grad_mul=mul, dtype=dt, grad_out=clipped)
+            assert np.array_equal(_host_bits(p.grad), g if defer else clipped), (context, step)
     for p, a, b in zip(params, P, B):
-        assert np.array_equal(p.detach().cpu().numpy().view(np.int32), a.view(np.int32)), context
+        assert np.array_equal(_host_bits(p), a), context
         if momentum:
-            buf = opt.inner.state[p]["momentum_buffer"].cpu().numpy()
-            assert np.array_equal(buf.view(np.int32), b.view(np.int32)), context
+            assert np.array_equal(_host_bits(opt.inner.state[p]["momentum_buffer"]), b), context
 
 
 @pytest.mark.parametrize("case", range(30))
