@@ -101,6 +101,78 @@ def test_random_fsdp_configurations(device, case):
         assert np.array_equal(out.cpu().numpy().view(np.int32), expect.view(np.int32)), (context, rank)
 
 
+@pytest.mark.parametrize("case", range(40))
+def test_random_fsdp_units_without_mixed_precision(device, case):
+    """Mixed precision off (``parallel/fsdp.py:379-392``): the master, compute and reduce
+    dtypes are the parameters' own, fp32, bf16 or fp16.  Every rank's shard packs bitwise in
+    that dtype, the gathered tensors come back bitwise, the local share and a two-micro-batch
+    ``no_sync`` reduction are the oracle's in that dtype, and one clipped AdamW step on each
+    rank's shard, with the norm taken from the local share's partials, is the oracle's."""
+    from hybrid_training_amd import OptimizerConfig, ShardedOptimizer
+
+    rng = np.random.default_rng(9000 + case)
+    shapes = _shapes(rng)
+    group = int(rng.integers(1, 10))
+    dtype = [torch.float32, torch.bfloat16, torch.float16][int(rng.integers(0, 3))]
+    dt = _NAMES[dtype]
+    gen = torch.Generator(device=device).manual_seed(case)
+    named = [(f"p{i}", torch.nn.Parameter((torch.randn(s, device=device, generator=gen) * 0.1).to(dtype)))
+             for i, s in enumerate(shapes)]
+    mp = MixedPrecisionConfig(enabled=False)
+    handles = [FlatParamHandle(named, None, GroupHandle.local_view("shard", group, r), FSDPConfig(), mp, device,
+                               keep_originals=True) for r in range(group)]
+    host = [p.detach().float().cpu().numpy() for _, p in named]   # exact widening
+    total = sum(int(np.prod(s)) for s in shapes)
+    shard, padded, _ = oracle.even_shards(total, group)
+    context = f"case {case}: shapes {shapes}, G={group}, {dt} without mixed precision"
+    for rank, h in enumerate(handles):
+        assert h.flat_param.dtype == dtype, context
+        expect = oracle.to_bits(oracle.pack_shard(host, group, rank), dt)
+        assert np.array_equal(_host_bits(h.flat_param), expect), (context, rank)
+    full = handles[0].full_tensors(peer_shards=[h.flat_param for h in handles])
+    for (name, p), values in zip(named, host):
+        assert full[name].dtype == dtype and full[name].shape == p.shape, context
+        assert np.array_equal(_host_bits(full[name]), oracle.to_bits(values, dt).reshape(p.shape)), context
+    grads = [[(torch.randn(padded, device=device, generator=gen) * 0.05).to(dtype) for _ in range(group)]
+             for _ in range(2)]
+    for g in grads[0] + grads[1]:
+        g[total:] = 0.0
+    divisor = float(group) if group > 1 else 1.0
+    wide = [[g.float().cpu().numpy() for g in micro] for micro in grads]
+    for rank, h in enumerate(handles):
+        valid = max(0, min(shard, total - rank * shard))
+        peers = grads[1] if group > 1 else None
+        out = h.reduce_scatter_gradient(grads[1][rank], peer_grads=peers)
+        share = oracle.to_bits(oracle.local_share(wide[1], rank, shard, valid, divisor, dt), dt)
+        assert out.dtype == dtype and np.array_equal(_host_bits(out), share), (context, rank)
+        # one clipped AdamW step on this rank's shard; the norm comes from the share's partials
+        param = h.flat_param
+        param.grad = out
+        opt = ShardedOptimizer([param], OptimizerConfig(learning_rate=1e-3, betas=(0.9, 0.999), eps=1e-3,
+                                                        weight_decay=0.01),
+                               norm_group=GroupHandle.local_view("world", group, rank), device=device)
+        P = _host_bits(param)
+        norm = float(opt.clip_grad_norm(0.01))
+        mul = oracle.clip_multiplier(norm, 0.01)
+        sq = oracle.sqnorm(share, dtype=dt)
+        assert abs(norm - sq ** 0.5) <= 1e-9 * max(norm, 1e-30), (context, rank)
+        opt.step()
+        sc = oracle.adamw_scalars(lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-3, weight_decay=0.01, step=1.0)
+        clipped = np.empty_like(share)
+        oracle.adamw_step(P, share.copy(), np.zeros_like(P), np.zeros_like(P), sc, grad_mul=mul, dtype=dt,
+                          grad_out=clipped)
+        assert np.array_equal(_host_bits(param), P), (context, rank)
+        assert np.array_equal(_host_bits(param.grad), clipped), (context, rank)
+        # no_sync: the first micro-batch accumulates, the second reduces the sums
+        h.set_accumulate_without_reduction(True)
+        assert h.reduce_scatter_gradient(grads[0][rank], peer_grads=grads[0] if group > 1 else None) is None
+        h.set_accumulate_without_reduction(False)
+        out = h.reduce_scatter_gradient(grads[1][rank], peer_grads=peers)
+        totals = [oracle.no_sync_accumulate([wide[m][q] for m in range(2)], dt) for q in range(group)]
+        expect = oracle.to_bits(oracle.local_share(totals, rank, shard, valid, divisor, dt), dt)
+        assert np.array_equal(_host_bits(out), expect), (context, rank)
+
+
 @pytest.mark.parametrize("case", range(60))
 def test_random_checkpoint_reshards(device, case):
     """Random layouts saved by 1-5 writers (fp64, fp32, bf16 or fp16) as per-tensor shard
