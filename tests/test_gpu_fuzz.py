@@ -434,8 +434,9 @@ def test_random_loss_scaled_runs(device, case):
 def test_random_offloaded_runs(device, monkeypatch, case):
     """Optimizer-state offload (``optim/sharded_optimizer.py:284-296``, ``:342-353``) with
     random tensor sizes, chunk sizes (so chunks split tensors at random points and the
-    two staging slots alternate), AdamW or SGD with momentum and deferred or eager
-    clipping: three steps bitwise those of the in-HBM path, state included."""
+    two staging slots alternate), fp32, bf16 or fp16 masters, AdamW or SGD with momentum
+    and deferred or eager clipping: three steps bitwise those of the in-HBM path, state
+    and ``.grad`` included."""
     from hybrid_training_amd import OptimizerConfig, ShardedOptimizer
     from hybrid_training_amd import optim as optim_module
 
@@ -444,33 +445,36 @@ def test_random_offloaded_runs(device, monkeypatch, case):
     sizes = [int(rng.integers(1, 40000)) for _ in range(int(rng.integers(1, 6)))]
     adamw = bool(rng.integers(0, 2))
     defer = bool(rng.integers(0, 2))
-    config = ({"name": "adamw", "learning_rate": 3e-4, "betas": (0.9, 0.95), "weight_decay": 0.1} if adamw
-              else {"name": "sgd", "learning_rate": 0.05, "momentum": 0.9, "weight_decay": 0.01})
+    dtype = [torch.float32, torch.float32, torch.bfloat16, torch.float16][int(rng.integers(0, 4))]
+    config = ({"name": "adamw", "learning_rate": 3e-4, "betas": (0.9, 0.95), "weight_decay": 0.1, "eps": 1e-4}
+              if adamw else {"name": "sgd", "learning_rate": 0.05, "momentum": 0.9, "weight_decay": 0.01})
     gen = torch.Generator(device=device).manual_seed(case)
-    init = [torch.randn(n, device=device, generator=gen) for n in sizes]
+    init = [torch.randn(n, device=device, generator=gen).to(dtype) for n in sizes]
     runs = []
     for offload in (False, True):
         params = [torch.nn.Parameter(t.clone()) for t in init]
         opt = ShardedOptimizer(params, OptimizerConfig(**{**config, "cpu_offload_state": offload}),
                                norm_group=GroupHandle.trivial(), device=device, defer_clip=defer)
         runs.append((params, opt))
-    context = f"case {case}: sizes {sizes}, adamw {adamw}, defer {defer}"
+    context = f"case {case}: sizes {sizes}, {dtype} masters, adamw {adamw}, defer {defer}"
     for step in range(3):
-        grads = [torch.randn(n, device=device, generator=gen) * 0.1 for n in sizes]
+        grads = [(torch.randn(n, device=device, generator=gen) * 0.1).to(dtype) for n in sizes]
         for params, opt in runs:
             for p, g in zip(params, grads):
                 p.grad = g.clone()
             opt.clip_grad_norm(0.5)
             opt.step()
         for a, b in zip(runs[0][0], runs[1][0]):
-            assert torch.equal(a.detach().view(torch.int32), b.detach().view(torch.int32)), (context, step)
+            assert np.array_equal(_host_bits(a), _host_bits(b)), (context, step)
+            assert np.array_equal(_host_bits(a.grad), _host_bits(b.grad)), (context, step)
     saved = [opt.state_dict()["state"] for _, opt in runs]
     for index, entry in saved[0].items():
         for key, value in entry.items():
-            if torch.is_tensor(value):  # every state tensor here is fp32: compare the bits
+            if torch.is_tensor(value):  # compare the bits at the tensor's own width
                 other = saved[1][index][key]
-                assert value.dtype == other.dtype == torch.float32, (context, index, key)
-                assert torch.equal(value.view(torch.int32), other.view(torch.int32)), (context, index, key)
+                assert value.dtype == other.dtype, (context, index, key)
+                assert value.dtype == (torch.float32 if key == "step" else dtype), (context, index, key)
+                assert np.array_equal(_host_bits(value), _host_bits(other)), (context, index, key)
 
 
 @pytest.mark.parametrize("case", range(30))
