@@ -35,30 +35,11 @@ namespace {
 constexpr int kCopyBlock = HBT_COPY_BLOCK;
 constexpr bool kCopyNT = HBT_COPY_NT != 0;
 
-// Aligned vector load/store of NW dwords (NW = 2 or 4), non-temporal when kCopyNT:
-// every byte is moved exactly once.
+// A vector of NW dwords (NW = 2 or 4).
 template <int NW>
 struct Vec {
     typedef uint32_t type __attribute__((ext_vector_type(NW)));
 };
-typedef Vec<4>::type u32x4v;
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-
-template <int NW>
-__device__ __forceinline__ typename Vec<NW>::type ldv(const void* p) {
-    typedef typename Vec<NW>::type V;
-    if constexpr (kCopyNT) return __builtin_nontemporal_load(reinterpret_cast<const V*>(p));
-    return *reinterpret_cast<const V*>(p);
-}
-template <int NW>
-__device__ __forceinline__ void stv(void* p, typename Vec<NW>::type x) {
-    typedef typename Vec<NW>::type V;
-    if constexpr (kCopyNT) {
-        __builtin_nontemporal_store(x, reinterpret_cast<V*>(p));
-    } else {
-        *reinterpret_cast<V*>(p) = x;
-    }
-}
 
 // The copy kernel reads its addresses from a table in device memory, so the compiler
 // cannot tell which address space they point into and would issue flat loads and
@@ -66,6 +47,8 @@ __device__ __forceinline__ void stv(void* p, typename Vec<NW>::type x) {
 // instructions, which wait on the vector counter alone.
 typedef __attribute__((address_space(1))) uint8_t gbyte;
 
+// Aligned vector load/store of NW dwords, non-temporal when kCopyNT: every byte is moved
+// exactly once.
 template <int NW>
 __device__ __forceinline__ typename Vec<NW>::type ldg(const gbyte* p) {
     typedef typename Vec<NW>::type V;
@@ -156,11 +139,6 @@ __device__ __forceinline__ uint32_t convert(uint32_t bits, float divisor) {
     return f32_to_elem<DB, H>(x);
 }
 
-template <int EB, typename B>
-__device__ __forceinline__ uint32_t load_elem(const B* p) {
-    if constexpr (EB == 4) return *reinterpret_cast<const uint32_t*>(p);
-    return *reinterpret_cast<const uint16_t*>(p);
-}
 template <int EB>
 __device__ __forceinline__ uint32_t load_elem(const gbyte* p) {
     typedef __attribute__((address_space(1))) const uint32_t G32;
