@@ -484,6 +484,8 @@ def bench_fsdp(steps: int, warmup: int) -> int:
 
     Pack: the 8 ranks' ``FlatParamHandle`` construction (read bf16 2 B + write fp32
     4 B per param).  Unpack: ``full_tensors`` from the 8 shards (read 4 B + write 4 B).
+    Gather: ``gather_full``, the all-gather's local side, casting the 8 fp32 shards into
+    the padded bf16 compute buffer in one launch (read 4 B + write 2 B).
     Local share: rank 0's ``reduce_scatter_gradient`` over the 8 ranks' padded bf16
     gradients resident on the device (read 8 x 2 B + write 4 B per shard element).
     no_sync: one micro-batch's accumulation of rank 0's slices of the 8 bf16 gradients
@@ -533,6 +535,17 @@ def bench_fsdp(steps: int, warmup: int) -> int:
           8 * total, {"params": total, "world": world, "bytes_per_param": 8},
           _secondary_traffic("fsdp", ["unpack: all 291 tensors from 8 shards"], [1]))
     outputs.clear()
+
+    def gather():
+        handles[0].gather_full(peer_shards=shards)
+
+    ms = _time_events(gather, max(steps, 3), max(warmup, 1))
+    _emit("FSDP gather with cast (gather_full: fp32 shards -> bf16 compute buffer): params/s", "params/s",
+          total / (ms * 1e-3), ms, max(steps, 3), max(warmup, 1), "f32->bf16",
+          f"Llama-3-8B, {world} fp32 master shards -> one padded bf16 compute buffer",
+          6 * total, {"params": total, "world": world, "bytes_per_param": 6},
+          _secondary_traffic("fsdp", ["gather with cast: 8 fp32 shards into the bf16 compute buffer"], [1]))
+    handles[0].reshard()
     del shards
     owner = handles[0]
     handles.clear()
