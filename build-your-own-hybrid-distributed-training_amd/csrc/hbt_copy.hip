@@ -160,9 +160,14 @@ __device__ __forceinline__ void store_elem(gbyte* p, uint32_t bits) {
 // Elements per lane unit: one 16-byte access on the wider side of the copy.
 template <int SB, int DB>
 constexpr int unit_elems() { return 16 / (SB > DB ? SB : DB); }
-// Elements per chunk (per workgroup): 16 bytes of source per lane.
+// Elements per chunk (per workgroup): 16 bytes of source per lane, 32 for a widening
+// 2-byte -> fp32 copy.  A widening chunk writes twice what it reads, and its stores do
+// not hold the workgroup, so with 1 KB of source the workgroups retired faster than
+// their writes drained: bf16 -> fp32 over 4 GB of output ran at 5.9 TB/s with 1 KB of
+// source per workgroup, 6.4 TB/s with 2 KB and 5.9 TB/s with 4 KB.  Doubling the chunk
+// of every pair lost 0.4 TB/s on same-size and narrowing copies.
 template <int SB, int DB>
-constexpr int64_t chunk_elems() { return int64_t(kCopyBlock) * 16 / SB; }
+constexpr int64_t chunk_elems() { return int64_t(kCopyBlock) * 16 / SB * (SB < DB ? 2 : 1); }
 
 // Unpack the U elements held in `words` (SB bytes each) into element bit patterns.
 template <int SB, int U>
@@ -225,7 +230,7 @@ template <int SB, int DB, int OP, bool H>
 __global__ __launch_bounds__(kCopyBlock) void copy_kernel(const int64_t* __restrict__ table,
                                                           int64_t count, float divisor, int64_t chunk_base,
                                                           const int64_t* __restrict__ hints) {
-    static_assert(kCopyBlock == 64, "a workgroup is one wave; its chunk is one wave-wide span of 16-byte source loads");
+    static_assert(kCopyBlock == 64, "a workgroup is one wave; its chunk is whole wave-wide spans of 16-byte source loads");
     const int64_t chunk = chunk_base + static_cast<int64_t>(blockIdx.x);
     const int64_t* rec = table + 4 * owning_record(table, count, chunk, hints);
     const gbyte* src = reinterpret_cast<const gbyte*>(static_cast<uintptr_t>(rec[0]));
@@ -473,7 +478,8 @@ int64_t hbt_copy_chunk_elems(int32_t src_dtype, int32_t dst_dtype) {
     const int dsz = dtype_size(dst_dtype);
     if (ssz == 0 || dsz == 0) return -1;
     if (ssz == 8 && dsz == 8) return -1;  // same-dtype 8-byte data travels as F32 dword pairs
-    return int64_t(kCopyBlock) * 16 / ssz;  // 1 KB of source
+    if (ssz == 2 && dsz == 4) return chunk_elems<2, 4>();  // 2 KB of source (chunk_elems)
+    return int64_t(kCopyBlock) * 16 / ssz;                  // 1 KB of source
 }
 
 int32_t hbt_copy_intervals(const int64_t* table, int64_t count, int64_t total_chunks,

@@ -209,7 +209,8 @@ int32_t hbt_grad_norm_noalloc(const void* const* grads, const int64_t* numels, c
  * where first_chunk is the exclusive prefix sum over records of
  * ceil(numel / hbt_copy_chunk_elems(src_dtype, dst_dtype)), and total_chunks is the
  * sum.  A chunk is 1 KB of source: 128 elements of an 8-byte source, 256 of a 4-byte
- * one, 512 of a 2-byte one; hbt_copy_chunk_elems returns -1 for F64 -> F64 (a same-dtype
+ * one, 512 of a 2-byte one, except 2 KB (1024 elements) for BF16/F16 -> F32, whose
+ * workgroups write twice what they read; hbt_copy_chunk_elems returns -1 for F64 -> F64 (a same-dtype
  * 8-byte copy travels as F32 dword pairs) and for unknown dtypes.  All records share src_dtype/dst_dtype and op:
  *   HBT_COPY_OP_COPY    dst = src               (same dtype: byte copy; F32->BF16
  *                                                rounds to nearest even, NaN -> 0x7FC0;

@@ -67,9 +67,10 @@ def test_library_loads_and_exports_every_declared_symbol():
     assert lib.hbt_norm_partials_count(_native.int64_array([1, 65536, 65537]), 3, 1) == 1 + 1 + 2
     assert lib.hbt_norm_partials_count(None, 99, 0) == -1
     assert lib.hbt_norm_partials_count(_native.int64_array([1]), 1, 7) == -1
-    # 1 KB of source per chunk
+    # 1 KB of source per chunk; 2 KB for the widening 2-byte -> fp32 copies
     assert lib.hbt_copy_chunk_elems(0, 0) == 256 and lib.hbt_copy_chunk_elems(1, 1) == 512
-    assert lib.hbt_copy_chunk_elems(0, 1) == 256 and lib.hbt_copy_chunk_elems(1, 0) == 512
+    assert lib.hbt_copy_chunk_elems(0, 1) == 256 and lib.hbt_copy_chunk_elems(1, 0) == 1024
+    assert lib.hbt_copy_chunk_elems(2, 0) == 1024 and lib.hbt_copy_chunk_elems(0, 2) == 256
     assert lib.hbt_copy_chunk_elems(3, 3) == -1
     assert lib.hbt_last_error() == b""
 
@@ -145,7 +146,7 @@ int main(void) {
     if (hbt_abi_version() != %(abi)d) { printf("abi %%d\n", hbt_abi_version()); failures++; }
     if (hbt_symbol_count() != %(symbols)d) { printf("symbols %%d\n", hbt_symbol_count()); failures++; }
     if (hbt_copy_chunk_elems(HBT_DTYPE_F32, HBT_DTYPE_F32) != 256) failures++;
-    if (hbt_copy_chunk_elems(HBT_DTYPE_BF16, HBT_DTYPE_F32) != 512) failures++;
+    if (hbt_copy_chunk_elems(HBT_DTYPE_BF16, HBT_DTYPE_F32) != 1024) failures++;
     /* refused on the host before any device work: a null table with records */
     if (hbt_copy_intervals(NULL, 1, 1, HBT_DTYPE_F32, HBT_DTYPE_F32, HBT_COPY_OP_COPY, 1.0f, 0, NULL)
         != HBT_ERR_INVALID_ARGUMENT) failures++;
