@@ -541,6 +541,25 @@ __device__ __forceinline__ float share_cast(float x) {
 #define HBT_SHARE_ISSUE 2
 #endif
 constexpr int kShareIssue = HBT_SHARE_ISSUE;
+
+// Where tile t's sum is stored among a launch's `tiles` tile sums.  Workgroup b owns
+// tile b, and the dispatcher deals consecutive workgroups to the 8 XCDs in turn, each
+// with its own L2: stored at index t, every 64-byte line of sums would be written back
+// by eight XCDs in eight partial pieces (measured: 125 MB of writes for 31 MB of sums
+// over a 1e9-element shard).  So the sums of the tiles XCD x runs are stored together:
+// within each launch slice of n tiles, tile b goes to (b mod 8) * (n / 8) + b / 8 (the
+// last n mod 8 keep their index).  Giving each XCD a contiguous eighth of the tiles
+// instead fixes the writes as well but slowed the launch by 2.6%.  The slot is a
+// bijection, and the reader applies the same one, so the partials do not change.
+constexpr int kXcds = 8;
+__device__ __forceinline__ int64_t tile_sum_slot(int64_t t, int64_t tiles) {
+    constexpr int64_t kSlice = kGridMaxItems / kShareBlock;  // launch_sliced's slices
+    const int64_t first = (t / kSlice) * kSlice;
+    const int64_t n = tiles - first < kSlice ? tiles - first : kSlice;
+    const int64_t b = t - first;
+    const int64_t per = n / kXcds;
+    return first + (b < per * kXcds ? (b % kXcds) * per + b / kXcds : b);
+}
 template <int ID, int kG, bool kRecip, int RD, int OD>
 __global__ __launch_bounds__(kShareBlock) void local_share_tiles_kernel(
     ShareRanks ranks, int32_t group_size, int64_t offset, int64_t shard_numel, int64_t valid_numel,
@@ -607,7 +626,7 @@ __global__ __launch_bounds__(kShareBlock) void local_share_tiles_kernel(
     }
     if (tile_sums == nullptr) return;
     acc = wave_sum(acc);
-    if (threadIdx.x == 0) tile_sums[tile] = acc;
+    if (threadIdx.x == 0) tile_sums[tile_sum_slot(tile, (shard_numel + kShareTile - 1) / kShareTile)] = acc;
 }
 
 // Reduce dtype float64: each rank's element widens exactly to double (IB = 8 reads a
@@ -639,15 +658,16 @@ __global__ __launch_bounds__(kShareBlock) void local_share_f64_tiles_kernel(
     }
     if (tile_sums == nullptr) return;
     acc = wave_sum(acc);
-    if (threadIdx.x == 0) tile_sums[tile] = acc;
+    if (threadIdx.x == 0) tile_sums[tile_sum_slot(tile, (shard_numel + kShareTile - 1) / kShareTile)] = acc;
 }
 
 // Chunk c < valid_chunks: the sum of its kTiles tile sums (those below valid_tiles), lane
 // l adding tiles l, l + 64, ... in order before the butterfly; padding chunks: 0, the
-// square sum of zeros.
+// square sum of zeros.  `tiles` is the tile count of the launch that wrote the sums
+// (their slots, tile_sum_slot); a chunk's sums lie in 8 runs of kTiles / 8 slots.
 template <int kTiles>
 __global__ __launch_bounds__(kShareBlock) void tile_sums_to_partials_kernel(
-    const double* __restrict__ tile_sums, int64_t valid_tiles, int64_t valid_chunks,
+    const double* __restrict__ tile_sums, int64_t tiles, int64_t valid_tiles, int64_t valid_chunks,
     double* __restrict__ partials, int64_t block_base) {
     const int64_t chunk = block_base + blockIdx.x;
     double acc = 0.0;
@@ -656,7 +676,7 @@ __global__ __launch_bounds__(kShareBlock) void tile_sums_to_partials_kernel(
 #pragma unroll
         for (int k = 0; k < kTiles / kShareBlock; ++k) {
             const int64_t a = first + int64_t(k) * kShareBlock;
-            if (a < valid_tiles) acc += tile_sums[a];
+            if (a < valid_tiles) acc += tile_sums[tile_sum_slot(a, tiles)];
         }
     }
     acc = wave_sum(acc);
@@ -1042,10 +1062,10 @@ int32_t local_share(const char* who, const void* const* rank_grads, int32_t grou
     return launch_sliced(who, valid_chunks + pad_chunks, kShareBlock, [&](int64_t first, dim3 grid) {
         if (out_dtype == F32) {
             tile_sums_to_partials_kernel<tiles_per_norm_chunk<F32>()><<<grid, kShareBlock, 0, st>>>(
-                tile_scratch, valid_tiles, valid_chunks, partials, first);
+                tile_scratch, tiles, valid_tiles, valid_chunks, partials, first);
         } else {
             tile_sums_to_partials_kernel<tiles_per_norm_chunk<BF16>()><<<grid, kShareBlock, 0, st>>>(
-                tile_scratch, valid_tiles, valid_chunks, partials, first);
+                tile_scratch, tiles, valid_tiles, valid_chunks, partials, first);
         }
     });
 }

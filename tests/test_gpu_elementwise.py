@@ -104,6 +104,46 @@ def test_local_share_tiles(device, in_dtype, group, misaligned, reduce, master):
     assert float(out_storage[:lead].float().sum()) == 7.0 * lead  # nothing written before the output
 
 
+@pytest.mark.parametrize("master", [torch.float32, torch.bfloat16])
+def test_local_share_partials_chunk_by_chunk(device, master):
+    """Each norm partial of ``hbt_grad_local_share_sqnorm`` is the squared norm of its own
+    chunk of the output: chunks of 32,768 fp32 (65,536 2-byte) elements from 0 up to
+    ``valid``, then zero partials over the padding.  The shard spans many chunks and 1,172
+    tiles, so a tile sum counted in the wrong chunk (the sums are stored in a permuted
+    order and read back through it) changes individual partials, which a check of their
+    total would not see.  Each partial is within 1e-12 of a brute-force fp64 sum."""
+    import math
+
+    lib = _native.library()
+    group, shard, valid = 4, 300_000, 250_001
+    gen = torch.Generator(device=device).manual_seed(17)
+    grads = [(torch.randn(group * shard, device=device, generator=gen) * 1e-2).to(torch.bfloat16)
+             for _ in range(group)]
+    host = [g.float().cpu().numpy() for g in grads]
+    out = torch.empty(shard, device=device, dtype=master)
+    chunk = 32768 if master == torch.float32 else 65536
+    valid_chunks, pad_chunks = -(-valid // chunk), -(-(shard - valid) // chunk)
+    partials = torch.full((valid_chunks + pad_chunks,), 7.0, dtype=torch.float64, device=device)
+    tile_sums = torch.empty(-(-shard // 256), dtype=torch.float64, device=device)
+    for rank in (0, group - 1):
+        status = lib.hbt_grad_local_share_sqnorm(
+            _native.pointer_array([g.data_ptr() for g in grads]), group, rank, shard, valid,
+            _native.dtype_code(torch.bfloat16), _native.dtype_code(torch.float32), float(group),
+            _native.dtype_code(master), ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(partials.data_ptr()),
+            ctypes.c_void_p(tile_sums.data_ptr()), ctypes.c_void_p(_native.stream_of(device)),
+        )
+        _native.check(status, "test.local_share_sqnorm")
+        values = out.double().cpu().numpy()
+        got = partials.cpu().numpy()
+        for c in range(valid_chunks):
+            ref = math.fsum(float(x) * float(x) for x in values[c * chunk : min((c + 1) * chunk, valid)])
+            assert abs(got[c] - ref) <= 1e-12 * ref, (rank, c, got[c], ref)
+        assert np.all(got[valid_chunks:] == 0.0) and np.all(values[valid:] == 0.0), rank
+        expect = oracle.local_share(host, rank, shard, valid, float(group))
+        assert np.array_equal(values.astype(np.float32), oracle.from_bits(oracle.to_bits(expect, _REDUCE[master]),
+                                                                         _REDUCE[master])), rank
+
+
 def _scale_reference(t: torch.Tensor, unscale: float, mul: float) -> torch.Tensor:
     """The reference's two in-place multiplies by Python floats, on the CPU in t's dtype."""
     return t.detach().cpu().clone().mul_(unscale).mul_(mul)
