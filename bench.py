@@ -433,8 +433,13 @@ def bench_reshard(steps: int, warmup: int) -> int:
 def bench_scaler(steps: int, warmup: int) -> int:
     """One Llama-3-70B FSDP rank at W=8: 8,819,213,312 fp32 master params, bf16 grads at scale 2^16.
 
-    Clean step: fused unscale + inf check + norm (2 B/param) and unscale + clip + AdamW
-    (26 B/param) = 28 B/param.  Overflowing step: the check pass only (2 B/param), then skip.
+    Clean step with the multipliers deferred (``defer_unscale``, ``defer_clip``): fused
+    unscale + inf check + norm (2 B/param) and unscale + clip + AdamW (26 B/param) =
+    28 B/param.  Overflowing step: the check pass only (2 B/param), then skip.  Clean step
+    with the reference's placement (the defaults): ``unscale_`` rewrites the gradient
+    (read and write bf16: 4 B/param), the norm pass (2 B) and the update, which writes the
+    clipped gradient back (26 + 2 B) = 34 B/param; the gradient is restored from a pristine
+    copy before each such step, outside the timed events.
     """
     import torch
 
@@ -454,6 +459,7 @@ def bench_scaler(steps: int, warmup: int) -> int:
                            norm_group=GroupHandle.trivial("world"), device=device, defer_clip=True)
     scaler = GradScaler(GradScalerConfig(enabled=True, init_scale=65536.0, growth_interval=10**9),
                         GroupHandle.trivial("world"), device, defer_unscale=True)
+    pristine = grad.clone()
 
     def engine_step():
         param.grad = grad
@@ -476,6 +482,42 @@ def bench_scaler(steps: int, warmup: int) -> int:
           max(steps, 5), max(warmup, 2), "bf16", "Llama-3-70B FSDP rank shard at W=8, bf16 grads, 0.1% inf",
           2 * n, {"params": n, "bytes_per_param": 2, "skipped": True},
           _secondary_traffic("scaler", ["unscale + check + norm"], [1]))
+    # The reference's placement: eager unscale_, the clip written back by the update.
+    del opt, scaler
+    torch.cuda.empty_cache()
+    opt = ShardedOptimizer([param], OptimizerConfig(learning_rate=3e-4, betas=(0.9, 0.95), weight_decay=0.1),
+                           norm_group=GroupHandle.trivial("world"), device=device)
+    scaler = GradScaler(GradScalerConfig(enabled=True, init_scale=65536.0, growth_interval=10**9),
+                        GroupHandle.trivial("world"), device)
+    stream = torch.cuda.current_stream(device)
+
+    def eager_step(events=None):
+        grad.copy_(pristine)  # the next backward's gradient (outside the timed events)
+        if events is not None:
+            events[0].record(stream)
+        param.grad = grad
+        scaler.unscale_([param])
+        opt.clip_grad_norm(1.0)
+        scaler.step(opt, [param], already_unscaled=True)
+        scaler.update(found_non_finite=False)
+        if events is not None:
+            events[1].record(stream)
+        opt.zero_grad(set_to_none=True)
+
+    eager_steps, eager_warmup = max(steps, 5), max(warmup, 2)
+    for _ in range(eager_warmup):
+        eager_step()
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(eager_steps)]
+    for e in events:
+        eager_step(e)
+    torch.cuda.synchronize()
+    ms = sum(e[0].elapsed_time(e[1]) for e in events) / eager_steps
+    if bool(torch.equal(grad[:4096], pristine[:4096])):  # the reference's in-place ops rewrite .grad
+        raise RuntimeError("the eager unscale and clip left .grad unchanged")
+    _emit("loss-scaled clipped AdamW step, reference placement (eager unscale_, clip written back): params/s",
+          "params/s", n / (ms * 1e-3), ms, eager_steps, eager_warmup, "f32",
+          "Llama-3-70B FSDP rank shard at W=8, bf16 grads, scale 2^16, defer_unscale=False, defer_clip=False",
+          34 * n, {"params": n, "bytes_per_param": 34, "skipped": False}, None)
     return 0
 
 
@@ -499,9 +541,7 @@ def bench_fsdp(steps: int, warmup: int) -> int:
     world = 8
     shapes = _llama3_shapes(32, 4096, 14336, 1024, 128256)
     gen = torch.Generator(device=device).manual_seed(5)
-    # Finite bf16 bit patterns of magnitude < 2 (exponent field below 0x80).
-    named = [(name, torch.nn.Parameter(torch.randint(-16000, 16000, shape, dtype=torch.int16, device=device,
-                                                      generator=gen).view(torch.bfloat16)))
+    named = [(name, torch.nn.Parameter(torch.randn(shape, dtype=torch.bfloat16, device=device, generator=gen)))
              for name, shape in shapes]
     total = sum(p.numel() for _, p in named)
     mp = MixedPrecisionConfig(enabled=True, param_dtype="bfloat16", reduce_dtype="float32", master_dtype="float32")
@@ -551,8 +591,7 @@ def bench_fsdp(steps: int, warmup: int) -> int:
     handles.clear()
     torch.cuda.empty_cache()
     padded = owner.padded_numel
-    grads = [torch.randint(-16000, 16000, (padded,), dtype=torch.int16, device=device, generator=gen)
-             .view(torch.bfloat16) for _ in range(world)]
+    grads = [torch.randn(padded, dtype=torch.bfloat16, device=device, generator=gen).mul_(1e-3) for _ in range(world)]
 
     def share():
         return owner.reduce_scatter_gradient(grads[0], peer_grads=grads)

@@ -8,6 +8,9 @@ is native:
 * ``unscale_`` multiplies each gradient by ``fp32(1/scale)`` in its own dtype
   (``hbt_scale_inplace``, as ``grad.mul_(inverse)`` does) and checks finiteness with
   one fp64 norm pass: the sum of squares is non-finite exactly when some element is.
+  That pass leaves its per-chunk partials on the gradients, so the optimizer's
+  ``clip_grad_norm`` that follows takes the norm from them without reading the
+  gradients a second time.
 * With ``defer_unscale=True`` the multiply is not applied to ``.grad`` here; the
   factor travels with each gradient tensor and the optimizer's norm pass and fused
   update pass apply it while they read the gradient, rounding the product to the
@@ -95,7 +98,9 @@ def _nonfinite_flag(params: Sequence[nn.Parameter]) -> torch.Tensor | None:
     if not grads:
         return None
     segments = [(g, 0, int(g.numel()), 1.0) for g in grads]
-    return gradient_norm_pass(segments, grads[0].device, max_norm=0.0).nonfinite
+    # The pass's partials stay on the gradients: an optimizer clipping the same,
+    # unchanged gradients next (the engine's order) reads them instead of the gradients.
+    return gradient_norm_pass(segments, grads[0].device, max_norm=0.0, tag=True).nonfinite
 
 
 class GradScaler:

@@ -282,6 +282,7 @@ def gradient_norm_pass(
     device: torch.device,
     *,
     max_norm: float,
+    tag: bool = False,
 ) -> NormResult:
     """Weighted fp64 squared norm of gradient segments, plus the clip multiplier.
 
@@ -289,7 +290,10 @@ def gradient_norm_pass(
     pending loss-scale factor is read through that factor.  Segments are batched
     by (dtype, factor) into launches of at most 16; every launch writes its own
     run of per-chunk partials and one finalize launch sums all of them in a fixed
-    order.
+    order.  With ``tag``, every segment of weight 1 read without a pending factor
+    leaves its partials on its gradient (:class:`NormPartials`), so a later pass over
+    the unchanged gradient, such as the clip after the loss scaler's overflow check,
+    reuses them instead of reading the gradient again.
     """
     lib = _native.library()
     batches: dict[tuple[torch.dtype, float], list[tuple[torch.Tensor, int, int, float]]] = {}
@@ -321,6 +325,7 @@ def gradient_norm_pass(
             launches.append((dtype, unscale, chunk, total_partials))
             total_partials += count
     partials = torch.empty(max(1, total_partials), dtype=torch.float64, device=device)
+    fresh: list[tuple[torch.Tensor, int, int, int, int]] = []  # segments whose partials are tagged
     outputs = torch.empty(2, dtype=torch.float64, device=device)
     grad_mul = torch.empty(1, dtype=torch.float32, device=device)
     nonfinite = torch.empty(1, dtype=torch.int32, device=device)
@@ -337,6 +342,8 @@ def gradient_norm_pass(
             for grad, offset, length, weight in items:
                 count = int(lib.hbt_norm_partials_count(_native.int64_array([length]), 1, _native.dtype_code(dtype)))
                 cached = _cached_partials(grad, offset, length, unscale)
+                if tag and cached is None and weight == 1.0 and unscale == 1.0:
+                    fresh.append((grad, offset, length, slot, count))
                 if cached is not None and cached.numel() == count:
                     _launch_sqnorm(lib, pending, dtype, unscale, partials, pending_first, stream)
                     pending = []
@@ -363,6 +370,16 @@ def gradient_norm_pass(
             stream,
         )
         _native.check(status, "optim.hbt_grad_norm_finalize")
+    records: dict[int, tuple[torch.Tensor, dict[tuple[int, int], torch.Tensor]]] = {}
+    for grad, offset, length, slot, count in fresh:
+        records.setdefault(id(grad), (grad, {}))[1][(offset, length)] = partials[slot : slot + count]
+    for grad, found in records.values():
+        record = getattr(grad, NORM_PARTIALS_ATTR, None)
+        if record is not None and (record.data_ptr, record.version, record.dtype) == (
+                grad.data_ptr(), grad._version, grad.dtype):
+            record.segments.update(found)  # keep a producer's still-valid segments
+        else:
+            setattr(grad, NORM_PARTIALS_ATTR, NormPartials(grad.data_ptr(), grad._version, found, grad.dtype))
     return NormResult(sum=outputs[0], norm=outputs[1], grad_mul=grad_mul, nonfinite=nonfinite)
 
 

@@ -227,3 +227,47 @@ def test_bf16_engine_sequence_eager_and_deferred_match_the_oracle(device, name):
         results[(defer_unscale, defer_clip)] = param.detach().cpu()
     first = results[(False, False)]
     assert all(torch.equal(first, r) for r in results.values())
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_eager_unscale_partials_feed_the_clip_norm(device, monkeypatch, dtype):
+    """After an eager ``unscale_``, the overflow check's norm pass leaves its partials on
+    the gradients, and ``clip_grad_norm`` on the unchanged gradients reads no gradient: it
+    launches no norm kernel, and its norm and multiplier are bitwise those of a pass over
+    untagged copies.  An in-place change to one gradient drops that gradient's partials
+    (its version counter moves), and only that gradient is read again."""
+    from hybrid_training_amd import optim as optim_module
+
+    gen = torch.Generator(device=device).manual_seed(33)
+    sizes = [100_003, 70_000, 1]
+    params = [torch.nn.Parameter(torch.randn(n, device=device, generator=gen)) for n in sizes]
+    for p in params:
+        p.grad_dtype = None
+        p.grad = (torch.randn(p.numel(), device=device, generator=gen) * 1000.0).to(dtype)
+    copies = [torch.nn.Parameter(p.detach().clone()) for p in params]
+    opt = ShardedOptimizer(params, OptimizerConfig(), norm_group=GroupHandle.trivial(), device=device)
+    scaler = GradScaler(GradScalerConfig(enabled=True, init_scale=1000.0), GroupHandle.trivial(), device)
+    assert not scaler.unscale_(params)
+    for c, p in zip(copies, params):
+        c.grad_dtype = None
+        c.grad = p.grad.clone()  # the unscaled values, without partials attached
+    launched = []
+    real = optim_module._launch_sqnorm
+
+    def counting(lib, items, *args):
+        launched.extend(g.numel() for g, _, _, _ in items)
+        return real(lib, items, *args)
+
+    monkeypatch.setattr(optim_module, "_launch_sqnorm", counting)
+    norm = opt.clip_grad_norm(1.0)
+    assert launched == []  # every segment came from the scaler's partials
+    ref_opt = ShardedOptimizer(copies, OptimizerConfig(), norm_group=GroupHandle.trivial(), device=device)
+    ref = ref_opt.clip_grad_norm(1.0)
+    assert sorted(launched) == sorted(sizes)  # the copies were read
+    assert float(norm) == float(ref)  # the clip multiplier is derived from the same fp64 sum
+    launched.clear()
+    params[1].grad.mul_(1.0)  # an in-place op: the version counter moves
+    # a fresh optimizer (the first one holds a pending clip, which refuses changed gradients)
+    again = ShardedOptimizer(params, OptimizerConfig(), norm_group=GroupHandle.trivial(), device=device)
+    assert float(again.clip_grad_norm(1.0)) == float(ref)
+    assert launched == [sizes[1]]
