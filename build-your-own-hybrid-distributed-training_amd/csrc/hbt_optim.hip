@@ -718,14 +718,18 @@ __global__ __launch_bounds__(kFinalBlock) void norm_finalize_kernel(
 }
 
 // ---- in-place scaling ---------------------------------------------------------------
-// Half-wave (32-thread) workgroups, two 16-byte vectors per lane: 256 fp32 or 512
-// bf16/fp16 elements per workgroup.  Measured on MI355X (in-place, 1e9 fp32): 6.8 TB/s,
-// against 6.0 TB/s for 64 threads with one vector and 5.5 TB/s with two.
-constexpr int kScaleBlock = 32;
+// Two 16-byte vectors per lane, in half-wave (32-thread) workgroups for fp32 (256
+// elements each) and full-wave workgroups for bf16/fp16 (1024 elements each), whose two
+// rounded multiplies per element keep the ALUs busier.  Measured on MI355X, in place
+// over 4 GB: fp32 6.68 TB/s with 32 threads against 6.06 with 64 (one vector) and 5.41
+// (two); bf16 6.17-6.26 TB/s with 64 threads against 4.9-5.2 with 32.
+template <int D>
+constexpr int scale_block() { return D == F32 ? 32 : 64; }
+constexpr int kScaleUnroll = 2;
 template <int D>
 constexpr int scale_vec() { return D == F32 ? 4 : 8; }
 template <int D>
-constexpr int64_t scale_tile() { return int64_t(kScaleBlock) * 2 * scale_vec<D>(); }
+constexpr int64_t scale_tile() { return int64_t(scale_block<D>()) * kScaleUnroll * scale_vec<D>(); }
 
 struct ScaleTable {
     void* x[kMaxT];
@@ -742,9 +746,10 @@ __device__ __forceinline__ float scale_one(float x, float unscale, float mul) {
 }
 
 template <int D>
-__global__ __launch_bounds__(kScaleBlock) void scale_kernel(ScaleTable tab, float unscale,
+__global__ __launch_bounds__(64) void scale_kernel(ScaleTable tab, float unscale,
                                                             const float* __restrict__ grad_mul, int64_t block_base) {
     constexpr int K = scale_vec<D>();
+    constexpr int kScaleBlock = scale_block<D>();
     constexpr int64_t kTile = scale_tile<D>();
     const int64_t block = block_base + blockIdx.x;
     const int t = owning_tensor(tab.first_block, tab.count, block);
@@ -753,11 +758,11 @@ __global__ __launch_bounds__(kScaleBlock) void scale_kernel(ScaleTable tab, floa
     const float mul = grad_mul != nullptr ? *grad_mul : 1.0f;
     void* X = tab.x[t];
     if (tab.vec_ok[t] && base + kTile <= n) {
-        float v[2][K];
+        float v[kScaleUnroll][K];
 #pragma unroll
-        for (int u = 0; u < 2; ++u) load_vec<D, K>(X, base + (int64_t(u) * kScaleBlock + threadIdx.x) * K, v[u]);
+        for (int u = 0; u < kScaleUnroll; ++u) load_vec<D, K>(X, base + (int64_t(u) * kScaleBlock + threadIdx.x) * K, v[u]);
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
+        for (int u = 0; u < kScaleUnroll; ++u) {
 #pragma unroll
             for (int c = 0; c < K; ++c) v[u][c] = scale_one<D>(v[u][c], unscale, mul);
             store_vec<D, K>(X, base + (int64_t(u) * kScaleBlock + threadIdx.x) * K, v[u]);
@@ -774,7 +779,8 @@ __global__ __launch_bounds__(kScaleBlock) void scale_kernel(ScaleTable tab, floa
 // rounded once (add_).  kAssign writes R(grad) instead: the first micro-batch's clone.
 // The scale kernel's shape: half-wave workgroups, two 4-element vectors per lane,
 // 256 accumulator elements per workgroup.
-constexpr int64_t kAccumTile = int64_t(kScaleBlock) * 2 * 4;
+constexpr int kAccumBlock = 32;  // half-wave workgroups, two 4-element vectors per lane
+constexpr int64_t kAccumTile = int64_t(kAccumBlock) * 2 * 4;
 
 struct AccumTable {
     void* acc[kMaxT];
@@ -787,7 +793,7 @@ struct AccumTable {
 
 // GD: the gradient's dtype; AD: the accumulator's.
 template <int GD, int AD, bool kAssign>
-__global__ __launch_bounds__(kScaleBlock) void accumulate_kernel(AccumTable tab, int64_t block_base) {
+__global__ __launch_bounds__(kAccumBlock) void accumulate_kernel(AccumTable tab, int64_t block_base) {
     const int64_t block = block_base + blockIdx.x;
     const int t = owning_tensor(tab.first_block, tab.count, block);
     const int64_t base = (block - tab.first_block[t]) * kAccumTile;
@@ -798,13 +804,13 @@ __global__ __launch_bounds__(kScaleBlock) void accumulate_kernel(AccumTable tab,
         float a[2][4], g[2][4];
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-            load_vec<GD, 4>(grad, base + (int64_t(u) * kScaleBlock + threadIdx.x) * 4, g[u]);
+            load_vec<GD, 4>(grad, base + (int64_t(u) * kAccumBlock + threadIdx.x) * 4, g[u]);
 #pragma unroll
             for (int c = 0; c < 4; ++c) g[u][c] = share_cast<GD, AD>(g[u][c]);
         }
         if constexpr (!kAssign) {
 #pragma unroll
-            for (int u = 0; u < 2; ++u) load_vec<AD, 4>(acc, base + (int64_t(u) * kScaleBlock + threadIdx.x) * 4, a[u]);
+            for (int u = 0; u < 2; ++u) load_vec<AD, 4>(acc, base + (int64_t(u) * kAccumBlock + threadIdx.x) * 4, a[u]);
         }
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
@@ -812,12 +818,12 @@ __global__ __launch_bounds__(kScaleBlock) void accumulate_kernel(AccumTable tab,
 #pragma unroll
                 for (int c = 0; c < 4; ++c) g[u][c] = round_to<AD>(a[u][c] + g[u][c]);
             }
-            store_vec<AD, 4>(acc, base + (int64_t(u) * kScaleBlock + threadIdx.x) * 4, g[u]);
+            store_vec<AD, 4>(acc, base + (int64_t(u) * kAccumBlock + threadIdx.x) * 4, g[u]);
         }
         return;
     }
     const int64_t end = base + kAccumTile < n ? base + kAccumTile : n;
-    for (int64_t i = base + threadIdx.x; i < end; i += kScaleBlock) {
+    for (int64_t i = base + threadIdx.x; i < end; i += kAccumBlock) {
         const float g = share_cast<GD, AD>(load_one<GD>(grad, i));
         store_one<AD>(acc, i, kAssign ? g : round_to<AD>(load_one<AD>(acc, i) + g));
     }
@@ -826,7 +832,7 @@ __global__ __launch_bounds__(kScaleBlock) void accumulate_kernel(AccumTable tab,
 // Accumulator float64: the gradient widens exactly (Tensor.to) and each add runs in
 // double, as add_ on float64 tensors does; kAssign writes the widened gradient.
 template <int SB, bool SH, bool kAssign>
-__global__ __launch_bounds__(kScaleBlock) void accumulate_f64_kernel(AccumTable tab, int64_t block_base) {
+__global__ __launch_bounds__(kAccumBlock) void accumulate_f64_kernel(AccumTable tab, int64_t block_base) {
     const int64_t block = block_base + blockIdx.x;
     const int t = owning_tensor(tab.first_block, tab.count, block);
     const int64_t base = (block - tab.first_block[t]) * kAccumTile;
@@ -834,7 +840,7 @@ __global__ __launch_bounds__(kScaleBlock) void accumulate_f64_kernel(AccumTable 
     double* __restrict__ acc = static_cast<double*>(tab.acc[t]);
     const unsigned char* __restrict__ grad = static_cast<const unsigned char*>(tab.grad[t]);
     const int64_t end = base + kAccumTile < n ? base + kAccumTile : n;
-    for (int64_t i = base + threadIdx.x; i < end; i += kScaleBlock) {
+    for (int64_t i = base + threadIdx.x; i < end; i += kAccumBlock) {
         const double g = widen_f64<SB, SH>(grad, i);
         acc[i] = kAssign ? g : acc[i] + g;
     }
@@ -1277,10 +1283,11 @@ int32_t hbt_scale_inplace(void* const* tensors, const int64_t* numels, int32_t c
     tab.first_block[count] = blocks;
     for (int i = count + 1; i <= kMaxT; ++i) tab.first_block[i] = blocks;
     hipStream_t st = as_stream(stream);
-    return launch_sliced("hbt_scale_inplace", blocks, kScaleBlock, [&](int64_t first, dim3 grid) {
-        if (dtype == F32) scale_kernel<F32><<<grid, kScaleBlock, 0, st>>>(tab, unscale, grad_mul, first);
-        else if (dtype == BF16) scale_kernel<BF16><<<grid, kScaleBlock, 0, st>>>(tab, unscale, grad_mul, first);
-        else scale_kernel<F16><<<grid, kScaleBlock, 0, st>>>(tab, unscale, grad_mul, first);
+    const int threads = dtype == F32 ? scale_block<F32>() : scale_block<BF16>();
+    return launch_sliced("hbt_scale_inplace", blocks, threads, [&](int64_t first, dim3 grid) {
+        if (dtype == F32) scale_kernel<F32><<<grid, threads, 0, st>>>(tab, unscale, grad_mul, first);
+        else if (dtype == BF16) scale_kernel<BF16><<<grid, threads, 0, st>>>(tab, unscale, grad_mul, first);
+        else scale_kernel<F16><<<grid, threads, 0, st>>>(tab, unscale, grad_mul, first);
     });
 }
 
@@ -1325,11 +1332,11 @@ int32_t hbt_grad_accumulate(void* const* accumulators, const void* const* grads,
     for (int i = count + 1; i <= kMaxT; ++i) tab.first_block[i] = blocks;
     hipStream_t st = as_stream(stream);
     const bool assign = (flags & HBT_ACCUMULATE_ASSIGN) != 0;
-    return launch_sliced("hbt_grad_accumulate", blocks, kScaleBlock, [&](int64_t first, dim3 grid) {
+    return launch_sliced("hbt_grad_accumulate", blocks, kAccumBlock, [&](int64_t first, dim3 grid) {
 #define HBT_ACC(GD, AD)                                                                        \
     do {                                                                                       \
-        if (assign) accumulate_kernel<GD, AD, true><<<grid, kScaleBlock, 0, st>>>(tab, first); \
-        else accumulate_kernel<GD, AD, false><<<grid, kScaleBlock, 0, st>>>(tab, first);       \
+        if (assign) accumulate_kernel<GD, AD, true><<<grid, kAccumBlock, 0, st>>>(tab, first); \
+        else accumulate_kernel<GD, AD, false><<<grid, kAccumBlock, 0, st>>>(tab, first);       \
     } while (0)
 #define HBT_ACC_A(GD)                                  \
     do {                                               \
@@ -1339,8 +1346,8 @@ int32_t hbt_grad_accumulate(void* const* accumulators, const void* const* grads,
     } while (0)
 #define HBT_ACC64(SB, SH)                                                                          \
     do {                                                                                           \
-        if (assign) accumulate_f64_kernel<SB, SH, true><<<grid, kScaleBlock, 0, st>>>(tab, first); \
-        else accumulate_f64_kernel<SB, SH, false><<<grid, kScaleBlock, 0, st>>>(tab, first);       \
+        if (assign) accumulate_f64_kernel<SB, SH, true><<<grid, kAccumBlock, 0, st>>>(tab, first); \
+        else accumulate_f64_kernel<SB, SH, false><<<grid, kAccumBlock, 0, st>>>(tab, first);       \
     } while (0)
         if (f64) {
             if (grad_dtype == HBT_DTYPE_F64) HBT_ACC64(8, false);
