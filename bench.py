@@ -517,7 +517,10 @@ def bench_scaler(steps: int, warmup: int) -> int:
     _emit("loss-scaled clipped AdamW step, reference placement (eager unscale_, clip written back): params/s",
           "params/s", n / (ms * 1e-3), ms, eager_steps, eager_warmup, "f32",
           "Llama-3-70B FSDP rank shard at W=8, bf16 grads, scale 2^16, defer_unscale=False, defer_clip=False",
-          34 * n, {"params": n, "bytes_per_param": 34, "skipped": False}, None)
+          34 * n, {"params": n, "bytes_per_param": 34, "skipped": False},
+          _secondary_traffic("scaler", ["reference placement: eager unscale_",
+                                        "reference placement: overflow check (its partials feed the clip)",
+                                        "reference placement: clip + AdamW, clipped g written back"], [1, 1, 1]))
     return 0
 
 
