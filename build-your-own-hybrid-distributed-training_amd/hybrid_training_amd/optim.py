@@ -648,10 +648,11 @@ class ShardedOptimizer:
             raise ShardingError(
                 format_error(
                     "optim.ShardedOptimizer",
-                    "gradients changed between a deferred clip and the step, so the clip "
-                    "can no longer be applied where the reference would have applied it",
-                    resolution="construct the optimizer with defer_clip=False when gradients "
-                    "are modified after clip_grad_norm()",
+                    "gradients changed between clip_grad_norm() and the step, which applies the "
+                    "clip, so the clip can no longer be applied where the reference applies it",
+                    resolution="call materialize_pending() right after clip_grad_norm() when the "
+                    "gradients are modified before the step: it clips them in place, as the "
+                    "reference's clip_grad_norm does",
                 )
             )
         return True

@@ -245,6 +245,41 @@ def test_clip_is_in_place_like_the_reference(device):
     assert torch.equal(results["write_back"], results["defer"])
 
 
+def test_gradients_changed_after_the_clip(device):
+    """The step applies the clip ``clip_grad_norm`` computed.  A gradient changed in place
+    in between (its version counter moves) can no longer be clipped where the reference
+    clipped it, so the step refuses rather than clipping the changed values; after
+    ``materialize_pending`` (the reference's in-place clip, done at once) the same change
+    is fine, and the result is the reference's clip-then-change sequence, bitwise."""
+    from hybrid_training_amd.errors import ShardingError
+
+    gen = torch.Generator(device=device).manual_seed(8)
+    g0 = torch.randn(10_000, device=device, generator=gen)
+    p0 = torch.randn(10_000, device=device, generator=gen) * 0.02
+    param = torch.nn.Parameter(p0.clone())
+    param.grad = g0.clone()
+    opt = _make_optimizer([param])
+    opt.clip_grad_norm(1.0)
+    param.grad.mul_(0.5)  # changed after the clip
+    with pytest.raises(ShardingError, match="materialize_pending"):
+        opt.step()
+
+    param = torch.nn.Parameter(p0.clone())
+    param.grad = g0.clone()
+    opt = _make_optimizer([param])
+    norm = float(opt.clip_grad_norm(1.0))
+    opt.materialize_pending()
+    param.grad.mul_(0.5)
+    opt.step()
+    # the same sequence with the clip multiplier applied by hand, then the change
+    ref = torch.nn.Parameter(p0.clone())
+    ref.grad = (g0 * oracle.clip_multiplier(norm, 1.0)) * 0.5
+    ref_opt = _make_optimizer([ref])
+    ref_opt.step()
+    assert torch.equal(param.grad, ref.grad)
+    assert torch.equal(param.detach(), ref.detach())
+
+
 def test_deferred_and_fused_paths_are_bitwise_equal(device):
     n = 300_007
     grads = [torch.randn(n, device=device) * 1e-2 for _ in range(3)]
