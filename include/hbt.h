@@ -304,7 +304,8 @@ int32_t hbt_grad_local_share(const void* const* rank_grads, int32_t group_size, 
  * a caller can stand them in for that pass.  Each is summed in a
  * fixed order (per 256-element tile, then per chunk), so it is reproducible, though
  * not bitwise the norm pass's own tree.  `tile_scratch` is caller-provided device
- * memory for ceil(shard_numel / 256) doubles.
+ * memory for ceil(shard_numel / 256) doubles; its contents are working storage (the
+ * per-tile sums, in an internal order grouped by XCD), not an output.
  * ---------------------------------------------------------------------------- */
 int32_t hbt_grad_local_share_sqnorm(const void* const* rank_grads, int32_t group_size, int32_t rank,
                                     int64_t shard_numel, int64_t valid_numel, int32_t in_dtype,
