@@ -225,6 +225,56 @@ def test_local_share_full_size_rank7_of_llama3_8b_w8(device):
     torch.cuda.empty_cache()
 
 
+def test_local_share_across_two_launch_slices(device):
+    """A shard whose tiles do not fit one launch: a HIP grid dimension holds at most
+    2^32 - 1 work-items, so 64-lane workgroups split after 67,108,863 tiles of 256
+    elements.  A G = 1 local share of 17,180,124,928 bf16 elements (1,000 tiles past the
+    limit) runs as two launches, and its tile sums sit in two differently sized
+    XCD-grouped slices.  The output must be the exact widening of every element (zeros
+    over the padding), and every norm partial must match an independent norm pass over
+    the output, chunk by chunk, within 1e-12."""
+    torch.cuda.empty_cache()
+    free, _ = torch.cuda.mem_get_info(device)
+    if free < 120e9:
+        pytest.skip(f"needs about 104 GB of free device memory, {free / 1e9:.0f} GB free")
+    lib = _native.library()
+    slice_tiles = (2**32 - 1) // 64
+    shard = (slice_tiles + 1000) * 256
+    valid = shard - 1000
+    gen = torch.Generator(device=device).manual_seed(91)
+    x = torch.randn(shard, dtype=torch.bfloat16, device=device, generator=gen)
+    out = torch.empty(shard, dtype=torch.float32, device=device)
+    chunk = 32768
+    valid_chunks, pad_chunks = -(-valid // chunk), -(-(shard - valid) // chunk)
+    partials = torch.empty(valid_chunks + pad_chunks, dtype=torch.float64, device=device)
+    tile_sums = torch.empty(-(-shard // 256), dtype=torch.float64, device=device)
+    status = lib.hbt_grad_local_share_sqnorm(
+        _native.pointer_array([x.data_ptr()]), 1, 0, shard, valid,
+        _native.dtype_code(torch.bfloat16), _native.dtype_code(torch.float32), 1.0,
+        _native.dtype_code(torch.float32), ctypes.c_void_p(out.data_ptr()),
+        ctypes.c_void_p(partials.data_ptr()), ctypes.c_void_p(tile_sums.data_ptr()),
+        ctypes.c_void_p(_native.stream_of(device)),
+    )
+    _native.check(status, "test.local_share_two_slices")
+    step = 1 << 30
+    for i in range(0, valid, step):
+        j = min(valid, i + step)
+        assert torch.equal(out[i:j].view(torch.int32), x[i:j].float().view(torch.int32)), i
+    assert bool((out[valid:] == 0.0).all())
+    del x
+    reference = torch.empty_like(partials)
+    status = lib.hbt_grad_sqnorm_partials(
+        _native.pointer_array([out.data_ptr(), out.data_ptr() + valid * 4]),
+        _native.int64_array([valid, shard - valid]), _native.double_array([1.0, 1.0]), 2,
+        _native.dtype_code(torch.float32), 1.0, reference.data_ptr(), _native.stream_of(device),
+    )
+    _native.check(status, "test.sqnorm_two_slices")
+    assert bool(((partials - reference).abs() <= 1e-12 * reference.abs()).all())
+    assert bool((partials[valid_chunks:] == 0.0).all())
+    del out, tile_sums, partials, reference
+    torch.cuda.empty_cache()
+
+
 @pytest.mark.parametrize("acc_dtype", [torch.float32, torch.bfloat16, torch.float16, torch.float64])
 @pytest.mark.parametrize("grad_dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("assign", [False, True])
