@@ -281,6 +281,38 @@ def test_float16_specials_match_torch(device):
     assert torch.equal(wide.cpu().view(torch.int32), finite.cpu().to(torch.float32).view(torch.int32))
 
 
+def test_copy_across_two_launch_slices(device):
+    """An interval plan whose chunks do not fit one launch: 64-lane workgroups split after
+    67,108,863 chunks, 34,359,737,856 bf16 elements at 512 per chunk.  Two records swap
+    the halves of a bf16 buffer 100 chunks longer than that (69 GB each way), so the copy
+    runs as two launches and the second finds its records through the hint table from a
+    nonzero first chunk.  Every element of both halves is compared bitwise."""
+    torch.cuda.empty_cache()
+    free, _ = torch.cuda.mem_get_info(device)
+    if free < 150e9:
+        pytest.skip(f"needs about 138 GB of free device memory, {free / 1e9:.0f} GB free")
+    slice_chunks = (2**32 - 1) // 64
+    n = (slice_chunks + 100) * 512
+    half = n // 2
+    src = torch.empty(n, dtype=torch.int16, device=device)
+    step = 1 << 30
+    gen = torch.Generator(device=device).manual_seed(12)
+    for i in range(0, n, step):
+        src[i : i + step] = torch.randint(-32768, 32767, (min(step, n - i),), dtype=torch.int16, device=device,
+                                          generator=gen)
+    dst = torch.empty_like(src)
+    plan = _native.CopyPlan(device)
+    a, b = src.view(torch.bfloat16), dst.view(torch.bfloat16)
+    plan.add(a, 0, b, half, half)
+    plan.add(a, half, b, 0, n - half)
+    plan.run(src_dtype=torch.bfloat16, dst_dtype=torch.bfloat16)
+    torch.cuda.synchronize(device)
+    assert torch.equal(dst[half:], src[:half])
+    assert torch.equal(dst[: n - half], src[half:])
+    del src, dst, a, b, plan
+    torch.cuda.empty_cache()
+
+
 def _f16_nan_rules():
     """The NaN bits of x86 F16C conversions, which torch's vectorised CPU ``.to`` uses:
     widening sets the quiet bit and keeps sign and payload; narrowing sets the quiet bit
