@@ -316,7 +316,9 @@ def collect_flat_shard_payload(
                 "storage_key": storage_key,
             })
 
-    hosts = [_pinned_copy(handle.flat_param)]
+    flat = handle.flat_param
+    # a shard kept in host memory (cpu_offload_params) is written from where it lies
+    hosts = [flat.detach().reshape(-1) if flat.device.type == "cpu" else _pinned_copy(flat)]
     add(hosts[0], key="{name}", category="model")
     if optimizer is not None:
         state = optimizer.inner.state.get(_state_key(optimizer, handle.flat_param), {})
@@ -337,7 +339,7 @@ def collect_flat_shard_payload(
                 host = _pinned_copy(value)
             hosts.append(host)
             add(host, key="{name}::" + state_name, category="optimizer", state_name=state_name)
-    torch.cuda.current_stream(handle.flat_param.device).synchronize()
+    torch.cuda.current_stream(handle.device).synchronize()
     return payload, records, scalars
 
 
@@ -497,7 +499,7 @@ def load_flat_shard_checkpoint(
     metadata = json.loads(metadata_path.read_text(encoding="utf-8")) if metadata_path.is_file() else {}
     flat = handle.flat_param
     if cache is None:
-        cache = ShardFileCache(directory, manifest, verify_checksums=verify_checksums, device=flat.device)
+        cache = ShardFileCache(directory, manifest, verify_checksums=verify_checksums, device=handle.device)
     layout = handle.local_piece_layout()
     keys = [[item.name] for item in layout]
     if optimizer is not None:
@@ -509,7 +511,12 @@ def load_flat_shard_checkpoint(
               for record in (manifest.tensors.get(name) for name in names) if record is not None
               for shard, _ in record.shards_overlapping(ShardRange(item.parameter_offset, item.length))]
     cache.prefetch(needed)
-    loaded = load_flat_shard(flat.data, layout, manifest.tensors_by_category("model"), cache, strict=strict)
+    # a shard kept in host memory is filled on the device and copied back
+    hosted = flat.device.type == "cpu"
+    destination = flat.data.to(handle.device) if hosted else flat.data
+    loaded = load_flat_shard(destination, layout, manifest.tensors_by_category("model"), cache, strict=strict)
+    if hosted:
+        flat.data.copy_(destination)
     increment_version(flat)
     if optimizer is None:
         return loaded
@@ -521,7 +528,7 @@ def load_flat_shard_checkpoint(
     index = next(i for i, p in enumerate(optimizer.parameters) if p is flat)
     entry: dict[str, Any] = {}
     for state_name in state_names:
-        buffer = torch.zeros(flat.numel(), dtype=flat.dtype, device=flat.device)
+        buffer = torch.zeros(flat.numel(), dtype=flat.dtype, device=handle.device)
         found = load_flat_shard(buffer, layout, records, cache,
                                 key_of=lambda item, s=state_name: f"{item.name}::{s}", strict=False)
         if found:

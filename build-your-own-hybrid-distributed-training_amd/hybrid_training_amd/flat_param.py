@@ -27,6 +27,13 @@ tensor work is the interval gather-copy kernel and the local-share kernel of
   refill the same bytes with the version counter kept).  The reference's autograd
   function, whose backward reduce-scatters, is outside this path: the caller hands
   the full gradient to ``reduce_scatter_gradient``.
+
+With ``FSDPConfig.cpu_offload_params`` the shard lives in pinned host memory, as the
+reference keeps it on the CPU (``fsdp.py:450-451``): it is built on the device and
+copied down, uploaded for every gather and unpack, and ``reduce_scatter_gradient``
+returns the gradient shard in pinned host memory (``fsdp.py:763-764``) with its norm
+partials still attached, so the clip does not read it back.  The optimizer steps such
+a shard on the device by streaming it through (``optim.ShardedOptimizer``).
 """
 
 from __future__ import annotations
@@ -43,7 +50,8 @@ from . import _native
 from .config import FSDPConfig, MixedPrecisionConfig, resolve_dtype
 from .errors import ShardingError, UnsupportedFeatureError, format_error
 from .groups import GroupHandle
-from .optim import NORM_PARTIALS_ATTR, NormPartials
+from .host_staging import is_host
+from .optim import NORM_PARTIALS_ATTR, NormPartials, norm_chunk_elems
 from .tensors import FlatEntry, ShardRange, build_flat_layout, intersect_ranges
 
 __all__ = [
@@ -219,11 +227,7 @@ class FlatParamHandle:
                         ),
                     )
                 )
-        if config.cpu_offload_params:
-            raise UnsupportedFeatureError(
-                format_error("fsdp.FlatParamHandle", "parameter CPU offload is not implemented by hybrid_training_amd",
-                             expected=False, observed=True)
-            )
+        self._offload_params = bool(config.cpu_offload_params)
         self.flat_param = self._build_shard()
         self._attach_gradient_norm_scale()
         self._reduction_count = 0
@@ -257,7 +261,22 @@ class FlatParamHandle:
             zero_plan.add_zero(shard, padding.start - local.start, padding.length)
         for dtype, plan in plans.items():
             plan.run(src_dtype=dtype, dst_dtype=self._master_dtype)
+        if self._offload_params:
+            shard = self._to_host(shard)
         return FlatParameter(shard, requires_grad=self._requires_grad)
+
+    @staticmethod
+    def _to_host(tensor: torch.Tensor) -> torch.Tensor:
+        """A pinned host copy of a device tensor, complete when this returns."""
+        host = torch.empty(tensor.shape, dtype=tensor.dtype, device="cpu", pin_memory=True)
+        host.copy_(tensor)
+        return host
+
+    def _on_device(self, tensor: torch.Tensor) -> torch.Tensor:
+        """``tensor`` itself if it is on the device, else its upload (``fsdp.py:575-577``),
+        ordered on the current stream before the launches that read it."""
+        tensor = tensor.detach()
+        return tensor.to(self._device, non_blocking=True) if is_host(tensor) else tensor
 
     def _attach_gradient_norm_scale(self) -> None:
         """Per-element norm weights: partitioned width on real elements, 0 on padding.
@@ -317,6 +336,11 @@ class FlatParamHandle:
     def names(self) -> tuple[str, ...]:
         """Managed parameter names in flat order."""
         return self._names
+
+    @property
+    def device(self) -> torch.device:
+        """The device this unit's kernels run on (its shard's, unless the shard is offloaded)."""
+        return self._device
 
     @property
     def total_numel(self) -> int:
@@ -405,7 +429,7 @@ class FlatParamHandle:
         _check_cast(src_dtype, self._compute_dtype, operation)
         plan = _native.CopyPlan(self._device)
         for rank, shard in enumerate(shards):
-            plan.add(_native.contiguous_source(shard.detach()), 0, full, rank * self._shard_numel,
+            plan.add(_native.contiguous_source(self._on_device(shard)), 0, full, rank * self._shard_numel,
                      self._shard_numel)
         plan.run(src_dtype=src_dtype, dst_dtype=self._compute_dtype)
 
@@ -475,7 +499,7 @@ class FlatParamHandle:
 
     def full_tensors(self, peer_shards: Sequence[torch.Tensor] | None = None) -> dict[str, torch.Tensor]:
         """Every managed parameter, reconstructed by copy (``fsdp.py:912-925``)."""
-        shards = self._all_shards(peer_shards, "fsdp.full_tensors")
+        shards = [self._on_device(s) for s in self._all_shards(peer_shards, "fsdp.full_tensors")]
         dtype = shards[0].dtype
         out = {e.name: torch.empty(e.shape, dtype=dtype, device=self._device) for e in self._entries}
         plan = _native.CopyPlan(self._device)
@@ -564,8 +588,7 @@ class FlatParamHandle:
         valid = max(0, min(self._shard_numel, self._total_numel - local.start))
         divisor = float(group) if (self._config.average_gradients and group > 1) else 1.0
         out = torch.empty(self._shard_numel, dtype=self._master_dtype, device=self._device)
-        # elements per norm partial: the norm pass's chunk for the master dtype
-        chunk = 32768 if self._master_dtype == torch.float32 else 65536
+        chunk = norm_chunk_elems(self._master_dtype)  # elements per norm partial
         valid_chunks = -(-valid // chunk)
         pad = self._shard_numel - valid
         partials = torch.empty(max(1, valid_chunks + -(-pad // chunk)), dtype=torch.float64, device=self._device)
@@ -595,6 +618,8 @@ class FlatParamHandle:
             segments[(0, valid)] = partials[:valid_chunks]
         if pad:
             segments[(valid, pad)] = partials[valid_chunks:]
+        if self._offload_params:
+            out = self._to_host(out)  # the partials stay on the device and describe the copy
         setattr(out, NORM_PARTIALS_ATTR, NormPartials(out.data_ptr(), out._version, segments, out.dtype))
         self._reduction_count += 1
         return out
@@ -649,6 +674,11 @@ class FlatParamHandle:
         padding = intersect_ranges(self.local_shard_range(), ShardRange(self._total_numel, self._padding))
         if padding is None or padding.length == 0:
             return
+        if is_host(shard_grad):  # a host shard's padding takes zeros written from the device
+            begin = padding.start - self.local_shard_range().start
+            zeros = torch.zeros(padding.length, dtype=shard_grad.dtype, device=self._device)
+            shard_grad.detach().view(-1)[begin : begin + padding.length].copy_(zeros)
+            return
         plan = _native.CopyPlan(self._device)
         plan.add_zero(shard_grad, padding.start - self.local_shard_range().start, padding.length)
         plan.run(src_dtype=shard_grad.dtype, dst_dtype=shard_grad.dtype)
@@ -674,8 +704,10 @@ class FlatParamHandle:
         return layout
 
     def local_pieces(self) -> list[ShardedTensorPiece]:
-        """This rank's slice of each owned parameter, copied out (``fsdp.py:845-860``)."""
-        shard = self.flat_param.detach()
+        """This rank's slice of each owned parameter, copied out (``fsdp.py:845-860``).
+
+        The pieces are on the device, a host-resident shard's too (uploaded first)."""
+        shard = self._on_device(self.flat_param)
         layout = self.local_piece_layout()
         datas = [torch.empty(item.length, dtype=shard.dtype, device=shard.device) for item in layout]
         plan = _native.CopyPlan(shard.device)
@@ -691,7 +723,9 @@ class FlatParamHandle:
     def load_local_pieces(self, pieces: dict[str, torch.Tensor]) -> None:
         """Write whole parameter tensors' owned parts into the shard (``fsdp.py:862-910``)."""
         local = self.local_shard_range()
-        shard = self.flat_param.data
+        host = self.flat_param.data if is_host(self.flat_param) else None
+        # a host-resident shard is written on the device and copied back
+        shard = self._on_device(self.flat_param.data) if host is not None else self.flat_param.data
         plans: dict[torch.dtype, _native.CopyPlan] = {}
         for entry in self._entries:
             tensor = pieces.get(entry.name)
@@ -727,6 +761,8 @@ class FlatParamHandle:
             )
         for dtype, plan in plans.items():
             plan.run(src_dtype=dtype, dst_dtype=shard.dtype)
+        if host is not None:
+            host.copy_(shard)
 
     def memory_summary(self) -> dict[str, int]:
         """Per-rank byte counts of this unit (``fsdp.py:927-942``)."""

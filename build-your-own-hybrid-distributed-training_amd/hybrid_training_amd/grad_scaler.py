@@ -41,7 +41,8 @@ from . import _native
 from .config import GradScalerConfig
 from .errors import UnsupportedFeatureError, format_error
 from .groups import GroupHandle
-from .optim import PENDING_UNSCALE_ATTR, gradient_norm_pass
+from .host_staging import is_host
+from .optim import PENDING_UNSCALE_ATTR, gradient_norm_pass, scale_gradients
 
 __all__ = ["GradScaler", "GradScalerState"]
 
@@ -93,14 +94,16 @@ class _DeviceFlag:
         return f"_DeviceFlag({'unevaluated' if self._value is None else self._value})"
 
 
-def _nonfinite_flag(params: Sequence[nn.Parameter]) -> torch.Tensor | None:
+def _nonfinite_flag(params: Sequence[nn.Parameter], device: torch.device) -> torch.Tensor | None:
     grads = [p.grad for p in params if p.grad is not None]
     if not grads:
         return None
     segments = [(g, 0, int(g.numel()), 1.0) for g in grads]
     # The pass's partials stay on the gradients: an optimizer clipping the same,
     # unchanged gradients next (the engine's order) reads them instead of the gradients.
-    return gradient_norm_pass(segments, grads[0].device, max_norm=0.0, tag=True).nonfinite
+    # Gradients in host memory stream through the scaler's device.
+    resident = next((g.device for g in grads if not is_host(g)), device)
+    return gradient_norm_pass(segments, resident, max_norm=0.0, tag=True).nonfinite
 
 
 class GradScaler:
@@ -157,32 +160,21 @@ class GradScaler:
                 setattr(p.grad, PENDING_UNSCALE_ATTR, inverse)
             self._unscaled = True
             return _DeviceFlag(lambda: self._detect_non_finite(params))  # type: ignore[return-value]
-        lib = _native.library()
         groups: dict[tuple[torch.device, torch.dtype], list[torch.Tensor]] = {}
         for p in params:
-            _native.require_device_tensor(p.grad, "grad_scaler.unscale_")
+            if not is_host(p.grad):
+                _native.require_device_tensor(p.grad, "grad_scaler.unscale_")
             _native.require_dense(p.grad, "grad_scaler.unscale_")
             if p.grad.dtype not in (torch.float32, torch.bfloat16, torch.float16):
                 raise UnsupportedFeatureError(
                     format_error("grad_scaler.unscale_", "gradients must be float32, bfloat16 or float16",
                                  observed=str(p.grad.dtype))
                 )
-            groups.setdefault((p.grad.device, p.grad.dtype), []).append(p.grad)
+            # a gradient in host memory streams through the scaler's device
+            device = self._device if is_host(p.grad) else p.grad.device
+            groups.setdefault((device, p.grad.dtype), []).append(p.grad)
         for (device, dtype), grads in groups.items():
-            with torch.cuda.device(device):
-                for start in range(0, len(grads), _native.MAX_TENSORS_PER_LAUNCH):
-                    chunk = grads[start : start + _native.MAX_TENSORS_PER_LAUNCH]
-                    status = lib.hbt_scale_inplace(
-                        _native.pointer_array([g.data_ptr() for g in chunk]),
-                        _native.int64_array([g.numel() for g in chunk]),
-                        len(chunk),
-                        _native.dtype_code(dtype),
-                        inverse,
-                        None,
-                        _native.stream_of(device),
-                    )
-                    _native.check(status, "grad_scaler.hbt_scale_inplace")
-                    torch.autograd.graph.increment_version(chunk)
+            scale_gradients(grads, dtype, inverse, None, device, "grad_scaler.hbt_scale_inplace")
         self._unscaled = True
         return self._detect_non_finite(params)
 
@@ -196,7 +188,7 @@ class GradScaler:
             if covered == {id(p) for p in parameters}:
                 flag = optimizer.last_nonfinite_flag()
         if flag is None:
-            flag = _nonfinite_flag(parameters)
+            flag = _nonfinite_flag(parameters, self._device)
         if flag is None:
             return False
         return bool(int(flag.item()) != 0)

@@ -50,6 +50,7 @@ from . import _native
 from .config import OptimizerConfig
 from .errors import ShardingError, UnsupportedFeatureError, format_error
 from .groups import GroupHandle
+from .host_staging import HostOperand, host_stream, is_host
 
 __all__ = [
     "NormContribution",
@@ -206,12 +207,18 @@ class NormContribution:
             return [(grad, offset, length, weight) for offset, length, weight in self.runs]
         return [(grad, 0, int(grad.numel()), float(self.scale))]
 
-    def squared_norm(self) -> torch.Tensor:
-        """This contribution's weighted squared norm as a 0-dim fp64 device tensor."""
+    def squared_norm(self, device: torch.device | None = None) -> torch.Tensor:
+        """This contribution's weighted squared norm as a 0-dim fp64 device tensor.
+
+        ``device``: where a gradient in host memory is summed (default: its own device,
+        or the current HIP device for a host gradient)."""
         grad = self.parameter.grad
+        if device is None:
+            owner = self.parameter if grad is None else grad
+            device = torch.device("cuda", torch.cuda.current_device()) if is_host(owner) else owner.device
         if grad is None:
-            return torch.zeros((), dtype=torch.float64, device=self.parameter.device)
-        result = gradient_norm_pass(self.segments(), grad.device, max_norm=0.0)
+            return torch.zeros((), dtype=torch.float64, device=device)
+        result = gradient_norm_pass(self.segments(), torch.device(device), max_norm=0.0)
         return result.sum
 
 
@@ -294,11 +301,17 @@ def gradient_norm_pass(
     leaves its partials on its gradient (:class:`NormPartials`), so a later pass over
     the unchanged gradient, such as the clip after the loss scaler's overflow check,
     reuses them instead of reading the gradient again.
+
+    A gradient in host memory (a parameter shard kept on the host) is uploaded through
+    the device's :class:`~hybrid_training_amd.host_staging.HostStream` and summed there
+    chunk by chunk; its partials are the ones the same values would give in HBM at the
+    same 16-byte alignment, so the result does not depend on where the gradient lives.
     """
     lib = _native.library()
     batches: dict[tuple[torch.dtype, float], list[tuple[torch.Tensor, int, int, float]]] = {}
     for grad, offset, length, weight in segments:
-        _native.require_device_tensor(grad, "optim.gradient_norm")
+        if not is_host(grad):
+            _native.require_device_tensor(grad, "optim.gradient_norm")
         if grad.dtype not in (torch.float32, torch.bfloat16, torch.float16):
             raise UnsupportedFeatureError(
                 format_error(
@@ -355,6 +368,11 @@ def gradient_norm_pass(
                     else:
                         torch.mul(cached, weight, out=target)
                     pending_first = slot + count
+                elif is_host(grad):
+                    _launch_sqnorm(lib, pending, dtype, unscale, partials, pending_first, stream)
+                    pending = []
+                    _stream_sqnorm(lib, grad, offset, length, weight, dtype, unscale, partials, slot, device)
+                    pending_first = slot + count
                 else:
                     pending.append((grad, offset, length, weight))
                 slot += count
@@ -383,6 +401,32 @@ def gradient_norm_pass(
     return NormResult(sum=outputs[0], norm=outputs[1], grad_mul=grad_mul, nonfinite=nonfinite)
 
 
+def norm_chunk_elems(dtype: torch.dtype) -> int:
+    """Elements per norm partial: 32768 of an fp32 gradient, 65536 of a 2-byte one."""
+    return 32768 if dtype == torch.float32 else 65536
+
+
+def _stream_sqnorm(lib, grad, offset, length, weight, dtype, unscale, partials, slot, device) -> None:
+    """The partials of a host gradient's segment, from slot ``slot``, summed on ``device``.
+
+    Each staged chunk holds whole norm chunks of the segment and starts at the
+    segment's own offset from a 16-byte boundary, so every partial is summed over the
+    same elements in the same order as a launch over the segment in HBM would sum it.
+    """
+    flat = grad.detach().reshape(-1)
+    size = flat.element_size()
+    lead = ((flat.data_ptr() + offset * size) % 16) // size
+    norm_chunk = norm_chunk_elems(dtype)
+    staging = host_stream(device)
+    chunk = max(norm_chunk, staging.chunk_elems // norm_chunk * norm_chunk)
+    stream = _native.stream_of(device)
+
+    def launch(start: int, n: int, staged: list[torch.Tensor]) -> None:
+        _launch_sqnorm(lib, [(staged[0], 0, n, weight)], dtype, unscale, partials, slot + start // norm_chunk, stream)
+
+    staging.run(length, [HostOperand(flat[offset : offset + length])], launch, lead=lead, chunk=chunk)
+
+
 def _launch_sqnorm(lib, items, dtype, unscale, partials, first, stream) -> None:
     """One ``hbt_grad_sqnorm_partials`` launch writing ``items``' partials from slot ``first``."""
     if not items:
@@ -399,6 +443,36 @@ def _launch_sqnorm(lib, items, dtype, unscale, partials, first, stream) -> None:
         stream,
     )
     _native.check(status, "optim.hbt_grad_sqnorm_partials")
+
+
+def scale_gradients(grads: Sequence[torch.Tensor], dtype: torch.dtype, unscale: float, grad_mul_ptr: int | None,
+                    device: torch.device, operation: str) -> None:
+    """Multiply dense gradients of one dtype in place by ``unscale`` and ``*grad_mul``,
+    each product rounded to the dtype (``hbt_scale_inplace``, the reference's
+    ``grad.mul_``).  Gradients in HBM go in launches of up to 16; a gradient in host
+    memory streams through ``device`` and is final on the host when this returns."""
+    lib = _native.library()
+    stream = _native.stream_of(device)
+
+    def call(ptrs: list[int], numels: list[int]) -> None:
+        status = lib.hbt_scale_inplace(_native.pointer_array(ptrs), _native.int64_array(numels), len(ptrs),
+                                       _native.dtype_code(dtype), unscale, grad_mul_ptr, stream)
+        _native.check(status, operation)
+
+    resident = [g for g in grads if not is_host(g)]
+    hosted = [g for g in grads if is_host(g)]
+    with torch.cuda.device(device):
+        for start in range(0, len(resident), _native.MAX_TENSORS_PER_LAUNCH):
+            chunk = resident[start : start + _native.MAX_TENSORS_PER_LAUNCH]
+            call([g.data_ptr() for g in chunk], [g.numel() for g in chunk])
+            increment_version(chunk)
+        if hosted:
+            staging = host_stream(device)
+            for g in hosted:
+                staging.run(g.numel(), [HostOperand(g, store=True)],
+                            lambda start, n, st: call([st[0].data_ptr()], [n]))
+            increment_version(hosted)
+            staging.synchronize()
 
 
 def _check_group(group: GroupHandle, operation: str) -> None:
@@ -449,81 +523,6 @@ def _pinned_like(p: torch.Tensor) -> torch.Tensor:
     return torch.empty(p.shape, dtype=p.dtype, device="cpu", pin_memory=True)
 
 
-class _HostStatePipeline:
-    """Streams host-resident optimizer state through device staging buffers.
-
-    The reference's offload path (``sharded_optimizer.py:284-296``, ``:342-353``) keeps
-    master parameters and state on the host, copies gradients down, steps on the CPU
-    and copies parameters back up, all synchronously.  Here the step runs on the
-    device parameter itself, and the state travels in chunks: while chunk ``c`` is
-    updated on the compute stream, chunk ``c + 1``'s state is uploaded on one copy
-    stream and chunk ``c - 1``'s updated state and master parameter are written back
-    on another.  Two staging slots per state tensor bound the device memory used.
-    """
-
-    #: Elements per chunk (128 MB of fp32 per state tensor and slot).
-    chunk_elems = 1 << 25
-    slots = 2
-
-    def __init__(self, device: torch.device) -> None:
-        self.device = device
-        self.upload = torch.cuda.Stream(device)
-        self.download = torch.cuda.Stream(device)
-        self._staging: dict[tuple[int, int], torch.Tensor] = {}
-        self.done: torch.cuda.Event | None = None
-
-    def _stage(self, slot: int, k: int, n: int, dtype: torch.dtype) -> torch.Tensor:
-        buf = self._staging.get((slot, k, dtype))
-        if buf is None or buf.numel() < n:
-            buf = torch.empty(n, dtype=dtype, device=self.device)
-            self._staging[(slot, k, dtype)] = buf
-        return buf[:n]
-
-    def run(self, device_param: torch.Tensor, host_param: torch.Tensor, host_states: list[torch.Tensor],
-            load_states: bool, launch) -> None:
-        """Update ``device_param`` chunk by chunk; ``launch(start, n, staged)`` runs the kernel."""
-        compute = torch.cuda.current_stream(self.device)
-        flat_dev = device_param.detach().view(-1)
-        flat_host = host_param.detach().view(-1)
-        flat_states = [s.view(-1) for s in host_states]
-        total = flat_dev.numel()
-        free: list[torch.cuda.Event | None] = [None] * self.slots
-        self.upload.wait_stream(compute)  # the previous step's copies and kernels are done
-        for index, start in enumerate(range(0, total, self.chunk_elems)):
-            n = min(self.chunk_elems, total - start)
-            slot = index % self.slots
-            staged = [self._stage(slot, k, n, h.dtype) for k, h in enumerate(flat_states)]
-            loaded = torch.cuda.Event()
-            with torch.cuda.stream(self.upload):
-                if free[slot] is not None:
-                    self.upload.wait_event(free[slot])
-                if load_states:
-                    for d, h in zip(staged, flat_states):
-                        d.copy_(h[start : start + n], non_blocking=True)
-                loaded.record(self.upload)
-            compute.wait_event(loaded)
-            launch(start, n, staged)
-            computed = torch.cuda.Event()
-            computed.record(compute)
-            released = torch.cuda.Event()
-            with torch.cuda.stream(self.download):
-                self.download.wait_event(computed)
-                for d, h in zip(staged, flat_states):
-                    h[start : start + n].copy_(d, non_blocking=True)
-                flat_host[start : start + n].copy_(flat_dev[start : start + n], non_blocking=True)
-                released.record(self.download)
-            free[slot] = released
-        end = torch.cuda.Event()
-        end.record(self.download)
-        compute.wait_event(end)  # later device work sees the finished copies
-        self.done = end
-
-    def synchronize(self) -> None:
-        """Block the host until the last step's write-back has landed."""
-        if self.done is not None:
-            self.done.synchronize()
-
-
 class ShardedOptimizer:
     """AdamW or SGD over this rank's shards with a global-norm clip, on HIP kernels.
 
@@ -534,8 +533,14 @@ class ShardedOptimizer:
     masters take gradients of their own dtype, fp32 masters fp32 or bf16 gradients.
     With ``config.cpu_offload_state`` the master copies and the optimizer state live in
     pinned host memory, as in the reference, and stream through the device each step
-    (:class:`_HostStatePipeline`).  ``amsgrad`` and ``maximize`` have no kernel and
-    raise :class:`UnsupportedFeatureError` rather than falling back to torch.
+    (:class:`~hybrid_training_amd.host_staging.HostStream`).
+
+    A parameter in host memory (an FSDP shard with ``cpu_offload_params``, which the
+    reference steps with torch's optimizer on the CPU) keeps its gradient and its state
+    on the host too; its norm pass and its step stream every operand through the device
+    and write the results back, bitwise what the same values in HBM give.  The step
+    returns once the host copies have landed.  ``amsgrad`` and ``maximize`` have no
+    kernel and raise :class:`UnsupportedFeatureError` rather than falling back to torch.
     """
 
     def __init__(
@@ -556,7 +561,8 @@ class ShardedOptimizer:
         self._defer_clip = defer_clip
         _check_group(norm_group, "optim.ShardedOptimizer")
         for param in self._parameters:
-            _native.require_device_tensor(param, "optim.ShardedOptimizer")
+            if not is_host(param):
+                _native.require_device_tensor(param, "optim.ShardedOptimizer")
             if param.dtype not in (torch.float32, torch.bfloat16, torch.float16):
                 raise UnsupportedFeatureError(
                     format_error(
@@ -569,17 +575,20 @@ class ShardedOptimizer:
         if self._offload:
             # As in the reference, master copies live on the host and the inner
             # optimizer's state is keyed by them; here they and the state sit in
-            # pinned memory and stream through the device every step.
+            # pinned memory and stream through the device every step.  A parameter
+            # already on the host is its own master.
             self._cpu_parameters = [
-                nn.Parameter(_pinned_like(p).copy_(p.detach()), requires_grad=True) for p in self._parameters
+                p if is_host(p) else nn.Parameter(_pinned_like(p).copy_(p.detach()), requires_grad=True)
+                for p in self._parameters
             ]
             self._optimizer = build_inner_optimizer(self._cpu_parameters, config)
-            self._pipeline: _HostStatePipeline | None = _HostStatePipeline(self._device)
         else:
             self._cpu_parameters = []
             self._optimizer = build_inner_optimizer(self._parameters, config)
-            self._pipeline = None
-        self._device_param = {id(h): d for h, d in zip(self._cpu_parameters, self._parameters)}
+        self._host_resident = any(is_host(p) for p in self._parameters)
+        self._stream = host_stream(self._device) if (self._offload or self._host_resident) else None
+        # host master copy -> the device parameter it follows (state offload only)
+        self._device_param = {id(h): d for h, d in zip(self._cpu_parameters, self._parameters) if h is not d}
         self._contributions = build_gradient_norm_contributions(
             self._parameters, world_size=norm_group.size
         )
@@ -596,7 +605,6 @@ class ShardedOptimizer:
 
     def _scale_grads(self, grad_mul: torch.Tensor | None, unscale_attr: bool) -> None:
         """Apply pending multipliers to the gradients in place (materialisation)."""
-        lib = _native.library()
         groups: dict[tuple[torch.dtype, float], list[torch.Tensor]] = {}
         for p in self._parameters:
             g = p.grad
@@ -605,21 +613,9 @@ class ShardedOptimizer:
             _native.require_dense(g, "optim.scale_gradients")
             unscale = _pending_unscale(g) if unscale_attr else 1.0
             groups.setdefault((g.dtype, unscale), []).append(g)
-        with torch.cuda.device(self._device):
-            for (dtype, unscale), grads in groups.items():
-                for start in range(0, len(grads), _native.MAX_TENSORS_PER_LAUNCH):
-                    chunk = grads[start : start + _native.MAX_TENSORS_PER_LAUNCH]
-                    status = lib.hbt_scale_inplace(
-                        _native.pointer_array([g.data_ptr() for g in chunk]),
-                        _native.int64_array([g.numel() for g in chunk]),
-                        len(chunk),
-                        _native.dtype_code(dtype),
-                        unscale,
-                        None if grad_mul is None else grad_mul.data_ptr(),
-                        _native.stream_of(self._device),
-                    )
-                    _native.check(status, "optim.hbt_scale_inplace")
-                    increment_version(chunk)
+        for (dtype, unscale), grads in groups.items():
+            scale_gradients(grads, dtype, unscale, None if grad_mul is None else grad_mul.data_ptr(),
+                            self._device, "optim.hbt_scale_inplace")
         if unscale_attr:
             for p in self._parameters:
                 if p.grad is not None and hasattr(p.grad, PENDING_UNSCALE_ATTR):
@@ -713,6 +709,8 @@ class ShardedOptimizer:
             self._run_sgd_step(grad_mul, write_back)
         else:
             self._run_adamw_step(grad_mul, write_back)
+        if self._host_resident:
+            self._stream.synchronize()  # host parameters, gradients and state are final
         if write_back:
             written = [p.grad for p in self._parameters if p.grad is not None]
             if written and (grad_mul is not None or any(_pending_unscale(g) != 1.0 for g in written)):
@@ -735,7 +733,14 @@ class ShardedOptimizer:
         grad = p.grad
         if grad is None:
             return None
-        _native.require_device_tensor(grad, "optim.ShardedOptimizer.step")
+        if is_host(p) != is_host(grad):
+            raise ShardingError(
+                format_error("optim.ShardedOptimizer.step",
+                             "a parameter and its gradient must both be in host memory or both on the device",
+                             expected=str(p.device), observed=str(grad.device))
+            )
+        if not is_host(grad):
+            _native.require_device_tensor(grad, "optim.ShardedOptimizer.step")
         if grad.shape != p.shape or not grad.is_contiguous() or not p.is_contiguous():
             raise ShardingError(
                 format_error(
@@ -798,11 +803,11 @@ class ShardedOptimizer:
         stream = _native.stream_of(self._device)
         mul_ptr = None if grad_mul is None else grad_mul.data_ptr()
         with torch.cuda.device(self._device):
-            for (scalars, pdtype, gdtype, unscale), params in batches.items():
-                if self._pipeline is not None:
-                    for p in params:
-                        self._offloaded_adamw(lib, p, scalars, pdtype, gdtype, unscale, mul_ptr, flags)
-                    continue
+            for (scalars, pdtype, gdtype, unscale), batch in batches.items():
+                for p in batch:
+                    if is_host(p):
+                        self._streamed_adamw(lib, p, scalars, pdtype, gdtype, unscale, mul_ptr, flags)
+                params = [p for p in batch if not is_host(p)]
                 for start in range(0, len(params), _native.MAX_TENSORS_PER_LAUNCH):
                     chunk = params[start : start + _native.MAX_TENSORS_PER_LAUNCH]
                     states = [self._optimizer.state[p] for p in chunk]
@@ -828,32 +833,36 @@ class ShardedOptimizer:
 
     def _place_state(self, value: torch.Tensor, reference: torch.Tensor) -> torch.Tensor:
         """A loaded state tensor on the reference parameter's device and dtype (pinned if host)."""
-        if self._pipeline is not None:
+        if is_host(reference):
             return _pinned_like(reference).copy_(value.detach().reshape(reference.shape))
         # The update kernels address numel consecutive elements, so the state is dense.
         return value.to(device=reference.device, dtype=reference.dtype).contiguous()
 
     def _zero_state(self, p: torch.Tensor) -> torch.Tensor:
-        """A zero state tensor beside ``p``: in HBM, or pinned host memory when offloaded."""
-        if self._pipeline is not None:
+        """A zero state tensor beside ``p``: in HBM, or pinned host memory for a host master."""
+        if is_host(p):
             return _pinned_like(p).zero_()
         return torch.zeros_like(p, memory_format=torch.preserve_format)
 
-    def _offloaded_adamw(self, lib, host_p, scalars, pdtype, gdtype, unscale, mul_ptr, flags) -> None:
-        """AdamW on the device parameter with its host-resident state streamed through."""
-        dev = self._device_param[id(host_p)]
-        grad = dev.grad
-        state = self._optimizer.state[host_p]
-        stream = _native.stream_of(self._device)
-        gsize = grad.element_size()
-        psize = dev.element_size()
+    def _streamed_adamw(self, lib, host_p, scalars, pdtype, gdtype, unscale, mul_ptr, flags) -> None:
+        """AdamW on a parameter whose state, or whose every operand, lives on the host.
 
-        def launch(start: int, n: int, staged: list[torch.Tensor]) -> None:
+        With state offload the device parameter and gradient stay in HBM and only
+        ``m`` and ``v`` stream, the updated parameter following them to its host copy;
+        a host-resident parameter streams ``p``, ``g``, ``m`` and ``v`` and writes back
+        ``p``, ``m``, ``v`` and, with in-place semantics, the scaled ``g``.
+        """
+        dev = self._device_param.get(id(host_p))
+        state = self._optimizer.state[host_p]
+        m, v = state["exp_avg"], state["exp_avg_sq"]
+        stream = _native.stream_of(self._device)
+
+        def call(p_ptr: int, g_ptr: int, m_ptr: int, v_ptr: int, n: int) -> None:
             status = lib.hbt_adamw_step(
-                _native.pointer_array([dev.data_ptr() + psize * start]),
-                _native.pointer_array([grad.data_ptr() + gsize * start]),
-                _native.pointer_array([staged[0].data_ptr()]),
-                _native.pointer_array([staged[1].data_ptr()]),
+                _native.pointer_array([p_ptr]),
+                _native.pointer_array([g_ptr]),
+                _native.pointer_array([m_ptr]),
+                _native.pointer_array([v_ptr]),
                 _native.int64_array([n]),
                 1,
                 _native.dtype_code(pdtype),
@@ -866,8 +875,25 @@ class ShardedOptimizer:
             )
             _native.check(status, "optim.hbt_adamw_step")
 
-        self._pipeline.run(dev, host_p, [state["exp_avg"], state["exp_avg_sq"]], True, launch)
-        increment_version([dev, host_p, state["exp_avg"], state["exp_avg_sq"]])
+        if dev is not None:
+            grad = dev.grad
+            psize, gsize = dev.element_size(), grad.element_size()
+            self._stream.run(
+                dev.numel(), [HostOperand(m, store=True), HostOperand(v, store=True)],
+                lambda start, n, st: call(dev.data_ptr() + psize * start, grad.data_ptr() + gsize * start,
+                                          st[0].data_ptr(), st[1].data_ptr(), n),
+                resident=(dev.detach().view(-1), host_p.detach().view(-1)),
+            )
+            increment_version([dev, host_p, m, v])
+            return
+        write_grad = bool(flags & _native.STEP_WRITE_GRAD)
+        self._stream.run(
+            host_p.numel(),
+            [HostOperand(host_p, store=True), HostOperand(host_p.grad, store=write_grad),
+             HostOperand(m, store=True), HostOperand(v, store=True)],
+            lambda start, n, st: call(st[0].data_ptr(), st[1].data_ptr(), st[2].data_ptr(), st[3].data_ptr(), n),
+        )
+        increment_version([host_p, m, v])
 
     def _run_sgd_step(self, grad_mul: torch.Tensor | None, write_back: bool) -> None:
         """torch.optim.SGD's step (``torch/optim/sgd.py``) as one fused kernel per batch."""
@@ -894,7 +920,7 @@ class ShardedOptimizer:
                     state = self._optimizer.state[p]
                     if state.get("momentum_buffer") is None:
                         # torch starts the buffer as a clone of the first gradient.
-                        state["momentum_buffer"] = (_pinned_like(p) if self._pipeline is not None
+                        state["momentum_buffer"] = (_pinned_like(p) if is_host(p)
                                                     else torch.empty_like(p, memory_format=torch.preserve_format))
                         flags |= _native.SGD_FIRST_STEP
                     else:
@@ -907,11 +933,11 @@ class ShardedOptimizer:
         stream = _native.stream_of(self._device)
         mul_ptr = None if grad_mul is None else grad_mul.data_ptr()
         with torch.cuda.device(self._device):
-            for (scalars, flags, pdtype, gdtype, unscale), params in batches.items():
-                if self._pipeline is not None:
-                    for p in params:
-                        self._offloaded_sgd(lib, p, scalars, flags, pdtype, gdtype, unscale, mul_ptr)
-                    continue
+            for (scalars, flags, pdtype, gdtype, unscale), batch in batches.items():
+                for p in batch:
+                    if is_host(p):
+                        self._streamed_sgd(lib, p, scalars, flags, pdtype, gdtype, unscale, mul_ptr)
+                params = [p for p in batch if not is_host(p)]
                 for start in range(0, len(params), _native.MAX_TENSORS_PER_LAUNCH):
                     chunk = params[start : start + _native.MAX_TENSORS_PER_LAUNCH]
                     buffers = ([self._optimizer.state[p]["momentum_buffer"] for p in chunk]
@@ -935,21 +961,22 @@ class ShardedOptimizer:
                     if buffers:
                         increment_version(buffers)
 
-    def _offloaded_sgd(self, lib, host_p, scalars, flags, pdtype, gdtype, unscale, mul_ptr) -> None:
-        """SGD on the device parameter with its host-resident momentum buffer streamed through."""
-        dev = self._device_param[id(host_p)]
-        grad = dev.grad
+    def _streamed_sgd(self, lib, host_p, scalars, flags, pdtype, gdtype, unscale, mul_ptr) -> None:
+        """SGD on a parameter whose momentum buffer, or whose every operand, lives on the
+        host (see :meth:`_streamed_adamw`).  A first step writes the buffer without
+        reading it, so the buffer is not uploaded then."""
+        dev = self._device_param.get(id(host_p))
         stream = _native.stream_of(self._device)
-        gsize = grad.element_size()
-        psize = dev.element_size()
         momentum = bool(flags & _native.SGD_MOMENTUM)
-        host_states = [self._optimizer.state[host_p]["momentum_buffer"]] if momentum else []
+        first = bool(flags & _native.SGD_FIRST_STEP)
+        buffers = ([HostOperand(self._optimizer.state[host_p]["momentum_buffer"], load=not first, store=True)]
+                   if momentum else [])
 
-        def launch(start: int, n: int, staged: list[torch.Tensor]) -> None:
+        def call(p_ptr: int, g_ptr: int, b_ptr: int | None, n: int) -> None:
             status = lib.hbt_sgd_step(
-                _native.pointer_array([dev.data_ptr() + psize * start]),
-                _native.pointer_array([grad.data_ptr() + gsize * start]),
-                _native.pointer_array([staged[0].data_ptr()]) if staged else None,
+                _native.pointer_array([p_ptr]),
+                _native.pointer_array([g_ptr]),
+                _native.pointer_array([b_ptr]) if b_ptr is not None else None,
                 _native.int64_array([n]),
                 1,
                 _native.dtype_code(pdtype),
@@ -962,9 +989,24 @@ class ShardedOptimizer:
             )
             _native.check(status, "optim.hbt_sgd_step")
 
-        # A first step writes the buffer without reading it: nothing to upload.
-        self._pipeline.run(dev, host_p, host_states, not (flags & _native.SGD_FIRST_STEP), launch)
-        increment_version([dev, host_p, *host_states])
+        if dev is not None:
+            grad = dev.grad
+            psize, gsize = dev.element_size(), grad.element_size()
+            self._stream.run(
+                dev.numel(), buffers,
+                lambda start, n, st: call(dev.data_ptr() + psize * start, grad.data_ptr() + gsize * start,
+                                          st[0].data_ptr() if st else None, n),
+                resident=(dev.detach().view(-1), host_p.detach().view(-1)),
+            )
+            increment_version([dev, host_p, *(b.host for b in buffers)])
+            return
+        write_grad = bool(flags & _native.STEP_WRITE_GRAD)
+        self._stream.run(
+            host_p.numel(),
+            [HostOperand(host_p, store=True), HostOperand(host_p.grad, store=write_grad), *buffers],
+            lambda start, n, st: call(st[0].data_ptr(), st[1].data_ptr(), st[2].data_ptr() if momentum else None, n),
+        )
+        increment_version([host_p, *(b.host for b in buffers)])
 
     def zero_grad(self, *, set_to_none: bool = True) -> None:
         """Release or zero the gradients (``sharded_optimizer.py:357-372``).
@@ -1026,8 +1068,8 @@ class ShardedOptimizer:
     # -- serialisation -------------------------------------------------------------------
     def state_dict(self) -> dict[str, Any]:
         """Optimizer state keyed by parameter index (``sharded_optimizer.py:420-443``)."""
-        if self._pipeline is not None:
-            self._pipeline.synchronize()
+        if self._stream is not None:
+            self._stream.synchronize()
         inner = self._optimizer.state_dict()
         state: dict[int, dict[str, Any]] = {}
         for index, entry in inner["state"].items():
@@ -1069,7 +1111,7 @@ class ShardedOptimizer:
             merged.update(saved)
             merged["params"] = existing["params"]
             groups.append(merged)
-        target = self._cpu_parameters if self._pipeline is not None else self._parameters
+        target = self._cpu_parameters if self._offload else self._parameters
         state: dict[int, dict[str, Any]] = {}
         for index, entry in payload["state"].items():
             reference = target[int(index)]

@@ -438,10 +438,10 @@ def test_random_offloaded_runs(device, monkeypatch, case):
     and deferred or eager clipping: three steps bitwise those of the in-HBM path, state
     and ``.grad`` included."""
     from hybrid_training_amd import OptimizerConfig, ShardedOptimizer
-    from hybrid_training_amd import optim as optim_module
+    from hybrid_training_amd.host_staging import HostStream
 
     rng = np.random.default_rng(4000 + case)
-    monkeypatch.setattr(optim_module._HostStatePipeline, "chunk_elems", int(rng.choice([1000, 4096, 65536])))
+    monkeypatch.setattr(HostStream, "chunk_elems", int(rng.choice([1000, 4096, 65536])))
     sizes = [int(rng.integers(1, 40000)) for _ in range(int(rng.integers(1, 6)))]
     adamw = bool(rng.integers(0, 2))
     defer = bool(rng.integers(0, 2))

@@ -18,6 +18,11 @@ forward.  Checked two ways:
 
 Per-rank gradients come from torch autograd on the CPU: the forward/backward pass
 is the caller of this path, not part of it.
+
+The same run with ``cpu_offload_params`` (the shards, their gradients and the AdamW
+state in pinned host memory, ``fsdp.py:450-451``, ``:763-764``) must give the same
+bits: the reference's offload test asserts that offload changes neither the gradient
+nor the update (``tests/unit/test_single_process_components.py:300-345``).
 """
 
 from __future__ import annotations
@@ -53,8 +58,9 @@ def _mlp(seed=3):
     return nn.Sequential(nn.Linear(23, 32), nn.ReLU(), nn.Linear(32, 32), nn.ReLU(), nn.Linear(32, 1))
 
 
+@pytest.mark.parametrize("offload", [False, True], ids=["hbm", "offload_params"])
 @pytest.mark.parametrize("world", [2, 4])
-def test_fsdp_mlp_matches_oracle_and_single_process(device, world):
+def test_fsdp_mlp_matches_oracle_and_single_process(device, world, offload):
     model = _mlp()
     reference = _mlp()
     named = [(n, p) for n, p in model.named_parameters()]
@@ -66,10 +72,13 @@ def test_fsdp_mlp_matches_oracle_and_single_process(device, world):
 
     dev_named = [(n, nn.Parameter(p.detach().to(device))) for n, p in named]
     handles = [
-        FlatParamHandle(dev_named, None, GroupHandle.local_view("shard", world, r), FSDPConfig(),
-                        MixedPrecisionConfig(), device, keep_originals=True)
+        FlatParamHandle(dev_named, None, GroupHandle.local_view("shard", world, r),
+                        FSDPConfig(cpu_offload_params=offload), MixedPrecisionConfig(), device,
+                        keep_originals=True)
         for r in range(world)
     ]
+    for h in handles:
+        assert (h.flat_param.device.type == "cpu") == offload and h.flat_param.is_pinned() == offload
     shard = handles[0].shard_numel
     assert shard == {2: 929, 4: 465}[world] and handles[0].padding == {2: 1, 4: 3}[world]
     opts = [
@@ -97,6 +106,7 @@ def test_fsdp_mlp_matches_oracle_and_single_process(device, world):
         dev_grads = [torch.from_numpy(g).to(device) for g in rank_grads]
         for r, (h, opt) in enumerate(zip(handles, opts)):
             h.flat_param.grad = h.reduce_scatter_gradient(dev_grads[r], peer_grads=dev_grads)
+            assert h.flat_param.grad.is_pinned() == offload
             opt.step()
             opt.zero_grad()
             valid = max(0, min(shard, 1857 - r * shard))
@@ -118,10 +128,15 @@ def test_fsdp_mlp_matches_oracle_and_single_process(device, world):
 
     expected = dict(reference.named_parameters())
     error = max(float((p.detach() - expected[n].detach()).abs().max()) for n, p in named)
-    print(f"[fsdp mlp W={world}] max weight error vs single-process AdamW after {STEPS} steps: {error:.2e} "
+    print(f"[fsdp mlp W={world}{' offload' if offload else ''}] max weight error vs single-process AdamW after {STEPS} steps: {error:.2e} "
           f"(reference README: {PUBLISHED[world]:.1e})", flush=True)
     assert error < OPTIMIZER_STEP_TOLERANCE, error
     assert error < PUBLISHED_SCALE_BOUND, error
     state_numel = sum(v.numel() for o in opts for s in o.inner.state.values() for v in s.values()
                       if torch.is_tensor(v) and v.numel() > 1)
     assert state_numel == 2 * shard * world  # optimizer state is sharded
+    for o in opts:
+        for s in o.inner.state.values():
+            for v in s.values():
+                if torch.is_tensor(v) and v.numel() > 1:
+                    assert (v.device.type == "cpu") == offload and v.is_pinned() == offload

@@ -24,14 +24,14 @@ import torch
 
 import oracle
 from hybrid_training_amd import GroupHandle, OptimizerConfig, ShardedOptimizer
-from hybrid_training_amd import optim as optim_module
+from hybrid_training_amd.host_staging import HostStream
 
 pytestmark = pytest.mark.gpu
 
 
 @pytest.fixture
 def small_chunks(monkeypatch):
-    monkeypatch.setattr(optim_module._HostStatePipeline, "chunk_elems", 4096)
+    monkeypatch.setattr(HostStream, "chunk_elems", 4096)
 
 
 def _pair(device, config, sizes, defer_clip=False):
