@@ -61,7 +61,7 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument(
         "--workload",
         choices=["adamw", "buckets", "reshard", "scaler", "fsdp", "inplace_clip", "torch_adamw", "sgd", "offload",
-                 "checkpoint", "copy_ceiling"],
+                 "param_offload", "checkpoint", "copy_ceiling"],
         default="adamw",
         help="adamw (default): the Llama-3-8B W=8 shard step above; buckets: GPT-2-small DDP bucket "
         "pack + AVG divide at W=8; reshard: Llama-3-8B bf16 flat shards W=4 -> W=8 and W=2; scaler: "
@@ -69,7 +69,8 @@ def parse_args() -> argparse.Namespace:
         "Llama-3-8B FSDP pack, unpack, gradient local share and no_sync accumulation at W=8; inplace_clip: the headline step with "
         "the reference's in-place clip; torch_adamw: the headline step with stock torch GPU kernels; sgd: "
         "the headline shard with SGD (momentum 0.9); offload: the headline step with AdamW state in pinned "
-        "host memory; checkpoint: Llama-3-8B bf16 saved by 4 FSDP ranks and loaded back at W=8; "
+        "host memory; param_offload: the headline shard as an FSDP unit with the shard, its gradient and "
+        "its AdamW state in pinned host memory; checkpoint: Llama-3-8B bf16 saved by 4 FSDP ranks and loaded back at W=8; "
         "copy_ceiling: torch's device-to-device copy against the interval copy on 1 and 16 GiB",
     )
     ap.add_argument(
@@ -862,15 +863,17 @@ def bench_offload(steps: int, warmup: int) -> int:
     (8 B) and writes back the master parameter, m and v (12 B) over the host link,
     overlapped with the update of neighbouring chunks.  The roofline is the link:
     PCIe 5.0 x16, 64 GB/s per direction, against the 12 B/param write-back direction.
-    The line also carries the link's measured rates (``_link_ceiling``, before the
-    timed steps): with both directions busy, as in the step, each gets less than alone.
+    The line also carries the link's measured rates (``_link_ceiling``, after the timed
+    steps): with both directions busy, as in the step, each gets less than alone.  The
+    probe runs after the steps because its copy streams, once they have copied, change
+    which copy resources the HIP runtime gives streams that copy later (measured: the
+    pipeline's streams, copying second in the process, serialised the two directions).
     """
     import torch
 
     from hybrid_training_amd import GroupHandle, OptimizerConfig, ShardedOptimizer
 
     device = torch.device("cuda", 0)
-    link = _link_ceiling(device)
     n = SHARD_NUMEL
     param, grad = _headline_inputs(device, n)
     opt = ShardedOptimizer([param], OptimizerConfig(learning_rate=LR, betas=BETAS, eps=EPS, weight_decay=WD,
@@ -885,6 +888,7 @@ def bench_offload(steps: int, warmup: int) -> int:
 
     steps, warmup = max(1, min(steps, 5)), max(1, min(warmup, 2))
     ms = _time_events(step, steps, warmup)
+    link = _link_ceiling(device)
     link_gbps = 12 * n / (ms * 1e-3) / 1e9
     line = {
         "metric": "sharded AdamW+clip step with host-offloaded state: params/s", "value": n / (ms * 1e-3),
@@ -897,6 +901,104 @@ def bench_offload(steps: int, warmup: int) -> int:
                      "frac": link_gbps / 64.0, "traffic": None, "traffic_per": "step, device-to-host direction"},
         "link_measured_gbps": link,
         "frac_of_measured_duplex": link_gbps / link["duplex_per_direction"],
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def bench_param_offload(steps: int, warmup: int) -> int:
+    """The headline shard as an FSDP unit with ``cpu_offload_params``: shard, gradient and
+    AdamW state in pinned host memory.
+
+    Per step, as the reference runs it (``fsdp.py:763-764``, then the clip and the
+    optimizer step on the host shard): the local share's gradient shard is copied down to
+    the host (4 B/param), the clip takes its norm from the local share's partials (no
+    read), and the step streams p, g, m, v up (16 B) and p, m, v and the clipped g down
+    (16 B), chunk by chunk, overlapped with the update.  The device holds none of the
+    shard or its state, only the staging slots.  The roofline is the link's heavier
+    direction, device to host: 20 B/param.  The line also gives the step's bound at the
+    link rates measured in the same process: the gradient copy alone in one direction
+    (it must have landed when the reduce-scatter returns), then the streamed step with
+    both directions busy.
+
+    Beside it, the reference's own step for this configuration: torch's CPU AdamW
+    (``foreach`` off, its CPU default) on a host shard after the in-place clip, timed on
+    a 2^25-element sample with torch's host threads and scaled to the full shard.  The
+    link's own rates are measured after the timed steps, for the reason given under
+    ``bench_offload``.
+    """
+    import torch
+    import torch.nn as nn
+
+    from hybrid_training_amd import (FlatParamHandle, FSDPConfig, GroupHandle, MixedPrecisionConfig,
+                                     OptimizerConfig, ShardedOptimizer)
+
+    device = torch.device("cuda", 0)
+    n = SHARD_NUMEL
+    param, grad_full = _headline_inputs(device, n)
+    handle = FlatParamHandle([("shard", nn.Parameter(param))], None, GroupHandle.trivial("shard"),
+                             FSDPConfig(cpu_offload_params=True), MixedPrecisionConfig(), device,
+                             keep_originals=True)
+    del param
+    torch.cuda.empty_cache()
+    opt = ShardedOptimizer([handle.flat_param], OptimizerConfig(learning_rate=LR, betas=BETAS, eps=EPS,
+                                                                weight_decay=WD),
+                           norm_group=GroupHandle.trivial("world"), device=device)
+
+    def step():
+        handle.flat_param.grad = handle.reduce_scatter_gradient(grad_full)
+        opt.clip_grad_norm(MAX_NORM)
+        opt.step()
+
+    steps, warmup = max(1, min(steps, 5)), max(1, min(warmup, 2))
+    ms = _time_events(step, steps, warmup)
+    link = _link_ceiling(device)
+    down, up = 20 * n, 16 * n
+    link_gbps = down / (ms * 1e-3) / 1e9
+
+    # the reference's step on the host: clip in place, then torch's CPU AdamW
+    sample = 1 << 25
+    gen = torch.Generator().manual_seed(0)
+    p_cpu = nn.Parameter(torch.randn(sample, generator=gen) * 0.02)
+    g_cpu = torch.randn(sample, generator=gen) * 1e-4
+    ref = torch.optim.AdamW([p_cpu], lr=LR, betas=BETAS, eps=EPS, weight_decay=WD)
+
+    def cpu_step():
+        g = g_cpu.clone()
+        norm = float(g.double().pow(2).sum().sqrt())
+        coef = MAX_NORM / (norm + 1e-6)
+        if coef < 1.0:
+            g.mul_(coef)
+        p_cpu.grad = g
+        ref.step()
+
+    cpu_step()
+    reps = 3
+    start = time.perf_counter()
+    for _ in range(reps):
+        cpu_step()
+    cpu_s = (time.perf_counter() - start) / reps
+    cpu_rate = sample / cpu_s
+    line = {
+        "metric": "FSDP step with the shard offloaded to host memory (gradient down, clip, AdamW): params/s",
+        "value": n / (ms * 1e-3), "unit": "params/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (device-generated)",
+        "config": {"workload": "Llama-3-8B FSDP rank shard at W=8, cpu_offload_params: shard, gradient and AdamW "
+                               "state in pinned host memory",
+                   "shard_numel": n, "link_bytes_per_param": {"host_to_device": 16, "device_to_host": 20},
+                   "link_bytes_per_step": {"host_to_device": up, "device_to_host": down}},
+        "roofline": {"bound": "pcie", "achieved": link_gbps, "peak": 64.0, "unit": "GB/s",
+                     "frac": link_gbps / 64.0, "traffic": None, "traffic_per": "step, device-to-host direction"},
+        "link_measured_gbps": link,
+        "frac_of_measured_duplex": link_gbps / link["duplex_per_direction"],
+        "link_bound_ms": (4 * n / link["device_to_host"] + 16 * n / link["duplex_per_direction"]) / 1e6,
+        "frac_of_link_bound": (4 * n / link["device_to_host"] + 16 * n / link["duplex_per_direction"]) / 1e6 / ms,
+        "reference_cpu_step": {"value": cpu_rate, "unit": "params/s", "cores": torch.get_num_threads(),
+                               "kind": "torch CPU AdamW (foreach off) after the in-place clip, the reference's "
+                                       "step on an offloaded shard",
+                               "sample": f"{sample} fp32 elements, mean of {reps} steps",
+                               "ms_per_step_at_shard": n / cpu_rate * 1e3},
     }
     print(json.dumps(line), flush=True)
     return 0
@@ -981,7 +1083,7 @@ def bench_copy_ceiling(steps: int, warmup: int) -> int:
 
 SECONDARY = {"buckets": bench_buckets, "reshard": bench_reshard, "scaler": bench_scaler, "fsdp": bench_fsdp,
              "inplace_clip": bench_inplace_clip, "torch_adamw": bench_torch_adamw, "sgd": bench_sgd,
-             "offload": bench_offload, "checkpoint": bench_checkpoint, "copy_ceiling": bench_copy_ceiling}
+             "offload": bench_offload, "param_offload": bench_param_offload, "checkpoint": bench_checkpoint, "copy_ceiling": bench_copy_ceiling}
 
 
 if __name__ == "__main__":

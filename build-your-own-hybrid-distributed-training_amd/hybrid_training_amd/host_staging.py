@@ -3,15 +3,23 @@
 No kernel of this package reads host memory.  Optimizer state kept on the host
 (``cpu_offload_state``), parameter shards kept on the host (``cpu_offload_params``) and
 the gradients of those shards reach the kernels through device staging buffers, chunk
-by chunk: while chunk ``c`` is processed on the compute stream, chunk ``c + 1`` is
-uploaded on one copy stream and chunk ``c - 1`` written back on another.  Two staging
-slots per operand bound the device memory a pass uses to
-``2 * operands * (chunk_elems + lead) * element size``.
+by chunk, on two streams of the pass's own: the upload stream copies chunk ``c`` in and
+runs its kernel, while the download stream writes chunk ``c - 1`` back, so the two link
+directions stay busy at once.  Two staging slots per operand bound the device memory a
+pass uses to ``2 * operands * (chunk_elems + lead) * element size``.
 
-A pass is ordered after the work already queued on the compute stream, and work
-queued on it afterwards waits for the pass's last write-back, so device-side
-consumers need no synchronisation.  Host-side readers of what a pass wrote call
-:meth:`HostStream.synchronize` first.
+The caller's (compute) stream takes no part inside a pass: the pass starts after the
+work already queued on it, and work queued on it afterwards waits for the pass's last
+write-back, so device-side consumers need no synchronisation.  Host-side readers of
+what a pass wrote call :meth:`HostStream.synchronize` first.
+
+The two directions overlap only when the HIP runtime gives the two streams' copies
+separate copy resources, and which it gives a stream depends on what other streams of
+the process copied before it: measured on MI355X, a pair of streams that was the second
+pair to copy in its process ran a 1e9-parameter AdamW pass in 564 ms against 339 ms,
+its directions serialised, while the first and third pairs overlapped.  Nothing here
+can choose those resources; one stream pair per device, created once, keeps the
+assignment stable for the life of the process.
 """
 
 from __future__ import annotations
@@ -89,14 +97,15 @@ class HostStream:
         self,
         total: int,
         operands: Sequence[HostOperand],
-        launch: Callable[[int, int, list[torch.Tensor]], None],
+        launch: Callable[[int, int, list[torch.Tensor], int], None],
         *,
         lead: int = 0,
         chunk: int | None = None,
         resident: tuple[torch.Tensor, torch.Tensor] | None = None,
     ) -> None:
-        """Call ``launch(start, n, staged)`` on the compute stream for every chunk
-        ``[start, start + n)`` of a ``total``-element pass.
+        """Call ``launch(start, n, staged, stream)`` for every chunk ``[start, start + n)``
+        of a ``total``-element pass; ``stream`` is the raw ``hipStream_t`` the chunk's
+        kernels go on (the upload stream, after the chunk's copies).
 
         ``staged[k]`` is the device copy of ``operands[k].host[start : start + n]``.  It
         begins ``lead`` elements into its staging buffer, whose base is 256-byte aligned,
@@ -126,18 +135,15 @@ class HostStream:
                 buf[lead * f.element_size() : (lead + n) * f.element_size()].view(f.dtype)
                 for buf, f in zip(buffers[slot], flats)
             ]
-            loaded = torch.cuda.Event()
+            computed = torch.cuda.Event()
             with torch.cuda.stream(self.upload):
                 if free[slot] is not None:
                     self.upload.wait_event(free[slot])  # the slot's previous chunk is written back
                 for op, d, h in zip(operands, staged, flats):
                     if op.load:
                         d.copy_(h[start : start + n], non_blocking=True)
-                loaded.record(self.upload)
-            compute.wait_event(loaded)
-            launch(start, n, staged)
-            computed = torch.cuda.Event()
-            computed.record(compute)
+                launch(start, n, staged, self.upload.cuda_stream)
+                computed.record(self.upload)
             released = torch.cuda.Event()
             with torch.cuda.stream(self.download):
                 self.download.wait_event(computed)

@@ -419,9 +419,8 @@ def _stream_sqnorm(lib, grad, offset, length, weight, dtype, unscale, partials, 
     norm_chunk = norm_chunk_elems(dtype)
     staging = host_stream(device)
     chunk = max(norm_chunk, staging.chunk_elems // norm_chunk * norm_chunk)
-    stream = _native.stream_of(device)
 
-    def launch(start: int, n: int, staged: list[torch.Tensor]) -> None:
+    def launch(start: int, n: int, staged: list[torch.Tensor], stream: int) -> None:
         _launch_sqnorm(lib, [(staged[0], 0, n, weight)], dtype, unscale, partials, slot + start // norm_chunk, stream)
 
     staging.run(length, [HostOperand(flat[offset : offset + length])], launch, lead=lead, chunk=chunk)
@@ -452,9 +451,8 @@ def scale_gradients(grads: Sequence[torch.Tensor], dtype: torch.dtype, unscale: 
     ``grad.mul_``).  Gradients in HBM go in launches of up to 16; a gradient in host
     memory streams through ``device`` and is final on the host when this returns."""
     lib = _native.library()
-    stream = _native.stream_of(device)
 
-    def call(ptrs: list[int], numels: list[int]) -> None:
+    def call(ptrs: list[int], numels: list[int], stream: int) -> None:
         status = lib.hbt_scale_inplace(_native.pointer_array(ptrs), _native.int64_array(numels), len(ptrs),
                                        _native.dtype_code(dtype), unscale, grad_mul_ptr, stream)
         _native.check(status, operation)
@@ -464,13 +462,13 @@ def scale_gradients(grads: Sequence[torch.Tensor], dtype: torch.dtype, unscale: 
     with torch.cuda.device(device):
         for start in range(0, len(resident), _native.MAX_TENSORS_PER_LAUNCH):
             chunk = resident[start : start + _native.MAX_TENSORS_PER_LAUNCH]
-            call([g.data_ptr() for g in chunk], [g.numel() for g in chunk])
+            call([g.data_ptr() for g in chunk], [g.numel() for g in chunk], _native.stream_of(device))
             increment_version(chunk)
         if hosted:
             staging = host_stream(device)
             for g in hosted:
                 staging.run(g.numel(), [HostOperand(g, store=True)],
-                            lambda start, n, st: call([st[0].data_ptr()], [n]))
+                            lambda start, n, st, stream: call([st[0].data_ptr()], [n], stream))
             increment_version(hosted)
             staging.synchronize()
 
@@ -855,9 +853,8 @@ class ShardedOptimizer:
         dev = self._device_param.get(id(host_p))
         state = self._optimizer.state[host_p]
         m, v = state["exp_avg"], state["exp_avg_sq"]
-        stream = _native.stream_of(self._device)
 
-        def call(p_ptr: int, g_ptr: int, m_ptr: int, v_ptr: int, n: int) -> None:
+        def call(p_ptr: int, g_ptr: int, m_ptr: int, v_ptr: int, n: int, stream: int) -> None:
             status = lib.hbt_adamw_step(
                 _native.pointer_array([p_ptr]),
                 _native.pointer_array([g_ptr]),
@@ -880,8 +877,8 @@ class ShardedOptimizer:
             psize, gsize = dev.element_size(), grad.element_size()
             self._stream.run(
                 dev.numel(), [HostOperand(m, store=True), HostOperand(v, store=True)],
-                lambda start, n, st: call(dev.data_ptr() + psize * start, grad.data_ptr() + gsize * start,
-                                          st[0].data_ptr(), st[1].data_ptr(), n),
+                lambda start, n, st, stream: call(dev.data_ptr() + psize * start, grad.data_ptr() + gsize * start,
+                                                  st[0].data_ptr(), st[1].data_ptr(), n, stream),
                 resident=(dev.detach().view(-1), host_p.detach().view(-1)),
             )
             increment_version([dev, host_p, m, v])
@@ -891,7 +888,8 @@ class ShardedOptimizer:
             host_p.numel(),
             [HostOperand(host_p, store=True), HostOperand(host_p.grad, store=write_grad),
              HostOperand(m, store=True), HostOperand(v, store=True)],
-            lambda start, n, st: call(st[0].data_ptr(), st[1].data_ptr(), st[2].data_ptr(), st[3].data_ptr(), n),
+            lambda start, n, st, stream: call(st[0].data_ptr(), st[1].data_ptr(), st[2].data_ptr(), st[3].data_ptr(),
+                                              n, stream),
         )
         increment_version([host_p, m, v])
 
@@ -966,13 +964,12 @@ class ShardedOptimizer:
         host (see :meth:`_streamed_adamw`).  A first step writes the buffer without
         reading it, so the buffer is not uploaded then."""
         dev = self._device_param.get(id(host_p))
-        stream = _native.stream_of(self._device)
         momentum = bool(flags & _native.SGD_MOMENTUM)
         first = bool(flags & _native.SGD_FIRST_STEP)
         buffers = ([HostOperand(self._optimizer.state[host_p]["momentum_buffer"], load=not first, store=True)]
                    if momentum else [])
 
-        def call(p_ptr: int, g_ptr: int, b_ptr: int | None, n: int) -> None:
+        def call(p_ptr: int, g_ptr: int, b_ptr: int | None, n: int, stream: int) -> None:
             status = lib.hbt_sgd_step(
                 _native.pointer_array([p_ptr]),
                 _native.pointer_array([g_ptr]),
@@ -994,8 +991,8 @@ class ShardedOptimizer:
             psize, gsize = dev.element_size(), grad.element_size()
             self._stream.run(
                 dev.numel(), buffers,
-                lambda start, n, st: call(dev.data_ptr() + psize * start, grad.data_ptr() + gsize * start,
-                                          st[0].data_ptr() if st else None, n),
+                lambda start, n, st, stream: call(dev.data_ptr() + psize * start, grad.data_ptr() + gsize * start,
+                                                  st[0].data_ptr() if st else None, n, stream),
                 resident=(dev.detach().view(-1), host_p.detach().view(-1)),
             )
             increment_version([dev, host_p, *(b.host for b in buffers)])
@@ -1004,7 +1001,8 @@ class ShardedOptimizer:
         self._stream.run(
             host_p.numel(),
             [HostOperand(host_p, store=True), HostOperand(host_p.grad, store=write_grad), *buffers],
-            lambda start, n, st: call(st[0].data_ptr(), st[1].data_ptr(), st[2].data_ptr() if momentum else None, n),
+            lambda start, n, st, stream: call(st[0].data_ptr(), st[1].data_ptr(),
+                                              st[2].data_ptr() if momentum else None, n, stream),
         )
         increment_version([host_p, *(b.host for b in buffers)])
 
