@@ -516,6 +516,13 @@ def _grad_signature(params: Sequence[nn.Parameter]) -> tuple[tuple[int, int, int
     return tuple(sig)
 
 
+def _write_back_flag(write_back: bool, grad_mul: torch.Tensor | None, unscale: float) -> int:
+    """``HBT_STEP_WRITE_GRAD`` when the update must store the scaled gradient: with
+    in-place semantics and a multiplier pending.  Without one the gradient is unchanged,
+    so neither the store nor, for a host gradient, the copy back is needed."""
+    return _native.STEP_WRITE_GRAD if write_back and (grad_mul is not None or unscale != 1.0) else 0
+
+
 def _pinned_like(p: torch.Tensor) -> torch.Tensor:
     """An uninitialised host tensor shaped like ``p``, in pinned (page-locked) memory."""
     return torch.empty(p.shape, dtype=p.dtype, device="cpu", pin_memory=True)
@@ -759,7 +766,6 @@ class ShardedOptimizer:
 
     def _run_adamw_step(self, grad_mul: torch.Tensor | None, write_back: bool) -> None:
         lib = _native.library()
-        flags = _native.STEP_WRITE_GRAD if write_back else 0
         batches: dict[tuple, list[nn.Parameter]] = {}
         for group in self._optimizer.param_groups:
             lr = float(group["lr"])
@@ -802,6 +808,7 @@ class ShardedOptimizer:
         mul_ptr = None if grad_mul is None else grad_mul.data_ptr()
         with torch.cuda.device(self._device):
             for (scalars, pdtype, gdtype, unscale), batch in batches.items():
+                flags = _write_back_flag(write_back, grad_mul, unscale)
                 for p in batch:
                     if is_host(p):
                         self._streamed_adamw(lib, p, scalars, pdtype, gdtype, unscale, mul_ptr, flags)
@@ -896,7 +903,6 @@ class ShardedOptimizer:
     def _run_sgd_step(self, grad_mul: torch.Tensor | None, write_back: bool) -> None:
         """torch.optim.SGD's step (``torch/optim/sgd.py``) as one fused kernel per batch."""
         lib = _native.library()
-        write_flag = _native.STEP_WRITE_GRAD if write_back else 0
         batches: dict[tuple, list[nn.Parameter]] = {}
         for group in self._optimizer.param_groups:
             lr = float(group["lr"])
@@ -926,7 +932,8 @@ class ShardedOptimizer:
                 # Scalars exactly as torch forms them: Python doubles, rounded to fp32 (and
                 # each alpha to a 2-byte parameter dtype inside the kernel's entry point).
                 scalars = (weight_decay, momentum, 1 - dampening, -lr)
-                key = (scalars, flags | write_flag, p.dtype, grad.dtype, _pending_unscale(grad))
+                unscale = _pending_unscale(grad)
+                key = (scalars, flags | _write_back_flag(write_back, grad_mul, unscale), p.dtype, grad.dtype, unscale)
                 batches.setdefault(key, []).append(p)
         stream = _native.stream_of(self._device)
         mul_ptr = None if grad_mul is None else grad_mul.data_ptr()
