@@ -15,7 +15,8 @@ HBM:
   random sizes, chunkings, master dtypes and clip placement (parameters, gradients and
   state), and for fp32 the oracle;
 * the norm pass over host gradients at every 16-byte alignment;
-* the loss scaler's eager unscale and overflow check on host gradients.
+* the loss scaler's eager unscale and overflow check on host gradients;
+* ``no_sync`` accumulation and the gathered buffer's storage cycle on an offloaded unit.
 """
 
 from __future__ import annotations
@@ -329,3 +330,58 @@ def test_offloaded_checkpoint_round_trip(device, tmp_path, small_chunks):
             state = opt.inner.state[h.flat_param]
             assert (state["exp_avg"].device.type == "cpu") == offload
             assert np.array_equal(_bits(state["exp_avg"][:valid]), _bits(m[start : start + valid])), (offload, r)
+
+
+@pytest.mark.parametrize("mixed", [False, True], ids=["fp32", "fp16_compute"])
+def test_offloaded_no_sync_and_storage_cycle(device, small_chunks, mixed):
+    """``no_sync`` accumulation (``fsdp.py:738-749``) and the gathered buffer's storage
+    cycle (``unshard`` / ``reshard`` / ``refill``, ``fsdp.py:624-701``) on an offloaded
+    unit at G = 3: every gradient shard and every refilled buffer is the in-HBM unit's,
+    bitwise; with fp16 compute the loss-scaled engine tail (eager unscale, clip, AdamW)
+    follows as well."""
+    mp = (MixedPrecisionConfig(enabled=True, param_dtype="float16", reduce_dtype="float32", master_dtype="float32",
+                               scaler=GradScalerConfig(enabled=True, init_scale=1024.0))
+          if mixed else MixedPrecisionConfig())
+    named = _named(device, seed=6)
+    group = 3
+    runs = []
+    for offload in (False, True):
+        handles = _handles(named, group, device, offload, mp)
+        opts = [ShardedOptimizer([h.flat_param], OptimizerConfig(learning_rate=1e-3, weight_decay=0.01),
+                                 norm_group=GroupHandle.local_view("world", group, r), device=device)
+                for r, h in enumerate(handles)]
+        scaler = GradScaler(GradScalerConfig(enabled=mixed, init_scale=1024.0), GroupHandle.trivial(), device)
+        runs.append((handles, opts, scaler))
+    gen = torch.Generator(device=device).manual_seed(13)
+    padded = runs[0][0][0].padded_numel
+    for step in range(2):
+        compute = torch.float16 if mixed else torch.float32
+        micro = [[(torch.randn(padded, device=device, generator=gen) * 0.05).to(compute) for _ in range(group)]
+                 for _ in range(3)]
+        shards = []
+        for handles, opts, scaler in runs:
+            fulls = []
+            for r, h in enumerate(handles):
+                full = h.unshard([x.flat_param for x in handles])
+                h.reshard()
+                assert full.untyped_storage().nbytes() == 0
+                h.refill(full, [x.flat_param for x in handles])
+                fulls.append(full)
+                h.set_accumulate_without_reduction(True)
+                for grads in micro[:-1]:
+                    assert h.reduce_scatter_gradient(grads[r], peer_grads=grads) is None
+                h.set_accumulate_without_reduction(False)
+                h.flat_param.grad = h.reduce_scatter_gradient(micro[-1][r], peer_grads=micro[-1])
+            for h, opt in zip(handles, opts):
+                params = [h.flat_param]
+                scaler.unscale_(params)
+                opt.clip_grad_norm(0.5)
+                scaler.step(opt, params, already_unscaled=True)
+                opt.zero_grad(set_to_none=False)
+            scaler.update()
+            shards.append(([_bits(h.flat_param) for h in handles], [_bits(f) for f in fulls]))
+        for r in range(group):
+            assert np.array_equal(shards[0][0][r], shards[1][0][r]), (step, r)
+            assert np.array_equal(shards[0][1][r], shards[1][1][r]), (step, r)
+        for h in runs[1][0]:
+            assert h.flat_param.device.type == "cpu" and not h.has_pending_accumulation
