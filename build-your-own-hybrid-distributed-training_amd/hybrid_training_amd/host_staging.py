@@ -129,6 +129,18 @@ class HostStream:
         compute = torch.cuda.current_stream(self.device)
         free: list[torch.cuda.Event | None] = [None] * self.slots
         self.upload.wait_stream(compute)  # earlier passes and kernels are done
+        try:
+            self._chunks(plan, operands, flats, buffers, lead, launch, resident, free)
+        finally:
+            # also after a failed launch: the copies already queued stay ordered before
+            # whatever the caller's stream does next
+            self.download.wait_stream(self.upload)
+            end = torch.cuda.Event()
+            end.record(self.download)
+            compute.wait_event(end)  # later device work sees the finished copies
+            self.done = end
+
+    def _chunks(self, plan, operands, flats, buffers, lead, launch, resident, free) -> None:
         for index, (start, n) in enumerate(plan):
             slot = index % self.slots
             staged = [
@@ -155,10 +167,6 @@ class HostStream:
                     host_flat[start : start + n].copy_(device_flat[start : start + n], non_blocking=True)
                 released.record(self.download)
             free[slot] = released
-        end = torch.cuda.Event()
-        end.record(self.download)
-        compute.wait_event(end)  # later device work sees the finished copies
-        self.done = end
 
     def synchronize(self) -> None:
         """Block the host until the last pass's write-back has landed."""

@@ -186,9 +186,10 @@ def test_offloaded_fsdp_step_matches_reference_offload_and_oracle(device, small_
 @pytest.mark.parametrize("case", range(12))
 def test_random_host_resident_parameters(device, monkeypatch, case):
     """Host-resident parameters (all or some of an optimizer's) with random sizes, chunk
-    sizes, fp32 / bf16 / fp16 masters, AdamW or SGD, eager or deferred clip, and state
-    offload on or off: three steps bitwise those of the same parameters in HBM, the
-    returned norms, ``.grad`` and the state included."""
+    sizes, fp32 / bf16 / fp16 masters, AdamW or SGD, eager or deferred clip, state
+    offload on or off, and pinned or pageable host memory (the reference keeps an
+    offloaded shard in pageable memory): three steps bitwise those of the same parameters
+    in HBM, the returned norms, ``.grad`` and the state included."""
     rng = np.random.default_rng(7000 + case)
     monkeypatch.setattr(HostStream, "chunk_elems", int(rng.choice([1000, 4096, 65536, 1 << 25])))
     sizes = [int(rng.integers(1, 150_000)) for _ in range(int(rng.integers(1, 5)))]
@@ -197,16 +198,18 @@ def test_random_host_resident_parameters(device, monkeypatch, case):
     adamw = bool(rng.integers(0, 2))
     defer = bool(rng.integers(0, 2))
     state_offload = bool(rng.integers(0, 2))
+    pinned = bool(rng.integers(0, 2))
+    host_of = (lambda t: t.cpu().pin_memory()) if pinned else (lambda t: t.cpu())
     dtype = [torch.float32, torch.float32, torch.bfloat16, torch.float16][int(rng.integers(0, 4))]
     config = ({"name": "adamw", "learning_rate": 3e-4, "betas": (0.9, 0.95), "weight_decay": 0.1, "eps": 1e-4}
               if adamw else {"name": "sgd", "learning_rate": 0.05, "momentum": 0.9, "weight_decay": 0.01})
     gen = torch.Generator(device=device).manual_seed(case)
     init = [torch.randn(n, device=device, generator=gen).to(dtype) for n in sizes]
     context = (f"case {case}: sizes {sizes}, hosted {hosted}, {dtype}, adamw {adamw}, defer {defer}, "
-               f"state offload {state_offload}, chunk {HostStream.chunk_elems}")
+               f"state offload {state_offload}, pinned {pinned}, chunk {HostStream.chunk_elems}")
     runs = []
     for host in (False, True):
-        params = [nn.Parameter(t.cpu().pin_memory() if host and h else t.clone()) for t, h in zip(init, hosted)]
+        params = [nn.Parameter(host_of(t) if host and h else t.clone()) for t, h in zip(init, hosted)]
         opt = ShardedOptimizer(params, OptimizerConfig(**{**config, "cpu_offload_state": state_offload}),
                                norm_group=GroupHandle.trivial(), device=device, defer_clip=defer)
         runs.append((params, opt))
@@ -215,7 +218,7 @@ def test_random_host_resident_parameters(device, monkeypatch, case):
         norms = []
         for params, opt in runs:
             for p, g in zip(params, grads):
-                p.grad = g.cpu().pin_memory() if p.device.type == "cpu" else g.clone()
+                p.grad = host_of(g) if p.device.type == "cpu" else g.clone()
             norms.append(float(opt.clip_grad_norm(0.5)))
             opt.step()
         assert norms[0] == norms[1], (context, step)
