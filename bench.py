@@ -437,10 +437,10 @@ def bench_scaler(steps: int, warmup: int) -> int:
     Clean step with the multipliers deferred (``defer_unscale``, ``defer_clip``): fused
     unscale + inf check + norm (2 B/param) and unscale + clip + AdamW (26 B/param) =
     28 B/param.  Overflowing step: the check pass only (2 B/param), then skip.  Clean step
-    with the reference's placement (the defaults): ``unscale_`` rewrites the gradient
-    (read and write bf16: 4 B/param), the norm pass (2 B) and the update, which writes the
-    clipped gradient back (26 + 2 B) = 34 B/param; the gradient is restored from a pristine
-    copy before each such step, outside the timed events.
+    with the reference's placement (the defaults): ``unscale_`` rewrites the gradient and
+    sums the squares of the result in the same pass (read and write bf16: 4 B/param), and
+    the update writes the clipped gradient back (26 + 2 B) = 32 B/param; the gradient is
+    restored from a pristine copy before each such step, outside the timed events.
     """
     import torch
 
@@ -518,10 +518,9 @@ def bench_scaler(steps: int, warmup: int) -> int:
     _emit("loss-scaled clipped AdamW step, reference placement (eager unscale_, clip written back): params/s",
           "params/s", n / (ms * 1e-3), ms, eager_steps, eager_warmup, "f32",
           "Llama-3-70B FSDP rank shard at W=8, bf16 grads, scale 2^16, defer_unscale=False, defer_clip=False",
-          34 * n, {"params": n, "bytes_per_param": 34, "skipped": False},
-          _secondary_traffic("scaler", ["reference placement: eager unscale_",
-                                        "reference placement: overflow check (its partials feed the clip)",
-                                        "reference placement: clip + AdamW, clipped g written back"], [1, 1, 1]))
+          32 * n, {"params": n, "bytes_per_param": 32, "skipped": False},
+          _secondary_traffic("scaler", ["reference placement: eager unscale_ with its overflow check, one pass",
+                                        "reference placement: clip + AdamW, clipped g written back"], [1, 1]))
     return 0
 
 

@@ -56,7 +56,7 @@ __all__ = [
     "stream_of",
 ]
 
-ABI_VERSION = 12
+ABI_VERSION = 13
 MAX_TENSORS_PER_LAUNCH = 16
 MAX_LOCAL_RANKS = 64
 
@@ -149,6 +149,10 @@ EXPORTED_SYMBOLS: dict[str, tuple[object, tuple[object, ...]]] = {
          _c_void_p, _c_void_p),
     ),
     "hbt_scale_inplace": (
+        _c_i32,
+        (_ptr_array, _i64_array, _c_i32, _c_i32, _c_f32, _c_void_p, _c_void_p),
+    ),
+    "hbt_scale_inplace_sqnorm": (
         _c_i32,
         (_ptr_array, _i64_array, _c_i32, _c_i32, _c_f32, _c_void_p, _c_void_p),
     ),

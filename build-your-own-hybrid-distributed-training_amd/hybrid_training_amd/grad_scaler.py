@@ -5,12 +5,12 @@ Drop-in for ``optim/grad_scaler.py`` of the reference: the state machine
 serialised state are the reference's (``grad_scaler.py:52-298``).  The gradient work
 is native:
 
-* ``unscale_`` multiplies each gradient by ``fp32(1/scale)`` in its own dtype
-  (``hbt_scale_inplace``, as ``grad.mul_(inverse)`` does) and checks finiteness with
-  one fp64 norm pass: the sum of squares is non-finite exactly when some element is.
-  That pass leaves its per-chunk partials on the gradients, so the optimizer's
-  ``clip_grad_norm`` that follows takes the norm from them without reading the
-  gradients a second time.
+* ``unscale_`` multiplies each gradient by ``fp32(1/scale)`` in its own dtype, as
+  ``grad.mul_(inverse)`` does, and in the same pass sums the squares of the result
+  into fp64 per-chunk partials (``hbt_scale_inplace_sqnorm``): the finiteness check
+  reads those (the sum of squares is non-finite exactly when some element is), and they
+  stay on the gradients, so the optimizer's ``clip_grad_norm`` that follows takes the
+  norm from them too.  Each gradient is read and written once.
 * With ``defer_unscale=True`` the multiply is not applied to ``.grad`` here; the
   factor travels with each gradient tensor and the optimizer's norm pass and fused
   update pass apply it while they read the gradient, rounding the product to the
@@ -42,7 +42,7 @@ from .config import GradScalerConfig
 from .errors import UnsupportedFeatureError, format_error
 from .groups import GroupHandle
 from .host_staging import is_host
-from .optim import PENDING_UNSCALE_ATTR, gradient_norm_pass, scale_gradients
+from .optim import PENDING_UNSCALE_ATTR, gradient_norm_pass, unscale_with_partials
 
 __all__ = ["GradScaler", "GradScalerState"]
 
@@ -174,7 +174,9 @@ class GradScaler:
             device = self._device if is_host(p.grad) else p.grad.device
             groups.setdefault((device, p.grad.dtype), []).append(p.grad)
         for (device, dtype), grads in groups.items():
-            scale_gradients(grads, dtype, inverse, None, device, "grad_scaler.hbt_scale_inplace")
+            # the unscale and the norm partials of its result in one pass; the check
+            # below and the optimizer's clip take the norm from those partials
+            unscale_with_partials(grads, dtype, inverse, device, "grad_scaler.hbt_scale_inplace_sqnorm")
         self._unscaled = True
         return self._detect_non_finite(params)
 

@@ -473,6 +473,62 @@ def scale_gradients(grads: Sequence[torch.Tensor], dtype: torch.dtype, unscale: 
             staging.synchronize()
 
 
+def unscale_with_partials(grads: Sequence[torch.Tensor], dtype: torch.dtype, unscale: float, device: torch.device,
+                          operation: str) -> None:
+    """The loss scaler's in-place unscale, ``g = R(g * unscale)`` rounded to the dtype (the
+    reference's ``grad.mul_(inverse)``), fused with the norm partials of the result
+    (``hbt_scale_inplace_sqnorm``): each gradient leaves with a :class:`NormPartials`
+    record of its whole length, so the overflow check and a following clip read none
+    of them again.  A gradient in host memory streams through ``device``, its staged
+    chunks placed at its own 16-byte alignment as the norm pass places them, and is
+    final on the host when this returns."""
+    lib = _native.library()
+    code = _native.dtype_code(dtype)
+    norm_chunk = norm_chunk_elems(dtype)
+
+    def call(ptrs: list[int], numels: list[int], partials_ptr: int, stream: int) -> None:
+        status = lib.hbt_scale_inplace_sqnorm(_native.pointer_array(ptrs), _native.int64_array(numels), len(ptrs),
+                                              code, unscale, partials_ptr, stream)
+        _native.check(status, operation)
+
+    def count_of(n: int) -> int:
+        return -(-n // norm_chunk)
+
+    resident = [g for g in grads if not is_host(g)]
+    hosted = [g for g in grads if is_host(g)]
+    records: list[tuple[torch.Tensor, torch.Tensor]] = []
+    with torch.cuda.device(device):
+        for start in range(0, len(resident), _native.MAX_TENSORS_PER_LAUNCH):
+            chunk = resident[start : start + _native.MAX_TENSORS_PER_LAUNCH]
+            counts = [count_of(g.numel()) for g in chunk]
+            partials = torch.empty(max(1, sum(counts)), dtype=torch.float64, device=device)
+            call([g.data_ptr() for g in chunk], [g.numel() for g in chunk], partials.data_ptr(),
+                 _native.stream_of(device))
+            offset = 0
+            for g, k in zip(chunk, counts):
+                records.append((g, partials[offset : offset + k]))
+                offset += k
+        if hosted:
+            staging = host_stream(device)
+            step = max(norm_chunk, staging.chunk_elems // norm_chunk * norm_chunk)
+            for g in hosted:
+                flat = g.detach().reshape(-1)
+                partials = torch.empty(max(1, count_of(flat.numel())), dtype=torch.float64, device=device)
+                lead = (flat.data_ptr() % 16) // flat.element_size()
+                staging.run(
+                    flat.numel(), [HostOperand(flat, store=True)],
+                    lambda first, n, st, stream, partials=partials: call(
+                        [st[0].data_ptr()], [n], partials.data_ptr() + 8 * (first // norm_chunk), stream),
+                    lead=lead, chunk=step,
+                )
+                records.append((g, partials[: count_of(flat.numel())]))
+            staging.synchronize()
+    increment_version([g for g, _ in records])
+    for g, partials in records:
+        if g.numel() > 0:
+            setattr(g, NORM_PARTIALS_ATTR, NormPartials(g.data_ptr(), g._version, {(0, g.numel()): partials}, g.dtype))
+
+
 def _check_group(group: GroupHandle, operation: str) -> None:
     if group.size > 1 and group.process_group is not None:
         raise UnsupportedFeatureError(

@@ -349,6 +349,25 @@ int32_t hbt_grad_accumulate(void* const* accumulators, const void* const* grads,
 int32_t hbt_scale_inplace(void* const* tensors, const int64_t* numels, int32_t count,
                           int32_t dtype, float unscale, const float* grad_mul, void* stream);
 
+/* ------------------------------------------------------------------------------
+ * In-place unscale fused with its overflow check: x = R(x * unscale) (dtype F32, BF16
+ * or F16, over up to HBT_MAX_TENSORS_PER_LAUNCH tensors), and in the same pass the
+ * squared-norm partials of the result, weight 1.
+ *
+ * Replaces: the grad.mul_(inverse) loop of GradScaler.unscale_
+ *   (optim/grad_scaler.py:181-186) followed by its finiteness check,
+ *   GradScaler._detect_non_finite (optim/grad_scaler.py:189-200).
+ * Writes exactly what hbt_scale_inplace(tensors, numels, count, dtype, unscale, NULL)
+ * writes, and exactly the partials hbt_grad_sqnorm_partials then computes over the
+ * scaled tensors with weights 1 and unscale 1 (hbt_norm_partials_count of them): the
+ * same per-chunk order, so hbt_grad_norm_finalize gives the overflow flag, and the same
+ * partials serve a later norm of the unchanged gradients.  Reads and writes each
+ * element once, where the two calls read it twice.  With unscale == 1 nothing is
+ * written and only the partials are computed.
+ * ---------------------------------------------------------------------------- */
+int32_t hbt_scale_inplace_sqnorm(void* const* tensors, const int64_t* numels, int32_t count,
+                                 int32_t dtype, float unscale, double* partials, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -10,6 +10,10 @@
   and ``optim/sharded_optimizer.py:333-337``): bitwise against torch's own CPU
   ``mul_`` by a Python float, twice, in the tensor's dtype, over several tensors per
   launch, tails of every length and a misaligned view.
+* ``hbt_scale_inplace_sqnorm`` (the loss scaler's unscale fused with its overflow
+  check, ``optim/grad_scaler.py:181-200``): bitwise the two calls it replaces,
+  ``hbt_scale_inplace`` then ``hbt_grad_sqnorm_partials``, in fp32, bf16 and fp16, over
+  tails, multi-chunk tensors, misaligned views and IEEE specials, partials included.
 * ``hbt_grad_accumulate`` (the ``no_sync`` accumulation of ``parallel/fsdp.py:738-749``):
   bitwise against torch's CPU ``add_`` (or the cast alone, for the first micro-batch)
   in an fp32, bf16 or fp16 accumulator, fp32, bf16 and fp16 gradients, tails of every
@@ -182,6 +186,48 @@ def test_scale_inplace_tiles(device, dtype):
         assert torch.equal(torch.isnan(got), nan)
         assert np.array_equal(_bits(got)[~nan.numpy()], _bits(expect)[~nan.numpy()])
     assert np.array_equal(_bits(base[:1]), lead)  # the element before the first tensor is untouched
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("specials", [False, True])
+def test_scale_inplace_sqnorm_is_the_two_calls(device, dtype, specials):
+    lib = _native.library()
+    gen = torch.Generator(device=device).manual_seed(9)
+    sizes = [1, 7, 4097, 65536, 3 * 65536 + 5, 300_001]
+    base = (torch.randn(sum(sizes) + 2, device=device, generator=gen) * 300.0).to(dtype)
+    if specials:
+        base[9] = float("inf")
+        base[5000] = float("nan")
+        base[70_000] = -float("inf")
+    tensors_a, tensors_b, cursor = [], [], 1  # the first tensor starts one element in: misaligned
+    twin = base.clone()
+    for n in sizes:
+        tensors_a.append(base[cursor : cursor + n])
+        tensors_b.append(twin[cursor : cursor + n])
+        cursor += n
+    code = _native.dtype_code(dtype)
+    unscale = float(np.float32(1.0 / 1000.0))
+    count = int(lib.hbt_norm_partials_count(_native.int64_array(sizes), len(sizes), code))
+    stream = ctypes.c_void_p(_native.stream_of(device))
+    # the two calls: the in-place unscale, then the norm partials of the result
+    _native.check(lib.hbt_scale_inplace(_native.pointer_array([t.data_ptr() for t in tensors_a]),
+                                        _native.int64_array(sizes), len(sizes), code, unscale, None, stream),
+                  "test.scale_inplace")
+    expect = torch.empty(count, dtype=torch.float64, device=device)
+    _native.check(lib.hbt_grad_sqnorm_partials(_native.pointer_array([t.data_ptr() for t in tensors_a]),
+                                               _native.int64_array(sizes), _native.double_array([1.0] * len(sizes)),
+                                               len(sizes), code, 1.0, ctypes.c_void_p(expect.data_ptr()), stream),
+                  "test.sqnorm")
+    # the fused call
+    got = torch.empty(count, dtype=torch.float64, device=device)
+    _native.check(lib.hbt_scale_inplace_sqnorm(_native.pointer_array([t.data_ptr() for t in tensors_b]),
+                                               _native.int64_array(sizes), len(sizes), code, unscale,
+                                               ctypes.c_void_p(got.data_ptr()), stream),
+                  "test.scale_inplace_sqnorm")
+    torch.cuda.synchronize(device)
+    assert np.array_equal(_bits(base), _bits(twin))  # every element, the untouched first one included
+    assert np.array_equal(expect.cpu().numpy().view(np.int64), got.cpu().numpy().view(np.int64))
+    assert bool(torch.isfinite(got).all()) != specials
 
 
 def test_local_share_full_size_rank7_of_llama3_8b_w8(device):

@@ -231,11 +231,12 @@ def test_bf16_engine_sequence_eager_and_deferred_match_the_oracle(device, name):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_eager_unscale_partials_feed_the_clip_norm(device, monkeypatch, dtype):
-    """After an eager ``unscale_``, the overflow check's norm pass leaves its partials on
-    the gradients, and ``clip_grad_norm`` on the unchanged gradients reads no gradient: it
-    launches no norm kernel, and its norm and multiplier are bitwise those of a pass over
-    untagged copies.  An in-place change to one gradient drops that gradient's partials
-    (its version counter moves), and only that gradient is read again."""
+    """An eager ``unscale_`` sums the squares of the unscaled values in the same pass that
+    writes them (``hbt_scale_inplace_sqnorm``): its overflow check launches no norm
+    kernel, the partials stay on the gradients, and ``clip_grad_norm`` on the unchanged
+    gradients reads no gradient either; its norm and multiplier are bitwise those of a
+    pass over untagged copies.  An in-place change to one gradient drops that gradient's
+    partials (its version counter moves), and only that gradient is read again."""
     from hybrid_training_amd import optim as optim_module
 
     gen = torch.Generator(device=device).manual_seed(33)
@@ -247,10 +248,6 @@ def test_eager_unscale_partials_feed_the_clip_norm(device, monkeypatch, dtype):
     copies = [torch.nn.Parameter(p.detach().clone()) for p in params]
     opt = ShardedOptimizer(params, OptimizerConfig(), norm_group=GroupHandle.trivial(), device=device)
     scaler = GradScaler(GradScalerConfig(enabled=True, init_scale=1000.0), GroupHandle.trivial(), device)
-    assert not scaler.unscale_(params)
-    for c, p in zip(copies, params):
-        c.grad_dtype = None
-        c.grad = p.grad.clone()  # the unscaled values, without partials attached
     launched = []
     real = optim_module._launch_sqnorm
 
@@ -259,6 +256,11 @@ def test_eager_unscale_partials_feed_the_clip_norm(device, monkeypatch, dtype):
         return real(lib, items, *args)
 
     monkeypatch.setattr(optim_module, "_launch_sqnorm", counting)
+    assert not scaler.unscale_(params)
+    assert launched == []  # the overflow check read the fused pass's partials
+    for c, p in zip(copies, params):
+        c.grad_dtype = None
+        c.grad = p.grad.clone()  # the unscaled values, without partials attached
     norm = opt.clip_grad_norm(1.0)
     assert launched == []  # every segment came from the scaler's partials
     ref_opt = ShardedOptimizer(copies, OptimizerConfig(), norm_group=GroupHandle.trivial(), device=device)
