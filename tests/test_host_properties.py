@@ -351,3 +351,27 @@ def test_flat_sharded_manifest_round_trips_and_validates(numels, writers, data):
     unfinished.complete = False
     with pytest.raises(IncompleteCheckpointError, match="not marked complete"):
         unfinished.validate()
+
+
+@settings(deadline=None)
+@given(total=st.integers(0, 2_000_000), chunk=st.integers(256, 1 << 22))
+def test_host_stream_chunks_tile_the_pass_once(total, chunk):
+    """The chunks of a streamed pass over host tensors cover [0, total) once, in order,
+    each at most ``chunk`` long, only the last one shorter; and the norm pass's staged
+    chunks, a whole number of norm chunks, keep every norm partial inside one chunk."""
+    from hybrid_training_amd.host_staging import chunk_plan
+    from hybrid_training_amd.optim import norm_chunk_elems
+
+    plan = chunk_plan(total, chunk)
+    assert sum(n for _, n in plan) == total
+    cursor = 0
+    for i, (start, n) in enumerate(plan):
+        assert start == cursor and 0 < n <= chunk and (n == chunk or i == len(plan) - 1)
+        cursor += n
+    for dtype in (torch.float32, torch.bfloat16):
+        nc = norm_chunk_elems(dtype)
+        step = max(nc, chunk // nc * nc)  # the norm pass's staged chunk
+        for start, n in chunk_plan(total, step):
+            assert start % nc == 0  # the chunk's partials start at partial start // nc
+    with pytest.raises(ValueError):
+        chunk_plan(10, 0)
