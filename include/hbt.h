@@ -337,7 +337,7 @@ int32_t hbt_grad_accumulate(void* const* accumulators, const void* const* grads,
 
 /* ------------------------------------------------------------------------------
  * In-place gradient scaling: x = (x * unscale) * (*grad_mul), each product rounded to
- * the tensor's dtype (F32 or BF16), over up to HBT_MAX_TENSORS_PER_LAUNCH tensors.
+ * the tensor's dtype (F32, BF16 or F16), over up to HBT_MAX_TENSORS_PER_LAUNCH tensors.
  *
  * Replaces: the grad.mul_(inverse) loop of GradScaler.unscale_
  *   (optim/grad_scaler.py:181-186) and the grad.mul_(clip_coefficient) loop of
