@@ -17,9 +17,11 @@ The two directions overlap only when the HIP runtime gives the two streams' copi
 separate copy resources, and which it gives a stream depends on what other streams of
 the process copied before it: measured on MI355X, a pair of streams that was the second
 pair to copy in its process ran a 1e9-parameter AdamW pass in 564 ms against 339 ms,
-its directions serialised, while the first and third pairs overlapped.  Nothing here
-can choose those resources; one stream pair per device, created once, keeps the
-assignment stable for the life of the process.
+its directions serialised, while the first and third pairs overlapped.  The copies run
+as the runtime's blit kernels on the streams' hardware queues (four per process unless
+GPU_MAX_HW_QUEUES says otherwise), and two streams on one queue run in order; with 16
+queues those pairs overlapped.  Nothing here can choose the queue; one stream pair per
+device, created once, keeps the assignment stable for the life of the process.
 """
 
 from __future__ import annotations
