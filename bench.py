@@ -534,7 +534,10 @@ def bench_fsdp(steps: int, warmup: int) -> int:
     Local share: rank 0's ``reduce_scatter_gradient`` over the 8 ranks' padded bf16
     gradients resident on the device (read 8 x 2 B + write 4 B per shard element).
     no_sync: one micro-batch's accumulation of rank 0's slices of the 8 bf16 gradients
-    into its fp32 accumulator (read 4 + 2 B, write 4 B per accumulated element).
+    into its fp32 accumulator (read 4 + 2 B, write 4 B per accumulated element).  no_sync
+    end: the call after the accumulation, which adds the last micro-batch to the 8
+    accumulated rows and reduces them in one pass (read 8 x (4 + 2) B + write 4 B per
+    shard element), the first micro-batch set up outside the timed events.
     """
     import torch
 
@@ -641,6 +644,33 @@ def bench_fsdp(steps: int, warmup: int) -> int:
           _secondary_traffic("fsdp", ["no_sync accumulation"], [1]))
     owner.set_accumulate_without_reduction(False)
     owner.flat_param.grad = owner.reduce_scatter_gradient(grads[0], peer_grads=grads)
+
+    stream = torch.cuda.current_stream(device)
+
+    def end_of_accumulation(events=None):
+        owner.set_accumulate_without_reduction(True)
+        owner.reduce_scatter_gradient(grads[0], peer_grads=grads)  # the first micro-batch, untimed
+        owner.set_accumulate_without_reduction(False)
+        if events is not None:
+            events[0].record(stream)
+        owner.flat_param.grad = owner.reduce_scatter_gradient(grads[0], peer_grads=grads)
+        if events is not None:
+            events[1].record(stream)
+
+    end_steps, end_warmup = max(steps, 5), max(warmup, 2)
+    for _ in range(end_warmup):
+        end_of_accumulation()
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(end_steps)]
+    for e in events:
+        end_of_accumulation(e)
+    torch.cuda.synchronize()
+    ms = sum(e[0].elapsed_time(e[1]) for e in events) / end_steps
+    _emit("FSDP no_sync end: last micro-batch added and reduced in one pass: shard elements/s", "elements/s",
+          shard / (ms * 1e-3), ms, end_steps, end_warmup, "bf16->f32",
+          f"Llama-3-8B rank 0 of W={world}: {world} accumulated fp32 rows plus the last micro-batch's bf16 "
+          "gradients -> fp32 shard, with norm partials", (6 * world + 4) * shard,
+          {"shard_numel": shard, "world": world, "bytes_per_element": 6 * world + 4},
+          _secondary_traffic("fsdp", ["no_sync end: accumulate and reduce in one pass"], [1]))
     del opt, grads, owner, named
     torch.cuda.empty_cache()
     return 0

@@ -529,6 +529,11 @@ __global__ __launch_bounds__(kNormBlock) void sqnorm_kernel(NormTable tab, float
 struct ShareRanks {
     const uint8_t* g[HBT_MAX_LOCAL_RANKS];
 };
+// The no_sync accumulator rows of the reduction that ends the accumulation: row q holds
+// rank q's accumulated gradient over this rank's slice, in the reduce dtype.
+struct ShareAcc {
+    const uint8_t* a[HBT_MAX_LOCAL_RANKS];
+};
 
 constexpr int kShareBlock = 64;
 constexpr int64_t kShareTile = int64_t(kShareBlock) * 4;  // 256 elements, one wave
@@ -567,6 +572,14 @@ __device__ __forceinline__ float share_cast(float x) {
 #define HBT_SHARE_ISSUE 2
 #endif
 constexpr int kShareIssue = HBT_SHARE_ISSUE;
+// With the accumulator rows (kAcc) each rank is two loads, its gradient and its row;
+// waiting after every rank's pair measured best: 8.62-8.65 ms for the 8-rank bf16 +
+// fp32-row reduction of a 1e9-element shard, against 8.84 waiting after every two ranks,
+// 8.82 after four or eight, and 8.70 with all gradients issued before the rows.
+#ifndef HBT_SHARE_ACC_ISSUE
+#define HBT_SHARE_ACC_ISSUE 1
+#endif
+constexpr int kShareAccIssue = HBT_SHARE_ACC_ISSUE;
 
 // Where tile t's sum is stored among a launch's `tiles` tile sums.  Workgroup b owns
 // tile b, and the dispatcher deals consecutive workgroups to the 8 XCDs in turn, each
@@ -586,9 +599,19 @@ __device__ __forceinline__ int64_t tile_sum_slot(int64_t t, int64_t tiles) {
     const int64_t per = n / kXcds;
     return first + (b < per * kXcds ? (b % kXcds) * per + b / kXcds : b);
 }
-template <int ID, int kG, bool kRecip, int RD, int OD>
+// Rank q's element in the reduce dtype: the gradient cast to RD and, when kAcc, added to
+// the accumulated one (R(grad + accumulator), both in RD, as the reference's final
+// no_sync step adds them before reducing).
+template <int ID, int RD, bool kAcc>
+__device__ __forceinline__ float share_input(float g, float a) {
+    const float x = share_cast<ID, RD>(g);
+    if constexpr (kAcc) return round_to<RD>(x + a);
+    return x;
+}
+
+template <int ID, int kG, bool kRecip, int RD, int OD, bool kAcc = false>
 __global__ __launch_bounds__(kShareBlock) void local_share_tiles_kernel(
-    ShareRanks ranks, int32_t group_size, int64_t offset, int64_t shard_numel, int64_t valid_numel,
+    ShareRanks ranks, ShareAcc accs, int32_t group_size, int64_t offset, int64_t shard_numel, int64_t valid_numel,
     float divisor, float recip, int32_t vec_ok, void* __restrict__ out, double* __restrict__ tile_sums,
     int64_t block_base) {
     constexpr int64_t IB = bytes_of<ID>();
@@ -600,29 +623,35 @@ __global__ __launch_bounds__(kShareBlock) void local_share_tiles_kernel(
         float sum[4];
         if constexpr (kG > 0) {
             float x[kG][4];
+            float a[kAcc ? kG : 1][4];
 #pragma unroll
             for (int q = 0; q < kG; ++q) {
                 load_vec<ID, 4>(ranks.g[q] + offset * IB, e, x[q]);
-                if ((q + 1) % kShareIssue == 0 && q + 1 < kG) wait_vmem();
+                if constexpr (kAcc) load_vec<RD, 4>(accs.a[q], e, a[q]);
+                if ((q + 1) % (kAcc ? kShareAccIssue : kShareIssue) == 0 && q + 1 < kG) wait_vmem();
             }
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
-                sum[c] = round_to<RD>(share_div<kRecip>(share_cast<ID, RD>(x[0][c]), divisor, recip));
+                sum[c] = round_to<RD>(share_div<kRecip>(share_input<ID, RD, kAcc>(x[0][c], a[0][c]), divisor, recip));
 #pragma unroll
                 for (int q = 1; q < kG; ++q) {
-                    sum[c] = round_to<RD>(sum[c] + round_to<RD>(share_div<kRecip>(share_cast<ID, RD>(x[q][c]), divisor, recip)));
+                    const float xq = share_input<ID, RD, kAcc>(x[q][c], a[kAcc ? q : 0][c]);
+                    sum[c] = round_to<RD>(sum[c] + round_to<RD>(share_div<kRecip>(xq, divisor, recip)));
                 }
             }
         } else {
             float x[4];
+            float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
             load_vec<ID, 4>(ranks.g[0] + offset * IB, e, x);
+            if constexpr (kAcc) load_vec<RD, 4>(accs.a[0], e, a);
 #pragma unroll
-            for (int c = 0; c < 4; ++c) sum[c] = round_to<RD>(share_div<kRecip>(share_cast<ID, RD>(x[c]), divisor, recip));
+            for (int c = 0; c < 4; ++c) sum[c] = round_to<RD>(share_div<kRecip>(share_input<ID, RD, kAcc>(x[c], a[c]), divisor, recip));
             for (int32_t q = 1; q < group_size; ++q) {
                 load_vec<ID, 4>(ranks.g[q] + offset * IB, e, x);
+                if constexpr (kAcc) load_vec<RD, 4>(accs.a[q], e, a);
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
-                    sum[c] = round_to<RD>(sum[c] + round_to<RD>(share_div<kRecip>(share_cast<ID, RD>(x[c]), divisor, recip)));
+                    sum[c] = round_to<RD>(sum[c] + round_to<RD>(share_div<kRecip>(share_input<ID, RD, kAcc>(x[c], a[c]), divisor, recip)));
                 }
             }
         }
@@ -639,9 +668,12 @@ __global__ __launch_bounds__(kShareBlock) void local_share_tiles_kernel(
         for (int64_t e = base + threadIdx.x; e < end; e += kShareBlock) {
             float v = 0.0f;
             if (e < valid_numel) {
-                v = round_to<RD>(share_div<kRecip>(share_cast<ID, RD>(load_one<ID>(ranks.g[0], offset + e)), divisor, recip));
+                const float a0 = kAcc ? load_one<RD>(accs.a[0], e) : 0.0f;
+                v = round_to<RD>(share_div<kRecip>(share_input<ID, RD, kAcc>(load_one<ID>(ranks.g[0], offset + e), a0),
+                                                   divisor, recip));
                 for (int32_t q = 1; q < group_size; ++q) {
-                    const float x = share_cast<ID, RD>(load_one<ID>(ranks.g[q], offset + e));
+                    const float aq = kAcc ? load_one<RD>(accs.a[q], e) : 0.0f;
+                    const float x = share_input<ID, RD, kAcc>(load_one<ID>(ranks.g[q], offset + e), aq);
                     v = round_to<RD>(v + round_to<RD>(share_div<kRecip>(x, divisor, recip)));
                 }
                 v = round_to<OD>(v);
@@ -988,12 +1020,13 @@ int32_t noalloc_scratch(const char* who, double** out) {
     return HBT_OK;
 }
 
-// Shared by hbt_grad_local_share and hbt_grad_local_share_sqnorm (tile_scratch and
-// partials null for the former).
+// Shared by hbt_grad_local_share, hbt_grad_local_share_sqnorm (tile_scratch and
+// partials null for the former) and hbt_grad_local_share_accumulated (accumulators
+// non-null: row q, in the reduce dtype, is added to rank q's gradient first).
 int32_t local_share(const char* who, const void* const* rank_grads, int32_t group_size, int32_t rank,
                     int64_t shard_numel, int64_t valid_numel, int32_t in_dtype, int32_t reduce_dtype,
                     float divisor, int32_t out_dtype, void* out, double* partials, double* tile_scratch,
-                    hipStream_t st) {
+                    hipStream_t st, const void* const* accumulators = nullptr) {
     if (rank_grads == nullptr || out == nullptr || group_size < 1 || group_size > HBT_MAX_LOCAL_RANKS ||
         rank < 0 || rank >= group_size || shard_numel < 0 || valid_numel < 0 || valid_numel > shard_numel) {
         set_error("%s: bad arguments (group_size=%d rank=%d shard=%lld valid=%lld)", who, group_size, rank,
@@ -1013,7 +1046,14 @@ int32_t local_share(const char* who, const void* const* rank_grads, int32_t grou
         set_error("%s: output (master) dtype %d is not F32, BF16 or F16", who, out_dtype);
         return HBT_ERR_INVALID_ARGUMENT;
     }
+    const bool with_acc = accumulators != nullptr;
+    if (with_acc && f64) {
+        set_error("%s: an accumulated reduction in reduce dtype F64 is not fused; add the last micro-batch "
+                  "with hbt_grad_accumulate and reduce the accumulator", who);
+        return HBT_ERR_UNSUPPORTED;
+    }
     ShareRanks ranks{};
+    ShareAcc accs{};
     const int elem = dtype_size(in_dtype);
     const int64_t offset = int64_t(rank) * shard_numel;
     int32_t vec_ok = aligned(out, 4 * static_cast<uintptr_t>(dtype_size(out_dtype)));
@@ -1025,6 +1065,14 @@ int32_t local_share(const char* who, const void* const* rank_grads, int32_t grou
         ranks.g[q] = static_cast<const uint8_t*>(rank_grads[q]);
         const uintptr_t a = reinterpret_cast<uintptr_t>(ranks.g[q]) + static_cast<uintptr_t>(offset * elem);
         if ((a & static_cast<uintptr_t>(4 * elem - 1)) != 0) vec_ok = 0;
+        if (with_acc) {
+            if (accumulators[q] == nullptr && valid_numel > 0) {
+                set_error("%s: rank %d accumulator pointer is null", who, q);
+                return HBT_ERR_INVALID_ARGUMENT;
+            }
+            accs.a[q] = static_cast<const uint8_t*>(accumulators[q]);
+            if (!aligned(accs.a[q], 4 * static_cast<uintptr_t>(dtype_size(reduce_dtype)))) vec_ok = 0;
+        }
     }
     const int64_t tiles = (shard_numel + kShareTile - 1) / kShareTile;
     if (tiles == 0) return HBT_OK;
@@ -1032,9 +1080,17 @@ int32_t local_share(const char* who, const void* const* rank_grads, int32_t grou
     const float recip = exact_reciprocal(divisor);
     const bool recip_exact = recip != 0.0f;
     int32_t status = launch_sliced(who, tiles, kShareBlock, [&](int64_t first, dim3 grid) {
-#define HBT_TILES(ID, G, R, RD, OD)                                                                         \
-    local_share_tiles_kernel<ID, G, R, RD, OD><<<grid, kShareBlock, 0, st>>>(                                 \
-        ranks, group_size, offset, shard_numel, valid_numel, divisor, recip, vec_ok, out, tile_scratch, first)
+#define HBT_TILES(ID, G, R, RD, OD)                                                                             \
+    do {                                                                                                       \
+        if (with_acc)                                                                                          \
+            local_share_tiles_kernel<ID, G, R, RD, OD, true><<<grid, kShareBlock, 0, st>>>(                      \
+                ranks, accs, group_size, offset, shard_numel, valid_numel, divisor, recip, vec_ok, out,          \
+                tile_scratch, first);                                                                          \
+        else                                                                                                   \
+            local_share_tiles_kernel<ID, G, R, RD, OD, false><<<grid, kShareBlock, 0, st>>>(                     \
+                ranks, accs, group_size, offset, shard_numel, valid_numel, divisor, recip, vec_ok, out,          \
+                tile_scratch, first);                                                                          \
+    } while (0)
 // The fp32 reduction into an fp32 master has group-size specialisations (the measured
 // configuration); other reduce and master dtypes run the run-time group size kernel.
 #define HBT_TILES_G(ID, R)                                       \
@@ -1438,6 +1494,24 @@ int32_t hbt_grad_local_share_sqnorm(const void* const* rank_grads, int32_t group
     }
     return local_share("hbt_grad_local_share_sqnorm", rank_grads, group_size, rank, shard_numel, valid_numel,
                        in_dtype, reduce_dtype, divisor, out_dtype, out, partials, tile_scratch, as_stream(stream));
+}
+
+int32_t hbt_grad_local_share_accumulated(const void* const* rank_grads, const void* const* accumulators,
+                                         int32_t group_size, int32_t rank, int64_t shard_numel, int64_t valid_numel,
+                                         int32_t in_dtype, int32_t reduce_dtype, float divisor, int32_t out_dtype,
+                                         void* out, double* partials, double* tile_scratch, void* stream) {
+    clear_error();
+    if (accumulators == nullptr) {
+        set_error("hbt_grad_local_share_accumulated: null accumulator table");
+        return HBT_ERR_INVALID_ARGUMENT;
+    }
+    if ((partials == nullptr) != (tile_scratch == nullptr)) {
+        set_error("hbt_grad_local_share_accumulated: partials and tile scratch must both be given or both null");
+        return HBT_ERR_INVALID_ARGUMENT;
+    }
+    return local_share("hbt_grad_local_share_accumulated", rank_grads, group_size, rank, shard_numel, valid_numel,
+                       in_dtype, reduce_dtype, divisor, out_dtype, out, partials, tile_scratch, as_stream(stream),
+                       accumulators);
 }
 
 int32_t hbt_sgd_step(void* const* params, void* const* grads, void* const* momentum_buffers,

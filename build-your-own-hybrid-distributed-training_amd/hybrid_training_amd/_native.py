@@ -56,7 +56,7 @@ __all__ = [
     "stream_of",
 ]
 
-ABI_VERSION = 13
+ABI_VERSION = 14
 MAX_TENSORS_PER_LAUNCH = 16
 MAX_LOCAL_RANKS = 64
 
@@ -147,6 +147,11 @@ EXPORTED_SYMBOLS: dict[str, tuple[object, tuple[object, ...]]] = {
         _c_i32,
         (_ptr_array, _c_i32, _c_i32, _c_i64, _c_i64, _c_i32, _c_i32, _c_f32, _c_i32, _c_void_p, _c_void_p,
          _c_void_p, _c_void_p),
+    ),
+    "hbt_grad_local_share_accumulated": (
+        _c_i32,
+        (_ptr_array, _ptr_array, _c_i32, _c_i32, _c_i64, _c_i64, _c_i32, _c_i32, _c_f32, _c_i32, _c_void_p,
+         _c_void_p, _c_void_p, _c_void_p),
     ),
     "hbt_scale_inplace": (
         _c_i32,

@@ -536,7 +536,9 @@ class FlatParamHandle:
         are accumulated in the reduce dtype instead and ``None`` is returned
         (``fsdp.py:738-745``): the first call keeps a copy of each, later calls add to
         it.  The next call outside ``no_sync`` adds its gradients to the accumulated
-        ones and reduces the sums (``fsdp.py:747-749``).
+        ones and reduces the sums (``fsdp.py:747-749``), in one pass that reads each
+        accumulated row once (``hbt_grad_local_share_accumulated``; a float64 reduce
+        dtype adds first and then reduces).
         """
         if self._reduce_dtype not in (torch.float32, torch.bfloat16, torch.float16, torch.float64) \
                 or self._master_dtype not in (torch.float32, torch.bfloat16, torch.float16):
@@ -574,17 +576,24 @@ class FlatParamHandle:
                     )
                 )
         local = self.local_shard_range()
-        if self._accumulate_without_reduction or self._grad_accumulator is not None:
+        source_rank = self._shard_group.local_rank
+        rows = None  # accumulator rows the reduction adds the last micro-batch to
+        if self._accumulate_without_reduction:
             self._accumulate(grads, local.start)
-            if self._accumulate_without_reduction:
-                return None
-            # Reduce the accumulated sums: row q is rank q's total restricted to this
-            # rank's slice, so the local share reads it at rank offset 0.
-            accumulator, self._grad_accumulator = self._grad_accumulator, None
-            grads = list(accumulator.unbind(0))
-            source_rank = 0
-        else:
-            source_rank = self._shard_group.local_rank
+            return None
+        if self._grad_accumulator is not None:
+            if self._reduce_dtype == torch.float64:
+                # Reduce the accumulated sums: row q is rank q's total restricted to this
+                # rank's slice, so the local share reads it at rank offset 0.
+                self._accumulate(grads, local.start)
+                accumulator, self._grad_accumulator = self._grad_accumulator, None
+                grads = list(accumulator.unbind(0))
+                source_rank = 0
+            else:
+                # The last micro-batch is added to the rows inside the reduction
+                # (hbt_grad_local_share_accumulated): the rows are read once, not
+                # rewritten and read again.
+                rows, self._grad_accumulator = self._grad_accumulator, None
         valid = max(0, min(self._shard_numel, self._total_numel - local.start))
         divisor = float(group) if (self._config.average_gradients and group > 1) else 1.0
         out = torch.empty(self._shard_numel, dtype=self._master_dtype, device=self._device)
@@ -594,23 +603,19 @@ class FlatParamHandle:
         partials = torch.empty(max(1, valid_chunks + -(-pad // chunk)), dtype=torch.float64, device=self._device)
         tile_sums = torch.empty(max(1, -(-self._shard_numel // 256)), dtype=torch.float64, device=self._device)
         lib = _native.library()
+        args = (group, source_rank, self._shard_numel, valid, _native.dtype_code(grads[0].dtype),
+                _native.dtype_code(self._reduce_dtype), divisor, _native.dtype_code(self._master_dtype),
+                out.data_ptr(), partials.data_ptr(), tile_sums.data_ptr(), _native.stream_of(self._device))
+        grad_ptrs = _native.pointer_array([g.data_ptr() for g in grads])
         with torch.cuda.device(self._device):
-            status = lib.hbt_grad_local_share_sqnorm(
-                _native.pointer_array([g.data_ptr() for g in grads]),
-                group,
-                source_rank,
-                self._shard_numel,
-                valid,
-                _native.dtype_code(grads[0].dtype),
-                _native.dtype_code(self._reduce_dtype),
-                divisor,
-                _native.dtype_code(self._master_dtype),
-                out.data_ptr(),
-                partials.data_ptr(),
-                tile_sums.data_ptr(),
-                _native.stream_of(self._device),
-            )
-        _native.check(status, "fsdp.hbt_grad_local_share_sqnorm")
+            if rows is None:
+                status = lib.hbt_grad_local_share_sqnorm(grad_ptrs, *args)
+                what = "fsdp.hbt_grad_local_share_sqnorm"
+            else:
+                status = lib.hbt_grad_local_share_accumulated(
+                    grad_ptrs, _native.pointer_array([rows[q].data_ptr() for q in range(group)]), *args)
+                what = "fsdp.hbt_grad_local_share_accumulated"
+        _native.check(status, what)
         # The squared-norm partials of the shard's real and padding segments ride on
         # the gradient, so the next clip_grad_norm does not read it again.
         segments = {}

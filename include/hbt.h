@@ -313,6 +313,29 @@ int32_t hbt_grad_local_share_sqnorm(const void* const* rank_grads, int32_t group
                                     double* partials, double* tile_scratch, void* stream);
 
 /* ------------------------------------------------------------------------------
+ * The reduction that ends a no_sync accumulation, in one pass: hbt_grad_local_share
+ * (or, with partials and tile_scratch, hbt_grad_local_share_sqnorm) where rank q's
+ * element is first added to its accumulated gradient, x_q = R(cast(g_q) + a_q), R
+ * rounding to the reduce dtype.
+ *
+ * Replaces: the final micro-batch of FlatParamHandle.reduce_scatter_gradient under
+ *   no_sync, `grad = grad + self._unsharded_grad_accumulator` then the reduce-scatter
+ *   (parallel/fsdp.py:747-769).
+ * accumulators[q] points at row q of the accumulator: rank q's accumulated gradient
+ * over this rank's slice, shard_numel elements in reduce_dtype (F32, BF16 or F16; an
+ * F64 reduce dtype returns HBT_ERR_UNSUPPORTED: accumulate with hbt_grad_accumulate and
+ * reduce the rows instead).  rank_grads[q] are the last micro-batch's padded full
+ * gradients, read at rank * shard_numel as in hbt_grad_local_share.  The outputs are
+ * bitwise those of hbt_grad_accumulate (acc = R(acc + R(grad))) over the rows followed
+ * by hbt_grad_local_share_sqnorm over them at rank offset 0, which read and write every
+ * row once more.  partials and tile_scratch are both given or both NULL.
+ * ---------------------------------------------------------------------------- */
+int32_t hbt_grad_local_share_accumulated(const void* const* rank_grads, const void* const* accumulators,
+                                         int32_t group_size, int32_t rank, int64_t shard_numel, int64_t valid_numel,
+                                         int32_t in_dtype, int32_t reduce_dtype, float divisor, int32_t out_dtype,
+                                         void* out, double* partials, double* tile_scratch, void* stream);
+
+/* ------------------------------------------------------------------------------
  * FSDP no_sync gradient accumulation over up to HBT_MAX_TENSORS_PER_LAUNCH
  * (accumulator, gradient) pairs.
  *

@@ -14,6 +14,11 @@
   check, ``optim/grad_scaler.py:181-200``): bitwise the two calls it replaces,
   ``hbt_scale_inplace`` then ``hbt_grad_sqnorm_partials``, in fp32, bf16 and fp16, over
   tails, multi-chunk tensors, misaligned views and IEEE specials, partials included.
+* ``hbt_grad_local_share_accumulated`` (the reduction that ends a ``no_sync``
+  accumulation, ``parallel/fsdp.py:747-769``): bitwise ``hbt_grad_accumulate`` over the
+  rows followed by ``hbt_grad_local_share_sqnorm`` at rank offset 0, outputs and norm
+  partials, for G in {1, 2, 3, 8}, every input / reduce / master dtype, padding, and a
+  misaligned row (scalar path); an fp64 reduce dtype is refused.
 * ``hbt_grad_accumulate`` (the ``no_sync`` accumulation of ``parallel/fsdp.py:738-749``):
   bitwise against torch's CPU ``add_`` (or the cast alone, for the first micro-batch)
   in an fp32, bf16 or fp16 accumulator, fp32, bf16 and fp16 gradients, tails of every
@@ -228,6 +233,63 @@ def test_scale_inplace_sqnorm_is_the_two_calls(device, dtype, specials):
     assert np.array_equal(_bits(base), _bits(twin))  # every element, the untouched first one included
     assert np.array_equal(expect.cpu().numpy().view(np.int64), got.cpu().numpy().view(np.int64))
     assert bool(torch.isfinite(got).all()) != specials
+
+
+@pytest.mark.parametrize("group", [1, 2, 3, 8])
+@pytest.mark.parametrize("in_dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("reduce", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("master", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("misaligned", [False, True])
+def test_local_share_accumulated_is_accumulate_then_share(device, group, in_dtype, reduce, master, misaligned):
+    lib = _native.library()
+    gen = torch.Generator(device=device).manual_seed(group * 7 + int(misaligned))
+    shard = 3 * 65536 + 300 if not misaligned else 70_001
+    valid = shard - 77
+    rank = group - 1
+    grads = [(torch.randn(group * shard, device=device, generator=gen) * 0.3).to(in_dtype) for _ in range(group)]
+    stride = -(-shard // 64) * 64 + (1 if misaligned else 0)
+    base = (torch.randn(group * stride, device=device, generator=gen) * 0.7).to(reduce)
+    rows_a = base.clone().view(group, stride)[:, :shard]
+    rows_b = base.clone().view(group, stride)[:, :shard]
+    code_in, code_red, code_out = (_native.dtype_code(d) for d in (in_dtype, reduce, master))
+    stream = ctypes.c_void_p(_native.stream_of(device))
+    divisor = float(group)
+    chunk = 32768 if master == torch.float32 else 65536
+    count = -(-valid // chunk) + -(-(shard - valid) // chunk)
+    tiles = -(-shard // 256)
+
+    def buffers():
+        return (torch.empty(shard, dtype=master, device=device), torch.empty(max(1, count), dtype=torch.float64,
+                device=device), torch.empty(tiles, dtype=torch.float64, device=device))
+
+    # the two calls: the last micro-batch added into the rows, then the rows reduced
+    offset = rank * shard * grads[0].element_size()
+    _native.check(lib.hbt_grad_accumulate(_native.pointer_array([rows_a[q].data_ptr() for q in range(group)]),
+                                          _native.pointer_array([g.data_ptr() + offset for g in grads]),
+                                          _native.int64_array([shard] * group), group, code_red, code_in, 0, stream),
+                  "test.accumulate")
+    out_a, part_a, scratch_a = buffers()
+    _native.check(lib.hbt_grad_local_share_sqnorm(_native.pointer_array([rows_a[q].data_ptr() for q in range(group)]),
+                                                  group, 0, shard, valid, code_red, code_red, divisor, code_out,
+                                                  out_a.data_ptr(), part_a.data_ptr(), scratch_a.data_ptr(), stream),
+                  "test.share")
+    # the fused call
+    out_b, part_b, scratch_b = buffers()
+    _native.check(lib.hbt_grad_local_share_accumulated(_native.pointer_array([g.data_ptr() for g in grads]),
+                                                       _native.pointer_array([rows_b[q].data_ptr() for q in range(group)]),
+                                                       group, rank, shard, valid, code_in, code_red, divisor, code_out,
+                                                       out_b.data_ptr(), part_b.data_ptr(), scratch_b.data_ptr(), stream),
+                  "test.share_accumulated")
+    torch.cuda.synchronize(device)
+    assert np.array_equal(_bits(out_a), _bits(out_b))
+    assert np.array_equal(part_a.cpu().numpy().view(np.int64), part_b.cpu().numpy().view(np.int64))
+    assert float(out_b[valid:].abs().sum()) == 0.0
+    if not misaligned and group == 2 and in_dtype == torch.float32:
+        f64 = lib.hbt_grad_local_share_accumulated(_native.pointer_array([g.data_ptr() for g in grads]),
+                                                   _native.pointer_array([rows_b[q].data_ptr() for q in range(group)]),
+                                                   group, rank, shard, valid, code_in, 3, divisor, code_out,
+                                                   out_b.data_ptr(), None, None, stream)
+        assert f64 == -2 and b"F64" in lib.hbt_last_error()  # HBT_ERR_UNSUPPORTED
 
 
 def test_local_share_full_size_rank7_of_llama3_8b_w8(device):
