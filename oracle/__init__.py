@@ -64,6 +64,10 @@ PINNED_BY = {
     "(test_single_process_components.py:364-371); torch fp64 sum",
     "adamw_step": "torch.optim.AdamW on CPU: bitwise with torch's own sqrt injected, within "
     "1e-6 relative otherwise; closed form of step 1",
+    "adamw_scalars": "with adamw_step: the step matches torch.optim.AdamW bitwise only when these host "
+    "scalars are the ones torch forms (test_oracle_adamw.py), and step 1's closed form fixes them",
+    "unpack_full": "round trip: the concatenated pack_shard pieces unpack to the original tensors bitwise "
+    "for G = 1, 2, 3, 4 and 7 (test_host_logic.py)",
     "f32_to_bf16": "torch Tensor.to(torch.bfloat16) bitwise on specials and random values",
     "sgd_step": "torch.optim.SGD(foreach=False) on CPU, bitwise, with and without momentum, "
     "weight decay, dampening and Nesterov; closed form of a plain step",

@@ -279,6 +279,17 @@ def test_oracle_pack_matches_concatenation():
         assert all(np.array_equal(a, b) for a, b in zip(back, tensors))
 
 
+def test_every_oracle_function_says_how_it_is_pinned():
+    """Each restatement in the oracle names the checks that pin it (known answers,
+    library routines, closed forms, brute force); only the bit-view and loader helpers
+    restate nothing."""
+    helpers = {"library", "to_bits", "from_bits"}
+    for name in oracle.__all__:
+        if callable(getattr(oracle, name)) and name not in helpers:
+            assert name in oracle.PINNED_BY, name
+    assert set(oracle.PINNED_BY) <= set(oracle.__all__)
+
+
 def test_norm_contribution_from_runs_matches_the_vector_form():
     from hybrid_training_amd import build_gradient_norm_contributions
     from hybrid_training_amd.flat_param import FlatParameter
