@@ -388,3 +388,31 @@ def test_offloaded_no_sync_and_storage_cycle(device, small_chunks, mixed):
             assert np.array_equal(shards[0][1][r], shards[1][1][r]), (step, r)
         for h in runs[1][0]:
             assert h.flat_param.device.type == "cpu" and not h.has_pending_accumulation
+
+
+def test_parameter_and_gradient_must_live_together(device):
+    """A host-resident parameter steps with a host gradient; torch itself refuses a device
+    gradient on it, a missing gradient leaves it untouched, and a gradient that is not
+    dense is refused before any copy or launch, with the reference's error class."""
+    from hybrid_training_amd.errors import ShardingError
+
+    host = nn.Parameter(torch.zeros(1000).pin_memory())
+    opt = ShardedOptimizer([host], OptimizerConfig(learning_rate=1e-3), norm_group=GroupHandle.trivial(),
+                           device=device)
+    host.grad = torch.ones(1000).pin_memory()
+    opt.step()  # fine
+    assert host.device.type == "cpu" and float(host.detach().abs().sum()) > 0
+    with pytest.raises(RuntimeError):
+        host.grad = torch.ones(1000, device=device)  # torch itself refuses the assignment
+    dev = nn.Parameter(torch.zeros(1000, device=device))
+    opt2 = ShardedOptimizer([dev], OptimizerConfig(learning_rate=1e-3), norm_group=GroupHandle.trivial(), device=device)
+    dev.grad = torch.ones(1000, device=device)
+    opt2.step()
+    before = host.detach().clone()
+    bad = ShardedOptimizer([host], OptimizerConfig(learning_rate=1e-3), norm_group=GroupHandle.trivial(), device=device)
+    host.grad = None
+    bad.step()  # no gradient: nothing to do
+    assert torch.equal(host.detach(), before)
+    with pytest.raises(ShardingError, match="dense"):
+        host.grad = torch.ones(2000).pin_memory()[::2]
+        bad.step()
