@@ -599,13 +599,23 @@ __device__ __forceinline__ int64_t tile_sum_slot(int64_t t, int64_t tiles) {
     const int64_t per = n / kXcds;
     return first + (b < per * kXcds ? (b % kXcds) * per + b / kXcds : b);
 }
+// The value a store to RD and a reload leave: round_to for fp32 and fp16, and for bf16 the
+// same rounding with any NaN stored as the canonical 0x7FC0, as f32_to_bf16 stores it.
+template <int RD>
+__device__ __forceinline__ float stored(float x) {
+    if constexpr (RD == BF16) return bf16_to_f32(f32_to_bf16(x));
+    return round_to<RD>(x);
+}
+
 // Rank q's element in the reduce dtype: the gradient cast to RD and, when kAcc, added to
-// the accumulated one (R(grad + accumulator), both in RD, as the reference's final
-// no_sync step adds them before reducing).
+// the accumulated one as the reference's final no_sync step adds them before reducing,
+// formed exactly as accumulate_kernel forms and stores R(acc + R(grad)), so the fused
+// reduction equals an accumulate launch followed by a reduction of the rows bit for bit,
+// NaNs included.
 template <int ID, int RD, bool kAcc>
 __device__ __forceinline__ float share_input(float g, float a) {
     const float x = share_cast<ID, RD>(g);
-    if constexpr (kAcc) return round_to<RD>(x + a);
+    if constexpr (kAcc) return stored<RD>(a + x);
     return x;
 }
 

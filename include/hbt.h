@@ -328,7 +328,8 @@ int32_t hbt_grad_local_share_sqnorm(const void* const* rank_grads, int32_t group
  * gradients, read at rank * shard_numel as in hbt_grad_local_share.  The outputs are
  * bitwise those of hbt_grad_accumulate (acc = R(acc + R(grad))) over the rows followed
  * by hbt_grad_local_share_sqnorm over them at rank offset 0, which read and write every
- * row once more.  partials and tile_scratch are both given or both NULL.
+ * row once more; NaNs included (a bf16 sum that is NaN is the canonical 0x7FC0, as the
+ * accumulator stores it).  partials and tile_scratch are both given or both NULL.
  * ---------------------------------------------------------------------------- */
 int32_t hbt_grad_local_share_accumulated(const void* const* rank_grads, const void* const* accumulators,
                                          int32_t group_size, int32_t rank, int64_t shard_numel, int64_t valid_numel,

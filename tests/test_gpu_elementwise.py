@@ -249,6 +249,13 @@ def test_local_share_accumulated_is_accumulate_then_share(device, group, in_dtyp
     grads = [(torch.randn(group * shard, device=device, generator=gen) * 0.3).to(in_dtype) for _ in range(group)]
     stride = -(-shard // 64) * 64 + (1 if misaligned else 0)
     base = (torch.randn(group * stride, device=device, generator=gen) * 0.7).to(reduce)
+    # IEEE specials in rank 0's slice and row: inf + -inf (a NaN), -0.0 + -0.0, a sum past the
+    # reduce dtype's range, and an inf that stays one
+    lo = rank * shard
+    big = 6.0e4 if reduce == torch.float16 or in_dtype == torch.float16 else 3.0e38
+    for e, gval, aval in ((5, float("inf"), -float("inf")), (6, -0.0, -0.0), (7, big, big), (8, float("inf"), 1.0)):
+        grads[0][lo + e] = gval
+        base[e] = aval
     rows_a = base.clone().view(group, stride)[:, :shard]
     rows_b = base.clone().view(group, stride)[:, :shard]
     code_in, code_red, code_out = (_native.dtype_code(d) for d in (in_dtype, reduce, master))
@@ -281,9 +288,9 @@ def test_local_share_accumulated_is_accumulate_then_share(device, group, in_dtyp
                                                        out_b.data_ptr(), part_b.data_ptr(), scratch_b.data_ptr(), stream),
                   "test.share_accumulated")
     torch.cuda.synchronize(device)
-    assert np.array_equal(_bits(out_a), _bits(out_b))
+    assert np.array_equal(_bits(out_a), _bits(out_b))  # NaNs included
     assert np.array_equal(part_a.cpu().numpy().view(np.int64), part_b.cpu().numpy().view(np.int64))
-    assert float(out_b[valid:].abs().sum()) == 0.0
+    assert bool(torch.isnan(out_b[5])) and float(out_b[valid:].abs().sum()) == 0.0
     if not misaligned and group == 2 and in_dtype == torch.float32:
         f64 = lib.hbt_grad_local_share_accumulated(_native.pointer_array([g.data_ptr() for g in grads]),
                                                    _native.pointer_array([rows_b[q].data_ptr() for q in range(group)]),
