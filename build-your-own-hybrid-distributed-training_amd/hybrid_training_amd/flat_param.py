@@ -592,8 +592,9 @@ class FlatParamHandle:
             else:
                 # The last micro-batch is added to the rows inside the reduction
                 # (hbt_grad_local_share_accumulated): the rows are read once, not
-                # rewritten and read again.
-                rows, self._grad_accumulator = self._grad_accumulator, None
+                # rewritten and read again.  The kernel only reads them, so they are
+                # dropped once it has been queued: a refused launch keeps them.
+                rows = self._grad_accumulator
         valid = max(0, min(self._shard_numel, self._total_numel - local.start))
         divisor = float(group) if (self._config.average_gradients and group > 1) else 1.0
         out = torch.empty(self._shard_numel, dtype=self._master_dtype, device=self._device)
@@ -616,6 +617,8 @@ class FlatParamHandle:
                     grad_ptrs, _native.pointer_array([rows[q].data_ptr() for q in range(group)]), *args)
                 what = "fsdp.hbt_grad_local_share_accumulated"
         _native.check(status, what)
+        if rows is not None:
+            self._grad_accumulator = None
         # The squared-norm partials of the shard's real and padding segments ride on
         # the gradient, so the next clip_grad_norm does not read it again.
         segments = {}

@@ -820,46 +820,60 @@ class ShardedOptimizer:
             )
         return grad
 
-    def _run_adamw_step(self, grad_mul: torch.Tensor | None, write_back: bool) -> None:
-        lib = _native.library()
-        batches: dict[tuple, list[nn.Parameter]] = {}
+    def _stepped_parameters(self) -> list[tuple[dict, nn.Parameter, torch.Tensor]]:
+        """``(group, parameter, gradient)`` of every parameter this step updates.
+
+        Every parameter, its gradient and its existing state are checked here, before
+        any state is created or any step counter advances, so a refused step leaves
+        the optimizer as it was.
+        """
+        stepped = []
         for group in self._optimizer.param_groups:
-            lr = float(group["lr"])
-            beta1, beta2 = (float(b) for b in group["betas"])
-            eps = float(group["eps"])
-            weight_decay = float(group["weight_decay"])
             for p in group["params"]:
                 grad = self._checked_grad(self._device_param.get(id(p), p), group)
                 if grad is None:
                     continue
-                state = self._optimizer.state[p]
-                if len(state) == 0:
-                    # Same initial state as torch.optim.Adam._init_group.
-                    state["step"] = torch.tensor(0.0, dtype=torch.float32)
-                    state["exp_avg"] = self._zero_state(p)
-                    state["exp_avg_sq"] = self._zero_state(p)
-                _native.require_dense(state["exp_avg"], "optim.ShardedOptimizer.step")
-                _native.require_dense(state["exp_avg_sq"], "optim.ShardedOptimizer.step")
-                step_t = state["step"]
-                step_t += 1
-                step = float(step_t.item())
-                # Host scalars exactly as torch/optim/adam.py:416-547 forms them (double).
-                bias_correction1 = 1 - beta1**step
-                bias_correction2 = 1 - beta2**step
-                step_size = lr / bias_correction1
-                bias_correction2_sqrt = bias_correction2**0.5
-                decay = 1 - lr * weight_decay if weight_decay != 0 else 1.0
-                scalars = (
-                    decay,
-                    1 - beta1,
-                    beta2,
-                    1 - beta2,
-                    bias_correction2_sqrt,
-                    eps,
-                    -step_size,
-                )
-                key = (scalars, p.dtype, grad.dtype, _pending_unscale(grad))
-                batches.setdefault(key, []).append(p)
+                for key in ("exp_avg", "exp_avg_sq", "momentum_buffer"):
+                    value = self._optimizer.state[p].get(key) if p in self._optimizer.state else None
+                    if value is not None:
+                        _native.require_dense(value, "optim.ShardedOptimizer.step")
+                stepped.append((group, p, grad))
+        return stepped
+
+    def _run_adamw_step(self, grad_mul: torch.Tensor | None, write_back: bool) -> None:
+        lib = _native.library()
+        batches: dict[tuple, list[nn.Parameter]] = {}
+        for group, p, grad in self._stepped_parameters():
+            lr = float(group["lr"])
+            beta1, beta2 = (float(b) for b in group["betas"])
+            eps = float(group["eps"])
+            weight_decay = float(group["weight_decay"])
+            state = self._optimizer.state[p]
+            if len(state) == 0:
+                # Same initial state as torch.optim.Adam._init_group.
+                state["step"] = torch.tensor(0.0, dtype=torch.float32)
+                state["exp_avg"] = self._zero_state(p)
+                state["exp_avg_sq"] = self._zero_state(p)
+            step_t = state["step"]
+            step_t += 1
+            step = float(step_t.item())
+            # Host scalars exactly as torch/optim/adam.py:416-547 forms them (double).
+            bias_correction1 = 1 - beta1**step
+            bias_correction2 = 1 - beta2**step
+            step_size = lr / bias_correction1
+            bias_correction2_sqrt = bias_correction2**0.5
+            decay = 1 - lr * weight_decay if weight_decay != 0 else 1.0
+            scalars = (
+                decay,
+                1 - beta1,
+                beta2,
+                1 - beta2,
+                bias_correction2_sqrt,
+                eps,
+                -step_size,
+            )
+            key = (scalars, p.dtype, grad.dtype, _pending_unscale(grad))
+            batches.setdefault(key, []).append(p)
         stream = _native.stream_of(self._device)
         mul_ptr = None if grad_mul is None else grad_mul.data_ptr()
         with torch.cuda.device(self._device):
@@ -960,37 +974,31 @@ class ShardedOptimizer:
         """torch.optim.SGD's step (``torch/optim/sgd.py``) as one fused kernel per batch."""
         lib = _native.library()
         batches: dict[tuple, list[nn.Parameter]] = {}
-        for group in self._optimizer.param_groups:
+        for group, p, grad in self._stepped_parameters():
             lr = float(group["lr"])
             momentum = float(group["momentum"])
             dampening = float(group["dampening"])
             weight_decay = float(group["weight_decay"])
             nesterov = bool(group["nesterov"])
-            for p in group["params"]:
-                grad = self._checked_grad(self._device_param.get(id(p), p), group)
-                if grad is None:
-                    continue
-                flags = 0
-                if weight_decay != 0:
-                    flags |= _native.SGD_WEIGHT_DECAY
-                if momentum != 0:
-                    flags |= _native.SGD_MOMENTUM
-                    if nesterov:
-                        flags |= _native.SGD_NESTEROV
-                    state = self._optimizer.state[p]
-                    if state.get("momentum_buffer") is None:
-                        # torch starts the buffer as a clone of the first gradient.
-                        state["momentum_buffer"] = (_pinned_like(p) if is_host(p)
-                                                    else torch.empty_like(p, memory_format=torch.preserve_format))
-                        flags |= _native.SGD_FIRST_STEP
-                    else:
-                        _native.require_dense(state["momentum_buffer"], "optim.ShardedOptimizer.step")
-                # Scalars exactly as torch forms them: Python doubles, rounded to fp32 (and
-                # each alpha to a 2-byte parameter dtype inside the kernel's entry point).
-                scalars = (weight_decay, momentum, 1 - dampening, -lr)
-                unscale = _pending_unscale(grad)
-                key = (scalars, flags | _write_back_flag(write_back, grad_mul, unscale), p.dtype, grad.dtype, unscale)
-                batches.setdefault(key, []).append(p)
+            flags = 0
+            if weight_decay != 0:
+                flags |= _native.SGD_WEIGHT_DECAY
+            if momentum != 0:
+                flags |= _native.SGD_MOMENTUM
+                if nesterov:
+                    flags |= _native.SGD_NESTEROV
+                state = self._optimizer.state[p]
+                if state.get("momentum_buffer") is None:
+                    # torch starts the buffer as a clone of the first gradient.
+                    state["momentum_buffer"] = (_pinned_like(p) if is_host(p)
+                                                else torch.empty_like(p, memory_format=torch.preserve_format))
+                    flags |= _native.SGD_FIRST_STEP
+            # Scalars exactly as torch forms them: Python doubles, rounded to fp32 (and
+            # each alpha to a 2-byte parameter dtype inside the kernel's entry point).
+            scalars = (weight_decay, momentum, 1 - dampening, -lr)
+            unscale = _pending_unscale(grad)
+            key = (scalars, flags | _write_back_flag(write_back, grad_mul, unscale), p.dtype, grad.dtype, unscale)
+            batches.setdefault(key, []).append(p)
         stream = _native.stream_of(self._device)
         mul_ptr = None if grad_mul is None else grad_mul.data_ptr()
         with torch.cuda.device(self._device):

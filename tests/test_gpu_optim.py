@@ -27,7 +27,7 @@ import pytest
 import torch
 
 import oracle
-from hybrid_training_amd import GroupHandle, OptimizerConfig, ShardedOptimizer, _native
+from hybrid_training_amd import GroupHandle, OptimizerConfig, ShardedOptimizer, ShardingError, _native
 from hybrid_training_amd.optim import PENDING_UNSCALE_ATTR, gradient_norm_pass
 
 pytestmark = pytest.mark.gpu
@@ -363,6 +363,49 @@ def test_loaded_non_contiguous_state_steps_like_dense_state(device):
         o.step()
     for a, b in zip(dense_params, copies):
         assert torch.equal(a.detach().view(torch.int32), b.detach().view(torch.int32))
+
+
+@pytest.mark.parametrize("name", ["adamw", "sgd"])
+@pytest.mark.parametrize("offload", [False, True])
+def test_refused_step_changes_no_state(device, name, offload):
+    """A step refused for one parameter (a non-dense gradient, listed after a good one)
+    creates no state and advances no step counter for any parameter: once the gradient
+    is made dense, the step is bitwise a fresh optimizer's first step."""
+    torch.manual_seed(5)
+    shapes = [(300,), (17, 5)]
+    init = [torch.randn(s) * 0.1 for s in shapes]
+    grads = [torch.randn(s) * 1e-2 for s in shapes]
+    config = OptimizerConfig(name=name, learning_rate=1e-2, weight_decay=0.01, momentum=0.9,
+                             cpu_offload_state=offload)
+
+    def make():
+        params = [torch.nn.Parameter(t.to(device)) for t in init]
+        return params, ShardedOptimizer(params, config, norm_group=GroupHandle.trivial(), device=device)
+
+    params, opt = make()
+    params[0].grad = grads[0].to(device)
+    params[1].grad = grads[1].t().contiguous().to(device).t()  # the right shape, not dense
+    with pytest.raises(ShardingError, match="dense"):
+        opt.step()  # (the norm pass refuses the gradient before the update is reached)
+    assert len(opt.inner.state) == 0
+    assert torch.equal(params[0].detach().cpu(), init[0]) and torch.equal(params[1].detach().cpu(), init[1])
+    params[1].grad = grads[1].to(device)
+    opt.clip_grad_norm(1.0)
+    opt.step()
+
+    fresh, fresh_opt = make()
+    for q, g in zip(fresh, grads):
+        q.grad = g.to(device)
+    fresh_opt.clip_grad_norm(1.0)
+    fresh_opt.step()
+    for a, b in zip(params, fresh):
+        assert torch.equal(a.detach().view(torch.int32), b.detach().view(torch.int32))
+        assert torch.equal(a.grad.view(torch.int32), b.grad.view(torch.int32))
+    # (with state offload the state is keyed by the parameters' host copies)
+    for a, b in zip(opt.inner.param_groups[0]["params"], fresh_opt.inner.param_groups[0]["params"]):
+        assert fresh_opt.inner.state[b]
+        for key, value in fresh_opt.inner.state[b].items():
+            assert torch.equal(opt.inner.state[a][key].cpu(), value.cpu()), key
 
 
 def test_pending_unscale_is_read_through(device):
