@@ -20,7 +20,10 @@ is native:
   the overflow decision from the optimizer's norm pass when it covered the same
   gradients.  An optimizer with in-place semantics (``defer_clip=False``) writes the
   unscaled, clipped gradients back during its step, or, when the step is skipped,
-  here.
+  here.  A factor still pending when ``unscale_`` is called again is applied in place
+  first (two calls multiply twice, as in the reference), and ``step`` applies pending
+  factors in place before handing the gradients to any optimizer other than
+  ``ShardedOptimizer``, which would not read them.
 
 The overflow decision is taken over this device's gradients only; the one-element
 MAX all-reduce that agrees on it across ranks (``grad_scaler.py:191-199``) is not
@@ -42,7 +45,7 @@ from .config import GradScalerConfig
 from .errors import UnsupportedFeatureError, format_error
 from .groups import GroupHandle
 from .host_staging import is_host
-from .optim import PENDING_UNSCALE_ATTR, gradient_norm_pass, unscale_with_partials
+from .optim import PENDING_UNSCALE_ATTR, ShardedOptimizer, gradient_norm_pass, scale_gradients, unscale_with_partials
 
 __all__ = ["GradScaler", "GradScalerState"]
 
@@ -106,6 +109,22 @@ def _nonfinite_flag(params: Sequence[nn.Parameter], device: torch.device) -> tor
     return gradient_norm_pass(segments, resident, max_norm=0.0, tag=True).nonfinite
 
 
+def _apply_pending_unscale(grads: Sequence[torch.Tensor], device: torch.device) -> None:
+    """Multiply each gradient that carries a deferred unscale factor by it in place,
+    rounded to the gradient's dtype as ``grad.mul_`` rounds (``hbt_scale_inplace``),
+    and drop the factor: the gradient is then what the in-place unscale leaves."""
+    groups: dict[tuple[torch.device, torch.dtype, float], list[torch.Tensor]] = {}
+    for g in grads:
+        if g is None or not hasattr(g, PENDING_UNSCALE_ATTR):
+            continue
+        resident = device if is_host(g) else g.device
+        groups.setdefault((resident, g.dtype, float(getattr(g, PENDING_UNSCALE_ATTR))), []).append(g)
+    for (resident, dtype, factor), batch in groups.items():
+        scale_gradients(batch, dtype, factor, None, resident, "grad_scaler.hbt_scale_inplace")
+        for g in batch:
+            delattr(g, PENDING_UNSCALE_ATTR)
+
+
 class GradScaler:
     """Loss scaler with a native unscale and overflow check (``grad_scaler.py:95-298``)."""
 
@@ -156,6 +175,9 @@ class GradScaler:
             return self._detect_non_finite(params)
         inverse = 1.0 / self._state.scale
         if self._defer:
+            # A factor still pending from an earlier unscale_ (no step since) is applied
+            # first, so two calls multiply twice, as two in-place multiplies do.
+            _apply_pending_unscale([p.grad for p in params], self._device)
             for p in params:
                 setattr(p.grad, PENDING_UNSCALE_ATTR, inverse)
             self._unscaled = True
@@ -208,6 +230,11 @@ class GradScaler:
             found = self._detect_non_finite([p for p in params if p.grad is not None], optimizer)
         else:
             found = bool(self.unscale_(params))
+        if not isinstance(optimizer, ShardedOptimizer):
+            # Only ShardedOptimizer applies a deferred factor while it reads the gradient;
+            # any other optimizer (the reference accepts a plain torch.optim.Optimizer)
+            # gets gradients that are already unscaled.
+            _apply_pending_unscale([p.grad for p in params], self._device)
         self._state.total_steps += 1
         self._skipped_on_last_step = found
         if found:

@@ -1087,11 +1087,13 @@ class ShardedOptimizer:
         self._pending_signature = None
         self._last_check = None
         for param in self._parameters:
+            # a deferred unscale factor belongs to the contents being discarded, also
+            # when the released tensor object is attached again later
+            if param.grad is not None and hasattr(param.grad, PENDING_UNSCALE_ATTR):
+                delattr(param.grad, PENDING_UNSCALE_ATTR)
             if set_to_none:
                 param.grad = None
             elif param.grad is not None:
-                if hasattr(param.grad, PENDING_UNSCALE_ATTR):
-                    delattr(param.grad, PENDING_UNSCALE_ATTR)
                 param.grad.detach().zero_()
 
     # -- introspection -------------------------------------------------------------------

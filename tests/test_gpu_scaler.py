@@ -273,3 +273,78 @@ def test_eager_unscale_partials_feed_the_clip_norm(device, monkeypatch, dtype):
     again = ShardedOptimizer(params, OptimizerConfig(), norm_group=GroupHandle.trivial(), device=device)
     assert float(again.clip_grad_norm(1.0)) == float(ref)
     assert launched == [sizes[1]]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_unscale_twice_before_a_step_multiplies_twice(device, dtype):
+    """Two ``unscale_`` calls with no step between them multiply twice, as the
+    reference's two ``grad.mul_(inverse)`` do (``grad_scaler.py:181-186``).  The eager
+    result is torch's own pair of in-place multiplies, bitwise; with ``defer_unscale``
+    the factor still pending from the first call is applied before the second is
+    deferred, so after the clipped step ``.grad``, the parameters and the norm are
+    bitwise the eager sequence's."""
+    n = 200_003
+    gen = torch.Generator(device=device).manual_seed(41)
+    p0 = torch.randn(n, device=device, generator=gen) * 0.02
+    g = (torch.randn(n, device=device, generator=gen) * 1e-3 * 1000.0).to(dtype)
+    inverse = 1.0 / 1000.0
+    twice = g.clone().mul_(inverse).mul_(inverse)
+    results = []
+    for defer in (False, True):
+        param = torch.nn.Parameter(p0.clone())
+        param.grad_dtype = None
+        opt = ShardedOptimizer([param], OptimizerConfig(learning_rate=3e-4, weight_decay=0.1),
+                               norm_group=GroupHandle.trivial(), device=device)
+        scaler = GradScaler(GradScalerConfig(enabled=True, init_scale=1000.0), GroupHandle.trivial(), device,
+                            defer_unscale=defer)
+        param.grad = g.clone()
+        assert not scaler.unscale_([param])
+        assert not scaler.unscale_([param])
+        if not defer:
+            assert torch.equal(param.grad.view(torch.int16 if dtype == torch.bfloat16 else torch.int32),
+                               twice.view(torch.int16 if dtype == torch.bfloat16 else torch.int32))
+        norm = opt.clip_grad_norm(1e-3)
+        assert scaler.step(opt, [param], already_unscaled=True)
+        results.append((param.detach().clone(), param.grad.detach().clone(), float(norm)))
+    (p_e, g_e, n_e), (p_d, g_d, n_d) = results
+    assert n_e == n_d
+    assert torch.equal(p_e.view(torch.int32), p_d.view(torch.int32))
+    bits = torch.int16 if dtype == torch.bfloat16 else torch.int32
+    assert torch.equal(g_e.view(bits), g_d.view(bits))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("finite", [True, False])
+def test_deferred_unscale_with_a_plain_torch_optimizer(device, dtype, finite):
+    """The reference's ``GradScaler.step`` takes any optimizer with a ``step()``, a plain
+    ``torch.optim.Optimizer`` included (``grad_scaler.py:202-241``).  Only
+    ``ShardedOptimizer`` applies a deferred unscale while it reads the gradient, so for
+    any other optimizer ``step`` applies it in place first, stepped or skipped: the plain
+    optimizer sees, and ``.grad`` keeps, exactly the eager unscale's gradient, which is
+    torch's ``grad.mul_(1 / scale)`` followed by torch's own SGD step."""
+    n = 100_003
+    gen = torch.Generator(device=device).manual_seed(43)
+    p0 = (torch.randn(n, device=device, generator=gen) * 0.02).to(dtype)
+    g = (torch.randn(n, device=device, generator=gen) * 1e-3 * SCALE).to(dtype)
+    if not finite:
+        g[77] = float("inf")
+    results = []
+    for defer in (False, True, None):
+        param = torch.nn.Parameter(p0.clone())
+        plain = torch.optim.SGD([param], lr=0.1, momentum=0.9)
+        param.grad = g.clone()
+        if defer is None:  # the reference's sequence in torch ops
+            param.grad.mul_(1.0 / SCALE)
+            stepped = bool(torch.isfinite(param.grad).all())
+            if stepped:
+                plain.step()
+        else:
+            scaler = GradScaler(GradScalerConfig(enabled=True, init_scale=SCALE), GroupHandle.trivial(), device,
+                                defer_unscale=defer)
+            stepped = scaler.step(plain, [param])
+        assert stepped == finite
+        results.append((param.detach().clone(), param.grad.detach().clone()))
+    bits = torch.int16 if dtype == torch.bfloat16 else torch.int32
+    for p, gr in results[:2]:
+        assert torch.equal(p.view(bits), results[2][0].view(bits))
+        assert torch.equal(gr.view(bits), results[2][1].view(bits))
