@@ -45,6 +45,7 @@ from hybrid_training_amd import (
 pytestmark = pytest.mark.gpu
 
 OPTIMIZER_STEP_TOLERANCE = 1e-5
+FLOAT32_REDUCTION_TOLERANCE = 1e-6
 #: The scale of the reference's published weight errors (3.0e-08 / 4.5e-08).
 PUBLISHED_SCALE_BOUND = 1e-7
 PUBLISHED = {2: 3.0e-08, 4: 4.5e-08}
@@ -140,3 +141,56 @@ def test_fsdp_mlp_matches_oracle_and_single_process(device, world, offload):
             for v in s.values():
                 if torch.is_tensor(v) and v.numel() > 1:
                     assert (v.device.type == "cpu") == offload and v.is_pinned() == offload
+
+
+@pytest.mark.parametrize("micro_steps", [2, 3])
+@pytest.mark.parametrize("world", [2, 4])
+def test_fsdp_mlp_no_sync_matches_a_summed_loss(device, world, micro_steps):
+    """``no_sync`` on the MLP (``tests/distributed/test_fsdp.py:522-533``, worker ``:224-270``):
+    each rank's loss over ``micro_steps`` micro-batches of 16 rows, each divided by
+    ``micro_steps``; all but the last micro-batch's gradients accumulate without a
+    reduction.  The accumulated shard equals the shard of the summed loss's gradient
+    (reduced once) within the reference's ``FLOAT32_REDUCTION_TOLERANCE`` (1e-6), and N
+    micro-batches cost one reduction."""
+    model = _mlp()
+    named = list(model.named_parameters())
+    gen = torch.Generator().manual_seed(13)
+    x = torch.randn(micro_steps * world * MICRO, 23, generator=gen)
+    y = torch.randn(micro_steps * world * MICRO, 1, generator=gen)
+    dev_named = [(n, nn.Parameter(p.detach().to(device))) for n, p in named]
+
+    def make_handles():
+        return [FlatParamHandle(dev_named, None, GroupHandle.local_view("shard", world, r), FSDPConfig(),
+                                MixedPrecisionConfig(), device, keep_originals=True) for r in range(world)]
+
+    handles = make_handles()
+    padded = handles[0].padded_numel
+
+    def rank_gradient(r, steps):
+        model.zero_grad(set_to_none=True)
+        total = None
+        for m in steps:
+            rows = slice((m * world + r) * MICRO, (m * world + r + 1) * MICRO)
+            piece = nn.functional.mse_loss(model(x[rows]), y[rows]) / micro_steps
+            total = piece if total is None else total + piece
+        total.backward()
+        flat = torch.zeros(padded)
+        flat[:1857] = torch.cat([p.grad.reshape(-1) for _, p in named])
+        return flat.to(device)
+
+    for m in range(micro_steps):
+        grads = [rank_gradient(r, [m]) for r in range(world)]
+        last = m == micro_steps - 1
+        for r, h in enumerate(handles):
+            h.set_accumulate_without_reduction(not last)
+            out = h.reduce_scatter_gradient(grads[r], peer_grads=grads)
+            if last:
+                h.flat_param.grad = out
+            else:
+                assert out is None
+    totals = [rank_gradient(r, range(micro_steps)) for r in range(world)]
+    for r, (h, ref) in enumerate(zip(handles, make_handles())):
+        expected = ref.reduce_scatter_gradient(totals[r], peer_grads=totals)
+        error = float((h.flat_param.grad - expected).abs().max())
+        assert error < FLOAT32_REDUCTION_TOLERANCE, (r, error)
+        assert h.reduction_count == 1

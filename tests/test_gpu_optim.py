@@ -408,6 +408,38 @@ def test_refused_step_changes_no_state(device, name, offload):
             assert torch.equal(opt.inner.state[a][key].cpu(), value.cpu()), key
 
 
+def test_norm_contributions_as_the_reference_tests_them(device):
+    """``tests/unit/test_single_process_components.py:364-406`` on the device: the
+    elementwise weights (2, 2, 1, 0) over 4 ranks on a ones gradient give 1.25; a
+    parameter without a gradient contributes exactly 0; at world size 1 the norm of an
+    MLP's gradients equals ``torch.nn.utils.clip_grad_norm_``'s (the reference's 1e-5
+    bound: torch sums in fp32, this in fp64); a gradient of norm 6 clipped to 1 comes out
+    at norm 1 once the clip lands in ``.grad`` (``materialize_pending``, or the step)."""
+    from hybrid_training_amd import build_gradient_norm_contributions
+
+    p = torch.nn.Parameter(torch.ones(4, device=device))
+    p.grad = torch.ones(4, device=device)
+    p.gradient_norm_scale_vector = torch.tensor([2.0, 2.0, 1.0, 0.0])
+    assert build_gradient_norm_contributions([p], world_size=4)[0].squared_norm().item() == 1.25
+    q = torch.nn.Parameter(torch.ones(4, device=device))
+    assert build_gradient_norm_contributions([q], world_size=1)[0].squared_norm().item() == 0.0
+
+    torch.manual_seed(0)
+    model = torch.nn.Sequential(torch.nn.Linear(4, 8), torch.nn.ReLU(), torch.nn.Linear(8, 2)).to(device)
+    model(torch.randn(3, 4, device=device)).sum().backward()
+    expected = torch.nn.utils.clip_grad_norm_(model.parameters(), max_norm=float("inf"))
+    opt = ShardedOptimizer(list(model.parameters()), OptimizerConfig(), norm_group=GroupHandle.trivial(),
+                           device=device)
+    assert abs(opt.clip_grad_norm(0.0).item() - expected.item()) <= 1e-5
+
+    r = torch.nn.Parameter(torch.ones(4, device=device))
+    r.grad = torch.full((4,), 3.0, device=device)
+    opt = ShardedOptimizer([r], OptimizerConfig(), norm_group=GroupHandle.trivial(), device=device)
+    assert opt.clip_grad_norm(1.0).item() == pytest.approx(6.0)
+    opt.materialize_pending()
+    assert r.grad.norm().item() == pytest.approx(1.0, abs=1e-5)
+
+
 def test_pending_unscale_is_read_through(device):
     n = 5000
     g = torch.randn(n, device=device) * 65536

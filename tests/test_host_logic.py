@@ -326,3 +326,52 @@ def test_copy_plan_table_and_alignment_class():
     assert not _native.plan_is_aligned([(4100, 8192, 4)], bf16, f32)
     assert not _native.plan_is_aligned([(4104, 8192, 4)], f32, bf16)  # 16-byte source units
     assert _native.plan_is_aligned([(0, 8192, 4)], bf16, bf16)         # zero fill
+
+
+def _mlp_23_32_32_1():
+    torch.manual_seed(3)
+    model = torch.nn.Sequential(torch.nn.Linear(23, 32), torch.nn.ReLU(), torch.nn.Linear(32, 32), torch.nn.ReLU(),
+                                torch.nn.Linear(32, 1))
+    return model, list(model.named_parameters())
+
+
+def test_flat_param_handle_refuses_the_reference_failure_modes():
+    """The reference's FSDP failure modes at the unit (``tests/distributed/test_fsdp.py:550-565``,
+    ``parallel/fsdp.py:333-420``), refused before anything is packed: a unit mixing frozen
+    and trainable parameters, a unit whose all-gather exceeds ``limit_all_gather_bytes``
+    (1024 bytes against the MLP's 7,432 at W=2) and a unit with no parameters."""
+    from hybrid_training_amd import (FlatParamHandle, FSDPConfig, GroupHandle, MixedPrecisionConfig, ShardingError,
+                                     UnsupportedFeatureError)
+
+    cpu = torch.device("cpu")
+    group = GroupHandle.local_view("shard", 2, 0)
+    model, named = _mlp_23_32_32_1()
+    model[4].weight.requires_grad_(False)
+    with pytest.raises(UnsupportedFeatureError, match="requires_grad"):
+        FlatParamHandle(named, None, group, FSDPConfig(), MixedPrecisionConfig(), cpu)
+    _, named = _mlp_23_32_32_1()
+    with pytest.raises(ShardingError, match="limit_all_gather_bytes"):
+        FlatParamHandle(named, None, group, FSDPConfig(limit_all_gather_bytes=1024), MixedPrecisionConfig(), cpu)
+    with pytest.raises(ShardingError, match="at least one parameter"):
+        FlatParamHandle([], None, group, FSDPConfig(), MixedPrecisionConfig(), cpu)
+    # nothing was detached from the module on the way
+    assert all(isinstance(p, torch.nn.Parameter) for _, p in named)
+
+
+def test_norm_weights_of_plain_parameters_and_refusals():
+    """``tests/unit/test_single_process_components.py:347-362``, ``:408-416``: a replicated
+    parameter weighs 1/W (0.25 at W=4), a parameter split 2 ways over 4 ranks weighs 2/4,
+    a world size of 0 and an optimizer over no parameters are refused."""
+    from hybrid_training_amd import OptimizerConfig, ShardingError, build_gradient_norm_contributions
+    from hybrid_training_amd.optim import build_inner_optimizer
+
+    replicated = torch.nn.Parameter(torch.ones(4))
+    assert build_gradient_norm_contributions([replicated], world_size=4)[0].scale == pytest.approx(0.25)
+    split = torch.nn.Parameter(torch.ones(4))
+    split.is_tensor_parallel_replicated = False
+    split.tensor_parallel_group_size = 2
+    assert build_gradient_norm_contributions([split], world_size=4)[0].scale == pytest.approx(0.5)
+    with pytest.raises(ShardingError, match="world_size must be positive"):
+        build_gradient_norm_contributions([torch.nn.Parameter(torch.ones(1))], world_size=0)
+    with pytest.raises(ShardingError, match="no trainable parameters"):
+        build_inner_optimizer([], OptimizerConfig())
