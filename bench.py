@@ -18,7 +18,10 @@ algorithmic bytes per launch (28 * numel) over its mean duration, taken from HIP
 events recorded on the launch stream around every timed launch.  ``traffic`` is
 read from the committed rocprofv3 counter summary when present.  ``cpu_baseline``
 times the reference's own CPU op sequence (torch CPU ops, torch.optim.AdamW) on a
-bounded sample of the same workload.
+bounded sample of the same workload.  The other workloads (``--workload``) carry a
+``cpu_baseline`` of the reference's op sequence for that workload too, on a bounded
+sample stated in the line; the loss scaler's clean steps carry none, because torch's
+CPU AdamW refuses bf16 gradients on fp32 parameters.
 """
 
 from __future__ import annotations
@@ -102,14 +105,15 @@ def calibrate_copy() -> int:
     return 0
 
 
-def _time_cpu_step(numel: int, steps: int, threads: int) -> float:
-    """Mean seconds of the reference's CPU step on ``numel`` elements with ``threads`` threads."""
+def _time_cpu_step(numel: int, steps: int, threads: int, momentum: float | None = None) -> float:
+    """Mean seconds of the reference's CPU step on ``numel`` elements with ``threads`` threads
+    (AdamW, or SGD with ``momentum``)."""
     import torch
 
     from oracle.cpu_reference_path import ReferenceCpuStep
 
     torch.set_num_threads(threads)
-    ref = ReferenceCpuStep(numel, lr=LR, betas=BETAS, eps=EPS, weight_decay=WD)
+    ref = ReferenceCpuStep(numel, lr=LR, betas=BETAS, eps=EPS, weight_decay=WD, momentum=momentum)
     ref.prepare()
     ref.step(MAX_NORM)  # warm-up
     elapsed = 0.0
@@ -120,6 +124,15 @@ def _time_cpu_step(numel: int, steps: int, threads: int) -> float:
         elapsed += time.perf_counter() - t0
     del ref
     return elapsed / steps
+
+
+def _cpu_step_line(numel: int, steps: int, momentum: float | None = None) -> dict:
+    """The reference's clipped CPU step (AdamW, or SGD with ``momentum``) on a bounded sample."""
+    seconds = _time_cpu_step(numel, steps, _cpu_threads(), momentum)
+    name = "torch.optim.AdamW" if momentum is None else f"torch.optim.SGD(momentum={momentum})"
+    return _cpu_line(numel, seconds, "params/s",
+                     f"{numel} fp32 elements, {steps} timed steps after 1 warm-up: fp64 norm + in-place clip + "
+                     f"{name}(foreach=False).step")
 
 
 def cpu_baseline(numel: int, steps: int) -> dict:
@@ -174,6 +187,8 @@ def main() -> int:
         )
         return 2
     if args.workload != "adamw":
+        global _WITH_CPU
+        _WITH_CPU = not args.no_cpu_baseline
         return SECONDARY[args.workload](args.steps, args.warmup)
 
     import torch
@@ -334,9 +349,12 @@ def _secondary_traffic(workload: str, labels: list[str], launches: list[int]) ->
         return None
 
 
-def _emit(metric, unit, value, ms, steps, warmup, dtype, workload, bytes_per_run, extra=None, traffic=None):
+def _emit(metric, unit, value, ms, steps, warmup, dtype, workload, bytes_per_run, extra=None, traffic=None,
+          cpu_baseline=None):
     """One JSON line for a secondary workload.  Its roofline is per step: algorithmic bytes
-    of the step over the step time, and HBM traffic per step (``traffic_per`` says so)."""
+    of the step over the step time, and HBM traffic per step (``traffic_per`` says so).
+    ``cpu_baseline``: the reference's op sequence for the workload timed on this host's
+    cores (a bounded sample, in the same unit as ``value``), or None."""
     gbps = bytes_per_run / (ms * 1e-3) / 1e9
     line = {
         "metric": metric, "value": value, "unit": unit, "n_gpus": 1, "steps": steps, "warmup": warmup,
@@ -344,10 +362,39 @@ def _emit(metric, unit, value, ms, steps, warmup, dtype, workload, bytes_per_run
         "data": "synthetic (device-generated)", "config": {"workload": workload},
         "roofline": {"bound": "hbm", "achieved": gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": gbps / HBM_PEAK_GBPS, "traffic": traffic, "traffic_per": "step"},
+        "cpu_baseline": cpu_baseline,
     }
     if extra:
         line["config"].update(extra)
     print(json.dumps(line), flush=True)
+
+
+#: Whether the secondary workloads time their CPU baselines (``--no-cpu-baseline`` clears it).
+_WITH_CPU = True
+
+
+def _cpu_threads() -> int:
+    return min(os.cpu_count() or 1, 16)
+
+
+def _cpu_time(fn, reps: int) -> float:
+    """Mean seconds of ``fn()`` on this host's cores (up to 16), after one warm-up call."""
+    import torch
+
+    torch.set_num_threads(_cpu_threads())
+    fn()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        fn()
+    return (time.perf_counter() - t0) / reps
+
+
+def _cpu_line(units_per_run: float, seconds: float, unit: str, sample: str) -> dict:
+    """A ``cpu_baseline`` object: ``units_per_run`` units of the workload per ``seconds``."""
+    threads = _cpu_threads()
+    return {"value": units_per_run / seconds, "unit": unit, "cores": threads, "kind": "port",
+            "sample": f"{sample}; torch CPU ops, {threads} threads, host has {os.cpu_count()} logical CPUs",
+            "ms_per_step": seconds * 1e3}
 
 
 def bench_buckets(steps: int, warmup: int) -> int:
@@ -369,10 +416,21 @@ def bench_buckets(steps: int, warmup: int) -> int:
         ddp.pack()
 
     ms = _time_events(run, max(steps, 20), max(warmup, 3))
+    cpu = None
+    if _WITH_CPU:
+        from oracle.cpu_reference_path import pack_buckets
+
+        host = {id(p): g.cpu() for (_, p), g in zip(named, grads)}
+        buckets = [(torch.empty(b.layout.total_numel, dtype=torch.float32),
+                    [(b.layout.offsets[i], host[id(q)]) for i, q in enumerate(b.parameters)]) for b in ddp.buckets]
+        cpu = _cpu_line(n, _cpu_time(lambda: pack_buckets(buckets, 8), 5), "params/s",
+                        f"all {n} gradients into the {len(buckets)} buckets, copy + div_(8) per bucket, "
+                        "5 timed runs after 1 warm-up")
+        del host, buckets
     _emit("DDP bucket pack + AVG divide: params/s", "params/s", n / (ms * 1e-3), ms, max(steps, 20),
           max(warmup, 3), "f32", "GPT-2 small gradients, 17 buckets of <= 25 MiB, W=8", 8 * n,
           {"params": n, "buckets": len(ddp.buckets), "bytes_per_param": 8},
-          _secondary_traffic("buckets", ["pack + AVG divide (one launch)"], [1]))
+          _secondary_traffic("buckets", ["pack + AVG divide (one launch)"], [1]), cpu)
     return 0
 
 
@@ -404,6 +462,27 @@ def bench_reshard(steps: int, warmup: int) -> int:
             cache.add(shard_filename(rank), key, shards[rank][ov.start - rank * s_src : ov.end - rank * s_src])
         records[name] = rec
         cursor += numel
+    cpu = None
+    if _WITH_CPU:
+        # The reference's re-slice of destination shard 0 at W=8 on host copies of the
+        # stored intervals it reads (all in source shard 0); its per-element rate is the
+        # baseline for both destination widths.
+        from oracle.cpu_reference_path import read_pieces_into_shard
+
+        s8 = -(-total // 8)
+        host_src = shards[0][:s8].cpu()
+        pieces, cur = [], 0
+        for (name, shape), numel in zip(shapes, numels):
+            ov = intersect_ranges(ShardRange(0, s8), ShardRange(cur, numel))
+            if ov is not None:
+                pieces.append((ov.start, [host_src[ov.start : ov.end]]))
+            cur += numel
+        out = torch.empty(s8, dtype=torch.bfloat16)
+        cpu = _cpu_line(s8, _cpu_time(lambda: read_pieces_into_shard(out, pieces), 3), "elements/s",
+                        f"destination shard 0 of W=8 ({s8} bf16 elements, {len(pieces)} pieces): per piece "
+                        "read_tensor_range into a fresh tensor, then a copy into the flat shard; 3 timed runs "
+                        "after 1 warm-up")
+        del host_src, pieces, out
     for w_dst in (8, 2):
         s_dst = -(-total // w_dst)
         dests = [torch.empty(s_dst, dtype=torch.bfloat16, device=device) for _ in range(w_dst)]
@@ -425,7 +504,8 @@ def bench_reshard(steps: int, warmup: int) -> int:
         _emit("flat-interval reshard: elements/s", "elements/s", total / (ms * 1e-3), ms, max(steps, 5),
               max(warmup, 2), "bf16", f"Llama-3-8B bf16 flat shards, W=4 -> W={w_dst}", 4 * total,
               {"elements": total, "bytes_per_element": 4},
-              _secondary_traffic("reshard", [f"one destination shard of {s_dst:,} elements (W={w_dst})"], [w_dst]))
+              _secondary_traffic("reshard", [f"one destination shard of {s_dst:,} elements (W={w_dst})"], [w_dst]),
+              cpu)
         del dests
         torch.cuda.empty_cache()
     return 0
@@ -482,7 +562,7 @@ def bench_scaler(steps: int, warmup: int) -> int:
     _emit("loss-scaled step with 0.1% inf gradients (skipped): params/s", "params/s", n / (ms * 1e-3), ms,
           max(steps, 5), max(warmup, 2), "bf16", "Llama-3-70B FSDP rank shard at W=8, bf16 grads, 0.1% inf",
           2 * n, {"params": n, "bytes_per_param": 2, "skipped": True},
-          _secondary_traffic("scaler", ["unscale + check + norm"], [1]))
+          _secondary_traffic("scaler", ["unscale + check + norm"], [1]), _scaler_cpu_baseline() if _WITH_CPU else None)
     # The reference's placement: eager unscale_, the clip written back by the update.
     del opt, scaler
     torch.cuda.empty_cache()
@@ -524,6 +604,91 @@ def bench_scaler(steps: int, warmup: int) -> int:
     return 0
 
 
+def _scaler_cpu_baseline() -> dict:
+    """The reference's skipped step on the host: ``unscale_`` (bf16 ``grad.mul_``) and the
+    finiteness scan, on 2^26 bf16 gradient elements with 0.1% inf.  The clean step has no
+    CPU counterpart: torch's CPU AdamW refuses bf16 gradients on fp32 parameters."""
+    import torch
+
+    from oracle.cpu_reference_path import unscale_and_check
+
+    n = 1 << 26
+    gen = torch.Generator().manual_seed(7)
+    grad = (torch.randn(n, generator=gen) * (1e-3 * 65536.0)).to(torch.bfloat16)
+    grad[torch.randint(0, n, (n // 1000,), generator=gen)] = float("inf")
+    seconds = _cpu_time(lambda: unscale_and_check([grad], 65536.0), 3)
+    return _cpu_line(n, seconds, "params/s", f"{n} bf16 gradient elements, 0.1% inf: grad.mul_(2^-16) + "
+                     "torch.isfinite scan, 3 timed runs after 1 warm-up")
+
+
+def _fsdp_cpu_baselines(named, world: int) -> dict:
+    """The reference's FSDP op sequences timed on this host (bounded samples).
+
+    pack: one rank's ``_build_shard`` on the embedding and the first transformer block
+    (the reference builds the whole padded flat buffer for every rank, so one host
+    building all ``world`` shards takes ``world`` times one rank's build); unpack and
+    gather on the same parameters.  share, tail, no_sync, no_sync end: rank 0's share of
+    2^26 elements per rank."""
+    import torch
+
+    from oracle.cpu_reference_path import ReferenceCpuStep, build_shard, full_tensors, gather_full, local_share
+
+    out = {}
+    subset = [p.detach().cpu() for name, p in named if name.startswith(("model.embed_tokens.", "model.layers.0."))]
+    n_sub = sum(p.numel() for p in subset)
+    shard = -(-n_sub // world)
+    seconds = _cpu_time(lambda: build_shard(subset, shard * world, shard, 0, torch.float32), 2)
+    out["pack"] = _cpu_line(n_sub, seconds * world, "params/s",
+                            f"_build_shard of rank 0 over {n_sub} bf16 params (embedding + block 0), 2 timed runs "
+                            f"after 1 warm-up; value = params / ({world} x one rank's build)")
+    flat = torch.zeros(shard * world, dtype=torch.float32)
+    entries, offset = [], 0
+    for p in subset:
+        flat[offset : offset + p.numel()].copy_(p.reshape(-1))
+        entries.append((offset, tuple(p.shape)))
+        offset += p.numel()
+    del subset
+    shards = [s.clone() for s in flat.split(shard)]
+    del flat
+    out["unpack"] = _cpu_line(n_sub, _cpu_time(lambda: full_tensors(shards, entries), 2), "params/s",
+                              f"full_tensors over the same {n_sub} params from {world} fp32 shards: all-gather "
+                              "(cat) + a clone per parameter, 2 timed runs after 1 warm-up")
+    out["gather"] = _cpu_line(n_sub, _cpu_time(lambda: gather_full(shards, torch.bfloat16), 2), "params/s",
+                              f"gather_full over the same {n_sub} params: {world} fp32 shards cast to bf16 and "
+                              "placed in the full buffer, 2 timed runs after 1 warm-up")
+    del shards
+    n = 1 << 26
+    gen = torch.Generator().manual_seed(6)
+    grads = [torch.randn(n, generator=gen).to(torch.bfloat16) for _ in range(world)]
+    rows = [torch.randn(n, generator=gen) for _ in range(world)]
+    out["share"] = _cpu_line(n, _cpu_time(lambda: local_share(grads, None, world, torch.float32, torch.float32), 3),
+                             "elements/s", f"rank 0's share of {n} elements over {world} bf16 gradients: cast, "
+                             "div, rank-order sum, 3 timed runs after 1 warm-up")
+
+    def accumulate():
+        for q in range(world):
+            rows[q].add_(grads[q].to(torch.float32))
+
+    out["no_sync"] = _cpu_line(world * n, _cpu_time(accumulate, 3), "elements/s",
+                               f"{world} x {n} bf16 gradient elements cast and added to fp32 accumulators (add_), "
+                               "3 timed runs after 1 warm-up")
+    tail = ReferenceCpuStep(n, lr=LR, betas=BETAS, eps=EPS, weight_decay=WD)
+
+    def tail_step():
+        tail.param.grad = local_share(grads, None, world, torch.float32, torch.float32)
+        tail.step(MAX_NORM)
+
+    out["tail"] = _cpu_line(n, _cpu_time(tail_step, 3), "elements/s",
+                            f"rank 0's share of {n} elements as above, then the fp64 norm, in-place clip and "
+                            "torch.optim.AdamW(foreach=False).step, 3 timed runs after 1 warm-up")
+    del tail
+    out["no_sync end"] = _cpu_line(n, _cpu_time(lambda: local_share(grads, rows, world, torch.float32,
+                                                                     torch.float32), 3), "elements/s",
+                                   f"rank 0's share of {n} elements: grad + accumulator for each of {world} ranks, "
+                                   "then div and rank-order sum, 3 timed runs after 1 warm-up")
+    return out
+
+
 def bench_fsdp(steps: int, warmup: int) -> int:
     """Llama-3-8B (291 bf16 tensors, 8,030,261,248 params), FSDP at W=8 with fp32 master shards.
 
@@ -551,6 +716,7 @@ def bench_fsdp(steps: int, warmup: int) -> int:
              for name, shape in shapes]
     total = sum(p.numel() for _, p in named)
     mp = MixedPrecisionConfig(enabled=True, param_dtype="bfloat16", reduce_dtype="float32", master_dtype="float32")
+    cpu = _fsdp_cpu_baselines(named, world) if _WITH_CPU else {}
 
     def build():
         return [FlatParamHandle(named, None, GroupHandle.local_view("shard", world, r), FSDPConfig(), mp, device,
@@ -567,7 +733,7 @@ def bench_fsdp(steps: int, warmup: int) -> int:
     _emit("FSDP pack/pad/shard (FlatParamHandle build): params/s", "params/s", total / (ms * 1e-3), ms,
           max(steps, 3), max(warmup, 1), "bf16->f32", f"Llama-3-8B bf16 params -> {world} fp32 master shards",
           6 * total, {"params": total, "world": world, "shard_numel": shard, "bytes_per_param": 6},
-          _secondary_traffic("fsdp", ["pack: one rank's fp32 master shard"], [world]))
+          _secondary_traffic("fsdp", ["pack: one rank's fp32 master shard"], [world]), cpu.get("pack"))
     shards = [h.flat_param for h in handles]
     outputs = {}
 
@@ -579,7 +745,7 @@ def bench_fsdp(steps: int, warmup: int) -> int:
     _emit("FSDP unpack (full_tensors from all shards): params/s", "params/s", total / (ms * 1e-3), ms,
           max(steps, 3), max(warmup, 1), "f32", f"Llama-3-8B, {world} fp32 shards -> 291 fp32 tensors",
           8 * total, {"params": total, "world": world, "bytes_per_param": 8},
-          _secondary_traffic("fsdp", ["unpack: all 291 tensors from 8 shards"], [1]))
+          _secondary_traffic("fsdp", ["unpack: all 291 tensors from 8 shards"], [1]), cpu.get("unpack"))
     outputs.clear()
 
     def gather():
@@ -590,7 +756,8 @@ def bench_fsdp(steps: int, warmup: int) -> int:
           total / (ms * 1e-3), ms, max(steps, 3), max(warmup, 1), "f32->bf16",
           f"Llama-3-8B, {world} fp32 master shards -> one padded bf16 compute buffer",
           6 * total, {"params": total, "world": world, "bytes_per_param": 6},
-          _secondary_traffic("fsdp", ["gather with cast: 8 fp32 shards into the bf16 compute buffer"], [1]))
+          _secondary_traffic("fsdp", ["gather with cast: 8 fp32 shards into the bf16 compute buffer"], [1]),
+          cpu.get("gather"))
     handles[0].reshard()
     del shards
     owner = handles[0]
@@ -607,7 +774,7 @@ def bench_fsdp(steps: int, warmup: int) -> int:
           shard / (ms * 1e-3), ms, max(steps, 5), max(warmup, 2), "bf16->f32",
           f"Llama-3-8B rank 0 of W={world}: {world} padded bf16 gradients -> fp32 shard, with norm partials",
           (2 * world + 4) * shard, {"shard_numel": shard, "world": world, "bytes_per_element": 2 * world + 4},
-          _secondary_traffic("fsdp", ["gradient local share with norm partials"], [1]))
+          _secondary_traffic("fsdp", ["gradient local share with norm partials"], [1]), cpu.get("share"))
 
     from hybrid_training_amd import OptimizerConfig, ShardedOptimizer
 
@@ -625,7 +792,7 @@ def bench_fsdp(steps: int, warmup: int) -> int:
           f"Llama-3-8B rank 0 of W={world}: local share with norm partials, clip from them, fused AdamW",
           (2 * world + 4 + 28) * shard, {"shard_numel": shard, "world": world, "bytes_per_element": 2 * world + 32},
           _secondary_traffic("fsdp", ["gradient local share with norm partials", "fused clip + AdamW in the tail"],
-                             [1, 1]))
+                             [1, 1]), cpu.get("tail"))
 
     # no_sync: the first micro-batch copies rank 0's slice of each rank's gradient into
     # the fp32 accumulator (untimed); each timed micro-batch adds the eight slices to it.
@@ -641,7 +808,7 @@ def bench_fsdp(steps: int, warmup: int) -> int:
           f"Llama-3-8B rank 0 of W={world}: one micro-batch of {world} bf16 gradient slices added to the fp32 "
           "accumulator", 10 * world * shard,
           {"shard_numel": shard, "world": world, "bytes_per_element": 10},
-          _secondary_traffic("fsdp", ["no_sync accumulation"], [1]))
+          _secondary_traffic("fsdp", ["no_sync accumulation"], [1]), cpu.get("no_sync"))
     owner.set_accumulate_without_reduction(False)
     owner.flat_param.grad = owner.reduce_scatter_gradient(grads[0], peer_grads=grads)
 
@@ -670,7 +837,7 @@ def bench_fsdp(steps: int, warmup: int) -> int:
           f"Llama-3-8B rank 0 of W={world}: {world} accumulated fp32 rows plus the last micro-batch's bf16 "
           "gradients -> fp32 shard, with norm partials", (6 * world + 4) * shard,
           {"shard_numel": shard, "world": world, "bytes_per_element": 6 * world + 4},
-          _secondary_traffic("fsdp", ["no_sync end: accumulate and reduce in one pass"], [1]))
+          _secondary_traffic("fsdp", ["no_sync end: accumulate and reduce in one pass"], [1]), cpu.get("no_sync end"))
     del opt, grads, owner, named
     torch.cuda.empty_cache()
     return 0
@@ -748,6 +915,7 @@ def bench_inplace_clip(steps: int, warmup: int) -> int:
         "roofline": {"bound": "hbm", "achieved": adamw_gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": adamw_gbps / HBM_PEAK_GBPS, "traffic": _secondary_traffic("inplace_clip", ["adamw"], [1]),
                      "traffic_per": "launch of the dominant kernel"},
+        "cpu_baseline": _cpu_step_line(1 << 26, 5) if _WITH_CPU else None,
     }
     print(json.dumps(line), flush=True)
     return 0
@@ -930,6 +1098,8 @@ def bench_offload(steps: int, warmup: int) -> int:
                      "frac": link_gbps / 64.0, "traffic": None, "traffic_per": "step, device-to-host direction"},
         "link_measured_gbps": link,
         "frac_of_measured_duplex": link_gbps / link["duplex_per_direction"],
+        # the reference's offload steps the host masters with torch's CPU AdamW
+        "cpu_baseline": _cpu_step_line(1 << 26, 5) if _WITH_CPU else None,
     }
     print(json.dumps(line), flush=True)
     return 0
@@ -1023,11 +1193,10 @@ def bench_param_offload(steps: int, warmup: int) -> int:
         "frac_of_measured_duplex": link_gbps / link["duplex_per_direction"],
         "link_bound_ms": (4 * n / link["device_to_host"] + 16 * n / link["duplex_per_direction"]) / 1e6,
         "frac_of_link_bound": (4 * n / link["device_to_host"] + 16 * n / link["duplex_per_direction"]) / 1e6 / ms,
-        "reference_cpu_step": {"value": cpu_rate, "unit": "params/s", "cores": torch.get_num_threads(),
-                               "kind": "torch CPU AdamW (foreach off) after the in-place clip, the reference's "
-                                       "step on an offloaded shard",
-                               "sample": f"{sample} fp32 elements, mean of {reps} steps",
-                               "ms_per_step_at_shard": n / cpu_rate * 1e3},
+        "cpu_baseline": {"value": cpu_rate, "unit": "params/s", "cores": torch.get_num_threads(), "kind": "port",
+                         "sample": f"{sample} fp32 elements, mean of {reps} steps: torch CPU AdamW (foreach off) "
+                                   "after the in-place clip, the reference's step on an offloaded shard",
+                         "ms_per_step": cpu_s * 1e3, "ms_per_step_at_shard": n / cpu_rate * 1e3},
     }
     print(json.dumps(line), flush=True)
     return 0
@@ -1059,7 +1228,8 @@ def bench_sgd(steps: int, warmup: int) -> int:
     _emit("sharded SGD(momentum 0.9)+clip step: params/s", "params/s", n / (ms * 1e-3), ms, steps, warmup, "f32",
           "Llama-3-8B FSDP rank shard at W=8: global-norm clip + SGD with momentum", 24 * n,
           {"shard_numel": n, "bytes_per_param": 24},
-          _secondary_traffic("sgd", ["SGD with momentum (20 B/param)", "norm pass"], [1, 1]))
+          _secondary_traffic("sgd", ["SGD with momentum (20 B/param)", "norm pass"], [1, 1]),
+          _cpu_step_line(1 << 26, 5, momentum=0.9) if _WITH_CPU else None)
     return 0
 
 
