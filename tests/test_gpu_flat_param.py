@@ -244,6 +244,41 @@ def test_gradient_local_share_in_reduce_dtype_matches_oracle(device, group, in_d
         assert torch.equal(out.to(getattr(torch, reduce)).to(torch.float32), out)  # representable in it
 
 
+@pytest.mark.parametrize("group", [2, 3])
+@pytest.mark.parametrize("in_dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("reduce", ["float32", "bfloat16", "float16", "float64"])
+def test_local_share_with_ieee_specials_matches_oracle(device, group, in_dtype, reduce):
+    """IEEE specials in the gradients (+inf, -inf, NaN, -0.0, values past fp16's range
+    and inf meeting -inf across ranks) through the local share in every reduce dtype:
+    every result bitwise the oracle's, NaNs compared as NaNs (a NaN's bits after bf16
+    arithmetic have no single torch pattern)."""
+    handles = _mp_handles(group, device, reduce)
+    padded, shard = handles[0].padded_numel, handles[0].shard_numel
+    gen = torch.Generator(device=device).manual_seed(group + 31)
+    grads = []
+    for q in range(group):
+        g = torch.randn(padded, device=device, generator=gen) * 3.0
+        for r in range(group):
+            base = r * shard
+            g[base + 1] = float("inf")
+            g[base + 2] = -float("inf") if q == 0 else float("inf")  # inf meets -inf: NaN
+            g[base + 3] = float("nan")
+            g[base + 4] = -0.0
+            g[base + 5] = 70000.0 * (q + 1)  # past fp16's range once cast
+            g[base + 6] = float("nan") if q == group - 1 else 1.0
+        grads.append(g.to(in_dtype))
+    host = [g.float().cpu().numpy() for g in grads]
+    divisor = float(group)
+    for rank, h in enumerate(handles):
+        out = h.reduce_scatter_gradient(grads[rank], peer_grads=grads).cpu().numpy()
+        valid = max(0, min(shard, 1857 - rank * shard))
+        expect = oracle.local_share(host, rank, shard, valid, divisor, reduce)
+        nan = np.isnan(expect)
+        assert np.array_equal(np.isnan(out), nan), rank
+        assert np.array_equal(out[~nan].view(np.int32), expect[~nan].view(np.int32)), rank
+        assert nan[2] and nan[3] and nan[6] and np.isinf(out[1]) and out[4] == 0.0 and np.signbit(out[4])
+
+
 def test_reduce_and_master_dtype_limits(device):
     """A bf16 master shard (mixed precision with ``master_dtype="bfloat16"``) packs and
     reduces into bf16; a float64 master packs (the copy kernel converts into float64) but
