@@ -117,6 +117,45 @@ def test_adamw_bf16_grads_with_unscale(device):
     assert np.array_equal(_bits(v), V.view(np.int32))
 
 
+@pytest.mark.parametrize("grad_dtype", [torch.float32, torch.bfloat16])
+def test_adamw_with_ieee_specials_matches_oracle(device, grad_dtype):
+    """IEEE specials through the fused update: gradients +inf, -inf, NaN, -0.0, the
+    largest finite value and a denormal, parameters -0.0 and NaN, exp_avg_sq +inf, over
+    a vector body and a tail, with and without a clip multiplier: every non-NaN result
+    bitwise the oracle's (torch's single-tensor AdamW restated), NaNs in the same places."""
+    n = 4096 + 37
+    gen = torch.Generator(device=device).manual_seed(71)
+    p = torch.randn(n, device=device, generator=gen) * 0.02
+    g = torch.randn(n, device=device, generator=gen) * 1e-3
+    m = torch.randn(n, device=device, generator=gen) * 1e-4
+    v = torch.rand(n, device=device, generator=gen) * 1e-8
+    big = torch.finfo(torch.float32).max if grad_dtype == torch.float32 else torch.finfo(torch.bfloat16).max
+    for base in (0, 4096):  # the vector body and the tail
+        g[base + 0] = float("inf")
+        g[base + 1] = -float("inf")
+        g[base + 2] = float("nan")
+        g[base + 3] = -0.0
+        g[base + 4] = big
+        g[base + 5] = 1e-40
+        p[base + 6] = -0.0
+        p[base + 7] = float("nan")
+        v[base + 8] = float("inf")
+    g = g.to(grad_dtype)
+    G = g.cpu().view(torch.int16).numpy().view(np.uint16) if grad_dtype == torch.bfloat16 else g.cpu().numpy()
+    for mul in (None, 0.25):
+        pp, mm, vv = p.clone(), m.clone(), v.clone()
+        P, M, V = pp.cpu().numpy(), mm.cpu().numpy(), vv.cpu().numpy()
+        sc = oracle.adamw_scalars(lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1, step=3.0)
+        grad_mul = None if mul is None else torch.tensor([mul], dtype=torch.float32, device=device)
+        _adamw_launch([pp], [g], [mm], [vv], sc, grad_mul=grad_mul)
+        oracle.adamw_step(P, G, M, V, sc, grad_mul=1.0 if mul is None else mul)
+        for got, want, what in ((pp, P, "param"), (mm, M, "exp_avg"), (vv, V, "exp_avg_sq")):
+            got = got.cpu().numpy()
+            nan = np.isnan(want)
+            assert np.array_equal(np.isnan(got), nan), (what, mul)
+            assert np.array_equal(got[~nan].view(np.int32), want[~nan].view(np.int32)), (what, mul)
+
+
 def _norm_of(tensors, weights, device, max_norm=0.0):
     segments = [(t, 0, t.numel(), w) for t, w in zip(tensors, weights)]
     return gradient_norm_pass(segments, device, max_norm=max_norm)
