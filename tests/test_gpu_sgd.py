@@ -108,3 +108,40 @@ def test_sgd_state_dict_round_trip(device):
     for p in params:
         assert torch.equal(fresh.inner.state[p]["momentum_buffer"], opt.inner.state[p]["momentum_buffer"])
     assert fresh.state_bytes() == opt.state_bytes() == 3 * 1000 * 4
+
+
+@pytest.mark.parametrize("nesterov", [False, True])
+def test_sgd_with_ieee_specials_matches_oracle(device, nesterov):
+    """IEEE specials through the fused SGD update over two steps (the buffer's first write,
+    then the momentum update): gradients ±inf, NaN, -0.0, the largest finite value and a
+    denormal, parameters -0.0 and NaN, in the vector body and the tail; every non-NaN
+    parameter and buffer element bitwise the oracle's, NaNs in the same places."""
+    n, lr = 4096 + 29, 0.05
+    gen = torch.Generator(device=device).manual_seed(73)
+    p0 = torch.randn(n, device=device, generator=gen)
+    for base in (0, 4096):
+        p0[base + 6] = -0.0
+        p0[base + 7] = float("nan")
+    param = torch.nn.Parameter(p0.clone())
+    opt = ShardedOptimizer([param], OptimizerConfig(name="sgd", learning_rate=lr, momentum=0.9, weight_decay=0.01),
+                           norm_group=GroupHandle.trivial(), device=device)
+    for group in opt.inner.param_groups:
+        group["nesterov"] = nesterov
+    hp, hb = p0.cpu().numpy().copy(), np.zeros(n, np.float32)
+    for step in range(2):
+        g = torch.randn(n, device=device, generator=gen) * 0.1
+        for base in (0, 4096):
+            g[base + 0] = float("inf")
+            g[base + 1] = -float("inf")
+            g[base + 2] = float("nan")
+            g[base + 3] = -0.0
+            g[base + 4] = torch.finfo(torch.float32).max
+            g[base + 5] = 1e-40
+        param.grad = g
+        opt.step()
+        oracle.sgd_step(hp, g.cpu().numpy(), hb, lr=lr, momentum=0.9, weight_decay=0.01, nesterov=nesterov,
+                        first=step == 0)
+        for got, want in ((param.detach().cpu().numpy(), hp), (opt.inner.state[param]["momentum_buffer"].cpu().numpy(), hb)):
+            nan = np.isnan(want)
+            assert np.array_equal(np.isnan(got), nan), step
+            assert np.array_equal(_i32(got[~nan]), _i32(want[~nan])), step
