@@ -174,3 +174,32 @@ def test_no_sync_accumulates_then_packs_the_sum(device):
         total = (total + micro[2][i].cpu().numpy()).astype(np.float32)
         expect = (total / np.float32(4)).astype(np.float32)
         assert np.array_equal(p.grad.detach().cpu().numpy().view(np.int32), expect.view(np.int32)), name
+
+
+def test_pack_with_ieee_specials(device):
+    """IEEE specials through the bucket pack and its AVG divide (W=3, not a power of two,
+    so a true division): ±inf, NaN, -0.0, the largest finite value and denormals, in an
+    fp32 and a bf16 bucket; every non-NaN element bitwise numpy's ``g / 3`` rounded to
+    the bucket dtype, NaNs in the same places."""
+    shapes = [(4099,), (33, 17)]
+    named = [(f"w{i}", torch.nn.Parameter(torch.empty(s, device=device, dtype=dt)))
+             for i, (s, dt) in enumerate(zip(shapes, (torch.float32, torch.bfloat16)))]
+    gen = torch.Generator(device=device).manual_seed(19)
+    for _, p in named:
+        g = torch.randn(p.shape, device=device, generator=gen).reshape(-1)
+        g[:7] = torch.tensor([float("inf"), -float("inf"), float("nan"), -0.0,
+                              torch.finfo(p.dtype).max, 1e-40, -1e-45], device=device)
+        p.grad = g.to(p.dtype).reshape(p.shape)
+    expect = {}
+    for name, p in named:
+        wide = p.grad.detach().float().cpu().numpy().reshape(-1)
+        expect[name] = torch.from_numpy((wide / np.float32(3)).astype(np.float32)).to(p.dtype)
+    ddp = BucketedGradients(named, GroupHandle.local_view("data_parallel", 3, 0), DDPConfig())
+    ddp.synchronize()
+    for name, p in named:
+        got = p.grad.detach().cpu().reshape(-1)
+        want = expect[name]
+        nan = torch.isnan(want)
+        assert torch.equal(torch.isnan(got), nan), name
+        bits = torch.int16 if p.dtype == torch.bfloat16 else torch.int32
+        assert torch.equal(got[~nan].view(bits), want[~nan].view(bits)), name
