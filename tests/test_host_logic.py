@@ -375,3 +375,31 @@ def test_norm_weights_of_plain_parameters_and_refusals():
         build_gradient_norm_contributions([torch.nn.Parameter(torch.ones(1))], world_size=0)
     with pytest.raises(ShardingError, match="no trainable parameters"):
         build_inner_optimizer([], OptimizerConfig())
+
+
+def test_pending_unscale_factors_are_applied_once_per_group(monkeypatch):
+    """``_apply_pending_unscale`` (a second deferred ``unscale_``, or a step handed to an
+    optimizer that does not read deferred factors): one in-place scaling per (device,
+    dtype, factor) group, each gradient's factor dropped afterwards, gradients without a
+    factor left alone.  The native scaling is recorded instead of run."""
+    from hybrid_training_amd import grad_scaler
+    from hybrid_training_amd.optim import PENDING_UNSCALE_ATTR
+
+    calls = []
+    monkeypatch.setattr(grad_scaler, "scale_gradients",
+                        lambda grads, dtype, factor, mul, device, op: calls.append(
+                            (tuple(id(g) for g in grads), dtype, factor, mul, str(device))))
+    a, b, c = torch.zeros(3), torch.zeros(4), torch.zeros(5, dtype=torch.bfloat16)
+    d, untouched = torch.zeros(2), torch.zeros(6)
+    for g, factor in ((a, 0.5), (b, 0.5), (c, 0.5), (d, 0.25)):
+        setattr(g, PENDING_UNSCALE_ATTR, factor)
+    grad_scaler._apply_pending_unscale([a, None, b, c, d, untouched], torch.device("cuda", 0))
+    assert sorted(calls, key=lambda x: (str(x[1]), x[2])) == sorted([
+        ((id(a), id(b)), torch.float32, 0.5, None, "cuda:0"),
+        ((id(c),), torch.bfloat16, 0.5, None, "cuda:0"),
+        ((id(d),), torch.float32, 0.25, None, "cuda:0"),
+    ], key=lambda x: (str(x[1]), x[2]))
+    assert not any(hasattr(g, PENDING_UNSCALE_ATTR) for g in (a, b, c, d, untouched))
+    calls.clear()
+    grad_scaler._apply_pending_unscale([a, b], torch.device("cuda", 0))  # nothing pending: no call
+    assert calls == []
