@@ -117,6 +117,14 @@ def _apply_pending_unscale(grads: Sequence[torch.Tensor], device: torch.device) 
     for g in grads:
         if g is None or not hasattr(g, PENDING_UNSCALE_ATTR):
             continue
+        # the in-place scaling addresses numel consecutive elements: checked for every
+        # gradient before any is scaled
+        _native.require_dense(g, "grad_scaler.unscale_")
+        if g.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+            raise UnsupportedFeatureError(
+                format_error("grad_scaler.unscale_", "gradients must be float32, bfloat16 or float16",
+                             observed=str(g.dtype))
+            )
         resident = device if is_host(g) else g.device
         groups.setdefault((resident, g.dtype, float(getattr(g, PENDING_UNSCALE_ATTR))), []).append(g)
     for (resident, dtype, factor), batch in groups.items():

@@ -833,7 +833,10 @@ class ShardedOptimizer:
                 grad = self._checked_grad(self._device_param.get(id(p), p), group)
                 if grad is None:
                     continue
-                for key in ("exp_avg", "exp_avg_sq", "momentum_buffer"):
+                # the state the update reads: AdamW's moments, or SGD's buffer with momentum
+                read = (("exp_avg", "exp_avg_sq") if "betas" in group
+                        else ("momentum_buffer",) if float(group.get("momentum", 0.0)) != 0.0 else ())
+                for key in read:
                     value = self._optimizer.state[p].get(key) if p in self._optimizer.state else None
                     if value is not None:
                         _native.require_dense(value, "optim.ShardedOptimizer.step")

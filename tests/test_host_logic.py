@@ -403,3 +403,12 @@ def test_pending_unscale_factors_are_applied_once_per_group(monkeypatch):
     calls.clear()
     grad_scaler._apply_pending_unscale([a, b], torch.device("cuda", 0))  # nothing pending: no call
     assert calls == []
+    # a strided gradient is refused before anything is scaled, the dense one included
+    from hybrid_training_amd import ShardingError
+
+    dense, strided = torch.zeros(4), torch.zeros(8)[::2]
+    for g in (dense, strided):
+        setattr(g, PENDING_UNSCALE_ATTR, 0.5)
+    with pytest.raises(ShardingError, match="dense"):
+        grad_scaler._apply_pending_unscale([dense, strided], torch.device("cuda", 0))
+    assert calls == [] and hasattr(dense, PENDING_UNSCALE_ATTR)
