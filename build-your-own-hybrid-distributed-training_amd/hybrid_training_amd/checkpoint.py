@@ -531,7 +531,8 @@ def load_flat_shard_checkpoint(
         buffer = torch.zeros(flat.numel(), dtype=flat.dtype, device=handle.device)
         found = load_flat_shard(buffer, layout, records, cache,
                                 key_of=lambda item, s=state_name: f"{item.name}::{s}", strict=False)
-        if found:
+        if found or not layout:
+            # a rank whose shard is all padding owns no piece to read: its state is zero
             entry[state_name] = buffer.view(flat.shape)
         elif strict:
             raise IncompleteCheckpointError(

@@ -107,3 +107,29 @@ def test_corrupt_payload_is_refused(device, saved):
     handles, opts = _world(named, 2, device)
     with pytest.raises(CheckpointCorruptionError, match="checksum"):
         load_flat_shard_checkpoint(path, handles[1], optimizer=opts[1])
+
+
+def test_padding_only_ranks_save_and_load_optimizer_state(device, tmp_path):
+    """A one-element model saved by 3 writers and loaded by 4 readers: every rank but the
+    first owns padding only, so it has no piece to write or read.  Its load still
+    succeeds, strict, with zero moments and the saved step; rank 0 gets the saved values."""
+    named = [("w", torch.nn.Parameter(torch.full((1,), 0.5, device=device)))]
+    handles, opts = _world(named, 3, device)
+    for h, opt in zip(handles, opts):
+        h.flat_param.grad = torch.full((h.shard_numel,), 0.25, device=device)
+        opt.step()
+    payloads = [(r, *collect_flat_shard_payload(h, rank=r, optimizer=o)) for r, (h, o) in
+                enumerate(zip(handles, opts))]
+    path = write_checkpoint(tmp_path, 1, payloads, topology={"fsdp": 3})
+    saved_p = handles[0].flat_param.detach()[:1].clone()
+    saved_m = opts[0].inner.state[handles[0].flat_param]["exp_avg"][:1].clone()
+    readers, reader_opts = _world([("w", torch.nn.Parameter(torch.zeros(1, device=device)))], 4, device)
+    for r, (h, o) in enumerate(zip(readers, reader_opts)):
+        load_flat_shard_checkpoint(path, h, optimizer=o)
+        state = o.inner.state[h.flat_param]
+        assert float(state["step"]) == 1.0, r
+        if r == 0:
+            assert torch.equal(h.flat_param.detach()[:1], saved_p) and torch.equal(state["exp_avg"][:1], saved_m)
+        else:
+            assert float(state["exp_avg"].abs().sum()) == 0.0 and float(state["exp_avg_sq"].abs().sum()) == 0.0
+            assert float(h.flat_param.detach().abs().sum()) == 0.0
