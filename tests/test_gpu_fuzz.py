@@ -15,6 +15,8 @@ on disk.
 
 from __future__ import annotations
 
+import sys
+
 import numpy as np
 import pytest
 import torch
@@ -566,3 +568,27 @@ def test_random_checkpoint_save_and_load(device, tmp_path, case):
         assert torch.equal(state["exp_avg"][:valid], m[start:start + valid]), (context, r)
         assert torch.equal(state["exp_avg_sq"][:valid], v[start:start + valid]), (context, r)
         assert float(state["step"]) == float(steps), (context, r)
+
+
+def _tiny_shapes(rng: np.random.Generator) -> list[tuple[int, ...]]:
+    """One to three tensors of 0-5 elements: with up to 9 ranks most shards are padding."""
+    shapes = [(int(rng.integers(0, 6)),) for _ in range(int(rng.integers(1, 4)))]
+    if all(s[0] == 0 for s in shapes):
+        shapes.append((1,))
+    return shapes
+
+
+@pytest.mark.parametrize("case", range(40))
+def test_random_tiny_fsdp_configurations(device, monkeypatch, case):
+    """The FSDP configurations above on models of a few elements, where most ranks own
+    padding only: pack, gather, local share and ``no_sync`` bitwise the oracle's."""
+    monkeypatch.setattr(sys.modules[__name__], "_shapes", _tiny_shapes)
+    test_random_fsdp_configurations(device, 5000 + case)
+
+
+@pytest.mark.parametrize("case", range(20))
+def test_random_tiny_checkpoint_save_and_load(device, tmp_path, monkeypatch, case):
+    """The checkpoint round trips above on models of a few elements: writers and readers
+    whose shards are all padding save nothing and load zero optimizer state."""
+    monkeypatch.setattr(sys.modules[__name__], "_shapes", _tiny_shapes)
+    test_random_checkpoint_save_and_load(device, tmp_path, 5000 + case)
