@@ -519,3 +519,45 @@ def test_unshard_reshard_refill_free_full_lifecycle(device):
     h.refill(full)  # a buffer that holds its storage is left alone
     h.free_full()
     assert h.is_sharded and module.weight.numel() == 0
+
+
+def test_local_share_at_the_rank_limit(device):
+    """``HBT_MAX_LOCAL_RANKS`` (64) ranks on the 1857-parameter MLP (shard 30, padding 63):
+    every 8th rank's local share and a two-micro-batch ``no_sync`` end are bitwise the
+    oracle's.  With 65 ranks the reduction is refused before any launch: no reduction is
+    counted, and a ``no_sync`` accumulation keeps its rows for a retry."""
+    from hybrid_training_amd.errors import NativeKernelError
+
+    group = 64
+    named = _params(MLP_1857_REFERENCE, device)
+    handles = [FlatParamHandle(named, None, GroupHandle.local_view("shard", group, r), FSDPConfig(),
+                               MixedPrecisionConfig(), device, keep_originals=True) for r in range(0, group, 8)]
+    padded, shard = handles[0].padded_numel, handles[0].shard_numel
+    assert shard == 30 and padded - 1857 == 63
+    gen = torch.Generator(device=device).manual_seed(64)
+    grads = [[torch.randn(padded, device=device, generator=gen) * 1e-2 for _ in range(group)] for _ in range(2)]
+    for h, rank in zip(handles, range(0, group, 8)):
+        valid = max(0, min(shard, 1857 - rank * shard))
+        out = h.reduce_scatter_gradient(grads[0][rank], peer_grads=grads[0])
+        expect = oracle.local_share([g.cpu().numpy() for g in grads[0]], rank, shard, valid, float(group))
+        assert np.array_equal(out.cpu().numpy().view(np.int32), expect.view(np.int32)), rank
+        h.set_accumulate_without_reduction(True)
+        assert h.reduce_scatter_gradient(grads[0][rank], peer_grads=grads[0]) is None
+        h.set_accumulate_without_reduction(False)
+        out = h.reduce_scatter_gradient(grads[1][rank], peer_grads=grads[1])
+        totals = [oracle.no_sync_accumulate([grads[m][q].cpu().numpy() for m in range(2)], "float32")
+                  for q in range(group)]
+        expect = oracle.local_share(totals, rank, shard, valid, float(group))
+        assert np.array_equal(out.cpu().numpy().view(np.int32), expect.view(np.int32)), rank
+    over = FlatParamHandle(named, None, GroupHandle.local_view("shard", group + 1, 0), FSDPConfig(),
+                           MixedPrecisionConfig(), device, keep_originals=True)
+    wide = [torch.zeros(over.padded_numel, device=device) for _ in range(group + 1)]
+    with pytest.raises(NativeKernelError):
+        over.reduce_scatter_gradient(wide[0], peer_grads=wide)
+    assert over.reduction_count == 0
+    over.set_accumulate_without_reduction(True)
+    over.reduce_scatter_gradient(wide[0], peer_grads=wide)
+    over.set_accumulate_without_reduction(False)
+    with pytest.raises(NativeKernelError):
+        over.reduce_scatter_gradient(wide[0], peer_grads=wide)
+    assert over.has_pending_accumulation and over.reduction_count == 0
