@@ -56,11 +56,11 @@ def _shapes(rng: np.random.Generator) -> list[tuple[int, ...]]:
     return shapes
 
 
-@pytest.mark.parametrize("case", range(120))
-def test_random_fsdp_configurations(device, case):
+def _fsdp_case(device, case: int, groups: tuple[int, ...] | None = None) -> None:
+    """One random FSDP configuration; ``groups``: the group sizes to draw from (default 1-9)."""
     rng = np.random.default_rng(1000 + case)
     shapes = _shapes(rng)
-    group = int(rng.integers(1, 10))
+    group = int(rng.integers(1, 10)) if groups is None else int(rng.choice(groups))
     param_dtype = [torch.float32, torch.bfloat16][int(rng.integers(0, 2))]
     grad_dtype = [torch.float32, torch.bfloat16, torch.float16][int(rng.integers(0, 3))]
     reduce = [torch.float32, torch.bfloat16, torch.float16, torch.float64][int(rng.integers(0, 4))]
@@ -101,6 +101,21 @@ def test_random_fsdp_configurations(device, case):
                   for q in range(group)]
         expect = oracle.local_share(totals, rank, shard, valid, divisor, _NAMES[reduce])
         assert np.array_equal(out.cpu().numpy().view(np.int32), expect.view(np.int32)), (context, rank)
+
+
+@pytest.mark.parametrize("case", range(120))
+def test_random_fsdp_configurations(device, case):
+    """Seeded FSDP configurations with 1-9 ranks: every rank's shard, the gathered
+    tensors, the local share and a two-micro-batch ``no_sync`` reduction bitwise the
+    oracle's."""
+    _fsdp_case(device, case)
+
+
+@pytest.mark.parametrize("case", range(12))
+def test_random_large_group_fsdp_configurations(device, case):
+    """The same configurations with 16 to 64 ranks (``HBT_MAX_LOCAL_RANKS``), the run-time
+    group-size kernels throughout."""
+    _fsdp_case(device, 7000 + case, (16, 31, 32, 33, 63, 64))
 
 
 @pytest.mark.parametrize("case", range(40))
@@ -583,7 +598,7 @@ def test_random_tiny_fsdp_configurations(device, monkeypatch, case):
     """The FSDP configurations above on models of a few elements, where most ranks own
     padding only: pack, gather, local share and ``no_sync`` bitwise the oracle's."""
     monkeypatch.setattr(sys.modules[__name__], "_shapes", _tiny_shapes)
-    test_random_fsdp_configurations(device, 5000 + case)
+    _fsdp_case(device, 5000 + case)
 
 
 @pytest.mark.parametrize("case", range(20))
