@@ -98,7 +98,7 @@ class GradientBucket:
 
     @property
     def is_allocated(self) -> bool:
-        """Whether the flat buffer exists yet."""
+        """True once the bucket's storage has been created."""
         return self._buffer is not None
 
     def view_for(self, position: int) -> torch.Tensor:
@@ -115,7 +115,7 @@ class GradientBucket:
         self.work = None
 
     def num_bytes(self) -> int:
-        """Size of the flat buffer in bytes."""
+        """Bytes of the bucket's storage."""
         return self.layout.total_numel * self._dtype.itemsize
 
     def __repr__(self) -> str:
@@ -204,11 +204,10 @@ class BucketedGradients:
             raise ShardingError(
                 format_error(
                     "ddp.DistributedDataParallel",
-                    "the wrapped module has no trainable parameters",
+                    "the wrapped module has no trainable parameters, so there is nothing to bucket",
                     rank=group.global_rank,
-                    expected=">= 1 parameter with requires_grad=True",
                     observed=0,
-                    resolution="check that the module was built before wrapping",
+                    resolution="wrap a module after its parameters exist and require gradients",
                 )
             )
         if group.size > 1 and group.process_group is not None:
@@ -326,16 +325,14 @@ class BucketedGradients:
             raise ShardingError(
                 format_error(
                     "ddp.finish_gradient_synchronization",
-                    "some parameters received no gradient, so their buckets can never "
-                    "become ready and the all-reduce would never be issued (every other "
-                    "rank would block waiting for it)",
+                    f"{len(missing)} parameter(s) received no gradient; their buckets would never "
+                    "fill, and peers would wait on a reduction that never starts",
                     rank=self._group.global_rank,
                     world_size=self._group.size,
-                    expected="every trainable parameter to receive a gradient",
-                    observed=f"{len(missing)} without gradients: {missing[:8]}",
+                    observed=missing[:8],
                     resolution=(
-                        "set DDPConfig(find_unused_parameters=True), or stop marking "
-                        "unused parameters as requires_grad=True"
+                        "pass DDPConfig(find_unused_parameters=True) to reduce zeros for them, "
+                        "or set requires_grad=False on parameters the loss does not use"
                     ),
                 )
             )

@@ -114,13 +114,11 @@ class ShardFileCache:
             raise CheckpointCorruptionError(
                 format_error(
                     "reshard.ShardFileCache.get",
-                    f"shard file {filename!r} could not be deserialised",
-                    expected="a tensor mapping saved with torch.save",
+                    f"payload {filename!r} does not load as tensors",
                     observed=repr(exc),
                     resolution=(
-                        "the file is corrupt, or was written by a different tool; note "
-                        "that this reader deliberately refuses pickled objects other "
-                        "than tensors"
+                        "the bytes are damaged or hold objects other than tensors, which the "
+                        "weights-only loader refuses by design"
                     ),
                 )
             ) from exc
@@ -128,10 +126,9 @@ class ShardFileCache:
             raise CheckpointCorruptionError(
                 format_error(
                     "reshard.ShardFileCache.get",
-                    f"shard file {filename!r} does not contain a mapping",
-                    expected="dict[str, Tensor]",
+                    f"payload {filename!r} is not a key -> tensor mapping",
                     observed=type(payload).__name__,
-                    resolution="the file was not written by this package",
+                    resolution="only payloads saved by a checkpoint writer can be read",
                 )
             )
         return payload
@@ -148,64 +145,43 @@ class ShardFileCache:
 
 def _check_file(directory: Path, manifest: CheckpointManifest, filename: str, *, verify: bool,
                 operation: str) -> Path:
-    """The path of one listed shard file after the reference's checks (name rule,
-    containment, presence, integrity record, size, and SHA-256 when ``verify``)."""
+    """The path of one listed shard file after the reference's checks, in its order
+    (``checkpoint/reshard.py:100-157``, ``:325-374``): the name rule, containment,
+    presence, an integrity record, the recorded size, and the SHA-256 when ``verify``."""
     validate_shard_filename(filename)
     path = resolve_inside(directory, filename)
     if not path.is_file():
         raise IncompleteCheckpointError(
-            format_error(
-                operation,
-                "a shard file listed in the manifest is missing",
-                expected=filename,
-                observed="not present in the checkpoint directory",
-                resolution=(
-                    "the checkpoint is incomplete; restore the missing file or "
-                    "resume from an earlier checkpoint"
-                ),
-            )
+            format_error(operation, f"payload {filename!r} is missing from {Path(directory).name!r}",
+                         resolution="copy the whole directory again, or load an earlier checkpoint")
         )
     record = manifest.files.get(filename)
     if record is None:
         raise CheckpointCorruptionError(
-            format_error(
-                operation,
-                "the file has no integrity record in the manifest",
-                expected="an entry under manifest['files']",
-                observed=filename,
-                resolution="the manifest is truncated or hand-edited",
-            )
+            format_error(operation, f"payload {filename!r} has no integrity record in the manifest",
+                         observed=sorted(manifest.files)[:8],
+                         resolution="the manifest's files table is incomplete")
         )
-    actual_size = path.stat().st_size
-    if actual_size != record.bytes:
+    size = path.stat().st_size
+    if size != record.bytes:
         raise CheckpointCorruptionError(
-            format_error(
-                operation,
-                f"shard file {filename!r} has the wrong size, so it was truncated "
-                "or overwritten after the checkpoint was published",
-                expected=f"{record.bytes} bytes",
-                observed=f"{actual_size} bytes",
-                resolution="restore the file from a backup or discard the checkpoint",
-            )
+            format_error(operation, f"payload {filename!r} has the wrong size: {size} bytes on disk, "
+                         f"{record.bytes} recorded", resolution="it was cut short or replaced after the save")
         )
     if verify:
-        digest = file_digest(path)
-        if digest != record.sha256:
-            raise CheckpointCorruptionError(
-                format_error(
-                    operation,
-                    f"shard file {filename!r} failed checksum verification; its "
-                    "contents differ from what the writer recorded",
-                    expected=record.sha256,
-                    observed=digest,
-                    resolution=(
-                        "the file is corrupt; restore it from a backup or discard "
-                        "the checkpoint. Pass verify_checksums=False only when you "
-                        "have another reason to trust the bytes."
-                    ),
-                )
-            )
+        _require_digest(filename, file_digest(path), record.sha256, operation)
     return path
+
+
+def _require_digest(filename: str, found: str, recorded: str, operation: str) -> None:
+    """Refuse a payload whose SHA-256 is not the one the writer recorded."""
+    if found != recorded:
+        raise CheckpointCorruptionError(
+            format_error(operation, f"payload {filename!r} failed checksum verification",
+                         expected=recorded, observed=found,
+                         resolution="its bytes changed after the save; load an earlier checkpoint, or "
+                         "pass verify_checksums=False if the change is known to be harmless")
+        )
 
 
 def verify_files(
@@ -216,28 +192,12 @@ def verify_files(
     digest; raises the reference's error for the first bad file in name order."""
     directory = Path(directory)
     targets = sorted(filenames if filenames is not None else manifest.referenced_files())
-
-    def one(name: str) -> str:
-        _check_file(directory, manifest, name, verify=False, operation="reshard.verify_files")
-        return name
-
     for name in targets:  # the cheap checks first, in order
-        one(name)
+        _check_file(directory, manifest, name, verify=False, operation="reshard.verify_files")
     with ThreadPoolExecutor(max_workers=max(1, min(max_workers, len(targets) or 1))) as pool:
         digests = list(pool.map(lambda n: file_digest(resolve_inside(directory, n)), targets))
     for name, digest in zip(targets, digests):
-        expected = manifest.files[name].sha256
-        if digest != expected:
-            raise CheckpointCorruptionError(
-                format_error(
-                    "reshard.verify_files",
-                    f"shard file {name!r} failed checksum verification; its contents differ "
-                    "from what the writer recorded",
-                    expected=expected,
-                    observed=digest,
-                    resolution="the file is corrupt; restore it from a backup or discard the checkpoint",
-                )
-            )
+        _require_digest(name, digest, manifest.files[name].sha256, "reshard.verify_files")
     return dict(zip(targets, digests))
 
 
@@ -458,11 +418,9 @@ def write_checkpoint(
         raise CheckpointError(
             format_error(
                 "checkpoint.save",
-                "the checkpoint could not be published; nothing was renamed into place, so the "
-                "checkpoint directory is unchanged",
-                expected="a validated manifest covering every tensor exactly once",
+                "the checkpoint could not be published; no directory was renamed into place",
                 observed=f"{type(error).__name__}: {error}",
-                resolution=f"the staging directory {staging.name!r} is left behind for inspection",
+                resolution=f"look in {staging.name!r}, which is kept as it was when the save failed",
             )
         ) from error
     return final
@@ -539,9 +497,8 @@ def load_flat_shard_checkpoint(
                 format_error(
                     "checkpoint.load_optimizer",
                     f"optimizer state {state_name!r} is missing for parameter {index}",
-                    expected=f"state entries for parameter {index}",
-                    observed="none",
-                    resolution="the checkpoint was written with save_optimizer=False",
+                    observed="no stored piece",
+                    resolution="this checkpoint holds model tensors only",
                 )
             )
     for name, value in scalars.items():

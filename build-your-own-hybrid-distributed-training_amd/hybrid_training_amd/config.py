@@ -49,7 +49,7 @@ def resolve_dtype(name: str | torch.dtype) -> torch.dtype:
                 "unknown dtype name",
                 expected=sorted(_DTYPE_NAMES),
                 observed=name,
-                resolution="use one of the listed dtype names",
+                resolution="name a float dtype as listed (case and a 'torch.' prefix are ignored)",
             )
         )
     return _DTYPE_NAMES[key]
@@ -76,10 +76,10 @@ class DDPConfig:
     def __post_init__(self) -> None:
         if self.bucket_cap_mb <= 0:
             _fail("DDPConfig", "bucket_cap_mb must be positive", "> 0", self.bucket_cap_mb,
-                  "use a positive bucket size, e.g. 25.0")
+                  "buckets hold at least one gradient, so the cap must be above zero")
         if self.source_rank_in_group < 0:
             _fail("DDPConfig", "source_rank_in_group must be non-negative", ">= 0",
-                  self.source_rank_in_group, "use a group-local rank index")
+                  self.source_rank_in_group, "index the source rank inside its group, from 0")
 
 
 @dataclass(frozen=True)
@@ -97,19 +97,18 @@ class FSDPConfig:
     def __post_init__(self) -> None:
         if self.auto_wrap_min_num_params < 0:
             _fail("FSDPConfig", "auto_wrap_min_num_params must be non-negative", ">= 0",
-                  self.auto_wrap_min_num_params, "use 0 to disable automatic wrapping")
+                  self.auto_wrap_min_num_params, "0 turns automatic wrapping off")
         if self.limit_all_gather_bytes < 0:
             _fail("FSDPConfig", "limit_all_gather_bytes must be non-negative", ">= 0",
-                  self.limit_all_gather_bytes, "use 0 to disable the guard rail")
+                  self.limit_all_gather_bytes, "0 means no limit")
         if not self.use_padding:
             _fail(
                 "FSDPConfig",
-                "use_padding=False is not supported: unpadded flat parameters make the local "
-                "shard size rank-dependent, which breaks the single-collective "
-                "all-gather/reduce-scatter fast path",
+                "use_padding=False is not supported: without padding, shard sizes would differ "
+                "between ranks and no single even split of the flat parameter would exist",
                 True,
                 False,
-                "leave use_padding at its default of True",
+                "keep use_padding=True",
             )
 
 
@@ -127,16 +126,16 @@ class GradScalerConfig:
     def __post_init__(self) -> None:
         if self.init_scale <= 0:
             _fail("GradScalerConfig", "init_scale must be positive", "> 0", self.init_scale,
-                  "use a power of two such as 65536")
+                  "a power of two keeps the scaling exact; 2**16 is the usual start")
         if not self.growth_factor > 1.0:
             _fail("GradScalerConfig", "growth_factor must exceed 1", "> 1.0", self.growth_factor,
-                  "use 2.0")
+                  "2.0 doubles the scale after each clean interval")
         if not 0.0 < self.backoff_factor < 1.0:
             _fail("GradScalerConfig", "backoff_factor must lie in (0, 1)", "0 < x < 1",
-                  self.backoff_factor, "use 0.5")
+                  self.backoff_factor, "0.5 halves the scale after an overflow")
         if self.growth_interval < 1:
             _fail("GradScalerConfig", "growth_interval must be at least 1", ">= 1",
-                  self.growth_interval, "use 2000")
+                  self.growth_interval, "count clean steps between growths, e.g. 2000")
 
 
 @dataclass(frozen=True)
@@ -156,11 +155,11 @@ class MixedPrecisionConfig:
         if self.enabled and self.scaler.enabled and resolve_dtype(self.param_dtype) is not torch.float16:
             _fail(
                 "MixedPrecisionConfig",
-                "dynamic loss scaling is only meaningful for float16 compute; bfloat16 has the "
-                "same exponent range as float32 and does not underflow in the same way",
-                "param_dtype=float16 when scaler.enabled",
+                "loss scaling is only meaningful for float16 compute: bfloat16 shares float32's "
+                "exponent range, so its gradients do not underflow where float16's do",
+                "float16",
                 self.param_dtype,
-                "either set param_dtype=float16 or scaler.enabled=false",
+                "compute in float16, or turn the scaler off",
             )
 
     @property
@@ -189,12 +188,12 @@ class OptimizerConfig:
     def __post_init__(self) -> None:
         if self.name not in {"adamw", "sgd"}:
             _fail("OptimizerConfig", "unknown optimizer", ["adamw", "sgd"], self.name,
-                  "use 'adamw' or 'sgd'")
+                  "the step kernels implement AdamW and SGD")
         if self.learning_rate <= 0:
             _fail("OptimizerConfig", "learning_rate must be positive", "> 0", self.learning_rate,
-                  "use a positive learning rate")
+                  "a step needs a learning rate above zero")
         betas = tuple(self.betas)
         if len(betas) != 2 or not all(0.0 <= b < 1.0 for b in betas):
             _fail("OptimizerConfig", "betas must be two values in [0, 1)",
-                  "(b1, b2) with 0 <= b < 1", self.betas, "use (0.9, 0.999)")
+                  "(b1, b2) with 0 <= b < 1", self.betas, "e.g. (0.9, 0.999)")
         object.__setattr__(self, "betas", betas)

@@ -151,11 +151,10 @@ class FlatParamHandle:
             raise ShardingError(
                 format_error(
                     "fsdp.FlatParamHandle",
-                    "an FSDP unit needs at least one parameter",
+                    "a flat parameter needs at least one parameter to flatten",
                     rank=shard_group.global_rank,
-                    expected=">= 1",
                     observed=0,
-                    resolution="do not create a unit for a parameter-free module",
+                    resolution="skip modules that own no parameters when building units",
                 )
             )
         flags = {bool(p.requires_grad) for _, p in named_parameters}
@@ -164,16 +163,11 @@ class FlatParamHandle:
             raise UnsupportedFeatureError(
                 format_error(
                     "fsdp.FlatParamHandle",
-                    "an FSDP unit flattens its parameters into a single tensor, so all of "
-                    "them must share one requires_grad flag; a unit cannot freeze part of "
-                    "its flat parameter",
+                    "mixed requires_grad in one unit: its flat parameter is one tensor with "
+                    "one gradient, so it is trained or frozen as a whole",
                     rank=shard_group.global_rank,
-                    expected="a uniform requires_grad within the unit",
-                    observed=f"frozen parameters present: {frozen[:8]}",
-                    resolution=(
-                        "wrap the frozen submodule as its own FSDP unit (auto-wrapping "
-                        "does this at module boundaries), or unfreeze it"
-                    ),
+                    observed={"frozen": frozen[:8]},
+                    resolution="give the frozen parameters a unit of their own",
                 )
             )
         if replica_group is not None and replica_group.size > 1:
@@ -324,12 +318,12 @@ class FlatParamHandle:
     # -- properties -------------------------------------------------------------------
     @property
     def entries(self) -> tuple[FlatEntry, ...]:
-        """Layout of the parameters inside the flat buffer."""
+        """One :class:`FlatEntry` per managed parameter, in flat order."""
         return self._entries
 
     @property
     def managed_parameters(self) -> tuple[nn.Parameter, ...]:
-        """The original parameter objects this unit flattened."""
+        """The caller's parameter objects, in flat order."""
         return self._params
 
     @property
@@ -344,12 +338,12 @@ class FlatParamHandle:
 
     @property
     def total_numel(self) -> int:
-        """Logical element count, excluding padding."""
+        """Elements of all managed parameters together (no padding)."""
         return self._total_numel
 
     @property
     def padded_numel(self) -> int:
-        """Element count including padding."""
+        """``shard_numel * group size``: the total rounded up to whole shards."""
         return self._padded_numel
 
     @property
@@ -364,7 +358,7 @@ class FlatParamHandle:
 
     @property
     def shard_group(self) -> GroupHandle:
-        """The group the flat parameter is split across."""
+        """The ranks that each hold one shard of the flat parameter."""
         return self._shard_group
 
     @property
@@ -741,22 +735,21 @@ class FlatParamHandle:
                 raise ShardingError(
                     format_error(
                         "fsdp.load_local_pieces",
-                        "missing parameter in the state dict",
+                        f"no tensor for parameter {entry.name!r} among the pieces to load",
                         rank=self._shard_group.global_rank,
-                        expected=entry.name,
                         observed=sorted(pieces)[:8],
-                        resolution="load a state dict produced by the same model definition",
+                        resolution="the pieces must come from a model of the same definition",
                     )
                 )
             if tuple(tensor.shape) != entry.shape:
                 raise ShardingError(
                     format_error(
                         "fsdp.load_local_pieces",
-                        f"shape mismatch for {entry.name!r}",
+                        f"{entry.name!r} has another shape than the unit's parameter",
                         rank=self._shard_group.global_rank,
                         expected=entry.shape,
                         observed=tuple(tensor.shape),
-                        resolution="the checkpoint was written by a differently shaped model",
+                        resolution="the pieces must come from a model of the same definition",
                     )
                 )
             overlap = intersect_ranges(local, ShardRange(entry.offset, entry.numel))
@@ -812,10 +805,9 @@ def reshard_state_dict_pieces(
         raise ShardingError(
             format_error(
                 "fsdp.reshard_state_dict_pieces",
-                "no pieces supplied",
-                expected=">= 1 piece",
+                "a tensor cannot be reassembled from zero pieces",
                 observed=0,
-                resolution="check that the manifest lists shards for this tensor",
+                resolution="pass every stored piece of the tensor",
             )
         )
     dtype = pieces[0].data.dtype
@@ -827,10 +819,10 @@ def reshard_state_dict_pieces(
             raise ShardingError(
                 format_error(
                     "fsdp.reshard_state_dict_pieces",
-                    f"piece for {piece.name!r} runs past the end of the tensor",
-                    expected=f"offset + length <= {total}",
+                    f"a piece of {piece.name!r} reaches past the end of the tensor",
+                    expected=f"end <= {total}",
                     observed=end,
-                    resolution="the manifest disagrees with the model definition",
+                    resolution="the pieces and the tensor's shape come from different models",
                 )
             )
         intervals.append((piece.offset, end))
@@ -847,7 +839,7 @@ def reshard_state_dict_pieces(
                 f"the supplied pieces leave {missing} element(s) of {pieces[0].name!r} uncovered",
                 expected=f"{total} covered elements",
                 observed=covered,
-                resolution="a shard file is missing from the checkpoint",
+                resolution="some piece of the tensor was not passed in",
             )
         )
     flat = torch.empty(total, dtype=dtype, device=device)

@@ -72,7 +72,7 @@ class GradScalerState:
 
     @classmethod
     def from_dict(cls, payload: dict[str, Any]) -> GradScalerState:
-        """Rebuild from :meth:`as_dict` output."""
+        """Inverse of :meth:`as_dict`."""
         return cls(
             scale=float(payload["scale"]),
             growth_tracker=int(payload.get("growth_tracker", 0)),
@@ -282,7 +282,7 @@ class GradScaler:
 
     @property
     def last_step_skipped(self) -> bool:
-        """Whether the most recent :meth:`step` was skipped."""
+        """True when the last :meth:`step` found a non-finite gradient and did not update."""
         return self._skipped_on_last_step
 
     def state_dict(self) -> dict[str, float]:

@@ -42,7 +42,7 @@ class GroupHandle:
 
     @property
     def size(self) -> int:
-        """Number of ranks in the group."""
+        """How many ranks the group spans."""
         return len(self.ranks)
 
     @property

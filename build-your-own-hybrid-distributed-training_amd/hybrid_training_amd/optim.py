@@ -109,10 +109,9 @@ def build_inner_optimizer(
         raise ShardingError(
             format_error(
                 "optim.build_inner_optimizer",
-                "no trainable parameters were supplied",
-                expected=">= 1 parameter with requires_grad=True",
+                "no trainable parameters were supplied to the optimizer",
                 observed=0,
-                resolution="check that the model was wrapped before the optimizer was built",
+                resolution="build the optimizer from the wrapped model's parameters",
             )
         )
     if config.name == "adamw":
@@ -240,7 +239,7 @@ def build_gradient_norm_contributions(
                 "world_size must be positive",
                 expected=">= 1",
                 observed=world_size,
-                resolution="pass the size of the reduction group",
+                resolution="the norm is summed over at least one rank",
             )
         )
     contributions: list[NormContribution] = []
@@ -1102,7 +1101,7 @@ class ShardedOptimizer:
     # -- introspection -------------------------------------------------------------------
     @property
     def parameters(self) -> tuple[nn.Parameter, ...]:
-        """The parameters this optimizer updates."""
+        """Every parameter a step updates, in construction order."""
         return tuple(self._parameters)
 
     @property
@@ -1112,7 +1111,7 @@ class ShardedOptimizer:
 
     @property
     def norm_group(self) -> GroupHandle:
-        """The group the gradient norm is reduced over."""
+        """The ranks whose squared-norm partials add up to the global norm."""
         return self._norm_group
 
     @property

@@ -56,14 +56,10 @@ class DeviceShardCache:
         if payload is None:
             raise IncompleteCheckpointError(
                 format_error(
-                    "reshard.ShardFileCache.get",
-                    "a shard file listed in the manifest is missing",
-                    expected=filename,
-                    observed="not present in the checkpoint directory",
-                    resolution=(
-                        "the checkpoint is incomplete; restore the missing file or "
-                        "resume from an earlier checkpoint"
-                    ),
+                    "reshard.DeviceShardCache.get",
+                    f"payload {filename!r} is missing from the device cache",
+                    observed=sorted(self._payloads)[:8],
+                    resolution="add every payload file the manifest lists before reading",
                 )
             )
         self._loaded.add(filename)
@@ -85,18 +81,17 @@ def _queue_range(
     """Queue the copies that fill ``wanted`` of ``record``; returns the first shard's dtype.
 
     ``add(source_flat, source_offset, dest_offset, length)`` receives one interval per
-    intersecting shard, in offset order.  The checks and messages are those of
-    ``reshard.py:224-302``.
+    intersecting shard, in offset order.  The checks are those of ``reshard.py:224-302``,
+    in the same order and with the same exception classes.
     """
     if wanted.end > record.numel:
         raise CheckpointError(
             format_error(
                 "reshard.read_tensor_range",
-                f"the requested range of {record.key!r} runs past the end of the tensor; "
-                "the current model is larger than the one that was saved",
-                expected=f"end <= {record.numel}",
+                f"range [{wanted.start}, {wanted.end}) of {record.key!r} reaches past the end of "
+                f"the saved tensor ({record.numel} elements)",
                 observed=wanted.end,
-                resolution="resume with the model definition that produced the checkpoint",
+                resolution="the model being loaded is larger than the one saved",
             )
         )
     overlaps = record.shards_overlapping(wanted)
@@ -104,10 +99,9 @@ def _queue_range(
         raise IncompleteCheckpointError(
             format_error(
                 "reshard.read_tensor_range",
-                f"no shard of {record.key!r} covers the requested range",
-                expected=f"a shard intersecting [{wanted.start}, {wanted.end})",
+                f"none of the saved intervals of {record.key!r} meets [{wanted.start}, {wanted.end})",
                 observed=[(s.offset, s.length) for s in record.shards],
-                resolution="the checkpoint is incomplete",
+                resolution="the writer that held this interval left no record",
             )
         )
     first_dtype: torch.dtype | None = None
@@ -118,10 +112,8 @@ def _queue_range(
             raise IncompleteCheckpointError(
                 format_error(
                     "reshard.read_tensor_range",
-                    f"a gap exists in the shards of {record.key!r}",
-                    expected=f"a shard starting at element {cursor}",
-                    observed=f"next shard starts at {overlap.start}",
-                    resolution="a shard file is missing from the checkpoint",
+                    f"elements [{cursor}, {overlap.start}) of {record.key!r} are in no shard (a gap)",
+                    resolution="the writer that held them left no record",
                 )
             )
         payload = cache.get(shard.file)
@@ -130,10 +122,9 @@ def _queue_range(
             raise CheckpointCorruptionError(
                 format_error(
                     "reshard.read_tensor_range",
-                    f"shard file {shard.file!r} does not contain key {shard.key!r}",
-                    expected=shard.key,
+                    f"payload {shard.file!r} holds no entry {shard.key!r}",
                     observed=sorted(payload)[:8],
-                    resolution="the manifest and the payload disagree; the checkpoint is corrupt",
+                    resolution="manifest and payload were not written together",
                 )
             )
         flat = _native.contiguous_source(stored.reshape(-1))
@@ -141,10 +132,8 @@ def _queue_range(
             raise CheckpointCorruptionError(
                 format_error(
                     "reshard.read_tensor_range",
-                    f"shard {shard.key!r} has a different length from its manifest record",
-                    expected=shard.length,
-                    observed=flat.numel(),
-                    resolution="the manifest and the payload disagree; the checkpoint is corrupt",
+                    f"entry {shard.key!r} holds {flat.numel()} elements, its record says {shard.length}",
+                    resolution="manifest and payload were not written together",
                 )
             )
         if first_dtype is None:
@@ -156,10 +145,9 @@ def _queue_range(
         raise IncompleteCheckpointError(
             format_error(
                 "reshard.read_tensor_range",
-                f"the shards of {record.key!r} cover only part of the requested range",
-                expected=wanted.length,
-                observed=filled,
-                resolution="a shard file is missing from the checkpoint",
+                f"the shards of {record.key!r} supply {filled} of the {wanted.length} elements "
+                f"of [{wanted.start}, {wanted.end})",
+                resolution="the writer that held the rest left no record",
             )
         )
     assert first_dtype is not None
@@ -281,10 +269,9 @@ def describe_reshard(manifest: CheckpointManifest, key: str, wanted: ShardRange)
         raise CheckpointError(
             format_error(
                 "reshard.describe_reshard",
-                "unknown tensor key",
-                expected=sorted(manifest.tensors)[:8],
-                observed=key,
-                resolution="check the key against the manifest",
+                f"unknown tensor key {key!r}",
+                observed=sorted(manifest.tensors)[:8],
+                resolution="use a key listed in the manifest's tensors",
             )
         )
     return {

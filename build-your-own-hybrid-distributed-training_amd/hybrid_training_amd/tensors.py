@@ -79,10 +79,9 @@ class ShardRange:
             raise ShardingError(
                 format_error(
                     "tensors.ShardRange",
-                    "shard ranges must be non-negative",
-                    expected="start >= 0 and length >= 0",
-                    observed=f"start={self.start}, length={self.length}",
-                    resolution="check the offset arithmetic that produced this range",
+                    "a range needs a non-negative start and length",
+                    observed=(self.start, self.length),
+                    resolution="the offset computation that built it went below zero",
                 )
             )
 
@@ -119,7 +118,7 @@ def build_flat_layout(
                 "cannot flatten an empty tensor list",
                 expected=">= 1 tensor",
                 observed=0,
-                resolution="do not create a flat parameter for a module with no parameters",
+                resolution="build flat parameters only for modules that own parameters",
             )
         )
     entries: list[FlatEntry] = []
@@ -130,14 +129,9 @@ def build_flat_layout(
             raise ShardingError(
                 format_error(
                     "tensors.build_flat_layout",
-                    "duplicate tensor name in a flat parameter; this indicates a shared "
-                    "(tied) tensor being registered twice in the same unit",
-                    expected="unique names",
+                    f"duplicate tensor name {name!r}: one tensor (a tied weight?) is listed twice",
                     observed=name,
-                    resolution=(
-                        "de-duplicate tied parameters before flattening, or place the "
-                        "tied tensors in the same unit exactly once"
-                    ),
+                    resolution="list every tied tensor once per unit",
                 )
             )
         names.add(name)
@@ -204,7 +198,7 @@ def shard_range_for(total_numel: int, num_shards: int, shard_index: int) -> Shar
                 "shard index outside the group",
                 expected=f"0 <= i < {num_shards}",
                 observed=shard_index,
-                resolution="pass the rank's index within the shard group",
+                resolution="use a rank index local to the shard group",
             )
         )
     return even_shard_ranges(total_numel, num_shards)[shard_index]
@@ -256,10 +250,10 @@ def flatten_dense_tensors(
             raise ShardingError(
                 format_error(
                     "tensors.flatten_dense_tensors",
-                    "all tensors in a flat buffer must share dtype and device",
+                    "tensors flattened together must share dtype and device",
                     expected=f"{dtype} on {device}",
                     observed=f"{tensor.dtype} on {tensor.device}",
-                    resolution="group parameters by dtype/device before flattening",
+                    resolution="flatten each (dtype, device) group on its own",
                 )
             )
         total += int(tensor.numel())
@@ -269,10 +263,10 @@ def flatten_dense_tensors(
         raise ShardingError(
             format_error(
                 "tensors.flatten_dense_tensors",
-                "destination buffer is the wrong size",
+                "the output buffer has the wrong size",
                 expected=total,
                 observed=out.numel(),
-                resolution="allocate a buffer with exactly the total element count",
+                resolution="size it to the sum of the tensors' element counts",
             )
         )
     plan = _native.CopyPlan(out.device)
@@ -294,10 +288,9 @@ def unflatten_to_views(flat: torch.Tensor, entries: Sequence[FlatEntry]) -> list
         raise ShardingError(
             format_error(
                 "tensors.unflatten_to_views",
-                "the flat buffer must be one-dimensional",
-                expected="dim() == 1",
+                "views are cut from a one-dimensional buffer only",
                 observed=flat.dim(),
-                resolution="reshape the buffer to (-1,) before unflattening",
+                resolution="pass buffer.reshape(-1)",
             )
         )
     needed = entries[-1].end if entries else 0
@@ -305,10 +298,10 @@ def unflatten_to_views(flat: torch.Tensor, entries: Sequence[FlatEntry]) -> list
         raise ShardingError(
             format_error(
                 "tensors.unflatten_to_views",
-                "flat buffer is too short for the layout",
+                "the buffer is too short for the layout's last tensor",
                 expected=f">= {needed} elements",
                 observed=flat.numel(),
-                resolution="allocate the padded size, not the logical size",
+                resolution="allocate the padded element count",
             )
         )
     return [flat.narrow(0, e.offset, e.numel).view(e.shape) for e in entries]
@@ -324,18 +317,16 @@ def pad_flat_tensor(flat: torch.Tensor, multiple: int, *, value: float = 0.0) ->
         raise ShardingError(
             format_error(
                 "tensors.pad_flat_tensor",
-                "expected a one-dimensional tensor",
-                expected="dim() == 1",
+                "padding applies to one-dimensional tensors only",
                 observed=flat.dim(),
-                resolution="flatten before padding",
+                resolution="pad tensor.reshape(-1)",
             )
         )
     if multiple < 1:
         raise ShardingError(
             format_error(
                 "tensors.pad_flat_tensor",
-                "the alignment multiple must be positive",
-                expected=">= 1",
+                "an alignment multiple must be positive",
                 observed=multiple,
                 resolution="pass the shard-group size",
             )
