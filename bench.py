@@ -189,7 +189,9 @@ def main() -> int:
     if args.workload != "adamw":
         global _WITH_CPU
         _WITH_CPU = not args.no_cpu_baseline
-        return SECONDARY[args.workload](args.steps, args.warmup)
+        status = SECONDARY[args.workload](args.steps, args.warmup)
+        _settle()
+        return status
 
     import torch
 
@@ -291,7 +293,17 @@ def main() -> int:
         log(f"CPU baseline on {args.cpu_numel} elements")
         result["cpu_baseline"] = cpu_baseline(args.cpu_numel, args.cpu_steps)
     print(json.dumps(result), flush=True)
+    _settle()
     return 0
+
+
+def _settle() -> None:
+    """Wait for every queued kernel and copy (a streamed pass may leave non-blocking copies
+    to pinned host memory in flight) before the process starts to exit."""
+    import torch
+
+    if torch.cuda.is_initialized():
+        torch.cuda.synchronize()
 
 
 # ---------------------------------------------------------------------------------------

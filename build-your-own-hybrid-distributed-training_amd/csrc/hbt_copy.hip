@@ -211,6 +211,7 @@ __device__ __forceinline__ int64_t owning_record(const int64_t* __restrict__ tab
                                                  int64_t chunk, const int64_t* __restrict__ hints) {
     if (hints != nullptr) {
         int64_t r = hints[chunk >> kHintShift];
+        r = r < 0 ? 0 : (r < count ? r : count - 1);  // a wrong hint stays inside the table
         while (r + 1 < count && table[4 * (r + 1) + 3] <= chunk) ++r;
         return r;
     }

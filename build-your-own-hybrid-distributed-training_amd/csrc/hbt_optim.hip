@@ -819,11 +819,14 @@ __global__ __launch_bounds__(64) void scale_kernel(ScaleTable tab, float unscale
     constexpr int K = scale_vec<D>();
     constexpr int kScaleBlock = scale_block<D>();
     constexpr int64_t kTile = scale_tile<D>();
+    const float mul = grad_mul != nullptr ? *grad_mul : 1.0f;
+    // Both factors 1: nothing to multiply.  The reference's clip multiplies only when its
+    // coefficient is below 1, so the gradient is left untouched, bits and all.
+    if (unscale == 1.0f && mul == 1.0f) return;
     const int64_t block = block_base + blockIdx.x;
     const int t = owning_tensor(tab.first_block, tab.count, block);
     const int64_t base = (block - tab.first_block[t]) * kTile;
     const int64_t n = tab.n[t];
-    const float mul = grad_mul != nullptr ? *grad_mul : 1.0f;
     void* X = tab.x[t];
     if (tab.vec_ok[t] && base + kTile <= n) {
         float v[kScaleUnroll][K];

@@ -71,3 +71,38 @@ from .tensors import (
 )
 
 __version__ = "0.1.0"
+
+
+def _release_device_state() -> None:
+    """Exit hook: settle the device before the C++ runtimes tear down.
+
+    Python exit hooks run before the static destructors of torch and of the HIP runtime.
+    By then a streamed pass may still have non-blocking copies in flight into pinned host
+    memory, and this package still caches device objects: the staging streams, their
+    events and buffers (``host_staging``) and the device tables of copy plans
+    (``_native``).  Waiting for every device, dropping those caches and handing torch's
+    cached device and pinned blocks back to the runtime here, while it is fully up, leaves
+    the static destructors nothing of this package's to free in an unknown order.
+    """
+    import gc
+
+    import torch
+
+    from . import _native, host_staging
+
+    if not torch.cuda.is_initialized():
+        return
+    for index in range(torch.cuda.device_count()):
+        with torch.cuda.device(index):
+            torch.cuda.synchronize()
+    host_staging.release_streams()
+    _native.release_tables()
+    gc.collect()
+    torch.cuda.empty_cache()
+    if hasattr(torch._C, "_host_emptyCache"):
+        torch._C._host_emptyCache()
+
+
+import atexit as _atexit  # noqa: E402  (registered after torch's own hooks, so it runs first)
+
+_atexit.register(_release_device_state)

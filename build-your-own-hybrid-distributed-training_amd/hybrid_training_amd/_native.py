@@ -18,9 +18,10 @@ import ctypes
 import os
 import threading
 from collections import OrderedDict
-from collections.abc import Sequence
+from collections.abc import Iterable, Sequence
 
 import torch
+from torch.autograd.graph import increment_version
 
 from .errors import NativeKernelError, ShardingError, UnsupportedFeatureError, format_error
 
@@ -178,6 +179,12 @@ _LIB: ctypes.CDLL | None = None
 # upload, which for a few hundred rows costs more than moving a GB on the device.
 _TABLE_CACHE: "OrderedDict[tuple, tuple[torch.Tensor, int, bool, bool]]" = OrderedDict()
 _TABLE_CACHE_SIZE = 256
+
+
+def release_tables() -> None:
+    """Drop every cached device table of a copy plan (rebuilt on the next use)."""
+    with _TABLE_LOCK:
+        _TABLE_CACHE.clear()
 
 
 def library_path() -> str:
@@ -414,6 +421,19 @@ def _prepared_plan(
     return entry
 
 
+def bump_versions(tensors: Iterable[torch.Tensor]) -> None:
+    """Advance the autograd version counter of every tensor a kernel wrote in place
+    (inference tensors carry none and are skipped).
+
+    Writes that bypass the counter, such as ones made through ``tensor.data`` or by
+    foreign code holding a raw pointer, are not seen: a gradient's cached norm partials
+    (keyed by address and version) then describe the old values.
+    """
+    written = [t for t in tensors if not t.is_inference()]
+    if written:
+        increment_version(written)
+
+
 class CopyPlan:
     """Interval table for one ``hbt_copy_intervals`` launch.
 
@@ -432,6 +452,10 @@ class CopyPlan:
         # and dropped before run() would hand its memory to the next allocation on the
         # stream, this plan's own table among them, before the kernel reads it.
         self._keep: list[torch.Tensor] = []
+        # The tensors the plan writes: run() bumps their autograd version counters, as the
+        # in-place copy_ it replaces would, so anything keyed on a version (a gradient's
+        # cached norm partials, autograd's saved-tensor checks) sees the change.
+        self._dests: dict[int, torch.Tensor] = {}
 
     def __len__(self) -> int:
         return len(self._rows)
@@ -442,7 +466,8 @@ class CopyPlan:
 
         For callers that have already checked every address against a dense device
         tensor of the plan's dtypes and every extent against that tensor's end, and
-        that keep those tensors alive until :meth:`run` has returned.
+        that keep those tensors alive until :meth:`run` has returned, and that bump the
+        version counters of the tensors written (:func:`bump_versions`).
         """
         plan = cls(device)
         plan._rows = [row for row in rows if row[2] > 0]
@@ -464,7 +489,7 @@ class CopyPlan:
         if n == 0:
             return
         self._keep.append(src)
-        self._keep.append(dst)
+        self._dests[id(dst)] = dst
         self._rows.append(
             (
                 src.data_ptr() + src_offset * src.element_size(),
@@ -482,7 +507,7 @@ class CopyPlan:
             raise ValueError("copy plans address dense tensors only")
         if n == 0:
             return
-        self._keep.append(dst)
+        self._dests[id(dst)] = dst
         self._rows.append((0, dst.data_ptr() + dst_offset * dst.element_size(), n))
 
     def run(
@@ -518,3 +543,4 @@ class CopyPlan:
                 stream_of(self.device),
             )
         check(status, "native.hbt_copy_intervals")
+        bump_versions(self._dests.values())

@@ -340,6 +340,8 @@ class BucketedGradients:
         for (device_index, src_dtype, dst_dtype), table in rows.items():
             plan = _native.CopyPlan.from_rows(torch.device("cuda", device_index), table)
             plan.run(src_dtype=src_dtype, dst_dtype=dst_dtype, op=op, divisor=divisor)
+        if rows:
+            _native.bump_versions([b.buffer for b in selected])
         self.statistics.unused_parameters = tuple(missing)
         self.statistics.buckets_reduced += len(selected)
         self.statistics.bytes_reduced += sum(b.num_bytes() for b in selected)

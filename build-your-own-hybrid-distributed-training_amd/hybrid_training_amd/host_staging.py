@@ -179,6 +179,13 @@ class HostStream:
 _STREAMS: dict[int, HostStream] = {}
 
 
+def release_streams() -> None:
+    """Forget every device's :class:`HostStream` (streams, events and staging buffers);
+    the next pass creates a new one.  Called at interpreter exit, after the devices have
+    been synchronised."""
+    _STREAMS.clear()
+
+
 def host_stream(device: torch.device) -> HostStream:
     """The :class:`HostStream` of ``device`` (one per device, shared by every pass)."""
     device = torch.device(device)

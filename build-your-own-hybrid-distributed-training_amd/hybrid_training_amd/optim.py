@@ -19,21 +19,24 @@ and owns ``param_groups`` and ``state``, so ``state_dict``/``load_state_dict``,
 ``step`` is never called.
 
 Clip placement.  The clip multiplier never leaves the device: ``clip_grad_norm``
-computes the norm and the multiplier, and the fused update pass applies it.  Every
-multiply is rounded to the gradient's dtype exactly as the reference's in-place
-``grad.mul_`` calls round it, so the parameters and state come out bitwise the same
-either way.  What differs is ``.grad``:
+computes the norm and the multiplier there, and no host synchronisation sits between
+the norm and the update.  Every multiply is rounded to the gradient's dtype exactly as
+the reference's in-place ``grad.mul_`` calls round it, so the parameters and state come
+out bitwise the same in all three placements.  What differs is when ``.grad`` changes,
+and the HBM traffic of a clipped fp32 step:
 
-* default (``defer_clip=False``, the reference's semantics): the update pass also
-  writes the clipped (and, with a deferred loss scale, unscaled) gradient back into
-  ``.grad``, so after ``step()`` the gradients hold exactly what the reference's
-  in-place clip leaves there, for one extra 4 B/element write instead of a separate
-  read-and-write pass.  Between ``clip_grad_norm()`` and ``step()`` ``.grad`` still
-  holds the unclipped values; :meth:`ShardedOptimizer.materialize_pending` applies the
-  clip in place at once for a caller that reads them in that window, and a loss scaler
-  that skips the step does so itself;
-* ``defer_clip=True``: the gradients are never written; ``.grad`` keeps the unclipped
-  values.  This saves the write-back (32 instead of 36 B/element per clipped step).
+* default (the reference's semantics, ``sharded_optimizer.py:333-337``):
+  ``clip_grad_norm`` clips ``.grad`` in place before it returns (``hbt_scale_inplace``,
+  which reads the multiplier from the device and does nothing when it is 1, as the
+  reference multiplies only below 1); the update then reads the clipped gradient.
+  4 + 8 + 28 = 40 B/element;
+* ``clip_in_step=True``: ``clip_grad_norm`` only records the multiplier; the update
+  applies it and writes the clipped gradient back, so ``.grad`` is the reference's after
+  ``step()`` but still unclipped between the two calls
+  (:meth:`ShardedOptimizer.materialize_pending` clips it at once for a caller that reads
+  it in that window; a loss scaler that skips the step does so itself).  36 B/element;
+* ``defer_clip=True``: the update applies the multiplier and the gradients are never
+  written; ``.grad`` keeps the unclipped values.  32 B/element.
 """
 
 from __future__ import annotations
@@ -48,7 +51,7 @@ from torch.autograd.graph import increment_version
 
 from . import _native
 from .config import OptimizerConfig
-from .errors import ShardingError, UnsupportedFeatureError, format_error
+from .errors import ConfigurationError, ShardingError, UnsupportedFeatureError, format_error
 from .groups import GroupHandle
 from .host_staging import HostOperand, host_stream, is_host
 
@@ -587,7 +590,8 @@ class ShardedOptimizer:
     """AdamW or SGD over this rank's shards with a global-norm clip, on HIP kernels.
 
     Same constructor, methods and properties as ``sharded_optimizer.py:244-499``.
-    ``defer_clip`` is the one addition (see the module docstring).  Master parameters
+    ``defer_clip`` and ``clip_in_step`` are the additions (see the module docstring);
+    with neither, the clip is the reference's in-place clip.  Master parameters
     are float32, bfloat16 or float16, as the reference's flat shards are (the
     parameters' own dtype when mixed precision is off, ``fsdp.py:379-384``); 2-byte
     masters take gradients of their own dtype, fp32 masters fp32 or bf16 gradients.
@@ -612,13 +616,21 @@ class ShardedOptimizer:
         device: torch.device,
         recorder: Any = None,
         defer_clip: bool = False,
+        clip_in_step: bool = False,
     ) -> None:
+        if defer_clip and clip_in_step:
+            raise ConfigurationError(
+                format_error("optim.ShardedOptimizer",
+                             "defer_clip and clip_in_step are two different clip placements; pick one",
+                             observed={"defer_clip": defer_clip, "clip_in_step": clip_in_step})
+            )
         self._parameters = [p for p in parameters if p.requires_grad]
         self._config = config
         self._norm_group = norm_group
         self._device = torch.device(device)
         self._recorder = recorder
         self._defer_clip = defer_clip
+        self._clip_in_step = clip_in_step
         _check_group(norm_group, "optim.ShardedOptimizer")
         for param in self._parameters:
             if not is_host(param):
@@ -716,9 +728,10 @@ class ShardedOptimizer:
     def clip_grad_norm(self, max_norm: float) -> torch.Tensor:
         """Clip to a global L2 norm; return the pre-clip norm (0-dim fp64 device tensor).
 
-        ``max_norm <= 0`` only computes the norm (``sharded_optimizer.py:310-338``).
-        The multiplier is applied by the next :meth:`step` (and, by default, written
-        back into ``.grad`` there; see the module docstring).
+        ``max_norm <= 0`` only computes the norm (``sharded_optimizer.py:310-338``).  By
+        default ``.grad`` is clipped in place before this returns, as in the reference;
+        with ``clip_in_step`` or ``defer_clip`` the next :meth:`step` applies the
+        multiplier instead (see the module docstring).
         """
         if self._pending_mul is not None:
             self.materialize_pending()
@@ -727,14 +740,17 @@ class ShardedOptimizer:
             return result.norm
         self._pending_mul = result.grad_mul
         self._pending_signature = _grad_signature(self._parameters)
+        if not (self._defer_clip or self._clip_in_step):
+            self.materialize_pending()  # the reference's grad.mul_(coefficient), on the device
         return result.norm
 
     def clip_and_step(self, max_norm: float) -> torch.Tensor:
         """``clip_grad_norm(max_norm)`` then ``step()``; returns the pre-clip norm.
 
-        Two kernels read the gradients: the norm (4 B/element for fp32) and the fused
-        update (28 B/element of p, g, m, v traffic, plus the 4 B/element write-back
-        of the clipped gradient unless ``defer_clip`` is set).
+        The norm reads the gradients (4 B/element for fp32) and the fused update moves
+        28 B/element of p, g, m and v; the default in-place clip adds a read and a write
+        of the gradients between them (8 B/element), ``clip_in_step`` a write of the
+        clipped gradient by the update (4 B/element), ``defer_clip`` nothing.
         """
         norm = self.clip_grad_norm(max_norm)
         self.step()
@@ -743,8 +759,8 @@ class ShardedOptimizer:
     @property
     def clips_in_place(self) -> bool:
         """Whether ``.grad`` ends up clipped (and unscaled) as the reference leaves it:
-        ``defer_clip=False``.  A loss scaler that skips the step materialises a pending
-        clip on such an optimizer (:meth:`materialize_pending`)."""
+        ``defer_clip=False``.  With ``clip_in_step`` a loss scaler that skips the step
+        materialises the pending clip (:meth:`materialize_pending`)."""
         return not self._defer_clip
 
     def last_nonfinite_flag(self) -> torch.Tensor | None:

@@ -368,7 +368,9 @@ int32_t hbt_grad_accumulate(void* const* accumulators, const void* const* grads,
  *   ShardedOptimizer.clip_grad_norm (optim/sharded_optimizer.py:333-337).  The fused
  *   optimizer path folds both multiplies into hbt_adamw_step instead; this entry
  *   point materialises them when a caller needs the scaled gradients themselves.
- * grad_mul may be NULL (treated as 1).
+ * grad_mul may be NULL (treated as 1).  When unscale == 1 and *grad_mul == 1 nothing is
+ * read or written: the reference multiplies only when its clip coefficient is below 1,
+ * so the gradient keeps its bits (a bf16 NaN payload included).
  * ---------------------------------------------------------------------------- */
 int32_t hbt_scale_inplace(void* const* tensors, const int64_t* numels, int32_t count,
                           int32_t dtype, float unscale, const float* grad_mul, void* stream);

@@ -370,11 +370,11 @@ def test_load_local_pieces_round_trip(device):
         assert np.array_equal(h.flat_param.detach().cpu().numpy(), oracle.pack_shard(host, 4, rank))
     full = handles[0].full_tensors(peer_shards=[h.flat_param for h in handles])
     assert all(torch.equal(full[n], state[n]) for n in state)
-    with pytest.raises(ShardingError, match="missing parameter"):
+    with pytest.raises(ShardingError, match="no tensor for parameter"):
         handles[0].load_local_pieces({})
     bad = dict(state)
     bad["p0"] = torch.zeros(3, device=device)
-    with pytest.raises(ShardingError, match="shape mismatch"):
+    with pytest.raises(ShardingError, match="another shape"):
         handles[0].load_local_pieces(bad)
 
 

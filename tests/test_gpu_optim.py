@@ -206,13 +206,14 @@ def test_norm_nonfinite(device):
     assert int(r.nonfinite) == 1
 
 
-def _make_optimizer(params, lr=3e-4, betas=(0.9, 0.95), wd=0.1, defer=False):
+def _make_optimizer(params, lr=3e-4, betas=(0.9, 0.95), wd=0.1, defer=False, in_step=False):
     return ShardedOptimizer(
         params,
         OptimizerConfig(name="adamw", learning_rate=lr, betas=betas, weight_decay=wd, eps=1e-8),
         norm_group=GroupHandle.trivial(),
         device=params[0].device,
         defer_clip=defer,
+        clip_in_step=in_step,
     )
 
 
@@ -256,32 +257,80 @@ def test_sharded_optimizer_vs_torch_adamw(device):
 
 
 def test_clip_is_in_place_like_the_reference(device):
-    """By default .grad ends up clipped as the reference's ``grad.mul_`` leaves it: written
-    back by the step's fused pass, or at once by ``materialize_pending``.  Both give the
-    same gradients and parameters; ``defer_clip=True`` leaves .grad unclipped."""
+    """By default ``clip_grad_norm`` clips .grad in place before it returns, as the
+    reference's ``grad.mul_`` does.  With ``clip_in_step`` the step's fused pass writes the
+    clipped gradient back instead (or ``materialize_pending`` at once); with
+    ``defer_clip`` .grad stays unclipped.  All four give the same parameters."""
     expect = torch.full((4,), 3.0).mul_(1.0 / (6.0 + 1e-6))
+    unclipped = torch.full((4,), 3.0)
     results = {}
-    for mode in ("write_back", "materialize", "defer"):
+    for mode in ("eager", "write_back", "materialize", "defer"):
         param = torch.nn.Parameter(torch.ones(4, device=device))
         param.grad = torch.full((4,), 3.0, device=device)
-        opt = _make_optimizer([param], defer=(mode == "defer"))
+        opt = _make_optimizer([param], defer=(mode == "defer"), in_step=mode in ("write_back", "materialize"))
+        before = param.grad._version
         norm = opt.clip_grad_norm(1.0)
         assert float(norm) == 6.0
+        assert torch.equal(param.grad.cpu(), expect if mode == "eager" else unclipped), mode
+        assert (param.grad._version > before) == (mode == "eager")
         if mode == "materialize":
             opt.materialize_pending()
             assert torch.equal(param.grad.cpu(), expect)
         version = param.grad._version
         opt.step()
         if mode == "defer":
-            assert torch.equal(param.grad.cpu(), torch.full((4,), 3.0))
+            assert torch.equal(param.grad.cpu(), unclipped)
         else:
             assert torch.equal(param.grad.cpu(), expect)
             assert abs(float(param.grad.double().norm()) - 1.0) < 1e-5
             # the write-back is an in-place change: it bumps the version counter
             assert (param.grad._version > version) == (mode == "write_back")
         results[mode] = param.detach().cpu()
-    assert torch.equal(results["write_back"], results["materialize"])
-    assert torch.equal(results["write_back"], results["defer"])
+    for mode in ("write_back", "materialize", "defer"):
+        assert torch.equal(results["eager"], results[mode]), mode
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_clip_then_read_grad_without_a_step(device, dtype):
+    """The default clip leaves ``.grad`` clipped as soon as ``clip_grad_norm`` returns,
+    with no step: a caller that logs or checks the clipped gradients, or hands them to a
+    plain torch optimizer, reads the reference's values.  Several tensors (one of them
+    misaligned and ragged) clipped by a multiplier that is not a power of two, compared
+    bitwise with the oracle's ``grad.mul_``; a norm below the threshold leaves every bit,
+    a bf16 NaN payload included, untouched (the reference multiplies only below 1).  The
+    expected gradients are the reference's own op, ``grad.mul_(coefficient)`` with the
+    Python-double coefficient, run by torch on the CPU."""
+    gen = torch.Generator(device=device).manual_seed(31)
+    sizes = (70_001, 4096, 33)
+    grads = [(torch.randn(n + 1, device=device, generator=gen) * 0.37).to(dtype)[1:] for n in sizes]
+    params = [torch.nn.Parameter(torch.zeros(g.shape, dtype=dtype, device=device)) for g in grads]
+    for p, g in zip(params, grads):
+        p.grad = g.clone()
+    opt = ShardedOptimizer(params, OptimizerConfig(), norm_group=GroupHandle.trivial(), device=device)
+    ints = torch.int32 if dtype == torch.float32 else torch.int16
+
+    def host(t):
+        t = t.detach().cpu()
+        return t.numpy() if dtype == torch.float32 else t.view(torch.int16).numpy().view(np.uint16)
+
+    ref_sq = sum(oracle.sqnorm(host(g)) for g in grads)
+    norm = float(opt.clip_grad_norm(1.0))
+    assert abs(norm**2 - ref_sq) <= 1e-12 * ref_sq
+    coef = 1.0 / (norm + 1e-6)  # sharded_optimizer.py:331-337, a Python double
+    assert coef < 1.0 and math.frexp(coef)[0] != 0.5
+    for p, g in zip(params, grads):
+        want = g.cpu().mul_(coef)
+        assert torch.equal(p.grad.cpu().view(ints), want.view(ints))
+
+    quiet = torch.zeros(9, dtype=dtype, device=device)
+    quiet[3] = 1e-3
+    if dtype == torch.bfloat16:
+        quiet.view(torch.int16)[5] = 0x7FA1  # a NaN with a payload the store would not keep
+    q = torch.nn.Parameter(torch.zeros(9, dtype=dtype, device=device))
+    q.grad = quiet.clone()
+    opt = ShardedOptimizer([q], OptimizerConfig(), norm_group=GroupHandle.trivial(), device=device)
+    opt.clip_grad_norm(1e9 if dtype == torch.float32 else 1.0)
+    assert torch.equal(q.grad.view(ints), quiet.view(ints))
 
 
 def test_gradients_changed_after_the_clip(device):
@@ -297,26 +346,31 @@ def test_gradients_changed_after_the_clip(device):
     p0 = torch.randn(10_000, device=device, generator=gen) * 0.02
     param = torch.nn.Parameter(p0.clone())
     param.grad = g0.clone()
-    opt = _make_optimizer([param])
+    opt = _make_optimizer([param], in_step=True)
     opt.clip_grad_norm(1.0)
     param.grad.mul_(0.5)  # changed after the clip
     with pytest.raises(ShardingError, match="materialize_pending"):
         opt.step()
 
-    param = torch.nn.Parameter(p0.clone())
-    param.grad = g0.clone()
-    opt = _make_optimizer([param])
-    norm = float(opt.clip_grad_norm(1.0))
-    opt.materialize_pending()
-    param.grad.mul_(0.5)
-    opt.step()
     # the same sequence with the clip multiplier applied by hand, then the change
     ref = torch.nn.Parameter(p0.clone())
-    ref.grad = (g0 * oracle.clip_multiplier(norm, 1.0)) * 0.5
-    ref_opt = _make_optimizer([ref])
-    ref_opt.step()
-    assert torch.equal(param.grad, ref.grad)
-    assert torch.equal(param.detach(), ref.detach())
+    ref_norm = None
+    for mode in ("materialize", "eager"):
+        param = torch.nn.Parameter(p0.clone())
+        param.grad = g0.clone()
+        opt = _make_optimizer([param], in_step=mode == "materialize")
+        norm = float(opt.clip_grad_norm(1.0))
+        if mode == "materialize":
+            opt.materialize_pending()
+        param.grad.mul_(0.5)
+        opt.step()
+        if ref_norm is None:
+            ref_norm = norm
+            ref.grad = (g0 * oracle.clip_multiplier(norm, 1.0)) * 0.5
+            _make_optimizer([ref]).step()
+        assert norm == ref_norm
+        assert torch.equal(param.grad, ref.grad), mode
+        assert torch.equal(param.detach(), ref.detach()), mode
 
 
 def test_deferred_and_fused_paths_are_bitwise_equal(device):

@@ -246,7 +246,9 @@ def test_eager_unscale_partials_feed_the_clip_norm(device, monkeypatch, dtype):
         p.grad_dtype = None
         p.grad = (torch.randn(p.numel(), device=device, generator=gen) * 1000.0).to(dtype)
     copies = [torch.nn.Parameter(p.detach().clone()) for p in params]
-    opt = ShardedOptimizer(params, OptimizerConfig(), norm_group=GroupHandle.trivial(), device=device)
+    # the clip is left to the step, so the gradients stay as the unscale wrote them
+    opt = ShardedOptimizer(params, OptimizerConfig(), norm_group=GroupHandle.trivial(), device=device,
+                           clip_in_step=True)
     scaler = GradScaler(GradScalerConfig(enabled=True, init_scale=1000.0), GroupHandle.trivial(), device)
     launched = []
     real = optim_module._launch_sqnorm
@@ -263,7 +265,8 @@ def test_eager_unscale_partials_feed_the_clip_norm(device, monkeypatch, dtype):
         c.grad = p.grad.clone()  # the unscaled values, without partials attached
     norm = opt.clip_grad_norm(1.0)
     assert launched == []  # every segment came from the scaler's partials
-    ref_opt = ShardedOptimizer(copies, OptimizerConfig(), norm_group=GroupHandle.trivial(), device=device)
+    ref_opt = ShardedOptimizer(copies, OptimizerConfig(), norm_group=GroupHandle.trivial(), device=device,
+                               clip_in_step=True)
     ref = ref_opt.clip_grad_norm(1.0)
     assert sorted(launched) == sorted(sizes)  # the copies were read
     assert float(norm) == float(ref)  # the clip multiplier is derived from the same fp64 sum

@@ -412,3 +412,30 @@ def test_pending_unscale_factors_are_applied_once_per_group(monkeypatch):
     with pytest.raises(ShardingError, match="dense"):
         grad_scaler._apply_pending_unscale([dense, strided], torch.device("cuda", 0))
     assert calls == [] and hasattr(dense, PENDING_UNSCALE_ATTR)
+
+
+def test_norm_partials_follow_the_version_counter_not_the_data():
+    """A gradient's cached norm partials are keyed by its address, dtype and autograd
+    version.  Any in-place torch op, and every kernel of this package that writes a tensor
+    (``_native.bump_versions``), moves the version and drops them; a write through
+    ``tensor.data`` bypasses the counter, so the stale partials are still returned: the
+    documented limit of the cache."""
+    from hybrid_training_amd import _native
+    from hybrid_training_amd.optim import NORM_PARTIALS_ATTR, NormPartials
+
+    g = torch.ones(8)
+    partials = torch.tensor([8.0], dtype=torch.float64)
+    setattr(g, NORM_PARTIALS_ATTR, NormPartials(g.data_ptr(), g._version, {(0, 8): partials}, g.dtype))
+    record = getattr(g, NORM_PARTIALS_ATTR)
+    assert record.lookup(g, 0, 8) is partials
+    g.data.mul_(2.0)  # no version bump: the cache cannot see it
+    assert record.lookup(g, 0, 8) is partials
+    _native.bump_versions([g])  # what a kernel writing g does
+    assert record.lookup(g, 0, 8) is None
+    h = torch.ones(8)
+    setattr(h, NORM_PARTIALS_ATTR, NormPartials(h.data_ptr(), h._version, {(0, 8): partials}, h.dtype))
+    h.mul_(2.0)
+    assert getattr(h, NORM_PARTIALS_ATTR).lookup(h, 0, 8) is None
+    with torch.inference_mode():
+        frozen = torch.ones(2)
+    _native.bump_versions([frozen])  # inference tensors have no counter: skipped, no error
