@@ -363,14 +363,19 @@ __global__ __launch_bounds__(kCopyBlock) void copy_aligned_kernel(const int64_t*
     }
 }
 
-// ---- element-wise conversions ----------------------------------------------------------
-// The dtype pairs the vector kernels do not move: float64 to or from another dtype, and
-// bf16 <-> fp16.  Each value widens exactly to double and narrows as torch's Tensor.to
-// does: to fp32 with one rounding to nearest even, then, for a 2-byte destination, to that
-// dtype (double -> fp32 -> bf16/fp16, as c10's conversions go; bf16 <-> fp16 through the
-// exact fp32 value).  A chunk is 1 KB of source, as in the vector kernels; lane l moves
-// elements l, l + 64, ... of it, so every load and store instruction of the wave covers
-// one contiguous span.
+// ---- conversions through double ---------------------------------------------------------
+// The dtype pairs the kernels above do not move: float64 to or from another dtype, float64
+// divided by the AVG divisor (the pre-divide of float64 DDP buckets), and bf16 <-> fp16.
+// Each value widens exactly to double and narrows as torch's Tensor.to does: kept for a
+// float64 destination, else to fp32 with one rounding to nearest even, then, for a 2-byte
+// destination, to that dtype (double -> fp32 -> bf16/fp16, as c10's conversions go;
+// bf16 <-> fp16 through the exact fp32 value).  DIVIDE divides the double by the divisor,
+// correctly rounded, as torch's div_ on a float64 tensor does; a power-of-two divisor runs
+// as a multiply by its exact reciprocal (kOpScale), with the same bits.  A chunk is 1 KB
+// of source, as in the kernels above.
+template <int D>
+constexpr int elem_bytes() { return D == HBT_DTYPE_F64 ? 8 : (D == HBT_DTYPE_F32 ? 4 : 2); }
+
 template <int D>
 __device__ __forceinline__ double widen_elem(const gbyte* p) {
     typedef __attribute__((address_space(1))) const double G64;
@@ -389,12 +394,82 @@ __device__ __forceinline__ void narrow_store(gbyte* p, double x) {
         store_elem<2>(p, f32_to_b16<D == HBT_DTYPE_F16>(static_cast<float>(x)));
     }
 }
-template <int D>
-constexpr int64_t elem_bytes() { return D == HBT_DTYPE_F64 ? 8 : (D == HBT_DTYPE_F32 ? 4 : 2); }
+template <int OP>
+__device__ __forceinline__ double apply_op(double x, double divisor) {
+    if constexpr (OP == HBT_COPY_OP_DIVIDE) return x / divisor;
+    if constexpr (OP == kOpScale) return x * divisor;
+    return x;
+}
 
-template <int SD, int DD>
+// NW dwords at p (4 * NW bytes, aligned to that), non-temporal when kCopyNT.
+template <int NW>
+__device__ __forceinline__ void load_words(const gbyte* p, uint32_t (&w)[NW]) {
+    if constexpr (NW == 1) {
+        typedef __attribute__((address_space(1))) const uint32_t G32;
+        if constexpr (kCopyNT) w[0] = __builtin_nontemporal_load(reinterpret_cast<G32*>(p));
+        else w[0] = *reinterpret_cast<G32*>(p);
+    } else {
+        const typename Vec<NW>::type v = ldg<NW>(p);
+#pragma unroll
+        for (int i = 0; i < NW; ++i) w[i] = v[i];
+    }
+}
+template <int NW>
+__device__ __forceinline__ void store_words(gbyte* p, const uint32_t (&w)[NW]) {
+    if constexpr (NW == 1) {
+        typedef __attribute__((address_space(1))) uint32_t G32;
+        if constexpr (kCopyNT) __builtin_nontemporal_store(w[0], reinterpret_cast<G32*>(p));
+        else *reinterpret_cast<G32*>(p) = w[0];
+    } else {
+        typename Vec<NW>::type v;
+#pragma unroll
+        for (int i = 0; i < NW; ++i) v[i] = w[i];
+        stg<NW>(p, v);
+    }
+}
+// U elements of dtype D held in dwords, to and from their double values (widening exact,
+// narrowing as narrow_store narrows).
+template <int D, int U>
+__device__ __forceinline__ void words_to_f64(const uint32_t (&w)[U * elem_bytes<D>() / 4], double (&x)[U]) {
+    if constexpr (D == HBT_DTYPE_F64) {
+#pragma unroll
+        for (int i = 0; i < U; ++i) x[i] = __hiloint2double(static_cast<int>(w[2 * i + 1]), static_cast<int>(w[2 * i]));
+    } else if constexpr (D == HBT_DTYPE_F32) {
+#pragma unroll
+        for (int i = 0; i < U; ++i) x[i] = static_cast<double>(__uint_as_float(w[i]));
+    } else {
+#pragma unroll
+        for (int i = 0; i < U / 2; ++i) {
+            x[2 * i] = static_cast<double>(b16_to_f32<D == HBT_DTYPE_F16>(w[i] & 0xFFFFu));
+            x[2 * i + 1] = static_cast<double>(b16_to_f32<D == HBT_DTYPE_F16>(w[i] >> 16));
+        }
+    }
+}
+template <int D, int U>
+__device__ __forceinline__ void f64_to_words(const double (&x)[U], uint32_t (&w)[U * elem_bytes<D>() / 4]) {
+    if constexpr (D == HBT_DTYPE_F64) {
+#pragma unroll
+        for (int i = 0; i < U; ++i) {
+            w[2 * i] = static_cast<uint32_t>(__double2loint(x[i]));
+            w[2 * i + 1] = static_cast<uint32_t>(__double2hiint(x[i]));
+        }
+    } else if constexpr (D == HBT_DTYPE_F32) {
+#pragma unroll
+        for (int i = 0; i < U; ++i) w[i] = __float_as_uint(static_cast<float>(x[i]));
+    } else {
+#pragma unroll
+        for (int i = 0; i < U / 2; ++i)
+            w[i] = f32_to_b16<D == HBT_DTYPE_F16>(static_cast<float>(x[2 * i])) |
+                   (f32_to_b16<D == HBT_DTYPE_F16>(static_cast<float>(x[2 * i + 1])) << 16);
+    }
+}
+
+// Any plan: lane l converts elements l, l + 64, ... of its chunk, so every load and store
+// instruction of the wave covers one contiguous span.
+template <int SD, int DD, int OP>
 __global__ __launch_bounds__(kCopyBlock) void convert_kernel(const int64_t* __restrict__ table, int64_t count,
-                                                             int64_t chunk_base, const int64_t* __restrict__ hints) {
+                                                             double divisor, int64_t chunk_base,
+                                                             const int64_t* __restrict__ hints) {
     constexpr int64_t SB = elem_bytes<SD>();
     constexpr int64_t DB = elem_bytes<DD>();
     constexpr int64_t kChunk = int64_t(kCopyBlock) * 16 / SB;
@@ -407,26 +482,100 @@ __global__ __launch_bounds__(kCopyBlock) void convert_kernel(const int64_t* __re
     gbyte* d = reinterpret_cast<gbyte*>(static_cast<uintptr_t>(rec[1])) + e0 * DB;
     if (s != nullptr) s += e0 * SB;
     for (int64_t i = threadIdx.x; i < len; i += kCopyBlock) {
-        narrow_store<DD>(d + i * DB, s != nullptr ? widen_elem<SD>(s + i * SB) : 0.0);
+        narrow_store<DD>(d + i * DB, s != nullptr ? apply_op<OP>(widen_elem<SD>(s + i * SB), divisor) : 0.0);
     }
 }
 
+// Aligned plans (every destination 16-byte aligned, every source aligned to its unit): a
+// lane moves units of U = 16 / max(source, destination bytes) elements, one access of
+// U * bytes on each side (16 on the wider side; 8 or 4 on the narrower one), consecutive
+// lanes on consecutive units; a 1 KB-of-source chunk is kPerLane units per lane (1 for a
+// float64 source, 2 or 4 when widening to float64), all loaded before the first store.
+// The bits are convert_kernel's.
+template <int SD, int DD, int OP>
+__global__ __launch_bounds__(kCopyBlock) void convert_aligned_kernel(const int64_t* __restrict__ table,
+                                                                     int64_t count, double divisor,
+                                                                     int64_t chunk_base,
+                                                                     const int64_t* __restrict__ hints) {
+    constexpr int SB = elem_bytes<SD>();
+    constexpr int DB = elem_bytes<DD>();
+    constexpr int U = 16 / (SB > DB ? SB : DB);
+    constexpr int SW = U * SB / 4;
+    constexpr int DW = U * DB / 4;
+    constexpr int64_t kChunk = int64_t(kCopyBlock) * 16 / SB;
+    constexpr int kPerLane = static_cast<int>(kChunk / (int64_t(kCopyBlock) * U));
+    static_assert(kChunk == int64_t(kPerLane) * kCopyBlock * U, "a chunk is whole units on every lane");
+    const int64_t chunk = chunk_base + static_cast<int64_t>(blockIdx.x);
+    const int64_t* rec = table + 4 * owning_record(table, count, chunk, hints);
+    const int64_t e0 = (chunk - rec[3]) * kChunk;
+    const int64_t n = rec[2];
+    const int64_t len = (n - e0) < kChunk ? (n - e0) : kChunk;
+    const int64_t units = len / U;
+    const gbyte* s = reinterpret_cast<const gbyte*>(static_cast<uintptr_t>(rec[0]));
+    gbyte* d = reinterpret_cast<gbyte*>(static_cast<uintptr_t>(rec[1])) + e0 * DB;
+    if (s == nullptr) {
+        uint32_t zero[DW];
+#pragma unroll
+        for (int i = 0; i < DW; ++i) zero[i] = 0u;
+#pragma unroll
+        for (int j = 0; j < kPerLane; ++j) {
+            const int64_t u = threadIdx.x + j * kCopyBlock;
+            if (u < units) store_words<DW>(d + u * U * DB, zero);
+        }
+        if (threadIdx.x < len - units * U) narrow_store<DD>(d + (units * U + threadIdx.x) * DB, 0.0);
+        return;
+    }
+    s += e0 * SB;
+    uint32_t w[kPerLane][SW];
+#pragma unroll
+    for (int j = 0; j < kPerLane; ++j) {
+        const int64_t u = threadIdx.x + j * kCopyBlock;
+        if (u < units) load_words<SW>(s + u * U * SB, w[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < kPerLane; ++j) {
+        const int64_t u = threadIdx.x + j * kCopyBlock;
+        if (u < units) {
+            double x[U];
+            words_to_f64<SD, U>(w[j], x);
+#pragma unroll
+            for (int i = 0; i < U; ++i) x[i] = apply_op<OP>(x[i], divisor);
+            uint32_t o[DW];
+            f64_to_words<DD, U>(x, o);
+            store_words<DW>(d + u * U * DB, o);
+        }
+    }
+    if (threadIdx.x < len - units * U) {
+        const int64_t e = units * U + threadIdx.x;
+        narrow_store<DD>(d + e * DB, apply_op<OP>(widen_elem<SD>(s + e * SB), divisor));
+    }
+}
+
+template <int OP>
 int32_t launch_convert(int32_t src_dtype, int32_t dst_dtype, const int64_t* table, int64_t count, int64_t chunks,
-                       const int64_t* hints, hipStream_t st) {
+                       double divisor, bool aligned, const int64_t* hints, hipStream_t st) {
     return launch_sliced("hbt_copy_intervals", chunks, kCopyBlock, [&](int64_t first, dim3 grid) {
-#define HBT_CVT(SD, DD) convert_kernel<SD, DD><<<grid, kCopyBlock, 0, st>>>(table, count, first, hints)
-#define HBT_CVT_TO(SD)                                                     \
-    do {                                                                   \
-        if (dst_dtype == HBT_DTYPE_F64) HBT_CVT(SD, HBT_DTYPE_F64);        \
-        else if (dst_dtype == HBT_DTYPE_F32) HBT_CVT(SD, HBT_DTYPE_F32);   \
-        else if (dst_dtype == HBT_DTYPE_BF16) HBT_CVT(SD, HBT_DTYPE_BF16); \
-        else HBT_CVT(SD, HBT_DTYPE_F16);                                   \
+#define HBT_CVT(SD, DD)                                                                                        \
+    do {                                                                                                       \
+        if (aligned) convert_aligned_kernel<SD, DD, OP><<<grid, kCopyBlock, 0, st>>>(table, count, divisor, first, hints); \
+        else convert_kernel<SD, DD, OP><<<grid, kCopyBlock, 0, st>>>(table, count, divisor, first, hints);    \
     } while (0)
-        if (src_dtype == HBT_DTYPE_F64) HBT_CVT_TO(HBT_DTYPE_F64);
-        else if (src_dtype == HBT_DTYPE_F32) HBT_CVT_TO(HBT_DTYPE_F32);
-        else if (src_dtype == HBT_DTYPE_BF16) HBT_CVT_TO(HBT_DTYPE_BF16);
-        else HBT_CVT_TO(HBT_DTYPE_F16);
+        if constexpr (OP != HBT_COPY_OP_COPY) {
+            HBT_CVT(HBT_DTYPE_F64, HBT_DTYPE_F64);  // the only division through double
+        } else {
+#define HBT_CVT_TO(SD)                                                                                   \
+    do {                                                                                                 \
+        if (dst_dtype == HBT_DTYPE_F64) HBT_CVT(SD, HBT_DTYPE_F64);                                      \
+        else if (dst_dtype == HBT_DTYPE_F32) HBT_CVT(SD, HBT_DTYPE_F32);                                 \
+        else if (dst_dtype == HBT_DTYPE_BF16) HBT_CVT(SD, HBT_DTYPE_BF16);                               \
+        else HBT_CVT(SD, HBT_DTYPE_F16);                                                                 \
+    } while (0)
+            if (src_dtype == HBT_DTYPE_F64) HBT_CVT_TO(HBT_DTYPE_F64);
+            else if (src_dtype == HBT_DTYPE_F32) HBT_CVT_TO(HBT_DTYPE_F32);
+            else if (src_dtype == HBT_DTYPE_BF16) HBT_CVT_TO(HBT_DTYPE_BF16);
+            else HBT_CVT_TO(HBT_DTYPE_F16);
 #undef HBT_CVT_TO
+        }
 #undef HBT_CVT
     });
 }
@@ -478,8 +627,8 @@ int64_t hbt_copy_chunk_elems(int32_t src_dtype, int32_t dst_dtype) {
     const int ssz = dtype_size(src_dtype);
     const int dsz = dtype_size(dst_dtype);
     if (ssz == 0 || dsz == 0) return -1;
-    if (ssz == 8 && dsz == 8) return -1;  // same-dtype 8-byte data travels as F32 dword pairs
-    if (ssz == 2 && dsz == 4) return chunk_elems<2, 4>();  // 2 KB of source (chunk_elems)
+    // F64 -> F64: the chunk of the DIVIDE op (a same-dtype COPY moves F32 dword pairs).
+    if (ssz == 2 && dsz == 4) return chunk_elems<2, 4>();  // 2 KB of source
     return int64_t(kCopyBlock) * 16 / ssz;                  // 1 KB of source
 }
 
@@ -506,6 +655,13 @@ int32_t hbt_copy_intervals(const int64_t* table, int64_t count, int64_t total_ch
         return HBT_ERR_INVALID_ARGUMENT;
     }
     hipStream_t s = as_stream(stream);
+    if (op == HBT_COPY_OP_DIVIDE && src_dtype == HBT_DTYPE_F64 && dst_dtype == HBT_DTYPE_F64) {
+        const float recip = exact_reciprocal(divisor);
+        if (recip != 0.0f)
+            return launch_convert<kOpScale>(src_dtype, dst_dtype, table, count, total_chunks, recip, aligned, hints, s);
+        return launch_convert<HBT_COPY_OP_DIVIDE>(src_dtype, dst_dtype, table, count, total_chunks, divisor, aligned,
+                                                  hints, s);
+    }
     if (op == HBT_COPY_OP_COPY && src_dtype == dst_dtype) {
         // Bit copy; fp64 moves as pairs of dwords (the host doubles its numels).
         if (ssz == 2) return launch_copy<2, 2, HBT_COPY_OP_COPY>(table, count, total_chunks, divisor, aligned, hints, s);
@@ -518,11 +674,12 @@ int32_t hbt_copy_intervals(const int64_t* table, int64_t count, int64_t total_ch
                           (src_dtype == HBT_DTYPE_F16 && dst_dtype == HBT_DTYPE_BF16);
     if (wide || mixed_16) {
         if (op != HBT_COPY_OP_COPY) {
-            set_error("hbt_copy_intervals: division moves F32, BF16 and F16 data within one dtype or "
+            set_error("hbt_copy_intervals: division moves data within one dtype (F64, F32, BF16 or F16) or "
                       "between F32 and a 2-byte dtype (got %d -> %d)", src_dtype, dst_dtype);
             return HBT_ERR_UNSUPPORTED;
         }
-        return launch_convert(src_dtype, dst_dtype, table, count, total_chunks, hints, s);
+        return launch_convert<HBT_COPY_OP_COPY>(src_dtype, dst_dtype, table, count, total_chunks, 1.0, aligned,
+                                                hints, s);
     }
     if (src_dtype == HBT_DTYPE_F16 || dst_dtype == HBT_DTYPE_F16) {
         return launch_arith<true>(ssz, dsz, op, divisor, table, count, total_chunks, aligned, hints, s);

@@ -104,6 +104,42 @@ __device__ __forceinline__ void store_one(void* base, int64_t e, float x) {
     }
 }
 
+// K consecutive doubles from element e (K even, e a multiple of 2, base 16-byte aligned):
+// K / 2 non-temporal 16-byte loads.
+typedef double f64x2 __attribute__((ext_vector_type(2)));
+template <int K>
+__device__ __forceinline__ void load_f64(const void* base, int64_t e, double (&x)[K]) {
+    static_assert(K % 2 == 0, "double vectors are two elements");
+    const f64x2* p = reinterpret_cast<const f64x2*>(static_cast<const double*>(base) + e);
+#pragma unroll
+    for (int i = 0; i < K / 2; ++i) {
+        const f64x2 w = __builtin_nontemporal_load(p + i);
+        x[2 * i] = w.x;
+        x[2 * i + 1] = w.y;
+    }
+}
+template <int K>
+__device__ __forceinline__ void store_f64(void* base, int64_t e, const double (&x)[K]) {
+    static_assert(K % 2 == 0, "double vectors are two elements");
+    f64x2* p = reinterpret_cast<f64x2*>(static_cast<double*>(base) + e);
+#pragma unroll
+    for (int i = 0; i < K / 2; ++i) __builtin_nontemporal_store(f64x2{x[2 * i], x[2 * i + 1]}, p + i);
+}
+// Four consecutive SB-byte elements (float64, float32, or bf16 / fp16 when SH) from
+// element e, widened exactly to double (Tensor.to(float64)), with 16-byte loads (8-byte
+// for 2-byte elements); base + e * SB must be aligned to 4 * SB bytes (16 for doubles).
+template <int SB, bool SH>
+__device__ __forceinline__ void load4_as_f64(const void* base, int64_t e, double (&x)[4]) {
+    if constexpr (SB == 8) {
+        load_f64<4>(base, e, x);
+    } else {
+        float f[4];
+        load_vec<dtype_of<SB, SH>(), 4>(base, e, f);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) x[c] = static_cast<double>(f[c]);
+    }
+}
+
 // Wait for every outstanding vector-memory load of this wave (s_waitcnt vmcnt(0)).
 // Issuing a lane's operand streams one after the other, rather than all at once, keeps
 // the HBM request mix per wave simpler and measured ~2% faster.
@@ -425,7 +461,12 @@ template <int GD>
 constexpr int64_t norm_tile() { return int64_t(kNormBlock) * norm_vec<GD>(); }
 template <int GD>
 constexpr int64_t norm_chunk() { return norm_tile<GD>() * kNormTilesPerChunk; }
-inline int64_t norm_chunk_of(int32_t dtype) { return dtype == F32 ? norm_chunk<F32>() : norm_chunk<BF16>(); }
+// Elements per norm partial: 32768 fp32, 65536 bf16 / fp16, 16384 float64 gradients
+// (norm_chunk<F64> is not instantiated: the float64 pass has its own kernel).
+inline int64_t norm_chunk_of(int32_t dtype) {
+    if (dtype == HBT_DTYPE_F64) return int64_t(kNormBlock) * 2 * kNormTilesPerChunk;
+    return dtype == F32 ? norm_chunk<F32>() : norm_chunk<BF16>();
+}
 
 struct NormTable {
     const void* g[kMaxT];
@@ -698,31 +739,91 @@ __global__ __launch_bounds__(kShareBlock) void local_share_tiles_kernel(
 }
 
 // Reduce dtype float64: each rank's element widens exactly to double (IB = 8 reads a
-// float64 no_sync accumulator), the divide and the rank-order sum run in double, both
-// correctly rounded as torch's float64 div and add are, and the sum narrows to the
-// master dtype OD as Tensor.to does (to fp32 rounding to nearest even, then, for a
-// 2-byte OD, to OD).  Lane l owns elements 4l .. 4l + 3 of its tile.  That is the fp32
-// kernel's order on full vector tiles; on a ragged tile the fp32 kernel walks elements
-// by lane stride instead, so tile sums there can round differently (the outputs are
-// the same).
-template <int IB, bool IH, int OD>
+// float64 no_sync accumulator or float64 gradients), the divide and the rank-order sum run
+// in double, both correctly rounded as torch's float64 div and add are (a power-of-two
+// divisor multiplies by its exact reciprocal, kRecip: the same bits), and the sum narrows
+// to the master dtype OD as Tensor.to does: kept for a float64 master, else to fp32
+// rounding to nearest even and then, for a 2-byte OD, to OD.  Lane l owns elements
+// 4l .. 4l + 3 of its 256-element tile on every path, so a tile's sum of squares has one
+// order.  On whole tiles each rank's four elements are one vector load (two for doubles),
+// the ranks issued two at a time ahead of their use, and the output is one vector store.
+template <int OD>
+__device__ __forceinline__ double narrow_from_f64(double s) {
+    if constexpr (OD == HBT_DTYPE_F64) return s;
+    return static_cast<double>(round_to<OD>(static_cast<float>(s)));
+}
+template <int OD>
+__device__ __forceinline__ void store4_from_f64(void* base, int64_t e, const double (&o)[4]) {
+    if constexpr (OD == HBT_DTYPE_F64) {
+        store_f64<4>(base, e, o);
+    } else {
+        const float f[4] = {static_cast<float>(o[0]), static_cast<float>(o[1]), static_cast<float>(o[2]),
+                            static_cast<float>(o[3])};  // exact: o already holds OD values
+        store_vec<OD, 4>(base, e, f);
+    }
+}
+template <int OD>
+__device__ __forceinline__ void store1_from_f64(void* base, int64_t e, double o) {
+    if constexpr (OD == HBT_DTYPE_F64) static_cast<double*>(base)[e] = o;
+    else store_one<OD>(base, e, static_cast<float>(o));
+}
+template <bool kRecip>
+__device__ __forceinline__ double share_div64(double x, double divisor, double recip) {
+    if constexpr (kRecip) return x * recip;
+    return x / divisor;
+}
+
+template <int IB, bool IH, int OD, bool kRecip>
 __global__ __launch_bounds__(kShareBlock) void local_share_f64_tiles_kernel(
     ShareRanks ranks, int32_t group_size, int64_t offset, int64_t shard_numel, int64_t valid_numel,
-    double divisor, void* __restrict__ out, double* __restrict__ tile_sums, int64_t block_base) {
+    double divisor, double recip, int32_t vec_ok, void* __restrict__ out, double* __restrict__ tile_sums,
+    int64_t block_base) {
     const int64_t tile = block_base + blockIdx.x;
     const int64_t first = tile * kShareTile + int64_t(threadIdx.x) * 4;
     double acc = 0.0;
-    for (int j = 0; j < 4; ++j) {
-        const int64_t e = first + j;
-        if (e >= shard_numel) break;
-        float v = 0.0f;
-        if (e < valid_numel) {
-            double s = widen_f64<IB, IH>(ranks.g[0], offset + e) / divisor;
-            for (int32_t q = 1; q < group_size; ++q) s = s + widen_f64<IB, IH>(ranks.g[q], offset + e) / divisor;
-            v = round_to<OD>(static_cast<float>(s));
+    if (vec_ok && tile * kShareTile + kShareTile <= valid_numel) {
+        double s[4], x[4], y[4];
+        load4_as_f64<IB, IH>(ranks.g[0] + offset * IB, first, x);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) s[c] = share_div64<kRecip>(x[c], divisor, recip);
+        int32_t q = 1;
+        for (; q + 1 < group_size; q += 2) {
+            load4_as_f64<IB, IH>(ranks.g[q] + offset * IB, first, x);
+            load4_as_f64<IB, IH>(ranks.g[q + 1] + offset * IB, first, y);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                s[c] = s[c] + share_div64<kRecip>(x[c], divisor, recip);
+                s[c] = s[c] + share_div64<kRecip>(y[c], divisor, recip);
+            }
         }
-        store_one<OD>(out, e, v);
-        acc += sq(v);
+        if (q < group_size) {
+            load4_as_f64<IB, IH>(ranks.g[q] + offset * IB, first, x);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) s[c] = s[c] + share_div64<kRecip>(x[c], divisor, recip);
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            s[c] = narrow_from_f64<OD>(s[c]);
+            acc += s[c] * s[c];
+        }
+        store4_from_f64<OD>(out, first, s);
+    } else if (vec_ok && tile * kShareTile >= valid_numel && tile * kShareTile + kShareTile <= shard_numel) {
+        const double zero[4] = {0.0, 0.0, 0.0, 0.0};
+        store4_from_f64<OD>(out, first, zero);
+    } else {
+        for (int j = 0; j < 4; ++j) {
+            const int64_t e = first + j;
+            if (e >= shard_numel) break;
+            double v = 0.0;
+            if (e < valid_numel) {
+                double s = share_div64<kRecip>(widen_f64<IB, IH>(ranks.g[0], offset + e), divisor, recip);
+                for (int32_t q = 1; q < group_size; ++q)
+                    s = s + share_div64<kRecip>(widen_f64<IB, IH>(ranks.g[q], offset + e), divisor, recip);
+                v = narrow_from_f64<OD>(s);
+            }
+            store1_from_f64<OD>(out, e, v);
+            acc += v * v;
+        }
     }
     if (tile_sums == nullptr) return;
     acc = wave_sum(acc);
@@ -755,7 +856,8 @@ constexpr int kFinalBlock = 1024;
 
 __global__ __launch_bounds__(kFinalBlock) void norm_finalize_kernel(
     const double* __restrict__ partials, int64_t count, double max_norm, double* __restrict__ sum_out,
-    double* __restrict__ norm_out, float* __restrict__ grad_mul_out, int32_t* __restrict__ nonfinite_out) {
+    double* __restrict__ norm_out, float* __restrict__ grad_mul_out, double* __restrict__ grad_mul64_out,
+    int32_t* __restrict__ nonfinite_out) {
     // Four independent accumulators per thread keep four loads in flight; they are
     // combined in a fixed order, so the sum stays reproducible.
     double a0 = 0.0, a1 = 0.0, a2 = 0.0, a3 = 0.0;
@@ -774,14 +876,16 @@ __global__ __launch_bounds__(kFinalBlock) void norm_finalize_kernel(
     const double norm = sqrt(clamped);
     if (sum_out != nullptr) sum_out[0] = total;
     if (norm_out != nullptr) norm_out[0] = norm;
-    if (grad_mul_out != nullptr) {
-        float mul = 1.0f;
-        if (max_norm > 0.0) {
-            const double coef = max_norm / (norm + 1e-6);
-            if (coef < 1.0) mul = static_cast<float>(coef);
-        }
-        grad_mul_out[0] = mul;
+    // The reference multiplies by the Python-double coefficient only when it is below 1:
+    // fp32, bf16 and fp16 gradients take it as torch passes it to their kernels, rounded
+    // to fp32; float64 gradients take the double itself.
+    double mul = 1.0;
+    if (max_norm > 0.0) {
+        const double coef = max_norm / (norm + 1e-6);
+        if (coef < 1.0) mul = coef;
     }
+    if (grad_mul_out != nullptr) grad_mul_out[0] = static_cast<float>(mul);
+    if (grad_mul64_out != nullptr) grad_mul64_out[0] = mul;
     if (nonfinite_out != nullptr) nonfinite_out[0] = isfinite(total) ? 0 : 1;
 }
 
@@ -844,6 +948,282 @@ __global__ __launch_bounds__(64) void scale_kernel(ScaleTable tab, float unscale
     for (int64_t i = base + threadIdx.x; i < end; i += kScaleBlock) store_one<D>(X, i, scale_one<D>(load_one<D>(X, i), unscale, mul));
 }
 
+// ---- float64 parameters ---------------------------------------------------------------
+// With mixed precision off the reference's masters, gradients and optimizer state have the
+// parameters' own dtype (parallel/fsdp.py:379-393), float64 included, and torch's optimizers
+// step float64 tensors with every Python scalar used as the double it is: nothing is
+// rounded to fp32.  These kernels run torch's per-element op sequences in double with
+// double scalars, in the shapes of their fp32 counterparts: 32-lane workgroups, one
+// stream at a time, 16-byte non-temporal vectors of two doubles, 1 KB per stream per
+// workgroup (512 B with the gradient write-back).
+constexpr int kF64Vec = 2;
+template <bool kWriteBack>
+constexpr int64_t adam_f64_tile() { return int64_t(kAdamBlock) * kF64Vec * adam_unroll<kWriteBack>(); }
+
+struct AdamScalarsF64 {
+    double unscale;
+    double decay;
+    double lerp_w;
+    double lerp_w_minus_1;
+    double beta2;
+    double one_minus_beta2;
+    double bc2_sqrt;
+    double eps;
+    double neg_step;
+};
+
+// The reference's in-place multiplies on a float64 gradient: the unscale (skipped at 1)
+// and the clip, each one rounded double product.
+template <bool kUnscale>
+__device__ __forceinline__ double scaled_grad64(double g, double unscale, double gmul) {
+    if constexpr (kUnscale) g = g * unscale;
+    return g * gmul;
+}
+
+// torch's _single_tensor_adam on float64 tensors, given the scaled gradient: the fp32
+// sequence of adamw_update with every operation in double.
+template <bool kLerpSmall>
+__device__ __forceinline__ void adamw_update_f64(double& p, double g, double& m, double& v, const AdamScalarsF64& s) {
+    p = p * s.decay;
+    const double diff = g - m;
+    m = kLerpSmall ? __builtin_fma(s.lerp_w, diff, m) : __builtin_fma(s.lerp_w_minus_1, diff, g);
+    v = v * s.beta2;
+    v = __builtin_fma(s.one_minus_beta2 * g, g, v);
+    const double denom = __builtin_sqrt(v) / s.bc2_sqrt + s.eps;
+    p = p + (s.neg_step * m) / denom;
+}
+
+template <bool kLerpSmall, bool kUnscale, bool kWriteBack>
+__global__ __launch_bounds__(kAdamBlock) void adamw_f64_kernel(AdamTable tab, AdamScalarsF64 s,
+                                                               const double* __restrict__ grad_mul,
+                                                               int64_t block_base) {
+    constexpr int K = kF64Vec;
+    constexpr int kUnroll = adam_unroll<kWriteBack>();
+    constexpr int64_t kTile = adam_f64_tile<kWriteBack>();
+    const int64_t block = block_base + blockIdx.x;
+    const int t = owning_tensor(tab.first_block, tab.count, block);
+    const int64_t base = (block - tab.first_block[t]) * kTile;
+    const int64_t n = tab.n[t];
+    const double gmul = grad_mul != nullptr ? *grad_mul : 1.0;
+    const bool write_g = kWriteBack && (kUnscale || gmul != 1.0);
+    void* P = tab.p[t];
+    void* G = tab.g[t];
+    void* M = tab.m[t];
+    void* V = tab.v[t];
+    if (tab.vec_ok[t] && base + kTile <= n) {
+        double pv[kUnroll][K], gv[kUnroll][K], mv[kUnroll][K], vv[kUnroll][K];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            const int64_t e = base + (int64_t(u) * kAdamBlock + threadIdx.x) * K;
+            load_f64<K>(G, e, gv[u]);
+            wait_vmem();
+            if (write_g) {
+#pragma unroll
+                for (int c = 0; c < K; ++c) gv[u][c] = scaled_grad64<kUnscale>(gv[u][c], s.unscale, gmul);
+                store_f64<K>(G, e, gv[u]);
+            }
+            load_f64<K>(M, e, mv[u]);
+            wait_vmem();
+            load_f64<K>(V, e, vv[u]);
+            wait_vmem();
+            load_f64<K>(P, e, pv[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+#pragma unroll
+            for (int c = 0; c < K; ++c) {
+                if (!write_g) gv[u][c] = scaled_grad64<kUnscale>(gv[u][c], s.unscale, gmul);
+                adamw_update_f64<kLerpSmall>(pv[u][c], gv[u][c], mv[u][c], vv[u][c], s);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            const int64_t e = base + (int64_t(u) * kAdamBlock + threadIdx.x) * K;
+            store_f64<K>(M, e, mv[u]);
+            store_f64<K>(V, e, vv[u]);
+            store_f64<K>(P, e, pv[u]);
+        }
+    } else {
+        const int64_t end = base + kTile < n ? base + kTile : n;
+        double* p = static_cast<double*>(P);
+        double* g = static_cast<double*>(G);
+        double* m = static_cast<double*>(M);
+        double* v = static_cast<double*>(V);
+        for (int64_t e = base + threadIdx.x; e < end; e += kAdamBlock) {
+            double pe = p[e], me = m[e], ve = v[e];
+            const double ge = scaled_grad64<kUnscale>(g[e], s.unscale, gmul);
+            adamw_update_f64<kLerpSmall>(pe, ge, me, ve, s);
+            p[e] = pe;
+            m[e] = me;
+            v[e] = ve;
+            if (write_g) g[e] = ge;
+        }
+    }
+}
+
+struct SgdScalarsF64 {
+    double unscale;
+    double weight_decay;
+    double momentum;
+    double one_minus_dampening;
+    double neg_lr;
+    int32_t apply_weight_decay;
+    int32_t nesterov;
+};
+
+// torch's _single_tensor_sgd on float64 tensors: each add(.., alpha=) one fused
+// multiply-add with the unrounded double alpha, mul_ one rounded product.
+template <int kMode>
+__device__ __forceinline__ void sgd_update_f64(double& p, double g, double& buf, const SgdScalarsF64& s) {
+    if (s.apply_weight_decay) g = __builtin_fma(p, s.weight_decay, g);
+    if constexpr (kMode == kSgdFirst) {
+        buf = g;
+    } else if constexpr (kMode == kSgdMomentum) {
+        buf = buf * s.momentum;
+        buf = __builtin_fma(g, s.one_minus_dampening, buf);
+    }
+    if constexpr (kMode != kSgdPlain) g = s.nesterov ? __builtin_fma(buf, s.momentum, g) : buf;
+    p = __builtin_fma(g, s.neg_lr, p);
+}
+
+template <bool kUnscale, int kMode, bool kWriteBack>
+__global__ __launch_bounds__(kAdamBlock) void sgd_f64_kernel(SgdTable tab, SgdScalarsF64 s,
+                                                             const double* __restrict__ grad_mul,
+                                                             int64_t block_base) {
+    constexpr int K = kF64Vec;
+    constexpr int kUnroll = adam_unroll<kWriteBack>();
+    constexpr int64_t kTile = adam_f64_tile<kWriteBack>();
+    const int64_t block = block_base + blockIdx.x;
+    const int t = owning_tensor(tab.first_block, tab.count, block);
+    const int64_t base = (block - tab.first_block[t]) * kTile;
+    const int64_t n = tab.n[t];
+    const double gmul = grad_mul != nullptr ? *grad_mul : 1.0;
+    const bool write_g = kWriteBack && (kUnscale || gmul != 1.0);
+    void* P = tab.p[t];
+    void* G = tab.g[t];
+    void* B = tab.buf[t];
+    if (tab.vec_ok[t] && base + kTile <= n) {
+        double pv[kUnroll][K], gv[kUnroll][K], bv[kUnroll][K];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            const int64_t e = base + (int64_t(u) * kAdamBlock + threadIdx.x) * K;
+            load_f64<K>(G, e, gv[u]);
+            wait_vmem();
+            if (write_g) {
+#pragma unroll
+                for (int c = 0; c < K; ++c) gv[u][c] = scaled_grad64<kUnscale>(gv[u][c], s.unscale, gmul);
+                store_f64<K>(G, e, gv[u]);
+            }
+            if constexpr (kMode == kSgdMomentum) {
+                load_f64<K>(B, e, bv[u]);
+                wait_vmem();
+            }
+            load_f64<K>(P, e, pv[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+#pragma unroll
+            for (int c = 0; c < K; ++c) {
+                if (!write_g) gv[u][c] = scaled_grad64<kUnscale>(gv[u][c], s.unscale, gmul);
+                double b = kMode == kSgdMomentum ? bv[u][c] : 0.0;
+                sgd_update_f64<kMode>(pv[u][c], gv[u][c], b, s);
+                bv[u][c] = b;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            const int64_t e = base + (int64_t(u) * kAdamBlock + threadIdx.x) * K;
+            if constexpr (kMode != kSgdPlain) store_f64<K>(B, e, bv[u]);
+            store_f64<K>(P, e, pv[u]);
+        }
+    } else {
+        const int64_t end = base + kTile < n ? base + kTile : n;
+        double* p = static_cast<double*>(P);
+        double* g = static_cast<double*>(G);
+        double* bufp = static_cast<double*>(B);
+        for (int64_t e = base + threadIdx.x; e < end; e += kAdamBlock) {
+            double pe = p[e], b = kMode == kSgdMomentum ? bufp[e] : 0.0;
+            const double ge = scaled_grad64<kUnscale>(g[e], s.unscale, gmul);
+            sgd_update_f64<kMode>(pe, ge, b, s);
+            p[e] = pe;
+            if constexpr (kMode != kSgdPlain) bufp[e] = b;
+            if (write_g) g[e] = ge;
+        }
+    }
+}
+
+// In-place x = (x * unscale) * (*grad_mul) on float64 tensors, each product rounded in
+// double; nothing when both factors are 1.  Half-wave workgroups, two 16-byte vectors
+// per lane (128 elements per workgroup, 1 KB).
+constexpr int64_t kScaleF64Tile = int64_t(32) * kScaleUnroll * kF64Vec;
+__global__ __launch_bounds__(32) void scale_f64_kernel(ScaleTable tab, double unscale,
+                                                       const double* __restrict__ grad_mul, int64_t block_base) {
+    const double mul = grad_mul != nullptr ? *grad_mul : 1.0;
+    if (unscale == 1.0 && mul == 1.0) return;
+    const int64_t block = block_base + blockIdx.x;
+    const int t = owning_tensor(tab.first_block, tab.count, block);
+    const int64_t base = (block - tab.first_block[t]) * kScaleF64Tile;
+    const int64_t n = tab.n[t];
+    void* X = tab.x[t];
+    if (tab.vec_ok[t] && base + kScaleF64Tile <= n) {
+        double v[kScaleUnroll][kF64Vec];
+#pragma unroll
+        for (int u = 0; u < kScaleUnroll; ++u) load_f64<kF64Vec>(X, base + (int64_t(u) * 32 + threadIdx.x) * kF64Vec, v[u]);
+#pragma unroll
+        for (int u = 0; u < kScaleUnroll; ++u) {
+#pragma unroll
+            for (int c = 0; c < kF64Vec; ++c) v[u][c] = (v[u][c] * unscale) * mul;
+            store_f64<kF64Vec>(X, base + (int64_t(u) * 32 + threadIdx.x) * kF64Vec, v[u]);
+        }
+        return;
+    }
+    const int64_t end = base + kScaleF64Tile < n ? base + kScaleF64Tile : n;
+    double* x = static_cast<double*>(X);
+    for (int64_t i = base + threadIdx.x; i < end; i += 32) x[i] = (x[i] * unscale) * mul;
+}
+
+// Squared norm of float64 gradients: sqnorm_kernel's 1024-thread workgroups, a tile one
+// 16-byte vector (two doubles) per lane, eight tiles (16384 elements) per chunk.  Each
+// square is one rounded double product, as g.to(float64).pow(2) gives; a thread adds its
+// squares in element order and the workgroup combines them with block_sum.  The loads of
+// four tiles are issued before the first of them is summed.
+constexpr int64_t kNormF64Tile = int64_t(kNormBlock) * kF64Vec;
+constexpr int64_t kNormF64Chunk = kNormF64Tile * kNormTilesPerChunk;
+__global__ __launch_bounds__(kNormBlock) void sqnorm_f64_kernel(NormTable tab, double* __restrict__ partials,
+                                                                int64_t block_base) {
+    const int64_t chunk = block_base + blockIdx.x;
+    const int t = owning_tensor(tab.first_chunk, tab.count, chunk);
+    const int64_t start = (chunk - tab.first_chunk[t]) * kNormF64Chunk;
+    const int64_t n = tab.n[t];
+    const double* g = static_cast<const double*>(tab.g[t]);
+    double acc = 0.0;
+    if (tab.vec_ok[t] && start + kNormF64Chunk <= n) {
+        constexpr int kBatch = 4;
+#pragma unroll
+        for (int k0 = 0; k0 < kNormTilesPerChunk; k0 += kBatch) {
+            double x[kBatch][kF64Vec];
+#pragma unroll
+            for (int k = 0; k < kBatch; ++k)
+                load_f64<kF64Vec>(g, start + int64_t(k0 + k) * kNormF64Tile + int64_t(threadIdx.x) * kF64Vec, x[k]);
+#pragma unroll
+            for (int k = 0; k < kBatch; ++k) {
+#pragma unroll
+                for (int c = 0; c < kF64Vec; ++c) acc += x[k][c] * x[k][c];
+            }
+        }
+    } else {
+        for (int k = 0; k < kNormTilesPerChunk; ++k) {
+            const int64_t tile = start + int64_t(k) * kNormF64Tile;
+            for (int c = 0; c < kF64Vec; ++c) {
+                const int64_t e = tile + int64_t(threadIdx.x) * kF64Vec + c;
+                if (e < n) acc += g[e] * g[e];
+            }
+        }
+    }
+    const double block_total = block_sum<kNormBlock>(acc);
+    if (threadIdx.x == 0) partials[chunk] = block_total * tab.w[t];
+}
+
 // ---- no_sync gradient accumulation ----------------------------------------------------
 // acc = R(acc + R(grad)), R rounding to the accumulator's dtype (the reduce dtype): the
 // gradient's cast to that dtype (Tensor.to) and one addition computed in fp32 and
@@ -901,7 +1281,9 @@ __global__ __launch_bounds__(kAccumBlock) void accumulate_kernel(AccumTable tab,
 }
 
 // Accumulator float64: the gradient widens exactly (Tensor.to) and each add runs in
-// double, as add_ on float64 tensors does; kAssign writes the widened gradient.
+// double, as add_ on float64 tensors does; kAssign writes the widened gradient.  The
+// layout of accumulate_kernel: each lane owns two runs of four elements, each one vector
+// load of the gradient and (without kAssign) two 16-byte loads of the accumulator.
 template <int SB, bool SH, bool kAssign>
 __global__ __launch_bounds__(kAccumBlock) void accumulate_f64_kernel(AccumTable tab, int64_t block_base) {
     const int64_t block = block_base + blockIdx.x;
@@ -910,6 +1292,24 @@ __global__ __launch_bounds__(kAccumBlock) void accumulate_f64_kernel(AccumTable 
     const int64_t n = tab.n[t];
     double* __restrict__ acc = static_cast<double*>(tab.acc[t]);
     const unsigned char* __restrict__ grad = static_cast<const unsigned char*>(tab.grad[t]);
+    if (tab.vec_ok[t] && base + kAccumTile <= n) {
+        double a[2][4], g[2][4];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int64_t e = base + (int64_t(u) * kAccumBlock + threadIdx.x) * 4;
+            load4_as_f64<SB, SH>(grad, e, g[u]);
+            if constexpr (!kAssign) load_f64<4>(acc, e, a[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            if constexpr (!kAssign) {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) g[u][c] = a[u][c] + g[u][c];
+            }
+            store_f64<4>(acc, base + (int64_t(u) * kAccumBlock + threadIdx.x) * 4, g[u]);
+        }
+        return;
+    }
     const int64_t end = base + kAccumTile < n ? base + kAccumTile : n;
     for (int64_t i = base + threadIdx.x; i < end; i += kAccumBlock) {
         const double g = widen_f64<SB, SH>(grad, i);
@@ -954,8 +1354,8 @@ int32_t build_norm_table(const char* who, const void* const* grads, const int64_
         set_error("%s: count must lie in [0, %d], got %d", who, kMaxT, count);
         return HBT_ERR_INVALID_ARGUMENT;
     }
-    if (grad_dtype != F32 && grad_dtype != BF16 && grad_dtype != F16) {
-        set_error("%s: gradient dtype %d is not F32, BF16 or F16", who, grad_dtype);
+    if (grad_dtype != F32 && grad_dtype != BF16 && grad_dtype != F16 && grad_dtype != HBT_DTYPE_F64) {
+        set_error("%s: gradient dtype %d is not F32, BF16, F16 or F64", who, grad_dtype);
         return HBT_ERR_INVALID_ARGUMENT;
     }
     if (count > 0 && (grads == nullptr || numels == nullptr || weights == nullptr)) {
@@ -988,6 +1388,12 @@ int32_t build_norm_table(const char* who, const void* const* grads, const int64_
 int32_t launch_sqnorm(const char* who, const NormTable& tab, int64_t chunks, int32_t grad_dtype, float unscale,
                       double* partials, hipStream_t st, bool store = false) {
     const bool scaled = unscale != 1.0f;
+    if (grad_dtype == HBT_DTYPE_F64) {
+        // The callers refuse a float64 unscale or store: the multiply belongs in double.
+        return launch_sliced(who, chunks, kNormBlock, [&](int64_t first, dim3 grid) {
+            sqnorm_f64_kernel<<<grid, kNormBlock, 0, st>>>(tab, partials, first);
+        });
+    }
     return launch_sliced(who, chunks, kNormBlock, [&](int64_t first, dim3 grid) {
 #define HBT_NORM(GD)                                                                                           \
     do {                                                                                                       \
@@ -1055,8 +1461,9 @@ int32_t local_share(const char* who, const void* const* rank_grads, int32_t grou
         set_error("%s: reduce dtype %d is not F32, BF16, F16 or F64", who, reduce_dtype);
         return HBT_ERR_INVALID_ARGUMENT;
     }
-    if (out_dtype != F32 && out_dtype != BF16 && out_dtype != F16) {
-        set_error("%s: output (master) dtype %d is not F32, BF16 or F16", who, out_dtype);
+    if (out_dtype != F32 && out_dtype != BF16 && out_dtype != F16 && !(f64 && out_dtype == HBT_DTYPE_F64)) {
+        set_error("%s: output (master) dtype %d is not F32, BF16 or F16 (or F64 with reduce dtype F64)", who,
+                  out_dtype);
         return HBT_ERR_INVALID_ARGUMENT;
     }
     const bool with_acc = accumulators != nullptr;
@@ -1129,14 +1536,21 @@ int32_t local_share(const char* who, const void* const* rank_grads, int32_t grou
         else if (reduce_dtype == BF16) HBT_TILES_OD(ID, R, BF16);        \
         else HBT_TILES_OD(ID, R, F16);                                   \
     } while (0)
-#define HBT_TILES64(IB, IH, OD)                                                                          \
-    local_share_f64_tiles_kernel<IB, IH, OD><<<grid, kShareBlock, 0, st>>>(                                \
-        ranks, group_size, offset, shard_numel, valid_numel, static_cast<double>(divisor), out, tile_scratch, first)
-#define HBT_TILES64_OD(IB, IH)                                 \
+#define HBT_TILES64R(IB, IH, OD, R)                                                                       \
+    local_share_f64_tiles_kernel<IB, IH, OD, R><<<grid, kShareBlock, 0, st>>>(                             \
+        ranks, group_size, offset, shard_numel, valid_numel, static_cast<double>(divisor),                 \
+        static_cast<double>(recip), vec_ok, out, tile_scratch, first)
+#define HBT_TILES64(IB, IH, OD)                                \
     do {                                                       \
-        if (out_dtype == F32) HBT_TILES64(IB, IH, F32);        \
-        else if (out_dtype == BF16) HBT_TILES64(IB, IH, BF16); \
-        else HBT_TILES64(IB, IH, F16);                         \
+        if (recip_exact) HBT_TILES64R(IB, IH, OD, true);       \
+        else HBT_TILES64R(IB, IH, OD, false);                  \
+    } while (0)
+#define HBT_TILES64_OD(IB, IH)                                                 \
+    do {                                                                       \
+        if (out_dtype == HBT_DTYPE_F64) HBT_TILES64(IB, IH, HBT_DTYPE_F64);    \
+        else if (out_dtype == F32) HBT_TILES64(IB, IH, F32);                   \
+        else if (out_dtype == BF16) HBT_TILES64(IB, IH, BF16);                 \
+        else HBT_TILES64(IB, IH, F16);                                         \
     } while (0)
         if (f64) {
             if (in_dtype == HBT_DTYPE_F64) HBT_TILES64_OD(8, false);
@@ -1152,6 +1566,7 @@ int32_t local_share(const char* who, const void* const* rank_grads, int32_t grou
         }
 #undef HBT_TILES64_OD
 #undef HBT_TILES64
+#undef HBT_TILES64R
 #undef HBT_TILES_RD
 #undef HBT_TILES_OD
 #undef HBT_TILES_G
@@ -1163,7 +1578,11 @@ int32_t local_share(const char* who, const void* const* rank_grads, int32_t grou
     const int64_t pad_chunks = (shard_numel - valid_numel + chunk - 1) / chunk;
     const int64_t valid_tiles = (valid_numel + kShareTile - 1) / kShareTile;
     return launch_sliced(who, valid_chunks + pad_chunks, kShareBlock, [&](int64_t first, dim3 grid) {
-        if (out_dtype == F32) {
+        if (out_dtype == HBT_DTYPE_F64) {
+            static_assert(kNormF64Chunk % kShareTile == 0, "a float64 norm chunk is whole tiles");
+            tile_sums_to_partials_kernel<static_cast<int>(kNormF64Chunk / kShareTile)><<<grid, kShareBlock, 0, st>>>(
+                tile_scratch, tiles, valid_tiles, valid_chunks, partials, first);
+        } else if (out_dtype == F32) {
             tile_sums_to_partials_kernel<tiles_per_norm_chunk<F32>()><<<grid, kShareBlock, 0, st>>>(
                 tile_scratch, tiles, valid_tiles, valid_chunks, partials, first);
         } else {
@@ -1280,7 +1699,7 @@ int32_t hbt_adamw_step(void* const* params, void* const* grads, void* const* exp
 
 int64_t hbt_norm_partials_count(const int64_t* numels, int32_t count, int32_t grad_dtype) {
     if (count < 0 || count > kMaxT || (count > 0 && numels == nullptr)) return -1;
-    if (grad_dtype != F32 && grad_dtype != BF16 && grad_dtype != F16) return -1;
+    if (grad_dtype != F32 && grad_dtype != BF16 && grad_dtype != F16 && grad_dtype != HBT_DTYPE_F64) return -1;
     const int64_t chunk = norm_chunk_of(grad_dtype);
     int64_t chunks = 0;
     for (int i = 0; i < count; ++i) {
@@ -1297,6 +1716,11 @@ int32_t hbt_grad_sqnorm_partials(const void* const* grads, const int64_t* numels
     if (count > 0 && partials == nullptr) {
         set_error("hbt_grad_sqnorm_partials: null partials pointer");
         return HBT_ERR_INVALID_ARGUMENT;
+    }
+    if (grad_dtype == HBT_DTYPE_F64 && unscale != 1.0f) {
+        set_error("hbt_grad_sqnorm_partials: float64 gradients are unscaled in double first "
+                  "(hbt_scale_inplace_f64); the norm takes unscale 1");
+        return HBT_ERR_UNSUPPORTED;
     }
     NormTable tab{};
     int64_t chunks = 0;
@@ -1318,6 +1742,11 @@ int32_t hbt_scale_inplace_sqnorm(void* const* tensors, const int64_t* numels, in
         set_error("hbt_scale_inplace_sqnorm: null tensor table");
         return HBT_ERR_INVALID_ARGUMENT;
     }
+    if (dtype == HBT_DTYPE_F64) {
+        set_error("hbt_scale_inplace_sqnorm: float64 tensors scale in double (hbt_scale_inplace_f64), then "
+                  "hbt_grad_sqnorm_partials");
+        return HBT_ERR_UNSUPPORTED;
+    }
     double ones[kMaxT];
     for (int i = 0; i < kMaxT; ++i) ones[i] = 1.0;
     const void* grads[kMaxT] = {};
@@ -1333,14 +1762,14 @@ int32_t hbt_scale_inplace_sqnorm(void* const* tensors, const int64_t* numels, in
 
 int32_t hbt_grad_norm_finalize(const double* partials, int64_t count, double max_norm,
                                double* sum_out, double* norm_out, float* grad_mul_out,
-                               int32_t* nonfinite_out, void* stream) {
+                               double* grad_mul64_out, int32_t* nonfinite_out, void* stream) {
     clear_error();
     if (count < 0 || (count > 0 && partials == nullptr)) {
         set_error("hbt_grad_norm_finalize: bad partials/count");
         return HBT_ERR_INVALID_ARGUMENT;
     }
-    norm_finalize_kernel<<<1, kFinalBlock, 0, as_stream(stream)>>>(partials, count, max_norm, sum_out,
-                                                                   norm_out, grad_mul_out, nonfinite_out);
+    norm_finalize_kernel<<<1, kFinalBlock, 0, as_stream(stream)>>>(partials, count, max_norm, sum_out, norm_out,
+                                                                   grad_mul_out, grad_mul64_out, nonfinite_out);
     return check_launch("hbt_grad_norm_finalize");
 }
 
@@ -1349,6 +1778,11 @@ int32_t hbt_grad_norm_noalloc(const void* const* grads, const int64_t* numels, c
                               double* sum_out, double* norm_out, float* grad_mul_out,
                               int32_t* nonfinite_out, void* stream) {
     clear_error();
+    if (grad_dtype == HBT_DTYPE_F64) {
+        set_error("hbt_grad_norm_noalloc: float64 gradients are not covered (their clip multiplier is a "
+                  "double; use hbt_grad_sqnorm_partials + hbt_grad_norm_finalize)");
+        return HBT_ERR_UNSUPPORTED;
+    }
     NormTable tab{};
     int64_t chunks = 0;
     int32_t status = build_norm_table("hbt_grad_norm_noalloc", grads, numels, weights, count, grad_dtype,
@@ -1371,7 +1805,7 @@ int32_t hbt_grad_norm_noalloc(const void* const* grads, const int64_t* numels, c
     status = launch_sqnorm("hbt_grad_norm_noalloc", tab, chunks, grad_dtype, unscale, partials, st);
     if (status != HBT_OK) return status;
     norm_finalize_kernel<<<1, kFinalBlock, 0, st>>>(partials, chunks, max_norm, sum_out, norm_out,
-                                                   grad_mul_out, nonfinite_out);
+                                                   grad_mul_out, nullptr, nonfinite_out);
     return check_launch("hbt_grad_norm_noalloc");
 }
 
@@ -1383,7 +1817,7 @@ int32_t hbt_scale_inplace(void* const* tensors, const int64_t* numels, int32_t c
         return HBT_ERR_INVALID_ARGUMENT;
     }
     if (dtype != F32 && dtype != BF16 && dtype != F16) {
-        set_error("hbt_scale_inplace: dtype %d is not F32, BF16 or F16", dtype);
+        set_error("hbt_scale_inplace: dtype %d is not F32, BF16 or F16 (float64: hbt_scale_inplace_f64)", dtype);
         return HBT_ERR_INVALID_ARGUMENT;
     }
     ScaleTable tab{};
@@ -1618,6 +2052,173 @@ int32_t hbt_sgd_step(void* const* params, void* const* grads, void* const* momen
 #undef HBT_SGD_MODES
 #undef HBT_SGD_WB
 #undef HBT_SGD
+    });
+}
+
+int32_t hbt_adamw_step_f64(double* const* params, double* const* grads, double* const* exp_avgs,
+                           double* const* exp_avg_sqs, const int64_t* numels, int32_t count, double unscale,
+                           const double* grad_mul, double decay, double lerp_weight, double beta2,
+                           double one_minus_beta2, double bias_correction2_sqrt, double eps, double neg_step_size,
+                           int32_t flags, void* stream) {
+    clear_error();
+    if (count < 0 || count > kMaxT) {
+        set_error("hbt_adamw_step_f64: count must lie in [0, %d], got %d", kMaxT, count);
+        return HBT_ERR_INVALID_ARGUMENT;
+    }
+    if ((flags & ~HBT_STEP_WRITE_GRAD) != 0) {
+        set_error("hbt_adamw_step_f64: unknown flags 0x%x", static_cast<unsigned>(flags));
+        return HBT_ERR_INVALID_ARGUMENT;
+    }
+    if (count > 0 && (params == nullptr || grads == nullptr || exp_avgs == nullptr || exp_avg_sqs == nullptr ||
+                      numels == nullptr)) {
+        set_error("hbt_adamw_step_f64: null table pointer");
+        return HBT_ERR_INVALID_ARGUMENT;
+    }
+    const bool write_back = (flags & HBT_STEP_WRITE_GRAD) != 0;
+    const int64_t tile = write_back ? adam_f64_tile<true>() : adam_f64_tile<false>();
+    AdamTable tab{};
+    tab.count = count;
+    int64_t blocks = 0;
+    for (int i = 0; i < count; ++i) {
+        if (numels[i] < 0 || (numels[i] > 0 && (params[i] == nullptr || grads[i] == nullptr ||
+                                                exp_avgs[i] == nullptr || exp_avg_sqs[i] == nullptr))) {
+            set_error("hbt_adamw_step_f64: tensor %d has a bad pointer or numel", i);
+            return HBT_ERR_INVALID_ARGUMENT;
+        }
+        tab.p[i] = params[i];
+        tab.g[i] = grads[i];
+        tab.m[i] = exp_avgs[i];
+        tab.v[i] = exp_avg_sqs[i];
+        tab.n[i] = numels[i];
+        tab.vec_ok[i] = aligned(params[i], 16) && aligned(grads[i], 16) && aligned(exp_avgs[i], 16) &&
+                        aligned(exp_avg_sqs[i], 16);
+        tab.first_block[i] = blocks;
+        blocks += (numels[i] + tile - 1) / tile;
+    }
+    tab.first_block[count] = blocks;
+    for (int i = count + 1; i <= kMaxT; ++i) tab.first_block[i] = blocks;
+    const AdamScalarsF64 s{unscale, decay, lerp_weight, lerp_weight - 1.0, beta2, one_minus_beta2,
+                           bias_correction2_sqrt, eps, neg_step_size};
+    const bool lerp_small = std::fabs(lerp_weight) < 0.5;
+    const bool scaled = unscale != 1.0;
+    hipStream_t st = as_stream(stream);
+    return launch_sliced("hbt_adamw_step_f64", blocks, kAdamBlock, [&](int64_t first, dim3 grid) {
+#define HBT_ADAMW64(SMALL, SCALED, WB) \
+    adamw_f64_kernel<SMALL, SCALED, WB><<<grid, kAdamBlock, 0, st>>>(tab, s, grad_mul, first)
+#define HBT_ADAMW64_WB(SMALL, SCALED)                     \
+    do {                                                  \
+        if (write_back) HBT_ADAMW64(SMALL, SCALED, true); \
+        else HBT_ADAMW64(SMALL, SCALED, false);           \
+    } while (0)
+#define HBT_ADAMW64_SCALED(SMALL)                \
+    do {                                         \
+        if (scaled) HBT_ADAMW64_WB(SMALL, true); \
+        else HBT_ADAMW64_WB(SMALL, false);       \
+    } while (0)
+        if (lerp_small) HBT_ADAMW64_SCALED(true);
+        else HBT_ADAMW64_SCALED(false);
+#undef HBT_ADAMW64_SCALED
+#undef HBT_ADAMW64_WB
+#undef HBT_ADAMW64
+    });
+}
+
+int32_t hbt_sgd_step_f64(double* const* params, double* const* grads, double* const* momentum_buffers,
+                         const int64_t* numels, int32_t count, double unscale, const double* grad_mul,
+                         double weight_decay, double momentum, double one_minus_dampening, double neg_lr,
+                         int32_t flags, void* stream) {
+    clear_error();
+    if (count < 0 || count > kMaxT) {
+        set_error("hbt_sgd_step_f64: count must lie in [0, %d], got %d", kMaxT, count);
+        return HBT_ERR_INVALID_ARGUMENT;
+    }
+    const int32_t known = HBT_SGD_MOMENTUM | HBT_SGD_FIRST_STEP | HBT_SGD_NESTEROV | HBT_SGD_WEIGHT_DECAY |
+                          HBT_STEP_WRITE_GRAD;
+    if ((flags & ~known) != 0 ||
+        ((flags & (HBT_SGD_FIRST_STEP | HBT_SGD_NESTEROV)) != 0 && (flags & HBT_SGD_MOMENTUM) == 0)) {
+        set_error("hbt_sgd_step_f64: bad flags 0x%x", flags);
+        return HBT_ERR_INVALID_ARGUMENT;
+    }
+    const bool with_momentum = (flags & HBT_SGD_MOMENTUM) != 0;
+    if (count > 0 && (params == nullptr || grads == nullptr || numels == nullptr ||
+                      (with_momentum && momentum_buffers == nullptr))) {
+        set_error("hbt_sgd_step_f64: null pointer argument");
+        return HBT_ERR_INVALID_ARGUMENT;
+    }
+    const bool write_back = (flags & HBT_STEP_WRITE_GRAD) != 0;
+    const int64_t tile = write_back ? adam_f64_tile<true>() : adam_f64_tile<false>();
+    SgdTable tab{};
+    tab.count = count;
+    int64_t blocks = 0;
+    for (int i = 0; i < count; ++i) {
+        if (numels[i] < 0 || (numels[i] > 0 && (params[i] == nullptr || grads[i] == nullptr ||
+                                                (with_momentum && momentum_buffers[i] == nullptr)))) {
+            set_error("hbt_sgd_step_f64: tensor %d has a bad pointer or numel", i);
+            return HBT_ERR_INVALID_ARGUMENT;
+        }
+        tab.p[i] = params[i];
+        tab.g[i] = grads[i];
+        tab.buf[i] = with_momentum ? momentum_buffers[i] : nullptr;
+        tab.n[i] = numels[i];
+        tab.vec_ok[i] = aligned(params[i], 16) && aligned(grads[i], 16) &&
+                        (!with_momentum || aligned(momentum_buffers[i], 16));
+        tab.first_block[i] = blocks;
+        blocks += (numels[i] + tile - 1) / tile;
+    }
+    tab.first_block[count] = blocks;
+    for (int i = count + 1; i <= kMaxT; ++i) tab.first_block[i] = blocks;
+    const SgdScalarsF64 sc{unscale, weight_decay, momentum, one_minus_dampening, neg_lr,
+                           (flags & HBT_SGD_WEIGHT_DECAY) != 0, (flags & HBT_SGD_NESTEROV) != 0};
+    const int mode = !with_momentum ? kSgdPlain : ((flags & HBT_SGD_FIRST_STEP) ? kSgdFirst : kSgdMomentum);
+    const bool scaled = unscale != 1.0;
+    hipStream_t st = as_stream(stream);
+    return launch_sliced("hbt_sgd_step_f64", blocks, kAdamBlock, [&](int64_t first, dim3 grid) {
+#define HBT_SGD64(SCALED, MODE, WB) sgd_f64_kernel<SCALED, MODE, WB><<<grid, kAdamBlock, 0, st>>>(tab, sc, grad_mul, first)
+#define HBT_SGD64_WB(SCALED, MODE)                     \
+    do {                                               \
+        if (write_back) HBT_SGD64(SCALED, MODE, true); \
+        else HBT_SGD64(SCALED, MODE, false);           \
+    } while (0)
+#define HBT_SGD64_MODES(SCALED)                                      \
+    do {                                                             \
+        if (mode == kSgdPlain) HBT_SGD64_WB(SCALED, kSgdPlain);      \
+        else if (mode == kSgdFirst) HBT_SGD64_WB(SCALED, kSgdFirst); \
+        else HBT_SGD64_WB(SCALED, kSgdMomentum);                     \
+    } while (0)
+        if (scaled) HBT_SGD64_MODES(true);
+        else HBT_SGD64_MODES(false);
+#undef HBT_SGD64_MODES
+#undef HBT_SGD64_WB
+#undef HBT_SGD64
+    });
+}
+
+int32_t hbt_scale_inplace_f64(double* const* tensors, const int64_t* numels, int32_t count, double unscale,
+                              const double* grad_mul, void* stream) {
+    clear_error();
+    if (count < 0 || count > kMaxT || (count > 0 && (tensors == nullptr || numels == nullptr))) {
+        set_error("hbt_scale_inplace_f64: bad table (count=%d)", count);
+        return HBT_ERR_INVALID_ARGUMENT;
+    }
+    ScaleTable tab{};
+    tab.count = count;
+    int64_t blocks = 0;
+    for (int i = 0; i < count; ++i) {
+        if (numels[i] < 0 || (numels[i] > 0 && tensors[i] == nullptr)) {
+            set_error("hbt_scale_inplace_f64: tensor %d has a bad pointer or numel", i);
+            return HBT_ERR_INVALID_ARGUMENT;
+        }
+        tab.x[i] = tensors[i];
+        tab.n[i] = numels[i];
+        tab.vec_ok[i] = aligned(tensors[i], 16);
+        tab.first_block[i] = blocks;
+        blocks += (numels[i] + kScaleF64Tile - 1) / kScaleF64Tile;
+    }
+    tab.first_block[count] = blocks;
+    for (int i = count + 1; i <= kMaxT; ++i) tab.first_block[i] = blocks;
+    hipStream_t st = as_stream(stream);
+    return launch_sliced("hbt_scale_inplace_f64", blocks, 32, [&](int64_t first, dim3 grid) {
+        scale_f64_kernel<<<grid, 32, 0, st>>>(tab, unscale, grad_mul, first);
     });
 }
 

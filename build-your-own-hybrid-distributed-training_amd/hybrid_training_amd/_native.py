@@ -57,7 +57,7 @@ __all__ = [
     "stream_of",
 ]
 
-ABI_VERSION = 14
+ABI_VERSION = 15
 MAX_TENSORS_PER_LAUNCH = 16
 MAX_LOCAL_RANKS = 64
 
@@ -89,6 +89,7 @@ STEP_WRITE_GRAD = 16
 OPTIMIZER_DTYPES = frozenset({
     (torch.float32, torch.float32), (torch.float32, torch.bfloat16),
     (torch.bfloat16, torch.bfloat16), (torch.float16, torch.float16),
+    (torch.float64, torch.float64),
 })
 
 _c_void_p = ctypes.c_void_p
@@ -128,7 +129,7 @@ EXPORTED_SYMBOLS: dict[str, tuple[object, tuple[object, ...]]] = {
     ),
     "hbt_grad_norm_finalize": (
         _c_i32,
-        (_c_void_p, _c_i64, _c_f64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p),
+        (_c_void_p, _c_i64, _c_f64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p),
     ),
     "hbt_grad_norm_noalloc": (
         _c_i32,
@@ -165,6 +166,24 @@ EXPORTED_SYMBOLS: dict[str, tuple[object, tuple[object, ...]]] = {
     "hbt_grad_accumulate": (
         _c_i32,
         (_ptr_array, _ptr_array, _i64_array, _c_i32, _c_i32, _c_i32, _c_i32, _c_void_p),
+    ),
+    "hbt_adamw_step_f64": (
+        _c_i32,
+        (
+            _ptr_array, _ptr_array, _ptr_array, _ptr_array, _i64_array, _c_i32, _c_f64, _c_void_p,
+            _c_f64, _c_f64, _c_f64, _c_f64, _c_f64, _c_f64, _c_f64, _c_i32, _c_void_p,
+        ),
+    ),
+    "hbt_sgd_step_f64": (
+        _c_i32,
+        (
+            _ptr_array, _ptr_array, _ptr_array, _i64_array, _c_i32, _c_f64, _c_void_p,
+            _c_f64, _c_f64, _c_f64, _c_f64, _c_i32, _c_void_p,
+        ),
+    ),
+    "hbt_scale_inplace_f64": (
+        _c_i32,
+        (_ptr_array, _i64_array, _c_i32, _c_f64, _c_void_p, _c_void_p),
     ),
 }
 

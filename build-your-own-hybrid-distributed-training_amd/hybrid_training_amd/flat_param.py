@@ -523,8 +523,10 @@ class FlatParamHandle:
         The gradients are cast to the reduce dtype (float32, bfloat16, float16 or
         float64), and the AVG divide and the sum are rounded to it, as the reference's
         ops in that dtype are (``collectives.py:593-594``); the result is cast to the
-        master dtype (float32, bfloat16 or float16) as ``Tensor.to`` casts.  With mixed
-        precision off, all three dtypes are the parameters' own (``fsdp.py:379-392``).
+        master dtype (float64, float32, bfloat16 or float16) as ``Tensor.to`` casts.  With
+        mixed precision off, all three dtypes are the parameters' own (``fsdp.py:379-392``),
+        float64 included.  A float64 master over a narrower reduce dtype is reduced into
+        float32 (which holds every value of the reduce dtype exactly) and widened.
 
         Inside ``no_sync`` (:meth:`set_accumulate_without_reduction`) the gradients
         are accumulated in the reduce dtype instead and ``None`` is returned
@@ -534,13 +536,13 @@ class FlatParamHandle:
         accumulated row once (``hbt_grad_local_share_accumulated``; a float64 reduce
         dtype adds first and then reduces).
         """
-        if self._reduce_dtype not in (torch.float32, torch.bfloat16, torch.float16, torch.float64) \
-                or self._master_dtype not in (torch.float32, torch.bfloat16, torch.float16):
+        floats = (torch.float32, torch.bfloat16, torch.float16, torch.float64)
+        if self._reduce_dtype not in floats or self._master_dtype not in floats:
             raise UnsupportedFeatureError(
                 format_error(
                     "fsdp.reduce_scatter_gradient",
-                    "the local-share kernel reduces in float32, bfloat16, float16 or float64 into a "
-                    "float32, bfloat16 or float16 master shard",
+                    "the local-share kernel reduces in float64, float32, bfloat16 or float16 into a "
+                    "master shard of one of those dtypes",
                     observed=f"reduce {self._reduce_dtype}, master {self._master_dtype}",
                 )
             )
@@ -558,17 +560,23 @@ class FlatParamHandle:
             )
         for g in grads:
             _native.require_device_tensor(g, "fsdp.reduce_scatter_gradient")
-            if g.numel() != self._padded_numel \
-                    or g.dtype not in (torch.float32, torch.bfloat16, torch.float16) \
+            if g.numel() != self._padded_numel or g.dtype not in floats \
                     or g.dtype != grads[0].dtype or not g.is_contiguous():
                 raise ShardingError(
                     format_error(
                         "fsdp.reduce_scatter_gradient",
                         "each gradient must be a dense padded full buffer of one float dtype",
-                        expected=f"{self._padded_numel} float32/bfloat16/float16 elements",
+                        expected=f"{self._padded_numel} float64/float32/bfloat16/float16 elements",
                         observed=f"{g.numel()} {g.dtype}",
                     )
                 )
+        if grads[0].dtype == torch.float64 and self._reduce_dtype != torch.float64:
+            raise UnsupportedFeatureError(
+                format_error("fsdp.reduce_scatter_gradient",
+                             "float64 gradients are reduced in float64 (the kernels narrow only after the sum)",
+                             observed=f"reduce dtype {self._reduce_dtype}",
+                             resolution="set reduce_dtype to float64, or compute in a narrower dtype")
+            )
         local = self.local_shard_range()
         source_rank = self._shard_group.local_rank
         rows = None  # accumulator rows the reduction adds the last micro-batch to
@@ -591,15 +599,18 @@ class FlatParamHandle:
                 rows = self._grad_accumulator
         valid = max(0, min(self._shard_numel, self._total_numel - local.start))
         divisor = float(group) if (self._config.average_gradients and group > 1) else 1.0
-        out = torch.empty(self._shard_numel, dtype=self._master_dtype, device=self._device)
-        chunk = norm_chunk_elems(self._master_dtype)  # elements per norm partial
+        # A float64 master over a narrower reduce dtype: reduce into float32, widen after.
+        widen = self._master_dtype == torch.float64 and self._reduce_dtype != torch.float64
+        out_dtype = torch.float32 if widen else self._master_dtype
+        out = torch.empty(self._shard_numel, dtype=out_dtype, device=self._device)
+        chunk = norm_chunk_elems(out_dtype)  # elements per norm partial
         valid_chunks = -(-valid // chunk)
         pad = self._shard_numel - valid
         partials = torch.empty(max(1, valid_chunks + -(-pad // chunk)), dtype=torch.float64, device=self._device)
         tile_sums = torch.empty(max(1, -(-self._shard_numel // 256)), dtype=torch.float64, device=self._device)
         lib = _native.library()
         args = (group, source_rank, self._shard_numel, valid, _native.dtype_code(grads[0].dtype),
-                _native.dtype_code(self._reduce_dtype), divisor, _native.dtype_code(self._master_dtype),
+                _native.dtype_code(self._reduce_dtype), divisor, _native.dtype_code(out_dtype),
                 out.data_ptr(), partials.data_ptr(), tile_sums.data_ptr(), _native.stream_of(self._device))
         grad_ptrs = _native.pointer_array([g.data_ptr() for g in grads])
         with torch.cuda.device(self._device):
@@ -620,6 +631,12 @@ class FlatParamHandle:
             segments[(0, valid)] = partials[:valid_chunks]
         if pad:
             segments[(valid, pad)] = partials[valid_chunks:]
+        if widen:
+            wide = torch.empty(self._shard_numel, dtype=torch.float64, device=self._device)
+            plan = _native.CopyPlan(self._device)
+            plan.add(out, 0, wide, 0, self._shard_numel)
+            plan.run(src_dtype=torch.float32, dst_dtype=torch.float64)
+            out, segments = wide, {}  # the partials were chunked for float32; the norm pass sums anew
         if self._offload_params:
             out = self._to_host(out)  # the partials stay on the device and describe the copy
         setattr(out, NORM_PARTIALS_ATTR, NormPartials(out.data_ptr(), out._version, segments, out.dtype))

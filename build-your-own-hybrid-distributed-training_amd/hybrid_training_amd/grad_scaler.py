@@ -6,7 +6,8 @@ serialised state are the reference's (``grad_scaler.py:52-298``).  The gradient 
 is native:
 
 * ``unscale_`` multiplies each gradient by ``fp32(1/scale)`` in its own dtype, as
-  ``grad.mul_(inverse)`` does, and in the same pass sums the squares of the result
+  ``grad.mul_(inverse)`` does (by the double ``1/scale`` for float64 gradients, without
+  the fused partials below), and in the same pass sums the squares of the result
   into fp64 per-chunk partials (``hbt_scale_inplace_sqnorm``): the finiteness check
   reads those (the sum of squares is non-finite exactly when some element is), and they
   stay on the gradients, so the optimizer's ``clip_grad_norm`` that follows takes the
@@ -19,8 +20,9 @@ is native:
   update pass.  ``unscale_`` then returns a lazily evaluated flag, and ``step`` takes
   the overflow decision from the optimizer's norm pass when it covered the same
   gradients.  An optimizer with in-place semantics (``defer_clip=False``) writes the
-  unscaled, clipped gradients back during its step, or, when the step is skipped,
-  here.  A factor still pending when ``unscale_`` is called again is applied in place
+  unscaled, clipped gradients back in its ``clip_grad_norm`` (by default) or its step
+  (``clip_in_step``), or, when the step is skipped, here.  Float64 gradients are always
+  unscaled at once, in double.  A factor still pending when ``unscale_`` is called again is applied in place
   first (two calls multiply twice, as in the reference), and ``step`` applies pending
   factors in place before handing the gradients to any optimizer other than
   ``ShardedOptimizer``, which would not read them.
@@ -120,9 +122,9 @@ def _apply_pending_unscale(grads: Sequence[torch.Tensor], device: torch.device) 
         # the in-place scaling addresses numel consecutive elements: checked for every
         # gradient before any is scaled
         _native.require_dense(g, "grad_scaler.unscale_")
-        if g.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+        if g.dtype not in (torch.float32, torch.bfloat16, torch.float16, torch.float64):
             raise UnsupportedFeatureError(
-                format_error("grad_scaler.unscale_", "gradients must be float32, bfloat16 or float16",
+                format_error("grad_scaler.unscale_", "gradients must be float64, float32, bfloat16 or float16",
                              observed=str(g.dtype))
             )
         resident = device if is_host(g) else g.device
@@ -186,8 +188,15 @@ class GradScaler:
             # A factor still pending from an earlier unscale_ (no step since) is applied
             # first, so two calls multiply twice, as two in-place multiplies do.
             _apply_pending_unscale([p.grad for p in params], self._device)
-            for p in params:
+            # Float64 gradients are unscaled at once, in double: the norm and the update
+            # read a deferred factor only through fp32 arithmetic.
+            wide = [p for p in params if p.grad.dtype == torch.float64]
+            for p in wide:
                 setattr(p.grad, PENDING_UNSCALE_ATTR, inverse)
+            _apply_pending_unscale([p.grad for p in wide], self._device)
+            for p in params:
+                if p.grad.dtype != torch.float64:
+                    setattr(p.grad, PENDING_UNSCALE_ATTR, inverse)
             self._unscaled = True
             return _DeviceFlag(lambda: self._detect_non_finite(params))  # type: ignore[return-value]
         groups: dict[tuple[torch.device, torch.dtype], list[torch.Tensor]] = {}
@@ -195,9 +204,9 @@ class GradScaler:
             if not is_host(p.grad):
                 _native.require_device_tensor(p.grad, "grad_scaler.unscale_")
             _native.require_dense(p.grad, "grad_scaler.unscale_")
-            if p.grad.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+            if p.grad.dtype not in (torch.float32, torch.bfloat16, torch.float16, torch.float64):
                 raise UnsupportedFeatureError(
-                    format_error("grad_scaler.unscale_", "gradients must be float32, bfloat16 or float16",
+                    format_error("grad_scaler.unscale_", "gradients must be float64, float32, bfloat16 or float16",
                                  observed=str(p.grad.dtype))
                 )
             # a gradient in host memory streams through the scaler's device

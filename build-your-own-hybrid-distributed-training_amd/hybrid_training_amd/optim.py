@@ -278,8 +278,22 @@ class NormResult:
 
     sum: torch.Tensor
     norm: torch.Tensor
-    grad_mul: torch.Tensor
+    grad_mul: torch.Tensor  # fp32 clip multiplier, for fp32, bf16 and fp16 gradients
     nonfinite: torch.Tensor
+    grad_mul64: torch.Tensor | None = None  # the double one, for float64 gradients
+
+    def multiplier_ptr(self, dtype: torch.dtype) -> int:
+        """Device address of the clip multiplier a gradient of ``dtype`` is scaled by: the
+        double coefficient for float64 gradients, its fp32 rounding for the others (as
+        torch hands a Python-double scalar to kernels of each dtype)."""
+        if dtype == torch.float64:
+            assert self.grad_mul64 is not None
+            return self.grad_mul64.data_ptr()
+        return self.grad_mul.data_ptr()
+
+
+def _mul_ptr(result: NormResult | None, dtype: torch.dtype) -> int | None:
+    return None if result is None else result.multiplier_ptr(dtype)
 
 
 def _pending_unscale(grad: torch.Tensor) -> float:
@@ -314,13 +328,19 @@ def gradient_norm_pass(
     for grad, offset, length, weight in segments:
         if not is_host(grad):
             _native.require_device_tensor(grad, "optim.gradient_norm")
-        if grad.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+        if grad.dtype not in (torch.float32, torch.bfloat16, torch.float16, torch.float64):
             raise UnsupportedFeatureError(
                 format_error(
                     "optim.gradient_norm",
-                    "gradients must be float32, bfloat16 or float16",
+                    "gradients must be float64, float32, bfloat16 or float16",
                     observed=str(grad.dtype),
                 )
+            )
+        if grad.dtype == torch.float64 and _pending_unscale(grad) != 1.0:
+            raise UnsupportedFeatureError(
+                format_error("optim.gradient_norm",
+                             "a float64 gradient is unscaled in place before its norm, not read through "
+                             "a deferred factor", resolution="unscale float64 gradients eagerly")
             )
         if not grad.is_contiguous():
             raise ShardingError(
@@ -341,7 +361,7 @@ def gradient_norm_pass(
             total_partials += count
     partials = torch.empty(max(1, total_partials), dtype=torch.float64, device=device)
     fresh: list[tuple[torch.Tensor, int, int, int, int]] = []  # segments whose partials are tagged
-    outputs = torch.empty(2, dtype=torch.float64, device=device)
+    outputs = torch.empty(3, dtype=torch.float64, device=device)  # sum, norm, double clip multiplier
     grad_mul = torch.empty(1, dtype=torch.float32, device=device)
     nonfinite = torch.empty(1, dtype=torch.int32, device=device)
     stream = _native.stream_of(device)
@@ -386,6 +406,7 @@ def gradient_norm_pass(
             outputs.data_ptr(),
             outputs.data_ptr() + 8,
             grad_mul.data_ptr(),
+            outputs.data_ptr() + 16,
             nonfinite.data_ptr(),
             stream,
         )
@@ -400,11 +421,15 @@ def gradient_norm_pass(
             record.segments.update(found)  # keep a producer's still-valid segments
         else:
             setattr(grad, NORM_PARTIALS_ATTR, NormPartials(grad.data_ptr(), grad._version, found, grad.dtype))
-    return NormResult(sum=outputs[0], norm=outputs[1], grad_mul=grad_mul, nonfinite=nonfinite)
+    return NormResult(sum=outputs[0], norm=outputs[1], grad_mul=grad_mul, nonfinite=nonfinite,
+                      grad_mul64=outputs[2:3])
 
 
 def norm_chunk_elems(dtype: torch.dtype) -> int:
-    """Elements per norm partial: 32768 of an fp32 gradient, 65536 of a 2-byte one."""
+    """Elements per norm partial: 32768 of an fp32 gradient, 65536 of a 2-byte one,
+    16384 of a float64 one."""
+    if dtype == torch.float64:
+        return 16384
     return 32768 if dtype == torch.float32 else 65536
 
 
@@ -449,14 +474,19 @@ def _launch_sqnorm(lib, items, dtype, unscale, partials, first, stream) -> None:
 def scale_gradients(grads: Sequence[torch.Tensor], dtype: torch.dtype, unscale: float, grad_mul_ptr: int | None,
                     device: torch.device, operation: str) -> None:
     """Multiply dense gradients of one dtype in place by ``unscale`` and ``*grad_mul``,
-    each product rounded to the dtype (``hbt_scale_inplace``, the reference's
-    ``grad.mul_``).  Gradients in HBM go in launches of up to 16; a gradient in host
-    memory streams through ``device`` and is final on the host when this returns."""
+    each product rounded to the dtype (``hbt_scale_inplace``, or ``hbt_scale_inplace_f64``
+    with a double multiplier for float64: the reference's ``grad.mul_``).  Gradients in
+    HBM go in launches of up to 16; a gradient in host memory streams through ``device``
+    and is final on the host when this returns."""
     lib = _native.library()
 
     def call(ptrs: list[int], numels: list[int], stream: int) -> None:
-        status = lib.hbt_scale_inplace(_native.pointer_array(ptrs), _native.int64_array(numels), len(ptrs),
-                                       _native.dtype_code(dtype), unscale, grad_mul_ptr, stream)
+        if dtype == torch.float64:
+            status = lib.hbt_scale_inplace_f64(_native.pointer_array(ptrs), _native.int64_array(numels), len(ptrs),
+                                               float(unscale), grad_mul_ptr, stream)
+        else:
+            status = lib.hbt_scale_inplace(_native.pointer_array(ptrs), _native.int64_array(numels), len(ptrs),
+                                           _native.dtype_code(dtype), unscale, grad_mul_ptr, stream)
         _native.check(status, operation)
 
     resident = [g for g in grads if not is_host(g)]
@@ -483,7 +513,11 @@ def unscale_with_partials(grads: Sequence[torch.Tensor], dtype: torch.dtype, uns
     record of its whole length, so the overflow check and a following clip read none
     of them again.  A gradient in host memory streams through ``device``, its staged
     chunks placed at its own 16-byte alignment as the norm pass places them, and is
-    final on the host when this returns."""
+    final on the host when this returns.  Float64 gradients are scaled in double
+    (``hbt_scale_inplace_f64``) without partials; the overflow check sums them after."""
+    if dtype == torch.float64:
+        scale_gradients(grads, dtype, unscale, None, device, operation)
+        return
     lib = _native.library()
     code = _native.dtype_code(dtype)
     norm_chunk = norm_chunk_elems(dtype)
@@ -574,11 +608,32 @@ def _grad_signature(params: Sequence[nn.Parameter]) -> tuple[tuple[int, int, int
     return tuple(sig)
 
 
-def _write_back_flag(write_back: bool, grad_mul: torch.Tensor | None, unscale: float) -> int:
+def _write_back_flag(write_back: bool, grad_mul: NormResult | None, unscale: float) -> int:
     """``HBT_STEP_WRITE_GRAD`` when the update must store the scaled gradient: with
     in-place semantics and a multiplier pending.  Without one the gradient is unchanged,
     so neither the store nor, for a host gradient, the copy back is needed."""
     return _native.STEP_WRITE_GRAD if write_back and (grad_mul is not None or unscale != 1.0) else 0
+
+
+def _adamw_call(lib, pdtype, gdtype, p, g, m, v, numels, unscale, mul_ptr, scalars, flags, stream) -> int:
+    """One ``hbt_adamw_step`` launch, or ``hbt_adamw_step_f64`` (double scalars) on float64
+    parameters; ``p``, ``g``, ``m``, ``v`` are lists of device addresses."""
+    tables = (_native.pointer_array(p), _native.pointer_array(g), _native.pointer_array(m),
+              _native.pointer_array(v), _native.int64_array(numels), len(numels))
+    if pdtype == torch.float64:
+        return lib.hbt_adamw_step_f64(*tables, float(unscale), mul_ptr, *scalars, flags, stream)
+    return lib.hbt_adamw_step(*tables, _native.dtype_code(pdtype), _native.dtype_code(gdtype), unscale, mul_ptr,
+                              *scalars, flags, stream)
+
+
+def _sgd_call(lib, pdtype, gdtype, p, g, buf, numels, unscale, mul_ptr, scalars, flags, stream) -> int:
+    """One ``hbt_sgd_step`` launch, or ``hbt_sgd_step_f64`` on float64 parameters."""
+    tables = (_native.pointer_array(p), _native.pointer_array(g),
+              None if buf is None else _native.pointer_array(buf), _native.int64_array(numels), len(numels))
+    if pdtype == torch.float64:
+        return lib.hbt_sgd_step_f64(*tables, float(unscale), mul_ptr, *scalars, flags, stream)
+    return lib.hbt_sgd_step(*tables, _native.dtype_code(pdtype), _native.dtype_code(gdtype), unscale, mul_ptr,
+                            *scalars, flags, stream)
 
 
 def _pinned_like(p: torch.Tensor) -> torch.Tensor:
@@ -635,11 +690,11 @@ class ShardedOptimizer:
         for param in self._parameters:
             if not is_host(param):
                 _native.require_device_tensor(param, "optim.ShardedOptimizer")
-            if param.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+            if param.dtype not in (torch.float32, torch.bfloat16, torch.float16, torch.float64):
                 raise UnsupportedFeatureError(
                     format_error(
                         "optim.ShardedOptimizer",
-                        "master parameters must be float32, bfloat16 or float16",
+                        "master parameters must be float64, float32, bfloat16 or float16",
                         observed=str(param.dtype),
                     )
                 )
@@ -664,7 +719,7 @@ class ShardedOptimizer:
         self._contributions = build_gradient_norm_contributions(
             self._parameters, world_size=norm_group.size
         )
-        self._pending_mul: torch.Tensor | None = None
+        self._pending_mul: NormResult | None = None  # the clip multipliers the next step applies
         self._pending_signature: tuple[tuple[int, int, int], ...] | None = None
         self._last_check: tuple[tuple[tuple[int, int, int], ...], torch.Tensor] | None = None
 
@@ -675,7 +730,7 @@ class ShardedOptimizer:
         self._last_check = (_grad_signature(self._parameters), result.nonfinite)
         return result
 
-    def _scale_grads(self, grad_mul: torch.Tensor | None, unscale_attr: bool) -> None:
+    def _scale_grads(self, grad_mul: NormResult | None, unscale_attr: bool) -> None:
         """Apply pending multipliers to the gradients in place (materialisation)."""
         groups: dict[tuple[torch.dtype, float], list[torch.Tensor]] = {}
         for p in self._parameters:
@@ -686,8 +741,8 @@ class ShardedOptimizer:
             unscale = _pending_unscale(g) if unscale_attr else 1.0
             groups.setdefault((g.dtype, unscale), []).append(g)
         for (dtype, unscale), grads in groups.items():
-            scale_gradients(grads, dtype, unscale, None if grad_mul is None else grad_mul.data_ptr(),
-                            self._device, "optim.hbt_scale_inplace")
+            scale_gradients(grads, dtype, unscale, _mul_ptr(grad_mul, dtype), self._device,
+                            "optim.hbt_scale_inplace")
         if unscale_attr:
             for p in self._parameters:
                 if p.grad is not None and hasattr(p.grad, PENDING_UNSCALE_ATTR):
@@ -738,7 +793,7 @@ class ShardedOptimizer:
         result = self._norm(max_norm)
         if max_norm <= 0:
             return result.norm
-        self._pending_mul = result.grad_mul
+        self._pending_mul = result
         self._pending_signature = _grad_signature(self._parameters)
         if not (self._defer_clip or self._clip_in_step):
             self.materialize_pending()  # the reference's grad.mul_(coefficient), on the device
@@ -776,7 +831,7 @@ class ShardedOptimizer:
         mul = self._pending_mul if self._pending_valid() else None
         self._run_step(mul)
 
-    def _run_step(self, grad_mul: torch.Tensor | None) -> None:
+    def _run_step(self, grad_mul: NormResult | None) -> None:
         # With in-place semantics the update pass writes the scaled gradient back: the
         # clip, and a loss-scale factor deferred by the scaler, land in .grad as the
         # reference's in-place multiplies would leave them.
@@ -858,7 +913,7 @@ class ShardedOptimizer:
                 stepped.append((group, p, grad))
         return stepped
 
-    def _run_adamw_step(self, grad_mul: torch.Tensor | None, write_back: bool) -> None:
+    def _run_adamw_step(self, grad_mul: NormResult | None, write_back: bool) -> None:
         lib = _native.library()
         batches: dict[tuple, list[nn.Parameter]] = {}
         for group, p, grad in self._stepped_parameters():
@@ -893,10 +948,10 @@ class ShardedOptimizer:
             key = (scalars, p.dtype, grad.dtype, _pending_unscale(grad))
             batches.setdefault(key, []).append(p)
         stream = _native.stream_of(self._device)
-        mul_ptr = None if grad_mul is None else grad_mul.data_ptr()
         with torch.cuda.device(self._device):
             for (scalars, pdtype, gdtype, unscale), batch in batches.items():
                 flags = _write_back_flag(write_back, grad_mul, unscale)
+                mul_ptr = _mul_ptr(grad_mul, gdtype)
                 for p in batch:
                     if is_host(p):
                         self._streamed_adamw(lib, p, scalars, pdtype, gdtype, unscale, mul_ptr, flags)
@@ -904,20 +959,14 @@ class ShardedOptimizer:
                 for start in range(0, len(params), _native.MAX_TENSORS_PER_LAUNCH):
                     chunk = params[start : start + _native.MAX_TENSORS_PER_LAUNCH]
                     states = [self._optimizer.state[p] for p in chunk]
-                    status = lib.hbt_adamw_step(
-                        _native.pointer_array([p.data_ptr() for p in chunk]),
-                        _native.pointer_array([p.grad.data_ptr() for p in chunk]),
-                        _native.pointer_array([s["exp_avg"].data_ptr() for s in states]),
-                        _native.pointer_array([s["exp_avg_sq"].data_ptr() for s in states]),
-                        _native.int64_array([p.numel() for p in chunk]),
-                        len(chunk),
-                        _native.dtype_code(pdtype),
-                        _native.dtype_code(gdtype),
-                        unscale,
-                        mul_ptr,
-                        *scalars,
-                        flags,
-                        stream,
+                    status = _adamw_call(
+                        lib, pdtype, gdtype,
+                        [p.data_ptr() for p in chunk],
+                        [p.grad.data_ptr() for p in chunk],
+                        [s["exp_avg"].data_ptr() for s in states],
+                        [s["exp_avg_sq"].data_ptr() for s in states],
+                        [p.numel() for p in chunk],
+                        unscale, mul_ptr, scalars, flags, stream,
                     )
                     _native.check(status, "optim.hbt_adamw_step")
                     increment_version(chunk)
@@ -950,21 +999,8 @@ class ShardedOptimizer:
         m, v = state["exp_avg"], state["exp_avg_sq"]
 
         def call(p_ptr: int, g_ptr: int, m_ptr: int, v_ptr: int, n: int, stream: int) -> None:
-            status = lib.hbt_adamw_step(
-                _native.pointer_array([p_ptr]),
-                _native.pointer_array([g_ptr]),
-                _native.pointer_array([m_ptr]),
-                _native.pointer_array([v_ptr]),
-                _native.int64_array([n]),
-                1,
-                _native.dtype_code(pdtype),
-                _native.dtype_code(gdtype),
-                unscale,
-                mul_ptr,
-                *scalars,
-                flags,
-                stream,
-            )
+            status = _adamw_call(lib, pdtype, gdtype, [p_ptr], [g_ptr], [m_ptr], [v_ptr], [n], unscale, mul_ptr,
+                                 scalars, flags, stream)
             _native.check(status, "optim.hbt_adamw_step")
 
         if dev is not None:
@@ -988,7 +1024,7 @@ class ShardedOptimizer:
         )
         increment_version([host_p, m, v])
 
-    def _run_sgd_step(self, grad_mul: torch.Tensor | None, write_back: bool) -> None:
+    def _run_sgd_step(self, grad_mul: NormResult | None, write_back: bool) -> None:
         """torch.optim.SGD's step (``torch/optim/sgd.py``) as one fused kernel per batch."""
         lib = _native.library()
         batches: dict[tuple, list[nn.Parameter]] = {}
@@ -1012,15 +1048,16 @@ class ShardedOptimizer:
                                                 else torch.empty_like(p, memory_format=torch.preserve_format))
                     flags |= _native.SGD_FIRST_STEP
             # Scalars exactly as torch forms them: Python doubles, rounded to fp32 (and
-            # each alpha to a 2-byte parameter dtype inside the kernel's entry point).
+            # each alpha to a 2-byte parameter dtype inside the kernel's entry point), or
+            # kept as doubles for float64 parameters.
             scalars = (weight_decay, momentum, 1 - dampening, -lr)
             unscale = _pending_unscale(grad)
             key = (scalars, flags | _write_back_flag(write_back, grad_mul, unscale), p.dtype, grad.dtype, unscale)
             batches.setdefault(key, []).append(p)
         stream = _native.stream_of(self._device)
-        mul_ptr = None if grad_mul is None else grad_mul.data_ptr()
         with torch.cuda.device(self._device):
             for (scalars, flags, pdtype, gdtype, unscale), batch in batches.items():
+                mul_ptr = _mul_ptr(grad_mul, gdtype)
                 for p in batch:
                     if is_host(p):
                         self._streamed_sgd(lib, p, scalars, flags, pdtype, gdtype, unscale, mul_ptr)
@@ -1029,20 +1066,10 @@ class ShardedOptimizer:
                     chunk = params[start : start + _native.MAX_TENSORS_PER_LAUNCH]
                     buffers = ([self._optimizer.state[p]["momentum_buffer"] for p in chunk]
                                if flags & _native.SGD_MOMENTUM else [])
-                    status = lib.hbt_sgd_step(
-                        _native.pointer_array([p.data_ptr() for p in chunk]),
-                        _native.pointer_array([p.grad.data_ptr() for p in chunk]),
-                        _native.pointer_array([b.data_ptr() for b in buffers]) if buffers else None,
-                        _native.int64_array([p.numel() for p in chunk]),
-                        len(chunk),
-                        _native.dtype_code(pdtype),
-                        _native.dtype_code(gdtype),
-                        unscale,
-                        mul_ptr,
-                        *scalars,
-                        flags,
-                        stream,
-                    )
+                    status = _sgd_call(lib, pdtype, gdtype, [p.data_ptr() for p in chunk],
+                                       [p.grad.data_ptr() for p in chunk],
+                                       [b.data_ptr() for b in buffers] if buffers else None,
+                                       [p.numel() for p in chunk], unscale, mul_ptr, scalars, flags, stream)
                     _native.check(status, "optim.hbt_sgd_step")
                     increment_version(chunk)
                     if buffers:
@@ -1059,20 +1086,8 @@ class ShardedOptimizer:
                    if momentum else [])
 
         def call(p_ptr: int, g_ptr: int, b_ptr: int | None, n: int, stream: int) -> None:
-            status = lib.hbt_sgd_step(
-                _native.pointer_array([p_ptr]),
-                _native.pointer_array([g_ptr]),
-                _native.pointer_array([b_ptr]) if b_ptr is not None else None,
-                _native.int64_array([n]),
-                1,
-                _native.dtype_code(pdtype),
-                _native.dtype_code(gdtype),
-                unscale,
-                mul_ptr,
-                *scalars,
-                flags,
-                stream,
-            )
+            status = _sgd_call(lib, pdtype, gdtype, [p_ptr], [g_ptr], None if b_ptr is None else [b_ptr], [n],
+                               unscale, mul_ptr, scalars, flags, stream)
             _native.check(status, "optim.hbt_sgd_step")
 
         if dev is not None:

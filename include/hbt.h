@@ -32,7 +32,8 @@ extern "C" {
 #define HBT_DTYPE_F32 0
 #define HBT_DTYPE_BF16 1
 #define HBT_DTYPE_F16 2
-#define HBT_DTYPE_F64 3 /* copies and conversions; local-share reduce dtype and accumulate dtype */
+#define HBT_DTYPE_F64 3 /* float64: the _f64 optimizer entry points, norms, copies, conversions,
+                           local-share reduce and master dtype, accumulate dtype */
 
 /* ---- per-call limits ---------------------------------------------------------- */
 #define HBT_MAX_TENSORS_PER_LAUNCH 16 /* AdamW / norm tables; the host splits larger lists */
@@ -135,9 +136,10 @@ int32_t hbt_sgd_step(void* const* params, void* const* grads, void* const* momen
  *   summed by distributed_gradient_norm (optim/sharded_optimizer.py:236-238).
  * Computes sum_i weights[i] * sum_j (double)(R_G(g_ij * unscale))^2 over up to
  * HBT_MAX_TENSORS_PER_LAUNCH gradient tensors (grad_dtype F32, BF16 or F16; R_G rounds
- * the unscaled value to that dtype, as the in-place unscale would have stored it),
- * writing hbt_norm_partials_count(numels, count, grad_dtype) doubles to partials: one
- * per chunk of consecutive elements of one tensor (32768 fp32 or 65536 bf16/fp16),
+ * the unscaled value to that dtype, as the in-place unscale would have stored it; or F64
+ * with unscale 1, each square one rounded double product), writing
+ * hbt_norm_partials_count(numels, count, grad_dtype) doubles to partials: one per chunk
+ * of consecutive elements of one tensor (32768 fp32, 65536 bf16/fp16, 16384 float64),
  * already multiplied by that tensor's weight.  The chunk -> partial map and every summation order depend only on the
  * numels, so the result is bitwise reproducible.  A non-finite element makes the
  * sum non-finite, which is the overflow signal of GradScaler._detect_non_finite
@@ -155,15 +157,17 @@ int32_t hbt_grad_sqnorm_partials(const void* const* grads, const int64_t* numels
  *   (optim/sharded_optimizer.py:241) and the clip-coefficient arithmetic of
  *   ShardedOptimizer.clip_grad_norm (optim/sharded_optimizer.py:331-337).
  * Writes sum_out[0] = the fp64 sum (if sum_out is non-NULL) and norm_out[0] =
- * sqrt(max(sum, 0)) (if norm_out is non-NULL).  If grad_mul_out is non-NULL it writes
- * fp32(max_norm / (norm + 1e-6)) when max_norm > 0 and that quotient is < 1, else
- * 1.0f.  If nonfinite_out is non-NULL it writes 1 when the sum is not finite, else 0.
- * In a multi-rank job the stage-1 sum is what an fp64 all-reduce would combine
+ * sqrt(max(sum, 0)) (if norm_out is non-NULL).  The clip multiplier is
+ * coef = max_norm / (norm + 1e-6) when max_norm > 0 and coef < 1, else 1: grad_mul_out
+ * (if non-NULL) receives fp32(coef), the value torch multiplies fp32, bf16 and fp16
+ * gradients by, and grad_mul64_out (if non-NULL) the double coef float64 gradients are
+ * multiplied by.  If nonfinite_out is non-NULL it writes 1 when the sum is not finite,
+ * else 0.  In a multi-rank job the stage-1 sum is what an fp64 all-reduce would combine
  * between the two stages.
  * ---------------------------------------------------------------------------- */
 int32_t hbt_grad_norm_finalize(const double* partials, int64_t count, double max_norm,
                                double* sum_out, double* norm_out, float* grad_mul_out,
-                               int32_t* nonfinite_out, void* stream);
+                               double* grad_mul64_out, int32_t* nonfinite_out, void* stream);
 
 /* ------------------------------------------------------------------------------
  * Weighted squared norm and clip coefficient with no allocation and no workspace.
@@ -175,7 +179,9 @@ int32_t hbt_grad_norm_finalize(const double* partials, int64_t count, double max
  * same summation order, so the outputs are bitwise equal), but keeps the partials in
  * a static device array of HBT_NOALLOC_MAX_PARTIALS doubles (2 MiB per device, held
  * until the process ends) instead of a caller workspace.  It calls no hipMalloc,
- * hipFree or other allocating routine.
+ * hipFree or other allocating routine.  grad_dtype F32, BF16 or F16 (F64 returns
+ * HBT_ERR_UNSUPPORTED).  The first call on a device looks up the array's device address;
+ * make it outside graph capture.
  * Limit: hbt_norm_partials_count(numels, count, grad_dtype) must not exceed
  * HBT_NOALLOC_MAX_PARTIALS (8,589,934,592 fp32 or 17,179,869,184 bf16 elements per
  * call); a larger request returns HBT_ERR_UNSUPPORTED before any launch.
@@ -210,8 +216,9 @@ int32_t hbt_grad_norm_noalloc(const void* const* grads, const int64_t* numels, c
  * ceil(numel / hbt_copy_chunk_elems(src_dtype, dst_dtype)), and total_chunks is the
  * sum.  A chunk is 1 KB of source: 128 elements of an 8-byte source, 256 of a 4-byte
  * one, 512 of a 2-byte one, except 2 KB (1024 elements) for BF16/F16 -> F32, whose
- * workgroups write twice what they read; hbt_copy_chunk_elems returns -1 for F64 -> F64 (a same-dtype
- * 8-byte copy travels as F32 dword pairs) and for unknown dtypes.  All records share src_dtype/dst_dtype and op:
+ * workgroups write twice what they read; hbt_copy_chunk_elems returns -1 for unknown dtypes.
+ * A same-dtype F64 COPY travels as F32 dword pairs (the numels doubled); F64 -> F64 with
+ * src_dtype = dst_dtype = F64 is the DIVIDE op's.  All records share src_dtype/dst_dtype and op:
  *   HBT_COPY_OP_COPY    dst = src               (same dtype: byte copy; F32->BF16
  *                                                rounds to nearest even, NaN -> 0x7FC0;
  *                                                F32->F16 rounds to nearest even, overflows
@@ -228,7 +235,9 @@ int32_t hbt_grad_norm_noalloc(const void* const* grads, const int64_t* numels, c
  *                                                widen exactly)
  *   HBT_COPY_OP_DIVIDE  dst = src / divisor     (true fp32 division, in fp32 for F32, BF16
  *                                                and F16 data, result rounded to dst_dtype;
- *                                                not for F64 or BF16 <-> F16 pairs)
+ *                                                F64 -> F64 divides in double, correctly
+ *                                                rounded, as div_ on a float64 tensor does;
+ *                                                not for other F64 or BF16 <-> F16 pairs)
  * Source and destination ranges of one call must not overlap.  Addresses need no
  * particular alignment.
  *
@@ -393,6 +402,37 @@ int32_t hbt_scale_inplace(void* const* tensors, const int64_t* numels, int32_t c
  * ---------------------------------------------------------------------------- */
 int32_t hbt_scale_inplace_sqnorm(void* const* tensors, const int64_t* numels, int32_t count,
                                  int32_t dtype, float unscale, double* partials, void* stream);
+
+/* ------------------------------------------------------------------------------
+ * Float64 parameters: the fused clip + AdamW step, the fused clip + SGD step and the
+ * in-place gradient scaling on float64 tensors, with double scalars.
+ *
+ * Replaces: the same reference lines as hbt_adamw_step, hbt_sgd_step and hbt_scale_inplace,
+ *   for the float64 masters the reference steps when mixed precision is off and the
+ *   parameters are float64 (parallel/fsdp.py:379-393; config.py:55-56 accepts "float64"),
+ *   and torch.optim.AdamW / SGD on float64 tensors (optim/sharded_optimizer.py:111-126).
+ * On float64 tensors torch uses every Python scalar as the double it is, so these take
+ * double scalars and compute in double: per element, the op sequences documented for
+ * hbt_adamw_step and hbt_sgd_step with R_G and R_P the identity, each operation one
+ * correctly rounded double result (fma fused), sqrt and the divisions correctly rounded.
+ * The host computes the scalars as torch does (decay = 1 - lr*wd, lerp_weight = 1 - beta1,
+ * bias_correction2_sqrt = (1 - beta2^step)^0.5, neg_step_size = -lr / (1 - beta1^step);
+ * for SGD the unrounded alphas).  grad_mul: the double clip multiplier
+ * (hbt_grad_norm_finalize's grad_mul64_out) or NULL for 1.  flags as for hbt_adamw_step /
+ * hbt_sgd_step.  hbt_scale_inplace_f64 multiplies x = (x * unscale) * (*grad_mul), each
+ * product rounded in double, and reads and writes nothing when both factors are 1.
+ * ---------------------------------------------------------------------------- */
+int32_t hbt_adamw_step_f64(double* const* params, double* const* grads, double* const* exp_avgs,
+                           double* const* exp_avg_sqs, const int64_t* numels, int32_t count, double unscale,
+                           const double* grad_mul, double decay, double lerp_weight, double beta2,
+                           double one_minus_beta2, double bias_correction2_sqrt, double eps, double neg_step_size,
+                           int32_t flags, void* stream);
+int32_t hbt_sgd_step_f64(double* const* params, double* const* grads, double* const* momentum_buffers,
+                         const int64_t* numels, int32_t count, double unscale, const double* grad_mul,
+                         double weight_decay, double momentum, double one_minus_dampening, double neg_lr,
+                         int32_t flags, void* stream);
+int32_t hbt_scale_inplace_f64(double* const* tensors, const int64_t* numels, int32_t count, double unscale,
+                              const double* grad_mul, void* stream);
 
 #ifdef __cplusplus
 }

@@ -26,8 +26,10 @@ __all__ = [
     "PINNED_BY",
     "adamw_scalars",
     "adamw_step",
+    "adamw_step_f64",
     "bucket_layout",
     "clip_multiplier",
+    "clip_multiplier64",
     "even_shards",
     "f16_nan_rules",
     "f32_to_bf16",
@@ -40,7 +42,9 @@ __all__ = [
     "read_range",
     "round_to",
     "sgd_step",
+    "sgd_step_f64",
     "sqnorm",
+    "sqnorm_f64",
     "to_bits",
     "unpack_full",
 ]
@@ -83,6 +87,14 @@ PINNED_BY = {
     "round_to": "torch Tensor.to(bfloat16 / float16).to(float32) bitwise on specials and random values",
     "f16_nan_rules": "torch's vectorised CPU Tensor.to (x86 F16C) bitwise on all 65,536 fp16 bit patterns "
     "(widening) and on NaN payloads of both signs, signalling and quiet (narrowing)",
+    "adamw_step_f64": "torch.optim.AdamW(foreach=False) stepping float64 CPU tensors: bitwise over 10 steps on "
+    "both lerp branches, with and without weight decay and clip, with torch's own sqrt injected, within 1e-15 "
+    "relative otherwise; step 1's closed form; a separately rounded addcmul product is shown to differ",
+    "sgd_step_f64": "torch.optim.SGD(foreach=False) stepping float64 CPU tensors, bitwise, for every "
+    "combination of momentum, dampening, weight decay and Nesterov",
+    "sqnorm_f64": "math.fsum of the rounded double squares; torch's float64 pow(2).sum()",
+    "clip_multiplier64": "the reference's Python-double coefficient: known answer norm 6 -> 1/(6+1e-6), "
+    "and torch's grad.mul_(coef) on float64 tensors bitwise",
 }
 
 
@@ -107,6 +119,13 @@ def library() -> ctypes.CDLL:
         lib.oracle_f32_to_bf16.argtypes = [f32p, u16p, i64]
         lib.oracle_f32_to_f16.restype = None
         lib.oracle_f32_to_f16.argtypes = [f32p, u16p, i64]
+        cd = ctypes.c_double
+        lib.oracle_adamw_f64.restype = None
+        lib.oracle_adamw_f64.argtypes = [vp, vp, vp, vp, i64, cd, cd, cd, cd, cd, cd, cd, cd, cd, vp, vp]
+        lib.oracle_sgd_f64.restype = None
+        lib.oracle_sgd_f64.argtypes = [vp, vp, vp, i64, cd, cd, ci, cd, ci, cd, cd, ci, cd, vp]
+        lib.oracle_sqnorm_f64.restype = cd
+        lib.oracle_sqnorm_f64.argtypes = [vp, i64]
         _LIB = lib
     return _LIB
 
@@ -270,6 +289,45 @@ def clip_multiplier(norm: float, max_norm: float) -> float:
     return float(np.float32(coef)) if coef < 1.0 else 1.0
 
 
+def clip_multiplier64(norm: float, max_norm: float) -> float:
+    """The double a float64 gradient is multiplied by (sharded_optimizer.py:331-337): the
+    Python-double coefficient itself when it is below 1, else exactly 1."""
+    if max_norm <= 0:
+        return 1.0
+    coef = float(max_norm) / (float(norm) + 1e-6)
+    return coef if coef < 1.0 else 1.0
+
+
+def _f64(a: np.ndarray) -> ctypes.c_void_p:
+    assert a.dtype == np.float64 and a.flags.c_contiguous, a.dtype
+    return ctypes.c_void_p(a.ctypes.data)
+
+
+def adamw_step_f64(p, g, m, v, scalars, *, unscale=1.0, grad_mul=1.0, sqrt_override=None, grad_out=None) -> None:
+    """One AdamW step in place on float64 ``p, m, v`` with float64 ``g`` and the double
+    scalars of :func:`adamw_scalars`, as torch steps float64 tensors."""
+    g = np.ascontiguousarray(g, np.float64)
+    root = None if sqrt_override is None else np.ascontiguousarray(sqrt_override, np.float64)
+    library().oracle_adamw_f64(_f64(p), _f64(g), _f64(m), _f64(v), p.size, unscale, grad_mul, *scalars,
+                               None if root is None else _f64(root), None if grad_out is None else _f64(grad_out))
+
+
+def sgd_step_f64(p, g, buf, *, lr, momentum=0.0, dampening=0.0, weight_decay=0.0, nesterov=False, first=False,
+                 unscale=1.0, grad_mul=1.0, grad_out=None) -> None:
+    """One SGD step in place on float64 ``p`` (and ``buf``), the alphas unrounded."""
+    g = np.ascontiguousarray(g, np.float64)
+    mode = 0 if momentum == 0 else (1 if first else 2)
+    library().oracle_sgd_f64(_f64(p), _f64(g), _f64(buf) if mode else None, p.size, unscale, grad_mul,
+                             int(weight_decay != 0), weight_decay, mode, momentum, 1 - dampening, int(nesterov),
+                             -lr, None if grad_out is None else _f64(grad_out))
+
+
+def sqnorm_f64(g: np.ndarray) -> float:
+    """Compensated sum of the rounded double squares of float64 ``g``."""
+    g = np.ascontiguousarray(g, np.float64)
+    return float(library().oracle_sqnorm_f64(_f64(g), g.size))
+
+
 def f16_nan_rules():
     """(widen, narrow): fp16 -> fp32 and fp32 -> fp16 on bit patterns, NaN bits included.
 
@@ -377,7 +435,7 @@ def round_to(x: np.ndarray, reduce: str = "float32") -> np.ndarray:
 
 
 def local_share(rank_grads: Sequence[np.ndarray], rank: int, shard: int, valid: int,
-                divisor: float, reduce: str = "float32") -> np.ndarray:
+                divisor: float, reduce: str = "float32", out: str = "float32") -> np.ndarray:
     """fp32 shard ``rank`` of the AVG reduce-scatter in the reduce dtype, summed in rank
     order (parallel/fsdp.py:733-769, distributed/collectives.py:593-594): each rank's
     slice cast to ``reduce``, divided by ``divisor`` and added, every result rounded to
@@ -386,16 +444,17 @@ def local_share(rank_grads: Sequence[np.ndarray], rank: int, shard: int, valid: 
 
     ``reduce="float64"`` widens each slice to float64 (the rank grads may then also be
     float64 arrays, the no_sync accumulator's rows), divides and sums in float64 and
-    rounds the sum once to fp32 (``Tensor.to``, round to nearest even)."""
+    rounds the sum once to fp32 (``Tensor.to``, round to nearest even), or, with
+    ``out="float64"`` (a float64 master), keeps the float64 sum."""
     if reduce == "float64":
         div64 = np.float64(divisor)
         with np.errstate(over="ignore", invalid="ignore"):
             acc64 = np.asarray(rank_grads[0], dtype=np.float64)[rank * shard : (rank + 1) * shard] / div64
             for g in rank_grads[1:]:
                 acc64 = acc64 + np.asarray(g, dtype=np.float64)[rank * shard : (rank + 1) * shard] / div64
-            out = acc64.astype(np.float32)
-        out[valid:] = 0.0
-        return out
+            result = acc64.copy() if out == "float64" else acc64.astype(np.float32)
+        result[valid:] = 0.0
+        return result
     div = np.float32(divisor)
 
     def term(g: np.ndarray) -> np.ndarray:

@@ -61,6 +61,14 @@
  *       GradScaler.unscale_ stores.
  *   oracle_f32_to_bf16 - round-to-nearest-even narrowing with NaN -> 0x7FC0, the
  *       conversion behind Tensor.to(torch.bfloat16).
+ *   oracle_adamw_f64, oracle_sgd_f64, oracle_sqnorm_f64 - the same three on float64
+ *       tensors, whose every operation torch computes in double with the Python scalars
+ *       unrounded (adam.py:396-547 and _single_tensor_sgd on float64; the reference's
+ *       masters are float64 when the parameters are and mixed precision is off,
+ *       parallel/fsdp.py:379-393): the op sequences above with every rounding the
+ *       identity of double arithmetic, fma() where the fp32 restatement has fmaf(), the
+ *       unscale and clip multiplies by the double factors, each square one rounded
+ *       double product (g.to(float64).pow(2)).
  */
 #include <math.h>
 #include <stdint.h>
@@ -244,6 +252,56 @@ double oracle_sqnorm(const void* g, int64_t n, int gdt, float unscale) {
         neumaier_add(&sum, &comp, x * x);
     }
     return isfinite(sum) ? sum + comp : sum; /* an inf square keeps the sum inf */
+}
+
+void oracle_adamw_f64(double* p, const double* g, double* m, double* v, int64_t n, double unscale, double grad_mul,
+                      double decay, double lerp_w, double beta2, double one_minus_beta2, double bc2_sqrt, double eps,
+                      double neg_step, const double* sqrt_override, double* grad_out) {
+    const int lerp_small = fabs(lerp_w) < 0.5;
+    const double lerp_w_minus_1 = lerp_w - 1.0;
+    for (int64_t i = 0; i < n; ++i) {
+        double gi = g[i];
+        if (unscale != 1.0) gi = gi * unscale;
+        gi = gi * grad_mul;
+        if (grad_out != 0) grad_out[i] = gi;
+        const double pi = p[i] * decay;
+        const double diff = gi - m[i];
+        const double mi = lerp_small ? fma(lerp_w, diff, m[i]) : fma(lerp_w_minus_1, diff, gi);
+        double vi = v[i] * beta2;
+        vi = fma(one_minus_beta2 * gi, gi, vi);
+        const double root = sqrt_override != 0 ? sqrt_override[i] : sqrt(vi);
+        const double denom = root / bc2_sqrt + eps;
+        p[i] = pi + (neg_step * mi) / denom;
+        m[i] = mi;
+        v[i] = vi;
+    }
+}
+
+/* mode as for oracle_sgd; every alpha is the unrounded double. */
+void oracle_sgd_f64(double* p, const double* g, double* buf, int64_t n, double unscale, double grad_mul,
+                    int apply_wd, double wd, int mode, double momentum, double one_minus_dampening, int nesterov,
+                    double neg_lr, double* grad_out) {
+    for (int64_t i = 0; i < n; ++i) {
+        double x = g[i];
+        if (unscale != 1.0) x = x * unscale;
+        x = x * grad_mul;
+        if (grad_out != 0) grad_out[i] = x;
+        const double pi = p[i];
+        if (apply_wd) x = fma(pi, wd, x);
+        if (mode == 1) {
+            buf[i] = x;
+        } else if (mode == 2) {
+            buf[i] = fma(x, one_minus_dampening, buf[i] * momentum);
+        }
+        if (mode != 0) x = nesterov ? fma(buf[i], momentum, x) : buf[i];
+        p[i] = fma(x, neg_lr, pi);
+    }
+}
+
+double oracle_sqnorm_f64(const double* g, int64_t n) {
+    double sum = 0.0, comp = 0.0;
+    for (int64_t i = 0; i < n; ++i) neumaier_add(&sum, &comp, g[i] * g[i]);
+    return isfinite(sum) ? sum + comp : sum;
 }
 
 void oracle_f32_to_bf16(const float* x, uint16_t* out, int64_t n) {

@@ -44,7 +44,8 @@ int main(void) {
     }
     // bad dtypes and pointers
     EXPECT(hbt_grad_sqnorm_partials(cptrs, numels, weights, 1, 7, 1.0f, partials, NULL) == HBT_ERR_INVALID_ARGUMENT);
-    EXPECT(hbt_scale_inplace_sqnorm(ptrs, numels, 1, 3, 0.5f, partials, NULL) == HBT_ERR_INVALID_ARGUMENT);
+    EXPECT(hbt_scale_inplace_sqnorm(ptrs, numels, 1, HBT_DTYPE_F64, 0.5f, partials, NULL) == HBT_ERR_UNSUPPORTED);
+    EXPECT(hbt_scale_inplace_sqnorm(ptrs, numels, 1, 7, 0.5f, partials, NULL) == HBT_ERR_INVALID_ARGUMENT);
     EXPECT(hbt_scale_inplace_sqnorm(ptrs, numels, 1, HBT_DTYPE_F32, 0.5f, NULL, NULL) == HBT_ERR_INVALID_ARGUMENT);
     EXPECT(hbt_scale_inplace_sqnorm(NULL, numels, 1, HBT_DTYPE_F32, 0.5f, partials, NULL) == HBT_ERR_INVALID_ARGUMENT);
     numels[0] = -1;
@@ -79,7 +80,14 @@ int main(void) {
     EXPECT(hbt_copy_intervals((const int64_t*)buf, 0, 0, HBT_DTYPE_F32, HBT_DTYPE_F32, HBT_COPY_OP_COPY, 1.0f, 0, NULL) == HBT_OK);
     EXPECT(hbt_copy_intervals((const int64_t*)buf, 1, 1, 9, HBT_DTYPE_F32, HBT_COPY_OP_COPY, 1.0f, 0, NULL) == HBT_ERR_INVALID_ARGUMENT);
     // finalize and the no-allocation norm: argument checks
-    EXPECT(hbt_grad_norm_finalize(NULL, 3, 1.0, NULL, NULL, NULL, NULL, NULL) == HBT_ERR_INVALID_ARGUMENT);
+    EXPECT(hbt_grad_norm_finalize(NULL, 3, 1.0, NULL, NULL, NULL, NULL, NULL, NULL) == HBT_ERR_INVALID_ARGUMENT);
+    // float64 entry points: argument checks
+    EXPECT(hbt_adamw_step_f64(NULL, NULL, NULL, NULL, NULL, HBT_MAX_TENSORS_PER_LAUNCH + 1, 1.0, NULL, 1.0, 0.1, 0.9,
+                              0.1, 1.0, 1e-8, -1e-3, 0, NULL) == HBT_ERR_INVALID_ARGUMENT);
+    EXPECT(hbt_sgd_step_f64(NULL, NULL, NULL, NULL, 0, 1.0, NULL, 0.0, 0.0, 1.0, -0.1, HBT_SGD_NESTEROV, NULL)
+           == HBT_ERR_INVALID_ARGUMENT);
+    EXPECT(hbt_scale_inplace_f64(NULL, NULL, 2, 1.0, NULL, NULL) == HBT_ERR_INVALID_ARGUMENT);
+    EXPECT(hbt_norm_partials_count(numels, 1, HBT_DTYPE_F64) >= 0);
     EXPECT(hbt_grad_norm_noalloc(cptrs, numels, weights, HBT_MAX_TENSORS_PER_LAUNCH + 1, HBT_DTYPE_F32, 1.0f, 1.0,
                                  NULL, NULL, NULL, NULL, NULL) != HBT_OK);
     (void)hbt_last_error();

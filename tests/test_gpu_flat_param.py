@@ -281,8 +281,9 @@ def test_local_share_with_ieee_specials_matches_oracle(device, group, in_dtype, 
 
 def test_reduce_and_master_dtype_limits(device):
     """A bf16 master shard (mixed precision with ``master_dtype="bfloat16"``) packs and
-    reduces into bf16; a float64 master packs (the copy kernel converts into float64) but
-    its gradient has no local-share kernel, so the reduction refuses it up front."""
+    reduces into bf16; a float64 master packs (the copy kernel converts into float64) and
+    reduces in float64 into a float64 gradient shard, padding zero; float64 gradients
+    with a narrower reduce dtype are refused up front."""
     named = _params(MLP_1857_REFERENCE, device)
     mp = MixedPrecisionConfig(enabled=True, master_dtype="bfloat16")
     h = FlatParamHandle(named, None, GroupHandle.trivial("shard"), FSDPConfig(), mp, device, keep_originals=True)
@@ -295,8 +296,14 @@ def test_reduce_and_master_dtype_limits(device):
     mp = MixedPrecisionConfig(enabled=True, reduce_dtype="float64", master_dtype="float64")
     h = FlatParamHandle(named, None, GroupHandle.trivial("shard"), FSDPConfig(), mp, device, keep_originals=True)
     assert torch.equal(h.flat_param.detach()[: flat.numel()], flat.to(torch.float64))
-    with pytest.raises(UnsupportedFeatureError, match="float32, bfloat16 or float16 master shard"):
-        h.reduce_scatter_gradient(torch.zeros(h.padded_numel, device=device))
+    out = h.reduce_scatter_gradient(grad)
+    expect = grad.to(torch.float64)
+    expect[h.total_numel:] = 0.0
+    assert out.dtype == torch.float64 and torch.equal(out, expect)
+    mp = MixedPrecisionConfig(enabled=True, param_dtype="float64", reduce_dtype="float32")
+    h = FlatParamHandle(named, None, GroupHandle.trivial("shard"), FSDPConfig(), mp, device, keep_originals=True)
+    with pytest.raises(UnsupportedFeatureError, match="float64 gradients are reduced in float64"):
+        h.reduce_scatter_gradient(torch.zeros(h.padded_numel, dtype=torch.float64, device=device))
 
 
 def test_local_share_needs_every_rank(device):

@@ -113,7 +113,7 @@ def test_unscale_return_value_is_the_overflow_flag(device):
 def test_unscale_refuses_gradients_the_kernel_cannot_address(device):
     """The in-place scale reads ``numel`` consecutive elements from a gradient's address:
     a strided gradient is refused (``ShardingError``) rather than scaled in the wrong
-    places, and a float64 gradient, which the kernel does not take, is refused up front."""
+    places, and a float64 one is unscaled in double."""
     scaler = GradScaler(GradScalerConfig(enabled=True, init_scale=1024.0), GroupHandle.trivial(), device)
     p = torch.nn.Parameter(torch.zeros(10, device=device))
     storage = torch.arange(20.0, device=device)
@@ -123,8 +123,8 @@ def test_unscale_refuses_gradients_the_kernel_cannot_address(device):
     assert torch.equal(storage, torch.arange(20.0, device=device))  # nothing was touched
     q = torch.nn.Parameter(torch.zeros(10, device=device, dtype=torch.float64))
     q.grad = torch.ones(10, device=device, dtype=torch.float64)
-    with pytest.raises(UnsupportedFeatureError, match="float32, bfloat16 or float16"):
-        scaler.unscale_([q])
+    assert not scaler.unscale_([q])
+    assert torch.equal(q.grad, torch.full((10,), 1.0 / 1024.0, dtype=torch.float64, device=device))
 
 
 def test_llama3_70b_rank_shard_full_size(device):

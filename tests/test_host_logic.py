@@ -191,14 +191,19 @@ def test_oracle_float64_local_share_against_torch_and_exact_mean(dtype):
     for group, shard, pad in ((1, 9, 2), (2, 7, 1), (3, 8, 3), (4, 6, 0), (8, 5, 4)):
         total = group * shard - pad
         grads = [(torch.randn(group * shard, generator=gen) * 3.0).to(dtype) for _ in range(group)]
-        summed = functools.reduce(torch.add, [g.to(torch.float64).div(group) for g in grads]).to(torch.float32)
-        summed[total:] = 0.0
+        wide = functools.reduce(torch.add, [g.to(torch.float64).div(group) for g in grads])
+        wide[total:] = 0.0
+        summed = wide.to(torch.float32)
         host = [g.float().numpy() for g in grads]
         for rank in range(group):
             valid = max(0, min(shard, total - rank * shard))
             got = oracle.local_share(host, rank, shard, valid, float(group), "float64")
             assert got.dtype == np.float32
             assert np.array_equal(got.view(np.uint32), summed[rank * shard:(rank + 1) * shard].numpy().view(np.uint32))
+            # a float64 master keeps the float64 sum: torch's ops without the final cast
+            kept = oracle.local_share(host, rank, shard, valid, float(group), "float64", out="float64")
+            want = wide[rank * shard:(rank + 1) * shard].numpy()
+            assert kept.dtype == np.float64 and np.array_equal(kept.view(np.uint64), want.view(np.uint64))
             if group & (group - 1) == 0:
                 for i in range(valid):
                     exact = sum(Fraction(float(h[rank * shard + i])) for h in host) / group

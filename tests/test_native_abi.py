@@ -71,7 +71,8 @@ def test_library_loads_and_exports_every_declared_symbol():
     assert lib.hbt_copy_chunk_elems(0, 0) == 256 and lib.hbt_copy_chunk_elems(1, 1) == 512
     assert lib.hbt_copy_chunk_elems(0, 1) == 256 and lib.hbt_copy_chunk_elems(1, 0) == 1024
     assert lib.hbt_copy_chunk_elems(2, 0) == 1024 and lib.hbt_copy_chunk_elems(0, 2) == 256
-    assert lib.hbt_copy_chunk_elems(3, 3) == -1
+    assert lib.hbt_copy_chunk_elems(3, 3) == 128  # the float64 AVG divide: 1 KB of source
+    assert lib.hbt_copy_chunk_elems(9, 0) == -1
     assert lib.hbt_last_error() == b""
 
 
@@ -114,10 +115,29 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     assert lib.hbt_copy_intervals(fake, 1, 1, 3, 0, 1, 2.0, 0, None) == -2
     assert lib.hbt_copy_intervals(fake, 1, 1, 1, 2, 1, 2.0, 0, None) == -2
     assert lib.hbt_copy_chunk_elems(3, 0) == 128 and lib.hbt_copy_chunk_elems(0, 3) == 256
-    assert lib.hbt_copy_chunk_elems(1, 2) == 512 and lib.hbt_copy_chunk_elems(3, 3) == -1
+    assert lib.hbt_copy_chunk_elems(1, 2) == 512 and lib.hbt_copy_chunk_elems(3, 3) == 128
     assert lib.hbt_grad_accumulate(None, None, None, 0, 0, 0, 2, None) == -1  # unknown flag
     assert lib.hbt_grad_accumulate(None, None, None, 1, 0, 0, 0, None) == -1  # null table
-    assert lib.hbt_grad_norm_finalize(None, 5, 1.0, None, None, None, None, None) == -1
+    assert lib.hbt_grad_norm_finalize(None, 5, 1.0, None, None, None, None, None, None) == -1
+    # float64 steps and scaling: table and flag checks on the host
+    assert lib.hbt_adamw_step_f64(None, None, None, None, None, 99, 1.0, None,
+                                  1.0, 0.1, 0.9, 0.1, 1.0, 1e-8, -1e-3, 0, None) == -1
+    assert b"hbt_adamw_step_f64" in lib.hbt_last_error()
+    assert lib.hbt_adamw_step_f64(None, None, None, None, None, 0, 1.0, None,
+                                  1.0, 0.1, 0.9, 0.1, 1.0, 1e-8, -1e-3, 1, None) == -1  # unknown flag
+    assert lib.hbt_adamw_step_f64(None, None, None, None, None, 0, 1.0, None,
+                                  1.0, 0.1, 0.9, 0.1, 1.0, 1e-8, -1e-3, 16, None) == 0  # empty table
+    assert lib.hbt_sgd_step_f64(None, None, None, None, 0, 1.0, None, 0.0, 0.0, 1.0, -0.1, 2, None) == -1
+    assert lib.hbt_sgd_step_f64(None, None, None, None, 0, 1.0, None, 0.0, 0.0, 1.0, -0.1, 16, None) == 0
+    assert lib.hbt_scale_inplace_f64(None, None, 1, 1.0, None, None) == -1
+    # float64 gradients: the norm takes unscale 1, the fused unscale and the no-allocation norm refuse them
+    assert lib.hbt_grad_sqnorm_partials(_native.pointer_array([4096]), _native.int64_array([1]),
+                                        _native.double_array([1.0]), 1, 3, 0.5, fake, None) == -2
+    assert lib.hbt_scale_inplace_sqnorm(_native.pointer_array([4096]), _native.int64_array([1]), 1, 3, 0.5,
+                                        fake, None) == -2
+    assert lib.hbt_grad_norm_noalloc(_native.pointer_array([4096]), _native.int64_array([1]),
+                                     _native.double_array([1.0]), 1, 3, 1.0, 1.0, None, None, None, None, None) == -2
+    assert lib.hbt_norm_partials_count(_native.int64_array([16384, 16385]), 2, 3) == 3
     # no-allocation norm: bad table, then a request beyond the static scratch, both refused
     # on the host before the scratch address is looked up or anything is launched
     assert lib.hbt_grad_norm_noalloc(None, None, None, 99, 0, 1.0, 1.0, None, None, None, None, None) == -1

@@ -36,7 +36,7 @@ def _run_workspace(lib, grads, weights, dtype_code, unscale, max_norm, device):
         "hbt_grad_sqnorm_partials")
     out = _outputs(device)
     _native.check(lib.hbt_grad_norm_finalize(partials.data_ptr(), count, max_norm, out[0].data_ptr(),
-                                             out[1].data_ptr(), out[2].data_ptr(), out[3].data_ptr(), stream),
+                                             out[1].data_ptr(), out[2].data_ptr(), None, out[3].data_ptr(), stream),
                   "hbt_grad_norm_finalize")
     return out
 
