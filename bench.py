@@ -528,11 +528,13 @@ def bench_scaler(steps: int, warmup: int) -> int:
 
     Clean step with the multipliers deferred (``defer_unscale``, ``defer_clip``): fused
     unscale + inf check + norm (2 B/param) and unscale + clip + AdamW (26 B/param) =
-    28 B/param.  Overflowing step: the check pass only (2 B/param), then skip.  Clean step
+    28 B/param.  Overflowing step: the check pass only (2 B/param), then skip.  Clean steps
     with the reference's placement (the defaults): ``unscale_`` rewrites the gradient and
-    sums the squares of the result in the same pass (read and write bf16: 4 B/param), and
-    the update writes the clipped gradient back (26 + 2 B) = 32 B/param; the gradient is
-    restored from a pristine copy before each such step, outside the timed events.
+    sums the squares of the result in the same pass (read and write bf16: 4 B/param), the
+    clip rewrites it again (4 B/param) and the update reads it (26 B/param) = 34 B/param;
+    with ``clip_in_step`` the update applies the clip and writes the clipped gradient back
+    (26 + 2 B) = 32 B/param.  The gradient is restored from a pristine copy before each such
+    step, outside the timed events.
     """
     import torch
 
@@ -575,44 +577,54 @@ def bench_scaler(steps: int, warmup: int) -> int:
           max(steps, 5), max(warmup, 2), "bf16", "Llama-3-70B FSDP rank shard at W=8, bf16 grads, 0.1% inf",
           2 * n, {"params": n, "bytes_per_param": 2, "skipped": True},
           _secondary_traffic("scaler", ["unscale + check + norm"], [1]), _scaler_cpu_baseline() if _WITH_CPU else None)
-    # The reference's placement: eager unscale_, the clip written back by the update.
+    # The reference's placement: eager unscale_, then the clip (in place on .grad by
+    # default, or fused into the update with clip_in_step), then the update.
     del opt, scaler
     torch.cuda.empty_cache()
-    opt = ShardedOptimizer([param], OptimizerConfig(learning_rate=3e-4, betas=(0.9, 0.95), weight_decay=0.1),
-                           norm_group=GroupHandle.trivial("world"), device=device)
-    scaler = GradScaler(GradScalerConfig(enabled=True, init_scale=65536.0, growth_interval=10**9),
-                        GroupHandle.trivial("world"), device)
     stream = torch.cuda.current_stream(device)
+    placements = [
+        (False, 34, "loss-scaled clipped AdamW step, reference placement (eager unscale_, eager in-place clip): params/s",
+         "defer_unscale=False, defer_clip=False", ["reference placement: eager unscale_ with its overflow check, one pass",
+                                                  "reference placement: eager in-place clip of .grad",
+                                                  "reference placement: AdamW of the clipped gradient"], [1, 1, 1]),
+        (True, 32, "loss-scaled clipped AdamW step, reference placement with the clip in the update: params/s",
+         "defer_unscale=False, clip_in_step=True", ["reference placement: eager unscale_ with its overflow check, one pass",
+                                                   "clip_in_step: clip + AdamW, clipped g written back"], [1, 1]),
+    ]
+    for in_step, per_param, metric, label, traffic_labels, launches in placements:
+        opt = ShardedOptimizer([param], OptimizerConfig(learning_rate=3e-4, betas=(0.9, 0.95), weight_decay=0.1),
+                               norm_group=GroupHandle.trivial("world"), device=device, clip_in_step=in_step)
+        scaler = GradScaler(GradScalerConfig(enabled=True, init_scale=65536.0, growth_interval=10**9),
+                            GroupHandle.trivial("world"), device)
 
-    def eager_step(events=None):
-        grad.copy_(pristine)  # the next backward's gradient (outside the timed events)
-        if events is not None:
-            events[0].record(stream)
-        param.grad = grad
-        scaler.unscale_([param])
-        opt.clip_grad_norm(1.0)
-        scaler.step(opt, [param], already_unscaled=True)
-        scaler.update(found_non_finite=False)
-        if events is not None:
-            events[1].record(stream)
-        opt.zero_grad(set_to_none=True)
+        def eager_step(events=None):
+            grad.copy_(pristine)  # the next backward's gradient (outside the timed events)
+            if events is not None:
+                events[0].record(stream)
+            param.grad = grad
+            scaler.unscale_([param])
+            opt.clip_grad_norm(1.0)
+            scaler.step(opt, [param], already_unscaled=True)
+            scaler.update(found_non_finite=False)
+            if events is not None:
+                events[1].record(stream)
+            opt.zero_grad(set_to_none=True)
 
-    eager_steps, eager_warmup = max(steps, 5), max(warmup, 2)
-    for _ in range(eager_warmup):
-        eager_step()
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(eager_steps)]
-    for e in events:
-        eager_step(e)
-    torch.cuda.synchronize()
-    ms = sum(e[0].elapsed_time(e[1]) for e in events) / eager_steps
-    if bool(torch.equal(grad[:4096], pristine[:4096])):  # the reference's in-place ops rewrite .grad
-        raise RuntimeError("the eager unscale and clip left .grad unchanged")
-    _emit("loss-scaled clipped AdamW step, reference placement (eager unscale_, clip written back): params/s",
-          "params/s", n / (ms * 1e-3), ms, eager_steps, eager_warmup, "f32",
-          "Llama-3-70B FSDP rank shard at W=8, bf16 grads, scale 2^16, defer_unscale=False, defer_clip=False",
-          32 * n, {"params": n, "bytes_per_param": 32, "skipped": False},
-          _secondary_traffic("scaler", ["reference placement: eager unscale_ with its overflow check, one pass",
-                                        "reference placement: clip + AdamW, clipped g written back"], [1, 1]))
+        eager_steps, eager_warmup = max(steps, 5), max(warmup, 2)
+        for _ in range(eager_warmup):
+            eager_step()
+        events = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(eager_steps)]
+        for e in events:
+            eager_step(e)
+        torch.cuda.synchronize()
+        ms = sum(e[0].elapsed_time(e[1]) for e in events) / eager_steps
+        if bool(torch.equal(grad[:4096], pristine[:4096])):  # the reference's in-place ops rewrite .grad
+            raise RuntimeError("the eager unscale and clip left .grad unchanged")
+        _emit(metric, "params/s", n / (ms * 1e-3), ms, eager_steps, eager_warmup, "f32",
+              f"Llama-3-70B FSDP rank shard at W=8, bf16 grads, scale 2^16, {label}",
+              per_param * n, {"params": n, "bytes_per_param": per_param, "skipped": False},
+              _secondary_traffic("scaler", traffic_labels, launches))
+        del opt, scaler
     return 0
 
 

@@ -158,11 +158,53 @@ __device__ __forceinline__ double widen_f64(const unsigned char* p, int64_t i) {
 }
 
 // ---- fixed-order reductions ----------------------------------------------------------
-// Butterfly over the 64 lanes of a wavefront; every lane ends with the same total and
-// the pairing order is fixed, so the result is reproducible bit for bit.
+// A double moved between lanes of each 16-lane row by the DPP control kCtrl (a row
+// rotation or a quad permutation).
+template <int kCtrl>
+__device__ __forceinline__ double dpp_move(double x) {
+    const uint64_t b = static_cast<uint64_t>(__double_as_longlong(x));
+    const uint32_t lo = __builtin_amdgcn_mov_dpp(static_cast<int>(static_cast<uint32_t>(b)), kCtrl, 0xF, 0xF, false);
+    const uint32_t hi = __builtin_amdgcn_mov_dpp(static_cast<int>(static_cast<uint32_t>(b >> 32)), kCtrl, 0xF, 0xF, false);
+    return __longlong_as_double(static_cast<long long>((uint64_t(hi) << 32) | lo));
+}
+// The double of lane ^ M, M = 32 or 16, by the gfx950 half-wave / row swaps: a swap of x
+// with itself leaves the upper half's (odd rows') values in the second result and the
+// lower half's (even rows') in the first; a lane takes the half it is not in.
+template <int M>
+__device__ __forceinline__ double swap_move(double x) {
+    const uint64_t b = static_cast<uint64_t>(__double_as_longlong(x));
+    const uint32_t lo = static_cast<uint32_t>(b), hi = static_cast<uint32_t>(b >> 32);
+    const bool upper = (__lane_id() & M) != 0;
+    uint32_t rlo, rhi;
+    if constexpr (M == 32) {
+        const auto l = __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
+        const auto h = __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
+        rlo = upper ? l[0] : l[1];
+        rhi = upper ? h[0] : h[1];
+    } else {
+        static_assert(M == 16, "row swaps exchange 32- or 16-lane groups");
+        const auto l = __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+        const auto h = __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+        rlo = upper ? l[0] : l[1];
+        rhi = upper ? h[0] : h[1];
+    }
+    return __longlong_as_double(static_cast<long long>((uint64_t(rhi) << 32) | rlo));
+}
+
+// Butterfly over the 64 lanes of a wavefront: x += x[lane ^ m] for m = 32, 16, ..., 1;
+// every lane ends with the same total and the pairing order is fixed, so the result is
+// reproducible bit for bit.  The exchanges are VALU moves, not LDS permutes: m = 32 and 16
+// by the half-wave and row swaps (lane ^ m exactly); m = 8, 4, 2, 1 by row rotations and
+// quad permutations, which read lane i ^ m ^ (a combination of the bits above m).  Those
+// bits are already summed over at that stage (a + b == b + a), so every such lane holds
+// lane i ^ m's value and each lane's sum is bitwise the exchange butterfly's.
 __device__ __forceinline__ double wave_sum(double x) {
-#pragma unroll
-    for (int offset = 32; offset >= 1; offset >>= 1) x += __shfl_xor(x, offset, 64);
+    x += swap_move<32>(x);
+    x += swap_move<16>(x);
+    x += dpp_move<0x128>(x);  // row_ror:8
+    x += dpp_move<0x124>(x);  // row_ror:4
+    x += dpp_move<0x4E>(x);   // quad_perm [2, 3, 0, 1]
+    x += dpp_move<0xB1>(x);   // quad_perm [1, 0, 3, 2]
     return x;
 }
 

@@ -428,33 +428,11 @@ __global__ __launch_bounds__(kAdamBlock) void sgd_kernel(SgdTable tab, SgdScalar
 // 16-byte load per lane (4 fp32 or 8 bf16/fp16 gradients).
 constexpr int kNormBlock = 1024;
 constexpr int kNormTilesPerChunk = 8;
-// Tiles whose loads a thread issues together in a whole chunk (0: the tile loop, which
-// the compiler pipelines by itself for fp32 but not for 2-byte gradients).
-#ifndef HBT_NORM_BATCH_F32
-#define HBT_NORM_BATCH_F32 0
-#endif
-#ifndef HBT_NORM_BATCH_B16
-#define HBT_NORM_BATCH_B16 4
-#endif
-// The same for the pass that also stores the unscaled values (kStore).  Measured on
-// MI355X, in place over 17.6 GB of bf16 (8.82e9 elements): all 8 tiles in flight 5.80 ms,
-// 4 tiles 6.13 ms, the hbt_scale_inplace + hbt_grad_sqnorm_partials pair 8.30 ms; over
-// 8.6 GB of fp32: 4 tiles 2.78 ms, the tile loop 3.13 ms, the pair 3.82 ms.
-#ifndef HBT_NORM_STORE_BATCH_F32
-#define HBT_NORM_STORE_BATCH_F32 4
-#endif
-#ifndef HBT_NORM_STORE_BATCH_B16
-#define HBT_NORM_STORE_BATCH_B16 8
-#endif
+// fp32: tiles whose loads a thread issues together in a whole chunk; 0 is the tile loop,
+// which the compiler pipelines by itself.  The pass that also stores the unscaled values
+// (kStore) issues four.
 template <int GD, bool kStore = false>
-constexpr int norm_batch() {
-    return kStore ? (GD == F32 ? HBT_NORM_STORE_BATCH_F32 : HBT_NORM_STORE_BATCH_B16)
-                  : (GD == F32 ? HBT_NORM_BATCH_F32 : HBT_NORM_BATCH_B16);
-}
-static_assert(HBT_NORM_BATCH_F32 == 0 || kNormTilesPerChunk % HBT_NORM_BATCH_F32 == 0, "whole batches of tiles");
-static_assert(HBT_NORM_BATCH_B16 == 0 || kNormTilesPerChunk % HBT_NORM_BATCH_B16 == 0, "whole batches of tiles");
-static_assert(HBT_NORM_STORE_BATCH_F32 == 0 || kNormTilesPerChunk % HBT_NORM_STORE_BATCH_F32 == 0, "whole batches");
-static_assert(HBT_NORM_STORE_BATCH_B16 == 0 || kNormTilesPerChunk % HBT_NORM_STORE_BATCH_B16 == 0, "whole batches");
+constexpr int norm_batch() { return kStore ? 4 : 0; }
 template <int GD>
 constexpr int norm_vec() { return GD == F32 ? 4 : 8; }
 template <int GD>
@@ -482,6 +460,145 @@ __device__ __forceinline__ double sq(float x) {
     return d * d;
 }
 
+// ---- two-level order of 2-byte gradients -----------------------------------------------
+// A piece is 64 lanes x one 16-byte vector: 512 bf16 / fp16 elements, lane l owning
+// elements 8l .. 8l + 7 of it; a chunk is 128 pieces.  Lane sums add the squares in
+// element order; a piece's sum is the butterfly (shfl_xor 32, 16, ..., 1) of its lane
+// sums; a chunk's partial is the butterfly of s_l + s_(l+64) over lanes l = 0..63, times the
+// tensor's weight.  Two passes compute it: the plain norm below (1024 threads per chunk,
+// wave w summing pieces 16k + w, k = 0..7), and the in-place unscale fused with it
+// (one wave per piece, then one wave per chunk), whose every piece moves 1 KB in and out in
+// a workgroup that retires at once.  Both give bitwise the same partials.
+constexpr int kPiecesPerChunk = 128;
+constexpr int64_t kPieceB16 = 64 * 8;
+
+// acc + x * x in double with one rounding: the square of an fp32 value (24-bit significand,
+// exponent range far inside double's) is exact in double, so the fused multiply-add rounds
+// exactly where acc + sq(x) rounds, in one instruction.
+__device__ __forceinline__ double add_sq(double acc, float x) {
+    const double d = static_cast<double>(x);
+    return __builtin_fma(d, d, acc);
+}
+
+// Two fp32 values rounded to the 2-byte dtype RD (nearest even) and packed low half first by
+// one packed conversion: the bits store_vec<RD> writes for them, except that a bf16 NaN keeps
+// the conversion's encoding (a caller that stores it writes 0x7FC0 instead).
+template <int RD>
+__device__ __forceinline__ uint32_t pack2_rounded(float a, float b) {
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    if constexpr (RD == BF16) {
+        typedef __bf16 r2 __attribute__((ext_vector_type(2)));
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{opaque(a), opaque(b)}, r2));
+    } else {
+        static_assert(RD == F16, "2-byte dtypes are bf16 and fp16");
+        typedef _Float16 r2 __attribute__((ext_vector_type(2)));
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{opaque(a), opaque(b)}, r2));
+    }
+}
+
+// Eight fp32 values rounded to the 2-byte dtype RD and packed into one 16-byte vector, a
+// bf16 NaN as 0x7FC0: the vector store_vec<RD, 8> writes for them, in 4 conversions and 8
+// compares where the float round trip through round_to and f32_to_b16 takes about 7
+// operations per element.
+template <int RD>
+__device__ __forceinline__ u32x4 pack8_rounded(const float (&y)[8]) {
+    u32x4 o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = pack2_rounded<RD>(y[2 * i], y[2 * i + 1]);
+    if constexpr (RD == BF16) {
+        bool nan = false;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) nan = nan || y[c] != y[c];
+        if (nan) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if (y[2 * i] != y[2 * i]) o[i] = (o[i] & 0xFFFF0000u) | 0x7FC0u;
+                if (y[2 * i + 1] != y[2 * i + 1]) o[i] = (o[i] & 0xFFFFu) | 0x7FC00000u;
+            }
+        }
+    }
+    return o;
+}
+
+// A lane's eight elements of a piece from element e0 (its first), squared after the
+// unscale: vector loads when the whole lane vector lies inside and is aligned.
+template <int GD, bool kUnscale>
+__device__ __forceinline__ double lane_sq_b16(const void* G, int64_t e0, int64_t n, bool vec, float unscale) {
+    double acc = 0.0;
+    if (vec) {
+        float x[8];
+        load_vec<GD, 8>(G, e0, x);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) acc = add_sq(acc, kUnscale ? round_to<GD>(x[c] * unscale) : x[c]);
+    } else {
+        for (int c = 0; c < 8 && e0 + c < n; ++c) {
+            const float y = load_one<GD>(G, e0 + c);
+            acc = add_sq(acc, kUnscale ? round_to<GD>(y * unscale) : y);
+        }
+    }
+    return acc;
+}
+
+// The eight piece sums of one wave (pieces 16k + w, a[k] its lane sums) by a reduce-scatter
+// butterfly: at stage xor 32 a lane keeps pieces 0-3 or 4-7 and adds its partner's, and so
+// on, so each piece's sum is the butterfly's bitwise (the same pairs at every stage, and
+// addition commutes) for 10 shuffles instead of 48.  Lane l ends with the sum of piece
+// 16 (l >> 3) + w.
+__device__ __forceinline__ double piece_sums8(const double (&a)[8], int lane) {
+    const bool h5 = lane & 32, h4 = lane & 16, h3 = lane & 8;
+    double b[4], c[2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) b[i] = (h5 ? a[4 + i] : a[i]) + __shfl_xor(h5 ? a[i] : a[4 + i], 32, 64);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) c[i] = (h4 ? b[2 + i] : b[i]) + __shfl_xor(h4 ? b[i] : b[2 + i], 16, 64);
+    double d = (h3 ? c[1] : c[0]) + __shfl_xor(h3 ? c[0] : c[1], 8, 64);
+    d += __shfl_xor(d, 4, 64);
+    d += __shfl_xor(d, 2, 64);
+    d += __shfl_xor(d, 1, 64);
+    return d;
+}
+
+// The plain pass for 2-byte gradients: chunk c's partial in the two-level order.
+template <int GD, bool kUnscale>
+__device__ __forceinline__ void sqnorm_b16_chunk(const NormTable& tab, float unscale, double* __restrict__ partials,
+                                                 int64_t chunk) {
+    __shared__ double piece_sums[kPiecesPerChunk];
+    const int t = owning_tensor(tab.first_chunk, tab.count, chunk);
+    const int64_t start = (chunk - tab.first_chunk[t]) * kPieceB16 * kPiecesPerChunk;
+    const int64_t n = tab.n[t];
+    const void* G = tab.g[t];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    double a[8];
+    if (tab.vec_ok[t] && start + kPieceB16 * kPiecesPerChunk <= n) {
+        // whole chunk: four pieces' loads in flight before the first is summed
+#pragma unroll
+        for (int k0 = 0; k0 < 8; k0 += 4) {
+            float x[4][8];
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                load_vec<GD, 8>(G, start + int64_t((k0 + k) * 16 + w) * kPieceB16 + int64_t(lane) * 8, x[k]);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                a[k0 + k] = 0.0;
+#pragma unroll
+                for (int c = 0; c < 8; ++c) a[k0 + k] = add_sq(a[k0 + k], kUnscale ? round_to<GD>(x[k][c] * unscale) : x[k][c]);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            a[k] = lane_sq_b16<GD, kUnscale>(G, start + int64_t(k * 16 + w) * kPieceB16 + int64_t(lane) * 8, n, false,
+                                             unscale);
+    }
+    const double d = piece_sums8(a, lane);
+    if ((lane & 7) == 0) piece_sums[(lane >> 3) * 16 + w] = d;
+    __syncthreads();
+    if (w == 0) {
+        const double s = wave_sum(piece_sums[lane] + piece_sums[lane + 64]);
+        if (lane == 0) partials[chunk] = s * tab.w[t];
+    }
+}
+
 // Workgroup c sums chunk c of the concatenated tensors (8 tiles of one tensor: 32768
 // fp32 or 65536 bf16/fp16 elements) into partials[c].  Inside a thread the squares are
 // added in element order; threads and waves are combined by the fixed trees of
@@ -494,68 +611,73 @@ template <int GD, bool kUnscale, bool kStore = false>
 __global__ __launch_bounds__(kNormBlock) void sqnorm_kernel(NormTable tab, float unscale,
                                                             double* __restrict__ partials, int64_t block_base) {
     static_assert(!kStore || kUnscale, "a store without an unscale rewrites the same values");
-    constexpr int K = norm_vec<GD>();
-    constexpr int64_t kTile = norm_tile<GD>();
-    constexpr int64_t kChunk = norm_chunk<GD>();
-    const int64_t chunk = block_base + blockIdx.x;
-    const int t = owning_tensor(tab.first_chunk, tab.count, chunk);
-    const int64_t start = (chunk - tab.first_chunk[t]) * kChunk;
-    const int64_t n = tab.n[t];
-    const void* G = tab.g[t];
-    double acc = 0.0;
-    constexpr int kNormBatch = norm_batch<GD, kStore>() > 0 ? norm_batch<GD, kStore>() : 1;
-    if (norm_batch<GD, kStore>() > 0 && tab.vec_ok[t] && start + kChunk <= n) {
-        // a whole chunk: kNormBatch tiles' loads in flight before the first of them is summed
-#pragma unroll
-        for (int k0 = 0; k0 < kNormTilesPerChunk; k0 += kNormBatch) {
-            float x[kNormBatch][K];
-#pragma unroll
-            for (int k = 0; k < kNormBatch; ++k)
-                load_vec<GD, K>(G, start + int64_t(k0 + k) * kTile + int64_t(threadIdx.x) * K, x[k]);
-#pragma unroll
-            for (int k = 0; k < kNormBatch; ++k) {
-#pragma unroll
+    static_assert(!kStore || GD == F32, "2-byte gradients unscale in place through unscale_pieces_kernel");
+    if constexpr (GD != F32) {
+        sqnorm_b16_chunk<GD, kUnscale>(tab, unscale, partials, block_base + blockIdx.x);
+    } else {
+        constexpr int K = norm_vec<GD>();
+        constexpr int64_t kTile = norm_tile<GD>();
+        constexpr int64_t kChunk = norm_chunk<GD>();
+        const int64_t chunk = block_base + blockIdx.x;
+        const int t = owning_tensor(tab.first_chunk, tab.count, chunk);
+        const int64_t start = (chunk - tab.first_chunk[t]) * kChunk;
+        const int64_t n = tab.n[t];
+        const void* G = tab.g[t];
+        double acc = 0.0;
+        constexpr int kNormBatch = norm_batch<GD, kStore>() > 0 ? norm_batch<GD, kStore>() : 1;
+        if (norm_batch<GD, kStore>() > 0 && tab.vec_ok[t] && start + kChunk <= n) {
+            // a whole chunk: kNormBatch tiles' loads in flight before the first of them is summed
+    #pragma unroll
+            for (int k0 = 0; k0 < kNormTilesPerChunk; k0 += kNormBatch) {
+                float x[kNormBatch][K];
+    #pragma unroll
+                for (int k = 0; k < kNormBatch; ++k)
+                    load_vec<GD, K>(G, start + int64_t(k0 + k) * kTile + int64_t(threadIdx.x) * K, x[k]);
+    #pragma unroll
+                for (int k = 0; k < kNormBatch; ++k) {
+    #pragma unroll
+                    for (int c = 0; c < K; ++c) {
+                        float y = x[k][c];
+                        if constexpr (kUnscale) y = round_to<GD>(y * unscale);
+                        if constexpr (kStore) x[k][c] = y;
+                        acc += sq(y);
+                    }
+                    if constexpr (kStore)
+                        store_vec<GD, K>(const_cast<void*>(G), start + int64_t(k0 + k) * kTile + int64_t(threadIdx.x) * K,
+                                         x[k]);
+                }
+            }
+            const double block_total = block_sum<kNormBlock>(acc);
+            if (threadIdx.x == 0) partials[chunk] = block_total * tab.w[t];
+            return;
+        }
+        for (int k = 0; k < kNormTilesPerChunk; ++k) {
+            const int64_t base = start + int64_t(k) * kTile;
+            if (base >= n) break;
+            if (tab.vec_ok[t] && base + kTile <= n) {
+                float x[K];
+                load_vec<GD, K>(G, base + int64_t(threadIdx.x) * K, x);
+    #pragma unroll
                 for (int c = 0; c < K; ++c) {
-                    float y = x[k][c];
+                    float y = x[c];
                     if constexpr (kUnscale) y = round_to<GD>(y * unscale);
-                    if constexpr (kStore) x[k][c] = y;
+                    if constexpr (kStore) x[c] = y;
                     acc += sq(y);
                 }
-                if constexpr (kStore)
-                    store_vec<GD, K>(const_cast<void*>(G), start + int64_t(k0 + k) * kTile + int64_t(threadIdx.x) * K,
-                                     x[k]);
+                if constexpr (kStore) store_vec<GD, K>(const_cast<void*>(G), base + int64_t(threadIdx.x) * K, x);
+            } else {
+                const int64_t end = base + kTile < n ? base + kTile : n;
+                for (int64_t e = base + threadIdx.x; e < end; e += kNormBlock) {
+                    float y = load_one<GD>(G, e);
+                    if constexpr (kUnscale) y = round_to<GD>(y * unscale);
+                    if constexpr (kStore) store_one<GD>(const_cast<void*>(G), e, y);
+                    acc += sq(y);
+                }
             }
         }
         const double block_total = block_sum<kNormBlock>(acc);
         if (threadIdx.x == 0) partials[chunk] = block_total * tab.w[t];
-        return;
     }
-    for (int k = 0; k < kNormTilesPerChunk; ++k) {
-        const int64_t base = start + int64_t(k) * kTile;
-        if (base >= n) break;
-        if (tab.vec_ok[t] && base + kTile <= n) {
-            float x[K];
-            load_vec<GD, K>(G, base + int64_t(threadIdx.x) * K, x);
-#pragma unroll
-            for (int c = 0; c < K; ++c) {
-                float y = x[c];
-                if constexpr (kUnscale) y = round_to<GD>(y * unscale);
-                if constexpr (kStore) x[c] = y;
-                acc += sq(y);
-            }
-            if constexpr (kStore) store_vec<GD, K>(const_cast<void*>(G), base + int64_t(threadIdx.x) * K, x);
-        } else {
-            const int64_t end = base + kTile < n ? base + kTile : n;
-            for (int64_t e = base + threadIdx.x; e < end; e += kNormBlock) {
-                float y = load_one<GD>(G, e);
-                if constexpr (kUnscale) y = round_to<GD>(y * unscale);
-                if constexpr (kStore) store_one<GD>(const_cast<void*>(G), e, y);
-                acc += sq(y);
-            }
-        }
-    }
-    const double block_total = block_sum<kNormBlock>(acc);
-    if (threadIdx.x == 0) partials[chunk] = block_total * tab.w[t];
 }
 
 // ---- FSDP gradient local share (optionally fused with the norm partials) ------------
@@ -640,6 +762,63 @@ __device__ __forceinline__ int64_t tile_sum_slot(int64_t t, int64_t tiles) {
     const int64_t per = n / kXcds;
     return first + (b < per * kXcds ? (b % kXcds) * per + b / kXcds : b);
 }
+// In-place unscale of 2-byte gradients fused with their norm partials, in the two-level
+// order of the plain pass: one wave per piece reads its 1 KB, stores the unscaled values,
+// then sums their squares and writes the piece sum (slots grouped by XCD, as the tile
+// sums are); fold_pieces_kernel then forms each chunk's partial.  Storing before summing
+// and retiring after 1 KB keeps the in-place stream at the rate of a plain copy, where
+// 1024-thread workgroups holding a chunk each stream about 6% slower.
+template <int GD>
+__global__ __launch_bounds__(64) void unscale_pieces_kernel(NormTable tab, float unscale,
+                                                            double* __restrict__ piece_sums, int64_t pieces,
+                                                            int64_t block_base) {
+    const int64_t p = block_base + blockIdx.x;
+    const int64_t chunk = p / kPiecesPerChunk;
+    const int t = owning_tensor(tab.first_chunk, tab.count, chunk);
+    const int64_t e0 = (chunk - tab.first_chunk[t]) * kPieceB16 * kPiecesPerChunk +
+                       (p % kPiecesPerChunk) * kPieceB16 + int64_t(threadIdx.x) * 8;
+    const int64_t n = tab.n[t];
+    uint16_t* G = static_cast<uint16_t*>(const_cast<void*>(tab.g[t]));  // written in place
+    constexpr bool kHalf = GD == F16;
+    double acc = 0.0;
+    if (tab.vec_ok[t] && e0 + 8 <= n) {
+        // Packed conversions, and the squares taken of the stored values: about 6.5 VALU
+        // operations per element, where rounding through round_to and store_vec took 14
+        // and left this pass ALU-bound.
+        const u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(G + e0));
+        float y[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            y[2 * i] = b16_to_f32<kHalf>(w[i] & 0xFFFFu) * unscale;
+            y[2 * i + 1] = b16_to_f32<kHalf>(w[i] >> 16) * unscale;
+        }
+        const u32x4 o = pack8_rounded<GD>(y);
+        __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(G + e0));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            acc = add_sq(acc, b16_to_f32<kHalf>(o[i] & 0xFFFFu));
+            acc = add_sq(acc, b16_to_f32<kHalf>(o[i] >> 16));
+        }
+    } else {
+        for (int c = 0; c < 8 && e0 + c < n; ++c) {
+            const uint32_t r = f32_to_b16<kHalf>(round_to<GD>(b16_to_f32<kHalf>(G[e0 + c]) * unscale));
+            G[e0 + c] = static_cast<uint16_t>(r);
+            acc = add_sq(acc, b16_to_f32<kHalf>(r));
+        }
+    }
+    acc = wave_sum(acc);
+    if (threadIdx.x == 0) piece_sums[tile_sum_slot(p, pieces)] = acc;
+}
+__global__ __launch_bounds__(64) void fold_pieces_kernel(NormTable tab, const double* __restrict__ piece_sums,
+                                                         int64_t pieces, double* __restrict__ partials,
+                                                         int64_t block_base) {
+    const int64_t chunk = block_base + blockIdx.x;
+    const int t = owning_tensor(tab.first_chunk, tab.count, chunk);
+    const int64_t p = chunk * kPiecesPerChunk + threadIdx.x;
+    const double s = wave_sum(piece_sums[tile_sum_slot(p, pieces)] + piece_sums[tile_sum_slot(p + 64, pieces)]);
+    if (threadIdx.x == 0) partials[chunk] = s * tab.w[t];
+}
+
 // The value a store to RD and a reload leave: round_to for fp32 and fp16, and for bf16 the
 // same rounding with any NaN stored as the canonical 0x7FC0, as f32_to_bf16 stores it.
 template <int RD>
@@ -890,18 +1069,18 @@ __global__ __launch_bounds__(kFinalBlock) void norm_finalize_kernel(
 }
 
 // ---- in-place scaling ---------------------------------------------------------------
-// Two 16-byte vectors per lane, in half-wave (32-thread) workgroups for fp32 (256
-// elements each) and full-wave workgroups for bf16/fp16 (1024 elements each), whose two
-// rounded multiplies per element keep the ALUs busier.  Measured on MI355X, in place
-// over 4 GB: fp32 6.68 TB/s with 32 threads against 6.06 with 64 (one vector) and 5.41
-// (two); bf16 6.17-6.26 TB/s with 64 threads against 4.9-5.2 with 32.
+// One kilobyte per workgroup, read and written in place: fp32 in half-wave (32-thread)
+// workgroups with two 16-byte vectors per lane, bf16/fp16 in full-wave workgroups with
+// one vector per lane, packed by pack8_rounded.  A workgroup that retires after 1 KB keeps
+// an in-place stream at the rate of a plain copy.
 template <int D>
 constexpr int scale_block() { return D == F32 ? 32 : 64; }
-constexpr int kScaleUnroll = 2;
+template <int D>
+constexpr int scale_unroll() { return D == F32 ? 2 : 1; }
 template <int D>
 constexpr int scale_vec() { return D == F32 ? 4 : 8; }
 template <int D>
-constexpr int64_t scale_tile() { return int64_t(scale_block<D>()) * kScaleUnroll * scale_vec<D>(); }
+constexpr int64_t scale_tile() { return int64_t(scale_block<D>()) * scale_unroll<D>() * scale_vec<D>(); }
 
 struct ScaleTable {
     void* x[kMaxT];
@@ -933,14 +1112,35 @@ __global__ __launch_bounds__(64) void scale_kernel(ScaleTable tab, float unscale
     const int64_t n = tab.n[t];
     void* X = tab.x[t];
     if (tab.vec_ok[t] && base + kTile <= n) {
-        float v[kScaleUnroll][K];
+        if constexpr (D == F32) {
+            constexpr int U = scale_unroll<D>();
+            float v[U][K];
 #pragma unroll
-        for (int u = 0; u < kScaleUnroll; ++u) load_vec<D, K>(X, base + (int64_t(u) * kScaleBlock + threadIdx.x) * K, v[u]);
+            for (int u = 0; u < U; ++u) load_vec<D, K>(X, base + (int64_t(u) * kScaleBlock + threadIdx.x) * K, v[u]);
 #pragma unroll
-        for (int u = 0; u < kScaleUnroll; ++u) {
+            for (int u = 0; u < U; ++u) {
 #pragma unroll
-            for (int c = 0; c < K; ++c) v[u][c] = scale_one<D>(v[u][c], unscale, mul);
-            store_vec<D, K>(X, base + (int64_t(u) * kScaleBlock + threadIdx.x) * K, v[u]);
+                for (int c = 0; c < K; ++c) v[u][c] = scale_one<D>(v[u][c], unscale, mul);
+                store_vec<D, K>(X, base + (int64_t(u) * kScaleBlock + threadIdx.x) * K, v[u]);
+            }
+        } else {
+            u32x4* P = reinterpret_cast<u32x4*>(static_cast<uint16_t*>(X) + base) + threadIdx.x;
+            const u32x4 w = __builtin_nontemporal_load(P);
+            float y[8];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                y[2 * i] = b16_to_f32<D == F16>(w[i] & 0xFFFFu);
+                y[2 * i + 1] = b16_to_f32<D == F16>(w[i] >> 16);
+            }
+            // x * 1 rounds to x (a NaN stays a NaN and is stored as one): the first multiply
+            // runs only when it can change a value.
+            if (unscale != 1.0f) {
+#pragma unroll
+                for (int c = 0; c < 8; ++c) y[c] = round_to<D>(y[c] * unscale);
+            }
+#pragma unroll
+            for (int c = 0; c < 8; ++c) y[c] = y[c] * mul;
+            __builtin_nontemporal_store(pack8_rounded<D>(y), P);
         }
         return;
     }
@@ -1155,7 +1355,8 @@ __global__ __launch_bounds__(kAdamBlock) void sgd_f64_kernel(SgdTable tab, SgdSc
 // In-place x = (x * unscale) * (*grad_mul) on float64 tensors, each product rounded in
 // double; nothing when both factors are 1.  Half-wave workgroups, two 16-byte vectors
 // per lane (128 elements per workgroup, 1 KB).
-constexpr int64_t kScaleF64Tile = int64_t(32) * kScaleUnroll * kF64Vec;
+constexpr int kScaleF64Unroll = 2;
+constexpr int64_t kScaleF64Tile = int64_t(32) * kScaleF64Unroll * kF64Vec;
 __global__ __launch_bounds__(32) void scale_f64_kernel(ScaleTable tab, double unscale,
                                                        const double* __restrict__ grad_mul, int64_t block_base) {
     const double mul = grad_mul != nullptr ? *grad_mul : 1.0;
@@ -1166,11 +1367,11 @@ __global__ __launch_bounds__(32) void scale_f64_kernel(ScaleTable tab, double un
     const int64_t n = tab.n[t];
     void* X = tab.x[t];
     if (tab.vec_ok[t] && base + kScaleF64Tile <= n) {
-        double v[kScaleUnroll][kF64Vec];
+        double v[kScaleF64Unroll][kF64Vec];
 #pragma unroll
-        for (int u = 0; u < kScaleUnroll; ++u) load_f64<kF64Vec>(X, base + (int64_t(u) * 32 + threadIdx.x) * kF64Vec, v[u]);
+        for (int u = 0; u < kScaleF64Unroll; ++u) load_f64<kF64Vec>(X, base + (int64_t(u) * 32 + threadIdx.x) * kF64Vec, v[u]);
 #pragma unroll
-        for (int u = 0; u < kScaleUnroll; ++u) {
+        for (int u = 0; u < kScaleF64Unroll; ++u) {
 #pragma unroll
             for (int c = 0; c < kF64Vec; ++c) v[u][c] = (v[u][c] * unscale) * mul;
             store_f64<kF64Vec>(X, base + (int64_t(u) * 32 + threadIdx.x) * kF64Vec, v[u]);
@@ -1384,10 +1585,25 @@ int32_t build_norm_table(const char* who, const void* const* grads, const int64_
 }
 
 // sqnorm_kernel launches writing partials[0, chunks).
-// With `store`, the unscaled values are also written back (nothing to write for unscale 1).
+// With `store`, the unscaled values are also written back (nothing to write for unscale 1);
+// 2-byte gradients then run unscale_pieces_kernel + fold_pieces_kernel, with
+// kPiecesPerChunk * chunks doubles of piece_scratch.
 int32_t launch_sqnorm(const char* who, const NormTable& tab, int64_t chunks, int32_t grad_dtype, float unscale,
-                      double* partials, hipStream_t st, bool store = false) {
+                      double* partials, hipStream_t st, bool store = false, double* piece_scratch = nullptr) {
     const bool scaled = unscale != 1.0f;
+    if (scaled && store && grad_dtype != F32 && grad_dtype != HBT_DTYPE_F64) {
+        const int64_t pieces = chunks * kPiecesPerChunk;
+        const int32_t status = launch_sliced(who, pieces, 64, [&](int64_t first, dim3 grid) {
+            if (grad_dtype == BF16)
+                unscale_pieces_kernel<BF16><<<grid, 64, 0, st>>>(tab, unscale, piece_scratch, pieces, first);
+            else
+                unscale_pieces_kernel<F16><<<grid, 64, 0, st>>>(tab, unscale, piece_scratch, pieces, first);
+        });
+        if (status != HBT_OK) return status;
+        return launch_sliced(who, chunks, 64, [&](int64_t first, dim3 grid) {
+            fold_pieces_kernel<<<grid, 64, 0, st>>>(tab, piece_scratch, pieces, partials, first);
+        });
+    }
     if (grad_dtype == HBT_DTYPE_F64) {
         // The callers refuse a float64 unscale or store: the multiply belongs in double.
         return launch_sliced(who, chunks, kNormBlock, [&](int64_t first, dim3 grid) {
@@ -1395,16 +1611,17 @@ int32_t launch_sqnorm(const char* who, const NormTable& tab, int64_t chunks, int
         });
     }
     return launch_sliced(who, chunks, kNormBlock, [&](int64_t first, dim3 grid) {
-#define HBT_NORM(GD)                                                                                           \
-    do {                                                                                                       \
-        if (scaled && store) sqnorm_kernel<GD, true, true><<<grid, kNormBlock, 0, st>>>(tab, unscale, partials, first); \
-        else if (scaled) sqnorm_kernel<GD, true><<<grid, kNormBlock, 0, st>>>(tab, unscale, partials, first);  \
-        else sqnorm_kernel<GD, false><<<grid, kNormBlock, 0, st>>>(tab, unscale, partials, first);             \
-    } while (0)
-        if (grad_dtype == F32) HBT_NORM(F32);
-        else if (grad_dtype == BF16) HBT_NORM(BF16);
-        else HBT_NORM(F16);
-#undef HBT_NORM
+        if (grad_dtype == F32) {
+            if (scaled && store) sqnorm_kernel<F32, true, true><<<grid, kNormBlock, 0, st>>>(tab, unscale, partials, first);
+            else if (scaled) sqnorm_kernel<F32, true><<<grid, kNormBlock, 0, st>>>(tab, unscale, partials, first);
+            else sqnorm_kernel<F32, false><<<grid, kNormBlock, 0, st>>>(tab, unscale, partials, first);
+        } else if (grad_dtype == BF16) {
+            if (scaled) sqnorm_kernel<BF16, true><<<grid, kNormBlock, 0, st>>>(tab, unscale, partials, first);
+            else sqnorm_kernel<BF16, false><<<grid, kNormBlock, 0, st>>>(tab, unscale, partials, first);
+        } else {
+            if (scaled) sqnorm_kernel<F16, true><<<grid, kNormBlock, 0, st>>>(tab, unscale, partials, first);
+            else sqnorm_kernel<F16, false><<<grid, kNormBlock, 0, st>>>(tab, unscale, partials, first);
+        }
     });
 }
 
@@ -1732,10 +1949,14 @@ int32_t hbt_grad_sqnorm_partials(const void* const* grads, const int64_t* numels
 }
 
 int32_t hbt_scale_inplace_sqnorm(void* const* tensors, const int64_t* numels, int32_t count, int32_t dtype,
-                                 float unscale, double* partials, void* stream) {
+                                 float unscale, double* partials, double* piece_scratch, void* stream) {
     clear_error();
     if (count > 0 && partials == nullptr) {
         set_error("hbt_scale_inplace_sqnorm: null partials pointer");
+        return HBT_ERR_INVALID_ARGUMENT;
+    }
+    if (count > 0 && piece_scratch == nullptr && (dtype == BF16 || dtype == F16) && unscale != 1.0f) {
+        set_error("hbt_scale_inplace_sqnorm: 2-byte gradients need the piece scratch");
         return HBT_ERR_INVALID_ARGUMENT;
     }
     if (count > 0 && tensors == nullptr) {
@@ -1757,7 +1978,7 @@ int32_t hbt_scale_inplace_sqnorm(void* const* tensors, const int64_t* numels, in
                                             count, dtype, tab, chunks);
     if (status != HBT_OK) return status;
     return launch_sqnorm("hbt_scale_inplace_sqnorm", tab, chunks, dtype, unscale, partials, as_stream(stream),
-                         /*store=*/true);
+                         /*store=*/true, piece_scratch);
 }
 
 int32_t hbt_grad_norm_finalize(const double* partials, int64_t count, double max_norm,

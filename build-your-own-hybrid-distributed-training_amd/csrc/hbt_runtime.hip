@@ -56,7 +56,7 @@ extern "C" {
 const char* hbt_last_error(void) { return hbt::g_last_error.c_str(); }
 
 // Bumped whenever an exported signature or a table layout changes.
-int32_t hbt_abi_version(void) { return 15; }
+int32_t hbt_abi_version(void) { return 16; }
 
 // Entry points declared in include/hbt.h (hbt_last_error .. hbt_scale_inplace_f64).
 int32_t hbt_symbol_count(void) { return 21; }

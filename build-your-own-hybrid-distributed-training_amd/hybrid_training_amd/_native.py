@@ -47,6 +47,7 @@ __all__ = [
     "EXPORTED_SYMBOLS",
     "MAX_LOCAL_RANKS",
     "MAX_TENSORS_PER_LAUNCH",
+    "PIECES_PER_NORM_CHUNK",
     "check",
     "contiguous_source",
     "dtype_code",
@@ -57,9 +58,11 @@ __all__ = [
     "stream_of",
 ]
 
-ABI_VERSION = 15
+ABI_VERSION = 16
 MAX_TENSORS_PER_LAUNCH = 16
 MAX_LOCAL_RANKS = 64
+#: Doubles of working storage hbt_scale_inplace_sqnorm takes per partial for 2-byte gradients.
+PIECES_PER_NORM_CHUNK = 128
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
@@ -161,7 +164,7 @@ EXPORTED_SYMBOLS: dict[str, tuple[object, tuple[object, ...]]] = {
     ),
     "hbt_scale_inplace_sqnorm": (
         _c_i32,
-        (_ptr_array, _i64_array, _c_i32, _c_i32, _c_f32, _c_void_p, _c_void_p),
+        (_ptr_array, _i64_array, _c_i32, _c_i32, _c_f32, _c_void_p, _c_void_p, _c_void_p),
     ),
     "hbt_grad_accumulate": (
         _c_i32,

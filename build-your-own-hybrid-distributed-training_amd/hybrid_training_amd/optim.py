@@ -522,13 +522,24 @@ def unscale_with_partials(grads: Sequence[torch.Tensor], dtype: torch.dtype, uns
     code = _native.dtype_code(dtype)
     norm_chunk = norm_chunk_elems(dtype)
 
-    def call(ptrs: list[int], numels: list[int], partials_ptr: int, stream: int) -> None:
+    # 2-byte gradients sum 512-element pieces first: the kernel's working storage is
+    # PIECES_PER_NORM_CHUNK doubles per partial.
+    pieces = _native.PIECES_PER_NORM_CHUNK if dtype in (torch.bfloat16, torch.float16) else 0
+
+    def call(ptrs: list[int], numels: list[int], partials_ptr: int, scratch: torch.Tensor | None,
+             stream: int) -> None:
         status = lib.hbt_scale_inplace_sqnorm(_native.pointer_array(ptrs), _native.int64_array(numels), len(ptrs),
-                                              code, unscale, partials_ptr, stream)
+                                              code, unscale, partials_ptr,
+                                              None if scratch is None else scratch.data_ptr(), stream)
         _native.check(status, operation)
 
     def count_of(n: int) -> int:
         return -(-n // norm_chunk)
+
+    def piece_scratch(partial_count: int) -> torch.Tensor | None:
+        if not pieces or unscale == 1.0:
+            return None
+        return torch.empty(max(1, partial_count) * pieces, dtype=torch.float64, device=device)
 
     resident = [g for g in grads if not is_host(g)]
     hosted = [g for g in grads if is_host(g)]
@@ -539,7 +550,7 @@ def unscale_with_partials(grads: Sequence[torch.Tensor], dtype: torch.dtype, uns
             counts = [count_of(g.numel()) for g in chunk]
             partials = torch.empty(max(1, sum(counts)), dtype=torch.float64, device=device)
             call([g.data_ptr() for g in chunk], [g.numel() for g in chunk], partials.data_ptr(),
-                 _native.stream_of(device))
+                 piece_scratch(sum(counts)), _native.stream_of(device))
             offset = 0
             for g, k in zip(chunk, counts):
                 records.append((g, partials[offset : offset + k]))
@@ -551,10 +562,12 @@ def unscale_with_partials(grads: Sequence[torch.Tensor], dtype: torch.dtype, uns
                 flat = g.detach().reshape(-1)
                 partials = torch.empty(max(1, count_of(flat.numel())), dtype=torch.float64, device=device)
                 lead = (flat.data_ptr() % 16) // flat.element_size()
+                # one staged chunk at a time on the staging stream: one scratch of a chunk's size serves all
+                scratch = piece_scratch(count_of(min(step, flat.numel())))
                 staging.run(
                     flat.numel(), [HostOperand(flat, store=True)],
-                    lambda first, n, st, stream, partials=partials: call(
-                        [st[0].data_ptr()], [n], partials.data_ptr() + 8 * (first // norm_chunk), stream),
+                    lambda first, n, st, stream, partials=partials, scratch=scratch: call(
+                        [st[0].data_ptr()], [n], partials.data_ptr() + 8 * (first // norm_chunk), scratch, stream),
                     lead=lead, chunk=step,
                 )
                 records.append((g, partials[: count_of(flat.numel())]))

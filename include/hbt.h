@@ -399,9 +399,16 @@ int32_t hbt_scale_inplace(void* const* tensors, const int64_t* numels, int32_t c
  * partials serve a later norm of the unchanged gradients.  Reads and writes each
  * element once, where the two calls read it twice.  With unscale == 1 nothing is
  * written and only the partials are computed.
+ * For BF16 and F16, piece_scratch is caller-provided device memory for
+ * 128 * hbt_norm_partials_count(numels, count, dtype) doubles (working storage: the sums
+ * of 512-element pieces, in an internal order grouped by XCD); it may be NULL for F32 or
+ * when unscale == 1.  The partials of 2-byte gradients, here and in
+ * hbt_grad_sqnorm_partials, are summed per piece (a butterfly over 64 lanes of 8-element
+ * lane sums) and then per chunk (a butterfly of s_l + s_(l+64)), so both passes agree.
  * ---------------------------------------------------------------------------- */
 int32_t hbt_scale_inplace_sqnorm(void* const* tensors, const int64_t* numels, int32_t count,
-                                 int32_t dtype, float unscale, double* partials, void* stream);
+                                 int32_t dtype, float unscale, double* partials, double* piece_scratch,
+                                 void* stream);
 
 /* ------------------------------------------------------------------------------
  * Float64 parameters: the fused clip + AdamW step, the fused clip + SGD step and the

@@ -31,7 +31,7 @@ int main(void) {
         EXPECT((c >= 0 && c <= HBT_MAX_TENSORS_PER_LAUNCH) ? rc == HBT_OK : rc == HBT_ERR_INVALID_ARGUMENT);
         rc = hbt_scale_inplace(ptrs, numels, c, HBT_DTYPE_F16, 0.5f, NULL, NULL);
         EXPECT((c >= 0 && c <= HBT_MAX_TENSORS_PER_LAUNCH) ? rc == HBT_OK : rc == HBT_ERR_INVALID_ARGUMENT);
-        rc = hbt_scale_inplace_sqnorm(ptrs, numels, c, HBT_DTYPE_BF16, 0.5f, partials, NULL);
+        rc = hbt_scale_inplace_sqnorm(ptrs, numels, c, HBT_DTYPE_BF16, 0.5f, partials, partials, NULL);
         EXPECT((c >= 0 && c <= HBT_MAX_TENSORS_PER_LAUNCH) ? rc == HBT_OK : rc == HBT_ERR_INVALID_ARGUMENT);
         rc = hbt_adamw_step(ptrs, ptrs, ptrs, ptrs, numels, c, HBT_DTYPE_F32, HBT_DTYPE_BF16, 1.0f, NULL,
                             1.0f, 0.1f, 0.9f, 0.1f, 1.0f, 1e-8f, -1e-3f, HBT_STEP_WRITE_GRAD, NULL);
@@ -44,12 +44,15 @@ int main(void) {
     }
     // bad dtypes and pointers
     EXPECT(hbt_grad_sqnorm_partials(cptrs, numels, weights, 1, 7, 1.0f, partials, NULL) == HBT_ERR_INVALID_ARGUMENT);
-    EXPECT(hbt_scale_inplace_sqnorm(ptrs, numels, 1, HBT_DTYPE_F64, 0.5f, partials, NULL) == HBT_ERR_UNSUPPORTED);
-    EXPECT(hbt_scale_inplace_sqnorm(ptrs, numels, 1, 7, 0.5f, partials, NULL) == HBT_ERR_INVALID_ARGUMENT);
-    EXPECT(hbt_scale_inplace_sqnorm(ptrs, numels, 1, HBT_DTYPE_F32, 0.5f, NULL, NULL) == HBT_ERR_INVALID_ARGUMENT);
-    EXPECT(hbt_scale_inplace_sqnorm(NULL, numels, 1, HBT_DTYPE_F32, 0.5f, partials, NULL) == HBT_ERR_INVALID_ARGUMENT);
+    EXPECT(hbt_scale_inplace_sqnorm(ptrs, numels, 1, HBT_DTYPE_F64, 0.5f, partials, NULL, NULL) == HBT_ERR_UNSUPPORTED);
+    EXPECT(hbt_scale_inplace_sqnorm(ptrs, numels, 1, HBT_DTYPE_BF16, 0.5f, partials, NULL, NULL) ==
+           HBT_ERR_INVALID_ARGUMENT);  /* 2-byte gradients need the piece scratch */
+    EXPECT(hbt_scale_inplace_sqnorm(ptrs, numels, 1, HBT_DTYPE_F16, 1.0f, partials, NULL, NULL) == HBT_OK);
+    EXPECT(hbt_scale_inplace_sqnorm(ptrs, numels, 1, 7, 0.5f, partials, NULL, NULL) == HBT_ERR_INVALID_ARGUMENT);
+    EXPECT(hbt_scale_inplace_sqnorm(ptrs, numels, 1, HBT_DTYPE_F32, 0.5f, NULL, NULL, NULL) == HBT_ERR_INVALID_ARGUMENT);
+    EXPECT(hbt_scale_inplace_sqnorm(NULL, numels, 1, HBT_DTYPE_F32, 0.5f, partials, NULL, NULL) == HBT_ERR_INVALID_ARGUMENT);
     numels[0] = -1;
-    EXPECT(hbt_scale_inplace_sqnorm(ptrs, numels, 1, HBT_DTYPE_F32, 0.5f, partials, NULL) == HBT_ERR_INVALID_ARGUMENT);
+    EXPECT(hbt_scale_inplace_sqnorm(ptrs, numels, 1, HBT_DTYPE_F32, 0.5f, partials, NULL, NULL) == HBT_ERR_INVALID_ARGUMENT);
     numels[0] = 0;
     // local shares: every group size to the limit and past it, empty shards (no launch)
     for (int g = 0; g <= HBT_MAX_LOCAL_RANKS + 1; ++g) {

@@ -158,8 +158,9 @@ def _scale_reference(t: torch.Tensor, unscale: float, mul: float) -> torch.Tenso
     return t.detach().cpu().clone().mul_(unscale).mul_(mul)
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_scale_inplace_tiles(device, dtype):
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("factors", [(1.0 / 65536.0, 0.31622776601683794), (1.0, 0.31622776601683794), (0.5, 1.0)])
+def test_scale_inplace_tiles(device, dtype, factors):
     lib = _native.library()
     gen = torch.Generator(device=device).manual_seed(3)
     sizes = [1, 7, 511, 512, 513, 4097, 100_003]
@@ -173,8 +174,7 @@ def test_scale_inplace_tiles(device, dtype):
         cursor += n
     before = [t.detach().cpu().clone() for t in tensors]
     lead = _bits(base[:1])
-    unscale = 1.0 / 65536.0
-    mul = 0.31622776601683794
+    unscale, mul = factors  # the loss scaler's unscale and the clip; one of them alone
     grad_mul = torch.tensor([mul], dtype=torch.float32, device=device)
     status = lib.hbt_scale_inplace(
         _native.pointer_array([t.data_ptr() for t in tensors]), _native.int64_array(sizes), len(sizes),
@@ -225,9 +225,11 @@ def test_scale_inplace_sqnorm_is_the_two_calls(device, dtype, specials):
                   "test.sqnorm")
     # the fused call
     got = torch.empty(count, dtype=torch.float64, device=device)
+    scratch = torch.empty(max(1, count) * _native.PIECES_PER_NORM_CHUNK, dtype=torch.float64, device=device)
     _native.check(lib.hbt_scale_inplace_sqnorm(_native.pointer_array([t.data_ptr() for t in tensors_b]),
                                                _native.int64_array(sizes), len(sizes), code, unscale,
-                                               ctypes.c_void_p(got.data_ptr()), stream),
+                                               ctypes.c_void_p(got.data_ptr()), ctypes.c_void_p(scratch.data_ptr()),
+                                               stream),
                   "test.scale_inplace_sqnorm")
     torch.cuda.synchronize(device)
     assert np.array_equal(_bits(base), _bits(twin))  # every element, the untouched first one included

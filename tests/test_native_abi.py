@@ -134,7 +134,10 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     assert lib.hbt_grad_sqnorm_partials(_native.pointer_array([4096]), _native.int64_array([1]),
                                         _native.double_array([1.0]), 1, 3, 0.5, fake, None) == -2
     assert lib.hbt_scale_inplace_sqnorm(_native.pointer_array([4096]), _native.int64_array([1]), 1, 3, 0.5,
-                                        fake, None) == -2
+                                        fake, None, None) == -2
+    # 2-byte gradients: the fused unscale needs its piece scratch (refused before any launch)
+    assert lib.hbt_scale_inplace_sqnorm(_native.pointer_array([4096]), _native.int64_array([1]), 1, 1, 0.5,
+                                        fake, None, None) == -1
     assert lib.hbt_grad_norm_noalloc(_native.pointer_array([4096]), _native.int64_array([1]),
                                      _native.double_array([1.0]), 1, 3, 1.0, 1.0, None, None, None, None, None) == -2
     assert lib.hbt_norm_partials_count(_native.int64_array([16384, 16385]), 2, 3) == 3
