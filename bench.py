@@ -64,7 +64,7 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument(
         "--workload",
         choices=["adamw", "buckets", "reshard", "scaler", "fsdp", "inplace_clip", "torch_adamw", "sgd", "offload",
-                 "param_offload", "checkpoint", "copy_ceiling"],
+                 "param_offload", "checkpoint", "copy_ceiling", "lowp", "mlp"],
         default="adamw",
         help="adamw (default): the Llama-3-8B W=8 shard step above; buckets: GPT-2-small DDP bucket "
         "pack + AVG divide at W=8; reshard: Llama-3-8B bf16 flat shards W=4 -> W=8 and W=2; scaler: "
@@ -74,7 +74,9 @@ def parse_args() -> argparse.Namespace:
         "the headline shard with SGD (momentum 0.9); offload: the headline step with AdamW state in pinned "
         "host memory; param_offload: the headline shard as an FSDP unit with the shard, its gradient and "
         "its AdamW state in pinned host memory; checkpoint: Llama-3-8B bf16 saved by 4 FSDP ranks and loaded back at W=8; "
-        "copy_ceiling: torch's device-to-device copy against the interval copy on 1 and 16 GiB",
+        "copy_ceiling: torch's device-to-device copy against the interval copy on 1 and 16 GiB; lowp: the headline "
+        "shard with bf16 masters (AdamW and SGD); mlp: the reference's 1,857-parameter MLP as FSDP units at W=2 and 4, "
+        "the per-rank tail (local share + clip + AdamW)",
     )
     ap.add_argument(
         "--calibrate-copy",
@@ -105,15 +107,16 @@ def calibrate_copy() -> int:
     return 0
 
 
-def _time_cpu_step(numel: int, steps: int, threads: int, momentum: float | None = None) -> float:
+def _time_cpu_step(numel: int, steps: int, threads: int, momentum: float | None = None, dtype=None) -> float:
     """Mean seconds of the reference's CPU step on ``numel`` elements with ``threads`` threads
-    (AdamW, or SGD with ``momentum``)."""
+    (AdamW, or SGD with ``momentum``; fp32 unless ``dtype``)."""
     import torch
 
     from oracle.cpu_reference_path import ReferenceCpuStep
 
     torch.set_num_threads(threads)
-    ref = ReferenceCpuStep(numel, lr=LR, betas=BETAS, eps=EPS, weight_decay=WD, momentum=momentum)
+    ref = ReferenceCpuStep(numel, lr=LR, betas=BETAS, eps=EPS, weight_decay=WD, momentum=momentum,
+                           dtype=dtype or torch.float32)
     ref.prepare()
     ref.step(MAX_NORM)  # warm-up
     elapsed = 0.0
@@ -126,12 +129,13 @@ def _time_cpu_step(numel: int, steps: int, threads: int, momentum: float | None 
     return elapsed / steps
 
 
-def _cpu_step_line(numel: int, steps: int, momentum: float | None = None) -> dict:
+def _cpu_step_line(numel: int, steps: int, momentum: float | None = None, dtype=None) -> dict:
     """The reference's clipped CPU step (AdamW, or SGD with ``momentum``) on a bounded sample."""
-    seconds = _time_cpu_step(numel, steps, _cpu_threads(), momentum)
+    seconds = _time_cpu_step(numel, steps, _cpu_threads(), momentum, dtype)
     name = "torch.optim.AdamW" if momentum is None else f"torch.optim.SGD(momentum={momentum})"
+    kind = "fp32" if dtype is None else str(dtype).replace("torch.", "")
     return _cpu_line(numel, seconds, "params/s",
-                     f"{numel} fp32 elements, {steps} timed steps after 1 warm-up: fp64 norm + in-place clip + "
+                     f"{numel} {kind} elements, {steps} timed steps after 1 warm-up: fp64 norm + in-place clip + "
                      f"{name}(foreach=False).step")
 
 
@@ -443,6 +447,34 @@ def bench_buckets(steps: int, warmup: int) -> int:
           max(warmup, 3), "f32", "GPT-2 small gradients, 17 buckets of <= 25 MiB, W=8", 8 * n,
           {"params": n, "buckets": len(ddp.buckets), "bytes_per_param": 8},
           _secondary_traffic("buckets", ["pack + AVG divide (one launch)"], [1]), cpu)
+    # The same model in bf16: bf16 gradients packed into bf16 buckets (read 2 B + write 2 B).
+    del ddp
+    named16 = [(name, torch.nn.Parameter(torch.empty(p.shape, dtype=torch.bfloat16, device=device)))
+               for name, p in named]
+    grads16 = [g.to(torch.bfloat16) for g in grads]
+    ddp16 = BucketedGradients(named16, GroupHandle.local_view("data_parallel", 8, 0), DDPConfig(bucket_cap_mb=25.0))
+
+    def run16():
+        for (_, p), g in zip(named16, grads16):
+            p.grad = g
+        ddp16.pack()
+
+    ms = _time_events(run16, max(steps, 20), max(warmup, 3))
+    cpu = None
+    if _WITH_CPU:
+        from oracle.cpu_reference_path import pack_buckets
+
+        host = {id(p): g.cpu() for (_, p), g in zip(named16, grads16)}
+        buckets = [(torch.empty(b.layout.total_numel, dtype=torch.bfloat16),
+                    [(b.layout.offsets[i], host[id(q)]) for i, q in enumerate(b.parameters)]) for b in ddp16.buckets]
+        cpu = _cpu_line(n, _cpu_time(lambda: pack_buckets(buckets, 8), 5), "params/s",
+                        f"all {n} bf16 gradients into the {len(buckets)} buckets, copy + div_(8) per bucket, "
+                        "5 timed runs after 1 warm-up")
+        del host, buckets
+    _emit("DDP bucket pack + AVG divide, bf16 gradients: params/s", "params/s", n / (ms * 1e-3), ms, max(steps, 20),
+          max(warmup, 3), "bf16", f"GPT-2 small bf16 gradients, {len(ddp16.buckets)} buckets of <= 25 MiB, W=8", 4 * n,
+          {"params": n, "buckets": len(ddp16.buckets), "bytes_per_param": 4},
+          _secondary_traffic("buckets", ["bf16 gradients: pack + AVG divide (one launch)"], [1]), cpu)
     return 0
 
 
@@ -520,6 +552,59 @@ def bench_reshard(steps: int, warmup: int) -> int:
               cpu)
         del dests
         torch.cuda.empty_cache()
+    # Re-slices that cast, W=4 -> W=8: the bf16 checkpoint into fp16 shards (read 2 B +
+    # write 2 B), then an fp32 save of the same model into float64 shards (read 4 B + write
+    # 8 B): ``read_tensor_range``'s ``.to(out.dtype)`` (``checkpoint/reshard.py:290``).
+    s8 = -(-total // 8)
+    layouts8 = []
+    for rank in range(8):
+        local, items, cur = ShardRange(rank * s8, s8), [], 0
+        for (name, shape), numel in zip(shapes, numels):
+            ov = intersect_ranges(local, ShardRange(cur, numel))
+            if ov is not None:
+                items.append(PieceLayout(name, tuple(shape), ov.start - cur, ov.length, ov.start - local.start))
+            cur += numel
+        layouts8.append(items)
+    dests = [torch.empty(s8, dtype=torch.float16, device=device) for _ in range(8)]
+
+    def run16():
+        for dest, items in zip(dests, layouts8):
+            load_flat_shard(dest, items, records, cache)
+
+    ms = _time_events(run16, max(steps, 5), max(warmup, 2))
+    _emit("flat-interval reshard with a cast, bf16 -> fp16: elements/s", "elements/s", total / (ms * 1e-3), ms,
+          max(steps, 5), max(warmup, 2), "bf16->f16", "Llama-3-8B bf16 flat shards, W=4 -> W=8 fp16 shards",
+          4 * total, {"elements": total, "bytes_per_element": 4},
+          _secondary_traffic("reshard", [f"bf16 -> fp16: one destination shard of {s8:,} elements (W=8)"], [8]))
+    del dests, shards, cache
+    torch.cuda.empty_cache()
+    shards32 = [torch.randn(s_src, device=device, generator=gen) for _ in range(4)]
+    records32, cache32, cursor = {}, DeviceShardCache(), 0
+    for (name, shape), numel in zip(shapes, numels):
+        rec = TensorRecord(key=name, name=name, global_shape=tuple(shape), dtype="torch.float32")
+        for rank in range(4):
+            ov = intersect_ranges(ShardRange(rank * s_src, s_src), ShardRange(cursor, numel))
+            if ov is None:
+                continue
+            key = f"model::{name}@{ov.start - cursor}"
+            rec.shards.append(ShardRecord(rank=rank, file=shard_filename(rank), offset=ov.start - cursor,
+                                          length=ov.length, key=key))
+            cache32.add(shard_filename(rank), key, shards32[rank][ov.start - rank * s_src : ov.end - rank * s_src])
+        records32[name] = rec
+        cursor += numel
+    dests = [torch.empty(s8, dtype=torch.float64, device=device) for _ in range(8)]
+
+    def run64():
+        for dest, items in zip(dests, layouts8):
+            load_flat_shard(dest, items, records32, cache32)
+
+    ms = _time_events(run64, max(steps, 5), max(warmup, 2))
+    _emit("flat-interval reshard with a cast, fp32 -> fp64: elements/s", "elements/s", total / (ms * 1e-3), ms,
+          max(steps, 5), max(warmup, 2), "f32->f64", "Llama-3-8B fp32 flat shards, W=4 -> W=8 float64 shards",
+          12 * total, {"elements": total, "bytes_per_element": 12},
+          _secondary_traffic("reshard", [f"fp32 -> fp64: one destination shard of {s8:,} elements (W=8)"], [8]))
+    del dests, shards32, cache32
+    torch.cuda.empty_cache()
     return 0
 
 
@@ -585,11 +670,13 @@ def bench_scaler(steps: int, warmup: int) -> int:
     placements = [
         (False, 34, "loss-scaled clipped AdamW step, reference placement (eager unscale_, eager in-place clip): params/s",
          "defer_unscale=False, defer_clip=False", ["reference placement: eager unscale_ with its overflow check, one pass",
+                                                  "reference placement: fold of the piece sums",
                                                   "reference placement: eager in-place clip of .grad",
-                                                  "reference placement: AdamW of the clipped gradient"], [1, 1, 1]),
+                                                  "reference placement: AdamW of the clipped gradient"], [1, 1, 1, 1]),
         (True, 32, "loss-scaled clipped AdamW step, reference placement with the clip in the update: params/s",
          "defer_unscale=False, clip_in_step=True", ["reference placement: eager unscale_ with its overflow check, one pass",
-                                                   "clip_in_step: clip + AdamW, clipped g written back"], [1, 1]),
+                                                   "reference placement: fold of the piece sums",
+                                                   "clip_in_step: clip + AdamW, clipped g written back"], [1, 1, 1]),
     ]
     for in_step, per_param, metric, label, traffic_labels, launches in placements:
         opt = ShardedOptimizer([param], OptimizerConfig(learning_rate=3e-4, betas=(0.9, 0.95), weight_decay=0.1),
@@ -799,6 +886,33 @@ def bench_fsdp(steps: int, warmup: int) -> int:
           f"Llama-3-8B rank 0 of W={world}: {world} padded bf16 gradients -> fp32 shard, with norm partials",
           (2 * world + 4) * shard, {"shard_numel": shard, "world": world, "bytes_per_element": 2 * world + 4},
           _secondary_traffic("fsdp", ["gradient local share with norm partials"], [1]), cpu.get("share"))
+
+    # The same share reduced in float64 into a float64 shard (reduce and master dtype
+    # float64): read 8 x 2 B + write 8 B per shard element, with float64 norm partials.
+    from hybrid_training_amd import _native
+
+    lib = _native.library()
+    out64 = torch.empty(shard, dtype=torch.float64, device=device)
+    chunk64 = 16384
+    partials64 = torch.empty(-(-shard // chunk64), dtype=torch.float64, device=device)
+    tiles64 = torch.empty(-(-shard // 256), dtype=torch.float64, device=device)
+    grad_ptrs = _native.pointer_array([g.data_ptr() for g in grads])
+
+    def share64():
+        _native.check(lib.hbt_grad_local_share_sqnorm(
+            grad_ptrs, world, 0, shard, shard, _native.dtype_code(torch.bfloat16), _native.dtype_code(torch.float64),
+            float(world), _native.dtype_code(torch.float64), out64.data_ptr(), partials64.data_ptr(),
+            tiles64.data_ptr(), _native.stream_of(device)), "bench.local_share_f64")
+
+    ms = _time_events(share64, max(steps, 5), max(warmup, 2))
+    _emit("FSDP gradient local share, float64 reduce: shard elements/s", "elements/s", shard / (ms * 1e-3), ms,
+          max(steps, 5), max(warmup, 2), "bf16->f64",
+          f"Llama-3-8B rank 0 of W={world}: {world} padded bf16 gradients reduced in float64 into a float64 shard, "
+          "with norm partials", (2 * world + 8) * shard,
+          {"shard_numel": shard, "world": world, "bytes_per_element": 2 * world + 8},
+          _secondary_traffic("fsdp", ["float64 reduce: local share with norm partials",
+                                      "float64 reduce: tile sums to partials"], [1, 1]))
+    del out64, partials64, tiles64
 
     from hybrid_training_amd import OptimizerConfig, ShardedOptimizer
 
@@ -1257,6 +1371,112 @@ def bench_sgd(steps: int, warmup: int) -> int:
     return 0
 
 
+def bench_lowp(steps: int, warmup: int) -> int:
+    """The headline shard with bf16 masters: a bf16 model with mixed precision off keeps its
+    parameters, gradients and optimizer state in bf16 (``parallel/fsdp.py:379-393``).
+
+    AdamW: norm pass (read g: 2 B) + fused clip + AdamW (read p, g, m, v: 8 B; write p, m,
+    v: 6 B) = 16 B/param.  SGD with momentum 0.9: norm pass (2 B) + fused clip + SGD (read
+    p, g, buf: 6 B; write p, buf: 4 B) = 12 B/param.
+    """
+    import torch
+
+    from hybrid_training_amd import GroupHandle, OptimizerConfig, ShardedOptimizer
+
+    device = torch.device("cuda", 0)
+    n = SHARD_NUMEL
+    gen = torch.Generator(device=device).manual_seed(12)
+    param = torch.nn.Parameter(torch.empty(n, dtype=torch.bfloat16, device=device))
+    grad = torch.empty(n, dtype=torch.bfloat16, device=device)
+    for start in range(0, n, 1 << 28):
+        stop = min(n, start + (1 << 28))
+        param.data[start:stop] = torch.randn(stop - start, device=device, generator=gen).mul_(0.02).to(torch.bfloat16)
+        grad[start:stop] = torch.randn(stop - start, device=device, generator=gen).mul_(1e-4).to(torch.bfloat16)
+    runs = [("adamw", OptimizerConfig(learning_rate=LR, betas=BETAS, eps=EPS, weight_decay=WD), 16, None,
+             "sharded AdamW+clip step, bf16 masters: params/s", ["bf16 masters: fused clip + AdamW", "norm pass"]),
+            ("sgd", OptimizerConfig(name="sgd", learning_rate=LR, momentum=0.9, weight_decay=WD), 12, 0.9,
+             "sharded SGD(momentum 0.9)+clip step, bf16 masters: params/s",
+             ["bf16 masters: fused clip + SGD with momentum", "norm pass"])]
+    for name, config, per_param, momentum, metric, labels in runs:
+        opt = ShardedOptimizer([param], config, norm_group=GroupHandle.trivial("world"), device=device, defer_clip=True)
+        param.grad = grad
+
+        def step():
+            opt.clip_grad_norm(MAX_NORM)
+            opt.step()
+            param.grad = grad
+
+        ms = _time_events(step, steps, warmup)
+        _emit(metric, "params/s", n / (ms * 1e-3), ms, steps, warmup, "bf16",
+              f"Llama-3-8B FSDP rank shard at W=8, bf16 parameters, gradients and {name} state", per_param * n,
+              {"shard_numel": n, "bytes_per_param": per_param},
+              _secondary_traffic("lowp", labels, [1, 1]),
+              _cpu_step_line(1 << 26, 3, momentum=momentum, dtype=torch.bfloat16) if _WITH_CPU else None)
+        del opt
+        param.grad = None
+        torch.cuda.empty_cache()
+    return 0
+
+
+def bench_mlp(steps: int, warmup: int) -> int:
+    """The reference's CPU-runnable case on the device: the MLP Linear(23,32)-ReLU-Linear(32,32)-
+    ReLU-Linear(32,1) (1,857 fp32 parameters) as FSDP units at W=2 (shards of 929, pad 1) and
+    W=4 (465, pad 3), all ranks on one GPU.  Per rank and step, the drop-in tail: the local
+    share of the ranks' padded gradients (the AVG reduce-scatter's arithmetic, with norm
+    partials), the clip from those partials and the fused AdamW (lr 1e-3, wd 0.01) on the
+    flat shard.  Microseconds per rank-step at this size measure launch cost, not HBM.
+    """
+    import torch
+
+    from hybrid_training_amd import (FlatParamHandle, FSDPConfig, GroupHandle, MixedPrecisionConfig,
+                                     OptimizerConfig, ShardedOptimizer)
+
+    device = torch.device("cuda", 0)
+    torch.manual_seed(0)
+    model = torch.nn.Sequential(torch.nn.Linear(23, 32), torch.nn.ReLU(), torch.nn.Linear(32, 32), torch.nn.ReLU(),
+                                torch.nn.Linear(32, 1)).to(device)
+    named = list(model.named_parameters())
+    mp = MixedPrecisionConfig(enabled=False)
+    for world in (2, 4):
+        handles = [FlatParamHandle(named, None, GroupHandle.local_view("shard", world, r), FSDPConfig(), mp, device,
+                                   keep_originals=True) for r in range(world)]
+        padded, shard = handles[0].padded_numel, handles[0].shard_numel
+        gen = torch.Generator(device=device).manual_seed(world)
+        grads = [torch.randn(padded, device=device, generator=gen) for _ in range(world)]
+        for g in grads:
+            g[1857:] = 0.0  # the padding carries no gradient
+        opts = [ShardedOptimizer([h.flat_param], OptimizerConfig(learning_rate=1e-3, weight_decay=0.01),
+                                 norm_group=GroupHandle.local_view("world", world, r), device=device, defer_clip=True)
+                for r, h in enumerate(handles)]
+
+        def tail():
+            for r, (h, opt) in enumerate(zip(handles, opts)):
+                h.flat_param.grad = h.reduce_scatter_gradient(grads[r], peer_grads=grads)
+                opt.clip_grad_norm(1.0)
+                opt.step()
+
+        ms = _time_events(tail, max(steps, 50), max(warmup, 10))
+        cpu = None
+        if _WITH_CPU:
+            from oracle.cpu_reference_path import ReferenceMlpTail
+
+            ref = ReferenceMlpTail([g.cpu() for g in grads], shard, lr=1e-3, weight_decay=0.01)
+            seconds = _cpu_time(lambda: ref.step(1.0), 200)
+            cpu = _cpu_line(world, seconds, "rank-steps/s",
+                            f"the {world}-rank tail on {shard}-element shards: local shares, fp64 norm, clip, "
+                            "torch.optim.AdamW(foreach=False) per rank (tensors this small run on one thread); "
+                            "200 timed steps after 1 warm-up")
+        per_rank_us = ms * 1e3 / world
+        _emit(f"FSDP MLP drop-in tail at W={world} (local share + clip + AdamW): rank-steps/s", "rank-steps/s",
+              world / (ms * 1e-3), ms, max(steps, 50), max(warmup, 10), "f32",
+              f"MLP 23-32-32-1 (1,857 fp32 params), FSDP W={world}: shards of {shard}, all ranks on one GPU",
+              world * shard * (4 * world + 4 + 28),
+              {"params": 1857, "world": world, "shard_numel": shard, "us_per_rank_step": per_rank_us},
+              None, cpu)
+        del handles, opts, grads
+    return 0
+
+
 def bench_torch_adamw(steps: int, warmup: int) -> int:
     """Stock PyTorch on the same GPU and shard: clip_grad_norm_ (foreach) + AdamW(fused=True).
 
@@ -1306,7 +1526,8 @@ def bench_copy_ceiling(steps: int, warmup: int) -> int:
 
 SECONDARY = {"buckets": bench_buckets, "reshard": bench_reshard, "scaler": bench_scaler, "fsdp": bench_fsdp,
              "inplace_clip": bench_inplace_clip, "torch_adamw": bench_torch_adamw, "sgd": bench_sgd,
-             "offload": bench_offload, "param_offload": bench_param_offload, "checkpoint": bench_checkpoint, "copy_ceiling": bench_copy_ceiling}
+             "offload": bench_offload, "param_offload": bench_param_offload, "checkpoint": bench_checkpoint, "copy_ceiling": bench_copy_ceiling,
+             "lowp": bench_lowp, "mlp": bench_mlp}
 
 
 if __name__ == "__main__":

@@ -472,7 +472,7 @@ __global__ __launch_bounds__(kCopyBlock) void convert_kernel(const int64_t* __re
                                                              const int64_t* __restrict__ hints) {
     constexpr int64_t SB = elem_bytes<SD>();
     constexpr int64_t DB = elem_bytes<DD>();
-    constexpr int64_t kChunk = int64_t(kCopyBlock) * 16 / SB;
+    constexpr int64_t kChunk = chunk_elems<SB, DB>();
     const int64_t chunk = chunk_base + static_cast<int64_t>(blockIdx.x);
     const int64_t* rec = table + 4 * owning_record(table, count, chunk, hints);
     const int64_t e0 = (chunk - rec[3]) * kChunk;
@@ -490,7 +490,8 @@ __global__ __launch_bounds__(kCopyBlock) void convert_kernel(const int64_t* __re
 // lane moves units of U = 16 / max(source, destination bytes) elements, one access of
 // U * bytes on each side (16 on the wider side; 8 or 4 on the narrower one), consecutive
 // lanes on consecutive units; a 1 KB-of-source chunk is kPerLane units per lane (1 for a
-// float64 source, 2 or 4 when widening to float64), all loaded before the first store.
+// float64 source; a widening chunk is 2 KB of source, 4 or 8 units per lane), all loaded
+// before the first store.
 // The bits are convert_kernel's.
 template <int SD, int DD, int OP>
 __global__ __launch_bounds__(kCopyBlock) void convert_aligned_kernel(const int64_t* __restrict__ table,
@@ -502,7 +503,7 @@ __global__ __launch_bounds__(kCopyBlock) void convert_aligned_kernel(const int64
     constexpr int U = 16 / (SB > DB ? SB : DB);
     constexpr int SW = U * SB / 4;
     constexpr int DW = U * DB / 4;
-    constexpr int64_t kChunk = int64_t(kCopyBlock) * 16 / SB;
+    constexpr int64_t kChunk = chunk_elems<SB, DB>();
     constexpr int kPerLane = static_cast<int>(kChunk / (int64_t(kCopyBlock) * U));
     static_assert(kChunk == int64_t(kPerLane) * kCopyBlock * U, "a chunk is whole units on every lane");
     const int64_t chunk = chunk_base + static_cast<int64_t>(blockIdx.x);
@@ -627,9 +628,10 @@ int64_t hbt_copy_chunk_elems(int32_t src_dtype, int32_t dst_dtype) {
     const int ssz = dtype_size(src_dtype);
     const int dsz = dtype_size(dst_dtype);
     if (ssz == 0 || dsz == 0) return -1;
-    // F64 -> F64: the chunk of the DIVIDE op (a same-dtype COPY moves F32 dword pairs).
-    if (ssz == 2 && dsz == 4) return chunk_elems<2, 4>();  // 2 KB of source
-    return int64_t(kCopyBlock) * 16 / ssz;                  // 1 KB of source
+    // 1 KB of source, 2 KB when widening (the convert kernels' chunks are the copy
+    // kernels'); F64 -> F64: the chunk of the DIVIDE op (a same-dtype COPY moves F32 dword
+    // pairs).
+    return int64_t(kCopyBlock) * 16 / ssz * (ssz < dsz ? 2 : 1);
 }
 
 int32_t hbt_copy_intervals(const int64_t* table, int64_t count, int64_t total_chunks,

@@ -38,6 +38,49 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 template <int D>
 constexpr int64_t bytes_of() { return D == F32 ? 4 : (D == HBT_DTYPE_F64 ? 8 : 2); }
 
+// Two fp32 values rounded to the 2-byte dtype RD (nearest even) and packed low half first by
+// one packed conversion: the bits f32_to_b16 gives for each, except that a bf16 NaN keeps the
+// conversion's encoding (pack_rounded and store_vec write 0x7FC0 instead).
+template <int RD>
+__device__ __forceinline__ uint32_t pack2_rounded(float a, float b) {
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    if constexpr (RD == BF16) {
+        typedef __bf16 r2 __attribute__((ext_vector_type(2)));
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{opaque(a), opaque(b)}, r2));
+    } else {
+        static_assert(RD == F16, "2-byte dtypes are bf16 and fp16");
+        typedef _Float16 r2 __attribute__((ext_vector_type(2)));
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{opaque(a), opaque(b)}, r2));
+    }
+}
+
+// 2N fp32 values rounded to the 2-byte dtype RD and packed into N dwords, a bf16 NaN as
+// 0x7FC0: f32_to_b16's bits for each, in N conversions and 2N compares, where f32_to_b16
+// takes about 7 operations per element.
+template <int RD, int N>
+__device__ __forceinline__ void pack_rounded(const float (&y)[2 * N], uint32_t (&o)[N]) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) o[i] = pack2_rounded<RD>(y[2 * i], y[2 * i + 1]);
+    if constexpr (RD == BF16) {
+        bool nan = false;
+#pragma unroll
+        for (int c = 0; c < 2 * N; ++c) nan = nan || y[c] != y[c];
+        if (nan) {
+#pragma unroll
+            for (int i = 0; i < N; ++i) {
+                if (y[2 * i] != y[2 * i]) o[i] = (o[i] & 0xFFFF0000u) | 0x7FC0u;
+                if (y[2 * i + 1] != y[2 * i + 1]) o[i] = (o[i] & 0xFFFFu) | 0x7FC00000u;
+            }
+        }
+    }
+}
+template <int RD>
+__device__ __forceinline__ u32x4 pack8_rounded(const float (&y)[8]) {
+    uint32_t o[4];
+    pack_rounded<RD, 4>(y, o);
+    return u32x4{o[0], o[1], o[2], o[3]};
+}
+
 // ---- vector memory helpers ----------------------------------------------------------
 // Every operand is touched exactly once per step, so loads and stores are marked
 // non-temporal: the lines are not kept in L2/MALL for reuse that never comes.
@@ -79,15 +122,12 @@ __device__ __forceinline__ void store_vec(void* base, int64_t e, const float (&x
         static_assert(K == 4, "fp32 vectors are four elements");
         __builtin_nontemporal_store(f32x4{x[0], x[1], x[2], x[3]}, reinterpret_cast<f32x4*>(static_cast<float*>(base) + e));
     } else if constexpr (K == 4) {
-        const u32x2 w{f32_to_b16<D == F16>(x[0]) | (f32_to_b16<D == F16>(x[1]) << 16),
-                      f32_to_b16<D == F16>(x[2]) | (f32_to_b16<D == F16>(x[3]) << 16)};
-        __builtin_nontemporal_store(w, reinterpret_cast<u32x2*>(static_cast<uint16_t*>(base) + e));
+        uint32_t w[2];
+        pack_rounded<D, 2>(x, w);
+        __builtin_nontemporal_store(u32x2{w[0], w[1]}, reinterpret_cast<u32x2*>(static_cast<uint16_t*>(base) + e));
     } else {
         static_assert(K == 8, "2-byte vectors are four or eight elements");
-        u32x4 w;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) w[i] = f32_to_b16<D == F16>(x[2 * i]) | (f32_to_b16<D == F16>(x[2 * i + 1]) << 16);
-        __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(static_cast<uint16_t*>(base) + e));
+        __builtin_nontemporal_store(pack8_rounded<D>(x), reinterpret_cast<u32x4*>(static_cast<uint16_t*>(base) + e));
     }
 }
 template <int D>
@@ -480,45 +520,6 @@ __device__ __forceinline__ double add_sq(double acc, float x) {
     return __builtin_fma(d, d, acc);
 }
 
-// Two fp32 values rounded to the 2-byte dtype RD (nearest even) and packed low half first by
-// one packed conversion: the bits store_vec<RD> writes for them, except that a bf16 NaN keeps
-// the conversion's encoding (a caller that stores it writes 0x7FC0 instead).
-template <int RD>
-__device__ __forceinline__ uint32_t pack2_rounded(float a, float b) {
-    typedef float f2 __attribute__((ext_vector_type(2)));
-    if constexpr (RD == BF16) {
-        typedef __bf16 r2 __attribute__((ext_vector_type(2)));
-        return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{opaque(a), opaque(b)}, r2));
-    } else {
-        static_assert(RD == F16, "2-byte dtypes are bf16 and fp16");
-        typedef _Float16 r2 __attribute__((ext_vector_type(2)));
-        return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{opaque(a), opaque(b)}, r2));
-    }
-}
-
-// Eight fp32 values rounded to the 2-byte dtype RD and packed into one 16-byte vector, a
-// bf16 NaN as 0x7FC0: the vector store_vec<RD, 8> writes for them, in 4 conversions and 8
-// compares where the float round trip through round_to and f32_to_b16 takes about 7
-// operations per element.
-template <int RD>
-__device__ __forceinline__ u32x4 pack8_rounded(const float (&y)[8]) {
-    u32x4 o;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) o[i] = pack2_rounded<RD>(y[2 * i], y[2 * i + 1]);
-    if constexpr (RD == BF16) {
-        bool nan = false;
-#pragma unroll
-        for (int c = 0; c < 8; ++c) nan = nan || y[c] != y[c];
-        if (nan) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                if (y[2 * i] != y[2 * i]) o[i] = (o[i] & 0xFFFF0000u) | 0x7FC0u;
-                if (y[2 * i + 1] != y[2 * i + 1]) o[i] = (o[i] & 0xFFFFu) | 0x7FC00000u;
-            }
-        }
-    }
-    return o;
-}
 
 // A lane's eight elements of a piece from element e0 (its first), squared after the
 // unscale: vector loads when the whole lane vector lies inside and is aligned.
@@ -952,7 +953,7 @@ __device__ __forceinline__ double share_div64(double x, double divisor, double r
     return x / divisor;
 }
 
-template <int IB, bool IH, int OD, bool kRecip>
+template <int IB, bool IH, int OD, bool kRecip, int kG = 0>
 __global__ __launch_bounds__(kShareBlock) void local_share_f64_tiles_kernel(
     ShareRanks ranks, int32_t group_size, int64_t offset, int64_t shard_numel, int64_t valid_numel,
     double divisor, double recip, int32_t vec_ok, void* __restrict__ out, double* __restrict__ tile_sums,
@@ -961,31 +962,64 @@ __global__ __launch_bounds__(kShareBlock) void local_share_f64_tiles_kernel(
     const int64_t first = tile * kShareTile + int64_t(threadIdx.x) * 4;
     double acc = 0.0;
     if (vec_ok && tile * kShareTile + kShareTile <= valid_numel) {
-        double s[4], x[4], y[4];
-        load4_as_f64<IB, IH>(ranks.g[0] + offset * IB, first, x);
+        double s[4];
+        if constexpr (kG > 0) {
+            // A fixed group of fp32 / 2-byte inputs: every rank's vector is loaded (the
+            // loads waited for in pairs, as in local_share_tiles_kernel) before the first
+            // is summed, and held in its own width until it is widened.
+            static_assert(IB < 8, "float64 inputs take the run-time group path");
+            float f[kG][4];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) s[c] = share_div64<kRecip>(x[c], divisor, recip);
-        int32_t q = 1;
-        for (; q + 1 < group_size; q += 2) {
-            load4_as_f64<IB, IH>(ranks.g[q] + offset * IB, first, x);
-            load4_as_f64<IB, IH>(ranks.g[q + 1] + offset * IB, first, y);
+            for (int q = 0; q < kG; ++q) {
+                load_vec<dtype_of<IB, IH>(), 4>(ranks.g[q] + offset * IB, first, f[q]);
+                if ((q + 1) % 2 == 0 && q + 1 < kG) wait_vmem();
+            }
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
-                s[c] = s[c] + share_div64<kRecip>(x[c], divisor, recip);
-                s[c] = s[c] + share_div64<kRecip>(y[c], divisor, recip);
-            }
-        }
-        if (q < group_size) {
-            load4_as_f64<IB, IH>(ranks.g[q] + offset * IB, first, x);
+                s[c] = share_div64<kRecip>(static_cast<double>(f[0][c]), divisor, recip);
 #pragma unroll
-            for (int c = 0; c < 4; ++c) s[c] = s[c] + share_div64<kRecip>(x[c], divisor, recip);
+                for (int q = 1; q < kG; ++q) s[c] = s[c] + share_div64<kRecip>(static_cast<double>(f[q][c]), divisor, recip);
+            }
+        } else {
+            double x[4], y[4];
+            load4_as_f64<IB, IH>(ranks.g[0] + offset * IB, first, x);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) s[c] = share_div64<kRecip>(x[c], divisor, recip);
+            int32_t q = 1;
+            for (; q + 1 < group_size; q += 2) {
+                load4_as_f64<IB, IH>(ranks.g[q] + offset * IB, first, x);
+                load4_as_f64<IB, IH>(ranks.g[q + 1] + offset * IB, first, y);
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    s[c] = s[c] + share_div64<kRecip>(x[c], divisor, recip);
+                    s[c] = s[c] + share_div64<kRecip>(y[c], divisor, recip);
+                }
+            }
+            if (q < group_size) {
+                load4_as_f64<IB, IH>(ranks.g[q] + offset * IB, first, x);
+#pragma unroll
+                for (int c = 0; c < 4; ++c) s[c] = s[c] + share_div64<kRecip>(x[c], divisor, recip);
+            }
         }
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             s[c] = narrow_from_f64<OD>(s[c]);
             acc += s[c] * s[c];
         }
-        store4_from_f64<OD>(out, first, s);
+        if constexpr (OD == HBT_DTYPE_F64) {
+            // A lane's four doubles are 32 contiguous bytes; staged through LDS, each store
+            // instruction writes 1 KB contiguous (lane l: elements 2l, 2l + 1 of each half
+            // of the tile) instead of every other 16 bytes of 2 KB.
+            __shared__ f64x2 stage[2 * kShareBlock];
+            stage[2 * threadIdx.x] = f64x2{s[0], s[1]};
+            stage[2 * threadIdx.x + 1] = f64x2{s[2], s[3]};
+            __syncthreads();
+            f64x2* o = reinterpret_cast<f64x2*>(static_cast<double*>(out) + tile * kShareTile);
+            __builtin_nontemporal_store(stage[threadIdx.x], o + threadIdx.x);
+            __builtin_nontemporal_store(stage[threadIdx.x + kShareBlock], o + kShareBlock + threadIdx.x);
+        } else {
+            store4_from_f64<OD>(out, first, s);
+        }
     } else if (vec_ok && tile * kShareTile >= valid_numel && tile * kShareTile + kShareTile <= shard_numel) {
         const double zero[4] = {0.0, 0.0, 0.0, 0.0};
         store4_from_f64<OD>(out, first, zero);
@@ -1753,10 +1787,16 @@ int32_t local_share(const char* who, const void* const* rank_grads, int32_t grou
         else if (reduce_dtype == BF16) HBT_TILES_OD(ID, R, BF16);        \
         else HBT_TILES_OD(ID, R, F16);                                   \
     } while (0)
-#define HBT_TILES64R(IB, IH, OD, R)                                                                       \
-    local_share_f64_tiles_kernel<IB, IH, OD, R><<<grid, kShareBlock, 0, st>>>(                             \
+#define HBT_TILES64G(IB, IH, OD, R, G)                                                                    \
+    local_share_f64_tiles_kernel<IB, IH, OD, R, G><<<grid, kShareBlock, 0, st>>>(                          \
         ranks, group_size, offset, shard_numel, valid_numel, static_cast<double>(divisor),                 \
         static_cast<double>(recip), vec_ok, out, tile_scratch, first)
+// Groups of 8 narrower inputs have their own instantiation (the measured configuration).
+#define HBT_TILES64R(IB, IH, OD, R)                                        \
+    do {                                                                   \
+        if (IB < 8 && group_size == 8) HBT_TILES64G(IB, IH, OD, R, (IB < 8 ? 8 : 0)); \
+        else HBT_TILES64G(IB, IH, OD, R, 0);                               \
+    } while (0)
 #define HBT_TILES64(IB, IH, OD)                                \
     do {                                                       \
         if (recip_exact) HBT_TILES64R(IB, IH, OD, true);       \
@@ -1784,6 +1824,7 @@ int32_t local_share(const char* who, const void* const* rank_grads, int32_t grou
 #undef HBT_TILES64_OD
 #undef HBT_TILES64
 #undef HBT_TILES64R
+#undef HBT_TILES64G
 #undef HBT_TILES_RD
 #undef HBT_TILES_OD
 #undef HBT_TILES_G

@@ -215,8 +215,9 @@ int32_t hbt_grad_norm_noalloc(const void* const* grads, const int64_t* numels, c
  * where first_chunk is the exclusive prefix sum over records of
  * ceil(numel / hbt_copy_chunk_elems(src_dtype, dst_dtype)), and total_chunks is the
  * sum.  A chunk is 1 KB of source: 128 elements of an 8-byte source, 256 of a 4-byte
- * one, 512 of a 2-byte one, except 2 KB (1024 elements) for BF16/F16 -> F32, whose
- * workgroups write twice what they read; hbt_copy_chunk_elems returns -1 for unknown dtypes.
+ * one, 512 of a 2-byte one, except 2 KB when the destination is wider (1024 elements for
+ * BF16/F16 -> F32 or F64, 512 for F32 -> F64), whose workgroups write more than they read;
+ * hbt_copy_chunk_elems returns -1 for unknown dtypes.
  * A same-dtype F64 COPY travels as F32 dword pairs (the numels doubled); F64 -> F64 with
  * src_dtype = dst_dtype = F64 is the DIVIDE op's.  All records share src_dtype/dst_dtype and op:
  *   HBT_COPY_OP_COPY    dst = src               (same dtype: byte copy; F32->BF16

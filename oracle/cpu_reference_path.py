@@ -23,13 +23,15 @@ import torch
 
 
 class ReferenceCpuStep:
-    """One flat fp32 shard with its gradient and a torch CPU AdamW."""
+    """One flat shard (fp32 unless ``dtype`` says otherwise: the parameters' own dtype
+    with mixed precision off) with its gradient and a torch CPU AdamW or SGD."""
 
     def __init__(self, numel: int, *, lr: float, betas: tuple[float, float], eps: float,
-                 weight_decay: float, seed: int = 0, momentum: float | None = None) -> None:
+                 weight_decay: float, seed: int = 0, momentum: float | None = None,
+                 dtype: torch.dtype = torch.float32) -> None:
         gen = torch.Generator().manual_seed(seed)
-        self.param = torch.nn.Parameter(torch.randn(numel, generator=gen) * 0.02)
-        self.grad = torch.randn(numel, generator=gen) * 1e-4
+        self.param = torch.nn.Parameter((torch.randn(numel, generator=gen) * 0.02).to(dtype))
+        self.grad = (torch.randn(numel, generator=gen) * 1e-4).to(dtype)
         if momentum is None:
             self.optimizer = torch.optim.AdamW(
                 [self.param], lr=lr, betas=betas, eps=eps, weight_decay=weight_decay, foreach=False
@@ -147,3 +149,44 @@ def unscale_and_check(grads: list[torch.Tensor], scale: float) -> bool:
         if not bool(torch.isfinite(g).all()):
             return True
     return False
+
+
+class ReferenceMlpTail:
+    """The per-step tail of the reference's FSDP MLP training at group size ``world``, all
+    ranks on this host (``tests/distributed/test_fsdp.py:86-151`` trains it with Gloo):
+    each rank's share of the AVG reduce-scatter of the ranks' padded flat gradients
+    (:func:`local_share`), the global gradient norm (each rank's ``grad.to(float64)
+    .pow(2).sum()``, the all-reduce's sum in rank order, ``clamp_min(0).sqrt()``,
+    ``optim/sharded_optimizer.py:151-158, 241``), the clip (``:333-337``) and each rank's
+    ``torch.optim.AdamW`` step on its flat shard (``:355``)."""
+
+    def __init__(self, full_grads: list[torch.Tensor], shard: int, *, lr: float, weight_decay: float,
+                 seed: int = 0) -> None:
+        gen = torch.Generator().manual_seed(seed)
+        self.world = len(full_grads)
+        self.shard = shard
+        self.grads = [g.detach().cpu().float().reshape(-1) for g in full_grads]
+        self.params = [torch.nn.Parameter(torch.randn(shard, generator=gen) * 0.1) for _ in range(self.world)]
+        self.optimizers = [torch.optim.AdamW([p], lr=lr, weight_decay=weight_decay, foreach=False)
+                           for p in self.params]
+
+    def step(self, max_norm: float) -> float:
+        """One step of every rank; returns the pre-clip global norm."""
+        shares = []
+        for rank in range(self.world):
+            lo = rank * self.shard
+            shares.append(local_share([g[lo : lo + self.shard] for g in self.grads], None, self.world,
+                                      torch.float32, torch.float32))
+        squared = None
+        for share in shares:
+            part = share.to(torch.float64).pow(2).sum()
+            squared = part if squared is None else squared + part
+        norm = float(squared.clamp_min(0).sqrt())
+        coefficient = float(max_norm) / (norm + 1e-6)
+        for p, share, opt in zip(self.params, shares, self.optimizers):
+            if coefficient < 1.0:
+                share.mul_(coefficient)
+            p.grad = share
+            opt.step()
+            p.grad = None
+        return norm

@@ -114,7 +114,8 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     # conversions: division is refused for float64 and bf16 <-> fp16 pairs (before the table is read)
     assert lib.hbt_copy_intervals(fake, 1, 1, 3, 0, 1, 2.0, 0, None) == -2
     assert lib.hbt_copy_intervals(fake, 1, 1, 1, 2, 1, 2.0, 0, None) == -2
-    assert lib.hbt_copy_chunk_elems(3, 0) == 128 and lib.hbt_copy_chunk_elems(0, 3) == 256
+    assert lib.hbt_copy_chunk_elems(3, 0) == 128 and lib.hbt_copy_chunk_elems(0, 3) == 512
+    assert lib.hbt_copy_chunk_elems(1, 3) == 1024 and lib.hbt_copy_chunk_elems(2, 3) == 1024
     assert lib.hbt_copy_chunk_elems(1, 2) == 512 and lib.hbt_copy_chunk_elems(3, 3) == 128
     assert lib.hbt_grad_accumulate(None, None, None, 0, 0, 0, 2, None) == -1  # unknown flag
     assert lib.hbt_grad_accumulate(None, None, None, 1, 0, 0, 0, None) == -1  # null table
