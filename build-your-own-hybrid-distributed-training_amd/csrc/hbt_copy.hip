@@ -21,19 +21,11 @@ namespace hbt {
 namespace {
 
 // One wavefront per workgroup reading 16 bytes of source per lane: a workgroup reads
-// 1 KB and retires.  Measured on MI355X with the aligned kernel:
-//   * fp32 -> fp32, Llama-3-8B unpack (298 records, 64 GB moved): 6.6 TB/s, against
-//     6.0 TB/s reading 2 KB per workgroup;
-//   * bf16 -> fp32 pack of the same model: 6.5 TB/s, against 5.0 TB/s reading 512 B.
-// 256-thread workgroups walking 64K-element chunks ran at 5.0 TB/s.
-#ifndef HBT_COPY_BLOCK
-#define HBT_COPY_BLOCK 64
-#endif
-#ifndef HBT_COPY_NT
-#define HBT_COPY_NT 1
-#endif
-constexpr int kCopyBlock = HBT_COPY_BLOCK;
-constexpr bool kCopyNT = HBT_COPY_NT != 0;
+// 1 KB and retires, the shape that streamed fastest against 512 B or 2 KB per
+// workgroup and against 256-thread workgroups walking larger chunks.
+constexpr int kCopyBlock = 64;
+// Non-temporal loads and stores: every byte is moved once.
+constexpr bool kCopyNT = true;
 
 // A vector of NW dwords (NW = 2 or 4).
 template <int NW>
@@ -160,12 +152,10 @@ __device__ __forceinline__ void store_elem(gbyte* p, uint32_t bits) {
 // Elements per lane unit: one 16-byte access on the wider side of the copy.
 template <int SB, int DB>
 constexpr int unit_elems() { return 16 / (SB > DB ? SB : DB); }
-// Elements per chunk (per workgroup): 16 bytes of source per lane, 32 for a widening
-// 2-byte -> fp32 copy.  A widening chunk writes twice what it reads, and its stores do
+// Elements per chunk (per workgroup): 16 bytes of source per lane, 32 when the
+// destination is wider.  A widening chunk writes more than it reads, and its stores do
 // not hold the workgroup, so with 1 KB of source the workgroups retired faster than
-// their writes drained: bf16 -> fp32 over 4 GB of output ran at 5.9 TB/s with 1 KB of
-// source per workgroup, 6.4 TB/s with 2 KB and 5.9 TB/s with 4 KB.  Doubling the chunk
-// of every pair lost 0.4 TB/s on same-size and narrowing copies.
+// their writes drained; same-size and narrowing copies keep 1 KB.
 template <int SB, int DB>
 constexpr int64_t chunk_elems() { return int64_t(kCopyBlock) * 16 / SB * (SB < DB ? 2 : 1); }
 
@@ -200,8 +190,8 @@ __device__ __forceinline__ void pack_unit_store(gbyte* d, const uint32_t (&e)[U]
 // Index of the record that owns `chunk`: the last record whose first_chunk <= chunk
 // (the host drops records with no chunks, so first_chunk strictly increases).  The
 // search runs on the scalar unit: its loads hit the scalar cache and do not queue behind
-// the vector traffic of the waves in flight.  (A 64-way search with one ballot over
-// vector loads measured slower: 5.8 against 6.5 TB/s on a 40-record reshard.)  With
+// the vector traffic of the waves in flight (a wave-wide search over vector loads waits
+// behind that traffic and was slower).  With
 // hints (the table followed by hints[j] = the record owning chunk j * kHintStride) the
 // search starts at the hinted record and steps forward, at most as many records as
 // start inside one hint stride; without them it bisects the whole table, log2(count)

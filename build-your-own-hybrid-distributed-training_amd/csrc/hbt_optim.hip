@@ -182,7 +182,7 @@ __device__ __forceinline__ void load4_as_f64(const void* base, int64_t e, double
 
 // Wait for every outstanding vector-memory load of this wave (s_waitcnt vmcnt(0)).
 // Issuing a lane's operand streams one after the other, rather than all at once, keeps
-// the HBM request mix per wave simpler and measured ~2% faster.
+// the HBM request mix per wave simpler, and streamed faster.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 // The table entry owning workgroup `block`: the last t with first[t] <= block.
@@ -204,25 +204,14 @@ __device__ __forceinline__ float scaled_grad(float g, float unscale, float gmul)
 // ---- AdamW -----------------------------------------------------------------------
 // 32-thread workgroups, i.e. half a wavefront each, two 16-byte vectors per lane and
 // fp32 operand: 256 elements per workgroup (512 for 2-byte parameters, whose 16-byte
-// vectors hold eight).  Measured on MI355X on the fp32 4-read/3-write stream (1e9
-// elements): 6.38 TB/s, against 5.87 TB/s for full-wave 64-thread workgroups, 5.4 TB/s
-// for 128 threads and under 5 TB/s for 16 threads or 256-thread workgroups; persistent
-// grid-stride variants are slower.
-#ifndef HBT_ADAM_BLOCK
-#define HBT_ADAM_BLOCK 32
-#endif
-constexpr int kAdamBlock = HBT_ADAM_BLOCK;
+// vectors hold eight).  Of the workgroup sizes, vector counts and persistent variants
+// tried on the fp32 4-read / 3-write stream, this short-lived shape streamed fastest.
+constexpr int kAdamBlock = 32;
 // Vectors per lane: two for the step alone; one when the scaled gradient is also written
-// back (4 reads and 4 writes per element), measured 3.5% faster there (5.19 against
-// 5.38 ms for AdamW on the 1e9-element fp32 shard); without the write-back the two tie.
-#ifndef HBT_ADAM_UNROLL
-#define HBT_ADAM_UNROLL 2
-#endif
-#ifndef HBT_ADAM_WB_UNROLL
-#define HBT_ADAM_WB_UNROLL 1
-#endif
+// back (4 reads and 4 writes per element), which was faster there; without the
+// write-back the two tie.
 template <bool kWriteBack>
-constexpr int adam_unroll() { return kWriteBack ? HBT_ADAM_WB_UNROLL : HBT_ADAM_UNROLL; }
+constexpr int adam_unroll() { return kWriteBack ? 1 : 2; }
 template <int PD>
 constexpr int adam_vec() { return PD == F32 ? 4 : 8; }
 template <int PD, bool kWriteBack>
@@ -307,12 +296,9 @@ __global__ __launch_bounds__(kAdamBlock) void adamw_kernel(AdamTable tab, AdamSc
     if (tab.vec_ok[t] && base + kTile <= n) {
         float pv[kUnroll][K], gv[kUnroll][K], mv[kUnroll][K], vv[kUnroll][K];
         // One stream at a time, each load waited for before the next stream's is issued,
-        // and the gradient written back (when it is) as soon as it is scaled.  Measured on
-        // MI355X over a 1e9-element fp32 shard (same process, alternated): 6.37 TB/s for
-        // this order, against 6.30 with both vectors of one stream issued before a wait,
-        // 6.23 with no waits and 6.18 with the streams in pairs; with the write-back,
-        // 5.25 ms for this order, 5.27 storing the gradient first among the stores and
-        // 5.32 storing it last.
+        // and the gradient written back (when it is) as soon as it is scaled: the fastest
+        // of the issue orders tried (both vectors of a stream before a wait, no waits,
+        // streams in pairs; the gradient stored first or last among the stores).
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
             const int64_t e = base + (int64_t(u) * kAdamBlock + threadIdx.x) * K;
@@ -721,39 +707,29 @@ __device__ __forceinline__ float share_cast(float x) {
     return round_to<RD>(x);
 }
 
-// One wave per 256-element tile: measured on MI355X (8 bf16 ranks -> fp32) this
-// short-lived shape streams at 6.4 TB/s, against 5.6 TB/s for the norm kernel's
-// 1024-thread, 8-tile workgroups.  kG > 0 fixes the group size so that every rank's
-// load is issued before the first is used; kG == 0 reads group_size at run time.  With
-// kG fixed the loads go out in pairs, each pair waited for before the next is issued:
-// 6.28 against 6.15 TB/s with all eight in flight at once (8 bf16 ranks in 16 GB
-// buffers; 6.63 against 6.38 TB/s when the rank slices are separate buffers).  Waiting
-// after every load, or after every four, measured no better than no wait.  The tile
-// sums cost nothing measurable (6.15 TB/s without them), and reducing them in LDS inside
-// 256- or 1024-thread workgroups measured slower (6.03 TB/s).
-// tile_sums may be null (the local share alone).
-#ifndef HBT_SHARE_ISSUE
-#define HBT_SHARE_ISSUE 2
-#endif
-constexpr int kShareIssue = HBT_SHARE_ISSUE;
+// One wave per 256-element tile, each rank's 512 B of bf16 read by one 8-byte load per
+// lane: of the per-wave sizes tried (128 to 512 elements) and the 1024-thread, 8-tile
+// workgroups of the norm kernel, this streams fastest, at the rate of a kernel that
+// only sums the same eight streams as raw words.  kG > 0 fixes the group size so that
+// every rank's load is issued before the first is used; kG == 0 reads group_size at run
+// time.  With kG fixed the loads go out in pairs, each pair waited for before the next
+// is issued, which beat all eight in flight at once, waiting after each load, and
+// waiting after four.  tile_sums may be null (the local share alone).
+constexpr int kShareIssue = 2;
 // With the accumulator rows (kAcc) each rank is two loads, its gradient and its row;
-// waiting after every rank's pair measured best: 8.62-8.65 ms for the 8-rank bf16 +
-// fp32-row reduction of a 1e9-element shard, against 8.84 waiting after every two ranks,
-// 8.82 after four or eight, and 8.70 with all gradients issued before the rows.
-#ifndef HBT_SHARE_ACC_ISSUE
-#define HBT_SHARE_ACC_ISSUE 1
-#endif
-constexpr int kShareAccIssue = HBT_SHARE_ACC_ISSUE;
+// waiting after every rank's pair streamed fastest (against every two, four or eight
+// ranks, or all gradients before the rows).
+constexpr int kShareAccIssue = 1;
 
 // Where tile t's sum is stored among a launch's `tiles` tile sums.  Workgroup b owns
 // tile b, and the dispatcher deals consecutive workgroups to the 8 XCDs in turn, each
 // with its own L2: stored at index t, every 64-byte line of sums would be written back
-// by eight XCDs in eight partial pieces (measured: 125 MB of writes for 31 MB of sums
-// over a 1e9-element shard).  So the sums of the tiles XCD x runs are stored together:
-// within each launch slice of n tiles, tile b goes to (b mod 8) * (n / 8) + b / 8 (the
-// last n mod 8 keep their index).  Giving each XCD a contiguous eighth of the tiles
-// instead fixes the writes as well but slowed the launch by 2.6%.  The slot is a
-// bijection, and the reader applies the same one, so the partials do not change.
+// by eight XCDs in eight partial pieces, four times the bytes of the sums.  So the sums
+// of the tiles XCD x runs are stored together: within each launch slice of n tiles,
+// tile b goes to (b mod 8) * (n / 8) + b / 8 (the last n mod 8 keep their index).
+// Giving each XCD a contiguous eighth of the tiles instead fixes the writes as well but
+// slowed the launch.  The slot is a bijection, and the reader applies the same one, so
+// the partials do not change.
 constexpr int kXcds = 8;
 __device__ __forceinline__ int64_t tile_sum_slot(int64_t t, int64_t tiles) {
     constexpr int64_t kSlice = kGridMaxItems / kShareBlock;  // launch_sliced's slices

@@ -337,8 +337,15 @@ def require_dense(tensor: torch.Tensor, operation: str) -> None:
         )
 
 
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(device: torch.device) -> int:
-    """Raw ``hipStream_t`` of torch's current stream on ``device``."""
+    """Raw ``hipStream_t`` of torch's current stream on ``device`` (read without building
+    a ``torch.cuda.Stream`` object: this is on every launch's host path)."""
+    if _RAW_STREAM is not None:
+        index = device.index if isinstance(device, torch.device) else torch.device(device).index
+        return int(_RAW_STREAM(torch.cuda.current_device() if index is None else index))
     return int(torch.cuda.current_stream(device).cuda_stream)
 
 

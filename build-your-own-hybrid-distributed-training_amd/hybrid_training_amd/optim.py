@@ -353,18 +353,31 @@ def gradient_norm_pass(
     launches: list[tuple[torch.dtype, float, list[tuple[torch.Tensor, int, int, float]], int]] = []
     total_partials = 0
     for (dtype, unscale), items in batches.items():
+        chunk_elems = norm_chunk_elems(dtype)  # hbt_norm_partials_count's chunk
         for start in range(0, len(items), _native.MAX_TENSORS_PER_LAUNCH):
             chunk = items[start : start + _native.MAX_TENSORS_PER_LAUNCH]
-            count = int(lib.hbt_norm_partials_count(_native.int64_array([n for _, _, n, _ in chunk]),
-                                                    len(chunk), _native.dtype_code(dtype)))
             launches.append((dtype, unscale, chunk, total_partials))
-            total_partials += count
+            total_partials += sum(-(-n // chunk_elems) for _, _, n, _ in chunk)
+    # sum, norm and the double clip multiplier, then the fp32 multiplier and the flag in
+    # the last 8 bytes: one allocation for the finalize's outputs.
+    scalars = torch.empty(4, dtype=torch.float64, device=device)
+    outputs = scalars[:3]
+    grad_mul = scalars[3:].view(torch.float32)[:1]
+    nonfinite = scalars[3:].view(torch.int32)[1:]
+    stream = _native.stream_of(device)
+    whole = _contiguous_cached_partials(launches, total_partials)
+    if whole is not None:
+        # Every segment's partials were written by its producer, with weight 1, one after
+        # another in one tensor in slot order: the finalize reads them where they are.
+        with torch.cuda.device(device):
+            _native.check(lib.hbt_grad_norm_finalize(whole, total_partials, float(max_norm), outputs.data_ptr(),
+                                                     outputs.data_ptr() + 8, grad_mul.data_ptr(),
+                                                     outputs.data_ptr() + 16, nonfinite.data_ptr(), stream),
+                          "optim.hbt_grad_norm_finalize")
+        return NormResult(sum=outputs[0], norm=outputs[1], grad_mul=grad_mul, nonfinite=nonfinite,
+                          grad_mul64=outputs[2:3])
     partials = torch.empty(max(1, total_partials), dtype=torch.float64, device=device)
     fresh: list[tuple[torch.Tensor, int, int, int, int]] = []  # segments whose partials are tagged
-    outputs = torch.empty(3, dtype=torch.float64, device=device)  # sum, norm, double clip multiplier
-    grad_mul = torch.empty(1, dtype=torch.float32, device=device)
-    nonfinite = torch.empty(1, dtype=torch.int32, device=device)
-    stream = _native.stream_of(device)
     with torch.cuda.device(device):
         for dtype, unscale, items, first in launches:
             # Items whose producer already wrote their partials take them from there
@@ -423,6 +436,33 @@ def gradient_norm_pass(
             setattr(grad, NORM_PARTIALS_ATTR, NormPartials(grad.data_ptr(), grad._version, found, grad.dtype))
     return NormResult(sum=outputs[0], norm=outputs[1], grad_mul=grad_mul, nonfinite=nonfinite,
                       grad_mul64=outputs[2:3])
+
+
+def _contiguous_cached_partials(launches, total_partials: int) -> int | None:
+    """The device address of the partials of every segment in ``launches``, when each
+    segment has a producer's partials (:class:`NormPartials`), weight 1 and no pending
+    unscale, and those partials lie one after another in one tensor in slot order, so a
+    finalize over that address sees what the copy into a fresh array would give it."""
+    address = None
+    expected = None
+    for dtype, unscale, items, _ in launches:
+        if unscale != 1.0:
+            return None
+        chunk_elems = norm_chunk_elems(dtype)
+        for grad, offset, length, weight in items:
+            if weight != 1.0:
+                return None
+            cached = _cached_partials(grad, offset, length, unscale)
+            if cached is None or cached.numel() != -(-length // chunk_elems) or not cached.is_contiguous():
+                return None
+            if address is None:
+                address = cached.data_ptr()
+            elif cached.data_ptr() != expected:
+                return None
+            expected = cached.data_ptr() + 8 * cached.numel()
+    if address is None or expected - address != 8 * total_partials:
+        return None
+    return address
 
 
 def norm_chunk_elems(dtype: torch.dtype) -> int:

@@ -107,3 +107,37 @@ def test_noalloc_norm_flags_nonfinite_and_refuses_oversize(device):
                                        None, None, None, None, _native.stream_of(device))
     assert status == -2
     assert b"static scratch" in lib.hbt_last_error()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_noalloc_norm_allocates_no_device_memory(device, dtype):
+    """The entry point takes no device memory of its own: after one warm-up call (which looks
+    up the static array's address and lets the runtime set up the launches), repeated calls
+    on inputs of different sizes leave the device's free memory (``hipMemGetInfo``, read by
+    ``torch.cuda.mem_get_info``) exactly where it was."""
+    lib = _native.library()
+    code = _native.dtype_code(dtype)
+    gen = torch.Generator(device=device).manual_seed(11)
+    inputs = [[torch.randn(n, device=device, generator=gen).to(dtype) for n in sizes]
+              for sizes in ((2_000_003, 65536 * 5), (1000,), (17, 4097, 300_000))]
+    out = _outputs(device)
+    numels = [[int(g.numel()) for g in grads] for grads in inputs]
+    ptrs = [_native.pointer_array([g.data_ptr() for g in grads]) for grads in inputs]
+    sizes = [_native.int64_array(n) for n in numels]
+    weights = [_native.double_array([1.0] * len(n)) for n in numels]
+    stream = _native.stream_of(device)
+
+    def call(k):
+        _native.check(lib.hbt_grad_norm_noalloc(ptrs[k], sizes[k], weights[k], len(numels[k]), code, 1.0, 1.0,
+                                                out[0].data_ptr(), out[1].data_ptr(), out[2].data_ptr(),
+                                                out[3].data_ptr(), stream), "hbt_grad_norm_noalloc")
+
+    call(0)
+    torch.cuda.synchronize(device)
+    free_before, _ = torch.cuda.mem_get_info(device)
+    for _ in range(3):
+        for k in range(len(inputs)):
+            call(k)
+    torch.cuda.synchronize(device)
+    free_after, _ = torch.cuda.mem_get_info(device)
+    assert free_after == free_before
