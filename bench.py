@@ -991,14 +991,18 @@ def _headline_inputs(device, n):
 
 
 def bench_inplace_clip(steps: int, warmup: int) -> int:
-    """The headline shard with the reference's in-place clip (``defer_clip=False``).
+    """The headline shard with the reference's in-place clip (``defer_clip=False``), in the
+    two placements the optimizer offers.
 
-    ``clip_grad_norm``: the norm pass (read g: 4 B/param); ``step``: the fused AdamW pass
-    that also writes the clipped gradient back into ``.grad`` (read p, g, m, v: 16 B;
-    write p, g, m, v: 16 B).  36 B/param in all.  Before each step the gradient is
+    Default (the reference's order): ``clip_grad_norm`` runs the norm pass (read g: 4 B)
+    and multiplies ``.grad`` in place (read and write g: 8 B); ``step`` runs the AdamW pass
+    on the clipped gradient (read p, g, m, v: 16 B; write p, m, v: 12 B): 40 B/param.
+    ``clip_in_step=True``: the update applies the multiplier and writes the clipped
+    gradient back in its own pass (read 16 B, write p, g, m, v: 16 B): 36 B/param, with
+    ``.grad`` clipped only once ``step`` has run.  Before each step the gradient is
     restored from a pristine copy (standing in for the next backward; not timed), so every
-    step clips (norm ~3.17, multiplier ~0.32) and writes back.  The step time is the HIP
-    event interval from the norm pass's launch to the end of the update.
+    step clips (norm ~3.17, multiplier ~0.32).  The step time is the HIP event interval from
+    the norm pass's launch to the end of the update.
     """
     import torch
 
@@ -1008,54 +1012,63 @@ def bench_inplace_clip(steps: int, warmup: int) -> int:
     n = SHARD_NUMEL
     param, pristine = _headline_inputs(device, n)
     grad = pristine.clone()
-    opt = ShardedOptimizer([param], OptimizerConfig(learning_rate=LR, betas=BETAS, eps=EPS, weight_decay=WD),
-                           norm_group=GroupHandle.trivial("world"), device=device, defer_clip=False)
-    param.grad = grad
     stream = torch.cuda.current_stream(device)
-    written = []
+    runs = [(False, 40, "sharded AdamW + in-place clip step: params/s",
+             "norm, clip written to .grad in place, AdamW on the clipped gradient (the reference's order)",
+             ["norm pass", "eager in-place clip of .grad", "AdamW of the clipped gradient"], "adamw"),
+            (True, 36, "sharded AdamW + in-place clip step, clip applied in the update: params/s",
+             "norm, then AdamW applying the clip and writing the clipped gradient back (clip_in_step)",
+             ["norm pass", "clip_in_step: clip + AdamW, clipped g written back"], "adamw_write_back")]
+    for in_step, per_param, metric, workload, labels, kernel in runs:
+        opt = ShardedOptimizer([param], OptimizerConfig(learning_rate=LR, betas=BETAS, eps=EPS, weight_decay=WD),
+                               norm_group=GroupHandle.trivial("world"), device=device, defer_clip=False,
+                               clip_in_step=in_step)
+        param.grad = grad
 
-    def step(events=None):
-        grad.copy_(pristine)  # the next backward's gradient (outside the timed events)
-        if events is not None:
-            events[0].record(stream)
-        opt.clip_grad_norm(MAX_NORM)
-        if events is not None:
-            events[1].record(stream)
-        opt.step()
-        if events is not None:
-            events[2].record(stream)
+        def step(events=None):
+            grad.copy_(pristine)  # the next backward's gradient (outside the timed events)
+            if events is not None:
+                events[0].record(stream)
+            opt.clip_grad_norm(MAX_NORM)
+            if events is not None:
+                events[1].record(stream)
+            opt.step()
+            if events is not None:
+                events[2].record(stream)
 
-    for _ in range(warmup):
-        step()
-    torch.cuda.synchronize()
-    # the write-back happened: .grad holds the clipped gradient
-    written.append(bool(torch.equal(grad[:4096], pristine[:4096])))
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
-    for k in range(steps):
-        step(events[k])
-    torch.cuda.synchronize()
-    norm_ms = sum(e[0].elapsed_time(e[1]) for e in events) / steps
-    adamw_ms = sum(e[1].elapsed_time(e[2]) for e in events) / steps
-    ms = sum(e[0].elapsed_time(e[2]) for e in events) / steps
-    if written[0]:
-        raise RuntimeError("the in-place clip did not write the clipped gradient back")
-    adamw_gbps = 32 * n / (adamw_ms * 1e-3) / 1e9
-    step_gbps = 36 * n / (ms * 1e-3) / 1e9
-    log(f"in-place clip: {ms:.3f} ms/step (norm {norm_ms:.3f} ms, AdamW + write-back {adamw_ms:.3f} ms)")
-    line = {
-        "metric": "sharded AdamW + in-place clip step: params/s", "value": n / (ms * 1e-3), "unit": "params/s",
-        "n_gpus": 1, "steps": steps, "warmup": warmup, "ms_per_step": ms, "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic (device-generated)",
-        "config": {"workload": "Llama-3-8B FSDP rank shard at W=8: norm, clip written back to .grad, AdamW "
-                               "(reference semantics)", "shard_numel": n, "bytes_per_param": 36},
-        "step_hbm_gbps": step_gbps, "step_frac_of_peak": step_gbps / HBM_PEAK_GBPS,
-        "kernel_ms": {"grad_norm": norm_ms, "adamw_write_back": adamw_ms},
-        "roofline": {"bound": "hbm", "achieved": adamw_gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": adamw_gbps / HBM_PEAK_GBPS, "traffic": _secondary_traffic("inplace_clip", ["adamw"], [1]),
-                     "traffic_per": "launch of the dominant kernel"},
-        "cpu_baseline": _cpu_step_line(1 << 26, 5) if _WITH_CPU else None,
-    }
-    print(json.dumps(line), flush=True)
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        if bool(torch.equal(grad[:4096], pristine[:4096])):
+            raise RuntimeError("the in-place clip did not leave the clipped gradient in .grad")
+        events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+        for k in range(steps):
+            step(events[k])
+        torch.cuda.synchronize()
+        clip_ms = sum(e[0].elapsed_time(e[1]) for e in events) / steps
+        adamw_ms = sum(e[1].elapsed_time(e[2]) for e in events) / steps
+        ms = sum(e[0].elapsed_time(e[2]) for e in events) / steps
+        adamw_bytes = (32 if in_step else 28) * n
+        adamw_gbps = adamw_bytes / (adamw_ms * 1e-3) / 1e9
+        step_gbps = per_param * n / (ms * 1e-3) / 1e9
+        log(f"in-place clip ({'in the update' if in_step else 'eager'}): {ms:.3f} ms/step "
+            f"(clip_grad_norm {clip_ms:.3f} ms, step {adamw_ms:.3f} ms)")
+        line = {
+            "metric": metric, "value": n / (ms * 1e-3), "unit": "params/s",
+            "n_gpus": 1, "steps": steps, "warmup": warmup, "ms_per_step": ms, "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic (device-generated)",
+            "config": {"workload": f"Llama-3-8B FSDP rank shard at W=8: {workload}", "shard_numel": n,
+                       "bytes_per_param": per_param},
+            "step_hbm_gbps": step_gbps, "step_frac_of_peak": step_gbps / HBM_PEAK_GBPS,
+            "kernel_ms": {"clip_grad_norm": clip_ms, kernel: adamw_ms},
+            "roofline": {"bound": "hbm", "achieved": adamw_gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                         "frac": adamw_gbps / HBM_PEAK_GBPS,
+                         "traffic": _secondary_traffic("inplace_clip", labels[-1:], [1]),
+                         "traffic_per": "launch of the dominant kernel"},
+            "cpu_baseline": _cpu_step_line(1 << 26, 5) if _WITH_CPU and not in_step else None,
+        }
+        print(json.dumps(line), flush=True)
+        del opt
     return 0
 
 
