@@ -78,10 +78,14 @@ class NormPartials:
 
     ``segments`` maps ``(offset, length)`` of the gradient to the partials of that
     segment: one fp64 per norm chunk from the segment's start (32768 elements of an
-    fp32 gradient, 65536 of a 2-byte one), the layout of ``hbt_grad_sqnorm_partials``
-    with weight 1, each summed in the producer's own fixed order.  The record is valid
-    while the gradient keeps the storage address, version counter and dtype it had when
-    the partials were written; any in-place change invalidates it.
+    fp32 gradient, 65536 of a 2-byte one, 16384 of a float64 one), the layout of
+    ``hbt_grad_sqnorm_partials`` with weight 1, each summed in the producer's own fixed
+    order.  The record is valid while the gradient keeps the storage address, version
+    counter and dtype it had when the partials were written.  Every in-place torch op
+    and every kernel of this package that writes the tensor moves the version counter
+    and so invalidates it; a write that bypasses the counter (through ``tensor.data``,
+    or a foreign kernel writing the storage) does not, and the next norm then uses the
+    stale partials.
     """
 
     data_ptr: int
