@@ -277,8 +277,10 @@ __device__ __forceinline__ void adamw_update(float& p, float g, float& m, float&
 // multiplies only when its coefficient is below 1) or an unscale factor is pending.
 template <int PD, int GD, bool kLerpSmall, bool kUnscale, bool kWriteBack>
 __global__ __launch_bounds__(kAdamBlock) void adamw_kernel(AdamTable tab, AdamScalars s,
+                                                           const AdamScalars* __restrict__ slot,
                                                            const float* __restrict__ grad_mul,
                                                            int64_t block_base) {
+    if (slot != nullptr) s = *slot;
     constexpr int K = adam_vec<PD>();
     constexpr int kUnroll = adam_unroll<kWriteBack>();
     constexpr int64_t kTile = adam_tile<PD, kWriteBack>();
@@ -388,8 +390,10 @@ __device__ __forceinline__ void sgd_update(float& p, float g, float& buf, const 
 
 template <int PD, int GD, bool kUnscale, int kMode, bool kWriteBack>
 __global__ __launch_bounds__(kAdamBlock) void sgd_kernel(SgdTable tab, SgdScalars s,
+                                                         const SgdScalars* __restrict__ slot,
                                                          const float* __restrict__ grad_mul,
                                                          int64_t block_base) {
+    if (slot != nullptr) s = *slot;
     constexpr int K = adam_vec<PD>();
     constexpr int kUnroll = adam_unroll<kWriteBack>();
     constexpr int64_t kTile = adam_tile<PD, kWriteBack>();
@@ -1205,8 +1209,10 @@ __device__ __forceinline__ void adamw_update_f64(double& p, double g, double& m,
 
 template <bool kLerpSmall, bool kUnscale, bool kWriteBack>
 __global__ __launch_bounds__(kAdamBlock) void adamw_f64_kernel(AdamTable tab, AdamScalarsF64 s,
+                                                               const AdamScalarsF64* __restrict__ slot,
                                                                const double* __restrict__ grad_mul,
                                                                int64_t block_base) {
+    if (slot != nullptr) s = *slot;
     constexpr int K = kF64Vec;
     constexpr int kUnroll = adam_unroll<kWriteBack>();
     constexpr int64_t kTile = adam_f64_tile<kWriteBack>();
@@ -1298,8 +1304,10 @@ __device__ __forceinline__ void sgd_update_f64(double& p, double g, double& buf,
 
 template <bool kUnscale, int kMode, bool kWriteBack>
 __global__ __launch_bounds__(kAdamBlock) void sgd_f64_kernel(SgdTable tab, SgdScalarsF64 s,
+                                                             const SgdScalarsF64* __restrict__ slot,
                                                              const double* __restrict__ grad_mul,
                                                              int64_t block_base) {
+    if (slot != nullptr) s = *slot;
     constexpr int K = kF64Vec;
     constexpr int kUnroll = adam_unroll<kWriteBack>();
     constexpr int64_t kTile = adam_f64_tile<kWriteBack>();
@@ -1554,6 +1562,121 @@ float host_round_to(float x, int32_t dtype) {
 bool optimizer_dtypes_ok(int32_t param_dtype, int32_t grad_dtype) {
     return (param_dtype == F32 && (grad_dtype == F32 || grad_dtype == BF16)) ||
            (param_dtype == BF16 && grad_dtype == BF16) || (param_dtype == F16 && grad_dtype == F16);
+}
+
+// The scalars each step kernel receives, built from an entry point's arguments.  The
+// step entry points pass them by value; the slot writers store the same records in
+// device memory for the slot forms of the steps to read.
+AdamScalars adam_scalars(int32_t param_dtype, float unscale, float decay, float lerp_weight, float beta2,
+                         float one_minus_beta2, float bias_correction2_sqrt, float eps, float neg_step_size) {
+    AdamScalars s{};
+    s.unscale = unscale;
+    s.decay = decay;
+    s.lerp_w = lerp_weight;
+    s.lerp_w_minus_1 = lerp_weight - 1.0f;
+    s.beta2 = beta2;
+    s.one_minus_beta2 = one_minus_beta2;
+    s.bc2_sqrt = bias_correction2_sqrt;
+    s.eps = host_round_to(eps, param_dtype);
+    s.neg_step = neg_step_size;
+    return s;
+}
+
+// torch rounds each `alpha` (and nothing multiplied by mul_) to the parameter dtype.
+SgdScalars sgd_scalars(int32_t param_dtype, float unscale, float weight_decay, float momentum,
+                       float one_minus_dampening, float neg_lr, int32_t flags) {
+    return SgdScalars{unscale,
+                      host_round_to(weight_decay, param_dtype),
+                      momentum,
+                      host_round_to(momentum, param_dtype),
+                      host_round_to(one_minus_dampening, param_dtype),
+                      host_round_to(neg_lr, param_dtype),
+                      (flags & HBT_SGD_WEIGHT_DECAY) != 0,
+                      (flags & HBT_SGD_NESTEROV) != 0};
+}
+
+AdamScalarsF64 adam_scalars_f64(double unscale, double decay, double lerp_weight, double beta2,
+                                double one_minus_beta2, double bias_correction2_sqrt, double eps,
+                                double neg_step_size) {
+    return AdamScalarsF64{unscale, decay, lerp_weight, lerp_weight - 1.0, beta2, one_minus_beta2,
+                          bias_correction2_sqrt, eps, neg_step_size};
+}
+
+SgdScalarsF64 sgd_scalars_f64(double unscale, double weight_decay, double momentum, double one_minus_dampening,
+                              double neg_lr, int32_t flags) {
+    return SgdScalarsF64{unscale, weight_decay, momentum, one_minus_dampening, neg_lr,
+                         (flags & HBT_SGD_WEIGHT_DECAY) != 0, (flags & HBT_SGD_NESTEROV) != 0};
+}
+
+// ---- small host-built data into device memory --------------------------------------------
+// One wave stores up to kWordsPerWrite 32-bit words that arrive in the launch's
+// arguments: lane i stores word i (one vector store instruction).  A recorded launch keeps
+// its arguments, so a graph replays the write with the words it was given.
+constexpr int kWordsPerWrite = 64;
+struct WordBlock {
+    uint32_t w[kWordsPerWrite];
+};
+
+__global__ __launch_bounds__(kWordsPerWrite) void write_words_kernel(uint32_t* __restrict__ dst, WordBlock words,
+                                                                      int32_t count) {
+    const int lane = threadIdx.x;
+    uint32_t word = 0u;
+#pragma unroll
+    for (int k = 0; k < kWordsPerWrite; ++k) word = lane == k ? words.w[k] : word;  // no indexed argument reads
+    if (lane < count) dst[lane] = word;
+}
+
+int32_t write_words(const char* who, void* dst, const uint32_t* words, int64_t count, hipStream_t st) {
+    if (count < 0 || (count > 0 && (dst == nullptr || words == nullptr))) {
+        set_error("%s: bad destination, words or count (%lld)", who, static_cast<long long>(count));
+        return HBT_ERR_INVALID_ARGUMENT;
+    }
+    if (!aligned(dst, 4)) {
+        set_error("%s: the destination must be 4-byte aligned", who);
+        return HBT_ERR_INVALID_ARGUMENT;
+    }
+    for (int64_t first = 0; first < count; first += kWordsPerWrite) {
+        const int32_t n = static_cast<int32_t>(count - first < kWordsPerWrite ? count - first : kWordsPerWrite);
+        WordBlock block{};
+        std::memcpy(block.w, words + first, sizeof(uint32_t) * static_cast<size_t>(n));
+        write_words_kernel<<<dim3(1), dim3(kWordsPerWrite), 0, st>>>(static_cast<uint32_t*>(dst) + first, block, n);
+        const int32_t status = check_launch(who);
+        if (status != HBT_OK) return status;
+    }
+    return HBT_OK;
+}
+
+// A scalar record written into a step slot.
+template <typename Record>
+int32_t write_slot(const char* who, void* slot, const Record& record, hipStream_t st) {
+    static_assert(sizeof(Record) % 4 == 0 && sizeof(Record) <= HBT_STEP_SLOT_BYTES, "a record fills part of a slot");
+    if (slot == nullptr || !aligned(slot, 16)) {
+        set_error("%s: the slot must be non-null, 16-byte aligned device memory", who);
+        return HBT_ERR_INVALID_ARGUMENT;
+    }
+    uint32_t words[sizeof(Record) / 4];
+    std::memcpy(words, &record, sizeof(Record));
+    return write_words(who, slot, words, static_cast<int64_t>(sizeof(Record) / 4), st);
+}
+
+// The SGD flags a step or a scalar record accepts.
+bool sgd_flags_ok(const char* who, int32_t flags) {
+    const int32_t known = HBT_SGD_MOMENTUM | HBT_SGD_FIRST_STEP | HBT_SGD_NESTEROV | HBT_SGD_WEIGHT_DECAY |
+                          HBT_STEP_WRITE_GRAD;
+    if ((flags & ~known) != 0 ||
+        ((flags & (HBT_SGD_FIRST_STEP | HBT_SGD_NESTEROV)) != 0 && (flags & HBT_SGD_MOMENTUM) == 0)) {
+        set_error("%s: bad flags 0x%x", who, static_cast<unsigned>(flags));
+        return false;
+    }
+    return true;
+}
+
+bool slot_ok(const char* who, const void* slot) {
+    if (slot == nullptr || !aligned(slot, 16)) {
+        set_error("%s: the slot must be non-null, 16-byte aligned device memory", who);
+        return false;
+    }
+    return true;
 }
 
 // Validates a gradient table and fills the norm kernel's table; `chunks` is the number
@@ -1833,29 +1956,29 @@ using namespace hbt;
 
 extern "C" {
 
-int32_t hbt_adamw_step(void* const* params, void* const* grads, void* const* exp_avgs,
+static int32_t adamw_step_impl(const char* who, void* const* params, void* const* grads, void* const* exp_avgs,
                        void* const* exp_avg_sqs, const int64_t* numels, int32_t count,
                        int32_t param_dtype, int32_t grad_dtype, float unscale, const float* grad_mul,
                        float decay, float lerp_weight, float beta2, float one_minus_beta2,
-                       float bias_correction2_sqrt, float eps, float neg_step_size, int32_t flags,
+                       float bias_correction2_sqrt, float eps, float neg_step_size, const AdamScalars* slot, int32_t flags,
                        void* stream) {
     clear_error();
     if (count < 0 || count > kMaxT) {
-        set_error("hbt_adamw_step: count must lie in [0, %d], got %d", kMaxT, count);
+        set_error("%s: count must lie in [0, %d], got %d", who, kMaxT, count);
         return HBT_ERR_INVALID_ARGUMENT;
     }
     if (!optimizer_dtypes_ok(param_dtype, grad_dtype)) {
-        set_error("hbt_adamw_step: (parameter, gradient) dtypes (%d, %d) are not (F32, F32), (F32, BF16), "
-                  "(BF16, BF16) or (F16, F16)", param_dtype, grad_dtype);
+        set_error("%s: (parameter, gradient) dtypes (%d, %d) are not (F32, F32), (F32, BF16), "
+                  "(BF16, BF16) or (F16, F16)", who, param_dtype, grad_dtype);
         return HBT_ERR_INVALID_ARGUMENT;
     }
     if ((flags & ~HBT_STEP_WRITE_GRAD) != 0) {
-        set_error("hbt_adamw_step: unknown flags 0x%x", static_cast<unsigned>(flags));
+        set_error("%s: unknown flags 0x%x", who, static_cast<unsigned>(flags));
         return HBT_ERR_INVALID_ARGUMENT;
     }
     if (count > 0 && (params == nullptr || grads == nullptr || exp_avgs == nullptr ||
                       exp_avg_sqs == nullptr || numels == nullptr)) {
-        set_error("hbt_adamw_step: null table pointer");
+        set_error("%s: null table pointer", who);
         return HBT_ERR_INVALID_ARGUMENT;
     }
     AdamTable tab{};
@@ -1868,13 +1991,13 @@ int32_t hbt_adamw_step(void* const* params, void* const* grads, void* const* exp
     int64_t blocks = 0;
     for (int i = 0; i < count; ++i) {
         if (numels[i] < 0) {
-            set_error("hbt_adamw_step: tensor %d has negative numel %lld", i,
+            set_error("%s: tensor %d has negative numel %lld", who, i,
                       static_cast<long long>(numels[i]));
             return HBT_ERR_INVALID_ARGUMENT;
         }
         if (numels[i] > 0 && (params[i] == nullptr || grads[i] == nullptr || exp_avgs[i] == nullptr ||
                               exp_avg_sqs[i] == nullptr)) {
-            set_error("hbt_adamw_step: tensor %d has a null data pointer", i);
+            set_error("%s: tensor %d has a null data pointer", who, i);
             return HBT_ERR_INVALID_ARGUMENT;
         }
         tab.p[i] = params[i];
@@ -1889,22 +2012,14 @@ int32_t hbt_adamw_step(void* const* params, void* const* grads, void* const* exp
     }
     tab.first_block[count] = blocks;
     for (int i = count + 1; i <= kMaxT; ++i) tab.first_block[i] = blocks;
-    AdamScalars s{};
-    s.unscale = unscale;
-    s.decay = decay;
-    s.lerp_w = lerp_weight;
-    s.lerp_w_minus_1 = lerp_weight - 1.0f;
-    s.beta2 = beta2;
-    s.one_minus_beta2 = one_minus_beta2;
-    s.bc2_sqrt = bias_correction2_sqrt;
-    s.eps = host_round_to(eps, param_dtype);
-    s.neg_step = neg_step_size;
+    const AdamScalars s = adam_scalars(param_dtype, unscale, decay, lerp_weight, beta2, one_minus_beta2,
+                                       bias_correction2_sqrt, eps, neg_step_size);
     const bool lerp_small = std::fabs(lerp_weight) < 0.5f;
     const bool scaled = unscale != 1.0f;
     hipStream_t st = as_stream(stream);
-    return launch_sliced("hbt_adamw_step", blocks, kAdamBlock, [&](int64_t first, dim3 grid) {
+    return launch_sliced(who, blocks, kAdamBlock, [&](int64_t first, dim3 grid) {
 #define HBT_ADAMW(PD, GD, SMALL, SCALED, WB) \
-    adamw_kernel<PD, GD, SMALL, SCALED, WB><<<grid, kAdamBlock, 0, st>>>(tab, s, grad_mul, first)
+    adamw_kernel<PD, GD, SMALL, SCALED, WB><<<grid, kAdamBlock, 0, st>>>(tab, s, slot, grad_mul, first)
 #define HBT_ADAMW_WB(PD, GD, SMALL, SCALED)                     \
     do {                                                        \
         if (write_back) HBT_ADAMW(PD, GD, SMALL, SCALED, true); \
@@ -2199,31 +2314,31 @@ int32_t hbt_grad_local_share_accumulated(const void* const* rank_grads, const vo
                        accumulators);
 }
 
-int32_t hbt_sgd_step(void* const* params, void* const* grads, void* const* momentum_buffers,
+static int32_t sgd_step_impl(const char* who, void* const* params, void* const* grads, void* const* momentum_buffers,
                      const int64_t* numels, int32_t count, int32_t param_dtype, int32_t grad_dtype, float unscale,
                      const float* grad_mul, float weight_decay, float momentum, float one_minus_dampening,
-                     float neg_lr, int32_t flags, void* stream) {
+                     float neg_lr, const SgdScalars* slot, int32_t flags, void* stream) {
     clear_error();
     if (count < 0 || count > kMaxT) {
-        set_error("hbt_sgd_step: count must lie in [0, %d], got %d", kMaxT, count);
+        set_error("%s: count must lie in [0, %d], got %d", who, kMaxT, count);
         return HBT_ERR_INVALID_ARGUMENT;
     }
     if (!optimizer_dtypes_ok(param_dtype, grad_dtype)) {
-        set_error("hbt_sgd_step: (parameter, gradient) dtypes (%d, %d) are not (F32, F32), (F32, BF16), "
-                  "(BF16, BF16) or (F16, F16)", param_dtype, grad_dtype);
+        set_error("%s: (parameter, gradient) dtypes (%d, %d) are not (F32, F32), (F32, BF16), "
+                  "(BF16, BF16) or (F16, F16)", who, param_dtype, grad_dtype);
         return HBT_ERR_INVALID_ARGUMENT;
     }
     const int32_t known = HBT_SGD_MOMENTUM | HBT_SGD_FIRST_STEP | HBT_SGD_NESTEROV | HBT_SGD_WEIGHT_DECAY |
                           HBT_STEP_WRITE_GRAD;
     if ((flags & ~known) != 0 ||
         ((flags & (HBT_SGD_FIRST_STEP | HBT_SGD_NESTEROV)) != 0 && (flags & HBT_SGD_MOMENTUM) == 0)) {
-        set_error("hbt_sgd_step: bad flags 0x%x", flags);
+        set_error("%s: bad flags 0x%x", who, flags);
         return HBT_ERR_INVALID_ARGUMENT;
     }
     const bool with_momentum = (flags & HBT_SGD_MOMENTUM) != 0;
     if (count > 0 && (params == nullptr || grads == nullptr || numels == nullptr ||
                       (with_momentum && momentum_buffers == nullptr))) {
-        set_error("hbt_sgd_step: null pointer argument");
+        set_error("%s: null pointer argument", who);
         return HBT_ERR_INVALID_ARGUMENT;
     }
     SgdTable tab{};
@@ -2237,7 +2352,7 @@ int32_t hbt_sgd_step(void* const* params, void* const* grads, void* const* momen
     for (int i = 0; i < count; ++i) {
         if (numels[i] < 0 || (numels[i] > 0 && (params[i] == nullptr || grads[i] == nullptr ||
                                                 (with_momentum && momentum_buffers[i] == nullptr)))) {
-            set_error("hbt_sgd_step: tensor %d has a bad pointer or numel", i);
+            set_error("%s: tensor %d has a bad pointer or numel", who, i);
             return HBT_ERR_INVALID_ARGUMENT;
         }
         tab.p[i] = params[i];
@@ -2251,21 +2366,14 @@ int32_t hbt_sgd_step(void* const* params, void* const* grads, void* const* momen
     }
     tab.first_block[count] = blocks;
     for (int i = count + 1; i <= kMaxT; ++i) tab.first_block[i] = blocks;
-    // torch rounds each `alpha` (and nothing multiplied by mul_) to the parameter dtype.
-    const SgdScalars sc{unscale,
-                        host_round_to(weight_decay, param_dtype),
-                        momentum,
-                        host_round_to(momentum, param_dtype),
-                        host_round_to(one_minus_dampening, param_dtype),
-                        host_round_to(neg_lr, param_dtype),
-                        (flags & HBT_SGD_WEIGHT_DECAY) != 0,
-                        (flags & HBT_SGD_NESTEROV) != 0};
+    const SgdScalars sc = sgd_scalars(param_dtype, unscale, weight_decay, momentum, one_minus_dampening, neg_lr,
+                                      flags);
     const int mode = !with_momentum ? kSgdPlain : ((flags & HBT_SGD_FIRST_STEP) ? kSgdFirst : kSgdMomentum);
     const bool scaled = unscale != 1.0f;
     hipStream_t st = as_stream(stream);
-    return launch_sliced("hbt_sgd_step", blocks, kAdamBlock, [&](int64_t first, dim3 grid) {
+    return launch_sliced(who, blocks, kAdamBlock, [&](int64_t first, dim3 grid) {
 #define HBT_SGD(PD, GD, SCALED, MODE, WB) \
-    sgd_kernel<PD, GD, SCALED, MODE, WB><<<grid, kAdamBlock, 0, st>>>(tab, sc, grad_mul, first)
+    sgd_kernel<PD, GD, SCALED, MODE, WB><<<grid, kAdamBlock, 0, st>>>(tab, sc, slot, grad_mul, first)
 #define HBT_SGD_WB(PD, GD, SCALED, MODE)                     \
     do {                                                     \
         if (write_back) HBT_SGD(PD, GD, SCALED, MODE, true); \
@@ -2293,23 +2401,23 @@ int32_t hbt_sgd_step(void* const* params, void* const* grads, void* const* momen
     });
 }
 
-int32_t hbt_adamw_step_f64(double* const* params, double* const* grads, double* const* exp_avgs,
+static int32_t adamw_step_f64_impl(const char* who, double* const* params, double* const* grads, double* const* exp_avgs,
                            double* const* exp_avg_sqs, const int64_t* numels, int32_t count, double unscale,
                            const double* grad_mul, double decay, double lerp_weight, double beta2,
                            double one_minus_beta2, double bias_correction2_sqrt, double eps, double neg_step_size,
-                           int32_t flags, void* stream) {
+                           const AdamScalarsF64* slot, int32_t flags, void* stream) {
     clear_error();
     if (count < 0 || count > kMaxT) {
-        set_error("hbt_adamw_step_f64: count must lie in [0, %d], got %d", kMaxT, count);
+        set_error("%s: count must lie in [0, %d], got %d", who, kMaxT, count);
         return HBT_ERR_INVALID_ARGUMENT;
     }
     if ((flags & ~HBT_STEP_WRITE_GRAD) != 0) {
-        set_error("hbt_adamw_step_f64: unknown flags 0x%x", static_cast<unsigned>(flags));
+        set_error("%s: unknown flags 0x%x", who, static_cast<unsigned>(flags));
         return HBT_ERR_INVALID_ARGUMENT;
     }
     if (count > 0 && (params == nullptr || grads == nullptr || exp_avgs == nullptr || exp_avg_sqs == nullptr ||
                       numels == nullptr)) {
-        set_error("hbt_adamw_step_f64: null table pointer");
+        set_error("%s: null table pointer", who);
         return HBT_ERR_INVALID_ARGUMENT;
     }
     const bool write_back = (flags & HBT_STEP_WRITE_GRAD) != 0;
@@ -2320,7 +2428,7 @@ int32_t hbt_adamw_step_f64(double* const* params, double* const* grads, double* 
     for (int i = 0; i < count; ++i) {
         if (numels[i] < 0 || (numels[i] > 0 && (params[i] == nullptr || grads[i] == nullptr ||
                                                 exp_avgs[i] == nullptr || exp_avg_sqs[i] == nullptr))) {
-            set_error("hbt_adamw_step_f64: tensor %d has a bad pointer or numel", i);
+            set_error("%s: tensor %d has a bad pointer or numel", who, i);
             return HBT_ERR_INVALID_ARGUMENT;
         }
         tab.p[i] = params[i];
@@ -2335,14 +2443,14 @@ int32_t hbt_adamw_step_f64(double* const* params, double* const* grads, double* 
     }
     tab.first_block[count] = blocks;
     for (int i = count + 1; i <= kMaxT; ++i) tab.first_block[i] = blocks;
-    const AdamScalarsF64 s{unscale, decay, lerp_weight, lerp_weight - 1.0, beta2, one_minus_beta2,
-                           bias_correction2_sqrt, eps, neg_step_size};
+    const AdamScalarsF64 s = adam_scalars_f64(unscale, decay, lerp_weight, beta2, one_minus_beta2,
+                                              bias_correction2_sqrt, eps, neg_step_size);
     const bool lerp_small = std::fabs(lerp_weight) < 0.5;
     const bool scaled = unscale != 1.0;
     hipStream_t st = as_stream(stream);
-    return launch_sliced("hbt_adamw_step_f64", blocks, kAdamBlock, [&](int64_t first, dim3 grid) {
+    return launch_sliced(who, blocks, kAdamBlock, [&](int64_t first, dim3 grid) {
 #define HBT_ADAMW64(SMALL, SCALED, WB) \
-    adamw_f64_kernel<SMALL, SCALED, WB><<<grid, kAdamBlock, 0, st>>>(tab, s, grad_mul, first)
+    adamw_f64_kernel<SMALL, SCALED, WB><<<grid, kAdamBlock, 0, st>>>(tab, s, slot, grad_mul, first)
 #define HBT_ADAMW64_WB(SMALL, SCALED)                     \
     do {                                                  \
         if (write_back) HBT_ADAMW64(SMALL, SCALED, true); \
@@ -2361,26 +2469,26 @@ int32_t hbt_adamw_step_f64(double* const* params, double* const* grads, double* 
     });
 }
 
-int32_t hbt_sgd_step_f64(double* const* params, double* const* grads, double* const* momentum_buffers,
+static int32_t sgd_step_f64_impl(const char* who, double* const* params, double* const* grads, double* const* momentum_buffers,
                          const int64_t* numels, int32_t count, double unscale, const double* grad_mul,
                          double weight_decay, double momentum, double one_minus_dampening, double neg_lr,
-                         int32_t flags, void* stream) {
+                         const SgdScalarsF64* slot, int32_t flags, void* stream) {
     clear_error();
     if (count < 0 || count > kMaxT) {
-        set_error("hbt_sgd_step_f64: count must lie in [0, %d], got %d", kMaxT, count);
+        set_error("%s: count must lie in [0, %d], got %d", who, kMaxT, count);
         return HBT_ERR_INVALID_ARGUMENT;
     }
     const int32_t known = HBT_SGD_MOMENTUM | HBT_SGD_FIRST_STEP | HBT_SGD_NESTEROV | HBT_SGD_WEIGHT_DECAY |
                           HBT_STEP_WRITE_GRAD;
     if ((flags & ~known) != 0 ||
         ((flags & (HBT_SGD_FIRST_STEP | HBT_SGD_NESTEROV)) != 0 && (flags & HBT_SGD_MOMENTUM) == 0)) {
-        set_error("hbt_sgd_step_f64: bad flags 0x%x", flags);
+        set_error("%s: bad flags 0x%x", who, flags);
         return HBT_ERR_INVALID_ARGUMENT;
     }
     const bool with_momentum = (flags & HBT_SGD_MOMENTUM) != 0;
     if (count > 0 && (params == nullptr || grads == nullptr || numels == nullptr ||
                       (with_momentum && momentum_buffers == nullptr))) {
-        set_error("hbt_sgd_step_f64: null pointer argument");
+        set_error("%s: null pointer argument", who);
         return HBT_ERR_INVALID_ARGUMENT;
     }
     const bool write_back = (flags & HBT_STEP_WRITE_GRAD) != 0;
@@ -2391,7 +2499,7 @@ int32_t hbt_sgd_step_f64(double* const* params, double* const* grads, double* co
     for (int i = 0; i < count; ++i) {
         if (numels[i] < 0 || (numels[i] > 0 && (params[i] == nullptr || grads[i] == nullptr ||
                                                 (with_momentum && momentum_buffers[i] == nullptr)))) {
-            set_error("hbt_sgd_step_f64: tensor %d has a bad pointer or numel", i);
+            set_error("%s: tensor %d has a bad pointer or numel", who, i);
             return HBT_ERR_INVALID_ARGUMENT;
         }
         tab.p[i] = params[i];
@@ -2405,13 +2513,12 @@ int32_t hbt_sgd_step_f64(double* const* params, double* const* grads, double* co
     }
     tab.first_block[count] = blocks;
     for (int i = count + 1; i <= kMaxT; ++i) tab.first_block[i] = blocks;
-    const SgdScalarsF64 sc{unscale, weight_decay, momentum, one_minus_dampening, neg_lr,
-                           (flags & HBT_SGD_WEIGHT_DECAY) != 0, (flags & HBT_SGD_NESTEROV) != 0};
+    const SgdScalarsF64 sc = sgd_scalars_f64(unscale, weight_decay, momentum, one_minus_dampening, neg_lr, flags);
     const int mode = !with_momentum ? kSgdPlain : ((flags & HBT_SGD_FIRST_STEP) ? kSgdFirst : kSgdMomentum);
     const bool scaled = unscale != 1.0;
     hipStream_t st = as_stream(stream);
-    return launch_sliced("hbt_sgd_step_f64", blocks, kAdamBlock, [&](int64_t first, dim3 grid) {
-#define HBT_SGD64(SCALED, MODE, WB) sgd_f64_kernel<SCALED, MODE, WB><<<grid, kAdamBlock, 0, st>>>(tab, sc, grad_mul, first)
+    return launch_sliced(who, blocks, kAdamBlock, [&](int64_t first, dim3 grid) {
+#define HBT_SGD64(SCALED, MODE, WB) sgd_f64_kernel<SCALED, MODE, WB><<<grid, kAdamBlock, 0, st>>>(tab, sc, slot, grad_mul, first)
 #define HBT_SGD64_WB(SCALED, MODE)                     \
     do {                                               \
         if (write_back) HBT_SGD64(SCALED, MODE, true); \
@@ -2458,6 +2565,144 @@ int32_t hbt_scale_inplace_f64(double* const* tensors, const int64_t* numels, int
     return launch_sliced("hbt_scale_inplace_f64", blocks, 32, [&](int64_t first, dim3 grid) {
         scale_f64_kernel<<<grid, 32, 0, st>>>(tab, unscale, grad_mul, first);
     });
+}
+
+// ---- the eager steps and their slot forms ---------------------------------------------
+int32_t hbt_adamw_step(void* const* params, void* const* grads, void* const* exp_avgs,
+                       void* const* exp_avg_sqs, const int64_t* numels, int32_t count,
+                       int32_t param_dtype, int32_t grad_dtype, float unscale, const float* grad_mul,
+                       float decay, float lerp_weight, float beta2, float one_minus_beta2,
+                       float bias_correction2_sqrt, float eps, float neg_step_size, int32_t flags,
+                       void* stream) {
+    return adamw_step_impl("hbt_adamw_step", params, grads, exp_avgs, exp_avg_sqs, numels, count, param_dtype,
+                           grad_dtype, unscale, grad_mul, decay, lerp_weight, beta2, one_minus_beta2,
+                           bias_correction2_sqrt, eps, neg_step_size, nullptr, flags, stream);
+}
+
+int32_t hbt_adamw_step_slot(void* const* params, void* const* grads, void* const* exp_avgs,
+                            void* const* exp_avg_sqs, const int64_t* numels, int32_t count,
+                            int32_t param_dtype, int32_t grad_dtype, float unscale, const float* grad_mul,
+                            float decay, float lerp_weight, float beta2, float one_minus_beta2,
+                            float bias_correction2_sqrt, float eps, float neg_step_size, const void* slot,
+                            int32_t flags, void* stream) {
+    clear_error();
+    if (!slot_ok("hbt_adamw_step_slot", slot)) return HBT_ERR_INVALID_ARGUMENT;
+    return adamw_step_impl("hbt_adamw_step_slot", params, grads, exp_avgs, exp_avg_sqs, numels, count, param_dtype,
+                           grad_dtype, unscale, grad_mul, decay, lerp_weight, beta2, one_minus_beta2,
+                           bias_correction2_sqrt, eps, neg_step_size, static_cast<const AdamScalars*>(slot), flags,
+                           stream);
+}
+
+int32_t hbt_adamw_write_scalars(void* slot, int32_t param_dtype, float unscale, float decay, float lerp_weight,
+                                float beta2, float one_minus_beta2, float bias_correction2_sqrt, float eps,
+                                float neg_step_size, void* stream) {
+    clear_error();
+    if (param_dtype != F32 && param_dtype != BF16 && param_dtype != F16) {
+        set_error("hbt_adamw_write_scalars: param_dtype %d is not F32, BF16 or F16", param_dtype);
+        return HBT_ERR_INVALID_ARGUMENT;
+    }
+    return write_slot("hbt_adamw_write_scalars", slot,
+                      adam_scalars(param_dtype, unscale, decay, lerp_weight, beta2, one_minus_beta2,
+                                   bias_correction2_sqrt, eps, neg_step_size),
+                      as_stream(stream));
+}
+
+int32_t hbt_sgd_step(void* const* params, void* const* grads, void* const* momentum_buffers,
+                     const int64_t* numels, int32_t count, int32_t param_dtype, int32_t grad_dtype, float unscale,
+                     const float* grad_mul, float weight_decay, float momentum, float one_minus_dampening,
+                     float neg_lr, int32_t flags, void* stream) {
+    return sgd_step_impl("hbt_sgd_step", params, grads, momentum_buffers, numels, count, param_dtype, grad_dtype,
+                         unscale, grad_mul, weight_decay, momentum, one_minus_dampening, neg_lr, nullptr, flags,
+                         stream);
+}
+
+int32_t hbt_sgd_step_slot(void* const* params, void* const* grads, void* const* momentum_buffers,
+                          const int64_t* numels, int32_t count, int32_t param_dtype, int32_t grad_dtype,
+                          float unscale, const float* grad_mul, float weight_decay, float momentum,
+                          float one_minus_dampening, float neg_lr, const void* slot, int32_t flags, void* stream) {
+    clear_error();
+    if (!slot_ok("hbt_sgd_step_slot", slot)) return HBT_ERR_INVALID_ARGUMENT;
+    return sgd_step_impl("hbt_sgd_step_slot", params, grads, momentum_buffers, numels, count, param_dtype,
+                         grad_dtype, unscale, grad_mul, weight_decay, momentum, one_minus_dampening, neg_lr,
+                         static_cast<const SgdScalars*>(slot), flags, stream);
+}
+
+int32_t hbt_sgd_write_scalars(void* slot, int32_t param_dtype, float unscale, float weight_decay, float momentum,
+                              float one_minus_dampening, float neg_lr, int32_t flags, void* stream) {
+    clear_error();
+    if (param_dtype != F32 && param_dtype != BF16 && param_dtype != F16) {
+        set_error("hbt_sgd_write_scalars: param_dtype %d is not F32, BF16 or F16", param_dtype);
+        return HBT_ERR_INVALID_ARGUMENT;
+    }
+    if (!sgd_flags_ok("hbt_sgd_write_scalars", flags)) return HBT_ERR_INVALID_ARGUMENT;
+    return write_slot("hbt_sgd_write_scalars", slot,
+                      sgd_scalars(param_dtype, unscale, weight_decay, momentum, one_minus_dampening, neg_lr, flags),
+                      as_stream(stream));
+}
+
+int32_t hbt_adamw_step_f64(double* const* params, double* const* grads, double* const* exp_avgs,
+                           double* const* exp_avg_sqs, const int64_t* numels, int32_t count, double unscale,
+                           const double* grad_mul, double decay, double lerp_weight, double beta2,
+                           double one_minus_beta2, double bias_correction2_sqrt, double eps, double neg_step_size,
+                           int32_t flags, void* stream) {
+    return adamw_step_f64_impl("hbt_adamw_step_f64", params, grads, exp_avgs, exp_avg_sqs, numels, count, unscale,
+                               grad_mul, decay, lerp_weight, beta2, one_minus_beta2, bias_correction2_sqrt, eps,
+                               neg_step_size, nullptr, flags, stream);
+}
+
+int32_t hbt_adamw_step_f64_slot(double* const* params, double* const* grads, double* const* exp_avgs,
+                                double* const* exp_avg_sqs, const int64_t* numels, int32_t count, double unscale,
+                                const double* grad_mul, double decay, double lerp_weight, double beta2,
+                                double one_minus_beta2, double bias_correction2_sqrt, double eps,
+                                double neg_step_size, const void* slot, int32_t flags, void* stream) {
+    clear_error();
+    if (!slot_ok("hbt_adamw_step_f64_slot", slot)) return HBT_ERR_INVALID_ARGUMENT;
+    return adamw_step_f64_impl("hbt_adamw_step_f64_slot", params, grads, exp_avgs, exp_avg_sqs, numels, count,
+                               unscale, grad_mul, decay, lerp_weight, beta2, one_minus_beta2, bias_correction2_sqrt,
+                               eps, neg_step_size, static_cast<const AdamScalarsF64*>(slot), flags, stream);
+}
+
+int32_t hbt_adamw_write_scalars_f64(void* slot, double unscale, double decay, double lerp_weight, double beta2,
+                                    double one_minus_beta2, double bias_correction2_sqrt, double eps,
+                                    double neg_step_size, void* stream) {
+    clear_error();
+    return write_slot("hbt_adamw_write_scalars_f64", slot,
+                      adam_scalars_f64(unscale, decay, lerp_weight, beta2, one_minus_beta2, bias_correction2_sqrt,
+                                       eps, neg_step_size),
+                      as_stream(stream));
+}
+
+int32_t hbt_sgd_step_f64(double* const* params, double* const* grads, double* const* momentum_buffers,
+                         const int64_t* numels, int32_t count, double unscale, const double* grad_mul,
+                         double weight_decay, double momentum, double one_minus_dampening, double neg_lr,
+                         int32_t flags, void* stream) {
+    return sgd_step_f64_impl("hbt_sgd_step_f64", params, grads, momentum_buffers, numels, count, unscale, grad_mul,
+                             weight_decay, momentum, one_minus_dampening, neg_lr, nullptr, flags, stream);
+}
+
+int32_t hbt_sgd_step_f64_slot(double* const* params, double* const* grads, double* const* momentum_buffers,
+                              const int64_t* numels, int32_t count, double unscale, const double* grad_mul,
+                              double weight_decay, double momentum, double one_minus_dampening, double neg_lr,
+                              const void* slot, int32_t flags, void* stream) {
+    clear_error();
+    if (!slot_ok("hbt_sgd_step_f64_slot", slot)) return HBT_ERR_INVALID_ARGUMENT;
+    return sgd_step_f64_impl("hbt_sgd_step_f64_slot", params, grads, momentum_buffers, numels, count, unscale,
+                             grad_mul, weight_decay, momentum, one_minus_dampening, neg_lr,
+                             static_cast<const SgdScalarsF64*>(slot), flags, stream);
+}
+
+int32_t hbt_sgd_write_scalars_f64(void* slot, double unscale, double weight_decay, double momentum,
+                                  double one_minus_dampening, double neg_lr, int32_t flags, void* stream) {
+    clear_error();
+    if (!sgd_flags_ok("hbt_sgd_write_scalars_f64", flags)) return HBT_ERR_INVALID_ARGUMENT;
+    return write_slot("hbt_sgd_write_scalars_f64", slot,
+                      sgd_scalars_f64(unscale, weight_decay, momentum, one_minus_dampening, neg_lr, flags),
+                      as_stream(stream));
+}
+
+int32_t hbt_write_words(void* dst, const uint32_t* words, int64_t count, void* stream) {
+    clear_error();
+    return write_words("hbt_write_words", dst, words, count, as_stream(stream));
 }
 
 }  // extern "C"

@@ -32,6 +32,7 @@ from .buckets import BucketedGradients, BucketLayout, GradientBucket, build_buck
 from .flat_param import (FlatParameter, FlatParamHandle, PieceLayout, ShardedTensorPiece, optimizer_parameter_layout,
                          reshard_state_dict_pieces)
 from .grad_scaler import GradScaler, GradScalerState
+from .graphs import StepGraph
 from .groups import GroupHandle
 from .manifest import (
     CheckpointManifest,

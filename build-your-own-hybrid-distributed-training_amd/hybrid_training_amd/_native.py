@@ -19,6 +19,8 @@ import os
 import threading
 from collections import OrderedDict
 from collections.abc import Iterable, Sequence
+from contextvars import ContextVar
+from typing import Any
 
 import torch
 from torch.autograd.graph import increment_version
@@ -32,6 +34,7 @@ __all__ = [
     "COPY_HINTS",
     "COPY_CONVERSIONS",
     "OPTIMIZER_DTYPES",
+    "STEP_SLOT_BYTES",
     "STEP_WRITE_GRAD",
     "COPY_OP_COPY",
     "COPY_OP_DIVIDE",
@@ -45,12 +48,14 @@ __all__ = [
     "DTYPE_F32",
     "DTYPE_F64",
     "EXPORTED_SYMBOLS",
+    "GraphRecording",
     "MAX_LOCAL_RANKS",
     "MAX_TENSORS_PER_LAUNCH",
     "PIECES_PER_NORM_CHUNK",
     "check",
     "contiguous_source",
     "dtype_code",
+    "graph_recording",
     "library",
     "library_path",
     "require_dense",
@@ -58,7 +63,7 @@ __all__ = [
     "stream_of",
 ]
 
-ABI_VERSION = 16
+ABI_VERSION = 17
 MAX_TENSORS_PER_LAUNCH = 16
 MAX_LOCAL_RANKS = 64
 #: Doubles of working storage hbt_scale_inplace_sqnorm takes per partial for 2-byte gradients.
@@ -88,6 +93,8 @@ SGD_NESTEROV = 4
 SGD_WEIGHT_DECAY = 8
 #: hbt_adamw_step / hbt_sgd_step flag: store the unscaled, clipped gradient back.
 STEP_WRITE_GRAD = 16
+#: Bytes of device memory one step-scalar slot occupies (HBT_STEP_SLOT_BYTES).
+STEP_SLOT_BYTES = 128
 #: (parameter, gradient) dtype pairs the optimizer kernels update.
 OPTIMIZER_DTYPES = frozenset({
     (torch.float32, torch.float32), (torch.float32, torch.bfloat16),
@@ -188,6 +195,52 @@ EXPORTED_SYMBOLS: dict[str, tuple[object, tuple[object, ...]]] = {
         _c_i32,
         (_ptr_array, _i64_array, _c_i32, _c_f64, _c_void_p, _c_void_p),
     ),
+    "hbt_adamw_step_slot": (
+        _c_i32,
+        (
+            _ptr_array, _ptr_array, _ptr_array, _ptr_array, _i64_array, _c_i32, _c_i32, _c_i32,
+            _c_f32, _c_void_p, _c_f32, _c_f32, _c_f32, _c_f32, _c_f32, _c_f32, _c_f32,
+            _c_void_p, _c_i32, _c_void_p,
+        ),
+    ),
+    "hbt_adamw_write_scalars": (
+        _c_i32,
+        (_c_void_p, _c_i32, _c_f32, _c_f32, _c_f32, _c_f32, _c_f32, _c_f32, _c_f32, _c_f32, _c_void_p),
+    ),
+    "hbt_sgd_step_slot": (
+        _c_i32,
+        (
+            _ptr_array, _ptr_array, _ptr_array, _i64_array, _c_i32, _c_i32, _c_i32, _c_f32, _c_void_p,
+            _c_f32, _c_f32, _c_f32, _c_f32, _c_void_p, _c_i32, _c_void_p,
+        ),
+    ),
+    "hbt_sgd_write_scalars": (
+        _c_i32,
+        (_c_void_p, _c_i32, _c_f32, _c_f32, _c_f32, _c_f32, _c_f32, _c_i32, _c_void_p),
+    ),
+    "hbt_adamw_step_f64_slot": (
+        _c_i32,
+        (
+            _ptr_array, _ptr_array, _ptr_array, _ptr_array, _i64_array, _c_i32, _c_f64, _c_void_p,
+            _c_f64, _c_f64, _c_f64, _c_f64, _c_f64, _c_f64, _c_f64, _c_void_p, _c_i32, _c_void_p,
+        ),
+    ),
+    "hbt_adamw_write_scalars_f64": (
+        _c_i32,
+        (_c_void_p, _c_f64, _c_f64, _c_f64, _c_f64, _c_f64, _c_f64, _c_f64, _c_f64, _c_void_p),
+    ),
+    "hbt_sgd_step_f64_slot": (
+        _c_i32,
+        (
+            _ptr_array, _ptr_array, _ptr_array, _i64_array, _c_i32, _c_f64, _c_void_p,
+            _c_f64, _c_f64, _c_f64, _c_f64, _c_void_p, _c_i32, _c_void_p,
+        ),
+    ),
+    "hbt_sgd_write_scalars_f64": (
+        _c_i32,
+        (_c_void_p, _c_f64, _c_f64, _c_f64, _c_f64, _c_f64, _c_i32, _c_void_p),
+    ),
+    "hbt_write_words": (_c_i32, (_c_void_p, ctypes.POINTER(ctypes.c_uint32), _c_i64, _c_void_p)),
 }
 
 _LOCK = threading.Lock()
@@ -201,6 +254,83 @@ _LIB: ctypes.CDLL | None = None
 # upload, which for a few hundred rows costs more than moving a GB on the device.
 _TABLE_CACHE: "OrderedDict[tuple, tuple[torch.Tensor, int, bool, bool]]" = OrderedDict()
 _TABLE_CACHE_SIZE = 256
+
+
+class GraphRecording:
+    """What a :class:`~hybrid_training_amd.graphs.StepGraph` collects while it records:
+    the optimizer launches whose scalars each replay rewrites (``steps``, objects whose
+    ``prepare()`` checks the recorded launch and returns the action that rewrites them)
+    and the device tables recorded launches read (``tables``), which must live as long
+    as the graph.
+
+    The step-scalar slots come from one slab allocated before the capture starts, not
+    from the graph's private pool: the host writes a slot before each replay and the
+    replay reads it, while a block of the private pool may also belong to a temporary
+    that an earlier recorded launch writes during the same replay.
+    """
+
+    #: Step-scalar slots one recording can hand out.
+    MAX_SLOTS = 256
+
+    def __init__(self, device: torch.device) -> None:
+        self.steps: list[Any] = []
+        self.tables: list[torch.Tensor] = []
+        self._slab = torch.zeros(self.MAX_SLOTS * STEP_SLOT_BYTES // 8, dtype=torch.float64, device=device)
+        self._used = 0
+
+    def new_slot(self) -> torch.Tensor:
+        """``STEP_SLOT_BYTES`` of device memory outside the graph's pool."""
+        if self._used == self.MAX_SLOTS:
+            raise UnsupportedFeatureError(
+                format_error("native.GraphRecording", "the step function launches more optimizer batches than "
+                             "one recording holds slots for", expected=f"at most {self.MAX_SLOTS}")
+            )
+        per = STEP_SLOT_BYTES // 8
+        slot = self._slab[self._used * per : (self._used + 1) * per]
+        self._used += 1
+        return slot
+
+
+_RECORDING: ContextVar[GraphRecording | None] = ContextVar("hbt_graph_recording", default=None)
+
+
+def graph_recording() -> GraphRecording | None:
+    """The recording in progress, or ``None`` when launches run eagerly.
+
+    Raises:
+        UnsupportedFeatureError: if torch's current stream is being captured into a
+            HIP graph without a recording (a bare ``torch.cuda.graph``): a recorded
+            step would replay the scalars and tables of its recording forever.
+    """
+    recording = _RECORDING.get()
+    if recording is None and torch.cuda.is_available() and torch.cuda.is_current_stream_capturing():
+        raise UnsupportedFeatureError(
+            format_error("native.graph_recording",
+                         "this work is being captured into a HIP graph outside hybrid_training_amd.StepGraph, "
+                         "whose replays would repeat the recorded step scalars and copy tables",
+                         resolution="record the step with hybrid_training_amd.StepGraph")
+        )
+    return recording
+
+
+def set_graph_recording(recording: GraphRecording | None):
+    """Make ``recording`` the current one; returns the token that restores the previous."""
+    return _RECORDING.set(recording)
+
+
+def reset_graph_recording(token) -> None:
+    _RECORDING.reset(token)
+
+
+def write_words(device: torch.device, dst: torch.Tensor, words: Sequence[int]) -> None:
+    """Write 32-bit ``words`` into the dense device tensor ``dst`` (at least as many bytes)
+    by launches that carry them as arguments (``hbt_write_words``) on the current stream."""
+    require_device_tensor(dst, "native.write_words")
+    if len(words) * 4 > dst.numel() * dst.element_size():
+        raise ValueError("more words than the destination holds")
+    host = (ctypes.c_uint32 * max(1, len(words)))(*words)
+    with torch.cuda.device(device):
+        check(library().hbt_write_words(dst.data_ptr(), host, len(words), stream_of(device)), "native.write_words")
 
 
 def release_tables() -> None:
@@ -425,13 +555,15 @@ def _prepared_plan(
 ) -> tuple[torch.Tensor, int, bool, bool]:
     """(device table, total chunks, aligned, hinted) for a plan, built once per distinct plan
     and stream.  The table is uploaded on that stream, so later launches on it see it."""
+    recording = graph_recording()
     stream = stream_of(device)
     key = (device, stream, src_code, dst_code, scale, rows)
-    with _TABLE_LOCK:
-        entry = _TABLE_CACHE.get(key)
-        if entry is not None:
-            _TABLE_CACHE.move_to_end(key)
-            return entry
+    if recording is None:
+        with _TABLE_LOCK:
+            entry = _TABLE_CACHE.get(key)
+            if entry is not None:
+                _TABLE_CACHE.move_to_end(key)
+                return entry
     chunk = _copy_chunk(library(), src_code, dst_code)
     flat, first = plan_table(rows, chunk, scale)
     aligned = plan_is_aligned(rows, src_code, dst_code)
@@ -439,6 +571,17 @@ def _prepared_plan(
     hinted = len(rows) > 1
     if hinted:
         flat = flat + plan_hints(flat[3::4], first)
+    if recording is not None:
+        # Inside a graph recording the table is written by launches that carry it in
+        # their arguments, so every replay rewrites it from the recorded words; the
+        # graph owns it (a host-to-device copy from pageable memory cannot be recorded).
+        table = torch.empty(len(flat), dtype=torch.int64, device=device)
+        words = []
+        for value in flat:
+            words.extend((value & 0xFFFFFFFF, (value >> 32) & 0xFFFFFFFF))
+        write_words(device, table, words)
+        recording.tables.append(table)
+        return table, first, aligned, hinted
     host = torch.tensor(flat, dtype=torch.int64).pin_memory()
     with torch.cuda.device(device):
         table = host.to(device, non_blocking=True)

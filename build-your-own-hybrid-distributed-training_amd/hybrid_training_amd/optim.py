@@ -41,7 +41,7 @@ and the HBM traffic of a clipped fp32 step:
 
 from __future__ import annotations
 
-from collections.abc import Iterable, Sequence
+from collections.abc import Callable, Iterable, Sequence
 from dataclasses import dataclass, field
 from typing import Any
 
@@ -672,25 +672,192 @@ def _write_back_flag(write_back: bool, grad_mul: NormResult | None, unscale: flo
     return _native.STEP_WRITE_GRAD if write_back and (grad_mul is not None or unscale != 1.0) else 0
 
 
-def _adamw_call(lib, pdtype, gdtype, p, g, m, v, numels, unscale, mul_ptr, scalars, flags, stream) -> int:
+def _adamw_call(lib, pdtype, gdtype, p, g, m, v, numels, unscale, mul_ptr, scalars, flags, stream,
+                slot: torch.Tensor | None = None) -> int:
     """One ``hbt_adamw_step`` launch, or ``hbt_adamw_step_f64`` (double scalars) on float64
-    parameters; ``p``, ``g``, ``m``, ``v`` are lists of device addresses."""
+    parameters; ``p``, ``g``, ``m``, ``v`` are lists of device addresses.  With ``slot`` the
+    ``*_slot`` form, whose kernels read the scalars from that device memory."""
     tables = (_native.pointer_array(p), _native.pointer_array(g), _native.pointer_array(m),
               _native.pointer_array(v), _native.int64_array(numels), len(numels))
     if pdtype == torch.float64:
+        if slot is not None:
+            return lib.hbt_adamw_step_f64_slot(*tables, float(unscale), mul_ptr, *scalars, slot.data_ptr(), flags,
+                                               stream)
         return lib.hbt_adamw_step_f64(*tables, float(unscale), mul_ptr, *scalars, flags, stream)
-    return lib.hbt_adamw_step(*tables, _native.dtype_code(pdtype), _native.dtype_code(gdtype), unscale, mul_ptr,
-                              *scalars, flags, stream)
+    codes = (_native.dtype_code(pdtype), _native.dtype_code(gdtype))
+    if slot is not None:
+        return lib.hbt_adamw_step_slot(*tables, *codes, unscale, mul_ptr, *scalars, slot.data_ptr(), flags, stream)
+    return lib.hbt_adamw_step(*tables, *codes, unscale, mul_ptr, *scalars, flags, stream)
 
 
-def _sgd_call(lib, pdtype, gdtype, p, g, buf, numels, unscale, mul_ptr, scalars, flags, stream) -> int:
-    """One ``hbt_sgd_step`` launch, or ``hbt_sgd_step_f64`` on float64 parameters."""
+def _sgd_call(lib, pdtype, gdtype, p, g, buf, numels, unscale, mul_ptr, scalars, flags, stream,
+              slot: torch.Tensor | None = None) -> int:
+    """One ``hbt_sgd_step`` launch, or ``hbt_sgd_step_f64`` on float64 parameters; with
+    ``slot`` the ``*_slot`` form."""
     tables = (_native.pointer_array(p), _native.pointer_array(g),
               None if buf is None else _native.pointer_array(buf), _native.int64_array(numels), len(numels))
     if pdtype == torch.float64:
+        if slot is not None:
+            return lib.hbt_sgd_step_f64_slot(*tables, float(unscale), mul_ptr, *scalars, slot.data_ptr(), flags,
+                                             stream)
         return lib.hbt_sgd_step_f64(*tables, float(unscale), mul_ptr, *scalars, flags, stream)
-    return lib.hbt_sgd_step(*tables, _native.dtype_code(pdtype), _native.dtype_code(gdtype), unscale, mul_ptr,
-                            *scalars, flags, stream)
+    codes = (_native.dtype_code(pdtype), _native.dtype_code(gdtype))
+    if slot is not None:
+        return lib.hbt_sgd_step_slot(*tables, *codes, unscale, mul_ptr, *scalars, slot.data_ptr(), flags, stream)
+    return lib.hbt_sgd_step(*tables, *codes, unscale, mul_ptr, *scalars, flags, stream)
+
+
+def _adamw_scalars(group: dict, step: float) -> tuple[float, ...]:
+    """The step's scalars exactly as torch/optim/adam.py:416-547 forms them (Python
+    doubles): decay, 1 - beta1, beta2, 1 - beta2, sqrt(bias_correction2), eps, -step_size."""
+    lr = float(group["lr"])
+    beta1, beta2 = (float(b) for b in group["betas"])
+    weight_decay = float(group["weight_decay"])
+    bias_correction1 = 1 - beta1**step
+    bias_correction2 = 1 - beta2**step
+    step_size = lr / bias_correction1
+    bias_correction2_sqrt = bias_correction2**0.5
+    decay = 1 - lr * weight_decay if weight_decay != 0 else 1.0
+    return (decay, 1 - beta1, beta2, 1 - beta2, bias_correction2_sqrt, float(group["eps"]), -step_size)
+
+
+def _sgd_scalars(group: dict) -> tuple[tuple[float, ...], int]:
+    """SGD's scalars (weight_decay, momentum, 1 - dampening, -lr; Python doubles, as torch
+    forms them) and the flags they select, without the first-step and write-back flags."""
+    lr = float(group["lr"])
+    momentum = float(group["momentum"])
+    weight_decay = float(group["weight_decay"])
+    flags = 0
+    if weight_decay != 0:
+        flags |= _native.SGD_WEIGHT_DECAY
+    if momentum != 0:
+        flags |= _native.SGD_MOMENTUM
+        if bool(group["nesterov"]):
+            flags |= _native.SGD_NESTEROV
+    return (weight_decay, momentum, 1 - float(group["dampening"]), -lr), flags
+
+
+def _unrecordable(reason: str) -> UnsupportedFeatureError:
+    return UnsupportedFeatureError(
+        format_error("optim.ShardedOptimizer.step", f"this step cannot be recorded into a HIP graph: {reason}",
+                     resolution="take such steps eagerly; record a step only after an eager one, with the "
+                     "gradients, parameters and state in device memory and no pending loss-scale factor")
+    )
+
+
+class _RecordedAdamW:
+    """One AdamW launch group recorded into a graph, whose kernels read their scalars
+    from ``slot``.  Before each replay, :meth:`prepare` checks that the recorded launch
+    still describes the step and returns the action that does what the eager step does
+    on the host: advance the parameters' step counters and write the new step's scalars,
+    formed as the eager step forms them, into the slot."""
+
+    def __init__(self, optimizer: "ShardedOptimizer", slot: torch.Tensor, params: list[nn.Parameter],
+                 pdtype: torch.dtype, unscale: float, scalars: tuple[float, ...]) -> None:
+        self._optimizer = optimizer
+        self._slot = slot
+        self._params = list(params)
+        self._grad_ptrs = [p.grad.data_ptr() for p in params]
+        self._pdtype = pdtype
+        self._unscale = unscale
+        self._lerp_small = abs(scalars[1]) < 0.5
+
+    @property
+    def parameters(self) -> list[nn.Parameter]:
+        return self._params
+
+    def prepare(self) -> Callable[[], None]:
+        opt = self._optimizer
+        groups = {id(p): g for g in opt._optimizer.param_groups for p in g["params"]}
+        for p, ptr in zip(self._params, self._grad_ptrs):
+            _check_recorded_grad(p, ptr)
+        states = [opt._optimizer.state[p] for p in self._params]
+        steps = {float(s["step"].item()) + 1.0 for s in states}
+        found = {_adamw_scalars(groups[id(p)], step) for p in self._params for step in steps}
+        if len(found) != 1:
+            raise _replay_error("the parameters recorded in one launch no longer share their step scalars")
+        scalars = found.pop()
+        if (abs(scalars[1]) < 0.5) != self._lerp_small:
+            raise _replay_error("beta1 crossed 0.5, which selects another recorded kernel")
+
+        def commit() -> None:
+            lib = _native.library()
+            stream = _native.stream_of(opt._device)
+            with torch.cuda.device(opt._device):
+                if self._pdtype == torch.float64:
+                    status = lib.hbt_adamw_write_scalars_f64(self._slot.data_ptr(), float(self._unscale), *scalars,
+                                                             stream)
+                else:
+                    status = lib.hbt_adamw_write_scalars(self._slot.data_ptr(), _native.dtype_code(self._pdtype),
+                                                         self._unscale, *scalars, stream)
+            _native.check(status, "optim.hbt_adamw_write_scalars")
+            for s in states:
+                s["step"] += 1
+            increment_version(self._params + [s["exp_avg"] for s in states] + [s["exp_avg_sq"] for s in states])
+
+        return commit
+
+
+class _RecordedSgd:
+    """One SGD launch group recorded into a graph (see :class:`_RecordedAdamW`); SGD's
+    scalars follow the learning rate and the other hyperparameters, not the step."""
+
+    def __init__(self, optimizer: "ShardedOptimizer", slot: torch.Tensor, params: list[nn.Parameter],
+                 pdtype: torch.dtype, unscale: float, flags: int) -> None:
+        self._optimizer = optimizer
+        self._slot = slot
+        self._params = list(params)
+        self._grad_ptrs = [p.grad.data_ptr() for p in params]
+        self._pdtype = pdtype
+        self._unscale = unscale
+        self._flags = flags
+
+    @property
+    def parameters(self) -> list[nn.Parameter]:
+        return self._params
+
+    def prepare(self) -> Callable[[], None]:
+        opt = self._optimizer
+        groups = {id(p): g for g in opt._optimizer.param_groups for p in g["params"]}
+        for p, ptr in zip(self._params, self._grad_ptrs):
+            _check_recorded_grad(p, ptr)
+        found = {_sgd_scalars(groups[id(p)]) for p in self._params}
+        if len(found) != 1:
+            raise _replay_error("the parameters recorded in one launch no longer share their scalars")
+        scalars, flags = found.pop()
+        kernel_flags = _native.SGD_WEIGHT_DECAY | _native.SGD_MOMENTUM | _native.SGD_NESTEROV
+        if flags != self._flags & kernel_flags:
+            raise _replay_error("momentum, Nesterov or weight decay was switched on or off, which selects "
+                                "another recorded kernel")
+        buffers = [opt._optimizer.state[p]["momentum_buffer"] for p in self._params] \
+            if self._flags & _native.SGD_MOMENTUM else []
+
+        def commit() -> None:
+            lib = _native.library()
+            stream = _native.stream_of(opt._device)
+            with torch.cuda.device(opt._device):
+                if self._pdtype == torch.float64:
+                    status = lib.hbt_sgd_write_scalars_f64(self._slot.data_ptr(), float(self._unscale), *scalars,
+                                                           self._flags, stream)
+                else:
+                    status = lib.hbt_sgd_write_scalars(self._slot.data_ptr(), _native.dtype_code(self._pdtype),
+                                                       self._unscale, *scalars, self._flags, stream)
+            _native.check(status, "optim.hbt_sgd_write_scalars")
+            increment_version(self._params + buffers)
+
+        return commit
+
+
+def _check_recorded_grad(p: nn.Parameter, recorded_ptr: int) -> None:
+    if p.grad is None or p.grad.data_ptr() != recorded_ptr:
+        raise _replay_error("a parameter's .grad was rebound after recording; a replay reads the gradient "
+                            "buffer it was recorded with (write new values into that tensor instead)")
+
+
+def _replay_error(reason: str) -> UnsupportedFeatureError:
+    return UnsupportedFeatureError(
+        format_error("graphs.StepGraph.replay", reason, resolution="record the step again")
+    )
 
 
 def _pinned_like(p: torch.Tensor) -> torch.Tensor:
@@ -972,37 +1139,24 @@ class ShardedOptimizer:
 
     def _run_adamw_step(self, grad_mul: NormResult | None, write_back: bool) -> None:
         lib = _native.library()
+        recording = self._recording_check()
         batches: dict[tuple, list[nn.Parameter]] = {}
         for group, p, grad in self._stepped_parameters():
-            lr = float(group["lr"])
-            beta1, beta2 = (float(b) for b in group["betas"])
-            eps = float(group["eps"])
-            weight_decay = float(group["weight_decay"])
             state = self._optimizer.state[p]
             if len(state) == 0:
+                if recording is not None:
+                    raise _unrecordable("the first step creates the optimizer state")
                 # Same initial state as torch.optim.Adam._init_group.
                 state["step"] = torch.tensor(0.0, dtype=torch.float32)
                 state["exp_avg"] = self._zero_state(p)
                 state["exp_avg_sq"] = self._zero_state(p)
             step_t = state["step"]
-            step_t += 1
-            step = float(step_t.item())
-            # Host scalars exactly as torch/optim/adam.py:416-547 forms them (double).
-            bias_correction1 = 1 - beta1**step
-            bias_correction2 = 1 - beta2**step
-            step_size = lr / bias_correction1
-            bias_correction2_sqrt = bias_correction2**0.5
-            decay = 1 - lr * weight_decay if weight_decay != 0 else 1.0
-            scalars = (
-                decay,
-                1 - beta1,
-                beta2,
-                1 - beta2,
-                bias_correction2_sqrt,
-                eps,
-                -step_size,
-            )
-            key = (scalars, p.dtype, grad.dtype, _pending_unscale(grad))
+            if recording is None:
+                step_t += 1
+                step = float(step_t.item())
+            else:
+                step = float(step_t.item()) + 1.0  # the step each replay advances to
+            key = (_adamw_scalars(group, step), p.dtype, grad.dtype, _pending_unscale(grad))
             batches.setdefault(key, []).append(p)
         stream = _native.stream_of(self._device)
         with torch.cuda.device(self._device):
@@ -1013,6 +1167,10 @@ class ShardedOptimizer:
                     if is_host(p):
                         self._streamed_adamw(lib, p, scalars, pdtype, gdtype, unscale, mul_ptr, flags)
                 params = [p for p in batch if not is_host(p)]
+                slot = None
+                if recording is not None and params:
+                    slot = recording.new_slot()
+                    recording.steps.append(_RecordedAdamW(self, slot, params, pdtype, unscale, scalars))
                 for start in range(0, len(params), _native.MAX_TENSORS_PER_LAUNCH):
                     chunk = params[start : start + _native.MAX_TENSORS_PER_LAUNCH]
                     states = [self._optimizer.state[p] for p in chunk]
@@ -1023,12 +1181,24 @@ class ShardedOptimizer:
                         [s["exp_avg"].data_ptr() for s in states],
                         [s["exp_avg_sq"].data_ptr() for s in states],
                         [p.numel() for p in chunk],
-                        unscale, mul_ptr, scalars, flags, stream,
+                        unscale, mul_ptr, scalars, flags, stream, slot,
                     )
                     _native.check(status, "optim.hbt_adamw_step")
                     increment_version(chunk)
                     increment_version([s["exp_avg"] for s in states])
                     increment_version([s["exp_avg_sq"] for s in states])
+
+    def _recording_check(self) -> "_native.GraphRecording | None":
+        """The graph recording this step joins, after refusing what a replay cannot repeat."""
+        recording = _native.graph_recording()
+        if recording is not None and (self._offload or self._host_resident):
+            raise _unrecordable("parameters or optimizer state in host memory stream through staging buffers "
+                                "and wait for the copies on the host")
+        if recording is not None:
+            for p in self._parameters:
+                if p.grad is not None and _pending_unscale(p.grad) != 1.0:
+                    raise _unrecordable("a loss-scaled step decides on the host whether to skip")
+        return recording
 
     def _place_state(self, value: torch.Tensor, reference: torch.Tensor) -> torch.Tensor:
         """A loaded state tensor on the reference parameter's device and dtype (pinned if host)."""
@@ -1084,30 +1254,22 @@ class ShardedOptimizer:
     def _run_sgd_step(self, grad_mul: NormResult | None, write_back: bool) -> None:
         """torch.optim.SGD's step (``torch/optim/sgd.py``) as one fused kernel per batch."""
         lib = _native.library()
+        recording = self._recording_check()
         batches: dict[tuple, list[nn.Parameter]] = {}
         for group, p, grad in self._stepped_parameters():
-            lr = float(group["lr"])
-            momentum = float(group["momentum"])
-            dampening = float(group["dampening"])
-            weight_decay = float(group["weight_decay"])
-            nesterov = bool(group["nesterov"])
-            flags = 0
-            if weight_decay != 0:
-                flags |= _native.SGD_WEIGHT_DECAY
-            if momentum != 0:
-                flags |= _native.SGD_MOMENTUM
-                if nesterov:
-                    flags |= _native.SGD_NESTEROV
+            # Scalars exactly as torch forms them: Python doubles, rounded to fp32 (and
+            # each alpha to a 2-byte parameter dtype inside the kernel's entry point), or
+            # kept as doubles for float64 parameters.
+            scalars, flags = _sgd_scalars(group)
+            if flags & _native.SGD_MOMENTUM:
                 state = self._optimizer.state[p]
                 if state.get("momentum_buffer") is None:
+                    if recording is not None:
+                        raise _unrecordable("the first step creates the momentum buffer")
                     # torch starts the buffer as a clone of the first gradient.
                     state["momentum_buffer"] = (_pinned_like(p) if is_host(p)
                                                 else torch.empty_like(p, memory_format=torch.preserve_format))
                     flags |= _native.SGD_FIRST_STEP
-            # Scalars exactly as torch forms them: Python doubles, rounded to fp32 (and
-            # each alpha to a 2-byte parameter dtype inside the kernel's entry point), or
-            # kept as doubles for float64 parameters.
-            scalars = (weight_decay, momentum, 1 - dampening, -lr)
             unscale = _pending_unscale(grad)
             key = (scalars, flags | _write_back_flag(write_back, grad_mul, unscale), p.dtype, grad.dtype, unscale)
             batches.setdefault(key, []).append(p)
@@ -1119,6 +1281,10 @@ class ShardedOptimizer:
                     if is_host(p):
                         self._streamed_sgd(lib, p, scalars, flags, pdtype, gdtype, unscale, mul_ptr)
                 params = [p for p in batch if not is_host(p)]
+                slot = None
+                if recording is not None and params:
+                    slot = recording.new_slot()
+                    recording.steps.append(_RecordedSgd(self, slot, params, pdtype, unscale, flags))
                 for start in range(0, len(params), _native.MAX_TENSORS_PER_LAUNCH):
                     chunk = params[start : start + _native.MAX_TENSORS_PER_LAUNCH]
                     buffers = ([self._optimizer.state[p]["momentum_buffer"] for p in chunk]
@@ -1126,7 +1292,7 @@ class ShardedOptimizer:
                     status = _sgd_call(lib, pdtype, gdtype, [p.data_ptr() for p in chunk],
                                        [p.grad.data_ptr() for p in chunk],
                                        [b.data_ptr() for b in buffers] if buffers else None,
-                                       [p.numel() for p in chunk], unscale, mul_ptr, scalars, flags, stream)
+                                       [p.numel() for p in chunk], unscale, mul_ptr, scalars, flags, stream, slot)
                     _native.check(status, "optim.hbt_sgd_step")
                     increment_version(chunk)
                     if buffers:

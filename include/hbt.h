@@ -442,6 +442,72 @@ int32_t hbt_sgd_step_f64(double* const* params, double* const* grads, double* co
 int32_t hbt_scale_inplace_f64(double* const* tensors, const int64_t* numels, int32_t count, double unscale,
                               const double* grad_mul, void* stream);
 
+/* ------------------------------------------------------------------------------
+ * The optimizer steps with their scalars read from device memory, for a step recorded
+ * once into a HIP graph and replayed.
+ *
+ * Replaces: the same reference step as hbt_adamw_step, hbt_sgd_step and their float64
+ *   forms (ShardedOptimizer.step, optim/sharded_optimizer.py:340-355, running
+ *   torch.optim.AdamW / SGD built at optim/sharded_optimizer.py:111-126), whose host
+ *   recomputes the bias corrections (torch/optim/adam.py) every step.
+ * A launch recorded into a graph keeps the scalar arguments it was recorded with, while
+ * AdamW's bias corrections change every step, and every scalar changes with the
+ * learning rate.  Each *_slot entry point takes the arguments of its eager form plus
+ * `slot`, HBT_STEP_SLOT_BYTES of 16-byte-aligned device memory; its kernels read their
+ * scalars from the slot when they run, not from the arguments.  The arguments still
+ * choose the kernel variant (unscale != 1; |lerp_weight| < 0.5 for AdamW; the flags) and
+ * are validated as by the eager form.  Each *_write_scalars call writes into a slot, by
+ * one launch on `stream`, exactly the scalars the eager form passes its kernels for the
+ * same arguments (for SGD, the flags' weight-decay and Nesterov bits).  Written on the
+ * replay's stream before each replay, they make the recorded step the eager step those
+ * arguments describe, bit for bit.  The values written must keep the variant that the
+ * step was recorded with, and the writer must match the step it feeds: AdamW or SGD,
+ * float64 or not, and the same param_dtype.
+ * ---------------------------------------------------------------------------- */
+#define HBT_STEP_SLOT_BYTES 128
+int32_t hbt_adamw_step_slot(void* const* params, void* const* grads, void* const* exp_avgs,
+                            void* const* exp_avg_sqs, const int64_t* numels, int32_t count,
+                            int32_t param_dtype, int32_t grad_dtype, float unscale, const float* grad_mul,
+                            float decay, float lerp_weight, float beta2, float one_minus_beta2,
+                            float bias_correction2_sqrt, float eps, float neg_step_size, const void* slot,
+                            int32_t flags, void* stream);
+int32_t hbt_adamw_write_scalars(void* slot, int32_t param_dtype, float unscale, float decay, float lerp_weight,
+                                float beta2, float one_minus_beta2, float bias_correction2_sqrt, float eps,
+                                float neg_step_size, void* stream);
+int32_t hbt_sgd_step_slot(void* const* params, void* const* grads, void* const* momentum_buffers,
+                          const int64_t* numels, int32_t count, int32_t param_dtype, int32_t grad_dtype,
+                          float unscale, const float* grad_mul, float weight_decay, float momentum,
+                          float one_minus_dampening, float neg_lr, const void* slot, int32_t flags, void* stream);
+int32_t hbt_sgd_write_scalars(void* slot, int32_t param_dtype, float unscale, float weight_decay, float momentum,
+                              float one_minus_dampening, float neg_lr, int32_t flags, void* stream);
+int32_t hbt_adamw_step_f64_slot(double* const* params, double* const* grads, double* const* exp_avgs,
+                                double* const* exp_avg_sqs, const int64_t* numels, int32_t count, double unscale,
+                                const double* grad_mul, double decay, double lerp_weight, double beta2,
+                                double one_minus_beta2, double bias_correction2_sqrt, double eps,
+                                double neg_step_size, const void* slot, int32_t flags, void* stream);
+int32_t hbt_adamw_write_scalars_f64(void* slot, double unscale, double decay, double lerp_weight, double beta2,
+                                    double one_minus_beta2, double bias_correction2_sqrt, double eps,
+                                    double neg_step_size, void* stream);
+int32_t hbt_sgd_step_f64_slot(double* const* params, double* const* grads, double* const* momentum_buffers,
+                              const int64_t* numels, int32_t count, double unscale, const double* grad_mul,
+                              double weight_decay, double momentum, double one_minus_dampening, double neg_lr,
+                              const void* slot, int32_t flags, void* stream);
+int32_t hbt_sgd_write_scalars_f64(void* slot, double unscale, double weight_decay, double momentum,
+                                  double one_minus_dampening, double neg_lr, int32_t flags, void* stream);
+
+/* ------------------------------------------------------------------------------
+ * Small host-built data written into device memory by kernel launches.
+ *
+ * This entry point has no counterpart in the reference.  It is for callers that record
+ * work into a HIP graph: a copy from pageable host memory cannot be recorded, and a
+ * recorded copy from pinned memory reads that memory at every replay.  It writes
+ * words[0 .. count) to `dst` (4-byte-aligned device memory) by launches on `stream` of
+ * at most 64 words each; the words travel in the launch arguments, so a recorded launch
+ * keeps them and the host buffer may be reused as soon as the call returns.  Used for
+ * the interval tables of copies recorded into a graph.
+ * ---------------------------------------------------------------------------- */
+int32_t hbt_write_words(void* dst, const uint32_t* words, int64_t count, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

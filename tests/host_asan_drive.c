@@ -9,7 +9,7 @@ static int fails = 0;
 #define EXPECT(cond) do { if (!(cond)) { printf("FAIL line %d: %s (%s)\n", __LINE__, #cond, hbt_last_error()); fails++; } } while (0)
 
 int main(void) {
-    static float buf[1 << 16];
+    static float buf[1 << 16] __attribute__((aligned(64)));  // 16-byte aligned slots
     void* ptrs[64];
     const void* cptrs[64];
     int64_t numels[64];
@@ -93,6 +93,40 @@ int main(void) {
     EXPECT(hbt_norm_partials_count(numels, 1, HBT_DTYPE_F64) >= 0);
     EXPECT(hbt_grad_norm_noalloc(cptrs, numels, weights, HBT_MAX_TENSORS_PER_LAUNCH + 1, HBT_DTYPE_F32, 1.0f, 1.0,
                                  NULL, NULL, NULL, NULL, NULL) != HBT_OK);
+    // slot forms of the steps: full tables of empty tensors launch nothing; bad slots and
+    // tables are refused; the writers check slot, dtype and flags before they launch
+    for (int c = 0; c <= HBT_MAX_TENSORS_PER_LAUNCH + 1; ++c) {
+        int rc = hbt_adamw_step_slot(ptrs, ptrs, ptrs, ptrs, numels, c, HBT_DTYPE_BF16, HBT_DTYPE_BF16, 1.0f, NULL,
+                                     1.0f, 0.1f, 0.9f, 0.1f, 1.0f, 1e-8f, -1e-3f, buf, 0, NULL);
+        EXPECT(rc == (c <= HBT_MAX_TENSORS_PER_LAUNCH ? HBT_OK : HBT_ERR_INVALID_ARGUMENT));
+        rc = hbt_sgd_step_slot(ptrs, ptrs, ptrs, numels, c, HBT_DTYPE_F32, HBT_DTYPE_F32, 1.0f, NULL, 0.01f, 0.9f,
+                               1.0f, -0.1f, buf, HBT_SGD_MOMENTUM, NULL);
+        EXPECT(rc == (c <= HBT_MAX_TENSORS_PER_LAUNCH ? HBT_OK : HBT_ERR_INVALID_ARGUMENT));
+        rc = hbt_adamw_step_f64_slot((double* const*)ptrs, (double* const*)ptrs, (double* const*)ptrs,
+                                     (double* const*)ptrs, numels, c, 1.0, NULL, 1.0, 0.1, 0.9, 0.1, 1.0, 1e-8, -1e-3,
+                                     buf, 0, NULL);
+        EXPECT(rc == (c <= HBT_MAX_TENSORS_PER_LAUNCH ? HBT_OK : HBT_ERR_INVALID_ARGUMENT));
+        rc = hbt_sgd_step_f64_slot((double* const*)ptrs, (double* const*)ptrs, NULL, numels, c, 1.0, NULL, 0.0, 0.0,
+                                   1.0, -0.1, buf, 0, NULL);
+        EXPECT(rc == (c <= HBT_MAX_TENSORS_PER_LAUNCH ? HBT_OK : HBT_ERR_INVALID_ARGUMENT));
+    }
+    EXPECT(hbt_adamw_step_slot(ptrs, ptrs, ptrs, ptrs, numels, 1, HBT_DTYPE_F32, HBT_DTYPE_F32, 1.0f, NULL, 1.0f,
+                               0.1f, 0.9f, 0.1f, 1.0f, 1e-8f, -1e-3f, NULL, 0, NULL) == HBT_ERR_INVALID_ARGUMENT);
+    EXPECT(hbt_adamw_step_slot(ptrs, ptrs, ptrs, ptrs, numels, 1, HBT_DTYPE_F32, HBT_DTYPE_F32, 1.0f, NULL, 1.0f,
+                               0.1f, 0.9f, 0.1f, 1.0f, 1e-8f, -1e-3f, (char*)buf + 4, 0, NULL)
+           == HBT_ERR_INVALID_ARGUMENT);
+    EXPECT(hbt_adamw_write_scalars(NULL, HBT_DTYPE_F32, 1.0f, 1.0f, 0.1f, 0.9f, 0.1f, 1.0f, 1e-8f, -1e-3f, NULL)
+           == HBT_ERR_INVALID_ARGUMENT);
+    EXPECT(hbt_adamw_write_scalars(buf, HBT_DTYPE_F64, 1.0f, 1.0f, 0.1f, 0.9f, 0.1f, 1.0f, 1e-8f, -1e-3f, NULL)
+           == HBT_ERR_INVALID_ARGUMENT);
+    EXPECT(hbt_sgd_write_scalars(buf, HBT_DTYPE_F32, 1.0f, 0.0f, 0.0f, 1.0f, -0.1f, HBT_SGD_FIRST_STEP, NULL)
+           == HBT_ERR_INVALID_ARGUMENT);
+    EXPECT(hbt_adamw_write_scalars_f64((char*)buf + 8, 1.0, 1.0, 0.1, 0.9, 0.1, 1.0, 1e-8, -1e-3, NULL)
+           == HBT_ERR_INVALID_ARGUMENT);
+    EXPECT(hbt_sgd_write_scalars_f64(buf, 1.0, 0.0, 0.0, 1.0, -0.1, 1 << 10, NULL) == HBT_ERR_INVALID_ARGUMENT);
+    EXPECT(hbt_write_words(NULL, NULL, 0, NULL) == HBT_OK);
+    EXPECT(hbt_write_words((char*)buf + 2, (const uint32_t*)buf, 1, NULL) == HBT_ERR_INVALID_ARGUMENT);
+    EXPECT(hbt_write_words(buf, NULL, 1, NULL) == HBT_ERR_INVALID_ARGUMENT);
     (void)hbt_last_error();
     printf("asan host drive: %d failures\n", fails);
     return fails;

@@ -1,0 +1,165 @@
+"""StepGraph: the drop-in tail recorded once into a HIP graph and replayed.
+
+Two copies of the same FSDP setup (the reference's 1,857-parameter MLP as W ranks'
+flat units, each with its ShardedOptimizer) take the same steps: one eagerly, one by
+replaying a recording of its first copy's step function.  Between steps the program
+writes new gradients into the gradient buffers (eager device work between replays) and,
+once, changes the learning rate.  After every step the parameters, gradients, optimizer
+state, step counters and returned norms must be bitwise equal: a replay is the eager
+step, with the step scalars (AdamW's bias corrections, the learning rate) taken from the
+host state of that step.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+import torch.nn as nn
+
+from hybrid_training_amd import (
+    FlatParamHandle,
+    FSDPConfig,
+    GroupHandle,
+    MixedPrecisionConfig,
+    OptimizerConfig,
+    ShardedOptimizer,
+    StepGraph,
+    UnsupportedFeatureError,
+)
+from hybrid_training_amd.optim import PENDING_UNSCALE_ATTR
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda", 0)
+TOTAL = 1857
+
+
+class _Tail:
+    """W ranks' FSDP units of one MLP, their optimizers, and full gradients in fixed buffers."""
+
+    def __init__(self, world: int, config: OptimizerConfig, dtype: torch.dtype = torch.float32, **placement):
+        torch.manual_seed(0)
+        model = nn.Sequential(nn.Linear(23, 32), nn.ReLU(), nn.Linear(32, 32), nn.ReLU(), nn.Linear(32, 1))
+        named = list(model.to(DEV, dtype).named_parameters())
+        self.handles = [FlatParamHandle(named, None, GroupHandle.local_view("shard", world, r), FSDPConfig(),
+                                        MixedPrecisionConfig(enabled=False), DEV, keep_originals=True)
+                        for r in range(world)]
+        padded = self.handles[0].padded_numel
+        self.grads = [torch.zeros(padded, device=DEV, dtype=dtype) for _ in range(world)]
+        self.opts = [ShardedOptimizer([h.flat_param], config, norm_group=GroupHandle.local_view("world", world, r),
+                                      device=DEV, **placement) for r, h in enumerate(self.handles)]
+
+    def load_grads(self, k: int) -> None:
+        gen = torch.Generator(device=DEV).manual_seed(100 + k)
+        for g in self.grads:
+            g.copy_(torch.randn(g.shape, device=DEV, generator=gen, dtype=torch.float32).to(g.dtype))
+            g[TOTAL:] = 0.0  # the padding carries no gradient
+
+    def step(self) -> list[torch.Tensor]:
+        norms = []
+        for r, (h, opt) in enumerate(zip(self.handles, self.opts)):
+            h.flat_param.grad = h.reduce_scatter_gradient(self.grads[r], peer_grads=self.grads)
+            norms.append(opt.clip_grad_norm(1.0))
+            opt.step()
+        return norms
+
+
+def _assert_same(eager: _Tail, graphed: _Tail, eager_norms, graphed_norms, k: int) -> None:
+    for r, (he, hg) in enumerate(zip(eager.handles, graphed.handles)):
+        assert torch.equal(he.flat_param, hg.flat_param), (k, r, "param")
+        assert torch.equal(he.flat_param.grad, hg.flat_param.grad), (k, r, "grad")
+    for oe, og in zip(eager.opts, graphed.opts):
+        (pe,), (pg,) = oe.parameters, og.parameters
+        se, sg = oe.inner.state[pe], og.inner.state[pg]
+        assert se.keys() == sg.keys()
+        for key in se:
+            assert torch.equal(se[key], sg[key]), (k, key)
+    for ne, ng in zip(eager_norms, graphed_norms):
+        assert torch.equal(ne, ng), (k, "norm")
+
+
+def _run(world: int, config: OptimizerConfig, dtype=torch.float32, replays: int = 5, **placement) -> StepGraph:
+    eager, graphed = _Tail(world, config, dtype, **placement), _Tail(world, config, dtype, **placement)
+    for tail in (eager, graphed):
+        tail.load_grads(0)
+        tail.step()  # the eager step that creates the optimizer state
+    graph = StepGraph(graphed.step)
+    assert graph.recorded_steps == world
+    for k in range(1, replays + 1):
+        if k == 3:
+            for tail in (eager, graphed):
+                for opt in tail.opts:
+                    opt.set_learning_rate(4e-4)
+        for tail in (eager, graphed):
+            tail.load_grads(k)
+        norms = eager.step()
+        graph.replay()
+        torch.cuda.synchronize()
+        _assert_same(eager, graphed, norms, graph.output, k)
+    return graph
+
+
+@pytest.mark.parametrize("world", [2, 4])
+@pytest.mark.parametrize("placement", [{}, {"clip_in_step": True}, {"defer_clip": True}],
+                         ids=["in_place_clip", "clip_in_step", "defer_clip"])
+def test_recorded_adamw_tail_replays_the_eager_steps(world, placement):
+    _run(world, OptimizerConfig(learning_rate=1e-3, weight_decay=0.01), **placement)
+
+
+def test_recorded_sgd_tail_replays_the_eager_steps():
+    _run(2, OptimizerConfig(name="sgd", learning_rate=1e-2, weight_decay=0.01, momentum=0.9))
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.bfloat16], ids=["float64", "bfloat16"])
+def test_recorded_tail_on_other_master_dtypes(dtype):
+    _run(2, OptimizerConfig(learning_rate=1e-3, weight_decay=0.01), dtype, replays=3)
+    _run(2, OptimizerConfig(name="sgd", learning_rate=1e-2, momentum=0.9), dtype, replays=3)
+
+
+# A refused recording ends its capture early, sometimes before any launch.
+@pytest.mark.filterwarnings("ignore:The CUDA Graph is empty")
+def test_recording_refuses_what_a_replay_cannot_repeat():
+    config = OptimizerConfig(learning_rate=1e-3)
+    tail = _Tail(2, config)
+    tail.load_grads(0)
+    # before any eager step the optimizer state does not exist yet
+    with pytest.raises(UnsupportedFeatureError, match="creates the optimizer state"):
+        StepGraph(tail.step)
+    tail.step()
+    # a pending loss-scale factor: the scaler decides on the host whether to skip
+    grad = tail.handles[0].flat_param.grad
+    setattr(grad, PENDING_UNSCALE_ATTR, 0.5)
+    with pytest.raises(UnsupportedFeatureError, match="loss-scaled"):
+        StepGraph(lambda: tail.opts[0].step())
+    delattr(grad, PENDING_UNSCALE_ATTR)
+    # a bare torch.cuda.graph capture of a step: its replays would keep the recorded scalars
+    with pytest.raises(UnsupportedFeatureError, match="StepGraph"):
+        with torch.cuda.graph(torch.cuda.CUDAGraph()):
+            tail.opts[0].step()
+    # a function that steps one optimizer twice
+    with pytest.raises(UnsupportedFeatureError, match="twice"):
+        StepGraph(lambda: (tail.opts[0].step(), tail.opts[0].step()))
+    # the eager path still works after the refusals
+    tail.step()
+    torch.cuda.synchronize()
+
+
+def test_replay_refuses_a_rebound_gradient_and_changes_nothing():
+    tail = _Tail(2, OptimizerConfig(learning_rate=1e-3))
+    tail.load_grads(0)
+    tail.step()
+    graph = StepGraph(tail.step)
+    graph.replay()
+    torch.cuda.synchronize()
+    p = tail.handles[0].flat_param
+    step_before = float(tail.opts[0].inner.state[p]["step"])
+    kept = p.grad
+    p.grad = kept.clone()
+    with pytest.raises(UnsupportedFeatureError, match="rebound"):
+        graph.replay()
+    assert float(tail.opts[0].inner.state[p]["step"]) == step_before
+    assert float(tail.opts[1].inner.state[tail.handles[1].flat_param]["step"]) == step_before
+    p.grad = kept
+    graph.replay()
+    torch.cuda.synchronize()
+    assert float(tail.opts[0].inner.state[p]["step"]) == step_before + 1

@@ -36,6 +36,8 @@ _HELPERS = {"hbt_last_error", "hbt_abi_version", "hbt_symbol_count", "hbt_copy_c
 # Entry points with no counterpart in the reference: their comment says so and names
 # the callers they serve instead of citing a reference function.
 _NO_COUNTERPART = {"hbt_grad_norm_noalloc"}
+# Plumbing for work recorded into a HIP graph, also with no reference counterpart.
+_GRAPH_PLUMBING = {"hbt_write_words"}
 
 
 def test_every_entry_point_cites_the_reference_interface_it_replaces():
@@ -50,6 +52,8 @@ def test_every_entry_point_cites_the_reference_interface_it_replaces():
         for name in re.findall(r"\b(hbt_[a-z0-9_]+)\s*\(", code):
             if name in _NO_COUNTERPART:
                 cited[name] = "no counterpart in the reference" in comment and "cannot allocate" in comment
+            elif name in _GRAPH_PLUMBING:
+                cited[name] = "no counterpart in the reference" in comment and "HIP graph" in comment
             else:
                 cited[name] = "Replaces:" in comment and re.search(r"[a-z_/]+\.py:\d+", comment) is not None
     compute = _declared_functions() - _HELPERS
@@ -151,6 +155,42 @@ def test_invalid_arguments_are_rejected_before_any_launch():
                                        _native.double_array([1.0]), 1, 0, 1.0, 1.0, None, None, None, None, None)
     assert status == -2
     assert b"static scratch" in lib.hbt_last_error()
+    # slot forms of the steps: a null or misaligned slot, or a bad table, is refused before
+    # any launch; an empty table with a slot launches nothing
+    adam = (1.0, None, 1.0, 0.1, 0.9, 0.1, 1.0, 1e-8, -1e-3)
+    assert lib.hbt_adamw_step_slot(None, None, None, None, None, 0, 0, 0, *adam, None, 0, None) == -1
+    assert b"hbt_adamw_step_slot" in lib.hbt_last_error() and b"16-byte aligned" in lib.hbt_last_error()
+    assert lib.hbt_adamw_step_slot(None, None, None, None, None, 0, 0, 0, *adam, ctypes.c_void_p(4104), 0,
+                                   None) == -1
+    assert lib.hbt_adamw_step_slot(None, None, None, None, None, 99, 0, 0, *adam, fake, 0, None) == -1
+    assert b"hbt_adamw_step_slot: count" in lib.hbt_last_error()
+    assert lib.hbt_adamw_step_slot(None, None, None, None, None, 0, 0, 0, *adam, fake, 0, None) == 0
+    assert lib.hbt_sgd_step_slot(None, None, None, None, 0, 0, 0, 1.0, None, 0.0, 0.0, 1.0, -0.1, None, 0,
+                                 None) == -1
+    assert lib.hbt_sgd_step_slot(None, None, None, None, 0, 0, 0, 1.0, None, 0.0, 0.0, 1.0, -0.1, fake, 2,
+                                 None) == -1  # FIRST_STEP without MOMENTUM
+    assert b"hbt_sgd_step_slot: bad flags" in lib.hbt_last_error()
+    assert lib.hbt_adamw_step_f64_slot(None, None, None, None, None, 0, *adam, None, 0, None) == -1
+    assert lib.hbt_adamw_step_f64_slot(None, None, None, None, None, 0, *adam, fake, 0, None) == 0
+    assert lib.hbt_sgd_step_f64_slot(None, None, None, None, 0, 1.0, None, 0.0, 0.0, 1.0, -0.1, None, 0,
+                                     None) == -1
+    # the writers check the slot, the dtype and the flags before they launch
+    assert lib.hbt_adamw_write_scalars(None, 0, 1.0, 1.0, 0.1, 0.9, 0.1, 1.0, 1e-8, -1e-3, None) == -1
+    assert lib.hbt_adamw_write_scalars(fake, 3, 1.0, 1.0, 0.1, 0.9, 0.1, 1.0, 1e-8, -1e-3, None) == -1
+    assert b"param_dtype 3" in lib.hbt_last_error()
+    assert lib.hbt_adamw_write_scalars_f64(ctypes.c_void_p(4100), 1.0, 1.0, 0.1, 0.9, 0.1, 1.0, 1e-8, -1e-3,
+                                           None) == -1
+    assert lib.hbt_sgd_write_scalars(fake, 0, 1.0, 0.0, 0.0, 1.0, -0.1, 4, None) == -1  # NESTEROV alone
+    assert lib.hbt_sgd_write_scalars(fake, 2, 1.0, 0.0, 0.0, 1.0, -0.1, 64, None) == -1  # unknown flag
+    assert lib.hbt_sgd_write_scalars_f64(None, 1.0, 0.0, 0.0, 1.0, -0.1, 0, None) == -1
+    assert lib.hbt_sgd_write_scalars_f64(fake, 1.0, 0.0, 0.0, 1.0, -0.1, 64, None) == -1
+    words = (ctypes.c_uint32 * 2)(1, 2)
+    assert lib.hbt_write_words(None, words, 2, None) == -1
+    assert lib.hbt_write_words(ctypes.c_void_p(4098), words, 2, None) == -1  # not 4-byte aligned
+    assert b"4-byte aligned" in lib.hbt_last_error()
+    assert lib.hbt_write_words(fake, None, 2, None) == -1
+    assert lib.hbt_write_words(fake, words, -1, None) == -1
+    assert lib.hbt_write_words(None, None, 0, None) == 0  # nothing to write, nothing launched
 
 
 def test_host_tensors_are_refused():
