@@ -639,7 +639,9 @@ class FlatParamHandle:
             out, segments = wide, {}  # the partials were chunked for float32; the norm pass sums anew
         if self._offload_params:
             out = self._to_host(out)  # the partials stay on the device and describe the copy
-        setattr(out, NORM_PARTIALS_ATTR, NormPartials(out.data_ptr(), out._version, segments, out.dtype))
+        # The padding is written as exact zeros, so its partials are +0.0.
+        zero = frozenset({(valid, pad)}) if pad and (valid, pad) in segments else frozenset()
+        setattr(out, NORM_PARTIALS_ATTR, NormPartials(out.data_ptr(), out._version, segments, out.dtype, zero))
         self._reduction_count += 1
         return out
 

@@ -92,6 +92,9 @@ class NormPartials:
     version: int
     segments: dict[tuple[int, int], torch.Tensor]
     dtype: torch.dtype = torch.float32
+    #: Segments the producer wrote as exact zeros (a flat shard's padding), whose
+    #: partials are therefore +0.0: any finite non-negative weight leaves them +0.0.
+    zero: frozenset[tuple[int, int]] = frozenset()
 
     def lookup(self, grad: torch.Tensor, offset: int, length: int) -> torch.Tensor | None:
         """The segment's partials if the record still describes ``grad``."""
@@ -442,11 +445,19 @@ def gradient_norm_pass(
                       grad_mul64=outputs[2:3])
 
 
+def _zero_segment(grad: torch.Tensor, offset: int, length: int) -> bool:
+    """Whether ``grad``'s producer wrote the segment as exact zeros (and the record is valid)."""
+    record = getattr(grad, NORM_PARTIALS_ATTR, None)
+    return record is not None and record.lookup(grad, offset, length) is not None and (offset, length) in record.zero
+
+
 def _contiguous_cached_partials(launches, total_partials: int) -> int | None:
     """The device address of the partials of every segment in ``launches``, when each
-    segment has a producer's partials (:class:`NormPartials`), weight 1 and no pending
-    unscale, and those partials lie one after another in one tensor in slot order, so a
-    finalize over that address sees what the copy into a fresh array would give it."""
+    segment has a producer's partials (:class:`NormPartials`) and no pending unscale,
+    has weight 1 or was written as exact zeros (its +0.0 partials times any finite
+    non-negative weight are the same +0.0), and those partials lie one after another in
+    one tensor in slot order, so a finalize over that address sees what the weighted
+    copy into a fresh array would give it."""
     address = None
     expected = None
     for dtype, unscale, items, _ in launches:
@@ -454,7 +465,7 @@ def _contiguous_cached_partials(launches, total_partials: int) -> int | None:
             return None
         chunk_elems = norm_chunk_elems(dtype)
         for grad, offset, length, weight in items:
-            if weight != 1.0:
+            if weight != 1.0 and not (0.0 <= weight < float("inf") and _zero_segment(grad, offset, length)):
                 return None
             cached = _cached_partials(grad, offset, length, unscale)
             if cached is None or cached.numel() != -(-length // chunk_elems) or not cached.is_contiguous():
