@@ -1438,6 +1438,8 @@ def bench_mlp(steps: int, warmup: int) -> int:
     share of the ranks' padded gradients (the AVG reduce-scatter's arithmetic, with norm
     partials), the clip from those partials and the fused AdamW (lr 1e-3, wd 0.01) on the
     flat shard.  Microseconds per rank-step at this size measure launch cost, not HBM.
+    Each W is timed eagerly and then replayed from one HIP graph recording of all ranks'
+    tails (``StepGraph``).
     """
     import torch
 
