@@ -10,7 +10,8 @@ follow, each against the global vector or torch's own CPU arithmetic, and random
 and SGD runs with the global-norm clip and loss-scaled runs with injected overflows
 against the oracle; offloaded runs against the in-HBM path; weighted norms against a
 brute-force fp64 sum; checkpoints saved and reloaded at random widths through the format
-on disk.
+on disk; and random optimizer steps replayed from a HIP graph recording against the same
+steps taken eagerly.
 """
 
 from __future__ import annotations
@@ -607,3 +608,73 @@ def test_random_tiny_checkpoint_save_and_load(device, tmp_path, monkeypatch, cas
     whose shards are all padding save nothing and load zero optimizer state."""
     monkeypatch.setattr(sys.modules[__name__], "_shapes", _tiny_shapes)
     test_random_checkpoint_save_and_load(device, tmp_path, 5000 + case)
+
+
+@pytest.mark.parametrize("case", range(24))
+def test_random_recorded_steps(device, case):
+    """Random optimizer steps taken eagerly and by replaying a ``StepGraph`` recording of
+    the same ``clip_grad_norm`` + ``step``: up to 40 tensors (launches split at 16, empty
+    ones included), fp32 / bf16 / fp16 / float64 masters, AdamW (both lerp branches) or SGD
+    (plain, momentum, Nesterov, weight decay), every clip placement, new gradients written
+    into the recorded buffers before every step and the learning rate halved after the
+    first replay.  Parameters, gradients, state, step counters and norms must be bitwise
+    equal after every step."""
+    from hybrid_training_amd import OptimizerConfig, ShardedOptimizer, StepGraph
+
+    rng = np.random.default_rng(9000 + case)
+    sizes = [int(rng.choice([0, 1, 7, 256, 1000, 4097])) if rng.random() < 0.3 else int(rng.integers(1, 20000))
+             for _ in range(int(rng.integers(1, 41)))]
+    dtype = [torch.float32, torch.float32, torch.bfloat16, torch.float16, torch.float64][int(rng.integers(0, 5))]
+    name = ["adamw", "sgd"][int(rng.integers(0, 2))]
+    placement = [{}, {"defer_clip": True}, {"clip_in_step": True}][int(rng.integers(0, 3))]
+    lr = float(rng.choice([1e-4, 1e-3, 1e-2]))
+    betas = [(0.9, 0.95), (0.8, 0.999), (0.4, 0.9)][int(rng.integers(0, 3))]
+    wd = float(rng.choice([0.0, 0.01]))
+    momentum = float(rng.choice([0.0, 0.9]))
+    nesterov = momentum != 0 and bool(rng.integers(0, 2))
+    eps = float(rng.choice([1e-4, 1e-3])) if dtype == torch.float16 else 1e-8
+    g_scale = 0.05 if dtype == torch.float16 else 1e-3
+    max_norm = float(rng.choice([1e-3, 0.05, 1.0, 100.0]))
+    config = OptimizerConfig(name=name, learning_rate=lr, betas=betas, weight_decay=wd, eps=eps, momentum=momentum)
+    context = (f"case {case}: {len(sizes)} tensors, {_NAMES[dtype]}, {name}, {placement}, lr {lr}, betas {betas}, "
+               f"wd {wd}, momentum {momentum}, nesterov {nesterov}, clip {max_norm}")
+
+    def build():
+        gen = torch.Generator(device=device).manual_seed(case)
+        params = [torch.nn.Parameter((torch.randn(n, device=device, generator=gen) * 0.02).to(dtype)) for n in sizes]
+        opt = ShardedOptimizer(params, config, norm_group=GroupHandle.trivial(), device=device, **placement)
+        if nesterov:
+            for group in opt.inner.param_groups:
+                group["nesterov"] = True
+        for p in params:
+            p.grad = torch.zeros_like(p)  # the gradient buffers every step writes into
+        return params, opt
+
+    def fill(params, k):
+        gen = torch.Generator(device=device).manual_seed(1000 * case + k)
+        for p in params:
+            p.grad.copy_((torch.randn(p.shape, device=device, generator=gen) * g_scale).to(dtype))
+
+    (pa, oa), (pb, ob) = build(), build()
+    for params, opt in ((pa, oa), (pb, ob)):
+        fill(params, 0)
+        opt.clip_grad_norm(max_norm)
+        opt.step()
+    graph = StepGraph(lambda: (ob.clip_grad_norm(max_norm), ob.step())[0])
+    for k in range(1, 4):
+        if k == 2:
+            oa.set_learning_rate(lr / 2)
+            ob.set_learning_rate(lr / 2)
+        fill(pa, k)
+        fill(pb, k)
+        norm = oa.clip_grad_norm(max_norm)
+        oa.step()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(norm, graph.output), (context, k)
+        for a, b in zip(pa, pb):
+            assert torch.equal(a, b) and torch.equal(a.grad, b.grad), (context, k)
+            sa, sb = oa.inner.state[a], ob.inner.state[b]
+            assert sa.keys() == sb.keys(), context
+            for key in sa:
+                assert torch.equal(sa[key], sb[key]), (context, k, key)
