@@ -783,7 +783,7 @@ class _RecordedAdamW:
         for p, ptr in zip(self._params, self._grad_ptrs):
             _check_recorded_grad(p, ptr)
         states = [opt._optimizer.state[p] for p in self._params]
-        steps = {float(s["step"].item()) + 1.0 for s in states}
+        steps = {float((s["step"] + 1).item()) for s in states}
         found = {_adamw_scalars(groups[id(p)], step) for p in self._params for step in steps}
         if len(found) != 1:
             raise _replay_error("the parameters recorded in one launch no longer share their step scalars")
@@ -1166,7 +1166,7 @@ class ShardedOptimizer:
                 step_t += 1
                 step = float(step_t.item())
             else:
-                step = float(step_t.item()) + 1.0  # the step each replay advances to
+                step = float((step_t + 1).item())  # the step each replay advances to, as step_t += 1 forms it
             key = (_adamw_scalars(group, step), p.dtype, grad.dtype, _pending_unscale(grad))
             batches.setdefault(key, []).append(p)
         stream = _native.stream_of(self._device)

@@ -37,15 +37,18 @@ TOTAL = 1857
 class _Tail:
     """W ranks' FSDP units of one MLP, their optimizers, and full gradients in fixed buffers."""
 
-    def __init__(self, world: int, config: OptimizerConfig, dtype: torch.dtype = torch.float32, **placement):
+    def __init__(self, world: int, config: OptimizerConfig, dtype: torch.dtype = torch.float32,
+                 mp: MixedPrecisionConfig | None = None, **placement):
         torch.manual_seed(0)
         model = nn.Sequential(nn.Linear(23, 32), nn.ReLU(), nn.Linear(32, 32), nn.ReLU(), nn.Linear(32, 1))
         named = list(model.to(DEV, dtype).named_parameters())
+        mp = mp or MixedPrecisionConfig(enabled=False)
         self.handles = [FlatParamHandle(named, None, GroupHandle.local_view("shard", world, r), FSDPConfig(),
-                                        MixedPrecisionConfig(enabled=False), DEV, keep_originals=True)
+                                        mp, DEV, keep_originals=True)
                         for r in range(world)]
         padded = self.handles[0].padded_numel
-        self.grads = [torch.zeros(padded, device=DEV, dtype=dtype) for _ in range(world)]
+        grad_dtype = getattr(torch, mp.param_dtype) if mp.enabled else dtype
+        self.grads = [torch.zeros(padded, device=DEV, dtype=grad_dtype) for _ in range(world)]
         self.opts = [ShardedOptimizer([h.flat_param], config, norm_group=GroupHandle.local_view("world", world, r),
                                       device=DEV, **placement) for r, h in enumerate(self.handles)]
 
@@ -163,3 +166,33 @@ def test_replay_refuses_a_rebound_gradient_and_changes_nothing():
     graph.replay()
     torch.cuda.synchronize()
     assert float(tail.opts[0].inner.state[p]["step"]) == step_before + 1
+
+
+@pytest.mark.parametrize("world", [2, 4])
+def test_recorded_fsdp_step_with_the_parameter_gather(world):
+    """The gather of every rank's fp32 master shard into the bf16 compute buffer (a cast
+    copy of W records, whose interval table the recording writes into the graph) recorded
+    with the tail: each replay's gathered buffers, shards and state bitwise the eager
+    step's."""
+    mp = MixedPrecisionConfig(enabled=True, param_dtype="bfloat16", reduce_dtype="float32", master_dtype="float32")
+    config = OptimizerConfig(learning_rate=1e-3, weight_decay=0.01)
+    eager, graphed = _Tail(world, config, mp=mp), _Tail(world, config, mp=mp)
+
+    def step(tail: _Tail):
+        shards = [h.flat_param for h in tail.handles]
+        fulls = [h.gather_full(peer_shards=shards) for h in tail.handles]
+        return fulls, tail.step()
+
+    for tail in (eager, graphed):
+        tail.load_grads(0)
+        step(tail)
+    graph = StepGraph(lambda: step(graphed))
+    for k in range(1, 5):
+        for tail in (eager, graphed):
+            tail.load_grads(k)
+        fulls, norms = step(eager)
+        graph.replay()
+        torch.cuda.synchronize()
+        for fe, fg in zip(fulls, graph.output[0]):
+            assert torch.equal(fe, fg), (k, "gathered")
+        _assert_same(eager, graphed, norms, graph.output[1], k)
