@@ -221,6 +221,21 @@ inline int64_t adam_tile_of(int32_t param_dtype, bool write_back) {
     if (param_dtype == F32) return write_back ? adam_tile<F32, true>() : adam_tile<F32, false>();
     return write_back ? adam_tile<BF16, true>() : adam_tile<BF16, false>();
 }
+// The AdamW kernel's shape: the one above for fp32 masters, whose update is bound by HBM.
+// For 2-byte masters the rounding after every op makes the update VALU-bound, and a
+// half-wave workgroup leaves half of every VALU instruction idle: full 64-lane waves with
+// one vector per lane (512 elements, 1 KB per stream per workgroup; 46 VGPRs for bf16).
+template <int PD>
+constexpr int adamw_block() { return PD == F32 ? kAdamBlock : 64; }
+template <int PD, bool kWriteBack>
+constexpr int adamw_unroll() { return PD == F32 ? adam_unroll<kWriteBack>() : 1; }
+template <int PD, bool kWriteBack>
+constexpr int64_t adamw_tile() { return int64_t(adamw_block<PD>()) * adam_vec<PD>() * adamw_unroll<PD, kWriteBack>(); }
+inline int64_t adamw_tile_of(int32_t param_dtype, bool write_back) {
+    if (param_dtype == F32) return write_back ? adamw_tile<F32, true>() : adamw_tile<F32, false>();
+    return write_back ? adamw_tile<BF16, true>() : adamw_tile<BF16, false>();
+}
+inline int adamw_block_of(int32_t param_dtype) { return param_dtype == F32 ? adamw_block<F32>() : adamw_block<BF16>(); }
 
 struct AdamTable {
     void* p[kMaxT];
@@ -276,14 +291,15 @@ __device__ __forceinline__ void adamw_update(float& p, float g, float& m, float&
 // g whenever a multiply changed it: the clip multiplier differs from 1 (the reference
 // multiplies only when its coefficient is below 1) or an unscale factor is pending.
 template <int PD, int GD, bool kLerpSmall, bool kUnscale, bool kWriteBack>
-__global__ __launch_bounds__(kAdamBlock) void adamw_kernel(AdamTable tab, AdamScalars s,
+__global__ __launch_bounds__(adamw_block<PD>()) void adamw_kernel(AdamTable tab, AdamScalars s,
                                                            const AdamScalars* __restrict__ slot,
                                                            const float* __restrict__ grad_mul,
                                                            int64_t block_base) {
     if (slot != nullptr) s = *slot;
     constexpr int K = adam_vec<PD>();
-    constexpr int kUnroll = adam_unroll<kWriteBack>();
-    constexpr int64_t kTile = adam_tile<PD, kWriteBack>();
+    constexpr int kBlock = adamw_block<PD>();
+    constexpr int kUnroll = adamw_unroll<PD, kWriteBack>();
+    constexpr int64_t kTile = adamw_tile<PD, kWriteBack>();
     const int64_t block = block_base + blockIdx.x;
     const int t = owning_tensor(tab.first_block, tab.count, block);
     const int64_t base = (block - tab.first_block[t]) * kTile;
@@ -303,7 +319,7 @@ __global__ __launch_bounds__(kAdamBlock) void adamw_kernel(AdamTable tab, AdamSc
         // streams in pairs; the gradient stored first or last among the stores).
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
-            const int64_t e = base + (int64_t(u) * kAdamBlock + threadIdx.x) * K;
+            const int64_t e = base + (int64_t(u) * kBlock + threadIdx.x) * K;
             load_vec<GD, K>(G, e, gv[u]);
             wait_vmem();
             if (write_g) {
@@ -327,14 +343,14 @@ __global__ __launch_bounds__(kAdamBlock) void adamw_kernel(AdamTable tab, AdamSc
         }
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
-            const int64_t e = base + (int64_t(u) * kAdamBlock + threadIdx.x) * K;
+            const int64_t e = base + (int64_t(u) * kBlock + threadIdx.x) * K;
             store_vec<PD, K>(M, e, mv[u]);
             store_vec<PD, K>(V, e, vv[u]);
             store_vec<PD, K>(P, e, pv[u]);
         }
     } else {
         const int64_t end = base + kTile < n ? base + kTile : n;
-        for (int64_t e = base + threadIdx.x; e < end; e += kAdamBlock) {
+        for (int64_t e = base + threadIdx.x; e < end; e += kBlock) {
             float p = load_one<PD>(P, e), m = load_one<PD>(M, e), v = load_one<PD>(V, e);
             const float g = scaled_grad<GD, kUnscale>(load_one<GD>(G, e), s.unscale, gmul);
             adamw_update<PD, kLerpSmall>(p, g, m, v, s);
@@ -1984,7 +2000,7 @@ static int32_t adamw_step_impl(const char* who, void* const* params, void* const
     AdamTable tab{};
     tab.count = count;
     const bool write_back = (flags & HBT_STEP_WRITE_GRAD) != 0;
-    const int64_t tile = adam_tile_of(param_dtype, write_back);
+    const int64_t tile = adamw_tile_of(param_dtype, write_back);
     const int vec = param_dtype == F32 ? adam_vec<F32>() : adam_vec<BF16>();
     const uintptr_t state_align = static_cast<uintptr_t>(vec * dtype_size(param_dtype));
     const uintptr_t grad_align = static_cast<uintptr_t>(vec * dtype_size(grad_dtype));
@@ -2017,9 +2033,9 @@ static int32_t adamw_step_impl(const char* who, void* const* params, void* const
     const bool lerp_small = std::fabs(lerp_weight) < 0.5f;
     const bool scaled = unscale != 1.0f;
     hipStream_t st = as_stream(stream);
-    return launch_sliced(who, blocks, kAdamBlock, [&](int64_t first, dim3 grid) {
+    return launch_sliced(who, blocks, adamw_block_of(param_dtype), [&](int64_t first, dim3 grid) {
 #define HBT_ADAMW(PD, GD, SMALL, SCALED, WB) \
-    adamw_kernel<PD, GD, SMALL, SCALED, WB><<<grid, kAdamBlock, 0, st>>>(tab, s, slot, grad_mul, first)
+    adamw_kernel<PD, GD, SMALL, SCALED, WB><<<grid, adamw_block<PD>(), 0, st>>>(tab, s, slot, grad_mul, first)
 #define HBT_ADAMW_WB(PD, GD, SMALL, SCALED)                     \
     do {                                                        \
         if (write_back) HBT_ADAMW(PD, GD, SMALL, SCALED, true); \
