@@ -17,6 +17,8 @@ import torch
 import torch.nn as nn
 
 from hybrid_training_amd import (
+    BucketedGradients,
+    DDPConfig,
     FlatParamHandle,
     FSDPConfig,
     GroupHandle,
@@ -196,3 +198,125 @@ def test_recorded_fsdp_step_with_the_parameter_gather(world):
         for fe, fg in zip(fulls, graph.output[0]):
             assert torch.equal(fe, fg), (k, "gathered")
         _assert_same(eager, graphed, norms, graph.output[1], k)
+
+
+class _DdpTail:
+    """One data-parallel replica: the MLP's parameters in several gradient buckets
+    (gradient-as-bucket-view after the first synchronize) and one AdamW over them."""
+
+    def __init__(self, world: int):
+        torch.manual_seed(0)
+        model = nn.Sequential(nn.Linear(23, 32), nn.ReLU(), nn.Linear(32, 32), nn.ReLU(), nn.Linear(32, 1))
+        named = list(model.to(DEV).named_parameters())
+        self.params = [p for _, p in named]
+        group = GroupHandle.local_view("data_parallel", world, 0) if world > 1 else GroupHandle.trivial()
+        # a 2 KiB cap puts the 1,857 parameters in several buckets
+        self.ddp = BucketedGradients(named, group, DDPConfig(bucket_cap_mb=2.0 / 1024))
+        self.opt = ShardedOptimizer(self.params, OptimizerConfig(learning_rate=1e-3, weight_decay=0.01),
+                                    norm_group=GroupHandle.trivial(), device=DEV)
+
+    def load_grads(self, k: int) -> None:
+        """New gradients in place, as a backward pass accumulating into zeroed
+        gradients writes them (into the bucket views once they are bound)."""
+        gen = torch.Generator(device=DEV).manual_seed(200 + k)
+        for p in self.params:
+            g = torch.randn(p.shape, device=DEV, generator=gen)
+            if p.grad is None:
+                p.grad = g
+            else:
+                p.grad.copy_(g)
+
+    def step(self) -> torch.Tensor:
+        self.ddp.synchronize()
+        norm = self.opt.clip_grad_norm(1.0)
+        self.opt.step()
+        return norm
+
+
+@pytest.mark.parametrize("world", [1, 2, 3])
+def test_recorded_ddp_step_replays_the_eager_steps(world):
+    """The data-parallel tail recorded: the bucket pack with its AVG divide by the group
+    size (in place, the gradients being bucket views), the clip over every bucket view
+    and AdamW; each replay bitwise the eager step, buckets included."""
+    eager, graphed = _DdpTail(world), _DdpTail(world)
+    assert len(graphed.ddp._buckets) > 2
+    for tail in (eager, graphed):
+        tail.load_grads(0)
+        tail.step()  # packs the separate gradients, binds the views, creates the state
+    graph = StepGraph(graphed.step)
+    assert graph.recorded_steps == 1  # one launch group: every parameter shares its scalars
+    for k in range(1, 6):
+        if k == 3:
+            for tail in (eager, graphed):
+                tail.opt.set_learning_rate(4e-4)
+        for tail in (eager, graphed):
+            tail.load_grads(k)
+        norm = eager.step()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(norm, graph.output), (k, "norm")
+        for be, bg in zip(eager.ddp._buckets, graphed.ddp._buckets):
+            assert torch.equal(be.buffer, bg.buffer), (k, "bucket")
+        for pe, pg in zip(eager.params, graphed.params):
+            assert torch.equal(pe, pg), (k, "param")
+            se, sg = eager.opt.inner.state[pe], graphed.opt.inner.state[pg]
+            for key in se:
+                assert torch.equal(se[key], sg[key]), (k, key)
+
+
+def test_recorded_training_step_with_forward_and_backward():
+    """A whole data-parallel training step in one graph: torch's forward and backward
+    (accumulating into the bound bucket views), the pack with its AVG divide, the clip
+    and AdamW.  Between replays the program writes the next batch into the static
+    input.  torch's matrix products may pick other kernels under capture than eagerly,
+    so the comparison with the eager steps allows 1e-5 relative; the bucket pack and
+    the optimizer alone replay bitwise (the tests above)."""
+    eager, graphed = _ModelTail(), _ModelTail()
+    x = torch.empty(64, 23, device=DEV)
+    y = torch.empty(64, 1, device=DEV)
+
+    def load_batch(k: int) -> None:
+        gen = torch.Generator(device=DEV).manual_seed(300 + k)
+        x.copy_(torch.randn(x.shape, device=DEV, generator=gen))
+        y.copy_(torch.randn(y.shape, device=DEV, generator=gen))
+
+    def step(tail: "_ModelTail") -> torch.Tensor:
+        tail.opt.zero_grad(set_to_none=False)
+        loss = nn.functional.mse_loss(tail.model(x), y)
+        loss.backward()
+        tail.ddp.synchronize()
+        tail.opt.clip_grad_norm(1.0)
+        tail.opt.step()
+        return loss.detach()
+
+    for tail in (eager, graphed):
+        load_batch(0)
+        for p in tail.model.parameters():
+            p.grad = torch.zeros_like(p)
+        step(tail)  # binds the bucket views and creates the optimizer state
+    graph = StepGraph(lambda: step(graphed))
+    start = [p.detach().clone() for p in graphed.model.parameters()]
+    for k in range(1, 6):
+        load_batch(k)
+        loss = step(eager)
+        graph.replay()
+        torch.cuda.synchronize()
+        torch.testing.assert_close(graph.output, loss, rtol=1e-5, atol=1e-7)
+        for pe, pg in zip(eager.model.parameters(), graphed.model.parameters()):
+            torch.testing.assert_close(pg, pe, rtol=1e-5, atol=1e-7)
+            torch.testing.assert_close(pg.grad, pe.grad, rtol=1e-5, atol=1e-7)
+    assert all(not torch.equal(s, p) for s, p in zip(start, graphed.model.parameters()))
+
+
+class _ModelTail:
+    """The MLP's parameters in 2 KiB gradient buckets (AVG over 2 replicas) with AdamW."""
+
+    def __init__(self):
+        torch.manual_seed(0)
+        self.model = nn.Sequential(nn.Linear(23, 32), nn.ReLU(), nn.Linear(32, 32), nn.ReLU(),
+                                   nn.Linear(32, 1)).to(DEV)
+        named = list(self.model.named_parameters())
+        self.ddp = BucketedGradients(named, GroupHandle.local_view("data_parallel", 2, 0),
+                                     DDPConfig(bucket_cap_mb=2.0 / 1024))
+        self.opt = ShardedOptimizer([p for _, p in named], OptimizerConfig(learning_rate=1e-3, weight_decay=0.01),
+                                    norm_group=GroupHandle.trivial(), device=DEV)
