@@ -1625,21 +1625,27 @@ SgdScalarsF64 sgd_scalars_f64(double unscale, double weight_decay, double moment
 }
 
 // ---- small host-built data into device memory --------------------------------------------
-// One wave stores up to kWordsPerWrite 32-bit words that arrive in the launch's
-// arguments: lane i stores word i (one vector store instruction).  A recorded launch keeps
-// its arguments, so a graph replays the write with the words it was given.
-constexpr int kWordsPerWrite = 64;
+// One launch stores up to kWordsPerWrite 32-bit words that arrive in its arguments, one
+// wave per kWordsPerBlock of them: lane i of block b stores word 64b + i (one vector store
+// instruction).  A recorded launch keeps its arguments, so a graph replays the write with
+// the words it was given.
+constexpr int kWordsPerWrite = 256;
+constexpr int kWordsPerBlock = 64;
 struct WordBlock {
     uint32_t w[kWordsPerWrite];
 };
 
-__global__ __launch_bounds__(kWordsPerWrite) void write_words_kernel(uint32_t* __restrict__ dst, WordBlock words,
+__global__ __launch_bounds__(kWordsPerBlock) void write_words_kernel(uint32_t* __restrict__ dst, WordBlock words,
                                                                       int32_t count) {
     const int lane = threadIdx.x;
+    // The block's words are read at wave-uniform offsets (scalar loads of the arguments);
+    // each lane keeps its own by selection, never by a per-lane argument index.  The grid
+    // has ceil(count / 64) <= 4 blocks, so base + k stays inside the block of words.
+    const int base = static_cast<int>(blockIdx.x) * kWordsPerBlock;
     uint32_t word = 0u;
 #pragma unroll
-    for (int k = 0; k < kWordsPerWrite; ++k) word = lane == k ? words.w[k] : word;  // no indexed argument reads
-    if (lane < count) dst[lane] = word;
+    for (int k = 0; k < kWordsPerBlock; ++k) word = lane == k ? words.w[base + k] : word;
+    if (base + lane < count) dst[base + lane] = word;
 }
 
 int32_t write_words(const char* who, void* dst, const uint32_t* words, int64_t count, hipStream_t st) {
@@ -1655,7 +1661,9 @@ int32_t write_words(const char* who, void* dst, const uint32_t* words, int64_t c
         const int32_t n = static_cast<int32_t>(count - first < kWordsPerWrite ? count - first : kWordsPerWrite);
         WordBlock block{};
         std::memcpy(block.w, words + first, sizeof(uint32_t) * static_cast<size_t>(n));
-        write_words_kernel<<<dim3(1), dim3(kWordsPerWrite), 0, st>>>(static_cast<uint32_t*>(dst) + first, block, n);
+        const unsigned blocks = static_cast<unsigned>((n + kWordsPerBlock - 1) / kWordsPerBlock);
+        write_words_kernel<<<dim3(blocks), dim3(kWordsPerBlock), 0, st>>>(static_cast<uint32_t*>(dst) + first, block,
+                                                                          n);
         const int32_t status = check_launch(who);
         if (status != HBT_OK) return status;
     }
@@ -1673,6 +1681,20 @@ int32_t write_slot(const char* who, void* slot, const Record& record, hipStream_
     uint32_t words[sizeof(Record) / 4];
     std::memcpy(words, &record, sizeof(Record));
     return write_words(who, slot, words, static_cast<int64_t>(sizeof(Record) / 4), st);
+}
+
+// A scalar record formatted into HBT_STEP_SLOT_BYTES of host memory, zero past its end,
+// for a caller that writes several slots at once.
+template <typename Record>
+int32_t format_slot(const char* who, void* record, const Record& value) {
+    static_assert(sizeof(Record) <= HBT_STEP_SLOT_BYTES, "a record fills part of a slot");
+    if (record == nullptr) {
+        set_error("%s: the record buffer is null", who);
+        return HBT_ERR_INVALID_ARGUMENT;
+    }
+    std::memset(record, 0, HBT_STEP_SLOT_BYTES);
+    std::memcpy(record, &value, sizeof(Record));
+    return HBT_OK;
 }
 
 // The SGD flags a step or a scalar record accepts.
@@ -2714,6 +2736,48 @@ int32_t hbt_sgd_write_scalars_f64(void* slot, double unscale, double weight_deca
     return write_slot("hbt_sgd_write_scalars_f64", slot,
                       sgd_scalars_f64(unscale, weight_decay, momentum, one_minus_dampening, neg_lr, flags),
                       as_stream(stream));
+}
+
+int32_t hbt_adamw_scalar_record(void* record, int32_t param_dtype, float unscale, float decay, float lerp_weight,
+                                float beta2, float one_minus_beta2, float bias_correction2_sqrt, float eps,
+                                float neg_step_size) {
+    clear_error();
+    if (param_dtype != F32 && param_dtype != BF16 && param_dtype != F16) {
+        set_error("hbt_adamw_scalar_record: param_dtype %d is not F32, BF16 or F16", param_dtype);
+        return HBT_ERR_INVALID_ARGUMENT;
+    }
+    return format_slot("hbt_adamw_scalar_record", record,
+                       adam_scalars(param_dtype, unscale, decay, lerp_weight, beta2, one_minus_beta2,
+                                    bias_correction2_sqrt, eps, neg_step_size));
+}
+
+int32_t hbt_sgd_scalar_record(void* record, int32_t param_dtype, float unscale, float weight_decay, float momentum,
+                              float one_minus_dampening, float neg_lr, int32_t flags) {
+    clear_error();
+    if (param_dtype != F32 && param_dtype != BF16 && param_dtype != F16) {
+        set_error("hbt_sgd_scalar_record: param_dtype %d is not F32, BF16 or F16", param_dtype);
+        return HBT_ERR_INVALID_ARGUMENT;
+    }
+    if (!sgd_flags_ok("hbt_sgd_scalar_record", flags)) return HBT_ERR_INVALID_ARGUMENT;
+    return format_slot("hbt_sgd_scalar_record", record,
+                       sgd_scalars(param_dtype, unscale, weight_decay, momentum, one_minus_dampening, neg_lr, flags));
+}
+
+int32_t hbt_adamw_scalar_record_f64(void* record, double unscale, double decay, double lerp_weight, double beta2,
+                                    double one_minus_beta2, double bias_correction2_sqrt, double eps,
+                                    double neg_step_size) {
+    clear_error();
+    return format_slot("hbt_adamw_scalar_record_f64", record,
+                       adam_scalars_f64(unscale, decay, lerp_weight, beta2, one_minus_beta2, bias_correction2_sqrt,
+                                        eps, neg_step_size));
+}
+
+int32_t hbt_sgd_scalar_record_f64(void* record, double unscale, double weight_decay, double momentum,
+                                  double one_minus_dampening, double neg_lr, int32_t flags) {
+    clear_error();
+    if (!sgd_flags_ok("hbt_sgd_scalar_record_f64", flags)) return HBT_ERR_INVALID_ARGUMENT;
+    return format_slot("hbt_sgd_scalar_record_f64", record,
+                       sgd_scalars_f64(unscale, weight_decay, momentum, one_minus_dampening, neg_lr, flags));
 }
 
 int32_t hbt_write_words(void* dst, const uint32_t* words, int64_t count, void* stream) {

@@ -56,10 +56,10 @@ extern "C" {
 const char* hbt_last_error(void) { return hbt::g_last_error.c_str(); }
 
 // Bumped whenever an exported signature or a table layout changes.
-int32_t hbt_abi_version(void) { return 17; }
+int32_t hbt_abi_version(void) { return 18; }
 
 // Entry points declared in include/hbt.h (hbt_last_error .. hbt_scale_inplace_f64).
-int32_t hbt_symbol_count(void) { return 30; }
+int32_t hbt_symbol_count(void) { return 34; }
 
 int64_t hbt_grid_slices(int64_t blocks, int32_t threads, int64_t* first, int64_t* count, int64_t capacity) {
     if (threads <= 0) return -1;

@@ -14,6 +14,7 @@ with the caller's other work on that stream.
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
 import threading
@@ -63,7 +64,7 @@ __all__ = [
     "stream_of",
 ]
 
-ABI_VERSION = 17
+ABI_VERSION = 18
 MAX_TENSORS_PER_LAUNCH = 16
 MAX_LOCAL_RANKS = 64
 #: Doubles of working storage hbt_scale_inplace_sqnorm takes per partial for 2-byte gradients.
@@ -240,6 +241,16 @@ EXPORTED_SYMBOLS: dict[str, tuple[object, tuple[object, ...]]] = {
         _c_i32,
         (_c_void_p, _c_f64, _c_f64, _c_f64, _c_f64, _c_f64, _c_i32, _c_void_p),
     ),
+    "hbt_adamw_scalar_record": (
+        _c_i32,
+        (_c_void_p, _c_i32, _c_f32, _c_f32, _c_f32, _c_f32, _c_f32, _c_f32, _c_f32, _c_f32),
+    ),
+    "hbt_sgd_scalar_record": (_c_i32, (_c_void_p, _c_i32, _c_f32, _c_f32, _c_f32, _c_f32, _c_f32, _c_i32)),
+    "hbt_adamw_scalar_record_f64": (
+        _c_i32,
+        (_c_void_p, _c_f64, _c_f64, _c_f64, _c_f64, _c_f64, _c_f64, _c_f64, _c_f64),
+    ),
+    "hbt_sgd_scalar_record_f64": (_c_i32, (_c_void_p, _c_f64, _c_f64, _c_f64, _c_f64, _c_f64, _c_i32)),
     "hbt_write_words": (_c_i32, (_c_void_p, ctypes.POINTER(ctypes.c_uint32), _c_i64, _c_void_p)),
 }
 
@@ -266,7 +277,10 @@ class GraphRecording:
     The step-scalar slots come from one slab allocated before the capture starts, not
     from the graph's private pool: the host writes a slot before each replay and the
     replay reads it, while a block of the private pool may also belong to a temporary
-    that an earlier recorded launch writes during the same replay.
+    that an earlier recorded launch writes during the same replay.  Each slot has a
+    host record of the same size (:meth:`record_address`): before a replay every
+    recorded step formats its scalars into its record, and :meth:`write_slots` copies
+    all of them into the slab with one launch per 256 words.
     """
 
     #: Step-scalar slots one recording can hand out.
@@ -275,8 +289,24 @@ class GraphRecording:
     def __init__(self, device: torch.device) -> None:
         self.steps: list[Any] = []
         self.tables: list[torch.Tensor] = []
+        self._device = device
         self._slab = torch.zeros(self.MAX_SLOTS * STEP_SLOT_BYTES // 8, dtype=torch.float64, device=device)
+        self._records = (ctypes.c_uint32 * (self.MAX_SLOTS * STEP_SLOT_BYTES // 4))()
         self._used = 0
+
+    def record_address(self, slot: torch.Tensor) -> int:
+        """Host address of the record that :meth:`write_slots` copies into ``slot``."""
+        offset = slot.data_ptr() - self._slab.data_ptr()
+        if not 0 <= offset < self._used * STEP_SLOT_BYTES or offset % STEP_SLOT_BYTES:
+            raise ValueError("not a slot of this recording")
+        return ctypes.addressof(self._records) + offset
+
+    def write_slots(self) -> None:
+        """Copy every handed-out slot's host record into the slab, on the current stream."""
+        if self._used:
+            check(library().hbt_write_words(self._slab.data_ptr(), self._records, self._used * STEP_SLOT_BYTES // 4,
+                                            stream_of(self._device)),
+                  "native.GraphRecording.write_slots")
 
     def new_slot(self) -> torch.Tensor:
         """``STEP_SLOT_BYTES`` of device memory outside the graph's pool."""
@@ -303,7 +333,9 @@ def graph_recording() -> GraphRecording | None:
             step would replay the scalars and tables of its recording forever.
     """
     recording = _RECORDING.get()
-    if recording is None and torch.cuda.is_available() and torch.cuda.is_current_stream_capturing():
+    # No capture can be in progress before torch has initialised the device; the raw
+    # query skips torch.cuda.is_available(), which reads the environment on every call.
+    if recording is None and torch.cuda.is_initialized() and _IS_CAPTURING is not None and _IS_CAPTURING():
         raise UnsupportedFeatureError(
             format_error("native.graph_recording",
                          "this work is being captured into a HIP graph outside hybrid_training_amd.StepGraph, "
@@ -468,6 +500,18 @@ def require_dense(tensor: torch.Tensor, operation: str) -> None:
 
 
 _RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+_IS_CAPTURING = getattr(torch._C, "_cuda_isCurrentStreamCapturing", None)
+_NO_GUARD = contextlib.nullcontext()
+
+
+def device_guard(device: torch.device):
+    """``torch.cuda.device(device)``, or a context that does nothing when ``device`` is
+    already the current one (the usual case: a guard costs about a microsecond of host
+    time, and every launch's host path takes one)."""
+    if isinstance(device, torch.device) and device.type == "cuda" and (
+            device.index is None or device.index == torch.cuda.current_device()):
+        return _NO_GUARD
+    return torch.cuda.device(device)
 
 
 def stream_of(device: torch.device) -> int:
@@ -702,7 +746,7 @@ class CopyPlan:
             scale = 2
         lib = library()
         table, first, aligned, hinted = _prepared_plan(self.device, tuple(self._rows), src_code, dst_code, scale)
-        with torch.cuda.device(self.device):
+        with device_guard(self.device):
             status = lib.hbt_copy_intervals(
                 table.data_ptr(),
                 len(self._rows),

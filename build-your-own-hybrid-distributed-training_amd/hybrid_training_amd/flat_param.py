@@ -63,6 +63,10 @@ __all__ = [
     "reshard_state_dict_pieces",
 ]
 
+#: Tile sums (doubles, one per 256 shard elements) up to which the local share keeps them
+#: in the norm partials' allocation: shards of up to 2 Mi elements.
+_SHARED_TILE_SUMS = 8192
+
 
 @dataclass(frozen=True)
 class ShardedTensorPiece:
@@ -606,14 +610,23 @@ class FlatParamHandle:
         chunk = norm_chunk_elems(out_dtype)  # elements per norm partial
         valid_chunks = -(-valid // chunk)
         pad = self._shard_numel - valid
-        partials = torch.empty(max(1, valid_chunks + -(-pad // chunk)), dtype=torch.float64, device=self._device)
-        tile_sums = torch.empty(max(1, -(-self._shard_numel // 256)), dtype=torch.float64, device=self._device)
+        n_partials = max(1, valid_chunks + -(-pad // chunk))
+        n_tiles = max(1, -(-self._shard_numel // 256))
+        if n_tiles <= _SHARED_TILE_SUMS:
+            # A small shard's launch is bound by host time: the partials and the kernel's
+            # tile sums share one allocation (a large shard's tile sums are freed at once).
+            partials = torch.empty(n_partials + n_tiles, dtype=torch.float64, device=self._device)
+            tile_sums_ptr = partials.data_ptr() + 8 * n_partials
+        else:
+            partials = torch.empty(n_partials, dtype=torch.float64, device=self._device)
+            tile_sums = torch.empty(n_tiles, dtype=torch.float64, device=self._device)
+            tile_sums_ptr = tile_sums.data_ptr()
         lib = _native.library()
         args = (group, source_rank, self._shard_numel, valid, _native.dtype_code(grads[0].dtype),
                 _native.dtype_code(self._reduce_dtype), divisor, _native.dtype_code(out_dtype),
-                out.data_ptr(), partials.data_ptr(), tile_sums.data_ptr(), _native.stream_of(self._device))
+                out.data_ptr(), partials.data_ptr(), tile_sums_ptr, _native.stream_of(self._device))
         grad_ptrs = _native.pointer_array([g.data_ptr() for g in grads])
-        with torch.cuda.device(self._device):
+        with _native.device_guard(self._device):
             if rows is None:
                 status = lib.hbt_grad_local_share_sqnorm(grad_ptrs, *args)
                 what = "fsdp.hbt_grad_local_share_sqnorm"
@@ -630,7 +643,7 @@ class FlatParamHandle:
         if valid:
             segments[(0, valid)] = partials[:valid_chunks]
         if pad:
-            segments[(valid, pad)] = partials[valid_chunks:]
+            segments[(valid, pad)] = partials[valid_chunks:n_partials]
         if widen:
             wide = torch.empty(self._shard_numel, dtype=torch.float64, device=self._device)
             plan = _native.CopyPlan(self._device)
@@ -662,7 +675,7 @@ class FlatParamHandle:
         lib = _native.library()
         step = _native.MAX_TENSORS_PER_LAUNCH
         offset_bytes = start * grads[0].element_size()
-        with torch.cuda.device(self._device):
+        with _native.device_guard(self._device):
             for first in range(0, len(grads), step):
                 rows = range(first, min(first + step, len(grads)))
                 status = lib.hbt_grad_accumulate(

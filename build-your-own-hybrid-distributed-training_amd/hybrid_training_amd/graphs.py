@@ -11,9 +11,10 @@ A replay changes what the eager step would change and nothing else.  The optimiz
 kernels of a recorded step read their scalars from small device slots
 (``hbt_*_step_slot``), since AdamW's bias corrections move every step and every
 scalar follows the learning rate.  Before each replay, :meth:`StepGraph.replay`
-advances each recorded optimizer's step counters and rewrites its slots from the host
-state (``hbt_*_write_scalars``, formed as the eager step forms them), so a replay is
-bitwise the eager step.  Copy tables that recorded launches read are written by the
+formats every recorded step's scalars from the host state (``hbt_*_scalar_record``,
+formed as the eager step forms them), writes all of the slots with one launch
+(``hbt_write_words``) and advances the step counters, so a replay is bitwise the eager
+step.  Copy tables that recorded launches read are written by the
 graph itself (``hbt_write_words``) and live as long as it does.
 
 Rules, checked where they can be:
@@ -94,8 +95,9 @@ class StepGraph:
         """Advance every recorded optimizer by one step and run the recorded launches,
         on torch's current stream.  Every recorded step is checked before any is
         advanced, so a refused replay changes nothing."""
-        with torch.cuda.device(self._device):
+        with _native.device_guard(self._device):
             commits = [recorded.prepare() for recorded in self._steps]
+            self._recording.write_slots()  # every step's new scalars, in one launch per 8 slots
             for commit in commits:
                 commit()
             self._graph.replay()

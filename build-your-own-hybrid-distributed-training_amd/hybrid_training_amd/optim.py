@@ -43,8 +43,10 @@ from __future__ import annotations
 
 from collections.abc import Callable, Iterable, Sequence
 from dataclasses import dataclass, field
+from functools import cached_property
 from typing import Any
 
+import numpy as np
 import torch
 import torch.nn as nn
 from torch.autograd.graph import increment_version
@@ -279,24 +281,42 @@ def build_gradient_norm_contributions(
     return contributions
 
 
-@dataclass
 class NormResult:
-    """Device outputs of one norm pass (all 0-dim or 1-element device tensors)."""
+    """Device outputs of one norm pass, in one allocation of four doubles: the weighted
+    squared sum, the norm, the double clip multiplier (for float64 gradients), then the
+    fp32 clip multiplier (for fp32, bf16 and fp16 gradients) and the int32 non-finite
+    flag in the last 8 bytes.  Each field is a 0-dim or 1-element view built on first
+    use: a view costs about a microsecond of host time, and a step needs only the
+    multiplier's address."""
 
-    sum: torch.Tensor
-    norm: torch.Tensor
-    grad_mul: torch.Tensor  # fp32 clip multiplier, for fp32, bf16 and fp16 gradients
-    nonfinite: torch.Tensor
-    grad_mul64: torch.Tensor | None = None  # the double one, for float64 gradients
+    def __init__(self, scalars: torch.Tensor) -> None:
+        self.scalars = scalars
+
+    @cached_property
+    def sum(self) -> torch.Tensor:
+        return self.scalars[0]
+
+    @cached_property
+    def norm(self) -> torch.Tensor:
+        return self.scalars[1]
+
+    @cached_property
+    def grad_mul64(self) -> torch.Tensor:
+        return self.scalars[2:3]
+
+    @cached_property
+    def grad_mul(self) -> torch.Tensor:
+        return self.scalars[3:].view(torch.float32)[:1]
+
+    @cached_property
+    def nonfinite(self) -> torch.Tensor:
+        return self.scalars[3:].view(torch.int32)[1:]
 
     def multiplier_ptr(self, dtype: torch.dtype) -> int:
         """Device address of the clip multiplier a gradient of ``dtype`` is scaled by: the
         double coefficient for float64 gradients, its fp32 rounding for the others (as
         torch hands a Python-double scalar to kernels of each dtype)."""
-        if dtype == torch.float64:
-            assert self.grad_mul64 is not None
-            return self.grad_mul64.data_ptr()
-        return self.grad_mul.data_ptr()
+        return self.scalars.data_ptr() + (16 if dtype == torch.float64 else 24)
 
 
 def _mul_ptr(result: NormResult | None, dtype: torch.dtype) -> int | None:
@@ -368,24 +388,20 @@ def gradient_norm_pass(
     # sum, norm and the double clip multiplier, then the fp32 multiplier and the flag in
     # the last 8 bytes: one allocation for the finalize's outputs.
     scalars = torch.empty(4, dtype=torch.float64, device=device)
-    outputs = scalars[:3]
-    grad_mul = scalars[3:].view(torch.float32)[:1]
-    nonfinite = scalars[3:].view(torch.int32)[1:]
+    out = scalars.data_ptr()
     stream = _native.stream_of(device)
     whole = _contiguous_cached_partials(launches, total_partials)
     if whole is not None:
         # Every segment's partials were written by its producer, with weight 1, one after
         # another in one tensor in slot order: the finalize reads them where they are.
-        with torch.cuda.device(device):
-            _native.check(lib.hbt_grad_norm_finalize(whole, total_partials, float(max_norm), outputs.data_ptr(),
-                                                     outputs.data_ptr() + 8, grad_mul.data_ptr(),
-                                                     outputs.data_ptr() + 16, nonfinite.data_ptr(), stream),
+        with _native.device_guard(device):
+            _native.check(lib.hbt_grad_norm_finalize(whole, total_partials, float(max_norm), out, out + 8,
+                                                     out + 24, out + 16, out + 28, stream),
                           "optim.hbt_grad_norm_finalize")
-        return NormResult(sum=outputs[0], norm=outputs[1], grad_mul=grad_mul, nonfinite=nonfinite,
-                          grad_mul64=outputs[2:3])
+        return NormResult(scalars)
     partials = torch.empty(max(1, total_partials), dtype=torch.float64, device=device)
     fresh: list[tuple[torch.Tensor, int, int, int, int]] = []  # segments whose partials are tagged
-    with torch.cuda.device(device):
+    with _native.device_guard(device):
         for dtype, unscale, items, first in launches:
             # Items whose producer already wrote their partials take them from there
             # (times the weight, as the kernel would multiply); the others are summed
@@ -419,17 +435,8 @@ def gradient_norm_pass(
                     pending.append((grad, offset, length, weight))
                 slot += count
             _launch_sqnorm(lib, pending, dtype, unscale, partials, pending_first, stream)
-        status = lib.hbt_grad_norm_finalize(
-            partials.data_ptr(),
-            total_partials,
-            float(max_norm),
-            outputs.data_ptr(),
-            outputs.data_ptr() + 8,
-            grad_mul.data_ptr(),
-            outputs.data_ptr() + 16,
-            nonfinite.data_ptr(),
-            stream,
-        )
+        status = lib.hbt_grad_norm_finalize(partials.data_ptr(), total_partials, float(max_norm), out, out + 8,
+                                            out + 24, out + 16, out + 28, stream)
         _native.check(status, "optim.hbt_grad_norm_finalize")
     records: dict[int, tuple[torch.Tensor, dict[tuple[int, int], torch.Tensor]]] = {}
     for grad, offset, length, slot, count in fresh:
@@ -441,8 +448,7 @@ def gradient_norm_pass(
             record.segments.update(found)  # keep a producer's still-valid segments
         else:
             setattr(grad, NORM_PARTIALS_ATTR, NormPartials(grad.data_ptr(), grad._version, found, grad.dtype))
-    return NormResult(sum=outputs[0], norm=outputs[1], grad_mul=grad_mul, nonfinite=nonfinite,
-                      grad_mul64=outputs[2:3])
+    return NormResult(scalars)
 
 
 def _zero_segment(grad: torch.Tensor, offset: int, length: int) -> bool:
@@ -546,7 +552,7 @@ def scale_gradients(grads: Sequence[torch.Tensor], dtype: torch.dtype, unscale: 
 
     resident = [g for g in grads if not is_host(g)]
     hosted = [g for g in grads if is_host(g)]
-    with torch.cuda.device(device):
+    with _native.device_guard(device):
         for start in range(0, len(resident), _native.MAX_TENSORS_PER_LAUNCH):
             chunk = resident[start : start + _native.MAX_TENSORS_PER_LAUNCH]
             call([g.data_ptr() for g in chunk], [g.numel() for g in chunk], _native.stream_of(device))
@@ -599,7 +605,7 @@ def unscale_with_partials(grads: Sequence[torch.Tensor], dtype: torch.dtype, uns
     resident = [g for g in grads if not is_host(g)]
     hosted = [g for g in grads if is_host(g)]
     records: list[tuple[torch.Tensor, torch.Tensor]] = []
-    with torch.cuda.device(device):
+    with _native.device_guard(device):
         for start in range(0, len(resident), _native.MAX_TENSORS_PER_LAUNCH):
             chunk = resident[start : start + _native.MAX_TENSORS_PER_LAUNCH]
             counts = [count_of(g.numel()) for g in chunk]
@@ -748,6 +754,18 @@ def _sgd_scalars(group: dict) -> tuple[tuple[float, ...], int]:
     return (weight_decay, momentum, 1 - float(group["dampening"]), -lr), flags
 
 
+def _next_step(step_t: torch.Tensor) -> float:
+    """The value ``step_t += 1`` leaves in an AdamW step counter, formed on the host: a
+    torch op on a 0-dim tensor costs a few microseconds, and a step takes one per
+    parameter.  For a float32 or float64 counter the exact double sum rounded to its
+    dtype is that sum, for every finite count; other dtypes take the torch op."""
+    if step_t.dtype == torch.float32:
+        return float(np.float32(float(step_t.item()) + 1.0))
+    if step_t.dtype == torch.float64:
+        return float(step_t.item()) + 1.0
+    return float((step_t + 1).item())
+
+
 def _unrecordable(reason: str) -> UnsupportedFeatureError:
     return UnsupportedFeatureError(
         format_error("optim.ShardedOptimizer.step", f"this step cannot be recorded into a HIP graph: {reason}",
@@ -759,14 +777,16 @@ def _unrecordable(reason: str) -> UnsupportedFeatureError:
 class _RecordedAdamW:
     """One AdamW launch group recorded into a graph, whose kernels read their scalars
     from ``slot``.  Before each replay, :meth:`prepare` checks that the recorded launch
-    still describes the step and returns the action that does what the eager step does
-    on the host: advance the parameters' step counters and write the new step's scalars,
-    formed as the eager step forms them, into the slot."""
+    still describes the step, formats the new step's scalars, formed as the eager step
+    forms them, into the slot's host record (``record``, which the replay copies into the
+    slot with every other recorded step's), and returns the action that does what the
+    eager step does to the host state: advance the parameters' step counters."""
 
-    def __init__(self, optimizer: "ShardedOptimizer", slot: torch.Tensor, params: list[nn.Parameter],
+    def __init__(self, optimizer: "ShardedOptimizer", slot: torch.Tensor, record: int, params: list[nn.Parameter],
                  pdtype: torch.dtype, unscale: float, scalars: tuple[float, ...]) -> None:
         self._optimizer = optimizer
         self._slot = slot
+        self._record = record
         self._params = list(params)
         self._grad_ptrs = [p.grad.data_ptr() for p in params]
         self._pdtype = pdtype
@@ -783,27 +803,24 @@ class _RecordedAdamW:
         for p, ptr in zip(self._params, self._grad_ptrs):
             _check_recorded_grad(p, ptr)
         states = [opt._optimizer.state[p] for p in self._params]
-        steps = {float((s["step"] + 1).item()) for s in states}
+        steps = {_next_step(s["step"]) for s in states}
         found = {_adamw_scalars(groups[id(p)], step) for p in self._params for step in steps}
         if len(found) != 1:
             raise _replay_error("the parameters recorded in one launch no longer share their step scalars")
         scalars = found.pop()
         if (abs(scalars[1]) < 0.5) != self._lerp_small:
             raise _replay_error("beta1 crossed 0.5, which selects another recorded kernel")
+        lib = _native.library()
+        if self._pdtype == torch.float64:
+            status = lib.hbt_adamw_scalar_record_f64(self._record, float(self._unscale), *scalars)
+        else:
+            status = lib.hbt_adamw_scalar_record(self._record, _native.dtype_code(self._pdtype), self._unscale,
+                                                 *scalars)
+        _native.check(status, "optim.hbt_adamw_scalar_record")
 
         def commit() -> None:
-            lib = _native.library()
-            stream = _native.stream_of(opt._device)
-            with torch.cuda.device(opt._device):
-                if self._pdtype == torch.float64:
-                    status = lib.hbt_adamw_write_scalars_f64(self._slot.data_ptr(), float(self._unscale), *scalars,
-                                                             stream)
-                else:
-                    status = lib.hbt_adamw_write_scalars(self._slot.data_ptr(), _native.dtype_code(self._pdtype),
-                                                         self._unscale, *scalars, stream)
-            _native.check(status, "optim.hbt_adamw_write_scalars")
             for s in states:
-                s["step"] += 1
+                s["step"].fill_(_next_step(s["step"]))  # s["step"] += 1
             increment_version(self._params + [s["exp_avg"] for s in states] + [s["exp_avg_sq"] for s in states])
 
         return commit
@@ -813,10 +830,11 @@ class _RecordedSgd:
     """One SGD launch group recorded into a graph (see :class:`_RecordedAdamW`); SGD's
     scalars follow the learning rate and the other hyperparameters, not the step."""
 
-    def __init__(self, optimizer: "ShardedOptimizer", slot: torch.Tensor, params: list[nn.Parameter],
+    def __init__(self, optimizer: "ShardedOptimizer", slot: torch.Tensor, record: int, params: list[nn.Parameter],
                  pdtype: torch.dtype, unscale: float, flags: int) -> None:
         self._optimizer = optimizer
         self._slot = slot
+        self._record = record
         self._params = list(params)
         self._grad_ptrs = [p.grad.data_ptr() for p in params]
         self._pdtype = pdtype
@@ -842,18 +860,15 @@ class _RecordedSgd:
                                 "another recorded kernel")
         buffers = [opt._optimizer.state[p]["momentum_buffer"] for p in self._params] \
             if self._flags & _native.SGD_MOMENTUM else []
+        lib = _native.library()
+        if self._pdtype == torch.float64:
+            status = lib.hbt_sgd_scalar_record_f64(self._record, float(self._unscale), *scalars, self._flags)
+        else:
+            status = lib.hbt_sgd_scalar_record(self._record, _native.dtype_code(self._pdtype), self._unscale,
+                                               *scalars, self._flags)
+        _native.check(status, "optim.hbt_sgd_scalar_record")
 
         def commit() -> None:
-            lib = _native.library()
-            stream = _native.stream_of(opt._device)
-            with torch.cuda.device(opt._device):
-                if self._pdtype == torch.float64:
-                    status = lib.hbt_sgd_write_scalars_f64(self._slot.data_ptr(), float(self._unscale), *scalars,
-                                                           self._flags, stream)
-                else:
-                    status = lib.hbt_sgd_write_scalars(self._slot.data_ptr(), _native.dtype_code(self._pdtype),
-                                                       self._unscale, *scalars, self._flags, stream)
-            _native.check(status, "optim.hbt_sgd_write_scalars")
             increment_version(self._params + buffers)
 
         return commit
@@ -981,14 +996,17 @@ class ShardedOptimizer:
         )
         self._pending_mul: NormResult | None = None  # the clip multipliers the next step applies
         self._pending_signature: tuple[tuple[int, int, int], ...] | None = None
-        self._last_check: tuple[tuple[tuple[int, int, int], ...], torch.Tensor] | None = None
+        # (gradient signature, the norm pass whose non-finite flag describes those gradients)
+        self._last_check: tuple[tuple[tuple[int, int, int], ...], NormResult | torch.Tensor] | None = None
 
     # -- norm and clip ---------------------------------------------------------------
-    def _norm(self, max_norm: float) -> NormResult:
+    def _norm(self, max_norm: float) -> tuple[NormResult, tuple[tuple[int, int, int], ...]]:
+        """The norm pass over the current gradients, and their signature."""
         segments = [s for c in self._contributions for s in c.segments()]
         result = gradient_norm_pass(segments, self._device, max_norm=max_norm)
-        self._last_check = (_grad_signature(self._parameters), result.nonfinite)
-        return result
+        signature = _grad_signature(self._parameters)
+        self._last_check = (signature, result)
+        return result, signature
 
     def _scale_grads(self, grad_mul: NormResult | None, unscale_attr: bool) -> None:
         """Apply pending multipliers to the gradients in place (materialisation)."""
@@ -1050,11 +1068,11 @@ class ShardedOptimizer:
         """
         if self._pending_mul is not None:
             self.materialize_pending()
-        result = self._norm(max_norm)
+        result, signature = self._norm(max_norm)
         if max_norm <= 0:
             return result.norm
         self._pending_mul = result
-        self._pending_signature = _grad_signature(self._parameters)
+        self._pending_signature = signature
         if not (self._defer_clip or self._clip_in_step):
             self.materialize_pending()  # the reference's grad.mul_(coefficient), on the device
         return result.norm
@@ -1083,6 +1101,8 @@ class ShardedOptimizer:
         if self._last_check is None:
             return None
         signature, flag = self._last_check
+        if isinstance(flag, NormResult):
+            flag = flag.nonfinite
         return flag if signature == _grad_signature(self._parameters) else None
 
     # -- update ----------------------------------------------------------------------
@@ -1188,14 +1208,14 @@ class ShardedOptimizer:
                 state["exp_avg_sq"] = self._zero_state(p, "exp_avg_sq")
             step_t = state["step"]
             if recording is None:
-                step_t += 1
-                step = float(step_t.item())
+                step = _next_step(step_t)
+                step_t.fill_(step)  # step_t += 1
             else:
-                step = float((step_t + 1).item())  # the step each replay advances to, as step_t += 1 forms it
+                step = _next_step(step_t)  # the step each replay advances to
             key = (_adamw_scalars(group, step), p.dtype, grad.dtype, _pending_unscale(grad))
             batches.setdefault(key, []).append(p)
         stream = _native.stream_of(self._device)
-        with torch.cuda.device(self._device):
+        with _native.device_guard(self._device):
             for (scalars, pdtype, gdtype, unscale), batch in batches.items():
                 flags = _write_back_flag(write_back, grad_mul, unscale)
                 mul_ptr = _mul_ptr(grad_mul, gdtype)
@@ -1206,7 +1226,8 @@ class ShardedOptimizer:
                 slot = None
                 if recording is not None and params:
                     slot = recording.new_slot()
-                    recording.steps.append(_RecordedAdamW(self, slot, params, pdtype, unscale, scalars))
+                    recording.steps.append(_RecordedAdamW(self, slot, recording.record_address(slot), params,
+                                                          pdtype, unscale, scalars))
                 for start in range(0, len(params), _native.MAX_TENSORS_PER_LAUNCH):
                     chunk = params[start : start + _native.MAX_TENSORS_PER_LAUNCH]
                     states = [self._optimizer.state[p] for p in chunk]
@@ -1220,9 +1241,7 @@ class ShardedOptimizer:
                         unscale, mul_ptr, scalars, flags, stream, slot,
                     )
                     _native.check(status, "optim.hbt_adamw_step")
-                    increment_version(chunk)
-                    increment_version([s["exp_avg"] for s in states])
-                    increment_version([s["exp_avg_sq"] for s in states])
+                    increment_version(chunk + [s["exp_avg"] for s in states] + [s["exp_avg_sq"] for s in states])
 
     def _recording_check(self) -> "_native.GraphRecording | None":
         """The graph recording this step joins, after refusing what a replay cannot repeat."""
@@ -1312,7 +1331,7 @@ class ShardedOptimizer:
             key = (scalars, flags | _write_back_flag(write_back, grad_mul, unscale), p.dtype, grad.dtype, unscale)
             batches.setdefault(key, []).append(p)
         stream = _native.stream_of(self._device)
-        with torch.cuda.device(self._device):
+        with _native.device_guard(self._device):
             for (scalars, flags, pdtype, gdtype, unscale), batch in batches.items():
                 mul_ptr = _mul_ptr(grad_mul, gdtype)
                 for p in batch:
@@ -1322,7 +1341,8 @@ class ShardedOptimizer:
                 slot = None
                 if recording is not None and params:
                     slot = recording.new_slot()
-                    recording.steps.append(_RecordedSgd(self, slot, params, pdtype, unscale, flags))
+                    recording.steps.append(_RecordedSgd(self, slot, recording.record_address(slot), params,
+                                                        pdtype, unscale, flags))
                 for start in range(0, len(params), _native.MAX_TENSORS_PER_LAUNCH):
                     chunk = params[start : start + _native.MAX_TENSORS_PER_LAUNCH]
                     buffers = ([self._optimizer.state[p]["momentum_buffer"] for p in chunk]
@@ -1332,9 +1352,7 @@ class ShardedOptimizer:
                                        [b.data_ptr() for b in buffers] if buffers else None,
                                        [p.numel() for p in chunk], unscale, mul_ptr, scalars, flags, stream, slot)
                     _native.check(status, "optim.hbt_sgd_step")
-                    increment_version(chunk)
-                    if buffers:
-                        increment_version(buffers)
+                    increment_version(chunk + buffers)
 
     def _streamed_sgd(self, lib, host_p, scalars, flags, pdtype, gdtype, unscale, mul_ptr) -> None:
         """SGD on a parameter whose momentum buffer, or whose every operand, lives on the

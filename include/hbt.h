@@ -496,15 +496,39 @@ int32_t hbt_sgd_write_scalars_f64(void* slot, double unscale, double weight_deca
                                   double one_minus_dampening, double neg_lr, int32_t flags, void* stream);
 
 /* ------------------------------------------------------------------------------
+ * The step scalars formatted on the host, for writing several slots at once.
+ *
+ * Replaces: the same reference step as the *_write_scalars entry points above
+ *   (ShardedOptimizer.step, optim/sharded_optimizer.py:340-355).
+ * Each *_scalar_record call validates its arguments as the *_write_scalars form with the
+ * same name does and writes into `record`, HBT_STEP_SLOT_BYTES of host memory, the
+ * bytes that form would write into a slot (zero past the scalars), launching nothing.
+ * A caller holding the records of consecutive slots writes them with one
+ * hbt_write_words call: a replay of several recorded steps then issues one launch for
+ * their scalars instead of one per step.
+ * ---------------------------------------------------------------------------- */
+int32_t hbt_adamw_scalar_record(void* record, int32_t param_dtype, float unscale, float decay, float lerp_weight,
+                                float beta2, float one_minus_beta2, float bias_correction2_sqrt, float eps,
+                                float neg_step_size);
+int32_t hbt_sgd_scalar_record(void* record, int32_t param_dtype, float unscale, float weight_decay, float momentum,
+                              float one_minus_dampening, float neg_lr, int32_t flags);
+int32_t hbt_adamw_scalar_record_f64(void* record, double unscale, double decay, double lerp_weight, double beta2,
+                                    double one_minus_beta2, double bias_correction2_sqrt, double eps,
+                                    double neg_step_size);
+int32_t hbt_sgd_scalar_record_f64(void* record, double unscale, double weight_decay, double momentum,
+                                  double one_minus_dampening, double neg_lr, int32_t flags);
+
+/* ------------------------------------------------------------------------------
  * Small host-built data written into device memory by kernel launches.
  *
  * This entry point has no counterpart in the reference.  It is for callers that record
  * work into a HIP graph: a copy from pageable host memory cannot be recorded, and a
  * recorded copy from pinned memory reads that memory at every replay.  It writes
  * words[0 .. count) to `dst` (4-byte-aligned device memory) by launches on `stream` of
- * at most 64 words each; the words travel in the launch arguments, so a recorded launch
+ * at most 256 words each; the words travel in the launch arguments, so a recorded launch
  * keeps them and the host buffer may be reused as soon as the call returns.  Used for
- * the interval tables of copies recorded into a graph.
+ * the interval tables of copies recorded into a graph, and for the step slots of a
+ * recorded step before each replay.
  * ---------------------------------------------------------------------------- */
 int32_t hbt_write_words(void* dst, const uint32_t* words, int64_t count, void* stream);
 

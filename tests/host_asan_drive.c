@@ -2,6 +2,7 @@
 // tests/test_host_asan.py: every entry point with tables up to and past its limits,
 // empty tensors (nothing to launch) and bad arguments, no device needed.
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 #include "hbt.h"
 
@@ -127,6 +128,21 @@ int main(void) {
     EXPECT(hbt_write_words(NULL, NULL, 0, NULL) == HBT_OK);
     EXPECT(hbt_write_words((char*)buf + 2, (const uint32_t*)buf, 1, NULL) == HBT_ERR_INVALID_ARGUMENT);
     EXPECT(hbt_write_words(buf, NULL, 1, NULL) == HBT_ERR_INVALID_ARGUMENT);
+    /* the host formatters write exactly one slot of host memory */
+    {
+        unsigned char* record = (unsigned char*)malloc(HBT_STEP_SLOT_BYTES);
+        EXPECT(record != NULL);
+        EXPECT(hbt_adamw_scalar_record(record, HBT_DTYPE_BF16, 1.0f, 1.0f, 0.1f, 0.9f, 0.1f, 1.0f, 1e-8f, -1e-3f)
+               == HBT_OK);
+        EXPECT(hbt_adamw_scalar_record(record, HBT_DTYPE_F64, 1.0f, 1.0f, 0.1f, 0.9f, 0.1f, 1.0f, 1e-8f, -1e-3f)
+               == HBT_ERR_INVALID_ARGUMENT);
+        EXPECT(hbt_sgd_scalar_record(record, HBT_DTYPE_F16, 1.0f, 0.01f, 0.9f, 1.0f, -0.1f,
+                                     HBT_SGD_MOMENTUM | HBT_SGD_NESTEROV) == HBT_OK);
+        EXPECT(hbt_adamw_scalar_record_f64(record, 1.0, 1.0, 0.1, 0.9, 0.1, 1.0, 1e-8, -1e-3) == HBT_OK);
+        EXPECT(hbt_sgd_scalar_record_f64(record, 1.0, 0.0, 0.0, 1.0, -0.1, HBT_SGD_WEIGHT_DECAY) == HBT_OK);
+        EXPECT(hbt_sgd_scalar_record_f64(NULL, 1.0, 0.0, 0.0, 1.0, -0.1, 0) == HBT_ERR_INVALID_ARGUMENT);
+        free(record);
+    }
     (void)hbt_last_error();
     printf("asan host drive: %d failures\n", fails);
     return fails;

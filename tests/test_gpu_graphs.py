@@ -12,6 +12,9 @@ host state of that step.
 
 from __future__ import annotations
 
+import ctypes
+
+import numpy as np
 import pytest
 import torch
 import torch.nn as nn
@@ -28,6 +31,7 @@ from hybrid_training_amd import (
     StepGraph,
     UnsupportedFeatureError,
 )
+from hybrid_training_amd import _native
 from hybrid_training_amd.optim import PENDING_UNSCALE_ATTR
 
 pytestmark = pytest.mark.gpu
@@ -320,3 +324,58 @@ class _ModelTail:
                                      DDPConfig(bucket_cap_mb=2.0 / 1024))
         self.opt = ShardedOptimizer([p for _, p in named], OptimizerConfig(learning_rate=1e-3, weight_decay=0.01),
                                     norm_group=GroupHandle.trivial(), device=DEV)
+
+
+def test_slots_written_from_host_records_equal_the_writers():
+    """Before a replay every recorded step's scalars are formatted on the host
+    (hbt_*_scalar_record) and all slots are written by one hbt_write_words call: the
+    slots must be bitwise what each step's own writer (hbt_*_write_scalars) leaves, for
+    every kind of step, with zeros after each record."""
+    lib = _native.library()
+    size = _native.STEP_SLOT_BYTES
+    rng = np.random.default_rng(11)
+    slots = 13  # two launches of at most 8 slots (256 words)
+    by_writers = torch.zeros(slots * size // 8, dtype=torch.float64, device=DEV)
+    together = torch.full_like(by_writers, float("nan"))
+    records = (ctypes.c_uint8 * (slots * size))()
+    stream = _native.stream_of(DEV)
+    momentum = int(_native.SGD_MOMENTUM)
+    for i in range(slots):
+        slot = by_writers.data_ptr() + i * size
+        record = ctypes.addressof(records) + i * size
+        values = [float(v) for v in rng.uniform(-2.0, 2.0, 7)]
+        dtype = int(i % 3)  # F32, BF16, F16
+        unscale = float(rng.choice([1.0, 2.0**-16]))
+        kind = i % 4
+        if kind == 0:
+            assert lib.hbt_adamw_write_scalars(slot, dtype, unscale, *values, stream) == 0
+            assert lib.hbt_adamw_scalar_record(record, dtype, unscale, *values) == 0
+        elif kind == 1:
+            assert lib.hbt_adamw_write_scalars_f64(slot, unscale, *values, stream) == 0
+            assert lib.hbt_adamw_scalar_record_f64(record, unscale, *values) == 0
+        elif kind == 2:
+            assert lib.hbt_sgd_write_scalars(slot, dtype, unscale, *values[:4], momentum, stream) == 0
+            assert lib.hbt_sgd_scalar_record(record, dtype, unscale, *values[:4], momentum) == 0
+        else:
+            assert lib.hbt_sgd_write_scalars_f64(slot, unscale, *values[:4], 0, stream) == 0
+            assert lib.hbt_sgd_scalar_record_f64(record, unscale, *values[:4], 0) == 0
+    words = ctypes.cast(records, ctypes.POINTER(ctypes.c_uint32))
+    assert lib.hbt_write_words(together.data_ptr(), words, slots * size // 4, stream) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(by_writers.view(torch.int32), together.view(torch.int32))
+
+
+@pytest.mark.parametrize("count", [1, 63, 64, 65, 255, 256, 257, 700])
+def test_write_words_across_blocks_and_launches(count):
+    """hbt_write_words carries up to 256 words per launch, 64 per block: every word lands
+    at its index and nothing past the count is touched."""
+    lib = _native.library()
+    rng = np.random.default_rng(count)
+    words = rng.integers(0, 2**32, count, dtype=np.uint64).astype(np.uint32)
+    dst = torch.full((count + 70,), -1, dtype=torch.int32, device=DEV)
+    host = (ctypes.c_uint32 * count)(*[int(w) for w in words])
+    assert lib.hbt_write_words(dst.data_ptr(), host, count, _native.stream_of(DEV)) == 0
+    torch.cuda.synchronize()
+    got = dst.cpu().numpy().view(np.uint32)
+    assert np.array_equal(got[:count], words)
+    assert np.all(got[count:] == np.uint32(0xFFFFFFFF))

@@ -444,3 +444,25 @@ def test_norm_partials_follow_the_version_counter_not_the_data():
     with torch.inference_mode():
         frozen = torch.ones(2)
     _native.bump_versions([frozen])  # inference tensors have no counter: skipped, no error
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.float16, torch.int64])
+def test_step_counter_advances_as_torch_adds_one(dtype):
+    """The AdamW step counter is advanced on the host (the value, then fill_): the value
+    must be what torch's ``step_t += 1`` stores, counts where float32 rounds included."""
+    from hybrid_training_amd.optim import _next_step
+
+    rng = np.random.default_rng(5)
+    counts = [0.0, 1.0, 2.0**24 - 1, 2.0**24, 2.0**24 + 2, 2.0**25 + 4, 3e7, 1e30, 2.0**127, -5.0, 0.5]
+    counts += list(rng.uniform(0, 2**26, 2000)) + list(np.floor(rng.uniform(0, 2**30, 2000)))
+    for value in counts:
+        if dtype == torch.float16 and abs(value) > 60000:
+            continue
+        if dtype == torch.int64 and (value != int(value) or abs(value) > 2**62):
+            continue
+        counter = torch.tensor(value, dtype=dtype)
+        expected = counter.clone()
+        expected += 1
+        got = _next_step(counter)
+        counter.fill_(got)
+        assert torch.equal(counter, expected) and got == float(expected.item()), (dtype, value)

@@ -10,6 +10,7 @@ import ctypes
 import os
 import re
 
+import numpy as np
 import pytest
 
 from hybrid_training_amd import _native
@@ -191,6 +192,45 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     assert lib.hbt_write_words(fake, None, 2, None) == -1
     assert lib.hbt_write_words(fake, words, -1, None) == -1
     assert lib.hbt_write_words(None, None, 0, None) == 0  # nothing to write, nothing launched
+    # the host formatters check what their writers check
+    assert lib.hbt_adamw_scalar_record(None, 0, 1.0, 1.0, 0.1, 0.9, 0.1, 1.0, 1e-8, -1e-3) == -1
+    assert b"hbt_adamw_scalar_record: the record buffer is null" in lib.hbt_last_error()
+    record = (ctypes.c_uint8 * _native.STEP_SLOT_BYTES)()
+    assert lib.hbt_adamw_scalar_record(record, 3, 1.0, 1.0, 0.1, 0.9, 0.1, 1.0, 1e-8, -1e-3) == -1
+    assert b"param_dtype 3" in lib.hbt_last_error()
+    assert lib.hbt_sgd_scalar_record(record, 0, 1.0, 0.0, 0.0, 1.0, -0.1, 4) == -1  # NESTEROV alone
+    assert lib.hbt_sgd_scalar_record(record, 5, 1.0, 0.0, 0.0, 1.0, -0.1, 0) == -1
+    assert lib.hbt_adamw_scalar_record_f64(None, 1.0, 1.0, 0.1, 0.9, 0.1, 1.0, 1e-8, -1e-3) == -1
+    assert lib.hbt_sgd_scalar_record_f64(record, 1.0, 0.0, 0.0, 1.0, -0.1, 64) == -1  # unknown flag
+    assert bytes(record) == bytes(_native.STEP_SLOT_BYTES)  # a refused call writes nothing
+
+
+def test_scalar_records_fill_the_slot_and_zero_its_tail():
+    """The host formatters launch nothing: each writes the whole slot, the scalars it
+    was given (as float32 or float64 bit patterns) and zeros after them."""
+    lib = _native.library()
+    size = _native.STEP_SLOT_BYTES
+
+    def formatted(call, *args):
+        record = (ctypes.c_uint8 * size)(*([0xAB] * size))
+        assert call(record, *args) == 0
+        return bytes(record)
+
+    adam = (0.99999, 0.1, 0.95, 0.05, 0.6324555, 1e-8, -3e-4)
+    for dtype in (0, 1, 2):
+        raw = formatted(lib.hbt_adamw_scalar_record, dtype, 0.5, *adam)
+        assert raw == formatted(lib.hbt_adamw_scalar_record, dtype, 0.5, *adam)  # deterministic
+        values = np.frombuffer(raw, dtype=np.float32)
+        # eps is kept rounded to a 2-byte parameter's dtype, as torch rounds it there
+        assert all(np.float32(a) in values for a in (adam if dtype == 0 else adam[:5] + adam[6:]))
+        assert raw.rstrip(b"\0") != raw and 0xAB not in raw
+    raw = formatted(lib.hbt_adamw_scalar_record_f64, 0.5, *adam)
+    values = np.frombuffer(raw, dtype=np.float64)
+    assert all(a in values for a in adam) and 0.5 in values and 0xAB not in raw
+    raw = formatted(lib.hbt_sgd_scalar_record, 0, 1.0, 0.01, 0.9, 1.0, -0.1, int(_native.SGD_MOMENTUM))
+    assert np.float32(-0.1) in np.frombuffer(raw, dtype=np.float32) and 0xAB not in raw
+    raw = formatted(lib.hbt_sgd_scalar_record_f64, 1.0, 0.01, 0.9, 1.0, -0.1, int(_native.SGD_MOMENTUM))
+    assert -0.1 in np.frombuffer(raw, dtype=np.float64) and 0xAB not in raw
 
 
 def test_host_tensors_are_refused():
