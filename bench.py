@@ -1452,6 +1452,9 @@ def bench_mlp(steps: int, warmup: int) -> int:
                                 torch.nn.Linear(32, 1)).to(device)
     named = list(model.named_parameters())
     mp = MixedPrecisionConfig(enabled=False)
+    # A step takes tens of microseconds: at least 500 timed steps (under 0.2 s) keep the
+    # launch-time jitter out of the mean.
+    mlp_steps, mlp_warmup = max(steps, 500), max(warmup, 50)
     for world in (2, 4):
         handles = [FlatParamHandle(named, None, GroupHandle.local_view("shard", world, r), FSDPConfig(), mp, device,
                                    keep_originals=True) for r in range(world)]
@@ -1470,7 +1473,7 @@ def bench_mlp(steps: int, warmup: int) -> int:
                 opt.clip_grad_norm(1.0)
                 opt.step()
 
-        ms = _time_events(tail, max(steps, 50), max(warmup, 10))
+        ms = _time_events(tail, mlp_steps, mlp_warmup)
         cpu = None
         if _WITH_CPU:
             from oracle.cpu_reference_path import ReferenceMlpTail
@@ -1483,7 +1486,7 @@ def bench_mlp(steps: int, warmup: int) -> int:
                             "200 timed steps after 1 warm-up")
         per_rank_us = ms * 1e3 / world
         _emit(f"FSDP MLP drop-in tail at W={world} (local share + clip + AdamW): rank-steps/s", "rank-steps/s",
-              world / (ms * 1e-3), ms, max(steps, 50), max(warmup, 10), "f32",
+              world / (ms * 1e-3), ms, mlp_steps, mlp_warmup, "f32",
               f"MLP 23-32-32-1 (1,857 fp32 params), FSDP W={world}: shards of {shard}, all ranks on one GPU",
               world * shard * (4 * world + 4 + 28),
               {"params": 1857, "world": world, "shard_numel": shard, "us_per_rank_step": per_rank_us},
@@ -1492,9 +1495,9 @@ def bench_mlp(steps: int, warmup: int) -> int:
         # optimizers' step scalars from their host state, then runs every rank's
         # launches with one graph launch.
         graph = StepGraph(tail)
-        ms = _time_events(graph.replay, max(steps, 50), max(warmup, 10))
+        ms = _time_events(graph.replay, mlp_steps, mlp_warmup)
         _emit(f"FSDP MLP drop-in tail at W={world}, replayed from one HIP graph: rank-steps/s", "rank-steps/s",
-              world / (ms * 1e-3), ms, max(steps, 50), max(warmup, 10), "f32",
+              world / (ms * 1e-3), ms, mlp_steps, mlp_warmup, "f32",
               f"MLP 23-32-32-1 (1,857 fp32 params), FSDP W={world}: the tail of all {world} ranks recorded "
               "into one HIP graph (StepGraph) and replayed", world * shard * (4 * world + 4 + 28),
               {"params": 1857, "world": world, "shard_numel": shard, "us_per_rank_step": ms * 1e3 / world},

@@ -1626,9 +1626,10 @@ SgdScalarsF64 sgd_scalars_f64(double unscale, double weight_decay, double moment
 
 // ---- small host-built data into device memory --------------------------------------------
 // One launch stores up to kWordsPerWrite 32-bit words that arrive in its arguments, one
-// wave per kWordsPerBlock of them: lane i of block b stores word 64b + i (one vector store
-// instruction).  A recorded launch keeps its arguments, so a graph replays the write with
-// the words it was given.
+// 64-lane block per kWordsPerBlock of them: thread i of the grid stores word i.  The
+// argument block lives in the kernarg segment, so each lane reads its word with one
+// vector load from there (no scratch copy).  A recorded launch keeps its arguments, so a
+// graph replays the write with the words it was given.
 constexpr int kWordsPerWrite = 256;
 constexpr int kWordsPerBlock = 64;
 struct WordBlock {
@@ -1637,15 +1638,10 @@ struct WordBlock {
 
 __global__ __launch_bounds__(kWordsPerBlock) void write_words_kernel(uint32_t* __restrict__ dst, WordBlock words,
                                                                       int32_t count) {
-    const int lane = threadIdx.x;
-    // The block's words are read at wave-uniform offsets (scalar loads of the arguments);
-    // each lane keeps its own by selection, never by a per-lane argument index.  The grid
-    // has ceil(count / 64) <= 4 blocks, so base + k stays inside the block of words.
-    const int base = static_cast<int>(blockIdx.x) * kWordsPerBlock;
-    uint32_t word = 0u;
-#pragma unroll
-    for (int k = 0; k < kWordsPerBlock; ++k) word = lane == k ? words.w[base + k] : word;
-    if (base + lane < count) dst[base + lane] = word;
+    // The grid has ceil(count / 64) <= 4 blocks and count <= 256, so i < count stays
+    // inside the block of words.
+    const int i = static_cast<int>(blockIdx.x) * kWordsPerBlock + static_cast<int>(threadIdx.x);
+    if (i < count) dst[i] = words.w[i];
 }
 
 int32_t write_words(const char* who, void* dst, const uint32_t* words, int64_t count, hipStream_t st) {
