@@ -836,17 +836,19 @@ __device__ __forceinline__ float share_input(float g, float a) {
     return x;
 }
 
-template <int ID, int kG, bool kRecip, int RD, int OD, bool kAcc = false>
-__global__ __launch_bounds__(kShareBlock) void local_share_tiles_kernel(
-    ShareRanks ranks, ShareAcc accs, int32_t group_size, int64_t offset, int64_t shard_numel, int64_t valid_numel,
-    float divisor, float recip, int32_t vec_ok, void* __restrict__ out, double* __restrict__ tile_sums,
-    int64_t block_base) {
+// One 256-element tile of the local share, run by the 64 lanes of one wave (`lane` is
+// this thread's lane): writes the tile's outputs and returns this lane's part of the tile's
+// squared norm.
+template <int ID, int kG, bool kRecip, int RD, int OD, bool kAcc>
+__device__ __forceinline__ double share_tile(const ShareRanks& ranks, const ShareAcc& accs, int32_t group_size,
+                                             int64_t offset, int64_t shard_numel, int64_t valid_numel, float divisor,
+                                             float recip, int32_t vec_ok, void* __restrict__ out, int64_t tile,
+                                             int lane) {
     constexpr int64_t IB = bytes_of<ID>();
-    const int64_t tile = block_base + blockIdx.x;
     const int64_t base = tile * kShareTile;
     double acc = 0.0;
     if (vec_ok && base + kShareTile <= valid_numel) {
-        const int64_t e = base + int64_t(threadIdx.x) * 4;
+        const int64_t e = base + int64_t(lane) * 4;
         float sum[4];
         if constexpr (kG > 0) {
             float x[kG][4];
@@ -889,10 +891,10 @@ __global__ __launch_bounds__(kShareBlock) void local_share_tiles_kernel(
         for (int c = 0; c < 4; ++c) acc += sq(sum[c]);
     } else if (vec_ok && base >= valid_numel && base + kShareTile <= shard_numel) {
         const float zero[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        store_vec<OD, 4>(out, base + int64_t(threadIdx.x) * 4, zero);
+        store_vec<OD, 4>(out, base + int64_t(lane) * 4, zero);
     } else {
         const int64_t end = base + kShareTile < shard_numel ? base + kShareTile : shard_numel;
-        for (int64_t e = base + threadIdx.x; e < end; e += kShareBlock) {
+        for (int64_t e = base + lane; e < end; e += kShareBlock) {
             float v = 0.0f;
             if (e < valid_numel) {
                 const float a0 = kAcc ? load_one<RD>(accs.a[0], e) : 0.0f;
@@ -909,10 +911,58 @@ __global__ __launch_bounds__(kShareBlock) void local_share_tiles_kernel(
             acc += sq(v);
         }
     }
+    return acc;
+}
+
+template <int ID, int kG, bool kRecip, int RD, int OD, bool kAcc = false>
+__global__ __launch_bounds__(kShareBlock) void local_share_tiles_kernel(
+    ShareRanks ranks, ShareAcc accs, int32_t group_size, int64_t offset, int64_t shard_numel, int64_t valid_numel,
+    float divisor, float recip, int32_t vec_ok, void* __restrict__ out, double* __restrict__ tile_sums,
+    int64_t block_base) {
+    const int64_t tile = block_base + blockIdx.x;
+    double acc = share_tile<ID, kG, kRecip, RD, OD, kAcc>(ranks, accs, group_size, offset, shard_numel, valid_numel,
+                                                          divisor, recip, vec_ok, out, tile,
+                                                          static_cast<int>(threadIdx.x));
     if (tile_sums == nullptr) return;
     acc = wave_sum(acc);
     if (threadIdx.x == 0) tile_sums[tile_sum_slot(tile, (shard_numel + kShareTile - 1) / kShareTile)] = acc;
 }
+
+// A shard of at most kSmallShareTiles tiles and its norm partials in one launch: one
+// workgroup with one wave per tile.  Wave w runs tile w as local_share_tiles_kernel runs
+// it; wave 0 then forms the partial of the shard's real segment from the tile sums as
+// tile_sums_to_partials_kernel does (lane l adds tile l's sum to +0.0, then the butterfly;
+// the segment is a single norm chunk) and writes +0.0 for the padding segment, so outputs
+// and partials are bitwise the two-launch form's.  A step of a small model is bound by
+// launch time, which this halves.
+constexpr int kSmallShareTiles = 16;
+
+template <int ID, int kG, bool kRecip, int RD, int OD>
+__global__ __launch_bounds__(kSmallShareTiles * kShareBlock) void local_share_small_kernel(
+    ShareRanks ranks, int32_t group_size, int64_t offset, int64_t shard_numel, int64_t valid_numel, float divisor,
+    float recip, int32_t vec_ok, void* __restrict__ out, double* __restrict__ partials) {
+    static_assert(kSmallShareTiles <= kShareBlock && kSmallShareTiles <= tiles_per_norm_chunk<OD>(),
+                  "a small shard's segments are one norm chunk each");
+    __shared__ double sums[kSmallShareTiles];
+    const int wave = static_cast<int>(threadIdx.x) / kShareBlock;  // the launch has one wave per tile
+    const int lane = static_cast<int>(threadIdx.x) % kShareBlock;
+    const ShareAcc none{};
+    const double s = wave_sum(share_tile<ID, kG, kRecip, RD, OD, false>(
+        ranks, none, group_size, offset, shard_numel, valid_numel, divisor, recip, vec_ok, out, wave, lane));
+    if (lane == 0) sums[wave] = s;
+    __syncthreads();
+    if (wave != 0) return;
+    const int64_t valid_tiles = (valid_numel + kShareTile - 1) / kShareTile;
+    double acc = 0.0;
+    if (lane < valid_tiles) acc += sums[lane];
+    acc = wave_sum(acc);
+    if (lane == 0) {
+        int slot = 0;
+        if (valid_numel > 0) partials[slot++] = acc;
+        if (shard_numel > valid_numel) partials[slot] = 0.0;
+    }
+}
+
 
 // Reduce dtype float64: each rank's element widens exactly to double (IB = 8 reads a
 // float64 no_sync accumulator or float64 gradients), the divide and the rank-order sum run
@@ -1883,10 +1933,16 @@ int32_t local_share(const char* who, const void* const* rank_grads, int32_t grou
     // An exact power of two (or 1) divides as a multiply by its exact reciprocal.
     const float recip = exact_reciprocal(divisor);
     const bool recip_exact = recip != 0.0f;
+    // A small shard's share and partials take one launch (local_share_small_kernel).
+    const bool small = partials != nullptr && !with_acc && !f64 && tiles <= kSmallShareTiles;
+    const unsigned small_threads = static_cast<unsigned>(tiles) * kShareBlock;
     int32_t status = launch_sliced(who, tiles, kShareBlock, [&](int64_t first, dim3 grid) {
 #define HBT_TILES(ID, G, R, RD, OD)                                                                             \
     do {                                                                                                       \
-        if (with_acc)                                                                                          \
+        if (small)                                                                                             \
+            local_share_small_kernel<ID, G, R, RD, OD><<<dim3(1), dim3(small_threads), 0, st>>>(                 \
+                ranks, group_size, offset, shard_numel, valid_numel, divisor, recip, vec_ok, out, partials);    \
+        else if (with_acc)                                                                                     \
             local_share_tiles_kernel<ID, G, R, RD, OD, true><<<grid, kShareBlock, 0, st>>>(                      \
                 ranks, accs, group_size, offset, shard_numel, valid_numel, divisor, recip, vec_ok, out,          \
                 tile_scratch, first);                                                                          \
@@ -1963,7 +2019,7 @@ int32_t local_share(const char* who, const void* const* rank_grads, int32_t grou
 #undef HBT_TILES_G
 #undef HBT_TILES
     });
-    if (status != HBT_OK || partials == nullptr) return status;
+    if (status != HBT_OK || partials == nullptr || small) return status;
     const int64_t chunk = norm_chunk_of(out_dtype);
     const int64_t valid_chunks = (valid_numel + chunk - 1) / chunk;
     const int64_t pad_chunks = (shard_numel - valid_numel + chunk - 1) / chunk;

@@ -29,6 +29,7 @@ The local share runs in each reduce dtype (fp32, bf16, fp16) against the oracle'
 from __future__ import annotations
 
 import ctypes
+import math
 
 import numpy as np
 import pytest
@@ -299,6 +300,79 @@ def test_local_share_accumulated_is_accumulate_then_share(device, group, in_dtyp
                                                    group, rank, shard, valid, code_in, 3, divisor, code_out,
                                                    out_b.data_ptr(), None, None, stream)
         assert f64 == -2 and b"F64" in lib.hbt_last_error()  # HBT_ERR_UNSUPPORTED
+
+
+_SMALL_DTYPES = [(torch.float32, torch.float32, torch.float32), (torch.bfloat16, torch.float32, torch.float32),
+                 (torch.bfloat16, torch.bfloat16, torch.bfloat16), (torch.float16, torch.float16, torch.float32),
+                 (torch.float32, torch.float32, torch.bfloat16)]
+
+
+@pytest.mark.parametrize("tiles", [1, 2, 5, 16, 17])
+@pytest.mark.parametrize("group", [1, 2, 3, 8])
+@pytest.mark.parametrize("dtypes", _SMALL_DTYPES, ids=lambda d: "-".join(str(x).split(".")[1] for x in d))
+@pytest.mark.parametrize("pad", [0, 3, 300])
+def test_small_shard_local_share_is_the_two_launch_form(device, tiles, group, dtypes, pad):
+    """A shard of at most 16 tiles of 256 elements takes one launch for its share and norm
+    partials (one wave per tile in one workgroup); the shards here straddle that size, and
+    300 padding elements make a one-tile shard all padding.  Outputs and partials must be
+    bitwise those of the two-launch form (tiles, then their sums into partials), here
+    ``hbt_grad_local_share_accumulated`` over all-zero rows, which always takes it (0 + x
+    is x for these finite inputs, none of them -0.0): on aligned inputs (vector path) with
+    finite values, and one element into the allocations (scalar path) with an inf planted.
+    The output also matches the oracle, and the partials sum to its squared norm."""
+    in_dtype, reduce, master = dtypes
+    lib = _native.library()
+    shard = tiles * 256 - 37
+    valid = max(0, shard - pad)
+    rank = group - 1
+    code_in, code_red, code_out = (_native.dtype_code(d) for d in (in_dtype, reduce, master))
+    stream = ctypes.c_void_p(_native.stream_of(device))
+    chunk = 32768 if master == torch.float32 else 65536
+    count = -(-valid // chunk) + -(-(shard - valid) // chunk)
+    stride = -(-shard // 64) * 64
+    rows = torch.zeros(group, stride, dtype=reduce, device=device)[:, :shard]
+    for lead in (0, 1):
+        gen = torch.Generator(device=device).manual_seed(tiles * 31 + group + lead)
+        storage = [(torch.randn(group * shard + lead, device=device, generator=gen) * 0.3).to(in_dtype)
+                   for _ in range(group)]
+        grads = [t[lead:] for t in storage]
+        if lead and valid > 1:
+            grads[0][rank * shard + 1] = float("inf")
+
+        def buffers():
+            return (torch.full((shard,), 7.0, dtype=master, device=device),
+                    torch.full((max(1, count),), 5.0, dtype=torch.float64, device=device),
+                    torch.empty(tiles, dtype=torch.float64, device=device))
+
+        out_a, part_a, scratch_a = buffers()
+        _native.check(lib.hbt_grad_local_share_sqnorm(_native.pointer_array([g.data_ptr() for g in grads]), group,
+                                                      rank, shard, valid, code_in, code_red, float(group), code_out,
+                                                      out_a.data_ptr(), part_a.data_ptr(), scratch_a.data_ptr(),
+                                                      stream),
+                      "test.share_sqnorm")
+        out_b, part_b, scratch_b = buffers()
+        _native.check(lib.hbt_grad_local_share_accumulated(
+            _native.pointer_array([g.data_ptr() for g in grads]),
+            _native.pointer_array([rows[q].data_ptr() for q in range(group)]), group, rank, shard, valid, code_in,
+            code_red, float(group), code_out, out_b.data_ptr(), part_b.data_ptr(), scratch_b.data_ptr(), stream),
+            "test.share_accumulated")
+        torch.cuda.synchronize(device)
+        case = (tiles, group, pad, lead)
+        assert np.array_equal(_bits(out_a), _bits(out_b)), case
+        assert np.array_equal(part_a[:count].cpu().numpy().view(np.int64),
+                              part_b[:count].cpu().numpy().view(np.int64)), case
+        assert float(out_a[valid:].abs().sum()) == 0.0, case
+        if reduce == torch.float32 and master == torch.float32:
+            host = [g.float().cpu().numpy() for g in grads]
+            expect = oracle.local_share(host, rank, shard, valid, float(group))
+            assert np.array_equal(_bits(out_a), expect.view(np.int32)), case
+        if valid and lead and valid > 1:
+            assert math.isinf(float(part_a[0])), case
+        elif valid:
+            ref = float((out_a[:valid].double() ** 2).sum())
+            assert abs(float(part_a[0]) - ref) <= 1e-12 * ref, case
+        if shard > valid:  # the padding segment's partial is +0.0
+            assert part_a[count - 1].cpu().numpy().view(np.int64) == 0, case
 
 
 def test_local_share_full_size_rank7_of_llama3_8b_w8(device):
