@@ -789,6 +789,7 @@ class _RecordedAdamW:
         self._record = record
         self._params = list(params)
         self._grad_ptrs = [p.grad.data_ptr() for p in params]
+        self._operands = _RecordedOperands(optimizer, self._params, ("exp_avg", "exp_avg_sq"))
         self._pdtype = pdtype
         self._unscale = unscale
         self._lerp_small = abs(scalars[1]) < 0.5
@@ -802,6 +803,7 @@ class _RecordedAdamW:
         groups = {id(p): g for g in opt._optimizer.param_groups for p in g["params"]}
         for p, ptr in zip(self._params, self._grad_ptrs):
             _check_recorded_grad(p, ptr)
+        self._operands.check()
         states = [opt._optimizer.state[p] for p in self._params]
         steps = {_next_step(s["step"]) for s in states}
         found = {_adamw_scalars(groups[id(p)], step) for p in self._params for step in steps}
@@ -837,6 +839,8 @@ class _RecordedSgd:
         self._record = record
         self._params = list(params)
         self._grad_ptrs = [p.grad.data_ptr() for p in params]
+        self._operands = _RecordedOperands(optimizer, self._params,
+                                           ("momentum_buffer",) if flags & _native.SGD_MOMENTUM else ())
         self._pdtype = pdtype
         self._unscale = unscale
         self._flags = flags
@@ -850,6 +854,7 @@ class _RecordedSgd:
         groups = {id(p): g for g in opt._optimizer.param_groups for p in g["params"]}
         for p, ptr in zip(self._params, self._grad_ptrs):
             _check_recorded_grad(p, ptr)
+        self._operands.check()
         found = {_sgd_scalars(groups[id(p)]) for p in self._params}
         if len(found) != 1:
             raise _replay_error("the parameters recorded in one launch no longer share their scalars")
@@ -872,6 +877,33 @@ class _RecordedSgd:
             increment_version(self._params + buffers)
 
         return commit
+
+
+class _RecordedOperands:
+    """The parameters and optimizer-state tensors a recorded launch updates, held for the
+    graph's life (their memory cannot be handed to another tensor while a replay may
+    write it) and checked before each replay: a ``load_state_dict`` places the state in
+    new tensors and an assignment to ``.data`` gives a parameter new storage, and a
+    replay would still update the recorded ones."""
+
+    def __init__(self, optimizer: "ShardedOptimizer", params: list[nn.Parameter], keys: tuple[str, ...]) -> None:
+        self._optimizer = optimizer
+        self._params = params
+        self._keys = keys
+        self._held = self._current()
+        self._ptrs = [t.data_ptr() for t in self._held]
+
+    def _current(self) -> list[torch.Tensor]:
+        state = self._optimizer._optimizer.state
+        return [p.detach() for p in self._params] + [state[p][k] for p in self._params for k in self._keys]
+
+    def check(self) -> None:
+        state = self._optimizer._optimizer.state
+        if any(k not in state[p] for p in self._params for k in self._keys) or \
+                [t.data_ptr() for t in self._current()] != self._ptrs:
+            raise _replay_error("a parameter or its optimizer state is no longer the tensor the step was recorded "
+                                "with (a load_state_dict or an assignment to .data since the recording); a replay "
+                                "updates the recorded tensors")
 
 
 def _check_recorded_grad(p: nn.Parameter, recorded_ptr: int) -> None:

@@ -174,6 +174,42 @@ def test_replay_refuses_a_rebound_gradient_and_changes_nothing():
     assert float(tail.opts[0].inner.state[p]["step"]) == step_before + 1
 
 
+@pytest.mark.parametrize("config", [OptimizerConfig(learning_rate=1e-3),
+                                    OptimizerConfig(name="sgd", learning_rate=1e-2, momentum=0.9)],
+                         ids=["adamw", "sgd"])
+def test_replay_refuses_replaced_parameters_or_state_and_changes_nothing(config):
+    """load_state_dict places the optimizer state in new tensors, and an assignment to
+    .data gives a parameter new storage: a replay would update the recorded tensors, so it
+    refuses before changing anything, and a new recording replays again."""
+    tail = _Tail(2, config)
+    tail.load_grads(0)
+    tail.step()
+    graph = StepGraph(tail.step)
+    graph.replay()
+    torch.cuda.synchronize()
+    opt = tail.opts[0]
+    (p,) = opt.parameters
+    state_before = {k: v.clone() for k, v in opt.inner.state[p].items()}
+    params_before = [h.flat_param.detach().clone() for h in tail.handles]
+    opt.load_state_dict(opt.state_dict())
+    with pytest.raises(UnsupportedFeatureError, match="no longer the tensor"):
+        graph.replay()
+    torch.cuda.synchronize()
+    for k, v in opt.inner.state[p].items():
+        assert torch.equal(v, state_before[k]), k
+    for h, before in zip(tail.handles, params_before):
+        assert torch.equal(h.flat_param, before)
+    if "step" in state_before:
+        assert float(tail.opts[1].inner.state[tail.handles[1].flat_param]["step"]) == float(state_before["step"])
+    graph = StepGraph(tail.step)  # recorded over the loaded state
+    graph.replay()
+    torch.cuda.synchronize()
+    assert not torch.equal(tail.handles[0].flat_param, params_before[0])
+    p.data = p.data.clone()
+    with pytest.raises(UnsupportedFeatureError, match="no longer the tensor"):
+        graph.replay()
+
+
 @pytest.mark.parametrize("world", [2, 4])
 def test_recorded_fsdp_step_with_the_parameter_gather(world):
     """The gather of every rank's fp32 master shard into the bf16 compute buffer (a cast
