@@ -800,7 +800,7 @@ class _RecordedAdamW:
 
     def prepare(self) -> Callable[[], None]:
         opt = self._optimizer
-        groups = {id(p): g for g in opt._optimizer.param_groups for p in g["params"]}
+        groups = _replay_groups(opt, self._params)
         for p, ptr in zip(self._params, self._grad_ptrs):
             _check_recorded_grad(p, ptr)
         self._operands.check()
@@ -851,7 +851,7 @@ class _RecordedSgd:
 
     def prepare(self) -> Callable[[], None]:
         opt = self._optimizer
-        groups = {id(p): g for g in opt._optimizer.param_groups for p in g["params"]}
+        groups = _replay_groups(opt, self._params)
         for p, ptr in zip(self._params, self._grad_ptrs):
             _check_recorded_grad(p, ptr)
         self._operands.check()
@@ -906,10 +906,26 @@ class _RecordedOperands:
                                 "updates the recorded tensors")
 
 
+def _replay_groups(optimizer: "ShardedOptimizer", params: list[nn.Parameter]) -> dict[int, dict]:
+    """The parameter group of each recorded parameter, refusing what the recorded kernels
+    cannot do: a parameter no longer in any group, amsgrad or maximize switched on."""
+    groups = {id(p): g for g in optimizer._optimizer.param_groups for p in g["params"]}
+    for p in params:
+        group = groups.get(id(p))
+        if group is None:
+            raise _replay_error("a recorded parameter is no longer in the optimizer's parameter groups")
+        if group.get("amsgrad") or group.get("maximize"):
+            raise _replay_error("amsgrad or maximize was switched on; they have no HIP kernel")
+    return groups
+
+
 def _check_recorded_grad(p: nn.Parameter, recorded_ptr: int) -> None:
     if p.grad is None or p.grad.data_ptr() != recorded_ptr:
         raise _replay_error("a parameter's .grad was rebound after recording; a replay reads the gradient "
                             "buffer it was recorded with (write new values into that tensor instead)")
+    if _pending_unscale(p.grad) != 1.0:
+        raise _replay_error("a loss-scale factor is pending on a recorded gradient (a deferred unscale_); the "
+                            "eager step would apply it and the recorded one cannot")
 
 
 def _replay_error(reason: str) -> UnsupportedFeatureError:

@@ -205,6 +205,25 @@ def test_replay_refuses_replaced_parameters_or_state_and_changes_nothing(config)
     graph.replay()
     torch.cuda.synchronize()
     assert not torch.equal(tail.handles[0].flat_param, params_before[0])
+    # what the eager step would do differently: a pending loss-scale factor, amsgrad
+    # switched on, a parameter dropped from the optimizer
+    grad = p.grad
+    setattr(grad, PENDING_UNSCALE_ATTR, 0.5)
+    with pytest.raises(UnsupportedFeatureError, match="loss-scale factor is pending"):
+        graph.replay()
+    delattr(grad, PENDING_UNSCALE_ATTR)
+    group = opt.inner.param_groups[0]
+    if "amsgrad" in group:
+        group["amsgrad"] = True
+        with pytest.raises(UnsupportedFeatureError, match="amsgrad or maximize"):
+            graph.replay()
+        group["amsgrad"] = False
+    kept, group["params"] = group["params"], []
+    with pytest.raises(UnsupportedFeatureError, match="no longer in the optimizer"):
+        graph.replay()
+    group["params"] = kept
+    graph.replay()
+    torch.cuda.synchronize()
     p.data = p.data.clone()
     with pytest.raises(UnsupportedFeatureError, match="no longer the tensor"):
         graph.replay()
