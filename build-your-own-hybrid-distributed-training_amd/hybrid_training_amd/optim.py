@@ -803,10 +803,10 @@ class _RecordedAdamW:
         groups = _replay_groups(opt, self._params)
         for p, ptr in zip(self._params, self._grad_ptrs):
             _check_recorded_grad(p, ptr)
-        self._operands.check()
         states = [opt._optimizer.state[p] for p in self._params]
-        steps = {_next_step(s["step"]) for s in states}
-        found = {_adamw_scalars(groups[id(p)], step) for p in self._params for step in steps}
+        self._operands.check(states)
+        nexts = [_next_step(s["step"]) for s in states]
+        found = {_adamw_scalars(groups[id(p)], step) for p in self._params for step in set(nexts)}
         if len(found) != 1:
             raise _replay_error("the parameters recorded in one launch no longer share their step scalars")
         scalars = found.pop()
@@ -821,9 +821,9 @@ class _RecordedAdamW:
         _native.check(status, "optim.hbt_adamw_scalar_record")
 
         def commit() -> None:
-            for s in states:
-                s["step"].fill_(_next_step(s["step"]))  # s["step"] += 1
-            increment_version(self._params + [s["exp_avg"] for s in states] + [s["exp_avg_sq"] for s in states])
+            for s, value in zip(states, nexts):
+                s["step"].fill_(value)  # s["step"] += 1
+            self._operands.bump_versions()
 
         return commit
 
@@ -854,7 +854,7 @@ class _RecordedSgd:
         groups = _replay_groups(opt, self._params)
         for p, ptr in zip(self._params, self._grad_ptrs):
             _check_recorded_grad(p, ptr)
-        self._operands.check()
+        self._operands.check([opt._optimizer.state[p] for p in self._params])
         found = {_sgd_scalars(groups[id(p)]) for p in self._params}
         if len(found) != 1:
             raise _replay_error("the parameters recorded in one launch no longer share their scalars")
@@ -863,8 +863,6 @@ class _RecordedSgd:
         if flags != self._flags & kernel_flags:
             raise _replay_error("momentum, Nesterov or weight decay was switched on or off, which selects "
                                 "another recorded kernel")
-        buffers = [opt._optimizer.state[p]["momentum_buffer"] for p in self._params] \
-            if self._flags & _native.SGD_MOMENTUM else []
         lib = _native.library()
         if self._pdtype == torch.float64:
             status = lib.hbt_sgd_scalar_record_f64(self._record, float(self._unscale), *scalars, self._flags)
@@ -874,7 +872,7 @@ class _RecordedSgd:
         _native.check(status, "optim.hbt_sgd_scalar_record")
 
         def commit() -> None:
-            increment_version(self._params + buffers)
+            self._operands.bump_versions()
 
         return commit
 
@@ -897,10 +895,21 @@ class _RecordedOperands:
         state = self._optimizer._optimizer.state
         return [p.detach() for p in self._params] + [state[p][k] for p in self._params for k in self._keys]
 
-    def check(self) -> None:
-        state = self._optimizer._optimizer.state
-        if any(k not in state[p] for p in self._params for k in self._keys) or \
-                [t.data_ptr() for t in self._current()] != self._ptrs:
+    def bump_versions(self) -> None:
+        """Advance the version counters of the tensors a replay updates (a detached
+        tensor shares its parameter's counter)."""
+        increment_version(self._held)
+
+    def check(self, states: list[dict]) -> None:
+        """``states``: the recorded parameters' current state dicts, in order."""
+        ptrs = [p.data_ptr() for p in self._params]
+        for st in states:
+            for key in self._keys:
+                tensor = st.get(key)
+                if tensor is None:
+                    break
+                ptrs.append(tensor.data_ptr())
+        if ptrs != self._ptrs:
             raise _replay_error("a parameter or its optimizer state is no longer the tensor the step was recorded "
                                 "with (a load_state_dict or an assignment to .data since the recording); a replay "
                                 "updates the recorded tensors")
