@@ -933,8 +933,8 @@ __global__ __launch_bounds__(kShareBlock) void local_share_tiles_kernel(
 // it; wave 0 then forms the partial of the shard's real segment from the tile sums as
 // tile_sums_to_partials_kernel does (lane l adds tile l's sum to +0.0, then the butterfly;
 // the segment is a single norm chunk) and writes +0.0 for the padding segment, so outputs
-// and partials are bitwise the two-launch form's.  A step of a small model is bound by
-// launch time, which this halves.
+// and partials are bitwise the two-launch form's.  A small model's step is bound by launch
+// time, and this takes one launch out of it.
 constexpr int kSmallShareTiles = 16;
 
 template <int ID, int kG, bool kRecip, int RD, int OD>
@@ -962,7 +962,6 @@ __global__ __launch_bounds__(kSmallShareTiles * kShareBlock) void local_share_sm
         if (shard_numel > valid_numel) partials[slot] = 0.0;
     }
 }
-
 
 // Reduce dtype float64: each rank's element widens exactly to double (IB = 8 reads a
 // float64 no_sync accumulator or float64 gradients), the divide and the rank-order sum run
