@@ -678,3 +678,71 @@ def test_random_recorded_steps(device, case):
             assert sa.keys() == sb.keys(), context
             for key in sa:
                 assert torch.equal(sa[key], sb[key]), (context, k, key)
+
+
+@pytest.mark.parametrize("case", range(16))
+def test_random_recorded_ddp_steps(device, case):
+    """Random data-parallel tails taken eagerly and by replaying a ``StepGraph``
+    recording: parameters of random shapes in gradient buckets of a random cap (the
+    gradients bound as bucket views after the first step, so each pack divides them in
+    place by the group size), group sizes 1 to 8, fp32 / bf16 / float64 parameters, AdamW
+    or SGD with every clip placement.  Buckets, parameters, state and norms must be
+    bitwise equal after every step."""
+    from hybrid_training_amd import BucketedGradients, DDPConfig, OptimizerConfig, ShardedOptimizer, StepGraph
+
+    rng = np.random.default_rng(9500 + case)
+    shapes = [tuple(int(d) for d in rng.integers(1, 40, int(rng.integers(1, 3)))) for _ in range(int(rng.integers(1, 13)))]
+    dtype = [torch.float32, torch.bfloat16, torch.float64][int(rng.integers(0, 3))]
+    world = int(rng.integers(1, 9))
+    cap_mb = float(rng.choice([0.5, 2.0, 8.0])) / 1024
+    name = ["adamw", "sgd"][int(rng.integers(0, 2))]
+    placement = [{}, {"defer_clip": True}, {"clip_in_step": True}][int(rng.integers(0, 3))]
+    max_norm = float(rng.choice([0.01, 1.0, 100.0]))
+    config = OptimizerConfig(name=name, learning_rate=1e-3, weight_decay=0.01, momentum=0.9)
+    context = f"case {case}: shapes {shapes}, {_NAMES[dtype]}, W={world}, cap {cap_mb} MiB, {name}, {placement}"
+
+    def build():
+        gen = torch.Generator(device=device).manual_seed(case)
+        named = [(f"p{i}", torch.nn.Parameter((torch.randn(s, device=device, generator=gen) * 0.02).to(dtype)))
+                 for i, s in enumerate(shapes)]
+        group = GroupHandle.local_view("data_parallel", world, 0) if world > 1 else GroupHandle.trivial()
+        ddp = BucketedGradients(named, group, DDPConfig(bucket_cap_mb=cap_mb))
+        params = [p for _, p in named]
+        opt = ShardedOptimizer(params, config, norm_group=GroupHandle.trivial(), device=device, **placement)
+        return params, ddp, opt
+
+    def fill(params, k):
+        gen = torch.Generator(device=device).manual_seed(1000 * case + k)
+        for p in params:
+            g = (torch.randn(p.shape, device=device, generator=gen) * 1e-2).to(dtype)
+            if p.grad is None:
+                p.grad = g
+            else:
+                p.grad.copy_(g)
+
+    def step(params, ddp, opt):
+        ddp.synchronize()
+        norm = opt.clip_grad_norm(max_norm)
+        opt.step()
+        return norm
+
+    a, b = build(), build()
+    for params, ddp, opt in (a, b):
+        fill(params, 0)
+        step(params, ddp, opt)
+    graph = StepGraph(lambda: step(*b))
+    for k in range(1, 4):
+        fill(a[0], k)
+        fill(b[0], k)
+        norm = step(*a)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(norm, graph.output), (context, k)
+        for ba, bb in zip(a[1]._buckets, b[1]._buckets):
+            assert torch.equal(ba.buffer, bb.buffer), (context, k, "bucket")
+        for pa, pb in zip(a[0], b[0]):
+            assert torch.equal(pa, pb), (context, k)
+            sa, sb = a[2].inner.state[pa], b[2].inner.state[pb]
+            assert sa.keys() == sb.keys(), context
+            for key in sa:
+                assert torch.equal(sa[key], sb[key]), (context, k, key)
