@@ -434,3 +434,45 @@ def test_write_words_across_blocks_and_launches(count):
     got = dst.cpu().numpy().view(np.uint32)
     assert np.array_equal(got[:count], words)
     assert np.all(got[count:] == np.uint32(0xFFFFFFFF))
+
+
+@pytest.mark.parametrize("world", [2, 4])
+def test_recorded_no_sync_cycle(world):
+    """A whole gradient-accumulation cycle recorded: one micro-batch accumulated without
+    reduction (no_sync), the next added to it and reduced in one pass, then the clip and
+    AdamW.  The accumulator rows the first micro-batch allocates belong to the graph, and
+    each replay repeats the cycle from its first micro-batch; every replay is bitwise the
+    eager cycle."""
+    config = OptimizerConfig(learning_rate=1e-3, weight_decay=0.01)
+    eager, graphed = _Tail(world, config), _Tail(world, config)
+    micro = [[torch.empty_like(g) for g in eager.grads] for _ in range(2)]
+
+    def load(k: int) -> None:
+        gen = torch.Generator(device=DEV).manual_seed(700 + k)
+        for batch in micro:
+            for g in batch:
+                g.copy_(torch.randn(g.shape, device=DEV, generator=gen))
+                g[TOTAL:] = 0.0
+
+    def cycle(tail: _Tail) -> list[torch.Tensor]:
+        norms = []
+        for r, (h, opt) in enumerate(zip(tail.handles, tail.opts)):
+            h.set_accumulate_without_reduction(True)
+            assert h.reduce_scatter_gradient(micro[0][r], peer_grads=micro[0]) is None
+            h.set_accumulate_without_reduction(False)
+            h.flat_param.grad = h.reduce_scatter_gradient(micro[1][r], peer_grads=micro[1])
+            norms.append(opt.clip_grad_norm(1.0))
+            opt.step()
+        return norms
+
+    load(0)
+    for tail in (eager, graphed):
+        cycle(tail)
+    graph = StepGraph(lambda: cycle(graphed))
+    assert not any(h.has_pending_accumulation for h in graphed.handles)
+    for k in range(1, 5):
+        load(k)
+        norms = cycle(eager)
+        graph.replay()
+        torch.cuda.synchronize()
+        _assert_same(eager, graphed, norms, graph.output, k)
