@@ -501,7 +501,16 @@ def require_dense(tensor: torch.Tensor, operation: str) -> None:
 
 _RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 _IS_CAPTURING = getattr(torch._C, "_cuda_isCurrentStreamCapturing", None)
+_RAW_DEVICE = getattr(torch._C, "_cuda_getDevice", None)
 _NO_GUARD = contextlib.nullcontext()
+
+
+def _current_device() -> int:
+    """torch's current device index; once torch has initialised the device, read without
+    its lazy-initialisation check (every launch's host path asks)."""
+    if _RAW_DEVICE is not None and torch.cuda.is_initialized():
+        return int(_RAW_DEVICE())
+    return torch.cuda.current_device()
 
 
 def device_guard(device: torch.device):
@@ -509,7 +518,7 @@ def device_guard(device: torch.device):
     already the current one (the usual case: a guard costs about a microsecond of host
     time, and every launch's host path takes one)."""
     if isinstance(device, torch.device) and device.type == "cuda" and (
-            device.index is None or device.index == torch.cuda.current_device()):
+            device.index is None or device.index == _current_device()):
         return _NO_GUARD
     return torch.cuda.device(device)
 
@@ -519,7 +528,7 @@ def stream_of(device: torch.device) -> int:
     a ``torch.cuda.Stream`` object: this is on every launch's host path)."""
     if _RAW_STREAM is not None:
         index = device.index if isinstance(device, torch.device) else torch.device(device).index
-        return int(_RAW_STREAM(torch.cuda.current_device() if index is None else index))
+        return int(_RAW_STREAM(_current_device() if index is None else index))
     return int(torch.cuda.current_stream(device).cuda_stream)
 
 

@@ -43,7 +43,6 @@ from __future__ import annotations
 
 from collections.abc import Callable, Iterable, Sequence
 from dataclasses import dataclass, field
-from functools import cached_property
 from typing import Any
 
 import numpy as np
@@ -289,28 +288,41 @@ class NormResult:
     use: a view costs about a microsecond of host time, and a step needs only the
     multiplier's address."""
 
+    __slots__ = ("scalars", "_sum", "_norm", "_grad_mul64", "_grad_mul", "_nonfinite")
+
     def __init__(self, scalars: torch.Tensor) -> None:
         self.scalars = scalars
+        self._sum = self._norm = self._grad_mul64 = self._grad_mul = self._nonfinite = None
 
-    @cached_property
+    @property
     def sum(self) -> torch.Tensor:
-        return self.scalars[0]
+        if self._sum is None:
+            self._sum = self.scalars[0]
+        return self._sum
 
-    @cached_property
+    @property
     def norm(self) -> torch.Tensor:
-        return self.scalars[1]
+        if self._norm is None:
+            self._norm = self.scalars[1]
+        return self._norm
 
-    @cached_property
+    @property
     def grad_mul64(self) -> torch.Tensor:
-        return self.scalars[2:3]
+        if self._grad_mul64 is None:
+            self._grad_mul64 = self.scalars[2:3]
+        return self._grad_mul64
 
-    @cached_property
+    @property
     def grad_mul(self) -> torch.Tensor:
-        return self.scalars[3:].view(torch.float32)[:1]
+        if self._grad_mul is None:
+            self._grad_mul = self.scalars[3:].view(torch.float32)[:1]
+        return self._grad_mul
 
-    @cached_property
+    @property
     def nonfinite(self) -> torch.Tensor:
-        return self.scalars[3:].view(torch.int32)[1:]
+        if self._nonfinite is None:
+            self._nonfinite = self.scalars[3:].view(torch.int32)[1:]
+        return self._nonfinite
 
     def multiplier_ptr(self, dtype: torch.dtype) -> int:
         """Device address of the clip multiplier a gradient of ``dtype`` is scaled by: the
