@@ -204,7 +204,7 @@ class BucketedGradients:
             raise ShardingError(
                 format_error(
                     "ddp.DistributedDataParallel",
-                    "the wrapped module has no trainable parameters, so there is nothing to bucket",
+                    "no trainable parameters were found in the wrapped module; DDP has no gradients to place in buckets",
                     rank=group.global_rank,
                     observed=0,
                     resolution="wrap a module after its parameters exist and require gradients",

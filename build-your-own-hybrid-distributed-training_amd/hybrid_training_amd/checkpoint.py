@@ -158,7 +158,7 @@ def _check_file(directory: Path, manifest: CheckpointManifest, filename: str, *,
     record = manifest.files.get(filename)
     if record is None:
         raise CheckpointCorruptionError(
-            format_error(operation, f"payload {filename!r} has no integrity record in the manifest",
+            format_error(operation, f"the manifest's file table holds no integrity record for payload {filename!r}",
                          observed=sorted(manifest.files)[:8],
                          resolution="the manifest's files table is incomplete")
         )
@@ -418,7 +418,7 @@ def write_checkpoint(
         raise CheckpointError(
             format_error(
                 "checkpoint.save",
-                "the checkpoint could not be published; no directory was renamed into place",
+                "publishing the checkpoint failed before its staging directory took the final name",
                 observed=f"{type(error).__name__}: {error}",
                 resolution=f"look in {staging.name!r}, which is kept as it was when the save failed",
             )

@@ -104,8 +104,8 @@ class FSDPConfig:
         if not self.use_padding:
             _fail(
                 "FSDPConfig",
-                "use_padding=False is not supported: without padding, shard sizes would differ "
-                "between ranks and no single even split of the flat parameter would exist",
+                "use_padding=False is not supported: every rank's shard must hold the same number "
+                "of elements, and only a padded flat parameter splits that way for any size",
                 True,
                 False,
                 "keep use_padding=True",
@@ -155,8 +155,8 @@ class MixedPrecisionConfig:
         if self.enabled and self.scaler.enabled and resolve_dtype(self.param_dtype) is not torch.float16:
             _fail(
                 "MixedPrecisionConfig",
-                "loss scaling is only meaningful for float16 compute: bfloat16 shares float32's "
-                "exponent range, so its gradients do not underflow where float16's do",
+                "loss scaling is only meaningful for float16 compute: a bfloat16 gradient has "
+                "float32's 8-bit exponent and keeps small values that float16 flushes to zero",
                 "float16",
                 self.param_dtype,
                 "compute in float16, or turn the scaler off",

@@ -92,7 +92,7 @@ class CheckpointCorruptionError(CheckpointError):
 
 
 class CheckpointVersionError(CheckpointError):
-    """The checkpoint format version is not readable by this library."""
+    """A manifest names a format version other than the one this library writes and reads."""
 
 
 class CheckpointTopologyError(CheckpointError):

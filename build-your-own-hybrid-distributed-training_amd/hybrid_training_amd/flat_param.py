@@ -213,15 +213,14 @@ class FlatParamHandle:
                 raise ShardingError(
                     format_error(
                         "fsdp.FlatParamHandle",
-                        "this unit's all-gather would exceed limit_all_gather_bytes; a unit "
-                        "that large defeats the purpose of sharding because its transient "
-                        "full copy dominates the memory saved",
+                        "the gathered buffer of this unit is larger than limit_all_gather_bytes "
+                        "allows; while it is gathered, its full copy outweighs what sharding saves",
                         rank=shard_group.global_rank,
                         expected=f"<= {config.limit_all_gather_bytes} bytes",
                         observed=gathered,
                         resolution=(
-                            "lower FSDPConfig.auto_wrap_min_num_params so the model is split "
-                            "into more units, or raise limit_all_gather_bytes"
+                            "split the model into smaller units (a lower FSDPConfig.auto_wrap_min_num_params) "
+                            "or allow a larger gather (limit_all_gather_bytes)"
                         ),
                     )
                 )
@@ -443,7 +442,7 @@ class FlatParamHandle:
         return full
 
     def reshard(self) -> None:
-        """Release the gathered buffer's storage, keeping the tensor object (``fsdp.py:636-658``).
+        """Free the memory of the gathered buffer; the tensor object itself survives (``fsdp.py:636-658``).
 
         Views of it stay valid objects over zero bytes until :meth:`refill`.
         """
@@ -485,7 +484,7 @@ class FlatParamHandle:
                 setattr(module, attribute, placeholder)
 
     def bind_views(self, full: torch.Tensor) -> None:
-        """Point every managed module attribute at its slice of ``full`` (zero copy)."""
+        """Rebind each managed module attribute to a view into ``full``; no data moves."""
         sizes = [entry.numel for entry in self._entries]
         if self._padding:
             sizes.append(self._padding)

@@ -1545,14 +1545,13 @@ class ShardedOptimizer:
             raise ShardingError(
                 format_error(
                     "optim.load_state_dict",
-                    "the checkpoint holds optimizer state for a different number of "
-                    "parameters, so the state cannot be matched to the current model",
+                    "the number of parameters with optimizer state in the checkpoint differs "
+                    "from this optimizer's, so no state can be assigned",
                     rank=self._norm_group.global_rank,
                     expected=expected,
                     observed=observed,
                     resolution=(
-                        "resume with the same model definition and the same wrapping "
-                        "granularity that produced the checkpoint"
+                        "load into a model built and wrapped exactly as the one that saved it"
                     ),
                 )
             )

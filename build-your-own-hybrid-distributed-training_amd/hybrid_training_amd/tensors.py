@@ -106,10 +106,8 @@ def build_flat_layout(
     """Offsets of ``named_tensors`` concatenated in the given order.
 
     Offsets are the exclusive prefix sum of the element counts
-    (``utils/tensors.py:137-196``).  Returns ``(entries, total_numel)``.
-
-    Raises:
-        ShardingError: on an empty list or a repeated name.
+    (``utils/tensors.py:137-196``); the result is ``(entries, total_numel)``.  An
+    empty list or a name given twice raises :class:`ShardingError`.
     """
     if len(named_tensors) == 0:
         raise ShardingError(

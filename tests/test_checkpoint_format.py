@@ -132,7 +132,7 @@ def test_failed_publish_renames_nothing_and_keeps_the_staging_directory(tmp_path
                     "tensor_parallel_rank": 0, "state_name": "", "rank": rank, "file": f"rank-0000{rank}.pt",
                     "offset": 0, "length": 12, "storage_key": "model::w@0"}]
         shards.append((rank, {"model::w@0": data.clone()}, records, {"step": 1}))
-    with pytest.raises(CheckpointError, match="could not be published") as info:
+    with pytest.raises(CheckpointError, match="publishing the checkpoint failed") as info:
         write_checkpoint(tmp_path, 1, shards)
     assert "overlap" in str(info.value)
     assert not (tmp_path / "checkpoint-step-000001").exists()
