@@ -2,8 +2,8 @@
 
 A small model's step is a handful of kernels of a few microseconds each.  Issued one by
 one from Python, each costs more on the host than it runs on the device: the drop-in
-tail of the reference's 1,857-parameter MLP (local share, clip, AdamW; five launches
-per rank) spends about 75 us of host time per rank-step on about 12 us of kernels.
+tail of the reference's 1,857-parameter MLP (local share, clip, AdamW; three launches
+per rank) spends several times longer in host code than its kernels run.
 :class:`StepGraph` records every launch a step function makes into one HIP graph
 (``torch.cuda.graph``) and replays them all with one launch.
 
@@ -12,8 +12,8 @@ kernels of a recorded step read their scalars from small device slots
 (``hbt_*_step_slot``), since AdamW's bias corrections move every step and every
 scalar follows the learning rate.  Before each replay, :meth:`StepGraph.replay`
 formats every recorded step's scalars from the host state (``hbt_*_scalar_record``,
-formed as the eager step forms them), writes all of the slots with one launch
-(``hbt_write_words``) and advances the step counters, so a replay is bitwise the eager
+formed as the eager step forms them), writes the slots with one launch per eight of
+them (``hbt_write_words``) and advances the step counters, so a replay is bitwise the eager
 step.  Copy tables that recorded launches read are written by the
 graph itself (``hbt_write_words``) and live as long as it does.
 
