@@ -275,6 +275,8 @@ def main() -> int:
             "shard_numel": n,
             "optimizer": {"lr": LR, "betas": list(BETAS), "eps": EPS, "weight_decay": WD},
             "max_grad_norm": MAX_NORM,
+            "clip": "multiplier applied inside the fused update (defer_clip): parameters and state bitwise "
+                    "those of the in-place .grad clip, which --workload inplace_clip measures",
             "bytes_per_param": BYTES_NORM + BYTES_ADAMW,
         },
         "step_hbm_gbps": step_gbps,
