@@ -21,6 +21,7 @@ this rank's pre-divided contribution, ready for it.
 
 from __future__ import annotations
 
+import operator
 from collections.abc import Iterable, Iterator, Sequence
 from contextlib import contextmanager
 from dataclasses import dataclass, field
@@ -33,6 +34,36 @@ from . import _native
 from .config import DDPConfig
 from .errors import ShardingError, UnsupportedFeatureError, format_error
 from .groups import GroupHandle
+
+_GRAD = operator.attrgetter("grad")
+_DTYPE = operator.attrgetter("dtype")
+
+
+@dataclass(frozen=True)
+class _PackMemo:
+    """The launches of the last full pack and the gradients they were built for: every
+    gradient's address, dtype and element count, all dense.  Rows depend on nothing
+    else, so equal values mean equal rows."""
+
+    ptrs: tuple[int, ...]
+    dtypes: tuple[torch.dtype, ...]
+    numels: tuple[int, ...]
+    divisor: float
+    op: int
+    plans: tuple[tuple[_native.CopyPlan, torch.dtype, torch.dtype], ...]
+
+
+def _gradient_signature(params: Sequence[nn.Parameter]) -> tuple | None:
+    """``(addresses, dtypes, element counts)`` of the parameters' gradients when every
+    one is present and dense, else ``None`` (C-level loops: this runs every step)."""
+    grads = list(map(_GRAD, params))
+    try:
+        ptrs = tuple(map(torch.Tensor.data_ptr, grads))
+    except (TypeError, RuntimeError):  # a parameter without a gradient, or a sparse one
+        return None
+    if not all(map(torch.Tensor.is_contiguous, grads)):
+        return None
+    return ptrs, tuple(map(_DTYPE, grads)), tuple(map(torch.Tensor.numel, grads))
 
 __all__ = ["BucketLayout", "BucketedGradients", "DDPStatistics", "GradientBucket", "build_buckets"]
 
@@ -222,6 +253,9 @@ class BucketedGradients:
             _native.require_device_tensor(p, "ddp.BucketedGradients")
         self._buckets = build_buckets(self._named, self._config.bucket_cap_mb)
         self._name_of = {id(p): n for n, p in self._named}
+        self._all_params = tuple(p for bucket in self._buckets for p in bucket.parameters)
+        self._all_bytes = sum(bucket.num_bytes() for bucket in self._buckets)
+        self._pack_memo: _PackMemo | None = None
         self._require_backward_grad_sync = True
         self.statistics = DDPStatistics()
 
@@ -268,7 +302,23 @@ class BucketedGradients:
         """
         if not self._require_backward_grad_sync:
             return
+        divisor = self._divisor()
+        signature = None
         if buckets is None:
+            # A full pack over the same dense gradients as the last one reuses its
+            # launches: the checks below have nothing new to find, and the per-parameter
+            # Python would cost more host time than the kernel takes on a model this size.
+            signature = _gradient_signature(self._all_params)
+            memo = self._pack_memo
+            if (signature is not None and memo is not None and memo.divisor == divisor
+                    and signature == (memo.ptrs, memo.dtypes, memo.numels)):
+                for plan, src_dtype, dst_dtype in memo.plans:
+                    plan.run(src_dtype=src_dtype, dst_dtype=dst_dtype, op=memo.op, divisor=divisor)
+                _native.bump_versions([b.buffer for b in self._buckets])
+                self.statistics.unused_parameters = ()
+                self.statistics.buckets_reduced += len(self._buckets)
+                self.statistics.bytes_reduced += self._all_bytes
+                return
             selected = self._buckets
         else:
             indices = list(buckets)
@@ -279,7 +329,6 @@ class BucketedGradients:
                 )
             selected = [self._buckets[i] for i in indices]
         missing: list[str] = []
-        divisor = self._divisor()
         # Rows per (device, source dtype, bucket dtype): (source address, destination
         # address, n), source address 0 meaning a zero fill.  Built with plain attribute
         # reads: this loop runs once per step over every parameter.
@@ -337,9 +386,15 @@ class BucketedGradients:
                 )
             )
         op = _native.COPY_OP_DIVIDE if divisor != 1.0 else _native.COPY_OP_COPY
+        plans = []
         for (device_index, src_dtype, dst_dtype), table in rows.items():
             plan = _native.CopyPlan.from_rows(torch.device("cuda", device_index), table)
             plan.run(src_dtype=src_dtype, dst_dtype=dst_dtype, op=op, divisor=divisor)
+            plans.append((plan, src_dtype, dst_dtype))
+        # Remembered only for a full pack of gradients that were all present and dense
+        # (no temporary copies stand in for them in the rows).
+        self._pack_memo = (_PackMemo(*signature, divisor, op, tuple(plans))
+                           if signature is not None and not missing and not dense_copies else None)
         if rows:
             _native.bump_versions([b.buffer for b in selected])
         self.statistics.unused_parameters = tuple(missing)

@@ -203,3 +203,57 @@ def test_pack_with_ieee_specials(device):
         assert torch.equal(torch.isnan(got), nan), name
         bits = torch.int16 if p.dtype == torch.bfloat16 else torch.int32
         assert torch.equal(got[~nan].view(bits), want[~nan].view(bits)), name
+
+
+@pytest.mark.parametrize("world", [8, 3])
+def test_repeated_packs_follow_gradient_changes(device, world):
+    """A full pack over the same dense gradients reuses the last full pack's launches;
+    each change the rows depend on (a gradient in another tensor, a non-contiguous
+    gradient, a missing one) is packed afresh, and every pack equals ``grad / W``."""
+    shapes = [(7, 5), (13,), (4, 4, 3), (1,), (33,)]
+    named = [(f"p{i}", torch.nn.Parameter(torch.empty(s, device=device))) for i, s in enumerate(shapes)]
+    gen = torch.Generator(device=device).manual_seed(world)
+
+    def fresh(shape):
+        return torch.randn(shape, device=device, generator=gen)
+
+    for _, p in named:
+        p.grad = fresh(p.shape)
+    ddp = BucketedGradients(named, GroupHandle.local_view("dp", world, 0),
+                            DDPConfig(bucket_cap_mb=0.0001, find_unused_parameters=True))
+    assert len(ddp.buckets) > 1
+
+    def packed_equals_grads():
+        ddp.pack()
+        for bucket in ddp.buckets:
+            buf = bucket.buffer.cpu().numpy()
+            for param, off, numel in zip(bucket.parameters, bucket.layout.offsets, bucket.layout.numels):
+                g = param.grad
+                expect = (np.zeros(numel, np.float32) if g is None
+                          else (g.detach().cpu().numpy().reshape(-1) / np.float32(world)).astype(np.float32))
+                assert np.array_equal(buf[off : off + numel].view(np.int32), expect.view(np.int32))
+
+    packed_equals_grads()
+    memo = ddp._pack_memo
+    assert memo is not None
+    for _, p in named:  # new values in the same tensors: the remembered launches
+        p.grad.copy_(fresh(p.shape))
+    packed_equals_grads()
+    assert ddp._pack_memo is memo
+    named[1][1].grad = fresh(shapes[1])  # another tensor
+    packed_equals_grads()
+    assert ddp._pack_memo is not memo and ddp._pack_memo is not None
+    named[0][1].grad = fresh((5, 7)).t()  # non-contiguous: packed through a dense copy, not remembered
+    packed_equals_grads()
+    assert ddp._pack_memo is None
+    named[0][1].grad = fresh(shapes[0])
+    named[2][1].grad = None  # unused: zeros, not remembered
+    packed_equals_grads()
+    assert ddp._pack_memo is None and ddp.statistics.unused_parameters == ("p2",)
+    named[2][1].grad = fresh(shapes[2])
+    packed_equals_grads()
+    assert ddp._pack_memo is not None and ddp.statistics.unused_parameters == ()
+    for _, p in named:
+        p.grad.mul_(3.0)
+    packed_equals_grads()
+    assert ddp.statistics.buckets_reduced == 7 * len(ddp.buckets)  # seven full packs
