@@ -867,10 +867,10 @@ def reshard_state_dict_pieces(
         raise ShardingError(
             format_error(
                 "fsdp.reshard_state_dict_pieces",
-                f"the supplied pieces leave {missing} element(s) of {pieces[0].name!r} uncovered",
-                expected=f"{total} covered elements",
+                f"{missing} element(s) of {pieces[0].name!r} lie in none of the given pieces",
+                expected=f"pieces covering all {total} elements",
                 observed=covered,
-                resolution="some piece of the tensor was not passed in",
+                resolution="pass every stored piece of the tensor",
             )
         )
     flat = torch.empty(total, dtype=dtype, device=device)
