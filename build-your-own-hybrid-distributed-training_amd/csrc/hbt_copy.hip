@@ -122,14 +122,22 @@ __device__ __forceinline__ uint32_t f32_to_elem(float x) {
 // kOpScale: HBT_COPY_OP_DIVIDE by a power of two, run as a multiply by its exact
 // reciprocal (passed in place of the divisor); the bits are those of the division.
 constexpr int kOpScale = 2;
-template <int SB, int DB, int OP, bool H>
-__device__ __forceinline__ uint32_t convert(uint32_t bits, float divisor) {
-    if constexpr (SB == DB && OP == HBT_COPY_OP_COPY) return bits;
+template <int SB, int OP, bool H>
+__device__ __forceinline__ float convert_value(uint32_t bits, float divisor) {
     float x = elem_to_f32<SB, H>(bits);
     if constexpr (OP == HBT_COPY_OP_DIVIDE) x = x / divisor;
     if constexpr (OP == kOpScale) x = x * divisor;
-    return f32_to_elem<DB, H>(x);
+    return x;
 }
+template <int SB, int DB, int OP, bool H>
+__device__ __forceinline__ uint32_t convert(uint32_t bits, float divisor) {
+    if constexpr (SB == DB && OP == HBT_COPY_OP_COPY) return bits;
+    return f32_to_elem<DB, H>(convert_value<SB, OP, H>(bits, divisor));
+}
+// Whether a copy rounds fp32 values to a 2-byte destination (a narrowing, or arithmetic on
+// 2-byte elements): the vector paths then round two values per packed conversion.
+template <int SB, int DB, int OP>
+constexpr bool rounds_to_b16() { return DB == 2 && !(SB == 2 && OP == HBT_COPY_OP_COPY); }
 
 template <int EB>
 __device__ __forceinline__ uint32_t load_elem(const gbyte* p) {
@@ -342,9 +350,22 @@ __global__ __launch_bounds__(kCopyBlock) void copy_aligned_kernel(const int64_t*
             for (int i = 0; i < kSrcWords; ++i) words[i] = x[j][i];
             uint32_t e[U];
             unpack_unit<SB, U>(words, e);
+            if constexpr (rounds_to_b16<SB, DB, OP>()) {
+                // Two values per packed conversion, each the bits f32_to_b16 gives.
+                float f[U];
 #pragma unroll
-            for (int i = 0; i < U; ++i) e[i] = convert<SB, DB, OP, H>(e[i], divisor);
-            pack_unit_store<DB, U>(d + u * U * DB, e);
+                for (int i = 0; i < U; ++i) f[i] = convert_value<SB, OP, H>(e[i], divisor);
+                uint32_t w[U / 2];
+                pack_rounded<H ? HBT_DTYPE_F16 : HBT_DTYPE_BF16, U / 2>(f, w);
+                typename Vec<U / 2>::type o;
+#pragma unroll
+                for (int i = 0; i < U / 2; ++i) o[i] = w[i];
+                stg<U / 2>(d + u * U * DB, o);
+            } else {
+#pragma unroll
+                for (int i = 0; i < U; ++i) e[i] = convert<SB, DB, OP, H>(e[i], divisor);
+                pack_unit_store<DB, U>(d + u * U * DB, e);
+            }
         }
     }
     if (threadIdx.x < len - units * U) {

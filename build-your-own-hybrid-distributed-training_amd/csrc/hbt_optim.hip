@@ -38,42 +38,6 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 template <int D>
 constexpr int64_t bytes_of() { return D == F32 ? 4 : (D == HBT_DTYPE_F64 ? 8 : 2); }
 
-// Two fp32 values rounded to the 2-byte dtype RD (nearest even) and packed low half first by
-// one packed conversion: the bits f32_to_b16 gives for each, except that a bf16 NaN keeps the
-// conversion's encoding (pack_rounded and store_vec write 0x7FC0 instead).
-template <int RD>
-__device__ __forceinline__ uint32_t pack2_rounded(float a, float b) {
-    typedef float f2 __attribute__((ext_vector_type(2)));
-    if constexpr (RD == BF16) {
-        typedef __bf16 r2 __attribute__((ext_vector_type(2)));
-        return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{opaque(a), opaque(b)}, r2));
-    } else {
-        static_assert(RD == F16, "2-byte dtypes are bf16 and fp16");
-        typedef _Float16 r2 __attribute__((ext_vector_type(2)));
-        return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{opaque(a), opaque(b)}, r2));
-    }
-}
-
-// 2N fp32 values rounded to the 2-byte dtype RD and packed into N dwords, a bf16 NaN as
-// 0x7FC0: f32_to_b16's bits for each, in N conversions and 2N compares, where f32_to_b16
-// takes about 7 operations per element.
-template <int RD, int N>
-__device__ __forceinline__ void pack_rounded(const float (&y)[2 * N], uint32_t (&o)[N]) {
-#pragma unroll
-    for (int i = 0; i < N; ++i) o[i] = pack2_rounded<RD>(y[2 * i], y[2 * i + 1]);
-    if constexpr (RD == BF16) {
-        bool nan = false;
-#pragma unroll
-        for (int c = 0; c < 2 * N; ++c) nan = nan || y[c] != y[c];
-        if (nan) {
-#pragma unroll
-            for (int i = 0; i < N; ++i) {
-                if (y[2 * i] != y[2 * i]) o[i] = (o[i] & 0xFFFF0000u) | 0x7FC0u;
-                if (y[2 * i + 1] != y[2 * i + 1]) o[i] = (o[i] & 0xFFFFu) | 0x7FC00000u;
-            }
-        }
-    }
-}
 template <int RD>
 __device__ __forceinline__ u32x4 pack8_rounded(const float (&y)[8]) {
     uint32_t o[4];
