@@ -178,6 +178,7 @@ __device__ __forceinline__ void pack_rounded(const float (&y)[2 * N], uint32_t (
         }
     }
 }
+
 // The dtype code of SB-byte elements (a 2-byte element being fp16 when H, else bf16).
 template <int SB, bool H>
 constexpr int dtype_of() {
