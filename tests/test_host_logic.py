@@ -466,3 +466,26 @@ def test_step_counter_advances_as_torch_adds_one(dtype):
         got = _next_step(counter)
         counter.fill_(got)
         assert torch.equal(counter, expected) and got == float(expected.item()), (dtype, value)
+
+
+def test_gradient_signature_of_a_full_bucket_pack():
+    """The key under which a full DDP pack reuses its launches: every gradient's address,
+    dtype and element count, and no key at all when a gradient is missing or strided
+    (such a pack goes through the checks and temporary dense copies every time)."""
+    from hybrid_training_amd.buckets import _gradient_signature
+
+    params = [torch.nn.Parameter(torch.zeros(s)) for s in ((3, 4), (5,), (2, 2, 2))]
+    for p in params:
+        p.grad = torch.randn(p.shape)
+    ptrs, dtypes, numels = _gradient_signature(params)
+    assert ptrs == tuple(p.grad.data_ptr() for p in params)
+    assert dtypes == (torch.float32,) * 3 and numels == (12, 5, 8)
+    again = _gradient_signature(params)
+    assert again == (ptrs, dtypes, numels)
+    params[1].grad = torch.randn(5)  # another tensor: another address
+    assert _gradient_signature(params)[0] != ptrs
+    params[0].grad = torch.randn(4, 3).t()  # strided
+    assert _gradient_signature(params) is None
+    params[0].grad = torch.randn(3, 4)
+    params[2].grad = None  # missing
+    assert _gradient_signature(params) is None
